@@ -1,0 +1,245 @@
+"""Benchmark of the MI355X LUT-linear hot path (BASELINE.json metric).
+
+One step = one hard LUT-linear forward + backward (grad_x, grad_palette, LoRA grads) over
+the seven Qwen-4B linear shapes at M = 16384 tokens (batch 32 x seq 512),
+straight-through through the frozen 2-bit indices, LoRA rank 16 (32 on o and down).
+`value` = sum over shapes of 6*M*K*N FLOP / step time (LoRA FLOP excluded, as in BASELINE).
+
+Also reported (same JSON line): the decode GEMV of config 2 (36 layers x 7 linears, M in
+{1, 4, 16}, one grouped launch per M) in GB/s of packed indices + palettes, the roofline of
+the dominant kernel (HIP events on the launch stream), and the reference's CPU PyTorch path
+(gather + matmul, torch autograd) timed on a bounded sample on the host cores.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only hard|gemv]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "qwen-palettize_amd"))
+
+# (name, K, N, LoRA rank) of the seven Qwen-4B linears
+SHAPES = [("q", 2560, 4096, 16), ("k", 2560, 1024, 16), ("v", 2560, 1024, 16),
+          ("o", 4096, 2560, 32), ("gate", 2560, 9728, 16), ("up", 2560, 9728, 16),
+          ("down", 9728, 2560, 32)]
+M_TRAIN = 16384
+LAYERS = 36
+PEAK_BF16_TFLOPS = 2500.0
+PEAK_HBM_GBS = 8000.0
+
+
+def _make_weight(N, K, gen, device):
+    import torch
+    from palettize_hip import ops
+    idx = torch.randint(0, 4, (N, K), generator=gen, device=device, dtype=torch.uint8)
+    pal = torch.sort(torch.randn(N, K // 256, 4, generator=gen, device=device) * 0.02,
+                     dim=-1).values.contiguous()
+    return ops.pack_indices(idx), pal, idx
+
+
+class HardStep:
+    """Inputs resident in HBM; run() issues one fwd+bwd of all seven shapes."""
+
+    def __init__(self, device, seed=0):
+        import torch
+        g = torch.Generator(device=device).manual_seed(seed)
+        self.items = []
+        for name, K, N, r in SHAPES:
+            packed, pal, _ = _make_weight(N, K, g, device)
+            x = torch.randn(M_TRAIN, K, generator=g, device=device).to(torch.bfloat16)
+            gy = torch.randn(M_TRAIN, N, generator=g, device=device).to(torch.bfloat16)
+            a = (torch.randn(r, K, generator=g, device=device) * 0.01).to(torch.bfloat16)
+            b = (torch.randn(N, r, generator=g, device=device) * 0.01).to(torch.bfloat16)
+            self.items.append(dict(name=name, K=K, N=N, r=r, packed=packed, pal=pal, x=x, gy=gy,
+                                   a=a, b=b))
+        self.flop = sum(6.0 * M_TRAIN * it["K"] * it["N"] for it in self.items)
+        self.events = None
+
+    def run(self, timed=False):
+        import torch
+        from palettize_hip import ops
+        rec = self.events if timed else None
+        for it in self.items:
+            x, gy, a, b = it["x"], it["gy"], it["a"], it["b"]
+            t = ops.lora_project(x, a, 1.0)
+            e = self._mark(rec, "fwd", it)
+            ops.lut_linear_fwd(x, it["packed"], it["pal"], None, t, b)
+            self._close(e)
+            gt = ops.lora_grad_t(gy, b, 1.0)
+            e = self._mark(rec, "grad_x", it)
+            ops.lut_linear_bwd_x(gy, it["packed"], it["pal"], gt, a)
+            self._close(e)
+            e = self._mark(rec, "grad_palette", it)
+            ops.lut_linear_bwd_palette(x, gy, it["packed"])
+            self._close(e)
+            ops.lora_weight_grads(x, gy, t, gt, 1.0, out_dtype=torch.bfloat16)
+
+    @staticmethod
+    def _mark(rec, kind, it):
+        if rec is None:
+            return None
+        import torch
+        s = torch.cuda.Event(enable_timing=True)
+        e = torch.cuda.Event(enable_timing=True)
+        s.record()
+        rec.setdefault(kind, []).append((s, e, 2.0 * M_TRAIN * it["K"] * it["N"]))
+        return e
+
+    @staticmethod
+    def _close(e):
+        if e is not None:
+            e.record()
+
+
+def kernel_rooflines(events):
+    """Per GEMM kind: algorithmic FLOP / summed event time -> TFLOP/s."""
+    out = {}
+    for kind, lst in events.items():
+        ms = sum(s.elapsed_time(e) for s, e, _ in lst)
+        fl = sum(f for _, _, f in lst)
+        out[kind] = dict(ms=ms, launches=len(lst), tflops=fl / (ms * 1e-3) / 1e12)
+    return out
+
+
+def bench_gemv(device, reps=20):
+    """Config 2: 36 layers x 7 linears per grouped launch; GB/s of packed idx + palettes."""
+    import torch
+    from palettize_hip import ops
+    g = torch.Generator(device=device).manual_seed(1)
+    weights = []
+    wbytes = 0
+    for _ in range(LAYERS):
+        for name, K, N, _r in SHAPES:
+            packed, pal, _ = _make_weight(N, K, g, device)
+            weights.append((packed, pal, K))
+            wbytes += packed.numel() * 4 + pal.numel() * 4
+    res = {}
+    for M in (1, 4, 16):
+        items = [(torch.randn(M, K, generator=g, device=device).to(torch.bfloat16), p, pl)
+                 for p, pl, K in weights]
+        grp = ops.GemvGroup(items)
+        for _ in range(3):
+            grp.run()
+        torch.cuda.synchronize()
+        s = torch.cuda.Event(enable_timing=True)
+        e = torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(reps):
+            grp.run()
+        e.record()
+        torch.cuda.synchronize()
+        ms = s.elapsed_time(e) / reps
+        gbs = wbytes / (ms * 1e-3) / 1e9
+        res[f"M{M}"] = dict(us=round(ms * 1e3, 2), gbs=round(gbs, 1),
+                            frac=round(gbs / PEAK_HBM_GBS, 4))
+        del grp, items
+    res["weight_bytes"] = wbytes
+    return res
+
+
+def cpu_baseline(budget_s=12.0):
+    """Reference CPU path (gather + matmul + LoRA, torch autograd) on a bounded sample of the
+    config-3 workload: M_cpu rows of every shape; TFLOP/s on the same 6*M*K*N count."""
+    import torch
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    from torch_ref import native_flat_idx, palettized_linear_cpu
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    g = torch.Generator().manual_seed(0)
+    M = 256
+    prepared = []
+    for name, K, N, r in SHAPES:
+        idx = torch.randint(0, 4, (N, K), generator=g, dtype=torch.uint8)
+        pal = torch.sort(torch.randn(N, K // 256, 4, generator=g) * 0.02, -1).values
+        prepared.append(dict(fi=native_flat_idx(idx), pal=pal.to(torch.bfloat16).requires_grad_(True),
+                             x=torch.randn(M, K, generator=g).to(torch.bfloat16).requires_grad_(True),
+                             gy=torch.randn(M, N, generator=g).to(torch.bfloat16),
+                             a=(0.01 * torch.randn(r, K, generator=g)).to(torch.bfloat16).requires_grad_(True),
+                             b=(0.01 * torch.randn(N, r, generator=g)).to(torch.bfloat16).requires_grad_(True),
+                             K=K, N=N))
+    flop_pass = sum(6.0 * M * p["K"] * p["N"] for p in prepared)
+    passes, t0 = 0, time.perf_counter()
+    while True:
+        for p in prepared:
+            y = palettized_linear_cpu(p["x"], p["pal"], p["fi"], None, p["a"], p["b"], 1.0)
+            y.backward(p["gy"])
+        passes += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or passes >= 50:
+            break
+    tflops = flop_pass * passes / el / 1e12
+    return dict(value=round(tflops, 5), unit="TFLOP/s", cores=cores, kind="port",
+                sample=f"hard fwd+bwd (torch CPU bf16 gather+matmul, autograd) of all 7 shapes "
+                       f"at M={M} rows, {passes} passes in {el:.1f}s")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only", choices=["hard", "gemv"], default=None)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one GPU only (the path has no multi-GPU "
+              "component; see DESIGN.md for how it would shard). Run with --gpus 1.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda:0")
+    from palettize_hip import _lib
+    _lib.lib()
+
+    out = {"metric": "LUT-linear fwd+bwd TFLOP/s @M=16384 (7 Qwen-4B shapes)",
+           "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+           "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+           "data": "synthetic (uniform 2-bit indices, N(0,0.02) sorted fp32 palettes, N(0,1) bf16 activations)",
+           "config": {"workload": "config3: hard fwd+bwd (grad_x, grad_palette, LoRA r16/r32) "
+                                  "of q,k,v,o,gate,up,down at M=16384",
+                      "M": M_TRAIN, "global_batch": 32, "seq_len": 512, "parallelism": "none (1 GPU)"}}
+
+    if args.only in (None, "hard"):
+        step = HardStep(dev)
+        for _ in range(args.warmup):
+            step.run()
+        torch.cuda.synchronize()
+        step.events = {}
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for _ in range(args.steps):
+            step.run(timed=True)
+        t1.record()
+        torch.cuda.synchronize()
+        ms = t0.elapsed_time(t1) / args.steps
+        tflops = step.flop / (ms * 1e-3) / 1e12
+        kr = kernel_rooflines(step.events)
+        dom = max(kr, key=lambda k: kr[k]["ms"])
+        out.update(value=round(tflops, 2), ms_per_step=round(ms, 3))
+        out["roofline"] = {"bound": "mfma", "kernel": f"gemm_kernel ({dom})",
+                           "achieved": round(kr[dom]["tflops"], 1), "peak": PEAK_BF16_TFLOPS,
+                           "unit": "TFLOP/s", "frac": round(kr[dom]["tflops"] / PEAK_BF16_TFLOPS, 4),
+                           "traffic": None}
+        out["kernels"] = {k: {"tflops": round(v["tflops"], 1),
+                              "ms_per_step": round(v["ms"] / args.steps, 3)} for k, v in kr.items()}
+        del step
+        torch.cuda.empty_cache()
+    if args.only in (None, "gemv"):
+        out["gemv"] = bench_gemv(dev)
+    if not args.no_cpu and args.only is None:
+        out["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,205 @@
+/* palettize_hip.h -- C ABI of the MI355X (gfx950) LUT-linear library libpalettize_hip.so.
+ *
+ * Every entry point takes raw device pointers, plain sizes and a hipStream_t passed as
+ * void*, returns PLZ_OK (0) or an error code, and never allocates device memory: outputs
+ * and workspaces are owned by the caller (workspace sizes come from the *_workspace
+ * queries). The last error message of the calling thread is returned by plz_last_error().
+ * Work is enqueued on the given stream only; nothing synchronises the host.
+ *
+ * bf16 tensors travel as uint16_t bit patterns. A palettized weight W[N,K] (output rows
+ * n, input columns k) is
+ *   packed  int32 [N, K/16]   2-bit indices, 16 per word along K, index of column k at
+ *                             bits 2*(k%16) (LSB first; same bytes as the reference's
+ *                             .idx2 packing, palettize_core.py:31-42)
+ *   palette fp32  [N, K/256, 4]  one 4-entry palette per row and per 256 columns
+ * and W[n,k] = bf16(palette[n, k/256, idx[n,k]]) (round to nearest even), the flat
+ * gather of qwen_model.py:97-102,185-186. The reference's own layout (palette group =
+ * 256 output channels spanning all of K) is the special case
+ * palette[n, g, :] = palette_ref[n/256, :] (expanded by the Python wrapper).
+ * K must be a multiple of 256 and N a multiple of 8 unless stated otherwise.
+ */
+#ifndef PALETTIZE_HIP_H
+#define PALETTIZE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PLZ_ABI_VERSION 1
+
+/* status codes */
+#define PLZ_OK 0
+#define PLZ_EINVAL 1       /* bad shape, dtype, alignment or null pointer */
+#define PLZ_EHIP 2         /* a HIP launch failed */
+#define PLZ_EUNSUPPORTED 3 /* valid request this build does not implement */
+#define PLZ_EWORKSPACE 4   /* workspace missing or smaller than the *_workspace query */
+
+/* dtype codes */
+#define PLZ_DT_BF16 0
+#define PLZ_DT_FP16 1
+#define PLZ_DT_FP32 2
+
+/* soft forward weight modes (plz_soft_build_w) */
+#define PLZ_W_SOFT 0       /* W = sum_c P_c pal_c                                        */
+#define PLZ_W_HARD_NOISY 1 /* W = pal[argmax_c P_c], first max wins (fused_lut_kernel.cu:1998-2003) */
+#define PLZ_W_HARD_PLAIN 2 /* W = pal[argmax_c logits_c], first max wins (triton_soft_forward.py:160-176) */
+
+/* ---- errors / version ------------------------------------------------------------ */
+const char* plz_last_error(void);
+int plz_abi_version(void);
+
+/* ---- index formats and dequantisation --------------------------------------------- */
+/* idx uint8 [rows, cols] (values 0..3) <-> packed int32 [rows, cols/16]; cols % 16 == 0.
+ * Replaces the reference's pack_idx2/unpack_idx2 (palettize_core.py:31-47,159-172) for the
+ * device layout (packing along the row). */
+int plz_pack_indices(const uint8_t* idx, int32_t* packed, int64_t rows, int64_t cols,
+                     void* stream);
+int plz_unpack_indices(const int32_t* packed, uint8_t* idx, int64_t rows, int64_t cols,
+                       void* stream);
+/* w bf16 [N, K] = dequantised weight. The gather of qwen_model.py:185-186. */
+int plz_dequant(const int32_t* packed, const float* palette, uint16_t* w, int64_t N, int64_t K,
+                void* stream);
+
+/* ---- hard LUT linear ------------------------------------------------------------- */
+/* y[M,N] = x[M,K] W^T (+ bias[N]) (+ lora_t[M,rank] lora_b[N,rank]^T).
+ * lora_t already carries the LoRA scaling (see plz_lora_project); rank in {0,8,...,64}.
+ * Replaces fused_lut_linear_fwd (fused_lut_linear_cuda.py:74-117) and its kernel
+ * fused_lut_linear_fwd_tc_kernel (fused_lut_kernel.cu:309-518), plus the LoRA add of
+ * QwenLoRA.forward (qwen_model.py:291-304). */
+int plz_lut_linear_fwd(const uint16_t* x, const int32_t* packed, const float* palette,
+                       const uint16_t* bias, const uint16_t* lora_t, const uint16_t* lora_b,
+                       int rank, uint16_t* y, int64_t M, int64_t N, int64_t K, void* stream);
+
+/* grad_x[M,K] = grad_y[M,N] W (+ lora_gt[M,rank] lora_a[rank,K]).
+ * Replaces the grad_x half of fused_lut_linear_bwd (fused_lut_linear_cuda.py:119-150) and
+ * fused_lut_linear_bwd_grad_x_tc_kernel (fused_lut_kernel.cu:551-720). */
+int plz_lut_linear_bwd_x(const uint16_t* grad_y, const int32_t* packed, const float* palette,
+                         const uint16_t* lora_gt, const uint16_t* lora_a, int rank,
+                         uint16_t* grad_x, int64_t M, int64_t N, int64_t K, void* stream);
+
+/* grad_palette fp32 [N, K/256, 4]: grad_palette[n,g,c] = sum over k in group g with
+ * idx[n,k] == c of (grad_y^T x)[n,k]. Deterministic (fixed-order two-stage reduction).
+ * Replaces the grad_palette half of fused_lut_linear_bwd (fused_lut_linear_cuda.py:152-170)
+ * and fused_lut_linear_bwd_grad_palette_kernel (fused_lut_kernel.cu:902-1123). */
+size_t plz_lut_linear_bwd_palette_workspace(int64_t M, int64_t N, int64_t K);
+int plz_lut_linear_bwd_palette(const uint16_t* x, const uint16_t* grad_y, const int32_t* packed,
+                               float* grad_palette, void* workspace, size_t workspace_bytes,
+                               int64_t M, int64_t N, int64_t K, void* stream);
+
+/* grad_bias fp32 [N] = sum_m grad_y[m, n]. Replaces fused_lut_linear_bwd_grad_bias_kernel
+ * (fused_lut_kernel.cu:1129-1147). Any N. */
+int plz_bias_grad(const uint16_t* grad_y, float* grad_bias, int64_t M, int64_t N, void* stream);
+
+/* ---- dense bf16 linear (soft path: W materialised by plz_soft_build_w) ---------------- */
+/* y = x w^T (+bias) (+lora); w bf16 [N, K]. Replaces the torch.matmul(x, W) of
+ * CUDAFusedLUTLinearSoft.forward (fused_lut_linear_cuda.py:912). K, N multiples of 8. */
+int plz_linear_fwd_dense(const uint16_t* x, const uint16_t* w, const uint16_t* bias,
+                         const uint16_t* lora_t, const uint16_t* lora_b, int rank, uint16_t* y,
+                         int64_t M, int64_t N, int64_t K, void* stream);
+/* grad_x = grad_y w (+lora). Replaces torch.matmul(grad_y, W.T)
+ * (fused_lut_linear_cuda.py:944). */
+int plz_linear_bwd_x_dense(const uint16_t* grad_y, const uint16_t* w, const uint16_t* lora_gt,
+                           const uint16_t* lora_a, int rank, uint16_t* grad_x, int64_t M,
+                           int64_t N, int64_t K, void* stream);
+
+/* ---- soft (Gumbel-softmax) path --------------------------------------------------- */
+/* noise fp32 [n] = -log(-log(u)), u from Philox4x32-10 (Salmon et al., SC'11) keyed by
+ * seed, counter = offset + element index / 4 (one 128-bit draw per 4 consecutive
+ * elements), u = (bits >> 8 + 0.5) * 2^-24. Replaces the in-kernel LCG sampler of
+ * fused_lut_kernel.cu:1245-1256 with a supplied-noise tensor. n % 4 == 0. */
+int plz_gumbel_philox(float* noise, int64_t n, uint64_t seed, uint64_t offset, void* stream);
+/* The reference's own sampler, bit-exact in its integer part: noise[n,k,c] =
+ * gumbel_sample(seed, (k*N + n)*4 + c) of fused_lut_kernel.cu:1245-1256 and
+ * triton_soft_forward.py:51-66, written in [N, K, 4] layout. */
+int plz_gumbel_lcg(float* noise, uint32_t seed, int64_t N, int64_t K, void* stream);
+
+/* Builds the forward weight of the soft path from logits [N, K, 4] (bf16 or fp16),
+ * noise fp32 [N, K, 4] and palette fp32 [N, K/256, 4]:
+ *   P_c = softmax_c((logit_c + noise_c) / tau)
+ *   w   bf16 [N, K]  per mode (PLZ_W_SOFT / PLZ_W_HARD_NOISY / PLZ_W_HARD_PLAIN)
+ *   w_soft bf16 [N, K] = sum_c P_c pal_c (optional, may be null)
+ * Replaces compute_P_W_hard_aos_kernel (fused_lut_kernel.cu:1946-2004) and
+ * compute_P_W_ste_kernel (triton_soft_forward.py:83-181). */
+int plz_soft_build_w(const uint16_t* logits, int logits_dtype, const float* noise,
+                     const float* palette, float tau, int mode, uint16_t* w, uint16_t* w_soft,
+                     int64_t N, int64_t K, void* stream);
+
+/* Soft backward, fused in the epilogue of dW = grad_y^T x (dW never leaves the chip):
+ *   grad_logits[n,k,c] = s * dW[n,k] P_c (pal_c - sum_d P_d pal_d)   (logits dtype)
+ *   grad_palette[n,g,c] = sum_{k in g} dW[n,k] P_c                   (fp32)
+ * with s = 1 (the reference, which omits 1/tau: fused_lut_kernel.cu:1914-1917,
+ * triton_soft_backward.py:276-279) or s = 1/tau when scale_grad_by_inv_tau != 0.
+ * Replaces soft_bwd_elementwise_aos_kernel (fused_lut_kernel.cu:1877-1924) together with
+ * the grad_W matmul before it (fused_lut_linear_cuda.py:952). */
+size_t plz_soft_bwd_workspace(int64_t M, int64_t N, int64_t K);
+int plz_soft_bwd(const uint16_t* x, const uint16_t* grad_y, const uint16_t* logits,
+                 int logits_dtype, const float* noise, const float* palette, float tau,
+                 int scale_grad_by_inv_tau, uint16_t* grad_logits, float* grad_palette,
+                 void* workspace, size_t workspace_bytes, int64_t M, int64_t N, int64_t K,
+                 void* stream);
+
+/* ---- LoRA (QwenLoRA, qwen_model.py:213-304): y += scale * (x A^T) B^T ------------------ */
+/* t[M,rank] = scale * x[M,K] lora_a[rank,K]^T  (bf16). rank in {8,16,24,32}. */
+int plz_lora_project(const uint16_t* x, const uint16_t* lora_a, float scale, uint16_t* t,
+                     int64_t M, int64_t K, int rank, void* stream);
+/* gt[M,rank] = scale * grad_y[M,N] lora_b[N,rank]  (bf16) */
+int plz_lora_grad_t(const uint16_t* grad_y, const uint16_t* lora_b, float scale, uint16_t* gt,
+                    int64_t M, int64_t N, int rank, void* stream);
+/* grad_b[N,rank] = scale * grad_y^T t  and  grad_a[rank,K] = gt^T x.
+ * With t from plz_lora_project (already scaled) and gt from plz_lora_grad_t, scale = 1
+ * gives the gradients of y += s (x A^T) B^T. out_dtype PLZ_DT_BF16 or PLZ_DT_FP32. */
+size_t plz_lora_weight_grads_workspace(int64_t M, int64_t N, int64_t K, int rank);
+int plz_lora_weight_grads(const uint16_t* x, const uint16_t* grad_y, const uint16_t* t,
+                          const uint16_t* gt, float scale, void* grad_a, void* grad_b,
+                          int out_dtype, void* workspace, size_t workspace_bytes, int64_t M,
+                          int64_t N, int64_t K, int rank, void* stream);
+
+/* ---- decode GEMV (M <= 16), no counterpart in the reference ---------------------------- */
+/* One palettized linear of a grouped launch. All pointers are device pointers. */
+typedef struct plz_gemv_desc {
+  const uint16_t* x;      /* [M, K] bf16 */
+  const int32_t* packed;  /* [N, K/16] */
+  const float* palette;   /* [N, K/256, 4] */
+  uint16_t* y;            /* [M, N] bf16 */
+  int64_t N, K;
+  int64_t block_begin;    /* filled by plz_gemv_plan: first row-block of this linear */
+} plz_gemv_desc;
+
+/* y[M,N] = x[M,K] W^T for 1 <= M <= 16 (bandwidth-bound; one pass over the packed weights).
+ * The reference would run fused_lut_linear_fwd_tc_kernel (fused_lut_kernel.cu:309-518) with
+ * a 64-row tile at M = 1. */
+int plz_lut_gemv(const uint16_t* x, const int32_t* packed, const float* palette, uint16_t* y,
+                 int64_t M, int64_t N, int64_t K, void* stream);
+/* Fills block_begin of n host descriptors and returns the total number of row blocks
+ * (or a negative status). */
+int64_t plz_gemv_plan(plz_gemv_desc* descs, int n, int M);
+/* Runs n independent GEMVs (all with the same M) in one launch. descs_device is a copy of
+ * the planned descriptors in device memory; total_blocks is plz_gemv_plan's result. */
+int plz_lut_gemv_grouped(const plz_gemv_desc* descs_device, int n, int64_t total_blocks, int M,
+                         void* stream);
+
+/* ---- fused RMSNorm and SwiGLU (HF Qwen3 RMSNorm / MLP) ----------------------------------- */
+/* y = bf16(weight * bf16(x * rsqrt(mean(x^2) + eps))) per row, fp32 statistics; rstd fp32
+ * [rows] saved for the backward. cols % 8 == 0. */
+int plz_rmsnorm_fwd(const uint16_t* x, const uint16_t* weight, uint16_t* y, float* rstd,
+                    int64_t rows, int64_t cols, float eps, void* stream);
+/* grad_x bf16 [rows, cols]; grad_weight fp32 [cols] (deterministic two-stage reduction). */
+size_t plz_rmsnorm_bwd_workspace(int64_t rows, int64_t cols);
+int plz_rmsnorm_bwd(const uint16_t* x, const uint16_t* weight, const float* rstd,
+                    const uint16_t* grad_y, uint16_t* grad_x, float* grad_weight,
+                    void* workspace, size_t workspace_bytes, int64_t rows, int64_t cols,
+                    void* stream);
+/* h = silu(gate) * up, elementwise over n elements (n % 8 == 0). */
+int plz_swiglu_fwd(const uint16_t* gate, const uint16_t* up, uint16_t* h, int64_t n,
+                   void* stream);
+int plz_swiglu_bwd(const uint16_t* gate, const uint16_t* up, const uint16_t* grad_h,
+                   uint16_t* grad_gate, uint16_t* grad_up, int64_t n, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PALETTIZE_HIP_H */

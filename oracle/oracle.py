@@ -1,0 +1,401 @@
+"""CPU oracle, numpy part -- TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import this module,
+and only as the checker; no product code path calls it. Each function restates the
+reference's algorithm (file:line cited) in plain numpy, in the native layout:
+  W[n, k] = bf16(palette[n, k // 256, idx[n, k]]), palette fp32 [N, K/256, 4],
+  logits / noise [N, K, 4].
+The C part (plz_oracle.c, loaded by ``clib()``) restates the bit-level pieces a second time.
+
+Pinning (what fixes each function independently of its own formula) is listed in
+tests/test_oracle.py; every function below has at least one such check.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+# --------------------------------------------------------------------------------------
+# bf16 / fp16 rounding
+# --------------------------------------------------------------------------------------
+
+
+def bf16_bits(x) -> np.ndarray:
+    """fp32 -> bf16 bit patterns (uint16), round to nearest even; NaN -> quiet NaN."""
+    u = np.asarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    nan = ((u & 0x7F800000) == 0x7F800000) & ((u & 0x007FFFFF) != 0)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) & 0xFFFF
+    r = np.where(nan, (u >> 16) | 0x40, r)
+    return r.astype(np.uint16)
+
+
+def bf16_to_f32(b) -> np.ndarray:
+    return (np.asarray(b, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def bf16_round(x) -> np.ndarray:
+    return bf16_to_f32(bf16_bits(x))
+
+
+# --------------------------------------------------------------------------------------
+# index packing (palettize_core.py:31-47, :159-172)
+# --------------------------------------------------------------------------------------
+
+
+def pack_idx2(flat) -> bytes:
+    """Reference .idx2 packing: 4 indices per byte, byte = a | b<<2 | c<<4 | d<<6
+    (palettize_core.py:31-42), with a zero-padded last byte."""
+    flat = np.asarray(flat, dtype=np.uint8).ravel() & 3
+    pad = (-flat.size) % 4
+    if pad:
+        flat = np.concatenate([flat, np.zeros(pad, np.uint8)])
+    q = flat.reshape(-1, 4)
+    return (q[:, 0] | (q[:, 1] << 2) | (q[:, 2] << 4) | (q[:, 3] << 6)).astype(np.uint8).tobytes()
+
+
+def unpack_idx2(data: bytes, n: int) -> np.ndarray:
+    """palettize_core.py:159-164."""
+    arr = np.frombuffer(data, dtype=np.uint8)
+    i = np.arange(n)
+    return ((arr[i // 4] >> ((i % 4) * 2)) & 3).astype(np.uint8)
+
+
+def pack_native(idx) -> np.ndarray:
+    """uint8 [rows, cols] -> int32 [rows, cols/16]: each row's .idx2 bytes read as
+    little-endian int32 words (16 indices per word, LSB first)."""
+    idx = np.asarray(idx, dtype=np.uint8)
+    rows, cols = idx.shape
+    assert cols % 16 == 0
+    out = np.empty((rows, cols // 16), dtype=np.int32)
+    for r in range(rows):
+        out[r] = np.frombuffer(pack_idx2(idx[r]), dtype="<i4")
+    return out
+
+
+def unpack_native(packed) -> np.ndarray:
+    packed = np.asarray(packed, dtype=np.int32)
+    rows, words = packed.shape
+    u = packed.view(np.uint32)[:, :, None]
+    shifts = (2 * np.arange(16, dtype=np.uint32))[None, None, :]
+    return ((u >> shifts) & 3).astype(np.uint8).reshape(rows, words * 16)
+
+
+# --------------------------------------------------------------------------------------
+# dequantisation (qwen_model.py:97-102, :185-186) and layout maps
+# --------------------------------------------------------------------------------------
+
+
+def dequant_bits(idx, palette) -> np.ndarray:
+    """idx uint8 [N, K], palette fp32 [N, K/256, 4] -> bf16 bits [N, K] via the flat gather
+    flat_palette[group_id * 4 + idx] with group_id = n * (K/256) + k // 256."""
+    idx = np.asarray(idx).astype(np.int64)
+    N, K = idx.shape
+    G = K // 256
+    group_id = np.arange(N)[:, None] * G + (np.arange(K) // 256)[None, :]
+    flat = np.asarray(palette, dtype=np.float32).reshape(-1)
+    return bf16_bits(flat[group_id * 4 + idx])
+
+
+def dequant(idx, palette) -> np.ndarray:
+    return bf16_to_f32(dequant_bits(idx, palette))
+
+
+def expand_reference_palette(pal_ref, N: int, K: int, group_size: int = 256) -> np.ndarray:
+    """Reference palette (G, 4) over output groups of `group_size` rows spanning all of K
+    (qwen_model.py:97-102) -> native [N, K/256, 4]."""
+    pal_ref = np.asarray(pal_ref, dtype=np.float32)
+    per_row = np.repeat(pal_ref, group_size, axis=0)[:N]
+    return np.ascontiguousarray(np.broadcast_to(per_row[:, None, :], (N, K // 256, 4)))
+
+
+def reference_weight(indices_kn, pal_ref, group_size: int = 256) -> np.ndarray:
+    """The reference's own gather, (K, N) layout: W[k, n] = palette[n // GS, idx[k, n]]
+    (qwen_model.py:97-102, 185-186), values rounded to bf16 as the bf16 palette is."""
+    indices_kn = np.asarray(indices_kn).astype(np.int64)
+    K, N = indices_kn.shape
+    flat_idx = (np.arange(N) // group_size)[None, :] * 4 + indices_kn
+    return bf16_round(np.asarray(pal_ref, np.float32).reshape(-1)[flat_idx])
+
+
+# --------------------------------------------------------------------------------------
+# hard linear: forward / backward (fused_lut_linear_cuda.py:755-818,
+# fused_lut_kernel.cu:309-518, 551-720, 902-1123, 1129-1147)
+# --------------------------------------------------------------------------------------
+
+
+def lut_linear_fwd(x, W, bias=None, t=None, lora_b=None) -> np.ndarray:
+    """fp64 y = x W^T (+ bias) (+ t lora_b^T)."""
+    y = np.asarray(x, np.float64) @ np.asarray(W, np.float64).T
+    if bias is not None:
+        y = y + np.asarray(bias, np.float64)[None, :]
+    if t is not None:
+        y = y + np.asarray(t, np.float64) @ np.asarray(lora_b, np.float64).T
+    return y
+
+
+def grad_x(gy, W) -> np.ndarray:
+    return np.asarray(gy, np.float64) @ np.asarray(W, np.float64)
+
+
+def grad_palette(x, gy, idx) -> np.ndarray:
+    """grad_pal[n, g, c] = sum_{k in group g, idx[n,k] = c} (gy^T x)[n, k]
+    (the class scatter of fused_lut_kernel.cu:1100-1120, in the native layout)."""
+    dW = np.asarray(gy, np.float64).T @ np.asarray(x, np.float64)  # [N, K]
+    idx = np.asarray(idx).astype(np.int64)
+    N, K = idx.shape
+    G = K // 256
+    gid = (np.arange(N)[:, None] * G + (np.arange(K) // 256)[None, :]) * 4 + idx
+    out = np.bincount(gid.ravel(), weights=dW.ravel(), minlength=N * G * 4)
+    return out.reshape(N, G, 4)
+
+
+def grad_bias(gy) -> np.ndarray:
+    return np.asarray(gy, np.float64).sum(axis=0)
+
+
+# --------------------------------------------------------------------------------------
+# Gumbel noise
+# --------------------------------------------------------------------------------------
+
+
+def lcg_bits(seed: int, idx) -> np.ndarray:
+    """Integer part of gumbel_sample (fused_lut_kernel.cu:1245-1253): 24-bit uniforms."""
+    x = np.uint32(seed) ^ (np.asarray(idx, np.uint32) * np.uint32(0x9E3779B9))
+    x = x ^ (x >> np.uint32(13))
+    x = x * np.uint32(1103515245) + np.uint32(12345)
+    x = x ^ (x >> np.uint32(17))
+    x = x * np.uint32(1103515245) + np.uint32(12345)
+    return x & np.uint32(0xFFFFFF)
+
+
+def lcg_gumbel(seed: int, N: int, K: int) -> np.ndarray:
+    """noise[n, k, c] = -log(-log(max(u, 1e-7))), u = bits / 2^24, idx = (k*N + n)*4 + c
+    (fused_lut_kernel.cu:1245-1256 with the indexing of :1974-1977), fp32 arithmetic."""
+    n = np.arange(N, dtype=np.uint32)[:, None, None]
+    k = np.arange(K, dtype=np.uint32)[None, :, None]
+    c = np.arange(4, dtype=np.uint32)[None, None, :]
+    with np.errstate(over="ignore"):
+        idx = (k * np.uint32(N) + n) * np.uint32(4) + c
+    u = lcg_bits(seed, idx).astype(np.float32) * np.float32(1.0 / 16777216.0)
+    u = np.maximum(u, np.float32(1e-7))
+    return (-np.log(-np.log(u))).astype(np.float32)
+
+
+_PHILOX_M = (np.uint64(0xD2511F53), np.uint64(0xCD9E8D57))
+_PHILOX_W = (np.uint32(0x9E3779B9), np.uint32(0xBB67AE85))
+
+
+def philox4x32_10(ctr, key) -> np.ndarray:
+    """Philox4x32-10 (Salmon et al., SC'11). ctr uint32 [n, 4], key uint32 [2]."""
+    c = np.asarray(ctr, dtype=np.uint32).reshape(-1, 4).copy()
+    k0, k1 = np.uint32(key[0]), np.uint32(key[1])
+    mask = np.uint64(0xFFFFFFFF)
+    for _ in range(10):
+        p0 = c[:, 0].astype(np.uint64) * _PHILOX_M[0]
+        p1 = c[:, 2].astype(np.uint64) * _PHILOX_M[1]
+        hi0, lo0 = (p0 >> np.uint64(32)).astype(np.uint32), (p0 & mask).astype(np.uint32)
+        hi1, lo1 = (p1 >> np.uint64(32)).astype(np.uint32), (p1 & mask).astype(np.uint32)
+        c = np.stack([hi1 ^ c[:, 1] ^ k0, lo1, hi0 ^ c[:, 3] ^ k1, lo0], axis=1)
+        with np.errstate(over="ignore"):
+            k0 = np.uint32(k0 + _PHILOX_W[0])
+            k1 = np.uint32(k1 + _PHILOX_W[1])
+    return c
+
+
+def gumbel_philox(n: int, seed: int, offset: int = 0) -> np.ndarray:
+    """Noise of plz_gumbel_philox: counter = offset + i/4, key = seed, u = (b>>8 + .5)/2^24."""
+    t = np.arange(n // 4, dtype=np.uint64) + np.uint64(offset)
+    ctr = np.zeros((n // 4, 4), np.uint32)
+    ctr[:, 0] = (t & np.uint64(0xFFFFFFFF)).astype(np.uint32)
+    ctr[:, 1] = (t >> np.uint64(32)).astype(np.uint32)
+    bits = philox4x32_10(ctr, (seed & 0xFFFFFFFF, (seed >> 32) & 0xFFFFFFFF)).reshape(-1)
+    u = ((bits >> np.uint32(8)).astype(np.float32) + np.float32(0.5)) * np.float32(1.0 / 16777216.0)
+    return (-np.log(-np.log(u))).astype(np.float32)
+
+
+# --------------------------------------------------------------------------------------
+# soft path (fused_lut_kernel.cu:1946-2004 forward, :1877-1924 backward;
+# triton_soft_forward.py:83-181; fused_lut_linear_cuda.py:880-970)
+# --------------------------------------------------------------------------------------
+
+W_SOFT, W_HARD_NOISY, W_HARD_PLAIN = 0, 1, 2
+
+
+def soft_probs(logits, noise, tau: float) -> np.ndarray:
+    """P = softmax_c((logit + noise) / tau) with max subtraction (fp64)."""
+    a = (np.asarray(logits, np.float64) + np.asarray(noise, np.float64)) / tau
+    a = a - a.max(axis=-1, keepdims=True)
+    e = np.exp(a)
+    return e / e.sum(axis=-1, keepdims=True)
+
+
+def _pal_per_weight(palette, K: int) -> np.ndarray:
+    return np.repeat(np.asarray(palette, np.float64), 256, axis=1)[:, :K, :]  # [N, K, 4]
+
+
+def soft_weights(logits, noise, palette, tau: float, mode: int = W_HARD_NOISY):
+    """Returns (P [N,K,4], W_soft [N,K], W_fwd [N,K]) in fp64 (W_fwd before bf16 rounding).
+    W_hard uses the first maximum: of P for W_HARD_NOISY (fused_lut_kernel.cu:1998-2003), of
+    the plain logits for W_HARD_PLAIN (triton_soft_forward.py:160-176)."""
+    logits = np.asarray(logits, np.float64)
+    N, K, _ = logits.shape
+    P = soft_probs(logits, noise, tau)
+    pw = _pal_per_weight(palette, K)
+    w_soft = (P * pw).sum(-1)
+    if mode == W_SOFT:
+        return P, w_soft, w_soft
+    src = P if mode == W_HARD_NOISY else logits
+    am = np.argmax(src, axis=-1)  # numpy argmax returns the first maximum
+    w_hard = np.take_along_axis(pw, am[..., None], axis=-1)[..., 0]
+    return P, w_soft, w_hard
+
+
+def soft_backward(x, gy, logits, noise, palette, tau: float, scale_by_inv_tau: bool = False):
+    """grad_logits[n,k,c] = s * dW P_c (pal_c - W_soft); grad_pal[n,g,c] = sum_{k in g} dW P_c
+    with dW = gy^T x and s = 1 (reference: soft_bwd_elementwise_aos_kernel,
+    fused_lut_kernel.cu:1914-1922) or 1/tau."""
+    dW = np.asarray(gy, np.float64).T @ np.asarray(x, np.float64)
+    P = soft_probs(logits, noise, tau)
+    N, K, _ = P.shape
+    pw = _pal_per_weight(palette, K)
+    w_soft = (P * pw).sum(-1, keepdims=True)
+    s = 1.0 / tau if scale_by_inv_tau else 1.0
+    g_logits = s * dW[..., None] * P * (pw - w_soft)
+    gp = (dW[..., None] * P).reshape(N, K // 256, 256, 4).sum(axis=2)
+    return g_logits, gp
+
+
+# --------------------------------------------------------------------------------------
+# LoRA (qwen_model.py:291-304), RMSNorm / SwiGLU (HF Qwen3, modeling_qwen3.py:50-83)
+# --------------------------------------------------------------------------------------
+
+
+def lora_forward(x, lora_a, lora_b, scale: float) -> np.ndarray:
+    """scale * (x A^T) B^T with A [r, K], B [N, r] (fp64)."""
+    return scale * (np.asarray(x, np.float64) @ np.asarray(lora_a, np.float64).T) @ np.asarray(
+        lora_b, np.float64).T
+
+
+def rmsnorm_fwd(x, weight, eps: float):
+    """y = bf16(w * bf16(x * rsqrt(mean(x^2) + eps))), statistics in fp32."""
+    xf = np.asarray(x, np.float32)
+    ms = (xf.astype(np.float64) ** 2).mean(axis=-1, keepdims=True)
+    r = (1.0 / np.sqrt(ms + eps)).astype(np.float32)
+    h = bf16_round(xf * r)
+    return bf16_round(np.asarray(weight, np.float32) * h), r[..., 0]
+
+
+def rmsnorm_bwd(x, weight, gy, eps: float):
+    x = np.asarray(x, np.float64)
+    w = np.asarray(weight, np.float64)
+    gy = np.asarray(gy, np.float64)
+    r = 1.0 / np.sqrt((x ** 2).mean(axis=-1, keepdims=True) + eps)
+    h = x * r
+    g = gy * w
+    gx = r * (g - h * (g * h).mean(axis=-1, keepdims=True))
+    gw = (gy * bf16_round(h.astype(np.float32))).sum(axis=0)
+    return gx, gw
+
+
+def silu(g):
+    g = np.asarray(g, np.float64)
+    return g / (1.0 + np.exp(-g))
+
+
+def swiglu_fwd(gate, up) -> np.ndarray:
+    """bf16(bf16(silu(gate)) * up)."""
+    return bf16_round(bf16_round(silu(gate).astype(np.float32)) * np.asarray(up, np.float32))
+
+
+def swiglu_bwd(gate, up, gh):
+    g = np.asarray(gate, np.float64)
+    u = np.asarray(up, np.float64)
+    d = np.asarray(gh, np.float64)
+    sg = 1.0 / (1.0 + np.exp(-g))
+    return d * u * sg * (1.0 + g * (1.0 - sg)), d * g * sg
+
+
+# --------------------------------------------------------------------------------------
+# C part
+# --------------------------------------------------------------------------------------
+_clib = None
+
+
+def clib():
+    """ctypes handle of liboracle.so (built by oracle/Makefile)."""
+    global _clib
+    if _clib is None:
+        path = os.path.join(HERE, "liboracle.so")
+        if not os.path.exists(path):
+            raise RuntimeError(f"{path} missing: run `make -C oracle`")
+        L = C.CDLL(path)
+        P = C.c_void_p
+        L.orc_f2bf.restype = C.c_uint16
+        L.orc_f2bf.argtypes = [C.c_float]
+        L.orc_pack.argtypes = [P, P, C.c_int64]
+        L.orc_unpack.argtypes = [P, P, C.c_int64]
+        L.orc_dequant.argtypes = [P, P, P, C.c_int64, C.c_int64]
+        L.orc_lcg_bits.argtypes = [P, C.c_uint32, P, C.c_int64]
+        L.orc_gumbel_lcg.argtypes = [P, C.c_uint32, C.c_int64, C.c_int64]
+        L.orc_philox.argtypes = [P, P, P]
+        L.orc_gumbel_philox.argtypes = [P, C.c_int64, C.c_uint64, C.c_uint64]
+        _clib = L
+    return _clib
+
+
+def _p(a: np.ndarray):
+    return a.ctypes.data_as(C.c_void_p)
+
+
+def c_pack(idx) -> np.ndarray:
+    idx = np.ascontiguousarray(idx, dtype=np.uint8)
+    out = np.empty((idx.shape[0], idx.shape[1] // 16), np.int32)
+    clib().orc_pack(_p(idx), _p(out), out.size)
+    return out
+
+
+def c_unpack(packed) -> np.ndarray:
+    packed = np.ascontiguousarray(packed, dtype=np.int32)
+    out = np.empty((packed.shape[0], packed.shape[1] * 16), np.uint8)
+    clib().orc_unpack(_p(packed), _p(out), packed.size)
+    return out
+
+
+def c_dequant_bits(packed, palette) -> np.ndarray:
+    packed = np.ascontiguousarray(packed, dtype=np.int32)
+    palette = np.ascontiguousarray(palette, dtype=np.float32)
+    N, K = packed.shape[0], packed.shape[1] * 16
+    out = np.empty((N, K), np.uint16)
+    clib().orc_dequant(_p(packed), _p(palette), _p(out), N, K)
+    return out
+
+
+def c_lcg_bits(seed: int, idx) -> np.ndarray:
+    idx = np.ascontiguousarray(idx, dtype=np.uint32)
+    out = np.empty_like(idx)
+    clib().orc_lcg_bits(_p(out), seed & 0xFFFFFFFF, _p(idx), idx.size)
+    return out
+
+
+def c_gumbel_lcg(seed: int, N: int, K: int) -> np.ndarray:
+    out = np.empty((N, K, 4), np.float32)
+    clib().orc_gumbel_lcg(_p(out), seed & 0xFFFFFFFF, N, K)
+    return out
+
+
+def c_philox(ctr, key) -> np.ndarray:
+    c = np.ascontiguousarray(ctr, dtype=np.uint32)
+    k = np.ascontiguousarray(key, dtype=np.uint32)
+    out = np.empty(4, np.uint32)
+    clib().orc_philox(_p(c), _p(k), _p(out))
+    return out
+
+
+def c_gumbel_philox(n: int, seed: int, offset: int = 0) -> np.ndarray:
+    out = np.empty(n, np.float32)
+    clib().orc_gumbel_philox(_p(out), n, seed, offset)
+    return out

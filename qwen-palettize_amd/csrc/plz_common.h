@@ -1,0 +1,125 @@
+// Shared device/host helpers for the palettize HIP library (gfx950 / CDNA4 only).
+//
+// Conventions used by every kernel in this library:
+//   * bf16 values travel as raw uint16_t bit patterns; conversion fp32->bf16 is
+//     round-to-nearest-even (the rounding torch's .to(torch.bfloat16) uses).
+//   * A palettized weight W[N,K] is stored as 2-bit indices packed 16 per int32
+//     along K, LSB first (index k of a 16-run sits at bits 2*(k%16)), which has the
+//     same bytes as the reference's .idx2 packing on little-endian hosts
+//     (palettize_core.py:31-42), plus fp32 palettes [N, K/256, 4]: one 4-entry
+//     palette per output row and per 256-wide chunk of K.
+//   * W[n,k] = bf16(palette[n, k/256, idx[n,k]]) -- the flat gather of
+//     qwen_model.py:97-102,185-186 with group_id = n*(K/256) + k/256.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+#include "palettize_hip.h"
+
+namespace plz {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kPalGroup = 256;   // K-extent of one palette group
+constexpr int kIdxPerWord = 16;  // 2-bit indices per int32
+
+// fp32 -> bf16 bits, round to nearest even; NaN stays a quiet NaN.
+__host__ __device__ __forceinline__ uint32_t f2bf(float f) {
+  uint32_t u = __builtin_bit_cast(uint32_t, f);
+  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (u >> 16) | 0x40u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+__host__ __device__ __forceinline__ float bf2f(uint32_t b) {
+  return __builtin_bit_cast(float, (uint32_t)(b << 16));
+}
+// fp32 -> fp16 bits (round to nearest even) through the hardware conversion.
+__device__ __forceinline__ uint32_t f2h(float f) {
+  _Float16 h = (_Float16)f;
+  return (uint32_t)__builtin_bit_cast(uint16_t, h);
+}
+__device__ __forceinline__ float h2f(uint32_t b) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)b);
+}
+
+// Byte permute: result byte i = byte sel.byte[i] of the 8-byte value {hi:lo}.
+__device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) {
+  return __builtin_amdgcn_perm(hi, lo, sel);
+}
+
+// A 4-entry palette prepared for byte-permute lookup: `lo` holds the low bytes of
+// the four bf16 entries, `hi` their high bytes (entry c in byte c).
+struct PalLut {
+  uint32_t lo, hi;
+};
+__device__ __forceinline__ PalLut make_lut(float p0, float p1, float p2, float p3) {
+  uint32_t b01 = f2bf(p0) | (f2bf(p1) << 16);
+  uint32_t b23 = f2bf(p2) | (f2bf(p3) << 16);
+  PalLut t;
+  t.lo = perm(b23, b01, 0x06040200u);
+  t.hi = perm(b23, b01, 0x07050301u);
+  return t;
+}
+
+// Dequantise one packed word (16 indices, natural k order) into 8 dwords of bf16
+// pairs: out[j] = {w[2j] (low half), w[2j+1] (high half)}.
+__device__ __forceinline__ void dequant16(uint32_t q, PalLut t, uint32_t out[8]) {
+  uint32_t u0 = q & 0x03030303u;          // idx 0,4,8,12
+  uint32_t u1 = (q >> 2) & 0x03030303u;   // idx 1,5,9,13
+  uint32_t u2 = (q >> 4) & 0x03030303u;   // idx 2,6,10,14
+  uint32_t u3 = (q >> 6) & 0x03030303u;   // idx 3,7,11,15
+  uint32_t l0 = perm(0, t.lo, u0), h0 = perm(0, t.hi, u0);
+  uint32_t l1 = perm(0, t.lo, u1), h1 = perm(0, t.hi, u1);
+  uint32_t l2 = perm(0, t.lo, u2), h2 = perm(0, t.hi, u2);
+  uint32_t l3 = perm(0, t.lo, u3), h3 = perm(0, t.hi, u3);
+  // {w_j, w_j+4} and {w_j+8, w_j+12}
+  uint32_t a0 = perm(h0, l0, 0x05010400u), b0 = perm(h0, l0, 0x07030602u);
+  uint32_t a1 = perm(h1, l1, 0x05010400u), b1 = perm(h1, l1, 0x07030602u);
+  uint32_t a2 = perm(h2, l2, 0x05010400u), b2 = perm(h2, l2, 0x07030602u);
+  uint32_t a3 = perm(h3, l3, 0x05010400u), b3 = perm(h3, l3, 0x07030602u);
+  out[0] = perm(a1, a0, 0x05040100u);  // w0 w1
+  out[1] = perm(a3, a2, 0x05040100u);  // w2 w3
+  out[2] = perm(a1, a0, 0x07060302u);  // w4 w5
+  out[3] = perm(a3, a2, 0x07060302u);  // w6 w7
+  out[4] = perm(b1, b0, 0x05040100u);  // w8 w9
+  out[5] = perm(b3, b2, 0x05040100u);  // w10 w11
+  out[6] = perm(b1, b0, 0x07060302u);  // w12 w13
+  out[7] = perm(b3, b2, 0x07060302u);  // w14 w15
+}
+
+// Dequantise the same 16 k positions of two rows (n, n+1) into 16 dwords
+// out[k] = {w[n][k] (low half), w[n+1][k] (high half)}: the layout a tile whose
+// reduction dimension is n wants.
+__device__ __forceinline__ void dequant16_pair(uint32_t qa, PalLut ta, uint32_t qb, PalLut tb,
+                                               uint32_t out[16]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    uint32_t ua = (qa >> (2 * j)) & 0x03030303u;  // row n:   idx j, j+4, j+8, j+12
+    uint32_t ub = (qb >> (2 * j)) & 0x03030303u;  // row n+1
+    uint32_t la = perm(0, ta.lo, ua), ha = perm(0, ta.hi, ua);
+    uint32_t lb = perm(0, tb.lo, ub), hb = perm(0, tb.hi, ub);
+    uint32_t ll0 = perm(lb, la, 0x05010400u), hh0 = perm(hb, ha, 0x05010400u);  // k=j, j+4
+    uint32_t ll1 = perm(lb, la, 0x07030602u), hh1 = perm(hb, ha, 0x07030602u);  // k=j+8, j+12
+    out[j] = perm(hh0, ll0, 0x05010400u);
+    out[j + 4] = perm(hh0, ll0, 0x07030602u);
+    out[j + 8] = perm(hh1, ll1, 0x05010400u);
+    out[j + 12] = perm(hh1, ll1, 0x07030602u);
+  }
+}
+
+// ---- error reporting shared by every entry point -------------------------------
+void set_error(const char* fmt, ...);
+int check_launch(const char* what);
+
+}  // namespace plz
+
+#define PLZ_REQUIRE(cond, ...)        \
+  do {                                \
+    if (!(cond)) {                    \
+      plz::set_error(__VA_ARGS__);    \
+      return PLZ_EINVAL;              \
+    }                                 \
+  } while (0)

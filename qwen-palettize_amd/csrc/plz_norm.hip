@@ -1,0 +1,305 @@
+// Fused RMSNorm and SwiGLU of the Qwen3 decoder layer, plus the bias-gradient reduction.
+//
+// RMSNorm follows HF Qwen3RMSNorm (transformers models/qwen3/modeling_qwen3.py:50-64):
+//   h = x.float() * rsqrt(mean(x.float()^2) + eps);  y = weight * h.to(bf16)
+// where the final product is a bf16 x bf16 multiply (fp32 compute, one rounding).
+// SwiGLU follows Qwen3MLP (modeling_qwen3.py:70-83): h = act(gate) * up with act = silu on
+// bf16 tensors: silu rounded to bf16, then the bf16 product rounded again.
+// There is no counterpart kernel in the reference (it calls the HF modules).
+#include "plz_common.h"
+
+namespace plz {
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
+  return v;
+}
+
+__device__ __forceinline__ void unpack8(uint4 v, float f[8]) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = bf2f(w[i] & 0xffffu);
+    f[2 * i + 1] = bf2f(w[i] >> 16);
+  }
+}
+__device__ __forceinline__ uint4 pack8(const float f[8]) {
+  uint32_t w[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) w[i] = f2bf(f[2 * i]) | (f2bf(f[2 * i + 1]) << 16);
+  return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+constexpr int kNormMaxChunks = 8;  // cols <= 8 * 512 = 4096
+
+// One wave per row; lane handles 8-column chunks c = lane + 64*i.
+__global__ __launch_bounds__(256) void rmsnorm_fwd_kernel(const uint16_t* __restrict__ x,
+                                                          const uint16_t* __restrict__ wt,
+                                                          uint16_t* __restrict__ y,
+                                                          float* __restrict__ rstd, int64_t rows,
+                                                          int64_t cols, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int nch = (int)(cols / 8);
+  const uint4* xr = reinterpret_cast<const uint4*>(x + row * cols);
+  uint4 xv[kNormMaxChunks];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < kNormMaxChunks; ++i) {
+    const int c = lane + 64 * i;
+    xv[i] = make_uint4(0, 0, 0, 0);
+    if (c < nch) {
+      xv[i] = xr[c];
+      float f[8];
+      unpack8(xv[i], f);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) ss += f[j] * f[j];
+    }
+  }
+  ss = wave_sum(ss);
+  const float r = rsqrtf(ss / (float)cols + eps);
+  if (lane == 0 && rstd) rstd[row] = r;
+  uint4* yr = reinterpret_cast<uint4*>(y + row * cols);
+  const uint4* wr = reinterpret_cast<const uint4*>(wt);
+#pragma unroll
+  for (int i = 0; i < kNormMaxChunks; ++i) {
+    const int c = lane + 64 * i;
+    if (c < nch) {
+      float f[8], w[8], o[8];
+      unpack8(xv[i], f);
+      unpack8(wr[c], w);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) o[j] = w[j] * bf2f(f2bf(f[j] * r));
+      yr[c] = pack8(o);
+    }
+  }
+}
+
+// Backward. With h = x r, g = grad_y * w (fp32):
+//   grad_x = r * (g - h * mean(g * h)),  grad_w = sum_rows grad_y * bf16(h)
+// Each workgroup takes a strided set of rows; per-lane column partials of grad_w are
+// summed over its 4 waves in LDS and written to partial[block][cols]; a second kernel adds
+// the blocks in a fixed order.
+__global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ wt, const float* __restrict__ rstd,
+    const uint16_t* __restrict__ gy, uint16_t* __restrict__ gx, float* __restrict__ partial,
+    int64_t rows, int64_t cols) {
+  __shared__ float red[4][kNormMaxChunks][64][8];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nch = (int)(cols / 8);
+  const uint4* wr = reinterpret_cast<const uint4*>(wt);
+  float gw[kNormMaxChunks][8];
+#pragma unroll
+  for (int i = 0; i < kNormMaxChunks; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) gw[i][j] = 0.f;
+  for (int64_t row = (int64_t)blockIdx.x * 4 + wave; row < rows; row += (int64_t)gridDim.x * 4) {
+    const float r = rstd[row];
+    const uint4* xr = reinterpret_cast<const uint4*>(x + row * cols);
+    const uint4* gr = reinterpret_cast<const uint4*>(gy + row * cols);
+    uint4 xv[kNormMaxChunks], gv[kNormMaxChunks];
+    float dot = 0.f;
+#pragma unroll
+    for (int i = 0; i < kNormMaxChunks; ++i) {
+      const int c = lane + 64 * i;
+      xv[i] = make_uint4(0, 0, 0, 0);
+      gv[i] = xv[i];
+      if (c < nch) {
+        xv[i] = xr[c];
+        gv[i] = gr[c];
+        float f[8], g[8], w[8];
+        unpack8(xv[i], f);
+        unpack8(gv[i], g);
+        unpack8(wr[c], w);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float h = f[j] * r;
+          dot += g[j] * w[j] * h;
+          gw[i][j] += g[j] * bf2f(f2bf(h));
+        }
+      }
+    }
+    dot = wave_sum(dot) / (float)cols;
+    uint4* outr = reinterpret_cast<uint4*>(gx + row * cols);
+#pragma unroll
+    for (int i = 0; i < kNormMaxChunks; ++i) {
+      const int c = lane + 64 * i;
+      if (c < nch) {
+        float f[8], g[8], w[8], o[8];
+        unpack8(xv[i], f);
+        unpack8(gv[i], g);
+        unpack8(wr[c], w);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o[j] = r * (g[j] * w[j] - f[j] * r * dot);
+        outr[c] = pack8(o);
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kNormMaxChunks; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) red[wave][i][lane][j] = gw[i][j];
+  __syncthreads();
+  // thread t sums column chunk (i = t / 64 ... ) over the 4 waves
+  for (int idx = threadIdx.x; idx < nch * 8; idx += 256) {
+    const int c = idx / 8, j = idx % 8;
+    const int i = c / 64, l = c % 64;
+    const float s = red[0][i][l][j] + red[1][i][l][j] + red[2][i][l][j] + red[3][i][l][j];
+    partial[(int64_t)blockIdx.x * cols + idx] = s;
+  }
+}
+
+__global__ void sum_blocks_kernel(const float* __restrict__ partial, float* __restrict__ out,
+                                  int blocks, int64_t cols) {
+  const int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= cols) return;
+  float s = 0.f;
+  for (int b = 0; b < blocks; ++b) s += partial[(int64_t)b * cols + c];
+  out[c] = s;
+}
+
+__device__ __forceinline__ float silu(float g) { return g / (1.f + __expf(-g)); }
+
+__global__ void swiglu_fwd_kernel(const uint16_t* __restrict__ gate, const uint16_t* __restrict__ up,
+                                  uint16_t* __restrict__ h, int64_t n8) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= n8) return;
+  float g[8], u[8], o[8];
+  unpack8(reinterpret_cast<const uint4*>(gate)[t], g);
+  unpack8(reinterpret_cast<const uint4*>(up)[t], u);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) o[j] = bf2f(f2bf(silu(g[j]))) * u[j];
+  reinterpret_cast<uint4*>(h)[t] = pack8(o);
+}
+
+__global__ void swiglu_bwd_kernel(const uint16_t* __restrict__ gate, const uint16_t* __restrict__ up,
+                                  const uint16_t* __restrict__ gh, uint16_t* __restrict__ gg,
+                                  uint16_t* __restrict__ gu, int64_t n8) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= n8) return;
+  float g[8], u[8], d[8], og[8], ou[8];
+  unpack8(reinterpret_cast<const uint4*>(gate)[t], g);
+  unpack8(reinterpret_cast<const uint4*>(up)[t], u);
+  unpack8(reinterpret_cast<const uint4*>(gh)[t], d);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float sg = 1.f / (1.f + __expf(-g[j]));
+    const float s = g[j] * sg;
+    ou[j] = d[j] * s;
+    og[j] = d[j] * u[j] * sg * (1.f + g[j] * (1.f - sg));
+  }
+  reinterpret_cast<uint4*>(gg)[t] = pack8(og);
+  reinterpret_cast<uint4*>(gu)[t] = pack8(ou);
+}
+
+// grad_bias[n] = sum_m grad_y[m, n]: one thread per column, rows in order.
+__global__ void bias_grad_kernel(const uint16_t* __restrict__ gy, float* __restrict__ gb,
+                                 int64_t M, int64_t N) {
+  const int64_t n = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (n >= N) return;
+  float s = 0.f;
+  for (int64_t m = 0; m < M; ++m) s += bf2f(gy[m * N + n]);
+  gb[n] = s;
+}
+
+static int rmsnorm_blocks(int64_t rows) {
+  int64_t b = (rows + 3) / 4;
+  return (int)(b < 1024 ? b : 1024);
+}
+
+static bool a16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+}  // namespace plz
+
+using namespace plz;
+
+extern "C" {
+
+int plz_rmsnorm_fwd(const uint16_t* x, const uint16_t* weight, uint16_t* y, float* rstd,
+                    int64_t rows, int64_t cols, float eps, void* stream) {
+  PLZ_REQUIRE(rows >= 0 && cols > 0 && cols % 8 == 0 && cols <= 64 * 8 * kNormMaxChunks,
+              "plz_rmsnorm_fwd: cols (%lld) must be a positive multiple of 8 up to 4096",
+              (long long)cols);
+  if (rows == 0) return PLZ_OK;
+  PLZ_REQUIRE(x && weight && y && a16(x) && a16(weight) && a16(y),
+              "plz_rmsnorm_fwd: x, weight, y must be non-null and 16-byte aligned");
+  hipLaunchKernelGGL(rmsnorm_fwd_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0,
+                     (hipStream_t)stream, x, weight, y, rstd, rows, cols, eps);
+  return check_launch("plz_rmsnorm_fwd");
+}
+
+size_t plz_rmsnorm_bwd_workspace(int64_t rows, int64_t cols) {
+  if (rows <= 0 || cols <= 0) return 0;
+  return (size_t)rmsnorm_blocks(rows) * cols * sizeof(float);
+}
+
+int plz_rmsnorm_bwd(const uint16_t* x, const uint16_t* weight, const float* rstd,
+                    const uint16_t* grad_y, uint16_t* grad_x, float* grad_weight,
+                    void* workspace, size_t workspace_bytes, int64_t rows, int64_t cols,
+                    void* stream) {
+  PLZ_REQUIRE(rows >= 0 && cols > 0 && cols % 8 == 0 && cols <= 64 * 8 * kNormMaxChunks,
+              "plz_rmsnorm_bwd: cols (%lld) must be a positive multiple of 8 up to 4096",
+              (long long)cols);
+  PLZ_REQUIRE(grad_weight, "plz_rmsnorm_bwd: null grad_weight");
+  if (rows == 0) {
+    hipMemsetAsync(grad_weight, 0, (size_t)cols * 4, (hipStream_t)stream);
+    return check_launch("plz_rmsnorm_bwd");
+  }
+  PLZ_REQUIRE(x && weight && rstd && grad_y && grad_x && a16(x) && a16(weight) && a16(grad_y) &&
+                  a16(grad_x),
+              "plz_rmsnorm_bwd: operands must be non-null and 16-byte aligned");
+  const size_t need = plz_rmsnorm_bwd_workspace(rows, cols);
+  if (!workspace || workspace_bytes < need) {
+    set_error("plz_rmsnorm_bwd: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+    return PLZ_EWORKSPACE;
+  }
+  const int blocks = rmsnorm_blocks(rows);
+  float* part = reinterpret_cast<float*>(workspace);
+  hipLaunchKernelGGL(rmsnorm_bwd_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream, x,
+                     weight, rstd, grad_y, grad_x, part, rows, cols);
+  int rc = check_launch("plz_rmsnorm_bwd");
+  if (rc) return rc;
+  hipLaunchKernelGGL(sum_blocks_kernel, dim3((unsigned)((cols + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, part, grad_weight, blocks, cols);
+  return check_launch("plz_rmsnorm_bwd/reduce");
+}
+
+int plz_swiglu_fwd(const uint16_t* gate, const uint16_t* up, uint16_t* h, int64_t n,
+                   void* stream) {
+  PLZ_REQUIRE(n >= 0 && n % 8 == 0, "plz_swiglu_fwd: n (%lld) must be a multiple of 8",
+              (long long)n);
+  if (n == 0) return PLZ_OK;
+  PLZ_REQUIRE(gate && up && h && a16(gate) && a16(up) && a16(h),
+              "plz_swiglu_fwd: operands must be non-null and 16-byte aligned");
+  const int64_t n8 = n / 8;
+  hipLaunchKernelGGL(swiglu_fwd_kernel, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, gate, up, h, n8);
+  return check_launch("plz_swiglu_fwd");
+}
+
+int plz_swiglu_bwd(const uint16_t* gate, const uint16_t* up, const uint16_t* grad_h,
+                   uint16_t* grad_gate, uint16_t* grad_up, int64_t n, void* stream) {
+  PLZ_REQUIRE(n >= 0 && n % 8 == 0, "plz_swiglu_bwd: n (%lld) must be a multiple of 8",
+              (long long)n);
+  if (n == 0) return PLZ_OK;
+  PLZ_REQUIRE(gate && up && grad_h && grad_gate && grad_up && a16(gate) && a16(up) &&
+                  a16(grad_h) && a16(grad_gate) && a16(grad_up),
+              "plz_swiglu_bwd: operands must be non-null and 16-byte aligned");
+  const int64_t n8 = n / 8;
+  hipLaunchKernelGGL(swiglu_bwd_kernel, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, gate, up, grad_h, grad_gate, grad_up, n8);
+  return check_launch("plz_swiglu_bwd");
+}
+
+int plz_bias_grad(const uint16_t* grad_y, float* grad_bias, int64_t M, int64_t N, void* stream) {
+  PLZ_REQUIRE(M >= 0 && N >= 0, "plz_bias_grad: negative shape");
+  if (N == 0) return PLZ_OK;
+  PLZ_REQUIRE(grad_bias && (M == 0 || grad_y), "plz_bias_grad: null pointer");
+  hipLaunchKernelGGL(bias_grad_kernel, dim3((unsigned)((N + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, grad_y, grad_bias, M, N);
+  return check_launch("plz_bias_grad");
+}
+
+}  // extern "C"

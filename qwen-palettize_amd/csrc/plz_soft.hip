@@ -1,0 +1,179 @@
+// Soft (Gumbel-softmax) forward: noise generation and the build-W kernel.
+//
+//   P_c = softmax_c((logit_c + noise_c) / tau)           fused_lut_kernel.cu:1974-1983
+//   W_soft = sum_c P_c pal_c                              fused_lut_kernel.cu:1995
+//   W_hard = pal[argmax_c P_c]   (first max wins)         fused_lut_kernel.cu:1998-2003
+//   W_hard = pal[argmax_c logit_c] (first max wins)       triton_soft_forward.py:160-176
+// The forward weight W = W_hard is the straight-through estimator's value
+// (fused_lut_linear_cuda.py:906-910); W_soft is what the backward differentiates.
+#include "plz_common.h"
+
+namespace plz {
+
+// ---- Philox4x32-10 (Salmon, Moraes, Dror, Shaw, SC'11) ---------------------------------
+struct U4 {
+  uint32_t x, y, z, w;
+};
+__host__ __device__ __forceinline__ U4 philox4x32_10(U4 c, uint32_t k0, uint32_t k1) {
+  const uint32_t M0 = 0xD2511F53u, M1 = 0xCD9E8D57u, W0 = 0x9E3779B9u, W1 = 0xBB67AE85u;
+#pragma unroll
+  for (int i = 0; i < 10; ++i) {
+    const uint64_t p0 = (uint64_t)M0 * c.x, p1 = (uint64_t)M1 * c.z;
+    const uint32_t hi0 = (uint32_t)(p0 >> 32), lo0 = (uint32_t)p0;
+    const uint32_t hi1 = (uint32_t)(p1 >> 32), lo1 = (uint32_t)p1;
+    c = U4{hi1 ^ c.y ^ k0, lo1, hi0 ^ c.w ^ k1, lo0};
+    k0 += W0;
+    k1 += W1;
+  }
+  return c;
+}
+
+__device__ __forceinline__ float gumbel_from_bits(uint32_t b) {
+  const float u = ((float)(b >> 8) + 0.5f) * (1.0f / 16777216.0f);  // (0, 1)
+  return -logf(-logf(u));
+}
+
+__global__ void philox_gumbel_kernel(float* __restrict__ out, int64_t n4, uint64_t seed,
+                                     uint64_t offset) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= n4) return;
+  const uint64_t ctr = offset + (uint64_t)t;
+  const U4 r = philox4x32_10(U4{(uint32_t)ctr, (uint32_t)(ctr >> 32), 0u, 0u}, (uint32_t)seed,
+                             (uint32_t)(seed >> 32));
+  *reinterpret_cast<float4*>(out + 4 * t) =
+      make_float4(gumbel_from_bits(r.x), gumbel_from_bits(r.y), gumbel_from_bits(r.z),
+                  gumbel_from_bits(r.w));
+}
+
+// The reference's LCG hash sampler (fused_lut_kernel.cu:1245-1256), element (n, k, c) drawn
+// with idx = (k*N + n)*4 + c in uint32 arithmetic, stored at [n, k, c].
+__device__ __forceinline__ float lcg_gumbel(uint32_t seed, uint32_t idx) {
+  uint32_t x = seed ^ (idx * 0x9E3779B9u);
+  x ^= x >> 13;
+  x = x * 1103515245u + 12345u;
+  x ^= x >> 17;
+  x = x * 1103515245u + 12345u;
+  float u = (float)(x & 0xFFFFFFu) * (1.0f / 16777216.0f);
+  u = fmaxf(u, 1e-7f);
+  return -logf(-logf(u));
+}
+
+__global__ void lcg_gumbel_kernel(float* __restrict__ out, uint32_t seed, int64_t N, int64_t K) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // element (n, k)
+  if (t >= N * K) return;
+  const int64_t n = t / K, k = t % K;
+  const uint32_t base = ((uint32_t)k * (uint32_t)N + (uint32_t)n) * 4u;
+  *reinterpret_cast<float4*>(out + 4 * t) =
+      make_float4(lcg_gumbel(seed, base), lcg_gumbel(seed, base + 1), lcg_gumbel(seed, base + 2),
+                  lcg_gumbel(seed, base + 3));
+}
+
+// ---- build W -------------------------------------------------------------------------
+// One thread per 2 consecutive k of one row: 16 B of logits, 32 B of noise in; 4 B out.
+__global__ void build_w_kernel(const uint16_t* __restrict__ logits, int f16,
+                               const float* __restrict__ noise, const float* __restrict__ pal,
+                               float inv_tau, int mode, uint16_t* __restrict__ w,
+                               uint16_t* __restrict__ w_soft, int64_t N, int64_t K) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t half = K / 2;
+  if (t >= N * half) return;
+  const int64_t n = t / half, k = 2 * (t % half);
+  const float4 p = *reinterpret_cast<const float4*>(pal + (n * (K / kPalGroup) + k / kPalGroup) * 4);
+  const float pc[4] = {p.x, p.y, p.z, p.w};
+  const int64_t e0 = (n * K + k) * 4;
+  const uint4 lg = *reinterpret_cast<const uint4*>(logits + e0);
+  const float4 z0 = *reinterpret_cast<const float4*>(noise + e0);
+  const float4 z1 = *reinterpret_cast<const float4*>(noise + e0 + 4);
+  const uint32_t lw[4] = {lg.x, lg.y, lg.z, lg.w};
+  const float nz[8] = {z0.x, z0.y, z0.z, z0.w, z1.x, z1.y, z1.z, z1.w};
+  uint32_t wo[2], so[2];
+#pragma unroll
+  for (int el = 0; el < 2; ++el) {
+    float l[4], a[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const uint32_t bits = (lw[2 * el + c / 2] >> (16 * (c & 1))) & 0xffffu;
+      l[c] = f16 ? h2f(bits) : bf2f(bits);
+      a[c] = (l[c] + nz[4 * el + c]) * inv_tau;
+    }
+    const float m = fmaxf(fmaxf(a[0], a[1]), fmaxf(a[2], a[3]));
+    float e[4], s = 0.f;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      e[c] = __expf(a[c] - m);
+      s += e[c];
+    }
+    float P[4], ws = 0.f;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      P[c] = e[c] / s;
+      ws += P[c] * pc[c];
+    }
+    // argmax, first maximum wins (strict >), over P (noisy) or over the plain logits
+    const float* v = mode == PLZ_W_HARD_PLAIN ? l : P;
+    int am = 0;
+    float best = v[0];
+#pragma unroll
+    for (int c = 1; c < 4; ++c)
+      if (v[c] > best) { best = v[c]; am = c; }
+    const float wh = am == 0 ? pc[0] : am == 1 ? pc[1] : am == 2 ? pc[2] : pc[3];
+    wo[el] = f2bf(mode == PLZ_W_SOFT ? ws : wh);
+    so[el] = f2bf(ws);
+  }
+  const int64_t o = n * K + k;
+  *reinterpret_cast<uint32_t*>(w + o) = wo[0] | (wo[1] << 16);
+  if (w_soft) *reinterpret_cast<uint32_t*>(w_soft + o) = so[0] | (so[1] << 16);
+}
+
+}  // namespace plz
+
+using namespace plz;
+
+extern "C" {
+
+int plz_gumbel_philox(float* noise, int64_t n, uint64_t seed, uint64_t offset, void* stream) {
+  PLZ_REQUIRE(n >= 0 && n % 4 == 0, "plz_gumbel_philox: n (%lld) must be a multiple of 4",
+              (long long)n);
+  if (n == 0) return PLZ_OK;
+  PLZ_REQUIRE(noise && ((uintptr_t)noise & 15) == 0,
+              "plz_gumbel_philox: noise must be non-null and 16-byte aligned");
+  const int64_t n4 = n / 4;
+  hipLaunchKernelGGL(philox_gumbel_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, noise, n4, seed, offset);
+  return check_launch("plz_gumbel_philox");
+}
+
+int plz_gumbel_lcg(float* noise, uint32_t seed, int64_t N, int64_t K, void* stream) {
+  PLZ_REQUIRE(N >= 0 && K >= 0, "plz_gumbel_lcg: negative shape");
+  if (N == 0 || K == 0) return PLZ_OK;
+  PLZ_REQUIRE(noise && ((uintptr_t)noise & 15) == 0,
+              "plz_gumbel_lcg: noise must be non-null and 16-byte aligned");
+  const int64_t n = N * K;
+  hipLaunchKernelGGL(lcg_gumbel_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, noise, seed, N, K);
+  return check_launch("plz_gumbel_lcg");
+}
+
+int plz_soft_build_w(const uint16_t* logits, int logits_dtype, const float* noise,
+                     const float* palette, float tau, int mode, uint16_t* w, uint16_t* w_soft,
+                     int64_t N, int64_t K, void* stream) {
+  PLZ_REQUIRE(N >= 0 && K >= 0, "plz_soft_build_w: negative shape");
+  PLZ_REQUIRE(K % 256 == 0, "plz_soft_build_w: K (%lld) must be a multiple of 256", (long long)K);
+  PLZ_REQUIRE(logits_dtype == PLZ_DT_BF16 || logits_dtype == PLZ_DT_FP16,
+              "plz_soft_build_w: logits dtype must be bf16 or fp16");
+  PLZ_REQUIRE(mode == PLZ_W_SOFT || mode == PLZ_W_HARD_NOISY || mode == PLZ_W_HARD_PLAIN,
+              "plz_soft_build_w: unknown mode %d", mode);
+  PLZ_REQUIRE(tau > 0.f, "plz_soft_build_w: tau must be positive");
+  if (N == 0 || K == 0) return PLZ_OK;
+  PLZ_REQUIRE(logits && noise && palette && w, "plz_soft_build_w: null pointer");
+  PLZ_REQUIRE((((uintptr_t)logits | (uintptr_t)noise | (uintptr_t)palette) & 15) == 0 &&
+                  (((uintptr_t)w | (uintptr_t)w_soft) & 3) == 0,
+              "plz_soft_build_w: misaligned pointer");
+  const int64_t n = N * K / 2;
+  hipLaunchKernelGGL(build_w_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, logits, logits_dtype == PLZ_DT_FP16 ? 1 : 0, noise,
+                     palette, 1.f / tau, mode, w, w_soft, N, K);
+  return check_launch("plz_soft_build_w");
+}
+
+}  // extern "C"

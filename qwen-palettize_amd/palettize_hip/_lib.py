@@ -1,0 +1,98 @@
+"""ctypes binding of libpalettize_hip.so (the C ABI declared in include/palettize_hip.h).
+
+The library is loaded from this package directory only; there is no fallback: every op
+raises if the library or a GPU is missing.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import threading
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libpalettize_hip.so")
+
+PLZ_OK, PLZ_EINVAL, PLZ_EHIP, PLZ_EUNSUPPORTED, PLZ_EWORKSPACE = 0, 1, 2, 3, 4
+PLZ_DT_BF16, PLZ_DT_FP16, PLZ_DT_FP32 = 0, 1, 2
+PLZ_W_SOFT, PLZ_W_HARD_NOISY, PLZ_W_HARD_PLAIN = 0, 1, 2
+
+p = C.c_void_p
+i32, i64, u32, u64, f32, sz = C.c_int, C.c_int64, C.c_uint32, C.c_uint64, C.c_float, C.c_size_t
+
+
+class GemvDesc(C.Structure):
+    _fields_ = [("x", p), ("packed", p), ("palette", p), ("y", p), ("N", i64), ("K", i64),
+                ("block_begin", i64)]
+
+
+# name -> (restype, argtypes); kept in the order of include/palettize_hip.h
+SIGNATURES: dict[str, tuple] = {
+    "plz_last_error": (C.c_char_p, []),
+    "plz_abi_version": (i32, []),
+    "plz_pack_indices": (i32, [p, p, i64, i64, p]),
+    "plz_unpack_indices": (i32, [p, p, i64, i64, p]),
+    "plz_dequant": (i32, [p, p, p, i64, i64, p]),
+    "plz_lut_linear_fwd": (i32, [p, p, p, p, p, p, i32, p, i64, i64, i64, p]),
+    "plz_lut_linear_bwd_x": (i32, [p, p, p, p, p, i32, p, i64, i64, i64, p]),
+    "plz_lut_linear_bwd_palette_workspace": (sz, [i64, i64, i64]),
+    "plz_lut_linear_bwd_palette": (i32, [p, p, p, p, p, sz, i64, i64, i64, p]),
+    "plz_bias_grad": (i32, [p, p, i64, i64, p]),
+    "plz_linear_fwd_dense": (i32, [p, p, p, p, p, i32, p, i64, i64, i64, p]),
+    "plz_linear_bwd_x_dense": (i32, [p, p, p, p, i32, p, i64, i64, i64, p]),
+    "plz_gumbel_philox": (i32, [p, i64, u64, u64, p]),
+    "plz_gumbel_lcg": (i32, [p, u32, i64, i64, p]),
+    "plz_soft_build_w": (i32, [p, i32, p, p, f32, i32, p, p, i64, i64, p]),
+    "plz_soft_bwd_workspace": (sz, [i64, i64, i64]),
+    "plz_soft_bwd": (i32, [p, p, p, i32, p, p, f32, i32, p, p, p, sz, i64, i64, i64, p]),
+    "plz_lora_project": (i32, [p, p, f32, p, i64, i64, i32, p]),
+    "plz_lora_grad_t": (i32, [p, p, f32, p, i64, i64, i32, p]),
+    "plz_lora_weight_grads_workspace": (sz, [i64, i64, i64, i32]),
+    "plz_lora_weight_grads": (i32, [p, p, p, p, f32, p, p, i32, p, sz, i64, i64, i64, i32, p]),
+    "plz_lut_gemv": (i32, [p, p, p, p, i64, i64, i64, p]),
+    "plz_gemv_plan": (i64, [C.POINTER(GemvDesc), i32, i32]),
+    "plz_lut_gemv_grouped": (i32, [p, i32, i64, i32, p]),
+    "plz_rmsnorm_fwd": (i32, [p, p, p, p, i64, i64, f32, p]),
+    "plz_rmsnorm_bwd_workspace": (sz, [i64, i64]),
+    "plz_rmsnorm_bwd": (i32, [p, p, p, p, p, p, p, sz, i64, i64, p]),
+    "plz_swiglu_fwd": (i32, [p, p, p, i64, p]),
+    "plz_swiglu_bwd": (i32, [p, p, p, p, p, i64, p]),
+}
+
+_lib = None
+_lock = threading.Lock()
+
+
+class PalettizeError(RuntimeError):
+    """Raised when a library call returns a non-zero status."""
+
+
+def lib():
+    """Loads and returns the library (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        with _lock:
+            if _lib is None:
+                if not os.path.exists(LIB_PATH):
+                    raise PalettizeError(
+                        f"{LIB_PATH} is missing: build it with __graft_entry__.build() "
+                        "(there is no CPU fallback)")
+                handle = C.CDLL(LIB_PATH)
+                for name, (res, args) in SIGNATURES.items():
+                    fn = getattr(handle, name)
+                    fn.restype = res
+                    fn.argtypes = args
+                _lib = handle
+    return _lib
+
+
+def call(name: str, *args) -> int:
+    """Calls an int-returning entry point and raises PalettizeError on failure."""
+    rc = getattr(lib(), name)(*args)
+    if rc != PLZ_OK:
+        msg = lib().plz_last_error().decode(errors="replace")
+        raise PalettizeError(f"{name} failed (status {rc}): {msg}")
+    return rc
+
+
+def query(name: str, *args) -> int:
+    return int(getattr(lib(), name)(*args))

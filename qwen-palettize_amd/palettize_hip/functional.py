@@ -1,0 +1,116 @@
+"""Autograd Functions of the LUT-linear path in the native layout.
+
+  lut_linear(x, packed, palette, bias, lora_a, lora_b, lora_scale)
+      hard path: y = x W^T + bias + s (x A^T) B^T with W = dequant(packed, palette).
+      Gradients: x, palette (fp32 [N, K/256, 4]), bias, lora_a [r, K], lora_b [N, r].
+      Straight-through in the sense of the reference's hard backward
+      (fused_lut_linear_cuda.py:787-818): the indices are frozen, the palette receives the
+      class-scattered dW.
+  soft_lut_linear(x, palette, logits, noise, tau, ...)
+      Gumbel-softmax path with straight-through forward (fused_lut_linear_cuda.py:880-970):
+      forward uses W_hard (or W_soft for mode=PLZ_W_SOFT), backward differentiates
+      W_soft = sum_c P_c pal_c without the 1/tau factor unless scale_by_inv_tau.
+
+Inputs are 2-D ([M, K]); callers flatten leading dimensions.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import ops
+from ._lib import PLZ_W_HARD_NOISY
+
+
+def _c(t):
+    return None if t is None else t.contiguous()
+
+
+class LUTLinearFunction(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, packed, palette, bias, lora_a, lora_b, lora_scale):
+        x = x.contiguous()
+        lora_a, lora_b = _c(lora_a), _c(lora_b)
+        t = ops.lora_project(x, lora_a, lora_scale) if lora_a is not None else None
+        y = ops.lut_linear_fwd(x, packed, palette, bias, t, lora_b)
+        ctx.save_for_backward(x, packed, palette, lora_a, lora_b, t)
+        ctx.lora_scale = float(lora_scale)
+        ctx.has_bias = bias is not None
+        ctx.bias_dtype = None if bias is None else bias.dtype
+        return y
+
+    @staticmethod
+    def backward(ctx, gy):
+        x, packed, palette, lora_a, lora_b, t = ctx.saved_tensors
+        gy = gy.contiguous()
+        need_x, _, need_pal, need_b, need_la, need_lb, _ = ctx.needs_input_grad
+        gt = None
+        if lora_a is not None and (need_x or need_la):
+            gt = ops.lora_grad_t(gy, lora_b, ctx.lora_scale)
+        grad_x = ops.lut_linear_bwd_x(gy, packed, palette, gt, lora_a) if need_x else None
+        grad_pal = ops.lut_linear_bwd_palette(x, gy, packed) if need_pal else None
+        grad_bias = ops.bias_grad(gy).to(ctx.bias_dtype) if (ctx.has_bias and need_b) else None
+        grad_a = grad_b = None
+        if lora_a is not None and (need_la or need_lb):
+            if gt is None:
+                gt = ops.lora_grad_t(gy, lora_b, ctx.lora_scale)
+            grad_a, grad_b = ops.lora_weight_grads(x, gy, t, gt, 1.0, out_dtype=lora_a.dtype)
+        return grad_x, None, grad_pal, grad_bias, grad_a, grad_b, None
+
+
+def lut_linear(x, packed, palette, bias=None, lora_a=None, lora_b=None, lora_scale=1.0):
+    """Hard palettized linear, native layout. x [..., K] -> y [..., N]."""
+    lead = x.shape[:-1]
+    y = LUTLinearFunction.apply(x.reshape(-1, x.shape[-1]), packed, palette, bias, lora_a, lora_b,
+                                lora_scale)
+    return y.reshape(*lead, y.shape[-1])
+
+
+class SoftLUTLinearFunction(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, palette, logits, noise, tau, bias, lora_a, lora_b, lora_scale, mode,
+                scale_by_inv_tau):
+        x = x.contiguous()
+        lora_a, lora_b = _c(lora_a), _c(lora_b)
+        w, _ = ops.soft_build_w(logits, noise, palette, tau, mode)
+        t = ops.lora_project(x, lora_a, lora_scale) if lora_a is not None else None
+        y = ops.linear_fwd_dense(x, w, bias, t, lora_b)
+        ctx.save_for_backward(x, palette, logits, noise, w, lora_a, lora_b, t)
+        ctx.tau = float(tau)
+        ctx.lora_scale = float(lora_scale)
+        ctx.scale_by_inv_tau = bool(scale_by_inv_tau)
+        ctx.has_bias = bias is not None
+        ctx.bias_dtype = None if bias is None else bias.dtype
+        return y
+
+    @staticmethod
+    def backward(ctx, gy):
+        x, palette, logits, noise, w, lora_a, lora_b, t = ctx.saved_tensors
+        gy = gy.contiguous()
+        need = ctx.needs_input_grad
+        need_x, need_pal, need_log, need_b, need_la, need_lb = (
+            need[0], need[1], need[2], need[5], need[6], need[7])
+        gt = None
+        if lora_a is not None and (need_x or need_la):
+            gt = ops.lora_grad_t(gy, lora_b, ctx.lora_scale)
+        grad_x = ops.linear_bwd_x_dense(gy, w, gt, lora_a) if need_x else None
+        grad_logits = grad_pal = None
+        if need_pal or need_log:
+            grad_logits, grad_pal = ops.soft_bwd(x, gy, logits, noise, palette, ctx.tau,
+                                                 ctx.scale_by_inv_tau)
+        grad_bias = ops.bias_grad(gy).to(ctx.bias_dtype) if (ctx.has_bias and need_b) else None
+        grad_a = grad_b = None
+        if lora_a is not None and (need_la or need_lb):
+            if gt is None:
+                gt = ops.lora_grad_t(gy, lora_b, ctx.lora_scale)
+            grad_a, grad_b = ops.lora_weight_grads(x, gy, t, gt, 1.0, out_dtype=lora_a.dtype)
+        return (grad_x, grad_pal if need_pal else None, grad_logits if need_log else None, None,
+                None, grad_bias, grad_a, grad_b, None, None, None)
+
+
+def soft_lut_linear(x, palette, logits, noise, tau, bias=None, lora_a=None, lora_b=None,
+                    lora_scale=1.0, mode=PLZ_W_HARD_NOISY, scale_by_inv_tau=False):
+    """Gumbel-softmax palettized linear, native layout. x [..., K] -> y [..., N]."""
+    lead = x.shape[:-1]
+    y = SoftLUTLinearFunction.apply(x.reshape(-1, x.shape[-1]), palette, logits, noise, tau, bias,
+                                    lora_a, lora_b, lora_scale, mode, scale_by_inv_tau)
+    return y.reshape(*lead, y.shape[-1])

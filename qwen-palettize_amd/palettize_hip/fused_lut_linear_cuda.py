@@ -1,0 +1,211 @@
+"""Drop-in replacement of the reference's ``fused_lut_linear_cuda`` module.
+
+Same names, arguments, layouts and gradient tuples as the reference
+(fused_lut_linear_cuda.py:755-994), backed by the MI355X kernels of libpalettize_hip.so:
+
+  fused_lut_linear(x, palette, indices, bias=None, group_size=256) -> y
+  CUDAFusedLUTLinear.apply(x, palette, indices, bias, group_size)
+      x (M, K) bf16; palette (G, 4) bf16 with G = N / group_size; indices (K, N) int8;
+      y = x @ W + bias with W[k, n] = palette[n // group_size, indices[k, n]].
+      backward -> (grad_x, grad_palette (G, 4) in palette's dtype, None, grad_bias, None)
+  fused_lut_linear_soft(x, palette, logits, bias=None, group_size=256, tau=1.0) -> y
+  CUDAFusedLUTLinearSoft.apply(x, palette, logits, bias, group_size, tau)
+      logits (4, K, N) fp16 (SoA planes, as the reference stores them). The Gumbel noise is
+      the reference's own LCG hash sampler with the same global step-seed counter
+      (fused_lut_linear_cuda.py:837-843, fused_lut_kernel.cu:1245-1256), so a run draws the
+      same noise integers as the reference. Forward value W_hard = palette[argmax of the
+      noisy P] (straight-through); backward -> (grad_x, grad_palette, grad_logits (4, K, N)
+      fp16, grad_bias, None, None) with the reference's formulas (no 1/tau factor).
+
+The reference layout (one palette per 256 output channels spanning all of K) is mapped onto
+the native one (palette per output row and 256-wide K chunk) by expanding the palette; its
+gradient is summed back over the expansion. K is zero-padded to a multiple of 256 when needed
+(the padded columns multiply zeros and contribute nothing).
+"""
+from __future__ import annotations
+
+from collections import OrderedDict
+
+import torch
+import torch.nn.functional as F
+from torch import Tensor
+
+from . import ops
+from ._lib import PLZ_W_HARD_NOISY
+
+GROUP_SIZE = 256
+_PACK_CACHE: "OrderedDict[tuple, Tensor]" = OrderedDict()
+_PACK_CACHE_SIZE = 64
+
+
+def _pad_k(K: int) -> int:
+    return (K + 255) // 256 * 256
+
+
+def packed_from_reference(indices: Tensor, pre_transposed: bool = False) -> Tensor:
+    """(K, N) int8/uint8/int64 indices (or (N, K) when pre_transposed) -> native packed
+    int32 [N, Kp/16]. Frozen index buffers are converted once and cached by identity."""
+    key = (indices.data_ptr(), indices._version, tuple(indices.shape), str(indices.device),
+           bool(pre_transposed))
+    hit = _PACK_CACHE.get(key)
+    if hit is not None:
+        _PACK_CACHE.move_to_end(key)
+        return hit
+    nk = indices if pre_transposed else indices.t()
+    N, K = nk.shape
+    Kp = _pad_k(K)
+    idx = nk.to(torch.uint8)
+    if Kp != K:
+        idx = F.pad(idx, (0, Kp - K))
+    packed = ops.pack_indices(idx.contiguous())
+    _PACK_CACHE[key] = packed
+    if len(_PACK_CACHE) > _PACK_CACHE_SIZE:
+        _PACK_CACHE.popitem(last=False)
+    return packed
+
+
+def palette_from_reference(palette: Tensor, N: int, K: int, group_size: int) -> Tensor:
+    """(G, 4) reference palette -> native fp32 [N, Kp/256, 4] (exact for bf16/fp16 input)."""
+    G = palette.shape[0]
+    if N % group_size or N // group_size != G:
+        raise ValueError(f"G mismatch: N/group_size={N // group_size} vs palette.size(0)={G}")
+    kg = _pad_k(K) // 256
+    per_row = palette.float().repeat_interleave(group_size, dim=0)  # [N, 4]
+    return per_row[:, None, :].expand(N, kg, 4).contiguous()
+
+
+def palette_grad_to_reference(grad: Tensor, group_size: int) -> Tensor:
+    """native [N, KG, 4] -> reference (G, 4): sum over the rows of a group and over KG."""
+    N, kg, _ = grad.shape
+    return grad.view(N // group_size, group_size, kg, 4).sum(dim=(1, 2))
+
+
+def _prep_x(x: Tensor, K: int) -> Tensor:
+    x = x.contiguous()
+    Kp = _pad_k(K)
+    return F.pad(x, (0, Kp - K)) if Kp != K else x
+
+
+class CUDAFusedLUTLinear(torch.autograd.Function):
+    """forward(ctx, x, palette, indices, bias, group_size) -> y
+    backward(ctx, grad_y) -> (grad_x, grad_palette, None, grad_bias, None)"""
+
+    @staticmethod
+    def forward(ctx, x, palette, indices, bias, group_size):
+        if x.dtype != torch.bfloat16:
+            raise TypeError("x must be bf16 cuda")
+        if palette.dim() != 2 or palette.shape[1] != 4:
+            raise ValueError("palette must have 4 entries per group")
+        K, N = indices.shape
+        if x.shape[-1] != K:
+            raise ValueError("indices K mismatch")
+        if N % 8:
+            raise ValueError(f"N ({N}) must be a multiple of 8")
+        packed = packed_from_reference(indices)
+        pal = palette_from_reference(palette, N, K, group_size)
+        xp = _prep_x(x, K)
+        b = None if bias is None else bias.to(torch.bfloat16).contiguous()
+        y = ops.lut_linear_fwd(xp, packed, pal, b)
+        ctx.save_for_backward(xp, packed, pal)
+        ctx.group_size, ctx.K = group_size, K
+        ctx.pal_dtype = palette.dtype
+        ctx.bias_requires_grad = bias is not None and bias.requires_grad
+        ctx.bias_dtype = None if bias is None else bias.dtype
+        return y
+
+    @staticmethod
+    def backward(ctx, grad_y):
+        xp, packed, pal = ctx.saved_tensors
+        grad_y = grad_y.contiguous()
+        grad_x = grad_pal = grad_bias = None
+        if ctx.needs_input_grad[0]:
+            grad_x = ops.lut_linear_bwd_x(grad_y, packed, pal)[:, : ctx.K].contiguous()
+        if ctx.needs_input_grad[1]:
+            g = ops.lut_linear_bwd_palette(xp, grad_y, packed)
+            grad_pal = palette_grad_to_reference(g, ctx.group_size).to(ctx.pal_dtype)
+        if ctx.bias_requires_grad:
+            grad_bias = ops.bias_grad(grad_y).to(ctx.bias_dtype)
+        return grad_x, grad_pal, None, grad_bias, None
+
+
+def fused_lut_linear(x: Tensor, palette: Tensor, indices: Tensor, bias: Tensor | None = None,
+                     group_size: int = GROUP_SIZE) -> Tensor:
+    """Functional interface -- supports autograd."""
+    return CUDAFusedLUTLinear.apply(x, palette, indices, bias, group_size)
+
+
+# Global step counter for the Gumbel seed (one increment per soft forward), as in the
+# reference (fused_lut_linear_cuda.py:837-843).
+_SOFT_STEP_SEED = 0
+
+
+def _next_soft_step_seed() -> int:
+    global _SOFT_STEP_SEED
+    _SOFT_STEP_SEED = (_SOFT_STEP_SEED + 1) & 0xFFFFFFFF
+    return _SOFT_STEP_SEED
+
+
+def logits_from_reference(logits: Tensor, K: int) -> Tensor:
+    """(4, K, N) SoA planes -> native [N, Kp, 4] (same dtype)."""
+    nk4 = logits.permute(2, 1, 0)
+    Kp = _pad_k(K)
+    if Kp != K:
+        nk4 = F.pad(nk4, (0, 0, 0, Kp - K))
+    return nk4.contiguous()
+
+
+class CUDAFusedLUTLinearSoft(torch.autograd.Function):
+    """forward(ctx, x, palette, logits, bias, group_size, tau) -> y
+    backward(ctx, grad_y) -> (grad_x, grad_palette, grad_logits, grad_bias, None, None)"""
+
+    @staticmethod
+    def forward(ctx, x, palette, logits, bias, group_size, tau):
+        if logits.dim() != 3 or logits.shape[0] != 4:
+            raise ValueError("logits first dim must be 4")
+        if logits.dtype not in (torch.float16, torch.bfloat16):
+            raise TypeError("logits must be fp16 or bf16")
+        _, K, N = logits.shape
+        if x.shape[-1] != K:
+            raise ValueError(f"x K={x.shape[-1]} != logits K={K}")
+        if N % group_size or N // group_size != palette.shape[0]:
+            raise ValueError("G mismatch")
+        if N % 8:
+            raise ValueError(f"N ({N}) must be a multiple of 8")
+        step_seed = _next_soft_step_seed()
+        xp = _prep_x(x, K)
+        Kp = xp.shape[1]
+        lg = logits_from_reference(logits, K)
+        noise = ops.gumbel_lcg(N, Kp, step_seed, device=x.device)
+        pal = palette_from_reference(palette, N, K, group_size)
+        w, _ = ops.soft_build_w(lg, noise, pal, float(tau), PLZ_W_HARD_NOISY)
+        b = None if bias is None else bias.to(torch.bfloat16).contiguous()
+        y = ops.linear_fwd_dense(xp, w, b)
+        ctx.save_for_backward(xp, pal, lg, noise, w)
+        ctx.group_size, ctx.K, ctx.tau = group_size, K, float(tau)
+        ctx.pal_dtype, ctx.logits_dtype = palette.dtype, logits.dtype
+        ctx.has_bias = bias is not None
+        ctx.bias_dtype = None if bias is None else bias.dtype
+        return y
+
+    @staticmethod
+    def backward(ctx, grad_y):
+        xp, pal, lg, noise, w = ctx.saved_tensors
+        grad_y = grad_y.contiguous()
+        grad_x = grad_pal = grad_logits = grad_bias = None
+        if ctx.needs_input_grad[0]:
+            grad_x = ops.linear_bwd_x_dense(grad_y, w)[:, : ctx.K].contiguous()
+        if ctx.needs_input_grad[1] or ctx.needs_input_grad[2]:
+            gl, gp = ops.soft_bwd(xp, grad_y, lg, noise, pal, ctx.tau)
+            if ctx.needs_input_grad[2]:
+                grad_logits = gl[:, : ctx.K, :].permute(2, 1, 0).contiguous().to(ctx.logits_dtype)
+            if ctx.needs_input_grad[1]:
+                grad_pal = palette_grad_to_reference(gp, ctx.group_size).to(ctx.pal_dtype)
+        if ctx.has_bias and ctx.needs_input_grad[3]:
+            grad_bias = ops.bias_grad(grad_y).to(ctx.bias_dtype)
+        return grad_x, grad_pal, grad_logits, grad_bias, None, None
+
+
+def fused_lut_linear_soft(x: Tensor, palette: Tensor, logits: Tensor, bias: Tensor | None = None,
+                          group_size: int = GROUP_SIZE, tau: float = 1.0) -> Tensor:
+    """Soft (Gumbel-Softmax) functional interface -- supports autograd."""
+    return CUDAFusedLUTLinearSoft.apply(x, palette, logits, bias, group_size, tau)

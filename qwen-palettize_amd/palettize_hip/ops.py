@@ -1,0 +1,387 @@
+"""Tensor-level wrappers of the C ABI (one function per entry point).
+
+PyTorch provides device memory and the current HIP stream; all arithmetic runs in the HIP
+kernels of libpalettize_hip.so. Outputs and workspaces are allocated here (the library
+never allocates). Inputs must be CUDA (HIP) tensors; nothing falls back to the CPU.
+
+Native layout (the one the kernels use):
+  packed  int32 [N, K/16]      2-bit indices, 16 per word along K, LSB first
+  palette fp32  [N, K/256, 4]  per output row and per 256 input columns
+  logits  bf16/fp16 [N, K, 4], noise fp32 [N, K, 4]
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import torch
+
+from . import _lib
+from ._lib import call, query
+
+_DT = {torch.bfloat16: _lib.PLZ_DT_BF16, torch.float16: _lib.PLZ_DT_FP16,
+       torch.float32: _lib.PLZ_DT_FP32}
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _need(t: torch.Tensor, name: str, dtype=None, ndim=None) -> torch.Tensor:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a tensor")
+    if not t.is_cuda:
+        raise RuntimeError(f"{name} must be a GPU tensor (palettize_hip has no CPU path)")
+    if dtype is not None and t.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
+    if ndim is not None and t.dim() != ndim:
+        raise ValueError(f"{name} must be {ndim}-D, got shape {tuple(t.shape)}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    return t
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def _workspace(nbytes: int, device) -> torch.Tensor:
+    return torch.empty(max(int(nbytes), 16), dtype=torch.uint8, device=device)
+
+
+# ---- formats ------------------------------------------------------------------------
+def pack_indices(idx: torch.Tensor) -> torch.Tensor:
+    """uint8 [rows, cols] (0..3) -> int32 [rows, cols/16], LSB first."""
+    _need(idx, "idx", torch.uint8, 2)
+    rows, cols = idx.shape
+    out = torch.empty((rows, cols // 16), dtype=torch.int32, device=idx.device)
+    call("plz_pack_indices", _ptr(idx), _ptr(out), rows, cols, _stream(idx))
+    return out
+
+
+def unpack_indices(packed: torch.Tensor) -> torch.Tensor:
+    _need(packed, "packed", torch.int32, 2)
+    rows, words = packed.shape
+    out = torch.empty((rows, words * 16), dtype=torch.uint8, device=packed.device)
+    call("plz_unpack_indices", _ptr(packed), _ptr(out), rows, words * 16, _stream(packed))
+    return out
+
+
+def _wshape(packed: torch.Tensor, palette: torch.Tensor):
+    _need(packed, "packed", torch.int32, 2)
+    _need(palette, "palette", torch.float32, 3)
+    N, K = packed.shape[0], packed.shape[1] * 16
+    if tuple(palette.shape) != (N, K // 256, 4):
+        raise ValueError(f"palette shape {tuple(palette.shape)} != {(N, K // 256, 4)}")
+    return N, K
+
+
+def dequant(packed: torch.Tensor, palette: torch.Tensor) -> torch.Tensor:
+    N, K = _wshape(packed, palette)
+    w = torch.empty((N, K), dtype=torch.bfloat16, device=packed.device)
+    call("plz_dequant", _ptr(packed), _ptr(palette), _ptr(w), N, K, _stream(packed))
+    return w
+
+
+# ---- hard linear --------------------------------------------------------------------
+def _lora_pair(a, b, first: str, second: str, rows_a: int, rows_b: int):
+    if (a is None) != (b is None):
+        raise ValueError(f"{first} and {second} must be given together")
+    if a is None:
+        return 0
+    _need(a, first, torch.bfloat16, 2)
+    _need(b, second, torch.bfloat16, 2)
+    r = a.shape[1]
+    if a.shape[0] != rows_a or b.shape[1] != r or b.shape[0] != rows_b:
+        raise ValueError(f"{first} {tuple(a.shape)} / {second} {tuple(b.shape)} mismatch")
+    return r
+
+
+def lut_linear_fwd(x, packed, palette, bias=None, lora_t=None, lora_b=None):
+    """y = x W^T (+ bias) (+ lora_t lora_b^T)."""
+    N, K = _wshape(packed, palette)
+    _need(x, "x", torch.bfloat16, 2)
+    M = x.shape[0]
+    if x.shape[1] != K:
+        raise ValueError(f"x has {x.shape[1]} columns, W has K={K}")
+    if bias is not None:
+        _need(bias, "bias", torch.bfloat16, 1)
+    rank = _lora_pair(lora_t, lora_b, "lora_t", "lora_b", M, N)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
+    call("plz_lut_linear_fwd", _ptr(x), _ptr(packed), _ptr(palette), _ptr(bias), _ptr(lora_t),
+         _ptr(lora_b), rank, _ptr(y), M, N, K, _stream(x))
+    return y
+
+
+def lut_linear_bwd_x(grad_y, packed, palette, lora_gt=None, lora_a=None):
+    """grad_x = grad_y W (+ lora_gt lora_a)."""
+    N, K = _wshape(packed, palette)
+    _need(grad_y, "grad_y", torch.bfloat16, 2)
+    M = grad_y.shape[0]
+    if grad_y.shape[1] != N:
+        raise ValueError("grad_y columns != N")
+    rank = 0
+    if lora_gt is not None or lora_a is not None:
+        if lora_gt is None or lora_a is None:
+            raise ValueError("lora_gt and lora_a must be given together")
+        _need(lora_gt, "lora_gt", torch.bfloat16, 2)
+        _need(lora_a, "lora_a", torch.bfloat16, 2)
+        rank = lora_gt.shape[1]
+        if lora_gt.shape[0] != M or tuple(lora_a.shape) != (rank, K):
+            raise ValueError("lora_gt / lora_a shape mismatch")
+    gx = torch.empty((M, K), dtype=torch.bfloat16, device=grad_y.device)
+    call("plz_lut_linear_bwd_x", _ptr(grad_y), _ptr(packed), _ptr(palette), _ptr(lora_gt),
+         _ptr(lora_a), rank, _ptr(gx), M, N, K, _stream(grad_y))
+    return gx
+
+
+def lut_linear_bwd_palette(x, grad_y, packed):
+    """fp32 [N, K/256, 4]: per-class sums of (grad_y^T x)[n, k] over each 256-k group."""
+    _need(packed, "packed", torch.int32, 2)
+    _need(x, "x", torch.bfloat16, 2)
+    _need(grad_y, "grad_y", torch.bfloat16, 2)
+    N, K = packed.shape[0], packed.shape[1] * 16
+    M = x.shape[0]
+    if x.shape[1] != K or tuple(grad_y.shape) != (M, N):
+        raise ValueError("x / grad_y shape mismatch")
+    out = torch.empty((N, K // 256, 4), dtype=torch.float32, device=x.device)
+    nbytes = query("plz_lut_linear_bwd_palette_workspace", M, N, K)
+    ws = _workspace(nbytes, x.device)
+    call("plz_lut_linear_bwd_palette", _ptr(x), _ptr(grad_y), _ptr(packed), _ptr(out), _ptr(ws),
+         ws.numel(), M, N, K, _stream(x))
+    return out
+
+
+def bias_grad(grad_y):
+    _need(grad_y, "grad_y", torch.bfloat16, 2)
+    M, N = grad_y.shape
+    out = torch.empty((N,), dtype=torch.float32, device=grad_y.device)
+    call("plz_bias_grad", _ptr(grad_y), _ptr(out), M, N, _stream(grad_y))
+    return out
+
+
+# ---- dense linear -----------------------------------------------------------------------
+def linear_fwd_dense(x, w, bias=None, lora_t=None, lora_b=None):
+    _need(x, "x", torch.bfloat16, 2)
+    _need(w, "w", torch.bfloat16, 2)
+    M, K = x.shape
+    N = w.shape[0]
+    if w.shape[1] != K:
+        raise ValueError("x / w shape mismatch")
+    if bias is not None:
+        _need(bias, "bias", torch.bfloat16, 1)
+    rank = _lora_pair(lora_t, lora_b, "lora_t", "lora_b", M, N)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
+    call("plz_linear_fwd_dense", _ptr(x), _ptr(w), _ptr(bias), _ptr(lora_t), _ptr(lora_b), rank,
+         _ptr(y), M, N, K, _stream(x))
+    return y
+
+
+def linear_bwd_x_dense(grad_y, w, lora_gt=None, lora_a=None):
+    _need(grad_y, "grad_y", torch.bfloat16, 2)
+    _need(w, "w", torch.bfloat16, 2)
+    M, N = grad_y.shape
+    K = w.shape[1]
+    if w.shape[0] != N:
+        raise ValueError("grad_y / w shape mismatch")
+    rank = 0
+    if lora_gt is not None:
+        _need(lora_gt, "lora_gt", torch.bfloat16, 2)
+        _need(lora_a, "lora_a", torch.bfloat16, 2)
+        rank = lora_gt.shape[1]
+    gx = torch.empty((M, K), dtype=torch.bfloat16, device=grad_y.device)
+    call("plz_linear_bwd_x_dense", _ptr(grad_y), _ptr(w), _ptr(lora_gt), _ptr(lora_a), rank,
+         _ptr(gx), M, N, K, _stream(grad_y))
+    return gx
+
+
+# ---- soft path ------------------------------------------------------------------------
+def gumbel_philox(shape, seed: int, offset: int = 0, device="cuda"):
+    n = 1
+    for s in shape:
+        n *= int(s)
+    out = torch.empty(tuple(shape), dtype=torch.float32, device=device)
+    call("plz_gumbel_philox", _ptr(out), n, int(seed) & (2**64 - 1), int(offset) & (2**64 - 1),
+         _stream(out))
+    return out
+
+
+def gumbel_lcg(N: int, K: int, seed: int, device="cuda"):
+    out = torch.empty((N, K, 4), dtype=torch.float32, device=device)
+    call("plz_gumbel_lcg", _ptr(out), int(seed) & 0xFFFFFFFF, N, K, _stream(out))
+    return out
+
+
+def _soft_shapes(logits, noise, palette):
+    if logits.dtype not in (torch.bfloat16, torch.float16):
+        raise TypeError("logits must be bf16 or fp16")
+    _need(logits, "logits", None, 3)
+    _need(noise, "noise", torch.float32, 3)
+    _need(palette, "palette", torch.float32, 3)
+    N, K, four = logits.shape
+    if four != 4 or tuple(noise.shape) != (N, K, 4) or tuple(palette.shape) != (N, K // 256, 4):
+        raise ValueError("logits [N,K,4], noise [N,K,4], palette [N,K/256,4] expected")
+    return N, K
+
+
+def soft_build_w(logits, noise, palette, tau: float, mode: int = _lib.PLZ_W_HARD_NOISY,
+                 want_soft: bool = False):
+    N, K = _soft_shapes(logits, noise, palette)
+    w = torch.empty((N, K), dtype=torch.bfloat16, device=logits.device)
+    ws = torch.empty((N, K), dtype=torch.bfloat16, device=logits.device) if want_soft else None
+    call("plz_soft_build_w", _ptr(logits), _DT[logits.dtype], _ptr(noise), _ptr(palette),
+         float(tau), int(mode), _ptr(w), _ptr(ws), N, K, _stream(logits))
+    return w, ws
+
+
+def soft_bwd(x, grad_y, logits, noise, palette, tau: float, scale_by_inv_tau: bool = False):
+    N, K = _soft_shapes(logits, noise, palette)
+    _need(x, "x", torch.bfloat16, 2)
+    _need(grad_y, "grad_y", torch.bfloat16, 2)
+    M = x.shape[0]
+    if x.shape[1] != K or tuple(grad_y.shape) != (M, N):
+        raise ValueError("x / grad_y shape mismatch")
+    gl = torch.empty_like(logits)
+    gp = torch.empty((N, K // 256, 4), dtype=torch.float32, device=x.device)
+    ws = _workspace(query("plz_soft_bwd_workspace", M, N, K), x.device)
+    call("plz_soft_bwd", _ptr(x), _ptr(grad_y), _ptr(logits), _DT[logits.dtype], _ptr(noise),
+         _ptr(palette), float(tau), int(bool(scale_by_inv_tau)), _ptr(gl), _ptr(gp), _ptr(ws),
+         ws.numel(), M, N, K, _stream(x))
+    return gl, gp
+
+
+# ---- LoRA -----------------------------------------------------------------------------
+def lora_project(x, lora_a, scale: float):
+    """t = scale * x lora_a^T, lora_a [r, K]."""
+    _need(x, "x", torch.bfloat16, 2)
+    _need(lora_a, "lora_a", torch.bfloat16, 2)
+    M, K = x.shape
+    r = lora_a.shape[0]
+    if lora_a.shape[1] != K:
+        raise ValueError("lora_a must be [r, K]")
+    t = torch.empty((M, r), dtype=torch.bfloat16, device=x.device)
+    call("plz_lora_project", _ptr(x), _ptr(lora_a), float(scale), _ptr(t), M, K, r, _stream(x))
+    return t
+
+
+def lora_grad_t(grad_y, lora_b, scale: float):
+    """gt = scale * grad_y lora_b, lora_b [N, r]."""
+    _need(grad_y, "grad_y", torch.bfloat16, 2)
+    _need(lora_b, "lora_b", torch.bfloat16, 2)
+    M, N = grad_y.shape
+    r = lora_b.shape[1]
+    if lora_b.shape[0] != N:
+        raise ValueError("lora_b must be [N, r]")
+    gt = torch.empty((M, r), dtype=torch.bfloat16, device=grad_y.device)
+    call("plz_lora_grad_t", _ptr(grad_y), _ptr(lora_b), float(scale), _ptr(gt), M, N, r,
+         _stream(grad_y))
+    return gt
+
+
+def lora_weight_grads(x, grad_y, t, gt, scale: float = 1.0, out_dtype=torch.float32):
+    """grad_a [r, K] = gt^T x ; grad_b [N, r] = scale * grad_y^T t."""
+    for name, v in (("x", x), ("grad_y", grad_y), ("t", t), ("gt", gt)):
+        _need(v, name, torch.bfloat16, 2)
+    M, K = x.shape
+    N = grad_y.shape[1]
+    r = t.shape[1]
+    ga = torch.empty((r, K), dtype=out_dtype, device=x.device)
+    gb = torch.empty((N, r), dtype=out_dtype, device=x.device)
+    ws = _workspace(query("plz_lora_weight_grads_workspace", M, N, K, r), x.device)
+    call("plz_lora_weight_grads", _ptr(x), _ptr(grad_y), _ptr(t), _ptr(gt), float(scale),
+         _ptr(ga), _ptr(gb), _DT[out_dtype], _ptr(ws), ws.numel(), M, N, K, r, _stream(x))
+    return ga, gb
+
+
+# ---- decode GEMV ------------------------------------------------------------------------
+def lut_gemv(x, packed, palette):
+    N, K = _wshape(packed, palette)
+    _need(x, "x", torch.bfloat16, 2)
+    M = x.shape[0]
+    if x.shape[1] != K:
+        raise ValueError("x / W shape mismatch")
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
+    call("plz_lut_gemv", _ptr(x), _ptr(packed), _ptr(palette), _ptr(y), M, N, K, _stream(x))
+    return y
+
+
+class GemvGroup:
+    """A fixed set of independent GEMVs (same M) run by one grouped launch.
+
+    ``items`` is a list of (x [M,K] bf16, packed, palette); outputs are allocated once and
+    reused by every ``run()``. The descriptor table lives in device memory.
+    """
+
+    def __init__(self, items):
+        if not items:
+            raise ValueError("empty GEMV group")
+        self.M = items[0][0].shape[0]
+        self.device = items[0][0].device
+        self.outputs = []
+        descs = (_lib.GemvDesc * len(items))()
+        for i, (x, packed, palette) in enumerate(items):
+            N, K = _wshape(packed, palette)
+            _need(x, "x", torch.bfloat16, 2)
+            if x.shape != (self.M, K):
+                raise ValueError(f"item {i}: x must be [{self.M}, {K}]")
+            y = torch.empty((self.M, N), dtype=torch.bfloat16, device=self.device)
+            self.outputs.append(y)
+            descs[i] = _lib.GemvDesc(x.data_ptr(), packed.data_ptr(), palette.data_ptr(),
+                                     y.data_ptr(), N, K, 0)
+        self._keep = items
+        total = _lib.lib().plz_gemv_plan(descs, len(items), self.M)
+        if total < 0:
+            raise _lib.PalettizeError(
+                "plz_gemv_plan failed: " + _lib.lib().plz_last_error().decode())
+        self.total_blocks = int(total)
+        raw = bytes(C.string_at(C.addressof(descs), C.sizeof(descs)))
+        host = torch.frombuffer(bytearray(raw), dtype=torch.uint8)
+        self.table = host.to(self.device)
+        self.n = len(items)
+
+    def run(self):
+        call("plz_lut_gemv_grouped", self.table.data_ptr(), self.n, self.total_blocks, self.M,
+             torch.cuda.current_stream(self.device).cuda_stream)
+        return self.outputs
+
+
+# ---- RMSNorm / SwiGLU -----------------------------------------------------------------------
+def rmsnorm_fwd(x, weight, eps: float):
+    _need(x, "x", torch.bfloat16, 2)
+    _need(weight, "weight", torch.bfloat16, 1)
+    rows, cols = x.shape
+    y = torch.empty_like(x)
+    rstd = torch.empty((rows,), dtype=torch.float32, device=x.device)
+    call("plz_rmsnorm_fwd", _ptr(x), _ptr(weight), _ptr(y), _ptr(rstd), rows, cols, float(eps),
+         _stream(x))
+    return y, rstd
+
+
+def rmsnorm_bwd(x, weight, rstd, grad_y):
+    _need(x, "x", torch.bfloat16, 2)
+    _need(grad_y, "grad_y", torch.bfloat16, 2)
+    rows, cols = x.shape
+    gx = torch.empty_like(x)
+    gw = torch.empty((cols,), dtype=torch.float32, device=x.device)
+    ws = _workspace(query("plz_rmsnorm_bwd_workspace", rows, cols), x.device)
+    call("plz_rmsnorm_bwd", _ptr(x), _ptr(weight), _ptr(rstd), _ptr(grad_y), _ptr(gx), _ptr(gw),
+         _ptr(ws), ws.numel(), rows, cols, _stream(x))
+    return gx, gw
+
+
+def swiglu_fwd(gate, up):
+    _need(gate, "gate", torch.bfloat16)
+    _need(up, "up", torch.bfloat16)
+    h = torch.empty_like(gate)
+    call("plz_swiglu_fwd", _ptr(gate), _ptr(up), _ptr(h), gate.numel(), _stream(gate))
+    return h
+
+
+def swiglu_bwd(gate, up, grad_h):
+    _need(gate, "gate", torch.bfloat16)
+    _need(up, "up", torch.bfloat16)
+    _need(grad_h, "grad_h", torch.bfloat16)
+    gg = torch.empty_like(gate)
+    gu = torch.empty_like(up)
+    call("plz_swiglu_bwd", _ptr(gate), _ptr(up), _ptr(grad_h), _ptr(gg), _ptr(gu), gate.numel(),
+         _stream(gate))
+    return gg, gu

@@ -1,0 +1,149 @@
+"""GPU parity: packing, dequant, hard LUT-linear forward / backward, GEMV (through the C ABI)."""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from helpers import assert_close, f32, make_weight, randn_bf16
+
+pytestmark = pytest.mark.gpu
+ops = pytest.importorskip("palettize_hip.ops")
+
+
+def _packed(idx, dev):
+    return ops.pack_indices(idx.to(dev))
+
+
+@pytest.mark.parametrize("N,K", [(8, 256), (24, 512), (2560, 2560), (1032, 768)])
+def test_pack_unpack_bit_exact(dev, N, K):
+    idx, _ = make_weight(N, K, seed=N + K)
+    p = _packed(idx, dev)
+    assert np.array_equal(p.cpu().numpy(), O.pack_native(idx.numpy()))
+    assert torch.equal(ops.unpack_indices(p).cpu(), idx)
+
+
+@pytest.mark.parametrize("N,K", [(8, 256), (2560, 2560), (1032, 768), (4096, 2560)])
+def test_dequant_bit_exact(dev, N, K):
+    idx, pal = make_weight(N, K, seed=7 * N + K)
+    w = ops.dequant(_packed(idx, dev), pal.to(dev))
+    got = w.view(torch.int16).cpu().numpy().view(np.uint16)
+    assert np.array_equal(got, O.dequant_bits(idx.numpy(), pal.numpy()))
+
+
+def test_dequant_rounds_fp32_palette_to_nearest_even(dev):
+    # palette entries on, just below and just above bf16 rounding ties (even and odd bases)
+    N, K = 8, 256
+    idx = torch.arange(4, dtype=torch.uint8).repeat(N, K // 4)
+    vals = []
+    for n in range(N):
+        b = (0x3C00 + 2 * n + (n % 2)) << 16
+        vals += [b | 0x8000, b | 0x7FFF, b | 0x8001, (b + 0x10000) | 0x8000]
+    pal = torch.from_numpy(np.array(vals, np.uint32).view(np.float32).reshape(N, 1, 4).copy())
+    w = ops.dequant(_packed(idx, dev), pal.to(dev)).view(torch.int16).cpu().numpy().view(np.uint16)
+    assert np.array_equal(w, O.dequant_bits(idx.numpy(), pal.numpy()))
+
+
+def _oracle_problem(M, N, K, seed, rank=0):
+    idx, pal = make_weight(N, K, seed=seed)
+    x = randn_bf16(M, K, seed=seed + 1)
+    W = O.dequant(idx.numpy(), pal.numpy())
+    lora = None
+    if rank:
+        a = randn_bf16(rank, K, seed=seed + 2, std=0.01)
+        b = randn_bf16(N, rank, seed=seed + 3, std=0.01)
+        lora = (a, b)
+    return idx, pal, x, W, lora
+
+
+@pytest.mark.parametrize("M,N,K,rank", [
+    (512, 2560, 2560, 16),   # config 1 shape
+    (1, 256, 256, 0), (3, 1032, 768, 8), (129, 384, 512, 16), (300, 136, 1024, 32),
+])
+def test_lut_linear_fwd(dev, M, N, K, rank):
+    idx, pal, x, W, lora = _oracle_problem(M, N, K, seed=M + N + K, rank=rank)
+    bias = randn_bf16(N, seed=5, std=0.1) if M % 2 else None
+    args = {}
+    t_ref = None
+    if rank:
+        a, b = lora
+        t = ops.lora_project(x.to(dev), a.to(dev), 1.0)
+        t_ref = f32(a)  # oracle recomputes t from x
+        assert_close(f32(t), O.bf16_round(f32(x) @ f32(a).T), what="lora t")
+        args = dict(lora_t=t, lora_b=b.to(dev))
+    y = ops.lut_linear_fwd(x.to(dev), _packed(idx, dev), pal.to(dev),
+                           None if bias is None else bias.to(dev), **args)
+    want = O.lut_linear_fwd(f32(x), W, None if bias is None else f32(bias))
+    if rank:
+        want = want + O.lora_forward(f32(x), t_ref, f32(lora[1]), 1.0)
+    assert_close(f32(y), want, what="y")
+
+
+@pytest.mark.parametrize("M,N,K,rank", [(512, 2560, 2560, 16), (1, 256, 256, 0),
+                                        (77, 1032, 768, 8), (256, 384, 1024, 32)])
+def test_lut_linear_bwd_x(dev, M, N, K, rank):
+    idx, pal, _, W, lora = _oracle_problem(M, N, K, seed=3 * M + N, rank=rank)
+    gy = randn_bf16(M, N, seed=9)
+    args = {}
+    want = O.grad_x(f32(gy), W)
+    if rank:
+        a, b = lora
+        gt = ops.lora_grad_t(gy.to(dev), b.to(dev), 2.0)
+        assert_close(f32(gt), 2.0 * f32(gy) @ f32(b), what="lora gt")
+        args = dict(lora_gt=gt, lora_a=a.to(dev))
+        want = want + f32(gt) @ f32(a)
+    gx = ops.lut_linear_bwd_x(gy.to(dev), _packed(idx, dev), pal.to(dev), **args)
+    assert_close(f32(gx), want, what="grad_x")
+
+
+@pytest.mark.parametrize("M,N,K", [(512, 2560, 2560), (1, 256, 256), (77, 1032, 768),
+                                   (2048, 128, 512), (64, 1024, 2560)])
+def test_lut_linear_bwd_palette(dev, M, N, K):
+    idx, pal, x, _, _ = _oracle_problem(M, N, K, seed=M * 5 + K)
+    gy = randn_bf16(M, N, seed=11)
+    g1 = ops.lut_linear_bwd_palette(x.to(dev), gy.to(dev), _packed(idx, dev))
+    want = O.grad_palette(f32(x), f32(gy), idx.numpy())
+    assert_close(f32(g1), want, max_rel=1e-3, min_cos=0.99999, what="grad_palette")
+    g2 = ops.lut_linear_bwd_palette(x.to(dev), gy.to(dev), _packed(idx, dev))
+    assert torch.equal(g1, g2), "grad_palette must be deterministic"
+
+
+def test_bias_grad(dev):
+    gy = randn_bf16(333, 136, seed=3)
+    assert_close(f32(ops.bias_grad(gy.to(dev))), O.grad_bias(f32(gy)), max_rel=1e-5,
+                 min_cos=0.999999)
+
+
+def test_empty_inputs(dev):
+    idx, pal = make_weight(16, 256, seed=1)
+    p, pl = _packed(idx, dev), pal.to(dev)
+    x = torch.empty(0, 256, dtype=torch.bfloat16, device=dev)
+    assert ops.lut_linear_fwd(x, p, pl).shape == (0, 16)
+    g = ops.lut_linear_bwd_palette(x, torch.empty(0, 16, dtype=torch.bfloat16, device=dev), p)
+    assert torch.count_nonzero(g) == 0
+
+
+# ---- decode GEMV ----------------------------------------------------------------------
+@pytest.mark.parametrize("M", [1, 4, 16])
+@pytest.mark.parametrize("N,K", [(1024, 2560), (2560, 9728), (264, 512)])
+def test_gemv(dev, M, N, K):
+    idx, pal = make_weight(N, K, seed=M * 31 + N)
+    x = randn_bf16(M, K, seed=M)
+    y = ops.lut_gemv(x.to(dev), _packed(idx, dev), pal.to(dev))
+    want = O.lut_linear_fwd(f32(x), O.dequant(idx.numpy(), pal.numpy()))
+    assert_close(f32(y), want, what=f"gemv M={M}")
+
+
+def test_gemv_grouped_matches_single(dev):
+    shapes = [(4096, 2560), (1024, 2560), (2560, 4096), (264, 512), (9728, 2560)]
+    M = 4
+    items, wants = [], []
+    for i, (N, K) in enumerate(shapes):
+        idx, pal = make_weight(N, K, seed=100 + i)
+        x = randn_bf16(M, K, seed=200 + i)
+        items.append((x.to(dev), _packed(idx, dev), pal.to(dev)))
+        wants.append(O.lut_linear_fwd(f32(x), O.dequant(idx.numpy(), pal.numpy())))
+    grp = ops.GemvGroup(items)
+    outs = grp.run()
+    for (x, p, pl), y, want in zip(items, outs, wants):
+        assert_close(f32(y), want, what="grouped gemv")
+        assert torch.equal(y, ops.lut_gemv(x, p, pl))

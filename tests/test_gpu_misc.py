@@ -1,0 +1,134 @@
+"""GPU parity: LoRA products, RMSNorm, SwiGLU, autograd Functions and the drop-in API."""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from helpers import assert_close, f32, gen, make_weight, randn_bf16
+
+pytestmark = pytest.mark.gpu
+ops = pytest.importorskip("palettize_hip.ops")
+import palettize_hip as P  # noqa: E402
+from palettize_hip import fused_lut_linear_cuda as FL  # noqa: E402
+
+
+@pytest.mark.parametrize("rank", [16, 32])
+def test_lora_weight_grads(dev, rank):
+    M, N, K = 1000, 264, 512
+    x = randn_bf16(M, K, seed=1)
+    gy = randn_bf16(M, N, seed=2)
+    t = randn_bf16(M, rank, seed=3)
+    gt = randn_bf16(M, rank, seed=4)
+    ga, gb = ops.lora_weight_grads(x.to(dev), gy.to(dev), t.to(dev), gt.to(dev), 0.5)
+    assert_close(f32(ga), f32(gt).T.astype(np.float64) @ f32(x), max_rel=1e-4, what="grad_a")
+    assert_close(f32(gb), 0.5 * f32(gy).T.astype(np.float64) @ f32(t), max_rel=1e-4, what="grad_b")
+
+
+@pytest.mark.parametrize("rows,cols", [(64, 2560), (300, 128), (17, 4096)])
+def test_rmsnorm(dev, rows, cols):
+    x = randn_bf16(rows, cols, seed=rows)
+    w = (1 + 0.1 * torch.randn(cols, generator=gen(1))).to(torch.bfloat16)
+    y, rstd = ops.rmsnorm_fwd(x.to(dev), w.to(dev), 1e-6)
+    want, want_r = O.rmsnorm_fwd(f32(x), f32(w), 1e-6)
+    d = np.abs(f32(y) - want)
+    assert np.all(d <= np.abs(want) * 2.0 ** -7 + 1e-30) and np.mean(d == 0) > 0.99
+    assert np.allclose(f32(rstd), want_r, rtol=1e-5)
+    gy = randn_bf16(rows, cols, seed=rows + 1)
+    gx, gw = ops.rmsnorm_bwd(x.to(dev), w.to(dev), rstd, gy.to(dev))
+    wgx, wgw = O.rmsnorm_bwd(f32(x), f32(w), f32(gy), 1e-6)
+    assert_close(f32(gx), wgx, what="rmsnorm grad_x")
+    assert_close(f32(gw), wgw, max_rel=1e-4, what="rmsnorm grad_w")
+
+
+def test_swiglu(dev):
+    n = 8 * 4096
+    g = randn_bf16(n, seed=1, std=3.0)
+    u = randn_bf16(n, seed=2)
+    h = ops.swiglu_fwd(g.to(dev), u.to(dev))
+    want = O.swiglu_fwd(f32(g), f32(u))
+    d = np.abs(f32(h) - want)
+    assert np.all(d <= np.abs(want) * 2.0 ** -7) and np.mean(d == 0) > 0.99
+    gh = randn_bf16(n, seed=3)
+    gg, gu = ops.swiglu_bwd(g.to(dev), u.to(dev), gh.to(dev))
+    wg, wu = O.swiglu_bwd(f32(g), f32(u), f32(gh))
+    assert_close(f32(gg), wg, what="swiglu grad_gate")
+    assert_close(f32(gu), wu, what="swiglu grad_up")
+
+
+def test_lut_linear_autograd_with_lora(dev):
+    M, N, K, r = 256, 384, 512, 16
+    idx, pal = make_weight(N, K, seed=5)
+    x = randn_bf16(M, K, seed=6).to(dev).requires_grad_(True)
+    pal_d = pal.to(dev).requires_grad_(True)
+    A = randn_bf16(r, K, seed=7, std=0.05).to(dev).requires_grad_(True)
+    B = randn_bf16(N, r, seed=8, std=0.05).to(dev).requires_grad_(True)
+    packed = ops.pack_indices(idx.to(dev))
+    y = P.lut_linear(x, packed, pal_d, None, A, B, 2.0)
+    gy = randn_bf16(M, N, seed=9).to(dev)
+    y.backward(gy)
+    W = O.dequant(idx.numpy(), pal.numpy()).astype(np.float64)
+    xs, As, Bs, gys = f32(x), f32(A), f32(B), f32(gy)
+    assert_close(f32(y), xs @ W.T + 2.0 * (xs @ As.T) @ Bs.T, what="y")
+    gt = 2.0 * gys @ Bs
+    assert_close(f32(x.grad), gys @ W + gt @ As, what="grad_x")
+    assert_close(f32(pal_d.grad), O.grad_palette(xs, gys, idx.numpy()), max_rel=1e-3,
+                 what="grad_palette")
+    assert_close(f32(A.grad), gt.T @ xs, what="grad_A")
+    assert_close(f32(B.grad), gys.T @ (2.0 * xs @ As.T), what="grad_B")
+
+
+def test_dropin_fused_lut_linear_reference_layout(dev):
+    # reference layout: indices (K, N) int8, palette (G, 4) bf16 per 256 output channels
+    M, K, N, GS = 96, 640, 512, 256   # K not a multiple of 256 exercises the padding
+    g = gen(21)
+    idx_kn = torch.randint(0, 4, (K, N), generator=g, dtype=torch.int8)
+    pal = torch.sort(torch.randn(N // GS, 4, generator=g) * 0.02, -1).values.to(torch.bfloat16)
+    bias = (0.1 * torch.randn(N, generator=g)).to(torch.bfloat16)
+    x = randn_bf16(M, K, seed=22)
+    xd = x.to(dev).requires_grad_(True)
+    pd = pal.to(dev).requires_grad_(True)
+    bd = bias.to(dev).requires_grad_(True)
+    y = FL.fused_lut_linear(xd, pd, idx_kn.to(dev), bd, GS)
+    W = O.reference_weight(idx_kn.numpy().astype(np.uint8), f32(pal), GS).astype(np.float64)
+    assert_close(f32(y), f32(x) @ W + f32(bias), what="drop-in y")
+    gy = randn_bf16(M, N, seed=23)
+    y.backward(gy.to(dev))
+    assert_close(f32(xd.grad), f32(gy) @ W.T, what="drop-in grad_x")
+    assert pd.grad.dtype == torch.bfloat16 and pd.grad.shape == (N // GS, 4)
+    dW = f32(x).T.astype(np.float64) @ f32(gy)          # (K, N)
+    want = np.zeros((N // GS, 4))
+    cls = idx_kn.numpy().astype(np.int64)
+    for gg in range(N // GS):
+        for c in range(4):
+            sl = slice(gg * GS, (gg + 1) * GS)
+            want[gg, c] = dW[:, sl][cls[:, sl] == c].sum()
+    assert_close(f32(pd.grad), want, what="drop-in grad_palette")
+    assert_close(f32(bd.grad), f32(gy).sum(0), what="drop-in grad_bias")
+
+
+def test_dropin_soft_reference_layout(dev):
+    M, K, N, GS, tau = 64, 512, 256, 256, 0.5
+    g = gen(31)
+    logits = torch.randn(4, K, N, generator=g).to(torch.float16)
+    pal = torch.sort(torch.randn(N // GS, 4, generator=g) * 0.02, -1).values.to(torch.bfloat16)
+    x = randn_bf16(M, K, seed=32)
+    xd = x.to(dev).requires_grad_(True)
+    pd = pal.to(dev).requires_grad_(True)
+    ld = logits.to(dev).requires_grad_(True)
+    seed_before = FL._SOFT_STEP_SEED
+    y = FL.fused_lut_linear_soft(xd, pd, ld, None, GS, tau)
+    seed = (seed_before + 1) & 0xFFFFFFFF
+    # oracle: LCG noise with the reference indexing, native layout
+    noise = O.c_gumbel_lcg(seed, N, K)
+    lg_nk4 = f32(logits).transpose(2, 1, 0)
+    pal_nat = O.expand_reference_palette(f32(pal), N, K, GS)
+    _, _, w_hard = O.soft_weights(lg_nk4, noise, pal_nat, tau, O.W_HARD_NOISY)
+    assert_close(f32(y), f32(x) @ O.bf16_round(w_hard.astype(np.float32)).T.astype(np.float64),
+                 what="drop-in soft y")
+    gy = randn_bf16(M, N, seed=33)
+    y.backward(gy.to(dev))
+    gl, gp = O.soft_backward(f32(x), f32(gy), lg_nk4, noise, pal_nat, tau)
+    assert ld.grad.shape == (4, K, N) and ld.grad.dtype == torch.float16
+    assert_close(f32(ld.grad), gl.transpose(2, 1, 0), what="drop-in grad_logits")
+    want_gp = gp.reshape(N // GS, GS, -1, 4).sum(axis=(1, 2))
+    assert_close(f32(pd.grad), want_gp, what="drop-in soft grad_palette")
