@@ -178,6 +178,10 @@ def cpu_baseline(budget_s=12.0):
                        f"at M={M} rows, {passes} passes in {el:.1f}s")
 
 
+def _log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -209,6 +213,7 @@ def main():
                       "M": M_TRAIN, "global_batch": 32, "seq_len": 512, "parallelism": "none (1 GPU)"}}
 
     if args.only in (None, "hard"):
+        _log("hard: building inputs")
         step = HardStep(dev)
         for _ in range(args.warmup):
             step.run()
@@ -232,12 +237,15 @@ def main():
                            "traffic": None}
         out["kernels"] = {k: {"tflops": round(v["tflops"], 1),
                               "ms_per_step": round(v["ms"] / args.steps, 3)} for k, v in kr.items()}
+        _log(f"hard: {ms:.3f} ms/step, {tflops:.1f} TFLOP/s")
         del step
         torch.cuda.empty_cache()
     if args.only in (None, "gemv"):
         out["gemv"] = bench_gemv(dev)
+        _log(f"gemv: {out['gemv']}")
     if not args.no_cpu and args.only is None:
         out["cpu_baseline"] = cpu_baseline()
+        _log("cpu baseline done")
     print(json.dumps(out), flush=True)
 
 
