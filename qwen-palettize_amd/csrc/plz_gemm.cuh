@@ -1,4 +1,4 @@
-// MFMA GEMM core for gfx950: C[I,J] = sum_r A(i,r) * B(j,r), bf16 operands, fp32 accumulate.
+// Skinny MFMA GEMM core for gfx950 (rank-r LoRA products): C[I,J] = sum_r A(i,r) * B(j,r), bf16 operands, fp32 accumulate.
 //
 // One workgroup = 256 threads = 4 wave64s arranged (BI/WI) x (BJ/WJ); each wave owns a
 // WI x WJ sub-tile built from 16x16 accumulator blocks of v_mfma_f32_16x16x32_bf16.
@@ -12,8 +12,6 @@
 //   LoadRC    dense bf16, element (row, r) at p[row*ld + r]            (r contiguous)
 //   LoadMNC   dense bf16, element (row, r) at p[r*ld + row]            (rows contiguous;
 //             8x8 blocks are transposed in registers before the LDS write)
-//   LoadLutRC palettized W[n,k] with the reduction over k (forward: y = x W^T)
-//   LoadLutNN palettized W[n,k] with the reduction over n (grad_x = grad_y W)
 #pragma once
 #include "plz_common.h"
 
@@ -147,106 +145,6 @@ struct LoadMNC {
           d[j] = perm(hi, lo, sel);
         }
         lds[swz(rb * 8 + i, kb)] = make_uint4(d[0], d[1], d[2], d[3]);
-      }
-    }
-  }
-};
-
-// Palettized W[n,k] (n = tile row), reduction over k. Item = (row, 32 consecutive k).
-template <int ROWS>
-struct LoadLutRC {
-  static constexpr int kItems = ROWS * (BK / 32);
-  static constexpr int kIters = (kItems + 255) / 256;
-  static constexpr int kRegs = 2 * kIters;  // {q0, q1, -, -} + palette
-  __device__ static void load(const GemmArgs& g, int64_t row0, int64_t r0, uint4* regs) {
-    const int64_t wpr = g.Kw / kIdxPerWord, gpr = g.Kw / kPalGroup;
-#pragma unroll
-    for (int it = 0; it < kIters; ++it) {
-      int item = threadIdx.x + 256 * it;
-      int row = item / 2, h = item % 2;
-      int64_t n = row0 + row;
-      uint4 q = make_uint4(0, 0, 0, 0), p = make_uint4(0, 0, 0, 0);
-      if ((kItems % 256 == 0 || item < kItems) && n < g.Nw) {
-        int64_t k = r0 + 32 * h;
-        const u32x2 w = *reinterpret_cast<const u32x2*>(g.packed + n * wpr + k / kIdxPerWord);
-        q.x = w.x; q.y = w.y;
-        p = *reinterpret_cast<const uint4*>(g.pal + (n * gpr + k / kPalGroup) * 4);
-      }
-      regs[2 * it] = q;
-      regs[2 * it + 1] = p;
-    }
-  }
-  __device__ static void store(uint4* lds, const uint4* regs) {
-#pragma unroll
-    for (int it = 0; it < kIters; ++it) {
-      int item = threadIdx.x + 256 * it;
-      if (!(kItems % 256 == 0 || item < kItems)) continue;
-      int row = item / 2, h = item % 2;
-      const uint4 p = regs[2 * it + 1];
-      PalLut t = make_lut(__builtin_bit_cast(float, p.x), __builtin_bit_cast(float, p.y),
-                          __builtin_bit_cast(float, p.z), __builtin_bit_cast(float, p.w));
-      uint32_t o[8];
-      dequant16(regs[2 * it].x, t, o);
-      lds[swz(row, 4 * h + 0)] = make_uint4(o[0], o[1], o[2], o[3]);
-      lds[swz(row, 4 * h + 1)] = make_uint4(o[4], o[5], o[6], o[7]);
-      dequant16(regs[2 * it].y, t, o);
-      lds[swz(row, 4 * h + 2)] = make_uint4(o[0], o[1], o[2], o[3]);
-      lds[swz(row, 4 * h + 3)] = make_uint4(o[4], o[5], o[6], o[7]);
-    }
-  }
-};
-
-// Palettized W[n,k] seen as B(k, n): tile rows are k, the reduction runs over n.
-// Item = (2 consecutive n, 16 consecutive k); the tile's k range must sit inside one
-// 256-wide palette group (ROWS divides 256 and row0 is a multiple of ROWS).
-template <int ROWS>
-struct LoadLutNN {
-  static constexpr int kKW = ROWS / 16;                 // packed words per tile row-span
-  static constexpr int kItems = kKW * (BK / 2);
-  static constexpr int kIters = (kItems + 255) / 256;
-  static constexpr int kRegs = 3 * kIters;              // {qa, qb}, pal a, pal b
-  __device__ static void load(const GemmArgs& g, int64_t row0, int64_t r0, uint4* regs) {
-    const int64_t wpr = g.Kw / kIdxPerWord, gpr = g.Kw / kPalGroup;
-#pragma unroll
-    for (int it = 0; it < kIters; ++it) {
-      int item = threadIdx.x + 256 * it;
-      int kw = item % kKW, np = item / kKW;
-      int64_t n = r0 + 2 * np, k = row0 + 16 * kw;
-      uint4 q = make_uint4(0, 0, 0, 0), pa = make_uint4(0, 0, 0, 0), pb = pa;
-      if ((kItems % 256 == 0 || item < kItems) && k < g.Kw) {
-        if (n < g.Nw) {
-          q.x = (uint32_t)g.packed[n * wpr + k / kIdxPerWord];
-          pa = *reinterpret_cast<const uint4*>(g.pal + (n * gpr + k / kPalGroup) * 4);
-        }
-        if (n + 1 < g.Nw) {
-          q.y = (uint32_t)g.packed[(n + 1) * wpr + k / kIdxPerWord];
-          pb = *reinterpret_cast<const uint4*>(g.pal + ((n + 1) * gpr + k / kPalGroup) * 4);
-        }
-      }
-      regs[3 * it] = q;
-      regs[3 * it + 1] = pa;
-      regs[3 * it + 2] = pb;
-    }
-  }
-  __device__ static void store(uint4* lds, const uint4* regs) {
-    uint32_t* lds32 = reinterpret_cast<uint32_t*>(lds);
-#pragma unroll
-    for (int it = 0; it < kIters; ++it) {
-      int item = threadIdx.x + 256 * it;
-      if (!(kItems % 256 == 0 || item < kItems)) continue;
-      int kw = item % kKW, np = item / kKW;
-      const uint4 pa = regs[3 * it + 1], pb = regs[3 * it + 2];
-      PalLut ta = make_lut(__builtin_bit_cast(float, pa.x), __builtin_bit_cast(float, pa.y),
-                           __builtin_bit_cast(float, pa.z), __builtin_bit_cast(float, pa.w));
-      PalLut tb = make_lut(__builtin_bit_cast(float, pb.x), __builtin_bit_cast(float, pb.y),
-                           __builtin_bit_cast(float, pb.z), __builtin_bit_cast(float, pb.w));
-      uint32_t o[16];
-      dequant16_pair(regs[3 * it].x, ta, regs[3 * it].y, tb, o);
-      const int rpos = 2 * np;  // reduction position of row n inside the tile
-#pragma unroll
-      for (int kk = 0; kk < 16; ++kk) {
-        int row = 16 * kw + kk;
-        lds32[swz(row, rpos / 8) * 4 + (rpos % 8) / 2] = o[kk];
       }
     }
   }

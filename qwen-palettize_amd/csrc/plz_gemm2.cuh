@@ -1,0 +1,157 @@
+// Large-tile MFMA GEMM core for gfx950 (the M = 16384 training shapes).
+//
+// C[I,J] = sum_r A(i,r) B(j,r), bf16 operands, fp32 accumulation, 256 threads = 4 wave64s
+// in a 2x2 grid, workgroup tile 256x256, 128x128 per wave (4x4 blocks of
+// v_mfma_f32_32x32x16_bf16, 256 accumulator registers), reduction stages of BK = 64,
+// double-buffered in LDS (2 x 64 KB).
+//
+// Each operand tile sits in LDS in one of two layouts:
+//   Row tile  [row][r]: 16-byte chunks of 8 consecutive r, chunk index XOR (row & 7).
+//             Fragments: one ds_read_b128 per lane (row = lane%32, chunk = 2*ks + lane/32).
+//   Col tile  [r][row]: the operand's own memory order when rows are contiguous
+//             (MN-contiguous: grad_y and x in dW, W in grad_x). Chunks of 8 consecutive
+//             rows, chunk index XOR 2*(r & 3). Fragments: two ds_read_b64_tr_b16 per lane.
+//             Within each 16-lane group lane i points at rows 4*(i%4)..+3 of reduction
+//             index kbase + i/4; the instruction hands lane j elements j, j+16, j+32, j+48
+//             of the group's 64 loaded values, i.e. row j at kbase..kbase+3 -- the MFMA
+//             operand order (k-slots 8*(lane/32) + s), the same as a Row-tile fragment.
+// Dense operands are copied global -> LDS by global_load_lds_dwordx4 (no VGPR staging;
+// lane l of an instruction writes LDS bytes base + 16*l, so the swizzle is applied to the
+// global address each lane reads). The palettized operand W[n,k] is dequantised by all
+// threads into a Row tile (forward, rows = n) or a Col tile (grad_x, rows = k, reduction n).
+#pragma once
+#include "plz_common.h"
+
+namespace plz {
+namespace g2 {
+
+constexpr int BK = 64;
+constexpr int TILE = 256;            // BI = BJ
+constexpr int TILE_BYTES = TILE * BK * 2;  // 32 KB per operand per stage
+
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
+
+__device__ __forceinline__ int row_chunk(int row, int c) { return row * (BK / 8) + (c ^ (row & 7)); }
+__device__ __forceinline__ int col_swz(int kr) { return 2 * (kr & 3); }
+__device__ __forceinline__ int col_chunk(int kr, int c) { return kr * (TILE / 8) + (c ^ col_swz(kr)); }
+
+struct Args {
+  const uint16_t* a; int64_t lda;   // dense A
+  const uint16_t* b; int64_t ldb;   // dense B
+  const int32_t* packed; const float* pal; int64_t Nw, Kw;  // palettized operand
+  int64_t I, J, R, r_split;
+  // rank-r second segment (R2 <= BK): A2 row-major [I, R2]; B2 row-major [J, R2] when the
+  // main B is a Row tile, reduction-major [R2, J] when it is a Col tile
+  const uint16_t* a2; const uint16_t* b2; int R2;
+  // epilogue
+  void* c; int64_t ldc; const uint16_t* bias; float alpha; float* partial;
+  const uint16_t* logits; const float* noise; float inv_tau, glog_scale; uint16_t* grad_logits;
+  int logits_f16;
+  int tiles_i, tiles_j;
+};
+
+// ---- dense operand copy, global -> LDS ---------------------------------------------------
+// Row tile from p[row*ld + r] (r contiguous): 2048 chunks, 8 instructions of 256 lanes.
+__device__ __forceinline__ void copy_row_tile(lds_u8* lds, const uint16_t* p, int64_t ld,
+                                              int64_t row0, int64_t nrows, int64_t r0) {
+#pragma unroll
+  for (int it = 0; it < 8; ++it) {
+    const int pch = it * 256 + threadIdx.x;          // physical chunk written by this lane
+    const int row = pch >> 3, c = (pch & 7) ^ (row & 7);
+    int64_t gr = row0 + row;
+    gr = gr < nrows ? gr : nrows - 1;                 // rows past the end: any valid row
+    const uint16_t* src = p + gr * ld + r0 + c * 8;
+    __builtin_amdgcn_global_load_lds(src, lds + it * 4096 + (threadIdx.x & ~63) * 16, 16, 0, 0);
+  }
+}
+// Col tile from p[r*ld + row] (rows contiguous): 64 reduction rows x 32 chunks.
+__device__ __forceinline__ void copy_col_tile(lds_u8* lds, const uint16_t* p, int64_t ld,
+                                              int64_t row0, int64_t nrows, int64_t r0) {
+#pragma unroll
+  for (int it = 0; it < 8; ++it) {
+    const int pch = it * 256 + threadIdx.x;
+    const int kr = pch >> 5, c = (pch & 31) ^ col_swz(kr);
+    int64_t gr = row0 + c * 8;
+    gr = gr < nrows ? gr : 0;                          // chunks past the end: any valid chunk
+    const uint16_t* src = p + (r0 + kr) * ld + gr;
+    __builtin_amdgcn_global_load_lds(src, lds + it * 4096 + (threadIdx.x & ~63) * 16, 16, 0, 0);
+  }
+}
+
+// ---- palettized operand: one thread per (row n, 64 k) -------------------------------------
+struct LutRegs {
+  uint4 q;
+  float4 p;
+};
+// Forward: tile rows are n (256 rows x 64 k); thread t owns row t.
+__device__ __forceinline__ void lut_row_load(const Args& g, int64_t n0, int64_t k0, LutRegs& r) {
+  const int64_t n = n0 + threadIdx.x;
+  r.q = make_uint4(0, 0, 0, 0);
+  r.p = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (n < g.Nw) {
+    r.q = *reinterpret_cast<const uint4*>(g.packed + n * (g.Kw / 16) + k0 / 16);
+    r.p = *reinterpret_cast<const float4*>(g.pal + (n * (g.Kw / 256) + k0 / 256) * 4);
+  }
+}
+__device__ __forceinline__ void lut_row_store(uint4* lds, const LutRegs& r) {
+  const PalLut t = make_lut(r.p.x, r.p.y, r.p.z, r.p.w);
+  const int row = threadIdx.x;
+  const uint32_t qs[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    uint32_t o[8];
+    dequant16(qs[w], t, o);
+    lds[row_chunk(row, 2 * w)] = make_uint4(o[0], o[1], o[2], o[3]);
+    lds[row_chunk(row, 2 * w + 1)] = make_uint4(o[4], o[5], o[6], o[7]);
+  }
+}
+// grad_x: tile rows are k (256), reduction n (64); thread t owns n = n0 + t/4 and
+// k = k0 + 64*(t%4) .. +64. The tile's k range lies in one palette group (k0 % 256 == 0).
+__device__ __forceinline__ void lut_col_load(const Args& g, int64_t k0, int64_t n0, LutRegs& r) {
+  const int64_t n = n0 + (threadIdx.x >> 2);
+  const int64_t k = k0 + 64 * (threadIdx.x & 3);
+  r.q = make_uint4(0, 0, 0, 0);
+  r.p = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (n < g.Nw && k < g.Kw) {
+    r.q = *reinterpret_cast<const uint4*>(g.packed + n * (g.Kw / 16) + k / 16);
+    r.p = *reinterpret_cast<const float4*>(g.pal + (n * (g.Kw / 256) + k / 256) * 4);
+  }
+}
+__device__ __forceinline__ void lut_col_store(uint4* lds, const LutRegs& r) {
+  const PalLut t = make_lut(r.p.x, r.p.y, r.p.z, r.p.w);
+  const int kr = threadIdx.x >> 2, cb = 8 * (threadIdx.x & 3);
+  const uint32_t qs[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    uint32_t o[8];
+    dequant16(qs[w], t, o);
+    lds[col_chunk(kr, cb + 2 * w)] = make_uint4(o[0], o[1], o[2], o[3]);
+    lds[col_chunk(kr, cb + 2 * w + 1)] = make_uint4(o[4], o[5], o[6], o[7]);
+  }
+}
+
+// ---- fragments (v_mfma_f32_32x32x16_bf16: lane l holds row l%32, k-slots 8*(l/32)..+7) --
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ bf16x8 frag_row(const uint4* lds, int rowbase, int ks, int lane) {
+  return __builtin_bit_cast(bf16x8, lds[row_chunk(rowbase + (lane & 31), 2 * ks + (lane >> 5))]);
+}
+// Col tile: per 16-lane group j = lane/16 the rows 16*(j&1)..+15 at k-group j>>1.
+__device__ __forceinline__ bf16x8 frag_col(const lds_u8* lds, int rowbase, int ks, int lane) {
+  const int j = lane >> 4, i = lane & 15, t = i >> 2, q = i & 3;
+  const int row = rowbase + 16 * (j & 1) + 4 * q;
+  const int kr1 = 16 * ks + 8 * (j >> 1) + t, kr2 = kr1 + 4;
+  const int c = row >> 3, off = (row & 7) * 2;
+  const v4i16 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (lds_v4i16*)(lds + col_chunk(kr1, c) * 16 + off));
+  const v4i16 v2 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (lds_v4i16*)(lds + col_chunk(kr2, c) * 16 + off));
+  typedef short v8i16 __attribute__((ext_vector_type(8)));
+  const v8i16 v = __builtin_shufflevector(v1, v2, 0, 1, 2, 3, 4, 5, 6, 7);
+  return __builtin_bit_cast(bf16x8, v);
+}
+
+}  // namespace g2
+}  // namespace plz

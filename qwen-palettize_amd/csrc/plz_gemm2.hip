@@ -1,0 +1,568 @@
+// The large GEMMs of the LUT-linear path on the 256x256 MFMA core (plz_gemm2.cuh):
+//
+//   plz_lut_linear_fwd          y = x W^T (+ bias) (+ t B^T)     fused_lut_kernel.cu:309-518
+//   plz_lut_linear_bwd_x        grad_x = grad_y W (+ gt A)       fused_lut_kernel.cu:551-720
+//   plz_lut_linear_bwd_palette  class-reduced dW = grad_y^T x    fused_lut_kernel.cu:902-1123
+//   plz_soft_bwd                soft grad_logits / grad_palette in the dW epilogue
+//                               (fused_lut_kernel.cu:1877-1924, triton_soft_backward.py:227-325)
+//   plz_linear_fwd_dense / plz_linear_bwd_x_dense   the same on a materialised bf16 W
+//                               (fused_lut_linear_cuda.py:912, 944)
+#include "plz_gemm2.cuh"
+#include "palettize_hip.h"
+
+namespace plz {
+namespace g2 {
+
+enum { OP_ROW = 0, OP_COL = 1, OP_LUT_ROW = 2, OP_LUT_COL = 3 };
+enum { EPI_BF16 = 0, EPI_PAL = 1, EPI_SOFT = 2 };
+
+// Masked register-path copies for a partial reduction stage (r >= rend reads as zero) and for
+// the rank-r second segment.
+__device__ __forceinline__ void copy_row_tile_masked(uint4* lds, const uint16_t* p, int64_t ld,
+                                                     int64_t row0, int64_t nrows, int64_t r0,
+                                                     int64_t rend) {
+#pragma unroll
+  for (int it = 0; it < 8; ++it) {
+    const int ch = it * 256 + threadIdx.x;
+    const int row = ch >> 3, c = ch & 7;
+    const int64_t gr = row0 + row, gk = r0 + 8 * c;
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (gr < nrows && gk < rend) v = *reinterpret_cast<const uint4*>(p + gr * ld + gk);
+    lds[row_chunk(row, c)] = v;
+  }
+}
+__device__ __forceinline__ void copy_col_tile_masked(uint4* lds, const uint16_t* p, int64_t ld,
+                                                     int64_t row0, int64_t nrows, int64_t r0,
+                                                     int64_t rend) {
+#pragma unroll
+  for (int it = 0; it < 8; ++it) {
+    const int ch = it * 256 + threadIdx.x;
+    const int kr = ch >> 5, c = ch & 31;
+    const int64_t gr = row0 + 8 * c, gk = r0 + kr;
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (gr < nrows && gk < rend) v = *reinterpret_cast<const uint4*>(p + gk * ld + gr);
+    lds[col_chunk(kr, c)] = v;
+  }
+}
+
+__device__ __forceinline__ int ptile(int row, int col) {  // 128 x 256 fp32 staging tile
+  return row * 256 + ((((col >> 2) ^ (row & 63))) << 2) + (col & 3);
+}
+
+// One reduction stage of MFMAs on LDS tiles: 4 k-steps of 16, 4x4 blocks of 32x32 per wave.
+// Fragments are double-buffered in registers: the LDS reads of k-step ks+1 are issued before
+// the 16 MFMAs of k-step ks, so one wave per SIMD keeps the matrix core busy.
+template <bool A_COL, bool B_COL>
+__device__ __forceinline__ void load_frags(const lds_u8* a_s, const lds_u8* b_s, int ks, int wi,
+                                           int wj, int lane, bf16x8 (&a)[4], bf16x8 (&b)[4]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    a[i] = A_COL ? frag_col(a_s, wi * 128 + 32 * i, ks, lane)
+                 : frag_row((const uint4*)a_s, wi * 128 + 32 * i, ks, lane);
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    b[j] = B_COL ? frag_col(b_s, wj * 128 + 32 * j, ks, lane)
+                 : frag_row((const uint4*)b_s, wj * 128 + 32 * j, ks, lane);
+}
+__device__ __forceinline__ void mma16(f32x16 (&acc)[4][4], const bf16x8 (&a)[4], const bf16x8 (&b)[4]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+}
+template <bool A_COL, bool B_COL>
+__device__ __forceinline__ void mma_stage(const lds_u8* a_s, const lds_u8* b_s, f32x16 (&acc)[4][4],
+                                          int wi, int wj, int lane) {
+  bf16x8 a0[4], b0[4], a1[4], b1[4];
+  load_frags<A_COL, B_COL>(a_s, b_s, 0, wi, wj, lane, a0, b0);
+  load_frags<A_COL, B_COL>(a_s, b_s, 1, wi, wj, lane, a1, b1);
+  mma16(acc, a0, b0);
+  load_frags<A_COL, B_COL>(a_s, b_s, 2, wi, wj, lane, a0, b0);
+  mma16(acc, a1, b1);
+  load_frags<A_COL, B_COL>(a_s, b_s, 3, wi, wj, lane, a1, b1);
+  mma16(acc, a0, b0);
+  mma16(acc, a1, b1);
+}
+
+template <int KA, int KB, int EPI>
+__global__ __launch_bounds__(256) void gemm2_kernel(const Args g) {
+  extern __shared__ uint4 smem[];
+  lds_u8* lbase = (lds_u8*)smem;
+  constexpr bool A_COL = KA == OP_COL;
+  constexpr bool B_COL = KB == OP_COL || KB == OP_LUT_COL;
+
+  int bid = blockIdx.x;
+  const int T = g.tiles_i * g.tiles_j;
+  if (T % 8 == 0) bid = (bid % 8) * (T / 8) + bid / 8;
+  const int GROUP = 8;
+  const int per_group = GROUP * g.tiles_j;
+  const int first_i = (bid / per_group) * GROUP;
+  const int gsz = min(g.tiles_i - first_i, GROUP);
+  const int tile_i = first_i + (bid % per_group) % gsz;
+  const int tile_j = (bid % per_group) / gsz;
+  const int64_t i0 = (int64_t)tile_i * TILE, j0 = (int64_t)tile_j * TILE;
+  const int64_t rbeg = (int64_t)blockIdx.z * g.r_split;
+  const int64_t rend = min(g.R, rbeg + g.r_split);
+  const int64_t rlen = rend > rbeg ? rend - rbeg : 0;
+  const int nfull = (int)(rlen / BK);
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wi = wave >> 1, wj = wave & 1;
+
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+  // Stage list: nfull full stages (asynchronous global->LDS copies), then optionally one
+  // partial stage (zero-filled register copy) and one rank-r LoRA stage. The LoRA operands
+  // have the same LDS layouts as the main ones (A row-major; B row tile in the forward,
+  // col tile in grad_x), so every stage runs the same MFMA body.
+  const bool tail = (rlen % BK) != 0;
+  const bool lora = EPI == EPI_BF16 && g.R2 > 0 && blockIdx.z == 0;
+  const int nst = nfull + (tail ? 1 : 0) + (lora ? 1 : 0);
+
+  LutRegs lr;
+  auto issue = [&](int s, int kt) {
+    lds_u8* As = lbase + s * 2 * TILE_BYTES;
+    lds_u8* Bs = As + TILE_BYTES;
+    if (kt < nfull) {
+      const int64_t r0 = rbeg + (int64_t)kt * BK;
+      if (KA == OP_ROW) copy_row_tile(As, g.a, g.lda, i0, g.I, r0);
+      else copy_col_tile(As, g.a, g.lda, i0, g.I, r0);
+      if (KB == OP_ROW) copy_row_tile(Bs, g.b, g.ldb, j0, g.J, r0);
+      else if (KB == OP_COL) copy_col_tile(Bs, g.b, g.ldb, j0, g.J, r0);
+      else if (KB == OP_LUT_ROW) lut_row_load(g, j0, r0, lr);
+      else lut_col_load(g, j0, r0, lr);
+    } else if (tail && kt == nfull) {
+      const int64_t r0 = rbeg + (int64_t)nfull * BK;
+      if (KA == OP_ROW) copy_row_tile_masked((uint4*)As, g.a, g.lda, i0, g.I, r0, rend);
+      else copy_col_tile_masked((uint4*)As, g.a, g.lda, i0, g.I, r0, rend);
+      if (KB == OP_ROW) copy_row_tile_masked((uint4*)Bs, g.b, g.ldb, j0, g.J, r0, rend);
+      else if (KB == OP_COL) copy_col_tile_masked((uint4*)Bs, g.b, g.ldb, j0, g.J, r0, rend);
+      else if (KB == OP_LUT_ROW) { lut_row_load(g, j0, r0, lr); lut_row_store((uint4*)Bs, lr); }
+      else { lut_col_load(g, j0, r0, lr); lut_col_store((uint4*)Bs, lr); }
+    } else {
+      copy_row_tile_masked((uint4*)As, g.a2, g.R2, i0, g.I, 0, g.R2);
+      if (B_COL) copy_col_tile_masked((uint4*)Bs, g.b2, g.J, j0, g.J, 0, g.R2);
+      else copy_row_tile_masked((uint4*)Bs, g.b2, g.R2, j0, g.J, 0, g.R2);
+    }
+  };
+  auto finish = [&](int s, int kt) {
+    uint4* Bs = (uint4*)(lbase + s * 2 * TILE_BYTES + TILE_BYTES);
+    if (kt < nfull) {
+      if (KB == OP_LUT_ROW) lut_row_store(Bs, lr);
+      if (KB == OP_LUT_COL) lut_col_store(Bs, lr);
+    }
+  };
+
+  if (nst > 0) {
+    issue(0, 0);
+    finish(0, 0);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  for (int kt = 0; kt < nst; ++kt) {
+    const int cur = kt & 1;
+    const bool more = kt + 1 < nst;
+    if (more) issue(cur ^ 1, kt + 1);
+    const lds_u8* As = lbase + cur * 2 * TILE_BYTES;
+    mma_stage<A_COL, B_COL>(As, As + TILE_BYTES, acc, wi, wj, lane);
+    if (more) finish(cur ^ 1, kt + 1);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
+
+  // ---- epilogues ----------------------------------------------------------------------
+  // acc[ti][tj][e]: row wi*128 + 32*ti + 8*(e/4) + 4*(lane/32) + e%4, col wj*128 + 32*tj + lane%32
+  if (EPI == EPI_BF16) {
+    uint16_t* C = reinterpret_cast<uint16_t*>(g.c);
+#pragma unroll
+    for (int tj = 0; tj < 4; ++tj) {
+      const int64_t j = j0 + wj * 128 + 32 * tj + (lane & 31);
+      if (j >= g.J) continue;
+      const float bj = g.bias ? bf2f(g.bias[j]) : 0.f;
+#pragma unroll
+      for (int ti = 0; ti < 4; ++ti)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int64_t i = i0 + wi * 128 + 32 * ti + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+          if (i < g.I) C[i * g.ldc + j] = (uint16_t)f2bf(g.alpha * acc[ti][tj][e] + bj);
+        }
+    }
+    return;
+  }
+
+  // dW tile (rows n = i, cols k = j) staged in two passes of 128 rows of fp32: pass p holds
+  // rows wi*128 + 64p .. +64 of every wave (staging row sr <-> tile row
+  // (sr/64)*128 + 64p + sr%64), so half of each wave's accumulators are dead after pass 0.
+  float* sC = reinterpret_cast<float*>(smem);
+  const int64_t segs = g.J / 128;
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {  // unrolled: acc must only see constant indices
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+      const int ti = 2 * half + tt;
+#pragma unroll
+      for (int tj = 0; tj < 4; ++tj)
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+          sC[ptile(wi * 64 + 32 * tt + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3),
+                   wj * 128 + 32 * tj + (lane & 31))] = acc[ti][tj][e];
+    }
+    __syncthreads();
+    if (EPI == EPI_PAL) {
+      const int row = threadIdx.x >> 1, h = threadIdx.x & 1;
+      const int64_t n = i0 + (row >> 6) * 128 + 64 * half + (row & 63);
+      const int64_t kseg = j0 + 128 * h;
+      if (n < g.I && kseg < g.J) {
+        const uint4* qp = reinterpret_cast<const uint4*>(g.packed + n * (g.Kw / 16) + kseg / 16);
+        float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+#pragma unroll
+        for (int qv = 0; qv < 2; ++qv) {
+          const uint4 q4 = qp[qv];
+          const uint32_t qs[4] = {q4.x, q4.y, q4.z, q4.w};
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+#pragma unroll
+            for (int cc = 0; cc < 4; ++cc) {
+              const int col = 128 * h + 64 * qv + 16 * w + 4 * cc;
+              const float4 v = *reinterpret_cast<const float4*>(&sC[ptile(row, col)]);
+              const float vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                const uint32_t c = (qs[w] >> (2 * (4 * cc + e))) & 3u;
+                s0 += c == 0 ? vv[e] : 0.f;
+                s1 += c == 1 ? vv[e] : 0.f;
+                s2 += c == 2 ? vv[e] : 0.f;
+                s3 += c == 3 ? vv[e] : 0.f;
+              }
+            }
+          }
+        }
+        float* dst = g.partial + (((int64_t)blockIdx.z * g.I + n) * segs + kseg / 128) * 4;
+        *reinterpret_cast<float4*>(dst) = make_float4(s0, s1, s2, s3);
+      }
+    } else {  // EPI_SOFT: each wave walks (row, 128-k segment) items; lane = 2 consecutive k
+      for (int item = wave; item < 256; item += 4) {
+        const int row = item >> 1, h = item & 1;
+        const int64_t n = i0 + (row >> 6) * 128 + 64 * half + (row & 63);
+        const int64_t k = j0 + 128 * h + 2 * lane;
+        if (n >= g.I || j0 + 128 * h >= g.J) continue;
+        const float2 gw = *reinterpret_cast<const float2*>(&sC[ptile(row, 128 * h + 2 * lane)]);
+        const float4 pal = *reinterpret_cast<const float4*>(g.pal + (n * (g.J / 256) + k / 256) * 4);
+        const float pc[4] = {pal.x, pal.y, pal.z, pal.w};
+        const int64_t e0 = (n * g.J + k) * 4;
+        const uint4 lg = *reinterpret_cast<const uint4*>(g.logits + e0);
+        const float4 z0 = *reinterpret_cast<const float4*>(g.noise + e0);
+        const float4 z1 = *reinterpret_cast<const float4*>(g.noise + e0 + 4);
+        const uint32_t lw[4] = {lg.x, lg.y, lg.z, lg.w};
+        const float nz[8] = {z0.x, z0.y, z0.z, z0.w, z1.x, z1.y, z1.z, z1.w};
+        float sp[4] = {0.f, 0.f, 0.f, 0.f};
+        uint32_t out[4];
+#pragma unroll
+        for (int el = 0; el < 2; ++el) {
+          float a[4];
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            const uint32_t bits = (lw[2 * el + c / 2] >> (16 * (c & 1))) & 0xffffu;
+            a[c] = ((g.logits_f16 ? h2f(bits) : bf2f(bits)) + nz[4 * el + c]) * g.inv_tau;
+          }
+          const float m = fmaxf(fmaxf(a[0], a[1]), fmaxf(a[2], a[3]));
+          float ex[4], s = 0.f;
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            ex[c] = __expf(a[c] - m);
+            s += ex[c];
+          }
+          const float rs = 1.f / s;
+          float P[4], ws = 0.f;
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            P[c] = ex[c] * rs;
+            ws += P[c] * pc[c];
+          }
+          const float gv = el == 0 ? gw.x : gw.y;
+          uint32_t o16[4];
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            const float gp = gv * P[c];
+            sp[c] += gp;
+            const float gl = g.glog_scale * gp * (pc[c] - ws);
+            o16[c] = g.logits_f16 ? f2h(gl) : f2bf(gl);
+          }
+          out[2 * el] = o16[0] | (o16[1] << 16);
+          out[2 * el + 1] = o16[2] | (o16[3] << 16);
+        }
+        *reinterpret_cast<uint4*>(g.grad_logits + e0) = make_uint4(out[0], out[1], out[2], out[3]);
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+          for (int off = 32; off >= 1; off >>= 1) sp[c] += __shfl_xor(sp[c], off);
+        if (lane == 0) {
+          float* dst = g.partial + (n * segs + (j0 + 128 * h) / 128) * 4;
+          *reinterpret_cast<float4*>(dst) = make_float4(sp[0], sp[1], sp[2], sp[3]);
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
+constexpr size_t kLds = 2 * 2 * TILE_BYTES;  // 128 KB
+
+template <int KA, int KB, int EPI>
+static int launch(Args g, int splits, hipStream_t stream, const char* what) {
+  g.tiles_i = (int)((g.I + TILE - 1) / TILE);
+  g.tiles_j = (int)((g.J + TILE - 1) / TILE);
+  if (g.r_split <= 0) g.r_split = g.R;
+  auto kern = gemm2_kernel<KA, KB, EPI>;
+  static bool attr = false;
+  if (!attr) {
+    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       (int)kLds);
+    if (e != hipSuccess) {
+      set_error("%s: cannot reserve %zu bytes of LDS: %s", what, kLds, hipGetErrorString(e));
+      return PLZ_EHIP;
+    }
+    attr = true;
+  }
+  const int64_t tiles = (int64_t)g.tiles_i * g.tiles_j;
+  if (tiles == 0 || splits == 0) return PLZ_OK;
+  hipLaunchKernelGGL(kern, dim3((unsigned)tiles, 1, (unsigned)splits), dim3(256), kLds, stream, g);
+  return check_launch(what);
+}
+
+// Reduction splits for a grid of `tiles` workgroups (one workgroup per CU at a time):
+// the split count whose grid best fills whole waves of 256 CUs, at least 8 stages per split.
+static int pick_splits(int64_t tiles, int64_t R) {
+  int best = 1;
+  double best_eff = 0.0;
+  const int64_t zmax = R / (8 * BK);
+  for (int z = 1; z <= 32 && z <= (zmax > 0 ? zmax : 1); ++z) {
+    const int64_t wgs = tiles * z;
+    const int64_t waves = (wgs + 255) / 256;
+    const double eff = (double)wgs / (double)(waves * 256);
+    if (eff > best_eff + 0.02) {
+      best_eff = eff;
+      best = z;
+    }
+  }
+  return best;
+}
+static int64_t split_len(int64_t R, int z) {
+  const int64_t per = (R + z - 1) / z;
+  return (per + BK - 1) / BK * BK;
+}
+
+__global__ void reduce_pal_kernel(const float* __restrict__ partial, float* __restrict__ out,
+                                  int64_t N, int64_t G, int Z) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= N * G) return;
+  const int64_t n = t / G, gg = t % G;
+  float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int z = 0; z < Z; ++z) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const float4 v = *reinterpret_cast<const float4*>(
+          partial + (((int64_t)z * N + n) * 2 * G + 2 * gg + h) * 4);
+      s.x += v.x; s.y += v.y; s.z += v.z; s.w += v.w;
+    }
+  }
+  *reinterpret_cast<float4*>(out + t * 4) = s;
+}
+
+static bool a16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+static int palette_splits(int64_t M, int64_t N, int64_t K) {
+  return pick_splits(((N + TILE - 1) / TILE) * ((K + TILE - 1) / TILE), M);
+}
+
+}  // namespace g2
+}  // namespace plz
+
+using namespace plz;
+using namespace plz::g2;
+
+extern "C" {
+
+int plz_lut_linear_fwd(const uint16_t* x, const int32_t* packed, const float* palette,
+                       const uint16_t* bias, const uint16_t* lora_t, const uint16_t* lora_b,
+                       int rank, uint16_t* y, int64_t M, int64_t N, int64_t K, void* stream) {
+  PLZ_REQUIRE(M >= 0 && N >= 0 && K >= 0, "plz_lut_linear_fwd: negative shape");
+  PLZ_REQUIRE(K % 256 == 0, "plz_lut_linear_fwd: K (%lld) must be a multiple of 256", (long long)K);
+  PLZ_REQUIRE(N % 8 == 0, "plz_lut_linear_fwd: N (%lld) must be a multiple of 8", (long long)N);
+  PLZ_REQUIRE(rank >= 0 && rank <= BK && rank % 8 == 0,
+              "plz_lut_linear_fwd: rank (%d) must be a multiple of 8 in [0, 64]", rank);
+  if (M == 0 || N == 0) return PLZ_OK;
+  PLZ_REQUIRE(x && packed && palette && y, "plz_lut_linear_fwd: null pointer");
+  PLZ_REQUIRE(a16(x) && a16(palette) && a16(packed),
+              "plz_lut_linear_fwd: x, packed and palette must be 16-byte aligned");
+  PLZ_REQUIRE(rank == 0 || (lora_t && lora_b && a16(lora_t) && a16(lora_b)),
+              "plz_lut_linear_fwd: rank > 0 needs 16-byte aligned lora_t and lora_b");
+  Args g = {};
+  g.a = x; g.lda = K;
+  g.packed = packed; g.pal = palette; g.Nw = N; g.Kw = K;
+  g.I = M; g.J = N; g.R = K;
+  g.a2 = lora_t; g.b2 = lora_b; g.R2 = rank;
+  g.c = y; g.ldc = N; g.bias = bias; g.alpha = 1.f;
+  return launch<OP_ROW, OP_LUT_ROW, EPI_BF16>(g, 1, (hipStream_t)stream, "plz_lut_linear_fwd");
+}
+
+int plz_lut_linear_bwd_x(const uint16_t* grad_y, const int32_t* packed, const float* palette,
+                         const uint16_t* lora_gt, const uint16_t* lora_a, int rank,
+                         uint16_t* grad_x, int64_t M, int64_t N, int64_t K, void* stream) {
+  PLZ_REQUIRE(M >= 0 && N >= 0 && K >= 0, "plz_lut_linear_bwd_x: negative shape");
+  PLZ_REQUIRE(K % 256 == 0, "plz_lut_linear_bwd_x: K (%lld) must be a multiple of 256",
+              (long long)K);
+  PLZ_REQUIRE(N % 8 == 0, "plz_lut_linear_bwd_x: N (%lld) must be a multiple of 8", (long long)N);
+  PLZ_REQUIRE(rank >= 0 && rank <= BK && rank % 8 == 0,
+              "plz_lut_linear_bwd_x: rank (%d) must be a multiple of 8 in [0, 64]", rank);
+  if (M == 0 || K == 0) return PLZ_OK;
+  PLZ_REQUIRE(grad_y && packed && palette && grad_x, "plz_lut_linear_bwd_x: null pointer");
+  PLZ_REQUIRE(a16(grad_y) && a16(palette) && a16(packed),
+              "plz_lut_linear_bwd_x: grad_y, packed and palette must be 16-byte aligned");
+  PLZ_REQUIRE(rank == 0 || (lora_gt && lora_a && a16(lora_gt) && a16(lora_a)),
+              "plz_lut_linear_bwd_x: rank > 0 needs 16-byte aligned lora_gt and lora_a");
+  Args g = {};
+  g.a = grad_y; g.lda = N;
+  g.packed = packed; g.pal = palette; g.Nw = N; g.Kw = K;
+  g.I = M; g.J = K; g.R = N;
+  g.a2 = lora_gt; g.b2 = lora_a; g.R2 = rank;
+  g.c = grad_x; g.ldc = K; g.alpha = 1.f;
+  return launch<OP_ROW, OP_LUT_COL, EPI_BF16>(g, 1, (hipStream_t)stream, "plz_lut_linear_bwd_x");
+}
+
+size_t plz_lut_linear_bwd_palette_workspace(int64_t M, int64_t N, int64_t K) {
+  if (M <= 0 || N <= 0 || K <= 0) return 0;
+  return (size_t)palette_splits(M, N, K) * N * (K / 128) * 4 * sizeof(float);
+}
+
+int plz_lut_linear_bwd_palette(const uint16_t* x, const uint16_t* grad_y, const int32_t* packed,
+                               float* grad_palette, void* workspace, size_t workspace_bytes,
+                               int64_t M, int64_t N, int64_t K, void* stream) {
+  PLZ_REQUIRE(M >= 0 && N >= 0 && K >= 0, "plz_lut_linear_bwd_palette: negative shape");
+  PLZ_REQUIRE(K % 256 == 0, "plz_lut_linear_bwd_palette: K (%lld) must be a multiple of 256",
+              (long long)K);
+  PLZ_REQUIRE(N % 8 == 0, "plz_lut_linear_bwd_palette: N (%lld) must be a multiple of 8",
+              (long long)N);
+  if (N == 0 || K == 0) return PLZ_OK;
+  PLZ_REQUIRE(packed && grad_palette, "plz_lut_linear_bwd_palette: null pointer");
+  if (M == 0) {
+    hipMemsetAsync(grad_palette, 0, (size_t)N * (K / 256) * 16, (hipStream_t)stream);
+    return check_launch("plz_lut_linear_bwd_palette");
+  }
+  PLZ_REQUIRE(x && grad_y && a16(x) && a16(grad_y) && a16(packed),
+              "plz_lut_linear_bwd_palette: x, grad_y and packed must be non-null, 16-byte aligned");
+  const size_t need = plz_lut_linear_bwd_palette_workspace(M, N, K);
+  if (!workspace || workspace_bytes < need) {
+    set_error("plz_lut_linear_bwd_palette: workspace of %zu bytes needed, %zu given", need,
+              workspace_bytes);
+    return PLZ_EWORKSPACE;
+  }
+  const int z = palette_splits(M, N, K);
+  Args g = {};
+  g.a = grad_y; g.lda = N;   // A(i=n, r=m) = grad_y[m, n]   (Col tile)
+  g.b = x; g.ldb = K;        // B(j=k, r=m) = x[m, k]        (Col tile)
+  g.packed = packed; g.Nw = N; g.Kw = K;
+  g.I = N; g.J = K; g.R = M; g.r_split = split_len(M, z);
+  g.partial = reinterpret_cast<float*>(workspace);
+  int rc = launch<OP_COL, OP_COL, EPI_PAL>(g, z, (hipStream_t)stream, "plz_lut_linear_bwd_palette");
+  if (rc != PLZ_OK) return rc;
+  const int64_t G = K / 256, n_out = N * G;
+  hipLaunchKernelGGL(reduce_pal_kernel, dim3((unsigned)((n_out + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, g.partial, grad_palette, N, G, z);
+  return check_launch("plz_lut_linear_bwd_palette/reduce");
+}
+
+int plz_linear_fwd_dense(const uint16_t* x, const uint16_t* w, const uint16_t* bias,
+                         const uint16_t* lora_t, const uint16_t* lora_b, int rank, uint16_t* y,
+                         int64_t M, int64_t N, int64_t K, void* stream) {
+  PLZ_REQUIRE(M >= 0 && N >= 0 && K >= 0, "plz_linear_fwd_dense: negative shape");
+  PLZ_REQUIRE(K % 8 == 0 && N % 8 == 0, "plz_linear_fwd_dense: K and N must be multiples of 8");
+  PLZ_REQUIRE(rank >= 0 && rank <= BK && rank % 8 == 0,
+              "plz_linear_fwd_dense: rank (%d) must be a multiple of 8 in [0, 64]", rank);
+  if (M == 0 || N == 0) return PLZ_OK;
+  PLZ_REQUIRE(x && w && y && a16(x) && a16(w),
+              "plz_linear_fwd_dense: x, w, y must be non-null; x, w 16-byte aligned");
+  PLZ_REQUIRE(rank == 0 || (lora_t && lora_b && a16(lora_t) && a16(lora_b)),
+              "plz_linear_fwd_dense: rank > 0 needs 16-byte aligned lora_t and lora_b");
+  Args g = {};
+  g.a = x; g.lda = K; g.b = w; g.ldb = K;
+  g.I = M; g.J = N; g.R = K;
+  g.a2 = lora_t; g.b2 = lora_b; g.R2 = rank;
+  g.c = y; g.ldc = N; g.bias = bias; g.alpha = 1.f;
+  return launch<OP_ROW, OP_ROW, EPI_BF16>(g, 1, (hipStream_t)stream, "plz_linear_fwd_dense");
+}
+
+int plz_linear_bwd_x_dense(const uint16_t* grad_y, const uint16_t* w, const uint16_t* lora_gt,
+                           const uint16_t* lora_a, int rank, uint16_t* grad_x, int64_t M,
+                           int64_t N, int64_t K, void* stream) {
+  PLZ_REQUIRE(M >= 0 && N >= 0 && K >= 0, "plz_linear_bwd_x_dense: negative shape");
+  PLZ_REQUIRE(K % 8 == 0 && N % 8 == 0, "plz_linear_bwd_x_dense: K and N must be multiples of 8");
+  PLZ_REQUIRE(rank >= 0 && rank <= BK && rank % 8 == 0,
+              "plz_linear_bwd_x_dense: rank (%d) must be a multiple of 8 in [0, 64]", rank);
+  if (M == 0 || K == 0) return PLZ_OK;
+  PLZ_REQUIRE(grad_y && w && grad_x && a16(grad_y) && a16(w),
+              "plz_linear_bwd_x_dense: grad_y, w, grad_x must be non-null; grad_y, w aligned");
+  PLZ_REQUIRE(rank == 0 || (lora_gt && lora_a && a16(lora_gt) && a16(lora_a)),
+              "plz_linear_bwd_x_dense: rank > 0 needs 16-byte aligned lora_gt and lora_a");
+  Args g = {};
+  g.a = grad_y; g.lda = N;
+  g.b = w; g.ldb = K;  // B(j=k, r=n) = w[n, k]   (Col tile)
+  g.I = M; g.J = K; g.R = N;
+  g.a2 = lora_gt; g.b2 = lora_a; g.R2 = rank;
+  g.c = grad_x; g.ldc = K; g.alpha = 1.f;
+  return launch<OP_ROW, OP_COL, EPI_BF16>(g, 1, (hipStream_t)stream, "plz_linear_bwd_x_dense");
+}
+
+size_t plz_soft_bwd_workspace(int64_t M, int64_t N, int64_t K) {
+  (void)M;
+  if (N <= 0 || K <= 0) return 0;
+  return (size_t)N * (K / 128) * 4 * sizeof(float);
+}
+
+int plz_soft_bwd(const uint16_t* x, const uint16_t* grad_y, const uint16_t* logits,
+                 int logits_dtype, const float* noise, const float* palette, float tau,
+                 int scale_grad_by_inv_tau, uint16_t* grad_logits, float* grad_palette,
+                 void* workspace, size_t workspace_bytes, int64_t M, int64_t N, int64_t K,
+                 void* stream) {
+  PLZ_REQUIRE(M >= 0 && N >= 0 && K >= 0, "plz_soft_bwd: negative shape");
+  PLZ_REQUIRE(K % 256 == 0, "plz_soft_bwd: K (%lld) must be a multiple of 256", (long long)K);
+  PLZ_REQUIRE(N % 8 == 0, "plz_soft_bwd: N (%lld) must be a multiple of 8", (long long)N);
+  PLZ_REQUIRE(logits_dtype == PLZ_DT_BF16 || logits_dtype == PLZ_DT_FP16,
+              "plz_soft_bwd: logits dtype must be bf16 or fp16");
+  PLZ_REQUIRE(tau > 0.f, "plz_soft_bwd: tau must be positive");
+  if (N == 0 || K == 0) return PLZ_OK;
+  PLZ_REQUIRE(x && grad_y && logits && noise && palette && grad_logits && grad_palette,
+              "plz_soft_bwd: null pointer");
+  PLZ_REQUIRE(a16(x) && a16(grad_y) && a16(logits) && a16(noise) && a16(palette) &&
+                  a16(grad_logits),
+              "plz_soft_bwd: operands must be 16-byte aligned");
+  const size_t need = plz_soft_bwd_workspace(M, N, K);
+  if (!workspace || workspace_bytes < need) {
+    set_error("plz_soft_bwd: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+    return PLZ_EWORKSPACE;
+  }
+  Args g = {};
+  g.a = grad_y; g.lda = N;
+  g.b = x; g.ldb = K;
+  g.pal = palette; g.Nw = N; g.Kw = K;
+  g.I = N; g.J = K; g.R = M; g.r_split = M > 0 ? M : 1;
+  g.partial = reinterpret_cast<float*>(workspace);
+  g.logits = logits; g.noise = noise; g.inv_tau = 1.f / tau;
+  g.glog_scale = scale_grad_by_inv_tau ? 1.f / tau : 1.f;
+  g.grad_logits = grad_logits; g.logits_f16 = logits_dtype == PLZ_DT_FP16;
+  int rc = launch<OP_COL, OP_COL, EPI_SOFT>(g, 1, (hipStream_t)stream, "plz_soft_bwd");
+  if (rc != PLZ_OK) return rc;
+  const int64_t G = K / 256, n_out = N * G;
+  hipLaunchKernelGGL(reduce_pal_kernel, dim3((unsigned)((n_out + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, g.partial, grad_palette, N, G, 1);
+  return check_launch("plz_soft_bwd/reduce");
+}
+
+}  // extern "C"
