@@ -6,11 +6,11 @@
 // double-buffered in LDS (2 x 64 KB).
 //
 // Each operand tile sits in LDS in one of two layouts:
-//   Row tile  [row][r]: 16-byte chunks of 8 consecutive r, chunk index XOR (row & 7).
-//             Fragments: one ds_read_b128 per lane (row = lane%32, chunk = 2*ks + lane/32).
+//   Row tile  [row][r]: 16-byte chunks of 8 consecutive r, chunk index XOR ((row >> 1) & 7).
+//             Fragments: two ds_read_b64 per lane (row = lane%32, chunk = 2*ks + lane/32).
 //   Col tile  [r][row]: the operand's own memory order when rows are contiguous
 //             (MN-contiguous: grad_y and x in dW, W in grad_x). Chunks of 8 consecutive
-//             rows, chunk index XOR 2*(r & 3). Fragments: two ds_read_b64_tr_b16 per lane.
+//             rows, chunk index XOR (r & 15). Fragments: two ds_read_b64_tr_b16 per lane.
 //             Within each 16-lane group lane i points at rows 4*(i%4)..+3 of reduction
 //             index kbase + i/4; the instruction hands lane j elements j, j+16, j+32, j+48
 //             of the group's 64 loaded values, i.e. row j at kbase..kbase+3 -- the MFMA
@@ -33,8 +33,9 @@ typedef short v4i16 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
 typedef __attribute__((address_space(3))) uint8_t lds_u8;
 
-__device__ __forceinline__ int row_chunk(int row, int c) { return row * (BK / 8) + (c ^ (row & 7)); }
-__device__ __forceinline__ int col_swz(int kr) { return 2 * (kr & 3); }
+__device__ __forceinline__ int row_swz(int row) { return (row >> 1) & 7; }
+__device__ __forceinline__ int row_chunk(int row, int c) { return row * (BK / 8) + (c ^ row_swz(row)); }
+__device__ __forceinline__ int col_swz(int kr) { return kr & 15; }
 __device__ __forceinline__ int col_chunk(int kr, int c) { return kr * (TILE / 8) + (c ^ col_swz(kr)); }
 
 struct Args {
@@ -50,6 +51,7 @@ struct Args {
   const uint16_t* logits; const float* noise; float inv_tau, glog_scale; uint16_t* grad_logits;
   int logits_f16;
   int tiles_i, tiles_j;
+  int group;  // tile-rows walked together (1: consecutive workgroups share the A panel)
 };
 
 // ---- dense operand copy, global -> LDS ---------------------------------------------------
@@ -59,7 +61,7 @@ __device__ __forceinline__ void copy_row_tile(lds_u8* lds, const uint16_t* p, in
 #pragma unroll
   for (int it = 0; it < 8; ++it) {
     const int pch = it * 256 + threadIdx.x;          // physical chunk written by this lane
-    const int row = pch >> 3, c = (pch & 7) ^ (row & 7);
+    const int row = pch >> 3, c = (pch & 7) ^ row_swz(row);
     int64_t gr = row0 + row;
     gr = gr < nrows ? gr : nrows - 1;                 // rows past the end: any valid row
     const uint16_t* src = p + gr * ld + r0 + c * 8;
@@ -107,11 +109,15 @@ __device__ __forceinline__ void lut_row_store(uint4* lds, const LutRegs& r) {
     lds[row_chunk(row, 2 * w + 1)] = make_uint4(o[4], o[5], o[6], o[7]);
   }
 }
-// grad_x: tile rows are k (256), reduction n (64); thread t owns n = n0 + t/4 and
-// k = k0 + 64*(t%4) .. +64. The tile's k range lies in one palette group (k0 % 256 == 0).
+// grad_x: tile rows are k (256), reduction n (64). Thread t = 64*w + l owns
+// n = n0 + 16*w + l%16 and k = k0 + 64*(l/16) .. +64, so that the 16-byte LDS stores of a
+// wave cover 16 reduction rows x 4 quarters and, with the (r & 15) chunk swizzle, never
+// collide in a bank. The tile's k range lies in one palette group (k0 % 256 == 0).
+__device__ __forceinline__ int lut_col_kr() { return (threadIdx.x & 15) + 16 * (threadIdx.x >> 6); }
+__device__ __forceinline__ int lut_col_quarter() { return (threadIdx.x >> 4) & 3; }
 __device__ __forceinline__ void lut_col_load(const Args& g, int64_t k0, int64_t n0, LutRegs& r) {
-  const int64_t n = n0 + (threadIdx.x >> 2);
-  const int64_t k = k0 + 64 * (threadIdx.x & 3);
+  const int64_t n = n0 + lut_col_kr();
+  const int64_t k = k0 + 64 * lut_col_quarter();
   r.q = make_uint4(0, 0, 0, 0);
   r.p = make_float4(0.f, 0.f, 0.f, 0.f);
   if (n < g.Nw && k < g.Kw) {
@@ -121,7 +127,7 @@ __device__ __forceinline__ void lut_col_load(const Args& g, int64_t k0, int64_t 
 }
 __device__ __forceinline__ void lut_col_store(uint4* lds, const LutRegs& r) {
   const PalLut t = make_lut(r.p.x, r.p.y, r.p.z, r.p.w);
-  const int kr = threadIdx.x >> 2, cb = 8 * (threadIdx.x & 3);
+  const int kr = lut_col_kr(), cb = 8 * lut_col_quarter();
   const uint32_t qs[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
 #pragma unroll
   for (int w = 0; w < 4; ++w) {
@@ -135,8 +141,16 @@ __device__ __forceinline__ void lut_col_store(uint4* lds, const LutRegs& r) {
 // ---- fragments (v_mfma_f32_32x32x16_bf16: lane l holds row l%32, k-slots 8*(l/32)..+7) --
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
+// Read as two 8-byte halves: on gfx950 two ds_read_b64 move a fragment through the LDS
+// faster than one ds_read_b128 (about 12 vs 16.5 CU cycles per KB for a wave, measured).
 __device__ __forceinline__ bf16x8 frag_row(const uint4* lds, int rowbase, int ks, int lane) {
-  return __builtin_bit_cast(bf16x8, lds[row_chunk(rowbase + (lane & 31), 2 * ks + (lane >> 5))]);
+  const int ch = row_chunk(rowbase + (lane & 31), 2 * ks + (lane >> 5));
+  const u32x2* p = reinterpret_cast<const u32x2*>(lds + ch);
+  int hi_off = 1;
+  asm("" : "+v"(hi_off));  // opaque offset: keeps the load/store vectorizer from fusing the halves
+  const u32x2 lo = p[0];
+  const u32x2 hi = p[hi_off];
+  return __builtin_bit_cast(bf16x8, u32x4{lo.x, lo.y, hi.x, hi.y});
 }
 // Col tile: per 16-lane group j = lane/16 the rows 16*(j&1)..+15 at k-group j>>1.
 __device__ __forceinline__ bf16x8 frag_col(const lds_u8* lds, int rowbase, int ks, int lane) {

@@ -95,7 +95,7 @@ __global__ __launch_bounds__(256) void gemm2_kernel(const Args g) {
   int bid = blockIdx.x;
   const int T = g.tiles_i * g.tiles_j;
   if (T % 8 == 0) bid = (bid % 8) * (T / 8) + bid / 8;
-  const int GROUP = 8;
+  const int GROUP = g.group;
   const int per_group = GROUP * g.tiles_j;
   const int first_i = (bid / per_group) * GROUP;
   const int gsz = min(g.tiles_i - first_i, GROUP);
@@ -180,19 +180,39 @@ __global__ __launch_bounds__(256) void gemm2_kernel(const Args g) {
   // ---- epilogues ----------------------------------------------------------------------
   // acc[ti][tj][e]: row wi*128 + 32*ti + 8*(e/4) + 4*(lane/32) + e%4, col wj*128 + 32*tj + lane%32
   if (EPI == EPI_BF16) {
-    uint16_t* C = reinterpret_cast<uint16_t*>(g.c);
+    // Stage the bf16 tile in LDS (rows padded to 528 B so the two 64-byte row segments a
+    // wave writes per instruction fall in different banks), then write it out with 16-byte
+    // coalesced stores: 32 per thread instead of 256 scattered 2-byte stores.
+    constexpr int RS = 528;  // staging row stride in bytes
+    lds_u8* st = lbase;
+    float bj[4];
 #pragma unroll
     for (int tj = 0; tj < 4; ++tj) {
       const int64_t j = j0 + wj * 128 + 32 * tj + (lane & 31);
-      if (j >= g.J) continue;
-      const float bj = g.bias ? bf2f(g.bias[j]) : 0.f;
+      bj[tj] = (g.bias && j < g.J) ? bf2f(g.bias[j]) : 0.f;
+    }
 #pragma unroll
-      for (int ti = 0; ti < 4; ++ti)
+    for (int ti = 0; ti < 4; ++ti)
+#pragma unroll
+      for (int tj = 0; tj < 4; ++tj)
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
-          const int64_t i = i0 + wi * 128 + 32 * ti + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-          if (i < g.I) C[i * g.ldc + j] = (uint16_t)f2bf(g.alpha * acc[ti][tj][e] + bj);
+          const int row = wi * 128 + 32 * ti + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+          const int col = wj * 128 + 32 * tj + (lane & 31);
+          *reinterpret_cast<__attribute__((address_space(3))) uint16_t*>(st + row * RS + col * 2) =
+              (uint16_t)f2bf(g.alpha * acc[ti][tj][e] + bj[tj]);
         }
+    __syncthreads();
+    uint16_t* C = reinterpret_cast<uint16_t*>(g.c);
+#pragma unroll 4
+    for (int it = 0; it < 32; ++it) {
+      const int ch = it * 256 + threadIdx.x;  // 32 chunks of 8 columns per row
+      const int row = ch >> 5, c8 = (ch & 31) * 8;
+      const int64_t i = i0 + row, j = j0 + c8;
+      if (i < g.I && j < g.J) {
+        const u32x4 v = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(st + row * RS + c8 * 2);
+        *reinterpret_cast<u32x4*>(C + i * g.ldc + j) = v;
+      }
     }
     return;
   }
@@ -313,13 +333,14 @@ __global__ __launch_bounds__(256) void gemm2_kernel(const Args g) {
   }
 }
 
-constexpr size_t kLds = 2 * 2 * TILE_BYTES;  // 128 KB
+constexpr size_t kLds = 256 * 528;  // 132 KB: two pipeline stages (128 KB) or the padded bf16 output tile
 
 template <int KA, int KB, int EPI>
 static int launch(Args g, int splits, hipStream_t stream, const char* what) {
   g.tiles_i = (int)((g.I + TILE - 1) / TILE);
   g.tiles_j = (int)((g.J + TILE - 1) / TILE);
   if (g.r_split <= 0) g.r_split = g.R;
+  if (g.group <= 0) g.group = 8;
   auto kern = gemm2_kernel<KA, KB, EPI>;
   static bool attr = false;
   if (!attr) {
@@ -410,6 +431,7 @@ int plz_lut_linear_fwd(const uint16_t* x, const int32_t* packed, const float* pa
   g.I = M; g.J = N; g.R = K;
   g.a2 = lora_t; g.b2 = lora_b; g.R2 = rank;
   g.c = y; g.ldc = N; g.bias = bias; g.alpha = 1.f;
+  g.group = 1;
   return launch<OP_ROW, OP_LUT_ROW, EPI_BF16>(g, 1, (hipStream_t)stream, "plz_lut_linear_fwd");
 }
 
@@ -434,6 +456,7 @@ int plz_lut_linear_bwd_x(const uint16_t* grad_y, const int32_t* packed, const fl
   g.I = M; g.J = K; g.R = N;
   g.a2 = lora_gt; g.b2 = lora_a; g.R2 = rank;
   g.c = grad_x; g.ldc = K; g.alpha = 1.f;
+  g.group = 1;
   return launch<OP_ROW, OP_LUT_COL, EPI_BF16>(g, 1, (hipStream_t)stream, "plz_lut_linear_bwd_x");
 }
 
