@@ -142,6 +142,74 @@ def bench_gemv(device, reps=20):
     return res
 
 
+def bench_soft(device, reps=5):
+    """Config 4: soft (Gumbel-softmax) fwd + bwd on the gate shape 2560 -> 9728 at M=16384;
+    logits bf16 [N, K, 4] ~ N(0,1), Philox noise fp32 passed in, tau in {2.0, 0.5, 0.1}."""
+    import torch
+    from palettize_hip import ops
+    K, N = 2560, 9728
+    g = torch.Generator(device=device).manual_seed(2)
+    logits = torch.randn(N, K, 4, generator=g, device=device).to(torch.bfloat16)
+    noise = ops.gumbel_philox((N, K, 4), seed=0, device=device)
+    pal = torch.sort(torch.randn(N, K // 256, 4, generator=g, device=device) * 0.02, -1).values.contiguous()
+    x = torch.randn(M_TRAIN, K, generator=g, device=device).to(torch.bfloat16)
+    gy = torch.randn(M_TRAIN, N, generator=g, device=device).to(torch.bfloat16)
+    out = {}
+    ev = lambda: torch.cuda.Event(enable_timing=True)
+    for tau in (2.0, 0.5, 0.1):
+        times = {"build_w": 0.0, "fwd_gemm": 0.0, "grad_x": 0.0, "soft_bwd": 0.0}
+        for rep in range(reps + 1):
+            e = [ev() for _ in range(5)]
+            e[0].record()
+            w, _ = ops.soft_build_w(logits, noise, pal, tau)
+            e[1].record()
+            ops.linear_fwd_dense(x, w)
+            e[2].record()
+            ops.linear_bwd_x_dense(gy, w)
+            e[3].record()
+            ops.soft_bwd(x, gy, logits, noise, pal, tau)
+            e[4].record()
+            torch.cuda.synchronize()
+            if rep:
+                for i, k in enumerate(times):
+                    times[k] += e[i].elapsed_time(e[i + 1]) / reps
+        tot = sum(times.values())
+        flop = 6.0 * M_TRAIN * K * N
+        bw_bytes = 26.0 * N * K  # build-W: 8 B logits + 16 B noise in, 2 B W out per weight
+        out[f"tau{tau}"] = dict(ms=round(tot, 3), tflops=round(flop / (tot * 1e-3) / 1e12, 1),
+                                build_w_gbs=round(bw_bytes / (times["build_w"] * 1e-3) / 1e9, 1),
+                                **{f"{k}_ms": round(v, 3) for k, v in times.items()})
+    bw = out["tau0.5"]["build_w_gbs"]
+    out["roofline_build_w"] = {"bound": "hbm", "achieved": bw, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                               "frac": round(bw / PEAK_HBM_GBS, 4)}
+    return out
+
+
+def bench_layer(device, steps=4, warmup=2):
+    """Config 5: one palettized Qwen-4B-shaped decoder-layer training step at 32 x 512."""
+    import torch
+    from palettize_hip.layer import LayerConfig, LayerTrainer
+    cfg = LayerConfig()
+    tr = LayerTrainer(cfg, device, seed=0, lora_b_std=0.01)
+    hs = torch.randn(32, 512, cfg.hidden, generator=torch.Generator(device=device).manual_seed(4),
+                     device=device).to(torch.bfloat16)
+    for _ in range(warmup):
+        tr.step(hs)
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    losses = []
+    for _ in range(steps):
+        loss, _ = tr.step(hs)
+        losses.append(loss)
+    e.record()
+    torch.cuda.synchronize()
+    ms = s.elapsed_time(e) / steps
+    return dict(ms_per_step=round(ms, 2), tokens_per_s=round(32 * 512 / (ms * 1e-3), 1),
+                loss_first=round(float(losses[0]), 5), loss_last=round(float(losses[-1]), 5),
+                config="hidden 2560, 32/8 heads x 128, SwiGLU 9728, 7 soft palettized linears + LoRA r16, batch 32 x 512")
+
+
 def cpu_baseline(budget_s=12.0):
     """Reference CPU path (gather + matmul + LoRA, torch autograd) on a bounded sample of the
     config-3 workload: M_cpu rows of every shape; TFLOP/s on the same 6*M*K*N count."""
@@ -188,7 +256,7 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["hard", "gemv"], default=None)
+    ap.add_argument("--only", choices=["hard", "gemv", "soft", "layer"], default=None)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (the path has no multi-GPU "
@@ -243,6 +311,14 @@ def main():
     if args.only in (None, "gemv"):
         out["gemv"] = bench_gemv(dev)
         _log(f"gemv: {out['gemv']}")
+    if args.only in (None, "soft"):
+        out["soft"] = bench_soft(dev)
+        _log(f"soft: {out['soft']}")
+        torch.cuda.empty_cache()
+    if args.only in (None, "layer"):
+        out["layer"] = bench_layer(dev)
+        _log(f"layer: {out['layer']}")
+        torch.cuda.empty_cache()
     if not args.no_cpu and args.only is None:
         out["cpu_baseline"] = cpu_baseline()
         _log("cpu baseline done")

@@ -108,7 +108,8 @@ int plz_linear_bwd_x_dense(const uint16_t* grad_y, const uint16_t* w, const uint
 /* ---- soft (Gumbel-softmax) path --------------------------------------------------- */
 /* noise fp32 [n] = -log(-log(u)), u from Philox4x32-10 (Salmon et al., SC'11) keyed by
  * seed, counter = offset + element index / 4 (one 128-bit draw per 4 consecutive
- * elements), u = (bits >> 8 + 0.5) * 2^-24. Replaces the in-kernel LCG sampler of
+ * elements), u = ((bits >> 9) + 0.5) * 2^-23, so 2^-24 <= u <= 1 - 2^-24 exactly in fp32
+ * and the noise is always finite. Replaces the in-kernel LCG sampler of
  * fused_lut_kernel.cu:1245-1256 with a supplied-noise tensor. n % 4 == 0. */
 int plz_gumbel_philox(float* noise, int64_t n, uint64_t seed, uint64_t offset, void* stream);
 /* The reference's own sampler, bit-exact in its integer part: noise[n,k,c] =

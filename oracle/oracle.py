@@ -207,13 +207,19 @@ def philox4x32_10(ctr, key) -> np.ndarray:
 
 
 def gumbel_philox(n: int, seed: int, offset: int = 0) -> np.ndarray:
-    """Noise of plz_gumbel_philox: counter = offset + i/4, key = seed, u = (b>>8 + .5)/2^24."""
+    """Noise of plz_gumbel_philox: counter = offset + i/4, key = seed, u = (b>>9 + .5)/2^23."""
     t = np.arange(n // 4, dtype=np.uint64) + np.uint64(offset)
     ctr = np.zeros((n // 4, 4), np.uint32)
     ctr[:, 0] = (t & np.uint64(0xFFFFFFFF)).astype(np.uint32)
     ctr[:, 1] = (t >> np.uint64(32)).astype(np.uint32)
     bits = philox4x32_10(ctr, (seed & 0xFFFFFFFF, (seed >> 32) & 0xFFFFFFFF)).reshape(-1)
-    u = ((bits >> np.uint32(8)).astype(np.float32) + np.float32(0.5)) * np.float32(1.0 / 16777216.0)
+    return gumbel_from_bits(bits)
+
+
+def gumbel_from_bits(bits) -> np.ndarray:
+    """u = (bits >> 9 + 0.5) / 2^23 in [2^-24, 1 - 2^-24] (exact in fp32); -log(-log u)."""
+    bits = np.asarray(bits, dtype=np.uint32)
+    u = ((bits >> np.uint32(9)).astype(np.float32) + np.float32(0.5)) * np.float32(1.0 / 8388608.0)
     return (-np.log(-np.log(u))).astype(np.float32)
 
 

@@ -114,7 +114,7 @@ void orc_gumbel_philox(float* out, int64_t n, uint64_t seed, uint64_t offset) {
     uint32_t c[4] = {(uint32_t)ctr, (uint32_t)(ctr >> 32), 0u, 0u}, r[4];
     orc_philox(c, key, r);
     for (int j = 0; j < 4; ++j) {
-      float u = ((float)(r[j] >> 8) + 0.5f) * (1.0f / 16777216.0f);
+      float u = ((float)(r[j] >> 9) + 0.5f) * (1.0f / 8388608.0f);
       out[4 * t + j] = -logf(-logf(u));
     }
   }

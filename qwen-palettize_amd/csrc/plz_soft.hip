@@ -28,8 +28,10 @@ __host__ __device__ __forceinline__ U4 philox4x32_10(U4 c, uint32_t k0, uint32_t
   return c;
 }
 
+// u = (top 23 bits + 0.5) / 2^23 lies in [2^-24, 1 - 2^-24]: every value is exact in fp32,
+// so u never rounds to 1 (which would make the noise +inf).
 __device__ __forceinline__ float gumbel_from_bits(uint32_t b) {
-  const float u = ((float)(b >> 8) + 0.5f) * (1.0f / 16777216.0f);  // (0, 1)
+  const float u = ((float)(b >> 9) + 0.5f) * (1.0f / 8388608.0f);
   return -logf(-logf(u));
 }
 

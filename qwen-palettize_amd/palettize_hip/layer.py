@@ -1,0 +1,362 @@
+"""One palettized Qwen3-shaped decoder layer and its distillation training step.
+
+The layer is HF Qwen3DecoderLayer's math (transformers models/qwen3/modeling_qwen3.py:
+RMSNorm :50-64, MLP :70-83, attention with per-head q/k RMSNorm and RoPE :140-160,211-318)
+with every linear replaced by a Gumbel-softmax palettized linear + LoRA, as the reference
+trains it (train_qwen.py:993-1414, qwen_model.py:65-304):
+
+  * linears: SoftPalettizedLinear -- logits [N, K, 4] (bf16), palette fp32 [N, K/256, 4],
+    LoRA A [r, K] / B [N, r] (bf16), straight-through forward through W_hard;
+    HIP kernels for build-W, the GEMMs and the fused soft backward;
+  * RMSNorm and SwiGLU: HIP kernels (plz_rmsnorm_*, plz_swiglu_*);
+  * attention: torch scaled_dot_product_attention (causal), RoPE in torch;
+  * loss: 0.5 * (1 - cos) + 0.5 * norm_mse against a dense bf16 teacher layer
+    (compute_loss, train_qwen.py:229-249);
+  * optimizer: AdamW (betas 0.9/0.95, eps 1e-8, wd 0) on fp32 masters of palettes, LoRA and
+    logits (FP32MasterOptimizer, train_qwen.py:154-221), two-tier gradient clipping
+    (logits 1.0, others 0.3; train_qwen.py:1303-1319), logits clamp +-5 tau after the step
+    (train_qwen.py:1343-1348), tau schedule of train_qwen.py:1176-1192.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import ops
+from ._lib import PLZ_W_HARD_NOISY
+from .functional import SoftLUTLinearFunction
+
+
+@dataclass
+class LayerConfig:
+    hidden: int = 2560
+    heads: int = 32
+    kv_heads: int = 8
+    head_dim: int = 128
+    intermediate: int = 9728
+    eps: float = 1e-6
+    rope_theta: float = 1e6
+    lora_rank: int = 16
+    lora_alpha: float = 16.0   # scaling alpha / r = 1 (BASELINE config: y += x A^T B^T)
+
+
+# ---- fused kernels as autograd Functions ----------------------------------------------
+class RMSNormFunction(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, weight, eps):
+        shape = x.shape
+        x2 = x.reshape(-1, shape[-1]).contiguous()
+        y, rstd = ops.rmsnorm_fwd(x2, weight.contiguous(), eps)
+        ctx.save_for_backward(x2, weight, rstd)
+        ctx.shape = shape
+        return y.reshape(shape)
+
+    @staticmethod
+    def backward(ctx, gy):
+        x2, weight, rstd = ctx.saved_tensors
+        gx, gw = ops.rmsnorm_bwd(x2, weight.contiguous(), rstd,
+                                 gy.reshape(x2.shape).contiguous())
+        return gx.reshape(ctx.shape), (gw.to(weight.dtype) if ctx.needs_input_grad[1] else None), None
+
+
+class RMSNorm(nn.Module):
+    def __init__(self, dim, eps, device=None):
+        super().__init__()
+        self.weight = nn.Parameter(torch.ones(dim, dtype=torch.bfloat16, device=device),
+                                   requires_grad=False)
+        self.eps = eps
+
+    def forward(self, x):
+        return RMSNormFunction.apply(x, self.weight, self.eps)
+
+
+class SwiGLUFunction(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, gate, up):
+        gate, up = gate.contiguous(), up.contiguous()
+        ctx.save_for_backward(gate, up)
+        return ops.swiglu_fwd(gate, up)
+
+    @staticmethod
+    def backward(ctx, gh):
+        gate, up = ctx.saved_tensors
+        return ops.swiglu_bwd(gate, up, gh.contiguous())
+
+
+# ---- palettized linear (native layout, soft path) ----------------------------------------
+class SoftPalettizedLinear(nn.Module):
+    """y = x W_ste^T + s (x A^T) B^T with W from logits + Gumbel noise + palette.
+
+    Parameters: logits bf16 [N, K, 4] (initialised one-hot +-10 from `indices`, like
+    qwen_model.py:135-143), palette fp32 [N, K/256, 4], lora_a bf16 [r, K] ~ N(0, 0.01),
+    lora_b bf16 [N, r] (zeros unless given). The noise is regenerated every forward from a
+    Philox stream (seed, counter) so steps are reproducible."""
+
+    def __init__(self, in_features, out_features, indices=None, palette=None, rank=16,
+                 lora_scale=1.0, seed=0, device=None, lora_b_std=0.0):
+        super().__init__()
+        N, K = out_features, in_features
+        self.in_features, self.out_features = K, N
+        g = torch.Generator(device="cpu").manual_seed(seed)
+        if indices is None:
+            indices = torch.randint(0, 4, (N, K), generator=g, dtype=torch.uint8)
+        if palette is None:
+            palette = torch.sort(torch.randn(N, K // 256, 4, generator=g) * 0.02, -1).values
+        onehot = F.one_hot(indices.long(), 4).bool()
+        logits = torch.where(onehot, torch.tensor(10.0), torch.tensor(-10.0))
+        self.index_logits = nn.Parameter(logits.to(torch.bfloat16).to(device).contiguous())
+        self.palette = nn.Parameter(palette.float().to(device).contiguous())
+        self.lora_a = nn.Parameter((torch.randn(rank, K, generator=g) * 0.01)
+                                   .to(torch.bfloat16).to(device))
+        self.lora_b = nn.Parameter((torch.randn(N, rank, generator=g) * lora_b_std)
+                                   .to(torch.bfloat16).to(device))
+        self.lora_scale = lora_scale
+        self.tau = 1.0
+        self.noise_seed = seed
+        self.noise_counter = 0
+        self.mode = PLZ_W_HARD_NOISY
+
+    def next_noise(self):
+        n = self.out_features * self.in_features * 4
+        off = self.noise_counter
+        self.noise_counter += n // 4
+        return ops.gumbel_philox((self.out_features, self.in_features, 4), seed=self.noise_seed,
+                                 offset=off, device=self.index_logits.device)
+
+    def forward(self, x):
+        lead = x.shape[:-1]
+        noise = self.next_noise()
+        y = SoftLUTLinearFunction.apply(x.reshape(-1, x.shape[-1]), self.palette, self.index_logits,
+                                        noise, self.tau, None, self.lora_a, self.lora_b,
+                                        self.lora_scale, self.mode, False)
+        return y.reshape(*lead, self.out_features)
+
+
+# ---- RoPE / attention -------------------------------------------------------------------------
+def rope_tables(seq, head_dim, theta, device):
+    inv = 1.0 / (theta ** (torch.arange(0, head_dim, 2, device=device, dtype=torch.float32) / head_dim))
+    t = torch.arange(seq, device=device, dtype=torch.float32)
+    freqs = torch.outer(t, inv)
+    emb = torch.cat([freqs, freqs], dim=-1)
+    return emb.cos(), emb.sin()
+
+
+def apply_rope(x, cos, sin):
+    """x [B, S, H, D]; HF rotate_half convention, computed in fp32, returned in x.dtype."""
+    xf = x.float()
+    d = xf.shape[-1] // 2
+    rot = torch.cat([-xf[..., d:], xf[..., :d]], dim=-1)
+    c = cos[None, :, None, :]
+    s = sin[None, :, None, :]
+    return (xf * c + rot * s).to(x.dtype)
+
+
+def attention(q, k, v, heads, kv_heads):
+    """q [B,S,H,D], k/v [B,S,Hkv,D] -> [B,S,H*D]; causal, grouped-query (kv repeated)."""
+    B, S, H, D = q.shape
+    rep = heads // kv_heads
+    qt = q.transpose(1, 2)
+    kt = k.repeat_interleave(rep, dim=2).transpose(1, 2)
+    vt = v.repeat_interleave(rep, dim=2).transpose(1, 2)
+    if q.is_cuda:
+        # flash / memory-efficient kernels only: the math fallback issues bf16 batched
+        # products on transposed operands, which this pool does not run reliably
+        from torch.nn.attention import SDPBackend, sdpa_kernel
+        with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+            o = F.scaled_dot_product_attention(qt, kt, vt, is_causal=True)
+    else:
+        o = F.scaled_dot_product_attention(qt, kt, vt, is_causal=True)
+    return o.transpose(1, 2).reshape(B, S, H * D)
+
+
+# ---- the layers -------------------------------------------------------------------------------
+class PalettizedDecoderLayer(nn.Module):
+    NAMES = ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj")
+
+    def __init__(self, cfg: LayerConfig, seed=0, device=None, lora_b_std=0.0):
+        super().__init__()
+        self.cfg = cfg
+        h, hd = cfg.hidden, cfg.head_dim
+        shapes = {"q_proj": (h, cfg.heads * hd), "k_proj": (h, cfg.kv_heads * hd),
+                  "v_proj": (h, cfg.kv_heads * hd), "o_proj": (cfg.heads * hd, h),
+                  "gate_proj": (h, cfg.intermediate), "up_proj": (h, cfg.intermediate),
+                  "down_proj": (cfg.intermediate, h)}
+        scale = cfg.lora_alpha / cfg.lora_rank
+        for i, name in enumerate(self.NAMES):
+            K, N = shapes[name]
+            self.add_module(name, SoftPalettizedLinear(K, N, rank=cfg.lora_rank, lora_scale=scale,
+                                                       seed=seed * 7 + i, device=device,
+                                                       lora_b_std=lora_b_std))
+        self.input_layernorm = RMSNorm(h, cfg.eps, device)
+        self.post_attention_layernorm = RMSNorm(h, cfg.eps, device)
+        self.q_norm = RMSNorm(hd, cfg.eps, device)
+        self.k_norm = RMSNorm(hd, cfg.eps, device)
+
+    def linears(self):
+        return [getattr(self, n) for n in self.NAMES]
+
+    def forward(self, hs, cos, sin):
+        cfg = self.cfg
+        B, S, _ = hs.shape
+        x = self.input_layernorm(hs)
+        q = self.q_norm(self.q_proj(x).view(B, S, cfg.heads, cfg.head_dim))
+        k = self.k_norm(self.k_proj(x).view(B, S, cfg.kv_heads, cfg.head_dim))
+        v = self.v_proj(x).view(B, S, cfg.kv_heads, cfg.head_dim)
+        q, k = apply_rope(q, cos, sin), apply_rope(k, cos, sin)
+        hs = hs + self.o_proj(attention(q, k, v, cfg.heads, cfg.kv_heads))
+        x = self.post_attention_layernorm(hs)
+        mlp = self.down_proj(SwiGLUFunction.apply(self.gate_proj(x), self.up_proj(x)))
+        return hs + mlp
+
+
+class DenseDecoderLayer(nn.Module):
+    """bf16 teacher with the same architecture (random init), forward only."""
+
+    def __init__(self, cfg: LayerConfig, seed=1, device=None):
+        super().__init__()
+        self.cfg = cfg
+        g = torch.Generator(device="cpu").manual_seed(seed)
+        h, hd = cfg.hidden, cfg.head_dim
+        dims = {"q_proj": (cfg.heads * hd, h), "k_proj": (cfg.kv_heads * hd, h),
+                "v_proj": (cfg.kv_heads * hd, h), "o_proj": (h, cfg.heads * hd),
+                "gate_proj": (cfg.intermediate, h), "up_proj": (cfg.intermediate, h),
+                "down_proj": (h, cfg.intermediate)}
+        for name, (n, k) in dims.items():
+            w = (torch.randn(n, k, generator=g) * 0.02).to(torch.bfloat16).to(device)
+            self.register_buffer(name, w)
+        self.input_layernorm = RMSNorm(h, cfg.eps, device)
+        self.post_attention_layernorm = RMSNorm(h, cfg.eps, device)
+        self.q_norm = RMSNorm(hd, cfg.eps, device)
+        self.k_norm = RMSNorm(hd, cfg.eps, device)
+
+    @torch.no_grad()
+    def forward(self, hs, cos, sin):
+        cfg = self.cfg
+        B, S, _ = hs.shape
+        x = self.input_layernorm(hs)
+        q = self.q_norm(F.linear(x, self.q_proj).view(B, S, cfg.heads, cfg.head_dim))
+        k = self.k_norm(F.linear(x, self.k_proj).view(B, S, cfg.kv_heads, cfg.head_dim))
+        v = F.linear(x, self.v_proj).view(B, S, cfg.kv_heads, cfg.head_dim)
+        q, k = apply_rope(q, cos, sin), apply_rope(k, cos, sin)
+        hs = hs + F.linear(attention(q, k, v, cfg.heads, cfg.kv_heads), self.o_proj)
+        x = self.post_attention_layernorm(hs)
+        g = F.linear(x, self.gate_proj)
+        u = F.linear(x, self.up_proj)
+        return hs + F.linear(SwiGLUFunction.apply(g, u), self.down_proj)
+
+
+# ---- loss / schedule / optimizer ----------------------------------------------------------------
+def compute_loss(student_out, teacher_out, w_cos=0.5, w_mse=0.5):
+    """train_qwen.py:229-249 (loss_type '1-cos+norm_mse', weights normalised)."""
+    s = student_out.float()
+    t = teacher_out.detach().float()
+    tot = w_cos + w_mse
+    cos_per = F.cosine_similarity(s.flatten(0, 1), t.flatten(0, 1), dim=-1, eps=1e-4)
+    l_cos = (1 - cos_per).mean()
+    t_var = (t * t).mean().clamp(min=1e-6)
+    l_mse = ((s - t) ** 2).mean() / t_var
+    return (w_cos / tot) * l_cos + (w_mse / tot) * l_mse, l_cos
+
+
+def tau_at(step, tau_init=2.0, tau_final=0.5, warmup=500, anneal=6000):
+    """train_qwen.py:1176-1192."""
+    if step < warmup:
+        return tau_init
+    if step < warmup + anneal:
+        p = (step - warmup) / anneal
+        return max(tau_final, tau_init * (1.0 - p) ** 2)
+    return tau_final
+
+
+class FP32MasterAdamW:
+    """AdamW on fp32 master copies of (possibly bf16) parameters (train_qwen.py:154-221)."""
+
+    def __init__(self, groups, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.0):
+        self.pairs = []
+        master_groups = []
+        for grp in groups:
+            ms = []
+            for p in grp["params"]:
+                m = p.detach().float().clone().requires_grad_(True)
+                self.pairs.append((m, p))
+                ms.append(m)
+            master_groups.append({"params": ms, "lr": grp["lr"]})
+        self.opt = torch.optim.AdamW(master_groups, betas=betas, eps=eps,
+                                     weight_decay=weight_decay, foreach=True)
+
+    def step(self):
+        for m, p in self.pairs:
+            m.grad = None if p.grad is None else p.grad.float()
+        self.opt.step()
+        with torch.no_grad():
+            for m, p in self.pairs:
+                p.copy_(m)
+
+    @torch.no_grad()
+    def clamp_(self, params, lo, hi):
+        """Clamp model parameters and their fp32 masters together."""
+        ids = {id(p) for p in params}
+        for m, p in self.pairs:
+            if id(p) in ids:
+                m.clamp_(lo, hi)
+                p.copy_(m)
+
+
+class LayerTrainer:
+    """Owns a student/teacher pair and runs config-5 training steps."""
+
+    def __init__(self, cfg: LayerConfig, device, lrs=None, seed=0, lora_b_std=0.0):
+        self.cfg = cfg
+        self.device = device
+        self.student = PalettizedDecoderLayer(cfg, seed=seed, device=device, lora_b_std=lora_b_std)
+        self.teacher = DenseDecoderLayer(cfg, seed=seed + 1, device=device)
+        lrs = lrs or {"palettes": 1e-4, "lora": 3e-4, "indices": 1e-2}
+        pal, lora, logits = [], [], []
+        for lin in self.student.linears():
+            pal.append(lin.palette)
+            lora += [lin.lora_a, lin.lora_b]
+            logits.append(lin.index_logits)
+        self.logits = logits
+        self.others = pal + lora
+        self.opt = FP32MasterAdamW([{"params": pal, "lr": lrs["palettes"]},
+                                    {"params": lora, "lr": lrs["lora"]},
+                                    {"params": logits, "lr": lrs["indices"]}])
+        self.step_idx = 0
+        self._rope = {}
+
+    def rope(self, seq):
+        if seq not in self._rope:
+            self._rope[seq] = rope_tables(seq, self.cfg.head_dim, self.cfg.rope_theta, self.device)
+        return self._rope[seq]
+
+    def forward_backward(self, hs):
+        """Teacher + student forward, loss, backward; returns (loss, 1 - cos mean)."""
+        tau = tau_at(self.step_idx)
+        for lin in self.student.linears():
+            lin.tau = tau
+        cos, sin = self.rope(hs.shape[1])
+        t_out = self.teacher(hs, cos, sin)
+        s_out = self.student(hs, cos, sin)
+        loss, l_cos = compute_loss(s_out, t_out)
+        for p in self.logits + self.others:
+            p.grad = None
+        loss.backward()
+        return loss.detach(), l_cos.detach()
+
+    def update(self):
+        """Two-tier clip, AdamW on fp32 masters, logits clamp +-5 tau, advance the step."""
+        tau = tau_at(self.step_idx)
+        torch.nn.utils.clip_grad_norm_(self.logits, 1.0)
+        torch.nn.utils.clip_grad_norm_(self.others, 0.3)
+        self.opt.step()
+        self.opt.clamp_(self.logits, -5.0 * tau, 5.0 * tau)
+        self.step_idx += 1
+
+    def step(self, hs):
+        loss, l_cos = self.forward_backward(hs)
+        self.update()
+        return loss, l_cos

@@ -1,0 +1,96 @@
+"""GPU parity of the palettized decoder-layer training step against the
+torch CPU restatement (oracle/torch_ref.py) at a small Qwen3-shaped configuration."""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+import torch_ref as R
+from helpers import assert_close, cosine, f32
+
+pytestmark = pytest.mark.gpu
+layer = pytest.importorskip("palettize_hip.layer")
+
+CFG = dict(hidden=256, heads=4, kv_heads=2, head_dim=64, intermediate=512, lora_rank=16,
+           lora_alpha=16.0)
+
+
+def _setup(dev, seed=3):
+    cfg = layer.LayerConfig(**CFG)
+    tr = layer.LayerTrainer(cfg, dev, seed=seed, lora_b_std=0.02)
+    hs = (torch.randn(2, 16, cfg.hidden, generator=torch.Generator().manual_seed(seed)))
+    return cfg, tr, hs.to(torch.bfloat16)
+
+
+def _cpu_params(tr):
+    st = tr.student
+    p = {}
+    for name in st.NAMES:
+        lin = getattr(st, name)
+        p[name] = dict(palette=lin.palette.detach().cpu().float().requires_grad_(True),
+                       logits=lin.index_logits.detach().cpu().float().requires_grad_(True),
+                       lora_a=lin.lora_a.detach().cpu().float().requires_grad_(True),
+                       lora_b=lin.lora_b.detach().cpu().float().requires_grad_(True),
+                       lora_scale=lin.lora_scale, seed=lin.noise_seed, counter=lin.noise_counter,
+                       shape=(lin.out_features, lin.in_features))
+    for n in ("input_layernorm", "post_attention_layernorm", "q_norm", "k_norm"):
+        p[n] = getattr(st, n).weight.detach().cpu().float()
+    t = tr.teacher
+    w = {n: getattr(t, n).detach().cpu().float() for n in st.NAMES}
+    for n in ("input_layernorm", "post_attention_layernorm", "q_norm", "k_norm"):
+        w[n] = getattr(t, n).weight.detach().cpu().float()
+    return p, w
+
+
+def test_layer_step_forward_backward_matches_cpu_reference(dev):
+    cfg, tr, hs = _setup(dev)
+    p, w = _cpu_params(tr)
+    noises = {}
+    for name in tr.student.NAMES:
+        N, K = p[name]["shape"]
+        noises[name] = torch.from_numpy(
+            O.gumbel_philox(N * K * 4, p[name]["seed"], p[name]["counter"]).reshape(N, K, 4))
+    loss, _ = tr.forward_backward(hs.to(dev))
+    tau = layer.tau_at(0)
+    s_out = R.layer_forward_ref(p, hs.float(), noises, tau, cfg)
+    t_out = R.teacher_forward_ref(w, hs.float(), cfg)
+    loss_ref = R.compute_loss_ref(s_out, t_out)
+    loss_ref.backward()
+    assert abs(float(loss) - float(loss_ref)) <= 1e-2 * abs(float(loss_ref))
+    for name in tr.student.NAMES:
+        lin = getattr(tr.student, name)
+        for attr, key in (("palette", "palette"), ("index_logits", "logits"),
+                          ("lora_a", "lora_a"), ("lora_b", "lora_b")):
+            got = f32(getattr(lin, attr).grad)
+            want = p[name][key].grad.numpy()
+            c = cosine(got, want)
+            assert c >= 0.999, f"{name}.{attr}: cosine {c:.6f}"
+
+
+def test_layer_update_matches_adamw_clip_clamp(dev):
+    cfg, tr, hs = _setup(dev, seed=5)
+    params = tr.logits + tr.others
+    before = [p.detach().float().cpu().clone() for p in params]
+    tr.forward_backward(hs.to(dev))
+    grads = [p.grad.detach().float().cpu().clone() for p in params]
+    tau = layer.tau_at(tr.step_idx)
+    tr.update()
+    # CPU replica: two-tier clip, AdamW(0.9, 0.95, eps 1e-8, wd 0) on fp32 masters, clamp
+    masters = [b.clone().requires_grad_(True) for b in before]
+    for m, g in zip(masters, grads):
+        m.grad = g.clone()
+    nl = len(tr.logits)
+    torch.nn.utils.clip_grad_norm_(masters[:nl], 1.0)
+    torch.nn.utils.clip_grad_norm_(masters[nl:], 0.3)
+    npal = len(tr.student.linears())
+    groups = [{"params": masters[nl:nl + npal], "lr": 1e-4}, {"params": masters[nl + npal:], "lr": 3e-4},
+              {"params": masters[:nl], "lr": 1e-2}]
+    opt = torch.optim.AdamW(groups, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.0)
+    opt.step()
+    with torch.no_grad():
+        for m in masters[:nl]:
+            m.clamp_(-5 * tau, 5 * tau)
+    for p, m in zip(params, masters):
+        want = m.detach().to(p.dtype).float().numpy()
+        got = f32(p)
+        assert np.allclose(got, want, rtol=1e-2, atol=1e-5), (p.shape, np.abs(got - want).max())

@@ -92,3 +92,34 @@ def test_dense_linear_matches_oracle(dev):
     assert_close(f32(y), f32(x).astype(np.float64) @ f32(w).T, what="dense fwd")
     gx = ops.linear_bwd_x_dense(gy.to(dev), w.to(dev))
     assert_close(f32(gx), f32(gy).astype(np.float64) @ f32(w), what="dense grad_x")
+
+
+def test_gumbel_philox_finite_and_bounded_at_scale(dev):
+    # 2^28 draws: a mapping that lets u reach 0 or 1 would show ~16 infinities here
+    n = 1 << 28
+    g = ops.gumbel_philox((n,), seed=0x5EED, offset=0, device=dev)
+    assert bool(torch.isfinite(g).all())
+    lo, hi = float(g.min()), float(g.max())
+    # u in [2^-24, 1 - 2^-24]  =>  noise in [-log(24 ln 2), -log(-log(1 - 2^-24))]
+    assert -2.82 < lo and hi < 16.64 + 1e-3
+    del g
+
+
+def test_soft_bwd_full_gate_shape_sampled_rows(dev):
+    # gate_proj of the layer config (N=9728, K=2560) with Philox noise made on the GPU;
+    # every output must be finite, and sampled output rows match the oracle
+    M, N, K, tau = 256, 9728, 2560, 0.5
+    _, pal = make_weight(N, K, seed=21)
+    logits = (torch.randn(N, K, 4, generator=gen(22)) * 2.0).to(torch.bfloat16)
+    noise = ops.gumbel_philox((N, K, 4), seed=1234, offset=0, device=dev)
+    x = randn_bf16(M, K, seed=23)
+    gy = randn_bf16(M, N, seed=24)
+    gl, gp = ops.soft_bwd(x.to(dev), gy.to(dev), logits.to(dev), noise, pal.to(dev), tau)
+    assert bool(torch.isfinite(gl).all()) and bool(torch.isfinite(gp).all())
+    rows = torch.tensor([0, 1, 255, 256, 4097, 7777, 9600, N - 1])
+    nz = noise[rows.to(dev)].cpu().numpy()
+    want_gl, want_gp = O.soft_backward(f32(x), f32(gy[:, rows]), f32(logits[rows]), nz,
+                                       pal[rows].numpy(), tau)
+    assert_close(f32(gl[rows.to(dev)]), want_gl, what="grad_logits sampled rows")
+    assert_close(f32(gp[rows.to(dev)]), want_gp, max_rel=1e-3, min_cos=0.99999,
+                 what="grad_palette sampled rows")

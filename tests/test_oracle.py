@@ -192,6 +192,13 @@ def test_gumbel_moments():
         assert abs(noise.var() - math.pi ** 2 / 6) < 0.03
 
 
+def test_gumbel_from_bits_is_finite_at_the_extremes():
+    # the largest and smallest 32-bit draws must map strictly inside (0, 1): no inf noise
+    g = O.gumbel_from_bits(np.array([0, 1, 0x1FF, 0xFFFFFE00, 0xFFFFFFFF], np.uint32))
+    assert np.all(np.isfinite(g))
+    assert g[-1] > 15.0 and g[0] < -2.5
+
+
 def test_philox_random123_known_answers():
     kat = [
         ((0, 0, 0, 0), (0, 0), (0x6627E8D5, 0xE169C58D, 0xBC57AC4C, 0x9B00DBD8)),
