@@ -182,7 +182,9 @@ int64_t plz_gemv_plan(plz_gemv_desc* descs, int n, int M);
 int plz_lut_gemv_grouped(const plz_gemv_desc* descs_device, int n, int64_t total_blocks, int M,
                          void* stream);
 
-/* ---- fused RMSNorm and SwiGLU (HF Qwen3 RMSNorm / MLP) ----------------------------------- */
+/* ---- fused RMSNorm and SwiGLU ------------------------------------------------------------
+ * The reference runs the HF Qwen3 modules unfused (Qwen3RMSNorm and Qwen3MLP, transformers
+ * models/qwen3/modeling_qwen3.py:50-83, used by the decoder layers that qwen_model.py wraps). */
 /* y = bf16(weight * bf16(x * rsqrt(mean(x^2) + eps))) per row, fp32 statistics; rstd fp32
  * [rows] saved for the backward. cols % 8 == 0. */
 int plz_rmsnorm_fwd(const uint16_t* x, const uint16_t* weight, uint16_t* y, float* rstd,
