@@ -26,12 +26,25 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 constexpr int kPalGroup = 256;   // K-extent of one palette group
 constexpr int kIdxPerWord = 16;  // 2-bit indices per int32
 
-// fp32 -> bf16 bits, round to nearest even; NaN stays a quiet NaN.
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// fp32 -> bf16 bits, round to nearest even; NaN stays a NaN. On the device this is the
+// gfx950 conversion instruction (v_cvt_pk_bf16_f32, round to nearest even); the host
+// restates it in integer arithmetic (NaN -> quiet NaN with the top payload bits).
 __host__ __device__ __forceinline__ uint32_t f2bf(float f) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return __builtin_bit_cast(uint16_t, (__bf16)f);
+#else
   uint32_t u = __builtin_bit_cast(uint32_t, f);
   if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (u >> 16) | 0x40u;
   u += 0x7fffu + ((u >> 16) & 1u);
   return u >> 16;
+#endif
+}
+// Two fp32 -> one dword of bf16 {lo, hi} with a single conversion instruction.
+__device__ __forceinline__ uint32_t f2bf2(float lo, float hi) {
+  const bf16x2 v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, v);
 }
 __host__ __device__ __forceinline__ float bf2f(uint32_t b) {
   return __builtin_bit_cast(float, (uint32_t)(b << 16));
@@ -45,6 +58,19 @@ __device__ __forceinline__ float h2f(uint32_t b) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)b);
 }
 
+// Raw buffer loads: a resource covering [p, p + bytes); a lane whose offset is out of range
+// reads zeros (the hardware range check), which replaces per-lane branches.
+typedef __amdgpu_buffer_rsrc_t BufRsrc;
+constexpr uint32_t kBufOob = 0x80000000u;  // an offset past any buffer this library builds
+__device__ __forceinline__ BufRsrc make_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes,
+                                           0x00020000);
+}
+__device__ __forceinline__ uint4 buf_load16(BufRsrc r, uint32_t off) {
+  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 // Byte permute: result byte i = byte sel.byte[i] of the 8-byte value {hi:lo}.
 __device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) {
   return __builtin_amdgcn_perm(hi, lo, sel);
@@ -56,8 +82,8 @@ struct PalLut {
   uint32_t lo, hi;
 };
 __device__ __forceinline__ PalLut make_lut(float p0, float p1, float p2, float p3) {
-  uint32_t b01 = f2bf(p0) | (f2bf(p1) << 16);
-  uint32_t b23 = f2bf(p2) | (f2bf(p3) << 16);
+  uint32_t b01 = f2bf2(p0, p1);
+  uint32_t b23 = f2bf2(p2, p3);
   PalLut t;
   t.lo = perm(b23, b01, 0x06040200u);
   t.hi = perm(b23, b01, 0x07050301u);

@@ -4,14 +4,22 @@
 // (fused_lut_kernel.cu:309-518). Here the work is bandwidth-bound: 2 bits of index plus
 // 0.5 bit of fp32 palette per weight are streamed once.
 //
-// Layout of the work. A workgroup (4 wave64s) owns RB blocks of 16 rows; its 4 waves
-// split K by palette groups (wave w takes groups w, w+4, ...) and the partial sums are
-// added in LDS at the end in a fixed order. Inside a wave, v_mfma_f32_16x16x32_bf16 computes
-// C[n][m] with A = 16 weight rows and B = x^T (columns m >= M are zero). Lane (n = l%16,
-// g = l/16) streams 16 bytes of indices = 64 consecutive k of row n per palette group, so
-// its 8 MFMA k-slots for a step come from one packed word. The dequantisation of a word
-// yields pairs {w_j, w_j+4} and {w_j+8, w_j+12} (the cheapest byte-permute order); the x
-// fragment is permuted into the same slot order in registers, which leaves the dot
+// Layout of the work. A workgroup (4 wave64s) owns 64*RB rows and streams the whole of K
+// in iterations of 4 palette groups (1024 k). Wave w owns RB blocks of 16 rows. Lane
+// (n = l%16, q = l/16) works on row n and palette group 4*it + q: it reads that group's 64
+// bytes of indices (4 x 16 B, contiguous) and its 16-byte palette, so the four lanes of a
+// row read 256 contiguous bytes of indices and 64 contiguous bytes of palettes per
+// iteration. These loads are issued one iteration ahead of their use.
+// x is shared by every wave: each iteration's x chunk is loaded once per workgroup,
+// permuted into MFMA fragment order and kept in LDS (2 KB per token, double buffered, one
+// barrier per iteration); waves read their fragments with one 16-byte LDS read each. A
+// GEMV that loads x per wave is limited by the vector-memory data-return path, not HBM.
+// Inside a wave, v_mfma_f32_16x16x32_bf16 computes C[n][m] with A = 16 weight rows and
+// B = x^T. Fragment lanes of tokens m >= M repeat token M-1: they only feed output columns
+// m >= M, which are never stored. The four lane quarters feed different palette groups
+// into the same MFMA, which is fine because the product sums over every k. A packed word
+// dequantises into the slots {w_j, w_j+4} and {w_j+8, w_j+12} (the cheapest byte-permute
+// order); the x fragments are permuted into the same slot order, which leaves the dot
 // product unchanged.
 #include "plz_common.h"
 
@@ -39,10 +47,24 @@ __device__ __forceinline__ void xslots(uint4 x0, uint4 x1, u32x4& s0, u32x4& s1)
              perm(x1.w, x1.y, 0x05040100u), perm(x1.w, x1.y, 0x07060302u)};
 }
 
+// Workgroup barrier without the memory fence of __syncthreads(), which would also wait for
+// the weight loads in flight: this wave's LDS operations complete, then s_barrier.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xF | (3 << 14) | (7 << 4));  // lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// LDS x fragments of one iteration: [sub-step 4][fragment 8][quarter 4][token m < M] x 16 B
+// = 2 KB per token, double buffered (dynamic LDS: 4 KB x M per workgroup).
+constexpr int kXFragBytesPerToken = 4 * 8 * 4 * 16;
+constexpr int kGemvRb = 2;                 // row blocks of 16 per wave
+constexpr int kGemvRows = 64 * kGemvRb;   // rows per workgroup
+
 template <int RB, bool GROUPED>
 __global__ __launch_bounds__(256) void gemv_kernel(const plz_gemv_desc* __restrict__ descs,
                                                    int n_desc, plz_gemv_desc single, int M) {
-  __shared__ f32x4 red[4][RB][64];
+  extern __shared__ u32x4 xlds[];  // [2][4*8*4*M]
   const int64_t blk = blockIdx.x;
   plz_gemv_desc d;
   if (GROUPED) {
@@ -56,74 +78,148 @@ __global__ __launch_bounds__(256) void gemv_kernel(const plz_gemv_desc* __restri
     d = single;
   }
   const int64_t N = d.N, K = d.K;
-  const int64_t n0 = (blk - d.block_begin) * (RB * 16);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int nl = lane & 15, g = lane >> 4;
-  const int64_t wpr = K / kIdxPerWord, gpr = K / kPalGroup;
-  const bool xl = nl < M;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t row0 = (blk - d.block_begin) * (64 * RB) + wave * (16 * RB);
+  const bool has_rows = row0 < N;  // waves without rows still take part in the barriers
+  const int nl = lane & 15, qg = lane >> 4;
+  const int gpr = (int)(K / kPalGroup);
+  const int iters = (gpr + 3) / 4;
+  // sizes were checked on the host to fit the 32-bit buffer range
+  const BufRsrc rq = make_rsrc(d.packed, (uint32_t)(N * K / 4));
+  const BufRsrc rp = make_rsrc(d.palette, (uint32_t)(N * gpr * 16));
+  const BufRsrc rx = make_rsrc(d.x, (uint32_t)(M * K * 2));
+  uint32_t oq[RB], op[RB];
+#pragma unroll
+  for (int r = 0; r < RB; ++r) {
+    const int64_t n = row0 + 16 * r + nl;
+    oq[r] = n < N ? (uint32_t)(n * (K / 4) + 64 * qg) : kBufOob;
+    op[r] = n < N ? (uint32_t)((n * gpr + qg) * 16) : kBufOob;
+  }
+
+  // x staging: item i < 64*M of an iteration is (m = i/64, q, sub-step st, word w); it
+  // covers x[m][k0 .. k0+16) with k0 = 256*(4*it + q) + 64*st + 16*w, and produces the two
+  // fragments 2w, 2w+1 of sub-step st for fragment lane m + 16*q.
+  const int n_items = 64 * M;
+  const int xbuf = 4 * 8 * 4 * M;  // u32x4 per buffer
+  // fragment lanes of tokens m >= M read token M-1 (a broadcast); their columns are dropped
+  const int xl = qg * M + (nl < M ? nl : M - 1);
+  auto stage_load = [&](int it, int i, uint4& a, uint4& b) {
+    const int m = i >> 6, q = (i >> 4) & 3, st = (i >> 2) & 3, w = i & 3;
+    const bool v = 4 * it + q < gpr;
+    const uint32_t o = v ? (uint32_t)((m * K + 256 * (4 * it + q) + 64 * st + 16 * w) * 2) : kBufOob;
+    a = buf_load16(rx, o);
+    b = buf_load16(rx, o + 16u);
+  };
+  auto stage_store = [&](int buf, int i, uint4 a, uint4 b) {
+    const int m = i >> 6, q = (i >> 4) & 3, st = (i >> 2) & 3, w = i & 3;
+    u32x4 s0, s1;
+    xslots(a, b, s0, s1);
+    u32x4* xb = xlds + buf * xbuf;
+    xb[((st * 8 + 2 * w) * 4 + q) * M + m] = s0;
+    xb[((st * 8 + 2 * w + 1) * 4 + q) * M + m] = s1;
+  };
+  // M <= 16, so a thread handles at most 4 items per iteration
+  constexpr int kMaxItems = 4;
+  uint4 xa[kMaxItems], xb[kMaxItems];
+  auto stage_issue = [&](int it) {
+#pragma unroll
+    for (int j = 0; j < kMaxItems; ++j)
+      if (tid + 256 * j < n_items) stage_load(it, tid + 256 * j, xa[j], xb[j]);
+  };
+  auto stage_commit = [&](int buf) {
+#pragma unroll
+    for (int j = 0; j < kMaxItems; ++j)
+      if (tid + 256 * j < n_items) stage_store(buf, tid + 256 * j, xa[j], xb[j]);
+  };
+
+  uint4 q[RB][4], p[RB];
+  auto load_w = [&](int it, uint4 (&qq)[RB][4], uint4 (&pp)[RB]) {
+    const bool v = 4 * it + qg < gpr;
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+      const uint32_t o = v ? oq[r] + 256u * it : kBufOob;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) qq[r][j] = buf_load16(rq, o + 16u * j);
+      pp[r] = buf_load16(rp, v ? op[r] + 64u * it : kBufOob);
+    }
+  };
 
   f32x4 acc[RB];
 #pragma unroll
   for (int r = 0; r < RB; ++r) acc[r] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  for (int64_t kg = wave; kg < gpr; kg += 4) {
-    // x[m = nl][kg*256 + 64g .. +64) -> 8 slot fragments (steps s = 0..7)
-    u32x4 xs[8];
-    {
-      const uint4* xp = reinterpret_cast<const uint4*>(d.x + (int64_t)nl * K + kg * kPalGroup + 64 * g);
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        uint4 x0 = make_uint4(0, 0, 0, 0), x1 = x0;
-        if (xl) { x0 = xp[2 * w]; x1 = xp[2 * w + 1]; }
-        xslots(x0, x1, xs[2 * w], xs[2 * w + 1]);
-      }
+  stage_issue(0);
+  if (has_rows) load_w(0, q, p);
+  stage_commit(0);
+  lds_barrier();
+  for (int it = 0; it < iters; ++it) {
+    const int buf = it & 1;
+    const bool more = it + 1 < iters;
+    uint4 qn[RB][4], pn[RB];
+    if (more) {
+      stage_issue(it + 1);
+      if (has_rows) load_w(it + 1, qn, pn);
     }
+    if (has_rows) {
+      PalLut t[RB];
 #pragma unroll
-    for (int r = 0; r < RB; ++r) {
-      const int64_t n = n0 + 16 * r + nl;
-      uint4 q = make_uint4(0, 0, 0, 0);
-      float4 p = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (n < N) {
-        q = *reinterpret_cast<const uint4*>(d.packed + n * wpr + kg * 16 + 4 * g);
-        p = *reinterpret_cast<const float4*>(d.palette + (n * gpr + kg) * 4);
-      }
-      const PalLut t = make_lut(p.x, p.y, p.z, p.w);
-      const uint32_t qs[4] = {q.x, q.y, q.z, q.w};
+      for (int r = 0; r < RB; ++r)
+        t[r] = make_lut(__uint_as_float(p[r].x), __uint_as_float(p[r].y),
+                        __uint_as_float(p[r].z), __uint_as_float(p[r].w));
 #pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        u32x4 a0, a1;
-        dequant16_slots(qs[w], t, a0, a1);
-        acc[r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a0),
-                                                         __builtin_bit_cast(bf16x8, xs[2 * w]),
-                                                         acc[r], 0, 0, 0);
-        acc[r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a1),
-                                                         __builtin_bit_cast(bf16x8, xs[2 * w + 1]),
-                                                         acc[r], 0, 0, 0);
-      }
-    }
-  }
+      for (int st = 0; st < 4; ++st) {
+        u32x4 xs[8];
 #pragma unroll
-  for (int r = 0; r < RB; ++r) red[wave][r][lane] = acc[r];
-  __syncthreads();
-  if (wave == 0) {
-    // acc lane l: C[n = 4*(l/16) + e][m = l%16]
+        for (int f = 0; f < 8; ++f) xs[f] = xlds[buf * xbuf + (st * 8 + f) * 4 * M + xl];
 #pragma unroll
-    for (int r = 0; r < RB; ++r) {
-      const f32x4 s = red[0][r][lane] + red[1][r][lane] + red[2][r][lane] + red[3][r][lane];
-      const int m = lane & 15;
-      if (m < M) {
+        for (int r = 0; r < RB; ++r) {
+          const uint32_t qs[4] = {q[r][st].x, q[r][st].y, q[r][st].z, q[r][st].w};
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int64_t n = n0 + 16 * r + 4 * (lane >> 4) + e;
-          if (n < N) d.y[(int64_t)m * N + n] = (uint16_t)f2bf(s[e]);
+          for (int w = 0; w < 4; ++w) {
+            u32x4 a0, a1;
+            dequant16_slots(qs[w], t[r], a0, a1);
+            acc[r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                __builtin_bit_cast(bf16x8, a0), __builtin_bit_cast(bf16x8, xs[2 * w]), acc[r],
+                0, 0, 0);
+            acc[r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                __builtin_bit_cast(bf16x8, a1), __builtin_bit_cast(bf16x8, xs[2 * w + 1]),
+                acc[r], 0, 0, 0);
+          }
         }
+      }
+    }
+    if (more) {
+      stage_commit(buf ^ 1);
+#pragma unroll
+      for (int r = 0; r < RB; ++r) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) q[r][j] = qn[r][j];
+        p[r] = pn[r];
+      }
+    }
+    lds_barrier();
+  }
+  if (!has_rows) return;
+  // acc lane l: C[n = 4*(l/16) + e][m = l%16]
+  const int m = lane & 15;
+  if (m < M) {
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int64_t n = row0 + 16 * r + 4 * (lane >> 4) + e;
+        if (n < N) d.y[(int64_t)m * N + n] = (uint16_t)f2bf(acc[r][e]);
       }
     }
   }
 }
 
-constexpr int kRbGrouped = 4;
-constexpr int kRbSingle = 1;
+template <bool GROUPED>
+static void launch_gemv(int M, dim3 grid, hipStream_t st, const plz_gemv_desc* descs, int n,
+                        plz_gemv_desc single) {
+  hipLaunchKernelGGL((gemv_kernel<kGemvRb, GROUPED>), grid, dim3(256),
+                     2 * kXFragBytesPerToken * M, st, descs, n, single, M);
+}
 
 static int check_desc(const plz_gemv_desc& d, int i) {
   PLZ_REQUIRE(d.N >= 0 && d.K >= 0, "plz_gemv: descriptor %d has a negative shape", i);
@@ -131,6 +227,9 @@ static int check_desc(const plz_gemv_desc& d, int i) {
               (long long)d.K);
   PLZ_REQUIRE(d.N == 0 || d.K == 0 || (d.x && d.packed && d.palette && d.y),
               "plz_gemv: descriptor %d has a null pointer", i);
+  PLZ_REQUIRE(d.N * d.K / 4 < (int64_t)kBufOob && d.N * (d.K / 256) * 16 < (int64_t)kBufOob &&
+                  16 * d.K * 2 < (int64_t)kBufOob,
+              "plz_gemv: descriptor %d is too large (packed or palette above 2 GiB)", i);
   PLZ_REQUIRE((((uintptr_t)d.x | (uintptr_t)d.packed | (uintptr_t)d.palette) & 15) == 0,
               "plz_gemv: descriptor %d: x, packed and palette must be 16-byte aligned", i);
   return PLZ_OK;
@@ -153,9 +252,8 @@ int plz_lut_gemv(const uint16_t* x, const int32_t* packed, const float* palette,
     hipMemsetAsync(y, 0, (size_t)M * N * 2, (hipStream_t)stream);
     return check_launch("plz_lut_gemv");
   }
-  const int64_t blocks = (N + 16 * kRbSingle - 1) / (16 * kRbSingle);
-  hipLaunchKernelGGL((gemv_kernel<kRbSingle, false>), dim3((unsigned)blocks), dim3(256), 0,
-                     (hipStream_t)stream, nullptr, 0, d, (int)M);
+  const int64_t blocks = (N + kGemvRows - 1) / kGemvRows;
+  launch_gemv<false>((int)M, dim3((unsigned)blocks), (hipStream_t)stream, nullptr, 0, d);
   return check_launch("plz_lut_gemv");
 }
 
@@ -169,7 +267,7 @@ int64_t plz_gemv_plan(plz_gemv_desc* descs, int n, int M) {
     int rc = check_desc(descs[i], i);
     if (rc) return -rc;
     descs[i].block_begin = total;
-    if (descs[i].K > 0) total += (descs[i].N + 16 * kRbGrouped - 1) / (16 * kRbGrouped);
+    if (descs[i].K > 0) total += (descs[i].N + kGemvRows - 1) / kGemvRows;
   }
   return total;
 }
@@ -181,8 +279,7 @@ int plz_lut_gemv_grouped(const plz_gemv_desc* descs_device, int n, int64_t total
   if (n == 0 || total_blocks == 0) return PLZ_OK;
   PLZ_REQUIRE(descs_device, "plz_lut_gemv_grouped: null descriptor table");
   plz_gemv_desc dummy = {};
-  hipLaunchKernelGGL((gemv_kernel<kRbGrouped, true>), dim3((unsigned)total_blocks), dim3(256), 0,
-                     (hipStream_t)stream, descs_device, n, dummy, M);
+  launch_gemv<true>(M, dim3((unsigned)total_blocks), (hipStream_t)stream, descs_device, n, dummy);
   return check_launch("plz_lut_gemv_grouped");
 }
 

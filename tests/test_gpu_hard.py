@@ -43,6 +43,30 @@ def test_dequant_rounds_fp32_palette_to_nearest_even(dev):
     assert np.array_equal(w, O.dequant_bits(idx.numpy(), pal.numpy()))
 
 
+def test_dequant_rounding_special_values(dev):
+    # fp32 denormals (rounding to bf16 denormals, up to the smallest normal, and ties),
+    # negative ties, overflow to inf, +-inf, +-0, the largest finite values, and a
+    # random sweep over all exponents; NaN must stay NaN
+    special = [0x00000001, 0x00007FFF, 0x00008000, 0x00018000, 0x0000FFFF, 0x007FFFFF,
+               0x007F8000, 0x80008000, 0x80018000, 0x807FFFFF, 0xBC018000, 0xBC028000,
+               0x7F7F7FFF, 0x7F7F8000, 0x7F7FFFFF, 0xFF7FFFFF, 0x7F800000, 0xFF800000,
+               0x00000000, 0x80000000, 0x7F7EFFFF, 0x3F808000, 0x3F818000, 0x3F80FFFF]
+    rnd = np.random.default_rng(5).integers(0, 2**32, size=4096 - len(special) - 4,
+                                            dtype=np.uint64).astype(np.uint32)
+    rnd = rnd[((rnd >> 23) & 0xFF) != 0xFF]  # finite only
+    bits = np.concatenate([np.array(special, np.uint32), rnd,
+                           np.zeros(4096 - len(special) - rnd.size - 4, np.uint32),
+                           np.array([0x7FC00000, 0x7F800001, 0xFFC12345, 0x7FFFFFFF], np.uint32)])
+    N, K = 64, 4096  # N * K/256 * 4 = 4096 palette entries, each selected by some weight
+    pal = torch.from_numpy(bits.view(np.float32).reshape(N, K // 256, 4).copy())
+    idx = torch.arange(4, dtype=torch.uint8).repeat(N, K // 4)
+    w = ops.dequant(_packed(idx, dev), pal.to(dev)).view(torch.int16).cpu().numpy().view(np.uint16)
+    want = O.dequant_bits(idx.numpy(), pal.numpy())
+    nan = np.isnan(O.bf16_to_f32(want))
+    assert np.array_equal(w[~nan], want[~nan])
+    assert np.all(np.isnan(O.bf16_to_f32(w[nan])))
+
+
 def _oracle_problem(M, N, K, seed, rank=0):
     idx, pal = make_weight(N, K, seed=seed)
     x = randn_bf16(M, K, seed=seed + 1)
