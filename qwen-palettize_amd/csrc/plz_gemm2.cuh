@@ -7,10 +7,11 @@
 //
 // Each operand tile sits in LDS in one of two layouts:
 //   Row tile  [row][r]: 16-byte chunks of 8 consecutive r, chunk index XOR ((row >> 1) & 7).
-//             Fragments: two ds_read_b64 per lane (row = lane%32, chunk = 2*ks + lane/32).
+//             Fragments: one ds_read_b128 per lane (row = lane%32, chunk = 2*ks + lane/32),
+//             free of bank conflicts with this swizzle.
 //   Col tile  [r][row]: the operand's own memory order when rows are contiguous
 //             (MN-contiguous: grad_y and x in dW, W in grad_x). Chunks of 8 consecutive
-//             rows, chunk index XOR (r & 15). Fragments: two ds_read_b64_tr_b16 per lane.
+//             rows, chunk index XOR col_swz(r). Fragments: two ds_read_b64_tr_b16 per lane.
 //             Within each 16-lane group lane i points at rows 4*(i%4)..+3 of reduction
 //             index kbase + i/4; the instruction hands lane j elements j, j+16, j+32, j+48
 //             of the group's 64 loaded values, i.e. row j at kbase..kbase+3 -- the MFMA
@@ -35,7 +36,10 @@ typedef __attribute__((address_space(3))) uint8_t lds_u8;
 
 __device__ __forceinline__ int row_swz(int row) { return (row >> 1) & 7; }
 __device__ __forceinline__ int row_chunk(int row, int c) { return row * (BK / 8) + (c ^ row_swz(row)); }
-__device__ __forceinline__ int col_swz(int kr) { return kr & 15; }
+// kr ^ 4*(kr & 3): the tr16 fragment reads (4 consecutive kr x 4 chunks per 32 lanes) and
+// the 16-byte dequant stores (16 consecutive kr per wave) are both free of bank conflicts
+// on gfx950 (measured with SQ_LDS_BANK_CONFLICT).
+__device__ __forceinline__ int col_swz(int kr) { return (kr ^ ((kr & 3) << 2)) & 15; }
 __device__ __forceinline__ int col_chunk(int kr, int c) { return kr * (TILE / 8) + (c ^ col_swz(kr)); }
 
 struct Args {
@@ -87,9 +91,14 @@ struct LutRegs {
   uint4 q;
   float4 p;
 };
-// Forward: tile rows are n (256 rows x 64 k); thread t owns row t.
+// Forward: tile rows are n (256 rows x 64 k); thread t owns row lut_row_of(t), a permutation
+// within groups of 8 under which the 4 lanes of each store group write rows with distinct
+// (row >> 1) & 3, i.e. distinct 16-byte columns of a 64-byte window (no bank conflicts).
+__device__ __forceinline__ int lut_row_of(int t) {
+  return (t & ~7) | ((t & 3) << 1) | ((t >> 2) & 1);
+}
 __device__ __forceinline__ void lut_row_load(const Args& g, int64_t n0, int64_t k0, LutRegs& r) {
-  const int64_t n = n0 + threadIdx.x;
+  const int64_t n = n0 + lut_row_of(threadIdx.x);
   r.q = make_uint4(0, 0, 0, 0);
   r.p = make_float4(0.f, 0.f, 0.f, 0.f);
   if (n < g.Nw) {
@@ -99,7 +108,7 @@ __device__ __forceinline__ void lut_row_load(const Args& g, int64_t n0, int64_t 
 }
 __device__ __forceinline__ void lut_row_store(uint4* lds, const LutRegs& r) {
   const PalLut t = make_lut(r.p.x, r.p.y, r.p.z, r.p.w);
-  const int row = threadIdx.x;
+  const int row = lut_row_of(threadIdx.x);
   const uint32_t qs[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
 #pragma unroll
   for (int w = 0; w < 4; ++w) {
@@ -108,6 +117,16 @@ __device__ __forceinline__ void lut_row_store(uint4* lds, const LutRegs& r) {
     lds[row_chunk(row, 2 * w)] = make_uint4(o[0], o[1], o[2], o[3]);
     lds[row_chunk(row, 2 * w + 1)] = make_uint4(o[4], o[5], o[6], o[7]);
   }
+}
+// The same store in four parts (part = word of the 64 k), for interleaving with MFMAs.
+__device__ __forceinline__ void lut_row_store_part(uint4* lds, const LutRegs& r, int part) {
+  const PalLut t = make_lut(r.p.x, r.p.y, r.p.z, r.p.w);
+  const int row = lut_row_of(threadIdx.x);
+  const uint32_t q = part == 0 ? r.q.x : part == 1 ? r.q.y : part == 2 ? r.q.z : r.q.w;
+  uint32_t o[8];
+  dequant16(q, t, o);
+  lds[row_chunk(row, 2 * part)] = make_uint4(o[0], o[1], o[2], o[3]);
+  lds[row_chunk(row, 2 * part + 1)] = make_uint4(o[4], o[5], o[6], o[7]);
 }
 // grad_x: tile rows are k (256), reduction n (64). Thread t = 64*w + l owns
 // n = n0 + 16*w + l%16 and k = k0 + 64*(l/16) .. +64, so that the 16-byte LDS stores of a
@@ -138,19 +157,25 @@ __device__ __forceinline__ void lut_col_store(uint4* lds, const LutRegs& r) {
   }
 }
 
+__device__ __forceinline__ void lut_col_store_part(uint4* lds, const LutRegs& r, int part) {
+  const PalLut t = make_lut(r.p.x, r.p.y, r.p.z, r.p.w);
+  const int kr = lut_col_kr(), cb = 8 * lut_col_quarter();
+  const uint32_t q = part == 0 ? r.q.x : part == 1 ? r.q.y : part == 2 ? r.q.z : r.q.w;
+  uint32_t o[8];
+  dequant16(q, t, o);
+  lds[col_chunk(kr, cb + 2 * part)] = make_uint4(o[0], o[1], o[2], o[3]);
+  lds[col_chunk(kr, cb + 2 * part + 1)] = make_uint4(o[4], o[5], o[6], o[7]);
+}
+
 // ---- fragments (v_mfma_f32_32x32x16_bf16: lane l holds row l%32, k-slots 8*(l/32)..+7) --
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-// Read as two 8-byte halves: on gfx950 two ds_read_b64 move a fragment through the LDS
-// faster than one ds_read_b128 (about 12 vs 16.5 CU cycles per KB for a wave, measured).
+// One ds_read_b128 per lane: with the row swizzle the 64 lanes hit no bank twice (two
+// ds_read_b64 halves of the same chunks conflict 2-way: half of every chunk sits in the
+// same banks).
 __device__ __forceinline__ bf16x8 frag_row(const uint4* lds, int rowbase, int ks, int lane) {
   const int ch = row_chunk(rowbase + (lane & 31), 2 * ks + (lane >> 5));
-  const u32x2* p = reinterpret_cast<const u32x2*>(lds + ch);
-  int hi_off = 1;
-  asm("" : "+v"(hi_off));  // opaque offset: keeps the load/store vectorizer from fusing the halves
-  const u32x2 lo = p[0];
-  const u32x2 hi = p[hi_off];
-  return __builtin_bit_cast(bf16x8, u32x4{lo.x, lo.y, hi.x, hi.y});
+  return __builtin_bit_cast(bf16x8, lds[ch]);
 }
 // Col tile: per 16-lane group j = lane/16 the rows 16*(j&1)..+15 at k-group j>>1.
 __device__ __forceinline__ bf16x8 frag_col(const lds_u8* lds, int rowbase, int ks, int lane) {

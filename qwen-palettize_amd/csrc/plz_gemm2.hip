@@ -51,7 +51,11 @@ __device__ __forceinline__ int ptile(int row, int col) {  // 128 x 256 fp32 stag
 
 // One reduction stage of MFMAs on LDS tiles: 4 k-steps of 16, 4x4 blocks of 32x32 per wave.
 // Fragments are double-buffered in registers: the LDS reads of k-step ks+1 are issued before
-// the 16 MFMAs of k-step ks, so one wave per SIMD keeps the matrix core busy.
+// the 16 MFMAs of k-step ks, so one wave per SIMD keeps the matrix core busy. The scheduling
+// barriers pin that order (left alone, the compiler sinks each A read next to its first
+// MFMA and exposes the LDS latency every 4 MFMAs). fill(part), part = 0..3, runs between
+// the MFMA groups: VALU work for the next stage (the palette dequantisation) that then
+// overlaps with the matrix core.
 template <bool A_COL, bool B_COL>
 __device__ __forceinline__ void load_frags(const lds_u8* a_s, const lds_u8* b_s, int ks, int wi,
                                            int wj, int lane, bf16x8 (&a)[4], bf16x8 (&b)[4]) {
@@ -71,18 +75,55 @@ __device__ __forceinline__ void mma16(f32x16 (&acc)[4][4], const bf16x8 (&a)[4],
     for (int j = 0; j < 4; ++j)
       acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
 }
-template <bool A_COL, bool B_COL>
+// Instruction interleave of one k-step: the LDS reads of the next k-step go one after each
+// of the first MFMAs, the VALU of fill() between the remaining ones, so that neither the
+// LDS queue nor the VALU stalls the issue of MFMAs (sched_group_barrier masks: 0x008 MFMA,
+// 0x100 LDS read, 0x200 LDS write, 0x002 VALU).
+template <int NREAD, int NVALU_PER_MFMA, int NWRITE>
+__device__ __forceinline__ void interleave_kstep() {
+#pragma unroll
+  for (int i = 0; i < NREAD; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+  }
+#pragma unroll
+  for (int i = NREAD; i < 16; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    if (NVALU_PER_MFMA > 0) __builtin_amdgcn_sched_group_barrier(0x002, NVALU_PER_MFMA, 0);
+    if (i - NREAD < NWRITE) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+  }
+}
+
+template <bool A_COL, bool B_COL, bool FILL, typename Fill>
 __device__ __forceinline__ void mma_stage(const lds_u8* a_s, const lds_u8* b_s, f32x16 (&acc)[4][4],
-                                          int wi, int wj, int lane) {
+                                          int wi, int wj, int lane, Fill&& fill) {
+  // LDS read instructions per k-step: a row fragment is one ds_read_b128, a col fragment two
+  // ds_read_b64_tr_b16
+  constexpr int NREAD = 4 * (A_COL ? 2 : 1) + 4 * (B_COL ? 2 : 1);
+  constexpr int NV = FILL ? 4 : 0;
+  constexpr int NW = FILL ? 2 : 0;
   bf16x8 a0[4], b0[4], a1[4], b1[4];
   load_frags<A_COL, B_COL>(a_s, b_s, 0, wi, wj, lane, a0, b0);
+  __builtin_amdgcn_sched_barrier(0);
   load_frags<A_COL, B_COL>(a_s, b_s, 1, wi, wj, lane, a1, b1);
   mma16(acc, a0, b0);
+  fill(0);
+  interleave_kstep<NREAD, NV, NW>();
+  __builtin_amdgcn_sched_barrier(0);
   load_frags<A_COL, B_COL>(a_s, b_s, 2, wi, wj, lane, a0, b0);
   mma16(acc, a1, b1);
+  fill(1);
+  interleave_kstep<NREAD, NV, NW>();
+  __builtin_amdgcn_sched_barrier(0);
   load_frags<A_COL, B_COL>(a_s, b_s, 3, wi, wj, lane, a1, b1);
   mma16(acc, a0, b0);
+  fill(2);
+  interleave_kstep<NREAD, NV, NW>();
+  __builtin_amdgcn_sched_barrier(0);
   mma16(acc, a1, b1);
+  fill(3);
+  interleave_kstep<0, NV, NW>();
+  __builtin_amdgcn_sched_barrier(0);
 }
 
 template <int KA, int KB, int EPI>
@@ -171,8 +212,15 @@ __global__ __launch_bounds__(256) void gemm2_kernel(const Args g) {
     const bool more = kt + 1 < nst;
     if (more) issue(cur ^ 1, kt + 1);
     const lds_u8* As = lbase + cur * 2 * TILE_BYTES;
-    mma_stage<A_COL, B_COL>(As, As + TILE_BYTES, acc, wi, wj, lane);
-    if (more) finish(cur ^ 1, kt + 1);
+    // the next stage's palette dequantisation runs between this stage's MFMA groups
+    uint4* Bn = (uint4*)(lbase + (cur ^ 1) * 2 * TILE_BYTES + TILE_BYTES);
+    const bool lut_next = more && kt + 1 < nfull && (KB == OP_LUT_ROW || KB == OP_LUT_COL);
+    mma_stage<A_COL, B_COL, KB == OP_LUT_ROW || KB == OP_LUT_COL>(
+        As, As + TILE_BYTES, acc, wi, wj, lane, [&](int part) {
+      if (!lut_next) return;
+      if (KB == OP_LUT_ROW) lut_row_store_part(Bn, lr, part);
+      if (KB == OP_LUT_COL) lut_col_store_part(Bn, lr, part);
+    });
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
   }
