@@ -7,6 +7,8 @@
 //                               (fused_lut_kernel.cu:1877-1924, triton_soft_backward.py:227-325)
 //   plz_linear_fwd_dense / plz_linear_bwd_x_dense   the same on a materialised bf16 W
 //                               (fused_lut_linear_cuda.py:912, 944)
+#include <type_traits>
+
 #include "plz_gemm2.cuh"
 #include "palettize_hip.h"
 
@@ -94,21 +96,37 @@ __device__ __forceinline__ void interleave_kstep() {
   }
 }
 
-template <bool A_COL, bool B_COL, bool FILL, typename Fill>
+// The first k-step also spreads the next stage's global->LDS copies (0x020 VMEM), one per MFMA:
+// issued as a burst at the stage start they stalled the wave behind the memory pipeline.
+template <int NREAD, int NVALU_PER_MFMA, int NWRITE, int NVMEM>
+__device__ __forceinline__ void interleave_kstep_vmem() {
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    if (i < NREAD) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    if (i < NVMEM) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+    if (i >= NREAD && NVALU_PER_MFMA > 0) __builtin_amdgcn_sched_group_barrier(0x002, NVALU_PER_MFMA, 0);
+    if (i >= NREAD && i - NREAD < NWRITE) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+  }
+}
+template <bool A_COL, bool B_COL, bool FILL, typename Dma, typename Fill>
 __device__ __forceinline__ void mma_stage(const lds_u8* a_s, const lds_u8* b_s, f32x16 (&acc)[4][4],
-                                          int wi, int wj, int lane, Fill&& fill) {
+                                          int wi, int wj, int lane, Dma&& dma, Fill&& fill) {
   // LDS read instructions per k-step: a row fragment is one ds_read_b128, a col fragment two
   // ds_read_b64_tr_b16
   constexpr int NREAD = 4 * (A_COL ? 2 : 1) + 4 * (B_COL ? 2 : 1);
   constexpr int NV = FILL ? 4 : 0;
   constexpr int NW = FILL ? 2 : 0;
+  // global->LDS copies of the next stage issued by dma(): 8 per dense operand
+  constexpr int NDMA = FILL ? 8 : 16;
   bf16x8 a0[4], b0[4], a1[4], b1[4];
   load_frags<A_COL, B_COL>(a_s, b_s, 0, wi, wj, lane, a0, b0);
   __builtin_amdgcn_sched_barrier(0);
   load_frags<A_COL, B_COL>(a_s, b_s, 1, wi, wj, lane, a1, b1);
+  dma();
   mma16(acc, a0, b0);
   fill(0);
-  interleave_kstep<NREAD, NV, NW>();
+  interleave_kstep_vmem<NREAD, NV, NW, NDMA>();
   __builtin_amdgcn_sched_barrier(0);
   load_frags<A_COL, B_COL>(a_s, b_s, 2, wi, wj, lane, a0, b0);
   mma16(acc, a1, b1);
@@ -167,7 +185,25 @@ __global__ __launch_bounds__(256) void gemm2_kernel(const Args g) {
   const bool lora = EPI == EPI_BF16 && g.R2 > 0 && blockIdx.z == 0;
   const int nst = nfull + (tail ? 1 : 0) + (lora ? 1 : 0);
 
-  LutRegs lr;
+  // The palette operand's registers are loaded one stage ahead of the copies: during stage
+  // kt, lr_cur holds the LUT words of stage kt+1 (loaded during stage kt-1), which are
+  // dequantised between this stage's MFMAs, and lr_next receives those of stage kt+2. So no
+  // wave waits on a fresh global load.
+  LutRegs lr_cur, lr_next;
+  auto lut_load = [&](int kt, LutRegs& r) {
+    const int64_t r0 = rbeg + (int64_t)kt * BK;
+    if (KB == OP_LUT_ROW) lut_row_load(g, j0, r0, r);
+    if (KB == OP_LUT_COL) lut_col_load(g, j0, r0, r);
+  };
+  auto issue_full = [&](int s, int kt) {
+    lds_u8* As = lbase + s * 2 * TILE_BYTES;
+    lds_u8* Bs = As + TILE_BYTES;
+    const int64_t r0 = rbeg + (int64_t)kt * BK;
+    if (KA == OP_ROW) copy_row_tile(As, g.a, g.lda, i0, g.I, r0);
+    else copy_col_tile(As, g.a, g.lda, i0, g.I, r0);
+    if (KB == OP_ROW) copy_row_tile(Bs, g.b, g.ldb, j0, g.J, r0);
+    else if (KB == OP_COL) copy_col_tile(Bs, g.b, g.ldb, j0, g.J, r0);
+  };
   auto issue = [&](int s, int kt) {
     lds_u8* As = lbase + s * 2 * TILE_BYTES;
     lds_u8* Bs = As + TILE_BYTES;
@@ -177,49 +213,61 @@ __global__ __launch_bounds__(256) void gemm2_kernel(const Args g) {
       else copy_col_tile(As, g.a, g.lda, i0, g.I, r0);
       if (KB == OP_ROW) copy_row_tile(Bs, g.b, g.ldb, j0, g.J, r0);
       else if (KB == OP_COL) copy_col_tile(Bs, g.b, g.ldb, j0, g.J, r0);
-      else if (KB == OP_LUT_ROW) lut_row_load(g, j0, r0, lr);
-      else lut_col_load(g, j0, r0, lr);
     } else if (tail && kt == nfull) {
       const int64_t r0 = rbeg + (int64_t)nfull * BK;
       if (KA == OP_ROW) copy_row_tile_masked((uint4*)As, g.a, g.lda, i0, g.I, r0, rend);
       else copy_col_tile_masked((uint4*)As, g.a, g.lda, i0, g.I, r0, rend);
       if (KB == OP_ROW) copy_row_tile_masked((uint4*)Bs, g.b, g.ldb, j0, g.J, r0, rend);
       else if (KB == OP_COL) copy_col_tile_masked((uint4*)Bs, g.b, g.ldb, j0, g.J, r0, rend);
-      else if (KB == OP_LUT_ROW) { lut_row_load(g, j0, r0, lr); lut_row_store((uint4*)Bs, lr); }
-      else { lut_col_load(g, j0, r0, lr); lut_col_store((uint4*)Bs, lr); }
+      else {
+        LutRegs t;
+        if (KB == OP_LUT_ROW) { lut_row_load(g, j0, r0, t); lut_row_store((uint4*)Bs, t); }
+        else { lut_col_load(g, j0, r0, t); lut_col_store((uint4*)Bs, t); }
+      }
     } else {
       copy_row_tile_masked((uint4*)As, g.a2, g.R2, i0, g.I, 0, g.R2);
       if (B_COL) copy_col_tile_masked((uint4*)Bs, g.b2, g.J, j0, g.J, 0, g.R2);
       else copy_row_tile_masked((uint4*)Bs, g.b2, g.R2, j0, g.J, 0, g.R2);
     }
   };
-  auto finish = [&](int s, int kt) {
-    uint4* Bs = (uint4*)(lbase + s * 2 * TILE_BYTES + TILE_BYTES);
-    if (kt < nfull) {
-      if (KB == OP_LUT_ROW) lut_row_store(Bs, lr);
-      if (KB == OP_LUT_COL) lut_col_store(Bs, lr);
-    }
-  };
-
+  constexpr bool LUT = KB == OP_LUT_ROW || KB == OP_LUT_COL;
   if (nst > 0) {
     issue(0, 0);
-    finish(0, 0);
+    if (LUT && nfull > 0) {
+      lut_load(0, lr_cur);
+      if (nfull > 1) lut_load(1, lr_next);
+      uint4* Bs = (uint4*)(lbase + TILE_BYTES);
+      if (KB == OP_LUT_ROW) lut_row_store(Bs, lr_cur);
+      if (KB == OP_LUT_COL) lut_col_store(Bs, lr_cur);
+    }
   }
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   for (int kt = 0; kt < nst; ++kt) {
     const int cur = kt & 1;
     const bool more = kt + 1 < nst;
-    if (more) issue(cur ^ 1, kt + 1);
+    if (LUT) {
+      lr_cur = lr_next;  // stage kt+1's words, loaded a stage ago
+      if (kt + 2 < nfull) lut_load(kt + 2, lr_next);
+    }
     const lds_u8* As = lbase + cur * 2 * TILE_BYTES;
+    // copies of stage kt+1 are issued inside the first k-step (interleaved with its MFMAs);
+    // in the last stage they reload stage nfull-1 (a valid stage) into the idle buffer, which
+    // keeps the instruction stream identical (the stage-end wait covers them before the
+    // epilogue)
+    const int kn = more ? kt + 1 : kt;
+    if (more && kt + 1 >= nfull) issue(cur ^ 1, kt + 1);  // partial / LoRA stage: register copies
     // the next stage's palette dequantisation runs between this stage's MFMA groups
     uint4* Bn = (uint4*)(lbase + (cur ^ 1) * 2 * TILE_BYTES + TILE_BYTES);
-    const bool lut_next = more && kt + 1 < nfull && (KB == OP_LUT_ROW || KB == OP_LUT_COL);
-    mma_stage<A_COL, B_COL, KB == OP_LUT_ROW || KB == OP_LUT_COL>(
-        As, As + TILE_BYTES, acc, wi, wj, lane, [&](int part) {
-      if (!lut_next) return;
-      if (KB == OP_LUT_ROW) lut_row_store_part(Bn, lr, part);
-      if (KB == OP_LUT_COL) lut_col_store_part(Bn, lr, part);
+    const bool lut_next = more && kt + 1 < nfull;
+    mma_stage<A_COL, B_COL, LUT>(As, As + TILE_BYTES, acc, wi, wj, lane, [&]() {
+      // with nfull == 0 (a reduction shorter than one stage) there is no full stage to
+      // reload: stage -1 would read before the start of the operands
+      if (kn < nfull || (!more && nfull > 0)) issue_full(cur ^ 1, kn < nfull ? kn : nfull - 1);
+    }, [&](int part) {
+      if (!LUT || !lut_next) return;
+      if (KB == OP_LUT_ROW) lut_row_store_part(Bn, lr_cur, part);
+      if (KB == OP_LUT_COL) lut_col_store_part(Bn, lr_cur, part);
     });
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
