@@ -1,8 +1,9 @@
 // Large-tile MFMA GEMM core for gfx950 (the M = 16384 training shapes).
 //
-// C[I,J] = sum_r A(i,r) B(j,r), bf16 operands, fp32 accumulation, 256 threads = 4 wave64s
-// in a 2x2 grid, workgroup tile 256x256, 128x128 per wave (4x4 blocks of
-// v_mfma_f32_32x32x16_bf16, 256 accumulator registers), reduction stages of BK = 64,
+// C[I,J] = sum_r A(i,r) B(j,r), bf16 operands, fp32 accumulation, 512 threads = 8 wave64s
+// in a 2x4 grid (two per SIMD, so that one wave's LDS and memory waits are covered by the
+// other's MFMAs), workgroup tile 256x256, 128x64 per wave (4x2 blocks of
+// v_mfma_f32_32x32x16_bf16, 128 accumulator registers), reduction stages of BK = 64,
 // double-buffered in LDS (2 x 64 KB).
 //
 // Each operand tile sits in LDS in one of two layouts:
@@ -29,6 +30,11 @@ namespace g2 {
 constexpr int BK = 64;
 constexpr int TILE = 256;            // BI = BJ
 constexpr int TILE_BYTES = TILE * BK * 2;  // 32 KB per operand per stage
+constexpr int NTHR = 512;            // 8 waves
+constexpr int WAVES_I = 2, WAVES_J = 4;
+constexpr int WT_I = TILE / WAVES_I / 32;  // 32x32 MFMA blocks per wave along i (4)
+constexpr int WT_J = TILE / WAVES_J / 32;  // ... along j (2)
+constexpr int COPY_INSTS = TILE * BK / 8 / NTHR;  // 16-byte copies per thread per operand (4)
 
 typedef short v4i16 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
@@ -59,112 +65,95 @@ struct Args {
 };
 
 // ---- dense operand copy, global -> LDS ---------------------------------------------------
-// Row tile from p[row*ld + r] (r contiguous): 2048 chunks, 8 instructions of 256 lanes.
+// Row tile from p[row*ld + r] (r contiguous): 2048 chunks, COPY_INSTS instructions per lane.
 __device__ __forceinline__ void copy_row_tile(lds_u8* lds, const uint16_t* p, int64_t ld,
                                               int64_t row0, int64_t nrows, int64_t r0) {
 #pragma unroll
-  for (int it = 0; it < 8; ++it) {
-    const int pch = it * 256 + threadIdx.x;          // physical chunk written by this lane
+  for (int it = 0; it < COPY_INSTS; ++it) {
+    const int pch = it * NTHR + threadIdx.x;         // physical chunk written by this lane
     const int row = pch >> 3, c = (pch & 7) ^ row_swz(row);
     int64_t gr = row0 + row;
     gr = gr < nrows ? gr : nrows - 1;                 // rows past the end: any valid row
     const uint16_t* src = p + gr * ld + r0 + c * 8;
-    __builtin_amdgcn_global_load_lds(src, lds + it * 4096 + (threadIdx.x & ~63) * 16, 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(src, lds + it * NTHR * 16 + (threadIdx.x & ~63) * 16, 16, 0, 0);
   }
 }
 // Col tile from p[r*ld + row] (rows contiguous): 64 reduction rows x 32 chunks.
 __device__ __forceinline__ void copy_col_tile(lds_u8* lds, const uint16_t* p, int64_t ld,
                                               int64_t row0, int64_t nrows, int64_t r0) {
 #pragma unroll
-  for (int it = 0; it < 8; ++it) {
-    const int pch = it * 256 + threadIdx.x;
+  for (int it = 0; it < COPY_INSTS; ++it) {
+    const int pch = it * NTHR + threadIdx.x;
     const int kr = pch >> 5, c = (pch & 31) ^ col_swz(kr);
     int64_t gr = row0 + c * 8;
     gr = gr < nrows ? gr : 0;                          // chunks past the end: any valid chunk
     const uint16_t* src = p + (r0 + kr) * ld + gr;
-    __builtin_amdgcn_global_load_lds(src, lds + it * 4096 + (threadIdx.x & ~63) * 16, 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(src, lds + it * NTHR * 16 + (threadIdx.x & ~63) * 16, 16, 0, 0);
   }
 }
 
-// ---- palettized operand: one thread per (row n, 64 k) -------------------------------------
+// ---- palettized operand: one thread per (row n, 32 k) -------------------------------------
 struct LutRegs {
-  uint4 q;
-  float4 p;
+  uint2 q;   // two packed words = 32 indices
+  float4 p;  // the palette of their group
 };
-// Forward: tile rows are n (256 rows x 64 k); thread t owns row lut_row_of(t), a permutation
-// within groups of 8 under which the 4 lanes of each store group write rows with distinct
-// (row >> 1) & 3, i.e. distinct 16-byte columns of a 64-byte window (no bank conflicts).
+// Forward: tile rows are n (256 rows x 64 k); thread t owns row lut_row_of(t % 256), half
+// t / 256 of the 64 k. The row permutation within groups of 8 makes the 4 lanes of each
+// store group write rows with distinct (row >> 1) & 3, i.e. distinct 16-byte columns of a
+// 64-byte window (no bank conflicts).
 __device__ __forceinline__ int lut_row_of(int t) {
   return (t & ~7) | ((t & 3) << 1) | ((t >> 2) & 1);
 }
 __device__ __forceinline__ void lut_row_load(const Args& g, int64_t n0, int64_t k0, LutRegs& r) {
-  const int64_t n = n0 + lut_row_of(threadIdx.x);
-  r.q = make_uint4(0, 0, 0, 0);
+  const int64_t n = n0 + lut_row_of(threadIdx.x & 255);
+  const int h = threadIdx.x >> 8;
+  r.q = make_uint2(0, 0);
   r.p = make_float4(0.f, 0.f, 0.f, 0.f);
   if (n < g.Nw) {
-    r.q = *reinterpret_cast<const uint4*>(g.packed + n * (g.Kw / 16) + k0 / 16);
+    r.q = *reinterpret_cast<const uint2*>(g.packed + n * (g.Kw / 16) + k0 / 16 + 2 * h);
     r.p = *reinterpret_cast<const float4*>(g.pal + (n * (g.Kw / 256) + k0 / 256) * 4);
   }
 }
-__device__ __forceinline__ void lut_row_store(uint4* lds, const LutRegs& r) {
-  const PalLut t = make_lut(r.p.x, r.p.y, r.p.z, r.p.w);
-  const int row = lut_row_of(threadIdx.x);
-  const uint32_t qs[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
-#pragma unroll
-  for (int w = 0; w < 4; ++w) {
-    uint32_t o[8];
-    dequant16(qs[w], t, o);
-    lds[row_chunk(row, 2 * w)] = make_uint4(o[0], o[1], o[2], o[3]);
-    lds[row_chunk(row, 2 * w + 1)] = make_uint4(o[4], o[5], o[6], o[7]);
-  }
-}
-// The same store in four parts (part = word of the 64 k), for interleaving with MFMAs.
+// part = word of the thread's 32 k: two 16-byte chunks
 __device__ __forceinline__ void lut_row_store_part(uint4* lds, const LutRegs& r, int part) {
   const PalLut t = make_lut(r.p.x, r.p.y, r.p.z, r.p.w);
-  const int row = lut_row_of(threadIdx.x);
-  const uint32_t q = part == 0 ? r.q.x : part == 1 ? r.q.y : part == 2 ? r.q.z : r.q.w;
+  const int row = lut_row_of(threadIdx.x & 255), cb = 4 * (threadIdx.x >> 8);
   uint32_t o[8];
-  dequant16(q, t, o);
-  lds[row_chunk(row, 2 * part)] = make_uint4(o[0], o[1], o[2], o[3]);
-  lds[row_chunk(row, 2 * part + 1)] = make_uint4(o[4], o[5], o[6], o[7]);
+  dequant16(part == 0 ? r.q.x : r.q.y, t, o);
+  lds[row_chunk(row, cb + 2 * part)] = make_uint4(o[0], o[1], o[2], o[3]);
+  lds[row_chunk(row, cb + 2 * part + 1)] = make_uint4(o[4], o[5], o[6], o[7]);
 }
-// grad_x: tile rows are k (256), reduction n (64). Thread t = 64*w + l owns
-// n = n0 + 16*w + l%16 and k = k0 + 64*(l/16) .. +64, so that the 16-byte LDS stores of a
-// wave cover 16 reduction rows x 4 quarters and, with the (r & 15) chunk swizzle, never
-// collide in a bank. The tile's k range lies in one palette group (k0 % 256 == 0).
-__device__ __forceinline__ int lut_col_kr() { return (threadIdx.x & 15) + 16 * (threadIdx.x >> 6); }
-__device__ __forceinline__ int lut_col_quarter() { return (threadIdx.x >> 4) & 3; }
+__device__ __forceinline__ void lut_row_store(uint4* lds, const LutRegs& r) {
+  lut_row_store_part(lds, r, 0);
+  lut_row_store_part(lds, r, 1);
+}
+// grad_x: tile rows are k (256), reduction n (64). Thread t owns n = n0 + t%64 and
+// k = k0 + 32*(t/64) .. +32: 4 consecutive lanes store 4 consecutive reduction rows, whose
+// col_swz low bits differ (no bank conflicts). The tile's k range lies in one palette group
+// (k0 % 256 == 0).
+__device__ __forceinline__ int lut_col_kr() { return threadIdx.x & 63; }
+__device__ __forceinline__ int lut_col_seg() { return threadIdx.x >> 6; }
 __device__ __forceinline__ void lut_col_load(const Args& g, int64_t k0, int64_t n0, LutRegs& r) {
   const int64_t n = n0 + lut_col_kr();
-  const int64_t k = k0 + 64 * lut_col_quarter();
-  r.q = make_uint4(0, 0, 0, 0);
+  const int64_t k = k0 + 32 * lut_col_seg();
+  r.q = make_uint2(0, 0);
   r.p = make_float4(0.f, 0.f, 0.f, 0.f);
   if (n < g.Nw && k < g.Kw) {
-    r.q = *reinterpret_cast<const uint4*>(g.packed + n * (g.Kw / 16) + k / 16);
+    r.q = *reinterpret_cast<const uint2*>(g.packed + n * (g.Kw / 16) + k / 16);
     r.p = *reinterpret_cast<const float4*>(g.pal + (n * (g.Kw / 256) + k / 256) * 4);
   }
 }
-__device__ __forceinline__ void lut_col_store(uint4* lds, const LutRegs& r) {
-  const PalLut t = make_lut(r.p.x, r.p.y, r.p.z, r.p.w);
-  const int kr = lut_col_kr(), cb = 8 * lut_col_quarter();
-  const uint32_t qs[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
-#pragma unroll
-  for (int w = 0; w < 4; ++w) {
-    uint32_t o[8];
-    dequant16(qs[w], t, o);
-    lds[col_chunk(kr, cb + 2 * w)] = make_uint4(o[0], o[1], o[2], o[3]);
-    lds[col_chunk(kr, cb + 2 * w + 1)] = make_uint4(o[4], o[5], o[6], o[7]);
-  }
-}
-
 __device__ __forceinline__ void lut_col_store_part(uint4* lds, const LutRegs& r, int part) {
   const PalLut t = make_lut(r.p.x, r.p.y, r.p.z, r.p.w);
-  const int kr = lut_col_kr(), cb = 8 * lut_col_quarter();
-  const uint32_t q = part == 0 ? r.q.x : part == 1 ? r.q.y : part == 2 ? r.q.z : r.q.w;
+  const int kr = lut_col_kr(), cb = 4 * lut_col_seg();
   uint32_t o[8];
-  dequant16(q, t, o);
+  dequant16(part == 0 ? r.q.x : r.q.y, t, o);
   lds[col_chunk(kr, cb + 2 * part)] = make_uint4(o[0], o[1], o[2], o[3]);
   lds[col_chunk(kr, cb + 2 * part + 1)] = make_uint4(o[4], o[5], o[6], o[7]);
+}
+__device__ __forceinline__ void lut_col_store(uint4* lds, const LutRegs& r) {
+  lut_col_store_part(lds, r, 0);
+  lut_col_store_part(lds, r, 1);
 }
 
 // ---- fragments (v_mfma_f32_32x32x16_bf16: lane l holds row l%32, k-slots 8*(l/32)..+7) --

@@ -24,8 +24,8 @@ __device__ __forceinline__ void copy_row_tile_masked(uint4* lds, const uint16_t*
                                                      int64_t row0, int64_t nrows, int64_t r0,
                                                      int64_t rend) {
 #pragma unroll
-  for (int it = 0; it < 8; ++it) {
-    const int ch = it * 256 + threadIdx.x;
+  for (int it = 0; it < COPY_INSTS; ++it) {
+    const int ch = it * NTHR + threadIdx.x;
     const int row = ch >> 3, c = ch & 7;
     const int64_t gr = row0 + row, gk = r0 + 8 * c;
     uint4 v = make_uint4(0, 0, 0, 0);
@@ -37,8 +37,8 @@ __device__ __forceinline__ void copy_col_tile_masked(uint4* lds, const uint16_t*
                                                      int64_t row0, int64_t nrows, int64_t r0,
                                                      int64_t rend) {
 #pragma unroll
-  for (int it = 0; it < 8; ++it) {
-    const int ch = it * 256 + threadIdx.x;
+  for (int it = 0; it < COPY_INSTS; ++it) {
+    const int ch = it * NTHR + threadIdx.x;
     const int kr = ch >> 5, c = ch & 31;
     const int64_t gr = row0 + 8 * c, gk = r0 + kr;
     uint4 v = make_uint4(0, 0, 0, 0);
@@ -55,97 +55,87 @@ __device__ __forceinline__ int ptile(int row, int col) {  // 128 x 256 fp32 stag
 // Fragments are double-buffered in registers: the LDS reads of k-step ks+1 are issued before
 // the 16 MFMAs of k-step ks, so one wave per SIMD keeps the matrix core busy. The scheduling
 // barriers pin that order (left alone, the compiler sinks each A read next to its first
-// MFMA and exposes the LDS latency every 4 MFMAs). fill(part), part = 0..3, runs between
+// MFMA and exposes the LDS latency every 4 MFMAs). fill(part), part = 0..1, runs between
 // the MFMA groups: VALU work for the next stage (the palette dequantisation) that then
 // overlaps with the matrix core.
 template <bool A_COL, bool B_COL>
 __device__ __forceinline__ void load_frags(const lds_u8* a_s, const lds_u8* b_s, int ks, int wi,
-                                           int wj, int lane, bf16x8 (&a)[4], bf16x8 (&b)[4]) {
+                                           int wj, int lane, bf16x8 (&a)[WT_I], bf16x8 (&b)[WT_J]) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-    a[i] = A_COL ? frag_col(a_s, wi * 128 + 32 * i, ks, lane)
-                 : frag_row((const uint4*)a_s, wi * 128 + 32 * i, ks, lane);
+  for (int i = 0; i < WT_I; ++i)
+    a[i] = A_COL ? frag_col(a_s, wi * (32 * WT_I) + 32 * i, ks, lane)
+                 : frag_row((const uint4*)a_s, wi * (32 * WT_I) + 32 * i, ks, lane);
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
-    b[j] = B_COL ? frag_col(b_s, wj * 128 + 32 * j, ks, lane)
-                 : frag_row((const uint4*)b_s, wj * 128 + 32 * j, ks, lane);
+  for (int j = 0; j < WT_J; ++j)
+    b[j] = B_COL ? frag_col(b_s, wj * (32 * WT_J) + 32 * j, ks, lane)
+                 : frag_row((const uint4*)b_s, wj * (32 * WT_J) + 32 * j, ks, lane);
 }
-__device__ __forceinline__ void mma16(f32x16 (&acc)[4][4], const bf16x8 (&a)[4], const bf16x8 (&b)[4]) {
+constexpr int MFMA_PER_KSTEP = WT_I * WT_J;  // 8
+__device__ __forceinline__ void mma_kstep(f32x16 (&acc)[WT_I][WT_J], const bf16x8 (&a)[WT_I],
+                                          const bf16x8 (&b)[WT_J]) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < WT_I; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < WT_J; ++j)
       acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
 }
-// Instruction interleave of one k-step: the LDS reads of the next k-step go one after each
-// of the first MFMAs, the VALU of fill() between the remaining ones, so that neither the
-// LDS queue nor the VALU stalls the issue of MFMAs (sched_group_barrier masks: 0x008 MFMA,
-// 0x100 LDS read, 0x200 LDS write, 0x002 VALU).
-template <int NREAD, int NVALU_PER_MFMA, int NWRITE>
+// Instruction interleave of one k-step (MFMA_PER_KSTEP MFMAs): the LDS reads of the next
+// k-step, the next stage's global->LDS copies (first k-step only) and the palette
+// dequantisation (VALU and LDS stores) are spread between the MFMAs, so that no burst of one
+// kind stalls the issue of MFMAs (sched_group_barrier masks: 0x008 MFMA, 0x100 LDS read,
+// 0x200 LDS write, 0x020 VMEM, 0x002 VALU).
+template <int NREAD, int NVMEM, int NVALU, int NWRITE>
 __device__ __forceinline__ void interleave_kstep() {
+  constexpr int M = MFMA_PER_KSTEP;
+  constexpr int R = (NREAD + M - 1) / M, V = (NVMEM + M - 1) / M;
+  constexpr int A = (NVALU + M - 1) / M, W = (NWRITE + M - 1) / M;
 #pragma unroll
-  for (int i = 0; i < NREAD; ++i) {
+  for (int i = 0; i < M; ++i) {
     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-  }
-#pragma unroll
-  for (int i = NREAD; i < 16; ++i) {
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-    if (NVALU_PER_MFMA > 0) __builtin_amdgcn_sched_group_barrier(0x002, NVALU_PER_MFMA, 0);
-    if (i - NREAD < NWRITE) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+    if (R > 0 && i * R < NREAD) __builtin_amdgcn_sched_group_barrier(0x100, R, 0);
+    if (V > 0 && i * V < NVMEM) __builtin_amdgcn_sched_group_barrier(0x020, V, 0);
+    if (A > 0) __builtin_amdgcn_sched_group_barrier(0x002, A, 0);
+    if (W > 0 && i * W < NWRITE) __builtin_amdgcn_sched_group_barrier(0x200, W, 0);
   }
 }
 
-// The first k-step also spreads the next stage's global->LDS copies (0x020 VMEM), one per MFMA:
-// issued as a burst at the stage start they stalled the wave behind the memory pipeline.
-template <int NREAD, int NVALU_PER_MFMA, int NWRITE, int NVMEM>
-__device__ __forceinline__ void interleave_kstep_vmem() {
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-    if (i < NREAD) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-    if (i < NVMEM) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-    if (i >= NREAD && NVALU_PER_MFMA > 0) __builtin_amdgcn_sched_group_barrier(0x002, NVALU_PER_MFMA, 0);
-    if (i >= NREAD && i - NREAD < NWRITE) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
-  }
-}
 template <bool A_COL, bool B_COL, bool FILL, typename Dma, typename Fill>
-__device__ __forceinline__ void mma_stage(const lds_u8* a_s, const lds_u8* b_s, f32x16 (&acc)[4][4],
-                                          int wi, int wj, int lane, Dma&& dma, Fill&& fill) {
+__device__ __forceinline__ void mma_stage(const lds_u8* a_s, const lds_u8* b_s,
+                                          f32x16 (&acc)[WT_I][WT_J], int wi, int wj, int lane,
+                                          Dma&& dma, Fill&& fill) {
   // LDS read instructions per k-step: a row fragment is one ds_read_b128, a col fragment two
   // ds_read_b64_tr_b16
-  constexpr int NREAD = 4 * (A_COL ? 2 : 1) + 4 * (B_COL ? 2 : 1);
-  constexpr int NV = FILL ? 4 : 0;
+  constexpr int NREAD = WT_I * (A_COL ? 2 : 1) + WT_J * (B_COL ? 2 : 1);
+  // palette dequantisation of one word: ~31 VALU and two 16-byte LDS stores (k-steps 0, 1)
+  constexpr int NV = FILL ? 32 : 0;
   constexpr int NW = FILL ? 2 : 0;
-  // global->LDS copies of the next stage issued by dma(): 8 per dense operand
-  constexpr int NDMA = FILL ? 8 : 16;
-  bf16x8 a0[4], b0[4], a1[4], b1[4];
+  // global->LDS copies of the next stage issued by dma(): COPY_INSTS per dense operand
+  constexpr int NDMA = COPY_INSTS * (FILL ? 1 : 2);
+  bf16x8 a0[WT_I], b0[WT_J], a1[WT_I], b1[WT_J];
   load_frags<A_COL, B_COL>(a_s, b_s, 0, wi, wj, lane, a0, b0);
   __builtin_amdgcn_sched_barrier(0);
   load_frags<A_COL, B_COL>(a_s, b_s, 1, wi, wj, lane, a1, b1);
   dma();
-  mma16(acc, a0, b0);
+  mma_kstep(acc, a0, b0);
   fill(0);
-  interleave_kstep_vmem<NREAD, NV, NW, NDMA>();
+  interleave_kstep<NREAD, NDMA, NV, NW>();
   __builtin_amdgcn_sched_barrier(0);
   load_frags<A_COL, B_COL>(a_s, b_s, 2, wi, wj, lane, a0, b0);
-  mma16(acc, a1, b1);
+  mma_kstep(acc, a1, b1);
   fill(1);
-  interleave_kstep<NREAD, NV, NW>();
+  interleave_kstep<NREAD, 0, NV, NW>();
   __builtin_amdgcn_sched_barrier(0);
   load_frags<A_COL, B_COL>(a_s, b_s, 3, wi, wj, lane, a1, b1);
-  mma16(acc, a0, b0);
-  fill(2);
-  interleave_kstep<NREAD, NV, NW>();
+  mma_kstep(acc, a0, b0);
+  interleave_kstep<NREAD, 0, 0, 0>();
   __builtin_amdgcn_sched_barrier(0);
-  mma16(acc, a1, b1);
-  fill(3);
-  interleave_kstep<0, NV, NW>();
+  mma_kstep(acc, a1, b1);
+  interleave_kstep<0, 0, 0, 0>();
   __builtin_amdgcn_sched_barrier(0);
 }
 
 template <int KA, int KB, int EPI>
-__global__ __launch_bounds__(256) void gemm2_kernel(const Args g) {
+__global__ __launch_bounds__(NTHR) void gemm2_kernel(const Args g) {
   extern __shared__ uint4 smem[];
   lds_u8* lbase = (lds_u8*)smem;
   constexpr bool A_COL = KA == OP_COL;
@@ -167,13 +157,13 @@ __global__ __launch_bounds__(256) void gemm2_kernel(const Args g) {
   const int nfull = (int)(rlen / BK);
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int wi = wave >> 1, wj = wave & 1;
+  const int wi = wave / WAVES_J, wj = wave % WAVES_J;
 
-  f32x16 acc[4][4];
+  f32x16 acc[WT_I][WT_J];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < WT_I; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < WT_J; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
@@ -274,35 +264,36 @@ __global__ __launch_bounds__(256) void gemm2_kernel(const Args g) {
   }
 
   // ---- epilogues ----------------------------------------------------------------------
-  // acc[ti][tj][e]: row wi*128 + 32*ti + 8*(e/4) + 4*(lane/32) + e%4, col wj*128 + 32*tj + lane%32
+  // acc[ti][tj][e]: row wi*128 + 32*ti + 8*(e/4) + 4*(lane/32) + e%4,
+  //                 col wj*64 + 32*tj + lane%32
   if (EPI == EPI_BF16) {
     // Stage the bf16 tile in LDS (rows padded to 528 B so the two 64-byte row segments a
     // wave writes per instruction fall in different banks), then write it out with 16-byte
-    // coalesced stores: 32 per thread instead of 256 scattered 2-byte stores.
+    // coalesced stores: 16 per thread instead of 128 scattered 2-byte stores.
     constexpr int RS = 528;  // staging row stride in bytes
     lds_u8* st = lbase;
-    float bj[4];
+    float bj[WT_J];
 #pragma unroll
-    for (int tj = 0; tj < 4; ++tj) {
-      const int64_t j = j0 + wj * 128 + 32 * tj + (lane & 31);
+    for (int tj = 0; tj < WT_J; ++tj) {
+      const int64_t j = j0 + wj * (32 * WT_J) + 32 * tj + (lane & 31);
       bj[tj] = (g.bias && j < g.J) ? bf2f(g.bias[j]) : 0.f;
     }
 #pragma unroll
-    for (int ti = 0; ti < 4; ++ti)
+    for (int ti = 0; ti < WT_I; ++ti)
 #pragma unroll
-      for (int tj = 0; tj < 4; ++tj)
+      for (int tj = 0; tj < WT_J; ++tj)
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
-          const int row = wi * 128 + 32 * ti + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-          const int col = wj * 128 + 32 * tj + (lane & 31);
+          const int row = wi * (32 * WT_I) + 32 * ti + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+          const int col = wj * (32 * WT_J) + 32 * tj + (lane & 31);
           *reinterpret_cast<__attribute__((address_space(3))) uint16_t*>(st + row * RS + col * 2) =
               (uint16_t)f2bf(g.alpha * acc[ti][tj][e] + bj[tj]);
         }
     __syncthreads();
     uint16_t* C = reinterpret_cast<uint16_t*>(g.c);
 #pragma unroll 4
-    for (int it = 0; it < 32; ++it) {
-      const int ch = it * 256 + threadIdx.x;  // 32 chunks of 8 columns per row
+    for (int it = 0; it < TILE * TILE / 8 / NTHR; ++it) {
+      const int ch = it * NTHR + threadIdx.x;  // 32 chunks of 8 columns per row
       const int row = ch >> 5, c8 = (ch & 31) * 8;
       const int64_t i = i0 + row, j = j0 + c8;
       if (i < g.I && j < g.J) {
@@ -324,18 +315,18 @@ __global__ __launch_bounds__(256) void gemm2_kernel(const Args g) {
     for (int tt = 0; tt < 2; ++tt) {
       const int ti = 2 * half + tt;
 #pragma unroll
-      for (int tj = 0; tj < 4; ++tj)
+      for (int tj = 0; tj < WT_J; ++tj)
 #pragma unroll
         for (int e = 0; e < 16; ++e)
           sC[ptile(wi * 64 + 32 * tt + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3),
-                   wj * 128 + 32 * tj + (lane & 31))] = acc[ti][tj][e];
+                   wj * (32 * WT_J) + 32 * tj + (lane & 31))] = acc[ti][tj][e];
     }
     __syncthreads();
-    if (EPI == EPI_PAL) {
-      const int row = threadIdx.x >> 1, h = threadIdx.x & 1;
+    if (EPI == EPI_PAL) {  // threads 0..255: one (row, 128-k segment) each
+      const int row = (threadIdx.x >> 1) & 127, h = threadIdx.x & 1;
       const int64_t n = i0 + (row >> 6) * 128 + 64 * half + (row & 63);
       const int64_t kseg = j0 + 128 * h;
-      if (n < g.I && kseg < g.J) {
+      if (threadIdx.x < 256 && n < g.I && kseg < g.J) {
         const uint4* qp = reinterpret_cast<const uint4*>(g.packed + n * (g.Kw / 16) + kseg / 16);
         float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
 #pragma unroll
@@ -364,7 +355,7 @@ __global__ __launch_bounds__(256) void gemm2_kernel(const Args g) {
         *reinterpret_cast<float4*>(dst) = make_float4(s0, s1, s2, s3);
       }
     } else {  // EPI_SOFT: each wave walks (row, 128-k segment) items; lane = 2 consecutive k
-      for (int item = wave; item < 256; item += 4) {
+      for (int item = wave; item < 256; item += NTHR / 64) {
         const int row = item >> 1, h = item & 1;
         const int64_t n = i0 + (row >> 6) * 128 + 64 * half + (row & 63);
         const int64_t k = j0 + 128 * h + 2 * lane;
@@ -450,7 +441,7 @@ static int launch(Args g, int splits, hipStream_t stream, const char* what) {
   }
   const int64_t tiles = (int64_t)g.tiles_i * g.tiles_j;
   if (tiles == 0 || splits == 0) return PLZ_OK;
-  hipLaunchKernelGGL(kern, dim3((unsigned)tiles, 1, (unsigned)splits), dim3(256), kLds, stream, g);
+  hipLaunchKernelGGL(kern, dim3((unsigned)tiles, 1, (unsigned)splits), dim3(NTHR), kLds, stream, g);
   return check_launch(what);
 }
 
