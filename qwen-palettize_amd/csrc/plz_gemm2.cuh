@@ -156,6 +156,21 @@ __device__ __forceinline__ void lut_col_store(uint4* lds, const LutRegs& r) {
   lut_col_store_part(lds, r, 1);
 }
 
+// Forward, register-dequant variant: the stage's palettized operand travels raw, 256 rows x
+// (4 packed words = 64 k | the row's palette), one 16-byte global->LDS copy per thread
+// (threads 0..255 the words of row t, threads 256..511 the palette of row t-256). Each wave
+// then dequantises its own B fragments in registers: no dequantised tile is written to or
+// read from LDS (16-byte LDS writes cost ~2.7x the reads per byte on gfx950).
+constexpr int LUT_RAW_PAL = 256 * 16;  // byte offset of the palettes in the raw slot
+__device__ __forceinline__ void copy_lut_raw(lds_u8* lds, const Args& g, int64_t n0, int64_t k0) {
+  const int t = threadIdx.x, r = t & 255;
+  int64_t n = n0 + r;
+  n = n < g.Nw ? n : g.Nw - 1;  // rows past the end: any valid row (never stored)
+  const void* src = t < 256 ? (const void*)(g.packed + n * (g.Kw / 16) + k0 / 16)
+                            : (const void*)(g.pal + (n * (g.Kw / 256) + k0 / 256) * 4);
+  __builtin_amdgcn_global_load_lds(src, lds + (t & ~63) * 16, 16, 0, 0);
+}
+
 // ---- fragments (v_mfma_f32_32x32x16_bf16: lane l holds row l%32, k-slots 8*(l/32)..+7) --
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
@@ -165,6 +180,10 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 __device__ __forceinline__ bf16x8 frag_row(const uint4* lds, int rowbase, int ks, int lane) {
   const int ch = row_chunk(rowbase + (lane & 31), 2 * ks + (lane >> 5));
   return __builtin_bit_cast(bf16x8, lds[ch]);
+}
+// Row tile fragment of an explicit chunk per lane (8 consecutive r of row rowbase + lane%32).
+__device__ __forceinline__ bf16x8 frag_row_chunk(const uint4* lds, int rowbase, int chunk, int lane) {
+  return __builtin_bit_cast(bf16x8, lds[row_chunk(rowbase + (lane & 31), chunk)]);
 }
 // Col tile: per 16-lane group j = lane/16 the rows 16*(j&1)..+15 at k-group j>>1.
 __device__ __forceinline__ bf16x8 frag_col(const lds_u8* lds, int rowbase, int ks, int lane) {

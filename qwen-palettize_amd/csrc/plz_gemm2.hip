@@ -15,7 +15,7 @@
 namespace plz {
 namespace g2 {
 
-enum { OP_ROW = 0, OP_COL = 1, OP_LUT_ROW = 2, OP_LUT_COL = 3 };
+enum { OP_ROW = 0, OP_COL = 1, OP_LUT_ROW = 2, OP_LUT_COL = 3, OP_LUT_REG = 4 };
 enum { EPI_BF16 = 0, EPI_PAL = 1, EPI_SOFT = 2 };
 
 // Masked register-path copies for a partial reduction stage (r >= rend reads as zero) and for
@@ -99,6 +99,19 @@ __device__ __forceinline__ void interleave_kstep() {
   }
 }
 
+// A whole stage without overlap (the partial and LoRA stages).
+template <bool A_COL, bool B_COL>
+__device__ __forceinline__ void mma_stage_sync(const lds_u8* a_s, const lds_u8* b_s,
+                                               f32x16 (&acc)[WT_I][WT_J], int wi, int wj,
+                                               int lane) {
+#pragma unroll
+  for (int ks = 0; ks < BK / 16; ++ks) {
+    bf16x8 a[WT_I], b[WT_J];
+    load_frags<A_COL, B_COL>(a_s, b_s, ks, wi, wj, lane, a, b);
+    mma_kstep(acc, a, b);
+  }
+}
+
 template <bool A_COL, bool B_COL, bool FILL, typename Dma, typename Fill>
 __device__ __forceinline__ void mma_stage(const lds_u8* a_s, const lds_u8* b_s,
                                           f32x16 (&acc)[WT_I][WT_J], int wi, int wj, int lane,
@@ -130,6 +143,76 @@ __device__ __forceinline__ void mma_stage(const lds_u8* a_s, const lds_u8* b_s,
   interleave_kstep<NREAD, 0, 0, 0>();
   __builtin_amdgcn_sched_barrier(0);
   mma_kstep(acc, a1, b1);
+  interleave_kstep<0, 0, 0, 0>();
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// One stage of the forward with the palettized operand dequantised in registers (B slot
+// holds the raw words and palettes, copy_lut_raw). MFMA k-slots are assigned so that no
+// dequantised weight is wasted: for the k-step pair p (32 k = two packed words per row),
+// lanes 0..31 feed word 2p and lanes 32..63 word 2p+1 -- the first MFMA of the pair takes
+// weights 0..7 of each lane's word, the second weights 8..15. The A fragments read the
+// matching 16-byte chunks (chunk 4p + 2*(lane/32) + s), so the products are unchanged.
+template <typename Dma>
+__device__ __forceinline__ void mma_stage_lutreg(const lds_u8* a_s, const lds_u8* b_s,
+                                                 f32x16 (&acc)[WT_I][WT_J], int wi, int wj,
+                                                 int lane, Dma&& dma) {
+  typedef __attribute__((address_space(3))) const u32x4 lds_u32x4;
+  typedef __attribute__((address_space(3))) const f32x4 lds_f32x4;
+  const int h = lane >> 5, nn = lane & 31;
+  u32x4 qv[WT_J];
+  PalLut t[WT_J];
+#pragma unroll
+  for (int j = 0; j < WT_J; ++j) {
+    const int row = wj * (32 * WT_J) + 32 * j + nn;
+    qv[j] = *reinterpret_cast<lds_u32x4*>(b_s + 16 * row);
+    const f32x4 p = *reinterpret_cast<lds_f32x4*>(b_s + LUT_RAW_PAL + 16 * row);
+    t[j] = make_lut(p[0], p[1], p[2], p[3]);
+  }
+  auto afrags = [&](int p, int s2, bf16x8 (&a)[WT_I]) {
+#pragma unroll
+    for (int i = 0; i < WT_I; ++i)
+      a[i] = frag_row_chunk((const uint4*)a_s, wi * (32 * WT_I) + 32 * i, 4 * p + 2 * h + s2, lane);
+  };
+  auto dequant_pair = [&](int p, uint32_t (&w)[WT_J][8]) {
+#pragma unroll
+    for (int j = 0; j < WT_J; ++j) {
+      const uint32_t q = p == 0 ? (h ? qv[j][1] : qv[j][0]) : (h ? qv[j][3] : qv[j][2]);
+      dequant16(q, t[j], w[j]);
+    }
+  };
+  auto mma = [&](const bf16x8 (&a)[WT_I], const uint32_t (&w)[WT_J][8], int s2) {
+#pragma unroll
+    for (int i = 0; i < WT_I; ++i)
+#pragma unroll
+      for (int j = 0; j < WT_J; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+            a[i], __builtin_bit_cast(bf16x8, u32x4{w[j][4 * s2], w[j][4 * s2 + 1],
+                                                   w[j][4 * s2 + 2], w[j][4 * s2 + 3]}),
+            acc[i][j], 0, 0, 0);
+  };
+  constexpr int NREAD = WT_I;
+  constexpr int NDMA = COPY_INSTS + 1;
+  bf16x8 a0[WT_I], a1[WT_I];
+  uint32_t w0[WT_J][8], w1[WT_J][8];
+  afrags(0, 0, a0);
+  dequant_pair(0, w0);
+  __builtin_amdgcn_sched_barrier(0);
+  afrags(0, 1, a1);
+  dma();
+  mma(a0, w0, 0);
+  interleave_kstep<NREAD, NDMA, 0, 0>();
+  __builtin_amdgcn_sched_barrier(0);
+  afrags(1, 0, a0);
+  mma(a1, w0, 1);
+  dequant_pair(1, w1);
+  interleave_kstep<NREAD, 0, 2 * 31, 0>();
+  __builtin_amdgcn_sched_barrier(0);
+  afrags(1, 1, a1);
+  mma(a0, w1, 0);
+  interleave_kstep<NREAD, 0, 0, 0>();
+  __builtin_amdgcn_sched_barrier(0);
+  mma(a1, w1, 1);
   interleave_kstep<0, 0, 0, 0>();
   __builtin_amdgcn_sched_barrier(0);
 }
@@ -193,6 +276,7 @@ __global__ __launch_bounds__(NTHR) void gemm2_kernel(const Args g) {
     else copy_col_tile(As, g.a, g.lda, i0, g.I, r0);
     if (KB == OP_ROW) copy_row_tile(Bs, g.b, g.ldb, j0, g.J, r0);
     else if (KB == OP_COL) copy_col_tile(Bs, g.b, g.ldb, j0, g.J, r0);
+    else if (KB == OP_LUT_REG) copy_lut_raw(Bs, g, j0, r0);
   };
   auto issue = [&](int s, int kt) {
     lds_u8* As = lbase + s * 2 * TILE_BYTES;
@@ -203,6 +287,7 @@ __global__ __launch_bounds__(NTHR) void gemm2_kernel(const Args g) {
       else copy_col_tile(As, g.a, g.lda, i0, g.I, r0);
       if (KB == OP_ROW) copy_row_tile(Bs, g.b, g.ldb, j0, g.J, r0);
       else if (KB == OP_COL) copy_col_tile(Bs, g.b, g.ldb, j0, g.J, r0);
+      else if (KB == OP_LUT_REG) copy_lut_raw(Bs, g, j0, r0);
     } else if (tail && kt == nfull) {
       const int64_t r0 = rbeg + (int64_t)nfull * BK;
       if (KA == OP_ROW) copy_row_tile_masked((uint4*)As, g.a, g.lda, i0, g.I, r0, rend);
@@ -211,7 +296,8 @@ __global__ __launch_bounds__(NTHR) void gemm2_kernel(const Args g) {
       else if (KB == OP_COL) copy_col_tile_masked((uint4*)Bs, g.b, g.ldb, j0, g.J, r0, rend);
       else {
         LutRegs t;
-        if (KB == OP_LUT_ROW) { lut_row_load(g, j0, r0, t); lut_row_store((uint4*)Bs, t); }
+        // (OP_LUT_REG: a partial stage is a dequantised row tile, multiplied by the dense body)
+        if (KB == OP_LUT_ROW || KB == OP_LUT_REG) { lut_row_load(g, j0, r0, t); lut_row_store((uint4*)Bs, t); }
         else { lut_col_load(g, j0, r0, t); lut_col_store((uint4*)Bs, t); }
       }
     } else {
@@ -221,9 +307,11 @@ __global__ __launch_bounds__(NTHR) void gemm2_kernel(const Args g) {
     }
   };
   constexpr bool LUT = KB == OP_LUT_ROW || KB == OP_LUT_COL;
-  if (nst > 0) {
+  // Full stages run through the pipelined loop (one MFMA body per kernel kind); the
+  // partial stage and the LoRA stage follow, synchronously, through buffer 0.
+  if (nfull > 0) {
     issue(0, 0);
-    if (LUT && nfull > 0) {
+    if (LUT) {
       lut_load(0, lr_cur);
       if (nfull > 1) lut_load(1, lr_next);
       uint4* Bs = (uint4*)(lbase + TILE_BYTES);
@@ -233,33 +321,37 @@ __global__ __launch_bounds__(NTHR) void gemm2_kernel(const Args g) {
   }
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  for (int kt = 0; kt < nst; ++kt) {
+  for (int kt = 0; kt < nfull; ++kt) {
     const int cur = kt & 1;
-    const bool more = kt + 1 < nst;
+    const bool more = kt + 1 < nfull;
     if (LUT) {
       lr_cur = lr_next;  // stage kt+1's words, loaded a stage ago
       if (kt + 2 < nfull) lut_load(kt + 2, lr_next);
     }
     const lds_u8* As = lbase + cur * 2 * TILE_BYTES;
     // copies of stage kt+1 are issued inside the first k-step (interleaved with its MFMAs);
-    // in the last stage they reload stage nfull-1 (a valid stage) into the idle buffer, which
-    // keeps the instruction stream identical (the stage-end wait covers them before the
-    // epilogue)
-    const int kn = more ? kt + 1 : kt;
-    if (more && kt + 1 >= nfull) issue(cur ^ 1, kt + 1);  // partial / LoRA stage: register copies
-    // the next stage's palette dequantisation runs between this stage's MFMA groups
-    uint4* Bn = (uint4*)(lbase + (cur ^ 1) * 2 * TILE_BYTES + TILE_BYTES);
-    const bool lut_next = more && kt + 1 < nfull;
-    mma_stage<A_COL, B_COL, LUT>(As, As + TILE_BYTES, acc, wi, wj, lane, [&]() {
-      // with nfull == 0 (a reduction shorter than one stage) there is no full stage to
-      // reload: stage -1 would read before the start of the operands
-      if (kn < nfull || (!more && nfull > 0)) issue_full(cur ^ 1, kn < nfull ? kn : nfull - 1);
-    }, [&](int part) {
-      if (!LUT || !lut_next) return;
-      if (KB == OP_LUT_ROW) lut_row_store_part(Bn, lr_cur, part);
-      if (KB == OP_LUT_COL) lut_col_store_part(Bn, lr_cur, part);
-    });
+    // the last stage reloads itself into the idle buffer, which keeps the instruction stream
+    // identical (the stage-end wait covers the copies before the buffers are reused)
+    auto dma = [&]() { issue_full(cur ^ 1, more ? kt + 1 : kt); };
+    if constexpr (KB == OP_LUT_REG) {
+      mma_stage_lutreg(As, As + TILE_BYTES, acc, wi, wj, lane, dma);
+    } else {
+      // the next stage's palette dequantisation runs between this stage's MFMA groups
+      uint4* Bn = (uint4*)(lbase + (cur ^ 1) * 2 * TILE_BYTES + TILE_BYTES);
+      mma_stage<A_COL, B_COL, LUT>(As, As + TILE_BYTES, acc, wi, wj, lane, dma, [&](int part) {
+        if (!LUT || !more) return;
+        if (KB == OP_LUT_ROW) lut_row_store_part(Bn, lr_cur, part);
+        if (KB == OP_LUT_COL) lut_col_store_part(Bn, lr_cur, part);
+      });
+    }
     __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
+  for (int kt = nfull; kt < nst; ++kt) {
+    issue(0, kt);  // register copies (zero-filled past the end)
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    mma_stage_sync<A_COL, B_COL>(lbase, lbase + TILE_BYTES, acc, wi, wj, lane);
     __syncthreads();
   }
 
@@ -519,7 +611,7 @@ int plz_lut_linear_fwd(const uint16_t* x, const int32_t* packed, const float* pa
   g.a2 = lora_t; g.b2 = lora_b; g.R2 = rank;
   g.c = y; g.ldc = N; g.bias = bias; g.alpha = 1.f;
   g.group = 1;
-  return launch<OP_ROW, OP_LUT_ROW, EPI_BF16>(g, 1, (hipStream_t)stream, "plz_lut_linear_fwd");
+  return launch<OP_ROW, OP_LUT_REG, EPI_BF16>(g, 1, (hipStream_t)stream, "plz_lut_linear_fwd");
 }
 
 int plz_lut_linear_bwd_x(const uint16_t* grad_y, const int32_t* packed, const float* palette,
