@@ -31,6 +31,14 @@ M_TRAIN = 16384
 LAYERS = 36
 PEAK_BF16_TFLOPS = 2500.0
 PEAK_HBM_GBS = 8000.0
+# HBM-side bytes per launch of each GEMM kind, averaged over the 7 shapes: rocprofv3 FETCH_SIZE x 2.0
+# + WRITE_SIZE x 1.0, the factors that make a plain 1 GiB device copy read as 1 GiB each way (two
+# --pmc runs of `bench.py --only hard --steps 1 --warmup 1 --no-cpu --calibration-copy`; counters,
+# commands and algorithmic bytes in profiles/lut_gemm_traffic_m16384.txt).
+GEMM_TRAFFIC_BYTES = {"fwd": 523.7e6, "grad_x": 481.5e6, "grad_palette": 1467.9e6}
+KERNEL_NAMES = {"fwd": "gemm2_kernel<OP_ROW, OP_LUT_REG, EPI_BF16> (fwd)",
+                "grad_x": "gemm2_kernel<OP_ROW, OP_LUT_COL, EPI_BF16> (grad_x)",
+                "grad_palette": "gemm2_kernel<OP_COL, OP_COL, EPI_PAL> (grad_palette)"}
 
 
 def _make_weight(N, K, gen, device):
@@ -257,6 +265,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", choices=["hard", "gemv", "soft", "layer"], default=None)
+    ap.add_argument("--calibration-copy", action="store_true",
+                    help="first run a plain 1 GiB device copy (fp32 -> fp32), the reference "
+                         "kernel that scales rocprofv3's FETCH_SIZE / WRITE_SIZE to bytes")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (the path has no multi-GPU "
@@ -280,6 +291,14 @@ def main():
                                   "of q,k,v,o,gate,up,down at M=16384",
                       "M": M_TRAIN, "global_batch": 32, "seq_len": 512, "parallelism": "none (1 GPU)"}}
 
+    if args.calibration_copy:
+        src = torch.empty(1 << 28, dtype=torch.float32, device=dev).fill_(1.0)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)  # reads 1 GiB, writes 1 GiB
+        torch.cuda.synchronize()
+        del src, dst
+        torch.cuda.empty_cache()
     if args.only in (None, "hard"):
         _log("hard: building inputs")
         step = HardStep(dev)
@@ -299,10 +318,10 @@ def main():
         kr = kernel_rooflines(step.events)
         dom = max(kr, key=lambda k: kr[k]["ms"])
         out.update(value=round(tflops, 2), ms_per_step=round(ms, 3))
-        out["roofline"] = {"bound": "mfma", "kernel": f"gemm_kernel ({dom})",
+        out["roofline"] = {"bound": "mfma", "kernel": KERNEL_NAMES[dom],
                            "achieved": round(kr[dom]["tflops"], 1), "peak": PEAK_BF16_TFLOPS,
                            "unit": "TFLOP/s", "frac": round(kr[dom]["tflops"] / PEAK_BF16_TFLOPS, 4),
-                           "traffic": None}
+                           "traffic": GEMM_TRAFFIC_BYTES[dom], "traffic_unit": "bytes/launch"}
         out["kernels"] = {k: {"tflops": round(v["tflops"], 1),
                               "ms_per_step": round(v["ms"] / args.steps, 3)} for k, v in kr.items()}
         _log(f"hard: {ms:.3f} ms/step, {tflops:.1f} TFLOP/s")

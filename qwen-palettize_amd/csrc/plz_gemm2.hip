@@ -224,9 +224,16 @@ __global__ __launch_bounds__(NTHR) void gemm2_kernel(const Args g) {
   constexpr bool A_COL = KA == OP_COL;
   constexpr bool B_COL = KB == OP_COL || KB == OP_LUT_COL;
 
-  int bid = blockIdx.x;
+  // Workgroups go to the 8 XCDs round-robin by linear id, and each XCD has its own L2. The
+  // (split, tile) items are renumbered so that XCD x runs one contiguous range of them:
+  // the ~32 workgroups resident on an XCD then share operand panels in that XCD's L2.
   const int T = g.tiles_i * g.tiles_j;
-  if (T % 8 == 0) bid = (bid % 8) * (T / 8) + bid / 8;
+  const int total = T * (int)gridDim.z;
+  const int lin = (int)blockIdx.x + T * (int)blockIdx.z;
+  const int xcd = lin % 8, q8 = total / 8, r8 = total % 8;
+  const int item = xcd * q8 + min(xcd, r8) + lin / 8;
+  const int zsl = item / T;
+  const int bid = item % T;
   const int GROUP = g.group;
   const int per_group = GROUP * g.tiles_j;
   const int first_i = (bid / per_group) * GROUP;
@@ -234,7 +241,7 @@ __global__ __launch_bounds__(NTHR) void gemm2_kernel(const Args g) {
   const int tile_i = first_i + (bid % per_group) % gsz;
   const int tile_j = (bid % per_group) / gsz;
   const int64_t i0 = (int64_t)tile_i * TILE, j0 = (int64_t)tile_j * TILE;
-  const int64_t rbeg = (int64_t)blockIdx.z * g.r_split;
+  const int64_t rbeg = (int64_t)zsl * g.r_split;
   const int64_t rend = min(g.R, rbeg + g.r_split);
   const int64_t rlen = rend > rbeg ? rend - rbeg : 0;
   const int nfull = (int)(rlen / BK);
@@ -255,7 +262,7 @@ __global__ __launch_bounds__(NTHR) void gemm2_kernel(const Args g) {
   // have the same LDS layouts as the main ones (A row-major; B row tile in the forward,
   // col tile in grad_x), so every stage runs the same MFMA body.
   const bool tail = (rlen % BK) != 0;
-  const bool lora = EPI == EPI_BF16 && g.R2 > 0 && blockIdx.z == 0;
+  const bool lora = EPI == EPI_BF16 && g.R2 > 0 && zsl == 0;
   const int nst = nfull + (tail ? 1 : 0) + (lora ? 1 : 0);
 
   // The palette operand's registers are loaded one stage ahead of the copies: during stage
@@ -443,7 +450,7 @@ __global__ __launch_bounds__(NTHR) void gemm2_kernel(const Args g) {
             }
           }
         }
-        float* dst = g.partial + (((int64_t)blockIdx.z * g.I + n) * segs + kseg / 128) * 4;
+        float* dst = g.partial + (((int64_t)zsl * g.I + n) * segs + kseg / 128) * 4;
         *reinterpret_cast<float4*>(dst) = make_float4(s0, s1, s2, s3);
       }
     } else {  // EPI_SOFT: each wave walks (row, 128-k segment) items; lane = 2 consecutive k
@@ -673,6 +680,7 @@ int plz_lut_linear_bwd_palette(const uint16_t* x, const uint16_t* grad_y, const 
   g.packed = packed; g.Nw = N; g.Kw = K;
   g.I = N; g.J = K; g.R = M; g.r_split = split_len(M, z);
   g.partial = reinterpret_cast<float*>(workspace);
+  g.group = 1;
   int rc = launch<OP_COL, OP_COL, EPI_PAL>(g, z, (hipStream_t)stream, "plz_lut_linear_bwd_palette");
   if (rc != PLZ_OK) return rc;
   const int64_t G = K / 256, n_out = N * G;
