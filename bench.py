@@ -74,28 +74,37 @@ class HardStep:
         rec = self.events if timed else None
         for it in self.items:
             x, gy, a, b = it["x"], it["gy"], it["a"], it["b"]
+            r = it["r"]
+            e = self._mark(rec, "lora", it, 2.0 * M_TRAIN * it["K"] * r, M_TRAIN * it["K"] * 2)
             t = ops.lora_project(x, a, 1.0)
+            self._close(e)
             e = self._mark(rec, "fwd", it)
             ops.lut_linear_fwd(x, it["packed"], it["pal"], None, t, b)
             self._close(e)
+            e = self._mark(rec, "lora", it, 2.0 * M_TRAIN * it["N"] * r, M_TRAIN * it["N"] * 2)
             gt = ops.lora_grad_t(gy, b, 1.0)
+            self._close(e)
             e = self._mark(rec, "grad_x", it)
             ops.lut_linear_bwd_x(gy, it["packed"], it["pal"], gt, a)
             self._close(e)
             e = self._mark(rec, "grad_palette", it)
             ops.lut_linear_bwd_palette(x, gy, it["packed"])
             self._close(e)
+            e = self._mark(rec, "lora", it, 2.0 * M_TRAIN * (it["K"] + it["N"]) * r,
+                           M_TRAIN * (it["K"] + it["N"]) * 2)
             ops.lora_weight_grads(x, gy, t, gt, 1.0, out_dtype=torch.bfloat16)
+            self._close(e)
 
     @staticmethod
-    def _mark(rec, kind, it):
+    def _mark(rec, kind, it, flop=None, nbytes=0):
         if rec is None:
             return None
         import torch
         s = torch.cuda.Event(enable_timing=True)
         e = torch.cuda.Event(enable_timing=True)
         s.record()
-        rec.setdefault(kind, []).append((s, e, 2.0 * M_TRAIN * it["K"] * it["N"]))
+        flop = 2.0 * M_TRAIN * it["K"] * it["N"] if flop is None else flop
+        rec.setdefault(kind, []).append((s, e, flop, nbytes))
         return e
 
     @staticmethod
@@ -105,12 +114,14 @@ class HardStep:
 
 
 def kernel_rooflines(events):
-    """Per GEMM kind: algorithmic FLOP / summed event time -> TFLOP/s."""
+    """Per kind: algorithmic FLOP (and activation bytes) / summed event time."""
     out = {}
     for kind, lst in events.items():
-        ms = sum(s.elapsed_time(e) for s, e, _ in lst)
-        fl = sum(f for _, _, f in lst)
-        out[kind] = dict(ms=ms, launches=len(lst), tflops=fl / (ms * 1e-3) / 1e12)
+        ms = sum(s.elapsed_time(e) for s, e, _, _ in lst)
+        fl = sum(f for _, _, f, _ in lst)
+        nb = sum(b for _, _, _, b in lst)
+        out[kind] = dict(ms=ms, launches=len(lst), tflops=fl / (ms * 1e-3) / 1e12,
+                         gbs=nb / (ms * 1e-3) / 1e9)
     return out
 
 
@@ -316,7 +327,7 @@ def main():
         ms = t0.elapsed_time(t1) / args.steps
         tflops = step.flop / (ms * 1e-3) / 1e12
         kr = kernel_rooflines(step.events)
-        dom = max(kr, key=lambda k: kr[k]["ms"])
+        dom = max((k for k in kr if k != "lora"), key=lambda k: kr[k]["ms"])
         out.update(value=round(tflops, 2), ms_per_step=round(ms, 3))
         out["roofline"] = {"bound": "mfma", "kernel": KERNEL_NAMES[dom],
                            "achieved": round(kr[dom]["tflops"], 1), "peak": PEAK_BF16_TFLOPS,
@@ -324,6 +335,8 @@ def main():
                            "traffic": GEMM_TRAFFIC_BYTES[dom], "traffic_unit": "bytes/launch"}
         out["kernels"] = {k: {"tflops": round(v["tflops"], 1),
                               "ms_per_step": round(v["ms"] / args.steps, 3)} for k, v in kr.items()}
+        # the LoRA products are HBM-bound: activation bytes streamed per second
+        out["kernels"]["lora"]["gbs"] = round(kr["lora"]["gbs"], 1)
         _log(f"hard: {ms:.3f} ms/step, {tflops:.1f} TFLOP/s")
         del step
         torch.cuda.empty_cache()

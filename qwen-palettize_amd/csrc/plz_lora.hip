@@ -1,0 +1,508 @@
+// Rank-r adapter products of QwenLoRA (qwen_model.py:291-304): y += s (x A^T) B^T.
+//
+//   plz_lora_project        t  = s x A^T          [M, r]   reduction over K (contiguous in x)
+//   plz_lora_grad_t         gt = s grad_y B       [M, r]   reduction over N (contiguous in grad_y)
+//   plz_lora_weight_grads   grad_A = gt^T x       [r, K]   reduction over M (strided)
+//                           grad_B = s grad_y^T t [N, r]
+//
+// All four stream one M x L activation (x or grad_y) and touch a rank-r operand that stays in
+// L2, so they are HBM-bound: the work per activation element is r <= 32 MACs. Two kernels:
+//
+// rows_kernel  (t, gt): the activation is the MFMA A operand read straight from global memory
+//   (16 bytes = 8 consecutive reduction elements per lane, the 16x16x32 operand layout). A
+//   workgroup owns 64 rows; its 4 waves take interleaved 32-wide reduction steps and meet in
+//   LDS at the end. lora_a [r, L] gives B fragments as 16-byte loads; lora_b [L, r] as eight
+//   2-byte loads (it is L2-resident and shared by the 64 rows).
+// cols_kernel  (grad_A, grad_B): the reduction index m is the activation's row, so fragments
+//   need a transpose. 64 x 256 activation tiles go global->LDS (buffer_load ... lds, 4-stage
+//   ring) and are read with ds_read_b64_tr_b16, which hands each lane 4 consecutive rows of
+//   one column. Split over M; reduce_kernel sums the split partials in a fixed order. Both
+//   weight gradients share one cols_kernel launch and one reduce_kernel launch.
+#include "plz_common.h"
+#include "palettize_hip.h"
+
+namespace plz {
+namespace lora {
+
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+
+__device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ bf16x8 as_frag(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+// ---------------------------------------------------------------------------------------
+// rows_kernel: out[M, r] = scale * X[M, L] Bop[L, r]
+//   BOP_T: Bop(l, j) = bop[j * L + l]  (lora_a, [r, L]);  else Bop(l, j) = bop[l * r + j]
+//   RG = 16-column groups (r <= 16 * RG)
+// ---------------------------------------------------------------------------------------
+#ifndef PLZ_RW_NG
+#define PLZ_RW_NG 4
+#endif
+#ifndef PLZ_RW_WAVES
+#define PLZ_RW_WAVES 4
+#endif
+#ifndef PLZ_RW_U
+#define PLZ_RW_U 4
+#endif
+constexpr int RW_NG = PLZ_RW_NG;        // MFMA row groups of 16 per workgroup
+constexpr int RW_ROWS = 16 * RW_NG;     // activation rows per workgroup
+constexpr int RW_WAVES = PLZ_RW_WAVES;  // waves per workgroup, interleaved over the reduction
+constexpr int RW_U = PLZ_RW_U;          // 32-wide reduction steps per wave per iteration
+
+template <bool BOP_T, int RG>
+__global__ __launch_bounds__(64 * RW_WAVES) void rows_kernel(const uint16_t* __restrict__ X,
+                                                             const uint16_t* __restrict__ bop,
+                                                             uint16_t* __restrict__ out,
+                                                             float scale, int64_t M, int L,
+                                                             int r) {
+  __shared__ float red[RW_WAVES][RW_ROWS][RG * 16 + 1];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int rr = lane & 15, q = lane >> 4;
+  const int64_t m0 = (int64_t)blockIdx.x * RW_ROWS;
+  const int rows = (int)min((int64_t)RW_ROWS, M - m0);
+  // rows past the end of X fall outside the descriptor's range and read as zero
+  const BufRsrc xr = make_rsrc(X + m0 * L, (uint32_t)rows * (uint32_t)L * 2u);
+  const BufRsrc br = make_rsrc(bop, (uint32_t)r * (uint32_t)L * 2u);
+  uint32_t xoff[RW_NG];
+#pragma unroll
+  for (int g = 0; g < RW_NG; ++g) xoff[g] = ((uint32_t)(16 * g + rr) * (uint32_t)L + 8u * q) * 2u;
+
+  const int nks = (L + 31) / 32;                                    // 32-wide reduction steps
+  const int nit = (nks + RW_WAVES * RW_U - 1) / (RW_WAVES * RW_U);  // iterations
+
+  auto load = [&](int it, uint4 (&xv)[RW_U][RW_NG], bf16x8 (&bv)[RW_U][RG]) {
+#pragma unroll
+    for (int u = 0; u < RW_U; ++u) {
+      const int s = wave + RW_WAVES * (RW_U * it + u);
+      const int l = 32 * s + 8 * q;  // this lane's 8 reduction elements: l .. l+7
+      const bool lin = l < L;
+#pragma unroll
+      for (int g = 0; g < RW_NG; ++g) xv[u][g] = buf_load16(xr, lin ? xoff[g] + 64u * s : kBufOob);
+#pragma unroll
+      for (int cg = 0; cg < RG; ++cg) {
+        const int j = 16 * cg + rr;
+        const bool ok = lin && j < r;
+        if constexpr (BOP_T) {
+          bv[u][cg] = as_frag(buf_load16(br, ok ? ((uint32_t)j * L + l) * 2u : kBufOob));
+        } else {
+          uint32_t w[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const uint32_t o0 = ok ? ((uint32_t)(l + 2 * e) * r + j) * 2u : kBufOob;
+            const uint32_t o1 = ok ? ((uint32_t)(l + 2 * e + 1) * r + j) * 2u : kBufOob;
+            const uint32_t lo = __builtin_amdgcn_raw_buffer_load_b16(br, (int)o0, 0, 0);
+            const uint32_t hi = __builtin_amdgcn_raw_buffer_load_b16(br, (int)o1, 0, 0);
+            w[e] = lo | (hi << 16);
+          }
+          bv[u][cg] = as_frag(make_uint4(w[0], w[1], w[2], w[3]));
+        }
+      }
+    }
+  };
+  f32x4 acc[RW_NG][RG];
+#pragma unroll
+  for (int g = 0; g < RW_NG; ++g)
+#pragma unroll
+    for (int cg = 0; cg < RG; ++cg) acc[g][cg] = f32x4{0.f, 0.f, 0.f, 0.f};
+  auto mma = [&](const uint4 (&xv)[RW_U][RW_NG], const bf16x8 (&bv)[RW_U][RG]) {
+#pragma unroll
+    for (int u = 0; u < RW_U; ++u)
+#pragma unroll
+      for (int g = 0; g < RW_NG; ++g)
+#pragma unroll
+        for (int cg = 0; cg < RG; ++cg) acc[g][cg] = mfma16(as_frag(xv[u][g]), bv[u][cg], acc[g][cg]);
+  };
+
+  // two register sets: the loads of iteration it+1 are in flight during the MFMAs of it
+  // (iterations past nit load nothing: every lane's offset is out of range and reads zero)
+  uint4 x0[RW_U][RW_NG], x1[RW_U][RW_NG];
+  bf16x8 b0[RW_U][RG], b1[RW_U][RG];
+  load(0, x0, b0);
+  for (int it = 0; it < nit; it += 2) {
+    load(it + 1, x1, b1);
+    mma(x0, b0);
+    if (it + 2 < nit) load(it + 2, x0, b0);
+    if (it + 1 < nit) mma(x1, b1);
+  }
+
+  // Cross-wave sum in wave order (C fragment: lane holds rows 4q..4q+3 of column rr in each
+  // 16x16 block).
+#pragma unroll
+  for (int g = 0; g < RW_NG; ++g)
+#pragma unroll
+    for (int cg = 0; cg < RG; ++cg)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) red[wave][16 * g + 4 * q + e][16 * cg + rr] = acc[g][cg][e];
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < rows * r; idx += 64 * RW_WAVES) {
+    const int row = idx / r, j = idx - row * r;
+    float s = 0.f;
+#pragma unroll
+    for (int w = 0; w < RW_WAVES; ++w) s += red[w][row][j];
+    out[(m0 + row) * r + j] = (uint16_t)f2bf(scale * s);
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// cols_kernel: partial[z][l][j] = scale * sum_{m in split z} X[m, l] T[m, j]
+//   X [M, L] and T [M, r] row-major. Workgroup: 256 columns l (4 waves x 64) x one M split.
+// ---------------------------------------------------------------------------------------
+constexpr int CL_L = 256;
+constexpr int CL_BM = 64;                        // rows per stage
+constexpr int CL_NS = 4;                         // LDS ring depth
+constexpr int CL_XBYTES = CL_BM * CL_L * 2;      // 32 KB
+constexpr int CL_TBYTES = 4096;                  // 64 rows x 32 ranks x 2 B
+constexpr int CL_STAGE = CL_XBYTES + CL_TBYTES;
+constexpr int CL_LDS = CL_NS * CL_STAGE;         // 144 KB
+constexpr int CL_LOADS = CL_XBYTES / (256 * 16) + 1;  // copies per thread per stage: 8 + 1
+
+// X tile layout: row m (512 B) holds 32 chunks of 16 B; chunk c sits at c ^ xsw(m). Rows
+// m..m+3 and m+8..m+11 (what one half-wave of a transposing read touches) land their two
+// chunks on 8 distinct bank pairs, so the fragment reads are conflict-free.
+__device__ __forceinline__ int xsw(int m) { return 2 * (m & 3) + 8 * ((m >> 3) & 1); }
+
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xF | (3 << 14) | (7 << 4));  // lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// One workgroup = one (problem, column tile, M split); problem 0 is grad_B, problem 1 grad_A,
+// so both weight gradients run in one launch.
+struct ColProb {
+  const uint16_t* X;  // [M, L]
+  const uint16_t* T;  // [M, r]
+  float* partial;     // [Z, L, r]
+  float scale;
+  int L, tiles;
+  int64_t split;      // rows per M split (a multiple of CL_BM)
+};
+struct ColsArgs {
+  ColProb p[2];
+  int nwg0;  // workgroups of problem 0
+  int64_t M;
+  int r;
+};
+
+template <int RG>
+__global__ __launch_bounds__(256) void cols_kernel(const ColsArgs args) {
+  extern __shared__ uint4 smem[];
+  lds_u8* lds = (lds_u8*)smem;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const bool second = (int)blockIdx.x >= args.nwg0;
+  const ColProb& pb = second ? args.p[1] : args.p[0];
+  const int bid = (int)blockIdx.x - (second ? args.nwg0 : 0);
+  const uint16_t* __restrict__ X = pb.X;
+  const uint16_t* __restrict__ T = pb.T;
+  const int L = pb.L, r = args.r, zi = bid / pb.tiles;
+  const int64_t M = args.M, split = pb.split;
+  const int lb = (bid % pb.tiles) * CL_L;
+  const int64_t mb = (int64_t)zi * split;
+  const int64_t me = min(M, mb + split);
+  const int rows = me > mb ? (int)(me - mb) : 0;
+  const int nst = (rows + CL_BM - 1) / CL_BM;
+  // rows past the split fall outside both descriptors' ranges and read as zero
+  const BufRsrc xr = make_rsrc(X + mb * L, (uint32_t)rows * (uint32_t)L * 2u);
+  const BufRsrc tr = make_rsrc(T + mb * r, (uint32_t)rows * (uint32_t)r * 2u);
+
+  // Copies of stage s into ring slot s % CL_NS: X by 8 instructions per lane (instruction it
+  // of wave w fills LDS bytes [(8w+it) KB, +1 KB) = rows 2(8w+it), +1), T by one (RG = 1 keeps
+  // 128 chunks, waves 2-3 write an unread duplicate so that every lane issues the same count).
+  auto issue = [&](int s) {
+    lds_u8* xs = lds + (s % CL_NS) * CL_STAGE;
+    const bool live = s < nst;
+#pragma unroll
+    for (int it = 0; it < CL_XBYTES / (256 * 16); ++it) {
+      const int p = (wave * 8 + it) * 64 + lane;  // physical chunk
+      const int m = p >> 5, gc = (p & 31) ^ xsw(m);
+      const int l = lb + 8 * gc;
+      const uint32_t off =
+          live && l < L ? ((uint32_t)(CL_BM * s + m) * (uint32_t)L + (uint32_t)l) * 2u : kBufOob;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_u8*)(xs + (wave * 8 + it) * 1024), 16, off,
+                                               0, 0, 0);
+    }
+    const int p = threadIdx.x % (RG * 128);  // T chunk: row p / (2 RG), 8 ranks (p % (2 RG))
+    const int m = p / (2 * RG), c = p % (2 * RG);
+    const uint32_t off = live && 8 * c < r ? ((uint32_t)(CL_BM * s + m) * (uint32_t)r + 8u * c) * 2u
+                                           : kBufOob;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(tr, (lds_u8*)(xs + CL_XBYTES + wave * 1024), 16, off,
+                                             0, 0, 0);
+  };
+
+  f32x4 acc[4][RG];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int cg = 0; cg < RG; ++cg) acc[i][cg] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int i16 = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int s = 0; s < CL_NS - 1; ++s) issue(s);
+  for (int s = 0; s < nst; ++s) {
+    wait_vmcnt<CL_LOADS*(CL_NS - 2)>();  // this lane's copies of stage s have landed
+    lds_barrier();                         // everyone's have; slot (s-1) % CL_NS is free
+    issue(s + CL_NS - 1);
+    const lds_u8* xs = lds + (s % CL_NS) * CL_STAGE;
+    const lds_u8* ts = xs + CL_XBYTES;
+#pragma unroll
+    for (int ks = 0; ks < CL_BM / 32; ++ks) {
+      // lane (i16, g) points at rows 32ks + 8g + i16/4 (+4) and 4 consecutive columns; the
+      // transposing read returns column i16 of the 16-wide block at 4 consecutive rows
+      const int m1 = 32 * ks + 8 * g + (i16 >> 2), m2 = m1 + 4;
+      bf16x8 a[4], b[RG];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int lc = 64 * wave + 16 * i + 4 * (i16 & 3);  // column within the tile
+        const int c = lc >> 3, o = (lc & 7) * 2;
+        const v4i16 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_v4i16*)(xs + m1 * 512 + ((c ^ xsw(m1)) << 4) + o));
+        const v4i16 v2 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_v4i16*)(xs + m2 * 512 + ((c ^ xsw(m2)) << 4) + o));
+        a[i] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(v1, v2, 0, 1, 2, 3, 4, 5, 6, 7));
+      }
+#pragma unroll
+      for (int cg = 0; cg < RG; ++cg) {
+        const int jc = 16 * cg + 4 * (i16 & 3);
+        const v4i16 v1 =
+            __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(ts + m1 * (RG * 32) + jc * 2));
+        const v4i16 v2 =
+            __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(ts + m2 * (RG * 32) + jc * 2));
+        b[cg] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(v1, v2, 0, 1, 2, 3, 4, 5, 6, 7));
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int cg = 0; cg < RG; ++cg) acc[i][cg] = mfma16(a[i], b[cg], acc[i][cg]);
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // drain the trailing (out-of-range) copies before exit
+
+  // C fragment: rows (columns l of X) 4g..4g+3, column (rank j) i16 of each 16x16 block
+  float* P = pb.partial + (int64_t)zi * L * r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int cg = 0; cg < RG; ++cg) {
+      const int j = 16 * cg + i16;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int l = lb + 64 * wave + 16 * i + 4 * g + e;
+        if (l < L && j < r) P[(int64_t)l * r + j] = pb.scale * acc[i][cg][e];
+      }
+    }
+}
+
+// out = sum_z partial[z][l][j] in z order, as bf16 or fp32, in [L, r] order or transposed to
+// [r, L]; one thread per output element, in output order (coalesced stores). Both problems of
+// a cols_kernel launch are reduced by one launch: threads [0, n0) problem a, the rest b.
+struct RedProb {
+  const float* partial;
+  void* out;
+  int64_t L;
+  int Z, transpose;
+};
+__global__ void reduce_kernel(const RedProb a, const RedProb b, int64_t n0, int64_t n, int r,
+                              int out_bf16) {
+  int64_t o = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (o >= n) return;
+  const bool second = o >= n0;
+  const RedProb& p = second ? b : a;
+  if (second) o -= n0;
+  const int64_t l = p.transpose ? o % p.L : o / r, j = p.transpose ? o / p.L : o % r;
+  const float* src = p.partial + l * r + j;
+  const int64_t zs = p.L * r;
+  // the loads of 8 splits are issued together, the adds stay in z order
+  float s = 0.f;
+  int z = 0;
+  for (; z + 8 <= p.Z; z += 8) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = src[(int64_t)(z + u) * zs];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) s += v[u];
+  }
+  for (; z < p.Z; ++z) s += src[(int64_t)z * zs];
+  if (out_bf16)
+    reinterpret_cast<uint16_t*>(p.out)[o] = (uint16_t)f2bf(s);
+  else
+    reinterpret_cast<float*>(p.out)[o] = s;
+}
+
+// M split of the column kernel: whole waves of 256 CUs (one workgroup per CU), each split
+// at least 4 stages deep; returns the split length in rows (a multiple of CL_BM).
+static int64_t col_split(int64_t M, int64_t L) {
+  const int64_t tiles = (L + CL_L - 1) / CL_L;
+  int best = 1;
+  double best_eff = 0.0;
+  for (int z = 1; z <= 64 && (int64_t)z * 4 * CL_BM <= M; ++z) {
+    const int64_t wgs = tiles * z, waves = (wgs + 255) / 256;
+    const double eff = (double)wgs / (double)(waves * 256);
+    if (eff > best_eff + 0.02) {
+      best_eff = eff;
+      best = z;
+    }
+  }
+  const int64_t per = (M + best - 1) / best;
+  return (per + CL_BM - 1) / CL_BM * CL_BM;
+}
+static int col_splits(int64_t M, int64_t L) {
+  const int64_t s = col_split(M, L);
+  return (int)((M + s - 1) / s);
+}
+
+template <typename K>
+static int reserve_lds(K kern, const char* what) {
+  static bool done = false;
+  if (done) return PLZ_OK;
+  const hipError_t e =
+      hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, CL_LDS);
+  if (e != hipSuccess) {
+    set_error("%s: cannot reserve %d bytes of LDS: %s", what, CL_LDS, hipGetErrorString(e));
+    return PLZ_EHIP;
+  }
+  done = true;
+  return PLZ_OK;
+}
+
+// grad_B = scale * grad_y^T t ([N, r]) and grad_A = (x^T gt)^T ([r, K]): one cols_kernel launch
+// over both, then one reduction launch. Workspace: split partials of B, then of A.
+static size_t cols_workspace_floats(int64_t M, int64_t N, int64_t K, int r) {
+  return ((size_t)col_splits(M, N) * N + (size_t)col_splits(M, K) * K) * r;
+}
+static int cols(const uint16_t* x, const uint16_t* grad_y, const uint16_t* t, const uint16_t* gt,
+                float scale, void* grad_a, void* grad_b, int out_bf16, float* ws, int64_t M,
+                int64_t N, int64_t K, int r, hipStream_t s, const char* what) {
+  ColsArgs g = {};
+  g.M = M;
+  g.r = r;
+  const int64_t Ls[2] = {N, K};
+  float* part = ws;
+  int nwg[2];
+  RedProb red[2];
+  for (int i = 0; i < 2; ++i) {
+    ColProb& p = g.p[i];
+    p.X = i == 0 ? grad_y : x;
+    p.T = i == 0 ? t : gt;
+    p.scale = i == 0 ? scale : 1.f;
+    p.L = (int)Ls[i];
+    p.tiles = (int)((Ls[i] + CL_L - 1) / CL_L);
+    p.split = col_split(M, Ls[i]);
+    p.partial = part;
+    const int z = (int)((M + p.split - 1) / p.split);
+    nwg[i] = p.tiles * z;
+    red[i] = RedProb{part, i == 0 ? grad_b : grad_a, Ls[i], z, i};
+    part += (size_t)z * Ls[i] * r;
+  }
+  g.nwg0 = nwg[0];
+  if (nwg[0] + nwg[1] == 0) return PLZ_OK;
+  const dim3 grid((unsigned)(nwg[0] + nwg[1]));
+  int rc;
+  if (r <= 16) {
+    if ((rc = reserve_lds(cols_kernel<1>, what))) return rc;
+    hipLaunchKernelGGL(cols_kernel<1>, grid, dim3(256), CL_LDS, s, g);
+  } else {
+    if ((rc = reserve_lds(cols_kernel<2>, what))) return rc;
+    hipLaunchKernelGGL(cols_kernel<2>, grid, dim3(256), CL_LDS, s, g);
+  }
+  if ((rc = check_launch(what))) return rc;
+  const int64_t n0 = N * r, n = n0 + K * r;
+  hipLaunchKernelGGL(reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, red[0],
+                     red[1], n0, n, r, out_bf16);
+  return check_launch(what);
+}
+
+template <bool BOP_T>
+static int rows(const uint16_t* X, const uint16_t* bop, float scale, uint16_t* out, int64_t M,
+                int64_t L, int r, hipStream_t s, const char* what) {
+  const dim3 grid((unsigned)((M + RW_ROWS - 1) / RW_ROWS));
+  if (r <= 16)
+    hipLaunchKernelGGL((rows_kernel<BOP_T, 1>), grid, dim3(64 * RW_WAVES), 0, s, X, bop, out, scale, M,
+                       (int)L, r);
+  else
+    hipLaunchKernelGGL((rows_kernel<BOP_T, 2>), grid, dim3(64 * RW_WAVES), 0, s, X, bop, out, scale, M,
+                       (int)L, r);
+  return check_launch(what);
+}
+
+static bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+}  // namespace lora
+}  // namespace plz
+
+using namespace plz;
+using namespace plz::lora;
+
+extern "C" {
+
+int plz_lora_project(const uint16_t* x, const uint16_t* lora_a, float scale, uint16_t* t,
+                     int64_t M, int64_t K, int rank, void* stream) {
+  PLZ_REQUIRE(M >= 0 && K >= 0 && rank > 0 && rank <= 32 && rank % 8 == 0,
+              "plz_lora_project: need M, K >= 0 and rank a multiple of 8 in [8, 32]");
+  PLZ_REQUIRE(K % 8 == 0, "plz_lora_project: K must be a multiple of 8");
+  PLZ_REQUIRE(K < (1 << 24) && RW_ROWS * K * 2 < (int64_t)1 << 31,
+              "plz_lora_project: K (%lld) too large", (long long)K);
+  if (M == 0) return PLZ_OK;
+  PLZ_REQUIRE(x && lora_a && t && aligned16(x) && aligned16(lora_a),
+              "plz_lora_project: null or misaligned pointer");
+  return rows<true>(x, lora_a, scale, t, M, K, rank, (hipStream_t)stream, "plz_lora_project");
+}
+
+int plz_lora_grad_t(const uint16_t* grad_y, const uint16_t* lora_b, float scale, uint16_t* gt,
+                    int64_t M, int64_t N, int rank, void* stream) {
+  PLZ_REQUIRE(M >= 0 && N >= 0 && rank > 0 && rank <= 32 && rank % 8 == 0,
+              "plz_lora_grad_t: need M, N >= 0 and rank a multiple of 8 in [8, 32]");
+  PLZ_REQUIRE(N % 8 == 0, "plz_lora_grad_t: N must be a multiple of 8");
+  PLZ_REQUIRE(N < (1 << 24) && RW_ROWS * N * 2 < (int64_t)1 << 31,
+              "plz_lora_grad_t: N (%lld) too large", (long long)N);
+  if (M == 0) return PLZ_OK;
+  PLZ_REQUIRE(grad_y && lora_b && gt && aligned16(grad_y) && aligned16(lora_b),
+              "plz_lora_grad_t: null or misaligned pointer");
+  return rows<false>(grad_y, lora_b, scale, gt, M, N, rank, (hipStream_t)stream,
+                     "plz_lora_grad_t");
+}
+
+size_t plz_lora_weight_grads_workspace(int64_t M, int64_t N, int64_t K, int rank) {
+  if (M <= 0 || rank <= 0) return 0;
+  return cols_workspace_floats(M, N, K, rank) * sizeof(float);
+}
+
+int plz_lora_weight_grads(const uint16_t* x, const uint16_t* grad_y, const uint16_t* t,
+                          const uint16_t* gt, float scale, void* grad_a, void* grad_b,
+                          int out_dtype, void* workspace, size_t workspace_bytes, int64_t M,
+                          int64_t N, int64_t K, int rank, void* stream) {
+  PLZ_REQUIRE(M >= 0 && N >= 0 && K >= 0 && rank > 0 && rank <= 32 && rank % 8 == 0,
+              "plz_lora_weight_grads: bad shape");
+  PLZ_REQUIRE(N % 8 == 0 && K % 8 == 0, "plz_lora_weight_grads: N and K must be multiples of 8");
+  PLZ_REQUIRE(out_dtype == PLZ_DT_BF16 || out_dtype == PLZ_DT_FP32,
+              "plz_lora_weight_grads: out dtype must be bf16 or fp32");
+  PLZ_REQUIRE(x && grad_y && t && gt && grad_a && grad_b, "plz_lora_weight_grads: null pointer");
+  PLZ_REQUIRE(aligned16(x) && aligned16(grad_y) && aligned16(t) && aligned16(gt),
+              "plz_lora_weight_grads: inputs must be 16-byte aligned");
+  hipStream_t s = (hipStream_t)stream;
+  const int bf = out_dtype == PLZ_DT_BF16;
+  if (M == 0) {
+    hipMemsetAsync(grad_b, 0, (size_t)N * rank * (bf ? 2 : 4), s);
+    hipMemsetAsync(grad_a, 0, (size_t)K * rank * (bf ? 2 : 4), s);
+    return check_launch("plz_lora_weight_grads");
+  }
+  const int64_t split_n = col_split(M, N), split_k = col_split(M, K);
+  PLZ_REQUIRE(split_n * N * 2 < (int64_t)1 << 31 && split_k * K * 2 < (int64_t)1 << 31,
+              "plz_lora_weight_grads: M split x N or K too large");
+  const size_t need = plz_lora_weight_grads_workspace(M, N, K, rank);
+  if (!workspace || workspace_bytes < need) {
+    set_error("plz_lora_weight_grads: workspace of %zu bytes needed, %zu given", need,
+              workspace_bytes);
+    return PLZ_EWORKSPACE;
+  }
+  return cols(x, grad_y, t, gt, scale, grad_a, grad_b, bf, reinterpret_cast<float*>(workspace), M,
+              N, K, rank, s, "plz_lora_weight_grads");
+}
+
+}  // extern "C"

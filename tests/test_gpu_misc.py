@@ -12,9 +12,25 @@ import palettize_hip as P  # noqa: E402
 from palettize_hip import fused_lut_linear_cuda as FL  # noqa: E402
 
 
-@pytest.mark.parametrize("rank", [16, 32])
-def test_lora_weight_grads(dev, rank):
-    M, N, K = 1000, 264, 512
+@pytest.mark.parametrize("M,L,rank", [(1, 8, 8), (77, 520, 24), (1000, 264, 16), (130, 4104, 32),
+                                      (16384, 2560, 16), (4096, 9728, 32)])
+def test_lora_project_and_grad_t(dev, M, L, rank):
+    """t = s x A^T (A [r, L]) and gt = s grad_y B (B [L, r]): ragged rows, reduction lengths
+    that are not multiples of 32 or 256, every supported rank, and the full C3 shapes."""
+    x = randn_bf16(M, L, seed=M + L)
+    a = randn_bf16(rank, L, seed=rank, std=0.05)
+    t = ops.lora_project(x.to(dev), a.to(dev), 0.5)
+    assert t.shape == (M, rank)
+    assert_close(f32(t), 0.5 * (f32(x).astype(np.float64) @ f32(a).T), what="lora t")
+    b = randn_bf16(L, rank, seed=rank + 1, std=0.05)
+    gt = ops.lora_grad_t(x.to(dev), b.to(dev), 2.0)
+    assert_close(f32(gt), 2.0 * (f32(x).astype(np.float64) @ f32(b)), what="lora gt")
+
+
+@pytest.mark.parametrize("M,N,K,rank", [(1000, 264, 512, 16), (1000, 264, 512, 32),
+                                        (1, 8, 8, 8), (77, 520, 264, 24),
+                                        (16384, 9728, 2560, 16), (16384, 2560, 9728, 32)])
+def test_lora_weight_grads(dev, M, N, K, rank):
     x = randn_bf16(M, K, seed=1)
     gy = randn_bf16(M, N, seed=2)
     t = randn_bf16(M, rank, seed=3)
