@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define PLZ_ABI_VERSION 1
+#define PLZ_ABI_VERSION 2
 
 /* status codes */
 #define PLZ_OK 0
@@ -166,7 +166,8 @@ typedef struct plz_gemv_desc {
   const float* palette;   /* [N, K/256, 4] */
   uint16_t* y;            /* [M, N] bf16 */
   int64_t N, K;
-  int64_t block_begin;    /* filled by plz_gemv_plan: first row-block of this linear */
+  int64_t block_begin;    /* filled by plz_gemv_plan: first 128-row work item of this linear */
+  int64_t cost_begin;     /* filled by plz_gemv_plan: sum of K over the items before it */
 } plz_gemv_desc;
 
 /* y[M,N] = x[M,K] W^T for 1 <= M <= 16 (bandwidth-bound; one pass over the packed weights).
@@ -174,8 +175,8 @@ typedef struct plz_gemv_desc {
  * a 64-row tile at M = 1. */
 int plz_lut_gemv(const uint16_t* x, const int32_t* packed, const float* palette, uint16_t* y,
                  int64_t M, int64_t N, int64_t K, void* stream);
-/* Fills block_begin of n host descriptors and returns the total number of row blocks
- * (or a negative status). */
+/* Fills block_begin and cost_begin of n host descriptors and returns the total number of
+ * 128-row work items (or a negative status). A descriptor with N > 0 needs K > 0. */
 int64_t plz_gemv_plan(plz_gemv_desc* descs, int n, int M);
 /* Runs n independent GEMVs (all with the same M) in one launch. descs_device is a copy of
  * the planned descriptors in device memory; total_blocks is plz_gemv_plan's result. */

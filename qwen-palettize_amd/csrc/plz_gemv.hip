@@ -2,223 +2,334 @@
 //
 // The reference has no decode path; at M = 1 it would run the 64-row-tile forward kernel
 // (fused_lut_kernel.cu:309-518). Here the work is bandwidth-bound: 2 bits of index plus
-// 0.5 bit of fp32 palette per weight are streamed once.
+// 0.5 bit of fp32 palette per weight are streamed once, and everything else is arranged so
+// that the stream never stops:
 //
-// Layout of the work. A workgroup (4 wave64s) owns 64*RB rows and streams the whole of K
-// in iterations of 4 palette groups (1024 k). Wave w owns RB blocks of 16 rows. Lane
-// (n = l%16, q = l/16) works on row n and palette group 4*it + q: it reads that group's 64
-// bytes of indices (4 x 16 B, contiguous) and its 16-byte palette, so the four lanes of a
-// row read 256 contiguous bytes of indices and 64 contiguous bytes of palettes per
-// iteration. These loads are issued one iteration ahead of their use.
-// x is shared by every wave: each iteration's x chunk is loaded once per workgroup,
-// permuted into MFMA fragment order and kept in LDS (2 KB per token, double buffered, one
-// barrier per iteration); waves read their fragments with one 16-byte LDS read each. A
-// GEMV that loads x per wave is limited by the vector-memory data-return path, not HBM.
-// Inside a wave, v_mfma_f32_16x16x32_bf16 computes C[n][m] with A = 16 weight rows and
-// B = x^T. Fragment lanes of tokens m >= M repeat token M-1: they only feed output columns
-// m >= M, which are never stored. The four lane quarters feed different palette groups
-// into the same MFMA, which is fine because the product sums over every k. A packed word
-// dequantises into the slots {w_j, w_j+4} and {w_j+8, w_j+12} (the cheapest byte-permute
-// order); the x fragments are permuted into the same slot order, which leaves the dot
-// product unchanged.
+// * Persistent workgroups, one per CU. The work items (128 rows of one linear, all of K) of
+//   a launch are cut into one contiguous range per workgroup, balanced by bytes (K per item).
+// * A workgroup walks its items as one sequence of stages (128 rows x 512 k). Each stage's
+//   packed indices, palettes and x slice go global->LDS by buffer_load ... lds (1 KB per
+//   instruction, whole cache lines, no VGPRs), three stages ahead in a 4-slot ring, across
+//   item boundaries -- the loads of the next item are in flight while this one finishes.
+// * Wave w owns rows 32w..32w+31 of the item (two MFMA row blocks of 16). Lane (row n%16,
+//   quarter q) dequantises 8 consecutive packed words (128 k) of its row per stage through
+//   v_perm_b32 byte tables into bf16 fragments (in a permuted k order that the x fragments
+//   repeat); v_mfma_f32_16x16x32_bf16
+//   computes C[n][m] for all M <= 16 tokens at once (fragment lanes of tokens m >= M read
+//   token M-1; their columns are never stored). x fragments come from the stage's x slice
+//   in LDS and serve both row blocks.
+// * LDS layouts are XOR-swizzled on the global side of the copies so that every fragment
+//   read is bank-conflict free.
 #include "plz_common.h"
+#include "palettize_hip.h"
 
 namespace plz {
+namespace gv {
 
-// Dequantise one word into MFMA slot order: s0 = k {0,4,1,5,2,6,3,7}, s1 = k {8,12,...,15}.
-__device__ __forceinline__ void dequant16_slots(uint32_t q, PalLut t, u32x4& s0, u32x4& s1) {
-  uint32_t a[4], b[4];
+// Dequantise one packed word (16 indices) into two MFMA fragments in the cheapest byte-permute
+// order: a = k {0,4,1,5,2,6,3,7}, b = k {8,12,9,13,10,14,11,15} (23 VALU per 16 weights).
+__device__ __forceinline__ void dequant16_slots(uint32_t q, PalLut t, u32x4& a, u32x4& b) {
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const uint32_t u = (q >> (2 * j)) & 0x03030303u;
+    const uint32_t u = (q >> (2 * j)) & 0x03030303u;  // indices j, j+4, j+8, j+12
     const uint32_t l = perm(0, t.lo, u), h = perm(0, t.hi, u);
     a[j] = perm(h, l, 0x05010400u);  // {w_j, w_j+4}
     b[j] = perm(h, l, 0x07030602u);  // {w_j+8, w_j+12}
   }
-  s0 = u32x4{a[0], a[1], a[2], a[3]};
-  s1 = u32x4{b[0], b[1], b[2], b[3]};
 }
 
-// x values of one 16-k word (natural order, two uint4) into the same slot order.
-__device__ __forceinline__ void xslots(uint4 x0, uint4 x1, u32x4& s0, u32x4& s1) {
-  s0 = u32x4{perm(x0.z, x0.x, 0x05040100u), perm(x0.z, x0.x, 0x07060302u),
-             perm(x0.w, x0.y, 0x05040100u), perm(x0.w, x0.y, 0x07060302u)};
-  s1 = u32x4{perm(x1.z, x1.x, 0x05040100u), perm(x1.z, x1.x, 0x07060302u),
-             perm(x1.w, x1.y, 0x05040100u), perm(x1.w, x1.y, 0x07060302u)};
-}
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
+typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
 
-// Workgroup barrier without the memory fence of __syncthreads(), which would also wait for
-// the weight loads in flight: this wave's LDS operations complete, then s_barrier.
+constexpr int WAVES = 4;
+constexpr int RB = 2;                         // MFMA row blocks of 16 per wave
+constexpr int ROWS = WAVES * 16 * RB;         // rows per work item: 128
+constexpr int KC = 256;                       // k per stage: one palette group
+constexpr int W_WAVE = 16 * RB * (KC / 4);    // packed bytes per wave and stage: 2 KB
+constexpr int W_BYTES = WAVES * W_WAVE;       // 8 KB
+constexpr int X_TOKEN = KC * 2;               // x bytes per token and stage: 512 B
+// Besides the packed words (2 copies per wave), each stage copies the item's palettes (128 rows
+// x 16 B = 2 KB) and the x slice (M x 512 B) in 1 KB copy slots g = 4j + wave (j < NPX): slots
+// 0-1 palettes, then two tokens per slot; slots past the data copy zeros.
+template <int NPX>
+constexpr int stage_bytes() { return W_BYTES + NPX * WAVES * 1024; }
+// LDS ring slots (NS - 1 stages in flight) and the workgroups that share a CU's 160 KB
+#ifndef PLZ_GV_NS
+#define PLZ_GV_NS 4
+#endif
+template <int NPX>
+constexpr int ring() { return PLZ_GV_NS; }
+template <int NPX>
+constexpr int lds_bytes() { return ring<NPX>() * stage_bytes<NPX>(); }
+template <int NPX>
+constexpr int wgs_per_cu() { return 160 * 1024 / lds_bytes<NPX>() < 4 ? 160 * 1024 / lds_bytes<NPX>() : 4; }
+__host__ __device__ constexpr int npx_for(int M) { return (2 + (M + 1) / 2 + WAVES - 1) / WAVES; }
+
+// swizzles (16-byte chunk index XOR): packed rows of 64 B (4 chunks), x rows of 512 B (32 chunks)
+__device__ __forceinline__ int w_swz(int row) { return (row >> 2) & 3; }
+__device__ __forceinline__ int x_swz(int m) { return m & 15; }
+
 __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_s_waitcnt(0xF | (3 << 14) | (7 << 4));  // lgkmcnt(0)
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
 }
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+__device__ __forceinline__ void dma16(BufRsrc r, uint32_t off, lds_u8* lds_wave_base) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds_wave_base, 16, off, 0, 0, 0);
+}
 
-// LDS x fragments of one iteration: [sub-step 4][fragment 8][quarter 4][token m < M] x 16 B
-// = 2 KB per token, double buffered (dynamic LDS: 4 KB x M per workgroup).
-constexpr int kXFragBytesPerToken = 4 * 8 * 4 * 16;
-constexpr int kGemvRb = 2;                 // row blocks of 16 per wave
-constexpr int kGemvRows = 64 * kGemvRb;   // rows per workgroup
-
-template <int RB, bool GROUPED>
-__global__ __launch_bounds__(256) void gemv_kernel(const plz_gemv_desc* __restrict__ descs,
-                                                   int n_desc, plz_gemv_desc single, int M) {
-  extern __shared__ u32x4 xlds[];  // [2][4*8*4*M]
-  const int64_t blk = blockIdx.x;
-  plz_gemv_desc d;
-  if (GROUPED) {
-    int lo = 0, hi = n_desc - 1;
+// The item list of a launch: items [block_begin, block_begin + ceil(N/ROWS)) belong to
+// descriptor d; item j of d starts at byte-cost cost_begin + j*K.
+template <bool GROUPED>
+struct Table {
+  const plz_gemv_desc* descs;
+  int n;
+  plz_gemv_desc single;
+  __device__ __forceinline__ plz_gemv_desc at(int i) const { return GROUPED ? descs[i] : single; }
+  __device__ __forceinline__ int find_item(int64_t item) const {  // descriptor of an item
+    if (!GROUPED) return 0;
+    int lo = 0, hi = n - 1;
     while (lo < hi) {
       const int mid = (lo + hi + 1) >> 1;
-      if (descs[mid].block_begin <= blk) lo = mid; else hi = mid - 1;
+      if (descs[mid].block_begin <= item) lo = mid; else hi = mid - 1;
     }
-    d = descs[lo];
-  } else {
-    d = single;
+    return lo;
   }
-  const int64_t N = d.N, K = d.K;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int64_t row0 = (blk - d.block_begin) * (64 * RB) + wave * (16 * RB);
-  const bool has_rows = row0 < N;  // waves without rows still take part in the barriers
-  const int nl = lane & 15, qg = lane >> 4;
-  const int gpr = (int)(K / kPalGroup);
-  const int iters = (gpr + 3) / 4;
-  // sizes were checked on the host to fit the 32-bit buffer range
-  const BufRsrc rq = make_rsrc(d.packed, (uint32_t)(N * K / 4));
-  const BufRsrc rp = make_rsrc(d.palette, (uint32_t)(N * gpr * 16));
-  const BufRsrc rx = make_rsrc(d.x, (uint32_t)(M * K * 2));
-  uint32_t oq[RB], op[RB];
-#pragma unroll
-  for (int r = 0; r < RB; ++r) {
-    const int64_t n = row0 + 16 * r + nl;
-    oq[r] = n < N ? (uint32_t)(n * (K / 4) + 64 * qg) : kBufOob;
-    op[r] = n < N ? (uint32_t)((n * gpr + qg) * 16) : kBufOob;
+  // the item whose start cost is nearest to c (ties to the later one)
+  __device__ __forceinline__ int64_t item_at_cost(int64_t c) const {
+    int lo = 0;
+    if (GROUPED) {
+      int hi = n - 1;
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (descs[mid].cost_begin <= c) lo = mid; else hi = mid - 1;
+      }
+    }
+    const plz_gemv_desc d = at(lo);
+    const int64_t items = d.K > 0 ? (d.N + ROWS - 1) / ROWS : 0;
+    if (items == 0) return d.block_begin;
+    const int64_t j = (c - d.cost_begin + d.K / 2) / d.K;
+    return d.block_begin + (j < items ? j : items);
   }
+  __device__ __forceinline__ int64_t total_cost() const {
+    const plz_gemv_desc d = at(GROUPED ? n - 1 : 0);
+    const int64_t items = d.K > 0 ? (d.N + ROWS - 1) / ROWS : 0;
+    return d.cost_begin + items * d.K;
+  }
+};
 
-  // x staging: item i < 64*M of an iteration is (m = i/64, q, sub-step st, word w); it
-  // covers x[m][k0 .. k0+16) with k0 = 256*(4*it + q) + 64*st + 16*w, and produces the two
-  // fragments 2w, 2w+1 of sub-step st for fragment lane m + 16*q.
-  const int n_items = 64 * M;
-  const int xbuf = 4 * 8 * 4 * M;  // u32x4 per buffer
-  // fragment lanes of tokens m >= M read token M-1 (a broadcast); their columns are dropped
-  const int xl = qg * M + (nl < M ? nl : M - 1);
-  auto stage_load = [&](int it, int i, uint4& a, uint4& b) {
-    const int m = i >> 6, q = (i >> 4) & 3, st = (i >> 2) & 3, w = i & 3;
-    const bool v = 4 * it + q < gpr;
-    const uint32_t o = v ? (uint32_t)((m * K + 256 * (4 * it + q) + 64 * st + 16 * w) * 2) : kBufOob;
-    a = buf_load16(rx, o);
-    b = buf_load16(rx, o + 16u);
-  };
-  auto stage_store = [&](int buf, int i, uint4 a, uint4 b) {
-    const int m = i >> 6, q = (i >> 4) & 3, st = (i >> 2) & 3, w = i & 3;
-    u32x4 s0, s1;
-    xslots(a, b, s0, s1);
-    u32x4* xb = xlds + buf * xbuf;
-    xb[((st * 8 + 2 * w) * 4 + q) * M + m] = s0;
-    xb[((st * 8 + 2 * w + 1) * 4 + q) * M + m] = s1;
-  };
-  // M <= 16, so a thread handles at most 4 items per iteration
-  constexpr int kMaxItems = 4;
-  uint4 xa[kMaxItems], xb[kMaxItems];
-  auto stage_issue = [&](int it) {
-#pragma unroll
-    for (int j = 0; j < kMaxItems; ++j)
-      if (tid + 256 * j < n_items) stage_load(it, tid + 256 * j, xa[j], xb[j]);
-  };
-  auto stage_commit = [&](int buf) {
-#pragma unroll
-    for (int j = 0; j < kMaxItems; ++j)
-      if (tid + 256 * j < n_items) stage_store(buf, tid + 256 * j, xa[j], xb[j]);
-  };
+// Position in a workgroup's stage sequence.
+struct Cursor {
+  int64_t item, end;
+  int kc, nkc;
+  plz_gemv_desc d;
+  int64_t row0;  // first row of the item
+};
+template <bool GROUPED>
+__device__ __forceinline__ void cursor_load(Cursor& c, const Table<GROUPED>& tb) {
+  c.kc = 0;
+  if (c.item >= c.end) {  // finished (or empty) range: a harmless, never-live cursor
+    c.nkc = 1;
+    c.d = plz_gemv_desc{};
+    c.row0 = 0;
+    return;
+  }
+  const int di = tb.find_item(c.item);
+  c.d = tb.at(di);
+  c.row0 = (c.item - c.d.block_begin) * ROWS;
+  c.nkc = (int)((c.d.K + KC - 1) / KC);
+}
+template <bool GROUPED>
+__device__ __forceinline__ void cursor_next(Cursor& c, const Table<GROUPED>& tb) {
+  if (++c.kc < c.nkc) return;
+  ++c.item;
+  cursor_load(c, tb);
+}
 
-  uint4 q[RB][4], p[RB];
-  auto load_w = [&](int it, uint4 (&qq)[RB][4], uint4 (&pp)[RB]) {
-    const bool v = 4 * it + qg < gpr;
-#pragma unroll
-    for (int r = 0; r < RB; ++r) {
-      const uint32_t o = v ? oq[r] + 256u * it : kBufOob;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) qq[r][j] = buf_load16(rq, o + 16u * j);
-      pp[r] = buf_load16(rp, v ? op[r] + 64u * it : kBufOob);
-    }
-  };
+template <int NPX, bool GROUPED>
+__global__ __launch_bounds__(64 * WAVES) void gemv_kernel(const plz_gemv_desc* __restrict__ descs,
+                                                          int n_desc, plz_gemv_desc single,
+                                                          int M) {
+  extern __shared__ uint4 smem[];
+  lds_u8* lds = (lds_u8*)smem;
+  constexpr int NS = ring<NPX>();
+  const Table<GROUPED> tb{descs, n_desc, single};
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+  const int nl = lane & 15, q = lane >> 4;
 
-  f32x4 acc[RB];
-#pragma unroll
-  for (int r = 0; r < RB; ++r) acc[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // this workgroup's items: those whose start cost lies in [wid*T/G, (wid+1)*T/G)
+  const int64_t T = tb.total_cost(), G = gridDim.x, wid = blockIdx.x;
+  Cursor pc, cc;
+  pc.item = cc.item = tb.item_at_cost(wid * T / G);
+  pc.end = cc.end = tb.item_at_cost((wid + 1) * T / G);
+  cursor_load(pc, tb);
+  cursor_load(cc, tb);
 
-  stage_issue(0);
-  if (has_rows) load_w(0, q, p);
-  stage_commit(0);
-  lds_barrier();
-  for (int it = 0; it < iters; ++it) {
-    const int buf = it & 1;
-    const bool more = it + 1 < iters;
-    uint4 qn[RB][4], pn[RB];
-    if (more) {
-      stage_issue(it + 1);
-      if (has_rows) load_w(it + 1, qn, pn);
-    }
-    if (has_rows) {
-      PalLut t[RB];
+  // Copies of the producer's stage into ring slot `slot` (out-of-range lanes write zeros;
+  // a stage past the workgroup's last item is all zeros and keeps the copy count uniform).
+  // Per item, each lane's byte offsets without the k term are computed once; rows past N and
+  // tokens past M fall outside the buffer ranges.
+  const int wrow0 = lane >> 2, wrow1 = 16 + (lane >> 2);  // rows of this lane's 2 packed copies
+  const int wch0 = (lane & 3) ^ w_swz(wrow0), wch1 = (lane & 3) ^ w_swz(wrow1);
+  static_assert(KC == kPalGroup, "one palette group per stage");
+  uint32_t wbase0 = 0, wbase1 = 0, mbase[NPX];
+  BufRsrc rq = make_rsrc(nullptr, 0), rp = rq, rx = rq;
+  int64_t p_item = -1;
+  auto issue = [&](int slot) {
+    lds_u8* st = lds + slot * stage_bytes<NPX>();
+    const bool live = pc.item < pc.end;
+    const int64_t N = pc.d.N, K = pc.d.K;
+    const int gpr = (int)(K / kPalGroup);
+    if (pc.item != p_item) {  // new item: descriptors and per-lane base offsets
+      p_item = pc.item;
+      rq = make_rsrc(pc.d.packed, live ? (uint32_t)(N * K / 4) : 0u);
+      rp = make_rsrc(pc.d.palette, live ? (uint32_t)(N * gpr * 16) : 0u);
+      rx = make_rsrc(pc.d.x, live ? (uint32_t)(M * K * 2) : 0u);
+      const uint32_t r0 = (uint32_t)pc.row0;
+      wbase0 = (r0 + 32 * wave + wrow0) * (uint32_t)(K / 4) + 16u * wch0;
+      wbase1 = (r0 + 32 * wave + wrow1) * (uint32_t)(K / 4) + 16u * wch1;
 #pragma unroll
-      for (int r = 0; r < RB; ++r)
-        t[r] = make_lut(__uint_as_float(p[r].x), __uint_as_float(p[r].y),
-                        __uint_as_float(p[r].z), __uint_as_float(p[r].w));
-#pragma unroll
-      for (int st = 0; st < 4; ++st) {
-        u32x4 xs[8];
-#pragma unroll
-        for (int f = 0; f < 8; ++f) xs[f] = xlds[buf * xbuf + (st * 8 + f) * 4 * M + xl];
-#pragma unroll
-        for (int r = 0; r < RB; ++r) {
-          const uint32_t qs[4] = {q[r][st].x, q[r][st].y, q[r][st].z, q[r][st].w};
-#pragma unroll
-          for (int w = 0; w < 4; ++w) {
-            u32x4 a0, a1;
-            dequant16_slots(qs[w], t[r], a0, a1);
-            acc[r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                __builtin_bit_cast(bf16x8, a0), __builtin_bit_cast(bf16x8, xs[2 * w]), acc[r],
-                0, 0, 0);
-            acc[r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                __builtin_bit_cast(bf16x8, a1), __builtin_bit_cast(bf16x8, xs[2 * w + 1]),
-                acc[r], 0, 0, 0);
-          }
+      for (int j = 0; j < NPX; ++j) {
+        const int g = WAVES * j + wave;
+        if (g < 2) {  // palettes of rows 64g + lane, group kc
+          mbase[j] = (r0 + 64 * g + lane) * (uint32_t)gpr * 16u;
+        } else {      // x tokens 2(g-2), 2(g-2)+1
+          const int m = 2 * (g - 2) + (lane >> 5);
+          mbase[j] = m < 16 ? ((uint32_t)m * (uint32_t)K + 8u * ((lane & 31) ^ x_swz(m))) * 2u
+                            : kBufOob;
         }
       }
     }
-    if (more) {
-      stage_commit(buf ^ 1);
+    // K is a multiple of 256 = KC, so every stage is whole
+    const uint32_t k0 = (uint32_t)pc.kc * KC;
+    dma16(rq, wbase0 + k0 / 4, st + wave * W_WAVE);
+    dma16(rq, wbase1 + k0 / 4, st + wave * W_WAVE + 1024);
+#pragma unroll
+    for (int j = 0; j < NPX; ++j) {
+      const int g = WAVES * j + wave;
+      lds_u8* dst = st + W_BYTES + g * 1024;
+      if (g < 2)
+        dma16(rp, mbase[j] + (uint32_t)pc.kc * 16u, dst);
+      else
+        dma16(rx, mbase[j] == kBufOob ? kBufOob : mbase[j] + k0 * 2u, dst);
+    }
+  };
+
+  const int mx = nl < M ? nl : M - 1;  // token whose x this fragment lane reads
+
+#pragma unroll
+  for (int s = 0; s < NS - 1; ++s) {
+    issue(s);
+    cursor_next(pc, tb);
+  }
+  int s = 0;
+  while (cc.item < cc.end) {  // one item (128 rows, all of K) per pass
+    f32x4 acc[RB];
+#pragma unroll
+    for (int r = 0; r < RB; ++r) acc[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int kc = 0; kc < cc.nkc; ++kc, ++s) {
+      wait_vmcnt<(2 + NPX) * (NS - 2)>();  // this lane's copies of stage s have landed
+      lds_barrier();                        // everyone's have; slot (s - 1) % NS is free
+      issue((s + NS - 1) % NS);
+      cursor_next(pc, tb);
+
+      const lds_u8* st = lds + (s % NS) * stage_bytes<NPX>();
+      const lds_u8* xs = st + W_BYTES + 2048 + mx * X_TOKEN;
+      // x fragments of this lane: k = 64q + 16t + 8h .. +7 (t = 0..3, h = 0..1), permuted
+      // into the dequantiser's slot order {k0, k4, k1, k5, k2, k6, k3, k7}
+      u32x4 xf[8];
+#pragma unroll
+      for (int f = 0; f < 8; ++f) {
+        const u32x4 v = *(const lds_u32x4*)(xs + (((8 * q + f) ^ x_swz(mx)) << 4));
+        xf[f] = u32x4{perm(v[2], v[0], 0x05040100u), perm(v[2], v[0], 0x07060302u),
+                      perm(v[3], v[1], 0x05040100u), perm(v[3], v[1], 0x07060302u)};
+      }
 #pragma unroll
       for (int r = 0; r < RB; ++r) {
+        const int row = 16 * r + nl;
+        const u32x4 wv =
+            *(const lds_u32x4*)(st + wave * W_WAVE + row * 64 + ((q ^ w_swz(row)) << 4));
+        const u32x4 pv = *(const lds_u32x4*)(st + W_BYTES + (32 * wave + row) * 16);
+        const PalLut t = make_lut(__uint_as_float(pv[0]), __uint_as_float(pv[1]),
+                                  __uint_as_float(pv[2]), __uint_as_float(pv[3]));
 #pragma unroll
-        for (int j = 0; j < 4; ++j) q[r][j] = qn[r][j];
-        p[r] = pn[r];
+        for (int w = 0; w < 4; ++w) {
+          u32x4 a0, a1;
+          dequant16_slots(wv[w], t, a0, a1);
+          acc[r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              __builtin_bit_cast(bf16x8, a0), __builtin_bit_cast(bf16x8, xf[2 * w]), acc[r], 0,
+              0, 0);
+          acc[r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              __builtin_bit_cast(bf16x8, a1), __builtin_bit_cast(bf16x8, xf[2 * w + 1]), acc[r],
+              0, 0, 0);
+        }
       }
     }
-    lds_barrier();
-  }
-  if (!has_rows) return;
-  // acc lane l: C[n = 4*(l/16) + e][m = l%16]
-  const int m = lane & 15;
-  if (m < M) {
+    // item done: acc lane l holds C[row 4q + e][token nl]
+    if (nl < M) {
 #pragma unroll
-    for (int r = 0; r < RB; ++r) {
+      for (int r = 0; r < RB; ++r)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int64_t n = row0 + 16 * r + 4 * (lane >> 4) + e;
-        if (n < N) d.y[(int64_t)m * N + n] = (uint16_t)f2bf(acc[r][e]);
-      }
+        for (int e = 0; e < 4; ++e) {
+          const int64_t n = cc.row0 + 32 * wave + 16 * r + 4 * q + e;
+          if (n < cc.d.N) cc.d.y[(int64_t)nl * cc.d.N + n] = (uint16_t)f2bf(acc[r][e]);
+        }
     }
+    ++cc.item;
+    cursor_load(cc, tb);
   }
+  __builtin_amdgcn_s_waitcnt(0);  // drain the trailing (empty) copies before the wave ends
 }
 
+static int cu_count() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cache[dev] == 0) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        v <= 0)
+      v = 256;
+    cache[dev] = v;
+  }
+  return cache[dev];
+}
+
+template <int NPX, bool GROUPED>
+static int launch_nx(int64_t items, hipStream_t st, const plz_gemv_desc* descs, int n,
+                     plz_gemv_desc single, int M, const char* what) {
+  auto kern = gemv_kernel<NPX, GROUPED>;
+  static bool attr = false;
+  if (!attr) {
+    const hipError_t e = hipFuncSetAttribute((const void*)kern,
+                                             hipFuncAttributeMaxDynamicSharedMemorySize,
+                                             lds_bytes<NPX>());
+    if (e != hipSuccess) {
+      set_error("%s: cannot reserve %d bytes of LDS: %s", what, lds_bytes<NPX>(),
+                hipGetErrorString(e));
+      return PLZ_EHIP;
+    }
+    attr = true;
+  }
+  const int64_t slots = wgs_per_cu<NPX>() * (int64_t)cu_count();
+  const int64_t g = items < slots ? items : slots;
+  hipLaunchKernelGGL(kern, dim3((unsigned)g), dim3(64 * WAVES), lds_bytes<NPX>(), st, descs, n,
+                     single, M);
+  return check_launch(what);
+}
 template <bool GROUPED>
-static void launch_gemv(int M, dim3 grid, hipStream_t st, const plz_gemv_desc* descs, int n,
-                        plz_gemv_desc single) {
-  hipLaunchKernelGGL((gemv_kernel<kGemvRb, GROUPED>), grid, dim3(256),
-                     2 * kXFragBytesPerToken * M, st, descs, n, single, M);
+static int launch(int64_t items, hipStream_t st, const plz_gemv_desc* descs, int n,
+                  plz_gemv_desc single, int M, const char* what) {
+  switch (npx_for(M)) {
+    case 1: return launch_nx<1, GROUPED>(items, st, descs, n, single, M, what);
+    case 2: return launch_nx<2, GROUPED>(items, st, descs, n, single, M, what);
+    default: return launch_nx<3, GROUPED>(items, st, descs, n, single, M, what);
+  }
 }
 
 static int check_desc(const plz_gemv_desc& d, int i) {
@@ -235,16 +346,18 @@ static int check_desc(const plz_gemv_desc& d, int i) {
   return PLZ_OK;
 }
 
+}  // namespace gv
 }  // namespace plz
 
 using namespace plz;
+using namespace plz::gv;
 
 extern "C" {
 
 int plz_lut_gemv(const uint16_t* x, const int32_t* packed, const float* palette, uint16_t* y,
                  int64_t M, int64_t N, int64_t K, void* stream) {
   PLZ_REQUIRE(M >= 1 && M <= 16, "plz_lut_gemv: M (%lld) must be in [1, 16]", (long long)M);
-  plz_gemv_desc d = {x, packed, palette, y, N, K, 0};
+  plz_gemv_desc d = {x, packed, palette, y, N, K, 0, 0};
   int rc = check_desc(d, 0);
   if (rc) return rc;
   if (N == 0) return PLZ_OK;
@@ -252,9 +365,8 @@ int plz_lut_gemv(const uint16_t* x, const int32_t* packed, const float* palette,
     hipMemsetAsync(y, 0, (size_t)M * N * 2, (hipStream_t)stream);
     return check_launch("plz_lut_gemv");
   }
-  const int64_t blocks = (N + kGemvRows - 1) / kGemvRows;
-  launch_gemv<false>((int)M, dim3((unsigned)blocks), (hipStream_t)stream, nullptr, 0, d);
-  return check_launch("plz_lut_gemv");
+  const int64_t items = (N + ROWS - 1) / ROWS;
+  return launch<false>(items, (hipStream_t)stream, nullptr, 1, d, (int)M, "plz_lut_gemv");
 }
 
 int64_t plz_gemv_plan(plz_gemv_desc* descs, int n, int M) {
@@ -262,14 +374,21 @@ int64_t plz_gemv_plan(plz_gemv_desc* descs, int n, int M) {
     set_error("plz_gemv_plan: need n >= 0, non-null descriptors and M in [1, 16]");
     return -PLZ_EINVAL;
   }
-  int64_t total = 0;
+  int64_t items = 0, cost = 0;
   for (int i = 0; i < n; ++i) {
     int rc = check_desc(descs[i], i);
     if (rc) return -rc;
-    descs[i].block_begin = total;
-    if (descs[i].K > 0) total += (descs[i].N + kGemvRows - 1) / kGemvRows;
+    if (descs[i].N > 0 && descs[i].K == 0) {
+      set_error("plz_gemv_plan: descriptor %d has K = 0", i);
+      return -PLZ_EINVAL;
+    }
+    descs[i].block_begin = items;
+    descs[i].cost_begin = cost;
+    const int64_t it = descs[i].K > 0 ? (descs[i].N + ROWS - 1) / ROWS : 0;
+    items += it;
+    cost += it * descs[i].K;
   }
-  return total;
+  return items;
 }
 
 int plz_lut_gemv_grouped(const plz_gemv_desc* descs_device, int n, int64_t total_blocks, int M,
@@ -279,8 +398,8 @@ int plz_lut_gemv_grouped(const plz_gemv_desc* descs_device, int n, int64_t total
   if (n == 0 || total_blocks == 0) return PLZ_OK;
   PLZ_REQUIRE(descs_device, "plz_lut_gemv_grouped: null descriptor table");
   plz_gemv_desc dummy = {};
-  launch_gemv<true>(M, dim3((unsigned)total_blocks), (hipStream_t)stream, descs_device, n, dummy);
-  return check_launch("plz_lut_gemv_grouped");
+  return launch<true>(total_blocks, (hipStream_t)stream, descs_device, n, dummy, M,
+                      "plz_lut_gemv_grouped");
 }
 
 }  // extern "C"

@@ -22,7 +22,7 @@ i32, i64, u32, u64, f32, sz = C.c_int, C.c_int64, C.c_uint32, C.c_uint64, C.c_fl
 
 class GemvDesc(C.Structure):
     _fields_ = [("x", p), ("packed", p), ("palette", p), ("y", p), ("N", i64), ("K", i64),
-                ("block_begin", i64)]
+                ("block_begin", i64), ("cost_begin", i64)]
 
 
 # name -> (restype, argtypes); kept in the order of include/palettize_hip.h

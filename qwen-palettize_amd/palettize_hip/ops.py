@@ -326,7 +326,7 @@ class GemvGroup:
             y = torch.empty((self.M, N), dtype=torch.bfloat16, device=self.device)
             self.outputs.append(y)
             descs[i] = _lib.GemvDesc(x.data_ptr(), packed.data_ptr(), palette.data_ptr(),
-                                     y.data_ptr(), N, K, 0)
+                                     y.data_ptr(), N, K, 0, 0)
         self._keep = items
         total = _lib.lib().plz_gemv_plan(descs, len(items), self.M)
         if total < 0:

@@ -157,6 +157,46 @@ def test_gemv(dev, M, N, K):
     assert_close(f32(y), want, what=f"gemv M={M}")
 
 
+@pytest.mark.parametrize("M,N,K", [(5, 264, 256), (13, 8, 768), (9, 136, 1280), (16, 2560, 9728)])
+def test_gemv_ragged(dev, M, N, K):
+    """Token counts of every LDS x-slice size, K ending mid-stage, N not a multiple of the
+    128-row work item."""
+    idx, pal = make_weight(N, K, seed=M * 7 + K)
+    x = randn_bf16(M, K, seed=M + 1)
+    y = ops.lut_gemv(x.to(dev), _packed(idx, dev), pal.to(dev))
+    want = O.lut_linear_fwd(f32(x), O.dequant(idx.numpy(), pal.numpy()))
+    assert_close(f32(y), want, what=f"gemv M={M} N={N} K={K}")
+
+
+@pytest.mark.parametrize("M", [1, 16])
+def test_gemv_grouped_many_linears(dev, M):
+    """A grouped launch over 3 x 7 Qwen-4B shapes plus empty linears: every output equals the
+    single-linear launch bit for bit, and sampled ones match the oracle."""
+    shapes = [(4096, 2560), (1024, 2560), (1024, 2560), (2560, 4096), (9728, 2560),
+              (9728, 2560), (2560, 9728)]
+    items, idxs = [], []
+    for layer in range(3):
+        for i, (N, K) in enumerate(shapes):
+            idx, pal = make_weight(N, K, seed=1000 + 7 * layer + i)
+            x = randn_bf16(M, K, seed=2000 + 7 * layer + i)
+            items.append((x.to(dev), _packed(idx, dev), pal.to(dev)))
+            idxs.append((idx, pal, x))
+        items.append((randn_bf16(M, 256, seed=7).to(dev), torch.zeros(0, 16, dtype=torch.int32, device=dev),
+                      torch.zeros(0, 1, 4, device=dev)))
+        idxs.append(None)
+    grp = ops.GemvGroup(items)
+    outs = grp.run()
+    for j, ((x, p, pl), y) in enumerate(zip(items, outs)):
+        if idxs[j] is None:
+            assert y.shape[1] == 0
+            continue
+        assert torch.equal(y, ops.lut_gemv(x, p, pl)), f"linear {j}"
+        if j % 5 == 0:
+            idx, pal, xc = idxs[j]
+            want = O.lut_linear_fwd(f32(xc), O.dequant(idx.numpy(), pal.numpy()))
+            assert_close(f32(y), want, what=f"grouped gemv linear {j}")
+
+
 def test_gemv_grouped_matches_single(dev):
     shapes = [(4096, 2560), (1024, 2560), (2560, 4096), (264, 512), (9728, 2560)]
     M = 4
