@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define PLZ_ABI_VERSION 2
+#define PLZ_ABI_VERSION 3
 
 /* status codes */
 #define PLZ_OK 0
@@ -168,6 +168,8 @@ typedef struct plz_gemv_desc {
   int64_t N, K;
   int64_t block_begin;    /* filled by plz_gemv_plan: first 128-row work item of this linear */
   int64_t cost_begin;     /* filled by plz_gemv_plan: sum of K over the items before it */
+  const float* palette_items; /* optional (may be NULL): the palettes repacked by
+                                 plz_gemv_pack_palettes, read instead of `palette` */
 } plz_gemv_desc;
 
 /* y[M,N] = x[M,K] W^T for 1 <= M <= 16 (bandwidth-bound; one pass over the packed weights).
@@ -175,6 +177,13 @@ typedef struct plz_gemv_desc {
  * a 64-row tile at M = 1. */
 int plz_lut_gemv(const uint16_t* x, const int32_t* packed, const float* palette, uint16_t* y,
                  int64_t M, int64_t N, int64_t K, void* stream);
+/* Decode weight layout (one-time repack, e.g. at model load): the fp32 palettes [N, K/256, 4]
+ * regrouped as [ceil(N/128)][K/256][128][4] (rows past N zero), so that the GEMV reads each
+ * stage's palettes as one contiguous 2 KB block instead of 128 scattered 16-byte pieces.
+ * Same bytes per weight as the native layout. */
+size_t plz_gemv_palette_items_bytes(int64_t N, int64_t K);
+int plz_gemv_pack_palettes(const float* palette, float* palette_items, int64_t N, int64_t K,
+                           void* stream);
 /* Fills block_begin and cost_begin of n host descriptors and returns the total number of
  * 128-row work items (or a negative status). A descriptor with N > 0 needs K > 0. */
 int64_t plz_gemv_plan(plz_gemv_desc* descs, int n, int M);

@@ -41,11 +41,14 @@ __device__ __forceinline__ void dequant16_slots(uint32_t q, PalLut t, u32x4& a, 
 typedef __attribute__((address_space(3))) uint8_t lds_u8;
 typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
 
-constexpr int WAVES = 4;
-constexpr int RB = 2;                         // MFMA row blocks of 16 per wave
+#ifndef PLZ_GV_WAVES
+#define PLZ_GV_WAVES 4
+#endif
+constexpr int WAVES = PLZ_GV_WAVES;           // waves per workgroup
+constexpr int RB = 8 / WAVES;                 // MFMA row blocks of 16 per wave
 constexpr int ROWS = WAVES * 16 * RB;         // rows per work item: 128
 constexpr int KC = 256;                       // k per stage: one palette group
-constexpr int W_WAVE = 16 * RB * (KC / 4);    // packed bytes per wave and stage: 2 KB
+constexpr int W_WAVE = 16 * RB * (KC / 4);    // packed bytes per wave and stage: RB KB
 constexpr int W_BYTES = WAVES * W_WAVE;       // 8 KB
 constexpr int X_TOKEN = KC * 2;               // x bytes per token and stage: 512 B
 // Besides the packed words (2 copies per wave), each stage copies the item's palettes (128 rows
@@ -62,7 +65,9 @@ constexpr int ring() { return PLZ_GV_NS; }
 template <int NPX>
 constexpr int lds_bytes() { return ring<NPX>() * stage_bytes<NPX>(); }
 template <int NPX>
-constexpr int wgs_per_cu() { return 160 * 1024 / lds_bytes<NPX>() < 4 ? 160 * 1024 / lds_bytes<NPX>() : 4; }
+constexpr int wgs_per_cu() {
+  return 160 * 1024 / lds_bytes<NPX>() < 16 / WAVES ? 160 * 1024 / lds_bytes<NPX>() : 16 / WAVES;
+}
 __host__ __device__ constexpr int npx_for(int M) { return (2 + (M + 1) / 2 + WAVES - 1) / WAVES; }
 
 // swizzles (16-byte chunk index XOR): packed rows of 64 B (4 chunks), x rows of 512 B (32 chunks)
@@ -174,10 +179,10 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(const plz_gemv_desc* _
   // a stage past the workgroup's last item is all zeros and keeps the copy count uniform).
   // Per item, each lane's byte offsets without the k term are computed once; rows past N and
   // tokens past M fall outside the buffer ranges.
-  const int wrow0 = lane >> 2, wrow1 = 16 + (lane >> 2);  // rows of this lane's 2 packed copies
-  const int wch0 = (lane & 3) ^ w_swz(wrow0), wch1 = (lane & 3) ^ w_swz(wrow1);
+  // packed copy i of this lane: row 16i + lane/4 of the wave's rows, 16-byte chunk lane%4
+  const int wrow = lane >> 2;
   static_assert(KC == kPalGroup, "one palette group per stage");
-  uint32_t wbase0 = 0, wbase1 = 0, mbase[NPX];
+  uint32_t wbase[RB], mbase[NPX], pstride = 16u;
   BufRsrc rq = make_rsrc(nullptr, 0), rp = rq, rx = rq;
   int64_t p_item = -1;
   auto issue = [&](int slot) {
@@ -188,16 +193,25 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(const plz_gemv_desc* _
     if (pc.item != p_item) {  // new item: descriptors and per-lane base offsets
       p_item = pc.item;
       rq = make_rsrc(pc.d.packed, live ? (uint32_t)(N * K / 4) : 0u);
-      rp = make_rsrc(pc.d.palette, live ? (uint32_t)(N * gpr * 16) : 0u);
+      // palettes: native [N, K/256, 4] (16 B per row and stage, rows gpr*16 B apart) or
+      // prepacked [item][group][128 rows][4] (2 KB contiguous per stage)
+      const bool pre = pc.d.palette_items != nullptr;
+      const int64_t pbytes = pre ? (N + ROWS - 1) / ROWS * ROWS * gpr * 16 : N * gpr * 16;
+      rp = make_rsrc(pre ? (const void*)pc.d.palette_items : (const void*)pc.d.palette,
+                     live ? (uint32_t)pbytes : 0u);
+      pstride = pre ? (uint32_t)(ROWS * 16) : 16u;
       rx = make_rsrc(pc.d.x, live ? (uint32_t)(M * K * 2) : 0u);
       const uint32_t r0 = (uint32_t)pc.row0;
-      wbase0 = (r0 + 32 * wave + wrow0) * (uint32_t)(K / 4) + 16u * wch0;
-      wbase1 = (r0 + 32 * wave + wrow1) * (uint32_t)(K / 4) + 16u * wch1;
+#pragma unroll
+      for (int i = 0; i < RB; ++i)
+        wbase[i] = (r0 + 16 * RB * wave + 16 * i + wrow) * (uint32_t)(K / 4) +
+                   16u * ((lane & 3) ^ w_swz(16 * i + wrow));
 #pragma unroll
       for (int j = 0; j < NPX; ++j) {
         const int g = WAVES * j + wave;
         if (g < 2) {  // palettes of rows 64g + lane, group kc
-          mbase[j] = (r0 + 64 * g + lane) * (uint32_t)gpr * 16u;
+          mbase[j] = pre ? (r0 * (uint32_t)gpr + 64 * g + lane) * 16u
+                         : (r0 + 64 * g + lane) * (uint32_t)gpr * 16u;
         } else {      // x tokens 2(g-2), 2(g-2)+1
           const int m = 2 * (g - 2) + (lane >> 5);
           mbase[j] = m < 16 ? ((uint32_t)m * (uint32_t)K + 8u * ((lane & 31) ^ x_swz(m))) * 2u
@@ -207,14 +221,14 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(const plz_gemv_desc* _
     }
     // K is a multiple of 256 = KC, so every stage is whole
     const uint32_t k0 = (uint32_t)pc.kc * KC;
-    dma16(rq, wbase0 + k0 / 4, st + wave * W_WAVE);
-    dma16(rq, wbase1 + k0 / 4, st + wave * W_WAVE + 1024);
+#pragma unroll
+    for (int i = 0; i < RB; ++i) dma16(rq, wbase[i] + k0 / 4, st + wave * W_WAVE + i * 1024);
 #pragma unroll
     for (int j = 0; j < NPX; ++j) {
       const int g = WAVES * j + wave;
       lds_u8* dst = st + W_BYTES + g * 1024;
       if (g < 2)
-        dma16(rp, mbase[j] + (uint32_t)pc.kc * 16u, dst);
+        dma16(rp, mbase[j] + (uint32_t)pc.kc * pstride, dst);
       else
         dma16(rx, mbase[j] == kBufOob ? kBufOob : mbase[j] + k0 * 2u, dst);
     }
@@ -233,7 +247,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(const plz_gemv_desc* _
 #pragma unroll
     for (int r = 0; r < RB; ++r) acc[r] = f32x4{0.f, 0.f, 0.f, 0.f};
     for (int kc = 0; kc < cc.nkc; ++kc, ++s) {
-      wait_vmcnt<(2 + NPX) * (NS - 2)>();  // this lane's copies of stage s have landed
+      wait_vmcnt<(RB + NPX) * (NS - 2)>();  // this lane's copies of stage s have landed
       lds_barrier();                        // everyone's have; slot (s - 1) % NS is free
       issue((s + NS - 1) % NS);
       cursor_next(pc, tb);
@@ -254,7 +268,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(const plz_gemv_desc* _
         const int row = 16 * r + nl;
         const u32x4 wv =
             *(const lds_u32x4*)(st + wave * W_WAVE + row * 64 + ((q ^ w_swz(row)) << 4));
-        const u32x4 pv = *(const lds_u32x4*)(st + W_BYTES + (32 * wave + row) * 16);
+        const u32x4 pv = *(const lds_u32x4*)(st + W_BYTES + (16 * RB * wave + row) * 16);
         const PalLut t = make_lut(__uint_as_float(pv[0]), __uint_as_float(pv[1]),
                                   __uint_as_float(pv[2]), __uint_as_float(pv[3]));
 #pragma unroll
@@ -276,7 +290,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(const plz_gemv_desc* _
       for (int r = 0; r < RB; ++r)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const int64_t n = cc.row0 + 32 * wave + 16 * r + 4 * q + e;
+          const int64_t n = cc.row0 + 16 * RB * wave + 16 * r + 4 * q + e;
           if (n < cc.d.N) cc.d.y[(int64_t)nl * cc.d.N + n] = (uint16_t)f2bf(acc[r][e]);
         }
     }
@@ -328,8 +342,21 @@ static int launch(int64_t items, hipStream_t st, const plz_gemv_desc* descs, int
   switch (npx_for(M)) {
     case 1: return launch_nx<1, GROUPED>(items, st, descs, n, single, M, what);
     case 2: return launch_nx<2, GROUPED>(items, st, descs, n, single, M, what);
-    default: return launch_nx<3, GROUPED>(items, st, descs, n, single, M, what);
+    case 3: return launch_nx<3, GROUPED>(items, st, descs, n, single, M, what);
+    case 4: return launch_nx<4, GROUPED>(items, st, descs, n, single, M, what);
+    default: return launch_nx<5, GROUPED>(items, st, descs, n, single, M, what);
   }
+}
+
+// palette [N, G, 4] -> [ceil(N/ROWS)][G][ROWS][4] (rows past N zero): one float4 per thread
+__global__ void pack_palettes_kernel(const float4* __restrict__ pal, float4* __restrict__ out,
+                                     int64_t N, int64_t G) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t items = (N + ROWS - 1) / ROWS;
+  if (t >= items * G * ROWS) return;
+  const int64_t row = t % ROWS, g = (t / ROWS) % G, item = t / (ROWS * G);
+  const int64_t n = item * ROWS + row;
+  out[t] = n < N ? pal[n * G + g] : make_float4(0.f, 0.f, 0.f, 0.f);
 }
 
 static int check_desc(const plz_gemv_desc& d, int i) {
@@ -341,8 +368,11 @@ static int check_desc(const plz_gemv_desc& d, int i) {
   PLZ_REQUIRE(d.N * d.K / 4 < (int64_t)kBufOob && d.N * (d.K / 256) * 16 < (int64_t)kBufOob &&
                   16 * d.K * 2 < (int64_t)kBufOob,
               "plz_gemv: descriptor %d is too large (packed or palette above 2 GiB)", i);
-  PLZ_REQUIRE((((uintptr_t)d.x | (uintptr_t)d.packed | (uintptr_t)d.palette) & 15) == 0,
-              "plz_gemv: descriptor %d: x, packed and palette must be 16-byte aligned", i);
+  PLZ_REQUIRE((((uintptr_t)d.x | (uintptr_t)d.packed | (uintptr_t)d.palette |
+                 (uintptr_t)d.palette_items) & 15) == 0,
+              "plz_gemv: descriptor %d: x, packed and palettes must be 16-byte aligned", i);
+  PLZ_REQUIRE((d.N + ROWS - 1) / ROWS * ROWS * (d.K / 256) * 16 < (int64_t)kBufOob,
+              "plz_gemv: descriptor %d: prepacked palettes above 2 GiB", i);
   return PLZ_OK;
 }
 
@@ -357,7 +387,7 @@ extern "C" {
 int plz_lut_gemv(const uint16_t* x, const int32_t* packed, const float* palette, uint16_t* y,
                  int64_t M, int64_t N, int64_t K, void* stream) {
   PLZ_REQUIRE(M >= 1 && M <= 16, "plz_lut_gemv: M (%lld) must be in [1, 16]", (long long)M);
-  plz_gemv_desc d = {x, packed, palette, y, N, K, 0, 0};
+  plz_gemv_desc d = {x, packed, palette, y, N, K, 0, 0, nullptr};
   int rc = check_desc(d, 0);
   if (rc) return rc;
   if (N == 0) return PLZ_OK;
@@ -367,6 +397,25 @@ int plz_lut_gemv(const uint16_t* x, const int32_t* packed, const float* palette,
   }
   const int64_t items = (N + ROWS - 1) / ROWS;
   return launch<false>(items, (hipStream_t)stream, nullptr, 1, d, (int)M, "plz_lut_gemv");
+}
+
+size_t plz_gemv_palette_items_bytes(int64_t N, int64_t K) {
+  if (N <= 0 || K <= 0) return 0;
+  return (size_t)((N + ROWS - 1) / ROWS) * ROWS * (K / kPalGroup) * 16;
+}
+
+int plz_gemv_pack_palettes(const float* palette, float* palette_items, int64_t N, int64_t K,
+                           void* stream) {
+  PLZ_REQUIRE(N >= 0 && K >= 0 && K % kPalGroup == 0,
+              "plz_gemv_pack_palettes: need N, K >= 0 and K a multiple of 256");
+  if (N == 0 || K == 0) return PLZ_OK;
+  PLZ_REQUIRE(palette && palette_items && (((uintptr_t)palette | (uintptr_t)palette_items) & 15) == 0,
+              "plz_gemv_pack_palettes: palette and palette_items must be non-null, 16-byte aligned");
+  const int64_t G = K / kPalGroup, total = (N + ROWS - 1) / ROWS * G * ROWS;
+  hipLaunchKernelGGL(pack_palettes_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, reinterpret_cast<const float4*>(palette),
+                     reinterpret_cast<float4*>(palette_items), N, G);
+  return check_launch("plz_gemv_pack_palettes");
 }
 
 int64_t plz_gemv_plan(plz_gemv_desc* descs, int n, int M) {

@@ -22,7 +22,7 @@ i32, i64, u32, u64, f32, sz = C.c_int, C.c_int64, C.c_uint32, C.c_uint64, C.c_fl
 
 class GemvDesc(C.Structure):
     _fields_ = [("x", p), ("packed", p), ("palette", p), ("y", p), ("N", i64), ("K", i64),
-                ("block_begin", i64), ("cost_begin", i64)]
+                ("block_begin", i64), ("cost_begin", i64), ("palette_items", p)]
 
 
 # name -> (restype, argtypes); kept in the order of include/palettize_hip.h
@@ -49,6 +49,8 @@ SIGNATURES: dict[str, tuple] = {
     "plz_lora_weight_grads_workspace": (sz, [i64, i64, i64, i32]),
     "plz_lora_weight_grads": (i32, [p, p, p, p, f32, p, p, i32, p, sz, i64, i64, i64, i32, p]),
     "plz_lut_gemv": (i32, [p, p, p, p, i64, i64, i64, p]),
+    "plz_gemv_palette_items_bytes": (sz, [i64, i64]),
+    "plz_gemv_pack_palettes": (i32, [p, p, i64, i64, p]),
     "plz_gemv_plan": (i64, [C.POINTER(GemvDesc), i32, i32]),
     "plz_lut_gemv_grouped": (i32, [p, i32, i64, i32, p]),
     "plz_rmsnorm_fwd": (i32, [p, p, p, p, i64, i64, f32, p]),

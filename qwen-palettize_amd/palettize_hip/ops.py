@@ -304,19 +304,32 @@ def lut_gemv(x, packed, palette):
     return y
 
 
+def gemv_pack_palettes(palette):
+    """One-time decode layout of a palette [N, K/256, 4]: [ceil(N/128), K/256, 128, 4]."""
+    _need(palette, "palette", torch.float32, 3)
+    N, G = palette.shape[0], palette.shape[1]
+    nbytes = query("plz_gemv_palette_items_bytes", N, G * 256)
+    out = torch.empty(max(nbytes // 4, 1), dtype=torch.float32, device=palette.device)
+    call("plz_gemv_pack_palettes", _ptr(palette), _ptr(out), N, G * 256, _stream(palette))
+    return out
+
+
 class GemvGroup:
     """A fixed set of independent GEMVs (same M) run by one grouped launch.
 
     ``items`` is a list of (x [M,K] bf16, packed, palette); outputs are allocated once and
-    reused by every ``run()``. The descriptor table lives in device memory.
+    reused by every ``run()``. The descriptor table lives in device memory. With
+    ``prepack=True`` (default) the palettes are repacked once into the decode layout
+    (plz_gemv_pack_palettes), which the kernel streams contiguously.
     """
 
-    def __init__(self, items):
+    def __init__(self, items, prepack=True):
         if not items:
             raise ValueError("empty GEMV group")
         self.M = items[0][0].shape[0]
         self.device = items[0][0].device
         self.outputs = []
+        self._packed_palettes = []
         descs = (_lib.GemvDesc * len(items))()
         for i, (x, packed, palette) in enumerate(items):
             N, K = _wshape(packed, palette)
@@ -325,8 +338,11 @@ class GemvGroup:
                 raise ValueError(f"item {i}: x must be [{self.M}, {K}]")
             y = torch.empty((self.M, N), dtype=torch.bfloat16, device=self.device)
             self.outputs.append(y)
+            pre = gemv_pack_palettes(palette) if prepack and N > 0 and K > 0 else None
+            self._packed_palettes.append(pre)
             descs[i] = _lib.GemvDesc(x.data_ptr(), packed.data_ptr(), palette.data_ptr(),
-                                     y.data_ptr(), N, K, 0, 0)
+                                     y.data_ptr(), N, K, 0, 0,
+                                     pre.data_ptr() if pre is not None else None)
         self._keep = items
         total = _lib.lib().plz_gemv_plan(descs, len(items), self.M)
         if total < 0:

@@ -4,7 +4,7 @@ import pytest
 import torch
 
 import oracle as O
-from helpers import assert_close, f32, make_weight, randn_bf16
+from helpers import gen, assert_close, f32, make_weight, randn_bf16
 
 pytestmark = pytest.mark.gpu
 ops = pytest.importorskip("palettize_hip.ops")
@@ -195,6 +195,18 @@ def test_gemv_grouped_many_linears(dev, M):
             idx, pal, xc = idxs[j]
             want = O.lut_linear_fwd(f32(xc), O.dequant(idx.numpy(), pal.numpy()))
             assert_close(f32(y), want, what=f"grouped gemv linear {j}")
+
+
+def test_gemv_pack_palettes_layout(dev):
+    """Decode palette layout: [ceil(N/128)][K/256][128][4], rows past N zero."""
+    N, K = 300, 768
+    pal = torch.randn(N, K // 256, 4, generator=gen(3))
+    out = ops.gemv_pack_palettes(pal.to(dev)).cpu()
+    items = (N + 127) // 128
+    want = torch.zeros(items * 128, K // 256, 4)
+    want[:N] = pal
+    want = want.view(items, 128, K // 256, 4).permute(0, 2, 1, 3).reshape(-1)
+    assert torch.equal(out, want)
 
 
 def test_gemv_grouped_matches_single(dev):
