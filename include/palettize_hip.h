@@ -192,6 +192,26 @@ int64_t plz_gemv_plan(plz_gemv_desc* descs, int n, int M);
 int plz_lut_gemv_grouped(const plz_gemv_desc* descs_device, int n, int64_t total_blocks, int M,
                          void* stream);
 
+/* ---- on-disk format converters ---------------------------------------------------------
+ * .idx2 = the (K, N) index matrix (W^T) flattened row-major, 4 indices per byte, LSB first
+ * (palettize_core.py:31-47 pack_idx2 / pack_indices_transposed_2bit; read back by
+ * palettize_core.py:159-172 unpack_idx2 / load_indices); .lut_scalar = fp16 palettes (G, 4),
+ * one per 256 output rows (palettize_pytorch.py:150-159 write_lut_scalar). */
+/* .idx2 bytes (device) -> native packed [N, K/16]. N % 4 == 0, K % 16 == 0. Replaces
+ * load_indices (palettize_core.py:167-172) followed by pack_indices on the device. */
+int plz_idx2_to_packed(const uint8_t* idx2, int32_t* packed, int64_t N, int64_t K, void* stream);
+/* native packed [N, K/16] -> .idx2 bytes (the save path, train_qwen.py:826-835 with frozen
+ * indices; palettize_core.py:45-47). */
+int plz_packed_to_idx2(const int32_t* packed, uint8_t* idx2, int64_t N, int64_t K, void* stream);
+/* argmax over the 4 index-logit planes (4, K, N) (fp16 or bf16, logits_dtype) written as .idx2
+ * bytes; the first maximal plane wins, as torch.argmax (train_qwen.py:826-829 save_state). */
+int plz_logits_argmax_idx2(const uint16_t* logits, int logits_dtype, uint8_t* idx2, int64_t N,
+                           int64_t K, void* stream);
+/* .lut_scalar fp16 (ceil(N/group_size), 4) -> native fp32 palette [N, K/256, 4]
+ * (qwen_model.py:97-102: row n uses palette n / group_size for every k). */
+int plz_lut_to_palette(const uint16_t* lut, float* palette, int64_t N, int64_t K, int group_size,
+                       void* stream);
+
 /* ---- fused RMSNorm and SwiGLU ------------------------------------------------------------
  * The reference runs the HF Qwen3 modules unfused (Qwen3RMSNorm and Qwen3MLP, transformers
  * models/qwen3/modeling_qwen3.py:50-83, used by the decoder layers that qwen_model.py wraps). */

@@ -84,6 +84,25 @@ def unpack_native(packed) -> np.ndarray:
     return ((u >> shifts) & 3).astype(np.uint8).reshape(rows, words * 16)
 
 
+def idx2_to_native(data: bytes, N: int, K: int) -> np.ndarray:
+    """.idx2 bytes of the (K, N) index matrix (palettize_core.py:167-172 load_indices) ->
+    native packed int32 [N, K/16]."""
+    kn = unpack_idx2(data, N * K).reshape(K, N)
+    return pack_native(np.ascontiguousarray(kn.T))
+
+
+def native_to_idx2(packed) -> bytes:
+    """Native packed [N, K/16] -> .idx2 bytes of its (K, N) transpose (palettize_core.py:45-47
+    pack_indices_transposed_2bit)."""
+    return pack_idx2(np.ascontiguousarray(unpack_native(packed).T))
+
+
+def logits_argmax(logits) -> np.ndarray:
+    """(4, K, N) index logits -> (K, N) argmax over the planes, first maximum winning
+    (torch.argmax; train_qwen.py:826-829)."""
+    return np.argmax(np.asarray(logits, dtype=np.float32), axis=0).astype(np.uint8)
+
+
 # --------------------------------------------------------------------------------------
 # dequantisation (qwen_model.py:97-102, :185-186) and layout maps
 # --------------------------------------------------------------------------------------

@@ -53,6 +53,10 @@ SIGNATURES: dict[str, tuple] = {
     "plz_gemv_pack_palettes": (i32, [p, p, i64, i64, p]),
     "plz_gemv_plan": (i64, [C.POINTER(GemvDesc), i32, i32]),
     "plz_lut_gemv_grouped": (i32, [p, i32, i64, i32, p]),
+    "plz_idx2_to_packed": (i32, [p, p, i64, i64, p]),
+    "plz_packed_to_idx2": (i32, [p, p, i64, i64, p]),
+    "plz_logits_argmax_idx2": (i32, [p, i32, p, i64, i64, p]),
+    "plz_lut_to_palette": (i32, [p, p, i64, i64, i32, p]),
     "plz_rmsnorm_fwd": (i32, [p, p, p, p, i64, i64, f32, p]),
     "plz_rmsnorm_bwd_workspace": (sz, [i64, i64]),
     "plz_rmsnorm_bwd": (i32, [p, p, p, p, p, p, p, sz, i64, i64, p]),
