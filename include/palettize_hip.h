@@ -128,6 +128,29 @@ int plz_soft_build_w(const uint16_t* logits, int logits_dtype, const float* nois
                      const float* palette, float tau, int mode, uint16_t* w, uint16_t* w_soft,
                      int64_t N, int64_t K, void* stream);
 
+/* Batched build W: the linears of a layer (or of several) in one launch, each with its own
+ * logits, noise, palette and outputs; the same tau and mode for all. Replaces
+ * fused_compute_P_W_batched (fused_lut_kernel.cu:2071-2211, fused_lut_linear_cuda.py:1016-1075),
+ * which decorrelates the layers' in-kernel noise by a per-layer seed; here each descriptor
+ * brings its own noise. */
+typedef struct plz_build_w_desc {
+  const uint16_t* logits;  /* [N, K, 4] bf16 or fp16 */
+  const float* noise;      /* [N, K, 4] fp32 */
+  const float* palette;    /* [N, K/256, 4] fp32 */
+  uint16_t* w;             /* [N, K] bf16 */
+  uint16_t* w_soft;        /* [N, K] bf16 or NULL */
+  int64_t N, K;
+  int32_t logits_dtype;    /* PLZ_DT_BF16 or PLZ_DT_FP16 */
+  int32_t reserved;
+  int64_t block_begin;     /* filled by plz_build_w_plan */
+} plz_build_w_desc;
+/* Checks n host descriptors, fills block_begin and returns the launch's block count (or a
+ * negative status). */
+int64_t plz_build_w_plan(plz_build_w_desc* descs, int n);
+/* descs_device: a device copy of the planned descriptors. */
+int plz_soft_build_w_batched(const plz_build_w_desc* descs_device, int n, int64_t total_blocks,
+                             float tau, int mode, void* stream);
+
 /* Soft backward, fused in the epilogue of dW = grad_y^T x (dW never leaves the chip):
  *   grad_logits[n,k,c] = s * dW[n,k] P_c (pal_c - sum_d P_d pal_d)   (logits dtype)
  *   grad_palette[n,g,c] = sum_{k in g} dW[n,k] P_c                   (fp32)
@@ -211,6 +234,33 @@ int plz_logits_argmax_idx2(const uint16_t* logits, int logits_dtype, uint8_t* id
  * (qwen_model.py:97-102: row n uses palette n / group_size for every k). */
 int plz_lut_to_palette(const uint16_t* lut, float* palette, int64_t N, int64_t K, int group_size,
                        void* stream);
+
+/* ---- fused optimizer step ---------------------------------------------------------------
+ * Replaces FP32MasterOptimizer.step (train_qwen.py:154-221: bf16 grads -> fp32 masters,
+ * torch.optim.AdamW, copy back), the two-tier clip_grad_norm_ (:1303-1319) and the logits
+ * clamp to +-5 tau (:1343-1348) by two streaming passes over all parameters. */
+typedef struct plz_adamw_desc {
+  void* param;           /* bf16 or fp32 parameter */
+  const void* grad;      /* its gradient, same dtype */
+  float* master;         /* fp32 master (required for bf16 params; NULL: param is the master) */
+  float* exp_avg;        /* fp32 first moment */
+  float* exp_avg_sq;     /* fp32 second moment */
+  int64_t n;             /* elements */
+  int32_t dtype;         /* PLZ_DT_BF16 or PLZ_DT_FP32 */
+  int32_t clip_group;    /* 0 or 1: which clip_grad_norm_ group the gradient belongs to */
+  float lr, clamp_lo, clamp_hi, reserved;  /* clamp_lo/hi = -/+inf for no clamp */
+  int64_t block_begin;   /* filled by plz_adamw_plan */
+} plz_adamw_desc;
+/* Checks n host descriptors, fills block_begin, returns the block count (or -status). */
+int64_t plz_adamw_plan(plz_adamw_desc* descs, int n);
+size_t plz_adamw_workspace(int64_t total_blocks);
+/* One step (step = 1, 2, ...): gradients clipped per group to max_norm0 / max_norm1 (<= 0: no
+ * clipping), AdamW(beta1, beta2, eps, weight_decay) on the masters, clamp, params rewritten.
+ * norms_out (device, optional): the two groups' unclipped gradient norms. */
+int plz_adamw_step(const plz_adamw_desc* descs_device, int n, int64_t total_blocks,
+                   float max_norm0, float max_norm1, double beta1, double beta2, float eps,
+                   float weight_decay, int64_t step, float* norms_out, void* workspace,
+                   size_t workspace_bytes, void* stream);
 
 /* ---- fused RMSNorm and SwiGLU ------------------------------------------------------------
  * The reference runs the HF Qwen3 modules unfused (Qwen3RMSNorm and Qwen3MLP, transformers

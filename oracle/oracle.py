@@ -299,6 +299,31 @@ def soft_backward(x, gy, logits, noise, palette, tau: float, scale_by_inv_tau: b
 # --------------------------------------------------------------------------------------
 
 
+def adamw_step(masters, grads, ms, vs, lrs, clip_groups, max_norms, clamps, step: int,
+               betas=(0.9, 0.95), eps: float = 1e-8, weight_decay: float = 0.0):
+    """One step of the layer optimizer in fp64, updating the lists in place: per clip group
+    G, grads scaled by min(1, max_norm_G / (||grad_G|| + 1e-6)) (torch clip_grad_norm_,
+    train_qwen.py:1303-1319); torch.optim.AdamW's update on the fp32 masters
+    (train_qwen.py:154-221, 600); clamp to (lo, hi) (train_qwen.py:1343-1348).
+    Returns the two groups' unclipped gradient norms."""
+    b1, b2 = betas
+    sq = [0.0, 0.0]
+    for g, G in zip(grads, clip_groups):
+        sq[G] += float(np.sum(np.asarray(g, np.float64) ** 2))
+    norms = [np.sqrt(x) for x in sq]
+    coef = [min(1.0, mx / (nrm + 1e-6)) if mx > 0 else 1.0 for mx, nrm in zip(max_norms, norms)]
+    bc1, bc2 = 1.0 - b1 ** step, 1.0 - b2 ** step
+    for i in range(len(masters)):
+        g = np.asarray(grads[i], np.float64) * coef[clip_groups[i]]
+        p = masters[i] * (1.0 - lrs[i] * weight_decay)
+        ms[i] = ms[i] + (1.0 - b1) * (g - ms[i])
+        vs[i] = b2 * vs[i] + (1.0 - b2) * g * g
+        p = p - (lrs[i] / bc1) * ms[i] / (np.sqrt(vs[i]) / np.sqrt(bc2) + eps)
+        lo, hi = clamps[i]
+        masters[i] = np.clip(p, lo, hi)
+    return norms
+
+
 def lora_forward(x, lora_a, lora_b, scale: float) -> np.ndarray:
     """scale * (x A^T) B^T with A [r, K], B [N, r] (fp64)."""
     return scale * (np.asarray(x, np.float64) @ np.asarray(lora_a, np.float64).T) @ np.asarray(

@@ -1,0 +1,211 @@
+// Fused optimizer step of the layer training (train_qwen.py:154-221 FP32MasterOptimizer,
+// :1303-1319 two-tier gradient clipping, :1343-1348 logits clamp to +-5 tau):
+//
+//   per clip group G:  coef_G = min(1, max_norm_G / (||grad over G||_2 + 1e-6))
+//                      (torch.nn.utils.clip_grad_norm_)
+//   per element:       g = grad * coef_G
+//                      p = p * (1 - lr * wd)
+//                      m = m + (1 - b1) (g - m)                 (torch lerp form)
+//                      v = b2 v + (1 - b2) g^2
+//                      p = p - (lr / bc1) m / (sqrt(v) / sqrt(bc2) + eps)
+//                      p = clamp(p, lo, hi)
+//                      param = bf16(p) (bf16 parameters keep an fp32 master p)
+// which is torch.optim.AdamW's multi-tensor step (betas, eps, weight decay as given) on fp32
+// masters. Two kernels stream every parameter once each: the squared-norm partials, then the
+// update (the norms are finished on the device in between; no host synchronisation). HBM-bound:
+// a bf16 parameter with master moves 30 bytes per element (grad read twice, m/v/master read and
+// written, param written).
+#include <cmath>
+
+#include "plz_common.h"
+#include "palettize_hip.h"
+
+namespace plz {
+namespace opt {
+
+constexpr int kThreads = 256;
+constexpr int kEpt = 8;                       // elements per thread
+constexpr int kBlockElems = kThreads * kEpt;  // elements per block
+
+__device__ __forceinline__ int find_desc(const plz_adamw_desc* d, int n, int64_t b) {
+  int lo = 0, hi = n - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (d[mid].block_begin <= b) lo = mid; else hi = mid - 1;
+  }
+  return lo;
+}
+__device__ __forceinline__ float grad_at(const plz_adamw_desc& d, int64_t i) {
+  return d.dtype == PLZ_DT_BF16 ? bf2f(reinterpret_cast<const uint16_t*>(d.grad)[i])
+                                : reinterpret_cast<const float*>(d.grad)[i];
+}
+
+__device__ __forceinline__ float block_sum(float v, float* red) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  float s = 0.f;
+  if (threadIdx.x == 0)
+    for (int w = 0; w < kThreads / 64; ++w) s += red[w];
+  return s;  // valid in thread 0
+}
+
+// partial[b] = sum of squared (unclipped) gradients of block b; group[b] = its clip group
+__global__ __launch_bounds__(kThreads) void sumsq_kernel(const plz_adamw_desc* __restrict__ descs,
+                                                         int n_desc, float* __restrict__ partial,
+                                                         int* __restrict__ group) {
+  __shared__ float red[kThreads / 64];
+  const int64_t b = blockIdx.x;
+  const plz_adamw_desc d = descs[find_desc(descs, n_desc, b)];
+  const int64_t base = (b - d.block_begin) * kBlockElems;
+  float s = 0.f;
+#pragma unroll
+  for (int e = 0; e < kEpt; ++e) {
+    const int64_t i = base + (int64_t)e * kThreads + threadIdx.x;
+    if (i < d.n) {
+      const float g = grad_at(d, i);
+      s += g * g;
+    }
+  }
+  s = block_sum(s, red);
+  if (threadIdx.x == 0) {
+    partial[b] = s;
+    group[b] = d.clip_group;
+  }
+}
+
+// coef[G] = min(1, max_norm[G] / (sqrt(sum of group G's partials, in block order) + 1e-6))
+__global__ __launch_bounds__(kThreads) void clip_coef_kernel(const float* __restrict__ partial,
+                                                             const int* __restrict__ group,
+                                                             int64_t nblocks, float max0,
+                                                             float max1, float* __restrict__ coef) {
+  __shared__ float red[kThreads / 64];
+  const int G = blockIdx.x;
+  // fixed assignment of partials to threads and a fixed reduction tree: deterministic
+  float s = 0.f;
+  for (int64_t i = threadIdx.x; i < nblocks; i += kThreads)
+    if (group[i] == G) s += partial[i];
+  s = block_sum(s, red);
+  if (threadIdx.x == 0) {
+    const float mx = G == 0 ? max0 : max1;
+    const float c = mx / (sqrtf(s) + 1e-6f);
+    coef[G] = mx > 0.f ? fminf(c, 1.f) : 1.f;   // max_norm <= 0: no clipping
+    coef[2 + G] = sqrtf(s);                      // the norm itself (returned to the caller)
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void adamw_kernel(const plz_adamw_desc* __restrict__ descs,
+                                                         int n_desc, const float* __restrict__ coef,
+                                                         float beta1, float beta2, float eps,
+                                                         float weight_decay, float bc1,
+                                                         float bc2_sqrt) {
+  const int64_t b = blockIdx.x;
+  const plz_adamw_desc d = descs[find_desc(descs, n_desc, b)];
+  const int64_t base = (b - d.block_begin) * kBlockElems;
+  const float c = coef[d.clip_group];
+  const float step_size = d.lr / bc1;
+  const float decay = 1.f - d.lr * weight_decay;
+  float* p32 = d.master ? d.master : reinterpret_cast<float*>(d.param);
+#pragma unroll
+  for (int e = 0; e < kEpt; ++e) {
+    const int64_t i = base + (int64_t)e * kThreads + threadIdx.x;
+    if (i >= d.n) continue;
+    const float g = grad_at(d, i) * c;
+    float p = p32[i];
+    if (weight_decay != 0.f) p *= decay;
+    float m = d.exp_avg[i], v = d.exp_avg_sq[i];
+    m = m + (1.f - beta1) * (g - m);
+    v = v * beta2;
+    v = v + (1.f - beta2) * g * g;
+    const float denom = sqrtf(v) / bc2_sqrt + eps;
+    p = p - step_size * (m / denom);
+    p = fminf(fmaxf(p, d.clamp_lo), d.clamp_hi);
+    d.exp_avg[i] = m;
+    d.exp_avg_sq[i] = v;
+    p32[i] = p;
+    if (d.master && d.dtype == PLZ_DT_BF16) reinterpret_cast<uint16_t*>(d.param)[i] = (uint16_t)f2bf(p);
+    if (d.master && d.dtype == PLZ_DT_FP32) reinterpret_cast<float*>(d.param)[i] = p;
+  }
+}
+
+static unsigned grid_of(int64_t n) { return (unsigned)n; }
+
+}  // namespace opt
+}  // namespace plz
+
+using namespace plz;
+using namespace plz::opt;
+
+extern "C" {
+
+int64_t plz_adamw_plan(plz_adamw_desc* descs, int n) {
+  if (n < 0 || (n > 0 && !descs)) {
+    set_error("plz_adamw_plan: need n >= 0 and non-null descriptors");
+    return -PLZ_EINVAL;
+  }
+  int64_t total = 0;
+  for (int i = 0; i < n; ++i) {
+    const plz_adamw_desc& d = descs[i];
+    if (d.n < 0 || (d.dtype != PLZ_DT_BF16 && d.dtype != PLZ_DT_FP32) ||
+        (d.clip_group != 0 && d.clip_group != 1) || !(d.clamp_lo <= d.clamp_hi)) {
+      set_error("plz_adamw_plan: descriptor %d: bad size, dtype, clip group or clamp range", i);
+      return -PLZ_EINVAL;
+    }
+    if (d.n > 0 && (!d.param || !d.grad || !d.exp_avg || !d.exp_avg_sq ||
+                    (d.dtype == PLZ_DT_BF16 && !d.master))) {
+      set_error("plz_adamw_plan: descriptor %d: null pointer (bf16 parameters need a master)", i);
+      return -PLZ_EINVAL;
+    }
+    descs[i].block_begin = total;
+    total += (d.n + kBlockElems - 1) / kBlockElems;
+  }
+  return total;
+}
+
+size_t plz_adamw_workspace(int64_t total_blocks) {
+  if (total_blocks <= 0) return 64;
+  return ((size_t)total_blocks * 8 + 63) / 64 * 64 + 64;
+}
+
+int plz_adamw_step(const plz_adamw_desc* descs_device, int n, int64_t total_blocks,
+                   float max_norm0, float max_norm1, double beta1, double beta2, float eps,
+                   float weight_decay, int64_t step, float* norms_out, void* workspace,
+                   size_t workspace_bytes, void* stream) {
+  PLZ_REQUIRE(n >= 0 && total_blocks >= 0 && step >= 1, "plz_adamw_step: bad count or step");
+  PLZ_REQUIRE(beta1 >= 0.f && beta1 < 1.f && beta2 >= 0.f && beta2 < 1.f && eps > 0.f,
+              "plz_adamw_step: need 0 <= betas < 1 and eps > 0");
+  if (n == 0 || total_blocks == 0) return PLZ_OK;
+  PLZ_REQUIRE(descs_device, "plz_adamw_step: null descriptor table");
+  PLZ_REQUIRE(total_blocks < (1ll << 31), "plz_adamw_step: too many elements");
+  const size_t need = plz_adamw_workspace(total_blocks);
+  if (!workspace || workspace_bytes < need) {
+    set_error("plz_adamw_step: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+    return PLZ_EWORKSPACE;
+  }
+  hipStream_t s = (hipStream_t)stream;
+  float* partial = reinterpret_cast<float*>(workspace);
+  int* group = reinterpret_cast<int*>(partial + total_blocks);
+  float* coef = reinterpret_cast<float*>((char*)workspace + need - 64);
+  hipLaunchKernelGGL(sumsq_kernel, dim3(grid_of(total_blocks)), dim3(kThreads), 0, s, descs_device,
+                     n, partial, group);
+  int rc = check_launch("plz_adamw_step/sumsq");
+  if (rc) return rc;
+  hipLaunchKernelGGL(clip_coef_kernel, dim3(2), dim3(kThreads), 0, s, partial, group, total_blocks,
+                     max_norm0, max_norm1, coef);
+  if ((rc = check_launch("plz_adamw_step/coef"))) return rc;
+  // bias corrections in double on the host, as torch computes its Python-float scalars
+  const float bc1 = (float)(1.0 - std::pow(beta1, (double)step));
+  const float bc2_sqrt = (float)std::sqrt(1.0 - std::pow(beta2, (double)step));
+  hipLaunchKernelGGL(adamw_kernel, dim3(grid_of(total_blocks)), dim3(kThreads), 0, s, descs_device,
+                     n, coef, (float)beta1, (float)beta2, eps, weight_decay, bc1, bc2_sqrt);
+  if ((rc = check_launch("plz_adamw_step/update"))) return rc;
+  if (norms_out) {
+    hipMemcpyAsync(norms_out, coef + 2, 2 * sizeof(float), hipMemcpyDeviceToDevice, s);
+    return check_launch("plz_adamw_step/norms");
+  }
+  return PLZ_OK;
+}
+
+}  // extern "C"

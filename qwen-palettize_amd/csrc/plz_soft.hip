@@ -7,6 +7,7 @@
 // The forward weight W = W_hard is the straight-through estimator's value
 // (fused_lut_linear_cuda.py:906-910); W_soft is what the backward differentiates.
 #include "plz_common.h"
+#include "palettize_hip.h"
 
 namespace plz {
 
@@ -72,13 +73,12 @@ __global__ void lcg_gumbel_kernel(float* __restrict__ out, uint32_t seed, int64_
 
 // ---- build W -------------------------------------------------------------------------
 // One thread per 2 consecutive k of one row: 16 B of logits, 32 B of noise in; 4 B out.
-__global__ void build_w_kernel(const uint16_t* __restrict__ logits, int f16,
-                               const float* __restrict__ noise, const float* __restrict__ pal,
-                               float inv_tau, int mode, uint16_t* __restrict__ w,
-                               uint16_t* __restrict__ w_soft, int64_t N, int64_t K) {
-  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+__device__ __forceinline__ void build_w_pair(const uint16_t* __restrict__ logits, int f16,
+                                             const float* __restrict__ noise,
+                                             const float* __restrict__ pal, float inv_tau,
+                                             int mode, uint16_t* __restrict__ w,
+                                             uint16_t* __restrict__ w_soft, int64_t K, int64_t t) {
   const int64_t half = K / 2;
-  if (t >= N * half) return;
   const int64_t n = t / half, k = 2 * (t % half);
   const float4 p = *reinterpret_cast<const float4*>(pal + (n * (K / kPalGroup) + k / kPalGroup) * 4);
   const float pc[4] = {p.x, p.y, p.z, p.w};
@@ -125,6 +125,33 @@ __global__ void build_w_kernel(const uint16_t* __restrict__ logits, int f16,
   const int64_t o = n * K + k;
   *reinterpret_cast<uint32_t*>(w + o) = wo[0] | (wo[1] << 16);
   if (w_soft) *reinterpret_cast<uint32_t*>(w_soft + o) = so[0] | (so[1] << 16);
+}
+
+__global__ void build_w_kernel(const uint16_t* __restrict__ logits, int f16,
+                               const float* __restrict__ noise, const float* __restrict__ pal,
+                               float inv_tau, int mode, uint16_t* __restrict__ w,
+                               uint16_t* __restrict__ w_soft, int64_t N, int64_t K) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= N * (K / 2)) return;
+  build_w_pair(logits, f16, noise, pal, inv_tau, mode, w, w_soft, K, t);
+}
+
+// Many linears in one launch (fused_lut_kernel.cu:2071-2211 batches the per-layer build the
+// same way): block b belongs to the descriptor whose block_begin is the last one <= b.
+constexpr int kBuildWBlock = 256;
+__global__ void build_w_batched_kernel(const plz_build_w_desc* __restrict__ descs, int n_desc,
+                                       float inv_tau, int mode) {
+  const int64_t b = blockIdx.x;
+  int lo = 0, hi = n_desc - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (descs[mid].block_begin <= b) lo = mid; else hi = mid - 1;
+  }
+  const plz_build_w_desc d = descs[lo];
+  const int64_t t = (b - d.block_begin) * kBuildWBlock + threadIdx.x;
+  if (t >= d.N * (d.K / 2)) return;
+  build_w_pair(d.logits, d.logits_dtype == PLZ_DT_FP16, d.noise, d.palette, inv_tau, mode, d.w,
+               d.w_soft, d.K, t);
 }
 
 }  // namespace plz
@@ -176,6 +203,45 @@ int plz_soft_build_w(const uint16_t* logits, int logits_dtype, const float* nois
                      (hipStream_t)stream, logits, logits_dtype == PLZ_DT_FP16 ? 1 : 0, noise,
                      palette, 1.f / tau, mode, w, w_soft, N, K);
   return check_launch("plz_soft_build_w");
+}
+
+int64_t plz_build_w_plan(plz_build_w_desc* descs, int n) {
+  if (n < 0 || (n > 0 && !descs)) {
+    set_error("plz_build_w_plan: need n >= 0 and non-null descriptors");
+    return -PLZ_EINVAL;
+  }
+  int64_t total = 0;
+  for (int i = 0; i < n; ++i) {
+    const plz_build_w_desc& d = descs[i];
+    if (d.N < 0 || d.K < 0 || d.K % 256 != 0 ||
+        (d.logits_dtype != PLZ_DT_BF16 && d.logits_dtype != PLZ_DT_FP16)) {
+      set_error("plz_build_w_plan: descriptor %d: need K %% 256 == 0 and bf16/fp16 logits", i);
+      return -PLZ_EINVAL;
+    }
+    if (d.N > 0 && d.K > 0 &&
+        (!d.logits || !d.noise || !d.palette || !d.w ||
+         (((uintptr_t)d.logits | (uintptr_t)d.noise | (uintptr_t)d.palette) & 15) ||
+         (((uintptr_t)d.w | (uintptr_t)d.w_soft) & 3))) {
+      set_error("plz_build_w_plan: descriptor %d: null or misaligned pointer", i);
+      return -PLZ_EINVAL;
+    }
+    descs[i].block_begin = total;
+    total += (d.N * (d.K / 2) + kBuildWBlock - 1) / kBuildWBlock;
+  }
+  return total;
+}
+
+int plz_soft_build_w_batched(const plz_build_w_desc* descs_device, int n, int64_t total_blocks,
+                             float tau, int mode, void* stream) {
+  PLZ_REQUIRE(n >= 0 && total_blocks >= 0, "plz_soft_build_w_batched: negative count");
+  PLZ_REQUIRE(mode == PLZ_W_SOFT || mode == PLZ_W_HARD_NOISY || mode == PLZ_W_HARD_PLAIN,
+              "plz_soft_build_w_batched: unknown mode %d", mode);
+  PLZ_REQUIRE(tau > 0.f, "plz_soft_build_w_batched: tau must be positive");
+  if (n == 0 || total_blocks == 0) return PLZ_OK;
+  PLZ_REQUIRE(descs_device, "plz_soft_build_w_batched: null descriptor table");
+  hipLaunchKernelGGL(build_w_batched_kernel, dim3((unsigned)total_blocks), dim3(kBuildWBlock), 0,
+                     (hipStream_t)stream, descs_device, n, 1.f / tau, mode);
+  return check_launch("plz_soft_build_w_batched");
 }
 
 }  // extern "C"

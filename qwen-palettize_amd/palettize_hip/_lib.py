@@ -20,6 +20,18 @@ p = C.c_void_p
 i32, i64, u32, u64, f32, sz = C.c_int, C.c_int64, C.c_uint32, C.c_uint64, C.c_float, C.c_size_t
 
 
+class BuildWDesc(C.Structure):
+    _fields_ = [("logits", p), ("noise", p), ("palette", p), ("w", p), ("w_soft", p),
+                ("N", i64), ("K", i64), ("logits_dtype", i32), ("reserved", i32),
+                ("block_begin", i64)]
+
+
+class AdamWDesc(C.Structure):
+    _fields_ = [("param", p), ("grad", p), ("master", p), ("exp_avg", p), ("exp_avg_sq", p),
+                ("n", i64), ("dtype", i32), ("clip_group", i32), ("lr", f32), ("clamp_lo", f32),
+                ("clamp_hi", f32), ("reserved", f32), ("block_begin", i64)]
+
+
 class GemvDesc(C.Structure):
     _fields_ = [("x", p), ("packed", p), ("palette", p), ("y", p), ("N", i64), ("K", i64),
                 ("block_begin", i64), ("cost_begin", i64), ("palette_items", p)]
@@ -42,6 +54,8 @@ SIGNATURES: dict[str, tuple] = {
     "plz_gumbel_philox": (i32, [p, i64, u64, u64, p]),
     "plz_gumbel_lcg": (i32, [p, u32, i64, i64, p]),
     "plz_soft_build_w": (i32, [p, i32, p, p, f32, i32, p, p, i64, i64, p]),
+    "plz_build_w_plan": (i64, [C.POINTER(BuildWDesc), i32]),
+    "plz_soft_build_w_batched": (i32, [p, i32, i64, f32, i32, p]),
     "plz_soft_bwd_workspace": (sz, [i64, i64, i64]),
     "plz_soft_bwd": (i32, [p, p, p, i32, p, p, f32, i32, p, p, p, sz, i64, i64, i64, p]),
     "plz_lora_project": (i32, [p, p, f32, p, i64, i64, i32, p]),
@@ -57,6 +71,10 @@ SIGNATURES: dict[str, tuple] = {
     "plz_packed_to_idx2": (i32, [p, p, i64, i64, p]),
     "plz_logits_argmax_idx2": (i32, [p, i32, p, i64, i64, p]),
     "plz_lut_to_palette": (i32, [p, p, i64, i64, i32, p]),
+    "plz_adamw_plan": (i64, [C.POINTER(AdamWDesc), i32]),
+    "plz_adamw_workspace": (sz, [i64]),
+    "plz_adamw_step": (i32, [p, i32, i64, f32, f32, C.c_double, C.c_double, f32, f32, i64, p, p,
+                             sz, p]),
     "plz_rmsnorm_fwd": (i32, [p, p, p, p, i64, i64, f32, p]),
     "plz_rmsnorm_bwd_workspace": (sz, [i64, i64]),
     "plz_rmsnorm_bwd": (i32, [p, p, p, p, p, p, p, sz, i64, i64, p]),

@@ -29,6 +29,7 @@ import torch.nn.functional as F
 from . import ops
 from ._lib import PLZ_W_HARD_NOISY
 from .functional import SoftLUTLinearFunction
+from .optim import FusedAdamW
 
 
 @dataclass
@@ -272,40 +273,6 @@ def tau_at(step, tau_init=2.0, tau_final=0.5, warmup=500, anneal=6000):
     return tau_final
 
 
-class FP32MasterAdamW:
-    """AdamW on fp32 master copies of (possibly bf16) parameters (train_qwen.py:154-221)."""
-
-    def __init__(self, groups, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.0):
-        self.pairs = []
-        master_groups = []
-        for grp in groups:
-            ms = []
-            for p in grp["params"]:
-                m = p.detach().float().clone().requires_grad_(True)
-                self.pairs.append((m, p))
-                ms.append(m)
-            master_groups.append({"params": ms, "lr": grp["lr"]})
-        self.opt = torch.optim.AdamW(master_groups, betas=betas, eps=eps,
-                                     weight_decay=weight_decay, foreach=True)
-
-    def step(self):
-        for m, p in self.pairs:
-            m.grad = None if p.grad is None else p.grad.float()
-        self.opt.step()
-        with torch.no_grad():
-            for m, p in self.pairs:
-                p.copy_(m)
-
-    @torch.no_grad()
-    def clamp_(self, params, lo, hi):
-        """Clamp model parameters and their fp32 masters together."""
-        ids = {id(p) for p in params}
-        for m, p in self.pairs:
-            if id(p) in ids:
-                m.clamp_(lo, hi)
-                p.copy_(m)
-
-
 class LayerTrainer:
     """Owns a student/teacher pair and runs config-5 training steps."""
 
@@ -322,9 +289,10 @@ class LayerTrainer:
             logits.append(lin.index_logits)
         self.logits = logits
         self.others = pal + lora
-        self.opt = FP32MasterAdamW([{"params": pal, "lr": lrs["palettes"]},
-                                    {"params": lora, "lr": lrs["lora"]},
-                                    {"params": logits, "lr": lrs["indices"]}])
+        # clip group 0: index logits (max norm 1.0, clamped to +-5 tau); group 1: the rest (0.3)
+        self.opt = FusedAdamW([{"params": logits, "lr": lrs["indices"], "clip_group": 0},
+                               {"params": pal, "lr": lrs["palettes"], "clip_group": 1},
+                               {"params": lora, "lr": lrs["lora"], "clip_group": 1}])
         self.step_idx = 0
         self._rope = {}
 
@@ -348,12 +316,11 @@ class LayerTrainer:
         return loss.detach(), l_cos.detach()
 
     def update(self):
-        """Two-tier clip, AdamW on fp32 masters, logits clamp +-5 tau, advance the step."""
+        """Two-tier clip, AdamW on fp32 masters, logits clamp +-5 tau, advance the step: one
+        fused step (plz_adamw_step)."""
         tau = tau_at(self.step_idx)
-        torch.nn.utils.clip_grad_norm_(self.logits, 1.0)
-        torch.nn.utils.clip_grad_norm_(self.others, 0.3)
-        self.opt.step()
-        self.opt.clamp_(self.logits, -5.0 * tau, 5.0 * tau)
+        self.opt.set_clamp(0, -5.0 * tau, 5.0 * tau)
+        self.opt.step(max_norms=(1.0, 0.3))
         self.step_idx += 1
 
     def step(self, hs):

@@ -233,6 +233,42 @@ def soft_build_w(logits, noise, palette, tau: float, mode: int = _lib.PLZ_W_HARD
     return w, ws
 
 
+class SoftBuildGroup:
+    """The forward weights of several soft linears built by one launch
+    (plz_soft_build_w_batched). ``items`` is a list of (logits, noise, palette); the outputs
+    (w and, with want_soft, w_soft) are allocated once and rewritten by every ``run(tau)``."""
+
+    def __init__(self, items, mode: int = _lib.PLZ_W_HARD_NOISY, want_soft: bool = False):
+        if not items:
+            raise ValueError("empty build group")
+        self.mode = int(mode)
+        self.device = items[0][0].device
+        self.outputs = []
+        descs = (_lib.BuildWDesc * len(items))()
+        for i, (logits, noise, palette) in enumerate(items):
+            N, K = _soft_shapes(logits, noise, palette)
+            w = torch.empty((N, K), dtype=torch.bfloat16, device=self.device)
+            ws = torch.empty((N, K), dtype=torch.bfloat16, device=self.device) if want_soft else None
+            self.outputs.append((w, ws))
+            descs[i] = _lib.BuildWDesc(logits.data_ptr(), noise.data_ptr(), palette.data_ptr(),
+                                       w.data_ptr(), ws.data_ptr() if ws is not None else None,
+                                       N, K, _DT[logits.dtype], 0, 0)
+        self._keep = items
+        total = _lib.lib().plz_build_w_plan(descs, len(items))
+        if total < 0:
+            raise _lib.PalettizeError(
+                "plz_build_w_plan failed: " + _lib.lib().plz_last_error().decode())
+        self.total_blocks = int(total)
+        raw = bytes(C.string_at(C.addressof(descs), C.sizeof(descs)))
+        self.table = torch.frombuffer(bytearray(raw), dtype=torch.uint8).to(self.device)
+        self.n = len(items)
+
+    def run(self, tau: float):
+        call("plz_soft_build_w_batched", self.table.data_ptr(), self.n, self.total_blocks,
+             float(tau), self.mode, torch.cuda.current_stream(self.device).cuda_stream)
+        return self.outputs
+
+
 def soft_bwd(x, grad_y, logits, noise, palette, tau: float, scale_by_inv_tau: bool = False):
     N, K = _soft_shapes(logits, noise, palette)
     _need(x, "x", torch.bfloat16, 2)

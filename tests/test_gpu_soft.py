@@ -56,6 +56,24 @@ def test_soft_build_w(dev, mode, tau, dtype):
     assert near(ws.view(torch.int16).cpu().numpy().view(np.uint16), w_soft)
 
 
+@pytest.mark.parametrize("mode", [PLZ_W_SOFT, PLZ_W_HARD_NOISY, PLZ_W_HARD_PLAIN])
+def test_soft_build_w_batched_matches_single(dev, mode):
+    """One launch over linears of different shapes and logit dtypes equals the per-linear
+    builds bit for bit, on two consecutive runs with different tau."""
+    shapes = [(64, 512, torch.bfloat16), (8, 256, torch.float16), (136, 768, torch.bfloat16),
+              (1024, 2560, torch.bfloat16)]
+    items = []
+    for i, (N, K, dt) in enumerate(shapes):
+        lg, nz, pl = _soft_inputs(N, K, seed=40 + i, dtype=dt)
+        items.append((lg.to(dev), nz.to(dev), pl.to(dev)))
+    grp = ops.SoftBuildGroup(items, mode, want_soft=True)
+    for tau in (0.7, 2.0):
+        outs = grp.run(tau)
+        for (lg, nz, pl), (w, ws) in zip(items, outs):
+            w1, ws1 = ops.soft_build_w(lg, nz, pl, tau, mode, want_soft=True)
+            assert torch.equal(w, w1) and torch.equal(ws, ws1)
+
+
 @pytest.mark.parametrize("tau", [2.0, 0.5, 0.1])
 @pytest.mark.parametrize("scaled", [False, True])
 def test_soft_bwd(dev, tau, scaled):

@@ -347,3 +347,32 @@ def test_swiglu_matches_torch():
     (torch.nn.functional.silu(gd) * ud).backward(gh)
     og, ou = O.swiglu_bwd(g.double().numpy(), u.double().numpy(), gh.numpy())
     assert np.allclose(og, gd.grad.numpy(), rtol=1e-9) and np.allclose(ou, ud.grad.numpy())
+
+
+# ---- layer optimizer: clip + AdamW + clamp vs torch ------------------------------------------
+def test_adamw_step_matches_torch_clip_adamw_clamp():
+    import torch
+    rng = np.random.default_rng(11)
+    shapes = [(7, 5), (300,), (2, 3, 4)]
+    groups = [0, 1, 1]
+    lrs = [1e-2, 1e-4, 3e-4]
+    clamps = [(-0.05, 0.05), (-np.inf, np.inf), (-np.inf, np.inf)]
+    masters = [rng.standard_normal(s) * 0.03 for s in shapes]
+    tparams = [torch.tensor(m, dtype=torch.float64, requires_grad=True) for m in masters]
+    opt = torch.optim.AdamW([{"params": [tparams[i]], "lr": lrs[i]} for i in range(3)],
+                            betas=(0.9, 0.95), eps=1e-8, weight_decay=0.0)
+    ms = [np.zeros(s) for s in shapes]
+    vs = [np.zeros(s) for s in shapes]
+    for step in range(1, 4):
+        grads = [rng.standard_normal(s) * (3.0 if step == 2 else 0.01) for s in shapes]
+        for t, g in zip(tparams, grads):
+            t.grad = torch.tensor(g)
+        n0 = torch.nn.utils.clip_grad_norm_([tparams[0]], 1.0)
+        n1 = torch.nn.utils.clip_grad_norm_(tparams[1:], 0.3)
+        opt.step()
+        with torch.no_grad():
+            tparams[0].clamp_(-0.05, 0.05)
+        norms = O.adamw_step(masters, grads, ms, vs, lrs, groups, (1.0, 0.3), clamps, step)
+        assert np.isclose(norms[0], float(n0)) and np.isclose(norms[1], float(n1))
+        for m, t in zip(masters, tparams):
+            assert np.allclose(m, t.detach().numpy(), rtol=1e-10, atol=1e-12)
