@@ -14,7 +14,7 @@
 // masters. Two kernels stream every parameter once each: the squared-norm partials, then the
 // update (the norms are finished on the device in between; no host synchronisation). HBM-bound:
 // a bf16 parameter with master moves 30 bytes per element (grad read twice, m/v/master read and
-// written, param written).
+// written, param written), in 16-byte accesses of 8 consecutive elements per thread.
 #include <cmath>
 
 #include "plz_common.h"
@@ -24,8 +24,9 @@ namespace plz {
 namespace opt {
 
 constexpr int kThreads = 256;
-constexpr int kEpt = 8;                       // elements per thread
-constexpr int kBlockElems = kThreads * kEpt;  // elements per block
+constexpr int kVec = 8;                                  // contiguous elements per chunk
+constexpr int kChunks = 4;                               // chunks per thread
+constexpr int kBlockElems = kThreads * kVec * kChunks;   // elements per block: 8192
 
 __device__ __forceinline__ int find_desc(const plz_adamw_desc* d, int n, int64_t b) {
   int lo = 0, hi = n - 1;
@@ -38,6 +39,30 @@ __device__ __forceinline__ int find_desc(const plz_adamw_desc* d, int n, int64_t
 __device__ __forceinline__ float grad_at(const plz_adamw_desc& d, int64_t i) {
   return d.dtype == PLZ_DT_BF16 ? bf2f(reinterpret_cast<const uint16_t*>(d.grad)[i])
                                 : reinterpret_cast<const float*>(d.grad)[i];
+}
+// 8 consecutive gradients starting at i (16-byte aligned: the whole chunk is in range)
+__device__ __forceinline__ void grad8(const plz_adamw_desc& d, int64_t i, float (&g)[kVec]) {
+  if (d.dtype == PLZ_DT_BF16) {
+    const uint4 v = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(d.grad) + i);
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      g[2 * j] = bf2f(w[j] & 0xffffu);
+      g[2 * j + 1] = bf2f(w[j] >> 16);
+    }
+  } else {
+    const float4* p = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(d.grad) + i);
+    const float4 a = p[0], b = p[1];
+    g[0] = a.x; g[1] = a.y; g[2] = a.z; g[3] = a.w; g[4] = b.x; g[5] = b.y; g[6] = b.z; g[7] = b.w;
+  }
+}
+__device__ __forceinline__ void load8(const float* p, float (&v)[kVec]) {
+  const float4 a = reinterpret_cast<const float4*>(p)[0], b = reinterpret_cast<const float4*>(p)[1];
+  v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+__device__ __forceinline__ void store8(float* p, const float (&v)[kVec]) {
+  reinterpret_cast<float4*>(p)[0] = make_float4(v[0], v[1], v[2], v[3]);
+  reinterpret_cast<float4*>(p)[1] = make_float4(v[4], v[5], v[6], v[7]);
 }
 
 __device__ __forceinline__ float block_sum(float v, float* red) {
@@ -62,11 +87,18 @@ __global__ __launch_bounds__(kThreads) void sumsq_kernel(const plz_adamw_desc* _
   const int64_t base = (b - d.block_begin) * kBlockElems;
   float s = 0.f;
 #pragma unroll
-  for (int e = 0; e < kEpt; ++e) {
-    const int64_t i = base + (int64_t)e * kThreads + threadIdx.x;
-    if (i < d.n) {
-      const float g = grad_at(d, i);
-      s += g * g;
+  for (int c = 0; c < kChunks; ++c) {
+    const int64_t i0 = base + ((int64_t)c * kThreads + threadIdx.x) * kVec;
+    if (i0 + kVec <= d.n) {
+      float g[kVec];
+      grad8(d, i0, g);
+#pragma unroll
+      for (int j = 0; j < kVec; ++j) s += g[j] * g[j];
+    } else {
+      for (int64_t i = i0; i < d.n; ++i) {
+        const float g = grad_at(d, i);
+        s += g * g;
+      }
     }
   }
   s = block_sum(s, red);
@@ -76,57 +108,96 @@ __global__ __launch_bounds__(kThreads) void sumsq_kernel(const plz_adamw_desc* _
   }
 }
 
-// coef[G] = min(1, max_norm[G] / (sqrt(sum of group G's partials, in block order) + 1e-6))
+// coef[G] = min(1, max_norm[G] / (sqrt(sum of group G's partials) + 1e-6)); coef[2 + G] = norm
+// (a fixed assignment of partials to threads and a fixed reduction tree: deterministic)
 __global__ __launch_bounds__(kThreads) void clip_coef_kernel(const float* __restrict__ partial,
                                                              const int* __restrict__ group,
                                                              int64_t nblocks, float max0,
                                                              float max1, float* __restrict__ coef) {
   __shared__ float red[kThreads / 64];
   const int G = blockIdx.x;
-  // fixed assignment of partials to threads and a fixed reduction tree: deterministic
-  float s = 0.f;
-  for (int64_t i = threadIdx.x; i < nblocks; i += kThreads)
-    if (group[i] == G) s += partial[i];
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  int64_t i = threadIdx.x;
+  for (; i + 7 * kThreads < nblocks; i += 8 * kThreads) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int64_t k = i + u * kThreads;
+      acc[u] += group[k] == G ? partial[k] : 0.f;
+    }
+  }
+  for (; i < nblocks; i += kThreads) acc[0] += group[i] == G ? partial[i] : 0.f;
+  float s = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
   s = block_sum(s, red);
   if (threadIdx.x == 0) {
     const float mx = G == 0 ? max0 : max1;
     const float c = mx / (sqrtf(s) + 1e-6f);
-    coef[G] = mx > 0.f ? fminf(c, 1.f) : 1.f;   // max_norm <= 0: no clipping
-    coef[2 + G] = sqrtf(s);                      // the norm itself (returned to the caller)
+    coef[G] = mx > 0.f ? fminf(c, 1.f) : 1.f;  // max_norm <= 0: no clipping
+    coef[2 + G] = sqrtf(s);
   }
+}
+
+struct Hyper {
+  float beta1, beta2, eps, weight_decay, bc1, bc2_sqrt;
+};
+__device__ __forceinline__ float adamw_one(float g, float& p, float& m, float& v, float step_size,
+                                           float decay, const Hyper& h, float lo, float hi) {
+  if (h.weight_decay != 0.f) p *= decay;
+  m = m + (1.f - h.beta1) * (g - m);
+  v = v * h.beta2;
+  v = v + (1.f - h.beta2) * g * g;
+  const float denom = sqrtf(v) / h.bc2_sqrt + h.eps;
+  p = p - step_size * (m / denom);
+  p = fminf(fmaxf(p, lo), hi);
+  return p;
 }
 
 __global__ __launch_bounds__(kThreads) void adamw_kernel(const plz_adamw_desc* __restrict__ descs,
                                                          int n_desc, const float* __restrict__ coef,
-                                                         float beta1, float beta2, float eps,
-                                                         float weight_decay, float bc1,
-                                                         float bc2_sqrt) {
+                                                         const Hyper h) {
   const int64_t b = blockIdx.x;
   const plz_adamw_desc d = descs[find_desc(descs, n_desc, b)];
   const int64_t base = (b - d.block_begin) * kBlockElems;
   const float c = coef[d.clip_group];
-  const float step_size = d.lr / bc1;
-  const float decay = 1.f - d.lr * weight_decay;
+  const float step_size = d.lr / h.bc1;
+  const float decay = 1.f - d.lr * h.weight_decay;
   float* p32 = d.master ? d.master : reinterpret_cast<float*>(d.param);
 #pragma unroll
-  for (int e = 0; e < kEpt; ++e) {
-    const int64_t i = base + (int64_t)e * kThreads + threadIdx.x;
-    if (i >= d.n) continue;
-    const float g = grad_at(d, i) * c;
-    float p = p32[i];
-    if (weight_decay != 0.f) p *= decay;
-    float m = d.exp_avg[i], v = d.exp_avg_sq[i];
-    m = m + (1.f - beta1) * (g - m);
-    v = v * beta2;
-    v = v + (1.f - beta2) * g * g;
-    const float denom = sqrtf(v) / bc2_sqrt + eps;
-    p = p - step_size * (m / denom);
-    p = fminf(fmaxf(p, d.clamp_lo), d.clamp_hi);
-    d.exp_avg[i] = m;
-    d.exp_avg_sq[i] = v;
-    p32[i] = p;
-    if (d.master && d.dtype == PLZ_DT_BF16) reinterpret_cast<uint16_t*>(d.param)[i] = (uint16_t)f2bf(p);
-    if (d.master && d.dtype == PLZ_DT_FP32) reinterpret_cast<float*>(d.param)[i] = p;
+  for (int ch = 0; ch < kChunks; ++ch) {
+    const int64_t i0 = base + ((int64_t)ch * kThreads + threadIdx.x) * kVec;
+    if (i0 + kVec <= d.n) {
+      float g[kVec], p[kVec], m[kVec], v[kVec];
+      grad8(d, i0, g);
+      load8(p32 + i0, p);
+      load8(d.exp_avg + i0, m);
+      load8(d.exp_avg_sq + i0, v);
+#pragma unroll
+      for (int j = 0; j < kVec; ++j)
+        adamw_one(g[j] * c, p[j], m[j], v[j], step_size, decay, h, d.clamp_lo, d.clamp_hi);
+      store8(d.exp_avg + i0, m);
+      store8(d.exp_avg_sq + i0, v);
+      store8(p32 + i0, p);
+      if (d.master && d.dtype == PLZ_DT_BF16) {
+        uint32_t w[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) w[j] = f2bf2(p[2 * j], p[2 * j + 1]);
+        *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(d.param) + i0) =
+            make_uint4(w[0], w[1], w[2], w[3]);
+      } else if (d.master) {
+        store8(reinterpret_cast<float*>(d.param) + i0, p);
+      }
+    } else {
+      for (int64_t i = i0; i < d.n; ++i) {
+        float p = p32[i], m = d.exp_avg[i], v = d.exp_avg_sq[i];
+        adamw_one(grad_at(d, i) * c, p, m, v, step_size, decay, h, d.clamp_lo, d.clamp_hi);
+        d.exp_avg[i] = m;
+        d.exp_avg_sq[i] = v;
+        p32[i] = p;
+        if (d.master && d.dtype == PLZ_DT_BF16)
+          reinterpret_cast<uint16_t*>(d.param)[i] = (uint16_t)f2bf(p);
+        else if (d.master)
+          reinterpret_cast<float*>(d.param)[i] = p;
+      }
+    }
   }
 }
 
@@ -156,6 +227,11 @@ int64_t plz_adamw_plan(plz_adamw_desc* descs, int n) {
     if (d.n > 0 && (!d.param || !d.grad || !d.exp_avg || !d.exp_avg_sq ||
                     (d.dtype == PLZ_DT_BF16 && !d.master))) {
       set_error("plz_adamw_plan: descriptor %d: null pointer (bf16 parameters need a master)", i);
+      return -PLZ_EINVAL;
+    }
+    if ((((uintptr_t)d.param | (uintptr_t)d.grad | (uintptr_t)d.master | (uintptr_t)d.exp_avg |
+          (uintptr_t)d.exp_avg_sq) & 15) != 0) {
+      set_error("plz_adamw_plan: descriptor %d: pointers must be 16-byte aligned", i);
       return -PLZ_EINVAL;
     }
     descs[i].block_begin = total;
@@ -198,8 +274,9 @@ int plz_adamw_step(const plz_adamw_desc* descs_device, int n, int64_t total_bloc
   // bias corrections in double on the host, as torch computes its Python-float scalars
   const float bc1 = (float)(1.0 - std::pow(beta1, (double)step));
   const float bc2_sqrt = (float)std::sqrt(1.0 - std::pow(beta2, (double)step));
+  const Hyper h{(float)beta1, (float)beta2, eps, weight_decay, bc1, bc2_sqrt};
   hipLaunchKernelGGL(adamw_kernel, dim3(grid_of(total_blocks)), dim3(kThreads), 0, s, descs_device,
-                     n, coef, (float)beta1, (float)beta2, eps, weight_decay, bc1, bc2_sqrt);
+                     n, coef, h);
   if ((rc = check_launch("plz_adamw_step/update"))) return rc;
   if (norms_out) {
     hipMemcpyAsync(norms_out, coef + 2, 2 * sizeof(float), hipMemcpyDeviceToDevice, s);
