@@ -139,6 +139,7 @@ __device__ __forceinline__ void dequant16_pair(uint32_t qa, PalLut ta, uint32_t 
 // ---- error reporting shared by every entry point -------------------------------
 void set_error(const char* fmt, ...);
 int check_launch(const char* what);
+void zero_async(void* p, size_t bytes, hipStream_t stream);  // kernel fill, capture-safe
 
 }  // namespace plz
 

@@ -29,6 +29,21 @@ int check_launch(const char* what) {
   return PLZ_OK;
 }
 
+// Zero fill by a kernel rather than hipMemsetAsync: a memset node recorded into a captured
+// HIP graph is not reliable on replay, and callers may capture any entry point. Used only for
+// the degenerate shapes (an empty reduction) whose outputs are all zero; bytes is even.
+__global__ void zero_kernel(uint16_t* __restrict__ p, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0;
+}
+
+void zero_async(void* p, size_t bytes, hipStream_t stream) {
+  const int64_t n = (int64_t)(bytes / 2);
+  if (n > 0)
+    hipLaunchKernelGGL(zero_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
+                       reinterpret_cast<uint16_t*>(p), n);
+}
+
 // ---- canonical packing: idx[r, c] (uint8 0..3) -> packed[r, c/16] -------------
 __global__ void pack_kernel(const uint8_t* __restrict__ idx, int32_t* __restrict__ packed,
                             int64_t n_words) {

@@ -662,7 +662,7 @@ int plz_lut_linear_bwd_palette(const uint16_t* x, const uint16_t* grad_y, const 
   if (N == 0 || K == 0) return PLZ_OK;
   PLZ_REQUIRE(packed && grad_palette, "plz_lut_linear_bwd_palette: null pointer");
   if (M == 0) {
-    hipMemsetAsync(grad_palette, 0, (size_t)N * (K / 256) * 16, (hipStream_t)stream);
+    zero_async(grad_palette, (size_t)N * (K / 256) * 16, (hipStream_t)stream);
     return check_launch("plz_lut_linear_bwd_palette");
   }
   PLZ_REQUIRE(x && grad_y && a16(x) && a16(grad_y) && a16(packed),

@@ -5,19 +5,21 @@
 // 0.5 bit of fp32 palette per weight are streamed once, and everything else is arranged so
 // that the stream never stops:
 //
-// * Persistent workgroups, one per CU. The work items (128 rows of one linear, all of K) of
-//   a launch are cut into one contiguous range per workgroup, balanced by bytes (K per item).
-// * A workgroup walks its items as one sequence of stages (128 rows x 512 k). Each stage's
-//   packed indices, palettes and x slice go global->LDS by buffer_load ... lds (1 KB per
-//   instruction, whole cache lines, no VGPRs), three stages ahead in a 4-slot ring, across
-//   item boundaries -- the loads of the next item are in flight while this one finishes.
+// * Persistent workgroups, a few per CU (as many as the LDS ring allows, at most 16 waves).
+//   The work items (128 rows of one linear, all of K) of a launch are cut into one contiguous
+//   range per workgroup, balanced by bytes (K per item).
+// * A workgroup walks its items as one sequence of stages (128 rows x 256 k = one palette
+//   group). Each stage's packed indices, palettes and x slice go global->LDS by
+//   buffer_load ... lds (1 KB per wave instruction, whole cache lines, no VGPRs), NS-1 stages
+//   ahead in an NS-slot ring, across item boundaries -- the loads of the next item are in
+//   flight while this one finishes. Palettes may come prepacked per item and stage (2 KB
+//   contiguous, plz_gemv_pack_palettes) instead of 16 B per row strided by K/256 groups.
 // * Wave w owns rows 32w..32w+31 of the item (two MFMA row blocks of 16). Lane (row n%16,
-//   quarter q) dequantises 8 consecutive packed words (128 k) of its row per stage through
-//   v_perm_b32 byte tables into bf16 fragments (in a permuted k order that the x fragments
-//   repeat); v_mfma_f32_16x16x32_bf16
-//   computes C[n][m] for all M <= 16 tokens at once (fragment lanes of tokens m >= M read
-//   token M-1; their columns are never stored). x fragments come from the stage's x slice
-//   in LDS and serve both row blocks.
+//   quarter q) dequantises 4 consecutive packed words (64 k) of its row per block and stage
+//   through v_perm_b32 byte tables into bf16 fragments (in a permuted k order that the x
+//   fragments repeat); v_mfma_f32_16x16x32_bf16 computes C[n][m] for all M <= 16 tokens at
+//   once (fragment lanes of tokens m >= M read token M-1; their columns are never stored).
+//   x fragments come from the stage's x slice in LDS and serve both row blocks.
 // * LDS layouts are XOR-swizzled on the global side of the copies so that every fragment
 //   read is bank-conflict free.
 #include "plz_common.h"
@@ -392,7 +394,7 @@ int plz_lut_gemv(const uint16_t* x, const int32_t* packed, const float* palette,
   if (rc) return rc;
   if (N == 0) return PLZ_OK;
   if (K == 0) {
-    hipMemsetAsync(y, 0, (size_t)M * N * 2, (hipStream_t)stream);
+    zero_async(y, (size_t)M * N * 2, (hipStream_t)stream);
     return check_launch("plz_lut_gemv");
   }
   const int64_t items = (N + ROWS - 1) / ROWS;

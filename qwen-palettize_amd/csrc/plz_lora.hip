@@ -482,16 +482,17 @@ int plz_lora_weight_grads(const uint16_t* x, const uint16_t* grad_y, const uint1
   PLZ_REQUIRE(N % 8 == 0 && K % 8 == 0, "plz_lora_weight_grads: N and K must be multiples of 8");
   PLZ_REQUIRE(out_dtype == PLZ_DT_BF16 || out_dtype == PLZ_DT_FP32,
               "plz_lora_weight_grads: out dtype must be bf16 or fp32");
+  PLZ_REQUIRE((grad_a || K == 0) && (grad_b || N == 0), "plz_lora_weight_grads: null output");
+  hipStream_t s = (hipStream_t)stream;
+  const int bf = out_dtype == PLZ_DT_BF16;
+  if (M == 0) {  // empty reduction: zero gradients (the inputs may be null)
+    zero_async(grad_b, (size_t)N * rank * (bf ? 2 : 4), s);
+    zero_async(grad_a, (size_t)K * rank * (bf ? 2 : 4), s);
+    return check_launch("plz_lora_weight_grads");
+  }
   PLZ_REQUIRE(x && grad_y && t && gt && grad_a && grad_b, "plz_lora_weight_grads: null pointer");
   PLZ_REQUIRE(aligned16(x) && aligned16(grad_y) && aligned16(t) && aligned16(gt),
               "plz_lora_weight_grads: inputs must be 16-byte aligned");
-  hipStream_t s = (hipStream_t)stream;
-  const int bf = out_dtype == PLZ_DT_BF16;
-  if (M == 0) {
-    hipMemsetAsync(grad_b, 0, (size_t)N * rank * (bf ? 2 : 4), s);
-    hipMemsetAsync(grad_a, 0, (size_t)K * rank * (bf ? 2 : 4), s);
-    return check_launch("plz_lora_weight_grads");
-  }
   const int64_t split_n = col_split(M, N), split_k = col_split(M, K);
   PLZ_REQUIRE(split_n * N * 2 < (int64_t)1 << 31 && split_k * K * 2 < (int64_t)1 << 31,
               "plz_lora_weight_grads: M split x N or K too large");

@@ -255,7 +255,7 @@ int plz_rmsnorm_bwd(const uint16_t* x, const uint16_t* weight, const float* rstd
               (long long)cols);
   PLZ_REQUIRE(grad_weight, "plz_rmsnorm_bwd: null grad_weight");
   if (rows == 0) {
-    hipMemsetAsync(grad_weight, 0, (size_t)cols * 4, (hipStream_t)stream);
+    zero_async(grad_weight, (size_t)cols * 4, (hipStream_t)stream);
     return check_launch("plz_rmsnorm_bwd");
   }
   PLZ_REQUIRE(x && weight && rstd && grad_y && grad_x && a16(x) && a16(weight) && a16(grad_y) &&

@@ -144,6 +144,16 @@ def test_empty_inputs(dev):
     assert ops.lut_linear_fwd(x, p, pl).shape == (0, 16)
     g = ops.lut_linear_bwd_palette(x, torch.empty(0, 16, dtype=torch.bfloat16, device=dev), p)
     assert torch.count_nonzero(g) == 0
+    # empty reductions of the other kernels are zero-filled too (by a kernel, not a memset)
+    e = lambda *s: torch.empty(*s, dtype=torch.bfloat16, device=dev)
+    for dt in (torch.float32, torch.bfloat16):
+        ga, gb = ops.lora_weight_grads(e(0, 256), e(0, 128), e(0, 16), e(0, 16), 2.0, dt)
+        assert ga.shape == (16, 256) and gb.shape == (128, 16)
+        assert torch.count_nonzero(ga) == 0 and torch.count_nonzero(gb) == 0
+    _, gw = ops.rmsnorm_bwd(e(0, 320), torch.ones(320, dtype=torch.bfloat16, device=dev),
+                            torch.empty(0, device=dev),
+                            e(0, 320))
+    assert gw.shape == (320,) and torch.count_nonzero(gw) == 0
 
 
 # ---- decode GEMV ----------------------------------------------------------------------
