@@ -60,6 +60,7 @@ struct Args {
   void* c; int64_t ldc; const uint16_t* bias; float alpha; float* partial;
   const uint16_t* logits; const float* noise; float inv_tau, glog_scale; uint16_t* grad_logits;
   int logits_f16;
+  float* acc_ws;  // EPI_F32: partial dW rows of each reduction split, [split][I][J] fp32
   int tiles_i, tiles_j;
   int group;  // tile-rows walked together (1: consecutive workgroups share the A panel)
 };

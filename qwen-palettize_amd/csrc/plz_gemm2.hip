@@ -16,7 +16,7 @@ namespace plz {
 namespace g2 {
 
 enum { OP_ROW = 0, OP_COL = 1, OP_LUT_ROW = 2, OP_LUT_COL = 3, OP_LUT_REG = 4 };
-enum { EPI_BF16 = 0, EPI_PAL = 1, EPI_SOFT = 2 };
+enum { EPI_BF16 = 0, EPI_PAL = 1, EPI_SOFT = 2, EPI_F32 = 3 };
 
 // Masked register-path copies for a partial reduction stage (r >= rend reads as zero) and for
 // the rank-r second segment.
@@ -215,6 +215,69 @@ __device__ __forceinline__ void mma_stage_lutreg(const lds_u8* a_s, const lds_u8
   mma(a1, w1, 1);
   interleave_kstep<0, 0, 0, 0>();
   __builtin_amdgcn_sched_barrier(0);
+}
+
+// Soft backward of one (row n, 128-k segment) item, one wave; lane holds dW at k = kseg + 2*lane,
+// +1. Recomputes P = softmax((logits + noise) / tau) per weight (fp32), writes
+//   grad_logits[n, k, c] = glog_scale * dW * P_c * (palette_c - W_soft)   (W_soft = sum_c P_c palette_c)
+// and the segment's P-weighted class sums of dW to partial[n][kseg/128][4] (the palette
+// gradient before the sum over the group's two segments): fused_lut_kernel.cu:1877-1924.
+__device__ __forceinline__ void soft_item(const Args& g, int64_t n, int64_t kseg, int lane,
+                                          float2 gw) {
+  const int64_t k = kseg + 2 * lane;
+  const float4 pal = *reinterpret_cast<const float4*>(g.pal + (n * (g.J / 256) + k / 256) * 4);
+  const float pc[4] = {pal.x, pal.y, pal.z, pal.w};
+  const int64_t e0 = (n * g.J + k) * 4;
+  const uint4 lg = *reinterpret_cast<const uint4*>(g.logits + e0);
+  const float4 z0 = *reinterpret_cast<const float4*>(g.noise + e0);
+  const float4 z1 = *reinterpret_cast<const float4*>(g.noise + e0 + 4);
+  const uint32_t lw[4] = {lg.x, lg.y, lg.z, lg.w};
+  const float nz[8] = {z0.x, z0.y, z0.z, z0.w, z1.x, z1.y, z1.z, z1.w};
+  float sp[4] = {0.f, 0.f, 0.f, 0.f};
+  uint32_t out[4];
+#pragma unroll
+  for (int el = 0; el < 2; ++el) {
+    float a[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const uint32_t bits = (lw[2 * el + c / 2] >> (16 * (c & 1))) & 0xffffu;
+      a[c] = ((g.logits_f16 ? h2f(bits) : bf2f(bits)) + nz[4 * el + c]) * g.inv_tau;
+    }
+    const float m = fmaxf(fmaxf(a[0], a[1]), fmaxf(a[2], a[3]));
+    float ex[4], s = 0.f;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      ex[c] = __expf(a[c] - m);
+      s += ex[c];
+    }
+    const float rs = 1.f / s;
+    float P[4], ws = 0.f;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      P[c] = ex[c] * rs;
+      ws += P[c] * pc[c];
+    }
+    const float gv = el == 0 ? gw.x : gw.y;
+    uint32_t o16[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const float gp = gv * P[c];
+      sp[c] += gp;
+      const float gl = g.glog_scale * gp * (pc[c] - ws);
+      o16[c] = g.logits_f16 ? f2h(gl) : f2bf(gl);
+    }
+    out[2 * el] = o16[0] | (o16[1] << 16);
+    out[2 * el + 1] = o16[2] | (o16[3] << 16);
+  }
+  *reinterpret_cast<uint4*>(g.grad_logits + e0) = make_uint4(out[0], out[1], out[2], out[3]);
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) sp[c] += __shfl_xor(sp[c], off);
+  if (lane == 0) {
+    float* dst = g.partial + (n * (g.J / 128) + kseg / 128) * 4;
+    *reinterpret_cast<float4*>(dst) = make_float4(sp[0], sp[1], sp[2], sp[3]);
+  }
 }
 
 template <int KA, int KB, int EPI>
@@ -453,70 +516,39 @@ __global__ __launch_bounds__(NTHR) void gemm2_kernel(const Args g) {
         float* dst = g.partial + (((int64_t)zsl * g.I + n) * segs + kseg / 128) * 4;
         *reinterpret_cast<float4*>(dst) = make_float4(s0, s1, s2, s3);
       }
-    } else {  // EPI_SOFT: each wave walks (row, 128-k segment) items; lane = 2 consecutive k
+    } else {  // EPI_SOFT / EPI_F32: each wave walks (row, 128-k segment) items; lane = 2 k
       for (int item = wave; item < 256; item += NTHR / 64) {
         const int row = item >> 1, h = item & 1;
         const int64_t n = i0 + (row >> 6) * 128 + 64 * half + (row & 63);
-        const int64_t k = j0 + 128 * h + 2 * lane;
-        if (n >= g.I || j0 + 128 * h >= g.J) continue;
+        const int64_t kseg = j0 + 128 * h;
+        if (n >= g.I || kseg >= g.J) continue;
         const float2 gw = *reinterpret_cast<const float2*>(&sC[ptile(row, 128 * h + 2 * lane)]);
-        const float4 pal = *reinterpret_cast<const float4*>(g.pal + (n * (g.J / 256) + k / 256) * 4);
-        const float pc[4] = {pal.x, pal.y, pal.z, pal.w};
-        const int64_t e0 = (n * g.J + k) * 4;
-        const uint4 lg = *reinterpret_cast<const uint4*>(g.logits + e0);
-        const float4 z0 = *reinterpret_cast<const float4*>(g.noise + e0);
-        const float4 z1 = *reinterpret_cast<const float4*>(g.noise + e0 + 4);
-        const uint32_t lw[4] = {lg.x, lg.y, lg.z, lg.w};
-        const float nz[8] = {z0.x, z0.y, z0.z, z0.w, z1.x, z1.y, z1.z, z1.w};
-        float sp[4] = {0.f, 0.f, 0.f, 0.f};
-        uint32_t out[4];
-#pragma unroll
-        for (int el = 0; el < 2; ++el) {
-          float a[4];
-#pragma unroll
-          for (int c = 0; c < 4; ++c) {
-            const uint32_t bits = (lw[2 * el + c / 2] >> (16 * (c & 1))) & 0xffffu;
-            a[c] = ((g.logits_f16 ? h2f(bits) : bf2f(bits)) + nz[4 * el + c]) * g.inv_tau;
-          }
-          const float m = fmaxf(fmaxf(a[0], a[1]), fmaxf(a[2], a[3]));
-          float ex[4], s = 0.f;
-#pragma unroll
-          for (int c = 0; c < 4; ++c) {
-            ex[c] = __expf(a[c] - m);
-            s += ex[c];
-          }
-          const float rs = 1.f / s;
-          float P[4], ws = 0.f;
-#pragma unroll
-          for (int c = 0; c < 4; ++c) {
-            P[c] = ex[c] * rs;
-            ws += P[c] * pc[c];
-          }
-          const float gv = el == 0 ? gw.x : gw.y;
-          uint32_t o16[4];
-#pragma unroll
-          for (int c = 0; c < 4; ++c) {
-            const float gp = gv * P[c];
-            sp[c] += gp;
-            const float gl = g.glog_scale * gp * (pc[c] - ws);
-            o16[c] = g.logits_f16 ? f2h(gl) : f2bf(gl);
-          }
-          out[2 * el] = o16[0] | (o16[1] << 16);
-          out[2 * el + 1] = o16[2] | (o16[3] << 16);
-        }
-        *reinterpret_cast<uint4*>(g.grad_logits + e0) = make_uint4(out[0], out[1], out[2], out[3]);
-#pragma unroll
-        for (int c = 0; c < 4; ++c)
-#pragma unroll
-          for (int off = 32; off >= 1; off >>= 1) sp[c] += __shfl_xor(sp[c], off);
-        if (lane == 0) {
-          float* dst = g.partial + (n * segs + (j0 + 128 * h) / 128) * 4;
-          *reinterpret_cast<float4*>(dst) = make_float4(sp[0], sp[1], sp[2], sp[3]);
-        }
+        if (EPI == EPI_SOFT)
+          soft_item(g, n, kseg, lane, gw);
+        else  // this split's partial dW rows, [split][N][K] fp32
+          *reinterpret_cast<float2*>(g.acc_ws + ((int64_t)zsl * g.I + n) * g.J + kseg + 2 * lane) = gw;
       }
     }
     __syncthreads();
   }
+}
+
+// Soft backward of a split launch: dW = the sum of the Z partial [N][K] fp32 slices, summed in
+// split order (deterministic), then the per-item soft math. One wave per (row, 128-k segment).
+__global__ __launch_bounds__(256) void soft_split_epilogue_kernel(const Args g, int Z) {
+  const int lane = threadIdx.x & 63;
+  const int64_t segs = g.J / 128;
+  const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);  // wave-uniform
+  if (item >= g.I * segs) return;
+  const int64_t n = item / segs, kseg = (item % segs) * 128;
+  const float* p = g.acc_ws + n * g.J + kseg + 2 * lane;
+  float2 gw = make_float2(0.f, 0.f);
+  for (int z = 0; z < Z; ++z) {
+    const float2 v = *reinterpret_cast<const float2*>(p + (int64_t)z * g.I * g.J);
+    gw.x += v.x;
+    gw.y += v.y;
+  }
+  soft_item(g, n, kseg, lane, gw);
 }
 
 constexpr size_t kLds = 256 * 528;  // 132 KB: two pipeline stages (128 KB) or the padded bf16 output tile
@@ -588,6 +620,35 @@ static bool a16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 static int palette_splits(int64_t M, int64_t N, int64_t K) {
   return pick_splits(((N + TILE - 1) / TILE) * ((K + TILE - 1) / TILE), M);
 }
+
+// Splits of the soft backward's reduction over M. The fused epilogue needs the whole sum, so
+// an unsplit launch has one workgroup per 256x256 output tile: 40 for k/v_proj, 160 for
+// q/o_proj, 380 for the MLP shapes, i.e. whole or partial waves on 256 CUs. A split launch
+// writes each split's partial dW rows in fp32 and a streaming kernel sums them and runs the
+// soft epilogue. The count minimises a model of the two: (waves of 256 workgroups) x (stages
+// per split) x 2.4 us, plus, when split, 32 B per weight of epilogue traffic and 8 B per weight
+// and split of partials, at 5 TB/s. On the Qwen-4B shapes at M = 16384 it picks 6 / 3 / 2
+// splits, the measured optimum of each.
+static int soft_splits(int64_t M, int64_t N, int64_t K) {
+  const int64_t tiles = ((N + TILE - 1) / TILE) * ((K + TILE - 1) / TILE);
+  if (tiles == 0 || M <= 0) return 1;
+  const double weights = (double)N * (double)K;
+  const double stage_us = 2.4, epi_us = 32.0 * weights / 5.0e6, part_us = 8.0 * weights / 5.0e6;
+  int best = 1;
+  double best_t = (double)((tiles + 255) / 256) * (double)((M + BK - 1) / BK) * stage_us;
+  for (int z = 2; z <= 16; ++z) {
+    const int64_t len = split_len(M, z);
+    if (len < 8 * BK || (int64_t)(z - 1) * len >= M) break;  // >= 8 stages, no empty split
+    const double t = (double)((tiles * z + 255) / 256) * (double)(len / BK) * stage_us + epi_us +
+                     z * part_us;
+    if (t < best_t * 0.97) {
+      best_t = t;
+      best = z;
+    }
+  }
+  return best;
+}
+static size_t soft_pal_bytes(int64_t N, int64_t K) { return (size_t)N * (K / 128) * 4 * sizeof(float); }
 
 }  // namespace g2
 }  // namespace plz
@@ -731,9 +792,9 @@ int plz_linear_bwd_x_dense(const uint16_t* grad_y, const uint16_t* w, const uint
 }
 
 size_t plz_soft_bwd_workspace(int64_t M, int64_t N, int64_t K) {
-  (void)M;
   if (N <= 0 || K <= 0) return 0;
-  return (size_t)N * (K / 128) * 4 * sizeof(float);
+  const int z = soft_splits(M, N, K);
+  return soft_pal_bytes(N, K) + (z > 1 ? (size_t)z * N * K * sizeof(float) : 0);
 }
 
 int plz_soft_bwd(const uint16_t* x, const uint16_t* grad_y, const uint16_t* logits,
@@ -758,16 +819,28 @@ int plz_soft_bwd(const uint16_t* x, const uint16_t* grad_y, const uint16_t* logi
     set_error("plz_soft_bwd: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
     return PLZ_EWORKSPACE;
   }
+  const int z = soft_splits(M, N, K);
   Args g = {};
   g.a = grad_y; g.lda = N;
   g.b = x; g.ldb = K;
   g.pal = palette; g.Nw = N; g.Kw = K;
-  g.I = N; g.J = K; g.R = M; g.r_split = M > 0 ? M : 1;
+  g.I = N; g.J = K; g.R = M; g.r_split = z > 1 ? split_len(M, z) : (M > 0 ? M : 1);
   g.partial = reinterpret_cast<float*>(workspace);
+  g.acc_ws = z > 1 ? reinterpret_cast<float*>((char*)workspace + soft_pal_bytes(N, K)) : nullptr;
   g.logits = logits; g.noise = noise; g.inv_tau = 1.f / tau;
   g.glog_scale = scale_grad_by_inv_tau ? 1.f / tau : 1.f;
   g.grad_logits = grad_logits; g.logits_f16 = logits_dtype == PLZ_DT_FP16;
-  int rc = launch<OP_COL, OP_COL, EPI_SOFT>(g, 1, (hipStream_t)stream, "plz_soft_bwd");
+  int rc;
+  if (z == 1) {
+    rc = launch<OP_COL, OP_COL, EPI_SOFT>(g, 1, (hipStream_t)stream, "plz_soft_bwd");
+  } else {
+    rc = launch<OP_COL, OP_COL, EPI_F32>(g, z, (hipStream_t)stream, "plz_soft_bwd");
+    if (rc != PLZ_OK) return rc;
+    const int64_t items = N * (K / 128);
+    hipLaunchKernelGGL(soft_split_epilogue_kernel, dim3((unsigned)((items + 3) / 4)), dim3(256),
+                       0, (hipStream_t)stream, g, z);
+    rc = check_launch("plz_soft_bwd/epilogue");
+  }
   if (rc != PLZ_OK) return rc;
   const int64_t G = K / 256, n_out = N * G;
   hipLaunchKernelGGL(reduce_pal_kernel, dim3((unsigned)((n_out + 255) / 256)), dim3(256), 0,

@@ -89,6 +89,26 @@ def test_soft_bwd(dev, tau, scaled):
     assert_close(f32(gp), want_gp, max_rel=1e-3, min_cos=0.99999, what="grad_palette")
 
 
+@pytest.mark.parametrize("M,N,K", [(2048, 1024, 2560), (1100, 256, 512), (4160, 264, 768)])
+def test_soft_bwd_split_reduction(dev, M, N, K):
+    """Output grids too small for the GPU split the reduction over M; the last split of each
+    tile sums the partials in a fixed order and runs the epilogue (ragged M: a partial stage
+    in the last split; N = 264: a ragged tile row)."""
+    pal_bytes = N * (K // 128) * 16
+    assert ops.query("plz_soft_bwd_workspace", M, N, K) > pal_bytes, "expected a split launch"
+    logits, noise, pal = _soft_inputs(N, K, seed=M)
+    x = randn_bf16(M, K, seed=M + 1)
+    gy = randn_bf16(M, N, seed=M + 2)
+    args = (x.to(dev), gy.to(dev), logits.to(dev), noise.to(dev), pal.to(dev), 0.5)
+    gl, gp = ops.soft_bwd(*args)
+    want_gl, want_gp = O.soft_backward(f32(x), f32(gy), f32(logits), noise.numpy(), pal.numpy(),
+                                       0.5)
+    assert_close(f32(gl), want_gl, what="grad_logits (split)")
+    assert_close(f32(gp), want_gp, max_rel=1e-3, min_cos=0.99999, what="grad_palette (split)")
+    gl2, gp2 = ops.soft_bwd(*args)
+    assert torch.equal(gl, gl2) and torch.equal(gp, gp2), "split soft backward must be deterministic"
+
+
 def test_soft_bwd_fp16_logits(dev):
     M, N, K = 64, 128, 256
     logits, noise, pal = _soft_inputs(N, K, seed=8, dtype=torch.float16)
