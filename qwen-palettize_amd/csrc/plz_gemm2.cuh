@@ -66,31 +66,52 @@ struct Args {
 };
 
 // ---- dense operand copy, global -> LDS ---------------------------------------------------
-// Row tile from p[row*ld + r] (r contiguous): 2048 chunks, COPY_INSTS instructions per lane.
-__device__ __forceinline__ void copy_row_tile(lds_u8* lds, const uint16_t* p, int64_t ld,
-                                              int64_t row0, int64_t nrows, int64_t r0) {
+// Each lane's byte offsets of its COPY_INSTS 16-byte chunks are fixed for a tile; a stage adds
+// a wave-uniform offset (the buffer instruction's soffset), so the main loop's copies need no
+// per-lane address arithmetic. The host checks that every operand spans < 4 GiB.
+struct TileDma {
+  BufRsrc r;
+  uint32_t off[COPY_INSTS];
+};
+// Row tile from p[row*ld + r] (r contiguous): 2048 chunks; lane l of an instruction writes
+// LDS bytes base + 16*l, so the swizzle is applied to the global address each lane reads.
+// Stage offset: 2*r0 bytes.
+__device__ __forceinline__ TileDma row_tile_dma(const uint16_t* p, int64_t ld, int64_t row0,
+                                                int64_t nrows) {
+  TileDma d;
+  d.r = make_rsrc(p, (uint32_t)(nrows * ld * 2));
 #pragma unroll
   for (int it = 0; it < COPY_INSTS; ++it) {
     const int pch = it * NTHR + threadIdx.x;         // physical chunk written by this lane
     const int row = pch >> 3, c = (pch & 7) ^ row_swz(row);
     int64_t gr = row0 + row;
     gr = gr < nrows ? gr : nrows - 1;                 // rows past the end: any valid row
-    const uint16_t* src = p + gr * ld + r0 + c * 8;
-    __builtin_amdgcn_global_load_lds(src, lds + it * NTHR * 16 + (threadIdx.x & ~63) * 16, 16, 0, 0);
+    d.off[it] = (uint32_t)((gr * ld + c * 8) * 2);
   }
+  return d;
 }
-// Col tile from p[r*ld + row] (rows contiguous): 64 reduction rows x 32 chunks.
-__device__ __forceinline__ void copy_col_tile(lds_u8* lds, const uint16_t* p, int64_t ld,
-                                              int64_t row0, int64_t nrows, int64_t r0) {
+// Col tile from p[r*ld + row] (rows contiguous): 64 reduction rows x 32 chunks. Stage offset:
+// 2*r0*ld bytes.
+__device__ __forceinline__ TileDma col_tile_dma(const uint16_t* p, int64_t ld, int64_t row0,
+                                                int64_t nrows, int64_t rtotal) {
+  TileDma d;
+  d.r = make_rsrc(p, (uint32_t)(rtotal * ld * 2));
 #pragma unroll
   for (int it = 0; it < COPY_INSTS; ++it) {
     const int pch = it * NTHR + threadIdx.x;
     const int kr = pch >> 5, c = (pch & 31) ^ col_swz(kr);
     int64_t gr = row0 + c * 8;
     gr = gr < nrows ? gr : 0;                          // chunks past the end: any valid chunk
-    const uint16_t* src = p + (r0 + kr) * ld + gr;
-    __builtin_amdgcn_global_load_lds(src, lds + it * NTHR * 16 + (threadIdx.x & ~63) * 16, 16, 0, 0);
+    d.off[it] = (uint32_t)((kr * ld + gr) * 2);
   }
+  return d;
+}
+__device__ __forceinline__ void tile_copy(lds_u8* lds, const TileDma& d, uint32_t soff) {
+  const int wbase = __builtin_amdgcn_readfirstlane((threadIdx.x >> 6) * 1024);
+#pragma unroll
+  for (int it = 0; it < COPY_INSTS; ++it)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(d.r, lds + it * NTHR * 16 + wbase, 16, d.off[it],
+                                             soff, 0, 0);
 }
 
 // ---- palettized operand: one thread per (row n, 32 k) -------------------------------------
@@ -163,13 +184,29 @@ __device__ __forceinline__ void lut_col_store(uint4* lds, const LutRegs& r) {
 // then dequantises its own B fragments in registers: no dequantised tile is written to or
 // read from LDS (16-byte LDS writes cost ~2.7x the reads per byte on gfx950).
 constexpr int LUT_RAW_PAL = 256 * 16;  // byte offset of the palettes in the raw slot
-__device__ __forceinline__ void copy_lut_raw(lds_u8* lds, const Args& g, int64_t n0, int64_t k0) {
+struct LutDma {
+  BufRsrc r;
+  uint32_t off;
+};
+__device__ __forceinline__ LutDma lut_raw_dma(const Args& g, int64_t n0) {
   const int t = threadIdx.x, r = t & 255;
   int64_t n = n0 + r;
   n = n < g.Nw ? n : g.Nw - 1;  // rows past the end: any valid row (never stored)
-  const void* src = t < 256 ? (const void*)(g.packed + n * (g.Kw / 16) + k0 / 16)
-                            : (const void*)(g.pal + (n * (g.Kw / 256) + k0 / 256) * 4);
-  __builtin_amdgcn_global_load_lds(src, lds + (t & ~63) * 16, 16, 0, 0);
+  LutDma d;
+  if (__builtin_amdgcn_readfirstlane(t >> 8) == 0) {
+    d.r = make_rsrc(g.packed, (uint32_t)(g.Nw * (g.Kw / 4)));
+    d.off = (uint32_t)(n * (g.Kw / 16) * 4);
+  } else {
+    d.r = make_rsrc(g.pal, (uint32_t)(g.Nw * (g.Kw / 256) * 16));
+    d.off = (uint32_t)(n * (g.Kw / 256) * 16);
+  }
+  return d;
+}
+// stage at k0: 16 bytes of words (k0/4 bytes into the row) or the row's palette of group k0/256
+__device__ __forceinline__ void copy_lut_raw(lds_u8* lds, const LutDma& d, int64_t k0) {
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t soff = w < 4 ? (uint32_t)(k0 / 4) : (uint32_t)((k0 / 256) * 16);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(d.r, lds + w * 1024, 16, d.off, soff, 0, 0);
 }
 
 // ---- fragments (v_mfma_f32_32x32x16_bf16: lane l holds row l%32, k-slots 8*(l/32)..+7) --

@@ -153,6 +153,32 @@ __device__ __forceinline__ void mma_stage(const lds_u8* a_s, const lds_u8* b_s,
 // lanes 0..31 feed word 2p and lanes 32..63 word 2p+1 -- the first MFMA of the pair takes
 // weights 0..7 of each lane's word, the second weights 8..15. The A fragments read the
 // matching 16-byte chunks (chunk 4p + 2*(lane/32) + s), so the products are unchanged.
+//
+// The instruction order is fixed by hand (sched_barrier(0) between groups): each MFMA is
+// followed by a slice of the dequantisation of a word needed by a later MFMA, the LDS reads
+// of the next A fragments and the next stage's copies, so that the ~31 VALU per word issue
+// while the matrix core is busy. Only the first word of the stage is dequantised up front.
+struct DqPart {
+  uint32_t a[4], b[4];
+};
+// lookups of index group g (indices g, g+4, g+8, g+12 of the word)
+__device__ __forceinline__ void dq_part(uint32_t q, PalLut t, DqPart& d, int g) {
+  const uint32_t u = g == 0 ? (q & 0x03030303u) : ((q >> (2 * g)) & 0x03030303u);
+  const uint32_t l = perm(0, t.lo, u), h = perm(0, t.hi, u);
+  d.a[g] = perm(h, l, 0x05010400u);  // {w_g, w_g+4}
+  d.b[g] = perm(h, l, 0x07030602u);  // {w_g+8, w_g+12}
+}
+// the word's 8 dwords of bf16 pairs in natural k order (as dequant16)
+__device__ __forceinline__ void dq_final(const DqPart& d, uint32_t (&out)[8]) {
+  out[0] = perm(d.a[1], d.a[0], 0x05040100u);
+  out[1] = perm(d.a[3], d.a[2], 0x05040100u);
+  out[2] = perm(d.a[1], d.a[0], 0x07060302u);
+  out[3] = perm(d.a[3], d.a[2], 0x07060302u);
+  out[4] = perm(d.b[1], d.b[0], 0x05040100u);
+  out[5] = perm(d.b[3], d.b[2], 0x05040100u);
+  out[6] = perm(d.b[1], d.b[0], 0x07060302u);
+  out[7] = perm(d.b[3], d.b[2], 0x07060302u);
+}
 template <typename Dma>
 __device__ __forceinline__ void mma_stage_lutreg(const lds_u8* a_s, const lds_u8* b_s,
                                                  f32x16 (&acc)[WT_I][WT_J], int wi, int wj,
@@ -169,51 +195,74 @@ __device__ __forceinline__ void mma_stage_lutreg(const lds_u8* a_s, const lds_u8
     const f32x4 p = *reinterpret_cast<lds_f32x4*>(b_s + LUT_RAW_PAL + 16 * row);
     t[j] = make_lut(p[0], p[1], p[2], p[3]);
   }
-  auto afrags = [&](int p, int s2, bf16x8 (&a)[WT_I]) {
-#pragma unroll
-    for (int i = 0; i < WT_I; ++i)
-      a[i] = frag_row_chunk((const uint4*)a_s, wi * (32 * WT_I) + 32 * i, 4 * p + 2 * h + s2, lane);
+  // word of pair p for block j: lanes 0..31 word 2p, lanes 32..63 word 2p+1
+  auto word = [&](int p, int j) -> uint32_t {
+    return p == 0 ? (h ? qv[j][1] : qv[j][0]) : (h ? qv[j][3] : qv[j][2]);
   };
-  auto dequant_pair = [&](int p, uint32_t (&w)[WT_J][8]) {
+  auto afrag = [&](int p, int s2, int i) {
+    return frag_row_chunk((const uint4*)a_s, wi * (32 * WT_I) + 32 * i, 4 * p + 2 * h + s2, lane);
+  };
+  auto mfma = [&](int i, int j, bf16x8 a, const uint32_t (&w)[8], int s2) {
+    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+        a, __builtin_bit_cast(bf16x8, u32x4{w[4 * s2], w[4 * s2 + 1], w[4 * s2 + 2], w[4 * s2 + 3]}),
+        acc[i][j], 0, 0, 0);
+  };
+  uint32_t w[2][WT_J][8];  // dequantised words, [pair][block]
+  DqPart d;
+  bf16x8 a0[WT_I], a1[WT_I];
+  // up front: A fragments of (p0, s0) and the word of (p0, j0)
+#pragma unroll
+  for (int i = 0; i < WT_I; ++i) a0[i] = afrag(0, 0, i);
+#pragma unroll
+  for (int g = 0; g < 4; ++g) dq_part(word(0, 0), t[0], d, g);
+  dq_final(d, w[0][0]);
+  __builtin_amdgcn_sched_barrier(0);
+  // (p0, s0, j0) x 4 with word (p0, j1) and the A fragments of (p0, s1)
+#pragma unroll
+  for (int i = 0; i < WT_I; ++i) {
+    mfma(i, 0, a0[i], w[0][0], 0);
+    dq_part(word(0, 1), t[1], d, i);
+    if (i == WT_I - 1) dq_final(d, w[0][1]);
+    a1[i] = afrag(0, 1, i);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  // (p0, s0, j1) x 4 with word (p1, j0) and the next stage's copies
+#pragma unroll
+  for (int i = 0; i < WT_I; ++i) {
+    mfma(i, 1, a0[i], w[0][1], 0);
+    dq_part(word(1, 0), t[0], d, i);
+    if (i == WT_I - 1) dq_final(d, w[1][0]);
+    if (i == 0) dma();
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  // (p0, s1, j0..1) x 8 with word (p1, j1) and the A fragments of (p1, s0)
+#pragma unroll
+  for (int i = 0; i < WT_I; ++i) {
 #pragma unroll
     for (int j = 0; j < WT_J; ++j) {
-      const uint32_t q = p == 0 ? (h ? qv[j][1] : qv[j][0]) : (h ? qv[j][3] : qv[j][2]);
-      dequant16(q, t[j], w[j]);
+      mfma(i, j, a1[i], w[0][j], 1);
+      if (j == 0) dq_part(word(1, 1), t[1], d, i);
+      if (j == 1) a0[i] = afrag(1, 0, i);
+      __builtin_amdgcn_sched_barrier(0);
     }
-  };
-  auto mma = [&](const bf16x8 (&a)[WT_I], const uint32_t (&w)[WT_J][8], int s2) {
+  }
+  dq_final(d, w[1][1]);
+  __builtin_amdgcn_sched_barrier(0);
+  // (p1, s0) x 8 with the A fragments of (p1, s1)
 #pragma unroll
-    for (int i = 0; i < WT_I; ++i)
+  for (int i = 0; i < WT_I; ++i) {
 #pragma unroll
-      for (int j = 0; j < WT_J; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-            a[i], __builtin_bit_cast(bf16x8, u32x4{w[j][4 * s2], w[j][4 * s2 + 1],
-                                                   w[j][4 * s2 + 2], w[j][4 * s2 + 3]}),
-            acc[i][j], 0, 0, 0);
-  };
-  constexpr int NREAD = WT_I;
-  constexpr int NDMA = COPY_INSTS + 1;
-  bf16x8 a0[WT_I], a1[WT_I];
-  uint32_t w0[WT_J][8], w1[WT_J][8];
-  afrags(0, 0, a0);
-  dequant_pair(0, w0);
-  __builtin_amdgcn_sched_barrier(0);
-  afrags(0, 1, a1);
-  dma();
-  mma(a0, w0, 0);
-  interleave_kstep<NREAD, NDMA, 0, 0>();
-  __builtin_amdgcn_sched_barrier(0);
-  afrags(1, 0, a0);
-  mma(a1, w0, 1);
-  dequant_pair(1, w1);
-  interleave_kstep<NREAD, 0, 2 * 31, 0>();
-  __builtin_amdgcn_sched_barrier(0);
-  afrags(1, 1, a1);
-  mma(a0, w1, 0);
-  interleave_kstep<NREAD, 0, 0, 0>();
-  __builtin_amdgcn_sched_barrier(0);
-  mma(a1, w1, 1);
-  interleave_kstep<0, 0, 0, 0>();
+    for (int j = 0; j < WT_J; ++j) {
+      mfma(i, j, a0[i], w[1][j], 0);
+      if (j == 1) a1[i] = afrag(1, 1, i);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  // (p1, s1) x 8
+#pragma unroll
+  for (int i = 0; i < WT_I; ++i)
+#pragma unroll
+    for (int j = 0; j < WT_J; ++j) mfma(i, j, a1[i], w[1][j], 1);
   __builtin_amdgcn_sched_barrier(0);
 }
 
@@ -338,26 +387,30 @@ __global__ __launch_bounds__(NTHR) void gemm2_kernel(const Args g) {
     if (KB == OP_LUT_ROW) lut_row_load(g, j0, r0, r);
     if (KB == OP_LUT_COL) lut_col_load(g, j0, r0, r);
   };
+  // this tile's copy plans (per-lane offsets; stages add uniform offsets)
+  TileDma dA, dB;
+  LutDma dL;
+  if (KA == OP_ROW) dA = row_tile_dma(g.a, g.lda, i0, g.I);
+  else dA = col_tile_dma(g.a, g.lda, i0, g.I, g.R);
+  if (KB == OP_ROW) dB = row_tile_dma(g.b, g.ldb, j0, g.J);
+  if (KB == OP_COL) dB = col_tile_dma(g.b, g.ldb, j0, g.J, g.R);
+  if (KB == OP_LUT_REG) dL = lut_raw_dma(g, j0);
+  auto copy_stage = [&](lds_u8* As, lds_u8* Bs, int64_t r0) {
+    tile_copy(As, dA, (uint32_t)(KA == OP_ROW ? r0 * 2 : r0 * g.lda * 2));
+    if (KB == OP_ROW) tile_copy(Bs, dB, (uint32_t)(r0 * 2));
+    else if (KB == OP_COL) tile_copy(Bs, dB, (uint32_t)(r0 * g.ldb * 2));
+    else if (KB == OP_LUT_REG) copy_lut_raw(Bs, dL, r0);
+  };
   auto issue_full = [&](int s, int kt) {
     lds_u8* As = lbase + s * 2 * TILE_BYTES;
     lds_u8* Bs = As + TILE_BYTES;
-    const int64_t r0 = rbeg + (int64_t)kt * BK;
-    if (KA == OP_ROW) copy_row_tile(As, g.a, g.lda, i0, g.I, r0);
-    else copy_col_tile(As, g.a, g.lda, i0, g.I, r0);
-    if (KB == OP_ROW) copy_row_tile(Bs, g.b, g.ldb, j0, g.J, r0);
-    else if (KB == OP_COL) copy_col_tile(Bs, g.b, g.ldb, j0, g.J, r0);
-    else if (KB == OP_LUT_REG) copy_lut_raw(Bs, g, j0, r0);
+    copy_stage(As, Bs, rbeg + (int64_t)kt * BK);
   };
   auto issue = [&](int s, int kt) {
     lds_u8* As = lbase + s * 2 * TILE_BYTES;
     lds_u8* Bs = As + TILE_BYTES;
     if (kt < nfull) {
-      const int64_t r0 = rbeg + (int64_t)kt * BK;
-      if (KA == OP_ROW) copy_row_tile(As, g.a, g.lda, i0, g.I, r0);
-      else copy_col_tile(As, g.a, g.lda, i0, g.I, r0);
-      if (KB == OP_ROW) copy_row_tile(Bs, g.b, g.ldb, j0, g.J, r0);
-      else if (KB == OP_COL) copy_col_tile(Bs, g.b, g.ldb, j0, g.J, r0);
-      else if (KB == OP_LUT_REG) copy_lut_raw(Bs, g, j0, r0);
+      copy_stage(As, Bs, rbeg + (int64_t)kt * BK);
     } else if (tail && kt == nfull) {
       const int64_t r0 = rbeg + (int64_t)nfull * BK;
       if (KA == OP_ROW) copy_row_tile_masked((uint4*)As, g.a, g.lda, i0, g.I, r0, rend);
@@ -572,6 +625,15 @@ static int launch(Args g, int splits, hipStream_t stream, const char* what) {
   }
   const int64_t tiles = (int64_t)g.tiles_i * g.tiles_j;
   if (tiles == 0 || splits == 0) return PLZ_OK;
+  // the copies address each operand through a 32-bit buffer offset
+  const int64_t lim = (int64_t)1 << 32;
+  const int64_t a_bytes = (KA == OP_ROW ? g.I : g.R) * g.lda * 2;
+  const int64_t b_bytes = KB == OP_ROW ? g.J * g.ldb * 2 : KB == OP_COL ? g.R * g.ldb * 2 : 0;
+  const int64_t l_bytes = KB == OP_LUT_REG ? g.Nw * (g.Kw / 4) : 0;
+  if (a_bytes >= lim || b_bytes >= lim || l_bytes >= lim) {
+    set_error("%s: an operand spans 4 GiB or more", what);
+    return PLZ_EUNSUPPORTED;
+  }
   hipLaunchKernelGGL(kern, dim3((unsigned)tiles, 1, (unsigned)splits), dim3(NTHR), kLds, stream, g);
   return check_launch(what);
 }
