@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define PLZ_ABI_VERSION 3
+#define PLZ_ABI_VERSION 4
 
 /* status codes */
 #define PLZ_OK 0
@@ -71,14 +71,22 @@ int plz_dequant(const int32_t* packed, const float* palette, uint16_t* w, int64_
  * QwenLoRA.forward (qwen_model.py:291-304). */
 int plz_lut_linear_fwd(const uint16_t* x, const int32_t* packed, const float* palette,
                        const uint16_t* bias, const uint16_t* lora_t, const uint16_t* lora_b,
-                       int rank, uint16_t* y, int64_t M, int64_t N, int64_t K, void* stream);
+                       int rank, uint16_t* y, void* workspace, size_t workspace_bytes, int64_t M,
+                       int64_t N, int64_t K, void* stream);
+/* Optional workspace of the four one-pass GEMMs (lut fwd / bwd_x, dense fwd / bwd_x): when the
+ * output tiles leave a last, partial wave on the GPU, those tiles are split over the
+ * reduction and summed by a second kernel (fp32 partials in the workspace). NULL disables the
+ * split; a smaller non-NULL workspace than the query returns PLZ_EWORKSPACE. 0 = no split. */
+size_t plz_lut_linear_fwd_workspace(int64_t M, int64_t N, int64_t K);
 
 /* grad_x[M,K] = grad_y[M,N] W (+ lora_gt[M,rank] lora_a[rank,K]).
  * Replaces the grad_x half of fused_lut_linear_bwd (fused_lut_linear_cuda.py:119-150) and
  * fused_lut_linear_bwd_grad_x_tc_kernel (fused_lut_kernel.cu:551-720). */
 int plz_lut_linear_bwd_x(const uint16_t* grad_y, const int32_t* packed, const float* palette,
                          const uint16_t* lora_gt, const uint16_t* lora_a, int rank,
-                         uint16_t* grad_x, int64_t M, int64_t N, int64_t K, void* stream);
+                         uint16_t* grad_x, void* workspace, size_t workspace_bytes, int64_t M,
+                         int64_t N, int64_t K, void* stream);
+size_t plz_lut_linear_bwd_x_workspace(int64_t M, int64_t N, int64_t K);
 
 /* grad_palette fp32 [N, K/256, 4]: grad_palette[n,g,c] = sum over k in group g with
  * idx[n,k] == c of (grad_y^T x)[n,k]. Deterministic (fixed-order two-stage reduction).
@@ -98,12 +106,16 @@ int plz_bias_grad(const uint16_t* grad_y, float* grad_bias, int64_t M, int64_t N
  * CUDAFusedLUTLinearSoft.forward (fused_lut_linear_cuda.py:912). K, N multiples of 8. */
 int plz_linear_fwd_dense(const uint16_t* x, const uint16_t* w, const uint16_t* bias,
                          const uint16_t* lora_t, const uint16_t* lora_b, int rank, uint16_t* y,
-                         int64_t M, int64_t N, int64_t K, void* stream);
+                         void* workspace, size_t workspace_bytes, int64_t M, int64_t N, int64_t K,
+                         void* stream);
+size_t plz_linear_fwd_dense_workspace(int64_t M, int64_t N, int64_t K);
 /* grad_x = grad_y w (+lora). Replaces torch.matmul(grad_y, W.T)
  * (fused_lut_linear_cuda.py:944). */
 int plz_linear_bwd_x_dense(const uint16_t* grad_y, const uint16_t* w, const uint16_t* lora_gt,
-                           const uint16_t* lora_a, int rank, uint16_t* grad_x, int64_t M,
-                           int64_t N, int64_t K, void* stream);
+                           const uint16_t* lora_a, int rank, uint16_t* grad_x, void* workspace,
+                           size_t workspace_bytes, int64_t M, int64_t N, int64_t K,
+                           void* stream);
+size_t plz_linear_bwd_x_dense_workspace(int64_t M, int64_t N, int64_t K);
 
 /* ---- soft (Gumbel-softmax) path --------------------------------------------------- */
 /* noise fp32 [n] = -log(-log(u)), u from Philox4x32-10 (Salmon et al., SC'11) keyed by

@@ -61,6 +61,12 @@ struct Args {
   const uint16_t* logits; const float* noise; float inv_tau, glog_scale; uint16_t* grad_logits;
   int logits_f16;
   float* acc_ws;  // EPI_F32: partial dW rows of each reduction split, [split][I][J] fp32
+  // EPI_BF16 tail split: tiles [tail_first, tiles) run as tail_split reduction parts of
+  // tail_len each, whose fp32 accumulators go to tail_ws (accumulator layout, 256 KB per part);
+  // tail_reduce_kernel sums them and stores the tiles
+  int tail_first, tail_split;
+  int64_t tail_len;
+  float* tail_ws;
   int tiles_i, tiles_j;
   int group;  // tile-rows walked together (1: consecutive workgroups share the A panel)
 };

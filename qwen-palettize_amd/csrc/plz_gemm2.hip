@@ -329,6 +329,55 @@ __device__ __forceinline__ void soft_item(const Args& g, int64_t n, int64_t kseg
   }
 }
 
+// Tile of work item bid: tile-columns are walked within groups of `group` tile-rows.
+__device__ __forceinline__ void tile_of(const Args& g, int bid, int& tile_i, int& tile_j) {
+  const int per_group = g.group * g.tiles_j;
+  const int first_i = (bid / per_group) * g.group;
+  const int gsz = min(g.tiles_i - first_i, g.group);
+  tile_i = first_i + (bid % per_group) % gsz;
+  tile_j = (bid % per_group) / gsz;
+}
+
+// bf16 epilogue: C = alpha * acc (+ bias). The tile is staged in LDS (rows padded to 528 B so
+// the two 64-byte row segments a wave writes per instruction fall in different banks), then
+// written out with 16-byte coalesced stores: 16 per thread instead of 128 scattered 2-byte
+// stores. acc[ti][tj][e]: row wi*128 + 32*ti + 8*(e/4) + 4*(lane/32) + e%4,
+// col wj*64 + 32*tj + lane%32.
+constexpr int EPI_RS = 528;  // staging row stride in bytes
+__device__ __forceinline__ void store_tile_bf16(const Args& g, const f32x16 (&acc)[WT_I][WT_J],
+                                                lds_u8* st, int64_t i0, int64_t j0, int wi,
+                                                int wj, int lane) {
+  float bj[WT_J];
+#pragma unroll
+  for (int tj = 0; tj < WT_J; ++tj) {
+    const int64_t j = j0 + wj * (32 * WT_J) + 32 * tj + (lane & 31);
+    bj[tj] = (g.bias && j < g.J) ? bf2f(g.bias[j]) : 0.f;
+  }
+#pragma unroll
+  for (int ti = 0; ti < WT_I; ++ti)
+#pragma unroll
+    for (int tj = 0; tj < WT_J; ++tj)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int row = wi * (32 * WT_I) + 32 * ti + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+        const int col = wj * (32 * WT_J) + 32 * tj + (lane & 31);
+        *reinterpret_cast<__attribute__((address_space(3))) uint16_t*>(st + row * EPI_RS + col * 2) =
+            (uint16_t)f2bf(g.alpha * acc[ti][tj][e] + bj[tj]);
+      }
+  __syncthreads();
+  uint16_t* C = reinterpret_cast<uint16_t*>(g.c);
+#pragma unroll 4
+  for (int it = 0; it < TILE * TILE / 8 / NTHR; ++it) {
+    const int ch = it * NTHR + threadIdx.x;  // 32 chunks of 8 columns per row
+    const int row = ch >> 5, c8 = (ch & 31) * 8;
+    const int64_t i = i0 + row, j = j0 + c8;
+    if (i < g.I && j < g.J) {
+      const u32x4 v = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(st + row * EPI_RS + c8 * 2);
+      *reinterpret_cast<u32x4*>(C + i * g.ldc + j) = v;
+    }
+  }
+}
+
 template <int KA, int KB, int EPI>
 __global__ __launch_bounds__(NTHR) void gemm2_kernel(const Args g) {
   extern __shared__ uint4 smem[];
@@ -339,22 +388,29 @@ __global__ __launch_bounds__(NTHR) void gemm2_kernel(const Args g) {
   // Workgroups go to the 8 XCDs round-robin by linear id, and each XCD has its own L2. The
   // (split, tile) items are renumbered so that XCD x runs one contiguous range of them:
   // the ~32 workgroups resident on an XCD then share operand panels in that XCD's L2.
+  // A tail-split launch (EPI_BF16) renumbers its tail_first whole tiles this way; the
+  // workgroups after them (the last, partial wave) each run one reduction part of a tail tile.
   const int T = g.tiles_i * g.tiles_j;
-  const int total = T * (int)gridDim.z;
-  const int lin = (int)blockIdx.x + T * (int)blockIdx.z;
-  const int xcd = lin % 8, q8 = total / 8, r8 = total % 8;
-  const int item = xcd * q8 + min(xcd, r8) + lin / 8;
-  const int zsl = item / T;
-  const int bid = item % T;
-  const int GROUP = g.group;
-  const int per_group = GROUP * g.tiles_j;
-  const int first_i = (bid / per_group) * GROUP;
-  const int gsz = min(g.tiles_i - first_i, GROUP);
-  const int tile_i = first_i + (bid % per_group) % gsz;
-  const int tile_j = (bid % per_group) / gsz;
+  const bool tail_part = EPI == EPI_BF16 && g.tail_split > 1 && (int)blockIdx.x >= g.tail_first;
+  int zsl = 0, bid = 0, part = 0;
+  if (tail_part) {
+    const int u = (int)blockIdx.x - g.tail_first;
+    bid = g.tail_first + u / g.tail_split;
+    part = u % g.tail_split;
+  } else {
+    const int whole = EPI == EPI_BF16 && g.tail_split > 1 ? g.tail_first : T;
+    const int total = whole * (int)gridDim.z;
+    const int lin = (int)blockIdx.x + whole * (int)blockIdx.z;
+    const int xcd = lin % 8, q8 = total / 8, r8 = total % 8;
+    const int item = xcd * q8 + min(xcd, r8) + lin / 8;
+    zsl = item / whole;
+    bid = item % whole;
+  }
+  int tile_i, tile_j;
+  tile_of(g, bid, tile_i, tile_j);
   const int64_t i0 = (int64_t)tile_i * TILE, j0 = (int64_t)tile_j * TILE;
-  const int64_t rbeg = (int64_t)zsl * g.r_split;
-  const int64_t rend = min(g.R, rbeg + g.r_split);
+  const int64_t rbeg = tail_part ? (int64_t)part * g.tail_len : (int64_t)zsl * g.r_split;
+  const int64_t rend = min(g.R, rbeg + (tail_part ? g.tail_len : g.r_split));
   const int64_t rlen = rend > rbeg ? rend - rbeg : 0;
   const int nfull = (int)(rlen / BK);
 
@@ -374,7 +430,7 @@ __global__ __launch_bounds__(NTHR) void gemm2_kernel(const Args g) {
   // have the same LDS layouts as the main ones (A row-major; B row tile in the forward,
   // col tile in grad_x), so every stage runs the same MFMA body.
   const bool tail = (rlen % BK) != 0;
-  const bool lora = EPI == EPI_BF16 && g.R2 > 0 && zsl == 0;
+  const bool lora = EPI == EPI_BF16 && g.R2 > 0 && zsl == 0 && part == 0;
   const int nst = nfull + (tail ? 1 : 0) + (lora ? 1 : 0);
 
   // The palette operand's registers are loaded one stage ahead of the copies: during stage
@@ -482,40 +538,21 @@ __global__ __launch_bounds__(NTHR) void gemm2_kernel(const Args g) {
   // acc[ti][tj][e]: row wi*128 + 32*ti + 8*(e/4) + 4*(lane/32) + e%4,
   //                 col wj*64 + 32*tj + lane%32
   if (EPI == EPI_BF16) {
-    // Stage the bf16 tile in LDS (rows padded to 528 B so the two 64-byte row segments a
-    // wave writes per instruction fall in different banks), then write it out with 16-byte
-    // coalesced stores: 16 per thread instead of 128 scattered 2-byte stores.
-    constexpr int RS = 528;  // staging row stride in bytes
-    lds_u8* st = lbase;
-    float bj[WT_J];
+    if (tail_part) {  // this part's accumulators, coalesced: [part][32 float4][thread]
+      float4* dst = reinterpret_cast<float4*>(g.tail_ws) +
+                    ((int64_t)(bid - g.tail_first) * g.tail_split + part) * (TILE * TILE / 4);
 #pragma unroll
-    for (int tj = 0; tj < WT_J; ++tj) {
-      const int64_t j = j0 + wj * (32 * WT_J) + 32 * tj + (lane & 31);
-      bj[tj] = (g.bias && j < g.J) ? bf2f(g.bias[j]) : 0.f;
+      for (int ti = 0; ti < WT_I; ++ti)
+#pragma unroll
+        for (int tj = 0; tj < WT_J; ++tj)
+#pragma unroll
+          for (int e4 = 0; e4 < 4; ++e4)
+            dst[((ti * WT_J + tj) * 4 + e4) * NTHR + threadIdx.x] =
+                make_float4(acc[ti][tj][4 * e4], acc[ti][tj][4 * e4 + 1],
+                            acc[ti][tj][4 * e4 + 2], acc[ti][tj][4 * e4 + 3]);
+      return;
     }
-#pragma unroll
-    for (int ti = 0; ti < WT_I; ++ti)
-#pragma unroll
-      for (int tj = 0; tj < WT_J; ++tj)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int row = wi * (32 * WT_I) + 32 * ti + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-          const int col = wj * (32 * WT_J) + 32 * tj + (lane & 31);
-          *reinterpret_cast<__attribute__((address_space(3))) uint16_t*>(st + row * RS + col * 2) =
-              (uint16_t)f2bf(g.alpha * acc[ti][tj][e] + bj[tj]);
-        }
-    __syncthreads();
-    uint16_t* C = reinterpret_cast<uint16_t*>(g.c);
-#pragma unroll 4
-    for (int it = 0; it < TILE * TILE / 8 / NTHR; ++it) {
-      const int ch = it * NTHR + threadIdx.x;  // 32 chunks of 8 columns per row
-      const int row = ch >> 5, c8 = (ch & 31) * 8;
-      const int64_t i = i0 + row, j = j0 + c8;
-      if (i < g.I && j < g.J) {
-        const u32x4 v = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(st + row * RS + c8 * 2);
-        *reinterpret_cast<u32x4*>(C + i * g.ldc + j) = v;
-      }
-    }
+    store_tile_bf16(g, acc, lbase, i0, j0, wi, wj, lane);
     return;
   }
 
@@ -604,6 +641,42 @@ __global__ __launch_bounds__(256) void soft_split_epilogue_kernel(const Args g, 
   soft_item(g, n, kseg, lane, gw);
 }
 
+// Tail tiles of a split launch: sum each tile's reduction parts in part order (deterministic)
+// and store it as the unsplit kernel would. One workgroup of 512 threads per tile, each thread
+// owning the accumulators the same thread of the GEMM held.
+__global__ __launch_bounds__(NTHR) void tail_reduce_kernel(const Args g) {
+  extern __shared__ uint4 smem[];
+  const int bid = g.tail_first + (int)blockIdx.x;
+  int tile_i, tile_j;
+  tile_of(g, bid, tile_i, tile_j);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const float4* src = reinterpret_cast<const float4*>(g.tail_ws) +
+                      (int64_t)blockIdx.x * g.tail_split * (TILE * TILE / 4);
+  f32x16 acc[WT_I][WT_J];
+#pragma unroll
+  for (int ti = 0; ti < WT_I; ++ti)
+#pragma unroll
+    for (int tj = 0; tj < WT_J; ++tj)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[ti][tj][e] = 0.f;
+  for (int p = 0; p < g.tail_split; ++p) {
+#pragma unroll
+    for (int ti = 0; ti < WT_I; ++ti)
+#pragma unroll
+      for (int tj = 0; tj < WT_J; ++tj)
+#pragma unroll
+        for (int e4 = 0; e4 < 4; ++e4) {
+          const float4 v = src[(int64_t)p * (TILE * TILE / 4) + ((ti * WT_J + tj) * 4 + e4) * NTHR + threadIdx.x];
+          acc[ti][tj][4 * e4] += v.x;
+          acc[ti][tj][4 * e4 + 1] += v.y;
+          acc[ti][tj][4 * e4 + 2] += v.z;
+          acc[ti][tj][4 * e4 + 3] += v.w;
+        }
+  }
+  store_tile_bf16(g, acc, (lds_u8*)smem, (int64_t)tile_i * TILE, (int64_t)tile_j * TILE,
+                  wave / WAVES_J, wave % WAVES_J, lane);
+}
+
 constexpr size_t kLds = 256 * 528;  // 132 KB: two pipeline stages (128 KB) or the padded bf16 output tile
 
 template <int KA, int KB, int EPI>
@@ -634,7 +707,23 @@ static int launch(Args g, int splits, hipStream_t stream, const char* what) {
     set_error("%s: an operand spans 4 GiB or more", what);
     return PLZ_EUNSUPPORTED;
   }
-  hipLaunchKernelGGL(kern, dim3((unsigned)tiles, 1, (unsigned)splits), dim3(NTHR), kLds, stream, g);
+  const bool tail = EPI == EPI_BF16 && g.tail_split > 1;
+  const int64_t gx = tail ? g.tail_first + (tiles - g.tail_first) * g.tail_split : tiles;
+  hipLaunchKernelGGL(kern, dim3((unsigned)gx, 1, (unsigned)splits), dim3(NTHR), kLds, stream, g);
+  int rc = check_launch(what);
+  if (rc != PLZ_OK || !tail) return rc;
+  static bool rattr = false;
+  if (!rattr) {
+    hipError_t e = hipFuncSetAttribute((const void*)tail_reduce_kernel,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLds);
+    if (e != hipSuccess) {
+      set_error("%s: cannot reserve %zu bytes of LDS: %s", what, kLds, hipGetErrorString(e));
+      return PLZ_EHIP;
+    }
+    rattr = true;
+  }
+  hipLaunchKernelGGL(tail_reduce_kernel, dim3((unsigned)(tiles - g.tail_first)), dim3(NTHR), kLds,
+                     stream, g);
   return check_launch(what);
 }
 
@@ -658,6 +747,72 @@ static int pick_splits(int64_t tiles, int64_t R) {
 static int64_t split_len(int64_t R, int z) {
   const int64_t per = (R + z - 1) / z;
   return (per + BK - 1) / BK * BK;
+}
+
+static int cu_count() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cache[dev] == 0) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        v <= 0)
+      v = 256;
+    cache[dev] = v;
+  }
+  return cache[dev];
+}
+
+// Tail split of a one-workgroup-per-tile GEMM (one workgroup per CU): when the tiles leave a
+// last, partial wave of rem < CUs/2 tiles, those tiles run as s = CUs/rem reduction parts
+// each, so the last wave takes 1/s of a tile-time. Taken when the time saved (2.15 us per
+// 256x256x64 stage) exceeds the cost of the fp32 partials (256 KB per part written and read
+// at ~5 TB/s) and one more launch.
+struct TailPlan {
+  int first = 0, split = 1;
+  int64_t len = 0;
+};
+static TailPlan tail_plan(int64_t I, int64_t J, int64_t R) {
+  TailPlan t;
+  const int64_t tiles = ((I + TILE - 1) / TILE) * ((J + TILE - 1) / TILE);
+  const int64_t C = cu_count();
+  const int64_t rem = tiles % C;
+  if (rem == 0 || R <= 0) return t;
+  const int64_t stages = (R + BK - 1) / BK;
+  int s = (int)(C / rem);
+  s = s < 16 ? s : 16;
+  while (s > 1 && (stages / s < 8 || (int64_t)(s - 1) * split_len(R, s) >= R)) --s;
+  if (s < 2) return t;
+  const double gain = (double)stages * 2.15 * (1.0 - 1.0 / s);
+  const double cost = (double)rem * s * 2.0 * TILE * TILE * 4 / 5.0e6 + 5.0;
+  if (gain <= cost) return t;
+  t.first = (int)(tiles - rem);
+  t.split = s;
+  t.len = split_len(R, s);
+  return t;
+}
+static size_t tail_bytes(int64_t I, int64_t J, int64_t R) {
+  const TailPlan t = tail_plan(I, J, R);
+  if (t.split < 2) return 0;
+  const int64_t tiles = ((I + TILE - 1) / TILE) * ((J + TILE - 1) / TILE);
+  return (size_t)(tiles - t.first) * t.split * TILE * TILE * sizeof(float);
+}
+// Sets g's tail fields from the plan; no workspace means no split.
+static int set_tail(Args& g, void* workspace, size_t workspace_bytes, const char* what) {
+  g.tail_split = 1;
+  if (!workspace) return PLZ_OK;
+  const size_t need = tail_bytes(g.I, g.J, g.R);
+  if (need == 0) return PLZ_OK;
+  if (workspace_bytes < need) {
+    set_error("%s: workspace of %zu bytes needed, %zu given", what, need, workspace_bytes);
+    return PLZ_EWORKSPACE;
+  }
+  const TailPlan t = tail_plan(g.I, g.J, g.R);
+  g.tail_first = t.first;
+  g.tail_split = t.split;
+  g.tail_len = t.len;
+  g.tail_ws = reinterpret_cast<float*>(workspace);
+  return PLZ_OK;
 }
 
 __global__ void reduce_pal_kernel(const float* __restrict__ partial, float* __restrict__ out,
@@ -720,9 +875,14 @@ using namespace plz::g2;
 
 extern "C" {
 
+size_t plz_lut_linear_fwd_workspace(int64_t M, int64_t N, int64_t K) {
+  return M > 0 && N > 0 && K > 0 ? tail_bytes(M, N, K) : 0;
+}
+
 int plz_lut_linear_fwd(const uint16_t* x, const int32_t* packed, const float* palette,
                        const uint16_t* bias, const uint16_t* lora_t, const uint16_t* lora_b,
-                       int rank, uint16_t* y, int64_t M, int64_t N, int64_t K, void* stream) {
+                       int rank, uint16_t* y, void* workspace, size_t workspace_bytes, int64_t M,
+                       int64_t N, int64_t K, void* stream) {
   PLZ_REQUIRE(M >= 0 && N >= 0 && K >= 0, "plz_lut_linear_fwd: negative shape");
   PLZ_REQUIRE(K % 256 == 0, "plz_lut_linear_fwd: K (%lld) must be a multiple of 256", (long long)K);
   PLZ_REQUIRE(N % 8 == 0, "plz_lut_linear_fwd: N (%lld) must be a multiple of 8", (long long)N);
@@ -741,12 +901,19 @@ int plz_lut_linear_fwd(const uint16_t* x, const int32_t* packed, const float* pa
   g.a2 = lora_t; g.b2 = lora_b; g.R2 = rank;
   g.c = y; g.ldc = N; g.bias = bias; g.alpha = 1.f;
   g.group = 1;
+  const int rc = set_tail(g, workspace, workspace_bytes, "plz_lut_linear_fwd");
+  if (rc != PLZ_OK) return rc;
   return launch<OP_ROW, OP_LUT_REG, EPI_BF16>(g, 1, (hipStream_t)stream, "plz_lut_linear_fwd");
+}
+
+size_t plz_lut_linear_bwd_x_workspace(int64_t M, int64_t N, int64_t K) {
+  return M > 0 && N > 0 && K > 0 ? tail_bytes(M, K, N) : 0;
 }
 
 int plz_lut_linear_bwd_x(const uint16_t* grad_y, const int32_t* packed, const float* palette,
                          const uint16_t* lora_gt, const uint16_t* lora_a, int rank,
-                         uint16_t* grad_x, int64_t M, int64_t N, int64_t K, void* stream) {
+                         uint16_t* grad_x, void* workspace, size_t workspace_bytes, int64_t M,
+                         int64_t N, int64_t K, void* stream) {
   PLZ_REQUIRE(M >= 0 && N >= 0 && K >= 0, "plz_lut_linear_bwd_x: negative shape");
   PLZ_REQUIRE(K % 256 == 0, "plz_lut_linear_bwd_x: K (%lld) must be a multiple of 256",
               (long long)K);
@@ -766,6 +933,8 @@ int plz_lut_linear_bwd_x(const uint16_t* grad_y, const int32_t* packed, const fl
   g.a2 = lora_gt; g.b2 = lora_a; g.R2 = rank;
   g.c = grad_x; g.ldc = K; g.alpha = 1.f;
   g.group = 1;
+  const int rc = set_tail(g, workspace, workspace_bytes, "plz_lut_linear_bwd_x");
+  if (rc != PLZ_OK) return rc;
   return launch<OP_ROW, OP_LUT_COL, EPI_BF16>(g, 1, (hipStream_t)stream, "plz_lut_linear_bwd_x");
 }
 
@@ -812,9 +981,14 @@ int plz_lut_linear_bwd_palette(const uint16_t* x, const uint16_t* grad_y, const 
   return check_launch("plz_lut_linear_bwd_palette/reduce");
 }
 
+size_t plz_linear_fwd_dense_workspace(int64_t M, int64_t N, int64_t K) {
+  return M > 0 && N > 0 && K > 0 ? tail_bytes(M, N, K) : 0;
+}
+
 int plz_linear_fwd_dense(const uint16_t* x, const uint16_t* w, const uint16_t* bias,
                          const uint16_t* lora_t, const uint16_t* lora_b, int rank, uint16_t* y,
-                         int64_t M, int64_t N, int64_t K, void* stream) {
+                         void* workspace, size_t workspace_bytes, int64_t M, int64_t N, int64_t K,
+                         void* stream) {
   PLZ_REQUIRE(M >= 0 && N >= 0 && K >= 0, "plz_linear_fwd_dense: negative shape");
   PLZ_REQUIRE(K % 8 == 0 && N % 8 == 0, "plz_linear_fwd_dense: K and N must be multiples of 8");
   PLZ_REQUIRE(rank >= 0 && rank <= BK && rank % 8 == 0,
@@ -829,12 +1003,20 @@ int plz_linear_fwd_dense(const uint16_t* x, const uint16_t* w, const uint16_t* b
   g.I = M; g.J = N; g.R = K;
   g.a2 = lora_t; g.b2 = lora_b; g.R2 = rank;
   g.c = y; g.ldc = N; g.bias = bias; g.alpha = 1.f;
+  g.group = 8;
+  const int rc = set_tail(g, workspace, workspace_bytes, "plz_linear_fwd_dense");
+  if (rc != PLZ_OK) return rc;
   return launch<OP_ROW, OP_ROW, EPI_BF16>(g, 1, (hipStream_t)stream, "plz_linear_fwd_dense");
 }
 
+size_t plz_linear_bwd_x_dense_workspace(int64_t M, int64_t N, int64_t K) {
+  return M > 0 && N > 0 && K > 0 ? tail_bytes(M, K, N) : 0;
+}
+
 int plz_linear_bwd_x_dense(const uint16_t* grad_y, const uint16_t* w, const uint16_t* lora_gt,
-                           const uint16_t* lora_a, int rank, uint16_t* grad_x, int64_t M,
-                           int64_t N, int64_t K, void* stream) {
+                           const uint16_t* lora_a, int rank, uint16_t* grad_x, void* workspace,
+                           size_t workspace_bytes, int64_t M, int64_t N, int64_t K,
+                           void* stream) {
   PLZ_REQUIRE(M >= 0 && N >= 0 && K >= 0, "plz_linear_bwd_x_dense: negative shape");
   PLZ_REQUIRE(K % 8 == 0 && N % 8 == 0, "plz_linear_bwd_x_dense: K and N must be multiples of 8");
   PLZ_REQUIRE(rank >= 0 && rank <= BK && rank % 8 == 0,
@@ -850,6 +1032,9 @@ int plz_linear_bwd_x_dense(const uint16_t* grad_y, const uint16_t* w, const uint
   g.I = M; g.J = K; g.R = N;
   g.a2 = lora_gt; g.b2 = lora_a; g.R2 = rank;
   g.c = grad_x; g.ldc = K; g.alpha = 1.f;
+  g.group = 8;
+  const int rc = set_tail(g, workspace, workspace_bytes, "plz_linear_bwd_x_dense");
+  if (rc != PLZ_OK) return rc;
   return launch<OP_ROW, OP_COL, EPI_BF16>(g, 1, (hipStream_t)stream, "plz_linear_bwd_x_dense");
 }
 

@@ -44,13 +44,17 @@ SIGNATURES: dict[str, tuple] = {
     "plz_pack_indices": (i32, [p, p, i64, i64, p]),
     "plz_unpack_indices": (i32, [p, p, i64, i64, p]),
     "plz_dequant": (i32, [p, p, p, i64, i64, p]),
-    "plz_lut_linear_fwd": (i32, [p, p, p, p, p, p, i32, p, i64, i64, i64, p]),
-    "plz_lut_linear_bwd_x": (i32, [p, p, p, p, p, i32, p, i64, i64, i64, p]),
+    "plz_lut_linear_fwd": (i32, [p, p, p, p, p, p, i32, p, p, sz, i64, i64, i64, p]),
+    "plz_lut_linear_fwd_workspace": (sz, [i64, i64, i64]),
+    "plz_lut_linear_bwd_x": (i32, [p, p, p, p, p, i32, p, p, sz, i64, i64, i64, p]),
+    "plz_lut_linear_bwd_x_workspace": (sz, [i64, i64, i64]),
     "plz_lut_linear_bwd_palette_workspace": (sz, [i64, i64, i64]),
     "plz_lut_linear_bwd_palette": (i32, [p, p, p, p, p, sz, i64, i64, i64, p]),
     "plz_bias_grad": (i32, [p, p, i64, i64, p]),
-    "plz_linear_fwd_dense": (i32, [p, p, p, p, p, i32, p, i64, i64, i64, p]),
-    "plz_linear_bwd_x_dense": (i32, [p, p, p, p, i32, p, i64, i64, i64, p]),
+    "plz_linear_fwd_dense": (i32, [p, p, p, p, p, i32, p, p, sz, i64, i64, i64, p]),
+    "plz_linear_fwd_dense_workspace": (sz, [i64, i64, i64]),
+    "plz_linear_bwd_x_dense": (i32, [p, p, p, p, i32, p, p, sz, i64, i64, i64, p]),
+    "plz_linear_bwd_x_dense_workspace": (sz, [i64, i64, i64]),
     "plz_gumbel_philox": (i32, [p, i64, u64, u64, p]),
     "plz_gumbel_lcg": (i32, [p, u32, i64, i64, p]),
     "plz_soft_build_w": (i32, [p, i32, p, p, f32, i32, p, p, i64, i64, p]),

@@ -48,6 +48,15 @@ def _workspace(nbytes: int, device) -> torch.Tensor:
     return torch.empty(max(int(nbytes), 16), dtype=torch.uint8, device=device)
 
 
+def _opt_workspace(nbytes: int, device):
+    """An optional workspace: None (NULL) when the query asks for none."""
+    return torch.empty(int(nbytes), dtype=torch.uint8, device=device) if nbytes > 0 else None
+
+
+def _numel(t) -> int:
+    return 0 if t is None else t.numel()
+
+
 # ---- formats ------------------------------------------------------------------------
 def pack_indices(idx: torch.Tensor) -> torch.Tensor:
     """uint8 [rows, cols] (0..3) -> int32 [rows, cols/16], LSB first."""
@@ -107,8 +116,9 @@ def lut_linear_fwd(x, packed, palette, bias=None, lora_t=None, lora_b=None):
         _need(bias, "bias", torch.bfloat16, 1)
     rank = _lora_pair(lora_t, lora_b, "lora_t", "lora_b", M, N)
     y = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
+    ws = _opt_workspace(query("plz_lut_linear_fwd_workspace", M, N, K), x.device)
     call("plz_lut_linear_fwd", _ptr(x), _ptr(packed), _ptr(palette), _ptr(bias), _ptr(lora_t),
-         _ptr(lora_b), rank, _ptr(y), M, N, K, _stream(x))
+         _ptr(lora_b), rank, _ptr(y), _ptr(ws), _numel(ws), M, N, K, _stream(x))
     return y
 
 
@@ -129,8 +139,9 @@ def lut_linear_bwd_x(grad_y, packed, palette, lora_gt=None, lora_a=None):
         if lora_gt.shape[0] != M or tuple(lora_a.shape) != (rank, K):
             raise ValueError("lora_gt / lora_a shape mismatch")
     gx = torch.empty((M, K), dtype=torch.bfloat16, device=grad_y.device)
+    ws = _opt_workspace(query("plz_lut_linear_bwd_x_workspace", M, N, K), grad_y.device)
     call("plz_lut_linear_bwd_x", _ptr(grad_y), _ptr(packed), _ptr(palette), _ptr(lora_gt),
-         _ptr(lora_a), rank, _ptr(gx), M, N, K, _stream(grad_y))
+         _ptr(lora_a), rank, _ptr(gx), _ptr(ws), _numel(ws), M, N, K, _stream(grad_y))
     return gx
 
 
@@ -171,8 +182,9 @@ def linear_fwd_dense(x, w, bias=None, lora_t=None, lora_b=None):
         _need(bias, "bias", torch.bfloat16, 1)
     rank = _lora_pair(lora_t, lora_b, "lora_t", "lora_b", M, N)
     y = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
+    ws = _opt_workspace(query("plz_linear_fwd_dense_workspace", M, N, K), x.device)
     call("plz_linear_fwd_dense", _ptr(x), _ptr(w), _ptr(bias), _ptr(lora_t), _ptr(lora_b), rank,
-         _ptr(y), M, N, K, _stream(x))
+         _ptr(y), _ptr(ws), _numel(ws), M, N, K, _stream(x))
     return y
 
 
@@ -189,8 +201,9 @@ def linear_bwd_x_dense(grad_y, w, lora_gt=None, lora_a=None):
         _need(lora_a, "lora_a", torch.bfloat16, 2)
         rank = lora_gt.shape[1]
     gx = torch.empty((M, K), dtype=torch.bfloat16, device=grad_y.device)
+    ws = _opt_workspace(query("plz_linear_bwd_x_dense_workspace", M, N, K), grad_y.device)
     call("plz_linear_bwd_x_dense", _ptr(grad_y), _ptr(w), _ptr(lora_gt), _ptr(lora_a), rank,
-         _ptr(gx), M, N, K, _stream(grad_y))
+         _ptr(gx), _ptr(ws), _numel(ws), M, N, K, _stream(grad_y))
     return gx
 
 

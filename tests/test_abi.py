@@ -36,15 +36,15 @@ def test_every_declared_symbol_is_exported(lib):
         assert hasattr(lib, n), f"{n} declared in the header but not exported"
         assert n in _lib.SIGNATURES, f"{n} has no ctypes signature"
     assert set(_lib.SIGNATURES) == set(names)
-    assert lib.plz_abi_version() == 3
+    assert lib.plz_abi_version() == 4
 
 
 def test_shape_errors_are_reported_without_touching_the_gpu(lib):
     rc = lib.plz_dequant(None, None, None, 8, 100, None)
     assert rc == 1 and b"multiple of 256" in lib.plz_last_error()
-    rc = lib.plz_lut_linear_fwd(None, None, None, None, None, None, 12, None, 4, 8, 256, None)
+    rc = lib.plz_lut_linear_fwd(None, None, None, None, None, None, 12, None, None, 0, 4, 8, 256, None)
     assert rc == 1 and b"rank" in lib.plz_last_error()
-    rc = lib.plz_lut_linear_fwd(None, None, None, None, None, None, 0, None, 4, 8, 256, None)
+    rc = lib.plz_lut_linear_fwd(None, None, None, None, None, None, 0, None, None, 0, 4, 8, 256, None)
     assert rc == 1 and b"null" in lib.plz_last_error()
     rc = lib.plz_lut_gemv(None, None, None, None, 17, 8, 256, None)
     assert rc == 1 and b"[1, 16]" in lib.plz_last_error()
@@ -54,11 +54,28 @@ def test_shape_errors_are_reported_without_touching_the_gpu(lib):
     assert rc == 1
 
 
+def test_tail_split_workspace_queries(lib):
+    # 640 output tiles on 256 CUs: a last wave of 128 tiles, split two ways when the reduction
+    # is long enough to pay for the partials; whole waves and short reductions need none
+    ws = lib.plz_lut_linear_fwd_workspace(16384, 2560, 9728)
+    assert ws == 128 * 2 * 256 * 256 * 4
+    assert lib.plz_lut_linear_bwd_x_workspace(16384, 9728, 2560) == 128 * 2 * 256 * 256 * 4
+    assert lib.plz_lut_linear_fwd_workspace(16384, 4096, 2560) == 0    # 1024 tiles
+    assert lib.plz_linear_fwd_dense_workspace(16384, 1024, 2560) == 0  # 256 tiles
+    assert lib.plz_linear_bwd_x_dense_workspace(16384, 1024, 2560) == 0  # 16 stages
+    assert lib.plz_lut_linear_fwd_workspace(0, 2560, 9728) == 0
+
+
 def test_workspace_queries_and_missing_workspace(lib):
     ws = lib.plz_lut_linear_bwd_palette_workspace(16384, 1024, 2560)
     assert ws > 0 and ws % (1024 * 20 * 16) == 0
     assert lib.plz_lut_linear_bwd_palette_workspace(0, 1024, 2560) == 0
-    assert lib.plz_soft_bwd_workspace(16384, 9728, 2560) == 9728 * 20 * 16
+    # soft backward: palette partials, plus fp32 dW rows per reduction split where it splits
+    # (gate at M = 16384: 2 splits; k_proj: 6; a short reduction: none)
+    pal = 9728 * 20 * 16
+    assert lib.plz_soft_bwd_workspace(16384, 9728, 2560) == pal + 2 * 9728 * 2560 * 4
+    assert lib.plz_soft_bwd_workspace(16384, 1024, 2560) == 1024 * 20 * 16 + 6 * 1024 * 2560 * 4
+    assert lib.plz_soft_bwd_workspace(192, 9728, 2560) == pal
     fake = C.c_void_p(16)  # never dereferenced: the size check fails first
     rc = lib.plz_lut_linear_bwd_palette(fake, fake, fake, fake, None, 0, 16384, 1024, 2560, None)
     assert rc == 4 and b"workspace" in lib.plz_last_error()

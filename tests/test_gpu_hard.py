@@ -233,3 +233,37 @@ def test_gemv_grouped_matches_single(dev):
     for (x, p, pl), y, want in zip(items, outs, wants):
         assert_close(f32(y), want, what="grouped gemv")
         assert torch.equal(y, ops.lut_gemv(x, p, pl))
+
+
+@pytest.mark.parametrize("M", [2048, 8192])
+def test_tail_split_gemms(dev, M):
+    """Launches whose last wave is partial split those tiles over the reduction (fp32 partials
+    in a workspace, summed by a second kernel): M=2048 splits every tile 3 ways, M=8192 the
+    last 64 of 320 tiles 4 ways. Sampled rows cover whole and split tiles; LoRA and bias ride
+    on the first part."""
+    N = K = 2560
+    assert ops.query("plz_lut_linear_fwd_workspace", M, N, K) > 0
+    assert ops.query("plz_lut_linear_bwd_x_workspace", M, N, K) > 0
+    idx, pal, x, W, (a, b) = _oracle_problem(M, N, K, seed=M, rank=16)
+    bias = randn_bf16(N, seed=3, std=0.1)
+    gy = randn_bf16(M, N, seed=4)
+    rows = torch.tensor([0, 1, 255, 777, M // 2 + 3, M - 1800, M - 257, M - 256, M - 1])
+    p, pl = _packed(idx, dev), pal.to(dev)
+    t = ops.lora_project(x.to(dev), a.to(dev), 1.0)
+    y = ops.lut_linear_fwd(x.to(dev), p, pl, bias.to(dev), lora_t=t, lora_b=b.to(dev))
+    xr = f32(x[rows])
+    want = O.lut_linear_fwd(xr, W, f32(bias)) + O.lora_forward(xr, f32(a), f32(b), 1.0)
+    assert_close(f32(y[rows.to(dev)]), want, what="fwd (tail split)")
+    gt = ops.lora_grad_t(gy.to(dev), b.to(dev), 1.0)
+    gx = ops.lut_linear_bwd_x(gy.to(dev), p, pl, lora_gt=gt, lora_a=a.to(dev))
+    want = O.grad_x(f32(gy[rows]), W) + f32(gt[rows.to(dev)]) @ f32(a)
+    assert_close(f32(gx[rows.to(dev)]), want, what="grad_x (tail split)")
+    # the dense GEMMs of the soft path on the dequantised weight
+    wd = ops.dequant(p, pl)
+    yd = ops.linear_fwd_dense(x.to(dev), wd, bias.to(dev))
+    assert_close(f32(yd[rows.to(dev)]), O.lut_linear_fwd(xr, W, f32(bias)), what="dense fwd")
+    gd = ops.linear_bwd_x_dense(gy.to(dev), wd)
+    assert_close(f32(gd[rows.to(dev)]), O.grad_x(f32(gy[rows]), W), what="dense grad_x")
+    # deterministic: the split sums its parts in a fixed order
+    y2 = ops.lut_linear_fwd(x.to(dev), p, pl, bias.to(dev), lora_t=t, lora_b=b.to(dev))
+    assert torch.equal(y, y2)
