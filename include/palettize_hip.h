@@ -293,6 +293,32 @@ int plz_swiglu_fwd(const uint16_t* gate, const uint16_t* up, uint16_t* h, int64_
 int plz_swiglu_bwd(const uint16_t* gate, const uint16_t* up, const uint16_t* grad_h,
                    uint16_t* grad_gate, uint16_t* grad_up, int64_t n, void* stream);
 
+/* ---- layer step around the linears -------------------------------------------------- */
+/* Rotary position embedding, HF Qwen3 rotate_half convention, fp32 math on bf16:
+ * y[row, head, j] = x[j] cos[pos, j] + rotate_half(x)[j] sin[pos, j], pos = row % seq;
+ * x, y bf16 [rows, heads, head_dim] (head_dim % 16 == 0), cos/sin fp32 [seq, head_dim].
+ * Replaces the torch expression of apply_rotary_pos_emb that the reference's HF Qwen layers
+ * run (transformers models/qwen3/modeling_qwen3.py, called through qwen_model.py:590).
+ * plz_rope_bwd is its transpose (grad_y -> grad_x). Bit-exact with the torch expression. */
+int plz_rope_fwd(const uint16_t* x, const float* cos_table, const float* sin_table, uint16_t* y,
+                 int64_t rows, int64_t seq, int heads, int head_dim, void* stream);
+int plz_rope_bwd(const uint16_t* grad_y, const float* cos_table, const float* sin_table,
+                 uint16_t* grad_x, int64_t rows, int64_t seq, int heads, int head_dim,
+                 void* stream);
+/* Distillation loss of train_qwen.py:229-249 (compute_loss, '1-cos+norm_mse'):
+ * loss = wc mean_rows(1 - cos(s_r, t_r)) + wm mean((s-t)^2) / max(mean(t^2), 1e-6), weights
+ * normalised to sum 1; student/teacher bf16 [rows, dim]. out4 (device fp32 [4]) receives
+ * {loss, l_cos, t_var, l_mse}; the workspace (per-row sums) is reused by the backward, which
+ * writes grad_student = grad_loss[0] * d loss / d student (bf16). */
+size_t plz_distill_loss_workspace(int64_t rows);
+int plz_distill_loss_fwd(const uint16_t* student, const uint16_t* teacher, float w_cos,
+                         float w_mse, float eps, float* out4, void* workspace,
+                         size_t workspace_bytes, int64_t rows, int64_t dim, void* stream);
+int plz_distill_loss_bwd(const uint16_t* student, const uint16_t* teacher, const float* out4,
+                         const float* grad_loss, float w_cos, float w_mse, float eps,
+                         uint16_t* grad_student, const void* workspace, size_t workspace_bytes,
+                         int64_t rows, int64_t dim, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

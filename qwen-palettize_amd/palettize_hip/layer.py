@@ -88,6 +88,39 @@ class SwiGLUFunction(torch.autograd.Function):
         return ops.swiglu_bwd(gate, up, gh.contiguous())
 
 
+class RopeFunction(torch.autograd.Function):
+    """apply_rope on the GPU: plz_rope_fwd / plz_rope_bwd (bit-exact with the torch expression)."""
+
+    @staticmethod
+    def forward(ctx, x, cos, sin):
+        ctx.save_for_backward(cos, sin)
+        return ops.rope_fwd(x.contiguous(), cos, sin)
+
+    @staticmethod
+    def backward(ctx, gy):
+        cos, sin = ctx.saved_tensors
+        return ops.rope_bwd(gy.contiguous(), cos, sin), None, None
+
+
+class DistillLossFunction(torch.autograd.Function):
+    """compute_loss on the GPU: one pass for the per-row sums, one for grad_student."""
+
+    @staticmethod
+    def forward(ctx, s, t, w_cos, w_mse):
+        s, t = s.contiguous(), t.contiguous()
+        out, ws = ops.distill_loss_fwd(s, t, w_cos, w_mse, 1e-4)
+        ctx.save_for_backward(s, t, out, ws)
+        ctx.w = (w_cos, w_mse)
+        ctx.mark_non_differentiable(out)
+        return out[0], out
+
+    @staticmethod
+    def backward(ctx, g_loss, _g_out):
+        s, t, out, ws = ctx.saved_tensors
+        gs = ops.distill_loss_bwd(s, t, out, ws, g_loss, ctx.w[0], ctx.w[1], 1e-4)
+        return gs, None, None, None
+
+
 # ---- palettized linear (native layout, soft path) ----------------------------------------
 class SoftPalettizedLinear(nn.Module):
     """y = x W_ste^T + s (x A^T) B^T with W from logits + Gumbel noise + palette.
@@ -148,6 +181,8 @@ def rope_tables(seq, head_dim, theta, device):
 
 def apply_rope(x, cos, sin):
     """x [B, S, H, D]; HF rotate_half convention, computed in fp32, returned in x.dtype."""
+    if x.is_cuda and x.dtype == torch.bfloat16:
+        return RopeFunction.apply(x, cos, sin)
     xf = x.float()
     d = xf.shape[-1] // 2
     rot = torch.cat([-xf[..., d:], xf[..., :d]], dim=-1)
@@ -156,20 +191,33 @@ def apply_rope(x, cos, sin):
     return (xf * c + rot * s).to(x.dtype)
 
 
+_GQA_NATIVE = [True]  # cleared when the SDPA backend refuses enable_gqa
+
+
 def attention(q, k, v, heads, kv_heads):
     """q [B,S,H,D], k/v [B,S,Hkv,D] -> [B,S,H*D]; causal, grouped-query (kv repeated)."""
     B, S, H, D = q.shape
     rep = heads // kv_heads
     qt = q.transpose(1, 2)
-    kt = k.repeat_interleave(rep, dim=2).transpose(1, 2)
-    vt = v.repeat_interleave(rep, dim=2).transpose(1, 2)
     if q.is_cuda:
         # flash / memory-efficient kernels only: the math fallback issues bf16 batched
         # products on transposed operands, which this pool does not run reliably
         from torch.nn.attention import SDPBackend, sdpa_kernel
         with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
-            o = F.scaled_dot_product_attention(qt, kt, vt, is_causal=True)
+            o = None
+            if _GQA_NATIVE[0]:
+                try:  # grouped-query heads without materialising the repeated k / v
+                    o = F.scaled_dot_product_attention(qt, k.transpose(1, 2), v.transpose(1, 2),
+                                                       is_causal=True, enable_gqa=True)
+                except RuntimeError:
+                    _GQA_NATIVE[0] = False
+            if o is None:
+                kt = k.repeat_interleave(rep, dim=2).transpose(1, 2)
+                vt = v.repeat_interleave(rep, dim=2).transpose(1, 2)
+                o = F.scaled_dot_product_attention(qt, kt, vt, is_causal=True)
     else:
+        kt = k.repeat_interleave(rep, dim=2).transpose(1, 2)
+        vt = v.repeat_interleave(rep, dim=2).transpose(1, 2)
         o = F.scaled_dot_product_attention(qt, kt, vt, is_causal=True)
     return o.transpose(1, 2).reshape(B, S, H * D)
 
@@ -253,6 +301,9 @@ class DenseDecoderLayer(nn.Module):
 # ---- loss / schedule / optimizer ----------------------------------------------------------------
 def compute_loss(student_out, teacher_out, w_cos=0.5, w_mse=0.5):
     """train_qwen.py:229-249 (loss_type '1-cos+norm_mse', weights normalised)."""
+    if student_out.is_cuda and student_out.dtype == torch.bfloat16:
+        loss, out = DistillLossFunction.apply(student_out, teacher_out.detach(), w_cos, w_mse)
+        return loss, out[1]
     s = student_out.float()
     t = teacher_out.detach().float()
     tot = w_cos + w_mse

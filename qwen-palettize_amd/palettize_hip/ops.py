@@ -450,3 +450,54 @@ def swiglu_bwd(gate, up, grad_h):
     call("plz_swiglu_bwd", _ptr(gate), _ptr(up), _ptr(grad_h), _ptr(gg), _ptr(gu), gate.numel(),
          _stream(gate))
     return gg, gu
+
+
+# ---- layer step: RoPE and the distillation loss ----------------------------------------------
+def _rope(name, x, cos, sin):
+    _need(x, "x", torch.bfloat16)
+    if x.dim() < 3 or not x.is_contiguous():
+        raise ValueError("x must be contiguous [..., seq, heads, head_dim]")
+    seq, heads, hd = x.shape[-3], x.shape[-2], x.shape[-1]
+    for t, nm in ((cos, "cos"), (sin, "sin")):
+        _need(t, nm, torch.float32, 2)
+        if tuple(t.shape) != (seq, hd):
+            raise ValueError(f"{nm} must be [seq={seq}, head_dim={hd}]")
+    y = torch.empty_like(x)
+    rows = x.numel() // (heads * hd)
+    call(name, _ptr(x), _ptr(cos), _ptr(sin), _ptr(y), rows, seq, heads, hd, _stream(x))
+    return y
+
+
+def rope_fwd(x, cos, sin):
+    """x bf16 [..., seq, heads, head_dim] -> x cos + rotate_half(x) sin (fp32 math, bf16 out)."""
+    return _rope("plz_rope_fwd", x, cos, sin)
+
+
+def rope_bwd(grad_y, cos, sin):
+    return _rope("plz_rope_bwd", grad_y, cos, sin)
+
+
+def distill_loss_fwd(student, teacher, w_cos=0.5, w_mse=0.5, eps=1e-4):
+    """Returns (out4 fp32 [4] = loss, l_cos, t_var, l_mse; workspace for the backward)."""
+    _need(student, "student", torch.bfloat16)
+    _need(teacher, "teacher", torch.bfloat16)
+    if student.shape != teacher.shape:
+        raise ValueError("student / teacher shape mismatch")
+    dim = student.shape[-1]
+    rows = student.numel() // dim
+    out = torch.empty(4, dtype=torch.float32, device=student.device)
+    ws = _workspace(query("plz_distill_loss_workspace", rows), student.device)
+    call("plz_distill_loss_fwd", _ptr(student), _ptr(teacher), float(w_cos), float(w_mse),
+         float(eps), _ptr(out), _ptr(ws), ws.numel(), rows, dim, _stream(student))
+    return out, ws
+
+
+def distill_loss_bwd(student, teacher, out4, ws, grad_loss, w_cos=0.5, w_mse=0.5, eps=1e-4):
+    dim = student.shape[-1]
+    rows = student.numel() // dim
+    gl = grad_loss.reshape(1).to(torch.float32).contiguous()
+    gs = torch.empty_like(student)
+    call("plz_distill_loss_bwd", _ptr(student), _ptr(teacher), _ptr(out4), _ptr(gl),
+         float(w_cos), float(w_mse), float(eps), _ptr(gs), _ptr(ws), ws.numel(), rows, dim,
+         _stream(student))
+    return gs

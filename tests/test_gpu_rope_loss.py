@@ -1,0 +1,75 @@
+"""GPU parity of the layer-step kernels around the linears: RoPE forward/backward (bit-exact
+against the torch expression of HF Qwen3's rotate_half embedding) and the distillation loss of
+train_qwen.py:229-249 (against torch autograd of the same expression in fp32 on the CPU)."""
+import pytest
+import torch
+
+from helpers import assert_close, f32
+
+pytestmark = pytest.mark.gpu
+layer = pytest.importorskip("palettize_hip.layer")
+ops = pytest.importorskip("palettize_hip.ops")
+
+
+def _rope_cpu(x, cos, sin):
+    xf = x.float()
+    d = xf.shape[-1] // 2
+    rot = torch.cat([-xf[..., d:], xf[..., :d]], dim=-1)
+    return (xf * cos[None, :, None, :] + rot * sin[None, :, None, :]).to(x.dtype)
+
+
+@pytest.mark.parametrize("B,S,H,D", [(2, 37, 4, 128), (1, 512, 8, 64), (3, 16, 32, 128)])
+def test_rope_bit_exact(dev, B, S, H, D):
+    g = torch.Generator().manual_seed(B * S + H)
+    x = (torch.randn(B, S, H, D, generator=g) * 3).to(torch.bfloat16)
+    cos, sin = layer.rope_tables(S, D, 1e6, "cpu")
+    y = ops.rope_fwd(x.to(dev), cos.to(dev), sin.to(dev)).cpu()
+    assert torch.equal(y.view(torch.int16), _rope_cpu(x, cos, sin).view(torch.int16))
+    # backward: torch autograd through the same expression
+    xr = x.clone().requires_grad_(True)
+    gy = (torch.randn(B, S, H, D, generator=g)).to(torch.bfloat16)
+    _rope_cpu(xr, cos, sin).backward(gy)
+    gx = ops.rope_bwd(gy.to(dev), cos.to(dev), sin.to(dev)).cpu()
+    assert torch.equal(gx.view(torch.int16), xr.grad.view(torch.int16))
+    # the autograd wrapper the layer uses
+    xg = x.to(dev).requires_grad_(True)
+    layer.apply_rope(xg, cos.to(dev), sin.to(dev)).backward(gy.to(dev))
+    assert torch.equal(xg.grad.cpu().view(torch.int16), xr.grad.view(torch.int16))
+
+
+def _loss_cpu(s, t, w_cos=0.5, w_mse=0.5):
+    sf, tf = s.float(), t.float()
+    tot = w_cos + w_mse
+    cos_per = torch.nn.functional.cosine_similarity(sf.flatten(0, 1), tf.flatten(0, 1), dim=-1,
+                                                    eps=1e-4)
+    l_cos = (1 - cos_per).mean()
+    t_var = (tf * tf).mean().clamp(min=1e-6)
+    l_mse = ((sf - tf) ** 2).mean() / t_var
+    return (w_cos / tot) * l_cos + (w_mse / tot) * l_mse, l_cos
+
+
+@pytest.mark.parametrize("B,S,Dm,w", [(2, 64, 256, (0.5, 0.5)), (4, 512, 2560, (0.5, 0.5)),
+                                      (1, 100, 2560, (1.0, 3.0))])
+def test_distill_loss_matches_torch(dev, B, S, Dm, w):
+    g = torch.Generator().manual_seed(S + Dm)
+    t = torch.randn(B, S, Dm, generator=g).to(torch.bfloat16)
+    s = (t.float() + 0.3 * torch.randn(B, S, Dm, generator=g)).to(torch.bfloat16)
+    sr = s.clone().requires_grad_(True)
+    want, want_cos = _loss_cpu(sr, t, *w)
+    want.backward()
+    sg = s.to(dev).requires_grad_(True)
+    loss, l_cos = layer.compute_loss(sg, t.to(dev), *w)
+    assert abs(float(loss) - float(want)) <= 1e-5 * abs(float(want)) + 1e-7
+    assert abs(float(l_cos) - float(want_cos)) <= 1e-5 * abs(float(want_cos)) + 1e-7
+    (2.0 * loss).backward()
+    assert_close(f32(sg.grad.cpu()), 2.0 * f32(sr.grad), what="grad_student")
+
+
+def test_distill_loss_identical_inputs(dev):
+    # s == t: l_cos = 0, l_mse = 0, gradient 0
+    t = torch.randn(2, 8, 128).to(torch.bfloat16).to(dev)
+    s = t.clone().requires_grad_(True)
+    loss, l_cos = layer.compute_loss(s, t)
+    assert abs(float(loss)) < 1e-6 and abs(float(l_cos)) < 1e-6
+    loss.backward()
+    assert float(s.grad.float().abs().max()) < 1e-6
