@@ -10,12 +10,6 @@
 
 namespace plz {
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
-  return v;
-}
-
 __device__ __forceinline__ void unpack8(uint4 v, float f[8]) {
   const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
@@ -33,24 +27,35 @@ __device__ __forceinline__ uint4 pack8(const float f[8]) {
 
 constexpr int kNormMaxChunks = 8;  // cols <= 8 * 512 = 4096
 
-// One wave per row; lane handles 8-column chunks c = lane + 64*i.
+// Row shapes: LPR lanes per row (RPW = 64 / LPR rows per wave) and up to MAXC 8-column chunks
+// per lane. Per-head norms (128 columns) put 4 rows in a wave, so no lane idles; hidden-size
+// rows (2560) take a whole wave with 5 chunks per lane.
+template <int LPR>
+__device__ __forceinline__ float row_sum(float v) {
+#pragma unroll
+  for (int off = LPR / 2; off >= 1; off >>= 1) v += __shfl_xor(v, off);
+  return v;
+}
+
+template <int LPR, int MAXC>
 __global__ __launch_bounds__(256) void rmsnorm_fwd_kernel(const uint16_t* __restrict__ x,
                                                           const uint16_t* __restrict__ wt,
                                                           uint16_t* __restrict__ y,
                                                           float* __restrict__ rstd, int64_t rows,
                                                           int64_t cols, float eps) {
-  const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= rows) return;
+  constexpr int RPW = 64 / LPR;
+  const int lane = threadIdx.x & 63, sub = lane / LPR, l = lane % LPR;
+  const int64_t row = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW + sub;
+  const bool valid = row < rows;  // lanes of a missing row compute on zeros (shuffles stay whole)
   const int nch = (int)(cols / 8);
-  const uint4* xr = reinterpret_cast<const uint4*>(x + row * cols);
-  uint4 xv[kNormMaxChunks];
+  const uint4* xr = reinterpret_cast<const uint4*>(x + (valid ? row : 0) * cols);
+  uint4 xv[MAXC];
   float ss = 0.f;
 #pragma unroll
-  for (int i = 0; i < kNormMaxChunks; ++i) {
-    const int c = lane + 64 * i;
+  for (int i = 0; i < MAXC; ++i) {
+    const int c = l + LPR * i;
     xv[i] = make_uint4(0, 0, 0, 0);
-    if (c < nch) {
+    if (valid && c < nch) {
       xv[i] = xr[c];
       float f[8];
       unpack8(xv[i], f);
@@ -58,14 +63,15 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_kernel(const uint16_t* __rest
       for (int j = 0; j < 8; ++j) ss += f[j] * f[j];
     }
   }
-  ss = wave_sum(ss);
+  ss = row_sum<LPR>(ss);
+  if (!valid) return;
   const float r = rsqrtf(ss / (float)cols + eps);
-  if (lane == 0 && rstd) rstd[row] = r;
+  if (l == 0 && rstd) rstd[row] = r;
   uint4* yr = reinterpret_cast<uint4*>(y + row * cols);
   const uint4* wr = reinterpret_cast<const uint4*>(wt);
 #pragma unroll
-  for (int i = 0; i < kNormMaxChunks; ++i) {
-    const int c = lane + 64 * i;
+  for (int i = 0; i < MAXC; ++i) {
+    const int c = l + LPR * i;
     if (c < nch) {
       float f[8], w[8], o[8];
       unpack8(xv[i], f);
@@ -79,75 +85,98 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_kernel(const uint16_t* __rest
 
 // Backward. With h = x r, g = grad_y * w (fp32):
 //   grad_x = r * (g - h * mean(g * h)),  grad_w = sum_rows grad_y * bf16(h)
-// Each workgroup takes a strided set of rows; per-lane column partials of grad_w are
-// summed over its 4 waves in LDS and written to partial[block][cols]; a second kernel adds
-// the blocks in a fixed order.
+// Each workgroup takes a strided set of row groups, U groups per iteration (their loads are
+// all issued before any is used, so short rows do not pay the memory latency per row);
+// per-lane column partials of grad_w are summed over the workgroup's rows in LDS (fixed order)
+// and written to partial[block][cols]; a second kernel adds the blocks in a fixed order.
+template <int LPR, int MAXC, int U>
 __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ wt, const float* __restrict__ rstd,
     const uint16_t* __restrict__ gy, uint16_t* __restrict__ gx, float* __restrict__ partial,
     int64_t rows, int64_t cols) {
-  __shared__ float red[4][kNormMaxChunks][64][8];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  constexpr int RPW = 64 / LPR;
+  __shared__ float red[4 * RPW][MAXC][LPR][8];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, sub = lane / LPR, l = lane % LPR;
   const int nch = (int)(cols / 8);
   const uint4* wr = reinterpret_cast<const uint4*>(wt);
-  float gw[kNormMaxChunks][8];
+  float gw[MAXC][8];
 #pragma unroll
-  for (int i = 0; i < kNormMaxChunks; ++i)
+  for (int i = 0; i < MAXC; ++i)
 #pragma unroll
     for (int j = 0; j < 8; ++j) gw[i][j] = 0.f;
-  for (int64_t row = (int64_t)blockIdx.x * 4 + wave; row < rows; row += (int64_t)gridDim.x * 4) {
-    const float r = rstd[row];
-    const uint4* xr = reinterpret_cast<const uint4*>(x + row * cols);
-    const uint4* gr = reinterpret_cast<const uint4*>(gy + row * cols);
-    uint4 xv[kNormMaxChunks], gv[kNormMaxChunks];
-    float dot = 0.f;
+  const int64_t step = (int64_t)gridDim.x * 4 * RPW;  // rows between a wave's row groups
+  for (int64_t r0 = ((int64_t)blockIdx.x * 4 + wave) * RPW; r0 < rows; r0 += step * U) {
+    uint4 xv[U][MAXC], gv[U][MAXC];
+    float rs[U];
 #pragma unroll
-    for (int i = 0; i < kNormMaxChunks; ++i) {
-      const int c = lane + 64 * i;
-      xv[i] = make_uint4(0, 0, 0, 0);
-      gv[i] = xv[i];
-      if (c < nch) {
-        xv[i] = xr[c];
-        gv[i] = gr[c];
-        float f[8], g[8], w[8];
-        unpack8(xv[i], f);
-        unpack8(gv[i], g);
-        unpack8(wr[c], w);
+    for (int u = 0; u < U; ++u) {
+      const int64_t row = r0 + step * u + sub;
+      const bool valid = row < rows;
+      rs[u] = valid ? rstd[row] : 0.f;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float h = f[j] * r;
-          dot += g[j] * w[j] * h;
-          gw[i][j] += g[j] * bf2f(f2bf(h));
+      for (int i = 0; i < MAXC; ++i) {
+        const int c = l + LPR * i;
+        xv[u][i] = make_uint4(0, 0, 0, 0);
+        gv[u][i] = xv[u][i];
+        if (valid && c < nch) {
+          xv[u][i] = reinterpret_cast<const uint4*>(x + row * cols)[c];
+          gv[u][i] = reinterpret_cast<const uint4*>(gy + row * cols)[c];
         }
       }
     }
-    dot = wave_sum(dot) / (float)cols;
-    uint4* outr = reinterpret_cast<uint4*>(gx + row * cols);
 #pragma unroll
-    for (int i = 0; i < kNormMaxChunks; ++i) {
-      const int c = lane + 64 * i;
-      if (c < nch) {
-        float f[8], g[8], w[8], o[8];
-        unpack8(xv[i], f);
-        unpack8(gv[i], g);
-        unpack8(wr[c], w);
+    for (int u = 0; u < U; ++u) {
+      const int64_t row = r0 + step * u + sub;
+      const float r = rs[u];
+      float dot = 0.f;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) o[j] = r * (g[j] * w[j] - f[j] * r * dot);
-        outr[c] = pack8(o);
+      for (int i = 0; i < MAXC; ++i) {
+        const int c = l + LPR * i;
+        if (c < nch) {
+          float f[8], g[8], w[8];
+          unpack8(xv[u][i], f);
+          unpack8(gv[u][i], g);
+          unpack8(wr[c], w);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const float h = f[j] * r;
+            dot += g[j] * w[j] * h;
+            gw[i][j] += g[j] * bf2f(f2bf(h));  // zero for a missing row (g = 0)
+          }
+        }
+      }
+      dot = row_sum<LPR>(dot) / (float)cols;
+      if (row < rows) {
+        uint4* outr = reinterpret_cast<uint4*>(gx + row * cols);
+#pragma unroll
+        for (int i = 0; i < MAXC; ++i) {
+          const int c = l + LPR * i;
+          if (c < nch) {
+            float f[8], g[8], w[8], o[8];
+            unpack8(xv[u][i], f);
+            unpack8(gv[u][i], g);
+            unpack8(wr[c], w);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) o[j] = r * (g[j] * w[j] - f[j] * r * dot);
+            outr[c] = pack8(o);
+          }
+        }
       }
     }
   }
 #pragma unroll
-  for (int i = 0; i < kNormMaxChunks; ++i)
+  for (int i = 0; i < MAXC; ++i)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) red[wave][i][lane][j] = gw[i][j];
+    for (int j = 0; j < 8; ++j) red[wave * RPW + sub][i][l][j] = gw[i][j];
   __syncthreads();
-  // thread t sums column chunk (i = t / 64 ... ) over the 4 waves
+  // column chunk c = l + LPR*i summed over the workgroup's 4*RPW row slots in order
   for (int idx = threadIdx.x; idx < nch * 8; idx += 256) {
     const int c = idx / 8, j = idx % 8;
-    const int i = c / 64, l = c % 64;
-    const float s = red[0][i][l][j] + red[1][i][l][j] + red[2][i][l][j] + red[3][i][l][j];
-    partial[(int64_t)blockIdx.x * cols + idx] = s;
+    const int i = c / LPR, ll = c % LPR;
+    float sum = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4 * RPW; ++w) sum += red[w][i][ll][j];
+    partial[(int64_t)blockIdx.x * cols + idx] = sum;
   }
 }
 
@@ -215,8 +244,19 @@ __global__ void bias_grad_kernel(const uint16_t* __restrict__ gy, float* __restr
   gb[n] = s;
 }
 
-static int rmsnorm_blocks(int64_t rows) {
-  int64_t b = (rows + 3) / 4;
+// Kernel shape of a row width: lanes per row, chunks per lane, row groups per iteration.
+struct NormShape {
+  int lpr, maxc, u;
+};
+static NormShape norm_shape(int64_t cols) {
+  if (cols <= 128) return {16, 1, 4};
+  if (cols <= 512) return {64, 1, 4};
+  return {64, kNormMaxChunks, 1};
+}
+static int rmsnorm_bwd_blocks(int64_t rows, int64_t cols) {
+  const NormShape sh = norm_shape(cols);
+  const int64_t per_block = 4LL * (64 / sh.lpr) * sh.u;
+  const int64_t b = (rows + per_block - 1) / per_block;
   return (int)(b < 1024 ? b : 1024);
 }
 
@@ -236,14 +276,24 @@ int plz_rmsnorm_fwd(const uint16_t* x, const uint16_t* weight, uint16_t* y, floa
   if (rows == 0) return PLZ_OK;
   PLZ_REQUIRE(x && weight && y && a16(x) && a16(weight) && a16(y),
               "plz_rmsnorm_fwd: x, weight, y must be non-null and 16-byte aligned");
-  hipLaunchKernelGGL(rmsnorm_fwd_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0,
-                     (hipStream_t)stream, x, weight, y, rstd, rows, cols, eps);
+  const NormShape sh = norm_shape(cols);
+  const int64_t per_block = 4LL * (64 / sh.lpr);
+  const dim3 grid((unsigned)((rows + per_block - 1) / per_block));
+  if (sh.lpr == 16)
+    hipLaunchKernelGGL((rmsnorm_fwd_kernel<16, 1>), grid, dim3(256), 0, (hipStream_t)stream, x,
+                       weight, y, rstd, rows, cols, eps);
+  else if (sh.maxc == 1)
+    hipLaunchKernelGGL((rmsnorm_fwd_kernel<64, 1>), grid, dim3(256), 0, (hipStream_t)stream, x,
+                       weight, y, rstd, rows, cols, eps);
+  else
+    hipLaunchKernelGGL((rmsnorm_fwd_kernel<64, kNormMaxChunks>), grid, dim3(256), 0,
+                       (hipStream_t)stream, x, weight, y, rstd, rows, cols, eps);
   return check_launch("plz_rmsnorm_fwd");
 }
 
 size_t plz_rmsnorm_bwd_workspace(int64_t rows, int64_t cols) {
   if (rows <= 0 || cols <= 0) return 0;
-  return (size_t)rmsnorm_blocks(rows) * cols * sizeof(float);
+  return (size_t)rmsnorm_bwd_blocks(rows, cols) * cols * sizeof(float);
 }
 
 int plz_rmsnorm_bwd(const uint16_t* x, const uint16_t* weight, const float* rstd,
@@ -266,10 +316,18 @@ int plz_rmsnorm_bwd(const uint16_t* x, const uint16_t* weight, const float* rstd
     set_error("plz_rmsnorm_bwd: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
     return PLZ_EWORKSPACE;
   }
-  const int blocks = rmsnorm_blocks(rows);
+  const int blocks = rmsnorm_bwd_blocks(rows, cols);
   float* part = reinterpret_cast<float*>(workspace);
-  hipLaunchKernelGGL(rmsnorm_bwd_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream, x,
-                     weight, rstd, grad_y, grad_x, part, rows, cols);
+  const NormShape sh = norm_shape(cols);
+  if (sh.lpr == 16)
+    hipLaunchKernelGGL((rmsnorm_bwd_kernel<16, 1, 4>), dim3(blocks), dim3(256), 0,
+                       (hipStream_t)stream, x, weight, rstd, grad_y, grad_x, part, rows, cols);
+  else if (sh.maxc == 1)
+    hipLaunchKernelGGL((rmsnorm_bwd_kernel<64, 1, 4>), dim3(blocks), dim3(256), 0,
+                       (hipStream_t)stream, x, weight, rstd, grad_y, grad_x, part, rows, cols);
+  else
+    hipLaunchKernelGGL((rmsnorm_bwd_kernel<64, kNormMaxChunks, 1>), dim3(blocks), dim3(256), 0,
+                       (hipStream_t)stream, x, weight, rstd, grad_y, grad_x, part, rows, cols);
   int rc = check_launch("plz_rmsnorm_bwd");
   if (rc) return rc;
   hipLaunchKernelGGL(sum_blocks_kernel, dim3((unsigned)((cols + 63) / 64)), dim3(256), 0,
