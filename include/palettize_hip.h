@@ -139,6 +139,13 @@ int plz_gumbel_lcg(float* noise, uint32_t seed, int64_t N, int64_t K, void* stre
 int plz_soft_build_w(const uint16_t* logits, int logits_dtype, const float* noise,
                      const float* palette, float tau, int mode, uint16_t* w, uint16_t* w_soft,
                      int64_t N, int64_t K, void* stream);
+/* The same with the noise drawn in the kernel: element (n, k, c) = the value
+ * plz_gumbel_philox(seed, offset) stores there (Philox counter offset + n*K + k), so no noise
+ * tensor is written or read. Replaces the in-kernel sampling of
+ * compute_P_W_hard_aos_kernel (fused_lut_kernel.cu:1946-2004) with this build's Philox. */
+int plz_soft_build_w_philox(const uint16_t* logits, int logits_dtype, uint64_t seed,
+                            uint64_t offset, const float* palette, float tau, int mode,
+                            uint16_t* w, uint16_t* w_soft, int64_t N, int64_t K, void* stream);
 
 /* Batched build W: the linears of a layer (or of several) in one launch, each with its own
  * logits, noise, palette and outputs; the same tau and mode for all. Replaces
@@ -176,6 +183,13 @@ int plz_soft_bwd(const uint16_t* x, const uint16_t* grad_y, const uint16_t* logi
                  int scale_grad_by_inv_tau, uint16_t* grad_logits, float* grad_palette,
                  void* workspace, size_t workspace_bytes, int64_t M, int64_t N, int64_t K,
                  void* stream);
+/* The same with the forward's Philox noise redrawn in the epilogue (see
+ * plz_soft_build_w_philox); same workspace. */
+int plz_soft_bwd_philox(const uint16_t* x, const uint16_t* grad_y, const uint16_t* logits,
+                        int logits_dtype, uint64_t seed, uint64_t offset, const float* palette,
+                        float tau, int scale_grad_by_inv_tau, uint16_t* grad_logits,
+                        float* grad_palette, void* workspace, size_t workspace_bytes, int64_t M,
+                        int64_t N, int64_t K, void* stream);
 
 /* ---- LoRA (QwenLoRA, qwen_model.py:213-304): y += scale * (x A^T) B^T ------------------ */
 /* t[M,rank] = scale * x[M,K] lora_a[rank,K]^T  (bf16). rank in {8,16,24,32}. */

@@ -136,6 +136,42 @@ __device__ __forceinline__ void dequant16_pair(uint32_t qa, PalLut ta, uint32_t 
   }
 }
 
+// ---- Philox4x32-10 (Salmon, Moraes, Dror, Shaw, SC'11) ---------------------------------
+struct U4 {
+  uint32_t x, y, z, w;
+};
+__host__ __device__ __forceinline__ U4 philox4x32_10(U4 c, uint32_t k0, uint32_t k1) {
+  const uint32_t M0 = 0xD2511F53u, M1 = 0xCD9E8D57u, W0 = 0x9E3779B9u, W1 = 0xBB67AE85u;
+#pragma unroll
+  for (int i = 0; i < 10; ++i) {
+    const uint64_t p0 = (uint64_t)M0 * c.x, p1 = (uint64_t)M1 * c.z;
+    const uint32_t hi0 = (uint32_t)(p0 >> 32), lo0 = (uint32_t)p0;
+    const uint32_t hi1 = (uint32_t)(p1 >> 32), lo1 = (uint32_t)p1;
+    c = U4{hi1 ^ c.y ^ k0, lo1, hi0 ^ c.w ^ k1, lo0};
+    k0 += W0;
+    k1 += W1;
+  }
+  return c;
+}
+
+// u = (top 23 bits + 0.5) / 2^23 lies in [2^-24, 1 - 2^-24]: every value is exact in fp32,
+// so u never rounds to 1 (which would make the noise +inf).
+__device__ __forceinline__ float gumbel_from_bits(uint32_t b) {
+  const float u = ((float)(b >> 9) + 0.5f) * (1.0f / 8388608.0f);
+  return -logf(-logf(u));
+}
+
+// The Gumbel noise of element (n, k, c) of an [N, K, 4] tensor drawn by Philox at counter
+// offset + n*K + k: one 128-bit draw gives the 4 classes of one weight.
+__device__ __forceinline__ void philox_gumbel4(uint64_t seed, uint64_t ctr, float (&z)[4]) {
+  const U4 r = philox4x32_10(U4{(uint32_t)ctr, (uint32_t)(ctr >> 32), 0u, 0u}, (uint32_t)seed,
+                             (uint32_t)(seed >> 32));
+  z[0] = gumbel_from_bits(r.x);
+  z[1] = gumbel_from_bits(r.y);
+  z[2] = gumbel_from_bits(r.z);
+  z[3] = gumbel_from_bits(r.w);
+}
+
 // ---- error reporting shared by every entry point -------------------------------
 void set_error(const char* fmt, ...);
 int check_launch(const char* what);

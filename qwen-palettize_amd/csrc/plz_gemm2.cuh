@@ -59,6 +59,7 @@ struct Args {
   // epilogue
   void* c; int64_t ldc; const uint16_t* bias; float alpha; float* partial;
   const uint16_t* logits; const float* noise; float inv_tau, glog_scale; uint16_t* grad_logits;
+  uint64_t noise_seed, noise_offset;  // noise == nullptr: Philox at noise_offset + n*K + k
   int logits_f16;
   float* acc_ws;  // EPI_F32: partial dW rows of each reduction split, [split][I][J] fp32
   // EPI_BF16 tail split: tiles [tail_first, tiles) run as tail_split reduction parts of

@@ -278,10 +278,20 @@ __device__ __forceinline__ void soft_item(const Args& g, int64_t n, int64_t kseg
   const float pc[4] = {pal.x, pal.y, pal.z, pal.w};
   const int64_t e0 = (n * g.J + k) * 4;
   const uint4 lg = *reinterpret_cast<const uint4*>(g.logits + e0);
-  const float4 z0 = *reinterpret_cast<const float4*>(g.noise + e0);
-  const float4 z1 = *reinterpret_cast<const float4*>(g.noise + e0 + 4);
   const uint32_t lw[4] = {lg.x, lg.y, lg.z, lg.w};
-  const float nz[8] = {z0.x, z0.y, z0.z, z0.w, z1.x, z1.y, z1.z, z1.w};
+  float nz[8];
+  if (g.noise) {
+    const float4 z0 = *reinterpret_cast<const float4*>(g.noise + e0);
+    const float4 z1 = *reinterpret_cast<const float4*>(g.noise + e0 + 4);
+    nz[0] = z0.x; nz[1] = z0.y; nz[2] = z0.z; nz[3] = z0.w;
+    nz[4] = z1.x; nz[5] = z1.y; nz[6] = z1.z; nz[7] = z1.w;
+  } else {  // the noise the forward drew: Philox at noise_offset + n*K + k
+    float z[4];
+    philox_gumbel4(g.noise_seed, g.noise_offset + (uint64_t)(n * g.J + k), z);
+    nz[0] = z[0]; nz[1] = z[1]; nz[2] = z[2]; nz[3] = z[3];
+    philox_gumbel4(g.noise_seed, g.noise_offset + (uint64_t)(n * g.J + k + 1), z);
+    nz[4] = z[0]; nz[5] = z[1]; nz[6] = z[2]; nz[7] = z[3];
+  }
   float sp[4] = {0.f, 0.f, 0.f, 0.f};
   uint32_t out[4];
 #pragma unroll
@@ -1044,11 +1054,11 @@ size_t plz_soft_bwd_workspace(int64_t M, int64_t N, int64_t K) {
   return soft_pal_bytes(N, K) + (z > 1 ? (size_t)z * N * K * sizeof(float) : 0);
 }
 
-int plz_soft_bwd(const uint16_t* x, const uint16_t* grad_y, const uint16_t* logits,
-                 int logits_dtype, const float* noise, const float* palette, float tau,
-                 int scale_grad_by_inv_tau, uint16_t* grad_logits, float* grad_palette,
-                 void* workspace, size_t workspace_bytes, int64_t M, int64_t N, int64_t K,
-                 void* stream) {
+static int soft_bwd(const uint16_t* x, const uint16_t* grad_y, const uint16_t* logits,
+                    int logits_dtype, bool gen, const float* noise, uint64_t seed, uint64_t offset,
+                    const float* palette, float tau, int scale_grad_by_inv_tau,
+                    uint16_t* grad_logits, float* grad_palette, void* workspace,
+                    size_t workspace_bytes, int64_t M, int64_t N, int64_t K, void* stream) {
   PLZ_REQUIRE(M >= 0 && N >= 0 && K >= 0, "plz_soft_bwd: negative shape");
   PLZ_REQUIRE(K % 256 == 0, "plz_soft_bwd: K (%lld) must be a multiple of 256", (long long)K);
   PLZ_REQUIRE(N % 8 == 0, "plz_soft_bwd: N (%lld) must be a multiple of 8", (long long)N);
@@ -1056,7 +1066,7 @@ int plz_soft_bwd(const uint16_t* x, const uint16_t* grad_y, const uint16_t* logi
               "plz_soft_bwd: logits dtype must be bf16 or fp16");
   PLZ_REQUIRE(tau > 0.f, "plz_soft_bwd: tau must be positive");
   if (N == 0 || K == 0) return PLZ_OK;
-  PLZ_REQUIRE(x && grad_y && logits && noise && palette && grad_logits && grad_palette,
+  PLZ_REQUIRE(x && grad_y && logits && palette && grad_logits && grad_palette && (gen || noise),
               "plz_soft_bwd: null pointer");
   PLZ_REQUIRE(a16(x) && a16(grad_y) && a16(logits) && a16(noise) && a16(palette) &&
                   a16(grad_logits),
@@ -1075,6 +1085,7 @@ int plz_soft_bwd(const uint16_t* x, const uint16_t* grad_y, const uint16_t* logi
   g.partial = reinterpret_cast<float*>(workspace);
   g.acc_ws = z > 1 ? reinterpret_cast<float*>((char*)workspace + soft_pal_bytes(N, K)) : nullptr;
   g.logits = logits; g.noise = noise; g.inv_tau = 1.f / tau;
+  g.noise_seed = seed; g.noise_offset = offset;
   g.glog_scale = scale_grad_by_inv_tau ? 1.f / tau : 1.f;
   g.grad_logits = grad_logits; g.logits_f16 = logits_dtype == PLZ_DT_FP16;
   int rc;
@@ -1093,6 +1104,26 @@ int plz_soft_bwd(const uint16_t* x, const uint16_t* grad_y, const uint16_t* logi
   hipLaunchKernelGGL(reduce_pal_kernel, dim3((unsigned)((n_out + 255) / 256)), dim3(256), 0,
                      (hipStream_t)stream, g.partial, grad_palette, N, G, 1);
   return check_launch("plz_soft_bwd/reduce");
+}
+
+int plz_soft_bwd(const uint16_t* x, const uint16_t* grad_y, const uint16_t* logits,
+                 int logits_dtype, const float* noise, const float* palette, float tau,
+                 int scale_grad_by_inv_tau, uint16_t* grad_logits, float* grad_palette,
+                 void* workspace, size_t workspace_bytes, int64_t M, int64_t N, int64_t K,
+                 void* stream) {
+  return soft_bwd(x, grad_y, logits, logits_dtype, false, noise, 0, 0, palette, tau,
+                  scale_grad_by_inv_tau, grad_logits, grad_palette, workspace, workspace_bytes, M,
+                  N, K, stream);
+}
+
+int plz_soft_bwd_philox(const uint16_t* x, const uint16_t* grad_y, const uint16_t* logits,
+                        int logits_dtype, uint64_t seed, uint64_t offset, const float* palette,
+                        float tau, int scale_grad_by_inv_tau, uint16_t* grad_logits,
+                        float* grad_palette, void* workspace, size_t workspace_bytes, int64_t M,
+                        int64_t N, int64_t K, void* stream) {
+  return soft_bwd(x, grad_y, logits, logits_dtype, true, nullptr, seed, offset, palette, tau,
+                  scale_grad_by_inv_tau, grad_logits, grad_palette, workspace, workspace_bytes, M,
+                  N, K, stream);
 }
 
 }  // extern "C"

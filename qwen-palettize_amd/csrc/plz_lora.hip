@@ -45,7 +45,7 @@ __device__ __forceinline__ bf16x8 as_frag(uint4 v) { return __builtin_bit_cast(b
 #define PLZ_RW_WAVES 4
 #endif
 #ifndef PLZ_RW_U
-#define PLZ_RW_U 4
+#define PLZ_RW_U 2
 #endif
 constexpr int RW_NG = PLZ_RW_NG;        // MFMA row groups of 16 per workgroup
 constexpr int RW_ROWS = 16 * RW_NG;     // activation rows per workgroup

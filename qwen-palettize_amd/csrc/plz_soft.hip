@@ -11,31 +11,6 @@
 
 namespace plz {
 
-// ---- Philox4x32-10 (Salmon, Moraes, Dror, Shaw, SC'11) ---------------------------------
-struct U4 {
-  uint32_t x, y, z, w;
-};
-__host__ __device__ __forceinline__ U4 philox4x32_10(U4 c, uint32_t k0, uint32_t k1) {
-  const uint32_t M0 = 0xD2511F53u, M1 = 0xCD9E8D57u, W0 = 0x9E3779B9u, W1 = 0xBB67AE85u;
-#pragma unroll
-  for (int i = 0; i < 10; ++i) {
-    const uint64_t p0 = (uint64_t)M0 * c.x, p1 = (uint64_t)M1 * c.z;
-    const uint32_t hi0 = (uint32_t)(p0 >> 32), lo0 = (uint32_t)p0;
-    const uint32_t hi1 = (uint32_t)(p1 >> 32), lo1 = (uint32_t)p1;
-    c = U4{hi1 ^ c.y ^ k0, lo1, hi0 ^ c.w ^ k1, lo0};
-    k0 += W0;
-    k1 += W1;
-  }
-  return c;
-}
-
-// u = (top 23 bits + 0.5) / 2^23 lies in [2^-24, 1 - 2^-24]: every value is exact in fp32,
-// so u never rounds to 1 (which would make the noise +inf).
-__device__ __forceinline__ float gumbel_from_bits(uint32_t b) {
-  const float u = ((float)(b >> 9) + 0.5f) * (1.0f / 8388608.0f);
-  return -logf(-logf(u));
-}
-
 __global__ void philox_gumbel_kernel(float* __restrict__ out, int64_t n4, uint64_t seed,
                                      uint64_t offset) {
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -73,10 +48,13 @@ __global__ void lcg_gumbel_kernel(float* __restrict__ out, uint32_t seed, int64_
 
 // ---- build W -------------------------------------------------------------------------
 // One thread per 2 consecutive k of one row: 16 B of logits, 32 B of noise in; 4 B out.
+// GEN: the noise is drawn here (Philox at counter offset + n*K + k, the values
+// plz_gumbel_philox would have stored) instead of read.
+template <bool GEN>
 __device__ __forceinline__ void build_w_pair(const uint16_t* __restrict__ logits, int f16,
-                                             const float* __restrict__ noise,
-                                             const float* __restrict__ pal, float inv_tau,
-                                             int mode, uint16_t* __restrict__ w,
+                                             const float* __restrict__ noise, uint64_t seed,
+                                             uint64_t offset, const float* __restrict__ pal,
+                                             float inv_tau, int mode, uint16_t* __restrict__ w,
                                              uint16_t* __restrict__ w_soft, int64_t K, int64_t t) {
   const int64_t half = K / 2;
   const int64_t n = t / half, k = 2 * (t % half);
@@ -84,10 +62,20 @@ __device__ __forceinline__ void build_w_pair(const uint16_t* __restrict__ logits
   const float pc[4] = {p.x, p.y, p.z, p.w};
   const int64_t e0 = (n * K + k) * 4;
   const uint4 lg = *reinterpret_cast<const uint4*>(logits + e0);
-  const float4 z0 = *reinterpret_cast<const float4*>(noise + e0);
-  const float4 z1 = *reinterpret_cast<const float4*>(noise + e0 + 4);
   const uint32_t lw[4] = {lg.x, lg.y, lg.z, lg.w};
-  const float nz[8] = {z0.x, z0.y, z0.z, z0.w, z1.x, z1.y, z1.z, z1.w};
+  float nz[8];
+  if constexpr (GEN) {
+    float z[4];
+    philox_gumbel4(seed, offset + (uint64_t)(n * K + k), z);
+    nz[0] = z[0]; nz[1] = z[1]; nz[2] = z[2]; nz[3] = z[3];
+    philox_gumbel4(seed, offset + (uint64_t)(n * K + k + 1), z);
+    nz[4] = z[0]; nz[5] = z[1]; nz[6] = z[2]; nz[7] = z[3];
+  } else {
+    const float4 z0 = *reinterpret_cast<const float4*>(noise + e0);
+    const float4 z1 = *reinterpret_cast<const float4*>(noise + e0 + 4);
+    nz[0] = z0.x; nz[1] = z0.y; nz[2] = z0.z; nz[3] = z0.w;
+    nz[4] = z1.x; nz[5] = z1.y; nz[6] = z1.z; nz[7] = z1.w;
+  }
   uint32_t wo[2], so[2];
 #pragma unroll
   for (int el = 0; el < 2; ++el) {
@@ -127,13 +115,15 @@ __device__ __forceinline__ void build_w_pair(const uint16_t* __restrict__ logits
   if (w_soft) *reinterpret_cast<uint32_t*>(w_soft + o) = so[0] | (so[1] << 16);
 }
 
+template <bool GEN>
 __global__ void build_w_kernel(const uint16_t* __restrict__ logits, int f16,
-                               const float* __restrict__ noise, const float* __restrict__ pal,
-                               float inv_tau, int mode, uint16_t* __restrict__ w,
-                               uint16_t* __restrict__ w_soft, int64_t N, int64_t K) {
+                               const float* __restrict__ noise, uint64_t seed, uint64_t offset,
+                               const float* __restrict__ pal, float inv_tau, int mode,
+                               uint16_t* __restrict__ w, uint16_t* __restrict__ w_soft, int64_t N,
+                               int64_t K) {
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= N * (K / 2)) return;
-  build_w_pair(logits, f16, noise, pal, inv_tau, mode, w, w_soft, K, t);
+  build_w_pair<GEN>(logits, f16, noise, seed, offset, pal, inv_tau, mode, w, w_soft, K, t);
 }
 
 // Many linears in one launch (fused_lut_kernel.cu:2071-2211 batches the per-layer build the
@@ -150,8 +140,8 @@ __global__ void build_w_batched_kernel(const plz_build_w_desc* __restrict__ desc
   const plz_build_w_desc d = descs[lo];
   const int64_t t = (b - d.block_begin) * kBuildWBlock + threadIdx.x;
   if (t >= d.N * (d.K / 2)) return;
-  build_w_pair(d.logits, d.logits_dtype == PLZ_DT_FP16, d.noise, d.palette, inv_tau, mode, d.w,
-               d.w_soft, d.K, t);
+  build_w_pair<false>(d.logits, d.logits_dtype == PLZ_DT_FP16, d.noise, 0, 0, d.palette, inv_tau,
+                      mode, d.w, d.w_soft, d.K, t);
 }
 
 }  // namespace plz
@@ -183,26 +173,47 @@ int plz_gumbel_lcg(float* noise, uint32_t seed, int64_t N, int64_t K, void* stre
   return check_launch("plz_gumbel_lcg");
 }
 
+static int build_w(const uint16_t* logits, int logits_dtype, bool gen, const float* noise,
+                   uint64_t seed, uint64_t offset, const float* palette, float tau, int mode,
+                   uint16_t* w, uint16_t* w_soft, int64_t N, int64_t K, void* stream,
+                   const char* what) {
+  PLZ_REQUIRE(N >= 0 && K >= 0, "%s: negative shape", what);
+  PLZ_REQUIRE(K % 256 == 0, "%s: K (%lld) must be a multiple of 256", what, (long long)K);
+  PLZ_REQUIRE(logits_dtype == PLZ_DT_BF16 || logits_dtype == PLZ_DT_FP16,
+              "%s: logits dtype must be bf16 or fp16", what);
+  PLZ_REQUIRE(mode == PLZ_W_SOFT || mode == PLZ_W_HARD_NOISY || mode == PLZ_W_HARD_PLAIN,
+              "%s: unknown mode %d", what, mode);
+  PLZ_REQUIRE(tau > 0.f, "%s: tau must be positive", what);
+  if (N == 0 || K == 0) return PLZ_OK;
+  PLZ_REQUIRE(logits && palette && w && (gen || noise), "%s: null pointer", what);
+  PLZ_REQUIRE((((uintptr_t)logits | (uintptr_t)noise | (uintptr_t)palette) & 15) == 0 &&
+                  (((uintptr_t)w | (uintptr_t)w_soft) & 3) == 0,
+              "%s: misaligned pointer", what);
+  const int64_t n = N * K / 2;
+  const dim3 grid((unsigned)((n + 255) / 256));
+  const int f16 = logits_dtype == PLZ_DT_FP16 ? 1 : 0;
+  if (gen)
+    hipLaunchKernelGGL(build_w_kernel<true>, grid, dim3(256), 0, (hipStream_t)stream, logits, f16,
+                       nullptr, seed, offset, palette, 1.f / tau, mode, w, w_soft, N, K);
+  else
+    hipLaunchKernelGGL(build_w_kernel<false>, grid, dim3(256), 0, (hipStream_t)stream, logits,
+                       f16, noise, (uint64_t)0, (uint64_t)0, palette, 1.f / tau, mode, w, w_soft,
+                       N, K);
+  return check_launch(what);
+}
+
 int plz_soft_build_w(const uint16_t* logits, int logits_dtype, const float* noise,
                      const float* palette, float tau, int mode, uint16_t* w, uint16_t* w_soft,
                      int64_t N, int64_t K, void* stream) {
-  PLZ_REQUIRE(N >= 0 && K >= 0, "plz_soft_build_w: negative shape");
-  PLZ_REQUIRE(K % 256 == 0, "plz_soft_build_w: K (%lld) must be a multiple of 256", (long long)K);
-  PLZ_REQUIRE(logits_dtype == PLZ_DT_BF16 || logits_dtype == PLZ_DT_FP16,
-              "plz_soft_build_w: logits dtype must be bf16 or fp16");
-  PLZ_REQUIRE(mode == PLZ_W_SOFT || mode == PLZ_W_HARD_NOISY || mode == PLZ_W_HARD_PLAIN,
-              "plz_soft_build_w: unknown mode %d", mode);
-  PLZ_REQUIRE(tau > 0.f, "plz_soft_build_w: tau must be positive");
-  if (N == 0 || K == 0) return PLZ_OK;
-  PLZ_REQUIRE(logits && noise && palette && w, "plz_soft_build_w: null pointer");
-  PLZ_REQUIRE((((uintptr_t)logits | (uintptr_t)noise | (uintptr_t)palette) & 15) == 0 &&
-                  (((uintptr_t)w | (uintptr_t)w_soft) & 3) == 0,
-              "plz_soft_build_w: misaligned pointer");
-  const int64_t n = N * K / 2;
-  hipLaunchKernelGGL(build_w_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
-                     (hipStream_t)stream, logits, logits_dtype == PLZ_DT_FP16 ? 1 : 0, noise,
-                     palette, 1.f / tau, mode, w, w_soft, N, K);
-  return check_launch("plz_soft_build_w");
+  return build_w(logits, logits_dtype, false, noise, 0, 0, palette, tau, mode, w, w_soft, N, K,
+                 stream, "plz_soft_build_w");
+}
+
+int plz_soft_build_w_philox(const uint16_t* logits, int logits_dtype, uint64_t seed,
+                            uint64_t offset, const float* palette, float tau, int mode,
+                            uint16_t* w, uint16_t* w_soft, int64_t N, int64_t K, void* stream) {
+  return build_w(logits, logits_dtype, true, nullptr, seed, offset, palette, tau, mode, w, w_soft,
+                 N, K, stream, "plz_soft_build_w_philox");
 }
 
 int64_t plz_build_w_plan(plz_build_w_desc* descs, int n) {

@@ -63,10 +63,12 @@ SIGNATURES: dict[str, tuple] = {
     "plz_gumbel_philox": (i32, [p, i64, u64, u64, p]),
     "plz_gumbel_lcg": (i32, [p, u32, i64, i64, p]),
     "plz_soft_build_w": (i32, [p, i32, p, p, f32, i32, p, p, i64, i64, p]),
+    "plz_soft_build_w_philox": (i32, [p, i32, u64, u64, p, f32, i32, p, p, i64, i64, p]),
     "plz_build_w_plan": (i64, [C.POINTER(BuildWDesc), i32]),
     "plz_soft_build_w_batched": (i32, [p, i32, i64, f32, i32, p]),
     "plz_soft_bwd_workspace": (sz, [i64, i64, i64]),
     "plz_soft_bwd": (i32, [p, p, p, i32, p, p, f32, i32, p, p, p, sz, i64, i64, i64, p]),
+    "plz_soft_bwd_philox": (i32, [p, p, p, i32, u64, u64, p, f32, i32, p, p, p, sz, i64, i64, i64, p]),
     "plz_lora_project": (i32, [p, p, f32, p, i64, i64, i32, p]),
     "plz_lora_grad_t": (i32, [p, p, f32, p, i64, i64, i32, p]),
     "plz_lora_weight_grads_workspace": (sz, [i64, i64, i64, i32]),

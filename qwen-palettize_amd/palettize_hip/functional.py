@@ -74,7 +74,10 @@ class SoftLUTLinearFunction(torch.autograd.Function):
         w, _ = ops.soft_build_w(logits, noise, palette, tau, mode)
         t = ops.lora_project(x, lora_a, lora_scale) if lora_a is not None else None
         y = ops.linear_fwd_dense(x, w, bias, t, lora_b)
-        ctx.save_for_backward(x, palette, logits, noise, w, lora_a, lora_b, t)
+        # a Philox noise descriptor is redrawn in the backward's epilogue, not stored
+        ctx.philox = noise if isinstance(noise, ops.PhiloxNoise) else None
+        ctx.save_for_backward(x, palette, logits, None if ctx.philox else noise, w, lora_a, lora_b,
+                              t)
         ctx.tau = float(tau)
         ctx.lora_scale = float(lora_scale)
         ctx.scale_by_inv_tau = bool(scale_by_inv_tau)
@@ -85,6 +88,8 @@ class SoftLUTLinearFunction(torch.autograd.Function):
     @staticmethod
     def backward(ctx, gy):
         x, palette, logits, noise, w, lora_a, lora_b, t = ctx.saved_tensors
+        if ctx.philox is not None:
+            noise = ctx.philox
         gy = gy.contiguous()
         need = ctx.needs_input_grad
         need_x, need_pal, need_log, need_b, need_la, need_lb = (

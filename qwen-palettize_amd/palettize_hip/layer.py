@@ -161,9 +161,15 @@ class SoftPalettizedLinear(nn.Module):
         return ops.gumbel_philox((self.out_features, self.in_features, 4), seed=self.noise_seed,
                                  offset=off, device=self.index_logits.device)
 
+    def next_noise_spec(self):
+        """The next forward's noise as a Philox descriptor (drawn inside the kernels)."""
+        off = self.noise_counter
+        self.noise_counter += self.out_features * self.in_features
+        return ops.PhiloxNoise(self.noise_seed, off)
+
     def forward(self, x):
         lead = x.shape[:-1]
-        noise = self.next_noise()
+        noise = self.next_noise_spec() if x.is_cuda else self.next_noise()
         y = SoftLUTLinearFunction.apply(x.reshape(-1, x.shape[-1]), self.palette, self.index_logits,
                                         noise, self.tau, None, self.lora_a, self.lora_b,
                                         self.lora_scale, self.mode, False)

@@ -224,14 +224,29 @@ def gumbel_lcg(N: int, K: int, seed: int, device="cuda"):
     return out
 
 
+class PhiloxNoise:
+    """Gumbel noise drawn inside the soft kernels instead of a tensor: the values
+    gumbel_philox(shape, seed, offset) would hold (Philox counter offset + n*K + k for the 4
+    classes of weight (n, k)). Accepted wherever a noise tensor [N, K, 4] is."""
+
+    def __init__(self, seed: int, offset: int):
+        self.seed, self.offset = int(seed), int(offset)
+
+    def materialize(self, N: int, K: int, device):
+        return gumbel_philox((N, K, 4), seed=self.seed, offset=self.offset, device=device)
+
+
 def _soft_shapes(logits, noise, palette):
     if logits.dtype not in (torch.bfloat16, torch.float16):
         raise TypeError("logits must be bf16 or fp16")
     _need(logits, "logits", None, 3)
-    _need(noise, "noise", torch.float32, 3)
     _need(palette, "palette", torch.float32, 3)
     N, K, four = logits.shape
-    if four != 4 or tuple(noise.shape) != (N, K, 4) or tuple(palette.shape) != (N, K // 256, 4):
+    if not isinstance(noise, PhiloxNoise):
+        _need(noise, "noise", torch.float32, 3)
+        if tuple(noise.shape) != (N, K, 4):
+            raise ValueError("logits [N,K,4], noise [N,K,4], palette [N,K/256,4] expected")
+    if four != 4 or tuple(palette.shape) != (N, K // 256, 4):
         raise ValueError("logits [N,K,4], noise [N,K,4], palette [N,K/256,4] expected")
     return N, K
 
@@ -241,8 +256,12 @@ def soft_build_w(logits, noise, palette, tau: float, mode: int = _lib.PLZ_W_HARD
     N, K = _soft_shapes(logits, noise, palette)
     w = torch.empty((N, K), dtype=torch.bfloat16, device=logits.device)
     ws = torch.empty((N, K), dtype=torch.bfloat16, device=logits.device) if want_soft else None
-    call("plz_soft_build_w", _ptr(logits), _DT[logits.dtype], _ptr(noise), _ptr(palette),
-         float(tau), int(mode), _ptr(w), _ptr(ws), N, K, _stream(logits))
+    if isinstance(noise, PhiloxNoise):
+        call("plz_soft_build_w_philox", _ptr(logits), _DT[logits.dtype], noise.seed, noise.offset,
+             _ptr(palette), float(tau), int(mode), _ptr(w), _ptr(ws), N, K, _stream(logits))
+    else:
+        call("plz_soft_build_w", _ptr(logits), _DT[logits.dtype], _ptr(noise), _ptr(palette),
+             float(tau), int(mode), _ptr(w), _ptr(ws), N, K, _stream(logits))
     return w, ws
 
 
@@ -292,9 +311,14 @@ def soft_bwd(x, grad_y, logits, noise, palette, tau: float, scale_by_inv_tau: bo
     gl = torch.empty_like(logits)
     gp = torch.empty((N, K // 256, 4), dtype=torch.float32, device=x.device)
     ws = _workspace(query("plz_soft_bwd_workspace", M, N, K), x.device)
-    call("plz_soft_bwd", _ptr(x), _ptr(grad_y), _ptr(logits), _DT[logits.dtype], _ptr(noise),
-         _ptr(palette), float(tau), int(bool(scale_by_inv_tau)), _ptr(gl), _ptr(gp), _ptr(ws),
-         ws.numel(), M, N, K, _stream(x))
+    if isinstance(noise, PhiloxNoise):
+        call("plz_soft_bwd_philox", _ptr(x), _ptr(grad_y), _ptr(logits), _DT[logits.dtype],
+             noise.seed, noise.offset, _ptr(palette), float(tau), int(bool(scale_by_inv_tau)),
+             _ptr(gl), _ptr(gp), _ptr(ws), ws.numel(), M, N, K, _stream(x))
+    else:
+        call("plz_soft_bwd", _ptr(x), _ptr(grad_y), _ptr(logits), _DT[logits.dtype], _ptr(noise),
+             _ptr(palette), float(tau), int(bool(scale_by_inv_tau)), _ptr(gl), _ptr(gp), _ptr(ws),
+             ws.numel(), M, N, K, _stream(x))
     return gl, gp
 
 

@@ -161,3 +161,29 @@ def test_soft_bwd_full_gate_shape_sampled_rows(dev):
     assert_close(f32(gl[rows.to(dev)]), want_gl, what="grad_logits sampled rows")
     assert_close(f32(gp[rows.to(dev)]), want_gp, max_rel=1e-3, min_cos=0.99999,
                  what="grad_palette sampled rows")
+
+
+@pytest.mark.parametrize("mode", [PLZ_W_SOFT, PLZ_W_HARD_NOISY, PLZ_W_HARD_PLAIN])
+def test_soft_build_w_philox_draws_the_tensor_noise(dev, mode):
+    """Noise drawn inside build-W equals plz_gumbel_philox's tensor bit for bit, so W too."""
+    N, K = 264, 768
+    logits, _, pal = _soft_inputs(N, K, seed=41)
+    spec = ops.PhiloxNoise(seed=0xABCDEF123, offset=977)
+    noise = spec.materialize(N, K, dev)
+    w1, s1 = ops.soft_build_w(logits.to(dev), noise, pal.to(dev), 0.5, mode, want_soft=True)
+    w2, s2 = ops.soft_build_w(logits.to(dev), spec, pal.to(dev), 0.5, mode, want_soft=True)
+    assert torch.equal(w1, w2) and torch.equal(s1, s2)
+
+
+@pytest.mark.parametrize("M,N,K", [(192, 256, 512), (2048, 1024, 2560)])
+def test_soft_bwd_philox_matches_tensor_noise(dev, M, N, K):
+    """The backward's epilogue redraws the forward's Philox noise: identical to passing the
+    materialised noise (fused epilogue and split-over-M paths)."""
+    logits, _, pal = _soft_inputs(N, K, seed=M)
+    x = randn_bf16(M, K, seed=M + 1)
+    gy = randn_bf16(M, N, seed=M + 2)
+    spec = ops.PhiloxNoise(seed=77, offset=12345)
+    noise = spec.materialize(N, K, dev)
+    a = ops.soft_bwd(x.to(dev), gy.to(dev), logits.to(dev), noise, pal.to(dev), 0.5)
+    b = ops.soft_bwd(x.to(dev), gy.to(dev), logits.to(dev), spec, pal.to(dev), 0.5)
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
