@@ -161,6 +161,40 @@ __global__ __launch_bounds__(kThreads) void adamw_kernel(const plz_adamw_desc* _
   const float step_size = d.lr / h.bc1;
   const float decay = 1.f - d.lr * h.weight_decay;
   float* p32 = d.master ? d.master : reinterpret_cast<float*>(d.param);
+  if (base + kBlockElems <= d.n) {
+    // whole block in range: every chunk's loads are issued before any chunk is updated (the
+    // state arrays may alias for all the compiler knows, so it would not hoist them itself)
+    float g[kChunks][kVec], p[kChunks][kVec], m[kChunks][kVec], v[kChunks][kVec];
+#pragma unroll
+    for (int ch = 0; ch < kChunks; ++ch) {
+      const int64_t i0 = base + ((int64_t)ch * kThreads + threadIdx.x) * kVec;
+      grad8(d, i0, g[ch]);
+      load8(p32 + i0, p[ch]);
+      load8(d.exp_avg + i0, m[ch]);
+      load8(d.exp_avg_sq + i0, v[ch]);
+    }
+#pragma unroll
+    for (int ch = 0; ch < kChunks; ++ch) {
+      const int64_t i0 = base + ((int64_t)ch * kThreads + threadIdx.x) * kVec;
+#pragma unroll
+      for (int j = 0; j < kVec; ++j)
+        adamw_one(g[ch][j] * c, p[ch][j], m[ch][j], v[ch][j], step_size, decay, h, d.clamp_lo,
+                  d.clamp_hi);
+      store8(d.exp_avg + i0, m[ch]);
+      store8(d.exp_avg_sq + i0, v[ch]);
+      store8(p32 + i0, p[ch]);
+      if (d.master && d.dtype == PLZ_DT_BF16) {
+        uint32_t w[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) w[j] = f2bf2(p[ch][2 * j], p[ch][2 * j + 1]);
+        *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(d.param) + i0) =
+            make_uint4(w[0], w[1], w[2], w[3]);
+      } else if (d.master) {
+        store8(reinterpret_cast<float*>(d.param) + i0, p[ch]);
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int ch = 0; ch < kChunks; ++ch) {
     const int64_t i0 = base + ((int64_t)ch * kThreads + threadIdx.x) * kVec;
