@@ -319,6 +319,16 @@ int plz_rope_fwd(const uint16_t* x, const float* cos_table, const float* sin_tab
 int plz_rope_bwd(const uint16_t* grad_y, const float* cos_table, const float* sin_table,
                  uint16_t* grad_x, int64_t rows, int64_t seq, int heads, int head_dim,
                  void* stream);
+/* Causal grouped-query attention forward (flash-style): q, o bf16 [batch, seq, heads, 128],
+ * k, v bf16 [batch, seq, kv_heads, 128], heads % kv_heads == 0, seq % 128 == 0;
+ * o = softmax(q k^T * scale, causal) v per head (kv head = head / (heads / kv_heads)),
+ * lse fp32 [batch, heads, seq] = log-sum-exp of the scaled scores. Replaces
+ * torch scaled_dot_product_attention(is_causal=True) of the HF Qwen3 attention the reference
+ * runs (transformers modeling_qwen3.py via qwen_model.py:590). head_dim != 128:
+ * PLZ_EUNSUPPORTED. */
+int plz_attn_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o, float* lse,
+                 int batch, int seq, int heads, int kv_heads, int head_dim, float scale,
+                 void* stream);
 /* Distillation loss of train_qwen.py:229-249 (compute_loss, '1-cos+norm_mse'):
  * loss = wc mean_rows(1 - cos(s_r, t_r)) + wm mean((s-t)^2) / max(mean(t^2), 1e-6), weights
  * normalised to sum 1; student/teacher bf16 [rows, dim]. out4 (device fp32 [4]) receives

@@ -44,6 +44,7 @@ SIGNATURES: dict[str, tuple] = {
     "plz_pack_indices": (i32, [p, p, i64, i64, p]),
     "plz_unpack_indices": (i32, [p, p, i64, i64, p]),
     "plz_dequant": (i32, [p, p, p, i64, i64, p]),
+    "plz_attn_fwd": (i32, [p, p, p, p, p, i32, i32, i32, i32, i32, f32, p]),
     "plz_rope_fwd": (i32, [p, p, p, p, i64, i64, i32, i32, p]),
     "plz_rope_bwd": (i32, [p, p, p, p, i64, i64, i32, i32, p]),
     "plz_distill_loss_workspace": (sz, [i64]),

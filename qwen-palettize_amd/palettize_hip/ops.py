@@ -525,3 +525,21 @@ def distill_loss_bwd(student, teacher, out4, ws, grad_loss, w_cos=0.5, w_mse=0.5
          float(w_cos), float(w_mse), float(eps), _ptr(gs), _ptr(ws), ws.numel(), rows, dim,
          _stream(student))
     return gs
+
+
+# ---- attention ---------------------------------------------------------------------------------
+def attn_fwd(q, k, v, scale=None):
+    """Causal grouped-query attention. q [B, S, Hq, 128], k/v [B, S, Hkv, 128] bf16 ->
+    (o [B, S, Hq, 128] bf16, lse [B, Hq, S] fp32)."""
+    for t, nm in ((q, "q"), (k, "k"), (v, "v")):
+        _need(t, nm, torch.bfloat16, 4)
+    B, S, Hq, D = q.shape
+    Hkv = k.shape[2]
+    if tuple(k.shape) != (B, S, Hkv, D) or tuple(v.shape) != (B, S, Hkv, D):
+        raise ValueError("q / k / v shape mismatch")
+    scale = D ** -0.5 if scale is None else float(scale)
+    o = torch.empty_like(q)
+    lse = torch.empty((B, Hq, S), dtype=torch.float32, device=q.device)
+    call("plz_attn_fwd", _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(lse), B, S, Hq, Hkv, D, scale,
+         _stream(q))
+    return o, lse
