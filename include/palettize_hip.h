@@ -329,6 +329,15 @@ int plz_rope_bwd(const uint16_t* grad_y, const float* cos_table, const float* si
 int plz_attn_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o, float* lse,
                  int batch, int seq, int heads, int kv_heads, int head_dim, float scale,
                  void* stream);
+/* Backward of plz_attn_fwd (the autograd of the same sdpa call): grad_q bf16 [batch, seq, heads,
+ * 128], grad_k, grad_v bf16 [batch, seq, kv_heads, 128] (summed over the heads sharing a kv
+ * head), from q, k, v, the forward's o and lse, and grad_o. Deterministic (no atomics); the
+ * workspace (fp32 [batch, heads, seq]: rowsum(grad_o * o)) comes from the query. */
+size_t plz_attn_bwd_workspace(int batch, int seq, int heads);
+int plz_attn_bwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* o,
+                 const uint16_t* grad_o, const float* lse, uint16_t* grad_q, uint16_t* grad_k,
+                 uint16_t* grad_v, void* workspace, size_t workspace_bytes, int batch, int seq,
+                 int heads, int kv_heads, int head_dim, float scale, void* stream);
 /* Distillation loss of train_qwen.py:229-249 (compute_loss, '1-cos+norm_mse'):
  * loss = wc mean_rows(1 - cos(s_r, t_r)) + wm mean((s-t)^2) / max(mean(t^2), 1e-6), weights
  * normalised to sum 1; student/teacher bf16 [rows, dim]. out4 (device fp32 [4]) receives

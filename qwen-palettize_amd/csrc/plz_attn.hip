@@ -16,6 +16,8 @@
 // read from LDS (ds_read_b64_tr_b16) in that same kv order. The running max and sum of each
 // query live in the two lanes that hold it (l and l^32). O^T is transposed through LDS so that
 // the bf16 output is written with 16-byte stores.
+#include <initializer_list>
+
 #include "plz_common.h"
 #include "palettize_hip.h"
 
@@ -215,46 +217,383 @@ __global__ __launch_bounds__(NT) void attn_fwd_kernel(const uint16_t* __restrict
 
 constexpr size_t kLds = 4 * TILE;  // 64 KB: two K/V blocks (also holds the output staging)
 
+// ---- backward -----------------------------------------------------------------------------
+// Two kernels, no atomics (deterministic):
+//   attn_bwd_dq_kernel   per 128 queries of one head: D_i = rowsum(dO o O) (written for the
+//                        second kernel), then over kv blocks S^T = K Q^T, dP^T = V dO^T,
+//                        dS^T = P^T o (dP^T - D), dQ^T += K^T dS^T; dQ = scale dQ.
+//   attn_bwd_dkv_kernel  per 128 kv rows of one kv head, over the G query heads sharing it and
+//                        the query blocks at or after the kv rows: S = Q K^T, dP = dO V^T,
+//                        P, dS as above, dV^T += dO^T P, dK^T += Q^T dS; dK = scale dK.
+// The accumulators of S / S^T are directly the B operands of the following products in the
+// permuted k order that tr_frag reads (as in the forward). Every [64][128] tile uses the vswz
+// layout, which is conflict-free for both row-fragment and transposing reads.
+
+// A or B operand rows r (= lane % 32 row of the tile), d chunk 2 ks + h2
+__device__ __forceinline__ bf16x8 row_frag(const lds_u8* t, int r, int ks, int h2) {
+  return __builtin_bit_cast(
+      bf16x8, *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(t + v_off(r, 2 * ks + h2)));
+}
+
+// per-thread source offsets of a [64 rows][128 d] tile copy into the vswz layout (4 chunks)
+__device__ __forceinline__ void tile_offsets(uint32_t row_bytes, uint32_t (&off)[4]) {
+#pragma unroll
+  for (int it = 0; it < 4; ++it) {
+    const int pch = it * NT + threadIdx.x, r = pch >> 4;
+    off[it] = (uint32_t)r * row_bytes + (uint32_t)(((pch & 15) ^ vswz(r)) << 4);
+  }
+}
+
+__device__ __forceinline__ float dot_bf8(u32x4 a, u32x4 b) {
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    s += bf2f(a[i] & 0xffffu) * bf2f(b[i] & 0xffffu) + bf2f(a[i] >> 16) * bf2f(b[i] >> 16);
+  return s;
+}
+
+// bf16 B-operand fragments (k-steps 2 mb, 2 mb + 1) from one 32x32 accumulator's values
+__device__ __forceinline__ void pack_frags(const float (&x)[16], bf16x8& lo, bf16x8& hi) {
+  lo = __builtin_bit_cast(bf16x8, u32x4{f2bf2(x[0], x[1]), f2bf2(x[2], x[3]), f2bf2(x[4], x[5]),
+                                        f2bf2(x[6], x[7])});
+  hi = __builtin_bit_cast(bf16x8, u32x4{f2bf2(x[8], x[9]), f2bf2(x[10], x[11]),
+                                        f2bf2(x[12], x[13]), f2bf2(x[14], x[15])});
+}
+
+// write a wave's transposed accumulators (rows d, columns = 32 output rows) as bf16 rows
+// [32][128] times mul, through this wave's LDS staging area (32 rows x 272 B)
+__device__ __forceinline__ void store_rows_t(const f32x16 (&acc)[D / 32], float mul, lds_u8* st,
+                                             uint16_t* out, int64_t row_stride, int lane) {
+  const int h2 = lane >> 5, ql = lane & 31;
+#pragma unroll
+  for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int d = 32 * db + 8 * (e >> 2) + 4 * h2 + (e & 3);
+      *reinterpret_cast<__attribute__((address_space(3))) uint16_t*>(st + ql * 272 + d * 2) =
+          (uint16_t)f2bf(acc[db][e] * mul);
+    }
+  __builtin_amdgcn_s_waitcnt(0);
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int it = 0; it < 8; ++it) {
+    const int ch = it * 64 + lane, r = ch >> 4, c = ch & 15;
+    const u32x4 val = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(st + r * 272 + c * 16);
+    *reinterpret_cast<u32x4*>(out + (int64_t)r * row_stride + 8 * c) = val;
+  }
+}
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+// grid: S/128 x Hq x B, in longest-first order (the last query blocks see the most kv blocks)
+__global__ __launch_bounds__(NT) void attn_bwd_dq_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+    const uint16_t* __restrict__ o, const uint16_t* __restrict__ dout,
+    const float* __restrict__ lse, uint16_t* __restrict__ dq, float* __restrict__ dsum_out, int B,
+    int S, int Hq, int Hkv, float scale_log2, float scale) {
+  extern __shared__ uint4 smem[];
+  lds_u8* lds = (lds_u8*)smem;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h2 = lane >> 5, ql = lane & 31;
+  const int nqb = S / BM;
+  int id = blockIdx.x;
+  const int qb = nqb - 1 - id / (Hq * B);
+  id %= Hq * B;
+  const int h = id % Hq, b = id / Hq;
+  const int hk = h / (Hq / Hkv);
+  const int q0 = qb * BM;
+  const int qrow = q0 + 32 * wave + ql;
+  const int64_t qstride = (int64_t)Hq * D, kstride = (int64_t)Hkv * D;
+
+  bf16x8 qf[D / 16], df[D / 16];
+  float dsum = 0.f;
+  {
+    const int64_t base = ((int64_t)b * S + qrow) * qstride + (int64_t)h * D + 8 * h2;
+#pragma unroll
+    for (int ks = 0; ks < D / 16; ++ks) {
+      const u32x4 qv = *reinterpret_cast<const u32x4*>(q + base + 16 * ks);
+      const u32x4 dv = *reinterpret_cast<const u32x4*>(dout + base + 16 * ks);
+      const u32x4 ov = *reinterpret_cast<const u32x4*>(o + base + 16 * ks);
+      qf[ks] = __builtin_bit_cast(bf16x8, qv);
+      df[ks] = __builtin_bit_cast(bf16x8, dv);
+      dsum += dot_bf8(dv, ov);
+    }
+  }
+  dsum += __shfl_xor(dsum, 32);
+  const int64_t li = ((int64_t)b * Hq + h) * S + qrow;
+  const float nl = -lse[li] * kLog2e;
+  if (h2 == 0) dsum_out[li] = dsum;
+
+  const int64_t kv_bytes = (int64_t)S * kstride * 2;
+  const BufRsrc rk = make_rsrc(k + (int64_t)b * S * kstride + (int64_t)hk * D, (uint32_t)kv_bytes);
+  const BufRsrc rv = make_rsrc(v + (int64_t)b * S * kstride + (int64_t)hk * D, (uint32_t)kv_bytes);
+  uint32_t off[4];
+  tile_offsets((uint32_t)(kstride * 2), off);
+  const int wb = __builtin_amdgcn_readfirstlane(wave * 1024);
+  auto issue = [&](int slot, int kb) {
+    lds_u8* ks_ = lds + slot * 2 * TILE;
+    const uint32_t base = (uint32_t)(kb * BN) * (uint32_t)(kstride * 2);
+#pragma unroll
+    for (int it = 0; it < 4; ++it) dma16(rk, ks_ + it * NT * 16 + wb, off[it] + base);
+#pragma unroll
+    for (int it = 0; it < 4; ++it) dma16(rv, ks_ + TILE + it * NT * 16 + wb, off[it] + base);
+  };
+
+  f32x16 dqt[D / 32];
+#pragma unroll
+  for (int db = 0; db < D / 32; ++db) dqt[db] = f32x16{};
+  const int nkb = (q0 + BM) / BN;
+  issue(0, 0);
+  for (int kb = 0; kb < nkb; ++kb) {
+    const int cur = kb & 1;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (kb + 1 < nkb) issue(cur ^ 1, kb + 1);
+    const lds_u8* ks_ = lds + cur * 2 * TILE;
+    const lds_u8* vs_ = ks_ + TILE;
+    const int kv0 = kb * BN;
+    if (kv0 > q0 + 32 * wave + 31) continue;
+    f32x16 st[2] = {f32x16{}, f32x16{}}, dpt[2] = {f32x16{}, f32x16{}};
+#pragma unroll
+    for (int ks = 0; ks < D / 16; ++ks)
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) {
+        st[nb] = mfma32(row_frag(ks_, 32 * nb + ql, ks, h2), qf[ks], st[nb]);
+        dpt[nb] = mfma32(row_frag(vs_, 32 * nb + ql, ks, h2), df[ks], dpt[nb]);
+      }
+    bf16x8 dsf[4];
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+      float ds[16];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int kv = kv0 + 32 * nb + 8 * (e >> 2) + 4 * h2 + (e & 3);
+        const float p = kv <= qrow ? exp2f(fmaf(st[nb][e], scale_log2, nl)) : 0.f;
+        ds[e] = p * (dpt[nb][e] - dsum);
+      }
+      pack_frags(ds, dsf[2 * nb], dsf[2 * nb + 1]);
+    }
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int db = 0; db < D / 32; ++db) dqt[db] = mfma32(vt_frag(ks_, 32 * db, ks, lane), dsf[ks], dqt[db]);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  store_rows_t(dqt, scale, lds + wave * (32 * 272),
+               dq + ((int64_t)b * S + q0 + 32 * wave) * qstride + (int64_t)h * D, qstride, lane);
+}
+
+constexpr int BKV = 128;  // kv rows per dK/dV workgroup (32 per wave)
+constexpr int BQ = 64;    // query rows per block of the dK/dV loop
+constexpr int QSLOT = 2 * TILE + 512;  // Q tile, dO tile, lse[64], D[64]
+constexpr size_t kLdsDkv = 2 * 4 * 32 * 272 > 2 * QSLOT ? 2 * 4 * 32 * 272 : 2 * QSLOT;
+
+// grid: S/128 x Hkv x B, in longest-first order (the first kv blocks see the most queries)
+__global__ __launch_bounds__(NT) void attn_bwd_dkv_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+    const uint16_t* __restrict__ dout, const float* __restrict__ lse,
+    const float* __restrict__ dsum, uint16_t* __restrict__ dk, uint16_t* __restrict__ dv, int B,
+    int S, int Hq, int Hkv, float scale_log2, float scale) {
+  extern __shared__ uint4 smem[];
+  lds_u8* lds = (lds_u8*)smem;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h2 = lane >> 5, ql = lane & 31;
+  int id = blockIdx.x;
+  const int kb = id / (Hkv * B);
+  id %= Hkv * B;
+  const int hk = id % Hkv, b = id / Hkv;
+  const int G = Hq / Hkv;
+  const int kv0 = kb * BKV, kvw = kv0 + 32 * wave, kvrow = kvw + ql;
+  const int64_t qstride = (int64_t)Hq * D, kstride = (int64_t)Hkv * D;
+
+  bf16x8 kf[D / 16], vf[D / 16];
+  {
+    const int64_t base = ((int64_t)b * S + kvrow) * kstride + (int64_t)hk * D + 8 * h2;
+#pragma unroll
+    for (int ks = 0; ks < D / 16; ++ks) {
+      kf[ks] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(k + base + 16 * ks));
+      vf[ks] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(v + base + 16 * ks));
+    }
+  }
+
+  uint32_t off[4];
+  tile_offsets((uint32_t)(qstride * 2), off);
+  const int wb = __builtin_amdgcn_readfirstlane(wave * 1024);
+  const int qstart = kv0 / BQ, nq = S / BQ - qstart, T = G * nq;
+  const int64_t q_bytes = (int64_t)S * qstride * 2;
+  auto issue = [&](int slot, int t) {
+    const int g = t / nq, qblk = qstart + t % nq, h = hk * G + g;
+    lds_u8* qs = lds + slot * QSLOT;
+    const int64_t hoff = (int64_t)b * S * qstride + (int64_t)h * D;
+    const BufRsrc rq = make_rsrc(q + hoff, (uint32_t)q_bytes);
+    const BufRsrc rd = make_rsrc(dout + hoff, (uint32_t)q_bytes);
+    const uint32_t base = (uint32_t)(qblk * BQ) * (uint32_t)(qstride * 2);
+#pragma unroll
+    for (int it = 0; it < 4; ++it) dma16(rq, qs + it * NT * 16 + wb, off[it] + base);
+#pragma unroll
+    for (int it = 0; it < 4; ++it) dma16(rd, qs + TILE + it * NT * 16 + wb, off[it] + base);
+    if (wave < 2 && lane < 16) {  // lse (wave 0) and D (wave 1) of the 64 queries
+      const float* src = (wave == 0 ? lse : dsum) + ((int64_t)b * Hq + h) * S;
+      dma16(make_rsrc(src, (uint32_t)S * 4), qs + 2 * TILE + 256 * wave, (uint32_t)(qblk * BQ) * 4 + lane * 16);
+    }
+  };
+
+  f32x16 dvt[D / 32], dkt[D / 32];
+#pragma unroll
+  for (int db = 0; db < D / 32; ++db) dvt[db] = dkt[db] = f32x16{};
+  issue(0, 0);
+  for (int t = 0; t < T; ++t) {
+    const int cur = t & 1;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (t + 1 < T) issue(cur ^ 1, t + 1);
+    const int qb0 = (qstart + t % nq) * BQ;
+    if (qb0 + BQ - 1 < kvw) continue;  // every query of the block is before this wave's kv
+    const lds_u8* qs = lds + cur * QSLOT;
+    const lds_u8* dos = qs + TILE;
+    const lds_u8* lsl = qs + 2 * TILE;  // lse[64], then D[64]
+    f32x16 s[2] = {f32x16{}, f32x16{}}, dp[2] = {f32x16{}, f32x16{}};
+#pragma unroll
+    for (int ks = 0; ks < D / 16; ++ks)
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb) {
+        s[mb] = mfma32(row_frag(qs, 32 * mb + ql, ks, h2), kf[ks], s[mb]);
+        dp[mb] = mfma32(row_frag(dos, 32 * mb + ql, ks, h2), vf[ks], dp[mb]);
+      }
+    bf16x8 pf[4], dsf[4];
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb) {
+      float p[16], ds[16];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int r = 32 * mb + 8 * j + 4 * h2;
+        const f32x4 L = *reinterpret_cast<const __attribute__((address_space(3))) f32x4*>(
+            lsl + r * 4);
+        const f32x4 Dv = *reinterpret_cast<const __attribute__((address_space(3))) f32x4*>(
+            lsl + 256 + r * 4);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int e = 4 * j + i;
+          const float pe = qb0 + r + i >= kvrow ? exp2f(fmaf(s[mb][e], scale_log2, -L[i] * kLog2e)) : 0.f;
+          p[e] = pe;
+          ds[e] = pe * (dp[mb][e] - Dv[i]);
+        }
+      }
+      pack_frags(p, pf[2 * mb], pf[2 * mb + 1]);
+      pack_frags(ds, dsf[2 * mb], dsf[2 * mb + 1]);
+    }
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int db = 0; db < D / 32; ++db) {
+        dvt[db] = mfma32(vt_frag(dos, 32 * db, ks, lane), pf[ks], dvt[db]);
+        dkt[db] = mfma32(vt_frag(qs, 32 * db, ks, lane), dsf[ks], dkt[db]);
+      }
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  const int64_t orow = ((int64_t)b * S + kvw) * kstride + (int64_t)hk * D;
+  store_rows_t(dkt, scale, lds + wave * (32 * 272), dk + orow, kstride, lane);
+  store_rows_t(dvt, 1.f, lds + (4 + wave) * (32 * 272), dv + orow, kstride, lane);
+}
+
 }  // namespace attn
 }  // namespace plz
 
 using namespace plz;
 using namespace plz::attn;
 
+namespace {
+
+int reserve_lds(const void* fn, size_t bytes, bool& done, const char* what) {
+  if (done) return PLZ_OK;
+  const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+  if (e != hipSuccess) {
+    set_error("%s: cannot reserve %zu bytes of LDS: %s", what, bytes, hipGetErrorString(e));
+    return PLZ_EHIP;
+  }
+  done = true;
+  return PLZ_OK;
+}
+
+// shared argument checks of the forward and backward; 1 = nothing to do
+int check_shape(const char* what, int batch, int seq, int heads, int kv_heads, int head_dim,
+                float scale) {
+  PLZ_REQUIRE(batch >= 0 && seq >= 0 && heads > 0 && kv_heads > 0 && heads % kv_heads == 0,
+              "%s: need heads a positive multiple of kv_heads", what);
+  if (head_dim != D) {
+    set_error("%s: head_dim %d is not supported (128 only)", what, head_dim);
+    return PLZ_EUNSUPPORTED;
+  }
+  PLZ_REQUIRE(seq % BM == 0, "%s: seq (%d) must be a multiple of %d", what, seq, BM);
+  PLZ_REQUIRE(scale > 0.f, "%s: scale must be positive", what);
+  PLZ_REQUIRE((int64_t)seq * heads * D * 2 < ((int64_t)1 << 31),
+              "%s: one sequence of q must span < 2 GiB", what);
+  return batch == 0 || seq == 0 ? 1 : PLZ_OK;
+}
+
+bool aligned16(std::initializer_list<const void*> ps) {
+  for (const void* p : ps)
+    if ((uintptr_t)p & 15) return false;
+  return true;
+}
+
+}  // namespace
+
 extern "C" {
 
 int plz_attn_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o, float* lse,
                  int batch, int seq, int heads, int kv_heads, int head_dim, float scale,
                  void* stream) {
-  PLZ_REQUIRE(batch >= 0 && seq >= 0 && heads > 0 && kv_heads > 0 && heads % kv_heads == 0,
-              "plz_attn_fwd: need heads a positive multiple of kv_heads");
-  if (head_dim != D) {
-    set_error("plz_attn_fwd: head_dim %d is not supported (128 only)", head_dim);
-    return PLZ_EUNSUPPORTED;
-  }
-  PLZ_REQUIRE(seq % BM == 0, "plz_attn_fwd: seq (%d) must be a multiple of %d", seq, BM);
-  PLZ_REQUIRE(scale > 0.f, "plz_attn_fwd: scale must be positive");
-  if (batch == 0 || seq == 0) return PLZ_OK;
+  const int rc = check_shape("plz_attn_fwd", batch, seq, heads, kv_heads, head_dim, scale);
+  if (rc != PLZ_OK) return rc == 1 ? PLZ_OK : rc;
   PLZ_REQUIRE(q && k && v && o && lse, "plz_attn_fwd: null pointer");
-  PLZ_REQUIRE((((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)o) & 15) == 0,
-              "plz_attn_fwd: q, k, v, o must be 16-byte aligned");
-  PLZ_REQUIRE((int64_t)seq * kv_heads * D * 2 < ((int64_t)1 << 31),
-              "plz_attn_fwd: one sequence of k or v must span < 2 GiB");
+  PLZ_REQUIRE(aligned16({q, k, v, o}), "plz_attn_fwd: q, k, v, o must be 16-byte aligned");
   static bool attr = false;
-  if (!attr) {
-    const hipError_t e = hipFuncSetAttribute((const void*)attn_fwd_kernel,
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLds);
-    if (e != hipSuccess) {
-      set_error("plz_attn_fwd: cannot reserve %zu bytes of LDS: %s", kLds, hipGetErrorString(e));
-      return PLZ_EHIP;
-    }
-    attr = true;
-  }
-  const float scale_log2 = scale * 1.4426950408889634f;
+  const int lr = reserve_lds((const void*)attn_fwd_kernel, kLds, attr, "plz_attn_fwd");
+  if (lr != PLZ_OK) return lr;
+  const float scale_log2 = scale * kLog2e;
   hipLaunchKernelGGL(attn_fwd_kernel, dim3((unsigned)(seq / BM), (unsigned)heads, (unsigned)batch),
                      dim3(NT), kLds, (hipStream_t)stream, q, k, v, o, lse, batch, seq, heads,
                      kv_heads, scale_log2);
   return check_launch("plz_attn_fwd");
+}
+
+size_t plz_attn_bwd_workspace(int batch, int seq, int heads) {
+  if (batch <= 0 || seq <= 0 || heads <= 0) return 0;
+  return (size_t)batch * (size_t)heads * (size_t)seq * sizeof(float);
+}
+
+int plz_attn_bwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* o,
+                 const uint16_t* grad_o, const float* lse, uint16_t* grad_q, uint16_t* grad_k,
+                 uint16_t* grad_v, void* workspace, size_t workspace_bytes, int batch, int seq,
+                 int heads, int kv_heads, int head_dim, float scale, void* stream) {
+  const int rc = check_shape("plz_attn_bwd", batch, seq, heads, kv_heads, head_dim, scale);
+  if (rc != PLZ_OK) return rc == 1 ? PLZ_OK : rc;
+  PLZ_REQUIRE(q && k && v && o && grad_o && lse && grad_q && grad_k && grad_v,
+              "plz_attn_bwd: null pointer");
+  PLZ_REQUIRE(aligned16({q, k, v, o, grad_o, lse, grad_q, grad_k, grad_v}),
+              "plz_attn_bwd: every tensor must be 16-byte aligned");
+  if (!workspace || workspace_bytes < plz_attn_bwd_workspace(batch, seq, heads) ||
+      ((uintptr_t)workspace & 15)) {
+    set_error("plz_attn_bwd: workspace of %zu bytes (16-byte aligned) required",
+              plz_attn_bwd_workspace(batch, seq, heads));
+    return PLZ_EWORKSPACE;
+  }
+  static bool attr_dq = false, attr_dkv = false;
+  int lr = reserve_lds((const void*)attn_bwd_dq_kernel, kLds, attr_dq, "plz_attn_bwd");
+  if (lr == PLZ_OK) lr = reserve_lds((const void*)attn_bwd_dkv_kernel, kLdsDkv, attr_dkv, "plz_attn_bwd");
+  if (lr != PLZ_OK) return lr;
+  const float scale_log2 = scale * kLog2e;
+  float* dsum = (float*)workspace;
+  hipLaunchKernelGGL(attn_bwd_dq_kernel, dim3((unsigned)(seq / BM) * heads * batch), dim3(NT), kLds,
+                     (hipStream_t)stream, q, k, v, o, grad_o, lse, grad_q, dsum, batch, seq,
+                     heads, kv_heads, scale_log2, scale);
+  int r = check_launch("plz_attn_bwd (dq)");
+  if (r != PLZ_OK) return r;
+  hipLaunchKernelGGL(attn_bwd_dkv_kernel, dim3((unsigned)(seq / BKV) * kv_heads * batch), dim3(NT),
+                     kLdsDkv, (hipStream_t)stream, q, k, v, grad_o, lse, dsum, grad_k, grad_v,
+                     batch, seq, heads, kv_heads, scale_log2, scale);
+  return check_launch("plz_attn_bwd (dk, dv)");
 }
 
 }  // extern "C"

@@ -45,6 +45,8 @@ SIGNATURES: dict[str, tuple] = {
     "plz_unpack_indices": (i32, [p, p, i64, i64, p]),
     "plz_dequant": (i32, [p, p, p, i64, i64, p]),
     "plz_attn_fwd": (i32, [p, p, p, p, p, i32, i32, i32, i32, i32, f32, p]),
+    "plz_attn_bwd_workspace": (sz, [i32, i32, i32]),
+    "plz_attn_bwd": (i32, [p, p, p, p, p, p, p, p, p, p, sz, i32, i32, i32, i32, i32, f32, p]),
     "plz_rope_fwd": (i32, [p, p, p, p, i64, i64, i32, i32, p]),
     "plz_rope_bwd": (i32, [p, p, p, p, i64, i64, i32, i32, p]),
     "plz_distill_loss_workspace": (sz, [i64]),

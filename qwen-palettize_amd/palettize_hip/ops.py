@@ -543,3 +543,21 @@ def attn_fwd(q, k, v, scale=None):
     call("plz_attn_fwd", _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(lse), B, S, Hq, Hkv, D, scale,
          _stream(q))
     return o, lse
+
+
+def attn_bwd(q, k, v, o, lse, grad_o, scale=None):
+    """Backward of attn_fwd: (grad_q, grad_k, grad_v), bf16 in the shapes of q, k, v."""
+    for t, nm in ((q, "q"), (k, "k"), (v, "v"), (o, "o"), (grad_o, "grad_o")):
+        _need(t, nm, torch.bfloat16, 4)
+    _need(lse, "lse", torch.float32, 3)
+    B, S, Hq, D = q.shape
+    Hkv = k.shape[2]
+    if (tuple(k.shape) != (B, S, Hkv, D) or tuple(v.shape) != (B, S, Hkv, D)
+            or o.shape != q.shape or grad_o.shape != q.shape or tuple(lse.shape) != (B, Hq, S)):
+        raise ValueError("attention backward shape mismatch")
+    scale = D ** -0.5 if scale is None else float(scale)
+    gq, gk, gv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    ws = _opt_workspace(query("plz_attn_bwd_workspace", B, S, Hq), q.device)
+    call("plz_attn_bwd", _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(grad_o), _ptr(lse), _ptr(gq),
+         _ptr(gk), _ptr(gv), _ptr(ws), _numel(ws), B, S, Hq, Hkv, D, scale, _stream(q))
+    return gq, gk, gv

@@ -42,3 +42,46 @@ def test_attn_fwd_matches_fp32(dev, B, S, Hq, Hkv, std):
     want_o, want_lse = _ref(q, k, v)
     assert_close(f32(o), want_o.numpy(), what="attention output")
     assert np.allclose(f32(lse), want_lse.numpy(), rtol=1e-4, atol=1e-4)
+
+
+def _ref_grads(q, k, v, go):
+    qf, kf, vf = (t.float().requires_grad_(True) for t in (q, k, v))
+    o, _ = _ref(qf, kf, vf)
+    o.backward(go.float())
+    return qf.grad, kf.grad, vf.grad
+
+
+@pytest.mark.parametrize("B,S,Hq,Hkv,std", [(2, 256, 8, 2, 1.0), (1, 512, 4, 4, 1.0),
+                                            (1, 128, 32, 8, 3.0), (1, 384, 6, 1, 1.0)])
+def test_attn_bwd_matches_fp32(dev, B, S, Hq, Hkv, std):
+    """dQ, dK, dV (dK / dV summed over the query heads of each kv head) against fp32 autograd
+    of the same attention; P and dS enter the products as bf16, as in the forward."""
+    q, k, v = _inputs(B, S, Hq, Hkv, seed=7 * S + Hq, std=std)
+    go = torch.randn(B, S, Hq, 128, generator=torch.Generator().manual_seed(S)).to(torch.bfloat16)
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    o, lse = ops.attn_fwd(qd, kd, vd)
+    gq, gk, gv = ops.attn_bwd(qd, kd, vd, o, lse, go.to(dev))
+    want = _ref_grads(q, k, v, go)
+    for got, ref, nm in zip((gq, gk, gv), want, ("grad_q", "grad_k", "grad_v")):
+        assert got.shape == ref.shape
+        assert_close(f32(got), ref.numpy(), what=nm)
+    again = ops.attn_bwd(qd, kd, vd, o, lse, go.to(dev))
+    assert all(torch.equal(a, b) for a, b in zip((gq, gk, gv), again)), "backward must be deterministic"
+
+
+def test_attn_bwd_layer_shape_sampled_heads(dev):
+    """The layer's shape (seq 512, 32 query / 8 kv heads, batch 2): every gradient finite, and
+    kv head 5 with its four query heads matches fp32 autograd."""
+    B, S, Hq, Hkv = 2, 512, 32, 8
+    q, k, v = _inputs(B, S, Hq, Hkv, seed=99)
+    go = torch.randn(B, S, Hq, 128, generator=torch.Generator().manual_seed(5)).to(torch.bfloat16)
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    o, lse = ops.attn_fwd(qd, kd, vd)
+    gq, gk, gv = ops.attn_bwd(qd, kd, vd, o, lse, go.to(dev))
+    assert all(bool(torch.isfinite(t).all()) for t in (gq, gk, gv))
+    hs = slice(20, 24)
+    want = _ref_grads(q[:, :, hs].contiguous(), k[:, :, 5:6].contiguous(),
+                      v[:, :, 5:6].contiguous(), go[:, :, hs].contiguous())
+    for got, ref, nm in zip((gq[:, :, hs], gk[:, :, 5:6], gv[:, :, 5:6]), want,
+                            ("grad_q", "grad_k", "grad_v")):
+        assert_close(f32(got), ref.numpy(), what=nm + " (layer shape)")
