@@ -200,10 +200,40 @@ def apply_rope(x, cos, sin):
 _GQA_NATIVE = [True]  # cleared when the SDPA backend refuses enable_gqa
 
 
+class AttentionFunction(torch.autograd.Function):
+    """Causal grouped-query attention on the GPU: plz_attn_fwd (o and the row log-sum-exp) and
+    plz_attn_bwd (dQ, and dK / dV summed over the query heads of each kv head)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v):
+        q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+        o, lse = ops.attn_fwd(q, k, v)
+        ctx.save_for_backward(q, k, v, o, lse)
+        return o
+
+    @staticmethod
+    def backward(ctx, go):
+        q, k, v, o, lse = ctx.saved_tensors
+        return ops.attn_bwd(q, k, v, o, lse, go.contiguous())
+
+
+def native_attention_ok(q, k):
+    """The attention kernels' shapes: bf16 GPU tensors, head_dim 128, seq a multiple of 128."""
+    return (q.is_cuda and q.dtype == torch.bfloat16 and k.dtype == torch.bfloat16
+            and q.shape[-1] == 128 and q.shape[1] % 128 == 0)
+
+
 def attention(q, k, v, heads, kv_heads):
-    """q [B,S,H,D], k/v [B,S,Hkv,D] -> [B,S,H*D]; causal, grouped-query (kv repeated)."""
+    """q [B,S,H,D], k/v [B,S,Hkv,D] -> [B,S,H*D]; causal, grouped-query (kv repeated).
+    The HIP kernels run where their shape constraints hold; torch SDPA otherwise."""
     B, S, H, D = q.shape
     rep = heads // kv_heads
+    if native_attention_ok(q, k):
+        if torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad):
+            o = AttentionFunction.apply(q, k, v)
+        else:
+            o, _ = ops.attn_fwd(q.contiguous(), k.contiguous(), v.contiguous())
+        return o.view(B, S, H * D)
     qt = q.transpose(1, 2)
     if q.is_cuda:
         # flash / memory-efficient kernels only: the math fallback issues bf16 batched

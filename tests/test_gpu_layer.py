@@ -13,12 +13,15 @@ layer = pytest.importorskip("palettize_hip.layer")
 
 CFG = dict(hidden=256, heads=4, kv_heads=2, head_dim=64, intermediate=512, lora_rank=16,
            lora_alpha=16.0)
+# head_dim 128 and a sequence of 128: attention runs through plz_attn_fwd / plz_attn_bwd
+CFG_ATTN = dict(hidden=256, heads=4, kv_heads=2, head_dim=128, intermediate=512, lora_rank=16,
+                lora_alpha=16.0)
 
 
-def _setup(dev, seed=3):
-    cfg = layer.LayerConfig(**CFG)
+def _setup(dev, seed=3, cfg_kw=CFG, batch=2, seq=16):
+    cfg = layer.LayerConfig(**cfg_kw)
     tr = layer.LayerTrainer(cfg, dev, seed=seed, lora_b_std=0.02)
-    hs = (torch.randn(2, 16, cfg.hidden, generator=torch.Generator().manual_seed(seed)))
+    hs = (torch.randn(batch, seq, cfg.hidden, generator=torch.Generator().manual_seed(seed)))
     return cfg, tr, hs.to(torch.bfloat16)
 
 
@@ -42,8 +45,14 @@ def _cpu_params(tr):
     return p, w
 
 
-def test_layer_step_forward_backward_matches_cpu_reference(dev):
-    cfg, tr, hs = _setup(dev)
+@pytest.mark.parametrize("cfg_kw,batch,seq", [(CFG, 2, 16), (CFG_ATTN, 2, 128)],
+                         ids=["sdpa-attention", "hip-attention"])
+def test_layer_step_forward_backward_matches_cpu_reference(dev, cfg_kw, batch, seq):
+    cfg, tr, hs = _setup(dev, cfg_kw=cfg_kw, batch=batch, seq=seq)
+    if cfg_kw is CFG_ATTN:
+        q = torch.zeros(batch, seq, cfg.heads, cfg.head_dim, dtype=torch.bfloat16, device=dev)
+        k = torch.zeros(batch, seq, cfg.kv_heads, cfg.head_dim, dtype=torch.bfloat16, device=dev)
+        assert layer.native_attention_ok(q, k)
     p, w = _cpu_params(tr)
     noises = {}
     for name in tr.student.NAMES:
