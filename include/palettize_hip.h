@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define PLZ_ABI_VERSION 4
+#define PLZ_ABI_VERSION 5
 
 /* status codes */
 #define PLZ_OK 0
@@ -219,6 +219,8 @@ typedef struct plz_gemv_desc {
   int64_t cost_begin;     /* filled by plz_gemv_plan: sum of K over the items before it */
   const float* palette_items; /* optional (may be NULL): the palettes repacked by
                                  plz_gemv_pack_palettes, read instead of `palette` */
+  const int32_t* packed_items; /* optional (may be NULL): the indices repacked by
+                                  plz_gemv_pack_indices, read instead of `packed` */
 } plz_gemv_desc;
 
 /* y[M,N] = x[M,K] W^T for 1 <= M <= 16 (bandwidth-bound; one pass over the packed weights).
@@ -233,13 +235,30 @@ int plz_lut_gemv(const uint16_t* x, const int32_t* packed, const float* palette,
 size_t plz_gemv_palette_items_bytes(int64_t N, int64_t K);
 int plz_gemv_pack_palettes(const float* palette, float* palette_items, int64_t N, int64_t K,
                            void* stream);
+/* Decode index layout (one-time repack): the packed indices [N, K/16] regrouped per 128-row
+ * item and 256-k stage into one contiguous 8 KB block each, in the order the GEMV's waves read
+ * them, with the 2-bit fields of every word permuted so that the dequantiser produces natural k
+ * order. Same bytes per weight (rows padded to a multiple of 128). */
+size_t plz_gemv_packed_items_bytes(int64_t N, int64_t K);
+int plz_gemv_pack_indices(const int32_t* packed, int32_t* packed_items, int64_t N, int64_t K,
+                          void* stream);
+/* plz_lut_gemv on weights in the two decode layouts (plz_gemv_pack_indices and
+ * plz_gemv_pack_palettes). */
+int plz_lut_gemv_decode(const uint16_t* x, const int32_t* packed_items,
+                        const float* palette_items, uint16_t* y, int64_t M, int64_t N, int64_t K,
+                        void* stream);
 /* Fills block_begin and cost_begin of n host descriptors and returns the total number of
  * 128-row work items (or a negative status). A descriptor with N > 0 needs K > 0. */
 int64_t plz_gemv_plan(plz_gemv_desc* descs, int n, int M);
+/* Index layout of a grouped launch: every descriptor's `packed` (native) or every
+ * descriptor's `packed_items` (decode layout). A descriptor whose array for the chosen layout is
+ * NULL reads zero indices (no fault). */
+#define PLZ_GEMV_NATIVE 0
+#define PLZ_GEMV_DECODE 1
 /* Runs n independent GEMVs (all with the same M) in one launch. descs_device is a copy of
  * the planned descriptors in device memory; total_blocks is plz_gemv_plan's result. */
 int plz_lut_gemv_grouped(const plz_gemv_desc* descs_device, int n, int64_t total_blocks, int M,
-                         void* stream);
+                         int layout, void* stream);
 
 /* ---- on-disk format converters ---------------------------------------------------------
  * .idx2 = the (K, N) index matrix (W^T) flattened row-major, 4 indices per byte, LSB first

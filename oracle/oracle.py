@@ -141,6 +141,34 @@ def reference_weight(indices_kn, pal_ref, group_size: int = 256) -> np.ndarray:
 
 
 # --------------------------------------------------------------------------------------
+# decode-GEMV index layout (this library's own; the reference has no decode path)
+# --------------------------------------------------------------------------------------
+
+
+def gemv_decode_k(B: int, j: int) -> int:
+    """k offset (within a word's 16) stored in field 8B + 2j of a decode-layout word."""
+    return (0 if B < 2 else 8) + 2 * j + (B & 1)
+
+
+def gemv_decode_layout(idx) -> np.ndarray:
+    """idx [N, K] (0..3) -> uint32 words [ceil(N/128), K/256, 4 waves, 2 blocks, 64 lanes, 4]:
+    lane l = 16q + r of block b of wave w holds the words of item row 32w + 16b + r for
+    k = 64q + 16t + (0..15) of the stage (t = word 0..3); field 8B + 2j of a word holds
+    k offset gemv_decode_k(B, j). Rows past N are zero."""
+    idx = np.asarray(idx, np.uint32)
+    N, K = idx.shape
+    items = (N + 127) // 128
+    full = np.zeros((items * 128, K), np.uint32)
+    full[:N] = idx
+    v = full.reshape(items, 4, 2, 16, K // 256, 4, 4, 16)  # item, w, b, r, stage, q, t, k16
+    out = np.zeros(v.shape[:-1], np.uint32)
+    for B in range(4):
+        for j in range(4):
+            out |= v[..., gemv_decode_k(B, j)] << np.uint32(8 * B + 2 * j)
+    return np.ascontiguousarray(out.transpose(0, 4, 1, 2, 5, 3, 6)).reshape(-1)
+
+
+# --------------------------------------------------------------------------------------
 # hard linear: forward / backward (fused_lut_linear_cuda.py:755-818,
 # fused_lut_kernel.cu:309-518, 551-720, 902-1123, 1129-1147)
 # --------------------------------------------------------------------------------------

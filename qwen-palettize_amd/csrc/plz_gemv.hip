@@ -13,7 +13,10 @@
 //   buffer_load ... lds (1 KB per wave instruction, whole cache lines, no VGPRs), NS-1 stages
 //   ahead in an NS-slot ring, across item boundaries -- the loads of the next item are in
 //   flight while this one finishes. Palettes may come prepacked per item and stage (2 KB
-//   contiguous, plz_gemv_pack_palettes) instead of 16 B per row strided by K/256 groups.
+//   contiguous, plz_gemv_pack_palettes) instead of 16 B per row strided by K/256 groups, and
+//   the packed indices may come in the decode layout (plz_gemv_pack_indices): each stage's
+//   8 KB contiguous in the order the waves read it, every word's 2-bit fields permuted so that
+//   the dequantiser emits natural k order (the x fragments are then plain 16-byte reads).
 // * Wave w owns rows 32w..32w+31 of the item (two MFMA row blocks of 16). Lane (row n%16,
 //   quarter q) dequantises 4 consecutive packed words (64 k) of its row per block and stage
 //   through v_perm_b32 byte tables into bf16 fragments (in a permuted k order that the x
@@ -38,6 +41,20 @@ __device__ __forceinline__ void dequant16_slots(uint32_t q, PalLut t, u32x4& a, 
     a[j] = perm(h, l, 0x05010400u);  // {w_j, w_j+4}
     b[j] = perm(h, l, 0x07030602u);  // {w_j+8, w_j+12}
   }
+}
+
+// Decode-layout word: field (8B + 2j) (j, B = 0..3) holds the index of k = kmap(B, j), so that
+// dequant16_slots returns a = k {0..7}, b = k {8..15} in order.
+__host__ __device__ constexpr int decode_k(int B, int j) {
+  return (B < 2 ? 0 : 8) + 2 * j + (B & 1);
+}
+__device__ __forceinline__ uint32_t decode_word(uint32_t w) {
+  uint32_t o = 0;
+#pragma unroll
+  for (int B = 0; B < 4; ++B)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o |= ((w >> (2 * decode_k(B, j))) & 3u) << (8 * B + 2 * j);
+  return o;
 }
 
 typedef __attribute__((address_space(3))) uint8_t lds_u8;
@@ -157,7 +174,8 @@ __device__ __forceinline__ void cursor_next(Cursor& c, const Table<GROUPED>& tb)
   cursor_load(c, tb);
 }
 
-template <int NPX, bool GROUPED>
+// DEC: indices in the decode layout (packed_items), else native (packed)
+template <int NPX, bool GROUPED, bool DEC>
 __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(const plz_gemv_desc* __restrict__ descs,
                                                           int n_desc, plz_gemv_desc single,
                                                           int M) {
@@ -194,20 +212,25 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(const plz_gemv_desc* _
     const int gpr = (int)(K / kPalGroup);
     if (pc.item != p_item) {  // new item: descriptors and per-lane base offsets
       p_item = pc.item;
-      rq = make_rsrc(pc.d.packed, live ? (uint32_t)(N * K / 4) : 0u);
+      // indices: native [N, K/16] words, or the decode layout [item][stage][8 KB]; a missing
+      // array (NULL) gets an empty range, so its copies read zeros
+      const void* qsrc = DEC ? (const void*)pc.d.packed_items : (const void*)pc.d.packed;
+      const int64_t qbytes = DEC ? (N + ROWS - 1) / ROWS * ROWS * (K / 4) : N * K / 4;
+      rq = make_rsrc(qsrc, live && qsrc ? (uint32_t)qbytes : 0u);
       // palettes: native [N, K/256, 4] (16 B per row and stage, rows gpr*16 B apart) or
       // prepacked [item][group][128 rows][4] (2 KB contiguous per stage)
       const bool pre = pc.d.palette_items != nullptr;
       const int64_t pbytes = pre ? (N + ROWS - 1) / ROWS * ROWS * gpr * 16 : N * gpr * 16;
-      rp = make_rsrc(pre ? (const void*)pc.d.palette_items : (const void*)pc.d.palette,
-                     live ? (uint32_t)pbytes : 0u);
+      const void* psrc = pre ? (const void*)pc.d.palette_items : (const void*)pc.d.palette;
+      rp = make_rsrc(psrc, live && psrc ? (uint32_t)pbytes : 0u);
       pstride = pre ? (uint32_t)(ROWS * 16) : 16u;
       rx = make_rsrc(pc.d.x, live ? (uint32_t)(M * K * 2) : 0u);
       const uint32_t r0 = (uint32_t)pc.row0;
 #pragma unroll
       for (int i = 0; i < RB; ++i)
-        wbase[i] = (r0 + 16 * RB * wave + 16 * i + wrow) * (uint32_t)(K / 4) +
-                   16u * ((lane & 3) ^ w_swz(16 * i + wrow));
+        wbase[i] = DEC ? r0 * (uint32_t)(K / 4) + wave * W_WAVE + i * 1024 + lane * 16
+                        : (r0 + 16 * RB * wave + 16 * i + wrow) * (uint32_t)(K / 4) +
+                              16u * ((lane & 3) ^ w_swz(16 * i + wrow));
 #pragma unroll
       for (int j = 0; j < NPX; ++j) {
         const int g = WAVES * j + wave;
@@ -223,8 +246,9 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(const plz_gemv_desc* _
     }
     // K is a multiple of 256 = KC, so every stage is whole
     const uint32_t k0 = (uint32_t)pc.kc * KC;
+    const uint32_t wk = DEC ? (uint32_t)pc.kc * (uint32_t)W_BYTES : k0 / 4;
 #pragma unroll
-    for (int i = 0; i < RB; ++i) dma16(rq, wbase[i] + k0 / 4, st + wave * W_WAVE + i * 1024);
+    for (int i = 0; i < RB; ++i) dma16(rq, wbase[i] + wk, st + wave * W_WAVE + i * 1024);
 #pragma unroll
     for (int j = 0; j < NPX; ++j) {
       const int g = WAVES * j + wave;
@@ -258,18 +282,23 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(const plz_gemv_desc* _
       const lds_u8* xs = st + W_BYTES + 2048 + mx * X_TOKEN;
       // x fragments of this lane: k = 64q + 16t + 8h .. +7 (t = 0..3, h = 0..1), permuted
       // into the dequantiser's slot order {k0, k4, k1, k5, k2, k6, k3, k7}
+      // (natural order with the decode layout)
       u32x4 xf[8];
 #pragma unroll
       for (int f = 0; f < 8; ++f) {
         const u32x4 v = *(const lds_u32x4*)(xs + (((8 * q + f) ^ x_swz(mx)) << 4));
-        xf[f] = u32x4{perm(v[2], v[0], 0x05040100u), perm(v[2], v[0], 0x07060302u),
-                      perm(v[3], v[1], 0x05040100u), perm(v[3], v[1], 0x07060302u)};
+        if (DEC)
+          xf[f] = v;
+        else
+          xf[f] = u32x4{perm(v[2], v[0], 0x05040100u), perm(v[2], v[0], 0x07060302u),
+                        perm(v[3], v[1], 0x05040100u), perm(v[3], v[1], 0x07060302u)};
       }
 #pragma unroll
       for (int r = 0; r < RB; ++r) {
         const int row = 16 * r + nl;
         const u32x4 wv =
-            *(const lds_u32x4*)(st + wave * W_WAVE + row * 64 + ((q ^ w_swz(row)) << 4));
+            DEC ? *(const lds_u32x4*)(st + wave * W_WAVE + r * 1024 + lane * 16)
+                : *(const lds_u32x4*)(st + wave * W_WAVE + row * 64 + ((q ^ w_swz(row)) << 4));
         const u32x4 pv = *(const lds_u32x4*)(st + W_BYTES + (16 * RB * wave + row) * 16);
         const PalLut t = make_lut(__uint_as_float(pv[0]), __uint_as_float(pv[1]),
                                   __uint_as_float(pv[2]), __uint_as_float(pv[3]));
@@ -316,10 +345,10 @@ static int cu_count() {
   return cache[dev];
 }
 
-template <int NPX, bool GROUPED>
+template <int NPX, bool GROUPED, bool DEC>
 static int launch_nx(int64_t items, hipStream_t st, const plz_gemv_desc* descs, int n,
                      plz_gemv_desc single, int M, const char* what) {
-  auto kern = gemv_kernel<NPX, GROUPED>;
+  auto kern = gemv_kernel<NPX, GROUPED, DEC>;
   static bool attr = false;
   if (!attr) {
     const hipError_t e = hipFuncSetAttribute((const void*)kern,
@@ -338,16 +367,22 @@ static int launch_nx(int64_t items, hipStream_t st, const plz_gemv_desc* descs, 
                      single, M);
   return check_launch(what);
 }
+template <bool GROUPED, bool DEC>
+static int launch_dec(int64_t items, hipStream_t st, const plz_gemv_desc* descs, int n,
+                      plz_gemv_desc single, int M, const char* what) {
+  switch (npx_for(M)) {
+    case 1: return launch_nx<1, GROUPED, DEC>(items, st, descs, n, single, M, what);
+    case 2: return launch_nx<2, GROUPED, DEC>(items, st, descs, n, single, M, what);
+    case 3: return launch_nx<3, GROUPED, DEC>(items, st, descs, n, single, M, what);
+    case 4: return launch_nx<4, GROUPED, DEC>(items, st, descs, n, single, M, what);
+    default: return launch_nx<5, GROUPED, DEC>(items, st, descs, n, single, M, what);
+  }
+}
 template <bool GROUPED>
 static int launch(int64_t items, hipStream_t st, const plz_gemv_desc* descs, int n,
-                  plz_gemv_desc single, int M, const char* what) {
-  switch (npx_for(M)) {
-    case 1: return launch_nx<1, GROUPED>(items, st, descs, n, single, M, what);
-    case 2: return launch_nx<2, GROUPED>(items, st, descs, n, single, M, what);
-    case 3: return launch_nx<3, GROUPED>(items, st, descs, n, single, M, what);
-    case 4: return launch_nx<4, GROUPED>(items, st, descs, n, single, M, what);
-    default: return launch_nx<5, GROUPED>(items, st, descs, n, single, M, what);
-  }
+                  plz_gemv_desc single, int M, bool dec, const char* what) {
+  return dec ? launch_dec<GROUPED, true>(items, st, descs, n, single, M, what)
+             : launch_dec<GROUPED, false>(items, st, descs, n, single, M, what);
 }
 
 // palette [N, G, 4] -> [ceil(N/ROWS)][G][ROWS][4] (rows past N zero): one float4 per thread
@@ -361,18 +396,43 @@ __global__ void pack_palettes_kernel(const float4* __restrict__ pal, float4* __r
   out[t] = n < N ? pal[n * G + g] : make_float4(0.f, 0.f, 0.f, 0.f);
 }
 
+// packed [N, K/16] -> decode layout [ceil(N/ROWS)][K/256][WAVES][RB][64 lanes][4 words]: lane
+// l = 16q + nl of block i of wave w holds words 4q..4q+3 (k 64q .. 64q+63 of the stage) of row
+// 16 RB w + 16 i + nl, each through decode_word; rows past N are zero. One 16-byte chunk per
+// thread.
+__global__ void pack_indices_kernel(const uint4* __restrict__ packed, uint4* __restrict__ out,
+                                    int64_t N, int64_t K) {
+  constexpr int CH = W_BYTES / 16;  // chunks per stage
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t stages = K / KC, items = (N + ROWS - 1) / ROWS;
+  if (t >= items * stages * CH) return;
+  const int c = (int)(t % CH);
+  const int64_t st = (t / CH) % stages, item = t / (CH * stages);
+  const int w = c / (W_WAVE / 16), i = (c / 64) % RB, l = c & 63;
+  const int64_t n = item * ROWS + 16 * RB * w + 16 * i + (l & 15);
+  uint4 v = make_uint4(0u, 0u, 0u, 0u);
+  if (n < N) {
+    const uint4 src = packed[n * (K / 64) + st * 4 + (l >> 4)];
+    v = make_uint4(decode_word(src.x), decode_word(src.y), decode_word(src.z), decode_word(src.w));
+  }
+  out[t] = v;
+}
+
 static int check_desc(const plz_gemv_desc& d, int i) {
   PLZ_REQUIRE(d.N >= 0 && d.K >= 0, "plz_gemv: descriptor %d has a negative shape", i);
   PLZ_REQUIRE(d.K % 256 == 0, "plz_gemv: descriptor %d: K (%lld) must be a multiple of 256", i,
               (long long)d.K);
-  PLZ_REQUIRE(d.N == 0 || d.K == 0 || (d.x && d.packed && d.palette && d.y),
+  PLZ_REQUIRE(d.N == 0 || d.K == 0 ||
+                  (d.x && (d.packed || d.packed_items) && (d.palette || d.palette_items) && d.y),
               "plz_gemv: descriptor %d has a null pointer", i);
   PLZ_REQUIRE(d.N * d.K / 4 < (int64_t)kBufOob && d.N * (d.K / 256) * 16 < (int64_t)kBufOob &&
                   16 * d.K * 2 < (int64_t)kBufOob,
               "plz_gemv: descriptor %d is too large (packed or palette above 2 GiB)", i);
   PLZ_REQUIRE((((uintptr_t)d.x | (uintptr_t)d.packed | (uintptr_t)d.palette |
-                 (uintptr_t)d.palette_items) & 15) == 0,
+                 (uintptr_t)d.palette_items | (uintptr_t)d.packed_items) & 15) == 0,
               "plz_gemv: descriptor %d: x, packed and palettes must be 16-byte aligned", i);
+  PLZ_REQUIRE((d.N + ROWS - 1) / ROWS * ROWS * (d.K / 4) < (int64_t)kBufOob,
+              "plz_gemv: descriptor %d: decode-layout indices above 2 GiB", i);
   PLZ_REQUIRE((d.N + ROWS - 1) / ROWS * ROWS * (d.K / 256) * 16 < (int64_t)kBufOob,
               "plz_gemv: descriptor %d: prepacked palettes above 2 GiB", i);
   return PLZ_OK;
@@ -389,7 +449,8 @@ extern "C" {
 int plz_lut_gemv(const uint16_t* x, const int32_t* packed, const float* palette, uint16_t* y,
                  int64_t M, int64_t N, int64_t K, void* stream) {
   PLZ_REQUIRE(M >= 1 && M <= 16, "plz_lut_gemv: M (%lld) must be in [1, 16]", (long long)M);
-  plz_gemv_desc d = {x, packed, palette, y, N, K, 0, 0, nullptr};
+  plz_gemv_desc d = {x, packed, palette, y, N, K, 0, 0, nullptr, nullptr};
+  PLZ_REQUIRE(N == 0 || K == 0 || (packed && palette), "plz_lut_gemv: null pointer");
   int rc = check_desc(d, 0);
   if (rc) return rc;
   if (N == 0) return PLZ_OK;
@@ -398,7 +459,45 @@ int plz_lut_gemv(const uint16_t* x, const int32_t* packed, const float* palette,
     return check_launch("plz_lut_gemv");
   }
   const int64_t items = (N + ROWS - 1) / ROWS;
-  return launch<false>(items, (hipStream_t)stream, nullptr, 1, d, (int)M, "plz_lut_gemv");
+  return launch<false>(items, (hipStream_t)stream, nullptr, 1, d, (int)M, false, "plz_lut_gemv");
+}
+
+int plz_lut_gemv_decode(const uint16_t* x, const int32_t* packed_items,
+                        const float* palette_items, uint16_t* y, int64_t M, int64_t N, int64_t K,
+                        void* stream) {
+  PLZ_REQUIRE(M >= 1 && M <= 16, "plz_lut_gemv_decode: M (%lld) must be in [1, 16]", (long long)M);
+  PLZ_REQUIRE(N == 0 || K == 0 || (packed_items && palette_items),
+              "plz_lut_gemv_decode: null pointer");
+  plz_gemv_desc d = {x, nullptr, nullptr, y, N, K, 0, 0, palette_items, packed_items};
+  int rc = check_desc(d, 0);
+  if (rc) return rc;
+  if (N == 0) return PLZ_OK;
+  if (K == 0) {
+    zero_async(y, (size_t)M * N * 2, (hipStream_t)stream);
+    return check_launch("plz_lut_gemv_decode");
+  }
+  const int64_t items = (N + ROWS - 1) / ROWS;
+  return launch<false>(items, (hipStream_t)stream, nullptr, 1, d, (int)M, true,
+                       "plz_lut_gemv_decode");
+}
+
+size_t plz_gemv_packed_items_bytes(int64_t N, int64_t K) {
+  if (N <= 0 || K <= 0) return 0;
+  return (size_t)((N + ROWS - 1) / ROWS) * ROWS * (size_t)(K / 4);
+}
+
+int plz_gemv_pack_indices(const int32_t* packed, int32_t* packed_items, int64_t N, int64_t K,
+                          void* stream) {
+  PLZ_REQUIRE(N >= 0 && K >= 0 && K % KC == 0,
+              "plz_gemv_pack_indices: need N, K >= 0 and K a multiple of 256");
+  if (N == 0 || K == 0) return PLZ_OK;
+  PLZ_REQUIRE(packed && packed_items && (((uintptr_t)packed | (uintptr_t)packed_items) & 15) == 0,
+              "plz_gemv_pack_indices: packed and packed_items must be non-null, 16-byte aligned");
+  const int64_t total = (N + ROWS - 1) / ROWS * (K / KC) * (W_BYTES / 16);
+  hipLaunchKernelGGL(pack_indices_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, reinterpret_cast<const uint4*>(packed),
+                     reinterpret_cast<uint4*>(packed_items), N, K);
+  return check_launch("plz_gemv_pack_indices");
 }
 
 size_t plz_gemv_palette_items_bytes(int64_t N, int64_t K) {
@@ -443,14 +542,16 @@ int64_t plz_gemv_plan(plz_gemv_desc* descs, int n, int M) {
 }
 
 int plz_lut_gemv_grouped(const plz_gemv_desc* descs_device, int n, int64_t total_blocks, int M,
-                         void* stream) {
+                         int layout, void* stream) {
   PLZ_REQUIRE(M >= 1 && M <= 16, "plz_lut_gemv_grouped: M (%d) must be in [1, 16]", M);
+  PLZ_REQUIRE(layout == PLZ_GEMV_NATIVE || layout == PLZ_GEMV_DECODE,
+              "plz_lut_gemv_grouped: unknown index layout %d", layout);
   PLZ_REQUIRE(n >= 0 && total_blocks >= 0, "plz_lut_gemv_grouped: negative count");
   if (n == 0 || total_blocks == 0) return PLZ_OK;
   PLZ_REQUIRE(descs_device, "plz_lut_gemv_grouped: null descriptor table");
   plz_gemv_desc dummy = {};
   return launch<true>(total_blocks, (hipStream_t)stream, descs_device, n, dummy, M,
-                      "plz_lut_gemv_grouped");
+                      layout == PLZ_GEMV_DECODE, "plz_lut_gemv_grouped");
 }
 
 }  // extern "C"

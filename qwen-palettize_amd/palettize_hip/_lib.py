@@ -15,6 +15,7 @@ LIB_PATH = os.path.join(HERE, "libpalettize_hip.so")
 PLZ_OK, PLZ_EINVAL, PLZ_EHIP, PLZ_EUNSUPPORTED, PLZ_EWORKSPACE = 0, 1, 2, 3, 4
 PLZ_DT_BF16, PLZ_DT_FP16, PLZ_DT_FP32 = 0, 1, 2
 PLZ_W_SOFT, PLZ_W_HARD_NOISY, PLZ_W_HARD_PLAIN = 0, 1, 2
+PLZ_GEMV_NATIVE, PLZ_GEMV_DECODE = 0, 1
 
 p = C.c_void_p
 i32, i64, u32, u64, f32, sz = C.c_int, C.c_int64, C.c_uint32, C.c_uint64, C.c_float, C.c_size_t
@@ -34,7 +35,8 @@ class AdamWDesc(C.Structure):
 
 class GemvDesc(C.Structure):
     _fields_ = [("x", p), ("packed", p), ("palette", p), ("y", p), ("N", i64), ("K", i64),
-                ("block_begin", i64), ("cost_begin", i64), ("palette_items", p)]
+                ("block_begin", i64), ("cost_begin", i64), ("palette_items", p),
+                ("packed_items", p)]
 
 
 # name -> (restype, argtypes); kept in the order of include/palettize_hip.h
@@ -79,8 +81,11 @@ SIGNATURES: dict[str, tuple] = {
     "plz_lut_gemv": (i32, [p, p, p, p, i64, i64, i64, p]),
     "plz_gemv_palette_items_bytes": (sz, [i64, i64]),
     "plz_gemv_pack_palettes": (i32, [p, p, i64, i64, p]),
+    "plz_gemv_packed_items_bytes": (sz, [i64, i64]),
+    "plz_gemv_pack_indices": (i32, [p, p, i64, i64, p]),
+    "plz_lut_gemv_decode": (i32, [p, p, p, p, i64, i64, i64, p]),
     "plz_gemv_plan": (i64, [C.POINTER(GemvDesc), i32, i32]),
-    "plz_lut_gemv_grouped": (i32, [p, i32, i64, i32, p]),
+    "plz_lut_gemv_grouped": (i32, [p, i32, i64, i32, i32, p]),
     "plz_idx2_to_packed": (i32, [p, p, i64, i64, p]),
     "plz_packed_to_idx2": (i32, [p, p, i64, i64, p]),
     "plz_logits_argmax_idx2": (i32, [p, i32, p, i64, i64, p]),

@@ -387,13 +387,39 @@ def gemv_pack_palettes(palette):
     return out
 
 
+def gemv_pack_indices(packed):
+    """One-time decode layout of packed indices [N, K/16] (plz_gemv_pack_indices): one
+    contiguous 8 KB block per 128-row item and 256-k stage, fields permuted for natural-order
+    dequantisation. Returned as a flat int32 tensor."""
+    _need(packed, "packed", torch.int32, 2)
+    N, K = packed.shape[0], packed.shape[1] * 16
+    nbytes = query("plz_gemv_packed_items_bytes", N, K)
+    out = torch.empty(max(nbytes // 4, 4), dtype=torch.int32, device=packed.device)
+    call("plz_gemv_pack_indices", _ptr(packed), _ptr(out), N, K, _stream(packed))
+    return out
+
+
+def lut_gemv_decode(x, packed_items, palette_items, N):
+    """lut_gemv on weights in the decode layouts (gemv_pack_indices, gemv_pack_palettes)."""
+    _need(x, "x", torch.bfloat16, 2)
+    M, K = x.shape
+    if packed_items.numel() * 4 < query("plz_gemv_packed_items_bytes", N, K) or \
+            palette_items.numel() * 4 < query("plz_gemv_palette_items_bytes", N, K):
+        raise ValueError("decode-layout weights smaller than N x K needs")
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
+    call("plz_lut_gemv_decode", _ptr(x), _ptr(packed_items), _ptr(palette_items), _ptr(y), M, N,
+         K, _stream(x))
+    return y
+
+
 class GemvGroup:
     """A fixed set of independent GEMVs (same M) run by one grouped launch.
 
     ``items`` is a list of (x [M,K] bf16, packed, palette); outputs are allocated once and
     reused by every ``run()``. The descriptor table lives in device memory. With
-    ``prepack=True`` (default) the palettes are repacked once into the decode layout
-    (plz_gemv_pack_palettes), which the kernel streams contiguously.
+    ``prepack=True`` (default) the indices and palettes are repacked once into the decode
+    layouts (plz_gemv_pack_indices, plz_gemv_pack_palettes), which the kernel streams
+    contiguously.
     """
 
     def __init__(self, items, prepack=True):
@@ -403,6 +429,7 @@ class GemvGroup:
         self.device = items[0][0].device
         self.outputs = []
         self._packed_palettes = []
+        self._packed_indices = []
         descs = (_lib.GemvDesc * len(items))()
         for i, (x, packed, palette) in enumerate(items):
             N, K = _wshape(packed, palette)
@@ -412,10 +439,13 @@ class GemvGroup:
             y = torch.empty((self.M, N), dtype=torch.bfloat16, device=self.device)
             self.outputs.append(y)
             pre = gemv_pack_palettes(palette) if prepack and N > 0 and K > 0 else None
+            pri = gemv_pack_indices(packed) if prepack and N > 0 and K > 0 else None
             self._packed_palettes.append(pre)
+            self._packed_indices.append(pri)
             descs[i] = _lib.GemvDesc(x.data_ptr(), packed.data_ptr(), palette.data_ptr(),
                                      y.data_ptr(), N, K, 0, 0,
-                                     pre.data_ptr() if pre is not None else None)
+                                     pre.data_ptr() if pre is not None else None,
+                                     pri.data_ptr() if pri is not None else None)
         self._keep = items
         total = _lib.lib().plz_gemv_plan(descs, len(items), self.M)
         if total < 0:
@@ -426,10 +456,11 @@ class GemvGroup:
         host = torch.frombuffer(bytearray(raw), dtype=torch.uint8)
         self.table = host.to(self.device)
         self.n = len(items)
+        self.layout = _lib.PLZ_GEMV_DECODE if prepack else _lib.PLZ_GEMV_NATIVE
 
     def run(self):
         call("plz_lut_gemv_grouped", self.table.data_ptr(), self.n, self.total_blocks, self.M,
-             torch.cuda.current_stream(self.device).cuda_stream)
+             self.layout, torch.cuda.current_stream(self.device).cuda_stream)
         return self.outputs
 
 

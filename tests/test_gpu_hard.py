@@ -178,10 +178,18 @@ def test_gemv_ragged(dev, M, N, K):
     assert_close(f32(y), want, what=f"gemv M={M} N={N} K={K}")
 
 
+def _single_gemv(x, p, pl, decode):
+    if decode:
+        return ops.lut_gemv_decode(x, ops.gemv_pack_indices(p), ops.gemv_pack_palettes(pl),
+                                   p.shape[0])
+    return ops.lut_gemv(x, p, pl)
+
+
+@pytest.mark.parametrize("decode", [False, True], ids=["native", "decode-layout"])
 @pytest.mark.parametrize("M", [1, 16])
-def test_gemv_grouped_many_linears(dev, M):
+def test_gemv_grouped_many_linears(dev, M, decode):
     """A grouped launch over 3 x 7 Qwen-4B shapes plus empty linears: every output equals the
-    single-linear launch bit for bit, and sampled ones match the oracle."""
+    single-linear launch on the same layout bit for bit, and sampled ones match the oracle."""
     shapes = [(4096, 2560), (1024, 2560), (1024, 2560), (2560, 4096), (9728, 2560),
               (9728, 2560), (2560, 9728)]
     items, idxs = [], []
@@ -194,13 +202,13 @@ def test_gemv_grouped_many_linears(dev, M):
         items.append((randn_bf16(M, 256, seed=7).to(dev), torch.zeros(0, 16, dtype=torch.int32, device=dev),
                       torch.zeros(0, 1, 4, device=dev)))
         idxs.append(None)
-    grp = ops.GemvGroup(items)
+    grp = ops.GemvGroup(items, prepack=decode)
     outs = grp.run()
     for j, ((x, p, pl), y) in enumerate(zip(items, outs)):
         if idxs[j] is None:
             assert y.shape[1] == 0
             continue
-        assert torch.equal(y, ops.lut_gemv(x, p, pl)), f"linear {j}"
+        assert torch.equal(y, _single_gemv(x, p, pl, decode)), f"linear {j}"
         if j % 5 == 0:
             idx, pal, xc = idxs[j]
             want = O.lut_linear_fwd(f32(xc), O.dequant(idx.numpy(), pal.numpy()))
@@ -219,7 +227,8 @@ def test_gemv_pack_palettes_layout(dev):
     assert torch.equal(out, want)
 
 
-def test_gemv_grouped_matches_single(dev):
+@pytest.mark.parametrize("decode", [False, True], ids=["native", "decode-layout"])
+def test_gemv_grouped_matches_single(dev, decode):
     shapes = [(4096, 2560), (1024, 2560), (2560, 4096), (264, 512), (9728, 2560)]
     M = 4
     items, wants = [], []
@@ -228,11 +237,33 @@ def test_gemv_grouped_matches_single(dev):
         x = randn_bf16(M, K, seed=200 + i)
         items.append((x.to(dev), _packed(idx, dev), pal.to(dev)))
         wants.append(O.lut_linear_fwd(f32(x), O.dequant(idx.numpy(), pal.numpy())))
-    grp = ops.GemvGroup(items)
+    grp = ops.GemvGroup(items, prepack=decode)
     outs = grp.run()
     for (x, p, pl), y, want in zip(items, outs, wants):
         assert_close(f32(y), want, what="grouped gemv")
-        assert torch.equal(y, ops.lut_gemv(x, p, pl))
+        assert torch.equal(y, _single_gemv(x, p, pl, decode))
+
+
+def test_gemv_pack_indices_layout(dev):
+    """plz_gemv_pack_indices equals the oracle's decode layout word for word (ragged N: padded
+    rows are zero)."""
+    N, K = 300, 768
+    idx, _ = make_weight(N, K, seed=4)
+    got = ops.gemv_pack_indices(_packed(idx, dev)).cpu().numpy().view(np.uint32)
+    want = O.gemv_decode_layout(idx.numpy())
+    assert got.size >= want.size and np.array_equal(got[:want.size], want)
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 4096, 2560), (4, 1024, 2560), (16, 2560, 9728),
+                                   (5, 264, 256), (13, 8, 768), (1, 136, 1280)])
+def test_gemv_decode_layout(dev, M, N, K):
+    """The GEMV on the decode layouts (indices and palettes) against the oracle, including
+    token counts of every x-slice size and N not a multiple of the 128-row item."""
+    idx, pal = make_weight(N, K, seed=M * 3 + N + K)
+    x = randn_bf16(M, K, seed=M + 2)
+    y = _single_gemv(x.to(dev), _packed(idx, dev), pal.to(dev), True)
+    want = O.lut_linear_fwd(f32(x), O.dequant(idx.numpy(), pal.numpy()))
+    assert_close(f32(y), want, what=f"decode gemv M={M} N={N} K={K}")
 
 
 @pytest.mark.parametrize("M", [2048, 8192])

@@ -376,3 +376,26 @@ def test_adamw_step_matches_torch_clip_adamw_clamp():
         assert np.isclose(norms[0], float(n0)) and np.isclose(norms[1], float(n1))
         for m, t in zip(masters, tparams):
             assert np.allclose(m, t.detach().numpy(), rtol=1e-10, atol=1e-12)
+
+
+def test_gemv_decode_layout_through_the_dequantiser_slot_order():
+    """Decode-layout words read through the GEMV dequantiser's field -> slot pairing (v_perm
+    selectors 0x05010400 / 0x07030602 on the bytes of (w >> 2j) & 0x03030303: slot 2j <- field
+    2j, 2j+1 <- field 8+2j, 8+2j <- field 16+2j, 9+2j <- field 24+2j) give back every row's
+    indices in natural k order; padded rows past N are zero. A wrong field map, row or lane
+    order fails here."""
+    rng = np.random.default_rng(5)
+    N, K = 200, 512
+    idx = rng.integers(0, 4, (N, K))
+    items, stages = (N + 127) // 128, K // 256
+    words = O.gemv_decode_layout(idx)
+    assert words.size == items * 128 * K // 16
+    words = words.reshape(items, stages, 4, 2, 4, 16, 4)  # item, stage, w, b, q, r, t
+    slot_field = [0] * 16
+    for j in range(4):
+        slot_field[2 * j], slot_field[2 * j + 1] = 2 * j, 8 + 2 * j
+        slot_field[8 + 2 * j], slot_field[9 + 2 * j] = 16 + 2 * j, 24 + 2 * j
+    dec = np.stack([(words >> np.uint32(f)) & 3 for f in slot_field], -1)
+    back = dec.transpose(0, 2, 3, 5, 1, 4, 6, 7).reshape(items * 128, K)
+    assert np.array_equal(back[:N], idx)
+    assert not back[N:].any()
