@@ -269,13 +269,47 @@ def _log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def bench_attn(device, reps=10):
+    """Causal grouped-query attention of the layer (B 32, S 512, 32 query / 8 kv heads x 128):
+    forward (o, lse) and backward (dq, dk, dv), HIP-event time per call and FLOP rate
+    (forward 4*B*Hq*S^2*D/2, backward 2.5x that)."""
+    import torch
+    from palettize_hip import ops
+    B, S, Hq, Hkv, D = 32, 512, 32, 8, 128
+    g = torch.Generator(device=device).manual_seed(4)
+    q = torch.randn(B, S, Hq, D, generator=g, device=device).to(torch.bfloat16)
+    k = torch.randn(B, S, Hkv, D, generator=g, device=device).to(torch.bfloat16)
+    v = torch.randn(B, S, Hkv, D, generator=g, device=device).to(torch.bfloat16)
+    go = torch.randn(B, S, Hq, D, generator=g, device=device).to(torch.bfloat16)
+    flop = 4.0 * B * Hq * S * S * D / 2
+    o, lse = ops.attn_fwd(q, k, v)
+
+    def timed(fn):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(reps):
+            fn()
+        e.record()
+        torch.cuda.synchronize()
+        return s.elapsed_time(e) / reps * 1e3
+
+    fwd_us = timed(lambda: ops.attn_fwd(q, k, v))
+    bwd_us = timed(lambda: ops.attn_bwd(q, k, v, o, lse, go))
+    return {"fwd_us": round(fwd_us, 1), "fwd_tflops": round(flop / fwd_us / 1e6, 1),
+            "bwd_us": round(bwd_us, 1), "bwd_tflops": round(2.5 * flop / bwd_us / 1e6, 1),
+            "config": "batch 32 x 512, 32/8 heads x 128, causal"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["hard", "gemv", "soft", "layer"], default=None)
+    ap.add_argument("--only", choices=["hard", "gemv", "soft", "layer", "attn"], default=None)
     ap.add_argument("--calibration-copy", action="store_true",
                     help="first run a plain 1 GiB device copy (fp32 -> fp32), the reference "
                          "kernel that scales rocprofv3's FETCH_SIZE / WRITE_SIZE to bytes")
@@ -346,6 +380,10 @@ def main():
     if args.only in (None, "soft"):
         out["soft"] = bench_soft(dev)
         _log(f"soft: {out['soft']}")
+        torch.cuda.empty_cache()
+    if args.only in (None, "attn"):
+        out["attn"] = bench_attn(dev)
+        _log(f"attn: {out['attn']}")
         torch.cuda.empty_cache()
     if args.only in (None, "layer"):
         out["layer"] = bench_layer(dev)
