@@ -14,8 +14,10 @@
 // registers are directly the B operand P^T of O^T += V^T P^T: lane l holds query l%32 and the
 // kv indices {4h+0..3, 8+4h+0..3} (h = l/32) of each 16-wide k-step, and the V^T fragments are
 // read from LDS (ds_read_b64_tr_b16) in that same kv order. The running max and sum of each
-// query live in the two lanes that hold it (l and l^32). O^T is transposed through LDS so that
-// the bf16 output is written with 16-byte stores.
+// query live in the two lanes that hold it (l and l^32); the max is moved (and O, l rescaled)
+// only when a block exceeds it by more than 8 in log2 units, and the causal mask is applied
+// only on blocks that cross the diagonal. O^T is transposed through LDS so that the bf16
+// output is written with 16-byte stores.
 #include <initializer_list>
 
 #include "plz_common.h"
@@ -68,7 +70,7 @@ __device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
-__global__ __launch_bounds__(NT) void attn_fwd_kernel(const uint16_t* __restrict__ q,
+__global__ __launch_bounds__(NT, 2) void attn_fwd_kernel(const uint16_t* __restrict__ q,
                                                       const uint16_t* __restrict__ k,
                                                       const uint16_t* __restrict__ v,
                                                       uint16_t* __restrict__ o,
@@ -77,7 +79,11 @@ __global__ __launch_bounds__(NT) void attn_fwd_kernel(const uint16_t* __restrict
   extern __shared__ uint4 smem[];
   lds_u8* lds = (lds_u8*)smem;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h2 = lane >> 5, ql = lane & 31;
-  const int qb = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  // 1-D grid in longest-first order: the last query blocks see the most kv blocks
+  int id = blockIdx.x;
+  const int qb = S / BM - 1 - id / (Hq * B);
+  id %= Hq * B;
+  const int h = id % Hq, b = id / Hq;
   const int hk = h / (Hq / Hkv);
   const int q0 = qb * BM;
   const int qrow = q0 + 32 * wave + ql;  // this lane's query
@@ -143,20 +149,37 @@ __global__ __launch_bounds__(NT) void attn_fwd_kernel(const uint16_t* __restrict
         st[nb] = mfma32(kf, qf[ks], st[nb]);
       }
     }
-    // scale, causal mask, online softmax (log2 domain)
+    // causal mask (only blocks that cross this wave's diagonal), online softmax in the log2
+    // domain on the raw scores: p = exp2(s * scale_log2 - m)
+    if (kv0 + BN - 1 > q0 + 32 * wave) {
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int kv = kv0 + 32 * nb + 8 * (e >> 2) + 4 * h2 + (e & 3);
+          if (kv > qrow) st[nb][e] = -INFINITY;
+        }
+    }
     float mx = -INFINITY;
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int kv = kv0 + 32 * nb + 8 * (e >> 2) + 4 * h2 + (e & 3);
-        const float s = kv <= qrow ? st[nb][e] * scale_log2 : -INFINITY;
-        st[nb][e] = s;
-        mx = fmaxf(mx, s);
-      }
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float mnew = fmaxf(mrun, mx);  // finite: block 0 always holds kv 0 <= qrow
-    const float alpha = exp2f(mrun - mnew);
+      for (int e = 0; e < 16; ++e) mx = fmaxf(mx, st[nb][e]);
+    mx = fmaxf(mx, __shfl_xor(mx, 32)) * scale_log2;
+    // Lazy rescaling: the reference max m only moves when the block max exceeds it by more
+    // than 8 (so every p stays <= 2^8, exact in fp32 and in range for bf16); the first block
+    // always sets it (kv 0 <= qrow). O and l are rescaled only when some lane moved.
+    if (__builtin_amdgcn_ballot_w64(mx > mrun + 8.f) != 0) {
+      const float mnew = mx > mrun + 8.f ? mx : mrun;
+      const float alpha = exp2f(mrun - mnew);
+      mrun = mnew;
+      lrun *= alpha;
+#pragma unroll
+      for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) ot[db][e] *= alpha;
+    }
+    const float nm = -mrun;
     float sum = 0.f;
     bf16x8 pf[4];  // P^T fragments for the 4 k-steps of 16 kv
 #pragma unroll
@@ -164,7 +187,7 @@ __global__ __launch_bounds__(NT) void attn_fwd_kernel(const uint16_t* __restrict
       float p[16];
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        p[e] = exp2f(st[nb][e] - mnew);
+        p[e] = exp2f(fmaf(st[nb][e], scale_log2, nm));
         sum += p[e];
       }
 #pragma unroll
@@ -177,12 +200,7 @@ __global__ __launch_bounds__(NT) void attn_fwd_kernel(const uint16_t* __restrict
       }
     }
     sum += __shfl_xor(sum, 32);
-    lrun = lrun * alpha + sum;
-    mrun = mnew;
-#pragma unroll
-    for (int db = 0; db < D / 32; ++db)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) ot[db][e] *= alpha;
+    lrun += sum;
     // O^T += V^T P^T
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
@@ -286,7 +304,7 @@ __device__ __forceinline__ void store_rows_t(const f32x16 (&acc)[D / 32], float 
 constexpr float kLog2e = 1.4426950408889634f;
 
 // grid: S/128 x Hq x B, in longest-first order (the last query blocks see the most kv blocks)
-__global__ __launch_bounds__(NT) void attn_bwd_dq_kernel(
+__global__ __launch_bounds__(NT, 2) void attn_bwd_dq_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const uint16_t* __restrict__ o, const uint16_t* __restrict__ dout,
     const float* __restrict__ lse, uint16_t* __restrict__ dq, float* __restrict__ dsum_out, int B,
@@ -360,6 +378,7 @@ __global__ __launch_bounds__(NT) void attn_bwd_dq_kernel(
         st[nb] = mfma32(row_frag(ks_, 32 * nb + ql, ks, h2), qf[ks], st[nb]);
         dpt[nb] = mfma32(row_frag(vs_, 32 * nb + ql, ks, h2), df[ks], dpt[nb]);
       }
+    const bool diag = kv0 + BN - 1 > q0 + 32 * wave;  // the block crosses this wave's diagonal
     bf16x8 dsf[4];
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) {
@@ -367,7 +386,8 @@ __global__ __launch_bounds__(NT) void attn_bwd_dq_kernel(
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int kv = kv0 + 32 * nb + 8 * (e >> 2) + 4 * h2 + (e & 3);
-        const float p = kv <= qrow ? exp2f(fmaf(st[nb][e], scale_log2, nl)) : 0.f;
+        float p = exp2f(fmaf(st[nb][e], scale_log2, nl));
+        if (diag && kv > qrow) p = 0.f;
         ds[e] = p * (dpt[nb][e] - dsum);
       }
       pack_frags(ds, dsf[2 * nb], dsf[2 * nb + 1]);
@@ -459,6 +479,7 @@ __global__ __launch_bounds__(NT) void attn_bwd_dkv_kernel(
         s[mb] = mfma32(row_frag(qs, 32 * mb + ql, ks, h2), kf[ks], s[mb]);
         dp[mb] = mfma32(row_frag(dos, 32 * mb + ql, ks, h2), vf[ks], dp[mb]);
       }
+    const bool diag = qb0 < kvw + 31;  // some query of the block precedes a kv row of the wave
     bf16x8 pf[4], dsf[4];
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb) {
@@ -473,7 +494,8 @@ __global__ __launch_bounds__(NT) void attn_bwd_dkv_kernel(
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int e = 4 * j + i;
-          const float pe = qb0 + r + i >= kvrow ? exp2f(fmaf(s[mb][e], scale_log2, -L[i] * kLog2e)) : 0.f;
+          float pe = exp2f(fmaf(s[mb][e], scale_log2, -L[i] * kLog2e));
+          if (diag && qb0 + r + i < kvrow) pe = 0.f;
           p[e] = pe;
           ds[e] = pe * (dp[mb][e] - Dv[i]);
         }
@@ -552,8 +574,7 @@ int plz_attn_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16
   const int lr = reserve_lds((const void*)attn_fwd_kernel, kLds, attr, "plz_attn_fwd");
   if (lr != PLZ_OK) return lr;
   const float scale_log2 = scale * kLog2e;
-  hipLaunchKernelGGL(attn_fwd_kernel, dim3((unsigned)(seq / BM), (unsigned)heads, (unsigned)batch),
-                     dim3(NT), kLds, (hipStream_t)stream, q, k, v, o, lse, batch, seq, heads,
+  hipLaunchKernelGGL(attn_fwd_kernel, dim3((unsigned)(seq / BM) * heads * batch), dim3(NT), kLds, (hipStream_t)stream, q, k, v, o, lse, batch, seq, heads,
                      kv_heads, scale_log2);
   return check_launch("plz_attn_fwd");
 }

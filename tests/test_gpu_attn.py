@@ -85,3 +85,23 @@ def test_attn_bwd_layer_shape_sampled_heads(dev):
     for got, ref, nm in zip((gq[:, :, hs], gk[:, :, 5:6], gv[:, :, 5:6]), want,
                             ("grad_q", "grad_k", "grad_v")):
         assert_close(f32(got), ref.numpy(), what=nm + " (layer shape)")
+
+
+@pytest.mark.parametrize("growth", [1.0, -1.0], ids=["rising-scores", "falling-scores"])
+def test_attn_running_max_jumps(dev, growth):
+    """Key norms that grow (or shrink) along the sequence make every later kv block move the
+    running max by far more than the lazy-rescale threshold (2^8) or never move it: both
+    branches of the online softmax, forward and backward, against fp32."""
+    B, S, Hq, Hkv = 1, 512, 4, 2
+    q, k, v = _inputs(B, S, Hq, Hkv, seed=11)
+    ramp = torch.exp(growth * torch.linspace(-1.5, 1.5, S)).view(1, S, 1, 1)
+    k = (k.float() * ramp).to(torch.bfloat16)
+    go = torch.randn(B, S, Hq, 128, generator=torch.Generator().manual_seed(12)).to(torch.bfloat16)
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    o, lse = ops.attn_fwd(qd, kd, vd)
+    want_o, want_lse = _ref(q, k, v)
+    assert_close(f32(o), want_o.numpy(), what="attention output")
+    assert np.allclose(f32(lse), want_lse.numpy(), rtol=1e-4, atol=1e-3)
+    grads = ops.attn_bwd(qd, kd, vd, o, lse, go.to(dev))
+    for got, ref, nm in zip(grads, _ref_grads(q, k, v, go), ("grad_q", "grad_k", "grad_v")):
+        assert_close(f32(got), ref.numpy(), what=nm)
