@@ -537,7 +537,9 @@ int reserve_lds(const void* fn, size_t bytes, bool& done, const char* what) {
   return PLZ_OK;
 }
 
-// shared argument checks of the forward and backward; 1 = nothing to do
+// shared argument checks of the forward and backward: PLZ_OK, an error status, or kEmpty
+// (valid, nothing to do)
+constexpr int kEmpty = -1;
 int check_shape(const char* what, int batch, int seq, int heads, int kv_heads, int head_dim,
                 float scale) {
   PLZ_REQUIRE(batch >= 0 && seq >= 0 && heads > 0 && kv_heads > 0 && heads % kv_heads == 0,
@@ -550,7 +552,7 @@ int check_shape(const char* what, int batch, int seq, int heads, int kv_heads, i
   PLZ_REQUIRE(scale > 0.f, "%s: scale must be positive", what);
   PLZ_REQUIRE((int64_t)seq * heads * D * 2 < ((int64_t)1 << 31),
               "%s: one sequence of q must span < 2 GiB", what);
-  return batch == 0 || seq == 0 ? 1 : PLZ_OK;
+  return batch == 0 || seq == 0 ? kEmpty : PLZ_OK;
 }
 
 bool aligned16(std::initializer_list<const void*> ps) {
@@ -567,7 +569,7 @@ int plz_attn_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16
                  int batch, int seq, int heads, int kv_heads, int head_dim, float scale,
                  void* stream) {
   const int rc = check_shape("plz_attn_fwd", batch, seq, heads, kv_heads, head_dim, scale);
-  if (rc != PLZ_OK) return rc == 1 ? PLZ_OK : rc;
+  if (rc != PLZ_OK) return rc == kEmpty ? PLZ_OK : rc;
   PLZ_REQUIRE(q && k && v && o && lse, "plz_attn_fwd: null pointer");
   PLZ_REQUIRE(aligned16({q, k, v, o}), "plz_attn_fwd: q, k, v, o must be 16-byte aligned");
   static bool attr = false;
@@ -589,7 +591,7 @@ int plz_attn_bwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, const 
                  uint16_t* grad_v, void* workspace, size_t workspace_bytes, int batch, int seq,
                  int heads, int kv_heads, int head_dim, float scale, void* stream) {
   const int rc = check_shape("plz_attn_bwd", batch, seq, heads, kv_heads, head_dim, scale);
-  if (rc != PLZ_OK) return rc == 1 ? PLZ_OK : rc;
+  if (rc != PLZ_OK) return rc == kEmpty ? PLZ_OK : rc;
   PLZ_REQUIRE(q && k && v && o && grad_o && lse && grad_q && grad_k && grad_v,
               "plz_attn_bwd: null pointer");
   PLZ_REQUIRE(aligned16({q, k, v, o, grad_o, lse, grad_q, grad_k, grad_v}),

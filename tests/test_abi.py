@@ -108,3 +108,44 @@ def test_dropin_layout_maps_match_oracle():
     assert nk4.shape == (8, 768, 4)
     assert torch.equal(nk4[:, :K, :], lg.permute(2, 1, 0))
     assert torch.count_nonzero(nk4[:, K:, :]) == 0
+
+
+def test_attention_argument_errors(lib):
+    """Shape, support and workspace checks of the attention entry points fail before any GPU
+    work (pointer 16 stands for an aligned device pointer and is never dereferenced)."""
+    f = C.c_void_p(16)
+    rc = lib.plz_attn_fwd(f, f, f, f, f, 1, 128, 4, 3, 128, 0.1, None)
+    assert rc == 1 and b"multiple of kv_heads" in lib.plz_last_error()
+    rc = lib.plz_attn_fwd(f, f, f, f, f, 1, 128, 4, 2, 64, 0.1, None)
+    assert rc == 3 and b"head_dim" in lib.plz_last_error()
+    rc = lib.plz_attn_fwd(f, f, f, f, f, 1, 100, 4, 2, 128, 0.1, None)
+    assert rc == 1 and b"multiple of 128" in lib.plz_last_error()
+    rc = lib.plz_attn_fwd(None, f, f, f, f, 1, 128, 4, 2, 128, 0.1, None)
+    assert rc == 1 and b"null" in lib.plz_last_error()
+    rc = lib.plz_attn_fwd(f, f, f, f, f, 1, 128, 4, 2, 128, -1.0, None)
+    assert rc == 1 and b"scale" in lib.plz_last_error()
+    assert lib.plz_attn_fwd(None, None, None, None, None, 0, 128, 4, 2, 128, 0.1, None) == 0
+    assert lib.plz_attn_bwd_workspace(2, 256, 8) == 2 * 8 * 256 * 4
+    assert lib.plz_attn_bwd_workspace(0, 256, 8) == 0
+    rc = lib.plz_attn_bwd(f, f, f, f, f, f, f, f, f, None, 0, 2, 256, 8, 2, 128, 0.1, None)
+    assert rc == 4 and b"workspace" in lib.plz_last_error()
+    rc = lib.plz_attn_bwd(f, f, f, f, f, f, f, f, f, f, 2 * 8 * 256 * 4 - 16, 2, 256, 8, 2, 128,
+                          0.1, None)
+    assert rc == 4
+    rc = lib.plz_attn_bwd(f, C.c_void_p(24), f, f, f, f, f, f, f, f, 1 << 20, 2, 256, 8, 2, 128,
+                          0.1, None)
+    assert rc == 1 and b"aligned" in lib.plz_last_error()
+
+
+def test_gemv_decode_layout_argument_errors(lib):
+    assert lib.plz_gemv_packed_items_bytes(300, 768) == 384 * 768 // 4
+    assert lib.plz_gemv_packed_items_bytes(0, 768) == 0
+    rc = lib.plz_gemv_pack_indices(None, None, 8, 100, None)
+    assert rc == 1 and b"multiple of 256" in lib.plz_last_error()
+    assert lib.plz_gemv_pack_indices(None, None, 0, 256, None) == 0
+    rc = lib.plz_lut_gemv_decode(None, None, None, None, 1, 8, 256, None)
+    assert rc == 1 and b"null" in lib.plz_last_error()
+    rc = lib.plz_lut_gemv_decode(None, None, None, None, 0, 8, 256, None)
+    assert rc == 1 and b"[1, 16]" in lib.plz_last_error()
+    rc = lib.plz_lut_gemv_grouped(None, 1, 1, 1, 7, None)
+    assert rc == 1 and b"layout" in lib.plz_last_error()
