@@ -99,13 +99,15 @@ __device__ __forceinline__ void interleave_kstep() {
   }
 }
 
-// A whole stage without overlap (the partial and LoRA stages).
+// A whole stage without overlap (the partial and LoRA stages). Only the first nks k-steps
+// hold data (the rest of the stage is zero fill), so only those run.
 template <bool A_COL, bool B_COL>
 __device__ __forceinline__ void mma_stage_sync(const lds_u8* a_s, const lds_u8* b_s,
                                                f32x16 (&acc)[WT_I][WT_J], int wi, int wj,
-                                               int lane) {
+                                               int lane, int nks) {
 #pragma unroll
   for (int ks = 0; ks < BK / 16; ++ks) {
+    if (ks >= nks) break;
     bf16x8 a[WT_I], b[WT_J];
     load_frags<A_COL, B_COL>(a_s, b_s, ks, wi, wj, lane, a, b);
     mma_kstep(acc, a, b);
@@ -540,7 +542,9 @@ __global__ __launch_bounds__(NTHR) void gemm2_kernel(const Args g) {
     issue(0, kt);  // register copies (zero-filled past the end)
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    mma_stage_sync<A_COL, B_COL>(lbase, lbase + TILE_BYTES, acc, wi, wj, lane);
+    // reduction length of this stage: the ragged tail of R, or the LoRA rank
+    const int len = tail && kt == nfull ? (int)(rend - (rbeg + (int64_t)nfull * BK)) : g.R2;
+    mma_stage_sync<A_COL, B_COL>(lbase, lbase + TILE_BYTES, acc, wi, wj, lane, (len + 15) / 16);
     __syncthreads();
   }
 
