@@ -126,7 +126,8 @@ def kernel_rooflines(events):
 
 
 def bench_gemv(device, reps=20):
-    """Config 2: 36 layers x 7 linears per grouped launch; GB/s of packed idx + palettes."""
+    """Config 2: 36 layers x 7 linears per grouped launch (decode layouts); GB/s of the packed
+    indices and palette lookup words streamed."""
     import torch
     from palettize_hip import ops
     g = torch.Generator(device=device).manual_seed(1)
@@ -136,7 +137,9 @@ def bench_gemv(device, reps=20):
         for name, K, N, _r in SHAPES:
             packed, pal, _ = _make_weight(N, K, g, device)
             weights.append((packed, pal, K))
-            wbytes += packed.numel() * 4 + pal.numel() * 4
+            # bytes the decode layouts stream: 2-bit indices + 8 B of bf16 lookup words per
+            # row and 256-k group (the fp32 palette would be 16 B)
+            wbytes += packed.numel() * 4 + pal.numel() * 2
     res = {}
     for M in (1, 4, 16):
         items = [(torch.randn(M, K, generator=g, device=device).to(torch.bfloat16), p, pl)

@@ -217,10 +217,10 @@ typedef struct plz_gemv_desc {
   int64_t N, K;
   int64_t block_begin;    /* filled by plz_gemv_plan: first 128-row work item of this linear */
   int64_t cost_begin;     /* filled by plz_gemv_plan: sum of K over the items before it */
-  const float* palette_items; /* optional (may be NULL): the palettes repacked by
-                                 plz_gemv_pack_palettes, read instead of `palette` */
-  const int32_t* packed_items; /* optional (may be NULL): the indices repacked by
-                                  plz_gemv_pack_indices, read instead of `packed` */
+  const uint32_t* palette_items; /* decode layout (plz_gemv_pack_palettes): read instead of
+                                    `palette` by decode-layout launches; may be NULL otherwise */
+  const int32_t* packed_items;    /* decode layout (plz_gemv_pack_indices): read instead of
+                                     `packed` by decode-layout launches; may be NULL otherwise */
 } plz_gemv_desc;
 
 /* y[M,N] = x[M,K] W^T for 1 <= M <= 16 (bandwidth-bound; one pass over the packed weights).
@@ -228,12 +228,13 @@ typedef struct plz_gemv_desc {
  * a 64-row tile at M = 1. */
 int plz_lut_gemv(const uint16_t* x, const int32_t* packed, const float* palette, uint16_t* y,
                  int64_t M, int64_t N, int64_t K, void* stream);
-/* Decode weight layout (one-time repack, e.g. at model load): the fp32 palettes [N, K/256, 4]
- * regrouped as [ceil(N/128)][K/256][128][4] (rows past N zero), so that the GEMV reads each
- * stage's palettes as one contiguous 2 KB block instead of 128 scattered 16-byte pieces.
- * Same bytes per weight as the native layout. */
+/* Decode palette layout (one-time repack, e.g. at model load): each row's 4-entry palette per
+ * 256-k group, rounded to bf16 as the GEMMs do, stored as the dequantiser's two lookup words
+ * (low bytes of entries 0..3, then their high bytes), regrouped as [ceil(N/128)][K/256][128]
+ * [lo, hi] (rows past N zero). A GEMV stage reads its 128 rows' tables as one contiguous 1 KB
+ * block; 8 B per row and group instead of the fp32 palette's 16 B. */
 size_t plz_gemv_palette_items_bytes(int64_t N, int64_t K);
-int plz_gemv_pack_palettes(const float* palette, float* palette_items, int64_t N, int64_t K,
+int plz_gemv_pack_palettes(const float* palette, uint32_t* palette_items, int64_t N, int64_t K,
                            void* stream);
 /* Decode index layout (one-time repack): the packed indices [N, K/16] regrouped per 128-row
  * item and 256-k stage into one contiguous 8 KB block each, in the order the GEMV's waves read
@@ -245,14 +246,14 @@ int plz_gemv_pack_indices(const int32_t* packed, int32_t* packed_items, int64_t 
 /* plz_lut_gemv on weights in the two decode layouts (plz_gemv_pack_indices and
  * plz_gemv_pack_palettes). */
 int plz_lut_gemv_decode(const uint16_t* x, const int32_t* packed_items,
-                        const float* palette_items, uint16_t* y, int64_t M, int64_t N, int64_t K,
-                        void* stream);
+                        const uint32_t* palette_items, uint16_t* y, int64_t M, int64_t N,
+                        int64_t K, void* stream);
 /* Fills block_begin and cost_begin of n host descriptors and returns the total number of
  * 128-row work items (or a negative status). A descriptor with N > 0 needs K > 0. */
 int64_t plz_gemv_plan(plz_gemv_desc* descs, int n, int M);
-/* Index layout of a grouped launch: every descriptor's `packed` (native) or every
- * descriptor's `packed_items` (decode layout). A descriptor whose array for the chosen layout is
- * NULL reads zero indices (no fault). */
+/* Weight layout of a grouped launch: PLZ_GEMV_NATIVE reads every descriptor's `packed` and
+ * `palette`, PLZ_GEMV_DECODE its `packed_items` and `palette_items`. A descriptor whose array
+ * for the chosen layout is NULL reads zeros there (no fault). */
 #define PLZ_GEMV_NATIVE 0
 #define PLZ_GEMV_DECODE 1
 /* Runs n independent GEMVs (all with the same M) in one launch. descs_device is a copy of

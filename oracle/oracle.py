@@ -168,6 +168,21 @@ def gemv_decode_layout(idx) -> np.ndarray:
     return np.ascontiguousarray(out.transpose(0, 4, 1, 2, 5, 3, 6)).reshape(-1)
 
 
+def gemv_palette_luts(palette) -> np.ndarray:
+    """palette fp32 [N, G, 4] -> uint32 [ceil(N/128), G, 128, 2]: per row and group the bf16
+    (RNE) entries' low bytes (entry c in byte c), then their high bytes; rows past N zero."""
+    pal = np.asarray(palette, np.float32)
+    N, G = pal.shape[:2]
+    items = (N + 127) // 128
+    bits = np.zeros((items * 128, G, 4), np.uint32)
+    bits[:N] = bf16_bits(pal).astype(np.uint32)
+    sh = np.arange(4, dtype=np.uint32) * 8
+    lo = ((bits & 0xFF) << sh).sum(-1, dtype=np.uint64).astype(np.uint32)
+    hi = ((bits >> 8) << sh).sum(-1, dtype=np.uint64).astype(np.uint32)
+    out = np.stack([lo, hi], -1).reshape(items, 128, G, 2).transpose(0, 2, 1, 3)
+    return np.ascontiguousarray(out).reshape(-1)
+
+
 # --------------------------------------------------------------------------------------
 # hard linear: forward / backward (fused_lut_linear_cuda.py:755-818,
 # fused_lut_kernel.cu:309-518, 551-720, 902-1123, 1129-1147)

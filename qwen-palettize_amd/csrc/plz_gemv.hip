@@ -217,13 +217,13 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(const plz_gemv_desc* _
       const void* qsrc = DEC ? (const void*)pc.d.packed_items : (const void*)pc.d.packed;
       const int64_t qbytes = DEC ? (N + ROWS - 1) / ROWS * ROWS * (K / 4) : N * K / 4;
       rq = make_rsrc(qsrc, live && qsrc ? (uint32_t)qbytes : 0u);
-      // palettes: native [N, K/256, 4] (16 B per row and stage, rows gpr*16 B apart) or
-      // prepacked [item][group][128 rows][4] (2 KB contiguous per stage)
-      const bool pre = pc.d.palette_items != nullptr;
-      const int64_t pbytes = pre ? (N + ROWS - 1) / ROWS * ROWS * gpr * 16 : N * gpr * 16;
-      const void* psrc = pre ? (const void*)pc.d.palette_items : (const void*)pc.d.palette;
+      // palettes: native fp32 [N, K/256, 4] (16 B per row and stage, rows gpr*16 B apart), or
+      // with the decode layout the lookup tables [item][group][128 rows][lo, hi] (1 KB
+      // contiguous per stage)
+      const int64_t pbytes = DEC ? (N + ROWS - 1) / ROWS * ROWS * gpr * 8 : N * gpr * 16;
+      const void* psrc = DEC ? (const void*)pc.d.palette_items : (const void*)pc.d.palette;
       rp = make_rsrc(psrc, live && psrc ? (uint32_t)pbytes : 0u);
-      pstride = pre ? (uint32_t)(ROWS * 16) : 16u;
+      pstride = DEC ? (uint32_t)(ROWS * 8) : 16u;
       rx = make_rsrc(pc.d.x, live ? (uint32_t)(M * K * 2) : 0u);
       const uint32_t r0 = (uint32_t)pc.row0;
 #pragma unroll
@@ -234,8 +234,8 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(const plz_gemv_desc* _
 #pragma unroll
       for (int j = 0; j < NPX; ++j) {
         const int g = WAVES * j + wave;
-        if (g < 2) {  // palettes of rows 64g + lane, group kc
-          mbase[j] = pre ? (r0 * (uint32_t)gpr + 64 * g + lane) * 16u
+        if (g < 2) {  // palettes of rows 64g + lane (native) or the stage's 1 KB of tables
+          mbase[j] = DEC ? (g == 0 ? r0 * (uint32_t)gpr * 8u + lane * 16u : kBufOob)
                          : (r0 + 64 * g + lane) * (uint32_t)gpr * 16u;
         } else {      // x tokens 2(g-2), 2(g-2)+1
           const int m = 2 * (g - 2) + (lane >> 5);
@@ -254,7 +254,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(const plz_gemv_desc* _
       const int g = WAVES * j + wave;
       lds_u8* dst = st + W_BYTES + g * 1024;
       if (g < 2)
-        dma16(rp, mbase[j] + (uint32_t)pc.kc * pstride, dst);
+        dma16(rp, mbase[j] == kBufOob ? kBufOob : mbase[j] + (uint32_t)pc.kc * pstride, dst);
       else
         dma16(rx, mbase[j] == kBufOob ? kBufOob : mbase[j] + k0 * 2u, dst);
     }
@@ -299,9 +299,17 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(const plz_gemv_desc* _
         const u32x4 wv =
             DEC ? *(const lds_u32x4*)(st + wave * W_WAVE + r * 1024 + lane * 16)
                 : *(const lds_u32x4*)(st + wave * W_WAVE + row * 64 + ((q ^ w_swz(row)) << 4));
-        const u32x4 pv = *(const lds_u32x4*)(st + W_BYTES + (16 * RB * wave + row) * 16);
-        const PalLut t = make_lut(__uint_as_float(pv[0]), __uint_as_float(pv[1]),
-                                  __uint_as_float(pv[2]), __uint_as_float(pv[3]));
+        PalLut t;
+        if (DEC) {
+          const u32x2 lv = *(const __attribute__((address_space(3))) u32x2*)(
+              st + W_BYTES + (16 * RB * wave + row) * 8);
+          t.lo = lv[0];
+          t.hi = lv[1];
+        } else {
+          const u32x4 pv = *(const lds_u32x4*)(st + W_BYTES + (16 * RB * wave + row) * 16);
+          t = make_lut(__uint_as_float(pv[0]), __uint_as_float(pv[1]), __uint_as_float(pv[2]),
+                       __uint_as_float(pv[3]));
+        }
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
           u32x4 a0, a1;
@@ -385,15 +393,22 @@ static int launch(int64_t items, hipStream_t st, const plz_gemv_desc* descs, int
              : launch_dec<GROUPED, false>(items, st, descs, n, single, M, what);
 }
 
-// palette [N, G, 4] -> [ceil(N/ROWS)][G][ROWS][4] (rows past N zero): one float4 per thread
-__global__ void pack_palettes_kernel(const float4* __restrict__ pal, float4* __restrict__ out,
+// palette [N, G, 4] -> lookup tables [ceil(N/ROWS)][G][ROWS][lo, hi] (make_lut of the row's
+// group, rows past N zero): one row and group per thread
+__global__ void pack_palettes_kernel(const float4* __restrict__ pal, uint2* __restrict__ out,
                                      int64_t N, int64_t G) {
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t items = (N + ROWS - 1) / ROWS;
   if (t >= items * G * ROWS) return;
   const int64_t row = t % ROWS, g = (t / ROWS) % G, item = t / (ROWS * G);
   const int64_t n = item * ROWS + row;
-  out[t] = n < N ? pal[n * G + g] : make_float4(0.f, 0.f, 0.f, 0.f);
+  uint2 v = make_uint2(0u, 0u);
+  if (n < N) {
+    const float4 p = pal[n * G + g];
+    const PalLut lut = make_lut(p.x, p.y, p.z, p.w);
+    v = make_uint2(lut.lo, lut.hi);
+  }
+  out[t] = v;
 }
 
 // packed [N, K/16] -> decode layout [ceil(N/ROWS)][K/256][WAVES][RB][64 lanes][4 words]: lane
@@ -433,7 +448,7 @@ static int check_desc(const plz_gemv_desc& d, int i) {
               "plz_gemv: descriptor %d: x, packed and palettes must be 16-byte aligned", i);
   PLZ_REQUIRE((d.N + ROWS - 1) / ROWS * ROWS * (d.K / 4) < (int64_t)kBufOob,
               "plz_gemv: descriptor %d: decode-layout indices above 2 GiB", i);
-  PLZ_REQUIRE((d.N + ROWS - 1) / ROWS * ROWS * (d.K / 256) * 16 < (int64_t)kBufOob,
+  PLZ_REQUIRE((d.N + ROWS - 1) / ROWS * ROWS * (d.K / 256) * 8 < (int64_t)kBufOob,
               "plz_gemv: descriptor %d: prepacked palettes above 2 GiB", i);
   return PLZ_OK;
 }
@@ -463,7 +478,7 @@ int plz_lut_gemv(const uint16_t* x, const int32_t* packed, const float* palette,
 }
 
 int plz_lut_gemv_decode(const uint16_t* x, const int32_t* packed_items,
-                        const float* palette_items, uint16_t* y, int64_t M, int64_t N, int64_t K,
+                        const uint32_t* palette_items, uint16_t* y, int64_t M, int64_t N, int64_t K,
                         void* stream) {
   PLZ_REQUIRE(M >= 1 && M <= 16, "plz_lut_gemv_decode: M (%lld) must be in [1, 16]", (long long)M);
   PLZ_REQUIRE(N == 0 || K == 0 || (packed_items && palette_items),
@@ -502,10 +517,10 @@ int plz_gemv_pack_indices(const int32_t* packed, int32_t* packed_items, int64_t 
 
 size_t plz_gemv_palette_items_bytes(int64_t N, int64_t K) {
   if (N <= 0 || K <= 0) return 0;
-  return (size_t)((N + ROWS - 1) / ROWS) * ROWS * (K / kPalGroup) * 16;
+  return (size_t)((N + ROWS - 1) / ROWS) * ROWS * (K / kPalGroup) * 8;
 }
 
-int plz_gemv_pack_palettes(const float* palette, float* palette_items, int64_t N, int64_t K,
+int plz_gemv_pack_palettes(const float* palette, uint32_t* palette_items, int64_t N, int64_t K,
                            void* stream) {
   PLZ_REQUIRE(N >= 0 && K >= 0 && K % kPalGroup == 0,
               "plz_gemv_pack_palettes: need N, K >= 0 and K a multiple of 256");
@@ -515,7 +530,7 @@ int plz_gemv_pack_palettes(const float* palette, float* palette_items, int64_t N
   const int64_t G = K / kPalGroup, total = (N + ROWS - 1) / ROWS * G * ROWS;
   hipLaunchKernelGGL(pack_palettes_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
                      (hipStream_t)stream, reinterpret_cast<const float4*>(palette),
-                     reinterpret_cast<float4*>(palette_items), N, G);
+                     reinterpret_cast<uint2*>(palette_items), N, G);
   return check_launch("plz_gemv_pack_palettes");
 }
 

@@ -378,11 +378,13 @@ def lut_gemv(x, packed, palette):
 
 
 def gemv_pack_palettes(palette):
-    """One-time decode layout of a palette [N, K/256, 4]: [ceil(N/128), K/256, 128, 4]."""
+    """One-time decode layout of a palette [N, K/256, 4] (plz_gemv_pack_palettes): per 128-row
+    item, group and row the two 32-bit lookup words of the bf16-rounded entries (low bytes, then
+    high bytes), [ceil(N/128), K/256, 128, 2]. Returned as a flat int32 tensor."""
     _need(palette, "palette", torch.float32, 3)
     N, G = palette.shape[0], palette.shape[1]
     nbytes = query("plz_gemv_palette_items_bytes", N, G * 256)
-    out = torch.empty(max(nbytes // 4, 1), dtype=torch.float32, device=palette.device)
+    out = torch.empty(max(nbytes // 4, 4), dtype=torch.int32, device=palette.device)
     call("plz_gemv_pack_palettes", _ptr(palette), _ptr(out), N, G * 256, _stream(palette))
     return out
 

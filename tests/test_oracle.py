@@ -399,3 +399,18 @@ def test_gemv_decode_layout_through_the_dequantiser_slot_order():
     back = dec.transpose(0, 2, 3, 5, 1, 4, 6, 7).reshape(items * 128, K)
     assert np.array_equal(back[:N], idx)
     assert not back[N:].any()
+
+
+def test_gemv_palette_luts_reassemble_torch_bf16():
+    """Byte c of the low word and byte c of the high word of each row's tables reassemble
+    entry c as torch rounds it to bf16; padded rows are zero."""
+    rng = np.random.default_rng(6)
+    pal = (rng.standard_normal((130, 3, 4)) * 0.02).astype(np.float32)
+    luts = O.gemv_palette_luts(pal).reshape(2, 3, 128, 2).transpose(0, 2, 1, 3).reshape(256, 3, 2)
+    c = np.arange(4, dtype=np.uint32) * 8
+    lo = (luts[..., 0:1] >> c) & 0xFF
+    hi = (luts[..., 1:2] >> c) & 0xFF
+    got = (lo | (hi << 8)).astype(np.uint16)
+    want = torch.from_numpy(pal).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got[:130], want)
+    assert not got[130:].any()
