@@ -93,10 +93,12 @@ __device__ __forceinline__ void build_w_pair(const uint16_t* __restrict__ logits
       e[c] = __expf(a[c] - m);
       s += e[c];
     }
+    // one reciprocal, as the soft backward's epilogue computes P: both passes see the same P
+    const float rs = 1.f / s;
     float P[4], ws = 0.f;
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      P[c] = e[c] / s;
+      P[c] = e[c] * rs;
       ws += P[c] * pc[c];
     }
     // argmax, first maximum wins (strict >), over P (noisy) or over the plain logits
