@@ -35,7 +35,7 @@ def _inputs(B, S, Hq, Hkv, seed, std=1.0):
 
 
 @pytest.mark.parametrize("B,S,Hq,Hkv,std", [(2, 256, 8, 2, 1.0), (1, 512, 4, 4, 1.0),
-                                            (1, 128, 32, 8, 3.0)])
+                                            (1, 128, 32, 8, 3.0), (1, 1024, 16, 2, 1.0)])
 def test_attn_fwd_matches_fp32(dev, B, S, Hq, Hkv, std):
     q, k, v = _inputs(B, S, Hq, Hkv, seed=S + Hq, std=std)
     o, lse = ops.attn_fwd(q.to(dev), k.to(dev), v.to(dev))
@@ -52,7 +52,8 @@ def _ref_grads(q, k, v, go):
 
 
 @pytest.mark.parametrize("B,S,Hq,Hkv,std", [(2, 256, 8, 2, 1.0), (1, 512, 4, 4, 1.0),
-                                            (1, 128, 32, 8, 3.0), (1, 384, 6, 1, 1.0)])
+                                            (1, 128, 32, 8, 3.0), (1, 384, 6, 1, 1.0),
+                                            (1, 1024, 16, 2, 1.0)])
 def test_attn_bwd_matches_fp32(dev, B, S, Hq, Hkv, std):
     """dQ, dK, dV (dK / dV summed over the query heads of each kv head) against fp32 autograd
     of the same attention; P and dS enter the products as bf16, as in the forward."""
