@@ -526,17 +526,6 @@ using namespace plz::attn;
 
 namespace {
 
-int reserve_lds(const void* fn, size_t bytes, bool& done, const char* what) {
-  if (done) return PLZ_OK;
-  const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
-  if (e != hipSuccess) {
-    set_error("%s: cannot reserve %zu bytes of LDS: %s", what, bytes, hipGetErrorString(e));
-    return PLZ_EHIP;
-  }
-  done = true;
-  return PLZ_OK;
-}
-
 // shared argument checks of the forward and backward: PLZ_OK, an error status, or kEmpty
 // (valid, nothing to do)
 constexpr int kEmpty = -1;
@@ -572,8 +561,8 @@ int plz_attn_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16
   if (rc != PLZ_OK) return rc == kEmpty ? PLZ_OK : rc;
   PLZ_REQUIRE(q && k && v && o && lse, "plz_attn_fwd: null pointer");
   PLZ_REQUIRE(aligned16({q, k, v, o}), "plz_attn_fwd: q, k, v, o must be 16-byte aligned");
-  static bool attr = false;
-  const int lr = reserve_lds((const void*)attn_fwd_kernel, kLds, attr, "plz_attn_fwd");
+  static uint64_t lds_done = 0;
+  const int lr = reserve_lds((const void*)attn_fwd_kernel, kLds, lds_done, "plz_attn_fwd");
   if (lr != PLZ_OK) return lr;
   const float scale_log2 = scale * kLog2e;
   hipLaunchKernelGGL(attn_fwd_kernel, dim3((unsigned)(seq / BM) * heads * batch), dim3(NT), kLds, (hipStream_t)stream, q, k, v, o, lse, batch, seq, heads,
@@ -602,9 +591,10 @@ int plz_attn_bwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, const 
               plz_attn_bwd_workspace(batch, seq, heads));
     return PLZ_EWORKSPACE;
   }
-  static bool attr_dq = false, attr_dkv = false;
-  int lr = reserve_lds((const void*)attn_bwd_dq_kernel, kLds, attr_dq, "plz_attn_bwd");
-  if (lr == PLZ_OK) lr = reserve_lds((const void*)attn_bwd_dkv_kernel, kLdsDkv, attr_dkv, "plz_attn_bwd");
+  static uint64_t lds_dq = 0, lds_dkv = 0;
+  int lr = reserve_lds((const void*)attn_bwd_dq_kernel, kLds, lds_dq, "plz_attn_bwd");
+  if (lr == PLZ_OK)
+    lr = reserve_lds((const void*)attn_bwd_dkv_kernel, kLdsDkv, lds_dkv, "plz_attn_bwd");
   if (lr != PLZ_OK) return lr;
   const float scale_log2 = scale * kLog2e;
   float* dsum = (float*)workspace;

@@ -176,6 +176,9 @@ __device__ __forceinline__ void philox_gumbel4(uint64_t seed, uint64_t ctr, floa
 void set_error(const char* fmt, ...);
 int check_launch(const char* what);
 void zero_async(void* p, size_t bytes, hipStream_t stream);  // kernel fill, capture-safe
+// Raises a kernel's dynamic-LDS limit to `bytes` on the current device, once per device (the
+// attribute is per device); `done` is the calling site's bit mask of devices already set up.
+int reserve_lds(const void* fn, size_t bytes, uint64_t& done, const char* what);
 
 }  // namespace plz
 

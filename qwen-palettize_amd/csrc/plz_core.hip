@@ -37,6 +37,20 @@ __global__ void zero_kernel(uint16_t* __restrict__ p, int64_t n) {
   if (i < n) p[i] = 0;
 }
 
+int reserve_lds(const void* fn, size_t bytes, uint64_t& done, const char* what) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+  const uint64_t bit = dev >= 0 && dev < 64 ? (uint64_t)1 << dev : 0;
+  if (bit != 0 && (done & bit) != 0) return PLZ_OK;
+  const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+  if (e != hipSuccess) {
+    set_error("%s: cannot reserve %zu bytes of LDS: %s", what, bytes, hipGetErrorString(e));
+    return PLZ_EHIP;
+  }
+  done |= bit;
+  return PLZ_OK;
+}
+
 void zero_async(void* p, size_t bytes, hipStream_t stream) {
   const int64_t n = (int64_t)(bytes / 2);
   if (n > 0)

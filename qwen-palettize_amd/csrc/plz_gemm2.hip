@@ -700,16 +700,8 @@ static int launch(Args g, int splits, hipStream_t stream, const char* what) {
   if (g.r_split <= 0) g.r_split = g.R;
   if (g.group <= 0) g.group = 8;
   auto kern = gemm2_kernel<KA, KB, EPI>;
-  static bool attr = false;
-  if (!attr) {
-    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       (int)kLds);
-    if (e != hipSuccess) {
-      set_error("%s: cannot reserve %zu bytes of LDS: %s", what, kLds, hipGetErrorString(e));
-      return PLZ_EHIP;
-    }
-    attr = true;
-  }
+  static uint64_t lds_done = 0;
+  if (int rc = reserve_lds((const void*)kern, kLds, lds_done, what)) return rc;
   const int64_t tiles = (int64_t)g.tiles_i * g.tiles_j;
   if (tiles == 0 || splits == 0) return PLZ_OK;
   // the copies address each operand through a 32-bit buffer offset
@@ -726,16 +718,8 @@ static int launch(Args g, int splits, hipStream_t stream, const char* what) {
   hipLaunchKernelGGL(kern, dim3((unsigned)gx, 1, (unsigned)splits), dim3(NTHR), kLds, stream, g);
   int rc = check_launch(what);
   if (rc != PLZ_OK || !tail) return rc;
-  static bool rattr = false;
-  if (!rattr) {
-    hipError_t e = hipFuncSetAttribute((const void*)tail_reduce_kernel,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLds);
-    if (e != hipSuccess) {
-      set_error("%s: cannot reserve %zu bytes of LDS: %s", what, kLds, hipGetErrorString(e));
-      return PLZ_EHIP;
-    }
-    rattr = true;
-  }
+  static uint64_t rlds_done = 0;
+  if ((rc = reserve_lds((const void*)tail_reduce_kernel, kLds, rlds_done, what))) return rc;
   hipLaunchKernelGGL(tail_reduce_kernel, dim3((unsigned)(tiles - g.tail_first)), dim3(NTHR), kLds,
                      stream, g);
   return check_launch(what);

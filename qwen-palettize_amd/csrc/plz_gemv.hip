@@ -357,18 +357,8 @@ template <int NPX, bool GROUPED, bool DEC>
 static int launch_nx(int64_t items, hipStream_t st, const plz_gemv_desc* descs, int n,
                      plz_gemv_desc single, int M, const char* what) {
   auto kern = gemv_kernel<NPX, GROUPED, DEC>;
-  static bool attr = false;
-  if (!attr) {
-    const hipError_t e = hipFuncSetAttribute((const void*)kern,
-                                             hipFuncAttributeMaxDynamicSharedMemorySize,
-                                             lds_bytes<NPX>());
-    if (e != hipSuccess) {
-      set_error("%s: cannot reserve %d bytes of LDS: %s", what, lds_bytes<NPX>(),
-                hipGetErrorString(e));
-      return PLZ_EHIP;
-    }
-    attr = true;
-  }
+  static uint64_t lds_done = 0;
+  if (int rc = reserve_lds((const void*)kern, (size_t)lds_bytes<NPX>(), lds_done, what)) return rc;
   const int64_t slots = wgs_per_cu<NPX>() * (int64_t)cu_count();
   const int64_t g = items < slots ? items : slots;
   hipLaunchKernelGGL(kern, dim3((unsigned)g), dim3(64 * WAVES), lds_bytes<NPX>(), st, descs, n,

@@ -357,19 +357,6 @@ static int col_splits(int64_t M, int64_t L) {
   return (int)((M + s - 1) / s);
 }
 
-template <typename K>
-static int reserve_lds(K kern, const char* what) {
-  static bool done = false;
-  if (done) return PLZ_OK;
-  const hipError_t e =
-      hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, CL_LDS);
-  if (e != hipSuccess) {
-    set_error("%s: cannot reserve %d bytes of LDS: %s", what, CL_LDS, hipGetErrorString(e));
-    return PLZ_EHIP;
-  }
-  done = true;
-  return PLZ_OK;
-}
 
 // grad_B = scale * grad_y^T t ([N, r]) and grad_A = (x^T gt)^T ([r, K]): one cols_kernel launch
 // over both, then one reduction launch. Workspace: split partials of B, then of A.
@@ -404,11 +391,13 @@ static int cols(const uint16_t* x, const uint16_t* grad_y, const uint16_t* t, co
   if (nwg[0] + nwg[1] == 0) return PLZ_OK;
   const dim3 grid((unsigned)(nwg[0] + nwg[1]));
   int rc;
+  // one device mask per kernel: each instance needs its own LDS attribute
+  static uint64_t lds_done1 = 0, lds_done2 = 0;
   if (r <= 16) {
-    if ((rc = reserve_lds(cols_kernel<1>, what))) return rc;
+    if ((rc = reserve_lds((const void*)cols_kernel<1>, CL_LDS, lds_done1, what))) return rc;
     hipLaunchKernelGGL(cols_kernel<1>, grid, dim3(256), CL_LDS, s, g);
   } else {
-    if ((rc = reserve_lds(cols_kernel<2>, what))) return rc;
+    if ((rc = reserve_lds((const void*)cols_kernel<2>, CL_LDS, lds_done2, what))) return rc;
     hipLaunchKernelGGL(cols_kernel<2>, grid, dim3(256), CL_LDS, s, g);
   }
   if ((rc = check_launch(what))) return rc;
