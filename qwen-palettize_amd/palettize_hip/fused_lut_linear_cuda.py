@@ -31,7 +31,7 @@ import torch.nn.functional as F
 from torch import Tensor
 
 from . import ops
-from ._lib import PLZ_W_HARD_NOISY
+from ._lib import PLZ_W_HARD_NOISY, PLZ_W_SOFT
 
 GROUP_SIZE = 256
 _PACK_CACHE: "OrderedDict[tuple, Tensor]" = OrderedDict()
@@ -154,58 +154,106 @@ def logits_from_reference(logits: Tensor, K: int) -> Tensor:
     return nk4.contiguous()
 
 
+def _noise_to_native(noise: Tensor, K: int, N: int, Kp: int) -> Tensor:
+    """Supplied Gumbel noise, fp32, in the logits' reference layout (4, K, N) or native
+    [N, K, 4] -> native [N, Kp, 4] (padded columns get zero noise; their x is zero)."""
+    if noise.dtype != torch.float32:
+        raise TypeError("noise must be fp32")
+    if tuple(noise.shape) == (4, K, N):
+        noise = noise.permute(2, 1, 0)
+    elif tuple(noise.shape) != (N, K, 4):
+        raise ValueError(f"noise must be (4, K, N) or [N, K, 4], got {tuple(noise.shape)}")
+    if Kp != K:
+        noise = F.pad(noise, (0, 0, 0, Kp - K))
+    return noise.contiguous()
+
+
+def _soft_forward(ctx, x, palette, logits, bias, group_size, tau, noise, ste):
+    """Forward of fused_lut_linear_soft: W from logits + noise + palette (W_hard of the noisy
+    P when ste, else W_soft), then y = x W^T + b. Saves what _soft_backward needs."""
+    if logits.dim() != 3 or logits.shape[0] != 4:
+        raise ValueError("logits first dim must be 4")
+    if logits.dtype not in (torch.float16, torch.bfloat16):
+        raise TypeError("logits must be fp16 or bf16")
+    _, K, N = logits.shape
+    if x.shape[-1] != K:
+        raise ValueError(f"x K={x.shape[-1]} != logits K={K}")
+    if N % group_size or N // group_size != palette.shape[0]:
+        raise ValueError("G mismatch")
+    if N % 8:
+        raise ValueError(f"N ({N}) must be a multiple of 8")
+    xp = _prep_x(x, K)
+    Kp = xp.shape[1]
+    lg = logits_from_reference(logits, K)
+    if noise is None:  # the reference's LCG draw, one seed per forward
+        noise = ops.gumbel_lcg(N, Kp, _next_soft_step_seed(), device=x.device)
+    else:
+        noise = _noise_to_native(noise, K, N, Kp)
+    pal = palette_from_reference(palette, N, K, group_size)
+    w, _ = ops.soft_build_w(lg, noise, pal, float(tau),
+                            PLZ_W_HARD_NOISY if ste else PLZ_W_SOFT)
+    b = None if bias is None else bias.to(torch.bfloat16).contiguous()
+    y = ops.linear_fwd_dense(xp, w, b)
+    ctx.save_for_backward(xp, pal, lg, noise, w)
+    ctx.group_size, ctx.K, ctx.tau = group_size, K, float(tau)
+    ctx.pal_dtype, ctx.logits_dtype = palette.dtype, logits.dtype
+    ctx.has_bias = bias is not None
+    ctx.bias_dtype = None if bias is None else bias.dtype
+    return y
+
+
+def _soft_backward(ctx, grad_y):
+    """(grad_x, grad_palette, grad_logits, grad_bias) in the reference layouts."""
+    xp, pal, lg, noise, w = ctx.saved_tensors
+    grad_y = grad_y.contiguous()
+    grad_x = grad_pal = grad_logits = grad_bias = None
+    if ctx.needs_input_grad[0]:
+        grad_x = ops.linear_bwd_x_dense(grad_y, w)[:, : ctx.K].contiguous()
+    if ctx.needs_input_grad[1] or ctx.needs_input_grad[2]:
+        gl, gp = ops.soft_bwd(xp, grad_y, lg, noise, pal, ctx.tau)
+        if ctx.needs_input_grad[2]:
+            grad_logits = gl[:, : ctx.K, :].permute(2, 1, 0).contiguous().to(ctx.logits_dtype)
+        if ctx.needs_input_grad[1]:
+            grad_pal = palette_grad_to_reference(gp, ctx.group_size).to(ctx.pal_dtype)
+    if ctx.has_bias and ctx.needs_input_grad[3]:
+        grad_bias = ops.bias_grad(grad_y).to(ctx.bias_dtype)
+    return grad_x, grad_pal, grad_logits, grad_bias
+
+
 class CUDAFusedLUTLinearSoft(torch.autograd.Function):
     """forward(ctx, x, palette, logits, bias, group_size, tau) -> y
     backward(ctx, grad_y) -> (grad_x, grad_palette, grad_logits, grad_bias, None, None)"""
 
     @staticmethod
     def forward(ctx, x, palette, logits, bias, group_size, tau):
-        if logits.dim() != 3 or logits.shape[0] != 4:
-            raise ValueError("logits first dim must be 4")
-        if logits.dtype not in (torch.float16, torch.bfloat16):
-            raise TypeError("logits must be fp16 or bf16")
-        _, K, N = logits.shape
-        if x.shape[-1] != K:
-            raise ValueError(f"x K={x.shape[-1]} != logits K={K}")
-        if N % group_size or N // group_size != palette.shape[0]:
-            raise ValueError("G mismatch")
-        if N % 8:
-            raise ValueError(f"N ({N}) must be a multiple of 8")
-        step_seed = _next_soft_step_seed()
-        xp = _prep_x(x, K)
-        Kp = xp.shape[1]
-        lg = logits_from_reference(logits, K)
-        noise = ops.gumbel_lcg(N, Kp, step_seed, device=x.device)
-        pal = palette_from_reference(palette, N, K, group_size)
-        w, _ = ops.soft_build_w(lg, noise, pal, float(tau), PLZ_W_HARD_NOISY)
-        b = None if bias is None else bias.to(torch.bfloat16).contiguous()
-        y = ops.linear_fwd_dense(xp, w, b)
-        ctx.save_for_backward(xp, pal, lg, noise, w)
-        ctx.group_size, ctx.K, ctx.tau = group_size, K, float(tau)
-        ctx.pal_dtype, ctx.logits_dtype = palette.dtype, logits.dtype
-        ctx.has_bias = bias is not None
-        ctx.bias_dtype = None if bias is None else bias.dtype
-        return y
+        return _soft_forward(ctx, x, palette, logits, bias, group_size, tau, None, True)
 
     @staticmethod
     def backward(ctx, grad_y):
-        xp, pal, lg, noise, w = ctx.saved_tensors
-        grad_y = grad_y.contiguous()
-        grad_x = grad_pal = grad_logits = grad_bias = None
-        if ctx.needs_input_grad[0]:
-            grad_x = ops.linear_bwd_x_dense(grad_y, w)[:, : ctx.K].contiguous()
-        if ctx.needs_input_grad[1] or ctx.needs_input_grad[2]:
-            gl, gp = ops.soft_bwd(xp, grad_y, lg, noise, pal, ctx.tau)
-            if ctx.needs_input_grad[2]:
-                grad_logits = gl[:, : ctx.K, :].permute(2, 1, 0).contiguous().to(ctx.logits_dtype)
-            if ctx.needs_input_grad[1]:
-                grad_pal = palette_grad_to_reference(gp, ctx.group_size).to(ctx.pal_dtype)
-        if ctx.has_bias and ctx.needs_input_grad[3]:
-            grad_bias = ops.bias_grad(grad_y).to(ctx.bias_dtype)
-        return grad_x, grad_pal, grad_logits, grad_bias, None, None
+        return _soft_backward(ctx, grad_y) + (None, None)
+
+
+class _SoftLUTLinearExt(torch.autograd.Function):
+    """fused_lut_linear_soft with supplied noise and / or the pure-soft forward (ste=False);
+    the backward is the same STE backward."""
+
+    @staticmethod
+    def forward(ctx, x, palette, logits, bias, group_size, tau, noise, ste):
+        return _soft_forward(ctx, x, palette, logits, bias, group_size, tau, noise, ste)
+
+    @staticmethod
+    def backward(ctx, grad_y):
+        return _soft_backward(ctx, grad_y) + (None, None, None, None)
 
 
 def fused_lut_linear_soft(x: Tensor, palette: Tensor, logits: Tensor, bias: Tensor | None = None,
-                          group_size: int = GROUP_SIZE, tau: float = 1.0) -> Tensor:
-    """Soft (Gumbel-Softmax) functional interface -- supports autograd."""
-    return CUDAFusedLUTLinearSoft.apply(x, palette, logits, bias, group_size, tau)
+                          group_size: int = GROUP_SIZE, tau: float = 1.0, *,
+                          noise: Tensor | None = None, ste: bool = True) -> Tensor:
+    """Soft (Gumbel-Softmax) functional interface -- supports autograd.
+
+    Beyond the reference's signature: ``noise`` (fp32, (4, K, N) like the logits or native
+    [N, K, 4]) replaces the internal LCG draw; ``ste=False`` makes the forward use W_soft =
+    sum_c P_c pal_c instead of the straight-through W_hard (the backward is unchanged)."""
+    if noise is None and ste:
+        return CUDAFusedLUTLinearSoft.apply(x, palette, logits, bias, group_size, tau)
+    return _SoftLUTLinearExt.apply(x, palette, logits, bias, group_size, tau, noise, ste)

@@ -151,3 +151,35 @@ def test_dropin_soft_reference_layout(dev):
     assert_close(f32(ld.grad), gl.transpose(2, 1, 0), what="drop-in grad_logits")
     want_gp = gp.reshape(N // GS, GS, -1, 4).sum(axis=(1, 2))
     assert_close(f32(pd.grad), want_gp, what="drop-in soft grad_palette")
+
+
+@pytest.mark.parametrize("ste", [True, False], ids=["ste", "pure-soft"])
+def test_dropin_soft_supplied_noise(dev, ste):
+    """fused_lut_linear_soft(..., noise=, ste=): noise in the logits' (4, K, N) layout replaces
+    the LCG draw (the step seed does not advance); ste=False puts W_soft in the forward. The
+    backward is the same STE backward either way."""
+    M, K, N, GS, tau = 64, 512, 256, 256, 0.7
+    g = gen(41)
+    logits = torch.randn(4, K, N, generator=g).to(torch.float16)
+    pal = torch.sort(torch.randn(N // GS, 4, generator=g) * 0.02, -1).values.to(torch.bfloat16)
+    noise_ref = torch.from_numpy(O.gumbel_philox(4 * K * N, seed=42).reshape(4, K, N))
+    x = randn_bf16(M, K, seed=43)
+    xd = x.to(dev).requires_grad_(True)
+    pd = pal.to(dev).requires_grad_(True)
+    ld = logits.to(dev).requires_grad_(True)
+    seed_before = FL._SOFT_STEP_SEED
+    y = FL.fused_lut_linear_soft(xd, pd, ld, None, GS, tau, noise=noise_ref.to(dev), ste=ste)
+    assert FL._SOFT_STEP_SEED == seed_before
+    lg_nk4 = f32(logits).transpose(2, 1, 0)
+    noise = noise_ref.numpy().transpose(2, 1, 0)
+    pal_nat = O.expand_reference_palette(f32(pal), N, K, GS)
+    mode = O.W_HARD_NOISY if ste else O.W_SOFT
+    _, _, w_fwd = O.soft_weights(lg_nk4, noise, pal_nat, tau, mode)
+    assert_close(f32(y), f32(x) @ O.bf16_round(w_fwd.astype(np.float32)).T.astype(np.float64),
+                 what="drop-in soft y (supplied noise)")
+    gy = randn_bf16(M, N, seed=44)
+    y.backward(gy.to(dev))
+    gl, gp = O.soft_backward(f32(x), f32(gy), lg_nk4, noise, pal_nat, tau)
+    assert_close(f32(ld.grad), gl.transpose(2, 1, 0), what="drop-in grad_logits (supplied noise)")
+    want_gp = gp.reshape(N // GS, GS, -1, 4).sum(axis=(1, 2))
+    assert_close(f32(pd.grad), want_gp, what="drop-in soft grad_palette (supplied noise)")
