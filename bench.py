@@ -126,20 +126,21 @@ def kernel_rooflines(events):
 
 
 def bench_gemv(device, reps=20):
-    """Config 2: 36 layers x 7 linears per grouped launch (decode layouts); GB/s of the packed
-    indices and palette lookup words streamed."""
+    """Config 2: 36 layers x 7 linears per grouped launch, on the decode layouts. GB/s as the
+    metric defines it: (packed indices + fp32 palettes) / time, 1,135,411,200 B per launch;
+    stream_gbs: the bytes the decode layouts actually stream (bf16 lookup words, 8 B per row
+    and 256-k group in place of 16)."""
     import torch
     from palettize_hip import ops
     g = torch.Generator(device=device).manual_seed(1)
     weights = []
-    wbytes = 0
+    wbytes = sbytes = 0
     for _ in range(LAYERS):
         for name, K, N, _r in SHAPES:
             packed, pal, _ = _make_weight(N, K, g, device)
             weights.append((packed, pal, K))
-            # bytes the decode layouts stream: 2-bit indices + 8 B of bf16 lookup words per
-            # row and 256-k group (the fp32 palette would be 16 B)
-            wbytes += packed.numel() * 4 + pal.numel() * 2
+            wbytes += packed.numel() * 4 + pal.numel() * 4
+            sbytes += packed.numel() * 4 + pal.numel() * 2
     res = {}
     for M in (1, 4, 16):
         items = [(torch.randn(M, K, generator=g, device=device).to(torch.bfloat16), p, pl)
@@ -158,9 +159,11 @@ def bench_gemv(device, reps=20):
         ms = s.elapsed_time(e) / reps
         gbs = wbytes / (ms * 1e-3) / 1e9
         res[f"M{M}"] = dict(us=round(ms * 1e3, 2), gbs=round(gbs, 1),
-                            frac=round(gbs / PEAK_HBM_GBS, 4))
+                            frac=round(gbs / PEAK_HBM_GBS, 4),
+                            stream_gbs=round(sbytes / (ms * 1e-3) / 1e9, 1))
         del grp, items
     res["weight_bytes"] = wbytes
+    res["stream_bytes"] = sbytes
     return res
 
 
@@ -227,7 +230,17 @@ def bench_layer(device, steps=4, warmup=2):
     e.record()
     torch.cuda.synchronize()
     ms = s.elapsed_time(e) / steps
-    return dict(ms_per_step=round(ms, 2), tokens_per_s=round(32 * 512 / (ms * 1e-3), 1),
+    # algorithmic FLOP of the step: student linears 6MKN (fwd, grad_x, dW), teacher 2MKN,
+    # LoRA 6Mr(K+N), causal attention 4*B*Hq*S^2*D/2 for the teacher's forward and 3x that
+    # for the student (fwd + bwd)
+    B, S, M = 32, 512, 32 * 512
+    h, q, kv, f = cfg.hidden, cfg.heads * cfg.head_dim, cfg.kv_heads * cfg.head_dim, cfg.intermediate
+    lin = [(h, q), (h, kv), (h, kv), (q, h), (h, f), (h, f), (f, h)]  # (K, N)
+    flop = sum(8.0 * M * k * n + 6.0 * M * cfg.lora_rank * (k + n) for k, n in lin)
+    flop += 4 * (4.0 * B * cfg.heads * S * S * cfg.head_dim / 2)
+    tflops = flop / (ms * 1e-3) / 1e12
+    return dict(ms_per_step=round(ms, 2), tokens_per_s=round(M / (ms * 1e-3), 1),
+                tflops=round(tflops, 1), mfma_frac=round(tflops / PEAK_BF16_TFLOPS, 4),
                 loss_first=round(float(losses[0]), 5), loss_last=round(float(losses[-1]), 5),
                 config="hidden 2560, 32/8 heads x 128, SwiGLU 9728, 7 soft palettized linears + LoRA r16, batch 32 x 512")
 
