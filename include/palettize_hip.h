@@ -109,6 +109,14 @@ int plz_linear_fwd_dense(const uint16_t* x, const uint16_t* w, const uint16_t* b
                          void* workspace, size_t workspace_bytes, int64_t M, int64_t N, int64_t K,
                          void* stream);
 size_t plz_linear_fwd_dense_workspace(int64_t M, int64_t N, int64_t K);
+/* Gate and up projections with the SwiGLU in the epilogue: h [M, N] = silu(x Wg^T) * (x Wu^T)
+ * as the HF Qwen3 MLP computes it in bf16 (transformers modeling_qwen3.py:70-83; the gate and
+ * up outputs are rounded to bf16 first, as the unfused path does, and never stored).
+ * w_gate_up bf16 [2N, K]: the rows of Wg and Wu interleaved in 128-row blocks (128 gate rows,
+ * the 128 matching up rows, ...). N a multiple of 128, K of 8; no bias, no LoRA. No
+ * counterpart in the reference, which runs the two nn.Linear and the activation apart. */
+int plz_linear_fwd_dense_swiglu(const uint16_t* x, const uint16_t* w_gate_up, uint16_t* h,
+                                int64_t M, int64_t N, int64_t K, void* stream);
 /* grad_x = grad_y w (+lora). Replaces torch.matmul(grad_y, W.T)
  * (fused_lut_linear_cuda.py:944). */
 int plz_linear_bwd_x_dense(const uint16_t* grad_y, const uint16_t* w, const uint16_t* lora_gt,

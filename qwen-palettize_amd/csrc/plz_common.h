@@ -172,6 +172,13 @@ __device__ __forceinline__ void philox_gumbel4(uint64_t seed, uint64_t ctr, floa
   z[3] = gumbel_from_bits(r.w);
 }
 
+// SwiGLU of one element as the HF Qwen3 MLP computes it on bf16 tensors: h = bf16(silu(g)) * u
+// for bf16 values g, u (the caller rounds h to bf16). Shared by the elementwise kernel and the
+// GEMM epilogue, so the fused and unfused paths agree bit for bit on the same g, u.
+__device__ __forceinline__ float swiglu_elem(float g, float u) {
+  return bf2f(f2bf(g / (1.f + __expf(-g)))) * u;
+}
+
 // ---- error reporting shared by every entry point -------------------------------
 void set_error(const char* fmt, ...);
 int check_launch(const char* what);

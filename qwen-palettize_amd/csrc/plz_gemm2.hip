@@ -16,7 +16,7 @@ namespace plz {
 namespace g2 {
 
 enum { OP_ROW = 0, OP_COL = 1, OP_LUT_ROW = 2, OP_LUT_COL = 3, OP_LUT_REG = 4 };
-enum { EPI_BF16 = 0, EPI_PAL = 1, EPI_SOFT = 2, EPI_F32 = 3 };
+enum { EPI_BF16 = 0, EPI_PAL = 1, EPI_SOFT = 2, EPI_F32 = 3, EPI_SWIGLU = 4 };
 
 // Masked register-path copies for a partial reduction stage (r >= rend reads as zero) and for
 // the rank-r second segment.
@@ -356,9 +356,10 @@ __device__ __forceinline__ void tile_of(const Args& g, int bid, int& tile_i, int
 // stores. acc[ti][tj][e]: row wi*128 + 32*ti + 8*(e/4) + 4*(lane/32) + e%4,
 // col wj*64 + 32*tj + lane%32.
 constexpr int EPI_RS = 528;  // staging row stride in bytes
-__device__ __forceinline__ void store_tile_bf16(const Args& g, const f32x16 (&acc)[WT_I][WT_J],
-                                                lds_u8* st, int64_t i0, int64_t j0, int wi,
-                                                int wj, int lane) {
+// The whole 256x256 tile as bf16 (alpha * acc + bias) in LDS, rows EPI_RS bytes apart.
+__device__ __forceinline__ void stage_tile_bf16(const Args& g, const f32x16 (&acc)[WT_I][WT_J],
+                                                lds_u8* st, int64_t j0, int wi, int wj,
+                                                int lane) {
   float bj[WT_J];
 #pragma unroll
   for (int tj = 0; tj < WT_J; ++tj) {
@@ -377,6 +378,11 @@ __device__ __forceinline__ void store_tile_bf16(const Args& g, const f32x16 (&ac
             (uint16_t)f2bf(g.alpha * acc[ti][tj][e] + bj[tj]);
       }
   __syncthreads();
+}
+__device__ __forceinline__ void store_tile_bf16(const Args& g, const f32x16 (&acc)[WT_I][WT_J],
+                                                lds_u8* st, int64_t i0, int64_t j0, int wi,
+                                                int wj, int lane) {
+  stage_tile_bf16(g, acc, st, j0, wi, wj, lane);
   uint16_t* C = reinterpret_cast<uint16_t*>(g.c);
 #pragma unroll 4
   for (int it = 0; it < TILE * TILE / 8 / NTHR; ++it) {
@@ -386,6 +392,37 @@ __device__ __forceinline__ void store_tile_bf16(const Args& g, const f32x16 (&ac
     if (i < g.I && j < g.J) {
       const u32x4 v = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(st + row * EPI_RS + c8 * 2);
       *reinterpret_cast<u32x4*>(C + i * g.ldc + j) = v;
+    }
+  }
+}
+
+// EPI_SWIGLU: the tile's columns are 128 gate columns followed by the 128 matching up columns
+// (the weight's rows interleaved in 128-row blocks); writes h = swiglu(gate, up) to the 128
+// columns j0/2 .. j0/2+127 of the [I, J/2] output, from the staged bf16 values, exactly as a
+// bf16 gate/up GEMM followed by the elementwise SwiGLU.
+__device__ __forceinline__ void store_tile_swiglu(const Args& g, const f32x16 (&acc)[WT_I][WT_J],
+                                                  lds_u8* st, int64_t i0, int64_t j0, int wi,
+                                                  int wj, int lane) {
+  stage_tile_bf16(g, acc, st, j0, wi, wj, lane);
+  uint16_t* C = reinterpret_cast<uint16_t*>(g.c);
+  const int64_t h0 = j0 / 2;
+#pragma unroll 2
+  for (int it = 0; it < TILE * (TILE / 2) / 8 / NTHR; ++it) {
+    const int ch = it * NTHR + threadIdx.x;  // 16 chunks of 8 output columns per row
+    const int row = ch >> 4, c8 = (ch & 15) * 8;
+    const int64_t i = i0 + row;
+    if (i < g.I) {
+      const lds_u8* r = st + row * EPI_RS;
+      const u32x4 gv = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(r + c8 * 2);
+      const u32x4 uv = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(r + (TILE / 2 + c8) * 2);
+      u32x4 hv;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const float lo = swiglu_elem(bf2f(gv[w] & 0xffffu), bf2f(uv[w] & 0xffffu));
+        const float hi = swiglu_elem(bf2f(gv[w] >> 16), bf2f(uv[w] >> 16));
+        hv[w] = f2bf2(lo, hi);
+      }
+      *reinterpret_cast<u32x4*>(C + i * g.ldc + h0 + c8) = hv;
     }
   }
 }
@@ -567,6 +604,10 @@ __global__ __launch_bounds__(NTHR) void gemm2_kernel(const Args g) {
       return;
     }
     store_tile_bf16(g, acc, lbase, i0, j0, wi, wj, lane);
+    return;
+  }
+  if (EPI == EPI_SWIGLU) {
+    store_tile_swiglu(g, acc, lbase, i0, j0, wi, wj, lane);
     return;
   }
 
@@ -1005,6 +1046,23 @@ int plz_linear_fwd_dense(const uint16_t* x, const uint16_t* w, const uint16_t* b
   const int rc = set_tail(g, workspace, workspace_bytes, "plz_linear_fwd_dense");
   if (rc != PLZ_OK) return rc;
   return launch<OP_ROW, OP_ROW, EPI_BF16>(g, 1, (hipStream_t)stream, "plz_linear_fwd_dense");
+}
+
+int plz_linear_fwd_dense_swiglu(const uint16_t* x, const uint16_t* w_gate_up, uint16_t* h,
+                                int64_t M, int64_t N, int64_t K, void* stream) {
+  PLZ_REQUIRE(M >= 0 && N >= 0 && K >= 0, "plz_linear_fwd_dense_swiglu: negative shape");
+  PLZ_REQUIRE(K % 8 == 0 && N % 128 == 0,
+              "plz_linear_fwd_dense_swiglu: K must be a multiple of 8 and N of 128");
+  if (M == 0 || N == 0) return PLZ_OK;
+  PLZ_REQUIRE(x && w_gate_up && h && a16(x) && a16(w_gate_up) && a16(h),
+              "plz_linear_fwd_dense_swiglu: x, w_gate_up, h must be non-null, 16-byte aligned");
+  Args g = {};
+  g.a = x; g.lda = K; g.b = w_gate_up; g.ldb = K;
+  g.I = M; g.J = 2 * N; g.R = K;
+  g.c = h; g.ldc = N; g.alpha = 1.f;
+  g.group = 8;
+  return launch<OP_ROW, OP_ROW, EPI_SWIGLU>(g, 1, (hipStream_t)stream,
+                                            "plz_linear_fwd_dense_swiglu");
 }
 
 size_t plz_linear_bwd_x_dense_workspace(int64_t M, int64_t N, int64_t K) {

@@ -210,7 +210,7 @@ __global__ void swiglu_fwd_kernel(const uint16_t* __restrict__ gate, const uint1
   unpack8(reinterpret_cast<const uint4*>(gate)[t], g);
   unpack8(reinterpret_cast<const uint4*>(up)[t], u);
 #pragma unroll
-  for (int j = 0; j < 8; ++j) o[j] = bf2f(f2bf(silu(g[j]))) * u[j];
+  for (int j = 0; j < 8; ++j) o[j] = swiglu_elem(g[j], u[j]);
   reinterpret_cast<uint4*>(h)[t] = pack8(o);
 }
 

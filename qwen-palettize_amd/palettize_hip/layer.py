@@ -329,9 +329,15 @@ class DenseDecoderLayer(nn.Module):
         q, k = apply_rope(q, cos, sin), apply_rope(k, cos, sin)
         hs = hs + F.linear(attention(q, k, v, cfg.heads, cfg.kv_heads), self.o_proj)
         x = self.post_attention_layernorm(hs)
-        g = F.linear(x, self.gate_proj)
-        u = F.linear(x, self.up_proj)
-        return hs + F.linear(SwiGLUFunction.apply(g, u), self.down_proj)
+        if x.is_cuda and cfg.intermediate % 128 == 0:
+            # gate and up in one GEMM with the SwiGLU in its epilogue (never stored)
+            if getattr(self, "_gate_up", None) is None:
+                self._gate_up = ops.swiglu_weight(self.gate_proj, self.up_proj)
+            h = ops.linear_fwd_dense_swiglu(x.reshape(-1, x.shape[-1]), self._gate_up)
+            h = h.view(B, S, -1)
+        else:
+            h = SwiGLUFunction.apply(F.linear(x, self.gate_proj), F.linear(x, self.up_proj))
+        return hs + F.linear(h, self.down_proj)
 
 
 # ---- loss / schedule / optimizer ----------------------------------------------------------------

@@ -171,6 +171,29 @@ def bias_grad(grad_y):
 
 
 # ---- dense linear -----------------------------------------------------------------------
+def swiglu_weight(w_gate, w_up):
+    """[N, K] gate and up weights -> the [2N, K] interleave of plz_linear_fwd_dense_swiglu
+    (128 gate rows, the 128 matching up rows, ...). N must be a multiple of 128."""
+    N, K = w_gate.shape
+    if w_up.shape != (N, K) or N % 128:
+        raise ValueError("gate / up must be the same [N, K] with N a multiple of 128")
+    return torch.stack([w_gate.reshape(N // 128, 128, K), w_up.reshape(N // 128, 128, K)],
+                       dim=1).reshape(2 * N, K).contiguous()
+
+
+def linear_fwd_dense_swiglu(x, w_gate_up):
+    """h = silu(x Wg^T) * (x Wu^T) in one GEMM (w_gate_up from swiglu_weight)."""
+    _need(x, "x", torch.bfloat16, 2)
+    _need(w_gate_up, "w_gate_up", torch.bfloat16, 2)
+    M, K = x.shape
+    N = w_gate_up.shape[0] // 2
+    if w_gate_up.shape[1] != K:
+        raise ValueError("x / w shape mismatch")
+    h = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
+    call("plz_linear_fwd_dense_swiglu", _ptr(x), _ptr(w_gate_up), _ptr(h), M, N, K, _stream(x))
+    return h
+
+
 def linear_fwd_dense(x, w, bias=None, lora_t=None, lora_b=None):
     _need(x, "x", torch.bfloat16, 2)
     _need(w, "w", torch.bfloat16, 2)

@@ -183,3 +183,23 @@ def test_dropin_soft_supplied_noise(dev, ste):
     assert_close(f32(ld.grad), gl.transpose(2, 1, 0), what="drop-in grad_logits (supplied noise)")
     want_gp = gp.reshape(N // GS, GS, -1, 4).sum(axis=(1, 2))
     assert_close(f32(pd.grad), want_gp, what="drop-in soft grad_palette (supplied noise)")
+
+
+@pytest.mark.parametrize("M,N,K", [(300, 256, 512), (64, 1024, 256)])
+def test_dense_swiglu_epilogue(dev, M, N, K):
+    """Gate and up in one GEMM with the SwiGLU in the epilogue: the HF bf16 formula against the
+    oracle, and bit for bit the unfused dense GEMMs + plz_swiglu_fwd (no tail split here, so
+    both accumulate every output in the same order)."""
+    x = randn_bf16(M, K, seed=51)
+    wg = randn_bf16(N, K, seed=52, std=0.05)
+    wu = randn_bf16(N, K, seed=53, std=0.05)
+    xd, wgd, wud = x.to(dev), wg.to(dev), wu.to(dev)
+    h = ops.linear_fwd_dense_swiglu(xd, ops.swiglu_weight(wgd, wud))
+    assert h.shape == (M, N)
+    g = O.bf16_round((f32(x).astype(np.float64) @ f32(wg).T).astype(np.float32))
+    u = O.bf16_round((f32(x).astype(np.float64) @ f32(wu).T).astype(np.float32))
+    want = O.bf16_round(O.silu(g).astype(np.float32)) * u
+    assert_close(f32(h), want, what="fused SwiGLU")
+    assert ops.query("plz_linear_fwd_dense_workspace", M, N, K) == 0
+    ref = ops.swiglu_fwd(ops.linear_fwd_dense(xd, wgd), ops.linear_fwd_dense(xd, wud))
+    assert torch.equal(h, ref)
