@@ -103,3 +103,33 @@ def test_layer_update_matches_adamw_clip_clamp(dev):
         want = m.detach().to(p.dtype).float().numpy()
         got = f32(p)
         assert np.allclose(got, want, rtol=1e-2, atol=1e-5), (p.shape, np.abs(got - want).max())
+
+
+def test_layer_step_full_config_deterministic_and_training(dev):
+    """The full Qwen-4B-shaped step (hidden 2560, 32/8 heads x 128, SwiGLU 9728, 32 x 512
+    tokens): repeating forward+backward on the same state and the same Gumbel draw (each
+    forward advances the linears' noise counters, as the reference's per-forward seed does, so
+    they are rewound) gives the same loss and gradients bit for bit -- every kernel on the path
+    is deterministic -- every gradient is finite, and the loss falls over a few optimizer
+    steps."""
+    cfg = layer.LayerConfig()
+    tr = layer.LayerTrainer(cfg, dev, seed=0, lora_b_std=0.01)
+    hs = torch.randn(32, 512, cfg.hidden, generator=torch.Generator().manual_seed(7))
+    hs = hs.to(torch.bfloat16).to(dev)
+    params = tr.logits + tr.others
+    counters = [lin.noise_counter for lin in tr.student.linears()]
+    loss_a, _ = tr.forward_backward(hs)
+    grads_a = [p.grad.clone() for p in params]
+    for lin, c in zip(tr.student.linears(), counters):
+        lin.noise_counter = c
+    loss_b, _ = tr.forward_backward(hs)
+    assert torch.equal(loss_a, loss_b)
+    for p, g in zip(params, grads_a):
+        assert torch.equal(p.grad, g)
+        assert bool(torch.isfinite(g).all())
+    losses = [float(loss_a)]
+    for _ in range(3):
+        tr.update()
+        loss, _ = tr.forward_backward(hs)
+        losses.append(float(loss))
+    assert all(np.isfinite(losses)) and losses[-1] < losses[0], losses
