@@ -217,10 +217,11 @@ __global__ __launch_bounds__(NT, 2) void attn_fwd_kernel(const uint16_t* __restr
 #pragma unroll
   for (int db = 0; db < D / 32; ++db)
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const int d = 32 * db + 8 * (e >> 2) + 4 * h2 + (e & 3);
-      *reinterpret_cast<__attribute__((address_space(3))) uint16_t*>(st_ + ql * 272 + d * 2) =
-          (uint16_t)f2bf(ot[db][e] * inv);
+    for (int j = 0; j < 4; ++j) {  // accumulator values 4j..4j+3: 4 consecutive d, one 8-B store
+      const int d = 32 * db + 8 * j + 4 * h2;
+      *reinterpret_cast<__attribute__((address_space(3))) u32x2*>(st_ + ql * 272 + d * 2) =
+          u32x2{f2bf2(ot[db][4 * j] * inv, ot[db][4 * j + 1] * inv),
+                f2bf2(ot[db][4 * j + 2] * inv, ot[db][4 * j + 3] * inv)};
     }
   if (h2 == 0) lse[((int64_t)b * Hq + h) * S + qrow] = (mrun + log2f(lrun)) * 0.69314718055994531f;
   __syncthreads();
@@ -286,10 +287,11 @@ __device__ __forceinline__ void store_rows_t(const f32x16 (&acc)[D / 32], float 
 #pragma unroll
   for (int db = 0; db < D / 32; ++db)
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const int d = 32 * db + 8 * (e >> 2) + 4 * h2 + (e & 3);
-      *reinterpret_cast<__attribute__((address_space(3))) uint16_t*>(st + ql * 272 + d * 2) =
-          (uint16_t)f2bf(acc[db][e] * mul);
+    for (int j = 0; j < 4; ++j) {  // accumulator values 4j..4j+3: 4 consecutive d, one 8-B store
+      const int d = 32 * db + 8 * j + 4 * h2;
+      *reinterpret_cast<__attribute__((address_space(3))) u32x2*>(st + ql * 272 + d * 2) =
+          u32x2{f2bf2(acc[db][4 * j] * mul, acc[db][4 * j + 1] * mul),
+                f2bf2(acc[db][4 * j + 2] * mul, acc[db][4 * j + 3] * mul)};
     }
   __builtin_amdgcn_s_waitcnt(0);
   __builtin_amdgcn_wave_barrier();
