@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define PLZ_ABI_VERSION 5
+#define PLZ_ABI_VERSION 6
 
 /* status codes */
 #define PLZ_OK 0
@@ -256,16 +256,19 @@ int plz_gemv_pack_indices(const int32_t* packed, int32_t* packed_items, int64_t 
 int plz_lut_gemv_decode(const uint16_t* x, const int32_t* packed_items,
                         const uint32_t* palette_items, uint16_t* y, int64_t M, int64_t N,
                         int64_t K, void* stream);
-/* Fills block_begin and cost_begin of n host descriptors and returns the total number of
- * 128-row work items (or a negative status). A descriptor with N > 0 needs K > 0. */
-int64_t plz_gemv_plan(plz_gemv_desc* descs, int n, int M);
 /* Weight layout of a grouped launch: PLZ_GEMV_NATIVE reads every descriptor's `packed` and
- * `palette`, PLZ_GEMV_DECODE its `packed_items` and `palette_items`. A descriptor whose array
- * for the chosen layout is NULL reads zeros there (no fault). */
+ * `palette`, PLZ_GEMV_DECODE its `packed_items` and `palette_items`. */
 #define PLZ_GEMV_NATIVE 0
 #define PLZ_GEMV_DECODE 1
+/* Fills block_begin and cost_begin of n host descriptors for a launch in `layout` and returns
+ * the total number of 128-row work items (or a negative status). A descriptor with N > 0
+ * needs K > 0, and a non-empty one must hold the two arrays the layout streams (non-null):
+ * a plan for the decode layout over a descriptor without decode arrays fails with
+ * -PLZ_EINVAL. */
+int64_t plz_gemv_plan(plz_gemv_desc* descs, int n, int M, int layout);
 /* Runs n independent GEMVs (all with the same M) in one launch. descs_device is a copy of
- * the planned descriptors in device memory; total_blocks is plz_gemv_plan's result. */
+ * the planned descriptors in device memory; total_blocks is plz_gemv_plan's result, and
+ * `layout` must be the layout the table was planned for. */
 int plz_lut_gemv_grouped(const plz_gemv_desc* descs_device, int n, int64_t total_blocks, int M,
                          int layout, void* stream);
 
@@ -368,8 +371,9 @@ int plz_attn_bwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, const 
                  int heads, int kv_heads, int head_dim, float scale, void* stream);
 /* Distillation loss of train_qwen.py:229-249 (compute_loss, '1-cos+norm_mse'):
  * loss = wc mean_rows(1 - cos(s_r, t_r)) + wm mean((s-t)^2) / max(mean(t^2), 1e-6), weights
- * normalised to sum 1; student/teacher bf16 [rows, dim]. out4 (device fp32 [4]) receives
- * {loss, l_cos, t_var, l_mse}; the workspace (per-row sums) is reused by the backward, which
+ * normalised to sum 1, cos = s.t / (max(|s|, eps) max(|t|, eps)) with each norm clamped on its
+ * own as torch's F.cosine_similarity does; student/teacher bf16 [rows, dim]. out4 (device
+ * fp32 [4]) receives {loss, l_cos, t_var, l_mse}; the workspace (per-row sums) is reused by the backward, which
  * writes grad_student = grad_loss[0] * d loss / d student (bf16). */
 size_t plz_distill_loss_workspace(int64_t rows);
 int plz_distill_loss_fwd(const uint16_t* student, const uint16_t* teacher, float w_cos,

@@ -524,9 +524,13 @@ int plz_gemv_pack_palettes(const float* palette, uint32_t* palette_items, int64_
   return check_launch("plz_gemv_pack_palettes");
 }
 
-int64_t plz_gemv_plan(plz_gemv_desc* descs, int n, int M) {
+int64_t plz_gemv_plan(plz_gemv_desc* descs, int n, int M, int layout) {
   if (n < 0 || !descs || M < 1 || M > 16) {
     set_error("plz_gemv_plan: need n >= 0, non-null descriptors and M in [1, 16]");
+    return -PLZ_EINVAL;
+  }
+  if (layout != PLZ_GEMV_NATIVE && layout != PLZ_GEMV_DECODE) {
+    set_error("plz_gemv_plan: unknown index layout %d", layout);
     return -PLZ_EINVAL;
   }
   int64_t items = 0, cost = 0;
@@ -535,6 +539,19 @@ int64_t plz_gemv_plan(plz_gemv_desc* descs, int n, int M) {
     if (rc) return -rc;
     if (descs[i].N > 0 && descs[i].K == 0) {
       set_error("plz_gemv_plan: descriptor %d has K = 0", i);
+      return -PLZ_EINVAL;
+    }
+    // every non-empty linear must hold the arrays the chosen layout streams
+    const bool nonempty = descs[i].N > 0 && descs[i].K > 0;
+    if (nonempty && layout == PLZ_GEMV_NATIVE && (!descs[i].packed || !descs[i].palette)) {
+      set_error("plz_gemv_plan: descriptor %d has a null packed or palette array (native "
+                "layout)", i);
+      return -PLZ_EINVAL;
+    }
+    if (nonempty && layout == PLZ_GEMV_DECODE &&
+        (!descs[i].packed_items || !descs[i].palette_items)) {
+      set_error("plz_gemv_plan: descriptor %d has a null packed_items or palette_items array "
+                "(decode layout)", i);
       return -PLZ_EINVAL;
     }
     descs[i].block_begin = items;

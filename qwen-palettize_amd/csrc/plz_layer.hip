@@ -13,7 +13,7 @@
 // bit for bit.
 //
 // The loss is train_qwen.py:229-249 compute_loss ('1-cos+norm_mse', weights normalised):
-//   l_cos = mean_rows(1 - cos(s_r, t_r)),  cos = s.t / max(|s| |t|, eps)
+//   l_cos = mean_rows(1 - cos(s_r, t_r)),  cos = s.t / (max(|s|, eps) max(|t|, eps))
 //   l_mse = mean((s - t)^2) / max(mean(t^2), 1e-6),  loss = wc l_cos + wm l_mse
 // over the student and teacher outputs s, t bf16 [rows, D], in fp32. loss_rows_kernel makes one
 // pass over s and t for the per-row sums, loss_final_kernel reduces them in a fixed order, and
@@ -126,7 +126,7 @@ __global__ __launch_bounds__(1024) void loss_final_kernel(const float4* __restri
   float c = 0.f, tt = 0.f, dd = 0.f;
   for (int64_t r = threadIdx.x; r < rows; r += 1024) {
     const float4 v = stats[r];
-    c += 1.f - v.x / fmaxf(sqrtf(v.y) * sqrtf(v.z), eps);
+    c += 1.f - v.x / (fmaxf(sqrtf(v.y), eps) * fmaxf(sqrtf(v.z), eps));
     tt += v.z;
     dd += v.w;
   }
@@ -153,8 +153,11 @@ __global__ __launch_bounds__(1024) void loss_final_kernel(const float4* __restri
   }
 }
 
-// grad_s = go * [ -wc/T * d cos_r/ds  +  wm * 2 (s - t) / (T D t_var) ],
-// d cos_r/ds = t / (|s||t|) - cos_r s / |s|^2  (when |s||t| > eps; else t / eps).
+// grad_s = go * [ -wc/T * d cos_r/ds  +  wm * 2 (s - t) / (T D t_var) ].
+// cos_r = s.t / (max(|s|, eps) max(|t|, eps)), each norm clamped on its own; the clamp passes
+// no gradient and the norm's own gradient s / |s| is kept even where the clamp is active (the
+// in-place no-grad clamp of torch's cosine_similarity, which train_qwen.py:234 calls):
+// d cos_r/ds = t / (ns' nt') - (s.t) s / (ns'^2 nt' |s|), ns' = max(|s|, eps), zero at s = 0.
 __global__ __launch_bounds__(256) void loss_bwd_kernel(const uint16_t* __restrict__ s,
                                                        const uint16_t* __restrict__ t,
                                                        const float4* __restrict__ stats,
@@ -168,16 +171,10 @@ __global__ __launch_bounds__(256) void loss_bwd_kernel(const uint16_t* __restric
   const float4 v = stats[row];
   const float go = grad_loss[0], t_var = scal[2];
   const float T = (float)rows;
-  const float ns = sqrtf(v.y), nt = sqrtf(v.z), den = ns * nt;
-  float ca, cb;  // d cos/ds = ca * t + cb * s
-  if (den > eps) {
-    const float cosr = v.x / den;
-    ca = 1.f / den;
-    cb = -cosr / (ns * ns);
-  } else {
-    ca = 1.f / eps;
-    cb = 0.f;
-  }
+  const float ns = sqrtf(v.y), nsc = fmaxf(ns, eps), ntc = fmaxf(sqrtf(v.z), eps);
+  // d cos/ds = ca * t + cb * s
+  const float ca = 1.f / (nsc * ntc);
+  const float cb = ns > 0.f ? -v.x / (nsc * nsc * ntc * ns) : 0.f;
   const float kc = -go * wc / T;
   const float km = go * wm * 2.f / (T * (float)D * t_var);
   const float a = kc * ca - km, b = kc * cb + km;  // grad = a t + b s

@@ -85,7 +85,7 @@ SIGNATURES: dict[str, tuple] = {
     "plz_gemv_packed_items_bytes": (sz, [i64, i64]),
     "plz_gemv_pack_indices": (i32, [p, p, i64, i64, p]),
     "plz_lut_gemv_decode": (i32, [p, p, p, p, i64, i64, i64, p]),
-    "plz_gemv_plan": (i64, [C.POINTER(GemvDesc), i32, i32]),
+    "plz_gemv_plan": (i64, [C.POINTER(GemvDesc), i32, i32, i32]),
     "plz_lut_gemv_grouped": (i32, [p, i32, i64, i32, i32, p]),
     "plz_idx2_to_packed": (i32, [p, p, i64, i64, p]),
     "plz_packed_to_idx2": (i32, [p, p, i64, i64, p]),

@@ -24,6 +24,7 @@ gradient is summed back over the expansion. K is zero-padded to a multiple of 25
 """
 from __future__ import annotations
 
+import weakref
 from collections import OrderedDict
 
 import torch
@@ -34,50 +35,94 @@ from . import ops
 from ._lib import PLZ_W_HARD_NOISY, PLZ_W_SOFT
 
 GROUP_SIZE = 256
-_PACK_CACHE: "OrderedDict[tuple, Tensor]" = OrderedDict()
-_PACK_CACHE_SIZE = 64
 
 
 def _pad_k(K: int) -> int:
     return (K + 255) // 256 * 256
 
 
-def packed_from_reference(indices: Tensor, pre_transposed: bool = False) -> Tensor:
-    """(K, N) int8/uint8/int64 indices (or (N, K) when pre_transposed) -> native packed
-    int32 [N, Kp/16]. Frozen index buffers are converted once and cached by identity."""
-    key = (indices.data_ptr(), indices._version, tuple(indices.shape), str(indices.device),
-           bool(pre_transposed))
-    hit = _PACK_CACHE.get(key)
-    if hit is not None:
-        _PACK_CACHE.move_to_end(key)
-        return hit
-    nk = indices if pre_transposed else indices.t()
-    N, K = nk.shape
-    Kp = _pad_k(K)
-    idx = nk.to(torch.uint8)
-    if Kp != K:
-        idx = F.pad(idx, (0, Kp - K))
-    packed = ops.pack_indices(idx.contiguous())
-    _PACK_CACHE[key] = packed
-    if len(_PACK_CACHE) > _PACK_CACHE_SIZE:
-        _PACK_CACHE.popitem(last=False)
-    return packed
+class _PackCache:
+    """Packed indices of frozen index tensors, reused while the source tensor lives unchanged.
+
+    An entry holds a weak reference to the tensor it was made from and that tensor's version
+    counter. A lookup hits only when the entry's tensor is the very object passed in (a new
+    tensor that the allocator placed at a freed tensor's address never matches: the weak
+    reference of the old one is dead) and nothing has written to it since."""
+
+    def __init__(self, size: int = 64):
+        self.size = size
+        self._d: "OrderedDict[tuple, tuple]" = OrderedDict()
+
+    def get(self, t: Tensor, make):
+        key = (t.data_ptr(), tuple(t.shape), tuple(t.stride()), str(t.device))
+        e = self._d.get(key)
+        if e is not None and e[0]() is t and e[1] == t._version:
+            self._d.move_to_end(key)
+            return e[2]
+        packed = make()
+        self._d[key] = (weakref.ref(t), t._version, packed)
+        self._d.move_to_end(key)
+        while len(self._d) > self.size:
+            self._d.popitem(last=False)
+        return packed
+
+    def clear(self):
+        self._d.clear()
+
+
+_PACK_CACHE = _PackCache()
+
+
+def packed_from_reference(indices: Tensor) -> Tensor:
+    """(K, N) int8/uint8/int64 indices -> native packed int32 [N, Kp/16] of their transpose,
+    K zero-padded to a multiple of 256. Frozen index buffers are packed once (see _PackCache)."""
+
+    def make():
+        N, K = indices.shape[1], indices.shape[0]
+        Kp = _pad_k(K)
+        idx = indices.t().to(torch.uint8)
+        if Kp != K:
+            idx = F.pad(idx, (0, Kp - K))
+        return ops.pack_indices(idx.contiguous())
+
+    return _PACK_CACHE.get(indices, make)
+
+
+def _groups_used(rows: int, group_size: int) -> int:
+    return -(-rows // group_size)
 
 
 def palette_from_reference(palette: Tensor, N: int, K: int, group_size: int) -> Tensor:
-    """(G, 4) reference palette -> native fp32 [N, Kp/256, 4] (exact for bf16/fp16 input)."""
+    """(G, 4) reference palette -> native fp32 [N, Kp/256, 4] (exact for bf16/fp16 input).
+
+    Row n takes group n // group_size, as the reference's flat gather does
+    (qwen_model.py:97-102: palette.reshape(-1)[(n // GS) * 4 + idx]). G may exceed the
+    ceil(N / group_size) groups the rows use; the last group may be partial."""
     G = palette.shape[0]
-    if N % group_size or N // group_size != G:
-        raise ValueError(f"G mismatch: N/group_size={N // group_size} vs palette.size(0)={G}")
+    need = _groups_used(N, group_size)
+    if palette.dim() != 2 or palette.shape[1] != 4:
+        raise ValueError("palette must be (G, 4)")
+    if G < need:
+        raise ValueError(f"G mismatch: {N} rows in groups of {group_size} need {need} palettes, "
+                         f"palette has {G}")
     kg = _pad_k(K) // 256
-    per_row = palette.float().repeat_interleave(group_size, dim=0)  # [N, 4]
+    per_row = palette[:need].float().repeat_interleave(group_size, dim=0)[:N]  # [N, 4]
     return per_row[:, None, :].expand(N, kg, 4).contiguous()
 
 
-def palette_grad_to_reference(grad: Tensor, group_size: int) -> Tensor:
-    """native [N, KG, 4] -> reference (G, 4): sum over the rows of a group and over KG."""
-    N, kg, _ = grad.shape
-    return grad.view(N // group_size, group_size, kg, 4).sum(dim=(1, 2))
+def palette_grad_to_reference(grad: Tensor, group_size: int, n_groups: int | None = None) -> Tensor:
+    """native [N, KG, 4] -> reference (G, 4): sum over the rows of a group and over KG; groups
+    no row uses (G above ceil(N / group_size)) get zero."""
+    N = grad.shape[0]
+    need = _groups_used(N, group_size)
+    G = need if n_groups is None else int(n_groups)
+    per_row = grad.sum(dim=1)  # [N, 4]
+    if need * group_size != N:
+        per_row = F.pad(per_row, (0, 0, 0, need * group_size - N))
+    out = per_row.view(need, group_size, 4).sum(dim=1)
+    if G > need:
+        out = F.pad(out, (0, 0, 0, G - need))
+    return out
 
 
 def _prep_x(x: Tensor, K: int) -> Tensor:
@@ -107,7 +152,7 @@ class CUDAFusedLUTLinear(torch.autograd.Function):
         b = None if bias is None else bias.to(torch.bfloat16).contiguous()
         y = ops.lut_linear_fwd(xp, packed, pal, b)
         ctx.save_for_backward(xp, packed, pal)
-        ctx.group_size, ctx.K = group_size, K
+        ctx.group_size, ctx.K, ctx.n_groups = group_size, K, palette.shape[0]
         ctx.pal_dtype = palette.dtype
         ctx.bias_requires_grad = bias is not None and bias.requires_grad
         ctx.bias_dtype = None if bias is None else bias.dtype
@@ -122,7 +167,7 @@ class CUDAFusedLUTLinear(torch.autograd.Function):
             grad_x = ops.lut_linear_bwd_x(grad_y, packed, pal)[:, : ctx.K].contiguous()
         if ctx.needs_input_grad[1]:
             g = ops.lut_linear_bwd_palette(xp, grad_y, packed)
-            grad_pal = palette_grad_to_reference(g, ctx.group_size).to(ctx.pal_dtype)
+            grad_pal = palette_grad_to_reference(g, ctx.group_size, ctx.n_groups).to(ctx.pal_dtype)
         if ctx.bias_requires_grad:
             grad_bias = ops.bias_grad(grad_y).to(ctx.bias_dtype)
         return grad_x, grad_pal, None, grad_bias, None
@@ -132,6 +177,68 @@ def fused_lut_linear(x: Tensor, palette: Tensor, indices: Tensor, bias: Tensor |
                      group_size: int = GROUP_SIZE) -> Tensor:
     """Functional interface -- supports autograd."""
     return CUDAFusedLUTLinear.apply(x, palette, indices, bias, group_size)
+
+
+class PreTransposedLUTLinear(torch.autograd.Function):
+    """The hard forward of PalettizedLinear(pre_transposed=True) (qwen_model.py:183-190): indices
+    are (out, in) and y = x @ W^T + bias with W^T[o, i] = palette[i // group_size][indices[o, i]],
+    so the palette groups run along the input dimension.
+
+    The kernels take the weight in its native orientation as W'[i, o] = W^T[o, i] (N' = in rows,
+    K' = out columns, one palette per row i, K' zero-padded to a multiple of 256): y = x W' is
+    the grad_x GEMM of W', grad_x = grad_y W'^T its forward GEMM, and dW' = x^T grad_y its
+    grad_palette GEMM with x and grad_y in swapped roles. Any group size works this way.
+    backward -> (grad_x, grad_palette (G, 4), None, grad_bias, None)."""
+
+    @staticmethod
+    def forward(ctx, x, palette, indices, bias, group_size):
+        if x.dtype != torch.bfloat16:
+            raise TypeError("x must be bf16 cuda")
+        if indices.dim() != 2:
+            raise ValueError("indices must be (out, in)")
+        out_f, in_f = indices.shape
+        if x.shape[-1] != in_f:
+            raise ValueError(f"x has {x.shape[-1]} columns, indices (out, in) have in={in_f}")
+        if in_f % 8:
+            raise ValueError(f"in_features ({in_f}) must be a multiple of 8")
+        packed = packed_from_reference(indices)                  # [in, Kp'/16]
+        pal = palette_from_reference(palette, in_f, out_f, group_size)  # [in, Kp'/256, 4]
+        xc = x.contiguous()
+        y = ops.lut_linear_bwd_x(xc, packed, pal)
+        if y.shape[1] != out_f:
+            y = y[:, :out_f].contiguous()
+        if bias is not None:
+            y = y + bias.to(y.dtype)
+        ctx.save_for_backward(xc, packed, pal)
+        ctx.group_size, ctx.out_f, ctx.n_groups = group_size, out_f, palette.shape[0]
+        ctx.pal_dtype = palette.dtype
+        ctx.bias_requires_grad = bias is not None and bias.requires_grad
+        ctx.bias_dtype = None if bias is None else bias.dtype
+        return y
+
+    @staticmethod
+    def backward(ctx, grad_y):
+        xc, packed, pal = ctx.saved_tensors
+        gy = grad_y.contiguous()
+        Kp = _pad_k(ctx.out_f)
+        gyp = F.pad(gy, (0, Kp - ctx.out_f)) if Kp != ctx.out_f else gy
+        grad_x = grad_pal = grad_bias = None
+        if ctx.needs_input_grad[0]:
+            grad_x = ops.lut_linear_fwd(gyp, packed, pal)
+        if ctx.needs_input_grad[1]:
+            g = ops.lut_linear_bwd_palette(gyp, xc, packed)      # [in, Kp'/256, 4]
+            grad_pal = palette_grad_to_reference(g, ctx.group_size, ctx.n_groups).to(ctx.pal_dtype)
+        if ctx.bias_requires_grad:
+            grad_bias = ops.bias_grad(gy).to(ctx.bias_dtype)
+        return grad_x, grad_pal, None, grad_bias, None
+
+
+def fused_lut_linear_pre_transposed(x: Tensor, palette: Tensor, indices: Tensor,
+                                    bias: Tensor | None = None,
+                                    group_size: int = GROUP_SIZE) -> Tensor:
+    """Hard forward of a pre-transposed PalettizedLinear (indices (out, in), palette groups
+    along the input dimension) -- supports autograd."""
+    return PreTransposedLUTLinear.apply(x, palette, indices, bias, group_size)
 
 
 # Global step counter for the Gumbel seed (one increment per soft forward), as in the
@@ -178,8 +285,6 @@ def _soft_forward(ctx, x, palette, logits, bias, group_size, tau, noise, ste):
     _, K, N = logits.shape
     if x.shape[-1] != K:
         raise ValueError(f"x K={x.shape[-1]} != logits K={K}")
-    if N % group_size or N // group_size != palette.shape[0]:
-        raise ValueError("G mismatch")
     if N % 8:
         raise ValueError(f"N ({N}) must be a multiple of 8")
     xp = _prep_x(x, K)
@@ -196,6 +301,7 @@ def _soft_forward(ctx, x, palette, logits, bias, group_size, tau, noise, ste):
     y = ops.linear_fwd_dense(xp, w, b)
     ctx.save_for_backward(xp, pal, lg, noise, w)
     ctx.group_size, ctx.K, ctx.tau = group_size, K, float(tau)
+    ctx.n_groups = palette.shape[0]
     ctx.pal_dtype, ctx.logits_dtype = palette.dtype, logits.dtype
     ctx.has_bias = bias is not None
     ctx.bias_dtype = None if bias is None else bias.dtype
@@ -214,7 +320,7 @@ def _soft_backward(ctx, grad_y):
         if ctx.needs_input_grad[2]:
             grad_logits = gl[:, : ctx.K, :].permute(2, 1, 0).contiguous().to(ctx.logits_dtype)
         if ctx.needs_input_grad[1]:
-            grad_pal = palette_grad_to_reference(gp, ctx.group_size).to(ctx.pal_dtype)
+            grad_pal = palette_grad_to_reference(gp, ctx.group_size, ctx.n_groups).to(ctx.pal_dtype)
     if ctx.has_bias and ctx.needs_input_grad[3]:
         grad_bias = ops.bias_grad(grad_y).to(ctx.bias_dtype)
     return grad_x, grad_pal, grad_logits, grad_bias

@@ -26,10 +26,14 @@ def _stream(t: torch.Tensor) -> int:
     return torch.cuda.current_stream(t.device).cuda_stream
 
 
+def _on_gpu(t: torch.Tensor) -> bool:
+    return t.is_cuda
+
+
 def _need(t: torch.Tensor, name: str, dtype=None, ndim=None) -> torch.Tensor:
     if not isinstance(t, torch.Tensor):
         raise TypeError(f"{name} must be a tensor")
-    if not t.is_cuda:
+    if not _on_gpu(t):
         raise RuntimeError(f"{name} must be a GPU tensor (palettize_hip has no CPU path)")
     if dtype is not None and t.dtype != dtype:
         raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
@@ -55,6 +59,16 @@ def _opt_workspace(nbytes: int, device):
 
 def _numel(t) -> int:
     return 0 if t is None else t.numel()
+
+
+def _bias(bias, N: int):
+    """bias must be None or bf16 [N]: the C ABI takes no bias length, the epilogue reads N."""
+    if bias is None:
+        return None
+    _need(bias, "bias", torch.bfloat16, 1)
+    if bias.numel() != N:
+        raise ValueError(f"bias has {bias.numel()} elements, the output has N={N} columns")
+    return bias
 
 
 # ---- formats ------------------------------------------------------------------------
@@ -112,8 +126,7 @@ def lut_linear_fwd(x, packed, palette, bias=None, lora_t=None, lora_b=None):
     M = x.shape[0]
     if x.shape[1] != K:
         raise ValueError(f"x has {x.shape[1]} columns, W has K={K}")
-    if bias is not None:
-        _need(bias, "bias", torch.bfloat16, 1)
+    _bias(bias, N)
     rank = _lora_pair(lora_t, lora_b, "lora_t", "lora_b", M, N)
     y = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
     ws = _opt_workspace(query("plz_lut_linear_fwd_workspace", M, N, K), x.device)
@@ -201,8 +214,7 @@ def linear_fwd_dense(x, w, bias=None, lora_t=None, lora_b=None):
     N = w.shape[0]
     if w.shape[1] != K:
         raise ValueError("x / w shape mismatch")
-    if bias is not None:
-        _need(bias, "bias", torch.bfloat16, 1)
+    _bias(bias, N)
     rank = _lora_pair(lora_t, lora_b, "lora_t", "lora_b", M, N)
     y = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
     ws = _opt_workspace(query("plz_linear_fwd_dense_workspace", M, N, K), x.device)
@@ -219,10 +231,14 @@ def linear_bwd_x_dense(grad_y, w, lora_gt=None, lora_a=None):
     if w.shape[0] != N:
         raise ValueError("grad_y / w shape mismatch")
     rank = 0
-    if lora_gt is not None:
+    if lora_gt is not None or lora_a is not None:
+        if lora_gt is None or lora_a is None:
+            raise ValueError("lora_gt and lora_a must be given together")
         _need(lora_gt, "lora_gt", torch.bfloat16, 2)
         _need(lora_a, "lora_a", torch.bfloat16, 2)
         rank = lora_gt.shape[1]
+        if lora_gt.shape[0] != M or tuple(lora_a.shape) != (rank, K):
+            raise ValueError("lora_gt / lora_a shape mismatch")
     gx = torch.empty((M, K), dtype=torch.bfloat16, device=grad_y.device)
     ws = _opt_workspace(query("plz_linear_bwd_x_dense_workspace", M, N, K), grad_y.device)
     call("plz_linear_bwd_x_dense", _ptr(grad_y), _ptr(w), _ptr(lora_gt), _ptr(lora_a), rank,
@@ -472,7 +488,8 @@ class GemvGroup:
                                      pre.data_ptr() if pre is not None else None,
                                      pri.data_ptr() if pri is not None else None)
         self._keep = items
-        total = _lib.lib().plz_gemv_plan(descs, len(items), self.M)
+        self.layout = _lib.PLZ_GEMV_DECODE if prepack else _lib.PLZ_GEMV_NATIVE
+        total = _lib.lib().plz_gemv_plan(descs, len(items), self.M, self.layout)
         if total < 0:
             raise _lib.PalettizeError(
                 "plz_gemv_plan failed: " + _lib.lib().plz_last_error().decode())
@@ -481,7 +498,6 @@ class GemvGroup:
         host = torch.frombuffer(bytearray(raw), dtype=torch.uint8)
         self.table = host.to(self.device)
         self.n = len(items)
-        self.layout = _lib.PLZ_GEMV_DECODE if prepack else _lib.PLZ_GEMV_NATIVE
 
     def run(self):
         call("plz_lut_gemv_grouped", self.table.data_ptr(), self.n, self.total_blocks, self.M,
@@ -490,10 +506,16 @@ class GemvGroup:
 
 
 # ---- RMSNorm / SwiGLU -----------------------------------------------------------------------
+def _norm_weight(weight, cols: int):
+    _need(weight, "weight", torch.bfloat16, 1)
+    if weight.numel() != cols:
+        raise ValueError(f"weight has {weight.numel()} elements, rows have {cols} columns")
+
+
 def rmsnorm_fwd(x, weight, eps: float):
     _need(x, "x", torch.bfloat16, 2)
-    _need(weight, "weight", torch.bfloat16, 1)
     rows, cols = x.shape
+    _norm_weight(weight, cols)
     y = torch.empty_like(x)
     rstd = torch.empty((rows,), dtype=torch.float32, device=x.device)
     call("plz_rmsnorm_fwd", _ptr(x), _ptr(weight), _ptr(y), _ptr(rstd), rows, cols, float(eps),
@@ -505,6 +527,10 @@ def rmsnorm_bwd(x, weight, rstd, grad_y):
     _need(x, "x", torch.bfloat16, 2)
     _need(grad_y, "grad_y", torch.bfloat16, 2)
     rows, cols = x.shape
+    _norm_weight(weight, cols)
+    _need(rstd, "rstd", torch.float32, 1)
+    if rstd.numel() != rows or grad_y.shape != x.shape:
+        raise ValueError("rstd must be [rows] and grad_y the shape of x")
     gx = torch.empty_like(x)
     gw = torch.empty((cols,), dtype=torch.float32, device=x.device)
     ws = _workspace(query("plz_rmsnorm_bwd_workspace", rows, cols), x.device)

@@ -1,11 +1,13 @@
 """PalettizedLinear and QwenLoRA with the reference's constructor API and attributes
 (qwen_model.py:65-304), running on the MI355X kernels.
 
-PalettizedLinear keeps the reference's buffers and parameters -- indices (in, out) int64,
-indices_int8, _flat_idx, palette (G, 4) bf16, index_logits (4, in, out) fp16 (+-10 one-hot,
-only with use_soft_indices), tau, group_size, n_groups, palette_size, pre_transposed,
-in_features, out_features, bias -- and dispatches like qwen_model.py:147-196: soft
-(Gumbel-softmax, straight-through) in training mode with soft indices, hard otherwise.
+PalettizedLinear keeps the reference's buffers and parameters -- indices (in, out) int64
+((out, in) when pre_transposed), indices_int8, _flat_idx, palette (G, 4) bf16, index_logits
+(4, in, out) fp16 (+-10 one-hot, only with use_soft_indices), tau, group_size, n_groups,
+palette_size, pre_transposed, in_features, out_features, bias -- and dispatches like
+qwen_model.py:147-196: soft (Gumbel-softmax, straight-through) in training mode with soft
+indices, hard otherwise. Palette groups run along the stored indices' second dimension: the
+output dimension normally, the input dimension when pre_transposed (qwen_model.py:97-102).
 Both dispatch to the drop-in fused_lut_linear_cuda functions; there is no CPU fallback
 (a CPU input raises).
 """
@@ -62,9 +64,9 @@ class PalettizedLinear(nn.Module):
             y = FL.fused_lut_linear_soft(x_flat, self.palette, self.index_logits, self.bias,
                                          self.group_size, self.tau)
         elif self.pre_transposed:
-            # indices are (out, in): transpose once to the reference's (in, out) orientation
-            y = FL.fused_lut_linear(x_flat, self.palette, self.indices_int8.t().contiguous(),
-                                    self.bias, self.group_size)
+            # indices (out, in), palette groups along the input dimension (qwen_model.py:187-190)
+            y = FL.fused_lut_linear_pre_transposed(x_flat, self.palette, self.indices_int8,
+                                                   self.bias, self.group_size)
         else:
             y = FL.fused_lut_linear(x_flat, self.palette, self.indices_int8, self.bias,
                                     self.group_size)
@@ -97,14 +99,17 @@ class QwenLoRA(nn.Module):
             in_dim, out_dim = base_module.in_features, base_module.out_features
         else:
             out_dim, in_dim = base_module.weight.shape
-        device = base_module.palette.device if hasattr(base_module, "palette") else \
-            next(base_module.parameters()).device
+        if hasattr(base_module, "weight"):
+            device = base_module.weight.device
+        elif hasattr(base_module, "palette"):
+            device = base_module.palette.device
+        else:
+            device = next(base_module.parameters()).device
         if init == "loftq" and original_weight is not None:
             with torch.no_grad():
                 if hasattr(base_module, "palette"):
-                    w_oi = self._reconstruct_base_weight(base_module).float()
-                    if not base_module.pre_transposed:
-                        w_oi = w_oi.t()
+                    # (in, out) for either orientation; the residual is taken as (out, in)
+                    w_oi = self._reconstruct_base_weight(base_module).float().t()
                 else:
                     w_oi = base_module.weight.data.float()
                 R = original_weight.float().to(w_oi.device) - w_oi
@@ -121,6 +126,9 @@ class QwenLoRA(nn.Module):
 
     @staticmethod
     def _reconstruct_base_weight(pal_module):
+        """The palettized weight as (in, out): the flat gather palette[(c // GS) * 4 + idx]
+        over the stored (rows, cols) indices, transposed back when they are (out, in)
+        (qwen_model.py:278-289)."""
         gathered = pal_module.palette.reshape(-1)[pal_module._flat_idx]
         return gathered if not pal_module.pre_transposed else gathered.T
 

@@ -36,7 +36,7 @@ def test_every_declared_symbol_is_exported(lib):
         assert hasattr(lib, n), f"{n} declared in the header but not exported"
         assert n in _lib.SIGNATURES, f"{n} has no ctypes signature"
     assert set(_lib.SIGNATURES) == set(names)
-    assert lib.plz_abi_version() == 5
+    assert lib.plz_abi_version() == 6
 
 
 def test_shape_errors_are_reported_without_touching_the_gpu(lib):
@@ -149,3 +149,74 @@ def test_gemv_decode_layout_argument_errors(lib):
     assert rc == 1 and b"[1, 16]" in lib.plz_last_error()
     rc = lib.plz_lut_gemv_grouped(None, 1, 1, 1, 7, None)
     assert rc == 1 and b"layout" in lib.plz_last_error()
+
+
+def test_gemv_plan_rejects_descriptors_without_the_layouts_arrays(lib):
+    """A plan for the decode layout over a descriptor that holds only the native arrays (or the
+    reverse) fails at plan time instead of launching a GEMV that would read zeros. Pointers are
+    never dereferenced by the plan."""
+    from palettize_hip import _lib
+    f = 4096  # stands for an aligned device address
+    native = _lib.GemvDesc(f, f, f, f, 256, 512, 0, 0, None, None)
+    decode = _lib.GemvDesc(f, None, None, f, 256, 512, 0, 0, f, f)
+    empty = _lib.GemvDesc(f, None, None, f, 0, 512, 0, 0, None, None)
+    for layout, ok, bad in ((_lib.PLZ_GEMV_NATIVE, native, decode),
+                            (_lib.PLZ_GEMV_DECODE, decode, native)):
+        descs = (_lib.GemvDesc * 2)(ok, empty)
+        assert lib.plz_gemv_plan(descs, 2, 4, layout) == 2
+        descs = (_lib.GemvDesc * 3)(ok, bad, empty)
+        assert lib.plz_gemv_plan(descs, 3, 4, layout) == -1
+        assert b"descriptor 1" in lib.plz_last_error()
+    descs = (_lib.GemvDesc * 1)(native)
+    assert lib.plz_gemv_plan(descs, 1, 4, 9) == -1 and b"layout" in lib.plz_last_error()
+
+
+@pytest.fixture
+def host_ops(monkeypatch):
+    """ops with the device check and the library stubbed out: argument checks run on CPU
+    tensors, and any call that would reach the library fails the test."""
+    from palettize_hip import ops
+
+    def no_call(name, *a):
+        raise AssertionError(f"{name} reached the library")
+
+    monkeypatch.setattr(ops, "_on_gpu", lambda t: True)
+    monkeypatch.setattr(ops, "call", no_call)
+    monkeypatch.setattr(ops, "query", lambda *a: 0)
+    return ops
+
+
+def test_bias_length_is_checked_before_the_call(host_ops):
+    ops = host_ops
+    bf = torch.bfloat16
+    x = torch.zeros(4, 256, dtype=bf)
+    packed = torch.zeros(24, 16, dtype=torch.int32)
+    pal = torch.zeros(24, 1, 4)
+    with pytest.raises(ValueError, match="bias has 16 elements"):
+        ops.lut_linear_fwd(x, packed, pal, torch.zeros(16, dtype=bf))
+    with pytest.raises(ValueError, match="bias has 25 elements"):
+        ops.linear_fwd_dense(x, torch.zeros(24, 256, dtype=bf), torch.zeros(25, dtype=bf))
+    with pytest.raises(TypeError):
+        ops.lut_linear_fwd(x, packed, pal, torch.zeros(24, dtype=torch.float32))
+    with pytest.raises(ValueError, match="lora_gt / lora_a"):
+        ops.linear_bwd_x_dense(torch.zeros(4, 24, dtype=bf), torch.zeros(24, 256, dtype=bf),
+                               torch.zeros(4, 16, dtype=bf), torch.zeros(16, 128, dtype=bf))
+    with pytest.raises(ValueError, match="together"):
+        ops.linear_bwd_x_dense(torch.zeros(4, 24, dtype=bf), torch.zeros(24, 256, dtype=bf),
+                               torch.zeros(4, 16, dtype=bf))
+
+
+def test_rmsnorm_weight_and_rstd_are_checked_before_the_call(host_ops):
+    ops = host_ops
+    bf = torch.bfloat16
+    x = torch.zeros(6, 320, dtype=bf)
+    with pytest.raises(ValueError, match="weight has 300"):
+        ops.rmsnorm_fwd(x, torch.zeros(300, dtype=bf), 1e-6)
+    with pytest.raises(TypeError):
+        ops.rmsnorm_fwd(x, torch.zeros(320), 1e-6)
+    with pytest.raises(ValueError, match="weight has 1"):
+        ops.rmsnorm_bwd(x, torch.zeros(1, dtype=bf), torch.zeros(6), x)
+    with pytest.raises(ValueError, match="rstd"):
+        ops.rmsnorm_bwd(x, torch.zeros(320, dtype=bf), torch.zeros(5), x)
+    with pytest.raises(TypeError):
+        ops.rmsnorm_bwd(x, torch.zeros(320, dtype=bf), torch.zeros(6, dtype=bf), x)

@@ -296,29 +296,3 @@ def test_tail_split_gemms(dev, M):
     # deterministic: the split sums its parts in a fixed order
     y2 = ops.lut_linear_fwd(x.to(dev), p, pl, bias.to(dev), lora_t=t, lora_b=b.to(dev))
     assert torch.equal(y, y2)
-
-
-def test_gemv_grouped_decode_missing_arrays_read_zero(dev):
-    """A decode-layout launch over a descriptor that has only the native arrays: its decode
-    arrays are NULL, so the kernel gives them an empty buffer range and the linear's output is
-    zero; the other linears of the launch are unaffected."""
-    import ctypes as C
-    from palettize_hip import _lib
-    M, shapes = 4, [(256, 512), (384, 768)]
-    items = []
-    for i, (N, K) in enumerate(shapes):
-        idx, pal = make_weight(N, K, seed=70 + i)
-        items.append((randn_bf16(M, K, seed=80 + i).to(dev), _packed(idx, dev), pal.to(dev)))
-    grp = ops.GemvGroup(items, prepack=True)
-    descs = (_lib.GemvDesc * len(items)).from_buffer_copy(bytes(grp.table.cpu().numpy()))
-    descs[1].packed_items = None
-    descs[1].palette_items = None
-    outs = [torch.full_like(y, 1.0) for y in grp.outputs]
-    for d, y in zip(descs, outs):
-        d.y = y.data_ptr()
-    table = torch.frombuffer(bytearray(bytes(descs)), dtype=torch.uint8).to(dev)
-    ops.call("plz_lut_gemv_grouped", table.data_ptr(), len(items), grp.total_blocks, M,
-             _lib.PLZ_GEMV_DECODE, torch.cuda.current_stream().cuda_stream)
-    torch.cuda.synchronize()
-    assert torch.equal(outs[0], grp.run()[0])
-    assert not bool(outs[1].any())

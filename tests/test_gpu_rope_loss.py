@@ -73,3 +73,34 @@ def test_distill_loss_identical_inputs(dev):
     assert abs(float(loss)) < 1e-6 and abs(float(l_cos)) < 1e-6
     loss.backward()
     assert float(s.grad.float().abs().max()) < 1e-6
+
+
+def test_distill_loss_near_zero_student_rows(dev):
+    """Rows whose student norm is below the cosine eps (1e-4) -- the zero-initialised
+    correction layer train_qwen.py:233 guards against -- and all-zero student rows: loss and
+    gradient follow torch's F.cosine_similarity, which clamps |s| and |t| separately."""
+    g = torch.Generator().manual_seed(11)
+    B, S, D = 2, 24, 256
+    t = torch.randn(B, S, D, generator=g).to(torch.bfloat16)
+    s = (t.float() + 0.5 * torch.randn(B, S, D, generator=g))
+    tiny = torch.zeros(B, S, dtype=torch.bool)
+    tiny[0, 3:9] = True
+    tiny[1, 17] = True
+    s[tiny] = torch.randn(int(tiny.sum()), D, generator=g) * 1e-7
+    zero = torch.zeros(B, S, dtype=torch.bool)
+    zero[1, 0:4] = True
+    s[zero] = 0.0
+    s = s.to(torch.bfloat16)
+    sr = s.clone().requires_grad_(True)
+    want, want_cos = _loss_cpu(sr, t)
+    want.backward()
+    sg = s.to(dev).requires_grad_(True)
+    loss, l_cos = layer.compute_loss(sg, t.to(dev))
+    assert abs(float(loss) - float(want)) <= 1e-5 * abs(float(want))
+    assert abs(float(l_cos) - float(want_cos)) <= 1e-5 * abs(float(want_cos))
+    loss.backward()
+    got = f32(sg.grad.cpu())
+    ref = f32(sr.grad)
+    normal = ~(tiny | zero)
+    for mask, what in ((tiny, "tiny rows"), (zero, "zero rows"), (normal, "normal rows")):
+        assert_close(got[mask.numpy()], ref[mask.numpy()], what=f"grad_student {what}")
