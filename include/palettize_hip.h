@@ -97,6 +97,19 @@ int plz_lut_linear_bwd_palette(const uint16_t* x, const uint16_t* grad_y, const 
                                float* grad_palette, void* workspace, size_t workspace_bytes,
                                int64_t M, int64_t N, int64_t K, void* stream);
 
+/* No counterpart in the reference: plz_lut_linear_bwd_palette for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). It takes no workspace and allocates nothing: the split-M partials live in a
+ * 32 MiB device array inside the library (one per GPU, held until the process ends), so
+ * N * K may be at most 268,435,456 (N x K/128 x 16 bytes per split; larger weights get
+ * PLZ_EINVAL). The split count is the workspace variant's, lowered where its partials would
+ * not fit (then the fp32 sums run in another order). Every call on a GPU shares that GPU's
+ * array: calls that overlap on one GPU (other streams, other threads) race and must be
+ * serialised by the caller. */
+int plz_lut_linear_bwd_palette_noalloc(const uint16_t* x, const uint16_t* grad_y,
+                                       const int32_t* packed, float* grad_palette, int64_t M,
+                                       int64_t N, int64_t K, void* stream);
+
 /* grad_bias fp32 [N] = sum_m grad_y[m, n]. Replaces fused_lut_linear_bwd_grad_bias_kernel
  * (fused_lut_kernel.cu:1129-1147). Any N. */
 int plz_bias_grad(const uint16_t* grad_y, float* grad_bias, int64_t M, int64_t N, void* stream);

@@ -7,6 +7,7 @@
 //                               (fused_lut_kernel.cu:1877-1924, triton_soft_backward.py:227-325)
 //   plz_linear_fwd_dense / plz_linear_bwd_x_dense   the same on a materialised bf16 W
 //                               (fused_lut_linear_cuda.py:912, 944)
+#include <mutex>
 #include <type_traits>
 
 #include "plz_gemm2.cuh"
@@ -877,6 +878,60 @@ static int palette_splits(int64_t M, int64_t N, int64_t K) {
   return pick_splits(((N + TILE - 1) / TILE) * ((K + TILE - 1) / TILE), M);
 }
 
+// The class-reduced dW GEMM over z splits of M (fp32 partials [z][N][K/128][4] in `partial`,
+// every entry written by the GEMM), then the fixed-order sum of the partials.
+static int bwd_palette(const uint16_t* x, const uint16_t* grad_y, const int32_t* packed,
+                       float* grad_palette, float* partial, int z, int64_t M, int64_t N,
+                       int64_t K, hipStream_t stream, const char* what) {
+  Args g = {};
+  g.a = grad_y; g.lda = N;   // A(i=n, r=m) = grad_y[m, n]   (Col tile)
+  g.b = x; g.ldb = K;        // B(j=k, r=m) = x[m, k]        (Col tile)
+  g.packed = packed; g.Nw = N; g.Kw = K;
+  g.I = N; g.J = K; g.R = M; g.r_split = split_len(M, z);
+  g.partial = partial;
+  g.group = 1;
+  int rc = launch<OP_COL, OP_COL, EPI_PAL>(g, z, stream, what);
+  if (rc != PLZ_OK) return rc;
+  const int64_t G = K / 256, n_out = N * G;
+  hipLaunchKernelGGL(reduce_pal_kernel, dim3((unsigned)((n_out + 255) / 256)), dim3(256), 0,
+                     stream, g.partial, grad_palette, N, G, z);
+  return check_launch(what);
+}
+
+// Scratch of plz_lut_linear_bwd_palette_noalloc: the split-M partials live in this
+// file-scope device array instead of a caller workspace, so that entry point allocates
+// nothing. Each device holds its own copy (at its own address) from the library's load on
+// that device until the process ends. In host code `pal_scratch_buf` names a host-side
+// stand-in, never device memory: kernels get the device address that hipGetSymbolAddress
+// returns for the current device, looked up once per device and kept in pal_scratch_addr.
+constexpr size_t kPalScratchBytes = (size_t)32 << 20;  // 32 MiB
+__device__ __align__(256) unsigned char pal_scratch_buf[kPalScratchBytes];
+static std::mutex pal_scratch_mu;
+static void* pal_scratch_addr[64] = {};
+
+static int pal_scratch(float** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= 64) {
+    set_error("plz_lut_linear_bwd_palette_noalloc: no current device (%s)",
+              hipGetErrorString(e));
+    return PLZ_EHIP;
+  }
+  std::lock_guard<std::mutex> lock(pal_scratch_mu);
+  if (!pal_scratch_addr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(pal_scratch_buf));
+    if (e != hipSuccess || !p) {
+      set_error("plz_lut_linear_bwd_palette_noalloc: hipGetSymbolAddress of the scratch "
+                "failed on device %d: %s", dev, hipGetErrorString(e));
+      return PLZ_EHIP;
+    }
+    pal_scratch_addr[dev] = p;
+  }
+  *out = reinterpret_cast<float*>(pal_scratch_addr[dev]);
+  return PLZ_OK;
+}
+
 // Splits of the soft backward's reduction over M. The fused epilogue needs the whole sum, so
 // an unsplit launch has one workgroup per 256x256 output tile: 40 for k/v_proj, 160 for
 // q/o_proj, 380 for the MLP shapes, i.e. whole or partial waves on 256 CUs. A split launch
@@ -1004,20 +1059,45 @@ int plz_lut_linear_bwd_palette(const uint16_t* x, const uint16_t* grad_y, const 
               workspace_bytes);
     return PLZ_EWORKSPACE;
   }
-  const int z = palette_splits(M, N, K);
-  Args g = {};
-  g.a = grad_y; g.lda = N;   // A(i=n, r=m) = grad_y[m, n]   (Col tile)
-  g.b = x; g.ldb = K;        // B(j=k, r=m) = x[m, k]        (Col tile)
-  g.packed = packed; g.Nw = N; g.Kw = K;
-  g.I = N; g.J = K; g.R = M; g.r_split = split_len(M, z);
-  g.partial = reinterpret_cast<float*>(workspace);
-  g.group = 1;
-  int rc = launch<OP_COL, OP_COL, EPI_PAL>(g, z, (hipStream_t)stream, "plz_lut_linear_bwd_palette");
-  if (rc != PLZ_OK) return rc;
-  const int64_t G = K / 256, n_out = N * G;
-  hipLaunchKernelGGL(reduce_pal_kernel, dim3((unsigned)((n_out + 255) / 256)), dim3(256), 0,
-                     (hipStream_t)stream, g.partial, grad_palette, N, G, z);
-  return check_launch("plz_lut_linear_bwd_palette/reduce");
+  return bwd_palette(x, grad_y, packed, grad_palette, reinterpret_cast<float*>(workspace),
+                     palette_splits(M, N, K), M, N, K, (hipStream_t)stream,
+                     "plz_lut_linear_bwd_palette");
+}
+
+int plz_lut_linear_bwd_palette_noalloc(const uint16_t* x, const uint16_t* grad_y,
+                                       const int32_t* packed, float* grad_palette, int64_t M,
+                                       int64_t N, int64_t K, void* stream) {
+  PLZ_REQUIRE(M >= 0 && N >= 0 && K >= 0, "plz_lut_linear_bwd_palette_noalloc: negative shape");
+  PLZ_REQUIRE(K % 256 == 0,
+              "plz_lut_linear_bwd_palette_noalloc: K (%lld) must be a multiple of 256",
+              (long long)K);
+  PLZ_REQUIRE(N % 8 == 0, "plz_lut_linear_bwd_palette_noalloc: N (%lld) must be a multiple of 8",
+              (long long)N);
+  if (N == 0 || K == 0) return PLZ_OK;
+  // the split-M partials of one split: N x K/128 class sums of 16 bytes
+  const size_t per_split = (size_t)N * (size_t)(K / 128) * 4 * sizeof(float);
+  PLZ_REQUIRE(per_split <= kPalScratchBytes,
+              "plz_lut_linear_bwd_palette_noalloc: N x K = %lld x %lld needs %zu bytes of "
+              "partials per split, above its %zu-byte scratch (N * K at most %zu); use "
+              "plz_lut_linear_bwd_palette with a workspace",
+              (long long)N, (long long)K, per_split, kPalScratchBytes, kPalScratchBytes * 8);
+  PLZ_REQUIRE(packed && grad_palette, "plz_lut_linear_bwd_palette_noalloc: null pointer");
+  if (M == 0) {
+    zero_async(grad_palette, (size_t)N * (K / 256) * 16, (hipStream_t)stream);
+    return check_launch("plz_lut_linear_bwd_palette_noalloc");
+  }
+  PLZ_REQUIRE(x && grad_y && a16(x) && a16(grad_y) && a16(packed),
+              "plz_lut_linear_bwd_palette_noalloc: x, grad_y and packed must be non-null, "
+              "16-byte aligned");
+  float* partial = nullptr;
+  if (int rc = pal_scratch(&partial)) return rc;
+  // the workspace variant's split count, lowered until its partials fit the scratch (a lower
+  // count only changes the order of the fp32 sums)
+  int z = palette_splits(M, N, K);
+  const int zfit = (int)(kPalScratchBytes / per_split);
+  z = z < zfit ? z : zfit;
+  return bwd_palette(x, grad_y, packed, grad_palette, partial, z, M, N, K, (hipStream_t)stream,
+                     "plz_lut_linear_bwd_palette_noalloc");
 }
 
 size_t plz_linear_fwd_dense_workspace(int64_t M, int64_t N, int64_t K) {

@@ -175,6 +175,28 @@ def lut_linear_bwd_palette(x, grad_y, packed):
     return out
 
 
+def lut_linear_bwd_palette_noalloc(x, grad_y, packed, out=None):
+    """lut_linear_bwd_palette through the entry point that allocates nothing (its split-M
+    partials live in a fixed device array of the library; calls that overlap on one GPU race).
+    ``out`` (fp32 [N, K/256, 4]) may be passed in so that the call allocates nothing here
+    either."""
+    _need(packed, "packed", torch.int32, 2)
+    _need(x, "x", torch.bfloat16, 2)
+    _need(grad_y, "grad_y", torch.bfloat16, 2)
+    N, K = packed.shape[0], packed.shape[1] * 16
+    M = x.shape[0]
+    if x.shape[1] != K or tuple(grad_y.shape) != (M, N):
+        raise ValueError("x / grad_y shape mismatch")
+    if out is None:
+        out = torch.empty((N, K // 256, 4), dtype=torch.float32, device=x.device)
+    _need(out, "out", torch.float32, 3)
+    if tuple(out.shape) != (N, K // 256, 4):
+        raise ValueError(f"out must be [{N}, {K // 256}, 4]")
+    call("plz_lut_linear_bwd_palette_noalloc", _ptr(x), _ptr(grad_y), _ptr(packed), _ptr(out),
+         M, N, K, _stream(x))
+    return out
+
+
 def bias_grad(grad_y):
     _need(grad_y, "grad_y", torch.bfloat16, 2)
     M, N = grad_y.shape
