@@ -9,13 +9,19 @@ trains it (train_qwen.py:993-1414, qwen_model.py:65-304):
     LoRA A [r, K] / B [N, r] (bf16), straight-through forward through W_hard;
     HIP kernels for build-W, the GEMMs and the fused soft backward;
   * RMSNorm and SwiGLU: HIP kernels (plz_rmsnorm_*, plz_swiglu_*);
-  * attention: torch scaled_dot_product_attention (causal), RoPE in torch;
+  * RoPE and causal grouped-query attention: HIP kernels (plz_rope_*, plz_attn_*; head_dim
+    128 and sequences a multiple of 128 -- other attention shapes run torch's flash /
+    memory-efficient SDPA kernels on the GPU);
   * loss: 0.5 * (1 - cos) + 0.5 * norm_mse against a dense bf16 teacher layer
-    (compute_loss, train_qwen.py:229-249);
+    (compute_loss, train_qwen.py:229-249), HIP kernels (plz_distill_loss_*); the teacher's
+    projections run on the same MFMA GEMM core (plz_linear_fwd_dense, gate/up with the SwiGLU
+    in the epilogue);
   * optimizer: AdamW (betas 0.9/0.95, eps 1e-8, wd 0) on fp32 masters of palettes, LoRA and
     logits (FP32MasterOptimizer, train_qwen.py:154-221), two-tier gradient clipping
     (logits 1.0, others 0.3; train_qwen.py:1303-1319), logits clamp +-5 tau after the step
     (train_qwen.py:1343-1348), tau schedule of train_qwen.py:1176-1192.
+Everything runs on the GPU: CPU tensors (or non-bf16 activations) raise, there is no CPU
+path.
 """
 from __future__ import annotations
 
@@ -30,6 +36,11 @@ from . import ops
 from ._lib import PLZ_W_HARD_NOISY
 from .functional import SoftLUTLinearFunction
 from .optim import FusedAdamW
+
+
+def _gpu_bf16(t, what):
+    if not (isinstance(t, torch.Tensor) and t.is_cuda and t.dtype == torch.bfloat16):
+        raise RuntimeError(f"{what} must be a bf16 GPU tensor (palettize_hip has no CPU path)")
 
 
 @dataclass
@@ -154,13 +165,6 @@ class SoftPalettizedLinear(nn.Module):
         self.noise_counter = 0
         self.mode = PLZ_W_HARD_NOISY
 
-    def next_noise(self):
-        n = self.out_features * self.in_features * 4
-        off = self.noise_counter
-        self.noise_counter += n // 4
-        return ops.gumbel_philox((self.out_features, self.in_features, 4), seed=self.noise_seed,
-                                 offset=off, device=self.index_logits.device)
-
     def next_noise_spec(self):
         """The next forward's noise as a Philox descriptor (drawn inside the kernels)."""
         off = self.noise_counter
@@ -168,8 +172,9 @@ class SoftPalettizedLinear(nn.Module):
         return ops.PhiloxNoise(self.noise_seed, off)
 
     def forward(self, x):
+        _gpu_bf16(x, "SoftPalettizedLinear input")
         lead = x.shape[:-1]
-        noise = self.next_noise_spec() if x.is_cuda else self.next_noise()
+        noise = self.next_noise_spec()
         y = SoftLUTLinearFunction.apply(x.reshape(-1, x.shape[-1]), self.palette, self.index_logits,
                                         noise, self.tau, None, self.lora_a, self.lora_b,
                                         self.lora_scale, self.mode, False)
@@ -186,15 +191,10 @@ def rope_tables(seq, head_dim, theta, device):
 
 
 def apply_rope(x, cos, sin):
-    """x [B, S, H, D]; HF rotate_half convention, computed in fp32, returned in x.dtype."""
-    if x.is_cuda and x.dtype == torch.bfloat16:
-        return RopeFunction.apply(x, cos, sin)
-    xf = x.float()
-    d = xf.shape[-1] // 2
-    rot = torch.cat([-xf[..., d:], xf[..., :d]], dim=-1)
-    c = cos[None, :, None, :]
-    s = sin[None, :, None, :]
-    return (xf * c + rot * s).to(x.dtype)
+    """x bf16 [B, S, H, D] on the GPU: HF's rotate_half embedding (x cos + rotate_half(x) sin),
+    computed in fp32 with fp32 tables, rounded once to bf16 (plz_rope_fwd / plz_rope_bwd)."""
+    _gpu_bf16(x, "apply_rope input")
+    return RopeFunction.apply(x, cos, sin)
 
 
 _GQA_NATIVE = [True]  # cleared when the SDPA backend refuses enable_gqa
@@ -234,27 +234,24 @@ def attention(q, k, v, heads, kv_heads):
         else:
             o, _ = ops.attn_fwd(q.contiguous(), k.contiguous(), v.contiguous())
         return o.view(B, S, H * D)
+    _gpu_bf16(q, "attention query")
     qt = q.transpose(1, 2)
-    if q.is_cuda:
-        # flash / memory-efficient kernels only: the math fallback issues bf16 batched
-        # products on transposed operands, which this pool does not run reliably
-        from torch.nn.attention import SDPBackend, sdpa_kernel
-        with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
-            o = None
-            if _GQA_NATIVE[0]:
-                try:  # grouped-query heads without materialising the repeated k / v
-                    o = F.scaled_dot_product_attention(qt, k.transpose(1, 2), v.transpose(1, 2),
-                                                       is_causal=True, enable_gqa=True)
-                except RuntimeError:
-                    _GQA_NATIVE[0] = False
-            if o is None:
-                kt = k.repeat_interleave(rep, dim=2).transpose(1, 2)
-                vt = v.repeat_interleave(rep, dim=2).transpose(1, 2)
-                o = F.scaled_dot_product_attention(qt, kt, vt, is_causal=True)
-    else:
-        kt = k.repeat_interleave(rep, dim=2).transpose(1, 2)
-        vt = v.repeat_interleave(rep, dim=2).transpose(1, 2)
-        o = F.scaled_dot_product_attention(qt, kt, vt, is_causal=True)
+    # other shapes: torch's flash / memory-efficient kernels on the GPU only (the math
+    # fallback issues bf16 batched products on transposed operands, which this pool does not
+    # run reliably)
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+        o = None
+        if _GQA_NATIVE[0]:
+            try:  # grouped-query heads without materialising the repeated k / v
+                o = F.scaled_dot_product_attention(qt, k.transpose(1, 2), v.transpose(1, 2),
+                                                   is_causal=True, enable_gqa=True)
+            except RuntimeError:
+                _GQA_NATIVE[0] = False
+        if o is None:
+            kt = k.repeat_interleave(rep, dim=2).transpose(1, 2)
+            vt = v.repeat_interleave(rep, dim=2).transpose(1, 2)
+            o = F.scaled_dot_product_attention(qt, kt, vt, is_causal=True)
     return o.transpose(1, 2).reshape(B, S, H * D)
 
 
@@ -318,42 +315,44 @@ class DenseDecoderLayer(nn.Module):
         self.q_norm = RMSNorm(hd, cfg.eps, device)
         self.k_norm = RMSNorm(hd, cfg.eps, device)
 
+    @staticmethod
+    def _linear(x, w):
+        """x [..., K] W^T on the MFMA GEMM core (plz_linear_fwd_dense)."""
+        return ops.linear_fwd_dense(x.reshape(-1, x.shape[-1]).contiguous(), w).view(
+            *x.shape[:-1], w.shape[0])
+
     @torch.no_grad()
     def forward(self, hs, cos, sin):
+        _gpu_bf16(hs, "DenseDecoderLayer input")
         cfg = self.cfg
         B, S, _ = hs.shape
+        lin = self._linear
         x = self.input_layernorm(hs)
-        q = self.q_norm(F.linear(x, self.q_proj).view(B, S, cfg.heads, cfg.head_dim))
-        k = self.k_norm(F.linear(x, self.k_proj).view(B, S, cfg.kv_heads, cfg.head_dim))
-        v = F.linear(x, self.v_proj).view(B, S, cfg.kv_heads, cfg.head_dim)
+        q = self.q_norm(lin(x, self.q_proj).view(B, S, cfg.heads, cfg.head_dim))
+        k = self.k_norm(lin(x, self.k_proj).view(B, S, cfg.kv_heads, cfg.head_dim))
+        v = lin(x, self.v_proj).view(B, S, cfg.kv_heads, cfg.head_dim)
         q, k = apply_rope(q, cos, sin), apply_rope(k, cos, sin)
-        hs = hs + F.linear(attention(q, k, v, cfg.heads, cfg.kv_heads), self.o_proj)
+        hs = hs + lin(attention(q, k, v, cfg.heads, cfg.kv_heads), self.o_proj)
         x = self.post_attention_layernorm(hs)
-        if x.is_cuda and cfg.intermediate % 128 == 0:
+        if cfg.intermediate % 128 == 0:
             # gate and up in one GEMM with the SwiGLU in its epilogue (never stored)
             if getattr(self, "_gate_up", None) is None:
                 self._gate_up = ops.swiglu_weight(self.gate_proj, self.up_proj)
             h = ops.linear_fwd_dense_swiglu(x.reshape(-1, x.shape[-1]), self._gate_up)
             h = h.view(B, S, -1)
         else:
-            h = SwiGLUFunction.apply(F.linear(x, self.gate_proj), F.linear(x, self.up_proj))
-        return hs + F.linear(h, self.down_proj)
+            h = SwiGLUFunction.apply(lin(x, self.gate_proj), lin(x, self.up_proj))
+        return hs + lin(h, self.down_proj)
 
 
 # ---- loss / schedule / optimizer ----------------------------------------------------------------
 def compute_loss(student_out, teacher_out, w_cos=0.5, w_mse=0.5):
-    """train_qwen.py:229-249 (loss_type '1-cos+norm_mse', weights normalised)."""
-    if student_out.is_cuda and student_out.dtype == torch.bfloat16:
-        loss, out = DistillLossFunction.apply(student_out, teacher_out.detach(), w_cos, w_mse)
-        return loss, out[1]
-    s = student_out.float()
-    t = teacher_out.detach().float()
-    tot = w_cos + w_mse
-    cos_per = F.cosine_similarity(s.flatten(0, 1), t.flatten(0, 1), dim=-1, eps=1e-4)
-    l_cos = (1 - cos_per).mean()
-    t_var = (t * t).mean().clamp(min=1e-6)
-    l_mse = ((s - t) ** 2).mean() / t_var
-    return (w_cos / tot) * l_cos + (w_mse / tot) * l_mse, l_cos
+    """train_qwen.py:229-249 (loss_type '1-cos+norm_mse', weights normalised) on bf16 GPU
+    outputs: plz_distill_loss_fwd / plz_distill_loss_bwd. Returns (loss, l_cos)."""
+    _gpu_bf16(student_out, "compute_loss student")
+    _gpu_bf16(teacher_out, "compute_loss teacher")
+    loss, out = DistillLossFunction.apply(student_out, teacher_out.detach(), w_cos, w_mse)
+    return loss, out[1]
 
 
 def tau_at(step, tau_init=2.0, tau_final=0.5, warmup=500, anneal=6000):

@@ -220,3 +220,26 @@ def test_rmsnorm_weight_and_rstd_are_checked_before_the_call(host_ops):
         ops.rmsnorm_bwd(x, torch.zeros(320, dtype=bf), torch.zeros(5), x)
     with pytest.raises(TypeError):
         ops.rmsnorm_bwd(x, torch.zeros(320, dtype=bf), torch.zeros(6, dtype=bf), x)
+
+
+def test_layer_step_has_no_cpu_path():
+    """The layer-step pieces refuse CPU tensors instead of computing in torch on the CPU."""
+    from palettize_hip import layer
+    x = torch.zeros(1, 128, 2, 128, dtype=torch.bfloat16)
+    cos = torch.ones(128, 128)
+    with pytest.raises(RuntimeError, match="no CPU path"):
+        layer.apply_rope(x, cos, cos)
+    with pytest.raises(RuntimeError, match="no CPU path"):
+        layer.attention(x, x, x, 2, 2)
+    with pytest.raises(RuntimeError, match="no CPU path"):
+        layer.compute_loss(torch.zeros(2, 3, 8, dtype=torch.bfloat16),
+                           torch.zeros(2, 3, 8, dtype=torch.bfloat16))
+    lin = layer.SoftPalettizedLinear(256, 16, rank=8)
+    with pytest.raises(RuntimeError, match="no CPU path"):
+        lin(torch.zeros(4, 256, dtype=torch.bfloat16))
+    from palettize_hip import qwen_model
+    import torch.nn as nn
+    m = qwen_model.PalettizedLinear(nn.Linear(256, 16, bias=False),
+                                    torch.zeros(256, 16, dtype=torch.long), 1, 4, 256, False)
+    with pytest.raises(RuntimeError, match="no CPU path"):
+        m(torch.zeros(2, 256, dtype=torch.bfloat16))

@@ -65,15 +65,21 @@ def test_layer_step_forward_backward_matches_cpu_reference(dev, cfg_kw, batch, s
     t_out = R.teacher_forward_ref(w, hs.float(), cfg)
     loss_ref = R.compute_loss_ref(s_out, t_out)
     loss_ref.backward()
-    assert abs(float(loss) - float(loss_ref)) <= 1e-2 * abs(float(loss_ref))
+    lr = float(loss_ref.detach())
+    rel_loss = abs(float(loss) - lr) / abs(lr)
+    cos = {}
     for name in tr.student.NAMES:
         lin = getattr(tr.student, name)
         for attr, key in (("palette", "palette"), ("index_logits", "logits"),
                           ("lora_a", "lora_a"), ("lora_b", "lora_b")):
             got = f32(getattr(lin, attr).grad)
             want = p[name][key].grad.numpy()
-            c = cosine(got, want)
-            assert c >= 0.999, f"{name}.{attr}: cosine {c:.6f}"
+            cos[f"{name}.{attr}"] = cosine(got, want)
+    worst = min(cos, key=cos.get)
+    print(f"loss rel-err {rel_loss:.3e}; worst gradient cosine {worst} {cos[worst]:.7f}",
+          flush=True)
+    assert rel_loss <= 1e-3, f"loss {float(loss)} vs {lr}"
+    assert cos[worst] >= 0.9999, f"{worst}: cosine {cos[worst]:.7f} (all: {cos})"
 
 
 def test_layer_update_matches_adamw_clip_clamp(dev):

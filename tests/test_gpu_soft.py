@@ -50,9 +50,21 @@ def test_soft_build_w(dev, mode, tau, dtype):
 
     if mode == PLZ_W_SOFT:
         assert near(got, w_fwd)
+    elif mode == PLZ_W_HARD_PLAIN:
+        # argmax of the bf16/fp16 logits themselves: exact, ties to the first index
+        assert np.array_equal(got, want)
     else:
-        # hard selection is a bit-exact palette copy; allow the rare near-tie flip
-        assert np.mean(got == want) > 0.9999
+        # argmax of the noisy P: a bit-exact palette copy, except where the top two of
+        # (logit + noise) / tau are so close that fp32 (GPU) and fp64 (oracle) may order them
+        # differently (the GPU's P rounds both to the same value and takes the first)
+        z = (f32(logits).astype(np.float64) + noise.numpy()) / tau
+        top2 = np.sort(z, axis=-1)[..., -2:]
+        gap = top2[..., 1] - top2[..., 0]
+        tie = gap <= 1e-5 * (1.0 + np.abs(top2[..., 1]))
+        bad = got != want
+        assert not np.any(bad & ~tie), (
+            f"{int(np.sum(bad & ~tie))} hard weights differ away from a near tie "
+            f"(smallest gap {gap[bad].min() if bad.any() else 0:.3e})")
     assert near(ws.view(torch.int16).cpu().numpy().view(np.uint16), w_soft)
 
 
