@@ -8,7 +8,8 @@ straight-through through the frozen 2-bit indices, LoRA rank 16 (32 on o and dow
 Also reported (same JSON line): the decode GEMV of config 2 (36 layers x 7 linears, M in
 {1, 4, 16}, one grouped launch per M) in GB/s of packed indices + palettes, the roofline of
 the dominant kernel (HIP events on the launch stream), and the reference's CPU PyTorch path
-(gather + matmul, torch autograd) timed on a bounded sample on the host cores.
+(gather + matmul, torch autograd) on the host cores: config 1 in full (median of 10), the gate
+shape's fwd+bwd at M = 16384 once, and a one-layer CPU GEMV.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only hard|gemv]
 """
@@ -245,40 +246,96 @@ def bench_layer(device, steps=4, warmup=2):
                 config="hidden 2560, 32/8 heads x 128, SwiGLU 9728, 7 soft palettized linears + LoRA r16, batch 32 x 512")
 
 
-def cpu_baseline(budget_s=12.0):
-    """Reference CPU path (gather + matmul + LoRA, torch autograd) on a bounded sample of the
-    config-3 workload: M_cpu rows of every shape; TFLOP/s on the same 6*M*K*N count."""
+def cpu_baseline():
+    """The reference's CPU PyTorch path (PalettizedLinear's fallback, qwen_model.py:183-192:
+    flat palette gather with the int64 _flat_idx buffer, x @ W^T, plus QwenLoRA's
+    (x A^T) B^T, qwen_model.py:291-304; backward by torch autograd) on the host cores, as
+    BASELINE.md plans it:
+      * value: the gate shape (2560 -> 9728, LoRA r16) hard fwd + bwd at M = 16384, timed
+        once after a warm-up at M = 512, in TFLOP/s of 6 M K N;
+      * config1: the single hard forward of config 1 (M 512, K = N = 2560, LoRA r16,
+        seed 0), median of 10 runs after 3 warm-ups;
+      * gemv: one layer's seven linears at M = 1 (gather + matmul), GB/s of packed indices +
+        fp32 palettes (31,539,200 B per layer); 36 layers = 36 x the per-layer time."""
+    import statistics
+
     import torch
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     from torch_ref import native_flat_idx, palettized_linear_cpu
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
-    g = torch.Generator().manual_seed(0)
-    M = 256
-    prepared = []
-    for name, K, N, r in SHAPES:
+    bf = torch.bfloat16
+
+    def weight(N, K, g):
         idx = torch.randint(0, 4, (N, K), generator=g, dtype=torch.uint8)
         pal = torch.sort(torch.randn(N, K // 256, 4, generator=g) * 0.02, -1).values
-        prepared.append(dict(fi=native_flat_idx(idx), pal=pal.to(torch.bfloat16).requires_grad_(True),
-                             x=torch.randn(M, K, generator=g).to(torch.bfloat16).requires_grad_(True),
-                             gy=torch.randn(M, N, generator=g).to(torch.bfloat16),
-                             a=(0.01 * torch.randn(r, K, generator=g)).to(torch.bfloat16).requires_grad_(True),
-                             b=(0.01 * torch.randn(N, r, generator=g)).to(torch.bfloat16).requires_grad_(True),
-                             K=K, N=N))
-    flop_pass = sum(6.0 * M * p["K"] * p["N"] for p in prepared)
-    passes, t0 = 0, time.perf_counter()
-    while True:
-        for p in prepared:
-            y = palettized_linear_cpu(p["x"], p["pal"], p["fi"], None, p["a"], p["b"], 1.0)
-            y.backward(p["gy"])
-        passes += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s or passes >= 50:
-            break
-    tflops = flop_pass * passes / el / 1e12
-    return dict(value=round(tflops, 5), unit="TFLOP/s", cores=cores, kind="port",
-                sample=f"hard fwd+bwd (torch CPU bf16 gather+matmul, autograd) of all 7 shapes "
-                       f"at M={M} rows, {passes} passes in {el:.1f}s")
+        return native_flat_idx(idx), pal.to(bf)
+
+    # config 1
+    g = torch.Generator().manual_seed(0)
+    M1, K1, N1 = 512, 2560, 2560
+    x1 = torch.randn(M1, K1, generator=g).to(bf)
+    fi1, pal1 = weight(N1, K1, g)
+    a1 = (0.01 * torch.randn(16, K1, generator=g)).to(bf)
+    b1 = (0.01 * torch.randn(N1, 16, generator=g)).to(bf)
+    times = []
+    with torch.no_grad():
+        for rep in range(13):
+            t0 = time.perf_counter()
+            palettized_linear_cpu(x1, pal1, fi1, None, a1, b1, 1.0)
+            if rep >= 3:
+                times.append(time.perf_counter() - t0)
+    c1 = statistics.median(times)
+    c1_flop = 2.0 * M1 * K1 * N1 + 2.0 * M1 * 16 * (K1 + N1)
+    _log(f"cpu config1: {c1 * 1e3:.2f} ms")
+
+    # config 3, gate shape, fwd + bwd once (warm-up at M = 512)
+    K, N, r = 2560, 9728, 16
+    fi, pal = weight(N, K, g)
+    a = (0.01 * torch.randn(r, K, generator=g)).to(bf)
+    b = (0.01 * torch.randn(N, r, generator=g)).to(bf)
+
+    def fwd_bwd(M):
+        x = torch.randn(M, K, generator=g).to(bf).requires_grad_(True)
+        gy = torch.randn(M, N, generator=g).to(bf)
+        ps = [t.detach().clone().requires_grad_(True) for t in (pal, a, b)]
+        t0 = time.perf_counter()
+        y = palettized_linear_cpu(x, ps[0], fi, None, ps[1], ps[2], 1.0)
+        y.backward(gy)
+        return time.perf_counter() - t0
+
+    fwd_bwd(512)
+    gate_s = fwd_bwd(M_TRAIN)
+    gate_tflops = 6.0 * M_TRAIN * K * N / gate_s / 1e12
+    _log(f"cpu gate fwd+bwd M={M_TRAIN}: {gate_s:.2f} s")
+    del fi, pal
+
+    # config 2: one layer's 7 GEMVs at M = 1
+    layer = []
+    wbytes = 0
+    for name, K, N, _r in SHAPES:
+        fi_l, pal_l = weight(N, K, g)
+        layer.append((torch.randn(1, K, generator=g).to(bf), fi_l, pal_l))
+        wbytes += N * K // 4 + N * (K // 256) * 16
+    lt = []
+    with torch.no_grad():
+        for rep in range(4):
+            t0 = time.perf_counter()
+            for x, fi_l, pal_l in layer:
+                palettized_linear_cpu(x, pal_l, fi_l)
+            if rep:
+                lt.append(time.perf_counter() - t0)
+    layer_s = statistics.median(lt)
+    _log(f"cpu gemv layer: {layer_s * 1e3:.1f} ms")
+    return dict(value=round(gate_tflops, 5), unit="TFLOP/s", cores=cores, kind="port",
+                sample=f"gate 2560->9728 hard fwd+bwd at M={M_TRAIN} (torch CPU bf16 gather + "
+                       f"matmul + LoRA r16, autograd), timed once: {gate_s:.2f} s",
+                config1=dict(ms_median=round(c1 * 1e3, 3), runs=10, warmup=3,
+                             tflops=round(c1_flop / c1 / 1e12, 5)),
+                gemv=dict(M=1, ms_per_layer=round(layer_s * 1e3, 3),
+                          ms_36_layers=round(36 * layer_s * 1e3, 1),
+                          gbs=round(wbytes / layer_s / 1e9, 3), weight_bytes_per_layer=wbytes,
+                          note="one layer timed (median of 3 after 1 warm-up); 36 layers = 36x"))
 
 
 def _log(msg):
