@@ -69,7 +69,8 @@ struct Args {
   int64_t tail_len;
   float* tail_ws;
   int tiles_i, tiles_j;
-  int group;  // tile-rows walked together (1: consecutive workgroups share the A panel)
+  int group;  // tile-rows walked together (1: consecutive workgroups share the A panel);
+              // < 0: column-major walk (consecutive workgroups share the B panel)
 };
 
 // ---- dense operand copy, global -> LDS ---------------------------------------------------

@@ -342,8 +342,14 @@ __device__ __forceinline__ void soft_item(const Args& g, int64_t n, int64_t kseg
   }
 }
 
-// Tile of work item bid: tile-columns are walked within groups of `group` tile-rows.
+// Tile of work item bid: tile-columns are walked within groups of `group` tile-rows, or, with
+// group < 0, tile-rows within each tile-column (column-major).
 __device__ __forceinline__ void tile_of(const Args& g, int bid, int& tile_i, int& tile_j) {
+  if (g.group < 0) {
+    tile_i = bid % g.tiles_i;
+    tile_j = bid / g.tiles_i;
+    return;
+  }
   const int per_group = g.group * g.tiles_j;
   const int first_i = (bid / per_group) * g.group;
   const int gsz = min(g.tiles_i - first_i, g.group);
@@ -740,7 +746,7 @@ static int launch(Args g, int splits, hipStream_t stream, const char* what) {
   g.tiles_i = (int)((g.I + TILE - 1) / TILE);
   g.tiles_j = (int)((g.J + TILE - 1) / TILE);
   if (g.r_split <= 0) g.r_split = g.R;
-  if (g.group <= 0) g.group = 8;
+  if (g.group == 0) g.group = 8;
   auto kern = gemm2_kernel<KA, KB, EPI>;
   static uint64_t lds_done = 0;
   if (int rc = reserve_lds((const void*)kern, kLds, lds_done, what)) return rc;
@@ -767,23 +773,6 @@ static int launch(Args g, int splits, hipStream_t stream, const char* what) {
   return check_launch(what);
 }
 
-// Reduction splits for a grid of `tiles` workgroups (one workgroup per CU at a time):
-// the split count whose grid best fills whole waves of 256 CUs, at least 8 stages per split.
-static int pick_splits(int64_t tiles, int64_t R) {
-  int best = 1;
-  double best_eff = 0.0;
-  const int64_t zmax = R / (8 * BK);
-  for (int z = 1; z <= 32 && z <= (zmax > 0 ? zmax : 1); ++z) {
-    const int64_t wgs = tiles * z;
-    const int64_t waves = (wgs + 255) / 256;
-    const double eff = (double)wgs / (double)(waves * 256);
-    if (eff > best_eff + 0.02) {
-      best_eff = eff;
-      best = z;
-    }
-  }
-  return best;
-}
 static int64_t split_len(int64_t R, int z) {
   const int64_t per = (R + z - 1) / z;
   return (per + BK - 1) / BK * BK;
@@ -874,8 +863,27 @@ __global__ void reduce_pal_kernel(const float* __restrict__ partial, float* __re
 
 static bool a16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
+// Reduction splits of the grad_palette GEMM. Its time is modelled as (waves of `tiles * z`
+// workgroups on the CUs) x (stages per split + the per-tile prologue and epilogue, worth
+// about 4 stages); the smallest modelled time wins. On the Qwen-4B shapes at M = 16384 this
+// picks 2 splits for the MLP shapes, 3 for q/o and 6 for k/v (measured: k/v 631 -> 861
+// TFLOP/s against the fill-the-waves choice of 19 splits).
 static int palette_splits(int64_t M, int64_t N, int64_t K) {
-  return pick_splits(((N + TILE - 1) / TILE) * ((K + TILE - 1) / TILE), M);
+  const int64_t tiles = ((N + TILE - 1) / TILE) * ((K + TILE - 1) / TILE);
+  const int64_t C = cu_count();
+  if (tiles == 0 || M <= 0) return 1;
+  int best = 1;
+  double best_t = 1e300;
+  for (int z = 1; z <= 32; ++z) {
+    const int64_t len = split_len(M, z);
+    if (z > 1 && (len < 8 * BK || (int64_t)(z - 1) * len >= M)) break;  // >= 8 stages, none empty
+    const double t = (double)((tiles * z + C - 1) / C) * ((double)len / BK + 4.0);
+    if (t < best_t * 0.99) {
+      best_t = t;
+      best = z;
+    }
+  }
+  return best;
 }
 
 // The class-reduced dW GEMM over z splits of M (fp32 partials [z][N][K/128][4] in `partial`,
@@ -889,7 +897,9 @@ static int bwd_palette(const uint16_t* x, const uint16_t* grad_y, const int32_t*
   g.packed = packed; g.Nw = N; g.Kw = K;
   g.I = N; g.J = K; g.R = M; g.r_split = split_len(M, z);
   g.partial = partial;
-  g.group = 1;
+  // XCD-contiguous item ranges walk the panels of the larger operand: a range then reads a
+  // slice of that operand and all of the smaller one (down_proj dW 966 -> 1056 TFLOP/s)
+  g.group = K > N ? -1 : 1;
   int rc = launch<OP_COL, OP_COL, EPI_PAL>(g, z, stream, what);
   if (rc != PLZ_OK) return rc;
   const int64_t G = K / 256, n_out = N * G;
