@@ -169,13 +169,15 @@ int plz_soft_build_w_philox(const uint16_t* logits, int logits_dtype, uint64_t s
                             uint16_t* w, uint16_t* w_soft, int64_t N, int64_t K, void* stream);
 
 /* Batched build W: the linears of a layer (or of several) in one launch, each with its own
- * logits, noise, palette and outputs; the same tau and mode for all. Replaces
- * fused_compute_P_W_batched (fused_lut_kernel.cu:2071-2211, fused_lut_linear_cuda.py:1016-1075),
- * which decorrelates the layers' in-kernel noise by a per-layer seed; here each descriptor
- * brings its own noise. */
+ * logits, palette and outputs and either its own noise tensor or its own Philox key; the same
+ * tau and mode for all. Replaces fused_compute_P_W_batched (fused_lut_kernel.cu:2071-2211,
+ * fused_lut_linear_cuda.py:1016-1075), which draws each layer's noise in the kernel from the
+ * step seed XOR a per-layer value (fused_lut_kernel.cu:2129): a descriptor whose noise is NULL
+ * draws element (n, k, c) as plz_gumbel_philox(noise_seed, offset) would store it, Philox
+ * counter offset + n*K + k with the launch's offset, so layers are decorrelated by key. */
 typedef struct plz_build_w_desc {
   const uint16_t* logits;  /* [N, K, 4] bf16 or fp16 */
-  const float* noise;      /* [N, K, 4] fp32 */
+  const float* noise;      /* [N, K, 4] fp32, or NULL: Philox noise drawn in the kernel */
   const float* palette;    /* [N, K/256, 4] fp32 */
   uint16_t* w;             /* [N, K] bf16 */
   uint16_t* w_soft;        /* [N, K] bf16 or NULL */
@@ -183,6 +185,7 @@ typedef struct plz_build_w_desc {
   int32_t logits_dtype;    /* PLZ_DT_BF16 or PLZ_DT_FP16 */
   int32_t reserved;
   int64_t block_begin;     /* filled by plz_build_w_plan */
+  uint64_t noise_seed;     /* Philox key of a descriptor without a noise tensor */
 } plz_build_w_desc;
 /* Checks n host descriptors, fills block_begin and returns the launch's block count (or a
  * negative status). */
@@ -190,6 +193,11 @@ int64_t plz_build_w_plan(plz_build_w_desc* descs, int n);
 /* descs_device: a device copy of the planned descriptors. */
 int plz_soft_build_w_batched(const plz_build_w_desc* descs_device, int n, int64_t total_blocks,
                              float tau, int mode, void* stream);
+/* plz_soft_build_w_batched with the Philox counter offset of the descriptors that draw their
+ * noise in the kernel (plz_soft_build_w_batched uses offset 0). */
+int plz_soft_build_w_batched_philox(const plz_build_w_desc* descs_device, int n,
+                                    int64_t total_blocks, uint64_t noise_offset, float tau,
+                                    int mode, void* stream);
 
 /* Soft backward, fused in the epilogue of dW = grad_y^T x (dW never leaves the chip):
  *   grad_logits[n,k,c] = s * dW[n,k] P_c (pal_c - sum_d P_d pal_d)   (logits dtype)

@@ -1224,6 +1224,7 @@ static int soft_bwd(const uint16_t* x, const uint16_t* grad_y, const uint16_t* l
   g.noise_seed = seed; g.noise_offset = offset;
   g.glog_scale = scale_grad_by_inv_tau ? 1.f / tau : 1.f;
   g.grad_logits = grad_logits; g.logits_f16 = logits_dtype == PLZ_DT_FP16;
+  g.group = K > N ? -1 : 1;  // walk the larger operand's panels, as the hard grad_palette GEMM
   int rc;
   if (z == 1) {
     rc = launch<OP_COL, OP_COL, EPI_SOFT>(g, 1, (hipStream_t)stream, "plz_soft_bwd");

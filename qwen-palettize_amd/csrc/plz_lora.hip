@@ -42,7 +42,7 @@ __device__ __forceinline__ bf16x8 as_frag(uint4 v) { return __builtin_bit_cast(b
 #define PLZ_RW_NG 4
 #endif
 #ifndef PLZ_RW_WAVES
-#define PLZ_RW_WAVES 4
+#define PLZ_RW_WAVES 8
 #endif
 #ifndef PLZ_RW_U
 #define PLZ_RW_U 2
@@ -336,12 +336,14 @@ __global__ void reduce_kernel(const RedProb a, const RedProb b, int64_t n0, int6
 }
 
 // M split of the column kernel: whole waves of 256 CUs (one workgroup per CU), each split
-// at least 4 stages deep; returns the split length in rows (a multiple of CL_BM).
+// at least 48 stages deep (short splits spend their time filling the copy ring: 48 against 4
+// took the seven Qwen-4B shapes' weight gradients from 555 to 530 us); returns the split
+// length in rows (a multiple of CL_BM).
 static int64_t col_split(int64_t M, int64_t L) {
   const int64_t tiles = (L + CL_L - 1) / CL_L;
   int best = 1;
   double best_eff = 0.0;
-  for (int z = 1; z <= 64 && (int64_t)z * 4 * CL_BM <= M; ++z) {
+  for (int z = 1; z <= 64 && (int64_t)z * 48 * CL_BM <= M; ++z) {
     const int64_t wgs = tiles * z, waves = (wgs + 255) / 256;
     const double eff = (double)wgs / (double)(waves * 256);
     if (eff > best_eff + 0.02) {

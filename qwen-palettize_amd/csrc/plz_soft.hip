@@ -132,7 +132,7 @@ __global__ void build_w_kernel(const uint16_t* __restrict__ logits, int f16,
 // same way): block b belongs to the descriptor whose block_begin is the last one <= b.
 constexpr int kBuildWBlock = 256;
 __global__ void build_w_batched_kernel(const plz_build_w_desc* __restrict__ descs, int n_desc,
-                                       float inv_tau, int mode) {
+                                       uint64_t offset, float inv_tau, int mode) {
   const int64_t b = blockIdx.x;
   int lo = 0, hi = n_desc - 1;
   while (lo < hi) {
@@ -142,8 +142,12 @@ __global__ void build_w_batched_kernel(const plz_build_w_desc* __restrict__ desc
   const plz_build_w_desc d = descs[lo];
   const int64_t t = (b - d.block_begin) * kBuildWBlock + threadIdx.x;
   if (t >= d.N * (d.K / 2)) return;
-  build_w_pair<false>(d.logits, d.logits_dtype == PLZ_DT_FP16, d.noise, 0, 0, d.palette, inv_tau,
-                      mode, d.w, d.w_soft, d.K, t);
+  if (d.noise)
+    build_w_pair<false>(d.logits, d.logits_dtype == PLZ_DT_FP16, d.noise, 0, 0, d.palette,
+                        inv_tau, mode, d.w, d.w_soft, d.K, t);
+  else  // the descriptor's own Philox key (uniform per block)
+    build_w_pair<true>(d.logits, d.logits_dtype == PLZ_DT_FP16, nullptr, d.noise_seed, offset,
+                       d.palette, inv_tau, mode, d.w, d.w_soft, d.K, t);
 }
 
 }  // namespace plz
@@ -232,7 +236,7 @@ int64_t plz_build_w_plan(plz_build_w_desc* descs, int n) {
       return -PLZ_EINVAL;
     }
     if (d.N > 0 && d.K > 0 &&
-        (!d.logits || !d.noise || !d.palette || !d.w ||
+        (!d.logits || !d.palette || !d.w ||
          (((uintptr_t)d.logits | (uintptr_t)d.noise | (uintptr_t)d.palette) & 15) ||
          (((uintptr_t)d.w | (uintptr_t)d.w_soft) & 3))) {
       set_error("plz_build_w_plan: descriptor %d: null or misaligned pointer", i);
@@ -244,8 +248,9 @@ int64_t plz_build_w_plan(plz_build_w_desc* descs, int n) {
   return total;
 }
 
-int plz_soft_build_w_batched(const plz_build_w_desc* descs_device, int n, int64_t total_blocks,
-                             float tau, int mode, void* stream) {
+int plz_soft_build_w_batched_philox(const plz_build_w_desc* descs_device, int n,
+                                    int64_t total_blocks, uint64_t noise_offset, float tau,
+                                    int mode, void* stream) {
   PLZ_REQUIRE(n >= 0 && total_blocks >= 0, "plz_soft_build_w_batched: negative count");
   PLZ_REQUIRE(mode == PLZ_W_SOFT || mode == PLZ_W_HARD_NOISY || mode == PLZ_W_HARD_PLAIN,
               "plz_soft_build_w_batched: unknown mode %d", mode);
@@ -253,8 +258,13 @@ int plz_soft_build_w_batched(const plz_build_w_desc* descs_device, int n, int64_
   if (n == 0 || total_blocks == 0) return PLZ_OK;
   PLZ_REQUIRE(descs_device, "plz_soft_build_w_batched: null descriptor table");
   hipLaunchKernelGGL(build_w_batched_kernel, dim3((unsigned)total_blocks), dim3(kBuildWBlock), 0,
-                     (hipStream_t)stream, descs_device, n, 1.f / tau, mode);
+                     (hipStream_t)stream, descs_device, n, noise_offset, 1.f / tau, mode);
   return check_launch("plz_soft_build_w_batched");
+}
+
+int plz_soft_build_w_batched(const plz_build_w_desc* descs_device, int n, int64_t total_blocks,
+                             float tau, int mode, void* stream) {
+  return plz_soft_build_w_batched_philox(descs_device, n, total_blocks, 0, tau, mode, stream);
 }
 
 }  // extern "C"

@@ -24,7 +24,7 @@ i32, i64, u32, u64, f32, sz = C.c_int, C.c_int64, C.c_uint32, C.c_uint64, C.c_fl
 class BuildWDesc(C.Structure):
     _fields_ = [("logits", p), ("noise", p), ("palette", p), ("w", p), ("w_soft", p),
                 ("N", i64), ("K", i64), ("logits_dtype", i32), ("reserved", i32),
-                ("block_begin", i64)]
+                ("block_begin", i64), ("noise_seed", u64)]
 
 
 class AdamWDesc(C.Structure):
@@ -73,6 +73,7 @@ SIGNATURES: dict[str, tuple] = {
     "plz_soft_build_w_philox": (i32, [p, i32, u64, u64, p, f32, i32, p, p, i64, i64, p]),
     "plz_build_w_plan": (i64, [C.POINTER(BuildWDesc), i32]),
     "plz_soft_build_w_batched": (i32, [p, i32, i64, f32, i32, p]),
+    "plz_soft_build_w_batched_philox": (i32, [p, i32, i64, u64, f32, i32, p]),
     "plz_soft_bwd_workspace": (sz, [i64, i64, i64]),
     "plz_soft_bwd": (i32, [p, p, p, i32, p, p, f32, i32, p, p, p, sz, i64, i64, i64, p]),
     "plz_soft_bwd_philox": (i32, [p, p, p, i32, u64, u64, p, f32, i32, p, p, p, sz, i64, i64, i64, p]),

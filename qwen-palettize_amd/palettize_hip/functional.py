@@ -66,12 +66,21 @@ def lut_linear(x, packed, palette, bias=None, lora_a=None, lora_b=None, lora_sca
 
 
 class SoftLUTLinearFunction(torch.autograd.Function):
+    """``prebuilt`` (optional): (w, group) with w the forward weight already built from these
+    logits, noise, palette and tau by ``group`` (an ops.SoftBuildGroup run); the backward
+    checks that no later run of the group has overwritten it."""
+
     @staticmethod
     def forward(ctx, x, palette, logits, noise, tau, bias, lora_a, lora_b, lora_scale, mode,
-                scale_by_inv_tau):
+                scale_by_inv_tau, prebuilt=None):
         x = x.contiguous()
         lora_a, lora_b = _c(lora_a), _c(lora_b)
-        w, _ = ops.soft_build_w(logits, noise, palette, tau, mode)
+        ctx.guard = None
+        if prebuilt is None:
+            w, _ = ops.soft_build_w(logits, noise, palette, tau, mode)
+        else:
+            w, group = prebuilt
+            ctx.guard = (group, group.generation)
         t = ops.lora_project(x, lora_a, lora_scale) if lora_a is not None else None
         y = ops.linear_fwd_dense(x, w, bias, t, lora_b)
         # a Philox noise descriptor is redrawn in the backward's epilogue, not stored
@@ -88,6 +97,9 @@ class SoftLUTLinearFunction(torch.autograd.Function):
     @staticmethod
     def backward(ctx, gy):
         x, palette, logits, noise, w, lora_a, lora_b, t = ctx.saved_tensors
+        if ctx.guard is not None and ctx.guard[0].generation != ctx.guard[1]:
+            raise RuntimeError("the prebuilt soft weight of this forward was rebuilt by a later "
+                               "forward before this backward ran")
         if ctx.philox is not None:
             noise = ctx.philox
         gy = gy.contiguous()
@@ -109,7 +121,7 @@ class SoftLUTLinearFunction(torch.autograd.Function):
                 gt = ops.lora_grad_t(gy, lora_b, ctx.lora_scale)
             grad_a, grad_b = ops.lora_weight_grads(x, gy, t, gt, 1.0, out_dtype=lora_a.dtype)
         return (grad_x, grad_pal if need_pal else None, grad_logits if need_log else None, None,
-                None, grad_bias, grad_a, grad_b, None, None, None)
+                None, grad_bias, grad_a, grad_b, None, None, None, None)
 
 
 def soft_lut_linear(x, palette, logits, noise, tau, bias=None, lora_a=None, lora_b=None,

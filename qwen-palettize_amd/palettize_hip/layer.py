@@ -133,6 +133,9 @@ class DistillLossFunction(torch.autograd.Function):
 
 
 # ---- palettized linear (native layout, soft path) ----------------------------------------
+NOISE_STRIDE = 1 << 32  # Philox counters consumed per forward of a soft linear (> N * K)
+
+
 class SoftPalettizedLinear(nn.Module):
     """y = x W_ste^T + s (x A^T) B^T with W from logits + Gumbel noise + palette.
 
@@ -166,18 +169,27 @@ class SoftPalettizedLinear(nn.Module):
         self.mode = PLZ_W_HARD_NOISY
 
     def next_noise_spec(self):
-        """The next forward's noise as a Philox descriptor (drawn inside the kernels)."""
+        """The next forward's noise as a Philox descriptor (drawn inside the kernels): key
+        noise_seed, counters noise_counter + n*K + k. The counter advances by NOISE_STRIDE per
+        forward (more than any N*K), so linears that start together stay on the same offset and
+        one batched build serves them all, decorrelated by their keys."""
         off = self.noise_counter
-        self.noise_counter += self.out_features * self.in_features
+        self.noise_counter += NOISE_STRIDE
         return ops.PhiloxNoise(self.noise_seed, off)
 
-    def forward(self, x):
+    def forward(self, x, prebuilt=None):
+        """prebuilt: (w, group) from the layer's batched build of this forward (the noise
+        counter has then been advanced by the layer)."""
         _gpu_bf16(x, "SoftPalettizedLinear input")
         lead = x.shape[:-1]
-        noise = self.next_noise_spec()
+        if prebuilt is None:
+            noise = self.next_noise_spec()
+        else:
+            w, group, noise = prebuilt
+            prebuilt = (w, group)
         y = SoftLUTLinearFunction.apply(x.reshape(-1, x.shape[-1]), self.palette, self.index_logits,
                                         noise, self.tau, None, self.lora_a, self.lora_b,
-                                        self.lora_scale, self.mode, False)
+                                        self.lora_scale, self.mode, False, prebuilt)
         return y.reshape(*lead, self.out_features)
 
 
@@ -277,21 +289,41 @@ class PalettizedDecoderLayer(nn.Module):
         self.post_attention_layernorm = RMSNorm(h, cfg.eps, device)
         self.q_norm = RMSNorm(hd, cfg.eps, device)
         self.k_norm = RMSNorm(hd, cfg.eps, device)
+        self._wgroup = None
 
     def linears(self):
         return [getattr(self, n) for n in self.NAMES]
 
+    def build_weights(self):
+        """The seven linears' forward weights in one launch (plz_soft_build_w_batched_philox):
+        each linear's own Philox key at the shared counter offset of this forward, the same
+        tau. Returns {name: (w, group, noise)} for the linears' forward."""
+        lins = self.linears()
+        if self._wgroup is None:
+            self._wgroup = ops.SoftBuildGroup(
+                [(l.index_logits, ops.PhiloxNoise(l.noise_seed, 0), l.palette) for l in lins],
+                PLZ_W_HARD_NOISY)
+        offset = lins[0].noise_counter
+        if any(l.noise_counter != offset or l.mode != PLZ_W_HARD_NOISY or l.tau != lins[0].tau
+               for l in lins):
+            raise RuntimeError("batched build: the linears must share noise offset, mode and tau")
+        specs = [l.next_noise_spec() for l in lins]
+        outs = self._wgroup.run(lins[0].tau, offset)
+        return {n: (w, self._wgroup, sp) for n, (w, _), sp in zip(self.NAMES, outs, specs)}
+
     def forward(self, hs, cos, sin):
         cfg = self.cfg
         B, S, _ = hs.shape
+        pw = self.build_weights()
         x = self.input_layernorm(hs)
-        q = self.q_norm(self.q_proj(x).view(B, S, cfg.heads, cfg.head_dim))
-        k = self.k_norm(self.k_proj(x).view(B, S, cfg.kv_heads, cfg.head_dim))
-        v = self.v_proj(x).view(B, S, cfg.kv_heads, cfg.head_dim)
+        q = self.q_norm(self.q_proj(x, pw["q_proj"]).view(B, S, cfg.heads, cfg.head_dim))
+        k = self.k_norm(self.k_proj(x, pw["k_proj"]).view(B, S, cfg.kv_heads, cfg.head_dim))
+        v = self.v_proj(x, pw["v_proj"]).view(B, S, cfg.kv_heads, cfg.head_dim)
         q, k = apply_rope(q, cos, sin), apply_rope(k, cos, sin)
-        hs = hs + self.o_proj(attention(q, k, v, cfg.heads, cfg.kv_heads))
+        hs = hs + self.o_proj(attention(q, k, v, cfg.heads, cfg.kv_heads), pw["o_proj"])
         x = self.post_attention_layernorm(hs)
-        mlp = self.down_proj(SwiGLUFunction.apply(self.gate_proj(x), self.up_proj(x)))
+        mlp = self.down_proj(SwiGLUFunction.apply(self.gate_proj(x, pw["gate_proj"]),
+                                                  self.up_proj(x, pw["up_proj"])), pw["down_proj"])
         return hs + mlp
 
 

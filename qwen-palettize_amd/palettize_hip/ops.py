@@ -328,8 +328,11 @@ def soft_build_w(logits, noise, palette, tau: float, mode: int = _lib.PLZ_W_HARD
 
 class SoftBuildGroup:
     """The forward weights of several soft linears built by one launch
-    (plz_soft_build_w_batched). ``items`` is a list of (logits, noise, palette); the outputs
-    (w and, with want_soft, w_soft) are allocated once and rewritten by every ``run(tau)``."""
+    (plz_soft_build_w_batched_philox). ``items`` is a list of (logits, noise, palette), where
+    noise is an fp32 [N, K, 4] tensor or a ``PhiloxNoise`` whose seed is that linear's Philox
+    key (its noise is then drawn in the kernel at the counter offset given to ``run``). The
+    outputs (w and, with want_soft, w_soft) are allocated once and rewritten by every run;
+    ``generation`` counts the runs."""
 
     def __init__(self, items, mode: int = _lib.PLZ_W_HARD_NOISY, want_soft: bool = False):
         if not items:
@@ -337,15 +340,19 @@ class SoftBuildGroup:
         self.mode = int(mode)
         self.device = items[0][0].device
         self.outputs = []
+        self.generation = 0
         descs = (_lib.BuildWDesc * len(items))()
         for i, (logits, noise, palette) in enumerate(items):
             N, K = _soft_shapes(logits, noise, palette)
             w = torch.empty((N, K), dtype=torch.bfloat16, device=self.device)
             ws = torch.empty((N, K), dtype=torch.bfloat16, device=self.device) if want_soft else None
             self.outputs.append((w, ws))
-            descs[i] = _lib.BuildWDesc(logits.data_ptr(), noise.data_ptr(), palette.data_ptr(),
-                                       w.data_ptr(), ws.data_ptr() if ws is not None else None,
-                                       N, K, _DT[logits.dtype], 0, 0)
+            philox = isinstance(noise, PhiloxNoise)
+            descs[i] = _lib.BuildWDesc(logits.data_ptr(), None if philox else noise.data_ptr(),
+                                       palette.data_ptr(), w.data_ptr(),
+                                       ws.data_ptr() if ws is not None else None,
+                                       N, K, _DT[logits.dtype], 0, 0,
+                                       (noise.seed & (2**64 - 1)) if philox else 0)
         self._keep = items
         total = _lib.lib().plz_build_w_plan(descs, len(items))
         if total < 0:
@@ -356,9 +363,11 @@ class SoftBuildGroup:
         self.table = torch.frombuffer(bytearray(raw), dtype=torch.uint8).to(self.device)
         self.n = len(items)
 
-    def run(self, tau: float):
-        call("plz_soft_build_w_batched", self.table.data_ptr(), self.n, self.total_blocks,
-             float(tau), self.mode, torch.cuda.current_stream(self.device).cuda_stream)
+    def run(self, tau: float, noise_offset: int = 0):
+        call("plz_soft_build_w_batched_philox", self.table.data_ptr(), self.n, self.total_blocks,
+             int(noise_offset) & (2**64 - 1), float(tau), self.mode,
+             torch.cuda.current_stream(self.device).cuda_stream)
+        self.generation += 1
         return self.outputs
 
 

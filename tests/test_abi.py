@@ -243,3 +243,20 @@ def test_layer_step_has_no_cpu_path():
                                     torch.zeros(256, 16, dtype=torch.long), 1, 4, 256, False)
     with pytest.raises(RuntimeError, match="no CPU path"):
         m(torch.zeros(2, 256, dtype=torch.bfloat16))
+
+
+def test_build_w_plan_accepts_philox_descriptors(lib):
+    """A batched build-W descriptor without a noise tensor (in-kernel Philox noise with its own
+    key) plans like one with a tensor; a missing logits pointer still fails. Pointers are never
+    dereferenced by the plan."""
+    from palettize_hip import _lib
+    f = 4096
+    assert C.sizeof(_lib.BuildWDesc) == 5 * 8 + 2 * 8 + 2 * 4 + 8 + 8
+    d = (_lib.BuildWDesc * 3)(
+        _lib.BuildWDesc(f, f, f, f, None, 64, 512, 0, 0, 0, 0),
+        _lib.BuildWDesc(f, None, f, f, None, 8, 256, 1, 0, 0, 7),
+        _lib.BuildWDesc(f, None, f, f, None, 0, 256, 0, 0, 0, 9))
+    assert lib.plz_build_w_plan(d, 3) == 64 * 256 // 256 + 8 * 128 // 256
+    assert d[1].block_begin == 64 and d[2].block_begin == 68
+    bad = (_lib.BuildWDesc * 1)(_lib.BuildWDesc(None, None, f, f, None, 8, 256, 0, 0, 0, 1))
+    assert lib.plz_build_w_plan(bad, 1) < 0

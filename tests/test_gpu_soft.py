@@ -86,6 +86,42 @@ def test_soft_build_w_batched_matches_single(dev, mode):
             assert torch.equal(w, w1) and torch.equal(ws, ws1)
 
 
+@pytest.mark.parametrize("mode", [PLZ_W_SOFT, PLZ_W_HARD_NOISY, PLZ_W_HARD_PLAIN])
+def test_soft_build_w_batched_philox(dev, mode):
+    """Descriptors without a noise tensor draw Philox noise in the kernel from their own key at
+    the launch's counter offset: each output equals the single-linear plz_soft_build_w_philox
+    bit for bit, and the oracle's build from the oracle's Philox noise (the reference's
+    per-layer decorrelated in-kernel draw, fused_lut_kernel.cu:2071-2211)."""
+    shapes = [(64, 512, torch.bfloat16, 11), (8, 256, torch.float16, 12),
+              (136, 768, torch.bfloat16, (3 << 32) | 5), (1024, 2560, torch.bfloat16, 14)]
+    items, host = [], []
+    for i, (N, K, dt, seed) in enumerate(shapes):
+        lg, _, pl = _soft_inputs(N, K, seed=60 + i, dtype=dt)
+        items.append((lg.to(dev), ops.PhiloxNoise(seed, 0), pl.to(dev)))
+        host.append((lg, pl, seed))
+    grp = ops.SoftBuildGroup(items, mode, want_soft=True)
+    for tau, offset in ((0.7, 0), (2.0, 1 << 32), (0.1, (5 << 32) + 12345)):
+        outs = grp.run(tau, offset)
+        for j, ((lg, nz, pl), (w, ws)) in enumerate(zip(items, outs)):
+            w1, ws1 = ops.soft_build_w(lg, ops.PhiloxNoise(nz.seed, offset), pl, tau, mode,
+                                       want_soft=True)
+            assert torch.equal(w, w1) and torch.equal(ws, ws1), f"linear {j} tau {tau}"
+            if j == 2:  # the oracle, from its own Philox noise
+                lgc, plc, seed = host[j]
+                N, K = lgc.shape[:2]
+                noise = O.gumbel_philox(N * K * 4, seed, offset).reshape(N, K, 4)
+                _, w_soft, w_fwd = O.soft_weights(f32(lgc), noise, plc.numpy(), tau, mode)
+                got = O.bf16_to_f32(w.view(torch.int16).cpu().numpy().view(np.uint16))
+                if mode == PLZ_W_SOFT:
+                    assert np.allclose(got, w_fwd, rtol=2.0 ** -7, atol=1e-6)
+                else:
+                    want = O.bf16_to_f32(O.bf16_bits(w_fwd.astype(np.float32)))
+                    assert np.mean(got == want) > 0.999
+                soft = O.bf16_to_f32(ws.view(torch.int16).cpu().numpy().view(np.uint16))
+                assert np.allclose(soft, w_soft, rtol=2.0 ** -7, atol=1e-6)
+    assert grp.generation == 3
+
+
 @pytest.mark.parametrize("tau", [2.0, 0.5, 0.1])
 @pytest.mark.parametrize("scaled", [False, True])
 def test_soft_bwd(dev, tau, scaled):
