@@ -246,5 +246,133 @@ __device__ __forceinline__ bf16x8 frag_col(const lds_u8* lds, int rowbase, int k
   return __builtin_bit_cast(bf16x8, v);
 }
 
+// ---- work-item map and launch planning (shared by the kernels and a host-side check) -------
+// A launch has tiles_i x tiles_j output tiles and gridDim.z reduction splits; a tail-split
+// launch (bf16 epilogue, tail_split > 1) runs its first tail_first tiles whole and each later
+// tile as tail_split reduction parts in the last, partial wave.
+struct Item {
+  int zsl, bid, part;  // reduction split, tile index, tail part
+  bool tail_part;
+};
+// Workgroups go to the 8 XCDs round-robin by linear id, and each XCD has its own L2: the
+// (split, tile) items are renumbered so that XCD x runs one contiguous range of them.
+__host__ __device__ __forceinline__ Item map_item(int tiles, bool tail, int tail_first,
+                                                  int tail_split, int bx, int bz, int gz) {
+  Item it{0, 0, 0, false};
+  if (tail && bx >= tail_first) {
+    const int u = bx - tail_first;
+    it.bid = tail_first + u / tail_split;
+    it.part = u % tail_split;
+    it.tail_part = true;
+    return it;
+  }
+  const int whole = tail ? tail_first : tiles;
+  const int total = whole * gz;
+  const int lin = bx + whole * bz;
+  const int xcd = lin % 8, q8 = total / 8, r8 = total % 8;
+  const int item = xcd * q8 + (xcd < r8 ? xcd : r8) + lin / 8;
+  it.zsl = item / whole;
+  it.bid = item % whole;
+  return it;
+}
+// Tile of item bid: tile-columns are walked within groups of `group` tile-rows, or, with
+// group < 0, tile-rows within each tile-column (column-major).
+__host__ __device__ __forceinline__ void tile_coords(int group, int tiles_i, int tiles_j, int bid,
+                                                     int& tile_i, int& tile_j) {
+  if (group < 0) {
+    tile_i = bid % tiles_i;
+    tile_j = bid / tiles_i;
+    return;
+  }
+  const int per_group = group * tiles_j;
+  const int first_i = (bid / per_group) * group;
+  const int gsz = tiles_i - first_i < group ? tiles_i - first_i : group;
+  tile_i = first_i + (bid % per_group) % gsz;
+  tile_j = (bid % per_group) / gsz;
+}
+
+// reduction length of each of z splits, a whole number of stages
+inline int64_t split_len(int64_t R, int z) {
+  const int64_t per = (R + z - 1) / z;
+  return (per + BK - 1) / BK * BK;
+}
+
+// Reduction splits of the grad_palette GEMM on C CUs. Its time is modelled as (waves of
+// `tiles * z` workgroups) x (stages per split + the per-tile prologue and epilogue, worth
+// about 4 stages); the smallest modelled time wins. On the Qwen-4B shapes at M = 16384 this
+// picks 2 splits for the MLP shapes, 3 for q/o and 6 for k/v (measured: k/v 631 -> 861
+// TFLOP/s against the fill-the-waves choice of 19 splits).
+inline int palette_splits_on(int64_t M, int64_t N, int64_t K, int64_t C) {
+  const int64_t tiles = ((N + TILE - 1) / TILE) * ((K + TILE - 1) / TILE);
+  if (tiles == 0 || M <= 0) return 1;
+  int best = 1;
+  double best_t = 1e300;
+  for (int z = 1; z <= 32; ++z) {
+    const int64_t len = split_len(M, z);
+    if (z > 1 && (len < 8 * BK || (int64_t)(z - 1) * len >= M)) break;  // >= 8 stages, none empty
+    const double t = (double)((tiles * z + C - 1) / C) * ((double)len / BK + 4.0);
+    if (t < best_t * 0.99) {
+      best_t = t;
+      best = z;
+    }
+  }
+  return best;
+}
+
+// Tail split of a one-workgroup-per-tile GEMM (one workgroup per CU) on C CUs: when the tiles
+// leave a last, partial wave of rem < C/2 tiles, those tiles run as s = C/rem reduction parts
+// each, so the last wave takes 1/s of a tile-time. Taken when the time saved (2.15 us per
+// 256x256x64 stage) exceeds the cost of the fp32 partials (256 KB per part written and read
+// at ~5 TB/s) and one more launch.
+struct TailPlan {
+  int first = 0, split = 1;
+  int64_t len = 0;
+};
+inline TailPlan tail_plan_on(int64_t I, int64_t J, int64_t R, int64_t C) {
+  TailPlan t;
+  const int64_t tiles = ((I + TILE - 1) / TILE) * ((J + TILE - 1) / TILE);
+  const int64_t rem = tiles % C;
+  if (rem == 0 || R <= 0) return t;
+  const int64_t stages = (R + BK - 1) / BK;
+  int s = (int)(C / rem);
+  s = s < 16 ? s : 16;
+  while (s > 1 && (stages / s < 8 || (int64_t)(s - 1) * split_len(R, s) >= R)) --s;
+  if (s < 2) return t;
+  const double gain = (double)stages * 2.15 * (1.0 - 1.0 / s);
+  const double cost = (double)rem * s * 2.0 * TILE * TILE * 4 / 5.0e6 + 5.0;
+  if (gain <= cost) return t;
+  t.first = (int)(tiles - rem);
+  t.split = s;
+  t.len = split_len(R, s);
+  return t;
+}
+
+// Splits of the soft backward's reduction over M. The fused epilogue needs the whole sum, so
+// an unsplit launch has one workgroup per 256x256 output tile: 40 for k/v_proj, 160 for
+// q/o_proj, 380 for the MLP shapes, i.e. whole or partial waves on 256 CUs. A split launch
+// writes each split's partial dW rows in fp32 and a streaming kernel sums them and runs the
+// soft epilogue. The count minimises a model of the two: (waves of 256 workgroups) x (stages
+// per split) x 2.4 us, plus, when split, 32 B per weight of epilogue traffic and 8 B per weight
+// and split of partials, at 5 TB/s. On the Qwen-4B shapes at M = 16384 it picks 6 / 3 / 2
+// splits, the measured optimum of each.
+inline int soft_splits(int64_t M, int64_t N, int64_t K) {
+  const int64_t tiles = ((N + TILE - 1) / TILE) * ((K + TILE - 1) / TILE);
+  if (tiles == 0 || M <= 0) return 1;
+  const double weights = (double)N * (double)K;
+  const double stage_us = 2.4, epi_us = 32.0 * weights / 5.0e6, part_us = 8.0 * weights / 5.0e6;
+  int best = 1;
+  double best_t = (double)((tiles + 255) / 256) * (double)((M + BK - 1) / BK) * stage_us;
+  for (int z = 2; z <= 16; ++z) {
+    const int64_t len = split_len(M, z);
+    if (len < 8 * BK || (int64_t)(z - 1) * len >= M) break;  // >= 8 stages, no empty split
+    const double t = (double)((tiles * z + 255) / 256) * (double)(len / BK) * stage_us + epi_us +
+                     z * part_us;
+    if (t < best_t * 0.97) {
+      best_t = t;
+      best = z;
+    }
+  }
+  return best;
+}
 }  // namespace g2
 }  // namespace plz

@@ -342,19 +342,8 @@ __device__ __forceinline__ void soft_item(const Args& g, int64_t n, int64_t kseg
   }
 }
 
-// Tile of work item bid: tile-columns are walked within groups of `group` tile-rows, or, with
-// group < 0, tile-rows within each tile-column (column-major).
 __device__ __forceinline__ void tile_of(const Args& g, int bid, int& tile_i, int& tile_j) {
-  if (g.group < 0) {
-    tile_i = bid % g.tiles_i;
-    tile_j = bid / g.tiles_i;
-    return;
-  }
-  const int per_group = g.group * g.tiles_j;
-  const int first_i = (bid / per_group) * g.group;
-  const int gsz = min(g.tiles_i - first_i, g.group);
-  tile_i = first_i + (bid % per_group) % gsz;
-  tile_j = (bid % per_group) / gsz;
+  tile_coords(g.group, g.tiles_i, g.tiles_j, bid, tile_i, tile_j);
 }
 
 // bf16 epilogue: C = alpha * acc (+ bias). The tile is staged in LDS (rows padded to 528 B so
@@ -441,27 +430,13 @@ __global__ __launch_bounds__(NTHR) void gemm2_kernel(const Args g) {
   constexpr bool A_COL = KA == OP_COL;
   constexpr bool B_COL = KB == OP_COL || KB == OP_LUT_COL;
 
-  // Workgroups go to the 8 XCDs round-robin by linear id, and each XCD has its own L2. The
-  // (split, tile) items are renumbered so that XCD x runs one contiguous range of them:
-  // the ~32 workgroups resident on an XCD then share operand panels in that XCD's L2.
-  // A tail-split launch (EPI_BF16) renumbers its tail_first whole tiles this way; the
-  // workgroups after them (the last, partial wave) each run one reduction part of a tail tile.
+  // (split, tile) items in XCD-contiguous ranges; in a tail-split launch the workgroups after
+  // the tail_first whole tiles each run one reduction part of a tail tile (map_item)
   const int T = g.tiles_i * g.tiles_j;
-  const bool tail_part = EPI == EPI_BF16 && g.tail_split > 1 && (int)blockIdx.x >= g.tail_first;
-  int zsl = 0, bid = 0, part = 0;
-  if (tail_part) {
-    const int u = (int)blockIdx.x - g.tail_first;
-    bid = g.tail_first + u / g.tail_split;
-    part = u % g.tail_split;
-  } else {
-    const int whole = EPI == EPI_BF16 && g.tail_split > 1 ? g.tail_first : T;
-    const int total = whole * (int)gridDim.z;
-    const int lin = (int)blockIdx.x + whole * (int)blockIdx.z;
-    const int xcd = lin % 8, q8 = total / 8, r8 = total % 8;
-    const int item = xcd * q8 + min(xcd, r8) + lin / 8;
-    zsl = item / whole;
-    bid = item % whole;
-  }
+  const Item itm = map_item(T, EPI == EPI_BF16 && g.tail_split > 1, g.tail_first, g.tail_split,
+                            (int)blockIdx.x, (int)blockIdx.z, (int)gridDim.z);
+  const bool tail_part = itm.tail_part;
+  const int zsl = itm.zsl, bid = itm.bid, part = itm.part;
   int tile_i, tile_j;
   tile_of(g, bid, tile_i, tile_j);
   const int64_t i0 = (int64_t)tile_i * TILE, j0 = (int64_t)tile_j * TILE;
@@ -773,11 +748,6 @@ static int launch(Args g, int splits, hipStream_t stream, const char* what) {
   return check_launch(what);
 }
 
-static int64_t split_len(int64_t R, int z) {
-  const int64_t per = (R + z - 1) / z;
-  return (per + BK - 1) / BK * BK;
-}
-
 static int cu_count() {
   static int cache[64] = {0};
   int dev = 0;
@@ -792,33 +762,8 @@ static int cu_count() {
   return cache[dev];
 }
 
-// Tail split of a one-workgroup-per-tile GEMM (one workgroup per CU): when the tiles leave a
-// last, partial wave of rem < CUs/2 tiles, those tiles run as s = CUs/rem reduction parts
-// each, so the last wave takes 1/s of a tile-time. Taken when the time saved (2.15 us per
-// 256x256x64 stage) exceeds the cost of the fp32 partials (256 KB per part written and read
-// at ~5 TB/s) and one more launch.
-struct TailPlan {
-  int first = 0, split = 1;
-  int64_t len = 0;
-};
 static TailPlan tail_plan(int64_t I, int64_t J, int64_t R) {
-  TailPlan t;
-  const int64_t tiles = ((I + TILE - 1) / TILE) * ((J + TILE - 1) / TILE);
-  const int64_t C = cu_count();
-  const int64_t rem = tiles % C;
-  if (rem == 0 || R <= 0) return t;
-  const int64_t stages = (R + BK - 1) / BK;
-  int s = (int)(C / rem);
-  s = s < 16 ? s : 16;
-  while (s > 1 && (stages / s < 8 || (int64_t)(s - 1) * split_len(R, s) >= R)) --s;
-  if (s < 2) return t;
-  const double gain = (double)stages * 2.15 * (1.0 - 1.0 / s);
-  const double cost = (double)rem * s * 2.0 * TILE * TILE * 4 / 5.0e6 + 5.0;
-  if (gain <= cost) return t;
-  t.first = (int)(tiles - rem);
-  t.split = s;
-  t.len = split_len(R, s);
-  return t;
+  return tail_plan_on(I, J, R, cu_count());
 }
 static size_t tail_bytes(int64_t I, int64_t J, int64_t R) {
   const TailPlan t = tail_plan(I, J, R);
@@ -863,27 +808,8 @@ __global__ void reduce_pal_kernel(const float* __restrict__ partial, float* __re
 
 static bool a16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
-// Reduction splits of the grad_palette GEMM. Its time is modelled as (waves of `tiles * z`
-// workgroups on the CUs) x (stages per split + the per-tile prologue and epilogue, worth
-// about 4 stages); the smallest modelled time wins. On the Qwen-4B shapes at M = 16384 this
-// picks 2 splits for the MLP shapes, 3 for q/o and 6 for k/v (measured: k/v 631 -> 861
-// TFLOP/s against the fill-the-waves choice of 19 splits).
 static int palette_splits(int64_t M, int64_t N, int64_t K) {
-  const int64_t tiles = ((N + TILE - 1) / TILE) * ((K + TILE - 1) / TILE);
-  const int64_t C = cu_count();
-  if (tiles == 0 || M <= 0) return 1;
-  int best = 1;
-  double best_t = 1e300;
-  for (int z = 1; z <= 32; ++z) {
-    const int64_t len = split_len(M, z);
-    if (z > 1 && (len < 8 * BK || (int64_t)(z - 1) * len >= M)) break;  // >= 8 stages, none empty
-    const double t = (double)((tiles * z + C - 1) / C) * ((double)len / BK + 4.0);
-    if (t < best_t * 0.99) {
-      best_t = t;
-      best = z;
-    }
-  }
-  return best;
+  return palette_splits_on(M, N, K, cu_count());
 }
 
 // The class-reduced dW GEMM over z splits of M (fp32 partials [z][N][K/128][4] in `partial`,
@@ -942,33 +868,6 @@ static int pal_scratch(float** out) {
   return PLZ_OK;
 }
 
-// Splits of the soft backward's reduction over M. The fused epilogue needs the whole sum, so
-// an unsplit launch has one workgroup per 256x256 output tile: 40 for k/v_proj, 160 for
-// q/o_proj, 380 for the MLP shapes, i.e. whole or partial waves on 256 CUs. A split launch
-// writes each split's partial dW rows in fp32 and a streaming kernel sums them and runs the
-// soft epilogue. The count minimises a model of the two: (waves of 256 workgroups) x (stages
-// per split) x 2.4 us, plus, when split, 32 B per weight of epilogue traffic and 8 B per weight
-// and split of partials, at 5 TB/s. On the Qwen-4B shapes at M = 16384 it picks 6 / 3 / 2
-// splits, the measured optimum of each.
-static int soft_splits(int64_t M, int64_t N, int64_t K) {
-  const int64_t tiles = ((N + TILE - 1) / TILE) * ((K + TILE - 1) / TILE);
-  if (tiles == 0 || M <= 0) return 1;
-  const double weights = (double)N * (double)K;
-  const double stage_us = 2.4, epi_us = 32.0 * weights / 5.0e6, part_us = 8.0 * weights / 5.0e6;
-  int best = 1;
-  double best_t = (double)((tiles + 255) / 256) * (double)((M + BK - 1) / BK) * stage_us;
-  for (int z = 2; z <= 16; ++z) {
-    const int64_t len = split_len(M, z);
-    if (len < 8 * BK || (int64_t)(z - 1) * len >= M) break;  // >= 8 stages, no empty split
-    const double t = (double)((tiles * z + 255) / 256) * (double)(len / BK) * stage_us + epi_us +
-                     z * part_us;
-    if (t < best_t * 0.97) {
-      best_t = t;
-      best = z;
-    }
-  }
-  return best;
-}
 static size_t soft_pal_bytes(int64_t N, int64_t K) { return (size_t)N * (K / 128) * 4 * sizeof(float); }
 
 }  // namespace g2

@@ -418,6 +418,7 @@ class LayerTrainer:
                                {"params": pal, "lr": lrs["palettes"], "clip_group": 1},
                                {"params": lora, "lr": lrs["lora"], "clip_group": 1}])
         self.step_idx = 0
+        self.skipped = 0
         self._rope = {}
 
     def rope(self, seq):
@@ -447,7 +448,29 @@ class LayerTrainer:
         self.opt.step(max_norms=(1.0, 0.3))
         self.step_idx += 1
 
-    def step(self, hs):
-        loss, l_cos = self.forward_backward(hs)
+    def step(self, hs, skip_nonfinite=False):
+        """forward_backward + update. With skip_nonfinite, a non-finite loss skips the
+        backward and the update as train_qwen.py:1282-1298 does: gradients are cleared, the
+        parameters and optimizer state stay as they are, the step counter still advances and
+        `skipped` counts the skip. The check reads the loss on the host (one synchronisation
+        between forward and backward), so it is off by default."""
+        if not skip_nonfinite:
+            loss, l_cos = self.forward_backward(hs)
+            self.update()
+            return loss, l_cos
+        tau = tau_at(self.step_idx)
+        for lin in self.student.linears():
+            lin.tau = tau
+        cos, sin = self.rope(hs.shape[1])
+        t_out = self.teacher(hs, cos, sin)
+        s_out = self.student(hs, cos, sin)
+        loss, l_cos = compute_loss(s_out, t_out)
+        for p in self.logits + self.others:
+            p.grad = None
+        if not bool(torch.isfinite(loss)):
+            self.skipped += 1
+            self.step_idx += 1
+            return loss.detach(), l_cos.detach()
+        loss.backward()
         self.update()
-        return loss, l_cos
+        return loss.detach(), l_cos.detach()
