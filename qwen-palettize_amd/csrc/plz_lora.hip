@@ -14,10 +14,12 @@
 //   LDS at the end. lora_a [r, L] gives B fragments as 16-byte loads; lora_b [L, r] as eight
 //   2-byte loads (it is L2-resident and shared by the 64 rows).
 // cols_kernel  (grad_A, grad_B): the reduction index m is the activation's row, so fragments
-//   need a transpose. 64 x 256 activation tiles go global->LDS (buffer_load ... lds, 4-stage
-//   ring) and are read with ds_read_b64_tr_b16, which hands each lane 4 consecutive rows of
-//   one column. Split over M; reduce_kernel sums the split partials in a fixed order. Both
-//   weight gradients share one cols_kernel launch and one reduce_kernel launch.
+//   need a transpose. 32 x 256 activation tiles go global->LDS (buffer_load ... lds, 4-stage
+//   ring of 20 KB stages, two workgroups per CU) and are read with ds_read_b64_tr_b16, which
+//   hands each lane 4 consecutive rows of one column. Split over M (one split length for both
+//   problems, enough splits to fill every CU); reduce_kernel sums the split partials in a
+//   fixed order. Both weight gradients share one cols_kernel launch and one reduce_kernel
+//   launch.
 #include "plz_common.h"
 #include "palettize_hip.h"
 
@@ -46,6 +48,9 @@ __device__ __forceinline__ bf16x8 as_frag(uint4 v) { return __builtin_bit_cast(b
 #endif
 #ifndef PLZ_RW_U
 #define PLZ_RW_U 2
+#endif
+#ifndef PLZ_RW_CONSEC
+#define PLZ_RW_CONSEC 0
 #endif
 constexpr int RW_NG = PLZ_RW_NG;        // MFMA row groups of 16 per workgroup
 constexpr int RW_ROWS = 16 * RW_NG;     // activation rows per workgroup
@@ -76,7 +81,11 @@ __global__ __launch_bounds__(64 * RW_WAVES) void rows_kernel(const uint16_t* __r
   auto load = [&](int it, uint4 (&xv)[RW_U][RW_NG], bf16x8 (&bv)[RW_U][RG]) {
 #pragma unroll
     for (int u = 0; u < RW_U; ++u) {
+#if PLZ_RW_CONSEC
+      const int s = RW_U * (wave + RW_WAVES * it) + u;  // a wave's RW_U steps are adjacent
+#else
       const int s = wave + RW_WAVES * (RW_U * it + u);
+#endif
       const int l = 32 * s + 8 * q;  // this lane's 8 reduction elements: l .. l+7
       const bool lin = l < L;
 #pragma unroll
@@ -147,17 +156,27 @@ __global__ __launch_bounds__(64 * RW_WAVES) void rows_kernel(const uint16_t* __r
 }
 
 // ---------------------------------------------------------------------------------------
-// cols_kernel: partial[z][l][j] = scale * sum_{m in split z} X[m, l] T[m, j]
+// cols_kernel: partial[z](l, j) = scale * sum_{m in split z} X[m, l] T[m, j]
 //   X [M, L] and T [M, r] row-major. Workgroup: 256 columns l (4 waves x 64) x one M split.
 // ---------------------------------------------------------------------------------------
+#ifndef PLZ_CL_BM
+#define PLZ_CL_BM 32
+#endif
+#ifndef PLZ_CL_NS
+#define PLZ_CL_NS 4
+#endif
+#ifndef PLZ_CL_MINST
+#define PLZ_CL_MINST 16
+#endif
 constexpr int CL_L = 256;
-constexpr int CL_BM = 64;                        // rows per stage
-constexpr int CL_NS = 4;                         // LDS ring depth
-constexpr int CL_XBYTES = CL_BM * CL_L * 2;      // 32 KB
-constexpr int CL_TBYTES = 4096;                  // 64 rows x 32 ranks x 2 B
+constexpr int CL_BM = PLZ_CL_BM;                 // rows per stage
+constexpr int CL_NS = PLZ_CL_NS;                 // LDS ring depth
+constexpr int CL_XBYTES = CL_BM * CL_L * 2;      // 16 KB
+constexpr int CL_TBYTES = 4096;                  // one 1 KB copy per wave (<= 64 rows x 32 ranks x 2 B)
 constexpr int CL_STAGE = CL_XBYTES + CL_TBYTES;
-constexpr int CL_LDS = CL_NS * CL_STAGE;         // 144 KB
-constexpr int CL_LOADS = CL_XBYTES / (256 * 16) + 1;  // copies per thread per stage: 8 + 1
+constexpr int CL_LDS = CL_NS * CL_STAGE;         // 80 KB
+constexpr int CL_XI = CL_XBYTES / (256 * 16);    // X copies per thread per stage (4)
+constexpr int CL_LOADS = CL_XI + 1;              // copies per thread per stage: 4 + 1
 
 // X tile layout: row m (512 B) holds 32 chunks of 16 B; chunk c sits at c ^ xsw(m). Rows
 // m..m+3 and m+8..m+11 (what one half-wave of a transposing read touches) land their two
@@ -182,6 +201,7 @@ struct ColProb {
   float* partial;     // [Z, L, r]
   float scale;
   int L, tiles;
+  int transpose;      // partials (and output) [r, L] instead of [L, r]
   int64_t split;      // rows per M split (a multiple of CL_BM)
 };
 struct ColsArgs {
@@ -212,23 +232,24 @@ __global__ __launch_bounds__(256) void cols_kernel(const ColsArgs args) {
   const BufRsrc xr = make_rsrc(X + mb * L, (uint32_t)rows * (uint32_t)L * 2u);
   const BufRsrc tr = make_rsrc(T + mb * r, (uint32_t)rows * (uint32_t)r * 2u);
 
-  // Copies of stage s into ring slot s % CL_NS: X by 8 instructions per lane (instruction it
-  // of wave w fills LDS bytes [(8w+it) KB, +1 KB) = rows 2(8w+it), +1), T by one (RG = 1 keeps
-  // 128 chunks, waves 2-3 write an unread duplicate so that every lane issues the same count).
+  // Copies of stage s into ring slot s % CL_NS: X by CL_XI instructions per lane (instruction
+  // it of wave w fills LDS bytes [(CL_XI w + it) KB, +1 KB) = rows 2(CL_XI w + it), +1), T by
+  // one (the 2 RG CL_BM chunks of T land in the first slots; the other lanes write unread
+  // duplicates so that every lane issues the same count).
   auto issue = [&](int s) {
     lds_u8* xs = lds + (s % CL_NS) * CL_STAGE;
     const bool live = s < nst;
 #pragma unroll
-    for (int it = 0; it < CL_XBYTES / (256 * 16); ++it) {
-      const int p = (wave * 8 + it) * 64 + lane;  // physical chunk
+    for (int it = 0; it < CL_XI; ++it) {
+      const int p = (wave * CL_XI + it) * 64 + lane;  // physical chunk
       const int m = p >> 5, gc = (p & 31) ^ xsw(m);
       const int l = lb + 8 * gc;
       const uint32_t off =
           live && l < L ? ((uint32_t)(CL_BM * s + m) * (uint32_t)L + (uint32_t)l) * 2u : kBufOob;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_u8*)(xs + (wave * 8 + it) * 1024), 16, off,
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_u8*)(xs + (wave * CL_XI + it) * 1024), 16, off,
                                                0, 0, 0);
     }
-    const int p = threadIdx.x % (RG * 128);  // T chunk: row p / (2 RG), 8 ranks (p % (2 RG))
+    const int p = threadIdx.x % (RG * 2 * CL_BM);  // T chunk: row p / (2 RG), 8 ranks (p % (2 RG))
     const int m = p / (2 * RG), c = p % (2 * RG);
     const uint32_t off = live && 8 * c < r ? ((uint32_t)(CL_BM * s + m) * (uint32_t)r + 8u * c) * 2u
                                            : kBufOob;
@@ -284,29 +305,37 @@ __global__ __launch_bounds__(256) void cols_kernel(const ColsArgs args) {
   }
   __builtin_amdgcn_s_waitcnt(0);  // drain the trailing (out-of-range) copies before exit
 
-  // C fragment: rows (columns l of X) 4g..4g+3, column (rank j) i16 of each 16x16 block
+  // C fragment: rows (columns l of X) 4g..4g+3, column (rank j) i16 of each 16x16 block.
+  // The split's partial is stored in the layout of the output ([L, r], or [r, L] transposed:
+  // then a lane's 4 consecutive l are one 16-byte store), so the reduction reads it in order.
   float* P = pb.partial + (int64_t)zi * L * r;
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int cg = 0; cg < RG; ++cg) {
       const int j = 16 * cg + i16;
+      const int l0 = lb + 64 * wave + 16 * i + 4 * g;  // L is a multiple of 8: all 4 or none
+      if (j >= r || l0 >= L) continue;
+      if (pb.transpose) {
+        *reinterpret_cast<float4*>(P + (int64_t)j * L + l0) =
+            make_float4(pb.scale * acc[i][cg][0], pb.scale * acc[i][cg][1],
+                        pb.scale * acc[i][cg][2], pb.scale * acc[i][cg][3]);
+      } else {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int l = lb + 64 * wave + 16 * i + 4 * g + e;
-        if (l < L && j < r) P[(int64_t)l * r + j] = pb.scale * acc[i][cg][e];
+        for (int e = 0; e < 4; ++e) P[(int64_t)(l0 + e) * r + j] = pb.scale * acc[i][cg][e];
       }
     }
 }
 
-// out = sum_z partial[z][l][j] in z order, as bf16 or fp32, in [L, r] order or transposed to
-// [r, L]; one thread per output element, in output order (coalesced stores). Both problems of
-// a cols_kernel launch are reduced by one launch: threads [0, n0) problem a, the rest b.
+// out = sum_z partial[z] in z order, as bf16 or fp32; the partials are in the output's layout
+// ([L, r] or [r, L]), so one thread per output element reads and writes in order. Both
+// problems of a cols_kernel launch are reduced by one launch: threads [0, n0) problem a, the
+// rest b.
 struct RedProb {
   const float* partial;
   void* out;
   int64_t L;
-  int Z, transpose;
+  int Z;
 };
 __global__ void reduce_kernel(const RedProb a, const RedProb b, int64_t n0, int64_t n, int r,
                               int out_bf16) {
@@ -315,8 +344,7 @@ __global__ void reduce_kernel(const RedProb a, const RedProb b, int64_t n0, int6
   const bool second = o >= n0;
   const RedProb& p = second ? b : a;
   if (second) o -= n0;
-  const int64_t l = p.transpose ? o % p.L : o / r, j = p.transpose ? o / p.L : o % r;
-  const float* src = p.partial + l * r + j;
+  const float* src = p.partial + o;
   const int64_t zs = p.L * r;
   // the loads of 8 splits are issued together, the adds stay in z order
   float s = 0.f;
@@ -335,35 +363,56 @@ __global__ void reduce_kernel(const RedProb a, const RedProb b, int64_t n0, int6
     reinterpret_cast<float*>(p.out)[o] = s;
 }
 
-// M split of the column kernel: whole waves of 256 CUs (one workgroup per CU), each split
-// at least 48 stages deep (short splits spend their time filling the copy ring: 48 against 4
-// took the seven Qwen-4B shapes' weight gradients from 555 to 530 us); returns the split
-// length in rows (a multiple of CL_BM).
-static int64_t col_split(int64_t M, int64_t L) {
-  const int64_t tiles = (L + CL_L - 1) / CL_L;
-  int best = 1;
-  double best_eff = 0.0;
-  for (int z = 1; z <= 64 && (int64_t)z * 48 * CL_BM <= M; ++z) {
-    const int64_t wgs = tiles * z, waves = (wgs + 255) / 256;
-    const double eff = (double)wgs / (double)(waves * 256);
-    if (eff > best_eff + 0.02) {
-      best_eff = eff;
+static int cu_count() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cache[dev] == 0) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        v <= 0)
+      v = 256;
+    cache[dev] = v;
+  }
+  return cache[dev];
+}
+
+// M split of the column kernel: one split length for both problems (so every workgroup
+// streams the same rows), the z that minimises waves x (stages per split + CL_RAMP), where a
+// wave is CL_PER_CU workgroups on every CU and a split keeps at least PLZ_CL_MINST stages
+// (CL_RAMP: the stages' worth of time a workgroup spends filling its copy ring). Returns the
+// split length in rows (a multiple of CL_BM).
+constexpr int CL_PER_CU = 160 * 1024 / CL_LDS;
+#ifndef PLZ_CL_RAMP
+#define PLZ_CL_RAMP 4
+#endif
+constexpr int CL_RAMP = PLZ_CL_RAMP;
+static int64_t col_split(int64_t M, int64_t N, int64_t K) {
+  const int64_t tiles = (N + CL_L - 1) / CL_L + (K + CL_L - 1) / CL_L;
+  const int64_t stages = (M + CL_BM - 1) / CL_BM;
+  const int64_t slots = (int64_t)CL_PER_CU * cu_count();
+  int64_t best = 1;
+  double best_t = 1e300;
+  for (int64_t z = 1; z <= 64 && (z == 1 || stages / z >= PLZ_CL_MINST); ++z) {
+    const int64_t per = (stages + z - 1) / z;
+    const int64_t waves = (tiles * z + slots - 1) / slots;
+    const double t = (double)waves * (double)(per + CL_RAMP);
+    if (t < best_t) {
+      best_t = t;
       best = z;
     }
   }
-  const int64_t per = (M + best - 1) / best;
-  return (per + CL_BM - 1) / CL_BM * CL_BM;
+  return (stages + best - 1) / best * CL_BM;
 }
-static int col_splits(int64_t M, int64_t L) {
-  const int64_t s = col_split(M, L);
-  return (int)((M + s - 1) / s);
+static int col_splits(int64_t M, int64_t N, int64_t K) {
+  const int64_t s = col_split(M, N, K);
+  return s > 0 ? (int)((M + s - 1) / s) : 0;
 }
-
 
 // grad_B = scale * grad_y^T t ([N, r]) and grad_A = (x^T gt)^T ([r, K]): one cols_kernel launch
 // over both, then one reduction launch. Workspace: split partials of B, then of A.
 static size_t cols_workspace_floats(int64_t M, int64_t N, int64_t K, int r) {
-  return ((size_t)col_splits(M, N) * N + (size_t)col_splits(M, K) * K) * r;
+  return (size_t)col_splits(M, N, K) * (size_t)(N + K) * r;
 }
 static int cols(const uint16_t* x, const uint16_t* grad_y, const uint16_t* t, const uint16_t* gt,
                 float scale, void* grad_a, void* grad_b, int out_bf16, float* ws, int64_t M,
@@ -372,6 +421,7 @@ static int cols(const uint16_t* x, const uint16_t* grad_y, const uint16_t* t, co
   g.M = M;
   g.r = r;
   const int64_t Ls[2] = {N, K};
+  const int64_t split = col_split(M, N, K);
   float* part = ws;
   int nwg[2];
   RedProb red[2];
@@ -382,11 +432,12 @@ static int cols(const uint16_t* x, const uint16_t* grad_y, const uint16_t* t, co
     p.scale = i == 0 ? scale : 1.f;
     p.L = (int)Ls[i];
     p.tiles = (int)((Ls[i] + CL_L - 1) / CL_L);
-    p.split = col_split(M, Ls[i]);
+    p.transpose = i;  // grad_A is [r, K]
+    p.split = split;
     p.partial = part;
     const int z = (int)((M + p.split - 1) / p.split);
     nwg[i] = p.tiles * z;
-    red[i] = RedProb{part, i == 0 ? grad_b : grad_a, Ls[i], z, i};
+    red[i] = RedProb{part, i == 0 ? grad_b : grad_a, Ls[i], z};
     part += (size_t)z * Ls[i] * r;
   }
   g.nwg0 = nwg[0];
@@ -484,8 +535,8 @@ int plz_lora_weight_grads(const uint16_t* x, const uint16_t* grad_y, const uint1
   PLZ_REQUIRE(x && grad_y && t && gt && grad_a && grad_b, "plz_lora_weight_grads: null pointer");
   PLZ_REQUIRE(aligned16(x) && aligned16(grad_y) && aligned16(t) && aligned16(gt),
               "plz_lora_weight_grads: inputs must be 16-byte aligned");
-  const int64_t split_n = col_split(M, N), split_k = col_split(M, K);
-  PLZ_REQUIRE(split_n * N * 2 < (int64_t)1 << 31 && split_k * K * 2 < (int64_t)1 << 31,
+  const int64_t split = col_split(M, N, K);
+  PLZ_REQUIRE(split * N * 2 < (int64_t)1 << 31 && split * K * 2 < (int64_t)1 << 31,
               "plz_lora_weight_grads: M split x N or K too large");
   const size_t need = plz_lora_weight_grads_workspace(M, N, K, rank);
   if (!workspace || workspace_bytes < need) {

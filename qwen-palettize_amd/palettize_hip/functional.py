@@ -25,44 +25,6 @@ def _c(t):
     return None if t is None else t.contiguous()
 
 
-_SIDE = {}
-
-
-def side_stream(device) -> torch.cuda.Stream:
-    """A second stream per device (default priority) for the weight-gradient half of a
-    backward, which needs none of the grad_x chain's results."""
-    key = torch.device(device).index
-    if key not in _SIDE:
-        _SIDE[key] = torch.cuda.Stream(device)
-    return _SIDE[key]
-
-
-class _Overlap:
-    """Runs the enclosed launches on the side stream after everything already queued on the
-    current stream; leave() makes the current stream wait for them. Tensors made on the side
-    stream and used later on the current one are recorded on it."""
-
-    def __init__(self, device):
-        self.main = torch.cuda.current_stream(device)
-        self.side = side_stream(device)
-        self.side.wait_stream(self.main)
-
-    def __enter__(self):
-        self._ctx = torch.cuda.stream(self.side)
-        self._ctx.__enter__()
-        return self
-
-    def __exit__(self, *exc):
-        self._ctx.__exit__(*exc)
-        return False
-
-    def leave(self, *made_on_side):
-        self.main.wait_stream(self.side)
-        for t in made_on_side:
-            if t is not None:
-                t.record_stream(self.main)
-
-
 class LUTLinearFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, packed, palette, bias, lora_a, lora_b, lora_scale):
@@ -81,19 +43,17 @@ class LUTLinearFunction(torch.autograd.Function):
         x, packed, palette, lora_a, lora_b, t = ctx.saved_tensors
         gy = gy.contiguous()
         need_x, _, need_pal, need_b, need_la, need_lb, _ = ctx.needs_input_grad
-        # grad_palette (x, gy only) runs on a side stream beside gt -> grad_x
-        ov = _Overlap(gy.device)
-        with ov:
-            grad_pal = ops.lut_linear_bwd_palette(x, gy, packed) if need_pal else None
+        # one stream: grad_palette beside grad_x on a second stream measured slower (both are
+        # MFMA-bound GEMMs that fill the GPU; they only contend)
         gt = None
         if lora_a is not None and (need_x or need_la or need_lb):
             gt = ops.lora_grad_t(gy, lora_b, ctx.lora_scale)
         grad_x = ops.lut_linear_bwd_x(gy, packed, palette, gt, lora_a) if need_x else None
         grad_bias = ops.bias_grad(gy).to(ctx.bias_dtype) if (ctx.has_bias and need_b) else None
+        grad_pal = ops.lut_linear_bwd_palette(x, gy, packed) if need_pal else None
         grad_a = grad_b = None
         if lora_a is not None and (need_la or need_lb):
             grad_a, grad_b = ops.lora_weight_grads(x, gy, t, gt, 1.0, out_dtype=lora_a.dtype)
-        ov.leave(grad_pal)
         return grad_x, None, grad_pal, grad_bias, grad_a, grad_b, None
 
 

@@ -33,7 +33,6 @@ from torch import Tensor
 
 from . import ops
 from ._lib import PLZ_W_HARD_NOISY, PLZ_W_SOFT
-from .functional import _Overlap
 
 GROUP_SIZE = 256
 
@@ -164,15 +163,10 @@ class CUDAFusedLUTLinear(torch.autograd.Function):
         xp, packed, pal = ctx.saved_tensors
         grad_y = grad_y.contiguous()
         grad_x = grad_pal = grad_bias = None
-        ov = _Overlap(grad_y.device)  # grad_palette beside grad_x on a second stream
-        g = None
-        with ov:
-            if ctx.needs_input_grad[1]:
-                g = ops.lut_linear_bwd_palette(xp, grad_y, packed)
         if ctx.needs_input_grad[0]:
             grad_x = ops.lut_linear_bwd_x(grad_y, packed, pal)[:, : ctx.K].contiguous()
-        ov.leave(g)
-        if g is not None:
+        if ctx.needs_input_grad[1]:
+            g = ops.lut_linear_bwd_palette(xp, grad_y, packed)
             grad_pal = palette_grad_to_reference(g, ctx.group_size, ctx.n_groups).to(ctx.pal_dtype)
         if ctx.bias_requires_grad:
             grad_bias = ops.bias_grad(grad_y).to(ctx.bias_dtype)
