@@ -4,10 +4,9 @@ One step = one hard LUT-linear forward + backward (grad_x, grad_palette, LoRA gr
 the seven Qwen-4B linear shapes at M = 16384 tokens (batch 32 x seq 512),
 straight-through through the frozen 2-bit indices, LoRA rank 16 (32 on o and down).
 `value` = sum over shapes of 6*M*K*N FLOP / step time (LoRA FLOP excluded, as in BASELINE),
-the step timed with each linear's grad_palette GEMM and LoRA weight grads on a second stream
-beside its forward / grad_x chain (they need only x, grad_y, t and gt). The per-kernel
-rooflines come from the same K steps run again on one stream with HIP events around every
-launch, so each kernel is timed alone.
+the step's kernels issued on one stream as the library's backward issues them. The
+per-kernel rooflines come from the same K steps run again with HIP events around every
+launch.
 
 Also reported (same JSON line): the decode GEMV of config 2 (36 layers x 7 linears, M in
 {1, 4, 16}, one grouped launch per M) in GB/s of packed indices + palettes, the roofline of
@@ -72,35 +71,6 @@ class HardStep:
                                    a=a, b=b))
         self.flop = sum(6.0 * M_TRAIN * it["K"] * it["N"] for it in self.items)
         self.events = None
-        self.side = torch.cuda.Stream(device)  # default priority
-
-    def run_overlapped(self):
-        """The step on two streams: per linear, the grad_palette GEMM runs on a second stream
-        next to the forward / grad_x chain (it needs only x and grad_y), and the LoRA weight
-        gradients follow it there once t and gt exist. Same kernels and results as run(); one
-        kernel's last partial wave and the HBM-bound LoRA passes then share the GPU with the
-        other stream's work (or contend with it: the bench times both schedules)."""
-        import torch
-        from palettize_hip import ops
-        main = torch.cuda.current_stream()
-        side = self.side
-        side.wait_stream(main)
-        for it in self.items:
-            x, gy, a, b = it["x"], it["gy"], it["a"], it["b"]
-            with torch.cuda.stream(side):
-                ops.lut_linear_bwd_palette(x, gy, it["packed"])
-            t = ops.lora_project(x, a, 1.0)
-            ops.lut_linear_fwd(x, it["packed"], it["pal"], None, t, b)
-            gt = ops.lora_grad_t(gy, b, 1.0)
-            ops.lut_linear_bwd_x(gy, it["packed"], it["pal"], gt, a)
-            ready = torch.cuda.Event()
-            ready.record(main)
-            with torch.cuda.stream(side):
-                side.wait_event(ready)
-                ops.lora_weight_grads(x, gy, t, gt, 1.0, out_dtype=torch.bfloat16)
-                t.record_stream(side)
-                gt.record_stream(side)
-        main.wait_stream(side)
 
     def run(self, timed=False):
         import torch
@@ -453,31 +423,22 @@ def main():
     if args.only in (None, "hard"):
         _log("hard: building inputs")
         step = HardStep(dev)
-        schedules = {"one_stream": step.run, "two_streams": step.run_overlapped}
         for _ in range(args.warmup):
-            for fn in schedules.values():
-                fn()
+            step.run()
         torch.cuda.synchronize()
+        # value: K steps bracketed by one event pair (no events between kernels: each one costs
+        # a few microseconds of stream time). One stream, as the library's backward runs: the
+        # grad_palette GEMM on a second stream beside grad_x measured slower (both GEMMs fill
+        # the GPU and only contend).
         t0 = torch.cuda.Event(enable_timing=True)
         t1 = torch.cuda.Event(enable_timing=True)
-
-        def timed_steps(fn, n):  # n steps bracketed by one event pair (no events between kernels)
-            torch.cuda.synchronize()
-            t0.record()
-            for _ in range(n):
-                fn()
-            t1.record()
-            torch.cuda.synchronize()
-            return t0.elapsed_time(t1) / n
-
-        # the schedule is chosen on separate calibration steps, then K steps of it are timed for
-        # `value`; the other schedule's K steps are reported beside it
-        calib = {k: timed_steps(fn, 3) for k, fn in schedules.items()}
-        best = min(calib, key=calib.get)
-        ms = timed_steps(schedules[best], args.steps)
+        t0.record()
+        for _ in range(args.steps):
+            step.run()
+        t1.record()
+        torch.cuda.synchronize()
+        ms = t0.elapsed_time(t1) / args.steps
         tflops = step.flop / (ms * 1e-3) / 1e12
-        other = "two_streams" if best == "one_stream" else "one_stream"
-        ms_other = timed_steps(schedules[other], args.steps)
         # per-kernel launch durations: one stream with an event pair around every kernel (no
         # other kernel shares the GPU)
         step.events = {}
@@ -487,8 +448,6 @@ def main():
         kr = kernel_rooflines(step.events)
         dom = max((k for k in kr if k != "lora"), key=lambda k: kr[k]["ms"])
         out.update(value=round(tflops, 2), ms_per_step=round(ms, 3))
-        out["schedule"] = best
-        out["ms_per_step_schedules"] = {best: round(ms, 3), other: round(ms_other, 3)}
         out["roofline"] = {"bound": "mfma", "kernel": KERNEL_NAMES[dom],
                            "achieved": round(kr[dom]["tflops"], 1), "peak": PEAK_BF16_TFLOPS,
                            "unit": "TFLOP/s", "frac": round(kr[dom]["tflops"] / PEAK_BF16_TFLOPS, 4),

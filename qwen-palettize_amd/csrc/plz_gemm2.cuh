@@ -35,6 +35,25 @@ constexpr int WAVES_I = 2, WAVES_J = 4;
 constexpr int WT_I = TILE / WAVES_I / 32;  // 32x32 MFMA blocks per wave along i (4)
 constexpr int WT_J = TILE / WAVES_J / 32;  // ... along j (2)
 constexpr int COPY_INSTS = TILE * BK / 8 / NTHR;  // 16-byte copies per thread per operand (4)
+constexpr int RING_SLOTS = 5;  // operand tiles in the dW kernels' copy ring (5 x 32 KB)
+
+// Workgroup barrier after this wave's LDS reads have completed, without the release fence of
+// __syncthreads() (which waits for every outstanding copy): the caller's wait_vmcnt decides
+// which copies must have landed. The empty asm statements keep the compiler from moving
+// memory accesses across it.
+__device__ __forceinline__ void stage_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xF | (3 << 14) | (7 << 4));  // lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// wait until at most N vector-memory operations of this wave are outstanding
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
 
 typedef short v4i16 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) v4i16 lds_v4i16;

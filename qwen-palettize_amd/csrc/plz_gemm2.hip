@@ -115,8 +115,15 @@ __device__ __forceinline__ void mma_stage_sync(const lds_u8* a_s, const lds_u8* 
   }
 }
 
+// a_s, b_s: this stage's tiles; na_s, nb_s: the LDS slots that dma(na_s, nb_s) and
+// fill(part, nb_s) write for a later stage. All four are distinct slots, and saying so
+// (__restrict__) lets the compiler see that the fragment reads cannot alias the copies in
+// flight: without it, it waits for every outstanding copy before the first LDS read that
+// follows them, one k-step after issuing the next stage's copies.
 template <bool A_COL, bool B_COL, bool FILL, typename Dma, typename Fill>
-__device__ __forceinline__ void mma_stage(const lds_u8* a_s, const lds_u8* b_s,
+__device__ __forceinline__ void mma_stage(const lds_u8* __restrict__ a_s,
+                                          const lds_u8* __restrict__ b_s,
+                                          lds_u8* __restrict__ na_s, lds_u8* __restrict__ nb_s,
                                           f32x16 (&acc)[WT_I][WT_J], int wi, int wj, int lane,
                                           Dma&& dma, Fill&& fill) {
   // LDS read instructions per k-step: a row fragment is one ds_read_b128, a col fragment two
@@ -131,14 +138,14 @@ __device__ __forceinline__ void mma_stage(const lds_u8* a_s, const lds_u8* b_s,
   load_frags<A_COL, B_COL>(a_s, b_s, 0, wi, wj, lane, a0, b0);
   __builtin_amdgcn_sched_barrier(0);
   load_frags<A_COL, B_COL>(a_s, b_s, 1, wi, wj, lane, a1, b1);
-  dma();
+  dma(na_s, nb_s);
   mma_kstep(acc, a0, b0);
-  fill(0);
+  fill(0, nb_s);
   interleave_kstep<NREAD, NDMA, NV, NW>();
   __builtin_amdgcn_sched_barrier(0);
   load_frags<A_COL, B_COL>(a_s, b_s, 2, wi, wj, lane, a0, b0);
   mma_kstep(acc, a1, b1);
-  fill(1);
+  fill(1, nb_s);
   interleave_kstep<NREAD, 0, NV, NW>();
   __builtin_amdgcn_sched_barrier(0);
   load_frags<A_COL, B_COL>(a_s, b_s, 3, wi, wj, lane, a1, b1);
@@ -183,7 +190,10 @@ __device__ __forceinline__ void dq_final(const DqPart& d, uint32_t (&out)[8]) {
   out[7] = perm(d.b[3], d.b[2], 0x07060302u);
 }
 template <typename Dma>
-__device__ __forceinline__ void mma_stage_lutreg(const lds_u8* a_s, const lds_u8* b_s,
+__device__ __forceinline__ void mma_stage_lutreg(const lds_u8* __restrict__ a_s,
+                                                 const lds_u8* __restrict__ b_s,
+                                                 lds_u8* __restrict__ na_s,
+                                                 lds_u8* __restrict__ nb_s,
                                                  f32x16 (&acc)[WT_I][WT_J], int wi, int wj,
                                                  int lane, Dma&& dma) {
   typedef __attribute__((address_space(3))) const u32x4 lds_u32x4;
@@ -235,7 +245,7 @@ __device__ __forceinline__ void mma_stage_lutreg(const lds_u8* a_s, const lds_u8
     mfma(i, 1, a0[i], w[0][1], 0);
     dq_part(word(1, 0), t[0], d, i);
     if (i == WT_I - 1) dq_final(d, w[1][0]);
-    if (i == 0) dma();
+    if (i == 0) dma(na_s, nb_s);
     __builtin_amdgcn_sched_barrier(0);
   }
   // (p0, s1, j0..1) x 8 with word (p1, j1) and the A fragments of (p1, s0)
@@ -447,6 +457,7 @@ __global__ __launch_bounds__(NTHR) void gemm2_kernel(const Args g) {
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wi = wave / WAVES_J, wj = wave % WAVES_J;
+  constexpr bool RING5 = KA == OP_COL && KB == OP_COL;
 
   f32x16 acc[WT_I][WT_J];
 #pragma unroll
@@ -488,11 +499,6 @@ __global__ __launch_bounds__(NTHR) void gemm2_kernel(const Args g) {
     else if (KB == OP_COL) tile_copy(Bs, dB, (uint32_t)(r0 * g.ldb * 2));
     else if (KB == OP_LUT_REG) copy_lut_raw(Bs, dL, r0);
   };
-  auto issue_full = [&](int s, int kt) {
-    lds_u8* As = lbase + s * 2 * TILE_BYTES;
-    lds_u8* Bs = As + TILE_BYTES;
-    copy_stage(As, Bs, rbeg + (int64_t)kt * BK);
-  };
   auto issue = [&](int s, int kt) {
     lds_u8* As = lbase + s * 2 * TILE_BYTES;
     lds_u8* Bs = As + TILE_BYTES;
@@ -519,6 +525,53 @@ __global__ __launch_bounds__(NTHR) void gemm2_kernel(const Args g) {
   constexpr bool LUT = KB == OP_LUT_ROW || KB == OP_LUT_COL;
   // Full stages run through the pipelined loop (one MFMA body per kernel kind); the
   // partial stage and the LoRA stage follow, synchronously, through buffer 0.
+  if constexpr (RING5) {
+    // Both operands are copied (32 KB each per stage) into a ring of 5 operand slots. The
+    // operand that changes between consecutive tiles of the walk (A when tile-rows are walked
+    // within a tile-column, else B) misses L2 more often and is copied two stages ahead, the
+    // other one stage ahead. Copy c of the sequence lead_0, other_0, lead_1, other_1, ... goes
+    // to slot c % 5: at stage s the slots of lead_s, other_s, lead_s+1, other_s+1 and lead_s+2
+    // are distinct, and the two copies issued during stage s (other_s+1, then lead_s+2) reuse
+    // the slots of stage s-1. Past the last stage the copies repeat stage nfull-1 into those
+    // free slots, so every stage issues the same instructions.
+    auto ring = [&](auto lead_tag) {
+      constexpr bool A_LEADS = decltype(lead_tag)::value;
+      auto slot = [&](bool is_a, int kt) -> lds_u8* {
+        return lbase + ((2 * kt + (is_a == A_LEADS ? 0 : 1)) % RING_SLOTS) * TILE_BYTES;
+      };
+      // copy of operand a (else b) of stage kt (past the last stage: of stage nfull-1) to dst
+      auto copy = [&](bool a, int kt, lds_u8* dst) {
+        const int ks = kt < nfull ? kt : nfull - 1;
+        const int64_t r0 = rbeg + (int64_t)ks * BK;
+        if (a) tile_copy(dst, dA, (uint32_t)(r0 * g.lda * 2));
+        else tile_copy(dst, dB, (uint32_t)(r0 * g.ldb * 2));
+      };
+      if (nfull > 0) {
+        copy(A_LEADS, 0, slot(A_LEADS, 0));
+        copy(!A_LEADS, 0, slot(!A_LEADS, 0));
+        __builtin_amdgcn_sched_barrier(0);
+        copy(A_LEADS, 1, slot(A_LEADS, 1));
+        wait_vmcnt<COPY_INSTS>();  // stage 0 has landed; lead_1 may be in flight
+        stage_barrier();
+      }
+      for (int kt = 0; kt < nfull; ++kt) {
+        auto dma = [&](lds_u8* other_next, lds_u8* lead_next2) {
+          copy(!A_LEADS, kt + 1, other_next);
+          __builtin_amdgcn_sched_barrier(0);  // other_kt+1 is issued before lead_kt+2
+          copy(A_LEADS, kt + 2, lead_next2);
+        };
+        mma_stage<A_COL, B_COL, false>(slot(true, kt), slot(false, kt), slot(!A_LEADS, kt + 1),
+                                       slot(A_LEADS, kt + 2), acc, wi, wj, lane, dma,
+                                       [](int, lds_u8*) {});
+        wait_vmcnt<COPY_INSTS>();  // stage kt+1 has landed; lead_kt+2 may be in flight
+        stage_barrier();
+      }
+    };
+    if (g.group < 0) ring(std::true_type{});
+    else ring(std::false_type{});
+    __builtin_amdgcn_s_waitcnt(0);  // the repeated copies past the last stage
+    __syncthreads();
+  } else {
   if (nfull > 0) {
     issue(0, 0);
     if (LUT) {
@@ -542,21 +595,24 @@ __global__ __launch_bounds__(NTHR) void gemm2_kernel(const Args g) {
     // copies of stage kt+1 are issued inside the first k-step (interleaved with its MFMAs);
     // the last stage reloads itself into the idle buffer, which keeps the instruction stream
     // identical (the stage-end wait covers the copies before the buffers are reused)
-    auto dma = [&]() { issue_full(cur ^ 1, more ? kt + 1 : kt); };
+    lds_u8* An = lbase + (cur ^ 1) * 2 * TILE_BYTES;
+    const int64_t r_next = rbeg + (int64_t)(more ? kt + 1 : kt) * BK;
+    auto dma = [&](lds_u8* na, lds_u8* nb) { copy_stage(na, nb, r_next); };
     if constexpr (KB == OP_LUT_REG) {
-      mma_stage_lutreg(As, As + TILE_BYTES, acc, wi, wj, lane, dma);
+      mma_stage_lutreg(As, As + TILE_BYTES, An, An + TILE_BYTES, acc, wi, wj, lane, dma);
     } else {
       // the next stage's palette dequantisation runs between this stage's MFMA groups
-      uint4* Bn = (uint4*)(lbase + (cur ^ 1) * 2 * TILE_BYTES + TILE_BYTES);
-      mma_stage<A_COL, B_COL, LUT>(As, As + TILE_BYTES, acc, wi, wj, lane, dma, [&](int part) {
+      mma_stage<A_COL, B_COL, LUT>(As, As + TILE_BYTES, An, An + TILE_BYTES, acc, wi, wj, lane,
+                                   dma, [&](int part, lds_u8* nb) {
         if (!LUT || !more) return;
-        if (KB == OP_LUT_ROW) lut_row_store_part(Bn, lr_cur, part);
-        if (KB == OP_LUT_COL) lut_col_store_part(Bn, lr_cur, part);
+        if (KB == OP_LUT_ROW) lut_row_store_part((uint4*)nb, lr_cur, part);
+        if (KB == OP_LUT_COL) lut_col_store_part((uint4*)nb, lr_cur, part);
       });
     }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
   }
+  }  // RING5
   for (int kt = nfull; kt < nst; ++kt) {
     issue(0, kt);  // register copies (zero-filled past the end)
     __builtin_amdgcn_s_waitcnt(0);
@@ -715,6 +771,7 @@ __global__ __launch_bounds__(NTHR) void tail_reduce_kernel(const Args g) {
 }
 
 constexpr size_t kLds = 256 * 528;  // 132 KB: two pipeline stages (128 KB) or the padded bf16 output tile
+constexpr size_t kLdsRing5 = RING_SLOTS * TILE_BYTES;  // 160 KB: the dW kernels' 5-slot ring
 
 template <int KA, int KB, int EPI>
 static int launch(Args g, int splits, hipStream_t stream, const char* what) {
@@ -724,7 +781,8 @@ static int launch(Args g, int splits, hipStream_t stream, const char* what) {
   if (g.group == 0) g.group = 8;
   auto kern = gemm2_kernel<KA, KB, EPI>;
   static uint64_t lds_done = 0;
-  if (int rc = reserve_lds((const void*)kern, kLds, lds_done, what)) return rc;
+  const size_t lds = KA == OP_COL && KB == OP_COL ? kLdsRing5 : kLds;
+  if (int rc = reserve_lds((const void*)kern, lds, lds_done, what)) return rc;
   const int64_t tiles = (int64_t)g.tiles_i * g.tiles_j;
   if (tiles == 0 || splits == 0) return PLZ_OK;
   // the copies address each operand through a 32-bit buffer offset
@@ -738,7 +796,7 @@ static int launch(Args g, int splits, hipStream_t stream, const char* what) {
   }
   const bool tail = EPI == EPI_BF16 && g.tail_split > 1;
   const int64_t gx = tail ? g.tail_first + (tiles - g.tail_first) * g.tail_split : tiles;
-  hipLaunchKernelGGL(kern, dim3((unsigned)gx, 1, (unsigned)splits), dim3(NTHR), kLds, stream, g);
+  hipLaunchKernelGGL(kern, dim3((unsigned)gx, 1, (unsigned)splits), dim3(NTHR), lds, stream, g);
   int rc = check_launch(what);
   if (rc != PLZ_OK || !tail) return rc;
   static uint64_t rlds_done = 0;

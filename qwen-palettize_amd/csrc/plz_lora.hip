@@ -236,8 +236,7 @@ __global__ __launch_bounds__(256) void cols_kernel(const ColsArgs args) {
   // it of wave w fills LDS bytes [(CL_XI w + it) KB, +1 KB) = rows 2(CL_XI w + it), +1), T by
   // one (the 2 RG CL_BM chunks of T land in the first slots; the other lanes write unread
   // duplicates so that every lane issues the same count).
-  auto issue = [&](int s) {
-    lds_u8* xs = lds + (s % CL_NS) * CL_STAGE;
+  auto issue = [&](int s, lds_u8* xs) {  // xs: ring slot s % CL_NS
     const bool live = s < nst;
 #pragma unroll
     for (int it = 0; it < CL_XI; ++it) {
@@ -264,13 +263,11 @@ __global__ __launch_bounds__(256) void cols_kernel(const ColsArgs args) {
     for (int cg = 0; cg < RG; ++cg) acc[i][cg] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const int i16 = lane & 15, g = lane >> 4;
-#pragma unroll
-  for (int s = 0; s < CL_NS - 1; ++s) issue(s);
-  for (int s = 0; s < nst; ++s) {
-    wait_vmcnt<CL_LOADS*(CL_NS - 2)>();  // this lane's copies of stage s have landed
-    lds_barrier();                         // everyone's have; slot (s-1) % CL_NS is free
-    issue(s + CL_NS - 1);
-    const lds_u8* xs = lds + (s % CL_NS) * CL_STAGE;
+  // One stage: the copies of stage s + CL_NS - 1 into slot ws, then the MFMAs on slot xs. The
+  // two slots are distinct, and saying so (__restrict__) keeps the compiler from waiting for
+  // the copies just issued before the first read of xs.
+  auto step = [&](int s, const lds_u8* __restrict__ xs, lds_u8* __restrict__ ws) {
+    issue(s + CL_NS - 1, ws);
     const lds_u8* ts = xs + CL_XBYTES;
 #pragma unroll
     for (int ks = 0; ks < CL_BM / 32; ++ks) {
@@ -302,6 +299,13 @@ __global__ __launch_bounds__(256) void cols_kernel(const ColsArgs args) {
 #pragma unroll
         for (int cg = 0; cg < RG; ++cg) acc[i][cg] = mfma16(a[i], b[cg], acc[i][cg]);
     }
+  };
+#pragma unroll
+  for (int s = 0; s < CL_NS - 1; ++s) issue(s, lds + s * CL_STAGE);
+  for (int s = 0; s < nst; ++s) {
+    wait_vmcnt<CL_LOADS*(CL_NS - 2)>();  // this lane's copies of stage s have landed
+    lds_barrier();                         // everyone's have; slot (s-1) % CL_NS is free
+    step(s, lds + (s % CL_NS) * CL_STAGE, lds + ((s + CL_NS - 1) % CL_NS) * CL_STAGE);
   }
   __builtin_amdgcn_s_waitcnt(0);  // drain the trailing (out-of-range) copies before exit
 
