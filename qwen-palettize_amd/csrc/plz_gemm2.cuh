@@ -35,7 +35,7 @@ constexpr int WAVES_I = 2, WAVES_J = 4;
 constexpr int WT_I = TILE / WAVES_I / 32;  // 32x32 MFMA blocks per wave along i (4)
 constexpr int WT_J = TILE / WAVES_J / 32;  // ... along j (2)
 constexpr int COPY_INSTS = TILE * BK / 8 / NTHR;  // 16-byte copies per thread per operand (4)
-constexpr int RING_SLOTS = 5;  // operand tiles in the dW kernels' copy ring (5 x 32 KB)
+constexpr int RING_SLOTS = 5;  // operand tiles in a copy ring (5 x 32 KB = 160 KB of LDS)
 
 // Workgroup barrier after this wave's LDS reads have completed, without the release fence of
 // __syncthreads() (which waits for every outstanding copy): the caller's wait_vmcnt decides

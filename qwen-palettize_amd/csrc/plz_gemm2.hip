@@ -457,7 +457,11 @@ __global__ __launch_bounds__(NTHR) void gemm2_kernel(const Args g) {
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wi = wave / WAVES_J, wj = wave % WAVES_J;
+  // copy rings: dW kernels (both operands transposed) -> 5 operand slots; grad_x (B written by
+  // this workgroup's VALU) -> 3 A slots + 2 B slots; the others -> two stage pairs (the dense
+  // kernels measured slower with the 5-slot ring)
   constexpr bool RING5 = KA == OP_COL && KB == OP_COL;
+  constexpr bool RING3A = KB == OP_LUT_COL;
 
   f32x16 acc[WT_I][WT_J];
 #pragma unroll
@@ -527,8 +531,8 @@ __global__ __launch_bounds__(NTHR) void gemm2_kernel(const Args g) {
   // partial stage and the LoRA stage follow, synchronously, through buffer 0.
   if constexpr (RING5) {
     // Both operands are copied (32 KB each per stage) into a ring of 5 operand slots. The
-    // operand that changes between consecutive tiles of the walk (A when tile-rows are walked
-    // within a tile-column, else B) misses L2 more often and is copied two stages ahead, the
+    // operand that changes between consecutive tiles of the walk (B when consecutive tiles
+    // share their tile-row, else A) misses L2 more often and is copied two stages ahead, the
     // other one stage ahead. Copy c of the sequence lead_0, other_0, lead_1, other_1, ... goes
     // to slot c % 5: at stage s the slots of lead_s, other_s, lead_s+1, other_s+1 and lead_s+2
     // are distinct, and the two copies issued during stage s (other_s+1, then lead_s+2) reuse
@@ -543,8 +547,8 @@ __global__ __launch_bounds__(NTHR) void gemm2_kernel(const Args g) {
       auto copy = [&](bool a, int kt, lds_u8* dst) {
         const int ks = kt < nfull ? kt : nfull - 1;
         const int64_t r0 = rbeg + (int64_t)ks * BK;
-        if (a) tile_copy(dst, dA, (uint32_t)(r0 * g.lda * 2));
-        else tile_copy(dst, dB, (uint32_t)(r0 * g.ldb * 2));
+        if (a) tile_copy(dst, dA, (uint32_t)(KA == OP_ROW ? r0 * 2 : r0 * g.lda * 2));
+        else tile_copy(dst, dB, (uint32_t)(KB == OP_ROW ? r0 * 2 : r0 * g.ldb * 2));
       };
       if (nfull > 0) {
         copy(A_LEADS, 0, slot(A_LEADS, 0));
@@ -567,8 +571,46 @@ __global__ __launch_bounds__(NTHR) void gemm2_kernel(const Args g) {
         stage_barrier();
       }
     };
-    if (g.group < 0) ring(std::true_type{});
+    if (g.group != 1) ring(std::true_type{});
     else ring(std::false_type{});
+    __builtin_amdgcn_s_waitcnt(0);  // the repeated copies past the last stage
+    __syncthreads();
+  } else if constexpr (RING3A) {
+    // grad_x: the A tiles (grad_y) are copied two stages ahead through 3 slots; the B tiles
+    // (dequantised W^T) are written by the workgroup's VALU one stage ahead into 2 slots, from
+    // palette words loaded into registers two stages ahead. Past the last stage the A copies
+    // repeat stage nfull-1 into the free slot.
+    lds_u8* const bbase = lbase + 3 * TILE_BYTES;
+    auto aslot = [&](int kt) { return lbase + (kt % 3) * TILE_BYTES; };
+    auto bslot = [&](int kt) { return bbase + (kt & 1) * TILE_BYTES; };
+    auto copy_a = [&](int kt, lds_u8* dst) {
+      const int ks = kt < nfull ? kt : nfull - 1;
+      tile_copy(dst, dA, (uint32_t)((rbeg + (int64_t)ks * BK) * 2));
+    };
+    if (nfull > 0) {
+      lut_load(0, lr_cur);
+      if (nfull > 1) lut_load(1, lr_next);
+      __builtin_amdgcn_sched_barrier(0);  // the palette words are issued before the copies
+      copy_a(0, aslot(0));
+      copy_a(1, aslot(1));
+      lut_col_store((uint4*)bslot(0), lr_cur);
+      wait_vmcnt<COPY_INSTS>();  // A_0 has landed; A_1 may be in flight
+      stage_barrier();
+    }
+    for (int kt = 0; kt < nfull; ++kt) {
+      const bool more = kt + 1 < nfull;
+      lr_cur = lr_next;  // stage kt+1's words, loaded a stage ago
+      if (kt + 2 < nfull) lut_load(kt + 2, lr_next);
+      __builtin_amdgcn_sched_barrier(0);  // the palette words are issued before the copies
+      mma_stage<A_COL, B_COL, true>(
+          aslot(kt), bslot(kt), aslot(kt + 2), bslot(kt + 1), acc, wi, wj, lane,
+          [&](lds_u8* na, lds_u8*) { copy_a(kt + 2, na); },
+          [&](int part, lds_u8* nb) {
+            if (more) lut_col_store_part((uint4*)nb, lr_cur, part);
+          });
+      wait_vmcnt<COPY_INSTS>();  // A_kt+1 (and the words of stage kt+2) landed; A_kt+2 may not
+      stage_barrier();           // also orders the B tile of stage kt+1 before its reads
+    }
     __builtin_amdgcn_s_waitcnt(0);  // the repeated copies past the last stage
     __syncthreads();
   } else {
@@ -771,7 +813,7 @@ __global__ __launch_bounds__(NTHR) void tail_reduce_kernel(const Args g) {
 }
 
 constexpr size_t kLds = 256 * 528;  // 132 KB: two pipeline stages (128 KB) or the padded bf16 output tile
-constexpr size_t kLdsRing5 = RING_SLOTS * TILE_BYTES;  // 160 KB: the dW kernels' 5-slot ring
+constexpr size_t kLdsRing = RING_SLOTS * TILE_BYTES;  // 160 KB: 5 operand slots (or 3 + 2)
 
 template <int KA, int KB, int EPI>
 static int launch(Args g, int splits, hipStream_t stream, const char* what) {
@@ -781,7 +823,7 @@ static int launch(Args g, int splits, hipStream_t stream, const char* what) {
   if (g.group == 0) g.group = 8;
   auto kern = gemm2_kernel<KA, KB, EPI>;
   static uint64_t lds_done = 0;
-  const size_t lds = KA == OP_COL && KB == OP_COL ? kLdsRing5 : kLds;
+  const size_t lds = (KA == OP_COL && KB == OP_COL) || KB == OP_LUT_COL ? kLdsRing : kLds;
   if (int rc = reserve_lds((const void*)kern, lds, lds_done, what)) return rc;
   const int64_t tiles = (int64_t)g.tiles_i * g.tiles_j;
   if (tiles == 0 || splits == 0) return PLZ_OK;
