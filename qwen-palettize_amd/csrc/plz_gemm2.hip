@@ -458,10 +458,11 @@ __global__ __launch_bounds__(NTHR) void gemm2_kernel(const Args g) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wi = wave / WAVES_J, wj = wave % WAVES_J;
   // copy rings: dW kernels (both operands transposed) -> 5 operand slots; grad_x (B written by
-  // this workgroup's VALU) -> 3 A slots + 2 B slots; the others -> two stage pairs (the dense
-  // kernels measured slower with the 5-slot ring)
+  // this workgroup's VALU) -> 3 A slots + 2 B slots; the forward -> 3 stage slots; the others
+  // -> two stage pairs (the dense kernels measured slower with the 5-slot ring)
   constexpr bool RING5 = KA == OP_COL && KB == OP_COL;
   constexpr bool RING3A = KB == OP_LUT_COL;
+  constexpr bool RING3 = KB == OP_LUT_REG;
 
   f32x16 acc[WT_I][WT_J];
 #pragma unroll
@@ -610,6 +611,30 @@ __global__ __launch_bounds__(NTHR) void gemm2_kernel(const Args g) {
           });
       wait_vmcnt<COPY_INSTS>();  // A_kt+1 (and the words of stage kt+2) landed; A_kt+2 may not
       stage_barrier();           // also orders the B tile of stage kt+1 before its reads
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // the repeated copies past the last stage
+    __syncthreads();
+  } else if constexpr (RING3) {
+    // forward: a stage is the x tile (32 KB) and the raw words and palettes (8 KB); both are
+    // copied two stages ahead through 3 stage slots (120 KB). Past the last stage the copies
+    // repeat stage nfull-1 into the free slot.
+    constexpr int SLOT = TILE_BYTES + 8192, PER_STAGE = COPY_INSTS + 1;
+    auto sa = [&](int kt) { return lbase + (kt % 3) * SLOT; };
+    auto copy = [&](int kt, lds_u8* a, lds_u8* b) {
+      const int ks = kt < nfull ? kt : nfull - 1;
+      copy_stage(a, b, rbeg + (int64_t)ks * BK);
+    };
+    if (nfull > 0) {
+      copy(0, sa(0), sa(0) + TILE_BYTES);
+      copy(1, sa(1), sa(1) + TILE_BYTES);
+      wait_vmcnt<PER_STAGE>();  // stage 0 has landed; stage 1 may be in flight
+      stage_barrier();
+    }
+    for (int kt = 0; kt < nfull; ++kt) {
+      mma_stage_lutreg(sa(kt), sa(kt) + TILE_BYTES, sa(kt + 2), sa(kt + 2) + TILE_BYTES, acc,
+                       wi, wj, lane, [&](lds_u8* na, lds_u8* nb) { copy(kt + 2, na, nb); });
+      wait_vmcnt<PER_STAGE>();  // stage kt+1 has landed; stage kt+2 may be in flight
+      stage_barrier();
     }
     __builtin_amdgcn_s_waitcnt(0);  // the repeated copies past the last stage
     __syncthreads();
