@@ -5,26 +5,25 @@
 // 0.5 bit of fp32 palette per weight are streamed once, and everything else is arranged so
 // that the stream never stops:
 //
-// * Persistent workgroups, a few per CU (as many as the LDS ring allows, at most 16 waves).
-//   The work items (128 rows of one linear, all of K) of a launch are cut into one contiguous
-//   range per workgroup, balanced by bytes (K per item).
+// * Persistent workgroups, a few per CU. The work items (128 rows of one linear, all of K) of
+//   a launch are cut into one contiguous range per workgroup, balanced by bytes (K per item).
 // * A workgroup walks its items as one sequence of stages (128 rows x 256 k = one palette
-//   group). Each stage's packed indices, palettes and x slice go global->LDS by
-//   buffer_load ... lds (1 KB per wave instruction, whole cache lines, no VGPRs), NS-1 stages
-//   ahead in an NS-slot ring, across item boundaries -- the loads of the next item are in
-//   flight while this one finishes. Palettes may come prepacked per item and stage (2 KB
-//   contiguous, plz_gemv_pack_palettes) instead of 16 B per row strided by K/256 groups, and
-//   the packed indices may come in the decode layout (plz_gemv_pack_indices): each stage's
-//   8 KB contiguous in the order the waves read it, every word's 2-bit fields permuted so that
-//   the dequantiser emits natural k order (the x fragments are then plain 16-byte reads).
+//   group), with the loads of the next item in flight while this one finishes.
 // * Wave w owns rows 32w..32w+31 of the item (two MFMA row blocks of 16). Lane (row n%16,
 //   quarter q) dequantises 4 consecutive packed words (64 k) of its row per block and stage
 //   through v_perm_b32 byte tables into bf16 fragments (in a permuted k order that the x
 //   fragments repeat); v_mfma_f32_16x16x32_bf16 computes C[n][m] for all M <= 16 tokens at
 //   once (fragment lanes of tokens m >= M read token M-1; their columns are never stored).
 //   x fragments come from the stage's x slice in LDS and serve both row blocks.
-// * LDS layouts are XOR-swizzled on the global side of the copies so that every fragment
-//   read is bank-conflict free.
+// * Native layouts (gemv_kernel): each stage's packed indices, palettes and x slice go
+//   global->LDS by buffer_load ... lds (1 KB per wave instruction, whole cache lines), NS-1
+//   stages ahead in an NS-slot ring; LDS layouts are XOR-swizzled on the global side of the
+//   copies so that every fragment read is bank-conflict free.
+// * Decode layouts (plz_gemv_pack_indices, plz_gemv_pack_palettes; gemv_reg_kernel): each
+//   stage's 8 KB of words lie contiguous in the order the lanes read them, every word's 2-bit
+//   fields permuted so that the dequantiser emits natural k order, and the palettes are ready
+//   lookup words (8 B per row and stage). Words and lookup words go straight into registers,
+//   RD stages ahead; only the x slice goes through LDS.
 #include "plz_common.h"
 #include "palettize_hip.h"
 
@@ -174,8 +173,9 @@ __device__ __forceinline__ void cursor_next(Cursor& c, const Table<GROUPED>& tb)
   cursor_load(c, tb);
 }
 
-// DEC: indices in the decode layout (packed_items), else native (packed)
-template <int NPX, bool GROUPED, bool DEC>
+// The native layouts (packed indices [N, K/16], fp32 palettes); the decode layouts run
+// gemv_reg_kernel below.
+template <int NPX, bool GROUPED>
 __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(const plz_gemv_desc* __restrict__ descs,
                                                           int n_desc, plz_gemv_desc single,
                                                           int M) {
@@ -202,7 +202,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(const plz_gemv_desc* _
   // packed copy i of this lane: row 16i + lane/4 of the wave's rows, 16-byte chunk lane%4
   const int wrow = lane >> 2;
   static_assert(KC == kPalGroup, "one palette group per stage");
-  uint32_t wbase[RB], mbase[NPX], pstride = 16u;
+  uint32_t wbase[RB], mbase[NPX];
   BufRsrc rq = make_rsrc(nullptr, 0), rp = rq, rx = rq;
   int64_t p_item = -1;
   auto issue = [&](int slot) {
@@ -212,31 +212,21 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(const plz_gemv_desc* _
     const int gpr = (int)(K / kPalGroup);
     if (pc.item != p_item) {  // new item: descriptors and per-lane base offsets
       p_item = pc.item;
-      // indices: native [N, K/16] words, or the decode layout [item][stage][8 KB]; a missing
-      // array (NULL) gets an empty range, so its copies read zeros
-      const void* qsrc = DEC ? (const void*)pc.d.packed_items : (const void*)pc.d.packed;
-      const int64_t qbytes = DEC ? (N + ROWS - 1) / ROWS * ROWS * (K / 4) : N * K / 4;
-      rq = make_rsrc(qsrc, live && qsrc ? (uint32_t)qbytes : 0u);
-      // palettes: native fp32 [N, K/256, 4] (16 B per row and stage, rows gpr*16 B apart), or
-      // with the decode layout the lookup tables [item][group][128 rows][lo, hi] (1 KB
-      // contiguous per stage)
-      const int64_t pbytes = DEC ? (N + ROWS - 1) / ROWS * ROWS * gpr * 8 : N * gpr * 16;
-      const void* psrc = DEC ? (const void*)pc.d.palette_items : (const void*)pc.d.palette;
-      rp = make_rsrc(psrc, live && psrc ? (uint32_t)pbytes : 0u);
-      pstride = DEC ? (uint32_t)(ROWS * 8) : 16u;
+      // indices [N, K/16] words; palettes fp32 [N, K/256, 4] (16 B per row and stage, rows
+      // gpr*16 B apart)
+      rq = make_rsrc(pc.d.packed, live && pc.d.packed ? (uint32_t)(N * K / 4) : 0u);
+      rp = make_rsrc(pc.d.palette, live && pc.d.palette ? (uint32_t)(N * gpr * 16) : 0u);
       rx = make_rsrc(pc.d.x, live ? (uint32_t)(M * K * 2) : 0u);
       const uint32_t r0 = (uint32_t)pc.row0;
 #pragma unroll
       for (int i = 0; i < RB; ++i)
-        wbase[i] = DEC ? r0 * (uint32_t)(K / 4) + wave * W_WAVE + i * 1024 + lane * 16
-                        : (r0 + 16 * RB * wave + 16 * i + wrow) * (uint32_t)(K / 4) +
-                              16u * ((lane & 3) ^ w_swz(16 * i + wrow));
+        wbase[i] = (r0 + 16 * RB * wave + 16 * i + wrow) * (uint32_t)(K / 4) +
+                   16u * ((lane & 3) ^ w_swz(16 * i + wrow));
 #pragma unroll
       for (int j = 0; j < NPX; ++j) {
         const int g = WAVES * j + wave;
-        if (g < 2) {  // palettes of rows 64g + lane (native) or the stage's 1 KB of tables
-          mbase[j] = DEC ? (g == 0 ? r0 * (uint32_t)gpr * 8u + lane * 16u : kBufOob)
-                         : (r0 + 64 * g + lane) * (uint32_t)gpr * 16u;
+        if (g < 2) {  // palettes of rows 64g + lane
+          mbase[j] = (r0 + 64 * g + lane) * (uint32_t)gpr * 16u;
         } else {      // x tokens 2(g-2), 2(g-2)+1
           const int m = 2 * (g - 2) + (lane >> 5);
           mbase[j] = m < 16 ? ((uint32_t)m * (uint32_t)K + 8u * ((lane & 31) ^ x_swz(m))) * 2u
@@ -246,7 +236,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(const plz_gemv_desc* _
     }
     // K is a multiple of 256 = KC, so every stage is whole
     const uint32_t k0 = (uint32_t)pc.kc * KC;
-    const uint32_t wk = DEC ? (uint32_t)pc.kc * (uint32_t)W_BYTES : k0 / 4;
+    const uint32_t wk = k0 / 4;
 #pragma unroll
     for (int i = 0; i < RB; ++i) dma16(rq, wbase[i] + wk, st + wave * W_WAVE + i * 1024);
 #pragma unroll
@@ -254,7 +244,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(const plz_gemv_desc* _
       const int g = WAVES * j + wave;
       lds_u8* dst = st + W_BYTES + g * 1024;
       if (g < 2)
-        dma16(rp, mbase[j] == kBufOob ? kBufOob : mbase[j] + (uint32_t)pc.kc * pstride, dst);
+        dma16(rp, mbase[j] + (uint32_t)pc.kc * 16u, dst);
       else
         dma16(rx, mbase[j] == kBufOob ? kBufOob : mbase[j] + k0 * 2u, dst);
     }
@@ -282,34 +272,21 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(const plz_gemv_desc* _
       const lds_u8* xs = st + W_BYTES + 2048 + mx * X_TOKEN;
       // x fragments of this lane: k = 64q + 16t + 8h .. +7 (t = 0..3, h = 0..1), permuted
       // into the dequantiser's slot order {k0, k4, k1, k5, k2, k6, k3, k7}
-      // (natural order with the decode layout)
       u32x4 xf[8];
 #pragma unroll
       for (int f = 0; f < 8; ++f) {
         const u32x4 v = *(const lds_u32x4*)(xs + (((8 * q + f) ^ x_swz(mx)) << 4));
-        if (DEC)
-          xf[f] = v;
-        else
-          xf[f] = u32x4{perm(v[2], v[0], 0x05040100u), perm(v[2], v[0], 0x07060302u),
-                        perm(v[3], v[1], 0x05040100u), perm(v[3], v[1], 0x07060302u)};
+        xf[f] = u32x4{perm(v[2], v[0], 0x05040100u), perm(v[2], v[0], 0x07060302u),
+                      perm(v[3], v[1], 0x05040100u), perm(v[3], v[1], 0x07060302u)};
       }
 #pragma unroll
       for (int r = 0; r < RB; ++r) {
         const int row = 16 * r + nl;
         const u32x4 wv =
-            DEC ? *(const lds_u32x4*)(st + wave * W_WAVE + r * 1024 + lane * 16)
-                : *(const lds_u32x4*)(st + wave * W_WAVE + row * 64 + ((q ^ w_swz(row)) << 4));
-        PalLut t;
-        if (DEC) {
-          const u32x2 lv = *(const __attribute__((address_space(3))) u32x2*)(
-              st + W_BYTES + (16 * RB * wave + row) * 8);
-          t.lo = lv[0];
-          t.hi = lv[1];
-        } else {
-          const u32x4 pv = *(const lds_u32x4*)(st + W_BYTES + (16 * RB * wave + row) * 16);
-          t = make_lut(__uint_as_float(pv[0]), __uint_as_float(pv[1]), __uint_as_float(pv[2]),
-                       __uint_as_float(pv[3]));
-        }
+            *(const lds_u32x4*)(st + wave * W_WAVE + row * 64 + ((q ^ w_swz(row)) << 4));
+        const u32x4 pv = *(const lds_u32x4*)(st + W_BYTES + (16 * RB * wave + row) * 16);
+        const PalLut t = make_lut(__uint_as_float(pv[0]), __uint_as_float(pv[1]),
+                                  __uint_as_float(pv[2]), __uint_as_float(pv[3]));
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
           u32x4 a0, a1;
@@ -339,6 +316,154 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(const plz_gemv_desc* _
   __builtin_amdgcn_s_waitcnt(0);  // drain the trailing (empty) copies before the wave ends
 }
 
+// ---- register-ring kernel for the decode layouts ---------------------------------------
+// The same items, stages, dequantiser and MFMAs as gemv_kernel, but a stage's packed words
+// and lookup words go from global memory straight into registers: each lane loads exactly
+// the 16 B of words per row block and the 8 B lookup words it dequantises (both layouts put
+// them where the lane reads them), RD stages ahead in a ring of registers. Only the stage's
+// x slice goes through LDS (shared by the four waves, one barrier per stage). The words in
+// flight are then bounded by registers, not by LDS: RD-1 stages of 2 KB per wave, against the
+// LDS ring's three stages of 8 KB per workgroup (which also held the x and palette slots).
+#ifndef PLZ_GV_RD
+#define PLZ_GV_RD 6
+#endif
+constexpr int RD = PLZ_GV_RD;
+template <int NX>
+constexpr int xstage_bytes() { return NX * WAVES * 1024; }  // x slots of one stage
+
+template <int NX, bool GROUPED>
+__global__ __launch_bounds__(64 * WAVES) void gemv_reg_kernel(const plz_gemv_desc* __restrict__ descs,
+                                                              int n_desc, plz_gemv_desc single,
+                                                              int M) {
+  extern __shared__ uint4 smem[];
+  lds_u8* lds = (lds_u8*)smem;
+  constexpr int XS = xstage_bytes<NX>();
+  constexpr int LOADS = 2 * RB + NX;  // vector-memory operations per lane and stage
+  const Table<GROUPED> tb{descs, n_desc, single};
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+  const int nl = lane & 15, q = lane >> 4;
+
+  const int64_t T = tb.total_cost(), G = gridDim.x, wid = blockIdx.x;
+  Cursor pc, cc;
+  pc.item = cc.item = tb.item_at_cost(wid * T / G);
+  pc.end = cc.end = tb.item_at_cost((wid + 1) * T / G);
+  cursor_load(pc, tb);
+  cursor_load(cc, tb);
+
+  // the issue cursor's per-item state; dead stages (past the range) read zeros
+  BufRsrc rq = make_rsrc(nullptr, 0), rp = rq, rx = rq;
+  uint32_t qbase = 0, pbase = 0, mbase[NX];
+  int64_t p_item = -1;
+  const uint32_t wlane = (uint32_t)(wave * W_WAVE + lane * 16);       // words of this lane
+  const uint32_t plane = (uint32_t)((16 * RB * wave + nl) * 8);       // lookup words of its row
+  uint4 wr[RD][RB];  // words, [ring slot][row block]
+  uint2 lr[RD][RB];  // lookup words {lo, hi}
+  auto issue = [&](int slot, lds_u8* __restrict__ xdst) {
+    const bool live = pc.item < pc.end;
+    const int64_t N = pc.d.N, K = pc.d.K;
+    if (pc.item != p_item) {
+      p_item = pc.item;
+      const int64_t rows = (N + ROWS - 1) / ROWS * ROWS;
+      rq = make_rsrc(pc.d.packed_items, live && pc.d.packed_items ? (uint32_t)(rows * (K / 4)) : 0u);
+      rp = make_rsrc(pc.d.palette_items,
+                     live && pc.d.palette_items ? (uint32_t)(rows * (K / kPalGroup) * 8) : 0u);
+      rx = make_rsrc(pc.d.x, live ? (uint32_t)(M * K * 2) : 0u);
+      qbase = (uint32_t)pc.row0 * (uint32_t)(K / 4);
+      pbase = (uint32_t)pc.row0 * (uint32_t)(K / kPalGroup) * 8u;
+#pragma unroll
+      for (int j = 0; j < NX; ++j) {  // x tokens 2g, 2g+1 of slot g = WAVES j + wave
+        const int m = 2 * (WAVES * j + wave) + (lane >> 5);
+        mbase[j] = m < 16 ? ((uint32_t)m * (uint32_t)K + 8u * ((lane & 31) ^ x_swz(m))) * 2u
+                          : kBufOob;
+      }
+    }
+    const uint32_t kc = (uint32_t)pc.kc;
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+      const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(
+          rq, (int)wlane, (int)(qbase + kc * (uint32_t)W_BYTES + (uint32_t)r * 1024u), 0);
+      wr[slot][r] = make_uint4(v.x, v.y, v.z, v.w);
+    }
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+      const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(
+          rp, (int)plane, (int)(pbase + kc * (uint32_t)(ROWS * 8) + (uint32_t)r * 128u), 0);
+      lr[slot][r] = make_uint2(v.x, v.y);
+    }
+#pragma unroll
+    for (int j = 0; j < NX; ++j)
+      dma16(rx, mbase[j] == kBufOob ? kBufOob : mbase[j] + kc * (uint32_t)(KC * 2),
+            xdst + (WAVES * j + wave) * 1024);
+  };
+
+  const int mx = nl < M ? nl : M - 1;  // token whose x this fragment lane reads
+  f32x4 acc[RB];
+#pragma unroll
+  for (int r = 0; r < RB; ++r) acc[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // One stage: the copies of stage s + RD - 1 (registers of slot sw, x into xw), then the
+  // MFMAs of stage s (registers of slot u, x from xr). xr and xw are distinct LDS slots, and
+  // saying so (__restrict__) keeps the compiler from waiting for the x copy just issued --
+  // and with it for every register load in flight -- before the x fragment reads.
+  auto stage = [&](int u, int sw, const lds_u8* __restrict__ xr, lds_u8* __restrict__ xw) {
+    issue(sw, xw);
+    cursor_next(pc, tb);
+    const lds_u8* xs = xr + mx * X_TOKEN;
+    u32x4 xf[8];
+#pragma unroll
+    for (int f = 0; f < 8; ++f) xf[f] = *(const lds_u32x4*)(xs + (((8 * q + f) ^ x_swz(mx)) << 4));
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+      PalLut t;
+      t.lo = lr[u][r].x;
+      t.hi = lr[u][r].y;
+      const uint4 wv = wr[u][r];
+      const uint32_t wq[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        u32x4 a0, a1;
+        dequant16_slots(wq[w], t, a0, a1);
+        acc[r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            __builtin_bit_cast(bf16x8, a0), __builtin_bit_cast(bf16x8, xf[2 * w]), acc[r], 0, 0, 0);
+        acc[r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            __builtin_bit_cast(bf16x8, a1), __builtin_bit_cast(bf16x8, xf[2 * w + 1]), acc[r], 0,
+            0, 0);
+      }
+    }
+  };
+
+#pragma unroll
+  for (int p = 0; p < RD - 1; ++p) {
+    issue(p, lds + p * XS);
+    cursor_next(pc, tb);
+  }
+  while (cc.item < cc.end) {  // RD stages per pass, unrolled so that ring slots are constants
+#pragma unroll
+    for (int u = 0; u < RD; ++u) {
+      if (cc.item >= cc.end) break;
+      wait_vmcnt<(RD - 2) * LOADS>();  // this lane's loads of stage s have landed
+      lds_barrier();                   // everyone's x copies have; slot (s - 1) % RD is free
+      stage(u, (u + RD - 1) % RD, lds + u * XS, lds + ((u + RD - 1) % RD) * XS);
+      if (++cc.kc == cc.nkc) {  // item done: acc lane l holds C[row 4q + e][token nl]
+        if (nl < M) {
+#pragma unroll
+          for (int r = 0; r < RB; ++r)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int64_t n = cc.row0 + 16 * RB * wave + 16 * r + 4 * q + e;
+              if (n < cc.d.N) cc.d.y[(int64_t)nl * cc.d.N + n] = (uint16_t)f2bf(acc[r][e]);
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < RB; ++r) acc[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+        ++cc.item;
+        cursor_load(cc, tb);
+      }
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // drain the trailing (empty) loads before the wave ends
+}
+
 static int cu_count() {
   static int cache[64] = {0};
   int dev = 0;
@@ -353,10 +478,10 @@ static int cu_count() {
   return cache[dev];
 }
 
-template <int NPX, bool GROUPED, bool DEC>
+template <int NPX, bool GROUPED>
 static int launch_nx(int64_t items, hipStream_t st, const plz_gemv_desc* descs, int n,
                      plz_gemv_desc single, int M, const char* what) {
-  auto kern = gemv_kernel<NPX, GROUPED, DEC>;
+  auto kern = gemv_kernel<NPX, GROUPED>;
   static uint64_t lds_done = 0;
   if (int rc = reserve_lds((const void*)kern, (size_t)lds_bytes<NPX>(), lds_done, what)) return rc;
   const int64_t slots = wgs_per_cu<NPX>() * (int64_t)cu_count();
@@ -365,22 +490,48 @@ static int launch_nx(int64_t items, hipStream_t st, const plz_gemv_desc* descs, 
                      single, M);
   return check_launch(what);
 }
-template <bool GROUPED, bool DEC>
-static int launch_dec(int64_t items, hipStream_t st, const plz_gemv_desc* descs, int n,
-                      plz_gemv_desc single, int M, const char* what) {
+template <bool GROUPED>
+static int launch_native(int64_t items, hipStream_t st, const plz_gemv_desc* descs, int n,
+                         plz_gemv_desc single, int M, const char* what) {
   switch (npx_for(M)) {
-    case 1: return launch_nx<1, GROUPED, DEC>(items, st, descs, n, single, M, what);
-    case 2: return launch_nx<2, GROUPED, DEC>(items, st, descs, n, single, M, what);
-    case 3: return launch_nx<3, GROUPED, DEC>(items, st, descs, n, single, M, what);
-    case 4: return launch_nx<4, GROUPED, DEC>(items, st, descs, n, single, M, what);
-    default: return launch_nx<5, GROUPED, DEC>(items, st, descs, n, single, M, what);
+    case 1: return launch_nx<1, GROUPED>(items, st, descs, n, single, M, what);
+    case 2: return launch_nx<2, GROUPED>(items, st, descs, n, single, M, what);
+    case 3: return launch_nx<3, GROUPED>(items, st, descs, n, single, M, what);
+    case 4: return launch_nx<4, GROUPED>(items, st, descs, n, single, M, what);
+    default: return launch_nx<5, GROUPED>(items, st, descs, n, single, M, what);
   }
+}
+// decode layouts: the register-ring kernel; x slots for 8 tokens per stage (M <= 8) or 16
+template <int NX, bool GROUPED>
+static int launch_reg_nx(int64_t items, hipStream_t st, const plz_gemv_desc* descs, int n,
+                         plz_gemv_desc single, int M, const char* what) {
+  auto kern = gemv_reg_kernel<NX, GROUPED>;
+  const size_t lds = (size_t)RD * xstage_bytes<NX>();
+  static uint64_t lds_done = 0;
+  if (int rc = reserve_lds((const void*)kern, lds, lds_done, what)) return rc;
+  static int per_cu[64] = {0};  // resident workgroups per CU, per device
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  if (per_cu[dev] == 0) {
+    int v = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, (const void*)kern, 64 * WAVES, lds) !=
+            hipSuccess ||
+        v < 1)
+      v = 1;
+    per_cu[dev] = v;
+  }
+  const int64_t slots = per_cu[dev] * (int64_t)cu_count();
+  const int64_t g = items < slots ? items : slots;
+  hipLaunchKernelGGL(kern, dim3((unsigned)g), dim3(64 * WAVES), lds, st, descs, n, single, M);
+  return check_launch(what);
 }
 template <bool GROUPED>
 static int launch(int64_t items, hipStream_t st, const plz_gemv_desc* descs, int n,
                   plz_gemv_desc single, int M, bool dec, const char* what) {
-  return dec ? launch_dec<GROUPED, true>(items, st, descs, n, single, M, what)
-             : launch_dec<GROUPED, false>(items, st, descs, n, single, M, what);
+  if (dec)
+    return M <= 8 ? launch_reg_nx<1, GROUPED>(items, st, descs, n, single, M, what)
+                  : launch_reg_nx<2, GROUPED>(items, st, descs, n, single, M, what);
+  return launch_native<GROUPED>(items, st, descs, n, single, M, what);
 }
 
 // palette [N, G, 4] -> lookup tables [ceil(N/ROWS)][G][ROWS][lo, hi] (make_lut of the row's
