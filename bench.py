@@ -41,7 +41,7 @@ PEAK_HBM_GBS = 8000.0
 # commands and algorithmic bytes in profiles/lut_gemm_traffic_m16384.txt).
 GEMM_TRAFFIC_BYTES = {"fwd": 584.4e6, "grad_x": 571.4e6, "grad_palette": 886.7e6}
 KERNEL_NAMES = {"fwd": "gemm2_kernel<OP_ROW, OP_LUT_REG, EPI_BF16> (fwd)",
-                "grad_x": "gemm2_kernel<OP_ROW, OP_LUT_COL, EPI_BF16> (grad_x)",
+                "grad_x": "dequant_kernel + gemm2_kernel<OP_ROW, OP_COL, EPI_BF16> (grad_x)",
                 "grad_palette": "gemm2_kernel<OP_COL, OP_COL, EPI_PAL> (grad_palette)"}
 
 

@@ -1034,8 +1034,20 @@ int plz_lut_linear_fwd(const uint16_t* x, const int32_t* packed, const float* pa
   return launch<OP_ROW, OP_LUT_REG, EPI_BF16>(g, 1, (hipStream_t)stream, "plz_lut_linear_fwd");
 }
 
+// grad_x from this many rows dequantises W into the workspace and runs the dense GEMM: the
+// LUT GEMM rebuilds each B tile in LDS once per 256-row tile of grad_y (about a quarter of its
+// time), while dequantising once costs N*K*(0.25 + 2) bytes written and read back, which a
+// 4096-row GEMM hides several times over.
+constexpr int64_t kStagedBwdXRows = 4096;
+
+static size_t staged_w_bytes(int64_t N, int64_t K) {
+  return ((size_t)N * (size_t)K * sizeof(uint16_t) + 255) & ~(size_t)255;
+}
+
 size_t plz_lut_linear_bwd_x_workspace(int64_t M, int64_t N, int64_t K) {
-  return M > 0 && N > 0 && K > 0 ? tail_bytes(M, K, N) : 0;
+  if (M <= 0 || N <= 0 || K <= 0) return 0;
+  if (M >= kStagedBwdXRows) return staged_w_bytes(N, K) + tail_bytes(M, K, N);
+  return tail_bytes(M, K, N);
 }
 
 int plz_lut_linear_bwd_x(const uint16_t* grad_y, const int32_t* packed, const float* palette,
@@ -1056,10 +1068,24 @@ int plz_lut_linear_bwd_x(const uint16_t* grad_y, const int32_t* packed, const fl
               "plz_lut_linear_bwd_x: rank > 0 needs 16-byte aligned lora_gt and lora_a");
   Args g = {};
   g.a = grad_y; g.lda = N;
-  g.packed = packed; g.pal = palette; g.Nw = N; g.Kw = K;
   g.I = M; g.J = K; g.R = N;
   g.a2 = lora_gt; g.b2 = lora_a; g.R2 = rank;
   g.c = grad_x; g.ldc = K; g.alpha = 1.f;
+  const size_t wbytes = staged_w_bytes(N, K);
+  if (N > 0 && workspace && a16(workspace) && M >= kStagedBwdXRows &&
+      workspace_bytes >= wbytes + tail_bytes(M, K, N)) {
+    // dequantised W in the workspace's head, the tail partials behind it
+    uint16_t* w = reinterpret_cast<uint16_t*>(workspace);
+    int rc = plz_dequant(packed, palette, w, N, K, stream);
+    if (rc != PLZ_OK) return rc;
+    g.b = w; g.ldb = K;  // B(j=k, r=n) = w[n, k]   (Col tile)
+    g.group = 8;
+    rc = set_tail(g, static_cast<uint8_t*>(workspace) + wbytes, workspace_bytes - wbytes,
+                  "plz_lut_linear_bwd_x");
+    if (rc != PLZ_OK) return rc;
+    return launch<OP_ROW, OP_COL, EPI_BF16>(g, 1, (hipStream_t)stream, "plz_lut_linear_bwd_x");
+  }
+  g.packed = packed; g.pal = palette; g.Nw = N; g.Kw = K;
   g.group = 1;
   const int rc = set_tail(g, workspace, workspace_bytes, "plz_lut_linear_bwd_x");
   if (rc != PLZ_OK) return rc;

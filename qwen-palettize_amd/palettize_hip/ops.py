@@ -135,8 +135,12 @@ def lut_linear_fwd(x, packed, palette, bias=None, lora_t=None, lora_b=None):
     return y
 
 
-def lut_linear_bwd_x(grad_y, packed, palette, lora_gt=None, lora_a=None):
-    """grad_x = grad_y W (+ lora_gt lora_a)."""
+def lut_linear_bwd_x(grad_y, packed, palette, lora_gt=None, lora_a=None, staged=True):
+    """grad_x = grad_y W (+ lora_gt lora_a).
+
+    staged: give the workspace the query asks for, so that from 4096 rows W is dequantised
+    into it and the dense GEMM runs on it; False keeps the one-pass LUT GEMM (workspace for
+    its tail partials only)."""
     N, K = _wshape(packed, palette)
     _need(grad_y, "grad_y", torch.bfloat16, 2)
     M = grad_y.shape[0]
@@ -152,7 +156,8 @@ def lut_linear_bwd_x(grad_y, packed, palette, lora_gt=None, lora_a=None):
         if lora_gt.shape[0] != M or tuple(lora_a.shape) != (rank, K):
             raise ValueError("lora_gt / lora_a shape mismatch")
     gx = torch.empty((M, K), dtype=torch.bfloat16, device=grad_y.device)
-    ws = _opt_workspace(query("plz_lut_linear_bwd_x_workspace", M, N, K), grad_y.device)
+    q = "plz_lut_linear_bwd_x_workspace" if staged else "plz_linear_bwd_x_dense_workspace"
+    ws = _opt_workspace(query(q, M, N, K), grad_y.device)
     call("plz_lut_linear_bwd_x", _ptr(grad_y), _ptr(packed), _ptr(palette), _ptr(lora_gt),
          _ptr(lora_a), rank, _ptr(gx), _ptr(ws), _numel(ws), M, N, K, _stream(grad_y))
     return gx

@@ -59,7 +59,12 @@ def test_tail_split_workspace_queries(lib):
     # is long enough to pay for the partials; whole waves and short reductions need none
     ws = lib.plz_lut_linear_fwd_workspace(16384, 2560, 9728)
     assert ws == 128 * 2 * 256 * 256 * 4
-    assert lib.plz_lut_linear_bwd_x_workspace(16384, 9728, 2560) == 128 * 2 * 256 * 256 * 4
+    # grad_x from 4096 rows: a bf16 copy of W ahead of the tail partials
+    assert lib.plz_lut_linear_bwd_x_workspace(16384, 9728, 2560) == (9728 * 2560 * 2
+                                                                    + 128 * 2 * 256 * 256 * 4)
+    assert lib.plz_lut_linear_bwd_x_workspace(4096, 1024, 2560) == 1024 * 2560 * 2
+    assert lib.plz_lut_linear_bwd_x_workspace(4095, 1024, 2560) == \
+        lib.plz_linear_bwd_x_dense_workspace(4095, 1024, 2560)
     assert lib.plz_lut_linear_fwd_workspace(16384, 4096, 2560) == 0    # 1024 tiles
     assert lib.plz_linear_fwd_dense_workspace(16384, 1024, 2560) == 0  # 256 tiles
     assert lib.plz_linear_bwd_x_dense_workspace(16384, 1024, 2560) == 0  # 16 stages

@@ -103,8 +103,10 @@ def test_lut_linear_fwd(dev, M, N, K, rank):
 
 
 @pytest.mark.parametrize("M,N,K,rank", [(512, 2560, 2560, 16), (1, 256, 256, 0),
-                                        (77, 1032, 768, 8), (256, 384, 1024, 32)])
+                                        (77, 1032, 768, 8), (256, 384, 1024, 32),
+                                        (4096, 1032, 768, 8)])
 def test_lut_linear_bwd_x(dev, M, N, K, rank):
+    """From 4096 rows the call dequantises W into its workspace and runs the dense GEMM."""
     idx, pal, _, W, lora = _oracle_problem(M, N, K, seed=3 * M + N, rank=rank)
     gy = randn_bf16(M, N, seed=9)
     args = {}
@@ -117,6 +119,9 @@ def test_lut_linear_bwd_x(dev, M, N, K, rank):
         want = want + f32(gt) @ f32(a)
     gx = ops.lut_linear_bwd_x(gy.to(dev), _packed(idx, dev), pal.to(dev), **args)
     assert_close(f32(gx), want, what="grad_x")
+    if M >= 4096:  # the one-pass LUT GEMM on the same problem
+        g1 = ops.lut_linear_bwd_x(gy.to(dev), _packed(idx, dev), pal.to(dev), staged=False, **args)
+        assert_close(f32(g1), want, what="grad_x (LUT GEMM)")
 
 
 @pytest.mark.parametrize("M,N,K", [(512, 2560, 2560), (1, 256, 256), (77, 1032, 768),
@@ -287,6 +292,8 @@ def test_tail_split_gemms(dev, M):
     gx = ops.lut_linear_bwd_x(gy.to(dev), p, pl, lora_gt=gt, lora_a=a.to(dev))
     want = O.grad_x(f32(gy[rows]), W) + f32(gt[rows.to(dev)]) @ f32(a)
     assert_close(f32(gx[rows.to(dev)]), want, what="grad_x (tail split)")
+    g1 = ops.lut_linear_bwd_x(gy.to(dev), p, pl, lora_gt=gt, lora_a=a.to(dev), staged=False)
+    assert_close(f32(g1[rows.to(dev)]), want, what="grad_x (LUT GEMM, tail split)")
     # the dense GEMMs of the soft path on the dequantised weight
     wd = ops.dequant(p, pl)
     yd = ops.linear_fwd_dense(x.to(dev), wd, bias.to(dev))

@@ -43,8 +43,9 @@ def test_forward_rows_of_a_nonfinite_input_go_nonfinite(dev, M, N, K):
     assert bool(torch.isnan(gv[3]).all()) and bool(torch.isfinite(gv[:3]).all())
 
 
-def test_grad_x_rows_of_a_nonfinite_gradient_go_nonfinite(dev):
-    M, N, K = 512, 1024, 2560
+@pytest.mark.parametrize("M", [512, 4096])  # the LUT GEMM; dequantised W + dense GEMM
+def test_grad_x_rows_of_a_nonfinite_gradient_go_nonfinite(dev, M):
+    N, K = 1024, 2560
     _, p, pl = _weight(N, K, 3, dev)
     gy = randn_bf16(M, N, seed=4).to(dev)
     clean = ops.lut_linear_bwd_x(gy, p, pl)
