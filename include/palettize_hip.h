@@ -76,19 +76,22 @@ int plz_lut_linear_fwd(const uint16_t* x, const int32_t* packed, const float* pa
 /* Optional workspace of the four one-pass GEMMs (lut fwd / bwd_x, dense fwd / bwd_x): when the
  * output tiles leave a last, partial wave on the GPU, those tiles are split over the
  * reduction and summed by a second kernel (fp32 partials in the workspace). NULL disables the
- * split; a smaller non-NULL workspace than the query returns PLZ_EWORKSPACE. 0 = no split. */
+ * split; a smaller non-NULL workspace than the tail partials need returns PLZ_EWORKSPACE.
+ * 0 = no split.
+ * The two LUT GEMMs (plz_lut_linear_fwd, plz_lut_linear_bwd_x) have two schedules, chosen by
+ * the workspace given: from M = 4096 rows their queries ask for room for a bf16 copy of W
+ * (N*K*2 bytes, rounded up to 256) ahead of the tail partials, and with that much workspace
+ * the call dequantises W into it and runs the dense GEMM on it (faster at these sizes than
+ * rebuilding W tiles inside the GEMM's loop); with less (or NULL) it runs the one-pass LUT
+ * GEMM, splitting its last wave when the workspace holds the tail partials
+ * (plz_linear_fwd_dense_workspace / plz_linear_bwd_x_dense_workspace give that size). The two
+ * schedules differ only in MFMA summation order (bf16 rounding of the output). */
 size_t plz_lut_linear_fwd_workspace(int64_t M, int64_t N, int64_t K);
 
 /* grad_x[M,K] = grad_y[M,N] W (+ lora_gt[M,rank] lora_a[rank,K]).
  * Replaces the grad_x half of fused_lut_linear_bwd (fused_lut_linear_cuda.py:119-150) and
- * fused_lut_linear_bwd_grad_x_tc_kernel (fused_lut_kernel.cu:551-720).
- * Two schedules, chosen by the workspace given: from M = 4096 rows the query asks for room
- * for a bf16 copy of W (N*K*2 bytes, rounded up to 256) ahead of the tail partials, and with
- * that much workspace the call dequantises W into it and runs the dense grad_x GEMM on it
- * (faster at these sizes than dequantising B tiles into LDS in the GEMM's loop); with less
- * (or NULL) it runs the one-pass LUT GEMM, splitting its last wave when the workspace holds
- * the tail partials (plz_linear_bwd_x_dense_workspace gives that size). The two differ only
- * in MFMA summation order (bf16 rounding of the output). */
+ * fused_lut_linear_bwd_grad_x_tc_kernel (fused_lut_kernel.cu:551-720). Workspace and
+ * schedules as for plz_lut_linear_fwd. */
 int plz_lut_linear_bwd_x(const uint16_t* grad_y, const int32_t* packed, const float* palette,
                          const uint16_t* lora_gt, const uint16_t* lora_a, int rank,
                          uint16_t* grad_x, void* workspace, size_t workspace_bytes, int64_t M,

@@ -1001,10 +1001,43 @@ static size_t soft_pal_bytes(int64_t N, int64_t K) { return (size_t)N * (K / 128
 using namespace plz;
 using namespace plz::g2;
 
+// From this many rows the forward and grad_x dequantise W into the workspace and run the
+// dense GEMM on it: the LUT GEMMs rebuild each W tile once per 256-row tile of the activations
+// (the forward in registers, grad_x in LDS; 10-25% of their time), while dequantising once
+// costs N*K*(0.25 + 2) bytes written and read back, which a 4096-row GEMM hides several times
+// over.
+constexpr int64_t kStagedRows = 4096;
+
+static size_t staged_w_bytes(int64_t N, int64_t K) {
+  return ((size_t)N * (size_t)K * sizeof(uint16_t) + 255) & ~(size_t)255;
+}
+
+// Dequantises W into the head of the workspace when it holds W and the tail partials behind
+// it; then points g at W (Row tile for the forward, Col tile for grad_x) and the tail
+// partials. Returns false (g untouched) when the rows are too few or the workspace too small;
+// when it returns true, *rc holds the status of the dequantisation and of the tail set-up.
+static bool stage_w(Args& g, const int32_t* packed, const float* palette, int64_t N, int64_t K,
+                    void* workspace, size_t workspace_bytes, const char* what, void* stream,
+                    int* rc) {
+  const size_t wbytes = staged_w_bytes(N, K);
+  if (!(N > 0 && workspace && a16(workspace) && g.I >= kStagedRows &&
+        workspace_bytes >= wbytes + tail_bytes(g.I, g.J, g.R)))
+    return false;
+  uint16_t* w = reinterpret_cast<uint16_t*>(workspace);
+  *rc = plz_dequant(packed, palette, w, N, K, stream);
+  if (*rc != PLZ_OK) return true;
+  g.b = w; g.ldb = K;
+  g.group = 8;
+  *rc = set_tail(g, static_cast<uint8_t*>(workspace) + wbytes, workspace_bytes - wbytes, what);
+  return true;
+}
+
 extern "C" {
 
 size_t plz_lut_linear_fwd_workspace(int64_t M, int64_t N, int64_t K) {
-  return M > 0 && N > 0 && K > 0 ? tail_bytes(M, N, K) : 0;
+  if (M <= 0 || N <= 0 || K <= 0) return 0;
+  if (M >= kStagedRows) return staged_w_bytes(N, K) + tail_bytes(M, N, K);
+  return tail_bytes(M, N, K);
 }
 
 int plz_lut_linear_fwd(const uint16_t* x, const int32_t* packed, const float* palette,
@@ -1024,29 +1057,25 @@ int plz_lut_linear_fwd(const uint16_t* x, const int32_t* packed, const float* pa
               "plz_lut_linear_fwd: rank > 0 needs 16-byte aligned lora_t and lora_b");
   Args g = {};
   g.a = x; g.lda = K;
-  g.packed = packed; g.pal = palette; g.Nw = N; g.Kw = K;
   g.I = M; g.J = N; g.R = K;
   g.a2 = lora_t; g.b2 = lora_b; g.R2 = rank;
   g.c = y; g.ldc = N; g.bias = bias; g.alpha = 1.f;
+  int rc = PLZ_OK;
+  if (stage_w(g, packed, palette, N, K, workspace, workspace_bytes, "plz_lut_linear_fwd", stream,
+              &rc)) {
+    if (rc != PLZ_OK) return rc;  // B(j=n, r=k) = w[n, k]   (Row tile)
+    return launch<OP_ROW, OP_ROW, EPI_BF16>(g, 1, (hipStream_t)stream, "plz_lut_linear_fwd");
+  }
+  g.packed = packed; g.pal = palette; g.Nw = N; g.Kw = K;
   g.group = 1;
-  const int rc = set_tail(g, workspace, workspace_bytes, "plz_lut_linear_fwd");
+  rc = set_tail(g, workspace, workspace_bytes, "plz_lut_linear_fwd");
   if (rc != PLZ_OK) return rc;
   return launch<OP_ROW, OP_LUT_REG, EPI_BF16>(g, 1, (hipStream_t)stream, "plz_lut_linear_fwd");
 }
 
-// grad_x from this many rows dequantises W into the workspace and runs the dense GEMM: the
-// LUT GEMM rebuilds each B tile in LDS once per 256-row tile of grad_y (about a quarter of its
-// time), while dequantising once costs N*K*(0.25 + 2) bytes written and read back, which a
-// 4096-row GEMM hides several times over.
-constexpr int64_t kStagedBwdXRows = 4096;
-
-static size_t staged_w_bytes(int64_t N, int64_t K) {
-  return ((size_t)N * (size_t)K * sizeof(uint16_t) + 255) & ~(size_t)255;
-}
-
 size_t plz_lut_linear_bwd_x_workspace(int64_t M, int64_t N, int64_t K) {
   if (M <= 0 || N <= 0 || K <= 0) return 0;
-  if (M >= kStagedBwdXRows) return staged_w_bytes(N, K) + tail_bytes(M, K, N);
+  if (M >= kStagedRows) return staged_w_bytes(N, K) + tail_bytes(M, K, N);
   return tail_bytes(M, K, N);
 }
 
@@ -1071,23 +1100,15 @@ int plz_lut_linear_bwd_x(const uint16_t* grad_y, const int32_t* packed, const fl
   g.I = M; g.J = K; g.R = N;
   g.a2 = lora_gt; g.b2 = lora_a; g.R2 = rank;
   g.c = grad_x; g.ldc = K; g.alpha = 1.f;
-  const size_t wbytes = staged_w_bytes(N, K);
-  if (N > 0 && workspace && a16(workspace) && M >= kStagedBwdXRows &&
-      workspace_bytes >= wbytes + tail_bytes(M, K, N)) {
-    // dequantised W in the workspace's head, the tail partials behind it
-    uint16_t* w = reinterpret_cast<uint16_t*>(workspace);
-    int rc = plz_dequant(packed, palette, w, N, K, stream);
-    if (rc != PLZ_OK) return rc;
-    g.b = w; g.ldb = K;  // B(j=k, r=n) = w[n, k]   (Col tile)
-    g.group = 8;
-    rc = set_tail(g, static_cast<uint8_t*>(workspace) + wbytes, workspace_bytes - wbytes,
-                  "plz_lut_linear_bwd_x");
-    if (rc != PLZ_OK) return rc;
+  int rc = PLZ_OK;
+  if (stage_w(g, packed, palette, N, K, workspace, workspace_bytes, "plz_lut_linear_bwd_x",
+              stream, &rc)) {
+    if (rc != PLZ_OK) return rc;  // B(j=k, r=n) = w[n, k]   (Col tile)
     return launch<OP_ROW, OP_COL, EPI_BF16>(g, 1, (hipStream_t)stream, "plz_lut_linear_bwd_x");
   }
   g.packed = packed; g.pal = palette; g.Nw = N; g.Kw = K;
   g.group = 1;
-  const int rc = set_tail(g, workspace, workspace_bytes, "plz_lut_linear_bwd_x");
+  rc = set_tail(g, workspace, workspace_bytes, "plz_lut_linear_bwd_x");
   if (rc != PLZ_OK) return rc;
   return launch<OP_ROW, OP_LUT_COL, EPI_BF16>(g, 1, (hipStream_t)stream, "plz_lut_linear_bwd_x");
 }

@@ -119,8 +119,12 @@ def _lora_pair(a, b, first: str, second: str, rows_a: int, rows_b: int):
     return r
 
 
-def lut_linear_fwd(x, packed, palette, bias=None, lora_t=None, lora_b=None):
-    """y = x W^T (+ bias) (+ lora_t lora_b^T)."""
+def lut_linear_fwd(x, packed, palette, bias=None, lora_t=None, lora_b=None, staged=True):
+    """y = x W^T (+ bias) (+ lora_t lora_b^T).
+
+    staged: give the workspace the query asks for, so that from 4096 rows W is dequantised
+    into it and the dense GEMM runs on it; False keeps the one-pass LUT GEMM (workspace for
+    its tail partials only)."""
     N, K = _wshape(packed, palette)
     _need(x, "x", torch.bfloat16, 2)
     M = x.shape[0]
@@ -129,7 +133,8 @@ def lut_linear_fwd(x, packed, palette, bias=None, lora_t=None, lora_b=None):
     _bias(bias, N)
     rank = _lora_pair(lora_t, lora_b, "lora_t", "lora_b", M, N)
     y = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
-    ws = _opt_workspace(query("plz_lut_linear_fwd_workspace", M, N, K), x.device)
+    q = "plz_lut_linear_fwd_workspace" if staged else "plz_linear_fwd_dense_workspace"
+    ws = _opt_workspace(query(q, M, N, K), x.device)
     call("plz_lut_linear_fwd", _ptr(x), _ptr(packed), _ptr(palette), _ptr(bias), _ptr(lora_t),
          _ptr(lora_b), rank, _ptr(y), _ptr(ws), _numel(ws), M, N, K, _stream(x))
     return y

@@ -56,16 +56,19 @@ def test_shape_errors_are_reported_without_touching_the_gpu(lib):
 
 def test_tail_split_workspace_queries(lib):
     # 640 output tiles on 256 CUs: a last wave of 128 tiles, split two ways when the reduction
-    # is long enough to pay for the partials; whole waves and short reductions need none
+    # is long enough to pay for the partials; whole waves and short reductions need none.
+    # The LUT GEMMs from 4096 rows: a bf16 copy of W ahead of the tail partials.
+    assert lib.plz_linear_fwd_dense_workspace(16384, 2560, 9728) == 128 * 2 * 256 * 256 * 4
     ws = lib.plz_lut_linear_fwd_workspace(16384, 2560, 9728)
-    assert ws == 128 * 2 * 256 * 256 * 4
-    # grad_x from 4096 rows: a bf16 copy of W ahead of the tail partials
+    assert ws == 2560 * 9728 * 2 + 128 * 2 * 256 * 256 * 4
     assert lib.plz_lut_linear_bwd_x_workspace(16384, 9728, 2560) == (9728 * 2560 * 2
                                                                     + 128 * 2 * 256 * 256 * 4)
     assert lib.plz_lut_linear_bwd_x_workspace(4096, 1024, 2560) == 1024 * 2560 * 2
     assert lib.plz_lut_linear_bwd_x_workspace(4095, 1024, 2560) == \
         lib.plz_linear_bwd_x_dense_workspace(4095, 1024, 2560)
-    assert lib.plz_lut_linear_fwd_workspace(16384, 4096, 2560) == 0    # 1024 tiles
+    assert lib.plz_lut_linear_fwd_workspace(16384, 4096, 2560) == 4096 * 2560 * 2  # 1024 tiles
+    assert lib.plz_lut_linear_fwd_workspace(2048, 4096, 2560) == \
+        lib.plz_linear_fwd_dense_workspace(2048, 4096, 2560)
     assert lib.plz_linear_fwd_dense_workspace(16384, 1024, 2560) == 0  # 256 tiles
     assert lib.plz_linear_bwd_x_dense_workspace(16384, 1024, 2560) == 0  # 16 stages
     assert lib.plz_lut_linear_fwd_workspace(0, 2560, 9728) == 0

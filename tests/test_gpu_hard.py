@@ -82,8 +82,10 @@ def _oracle_problem(M, N, K, seed, rank=0):
 @pytest.mark.parametrize("M,N,K,rank", [
     (512, 2560, 2560, 16),   # config 1 shape
     (1, 256, 256, 0), (3, 1032, 768, 8), (129, 384, 512, 16), (300, 136, 1024, 32),
+    (4097, 1032, 768, 8),
 ])
 def test_lut_linear_fwd(dev, M, N, K, rank):
+    """From 4096 rows the call dequantises W into its workspace and runs the dense GEMM."""
     idx, pal, x, W, lora = _oracle_problem(M, N, K, seed=M + N + K, rank=rank)
     bias = randn_bf16(N, seed=5, std=0.1) if M % 2 else None
     args = {}
@@ -100,6 +102,10 @@ def test_lut_linear_fwd(dev, M, N, K, rank):
     if rank:
         want = want + O.lora_forward(f32(x), t_ref, f32(lora[1]), 1.0)
     assert_close(f32(y), want, what="y")
+    if M >= 4096:  # the one-pass LUT GEMM on the same problem
+        y1 = ops.lut_linear_fwd(x.to(dev), _packed(idx, dev), pal.to(dev),
+                                None if bias is None else bias.to(dev), staged=False, **args)
+        assert_close(f32(y1), want, what="y (LUT GEMM)")
 
 
 @pytest.mark.parametrize("M,N,K,rank", [(512, 2560, 2560, 16), (1, 256, 256, 0),
@@ -288,6 +294,9 @@ def test_tail_split_gemms(dev, M):
     xr = f32(x[rows])
     want = O.lut_linear_fwd(xr, W, f32(bias)) + O.lora_forward(xr, f32(a), f32(b), 1.0)
     assert_close(f32(y[rows.to(dev)]), want, what="fwd (tail split)")
+    y1 = ops.lut_linear_fwd(x.to(dev), p, pl, bias.to(dev), lora_t=t, lora_b=b.to(dev),
+                            staged=False)
+    assert_close(f32(y1[rows.to(dev)]), want, what="fwd (LUT GEMM, tail split)")
     gt = ops.lora_grad_t(gy.to(dev), b.to(dev), 1.0)
     gx = ops.lut_linear_bwd_x(gy.to(dev), p, pl, lora_gt=gt, lora_a=a.to(dev))
     want = O.grad_x(f32(gy[rows]), W) + f32(gt[rows.to(dev)]) @ f32(a)

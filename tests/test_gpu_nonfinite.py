@@ -25,15 +25,18 @@ def _weight(N, K, seed, dev):
     return idx, ops.pack_indices(idx.to(dev)), pal.to(dev)
 
 
-@pytest.mark.parametrize("M,N,K", [(300, 1032, 768), (4096, 2560, 2560)])
-def test_forward_rows_of_a_nonfinite_input_go_nonfinite(dev, M, N, K):
+@pytest.mark.parametrize("M,N,K,staged", [(300, 1032, 768, True), (4096, 2560, 2560, True),
+                                          (4096, 2560, 2560, False)])
+def test_forward_rows_of_a_nonfinite_input_go_nonfinite(dev, M, N, K, staged):
+    """staged: from 4096 rows W dequantised into the workspace and the dense GEMM; else the
+    one-pass LUT GEMM."""
     _, p, pl = _weight(N, K, 1, dev)
     x = randn_bf16(M, K, seed=2).to(dev)
-    clean = ops.lut_linear_fwd(x, p, pl)
+    clean = ops.lut_linear_fwd(x, p, pl, staged=staged)
     xb = x.clone()
     xb[3, 100] = NAN
     xb[M - 1, 5] = INF
-    y = ops.lut_linear_fwd(xb, p, pl)
+    y = ops.lut_linear_fwd(xb, p, pl, staged=staged)
     bad = torch.zeros(M, dtype=torch.bool, device=dev)
     bad[3] = bad[M - 1] = True
     assert bool(torch.isnan(y[3]).all())
