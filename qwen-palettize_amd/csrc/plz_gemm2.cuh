@@ -251,15 +251,54 @@ __device__ __forceinline__ bf16x8 frag_row_chunk(const uint4* lds, int rowbase, 
   return __builtin_bit_cast(bf16x8, lds[row_chunk(rowbase + (lane & 31), chunk)]);
 }
 // Col tile: per 16-lane group j = lane/16 the rows 16*(j&1)..+15 at k-group j>>1.
+// col_swz sees only the low 4 bits of the reduction row, so k-step ks moves both reads by
+// the constant 16*ks rows: the lane-dependent part is formed for ks = 0 and the k-step
+// becomes the read instruction's immediate offset (one address per fragment and stage
+// instead of one per k-step).
 __device__ __forceinline__ bf16x8 frag_col(const lds_u8* lds, int rowbase, int ks, int lane) {
   const int j = lane >> 4, i = lane & 15, t = i >> 2, q = i & 3;
   const int row = rowbase + 16 * (j & 1) + 4 * q;
-  const int kr1 = 16 * ks + 8 * (j >> 1) + t, kr2 = kr1 + 4;
+  const int kr1 = 8 * (j >> 1) + t, kr2 = kr1 + 4;
   const int c = row >> 3, off = (row & 7) * 2;
+  const lds_u8* kb = lds + ks * (16 * TILE * 2);
   const v4i16 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (lds_v4i16*)(lds + col_chunk(kr1, c) * 16 + off));
+      (lds_v4i16*)(kb + col_chunk(kr1, c) * 16 + off));
   const v4i16 v2 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (lds_v4i16*)(lds + col_chunk(kr2, c) * 16 + off));
+      (lds_v4i16*)(kb + col_chunk(kr2, c) * 16 + off));
+  typedef short v8i16 __attribute__((ext_vector_type(8)));
+  const v8i16 v = __builtin_shufflevector(v1, v2, 0, 1, 2, 3, 4, 5, 6, 7);
+  return __builtin_bit_cast(bf16x8, v);
+}
+
+// Read addresses of a Col tile's fragments for one stage: two per 32-row block, at k-step 0.
+// The empty asm statement makes each address an opaque register value, so that the k-steps
+// use the read instruction's immediate offset (+16*ks rows) and the compiler does not keep
+// one precomputed address per k-step and re-add the stage's slot base to every one of them.
+template <int NB>
+struct ColBases {
+  uint32_t p1[NB], p2[NB];
+};
+template <int NB>
+__device__ __forceinline__ void col_bases(const lds_u8* lds, int rowbase0, int lane,
+                                          ColBases<NB>& cb) {
+  const int j = lane >> 4, i = lane & 15, t = i >> 2, q = i & 3;
+  const int kr1 = 8 * (j >> 1) + t, kr2 = kr1 + 4;
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    const int row = rowbase0 + 32 * b + 16 * (j & 1) + 4 * q;
+    const int c = row >> 3, off = (row & 7) * 2;
+    uint32_t p1 = (uint32_t)(uintptr_t)lds + col_chunk(kr1, c) * 16 + off;
+    uint32_t p2 = (uint32_t)(uintptr_t)lds + col_chunk(kr2, c) * 16 + off;
+    asm volatile("" : "+v"(p1), "+v"(p2));
+    cb.p1[b] = p1;
+    cb.p2[b] = p2;
+  }
+}
+__device__ __forceinline__ bf16x8 frag_col_at(uint32_t p1, uint32_t p2, int ks) {
+  const v4i16 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (lds_v4i16*)(uintptr_t)(p1 + ks * (16 * TILE * 2)));
+  const v4i16 v2 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (lds_v4i16*)(uintptr_t)(p2 + ks * (16 * TILE * 2)));
   typedef short v8i16 __attribute__((ext_vector_type(8)));
   const v8i16 v = __builtin_shufflevector(v1, v2, 0, 1, 2, 3, 4, 5, 6, 7);
   return __builtin_bit_cast(bf16x8, v);

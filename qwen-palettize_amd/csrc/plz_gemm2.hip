@@ -134,21 +134,39 @@ __device__ __forceinline__ void mma_stage(const lds_u8* __restrict__ a_s,
   constexpr int NW = FILL ? 2 : 0;
   // global->LDS copies of the next stage issued by dma(): COPY_INSTS per dense operand
   constexpr int NDMA = COPY_INSTS * (FILL ? 1 : 2);
+  ColBases<WT_I> ca;
+  ColBases<WT_J> cb;
+  if constexpr (A_COL) col_bases(a_s, wi * (32 * WT_I), lane, ca);
+  if constexpr (A_COL && B_COL) col_bases(b_s, wj * (32 * WT_J), lane, cb);
+  auto frags = [&](int ks, bf16x8 (&a)[WT_I], bf16x8 (&b)[WT_J]) {
+    if constexpr (!A_COL) {  // one Col operand at most: the compiler's own addressing is as good
+      load_frags<false, B_COL>(a_s, b_s, ks, wi, wj, lane, a, b);
+      return;
+    }
+#pragma unroll
+    for (int i = 0; i < WT_I; ++i)
+      a[i] = A_COL ? frag_col_at(ca.p1[i], ca.p2[i], ks)
+                   : frag_row((const uint4*)a_s, wi * (32 * WT_I) + 32 * i, ks, lane);
+#pragma unroll
+    for (int j = 0; j < WT_J; ++j)
+      b[j] = B_COL ? frag_col_at(cb.p1[j], cb.p2[j], ks)
+                   : frag_row((const uint4*)b_s, wj * (32 * WT_J) + 32 * j, ks, lane);
+  };
   bf16x8 a0[WT_I], b0[WT_J], a1[WT_I], b1[WT_J];
-  load_frags<A_COL, B_COL>(a_s, b_s, 0, wi, wj, lane, a0, b0);
+  frags(0, a0, b0);
   __builtin_amdgcn_sched_barrier(0);
-  load_frags<A_COL, B_COL>(a_s, b_s, 1, wi, wj, lane, a1, b1);
+  frags(1, a1, b1);
   dma(na_s, nb_s);
   mma_kstep(acc, a0, b0);
   fill(0, nb_s);
   interleave_kstep<NREAD, NDMA, NV, NW>();
   __builtin_amdgcn_sched_barrier(0);
-  load_frags<A_COL, B_COL>(a_s, b_s, 2, wi, wj, lane, a0, b0);
+  frags(2, a0, b0);
   mma_kstep(acc, a1, b1);
   fill(1, nb_s);
   interleave_kstep<NREAD, 0, NV, NW>();
   __builtin_amdgcn_sched_barrier(0);
-  load_frags<A_COL, B_COL>(a_s, b_s, 3, wi, wj, lane, a1, b1);
+  frags(3, a1, b1);
   mma_kstep(acc, a0, b0);
   interleave_kstep<NREAD, 0, 0, 0>();
   __builtin_amdgcn_sched_barrier(0);
