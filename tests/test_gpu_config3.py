@@ -3,7 +3,9 @@ seven Qwen-4B linear shapes, LoRA rank 16 (32 on o and down), through the C ABI.
 
 These are the launch geometries the benchmark times: 640- and 2432-tile launches whose last
 partial wave is split over the reduction, the split-M grad_palette GEMM (up to 32 ways) and
-down's 38 palette groups along K. Outputs are checked on sampled rows against the fp64 oracle
+down's 38 palette groups along K. The forward and grad_x run both of their schedules:
+staged (W dequantised into the workspace, then the dense GEMM: what the query's workspace
+selects at this M) and the one-pass LUT GEMMs (a workspace for the tail partials only). Outputs are checked on sampled rows against the fp64 oracle
 (rows of y and grad_x; output rows n of grad_palette, which need only gy[:, n]^T x), at the
 north-star bar (max-rel-err 1e-2, cosine 0.9999); grad_palette must also be bit-repeatable.
 Inputs are drawn on the GPU from a seeded generator and copied to the host for the oracle.
@@ -50,28 +52,30 @@ def problems(dev):
     return out
 
 
+@pytest.mark.parametrize("staged", [True, False])
 @pytest.mark.parametrize("name", [s[0] for s in SHAPES])
-def test_config3_forward(dev, problems, name):
+def test_config3_forward(dev, problems, name, staged):
     p = problems[name]
     rows = torch.tensor(_rows(M, 1), device=dev)
     t = ops.lora_project(p["x"], p["a"], 1.0)
-    y = ops.lut_linear_fwd(p["x"], p["packed"], p["pal"], None, t, p["b"])
+    y = ops.lut_linear_fwd(p["x"], p["packed"], p["pal"], None, t, p["b"], staged=staged)
     W = O.dequant(p["idx"].cpu().numpy(), p["pal"].cpu().numpy())
     xr = f32(p["x"][rows])
     want = O.lut_linear_fwd(xr, W) + O.lora_forward(xr, f32(p["a"]), f32(p["b"]), 1.0)
-    assert_close(f32(y[rows]), want, what=f"{name} y (M={M})")
+    assert_close(f32(y[rows]), want, what=f"{name} y (M={M}, staged={staged})")
 
 
+@pytest.mark.parametrize("staged", [True, False])
 @pytest.mark.parametrize("name", [s[0] for s in SHAPES])
-def test_config3_grad_x(dev, problems, name):
+def test_config3_grad_x(dev, problems, name, staged):
     p = problems[name]
     rows = torch.tensor(_rows(M, 2), device=dev)
     gt = ops.lora_grad_t(p["gy"], p["b"], 1.0)
-    gx = ops.lut_linear_bwd_x(p["gy"], p["packed"], p["pal"], gt, p["a"])
+    gx = ops.lut_linear_bwd_x(p["gy"], p["packed"], p["pal"], gt, p["a"], staged=staged)
     W = O.dequant(p["idx"].cpu().numpy(), p["pal"].cpu().numpy())
     gyr = f32(p["gy"][rows]).astype(np.float64)
     want = O.grad_x(gyr, W) + (gyr @ f32(p["b"]).astype(np.float64)) @ f32(p["a"])
-    assert_close(f32(gx[rows]), want, what=f"{name} grad_x (M={M})")
+    assert_close(f32(gx[rows]), want, what=f"{name} grad_x (M={M}, staged={staged})")
 
 
 @pytest.mark.parametrize("name", [s[0] for s in SHAPES])
