@@ -4,9 +4,11 @@ One step = one hard LUT-linear forward + backward (grad_x, grad_palette, LoRA gr
 the seven Qwen-4B linear shapes at M = 16384 tokens (batch 32 x seq 512),
 straight-through through the frozen 2-bit indices, LoRA rank 16 (32 on o and down).
 `value` = sum over shapes of 6*M*K*N FLOP / step time (LoRA FLOP excluded, as in BASELINE),
-the step's kernels issued on one stream as the library's backward issues them. The
-per-kernel rooflines come from the same K steps run again with HIP events around every
-launch.
+the step's kernels issued on one stream as the library's backward issues them: the forward
+and grad_x dequantise W into their workspace and run the dense GEMM (from 4096 rows), and the
+grad_palette GEMM also yields both LoRA weight gradients from its dW tiles; the LoRA row
+products t = x A^T and gt = grad_y B run as their own HBM-bound kernels. The per-kernel
+rooflines come from the same K steps run again with HIP events around every launch.
 
 Also reported (same JSON line): the decode GEMV of config 2 (36 layers x 7 linears, M in
 {1, 4, 16}, one grouped launch per M) in GB/s of packed indices + palettes, the roofline of
@@ -42,9 +44,10 @@ PEAK_HBM_GBS = 8000.0
 # fwd and grad_x count their dequant_kernel launch too (from 4096 rows they dequantise W into the
 # workspace and run the dense GEMM on it).
 GEMM_TRAFFIC_BYTES = {"fwd": 975.7e6, "grad_x": 969.2e6, "grad_palette": 886.1e6}
-KERNEL_NAMES = {"fwd": "gemm2_kernel<OP_ROW, OP_LUT_REG, EPI_BF16> (fwd)",
+KERNEL_NAMES = {"fwd": "dequant_kernel + gemm2_kernel<OP_ROW, OP_ROW, EPI_BF16> (fwd)",
                 "grad_x": "dequant_kernel + gemm2_kernel<OP_ROW, OP_COL, EPI_BF16> (grad_x)",
-                "grad_palette": "gemm2_kernel<OP_COL, OP_COL, EPI_PAL> (grad_palette)"}
+                "grad_palette": "gemm2_kernel<OP_COL, OP_COL, EPI_PAL> (grad_palette + LoRA "
+                                "weight gradients)"}
 
 
 def _make_weight(N, K, gen, device):
@@ -93,12 +96,11 @@ class HardStep:
             e = self._mark(rec, "grad_x", it)
             ops.lut_linear_bwd_x(gy, it["packed"], it["pal"], gt, a)
             self._close(e)
+            # grad_palette and both LoRA weight gradients from one dW GEMM, as the library's
+            # backward runs it (functional.LUTLinearFunction)
             e = self._mark(rec, "grad_palette", it)
-            ops.lut_linear_bwd_palette(x, gy, it["packed"])
-            self._close(e)
-            e = self._mark(rec, "lora", it, 2.0 * M_TRAIN * (it["K"] + it["N"]) * r,
-                           M_TRAIN * (it["K"] + it["N"]) * 2)
-            ops.lora_weight_grads(x, gy, t, gt, 1.0, out_dtype=torch.bfloat16)
+            ops.lut_linear_bwd_palette_lora(x, gy, it["packed"], a, b, 1.0,
+                                            out_dtype=torch.bfloat16)
             self._close(e)
 
     @staticmethod

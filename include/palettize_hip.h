@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define PLZ_ABI_VERSION 6
+#define PLZ_ABI_VERSION 7
 
 /* status codes */
 #define PLZ_OK 0
@@ -106,6 +106,23 @@ size_t plz_lut_linear_bwd_palette_workspace(int64_t M, int64_t N, int64_t K);
 int plz_lut_linear_bwd_palette(const uint16_t* x, const uint16_t* grad_y, const int32_t* packed,
                                float* grad_palette, void* workspace, size_t workspace_bytes,
                                int64_t M, int64_t N, int64_t K, void* stream);
+
+/* grad_palette as plz_lut_linear_bwd_palette (bit for bit), plus both LoRA weight gradients
+ * from the same dW tiles: grad_a [rank, K] = scale * lora_b^T dW and grad_b [N, rank] =
+ * scale * dW lora_a^T with dW = grad_y^T x, lora_a [rank, K], lora_b [N, rank] bf16, rank a
+ * multiple of 8 in [8, 32]; grads_dtype PLZ_DT_BF16 or PLZ_DT_FP32 for grad_a / grad_b.
+ * These are the reference's LoRA weight gradients (autograd of QwenLoRA.forward,
+ * qwen_model.py:291-304: grad_B = grad_y^T (x A) s, grad_A = x^T (grad_y B) s), computed
+ * here in fp32 from dW without a further pass over x and grad_y (the separate route is
+ * plz_lora_weight_grads on t and gt). Deterministic (fixed-order sums). The workspace holds
+ * the grad_palette partials and the LoRA partials (query below; 16-byte aligned). */
+size_t plz_lut_linear_bwd_palette_lora_workspace(int64_t M, int64_t N, int64_t K, int rank);
+int plz_lut_linear_bwd_palette_lora(const uint16_t* x, const uint16_t* grad_y,
+                                    const int32_t* packed, const uint16_t* lora_a,
+                                    const uint16_t* lora_b, int rank, float scale,
+                                    float* grad_palette, void* grad_a, void* grad_b,
+                                    int grads_dtype, void* workspace, size_t workspace_bytes,
+                                    int64_t M, int64_t N, int64_t K, void* stream);
 
 /* No counterpart in the reference: plz_lut_linear_bwd_palette for callers that cannot
  * allocate (code under HIP graph capture, tight serving loops, harnesses that forbid

@@ -373,6 +373,17 @@ def lora_forward(x, lora_a, lora_b, scale: float) -> np.ndarray:
         lora_b, np.float64).T
 
 
+def lora_weight_grads(x, gy, lora_a, lora_b, scale: float):
+    """Gradients of y = scale (x A^T) B^T (QwenLoRA.forward, qwen_model.py:291-304, in the
+    native layout A [r, K], B [N, r]) for the output gradient gy: (grad_A [r, K], grad_B [N, r])
+    = (scale (gy B)^T x, scale gy^T (x A^T)) in fp64."""
+    x = np.asarray(x, np.float64)
+    gy = np.asarray(gy, np.float64)
+    a = np.asarray(lora_a, np.float64)
+    b = np.asarray(lora_b, np.float64)
+    return scale * (gy @ b).T @ x, scale * gy.T @ (x @ a.T)
+
+
 def rmsnorm_fwd(x, weight, eps: float):
     """y = bf16(w * bf16(x * rsqrt(mean(x^2) + eps))), statistics in fp32."""
     xf = np.asarray(x, np.float32)

@@ -81,6 +81,10 @@ struct Args {
   uint64_t noise_seed, noise_offset;  // noise == nullptr: Philox at noise_offset + n*K + k
   int logits_f16;
   float* acc_ws;  // EPI_F32: partial dW rows of each reduction split, [split][I][J] fp32
+  // EPI_PAL with wg_r > 0: the LoRA weight gradients from the dW tile (wg_a = lora_a [r, K],
+  // wg_b = lora_b [N, r]); partials [split][tiles_i][r][K] and [split][tiles_j][r][N]
+  const uint16_t* wg_a; const uint16_t* wg_b; int wg_r;
+  float* wg_part_a; float* wg_part_b;
   // EPI_BF16 tail split: tiles [tail_first, tiles) run as tail_split reduction parts of
   // tail_len each, whose fp32 accumulators go to tail_ws (accumulator layout, 256 KB per part);
   // tail_reduce_kernel sums them and stores the tiles

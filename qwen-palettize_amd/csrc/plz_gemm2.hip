@@ -52,6 +52,131 @@ __device__ __forceinline__ int ptile(int row, int col) {  // 128 x 256 fp32 stag
   return row * 256 + ((((col >> 2) ^ (row & 63))) << 2) + (col & 3);
 }
 
+// ---- LoRA weight gradients from the hard dW tile (EPI_PAL with g.wg_r > 0) ---------------
+// With t = s x A^T and gt = s grad_y B (A = lora_a [r, K], B = lora_b [N, r]):
+//   grad_B = grad_y^T t = s dW A^T,   grad_A = gt^T x = s B^T dW,   dW = grad_y^T x.
+// Every dW tile (256 n x 256 k of one M split) adds its share: grad_A's from the accumulator
+// registers (they are directly the dW^T operand of an MFMA: lane = k, registers = n), grad_B's
+// from the fp32 staging the palette epilogue already writes (rows n as MFMA A fragments).
+// Partials: [split][tiles_i][r][K] (the two wave rows summed in LDS) and
+// [split][tiles_j][r][N], summed in a fixed order by wg_reduce_kernel, which also applies s.
+// 32x32x16 MFMAs with the rank padded to 32 columns (lanes j >= r feed zeros).
+constexpr int WG_BT_OFF = 128 * 1024;  // B^T of the tile's rows in LDS: [32][256] bf16
+constexpr int WG_AT_OFF = 144 * 1024;  // A's slice of the tile's k: [32][256] bf16, 16-byte
+                                       // chunk c of row j at chunk c ^ (j & 31)
+typedef __attribute__((address_space(3))) uint16_t lds_u16;
+typedef __attribute__((address_space(3))) u32x2 lds_u32x2;
+typedef __attribute__((address_space(3))) u32x4 lds_w4;
+
+// The tile's slices of both LoRA operands into LDS (all threads; every global load is issued
+// before any is used): B^T[j][n - i0] for its 256 rows (zero past N) and A[j][k - j0].
+__device__ __forceinline__ void stage_lora_operands(const Args& g, lds_u8* lbase, int64_t i0,
+                                                    int64_t j0) {
+  lds_u16* bt = reinterpret_cast<lds_u16*>(lbase + WG_BT_OFF);
+  lds_w4* at = reinterpret_cast<lds_w4*>(lbase + WG_AT_OFF);
+  const int r = g.wg_r, cpr = r / 8;  // 16-byte chunks per row of B
+  const int64_t K = g.J;
+  constexpr int MAXIT = TILE * 4 / NTHR;  // rank 32: 2 chunks of B and 2 of A per thread
+  uint4 vb[MAXIT], va[MAXIT];
+#pragma unroll
+  for (int it = 0; it < MAXIT; ++it) {
+    const int idx = threadIdx.x + it * NTHR;
+    vb[it] = va[it] = make_uint4(0, 0, 0, 0);
+    if (idx < TILE * cpr) {
+      const int nl = idx / cpr, c = idx - nl * cpr;
+      if (i0 + nl < g.I) vb[it] = *reinterpret_cast<const uint4*>(g.wg_b + (i0 + nl) * r + 8 * c);
+    }
+    if (idx < r * (TILE / 8)) {
+      const int j = idx >> 5, c = idx & 31;
+      if (j0 + 8 * c < K) va[it] = *reinterpret_cast<const uint4*>(g.wg_a + j * K + j0 + 8 * c);
+    }
+  }
+#pragma unroll
+  for (int it = 0; it < MAXIT; ++it) {
+    const int idx = threadIdx.x + it * NTHR;
+    if (idx < TILE * cpr) {
+      const int nl = idx / cpr, c = idx - nl * cpr;
+      const uint32_t w[4] = {vb[it].x, vb[it].y, vb[it].z, vb[it].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        bt[(8 * c + 2 * e) * TILE + nl] = (uint16_t)(w[e] & 0xffffu);
+        bt[(8 * c + 2 * e + 1) * TILE + nl] = (uint16_t)(w[e] >> 16);
+      }
+    }
+    if (idx < r * (TILE / 8)) {
+      const int j = idx >> 5, c = idx & 31;
+      at[j * 32 + (c ^ (j & 31))] = u32x4{va[it].x, va[it].y, va[it].z, va[it].w};
+    }
+  }
+}
+
+// grad_A share of this wave's 128 x 64 of dW: C^T[k][j] = sum_n dW[n][k] B[n][j]. MFMA slot
+// s = 8h + i (h = lane / 32) of block (ti, eh) is n = 32 ti + 16 eh + 8 (i / 4) + 4 h + i % 4:
+// the accumulator registers 8 eh .. 8 eh + 7 of lane (k, h) hold exactly those n.
+__device__ __forceinline__ void lora_grad_a(const Args& g, const f32x16 (&acc)[WT_I][WT_J],
+                                            const lds_u8* lbase, int wi, int lane,
+                                            f32x16 (&ca)[WT_J]) {
+  const lds_u16* bt = reinterpret_cast<const lds_u16*>(lbase + WG_BT_OFF);
+  const int j = lane & 31, h = lane >> 5;
+  const bool jv = j < g.wg_r;
+#pragma unroll
+  for (int tj = 0; tj < WT_J; ++tj) ca[tj] = f32x16{};
+#pragma unroll
+  for (int ti = 0; ti < WT_I; ++ti)
+#pragma unroll
+    for (int eh = 0; eh < 2; ++eh) {
+      const int nl = wi * 128 + 32 * ti + 16 * eh + 4 * h;
+      u32x2 lo = {0u, 0u}, hi = {0u, 0u};
+      if (jv) {
+        lo = *reinterpret_cast<const lds_u32x2*>(bt + j * TILE + nl);
+        hi = *reinterpret_cast<const lds_u32x2*>(bt + j * TILE + nl + 8);
+      }
+      const bf16x8 bf = __builtin_bit_cast(bf16x8, u32x4{lo.x, lo.y, hi.x, hi.y});
+#pragma unroll
+      for (int tj = 0; tj < WT_J; ++tj) {
+        const f32x16& a = acc[ti][tj];
+        const bf16x8 af = __builtin_bit_cast(
+            bf16x8, u32x4{f2bf2(a[8 * eh], a[8 * eh + 1]), f2bf2(a[8 * eh + 2], a[8 * eh + 3]),
+                          f2bf2(a[8 * eh + 4], a[8 * eh + 5]), f2bf2(a[8 * eh + 6], a[8 * eh + 7])});
+        ca[tj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, bf, ca[tj], 0, 0, 0);
+      }
+    }
+}
+
+// grad_B share of one 32-row block of the staged half (staging rows 32 q .. 32 q + 31) over the
+// tile's 256 k: C[n][j] = sum_k dW[n][k] A[j][k].
+__device__ __forceinline__ void lora_grad_b(const Args& g, const float* sC, const lds_u8* lbase,
+                                            int64_t i0, int half, int zsl, int tile_j, int q,
+                                            int lane) {
+  const lds_w4* at = reinterpret_cast<const lds_w4*>(lbase + WG_AT_OFF);
+  const int j = lane & 31, h = lane >> 5;
+  const bool jv = j < g.wg_r;
+  const int sr = 32 * q + (lane & 31);
+  f32x16 cb = f32x16{};
+#pragma unroll 4
+  for (int ks = 0; ks < TILE / 16; ++ks) {
+    const int col = 16 * ks + 8 * h;
+    const float4 v0 = *reinterpret_cast<const float4*>(&sC[ptile(sr, col)]);
+    const float4 v1 = *reinterpret_cast<const float4*>(&sC[ptile(sr, col + 4)]);
+    const bf16x8 af = __builtin_bit_cast(
+        bf16x8, u32x4{f2bf2(v0.x, v0.y), f2bf2(v0.z, v0.w), f2bf2(v1.x, v1.y), f2bf2(v1.z, v1.w)});
+    u32x4 bv = {0u, 0u, 0u, 0u};
+    if (jv) bv = at[j * 32 + ((2 * ks + h) ^ (j & 31))];
+    cb = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, __builtin_bit_cast(bf16x8, bv), cb, 0, 0, 0);
+  }
+  if (!jv) return;
+  // j-major partial [split][tiles_j][r][N]: registers 4 e4 .. 4 e4 + 3 are 4 consecutive rows
+  float* dst = g.wg_part_b + (((int64_t)zsl * g.tiles_j + tile_j) * g.wg_r + j) * g.I;
+#pragma unroll
+  for (int e4 = 0; e4 < 4; ++e4) {
+    const int srr = 32 * q + 8 * e4 + 4 * h;
+    const int64_t n = i0 + (srr >> 6) * 128 + 64 * half + (srr & 63);
+    if (n < g.I)
+      *reinterpret_cast<float4*>(dst + n) =
+          make_float4(cb[4 * e4], cb[4 * e4 + 1], cb[4 * e4 + 2], cb[4 * e4 + 3]);
+  }
+}
+
 // One reduction stage of MFMAs on LDS tiles: 4 k-steps of 16, 4x4 blocks of 32x32 per wave.
 // Fragments are double-buffered in registers: the LDS reads of k-step ks+1 are issued before
 // the 16 MFMAs of k-step ks, so one wave per SIMD keeps the matrix core busy. The scheduling
@@ -734,6 +859,42 @@ __global__ __launch_bounds__(NTHR) void gemm2_kernel(const Args g) {
     return;
   }
 
+  // LoRA weight gradients (hard grad_palette only): grad_A's share from the accumulators
+  // before they are staged (B^T of the tile's rows through LDS past the staging area)
+  const bool wgrad = EPI == EPI_PAL && g.wg_r > 0;
+  if (EPI == EPI_PAL && wgrad) {
+    stage_lora_operands(g, lbase, i0, j0);
+    __syncthreads();
+    f32x16 ca[WT_J];
+    lora_grad_a(g, acc, lbase, wi, lane, ca);
+    // the two wave rows' shares of the same k columns meet in LDS (the staging area, free until
+    // the staging below): [wj][tj][register][lane]
+    float* xs = reinterpret_cast<float*>(smem);
+    if (wi == 1)
+#pragma unroll
+      for (int tj = 0; tj < WT_J; ++tj)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) xs[((wj * WT_J + tj) * 16 + e) * 64 + lane] = ca[tj][e];
+    __syncthreads();
+    const int jr = lane & 31, hr = lane >> 5;
+    if (wi == 0 && jr < g.wg_r) {
+      // ca[tj]: rows k = 8 (e / 4) + 4 h + e % 4 of the wave's k-block tj, column j
+      float* dst = g.wg_part_a + (((int64_t)zsl * g.tiles_i + tile_i) * g.wg_r + jr) * g.J;
+#pragma unroll
+      for (int tj = 0; tj < WT_J; ++tj)
+#pragma unroll
+        for (int e4 = 0; e4 < 4; ++e4) {
+          float v[4];
+#pragma unroll
+          for (int u = 0; u < 4; ++u)
+            v[u] = ca[tj][4 * e4 + u] + xs[((wj * WT_J + tj) * 16 + 4 * e4 + u) * 64 + lane];
+          const int64_t k = j0 + wj * (32 * WT_J) + 32 * tj + 8 * e4 + 4 * hr;
+          if (k < g.J) *reinterpret_cast<float4*>(dst + k) = make_float4(v[0], v[1], v[2], v[3]);
+        }
+    }
+    __syncthreads();  // the staging below overwrites xs
+  }
+
   // dW tile (rows n = i, cols k = j) staged in two passes of 128 rows of fp32: pass p holds
   // rows wi*128 + 64p .. +64 of every wave (staging row sr <-> tile row
   // (sr/64)*128 + 64p + sr%64), so half of each wave's accumulators are dead after pass 0.
@@ -784,6 +945,9 @@ __global__ __launch_bounds__(NTHR) void gemm2_kernel(const Args g) {
         float* dst = g.partial + (((int64_t)zsl * g.I + n) * segs + kseg / 128) * 4;
         *reinterpret_cast<float4*>(dst) = make_float4(s0, s1, s2, s3);
       }
+      // waves 4..7 (idle in the class sums): grad_B's share of the staged half
+      if (wgrad && threadIdx.x >= 256)
+        lora_grad_b(g, sC, lbase, i0, half, zsl, tile_j, wave - 4, lane);
     } else {  // EPI_SOFT / EPI_F32: each wave walks (row, 128-k segment) items; lane = 2 k
       for (int item = wave; item < 256; item += NTHR / 64) {
         const int row = item >> 1, h = item & 1;
@@ -949,6 +1113,30 @@ __global__ void reduce_pal_kernel(const float* __restrict__ partial, float* __re
   *reinterpret_cast<float4*>(out + t * 4) = s;
 }
 
+// grad_A [r, K] and grad_B [N, r] = scale x the sum of their partials, in partial order
+// (threads 0 .. la-1: grad_A from [p][r][K]; then grad_B from the j-major [p][r][N], thread
+// j * N + n writing grad_B[n][j]); bf16 (out_bf16) or fp32 out.
+__global__ void wg_reduce_kernel(const float* __restrict__ pa, const float* __restrict__ pb,
+                                 void* ga, void* gb, int64_t la, int na, int64_t lb, int nb,
+                                 int64_t N, int r, float scale, int out_bf16) {
+  int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const bool second = t >= la;
+  if (second) t -= la;
+  const int64_t L = second ? lb : la;
+  if (t >= L) return;
+  const float* src = (second ? pb : pa) + t;
+  const int np = second ? nb : na;
+  float s = 0.f;
+  for (int p = 0; p < np; ++p) s += src[(int64_t)p * L];
+  s *= scale;
+  const int64_t o = second ? (t % N) * r + t / N : t;
+  void* out = second ? gb : ga;
+  if (out_bf16)
+    reinterpret_cast<uint16_t*>(out)[o] = (uint16_t)f2bf(s);
+  else
+    reinterpret_cast<float*>(out)[o] = s;
+}
+
 static bool a16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 static int palette_splits(int64_t M, int64_t N, int64_t K) {
@@ -957,15 +1145,38 @@ static int palette_splits(int64_t M, int64_t N, int64_t K) {
 
 // The class-reduced dW GEMM over z splits of M (fp32 partials [z][N][K/128][4] in `partial`,
 // every entry written by the GEMM), then the fixed-order sum of the partials.
+// LoRA weight gradients riding on the hard grad_palette GEMM (optional)
+struct WgradArgs {
+  const uint16_t* lora_a = nullptr;  // [r, K]
+  const uint16_t* lora_b = nullptr;  // [N, r]
+  int rank = 0;
+  float scale = 1.f;
+  void* grad_a = nullptr;  // [r, K]
+  void* grad_b = nullptr;  // [N, r]
+  int out_bf16 = 1;
+  float* part_a = nullptr;
+  float* part_b = nullptr;
+};
+static size_t wg_part_a_floats(int z, int64_t N, int64_t K, int r) {
+  return (size_t)z * ((N + TILE - 1) / TILE) * r * K;
+}
+static size_t wg_part_b_floats(int z, int64_t N, int64_t K, int r) {
+  return (size_t)z * ((K + TILE - 1) / TILE) * N * r;
+}
+
 static int bwd_palette(const uint16_t* x, const uint16_t* grad_y, const int32_t* packed,
                        float* grad_palette, float* partial, int z, int64_t M, int64_t N,
-                       int64_t K, hipStream_t stream, const char* what) {
+                       int64_t K, hipStream_t stream, const char* what,
+                       const WgradArgs& wg = WgradArgs()) {
   Args g = {};
   g.a = grad_y; g.lda = N;   // A(i=n, r=m) = grad_y[m, n]   (Col tile)
   g.b = x; g.ldb = K;        // B(j=k, r=m) = x[m, k]        (Col tile)
   g.packed = packed; g.Nw = N; g.Kw = K;
   g.I = N; g.J = K; g.R = M; g.r_split = split_len(M, z);
   g.partial = partial;
+  g.wg_r = wg.rank;
+  g.wg_a = wg.lora_a; g.wg_b = wg.lora_b;
+  g.wg_part_a = wg.part_a; g.wg_part_b = wg.part_b;
   // XCD-contiguous item ranges walk the panels of the larger operand: a range then reads a
   // slice of that operand and all of the smaller one (down_proj dW 966 -> 1056 TFLOP/s)
   g.group = K > N ? -1 : 1;
@@ -974,6 +1185,13 @@ static int bwd_palette(const uint16_t* x, const uint16_t* grad_y, const int32_t*
   const int64_t G = K / 256, n_out = N * G;
   hipLaunchKernelGGL(reduce_pal_kernel, dim3((unsigned)((n_out + 255) / 256)), dim3(256), 0,
                      stream, g.partial, grad_palette, N, G, z);
+  if (wg.rank > 0) {
+    const int64_t la = (int64_t)wg.rank * K, lb = N * wg.rank;
+    const int na = z * (int)((N + TILE - 1) / TILE), nb = z * (int)((K + TILE - 1) / TILE);
+    hipLaunchKernelGGL(wg_reduce_kernel, dim3((unsigned)((la + lb + 255) / 256)), dim3(256), 0,
+                       stream, wg.part_a, wg.part_b, wg.grad_a, wg.grad_b, la, na, lb, nb, N,
+                       wg.rank, wg.scale, wg.out_bf16);
+  }
   return check_launch(what);
 }
 
@@ -1161,6 +1379,62 @@ int plz_lut_linear_bwd_palette(const uint16_t* x, const uint16_t* grad_y, const 
   return bwd_palette(x, grad_y, packed, grad_palette, reinterpret_cast<float*>(workspace),
                      palette_splits(M, N, K), M, N, K, (hipStream_t)stream,
                      "plz_lut_linear_bwd_palette");
+}
+
+static size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+size_t plz_lut_linear_bwd_palette_lora_workspace(int64_t M, int64_t N, int64_t K, int rank) {
+  if (M <= 0 || N <= 0 || K <= 0 || rank <= 0) return plz_lut_linear_bwd_palette_workspace(M, N, K);
+  const int z = palette_splits(M, N, K);
+  return align256(plz_lut_linear_bwd_palette_workspace(M, N, K)) +
+         align256(wg_part_a_floats(z, N, K, rank) * sizeof(float)) +
+         align256(wg_part_b_floats(z, N, K, rank) * sizeof(float));
+}
+
+int plz_lut_linear_bwd_palette_lora(const uint16_t* x, const uint16_t* grad_y,
+                                    const int32_t* packed, const uint16_t* lora_a,
+                                    const uint16_t* lora_b, int rank, float scale,
+                                    float* grad_palette, void* grad_a, void* grad_b,
+                                    int grads_dtype, void* workspace, size_t workspace_bytes,
+                                    int64_t M, int64_t N, int64_t K, void* stream) {
+  const char* what = "plz_lut_linear_bwd_palette_lora";
+  PLZ_REQUIRE(M >= 0 && N >= 0 && K >= 0, "%s: negative shape", what);
+  PLZ_REQUIRE(K % 256 == 0, "%s: K (%lld) must be a multiple of 256", what, (long long)K);
+  PLZ_REQUIRE(N % 8 == 0, "%s: N (%lld) must be a multiple of 8", what, (long long)N);
+  PLZ_REQUIRE(rank > 0 && rank <= 32 && rank % 8 == 0,
+              "%s: rank (%d) must be a multiple of 8 in [8, 32]", what, rank);
+  PLZ_REQUIRE(grads_dtype == PLZ_DT_BF16 || grads_dtype == PLZ_DT_FP32,
+              "%s: grads_dtype must be PLZ_DT_BF16 or PLZ_DT_FP32", what);
+  if (N == 0 || K == 0) return PLZ_OK;
+  PLZ_REQUIRE(packed && grad_palette && lora_a && lora_b && grad_a && grad_b,
+              "%s: null pointer", what);
+  PLZ_REQUIRE(a16(lora_a) && a16(lora_b), "%s: lora_a and lora_b must be 16-byte aligned", what);
+  const size_t esz = grads_dtype == PLZ_DT_BF16 ? 2 : 4;
+  if (M == 0) {  // empty reduction: every gradient is zero
+    zero_async(grad_palette, (size_t)N * (K / 256) * 16, (hipStream_t)stream);
+    zero_async(grad_a, (size_t)rank * K * esz, (hipStream_t)stream);
+    zero_async(grad_b, (size_t)N * rank * esz, (hipStream_t)stream);
+    return check_launch(what);
+  }
+  PLZ_REQUIRE(x && grad_y && a16(x) && a16(grad_y) && a16(packed),
+              "%s: x, grad_y and packed must be non-null, 16-byte aligned", what);
+  const size_t need = plz_lut_linear_bwd_palette_lora_workspace(M, N, K, rank);
+  if (!workspace || !a16(workspace) || workspace_bytes < need) {
+    set_error("%s: workspace of %zu bytes (16-byte aligned) needed, %zu given", what, need,
+              workspace_bytes);
+    return PLZ_EWORKSPACE;
+  }
+  const int z = palette_splits(M, N, K);
+  uint8_t* w = static_cast<uint8_t*>(workspace);
+  WgradArgs wg;
+  wg.lora_a = lora_a; wg.lora_b = lora_b; wg.rank = rank; wg.scale = scale;
+  wg.grad_a = grad_a; wg.grad_b = grad_b; wg.out_bf16 = grads_dtype == PLZ_DT_BF16;
+  const size_t pal_bytes = align256(plz_lut_linear_bwd_palette_workspace(M, N, K));
+  wg.part_a = reinterpret_cast<float*>(w + pal_bytes);
+  wg.part_b = reinterpret_cast<float*>(
+      w + pal_bytes + align256(wg_part_a_floats(z, N, K, rank) * sizeof(float)));
+  return bwd_palette(x, grad_y, packed, grad_palette, reinterpret_cast<float*>(w), z, M, N, K,
+                     (hipStream_t)stream, what, wg);
 }
 
 int plz_lut_linear_bwd_palette_noalloc(const uint16_t* x, const uint16_t* grad_y,

@@ -61,6 +61,9 @@ SIGNATURES: dict[str, tuple] = {
     "plz_lut_linear_bwd_palette_workspace": (sz, [i64, i64, i64]),
     "plz_lut_linear_bwd_palette": (i32, [p, p, p, p, p, sz, i64, i64, i64, p]),
     "plz_lut_linear_bwd_palette_noalloc": (i32, [p, p, p, p, i64, i64, i64, p]),
+    "plz_lut_linear_bwd_palette_lora_workspace": (sz, [i64, i64, i64, i32]),
+    "plz_lut_linear_bwd_palette_lora": (i32, [p, p, p, p, p, i32, f32, p, p, p, i32, p, sz,
+                                              i64, i64, i64, p]),
     "plz_bias_grad": (i32, [p, p, i64, i64, p]),
     "plz_linear_fwd_dense": (i32, [p, p, p, p, p, i32, p, p, sz, i64, i64, i64, p]),
     "plz_linear_fwd_dense_workspace": (sz, [i64, i64, i64]),

@@ -45,15 +45,23 @@ class LUTLinearFunction(torch.autograd.Function):
         need_x, _, need_pal, need_b, need_la, need_lb, _ = ctx.needs_input_grad
         # one stream: grad_palette beside grad_x on a second stream measured slower (both are
         # MFMA-bound GEMMs that fill the GPU; they only contend)
+        need_lora = lora_a is not None and (need_la or need_lb)
+        # the LoRA weight gradients ride on the grad_palette GEMM (from its dW tiles) when both
+        # are wanted and the rank is one the fused epilogue takes
+        fused = need_lora and need_pal and lora_a.shape[0] in (8, 16, 24, 32)
         gt = None
-        if lora_a is not None and (need_x or need_la or need_lb):
+        if lora_a is not None and (need_x or (need_lora and not fused)):
             gt = ops.lora_grad_t(gy, lora_b, ctx.lora_scale)
         grad_x = ops.lut_linear_bwd_x(gy, packed, palette, gt, lora_a) if need_x else None
         grad_bias = ops.bias_grad(gy).to(ctx.bias_dtype) if (ctx.has_bias and need_b) else None
-        grad_pal = ops.lut_linear_bwd_palette(x, gy, packed) if need_pal else None
-        grad_a = grad_b = None
-        if lora_a is not None and (need_la or need_lb):
-            grad_a, grad_b = ops.lora_weight_grads(x, gy, t, gt, 1.0, out_dtype=lora_a.dtype)
+        grad_pal = grad_a = grad_b = None
+        if fused:
+            grad_pal, grad_a, grad_b = ops.lut_linear_bwd_palette_lora(
+                x, gy, packed, lora_a, lora_b, ctx.lora_scale, out_dtype=lora_a.dtype)
+        else:
+            grad_pal = ops.lut_linear_bwd_palette(x, gy, packed) if need_pal else None
+            if need_lora:
+                grad_a, grad_b = ops.lora_weight_grads(x, gy, t, gt, 1.0, out_dtype=lora_a.dtype)
         return grad_x, None, grad_pal, grad_bias, grad_a, grad_b, None
 
 

@@ -185,6 +185,31 @@ def lut_linear_bwd_palette(x, grad_y, packed):
     return out
 
 
+def lut_linear_bwd_palette_lora(x, grad_y, packed, lora_a, lora_b, scale: float = 1.0,
+                                out_dtype=torch.bfloat16):
+    """(grad_palette, grad_a [r, K], grad_b [N, r]) from one dW GEMM: the palette gradient as
+    lut_linear_bwd_palette, and the LoRA weight gradients scale * lora_b^T dW and
+    scale * dW lora_a^T (dW = grad_y^T x), which lora_weight_grads computes from t and gt."""
+    _need(packed, "packed", torch.int32, 2)
+    for name, v in (("x", x), ("grad_y", grad_y), ("lora_a", lora_a), ("lora_b", lora_b)):
+        _need(v, name, torch.bfloat16, 2)
+    N, K = packed.shape[0], packed.shape[1] * 16
+    M = x.shape[0]
+    r = lora_a.shape[0]
+    if x.shape[1] != K or tuple(grad_y.shape) != (M, N):
+        raise ValueError("x / grad_y shape mismatch")
+    if tuple(lora_a.shape) != (r, K) or tuple(lora_b.shape) != (N, r):
+        raise ValueError("lora_a must be [r, K] and lora_b [N, r]")
+    out = torch.empty((N, K // 256, 4), dtype=torch.float32, device=x.device)
+    ga = torch.empty((r, K), dtype=out_dtype, device=x.device)
+    gb = torch.empty((N, r), dtype=out_dtype, device=x.device)
+    ws = _workspace(query("plz_lut_linear_bwd_palette_lora_workspace", M, N, K, r), x.device)
+    call("plz_lut_linear_bwd_palette_lora", _ptr(x), _ptr(grad_y), _ptr(packed), _ptr(lora_a),
+         _ptr(lora_b), r, float(scale), _ptr(out), _ptr(ga), _ptr(gb), _DT[out_dtype], _ptr(ws),
+         ws.numel(), M, N, K, _stream(x))
+    return out, ga, gb
+
+
 def lut_linear_bwd_palette_noalloc(x, grad_y, packed, out=None):
     """lut_linear_bwd_palette through the entry point that allocates nothing (its split-M
     partials live in a fixed device array of the library; calls that overlap on one GPU race).

@@ -36,7 +36,7 @@ def test_every_declared_symbol_is_exported(lib):
         assert hasattr(lib, n), f"{n} declared in the header but not exported"
         assert n in _lib.SIGNATURES, f"{n} has no ctypes signature"
     assert set(_lib.SIGNATURES) == set(names)
-    assert lib.plz_abi_version() == 6
+    assert lib.plz_abi_version() == 7
 
 
 def test_shape_errors_are_reported_without_touching_the_gpu(lib):
@@ -52,6 +52,12 @@ def test_shape_errors_are_reported_without_touching_the_gpu(lib):
     assert rc == 1 and b"tau" in lib.plz_last_error()
     rc = lib.plz_rmsnorm_fwd(None, None, None, None, 4, 5000, 1e-6, None)
     assert rc == 1
+    rc = lib.plz_lut_linear_bwd_palette_lora(None, None, None, None, None, 12, 1.0, None, None,
+                                             None, 0, None, 0, 64, 256, 256, None)
+    assert rc == 1 and b"rank" in lib.plz_last_error()
+    rc = lib.plz_lut_linear_bwd_palette_lora(None, None, None, None, None, 16, 1.0, None, None,
+                                             None, 0, None, 0, 64, 256, 256, None)
+    assert rc == 1 and b"null" in lib.plz_last_error()
 
 
 def test_tail_split_workspace_queries(lib):

@@ -1,0 +1,71 @@
+"""GPU: the LoRA weight gradients computed inside the hard grad_palette GEMM
+(plz_lut_linear_bwd_palette_lora) against the fp64 oracle of QwenLoRA's autograd
+(qwen_model.py:291-304): grad_A = s (gy B)^T x, grad_B = s gy^T (x A^T). The palette gradient
+of the same call must be bit-equal to plz_lut_linear_bwd_palette's, and the whole result
+bit-repeatable. Shapes cover a ragged last row tile (N = 1032), a reduction shorter than one
+stage, split-M launches and every supported rank."""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from helpers import assert_close, f32, make_weight, randn_bf16
+
+pytestmark = pytest.mark.gpu
+ops = pytest.importorskip("palettize_hip.ops")
+
+
+@pytest.mark.parametrize("M,N,K,rank,scale", [
+    (512, 2560, 2560, 16, 2.0),   # config 1 shape
+    (300, 1032, 768, 8, 1.0),
+    (77, 136, 256, 24, 0.5),
+    (2048, 256, 512, 32, 1.0),
+    (4096, 1024, 2560, 16, 2.0),
+])
+def test_bwd_palette_lora(dev, M, N, K, rank, scale):
+    idx, _ = make_weight(N, K, seed=M + N)
+    p = ops.pack_indices(idx.to(dev))
+    x = randn_bf16(M, K, seed=1).to(dev)
+    gy = randn_bf16(M, N, seed=2).to(dev)
+    a = randn_bf16(rank, K, seed=3, std=0.01).to(dev)
+    b = randn_bf16(N, rank, seed=4, std=0.01).to(dev)
+    gp, ga, gb = ops.lut_linear_bwd_palette_lora(x, gy, p, a, b, scale)
+    assert torch.equal(gp, ops.lut_linear_bwd_palette(x, gy, p))
+    wa, wb = O.lora_weight_grads(f32(x), f32(gy), f32(a), f32(b), scale)
+    assert_close(f32(ga), wa, what="grad_a")
+    assert_close(f32(gb), wb, what="grad_b")
+    gp2, ga2, gb2 = ops.lut_linear_bwd_palette_lora(x, gy, p, a, b, scale)
+    assert torch.equal(gp, gp2) and torch.equal(ga, ga2) and torch.equal(gb, gb2)
+    # fp32 outputs: the same sums before the bf16 rounding
+    _, fa, fb = ops.lut_linear_bwd_palette_lora(x, gy, p, a, b, scale, out_dtype=torch.float32)
+    assert torch.equal(fa.to(torch.bfloat16), ga) and torch.equal(fb.to(torch.bfloat16), gb)
+
+
+def test_bwd_palette_lora_agrees_with_the_separate_route(dev):
+    """Against lora_weight_grads on t = s x A^T and gt = s gy B (bf16), the route the fused
+    call replaces: equal within the bf16 rounding of t and gt."""
+    M, N, K, r, s = 1024, 512, 1024, 16, 2.0
+    idx, _ = make_weight(N, K, seed=5)
+    p = ops.pack_indices(idx.to(dev))
+    x = randn_bf16(M, K, seed=6).to(dev)
+    gy = randn_bf16(M, N, seed=7).to(dev)
+    a = randn_bf16(r, K, seed=8, std=0.01).to(dev)
+    b = randn_bf16(N, r, seed=9, std=0.01).to(dev)
+    _, ga, gb = ops.lut_linear_bwd_palette_lora(x, gy, p, a, b, s)
+    t = ops.lora_project(x, a, s)
+    gt = ops.lora_grad_t(gy, b, s)
+    ra, rb = ops.lora_weight_grads(x, gy, t, gt, 1.0, out_dtype=torch.bfloat16)
+    assert_close(f32(ga), f32(ra).astype(np.float64), max_rel=2e-2, min_cos=0.9999, what="grad_a")
+    assert_close(f32(gb), f32(rb).astype(np.float64), max_rel=2e-2, min_cos=0.9999, what="grad_b")
+
+
+def test_bwd_palette_lora_empty_reduction_gives_zeros(dev):
+    N, K, r = 256, 512, 16
+    idx, _ = make_weight(N, K, seed=10)
+    p = ops.pack_indices(idx.to(dev))
+    x = torch.empty(0, K, dtype=torch.bfloat16, device=dev)
+    gy = torch.empty(0, N, dtype=torch.bfloat16, device=dev)
+    a = randn_bf16(r, K, seed=11).to(dev)
+    b = randn_bf16(N, r, seed=12).to(dev)
+    gp, ga, gb = ops.lut_linear_bwd_palette_lora(x, gy, p, a, b, 1.0)
+    assert not gp.any() and not ga.any() and not gb.any()

@@ -303,6 +303,11 @@ def test_lora_forward_and_grads_vs_torch_autograd():
     y = 2.0 * (x @ A.T) @ B.T
     assert np.allclose(O.lora_forward(x.numpy(), A.detach().numpy(), B.detach().numpy(), 2.0),
                        y.detach().numpy())
+    gy = torch.randn(5, 32, dtype=torch.float64, generator=g)
+    y.backward(gy)
+    ga, gb = O.lora_weight_grads(x.numpy(), gy.numpy(), A.detach().numpy(), B.detach().numpy(),
+                                 2.0)
+    assert np.allclose(ga, A.grad.numpy()) and np.allclose(gb, B.grad.numpy())
 
 
 def test_rmsnorm_matches_hf_formula():
