@@ -1126,8 +1126,17 @@ __global__ void wg_reduce_kernel(const float* __restrict__ pa, const float* __re
   if (t >= L) return;
   const float* src = (second ? pb : pa) + t;
   const int np = second ? nb : na;
+  // the loads of 8 partials are issued together, the adds stay in partial order
   float s = 0.f;
-  for (int p = 0; p < np; ++p) s += src[(int64_t)p * L];
+  int p = 0;
+  for (; p + 8 <= np; p += 8) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = src[(int64_t)(p + u) * L];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) s += v[u];
+  }
+  for (; p < np; ++p) s += src[(int64_t)p * L];
   s *= scale;
   const int64_t o = second ? (t % N) * r + t / N : t;
   void* out = second ? gb : ga;
