@@ -61,7 +61,9 @@ __device__ __forceinline__ int ptile(int row, int col) {  // 128 x 256 fp32 stag
 // Partials: [split][tiles_i][r][K] (the two wave rows summed in LDS) and
 // [split][tiles_j][r][N], summed in a fixed order by wg_reduce_kernel, which also applies s.
 // 32x32x16 MFMAs with the rank padded to 32 columns (lanes j >= r feed zeros).
-constexpr int WG_BT_OFF = 128 * 1024;  // B^T of the tile's rows in LDS: [32][256] bf16
+constexpr int WG_BT_OFF = 128 * 1024;  // B^T of the tile's rows in LDS: [32][256] bf16,
+                                       // column n of row j at n ^ bt_swz(j)
+__device__ __forceinline__ int bt_swz(int j) { return (j & 15) << 2; }  // keeps 4-n groups
 constexpr int WG_AT_OFF = 144 * 1024;  // A's slice of the tile's k: [32][256] bf16, 16-byte
                                        // chunk c of row j at chunk c ^ (j & 31)
 typedef __attribute__((address_space(3))) uint16_t lds_u16;
@@ -99,8 +101,9 @@ __device__ __forceinline__ void stage_lora_operands(const Args& g, lds_u8* lbase
       const uint32_t w[4] = {vb[it].x, vb[it].y, vb[it].z, vb[it].w};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        bt[(8 * c + 2 * e) * TILE + nl] = (uint16_t)(w[e] & 0xffffu);
-        bt[(8 * c + 2 * e + 1) * TILE + nl] = (uint16_t)(w[e] >> 16);
+        const int j0r = 8 * c + 2 * e, j1r = j0r + 1;
+        bt[j0r * TILE + (nl ^ bt_swz(j0r))] = (uint16_t)(w[e] & 0xffffu);
+        bt[j1r * TILE + (nl ^ bt_swz(j1r))] = (uint16_t)(w[e] >> 16);
       }
     }
     if (idx < r * (TILE / 8)) {
@@ -128,8 +131,8 @@ __device__ __forceinline__ void lora_grad_a(const Args& g, const f32x16 (&acc)[W
       const int nl = wi * 128 + 32 * ti + 16 * eh + 4 * h;
       u32x2 lo = {0u, 0u}, hi = {0u, 0u};
       if (jv) {
-        lo = *reinterpret_cast<const lds_u32x2*>(bt + j * TILE + nl);
-        hi = *reinterpret_cast<const lds_u32x2*>(bt + j * TILE + nl + 8);
+        lo = *reinterpret_cast<const lds_u32x2*>(bt + j * TILE + (nl ^ bt_swz(j)));
+        hi = *reinterpret_cast<const lds_u32x2*>(bt + j * TILE + ((nl + 8) ^ bt_swz(j)));
       }
       const bf16x8 bf = __builtin_bit_cast(bf16x8, u32x4{lo.x, lo.y, hi.x, hi.y});
 #pragma unroll
