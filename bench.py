@@ -4,8 +4,8 @@ One step = one hard LUT-linear forward + backward (grad_x, grad_palette, LoRA gr
 the seven Qwen-4B linear shapes at M = 16384 tokens (batch 32 x seq 512),
 straight-through through the frozen 2-bit indices, LoRA rank 16 (32 on o and down).
 `value` = sum over shapes of 6*M*K*N FLOP / step time (LoRA FLOP excluded, as in BASELINE),
-the step's kernels issued on one stream as the library's backward issues them: the forward
-and grad_x dequantise W into their workspace and run the dense GEMM (from 4096 rows), and the
+the step's kernels issued on one stream as the library's autograd issues them: from 4096
+rows the forward dequantises W once and runs the dense GEMM, and grad_x reuses that W; the
 grad_palette GEMM also yields both LoRA weight gradients from its dW tiles; the LoRA row
 products t = x A^T and gt = grad_y B run as their own HBM-bound kernels. The per-kernel
 rooflines come from the same K steps run again with HIP events around every launch.
@@ -45,7 +45,7 @@ PEAK_HBM_GBS = 8000.0
 # workspace and run the dense GEMM on it).
 GEMM_TRAFFIC_BYTES = {"fwd": 975.7e6, "grad_x": 969.2e6, "grad_palette": 886.1e6}
 KERNEL_NAMES = {"fwd": "dequant_kernel + gemm2_kernel<OP_ROW, OP_ROW, EPI_BF16> (fwd)",
-                "grad_x": "dequant_kernel + gemm2_kernel<OP_ROW, OP_COL, EPI_BF16> (grad_x)",
+                "grad_x": "gemm2_kernel<OP_ROW, OP_COL, EPI_BF16> (grad_x on the forward's W)",
                 "grad_palette": "gemm2_kernel<OP_COL, OP_COL, EPI_PAL> (grad_palette + LoRA "
                                 "weight gradients)"}
 
@@ -87,14 +87,24 @@ class HardStep:
             e = self._mark(rec, "lora", it, 2.0 * M_TRAIN * it["K"] * r, M_TRAIN * it["K"] * 2)
             t = ops.lora_project(x, a, 1.0)
             self._close(e)
+            # as the library's autograd (functional.LUTLinearFunction) runs it: where the
+            # library dequantises W for the forward GEMM, that W serves grad_x too
+            staged = ops.lut_linear_staged(M_TRAIN, it["N"], it["K"])
             e = self._mark(rec, "fwd", it)
-            ops.lut_linear_fwd(x, it["packed"], it["pal"], None, t, b)
+            if staged:
+                w = ops.dequant(it["packed"], it["pal"])
+                ops.linear_fwd_dense(x, w, None, t, b)
+            else:
+                ops.lut_linear_fwd(x, it["packed"], it["pal"], None, t, b)
             self._close(e)
             e = self._mark(rec, "lora", it, 2.0 * M_TRAIN * it["N"] * r, M_TRAIN * it["N"] * 2)
             gt = ops.lora_grad_t(gy, b, 1.0)
             self._close(e)
             e = self._mark(rec, "grad_x", it)
-            ops.lut_linear_bwd_x(gy, it["packed"], it["pal"], gt, a)
+            if staged:
+                ops.linear_bwd_x_dense(gy, w, gt, a)
+            else:
+                ops.lut_linear_bwd_x(gy, it["packed"], it["pal"], gt, a)
             self._close(e)
             # grad_palette and both LoRA weight gradients from one dW GEMM, as the library's
             # backward runs it (functional.LUTLinearFunction)

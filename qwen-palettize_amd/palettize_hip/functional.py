@@ -26,13 +26,22 @@ def _c(t):
 
 
 class LUTLinearFunction(torch.autograd.Function):
+    """Where the library dequantises W for the forward GEMM (from 4096 rows, see
+    ops.lut_linear_staged), the bf16 W is kept for the backward's grad_x instead of being
+    dequantised a second time (N*K*2 bytes held from forward to backward)."""
+
     @staticmethod
     def forward(ctx, x, packed, palette, bias, lora_a, lora_b, lora_scale):
         x = x.contiguous()
         lora_a, lora_b = _c(lora_a), _c(lora_b)
         t = ops.lora_project(x, lora_a, lora_scale) if lora_a is not None else None
-        y = ops.lut_linear_fwd(x, packed, palette, bias, t, lora_b)
-        ctx.save_for_backward(x, packed, palette, lora_a, lora_b, t)
+        w = None
+        if ops.lut_linear_staged(x.shape[0], packed.shape[0], x.shape[1]):
+            w = ops.dequant(packed, palette)
+            y = ops.linear_fwd_dense(x, w, bias, t, lora_b)
+        else:
+            y = ops.lut_linear_fwd(x, packed, palette, bias, t, lora_b)
+        ctx.save_for_backward(x, packed, palette, lora_a, lora_b, t, w)
         ctx.lora_scale = float(lora_scale)
         ctx.has_bias = bias is not None
         ctx.bias_dtype = None if bias is None else bias.dtype
@@ -40,7 +49,7 @@ class LUTLinearFunction(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, gy):
-        x, packed, palette, lora_a, lora_b, t = ctx.saved_tensors
+        x, packed, palette, lora_a, lora_b, t, w = ctx.saved_tensors
         gy = gy.contiguous()
         need_x, _, need_pal, need_b, need_la, need_lb, _ = ctx.needs_input_grad
         # one stream: grad_palette beside grad_x on a second stream measured slower (both are
@@ -52,7 +61,10 @@ class LUTLinearFunction(torch.autograd.Function):
         gt = None
         if lora_a is not None and (need_x or (need_lora and not fused)):
             gt = ops.lora_grad_t(gy, lora_b, ctx.lora_scale)
-        grad_x = ops.lut_linear_bwd_x(gy, packed, palette, gt, lora_a) if need_x else None
+        grad_x = None
+        if need_x:
+            grad_x = (ops.linear_bwd_x_dense(gy, w, gt, lora_a) if w is not None else
+                      ops.lut_linear_bwd_x(gy, packed, palette, gt, lora_a))
         grad_bias = ops.bias_grad(gy).to(ctx.bias_dtype) if (ctx.has_bias and need_b) else None
         grad_pal = grad_a = grad_b = None
         if fused:

@@ -119,6 +119,13 @@ def _lora_pair(a, b, first: str, second: str, rows_a: int, rows_b: int):
     return r
 
 
+def lut_linear_staged(M: int, N: int, K: int) -> bool:
+    """True when the library runs the hard forward / grad_x at this size by dequantising W into
+    the workspace and running the dense GEMM (its workspace query then asks for the bf16 W)."""
+    return (query("plz_lut_linear_fwd_workspace", M, N, K) >
+            query("plz_linear_fwd_dense_workspace", M, N, K))
+
+
 def lut_linear_fwd(x, packed, palette, bias=None, lora_t=None, lora_b=None, staged=True):
     """y = x W^T (+ bias) (+ lora_t lora_b^T).
 
