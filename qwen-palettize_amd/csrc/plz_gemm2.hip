@@ -59,7 +59,8 @@ __device__ __forceinline__ int ptile(int row, int col) {  // 128 x 256 fp32 stag
 // registers (they are directly the dW^T operand of an MFMA: lane = k, registers = n), grad_B's
 // from the fp32 staging the palette epilogue already writes (rows n as MFMA A fragments).
 // Partials: [split][tiles_i][r][K] (the two wave rows summed in LDS) and
-// [split][tiles_j][r][N], summed in a fixed order by wg_reduce_kernel, which also applies s.
+// [split][tiles_j][r][N], summed in a fixed order by pal_wg_reduce_kernel, which also
+// applies s.
 // 32x32x16 MFMAs with the rank padded to 32 columns (lanes j >= r feed zeros).
 constexpr int WG_BT_OFF = 128 * 1024;  // B^T of the tile's rows in LDS: [32][256] bf16,
                                        // column n of row j at n ^ bt_swz(j)
@@ -1099,9 +1100,9 @@ static int set_tail(Args& g, void* workspace, size_t workspace_bytes, const char
   return PLZ_OK;
 }
 
-__global__ void reduce_pal_kernel(const float* __restrict__ partial, float* __restrict__ out,
-                                  int64_t N, int64_t G, int Z) {
-  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+__device__ __forceinline__ void reduce_pal(const float* __restrict__ partial,
+                                           float* __restrict__ out, int64_t N, int64_t G, int Z,
+                                           int64_t t) {
   if (t >= N * G) return;
   const int64_t n = t / G, gg = t % G;
   float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -1115,14 +1116,26 @@ __global__ void reduce_pal_kernel(const float* __restrict__ partial, float* __re
   }
   *reinterpret_cast<float4*>(out + t * 4) = s;
 }
+__global__ void reduce_pal_kernel(const float* __restrict__ partial, float* __restrict__ out,
+                                  int64_t N, int64_t G, int Z) {
+  reduce_pal(partial, out, N, G, Z, (int64_t)blockIdx.x * blockDim.x + threadIdx.x);
+}
 
 // grad_A [r, K] and grad_B [N, r] = scale x the sum of their partials, in partial order
 // (threads 0 .. la-1: grad_A from [p][r][K]; then grad_B from the j-major [p][r][N], thread
 // j * N + n writing grad_B[n][j]); bf16 (out_bf16) or fp32 out.
-__global__ void wg_reduce_kernel(const float* __restrict__ pa, const float* __restrict__ pb,
-                                 void* ga, void* gb, int64_t la, int na, int64_t lb, int nb,
-                                 int64_t N, int r, float scale, int out_bf16) {
-  int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+struct WgRed {
+  const float* pa; const float* pb;
+  void* ga; void* gb;
+  int64_t la, lb, N;
+  int na, nb, r, out_bf16;
+  float scale;
+};
+__device__ __forceinline__ void wg_reduce(const WgRed& w, int64_t t) {
+  const float* __restrict__ pa = w.pa;
+  const float* __restrict__ pb = w.pb;
+  const int64_t la = w.la, lb = w.lb, N = w.N;
+  const int na = w.na, nb = w.nb, r = w.r;
   const bool second = t >= la;
   if (second) t -= la;
   const int64_t L = second ? lb : la;
@@ -1140,13 +1153,23 @@ __global__ void wg_reduce_kernel(const float* __restrict__ pa, const float* __re
     for (int u = 0; u < 8; ++u) s += v[u];
   }
   for (; p < np; ++p) s += src[(int64_t)p * L];
-  s *= scale;
+  s *= w.scale;
   const int64_t o = second ? (t % N) * r + t / N : t;
-  void* out = second ? gb : ga;
-  if (out_bf16)
+  void* out = second ? w.gb : w.ga;
+  if (w.out_bf16)
     reinterpret_cast<uint16_t*>(out)[o] = (uint16_t)f2bf(s);
   else
     reinterpret_cast<float*>(out)[o] = s;
+}
+// one launch for both sums of the LoRA grad_palette call: blocks [0, pal_blocks) reduce the
+// palette partials, the rest the LoRA weight-gradient partials
+__global__ void pal_wg_reduce_kernel(const float* __restrict__ partial,
+                                     float* __restrict__ out, int64_t N, int64_t G, int Z,
+                                     int pal_blocks, const WgRed w) {
+  if ((int)blockIdx.x < pal_blocks)
+    reduce_pal(partial, out, N, G, Z, (int64_t)blockIdx.x * blockDim.x + threadIdx.x);
+  else
+    wg_reduce(w, (int64_t)(blockIdx.x - pal_blocks) * blockDim.x + threadIdx.x);
 }
 
 static bool a16(const void* p) { return ((uintptr_t)p & 15) == 0; }
@@ -1195,14 +1218,19 @@ static int bwd_palette(const uint16_t* x, const uint16_t* grad_y, const int32_t*
   int rc = launch<OP_COL, OP_COL, EPI_PAL>(g, z, stream, what);
   if (rc != PLZ_OK) return rc;
   const int64_t G = K / 256, n_out = N * G;
-  hipLaunchKernelGGL(reduce_pal_kernel, dim3((unsigned)((n_out + 255) / 256)), dim3(256), 0,
-                     stream, g.partial, grad_palette, N, G, z);
+  const int pal_blocks = (int)((n_out + 255) / 256);
   if (wg.rank > 0) {
-    const int64_t la = (int64_t)wg.rank * K, lb = N * wg.rank;
-    const int na = z * (int)((N + TILE - 1) / TILE), nb = z * (int)((K + TILE - 1) / TILE);
-    hipLaunchKernelGGL(wg_reduce_kernel, dim3((unsigned)((la + lb + 255) / 256)), dim3(256), 0,
-                       stream, wg.part_a, wg.part_b, wg.grad_a, wg.grad_b, la, na, lb, nb, N,
-                       wg.rank, wg.scale, wg.out_bf16);
+    WgRed w;
+    w.pa = wg.part_a; w.pb = wg.part_b; w.ga = wg.grad_a; w.gb = wg.grad_b;
+    w.la = (int64_t)wg.rank * K; w.lb = N * wg.rank; w.N = N;
+    w.na = z * (int)((N + TILE - 1) / TILE); w.nb = z * (int)((K + TILE - 1) / TILE);
+    w.r = wg.rank; w.out_bf16 = wg.out_bf16; w.scale = wg.scale;
+    const int wg_blocks = (int)((w.la + w.lb + 255) / 256);
+    hipLaunchKernelGGL(pal_wg_reduce_kernel, dim3((unsigned)(pal_blocks + wg_blocks)), dim3(256),
+                       0, stream, g.partial, grad_palette, N, G, z, pal_blocks, w);
+  } else {
+    hipLaunchKernelGGL(reduce_pal_kernel, dim3((unsigned)pal_blocks), dim3(256), 0, stream,
+                       g.partial, grad_palette, N, G, z);
   }
   return check_launch(what);
 }
