@@ -41,9 +41,9 @@ PEAK_HBM_GBS = 8000.0
 # + WRITE_SIZE x 1.0, the factors that make a plain 1 GiB device copy read as 1 GiB each way (two
 # --pmc runs of `bench.py --only hard --steps 1 --warmup 1 --no-cpu --calibration-copy`; counters,
 # commands and algorithmic bytes in profiles/lut_gemm_traffic_m16384.txt).
-# fwd and grad_x count their dequant_kernel launch too (from 4096 rows they dequantise W into the
-# workspace and run the dense GEMM on it).
-GEMM_TRAFFIC_BYTES = {"fwd": 975.7e6, "grad_x": 969.2e6, "grad_palette": 886.1e6}
+# fwd counts its dequant_kernel launch too (from 4096 rows it dequantises W and runs the dense
+# GEMM; grad_x runs on the same W); grad_palette includes the LoRA weight-gradient partials.
+GEMM_TRAFFIC_BYTES = {"fwd": 1003.3e6, "grad_x": 970.8e6, "grad_palette": 876.3e6}
 KERNEL_NAMES = {"fwd": "dequant_kernel + gemm2_kernel<OP_ROW, OP_ROW, EPI_BF16> (fwd)",
                 "grad_x": "gemm2_kernel<OP_ROW, OP_COL, EPI_BF16> (grad_x on the forward's W)",
                 "grad_palette": "gemm2_kernel<OP_COL, OP_COL, EPI_PAL> (grad_palette + LoRA "
