@@ -154,11 +154,23 @@ __host__ __device__ __forceinline__ U4 philox4x32_10(U4 c, uint32_t k0, uint32_t
   return c;
 }
 
+// Natural log of a positive, normal, finite x: log2 from v_log_f32, times ln 2 carried in two
+// parts (ln2_hi + ln2_lo, with the rounding error of r * ln2_hi recovered by an fma). This is
+// the arithmetic logf performs for such x; logf adds a rescaling of subnormal inputs and a
+// pass-through of infinities around it, which these callers never need.
+__device__ __forceinline__ float log_normal(float x) {
+  const float ln2_hi = 0x1.62e42ep-1f, ln2_lo = 0x1.efa39ep-25f;  // ln2_lo = ln 2 - ln2_hi
+  const float r = __builtin_amdgcn_logf(x);
+  const float p = r * ln2_hi;
+  return __builtin_fmaf(r, ln2_hi, __builtin_fmaf(r, ln2_lo, __builtin_fmaf(r, ln2_hi, -p)));
+}
+
 // u = (top 23 bits + 0.5) / 2^23 lies in [2^-24, 1 - 2^-24]: every value is exact in fp32,
-// so u never rounds to 1 (which would make the noise +inf).
+// so u never rounds to 1 (which would make the noise +inf). Both logs see normal inputs:
+// u >= 2^-24 and -log(u) >= -log(1 - 2^-24) ~ 5.96e-8.
 __device__ __forceinline__ float gumbel_from_bits(uint32_t b) {
   const float u = ((float)(b >> 9) + 0.5f) * (1.0f / 8388608.0f);
-  return -logf(-logf(u));
+  return -log_normal(-log_normal(u));
 }
 
 // The Gumbel noise of element (n, k, c) of an [N, K, 4] tensor drawn by Philox at counter
