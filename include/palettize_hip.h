@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define PLZ_ABI_VERSION 7
+#define PLZ_ABI_VERSION 8
 
 /* status codes */
 #define PLZ_OK 0
@@ -246,6 +246,24 @@ int plz_soft_bwd_philox(const uint16_t* x, const uint16_t* grad_y, const uint16_
                         float tau, int scale_grad_by_inv_tau, uint16_t* grad_logits,
                         float* grad_palette, void* workspace, size_t workspace_bytes, int64_t M,
                         int64_t N, int64_t K, void* stream);
+/* The soft backward (noise == NULL: the Philox noise of seed and offset, as
+ * plz_soft_bwd_philox) plus both LoRA weight gradients from the same dW tiles, as
+ * plz_lut_linear_bwd_palette_lora computes them for the hard path: grad_a [rank, K] =
+ * scale * lora_b^T dW and grad_b [N, rank] = scale * dW lora_a^T, dW = grad_y^T x, rank a
+ * multiple of 8 in [8, 32], grads_dtype PLZ_DT_BF16 or PLZ_DT_FP32. grad_logits and
+ * grad_palette are those of plz_soft_bwd bit for bit. Replaces, for a soft PalettizedLinear
+ * under QwenLoRA, the LoRA weight gradients of QwenLoRA.forward's autograd
+ * (qwen_model.py:291-304) beside the soft backward's grad_W matmul
+ * (fused_lut_linear_cuda.py:952). Deterministic; the workspace (query below, 16-byte aligned)
+ * holds the soft backward's and the LoRA partials. */
+size_t plz_soft_bwd_lora_workspace(int64_t M, int64_t N, int64_t K, int rank);
+int plz_soft_bwd_lora(const uint16_t* x, const uint16_t* grad_y, const uint16_t* logits,
+                      int logits_dtype, const float* noise, uint64_t seed, uint64_t offset,
+                      const float* palette, float tau, int scale_grad_by_inv_tau,
+                      const uint16_t* lora_a, const uint16_t* lora_b, int rank, float scale,
+                      uint16_t* grad_logits, float* grad_palette, void* grad_a, void* grad_b,
+                      int grads_dtype, void* workspace, size_t workspace_bytes, int64_t M,
+                      int64_t N, int64_t K, void* stream);
 
 /* ---- LoRA (QwenLoRA, qwen_model.py:213-304): y += scale * (x A^T) B^T ------------------ */
 /* t[M,rank] = scale * x[M,K] lora_a[rank,K]^T  (bf16). rank in {8,16,24,32}. */

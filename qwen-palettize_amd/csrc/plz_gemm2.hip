@@ -52,12 +52,13 @@ __device__ __forceinline__ int ptile(int row, int col) {  // 128 x 256 fp32 stag
   return row * 256 + ((((col >> 2) ^ (row & 63))) << 2) + (col & 3);
 }
 
-// ---- LoRA weight gradients from the hard dW tile (EPI_PAL with g.wg_r > 0) ---------------
+// ---- LoRA weight gradients from a dW tile (EPI_PAL / EPI_SOFT / EPI_F32 with g.wg_r > 0) ---
 // With t = s x A^T and gt = s grad_y B (A = lora_a [r, K], B = lora_b [N, r]):
 //   grad_B = grad_y^T t = s dW A^T,   grad_A = gt^T x = s B^T dW,   dW = grad_y^T x.
 // Every dW tile (256 n x 256 k of one M split) adds its share: grad_A's from the accumulator
 // registers (they are directly the dW^T operand of an MFMA: lane = k, registers = n), grad_B's
-// from the fp32 staging the palette epilogue already writes (rows n as MFMA A fragments).
+// from the fp32 staging the palette and soft epilogues already write (rows n as MFMA A
+// fragments).
 // Partials: [split][tiles_i][r][K] (the two wave rows summed in LDS) and
 // [split][tiles_j][r][N], summed in a fixed order by pal_wg_reduce_kernel, which also
 // applies s.
@@ -863,10 +864,11 @@ __global__ __launch_bounds__(NTHR) void gemm2_kernel(const Args g) {
     return;
   }
 
-  // LoRA weight gradients (hard grad_palette only): grad_A's share from the accumulators
-  // before they are staged (B^T of the tile's rows through LDS past the staging area)
-  const bool wgrad = EPI == EPI_PAL && g.wg_r > 0;
-  if (EPI == EPI_PAL && wgrad) {
+  // LoRA weight gradients (dW epilogues: hard grad_palette, soft backward): grad_A's share
+  // from the accumulators before they are staged (B^T of the tile's rows through LDS past the
+  // staging area)
+  const bool wgrad = (EPI == EPI_PAL || EPI == EPI_SOFT || EPI == EPI_F32) && g.wg_r > 0;
+  if (wgrad) {
     stage_lora_operands(g, lbase, i0, j0);
     __syncthreads();
     f32x16 ca[WT_J];
@@ -952,8 +954,11 @@ __global__ __launch_bounds__(NTHR) void gemm2_kernel(const Args g) {
       // waves 4..7 (idle in the class sums): grad_B's share of the staged half
       if (wgrad && threadIdx.x >= 256)
         lora_grad_b(g, sC, lbase, i0, half, zsl, tile_j, wave - 4, lane);
-    } else {  // EPI_SOFT / EPI_F32: each wave walks (row, 128-k segment) items; lane = 2 k
-      for (int item = wave; item < 256; item += NTHR / 64) {
+    } else {  // EPI_SOFT / EPI_F32: waves walk (row, 128-k segment) items; lane = 2 k
+      // with the LoRA weight gradients, waves 4..7 take grad_B's share of the staged half: beside
+      // the four waves that store the F32 items (cheap), after all eight walked the soft ones
+      const int walkers = wgrad && EPI == EPI_F32 ? 4 : NTHR / 64;
+      for (int item = wave; wave < walkers && item < 256; item += walkers) {
         const int row = item >> 1, h = item & 1;
         const int64_t n = i0 + (row >> 6) * 128 + 64 * half + (row & 63);
         const int64_t kseg = j0 + 128 * h;
@@ -964,6 +969,8 @@ __global__ __launch_bounds__(NTHR) void gemm2_kernel(const Args g) {
         else  // this split's partial dW rows, [split][N][K] fp32
           *reinterpret_cast<float2*>(g.acc_ws + ((int64_t)zsl * g.I + n) * g.J + kseg + 2 * lane) = gw;
       }
+      if (wgrad && threadIdx.x >= 256)
+        lora_grad_b(g, sC, lbase, i0, half, zsl, tile_j, wave - 4, lane);
     }
     __syncthreads();
   }
@@ -1597,11 +1604,14 @@ size_t plz_soft_bwd_workspace(int64_t M, int64_t N, int64_t K) {
   return soft_pal_bytes(N, K) + (z > 1 ? (size_t)z * N * K * sizeof(float) : 0);
 }
 
+// wg.rank > 0: the LoRA weight gradients from the same dW tiles (their partials in wg.part_a /
+// wg.part_b, past the soft workspace), summed with the palette by pal_wg_reduce_kernel
 static int soft_bwd(const uint16_t* x, const uint16_t* grad_y, const uint16_t* logits,
                     int logits_dtype, bool gen, const float* noise, uint64_t seed, uint64_t offset,
                     const float* palette, float tau, int scale_grad_by_inv_tau,
                     uint16_t* grad_logits, float* grad_palette, void* workspace,
-                    size_t workspace_bytes, int64_t M, int64_t N, int64_t K, void* stream) {
+                    size_t workspace_bytes, int64_t M, int64_t N, int64_t K, void* stream,
+                    const WgradArgs& wg = WgradArgs()) {
   PLZ_REQUIRE(M >= 0 && N >= 0 && K >= 0, "plz_soft_bwd: negative shape");
   PLZ_REQUIRE(K % 256 == 0, "plz_soft_bwd: K (%lld) must be a multiple of 256", (long long)K);
   PLZ_REQUIRE(N % 8 == 0, "plz_soft_bwd: N (%lld) must be a multiple of 8", (long long)N);
@@ -1609,8 +1619,19 @@ static int soft_bwd(const uint16_t* x, const uint16_t* grad_y, const uint16_t* l
               "plz_soft_bwd: logits dtype must be bf16 or fp16");
   PLZ_REQUIRE(tau > 0.f, "plz_soft_bwd: tau must be positive");
   if (N == 0 || K == 0) return PLZ_OK;
-  PLZ_REQUIRE(x && grad_y && logits && palette && grad_logits && grad_palette && (gen || noise),
+  PLZ_REQUIRE(logits && palette && grad_logits && grad_palette && (gen || noise),
               "plz_soft_bwd: null pointer");
+  if (M == 0) {  // empty reduction: every gradient is zero
+    zero_async(grad_logits, (size_t)N * K * 4 * 2, (hipStream_t)stream);
+    zero_async(grad_palette, (size_t)N * (K / 256) * 16, (hipStream_t)stream);
+    if (wg.rank > 0) {
+      const size_t esz = wg.out_bf16 ? 2 : 4;
+      zero_async(wg.grad_a, (size_t)wg.rank * K * esz, (hipStream_t)stream);
+      zero_async(wg.grad_b, (size_t)N * wg.rank * esz, (hipStream_t)stream);
+    }
+    return check_launch("plz_soft_bwd");
+  }
+  PLZ_REQUIRE(x && grad_y, "plz_soft_bwd: null pointer");
   PLZ_REQUIRE(a16(x) && a16(grad_y) && a16(logits) && a16(noise) && a16(palette) &&
                   a16(grad_logits),
               "plz_soft_bwd: operands must be 16-byte aligned");
@@ -1632,6 +1653,9 @@ static int soft_bwd(const uint16_t* x, const uint16_t* grad_y, const uint16_t* l
   g.glog_scale = scale_grad_by_inv_tau ? 1.f / tau : 1.f;
   g.grad_logits = grad_logits; g.logits_f16 = logits_dtype == PLZ_DT_FP16;
   g.group = K > N ? -1 : 1;  // walk the larger operand's panels, as the hard grad_palette GEMM
+  g.wg_r = wg.rank;
+  g.wg_a = wg.lora_a; g.wg_b = wg.lora_b;
+  g.wg_part_a = wg.part_a; g.wg_part_b = wg.part_b;
   int rc;
   if (z == 1) {
     rc = launch<OP_COL, OP_COL, EPI_SOFT>(g, 1, (hipStream_t)stream, "plz_soft_bwd");
@@ -1645,8 +1669,20 @@ static int soft_bwd(const uint16_t* x, const uint16_t* grad_y, const uint16_t* l
   }
   if (rc != PLZ_OK) return rc;
   const int64_t G = K / 256, n_out = N * G;
-  hipLaunchKernelGGL(reduce_pal_kernel, dim3((unsigned)((n_out + 255) / 256)), dim3(256), 0,
-                     (hipStream_t)stream, g.partial, grad_palette, N, G, 1);
+  const int pal_blocks = (int)((n_out + 255) / 256);
+  if (wg.rank > 0) {
+    WgRed w;
+    w.pa = wg.part_a; w.pb = wg.part_b; w.ga = wg.grad_a; w.gb = wg.grad_b;
+    w.la = (int64_t)wg.rank * K; w.lb = N * wg.rank; w.N = N;
+    w.na = z * (int)((N + TILE - 1) / TILE); w.nb = z * (int)((K + TILE - 1) / TILE);
+    w.r = wg.rank; w.out_bf16 = wg.out_bf16; w.scale = wg.scale;
+    const int wg_blocks = (int)((w.la + w.lb + 255) / 256);
+    hipLaunchKernelGGL(pal_wg_reduce_kernel, dim3((unsigned)(pal_blocks + wg_blocks)), dim3(256),
+                       0, (hipStream_t)stream, g.partial, grad_palette, N, G, 1, pal_blocks, w);
+  } else {
+    hipLaunchKernelGGL(reduce_pal_kernel, dim3((unsigned)pal_blocks), dim3(256), 0,
+                       (hipStream_t)stream, g.partial, grad_palette, N, G, 1);
+  }
   return check_launch("plz_soft_bwd/reduce");
 }
 
@@ -1658,6 +1694,51 @@ int plz_soft_bwd(const uint16_t* x, const uint16_t* grad_y, const uint16_t* logi
   return soft_bwd(x, grad_y, logits, logits_dtype, false, noise, 0, 0, palette, tau,
                   scale_grad_by_inv_tau, grad_logits, grad_palette, workspace, workspace_bytes, M,
                   N, K, stream);
+}
+
+size_t plz_soft_bwd_lora_workspace(int64_t M, int64_t N, int64_t K, int rank) {
+  if (N <= 0 || K <= 0 || rank <= 0) return plz_soft_bwd_workspace(M, N, K);
+  const int z = soft_splits(M, N, K);
+  return align256(plz_soft_bwd_workspace(M, N, K)) +
+         align256(wg_part_a_floats(z, N, K, rank) * sizeof(float)) +
+         align256(wg_part_b_floats(z, N, K, rank) * sizeof(float));
+}
+
+int plz_soft_bwd_lora(const uint16_t* x, const uint16_t* grad_y, const uint16_t* logits,
+                      int logits_dtype, const float* noise, uint64_t seed, uint64_t offset,
+                      const float* palette, float tau, int scale_grad_by_inv_tau,
+                      const uint16_t* lora_a, const uint16_t* lora_b, int rank, float scale,
+                      uint16_t* grad_logits, float* grad_palette, void* grad_a, void* grad_b,
+                      int grads_dtype, void* workspace, size_t workspace_bytes, int64_t M,
+                      int64_t N, int64_t K, void* stream) {
+  const char* what = "plz_soft_bwd_lora";
+  PLZ_REQUIRE(rank > 0 && rank <= 32 && rank % 8 == 0,
+              "%s: rank (%d) must be a multiple of 8 in [8, 32]", what, rank);
+  PLZ_REQUIRE(grads_dtype == PLZ_DT_BF16 || grads_dtype == PLZ_DT_FP32,
+              "%s: grads_dtype must be PLZ_DT_BF16 or PLZ_DT_FP32", what);
+  PLZ_REQUIRE(M >= 0 && N >= 0 && K >= 0, "%s: negative shape", what);
+  if (N == 0 || K == 0) return PLZ_OK;
+  PLZ_REQUIRE(lora_a && lora_b && grad_a && grad_b && a16(lora_a) && a16(lora_b),
+              "%s: lora_a, lora_b, grad_a, grad_b must be non-null; lora_a, lora_b 16-byte "
+              "aligned", what);
+  const size_t need = plz_soft_bwd_lora_workspace(M, N, K, rank);
+  if (!workspace || !a16(workspace) || workspace_bytes < need) {
+    set_error("%s: workspace of %zu bytes (16-byte aligned) needed, %zu given", what, need,
+              workspace_bytes);
+    return PLZ_EWORKSPACE;
+  }
+  const int z = soft_splits(M, N, K);
+  uint8_t* w = static_cast<uint8_t*>(workspace);
+  WgradArgs wg;
+  wg.lora_a = lora_a; wg.lora_b = lora_b; wg.rank = rank; wg.scale = scale;
+  wg.grad_a = grad_a; wg.grad_b = grad_b; wg.out_bf16 = grads_dtype == PLZ_DT_BF16;
+  const size_t soft_bytes = align256(plz_soft_bwd_workspace(M, N, K));
+  wg.part_a = reinterpret_cast<float*>(w + soft_bytes);
+  wg.part_b = reinterpret_cast<float*>(
+      w + soft_bytes + align256(wg_part_a_floats(z, N, K, rank) * sizeof(float)));
+  return soft_bwd(x, grad_y, logits, logits_dtype, noise == nullptr, noise, seed, offset, palette,
+                  tau, scale_grad_by_inv_tau, grad_logits, grad_palette, workspace,
+                  soft_bytes, M, N, K, stream, wg);
 }
 
 int plz_soft_bwd_philox(const uint16_t* x, const uint16_t* grad_y, const uint16_t* logits,

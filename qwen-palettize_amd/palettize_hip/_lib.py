@@ -80,6 +80,9 @@ SIGNATURES: dict[str, tuple] = {
     "plz_soft_bwd_workspace": (sz, [i64, i64, i64]),
     "plz_soft_bwd": (i32, [p, p, p, i32, p, p, f32, i32, p, p, p, sz, i64, i64, i64, p]),
     "plz_soft_bwd_philox": (i32, [p, p, p, i32, u64, u64, p, f32, i32, p, p, p, sz, i64, i64, i64, p]),
+    "plz_soft_bwd_lora_workspace": (sz, [i64, i64, i64, i32]),
+    "plz_soft_bwd_lora": (i32, [p, p, p, i32, p, u64, u64, p, f32, i32, p, p, i32, f32, p, p, p, p,
+                                i32, p, sz, i64, i64, i64, p]),
     "plz_lora_project": (i32, [p, p, f32, p, i64, i64, i32, p]),
     "plz_lora_grad_t": (i32, [p, p, f32, p, i64, i64, i32, p]),
     "plz_lora_weight_grads_workspace": (sz, [i64, i64, i64, i32]),

@@ -128,17 +128,25 @@ class SoftLUTLinearFunction(torch.autograd.Function):
             need[0], need[1], need[2], need[5], need[6], need[7])
         # one stream: the soft dW GEMM and the grad_x GEMM are both long MFMA-bound launches,
         # and running them side by side measured no faster in the layer step
+        need_lora = lora_a is not None and (need_la or need_lb)
+        need_soft = need_pal or need_log
+        # the LoRA weight gradients ride on the soft dW GEMM (from its dW tiles) when both are
+        # wanted and the rank is one the fused epilogue takes
+        fused = need_lora and need_soft and lora_a.shape[0] in (8, 16, 24, 32)
         gt = None
-        if lora_a is not None and (need_x or need_la or need_lb):
+        if lora_a is not None and (need_x or (need_lora and not fused)):
             gt = ops.lora_grad_t(gy, lora_b, ctx.lora_scale)
         grad_x = ops.linear_bwd_x_dense(gy, w, gt, lora_a) if need_x else None
-        grad_logits = grad_pal = None
-        if need_pal or need_log:
+        grad_logits = grad_pal = grad_a = grad_b = None
+        if fused:
+            grad_logits, grad_pal, grad_a, grad_b = ops.soft_bwd_lora(
+                x, gy, logits, noise, palette, ctx.tau, lora_a, lora_b, ctx.lora_scale,
+                ctx.scale_by_inv_tau, out_dtype=lora_a.dtype)
+        elif need_soft:
             grad_logits, grad_pal = ops.soft_bwd(x, gy, logits, noise, palette, ctx.tau,
                                                  ctx.scale_by_inv_tau)
         grad_bias = ops.bias_grad(gy).to(ctx.bias_dtype) if (ctx.has_bias and need_b) else None
-        grad_a = grad_b = None
-        if lora_a is not None and (need_la or need_lb):
+        if need_lora and not fused:
             grad_a, grad_b = ops.lora_weight_grads(x, gy, t, gt, 1.0, out_dtype=lora_a.dtype)
         return (grad_x, grad_pal if need_pal else None, grad_logits if need_log else None, None,
                 None, grad_bias, grad_a, grad_b, None, None, None, None)

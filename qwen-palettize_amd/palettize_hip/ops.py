@@ -434,6 +434,34 @@ def soft_bwd(x, grad_y, logits, noise, palette, tau: float, scale_by_inv_tau: bo
     return gl, gp
 
 
+def soft_bwd_lora(x, grad_y, logits, noise, palette, tau: float, lora_a, lora_b,
+                  scale: float = 1.0, scale_by_inv_tau: bool = False, out_dtype=torch.bfloat16):
+    """(grad_logits, grad_palette, grad_a [r, K], grad_b [N, r]) from one dW GEMM: the soft
+    backward as soft_bwd (bit for bit), and the LoRA weight gradients scale * lora_b^T dW and
+    scale * dW lora_a^T (dW = grad_y^T x), which lora_weight_grads computes from t and gt."""
+    N, K = _soft_shapes(logits, noise, palette)
+    for name, v in (("x", x), ("grad_y", grad_y), ("lora_a", lora_a), ("lora_b", lora_b)):
+        _need(v, name, torch.bfloat16, 2)
+    M = x.shape[0]
+    r = lora_a.shape[0]
+    if x.shape[1] != K or tuple(grad_y.shape) != (M, N):
+        raise ValueError("x / grad_y shape mismatch")
+    if tuple(lora_a.shape) != (r, K) or tuple(lora_b.shape) != (N, r):
+        raise ValueError("lora_a must be [r, K] and lora_b [N, r]")
+    gl = torch.empty_like(logits)
+    gp = torch.empty((N, K // 256, 4), dtype=torch.float32, device=x.device)
+    ga = torch.empty((r, K), dtype=out_dtype, device=x.device)
+    gb = torch.empty((N, r), dtype=out_dtype, device=x.device)
+    ws = _workspace(query("plz_soft_bwd_lora_workspace", M, N, K, r), x.device)
+    philox = isinstance(noise, PhiloxNoise)
+    call("plz_soft_bwd_lora", _ptr(x), _ptr(grad_y), _ptr(logits), _DT[logits.dtype],
+         None if philox else _ptr(noise), noise.seed if philox else 0,
+         noise.offset if philox else 0, _ptr(palette), float(tau), int(bool(scale_by_inv_tau)),
+         _ptr(lora_a), _ptr(lora_b), r, float(scale), _ptr(gl), _ptr(gp), _ptr(ga), _ptr(gb),
+         _DT[out_dtype], _ptr(ws), ws.numel(), M, N, K, _stream(x))
+    return gl, gp, ga, gb
+
+
 # ---- LoRA -----------------------------------------------------------------------------
 def lora_project(x, lora_a, scale: float):
     """t = scale * x lora_a^T, lora_a [r, K]."""

@@ -36,7 +36,7 @@ def test_every_declared_symbol_is_exported(lib):
         assert hasattr(lib, n), f"{n} declared in the header but not exported"
         assert n in _lib.SIGNATURES, f"{n} has no ctypes signature"
     assert set(_lib.SIGNATURES) == set(names)
-    assert lib.plz_abi_version() == 7
+    assert lib.plz_abi_version() == 8
 
 
 def test_shape_errors_are_reported_without_touching_the_gpu(lib):
@@ -57,6 +57,12 @@ def test_shape_errors_are_reported_without_touching_the_gpu(lib):
     assert rc == 1 and b"rank" in lib.plz_last_error()
     rc = lib.plz_lut_linear_bwd_palette_lora(None, None, None, None, None, 16, 1.0, None, None,
                                              None, 0, None, 0, 64, 256, 256, None)
+    assert rc == 1 and b"null" in lib.plz_last_error()
+    rc = lib.plz_soft_bwd_lora(None, None, None, 0, None, 0, 0, None, 0.5, 0, None, None, 12,
+                               1.0, None, None, None, None, 0, None, 0, 64, 256, 256, None)
+    assert rc == 1 and b"rank" in lib.plz_last_error()
+    rc = lib.plz_soft_bwd_lora(None, None, None, 0, None, 0, 0, None, 0.5, 0, None, None, 16,
+                               1.0, None, None, None, None, 0, None, 0, 64, 256, 256, None)
     assert rc == 1 and b"null" in lib.plz_last_error()
 
 
@@ -90,6 +96,13 @@ def test_workspace_queries_and_missing_workspace(lib):
     assert lib.plz_soft_bwd_workspace(16384, 9728, 2560) == pal + 2 * 9728 * 2560 * 4
     assert lib.plz_soft_bwd_workspace(16384, 1024, 2560) == 1024 * 20 * 16 + 6 * 1024 * 2560 * 4
     assert lib.plz_soft_bwd_workspace(192, 9728, 2560) == pal
+    # with the LoRA weight gradients (rank 16): their partials [z][tiles_i][r][K] and
+    # [z][tiles_j][r][N] behind the soft workspace, each start 256-byte aligned
+    a256 = lambda b: (b + 255) // 256 * 256
+    soft = lib.plz_soft_bwd_workspace(16384, 9728, 2560)
+    assert lib.plz_soft_bwd_lora_workspace(16384, 9728, 2560, 16) == (
+        a256(soft) + a256(2 * 38 * 16 * 2560 * 4) + a256(2 * 10 * 16 * 9728 * 4))
+    assert lib.plz_soft_bwd_lora_workspace(16384, 9728, 2560, 0) == soft
     fake = C.c_void_p(16)  # never dereferenced: the size check fails first
     rc = lib.plz_lut_linear_bwd_palette(fake, fake, fake, fake, None, 0, 16384, 1024, 2560, None)
     assert rc == 4 and b"workspace" in lib.plz_last_error()

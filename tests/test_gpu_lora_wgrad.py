@@ -1,15 +1,16 @@
 """GPU: the LoRA weight gradients computed inside the hard grad_palette GEMM
-(plz_lut_linear_bwd_palette_lora) against the fp64 oracle of QwenLoRA's autograd
-(qwen_model.py:291-304): grad_A = s (gy B)^T x, grad_B = s gy^T (x A^T). The palette gradient
-of the same call must be bit-equal to plz_lut_linear_bwd_palette's, and the whole result
-bit-repeatable. Shapes cover a ragged last row tile (N = 1032), a reduction shorter than one
-stage, split-M launches and every supported rank."""
+(plz_lut_linear_bwd_palette_lora) and the soft backward's dW GEMM (plz_soft_bwd_lora) against
+the fp64 oracle of QwenLoRA's autograd (qwen_model.py:291-304): grad_A = s (gy B)^T x,
+grad_B = s gy^T (x A^T). The palette (and logits) gradients of the same call must be
+bit-equal to those of the call without LoRA, and the whole result bit-repeatable. Shapes cover
+a ragged last row tile (N = 1032), a reduction shorter than one stage, split-M launches (the
+soft backward's fp32 split rows among them) and every supported rank."""
 import numpy as np
 import pytest
 import torch
 
 import oracle as O
-from helpers import assert_close, f32, make_weight, randn_bf16
+from helpers import assert_close, f32, gen, make_weight, randn_bf16
 
 pytestmark = pytest.mark.gpu
 ops = pytest.importorskip("palettize_hip.ops")
@@ -69,3 +70,76 @@ def test_bwd_palette_lora_empty_reduction_gives_zeros(dev):
     b = randn_bf16(N, r, seed=12).to(dev)
     gp, ga, gb = ops.lut_linear_bwd_palette_lora(x, gy, p, a, b, 1.0)
     assert not gp.any() and not ga.any() and not gb.any()
+
+
+def _soft_case(N, K, seed):
+    _, pal = make_weight(N, K, seed=seed)
+    logits = torch.randn(N, K, 4, generator=gen(seed + 1)).to(torch.bfloat16)
+    return logits, pal
+
+
+@pytest.mark.parametrize("M,N,K,rank,scale,philox", [
+    (512, 2560, 2560, 16, 2.0, True),    # config 1 shape, unsplit (fused soft epilogue)
+    (300, 1032, 768, 8, 1.0, False),     # ragged last row tile, noise tensor
+    (77, 136, 256, 24, 0.5, True),
+    (1024, 512, 1024, 32, 1.0, False),   # 2 splits: fp32 dW rows + split epilogue
+    (2048, 1024, 2560, 16, 2.0, True),   # 4 splits
+])
+def test_soft_bwd_lora(dev, M, N, K, rank, scale, philox):
+    logits, pal = _soft_case(N, K, seed=M + N)
+    logits, pal = logits.to(dev), pal.to(dev)
+    noise = (ops.PhiloxNoise(seed=99, offset=M) if philox else
+             ops.gumbel_philox((N, K, 4), seed=98, offset=0, device=dev))
+    x = randn_bf16(M, K, seed=1).to(dev)
+    gy = randn_bf16(M, N, seed=2).to(dev)
+    a = randn_bf16(rank, K, seed=3, std=0.01).to(dev)
+    b = randn_bf16(N, rank, seed=4, std=0.01).to(dev)
+    gl, gp, ga, gb = ops.soft_bwd_lora(x, gy, logits, noise, pal, 0.5, a, b, scale)
+    rl, rp = ops.soft_bwd(x, gy, logits, noise, pal, 0.5)
+    assert torch.equal(gl, rl) and torch.equal(gp, rp)
+    wa, wb = O.lora_weight_grads(f32(x), f32(gy), f32(a), f32(b), scale)
+    assert_close(f32(ga), wa, what="grad_a")
+    assert_close(f32(gb), wb, what="grad_b")
+    out2 = ops.soft_bwd_lora(x, gy, logits, noise, pal, 0.5, a, b, scale)
+    assert all(torch.equal(u, v) for u, v in zip((gl, gp, ga, gb), out2))
+    _, _, fa, fb = ops.soft_bwd_lora(x, gy, logits, noise, pal, 0.5, a, b, scale,
+                                     out_dtype=torch.float32)
+    assert torch.equal(fa.to(torch.bfloat16), ga) and torch.equal(fb.to(torch.bfloat16), gb)
+
+
+def test_soft_bwd_lora_empty_reduction_gives_zeros(dev):
+    N, K, r = 256, 512, 16
+    logits, pal = _soft_case(N, K, seed=13)
+    x = torch.empty(0, K, dtype=torch.bfloat16, device=dev)
+    gy = torch.empty(0, N, dtype=torch.bfloat16, device=dev)
+    a = randn_bf16(r, K, seed=14).to(dev)
+    b = randn_bf16(N, r, seed=15).to(dev)
+    gl, gp, ga, gb = ops.soft_bwd_lora(x, gy, logits.to(dev), ops.PhiloxNoise(1, 0), pal.to(dev),
+                                       0.5, a, b, 1.0)
+    assert not gl.any() and not gp.any() and not ga.any() and not gb.any()
+    rl, rp = ops.soft_bwd(x, gy, logits.to(dev), ops.PhiloxNoise(1, 0), pal.to(dev), 0.5)
+    assert not rl.any() and not rp.any()
+
+
+@pytest.mark.parametrize("M,N,K", [(300, 1032, 768), (2048, 1024, 2560)])
+def test_soft_autograd_lora_weight_grads_ride_on_the_dw_gemm(dev, M, N, K):
+    """soft_lut_linear with LoRA: the backward takes grad_A, grad_B from the soft dW GEMM
+    (plz_soft_bwd_lora); logits and palette gradients equal ops.soft_bwd's bit for bit."""
+    from palettize_hip import soft_lut_linear
+    r, s, tau = 16, 2.0, 0.5
+    logits, pal = _soft_case(N, K, seed=M)
+    logits = logits.to(dev).requires_grad_()
+    pal = pal.to(dev).requires_grad_()
+    spec = ops.PhiloxNoise(seed=5, offset=17)
+    x = randn_bf16(M, K, seed=21).to(dev).requires_grad_()
+    a = randn_bf16(r, K, seed=22, std=0.01).to(dev).requires_grad_()
+    b = randn_bf16(N, r, seed=23, std=0.01).to(dev).requires_grad_()
+    gy = randn_bf16(M, N, seed=24).to(dev)
+    y = soft_lut_linear(x, pal, logits, spec, tau, lora_a=a, lora_b=b, lora_scale=s)
+    y.backward(gy)
+    wa, wb = O.lora_weight_grads(f32(x.detach()), f32(gy), f32(a.detach()), f32(b.detach()), s)
+    assert_close(f32(a.grad), wa, what="grad_a")
+    assert_close(f32(b.grad), wb, what="grad_b")
+    rl, rp = ops.soft_bwd(x.detach(), gy, logits.detach(), spec, pal.detach(), tau)
+    assert torch.equal(logits.grad, rl) and torch.equal(pal.grad, rp)
+    assert bool(torch.isfinite(x.grad.float()).all())
