@@ -995,39 +995,72 @@ __global__ __launch_bounds__(256) void soft_split_epilogue_kernel(const Args g, 
 }
 
 // Tail tiles of a split launch: sum each tile's reduction parts in part order (deterministic)
-// and store it as the unsplit kernel would. One workgroup of 512 threads per tile, each thread
-// owning the accumulators the same thread of the GEMM held.
-__global__ __launch_bounds__(NTHR) void tail_reduce_kernel(const Args g) {
+// and store it as the unsplit kernel would. Four workgroups of 256 threads per tile, one per
+// 64-row slab q: thread t holds what GEMM thread (q / 2) * 256 + t held for its accumulator
+// blocks ti = 2 (q % 2), +1 (rows 64 q .. 64 q + 63), so the slabs read and write disjoint
+// parts and the launch fills every CU.
+constexpr int TAIL_SLABS = 4;
+constexpr int TAIL_THREADS = NTHR / 2;
+constexpr size_t kLdsTail = (size_t)(TILE / TAIL_SLABS) * EPI_RS;
+__global__ __launch_bounds__(TAIL_THREADS) void tail_reduce_kernel(const Args g) {
   extern __shared__ uint4 smem[];
-  const int bid = g.tail_first + (int)blockIdx.x;
+  lds_u8* st = (lds_u8*)smem;
+  const int tt = (int)blockIdx.x / TAIL_SLABS, q = (int)blockIdx.x % TAIL_SLABS;
   int tile_i, tile_j;
-  tile_of(g, bid, tile_i, tile_j);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  tile_of(g, g.tail_first + tt, tile_i, tile_j);
+  const int wi = q >> 1, ti0 = 2 * (q & 1);
+  const int gt = wi * TAIL_THREADS + threadIdx.x;  // the GEMM thread of these accumulators
+  const int wj = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const float4* src = reinterpret_cast<const float4*>(g.tail_ws) +
-                      (int64_t)blockIdx.x * g.tail_split * (TILE * TILE / 4);
-  f32x16 acc[WT_I][WT_J];
+                      (int64_t)tt * g.tail_split * (TILE * TILE / 4);
+  float a[2][WT_J][16];
 #pragma unroll
-  for (int ti = 0; ti < WT_I; ++ti)
+  for (int tl = 0; tl < 2; ++tl)
 #pragma unroll
     for (int tj = 0; tj < WT_J; ++tj)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) acc[ti][tj][e] = 0.f;
+      for (int e = 0; e < 16; ++e) a[tl][tj][e] = 0.f;
   for (int p = 0; p < g.tail_split; ++p) {
 #pragma unroll
-    for (int ti = 0; ti < WT_I; ++ti)
+    for (int tl = 0; tl < 2; ++tl)
 #pragma unroll
       for (int tj = 0; tj < WT_J; ++tj)
 #pragma unroll
         for (int e4 = 0; e4 < 4; ++e4) {
-          const float4 v = src[(int64_t)p * (TILE * TILE / 4) + ((ti * WT_J + tj) * 4 + e4) * NTHR + threadIdx.x];
-          acc[ti][tj][4 * e4] += v.x;
-          acc[ti][tj][4 * e4 + 1] += v.y;
-          acc[ti][tj][4 * e4 + 2] += v.z;
-          acc[ti][tj][4 * e4 + 3] += v.w;
+          const float4 v = src[(int64_t)p * (TILE * TILE / 4) +
+                               (((ti0 + tl) * WT_J + tj) * 4 + e4) * NTHR + gt];
+          a[tl][tj][4 * e4] += v.x;
+          a[tl][tj][4 * e4 + 1] += v.y;
+          a[tl][tj][4 * e4 + 2] += v.z;
+          a[tl][tj][4 * e4 + 3] += v.w;
         }
   }
-  store_tile_bf16(g, acc, (lds_u8*)smem, (int64_t)tile_i * TILE, (int64_t)tile_j * TILE,
-                  wave / WAVES_J, wave % WAVES_J, lane);
+  // bf16 (alpha * acc + bias) of the slab's 64 rows in LDS, as stage_tile_bf16 computes it
+  const int64_t i0 = (int64_t)tile_i * TILE + (TILE / TAIL_SLABS) * q, j0 = (int64_t)tile_j * TILE;
+#pragma unroll
+  for (int tj = 0; tj < WT_J; ++tj) {
+    const int col = wj * (32 * WT_J) + 32 * tj + (lane & 31);
+    const float bj = (g.bias && j0 + col < g.J) ? bf2f(g.bias[j0 + col]) : 0.f;
+#pragma unroll
+    for (int tl = 0; tl < 2; ++tl)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int row = 32 * tl + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+        *reinterpret_cast<__attribute__((address_space(3))) uint16_t*>(st + row * EPI_RS + col * 2) =
+            (uint16_t)f2bf(g.alpha * a[tl][tj][e] + bj);
+      }
+  }
+  __syncthreads();
+  uint16_t* C = reinterpret_cast<uint16_t*>(g.c);
+#pragma unroll
+  for (int it = 0; it < (TILE / TAIL_SLABS) * TILE / 8 / TAIL_THREADS; ++it) {
+    const int ch = it * TAIL_THREADS + threadIdx.x;  // 32 chunks of 8 columns per row
+    const int row = ch >> 5, c8 = (ch & 31) * 8;
+    const int64_t i = i0 + row, j = j0 + c8;
+    if (i < g.I && j < g.J)
+      *reinterpret_cast<u32x4*>(C + i * g.ldc + j) =
+          *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(st + row * EPI_RS + c8 * 2);
+  }
 }
 
 constexpr size_t kLds = 256 * 528;  // 132 KB: two pipeline stages (128 KB) or the padded bf16 output tile
@@ -1059,10 +1092,8 @@ static int launch(Args g, int splits, hipStream_t stream, const char* what) {
   hipLaunchKernelGGL(kern, dim3((unsigned)gx, 1, (unsigned)splits), dim3(NTHR), lds, stream, g);
   int rc = check_launch(what);
   if (rc != PLZ_OK || !tail) return rc;
-  static uint64_t rlds_done = 0;
-  if ((rc = reserve_lds((const void*)tail_reduce_kernel, kLds, rlds_done, what))) return rc;
-  hipLaunchKernelGGL(tail_reduce_kernel, dim3((unsigned)(tiles - g.tail_first)), dim3(NTHR), kLds,
-                     stream, g);
+  hipLaunchKernelGGL(tail_reduce_kernel, dim3((unsigned)((tiles - g.tail_first) * TAIL_SLABS)),
+                     dim3(TAIL_THREADS), kLdsTail, stream, g);
   return check_launch(what);
 }
 
