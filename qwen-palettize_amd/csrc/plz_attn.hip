@@ -66,6 +66,11 @@ __device__ __forceinline__ bf16x8 vt_frag(const lds_u8* vs, int dbase, int ks, i
   return __builtin_bit_cast(bf16x8, __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7));
 }
 
+// 2^x by v_exp_f32 alone. exp2f wraps the same instruction in a rescaling of arguments below
+// -126 so that it can return subnormal results; here those probabilities (< 2^-126) become 0,
+// and every other result, +-inf and NaN included, is the same.
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
 __device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
@@ -171,7 +176,7 @@ __global__ __launch_bounds__(NT, 2) void attn_fwd_kernel(const uint16_t* __restr
     // always sets it (kv 0 <= qrow). O and l are rescaled only when some lane moved.
     if (__builtin_amdgcn_ballot_w64(mx > mrun + 8.f) != 0) {
       const float mnew = mx > mrun + 8.f ? mx : mrun;
-      const float alpha = exp2f(mrun - mnew);
+      const float alpha = exp2_fast(mrun - mnew);
       mrun = mnew;
       lrun *= alpha;
 #pragma unroll
@@ -187,7 +192,7 @@ __global__ __launch_bounds__(NT, 2) void attn_fwd_kernel(const uint16_t* __restr
       float p[16];
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        p[e] = exp2f(fmaf(st[nb][e], scale_log2, nm));
+        p[e] = exp2_fast(fmaf(st[nb][e], scale_log2, nm));
         sum += p[e];
       }
 #pragma unroll
@@ -388,7 +393,7 @@ __global__ __launch_bounds__(NT, 2) void attn_bwd_dq_kernel(
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int kv = kv0 + 32 * nb + 8 * (e >> 2) + 4 * h2 + (e & 3);
-        float p = exp2f(fmaf(st[nb][e], scale_log2, nl));
+        float p = exp2_fast(fmaf(st[nb][e], scale_log2, nl));
         if (diag && kv > qrow) p = 0.f;
         ds[e] = p * (dpt[nb][e] - dsum);
       }
@@ -496,7 +501,7 @@ __global__ __launch_bounds__(NT) void attn_bwd_dkv_kernel(
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int e = 4 * j + i;
-          float pe = exp2f(fmaf(s[mb][e], scale_log2, -L[i] * kLog2e));
+          float pe = exp2_fast(fmaf(s[mb][e], scale_log2, -L[i] * kLog2e));
           if (diag && qb0 + r + i < kvrow) pe = 0.f;
           p[e] = pe;
           ds[e] = pe * (dp[mb][e] - Dv[i]);
