@@ -389,14 +389,16 @@ __global__ __launch_bounds__(NT, 2) void attn_bwd_dq_kernel(
     bf16x8 dsf[4];
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) {
-      float ds[16];
+      float p[16], ds[16];
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int kv = kv0 + 32 * nb + 8 * (e >> 2) + 4 * h2 + (e & 3);
-        float p = exp2_fast(fmaf(st[nb][e], scale_log2, nl));
-        if (diag && kv > qrow) p = 0.f;
-        ds[e] = p * (dpt[nb][e] - dsum);
+      for (int e = 0; e < 16; ++e) p[e] = exp2_fast(fmaf(st[nb][e], scale_log2, nl));
+      if (diag) {  // a wave-uniform branch: the other blocks run no mask code
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+          if (kv0 + 32 * nb + 8 * (e >> 2) + 4 * h2 + (e & 3) > qrow) p[e] = 0.f;
       }
+#pragma unroll
+      for (int e = 0; e < 16; ++e) ds[e] = p[e] * (dpt[nb][e] - dsum);
       pack_frags(ds, dsf[2 * nb], dsf[2 * nb + 1]);
     }
 #pragma unroll
@@ -496,16 +498,22 @@ __global__ __launch_bounds__(NT) void attn_bwd_dkv_kernel(
         const int r = 32 * mb + 8 * j + 4 * h2;
         const f32x4 L = *reinterpret_cast<const __attribute__((address_space(3))) f32x4*>(
             lsl + r * 4);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          p[4 * j + i] = exp2_fast(fmaf(s[mb][4 * j + i], scale_log2, -L[i] * kLog2e));
+      }
+      if (diag) {  // a wave-uniform branch: the other blocks run no mask code
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+          if (qb0 + 32 * mb + 8 * (e >> 2) + 4 * h2 + (e & 3) < kvrow) p[e] = 0.f;
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int r = 32 * mb + 8 * j + 4 * h2;
         const f32x4 Dv = *reinterpret_cast<const __attribute__((address_space(3))) f32x4*>(
             lsl + 256 + r * 4);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int e = 4 * j + i;
-          float pe = exp2_fast(fmaf(s[mb][e], scale_log2, -L[i] * kLog2e));
-          if (diag && qb0 + r + i < kvrow) pe = 0.f;
-          p[e] = pe;
-          ds[e] = pe * (dp[mb][e] - Dv[i]);
-        }
+        for (int i = 0; i < 4; ++i) ds[4 * j + i] = p[4 * j + i] * (dp[mb][4 * j + i] - Dv[i]);
       }
       pack_frags(p, pf[2 * mb], pf[2 * mb + 1]);
       pack_frags(ds, dsf[2 * mb], dsf[2 * mb + 1]);
