@@ -8,11 +8,10 @@
 // All four stream one M x L activation (x or grad_y) and touch a rank-r operand that stays in
 // L2, so they are HBM-bound: the work per activation element is r <= 32 MACs. Two kernels:
 //
-// rows_kernel  (t, gt): the activation is the MFMA A operand read straight from global memory
-//   (16 bytes = 8 consecutive reduction elements per lane, the 16x16x32 operand layout). A
-//   workgroup owns 64 rows; its 4 waves take interleaved 32-wide reduction steps and meet in
-//   LDS at the end. lora_a [r, L] gives B fragments as 16-byte loads; lora_b [L, r] as eight
-//   2-byte loads (it is L2-resident and shared by the 64 rows).
+// rows_ring_kernel  (t, gt): a workgroup owns 64 rows of the activation and streams them
+//   through a 3-slot LDS ring of 256-element stages (whole 512-byte row segments per copy);
+//   its 8 waves take one 32-wide 16x16x32 k-step of each stage and meet in LDS at the end.
+//   lora_a [r, L] is staged in the same row layout, lora_b [L, r] as its contiguous block.
 // cols_kernel  (grad_A, grad_B): the reduction index m is the activation's row, so fragments
 //   need a transpose. 32 x 256 activation tiles go global->LDS (buffer_load ... lds, 4-stage
 //   ring of 20 KB stages, two workgroups per CU) and are read with ds_read_b64_tr_b16, which
@@ -29,6 +28,21 @@ namespace lora {
 typedef __attribute__((address_space(3))) uint8_t lds_u8;
 typedef short v4i16 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+typedef __attribute__((address_space(3))) u32x4 lds_w4;
+typedef __attribute__((address_space(3))) uint16_t lds_u16;
+
+// workgroup barrier once this wave's LDS accesses are done (its global->LDS copies are waited
+// for separately, by wait_vmcnt)
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xF | (3 << 14) | (7 << 4));  // lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+// wait until at most N vector-memory operations of this wave are outstanding
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
 
 __device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
@@ -36,122 +50,140 @@ __device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
 __device__ __forceinline__ bf16x8 as_frag(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
 
 // ---------------------------------------------------------------------------------------
-// rows_kernel: out[M, r] = scale * X[M, L] Bop[L, r]
+// rows_ring_kernel: out[M, r] = scale * X[M, L] Bop[L, r]
 //   BOP_T: Bop(l, j) = bop[j * L + l]  (lora_a, [r, L]);  else Bop(l, j) = bop[l * r + j]
 //   RG = 16-column groups (r <= 16 * RG)
+// The activation is staged through LDS. A workgroup owns
+// 64 rows; a stage is their next 256 reduction elements (32 KB) plus the matching slice of
+// Bop, copied global -> LDS by buffer_load ... lds into a 3-slot ring two stages ahead. Every
+// copy instruction moves 1 KB of whole 512-byte row segments, so the stream reads whole cache
+// lines in order instead of 16 rows x 64 B per instruction (an 84 MB probe of the two
+// patterns: 15 against 18-19 us). The 8 waves split each stage's 256 elements (32 each: one
+// 16x16x32 k-step per row group).
+//   X stage:  row m (512 B) holds 32 chunks of 16 B, logical chunk c at c ^ (m & 15): the 16
+//             rows of a fragment read land on 16 distinct 16-byte bank groups.
+//   Bop (BOP_T, lora_a [r, L]): rows j of the same layout.
+//   Bop (else, lora_b [L, r]): the stage's contiguous [256][r] block as it is in memory.
 // ---------------------------------------------------------------------------------------
-#ifndef PLZ_RW_NG
-#define PLZ_RW_NG 4
-#endif
-#ifndef PLZ_RW_WAVES
-#define PLZ_RW_WAVES 8
-#endif
-#ifndef PLZ_RW_U
-#define PLZ_RW_U 2
-#endif
-#ifndef PLZ_RW_CONSEC
-#define PLZ_RW_CONSEC 0
-#endif
-constexpr int RW_NG = PLZ_RW_NG;        // MFMA row groups of 16 per workgroup
-constexpr int RW_ROWS = 16 * RW_NG;     // activation rows per workgroup
-constexpr int RW_WAVES = PLZ_RW_WAVES;  // waves per workgroup, interleaved over the reduction
-constexpr int RW_U = PLZ_RW_U;          // 32-wide reduction steps per wave per iteration
+constexpr int RR_ROWS = 64;                       // activation rows per workgroup
+constexpr int RR_KC = 256;                        // reduction elements per stage
+constexpr int RR_NS = 3;                          // ring slots (copies two stages ahead)
+constexpr int RR_XBYTES = RR_ROWS * RR_KC * 2;    // 32 KB
+constexpr int RR_XI = RR_XBYTES / (512 * 16);     // X copies per thread per stage (4)
+template <int RG>
+constexpr int rr_stage_bytes() { return RR_XBYTES + RG * 8192; }  // + Bop: RG x 8 KB
 
 template <bool BOP_T, int RG>
-__global__ __launch_bounds__(64 * RW_WAVES) void rows_kernel(const uint16_t* __restrict__ X,
-                                                             const uint16_t* __restrict__ bop,
-                                                             uint16_t* __restrict__ out,
-                                                             float scale, int64_t M, int L,
-                                                             int r) {
-  __shared__ float red[RW_WAVES][RW_ROWS][RG * 16 + 1];
+__global__ __launch_bounds__(512) void rows_ring_kernel(const uint16_t* __restrict__ X,
+                                                        const uint16_t* __restrict__ bop,
+                                                        uint16_t* __restrict__ out, float scale,
+                                                        int64_t M, int L, int r) {
+  extern __shared__ uint4 smem[];
+  lds_u8* lds = (lds_u8*)smem;
+  constexpr int STAGE = rr_stage_bytes<RG>();
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int rr = lane & 15, q = lane >> 4;
-  const int64_t m0 = (int64_t)blockIdx.x * RW_ROWS;
-  const int rows = (int)min((int64_t)RW_ROWS, M - m0);
-  // rows past the end of X fall outside the descriptor's range and read as zero
+  const int64_t m0 = (int64_t)blockIdx.x * RR_ROWS;
+  const int rows = (int)min((int64_t)RR_ROWS, M - m0);
+  const int nst = (L + RR_KC - 1) / RR_KC;
+  // rows past the end of X, and reduction indices past L, read as zero (range check or kBufOob)
   const BufRsrc xr = make_rsrc(X + m0 * L, (uint32_t)rows * (uint32_t)L * 2u);
   const BufRsrc br = make_rsrc(bop, (uint32_t)r * (uint32_t)L * 2u);
-  uint32_t xoff[RW_NG];
-#pragma unroll
-  for (int g = 0; g < RW_NG; ++g) xoff[g] = ((uint32_t)(16 * g + rr) * (uint32_t)L + 8u * q) * 2u;
 
-  const int nks = (L + 31) / 32;                                    // 32-wide reduction steps
-  const int nit = (nks + RW_WAVES * RW_U - 1) / (RW_WAVES * RW_U);  // iterations
-
-  auto load = [&](int it, uint4 (&xv)[RW_U][RW_NG], bf16x8 (&bv)[RW_U][RG]) {
+  // Copies of stage s into slot ss; stages past the last one copy nothing (every lane still
+  // issues the same count, so one vmcnt serves every stage).
+  auto issue = [&](int s, lds_u8* ss) {
+    const bool live = s < nst;
+    const int k0 = RR_KC * s;
 #pragma unroll
-    for (int u = 0; u < RW_U; ++u) {
-#if PLZ_RW_CONSEC
-      const int s = RW_U * (wave + RW_WAVES * it) + u;  // a wave's RW_U steps are adjacent
-#else
-      const int s = wave + RW_WAVES * (RW_U * it + u);
-#endif
-      const int l = 32 * s + 8 * q;  // this lane's 8 reduction elements: l .. l+7
-      const bool lin = l < L;
+    for (int it = 0; it < RR_XI; ++it) {
+      const int p = (wave * RR_XI + it) * 64 + lane;  // physical chunk: row p / 32
+      const int m = p >> 5, k = k0 + 8 * ((p & 31) ^ (m & 15));
+      const uint32_t off = live && k < L ? ((uint32_t)m * (uint32_t)L + (uint32_t)k) * 2u : kBufOob;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_u8*)(ss + (wave * RR_XI + it) * 1024), 16,
+                                               off, 0, 0, 0);
+    }
 #pragma unroll
-      for (int g = 0; g < RW_NG; ++g) xv[u][g] = buf_load16(xr, lin ? xoff[g] + 64u * s : kBufOob);
-#pragma unroll
-      for (int cg = 0; cg < RG; ++cg) {
-        const int j = 16 * cg + rr;
-        const bool ok = lin && j < r;
-        if constexpr (BOP_T) {
-          bv[u][cg] = as_frag(buf_load16(br, ok ? ((uint32_t)j * L + l) * 2u : kBufOob));
-        } else {
-          uint32_t w[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const uint32_t o0 = ok ? ((uint32_t)(l + 2 * e) * r + j) * 2u : kBufOob;
-            const uint32_t o1 = ok ? ((uint32_t)(l + 2 * e + 1) * r + j) * 2u : kBufOob;
-            const uint32_t lo = __builtin_amdgcn_raw_buffer_load_b16(br, (int)o0, 0, 0);
-            const uint32_t hi = __builtin_amdgcn_raw_buffer_load_b16(br, (int)o1, 0, 0);
-            w[e] = lo | (hi << 16);
-          }
-          bv[u][cg] = as_frag(make_uint4(w[0], w[1], w[2], w[3]));
-        }
+    for (int it = 0; it < RG; ++it) {
+      const int p = (wave * RG + it) * 64 + lane;
+      uint32_t off = kBufOob;
+      if constexpr (BOP_T) {
+        const int j = p >> 5, k = k0 + 8 * ((p & 31) ^ (j & 15));
+        if (live && j < r && k < L) off = ((uint32_t)j * (uint32_t)L + (uint32_t)k) * 2u;
+      } else {  // 16-byte chunk p of the contiguous [256][r] block (past L: out of range)
+        if (live && 8 * p < RR_KC * r) off = ((uint32_t)k0 * (uint32_t)r + 8u * p) * 2u;
       }
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          br, (lds_u8*)(ss + RR_XBYTES + (wave * RG + it) * 1024), 16, off, 0, 0, 0);
     }
   };
-  f32x4 acc[RW_NG][RG];
+
+  f32x4 acc[4][RG];
 #pragma unroll
-  for (int g = 0; g < RW_NG; ++g)
+  for (int g = 0; g < 4; ++g)
 #pragma unroll
     for (int cg = 0; cg < RG; ++cg) acc[g][cg] = f32x4{0.f, 0.f, 0.f, 0.f};
-  auto mma = [&](const uint4 (&xv)[RW_U][RW_NG], const bf16x8 (&bv)[RW_U][RG]) {
+  // lane (rr, q) of wave w: logical chunk 4w + q (reduction elements 32w + 8q .. +7 of the stage)
+  const int c = 4 * wave + q;
+  const int xoff = rr * 512 + ((c ^ rr) << 4);  // row rr of a group; (16g + rr) & 15 == rr
+  // the copies of stage s + RR_NS - 1 go to slot ws before the MFMAs read slot xs (distinct
+  // slots: __restrict__ keeps the compiler from waiting on the new copies first)
+  auto step = [&](int s, const lds_u8* __restrict__ xs, lds_u8* __restrict__ ws) {
+    issue(s + RR_NS - 1, ws);
+    bf16x8 a[4], b[RG];
 #pragma unroll
-    for (int u = 0; u < RW_U; ++u)
+    for (int g = 0; g < 4; ++g)
+      a[g] = __builtin_bit_cast(bf16x8, *(const lds_w4*)(xs + g * 16 * 512 + xoff));
+    const lds_u8* bs = xs + RR_XBYTES;
 #pragma unroll
-      for (int g = 0; g < RW_NG; ++g)
+    for (int cg = 0; cg < RG; ++cg) {
+      if constexpr (BOP_T) {
+        b[cg] = __builtin_bit_cast(bf16x8, *(const lds_w4*)(bs + cg * 16 * 512 + xoff));
+      } else {  // Bop(k, j) at (k r + j): 8 consecutive k of column j = 16 cg + rr
+        const int j = 16 * cg + rr;
+        uint32_t w[4] = {0u, 0u, 0u, 0u};
+        if (j < r) {
+          const lds_u16* bp = reinterpret_cast<const lds_u16*>(bs) + 8 * c * r + j;
 #pragma unroll
-        for (int cg = 0; cg < RG; ++cg) acc[g][cg] = mfma16(as_frag(xv[u][g]), bv[u][cg], acc[g][cg]);
+          for (int e = 0; e < 4; ++e)
+            w[e] = (uint32_t)bp[(2 * e) * r] | ((uint32_t)bp[(2 * e + 1) * r] << 16);
+        }
+        b[cg] = __builtin_bit_cast(bf16x8, u32x4{w[0], w[1], w[2], w[3]});
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+#pragma unroll
+      for (int cg = 0; cg < RG; ++cg) acc[g][cg] = mfma16(a[g], b[cg], acc[g][cg]);
   };
-
-  // two register sets: the loads of iteration it+1 are in flight during the MFMAs of it
-  // (iterations past nit load nothing: every lane's offset is out of range and reads zero)
-  uint4 x0[RW_U][RW_NG], x1[RW_U][RW_NG];
-  bf16x8 b0[RW_U][RG], b1[RW_U][RG];
-  load(0, x0, b0);
-  for (int it = 0; it < nit; it += 2) {
-    load(it + 1, x1, b1);
-    mma(x0, b0);
-    if (it + 2 < nit) load(it + 2, x0, b0);
-    if (it + 1 < nit) mma(x1, b1);
-  }
-
-  // Cross-wave sum in wave order (C fragment: lane holds rows 4q..4q+3 of column rr in each
-  // 16x16 block).
 #pragma unroll
-  for (int g = 0; g < RW_NG; ++g)
+  for (int s = 0; s < RR_NS - 1; ++s) issue(s, lds + s * STAGE);
+  for (int s = 0; s < nst; ++s) {
+    wait_vmcnt<(RR_XI + RG) * (RR_NS - 2)>();  // this lane's copies of stage s have landed
+    lds_barrier();                               // everyone's have; slot (s-1) % RR_NS is free
+    step(s, lds + (s % RR_NS) * STAGE, lds + ((s + RR_NS - 1) % RR_NS) * STAGE);
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // drain the trailing (empty) copies
+  lds_barrier();                  // the ring is free: the cross-wave sums reuse it
+
+  // C fragment of block (g, cg): rows 16 g + 4 q + e, column 16 cg + rr; summed over the 8
+  // waves in wave order
+  constexpr int RS = RG * 16 + 1;
+  float* red = reinterpret_cast<float*>(smem);
+#pragma unroll
+  for (int g = 0; g < 4; ++g)
 #pragma unroll
     for (int cg = 0; cg < RG; ++cg)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) red[wave][16 * g + 4 * q + e][16 * cg + rr] = acc[g][cg][e];
+      for (int e = 0; e < 4; ++e)
+        red[(wave * RR_ROWS + 16 * g + 4 * q + e) * RS + 16 * cg + rr] = acc[g][cg][e];
   __syncthreads();
-  for (int idx = threadIdx.x; idx < rows * r; idx += 64 * RW_WAVES) {
+  for (int idx = threadIdx.x; idx < rows * r; idx += 512) {
     const int row = idx / r, j = idx - row * r;
-    float s = 0.f;
+    float sum = 0.f;
 #pragma unroll
-    for (int w = 0; w < RW_WAVES; ++w) s += red[w][row][j];
-    out[(m0 + row) * r + j] = (uint16_t)f2bf(scale * s);
+    for (int w = 0; w < 8; ++w) sum += red[(w * RR_ROWS + row) * RS + j];
+    out[(m0 + row) * r + j] = (uint16_t)f2bf(scale * sum);
   }
 }
 
@@ -183,15 +215,6 @@ constexpr int CL_LOADS = CL_XI + 1;              // copies per thread per stage:
 // chunks on 8 distinct bank pairs, so the fragment reads are conflict-free.
 __device__ __forceinline__ int xsw(int m) { return 2 * (m & 3) + 8 * ((m >> 3) & 1); }
 
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_s_waitcnt(0xF | (3 << 14) | (7 << 4));  // lgkmcnt(0)
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
 
 // One workgroup = one (problem, column tile, M split); problem 0 is grad_B, problem 1 grad_A,
 // so both weight gradients run in one launch.
@@ -467,13 +490,20 @@ static int cols(const uint16_t* x, const uint16_t* grad_y, const uint16_t* t, co
 template <bool BOP_T>
 static int rows(const uint16_t* X, const uint16_t* bop, float scale, uint16_t* out, int64_t M,
                 int64_t L, int r, hipStream_t s, const char* what) {
-  const dim3 grid((unsigned)((M + RW_ROWS - 1) / RW_ROWS));
-  if (r <= 16)
-    hipLaunchKernelGGL((rows_kernel<BOP_T, 1>), grid, dim3(64 * RW_WAVES), 0, s, X, bop, out, scale, M,
-                       (int)L, r);
-  else
-    hipLaunchKernelGGL((rows_kernel<BOP_T, 2>), grid, dim3(64 * RW_WAVES), 0, s, X, bop, out, scale, M,
-                       (int)L, r);
+  const dim3 grid((unsigned)((M + RR_ROWS - 1) / RR_ROWS));
+  static uint64_t done1 = 0, done2 = 0;
+  int rc;
+  if (r <= 16) {
+    constexpr size_t lds = (size_t)RR_NS * rr_stage_bytes<1>();
+    if ((rc = reserve_lds((const void*)rows_ring_kernel<BOP_T, 1>, lds, done1, what))) return rc;
+    hipLaunchKernelGGL((rows_ring_kernel<BOP_T, 1>), grid, dim3(512), lds, s, X, bop, out, scale,
+                       M, (int)L, r);
+  } else {
+    constexpr size_t lds = (size_t)RR_NS * rr_stage_bytes<2>();
+    if ((rc = reserve_lds((const void*)rows_ring_kernel<BOP_T, 2>, lds, done2, what))) return rc;
+    hipLaunchKernelGGL((rows_ring_kernel<BOP_T, 2>), grid, dim3(512), lds, s, X, bop, out, scale,
+                       M, (int)L, r);
+  }
   return check_launch(what);
 }
 
@@ -492,7 +522,7 @@ int plz_lora_project(const uint16_t* x, const uint16_t* lora_a, float scale, uin
   PLZ_REQUIRE(M >= 0 && K >= 0 && rank > 0 && rank <= 32 && rank % 8 == 0,
               "plz_lora_project: need M, K >= 0 and rank a multiple of 8 in [8, 32]");
   PLZ_REQUIRE(K % 8 == 0, "plz_lora_project: K must be a multiple of 8");
-  PLZ_REQUIRE(K < (1 << 24) && RW_ROWS * K * 2 < (int64_t)1 << 31,
+  PLZ_REQUIRE(K < (1 << 24) && RR_ROWS * K * 2 < (int64_t)1 << 31,
               "plz_lora_project: K (%lld) too large", (long long)K);
   if (M == 0) return PLZ_OK;
   PLZ_REQUIRE(x && lora_a && t && aligned16(x) && aligned16(lora_a),
@@ -505,7 +535,7 @@ int plz_lora_grad_t(const uint16_t* grad_y, const uint16_t* lora_b, float scale,
   PLZ_REQUIRE(M >= 0 && N >= 0 && rank > 0 && rank <= 32 && rank % 8 == 0,
               "plz_lora_grad_t: need M, N >= 0 and rank a multiple of 8 in [8, 32]");
   PLZ_REQUIRE(N % 8 == 0, "plz_lora_grad_t: N must be a multiple of 8");
-  PLZ_REQUIRE(N < (1 << 24) && RW_ROWS * N * 2 < (int64_t)1 << 31,
+  PLZ_REQUIRE(N < (1 << 24) && RR_ROWS * N * 2 < (int64_t)1 << 31,
               "plz_lora_grad_t: N (%lld) too large", (long long)N);
   if (M == 0) return PLZ_OK;
   PLZ_REQUIRE(grad_y && lora_b && gt && aligned16(grad_y) && aligned16(lora_b),
