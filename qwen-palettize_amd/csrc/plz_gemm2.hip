@@ -919,39 +919,47 @@ __global__ __launch_bounds__(NTHR) void gemm2_kernel(const Args g) {
                    wj * (32 * WT_J) + 32 * tj + (lane & 31))] = acc[ti][tj][e];
     }
     __syncthreads();
-    if (EPI == EPI_PAL) {  // threads 0..255: one (row, 128-k segment) each
-      const int row = (threadIdx.x >> 1) & 127, h = threadIdx.x & 1;
+    if (EPI == EPI_PAL) {
+      // class sums: thread pair (2i, 2i+1) owns one (row, 128-k segment), 64 k each. A class
+      // mask comes from the sign-extended index bits (0 or all ones), so each value is routed
+      // with bitwise ANDs instead of compares and selects; the pair's halves are added in order.
+      const int row = (threadIdx.x >> 2) & 127, h = (threadIdx.x >> 1) & 1, sub = threadIdx.x & 1;
       const int64_t n = i0 + (row >> 6) * 128 + 64 * half + (row & 63);
       const int64_t kseg = j0 + 128 * h;
-      if (threadIdx.x < 256 && n < g.I && kseg < g.J) {
-        const uint4* qp = reinterpret_cast<const uint4*>(g.packed + n * (g.Kw / 16) + kseg / 16);
-        float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+      const bool live = n < g.I && kseg < g.J;
+      float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+      if (live) {
+        const uint4 q4 =
+            reinterpret_cast<const uint4*>(g.packed + n * (g.Kw / 16) + kseg / 16)[sub];
+        const uint32_t qs[4] = {q4.x, q4.y, q4.z, q4.w};
 #pragma unroll
-        for (int qv = 0; qv < 2; ++qv) {
-          const uint4 q4 = qp[qv];
-          const uint32_t qs[4] = {q4.x, q4.y, q4.z, q4.w};
+        for (int w = 0; w < 4; ++w) {
 #pragma unroll
-          for (int w = 0; w < 4; ++w) {
+          for (int cc = 0; cc < 4; ++cc) {
+            const int col = 128 * h + 64 * sub + 16 * w + 4 * cc;
+            const float4 v = *reinterpret_cast<const float4*>(&sC[ptile(row, col)]);
+            const uint32_t vb[4] = {__float_as_uint(v.x), __float_as_uint(v.y),
+                                    __float_as_uint(v.z), __float_as_uint(v.w)};
 #pragma unroll
-            for (int cc = 0; cc < 4; ++cc) {
-              const int col = 128 * h + 64 * qv + 16 * w + 4 * cc;
-              const float4 v = *reinterpret_cast<const float4*>(&sC[ptile(row, col)]);
-              const float vv[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-              for (int e = 0; e < 4; ++e) {
-                const uint32_t c = (qs[w] >> (2 * (4 * cc + e))) & 3u;
-                s0 += c == 0 ? vv[e] : 0.f;
-                s1 += c == 1 ? vv[e] : 0.f;
-                s2 += c == 2 ? vv[e] : 0.f;
-                s3 += c == 3 ? vv[e] : 0.f;
-              }
+            for (int e = 0; e < 4; ++e) {
+              const int bit = 2 * (4 * cc + e);
+              const uint32_t m0 = (uint32_t)((int32_t)(qs[w] << (31 - bit)) >> 31);  // index bit 0
+              const uint32_t m1 = (uint32_t)((int32_t)(qs[w] << (30 - bit)) >> 31);  // index bit 1
+              s0 += __uint_as_float(vb[e] & ~m0 & ~m1);
+              s1 += __uint_as_float(vb[e] & m0 & ~m1);
+              s2 += __uint_as_float(vb[e] & ~m0 & m1);
+              s3 += __uint_as_float(vb[e] & m0 & m1);
             }
           }
         }
-        float* dst = g.partial + (((int64_t)zsl * g.I + n) * segs + kseg / 128) * 4;
-        *reinterpret_cast<float4*>(dst) = make_float4(s0, s1, s2, s3);
       }
-      // waves 4..7 (idle in the class sums): grad_B's share of the staged half
+      const float o0 = __shfl_xor(s0, 1), o1 = __shfl_xor(s1, 1);
+      const float o2 = __shfl_xor(s2, 1), o3 = __shfl_xor(s3, 1);
+      if (live && sub == 0) {
+        float* dst = g.partial + (((int64_t)zsl * g.I + n) * segs + kseg / 128) * 4;
+        *reinterpret_cast<float4*>(dst) = make_float4(s0 + o0, s1 + o1, s2 + o2, s3 + o3);
+      }
+      // waves 4..7: grad_B's share of the staged half
       if (wgrad && threadIdx.x >= 256)
         lora_grad_b(g, sC, lbase, i0, half, zsl, tile_j, wave - 4, lane);
     } else {  // EPI_SOFT / EPI_F32: waves walk (row, 128-k segment) items; lane = 2 k
