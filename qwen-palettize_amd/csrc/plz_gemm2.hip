@@ -545,7 +545,9 @@ __device__ __forceinline__ void store_tile_bf16(const Args& g, const f32x16 (&ac
     const int64_t i = i0 + row, j = j0 + c8;
     if (i < g.I && j < g.J) {
       const u32x4 v = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(st + row * EPI_RS + c8 * 2);
-      *reinterpret_cast<u32x4*>(C + i * g.ldc + j) = v;
+      // streaming store: the output is not read again by this launch, so it should not take
+      // cache lines from the operands the other workgroups are still reading
+      __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(C + i * g.ldc + j));
     }
   }
 }
@@ -576,7 +578,7 @@ __device__ __forceinline__ void store_tile_swiglu(const Args& g, const f32x16 (&
         const float hi = swiglu_elem(bf2f(gv[w] >> 16), bf2f(uv[w] >> 16));
         hv[w] = f2bf2(lo, hi);
       }
-      *reinterpret_cast<u32x4*>(C + i * g.ldc + h0 + c8) = hv;
+      __builtin_nontemporal_store(hv, reinterpret_cast<u32x4*>(C + i * g.ldc + h0 + c8));
     }
   }
 }
@@ -1065,9 +1067,10 @@ __global__ __launch_bounds__(TAIL_THREADS) void tail_reduce_kernel(const Args g)
     const int ch = it * TAIL_THREADS + threadIdx.x;  // 32 chunks of 8 columns per row
     const int row = ch >> 5, c8 = (ch & 31) * 8;
     const int64_t i = i0 + row, j = j0 + c8;
-    if (i < g.I && j < g.J)
-      *reinterpret_cast<u32x4*>(C + i * g.ldc + j) =
-          *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(st + row * EPI_RS + c8 * 2);
+    if (i < g.I && j < g.J)  // streaming store, as store_tile_bf16
+      __builtin_nontemporal_store(
+          *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(st + row * EPI_RS + c8 * 2),
+          reinterpret_cast<u32x4*>(C + i * g.ldc + j));
   }
 }
 
