@@ -65,6 +65,7 @@ __device__ __forceinline__ void store8(float* p, const float (&v)[kVec]) {
   reinterpret_cast<float4*>(p)[1] = make_float4(v[4], v[5], v[6], v[7]);
 }
 
+template <int NT = kThreads>
 __device__ __forceinline__ float block_sum(float v, float* red) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
@@ -73,7 +74,7 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
   __syncthreads();
   float s = 0.f;
   if (threadIdx.x == 0)
-    for (int w = 0; w < kThreads / 64; ++w) s += red[w];
+    for (int w = 0; w < NT / 64; ++w) s += red[w];
   return s;  // valid in thread 0
 }
 
@@ -110,24 +111,38 @@ __global__ __launch_bounds__(kThreads) void sumsq_kernel(const plz_adamw_desc* _
 
 // coef[G] = min(1, max_norm[G] / (sqrt(sum of group G's partials) + 1e-6)); coef[2 + G] = norm
 // (a fixed assignment of partials to threads and a fixed reduction tree: deterministic)
-__global__ __launch_bounds__(kThreads) void clip_coef_kernel(const float* __restrict__ partial,
-                                                             const int* __restrict__ group,
-                                                             int64_t nblocks, float max0,
-                                                             float max1, float* __restrict__ coef) {
-  __shared__ float red[kThreads / 64];
+// One workgroup per clip group reads every partial: 1024 threads with 16 independent loads of
+// each array in flight per thread, so the walk over the partials is a few memory round trips.
+constexpr int kCoefThreads = 1024;
+constexpr int kCoefUnroll = 16;
+__global__ __launch_bounds__(kCoefThreads) void clip_coef_kernel(const float* __restrict__ partial,
+                                                                 const int* __restrict__ group,
+                                                                 int64_t nblocks, float max0,
+                                                                 float max1,
+                                                                 float* __restrict__ coef) {
+  __shared__ float red[kCoefThreads / 64];
   const int G = blockIdx.x;
-  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  int64_t i = threadIdx.x;
-  for (; i + 7 * kThreads < nblocks; i += 8 * kThreads) {
+  float acc[kCoefUnroll];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int64_t k = i + u * kThreads;
-      acc[u] += group[k] == G ? partial[k] : 0.f;
+  for (int u = 0; u < kCoefUnroll; ++u) acc[u] = 0.f;
+  int64_t i = threadIdx.x;
+  for (; i + (kCoefUnroll - 1) * kCoefThreads < nblocks; i += kCoefUnroll * kCoefThreads) {
+    int gr[kCoefUnroll];
+    float pv[kCoefUnroll];
+#pragma unroll
+    for (int u = 0; u < kCoefUnroll; ++u) {
+      gr[u] = group[i + u * kCoefThreads];
+      pv[u] = partial[i + u * kCoefThreads];
     }
+#pragma unroll
+    for (int u = 0; u < kCoefUnroll; ++u) acc[u] += gr[u] == G ? pv[u] : 0.f;
   }
-  for (; i < nblocks; i += kThreads) acc[0] += group[i] == G ? partial[i] : 0.f;
-  float s = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
-  s = block_sum(s, red);
+  for (; i < nblocks; i += kCoefThreads) acc[0] += group[i] == G ? partial[i] : 0.f;
+#pragma unroll
+  for (int w = kCoefUnroll / 2; w > 0; w >>= 1)
+#pragma unroll
+    for (int u = 0; u < w; ++u) acc[u] += acc[u + w];
+  const float s = block_sum<kCoefThreads>(acc[0], red);
   if (threadIdx.x == 0) {
     const float mx = G == 0 ? max0 : max1;
     const float c = mx / (sqrtf(s) + 1e-6f);
@@ -302,8 +317,8 @@ int plz_adamw_step(const plz_adamw_desc* descs_device, int n, int64_t total_bloc
                      n, partial, group);
   int rc = check_launch("plz_adamw_step/sumsq");
   if (rc) return rc;
-  hipLaunchKernelGGL(clip_coef_kernel, dim3(2), dim3(kThreads), 0, s, partial, group, total_blocks,
-                     max_norm0, max_norm1, coef);
+  hipLaunchKernelGGL(clip_coef_kernel, dim3(2), dim3(kCoefThreads), 0, s, partial, group,
+                     total_blocks, max_norm0, max_norm1, coef);
   if ((rc = check_launch("plz_adamw_step/coef"))) return rc;
   // bias corrections in double on the host, as torch computes its Python-float scalars
   const float bc1 = (float)(1.0 - std::pow(beta1, (double)step));
