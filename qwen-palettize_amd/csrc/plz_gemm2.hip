@@ -1191,17 +1191,17 @@ __device__ __forceinline__ void wg_reduce(const WgRed& w, int64_t t) {
   if (t >= L) return;
   const float* src = (second ? pb : pa) + t;
   const int np = second ? nb : na;
-  // the loads of 8 partials are issued together, the adds stay in partial order
+  // the loads of 16 partials are issued together (the last batch predicated), the adds stay
+  // in partial order
   float s = 0.f;
-  int p = 0;
-  for (; p + 8 <= np; p += 8) {
-    float v[8];
+  for (int p = 0; p < np; p += 16) {
+    float v[16];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) v[u] = src[(int64_t)(p + u) * L];
+    for (int u = 0; u < 16; ++u) v[u] = p + u < np ? src[(int64_t)(p + u) * L] : 0.f;
 #pragma unroll
-    for (int u = 0; u < 8; ++u) s += v[u];
+    for (int u = 0; u < 16; ++u)
+      if (p + u < np) s += v[u];
   }
-  for (; p < np; ++p) s += src[(int64_t)p * L];
   s *= w.scale;
   const int64_t o = second ? (t % N) * r + t / N : t;
   void* out = second ? w.gb : w.ga;
