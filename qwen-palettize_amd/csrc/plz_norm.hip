@@ -180,24 +180,34 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(
   }
 }
 
-// out[c] = sum over the blocks' partials of column c: 64 columns per workgroup, its 4 waves
-// take every 4th block (8 loads in flight per lane), then add their sums in wave order.
-__global__ void sum_blocks_kernel(const float* __restrict__ partial, float* __restrict__ out,
-                                  int blocks, int64_t cols) {
-  __shared__ float red[4][64];
+// out[c] = sum over the blocks' partials of column c: 64 columns per workgroup, its 16 waves
+// take every 16th block (8 loads in flight per lane), then their sums are added in a fixed tree.
+constexpr int kSumWaves = 16;
+__global__ __launch_bounds__(kSumWaves * 64) void sum_blocks_kernel(
+    const float* __restrict__ partial, float* __restrict__ out, int blocks, int64_t cols) {
+  __shared__ float red[kSumWaves][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t c = (int64_t)blockIdx.x * 64 + lane;
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   if (c < cols) {
     int b = wave;
-    for (; b + 28 < blocks; b += 32)
+    for (; b + 7 * kSumWaves < blocks; b += 8 * kSumWaves)
 #pragma unroll
-      for (int u = 0; u < 8; ++u) acc[u] += partial[(int64_t)(b + 4 * u) * cols + c];
-    for (; b < blocks; b += 4) acc[0] += partial[(int64_t)b * cols + c];
+      for (int u = 0; u < 8; ++u) acc[u] += partial[(int64_t)(b + kSumWaves * u) * cols + c];
+    for (; b < blocks; b += kSumWaves) acc[0] += partial[(int64_t)b * cols + c];
   }
   red[wave][lane] = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
   __syncthreads();
-  if (wave == 0 && c < cols) out[c] = (red[0][lane] + red[1][lane]) + (red[2][lane] + red[3][lane]);
+  if (wave == 0 && c < cols) {
+    float v[kSumWaves];
+#pragma unroll
+    for (int w = 0; w < kSumWaves; ++w) v[w] = red[w][lane];
+#pragma unroll
+    for (int h = kSumWaves / 2; h > 0; h >>= 1)
+#pragma unroll
+      for (int w = 0; w < h; ++w) v[w] += v[w + h];
+    out[c] = v[0];
+  }
 }
 
 __device__ __forceinline__ float silu(float g) { return g / (1.f + __expf(-g)); }
@@ -330,8 +340,8 @@ int plz_rmsnorm_bwd(const uint16_t* x, const uint16_t* weight, const float* rstd
                        (hipStream_t)stream, x, weight, rstd, grad_y, grad_x, part, rows, cols);
   int rc = check_launch("plz_rmsnorm_bwd");
   if (rc) return rc;
-  hipLaunchKernelGGL(sum_blocks_kernel, dim3((unsigned)((cols + 63) / 64)), dim3(256), 0,
-                     (hipStream_t)stream, part, grad_weight, blocks, cols);
+  hipLaunchKernelGGL(sum_blocks_kernel, dim3((unsigned)((cols + 63) / 64)),
+                     dim3(kSumWaves * 64), 0, (hipStream_t)stream, part, grad_weight, blocks, cols);
   return check_launch("plz_rmsnorm_bwd/reduce");
 }
 
