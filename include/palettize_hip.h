@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define PLZ_ABI_VERSION 8
+#define PLZ_ABI_VERSION 9
 
 /* status codes */
 #define PLZ_OK 0
@@ -176,6 +176,36 @@ int plz_gumbel_philox(float* noise, int64_t n, uint64_t seed, uint64_t offset, v
  * gumbel_sample(seed, (k*N + n)*4 + c) of fused_lut_kernel.cu:1245-1256 and
  * triton_soft_forward.py:51-66, written in [N, K, 4] layout. */
 int plz_gumbel_lcg(float* noise, uint32_t seed, int64_t N, int64_t K, void* stream);
+/* The Triton sampler _gumbel_sample (triton_soft_forward.py:51-66), which the reference's
+ * preferred soft path (TritonSoftLinear, triton_soft_forward.py:317-411) draws from: the same
+ * statements in int32, where >> is an arithmetic shift, so it differs from plz_gumbel_lcg
+ * wherever a shifted intermediate has bit 31 set. Same [N, K, 4] layout and index. */
+int plz_gumbel_lcg_triton(float* noise, uint32_t seed, int64_t N, int64_t K, void* stream);
+
+/* Batched soft P / W in the reference's own layouts. Replaces fused_compute_P_W_batched
+ * (fused_lut_linear_cuda.py:513-607 and :1016-1077, kernel fused_lut_kernel.cu:2097-2158):
+ *   logits  (4, K, N) fp16 planes      palette (G, 4) bf16, row o in group o / group_size
+ *   p_aos   (K, N, 4) fp16 = softmax_c((logit_c + g_c) / tau)
+ *   w       (K, N) bf16    = sum_c P_c pal_c (the soft weight, as the reference returns)
+ * with g_c the CUDA LCG draw gumbel_sample(step_seed ^ (seed_offset * 0x9E3779B9),
+ * (j*N + o)*4 + c) (fused_lut_kernel.cu:2129); seed_offset is the layer's position. */
+typedef struct plz_pw_ref_desc {
+  const uint16_t* logits;   /* (4, K, N) fp16 */
+  const uint16_t* palette;  /* (G, 4) bf16 */
+  uint16_t* p_aos;          /* (K, N, 4) fp16 */
+  uint16_t* w;              /* (K, N) bf16 */
+  int64_t K, N;
+  int64_t block_begin;      /* filled by plz_pw_ref_plan */
+  uint32_t seed_offset;     /* the layer's index in the batch */
+  int32_t vec;              /* filled by plz_pw_ref_plan */
+} plz_pw_ref_desc;
+/* Checks n host descriptors (N % group_size == 0, 4*K*N < 2^32, pointers at least 2-byte
+ * aligned, the palette 8-byte aligned), fills block_begin and vec, and returns the launch's
+ * block count (or a negative status). */
+int64_t plz_pw_ref_plan(plz_pw_ref_desc* descs, int n, int64_t group_size);
+/* descs_device: a device copy of the planned descriptors. */
+int plz_soft_pw_ref_batched(const plz_pw_ref_desc* descs_device, int n, int64_t total_blocks,
+                            int64_t group_size, float tau, uint32_t step_seed, void* stream);
 
 /* Builds the forward weight of the soft path from logits [N, K, 4] (bf16 or fp16),
  * noise fp32 [N, K, 4] and palette fp32 [N, K/256, 4]:

@@ -234,17 +234,63 @@ def lcg_bits(seed: int, idx) -> np.ndarray:
     return x & np.uint32(0xFFFFFF)
 
 
-def lcg_gumbel(seed: int, N: int, K: int) -> np.ndarray:
-    """noise[n, k, c] = -log(-log(max(u, 1e-7))), u = bits / 2^24, idx = (k*N + n)*4 + c
-    (fused_lut_kernel.cu:1245-1256 with the indexing of :1974-1977), fp32 arithmetic."""
+def lcg_bits_i32(seed: int, idx) -> np.ndarray:
+    """Integer part of the Triton sampler _gumbel_sample (triton_soft_forward.py:51-66): the
+    same statements in int32, where ``>>`` is an arithmetic shift and 0x9E3779B9 is written
+    as -1640531527. Wherever neither shifted intermediate has bit 31 set it equals lcg_bits
+    (see lcg_variants_agree); elsewhere the two samplers draw different numbers."""
+    s = np.uint32(seed & 0xFFFFFFFF).view(np.int32)
+    with np.errstate(over="ignore"):
+        x = s ^ (np.asarray(idx, np.uint32).view(np.int32) * np.int32(-1640531527))
+        x = x ^ (x >> np.int32(13))
+        x = x * np.int32(1103515245) + np.int32(12345)
+        x = x ^ (x >> np.int32(17))
+        x = x * np.int32(1103515245) + np.int32(12345)
+    return (x & np.int32(0xFFFFFF)).astype(np.uint32)
+
+
+def lcg_variants_agree(seed: int, idx) -> np.ndarray:
+    """True where the CUDA (uint32) and Triton (int32) hashes give the same bits: the value
+    shifted right by 13 and the value shifted right by 17 both have bit 31 clear, so the
+    logical and arithmetic shifts coincide. Both are taken from the uint32 hash; up to the
+    first shift the two hashes are identical, and up to the second one wherever the first
+    shift agreed."""
+    x = np.uint32(seed & 0xFFFFFFFF) ^ (np.asarray(idx, np.uint32) * np.uint32(0x9E3779B9))
+    ok = (x >> np.uint32(31)) == 0
+    x = x ^ (x >> np.uint32(13))
+    x = x * np.uint32(1103515245) + np.uint32(12345)
+    return ok & ((x >> np.uint32(31)) == 0)
+
+
+def lcg_index(N: int, K: int) -> np.ndarray:
+    """idx [N, K, 4] of element (n, k, c): (k*N + n)*4 + c in uint32, the flat (K, N) index of
+    the reference's (4, K, N) logits times 4 plus the class (fused_lut_kernel.cu:1960-1977,
+    triton_soft_forward.py:124-138)."""
     n = np.arange(N, dtype=np.uint32)[:, None, None]
     k = np.arange(K, dtype=np.uint32)[None, :, None]
     c = np.arange(4, dtype=np.uint32)[None, None, :]
     with np.errstate(over="ignore"):
-        idx = (k * np.uint32(N) + n) * np.uint32(4) + c
-    u = lcg_bits(seed, idx).astype(np.float32) * np.float32(1.0 / 16777216.0)
+        return (k * np.uint32(N) + n) * np.uint32(4) + c
+
+
+def gumbel_from_bits24(bits) -> np.ndarray:
+    """-log(-log(max(u, 1e-7))), u = bits / 2^24, in fp32 (fused_lut_kernel.cu:1253-1255,
+    triton_soft_forward.py:63-66)."""
+    u = np.asarray(bits, np.uint32).astype(np.float32) * np.float32(1.0 / 16777216.0)
     u = np.maximum(u, np.float32(1e-7))
     return (-np.log(-np.log(u))).astype(np.float32)
+
+
+def lcg_gumbel(seed: int, N: int, K: int, variant: str = "cuda") -> np.ndarray:
+    """noise[n, k, c] of the reference's LCG sampler, idx = (k*N + n)*4 + c, fp32 arithmetic:
+    the CUDA hash (fused_lut_kernel.cu:1245-1256, variant "cuda") or the Triton one
+    (triton_soft_forward.py:51-66, variant "triton")."""
+    idx = lcg_index(N, K)
+    if variant == "cuda":
+        return gumbel_from_bits24(lcg_bits(seed, idx))
+    if variant == "triton":
+        return gumbel_from_bits24(lcg_bits_i32(seed, idx))
+    raise ValueError(f"unknown LCG variant {variant!r}")
 
 
 _PHILOX_M = (np.uint64(0xD2511F53), np.uint64(0xCD9E8D57))
@@ -444,7 +490,8 @@ def clib():
         L.orc_unpack.argtypes = [P, P, C.c_int64]
         L.orc_dequant.argtypes = [P, P, P, C.c_int64, C.c_int64]
         L.orc_lcg_bits.argtypes = [P, C.c_uint32, P, C.c_int64]
-        L.orc_gumbel_lcg.argtypes = [P, C.c_uint32, C.c_int64, C.c_int64]
+        L.orc_lcg_bits_i32.argtypes = [P, C.c_uint32, P, C.c_int64]
+        L.orc_gumbel_lcg.argtypes = [P, C.c_uint32, C.c_int64, C.c_int64, C.c_int]
         L.orc_philox.argtypes = [P, P, P]
         L.orc_gumbel_philox.argtypes = [P, C.c_int64, C.c_uint64, C.c_uint64]
         _clib = L
@@ -485,9 +532,18 @@ def c_lcg_bits(seed: int, idx) -> np.ndarray:
     return out
 
 
-def c_gumbel_lcg(seed: int, N: int, K: int) -> np.ndarray:
+def c_lcg_bits_i32(seed: int, idx) -> np.ndarray:
+    idx = np.ascontiguousarray(idx, dtype=np.uint32)
+    out = np.empty_like(idx)
+    clib().orc_lcg_bits_i32(_p(out), seed & 0xFFFFFFFF, _p(idx), idx.size)
+    return out
+
+
+def c_gumbel_lcg(seed: int, N: int, K: int, variant: str = "cuda") -> np.ndarray:
+    if variant not in ("cuda", "triton"):
+        raise ValueError(f"unknown LCG variant {variant!r}")
     out = np.empty((N, K, 4), np.float32)
-    clib().orc_gumbel_lcg(_p(out), seed & 0xFFFFFFFF, N, K)
+    clib().orc_gumbel_lcg(_p(out), seed & 0xFFFFFFFF, N, K, int(variant == "triton"))
     return out
 
 

@@ -9,9 +9,10 @@
  *                           viewed as 16 indices per little-endian int32 along a row
  *   orc_dequant             W[n,k] = bf16_rne(palette[n, k/256, idx[n,k]])
  *                           (the flat gather of qwen_model.py:97-102,185-186)
- *   orc_gumbel_lcg          the reference's LCG hash sampler (fused_lut_kernel.cu:1245-1256,
- *                           triton_soft_forward.py:51-66), element (n,k,c) drawn with
- *                           idx = (k*N + n)*4 + c, stored [N, K, 4]
+ *   orc_gumbel_lcg          the reference's LCG hash sampler, element (n,k,c) drawn with
+ *                           idx = (k*N + n)*4 + c, stored [N, K, 4]: the CUDA hash in uint32
+ *                           (fused_lut_kernel.cu:1245-1256) or the Triton one in int32 with
+ *                           arithmetic shifts (triton_soft_forward.py:51-66)
  *   orc_philox / orc_gumbel_philox
  *                           Philox4x32-10 (Salmon et al., SC'11) and the supplied-noise
  *                           generator of this build (no reference counterpart; pinned by
@@ -61,34 +62,44 @@ void orc_dequant(const int32_t* packed, const float* pal, uint16_t* w, int64_t N
     }
 }
 
-static float lcg_gumbel(uint32_t seed, uint32_t idx) {
+/* x >> s on an int32 as an arithmetic shift, written out on the uint32 bit pattern */
+static uint32_t sra32(uint32_t x, int s) {
+  return (x >> s) | ((x & 0x80000000u) ? ~(0xFFFFFFFFu >> s) : 0u);
+}
+
+/* 24-bit integer of the hash; arith != 0 shifts as the Triton sampler's int32 does
+ * (triton_soft_forward.py:58-62), else logically as the CUDA one (fused_lut_kernel.cu:1247-1251).
+ * Wrapping multiplies and adds are the same bits in both. */
+static uint32_t lcg24(uint32_t seed, uint32_t idx, int arith) {
   uint32_t x = seed ^ (idx * 0x9E3779B9u);
-  x ^= x >> 13;
+  x ^= arith ? sra32(x, 13) : x >> 13;
   x = x * 1103515245u + 12345u;
-  x ^= x >> 17;
+  x ^= arith ? sra32(x, 17) : x >> 17;
   x = x * 1103515245u + 12345u;
-  float u = (float)(x & 0xFFFFFFu) * (1.0f / 16777216.0f);
+  return x & 0xFFFFFFu;
+}
+
+static float lcg_gumbel(uint32_t seed, uint32_t idx, int arith) {
+  float u = (float)lcg24(seed, idx, arith) * (1.0f / 16777216.0f);
   if (u < 1e-7f) u = 1e-7f;
   return -logf(-logf(u));
 }
 
 /* raw 24-bit uniform integers of the hash (bit-exact check target) */
 void orc_lcg_bits(uint32_t* out, uint32_t seed, const uint32_t* idx, int64_t n) {
-  for (int64_t i = 0; i < n; ++i) {
-    uint32_t x = seed ^ (idx[i] * 0x9E3779B9u);
-    x ^= x >> 13;
-    x = x * 1103515245u + 12345u;
-    x ^= x >> 17;
-    x = x * 1103515245u + 12345u;
-    out[i] = x & 0xFFFFFFu;
-  }
+  for (int64_t i = 0; i < n; ++i) out[i] = lcg24(seed, idx[i], 0);
 }
 
-void orc_gumbel_lcg(float* out, uint32_t seed, int64_t N, int64_t K) {
+void orc_lcg_bits_i32(uint32_t* out, uint32_t seed, const uint32_t* idx, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = lcg24(seed, idx[i], 1);
+}
+
+void orc_gumbel_lcg(float* out, uint32_t seed, int64_t N, int64_t K, int arith) {
   for (int64_t n = 0; n < N; ++n)
     for (int64_t k = 0; k < K; ++k) {
       uint32_t base = ((uint32_t)k * (uint32_t)N + (uint32_t)n) * 4u;
-      for (int c = 0; c < 4; ++c) out[(n * K + k) * 4 + c] = lcg_gumbel(seed, base + (uint32_t)c);
+      for (int c = 0; c < 4; ++c)
+        out[(n * K + k) * 4 + c] = lcg_gumbel(seed, base + (uint32_t)c, arith);
     }
 }
 

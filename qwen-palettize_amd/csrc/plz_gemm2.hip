@@ -1476,6 +1476,18 @@ int plz_lut_linear_bwd_palette(const uint16_t* x, const uint16_t* grad_y, const 
 
 static size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 
+// An empty weight (N == 0 or K == 0) has an empty palette gradient, but the LoRA factor of
+// the other side is not empty: grad_a [rank, K] is zero when N == 0 (no output row contributes)
+// and grad_b [N, rank] is zero when K == 0 (x A^T is zero).
+static int lora_grads_of_empty_weight(void* grad_a, void* grad_b, int rank, int grads_dtype,
+                                      int64_t N, int64_t K, hipStream_t stream, const char* what) {
+  const size_t esz = grads_dtype == PLZ_DT_BF16 ? 2 : 4;
+  PLZ_REQUIRE((K == 0 || grad_a) && (N == 0 || grad_b), "%s: null pointer", what);
+  if (K > 0) zero_async(grad_a, (size_t)rank * K * esz, stream);
+  if (N > 0) zero_async(grad_b, (size_t)N * rank * esz, stream);
+  return check_launch(what);
+}
+
 size_t plz_lut_linear_bwd_palette_lora_workspace(int64_t M, int64_t N, int64_t K, int rank) {
   if (M <= 0 || N <= 0 || K <= 0 || rank <= 0) return plz_lut_linear_bwd_palette_workspace(M, N, K);
   const int z = palette_splits(M, N, K);
@@ -1498,7 +1510,8 @@ int plz_lut_linear_bwd_palette_lora(const uint16_t* x, const uint16_t* grad_y,
               "%s: rank (%d) must be a multiple of 8 in [8, 32]", what, rank);
   PLZ_REQUIRE(grads_dtype == PLZ_DT_BF16 || grads_dtype == PLZ_DT_FP32,
               "%s: grads_dtype must be PLZ_DT_BF16 or PLZ_DT_FP32", what);
-  if (N == 0 || K == 0) return PLZ_OK;
+  if (N == 0 || K == 0) return lora_grads_of_empty_weight(grad_a, grad_b, rank, grads_dtype, N,
+                                                          K, (hipStream_t)stream, what);
   PLZ_REQUIRE(packed && grad_palette && lora_a && lora_b && grad_a && grad_b,
               "%s: null pointer", what);
   PLZ_REQUIRE(a16(lora_a) && a16(lora_b), "%s: lora_a and lora_b must be 16-byte aligned", what);
@@ -1759,7 +1772,8 @@ int plz_soft_bwd_lora(const uint16_t* x, const uint16_t* grad_y, const uint16_t*
   PLZ_REQUIRE(grads_dtype == PLZ_DT_BF16 || grads_dtype == PLZ_DT_FP32,
               "%s: grads_dtype must be PLZ_DT_BF16 or PLZ_DT_FP32", what);
   PLZ_REQUIRE(M >= 0 && N >= 0 && K >= 0, "%s: negative shape", what);
-  if (N == 0 || K == 0) return PLZ_OK;
+  if (N == 0 || K == 0) return lora_grads_of_empty_weight(grad_a, grad_b, rank, grads_dtype, N,
+                                                          K, (hipStream_t)stream, what);
   PLZ_REQUIRE(lora_a && lora_b && grad_a && grad_b && a16(lora_a) && a16(lora_b),
               "%s: lora_a, lora_b, grad_a, grad_b must be non-null; lora_a, lora_b 16-byte "
               "aligned", what);

@@ -23,27 +23,120 @@ __global__ void philox_gumbel_kernel(float* __restrict__ out, int64_t n4, uint64
                   gumbel_from_bits(r.w));
 }
 
-// The reference's LCG hash sampler (fused_lut_kernel.cu:1245-1256), element (n, k, c) drawn
-// with idx = (k*N + n)*4 + c in uint32 arithmetic, stored at [n, k, c].
+// The reference's LCG hash samplers. ARITH = false: the CUDA one (fused_lut_kernel.cu:1245-1256),
+// uint32 throughout. ARITH = true: the Triton one (triton_soft_forward.py:51-66), the same
+// statements in int32, where >> is an arithmetic shift; multiplies and adds wrap to the same
+// bits either way, so only the two shifts differ (when the shifted value has bit 31 set).
+template <bool ARITH>
+__device__ __forceinline__ uint32_t lcg_shr(uint32_t x, int s) {
+  return ARITH ? (uint32_t)((int32_t)x >> s) : x >> s;
+}
+template <bool ARITH>
 __device__ __forceinline__ float lcg_gumbel(uint32_t seed, uint32_t idx) {
   uint32_t x = seed ^ (idx * 0x9E3779B9u);
-  x ^= x >> 13;
+  x ^= lcg_shr<ARITH>(x, 13);
   x = x * 1103515245u + 12345u;
-  x ^= x >> 17;
+  x ^= lcg_shr<ARITH>(x, 17);
   x = x * 1103515245u + 12345u;
   float u = (float)(x & 0xFFFFFFu) * (1.0f / 16777216.0f);
   u = fmaxf(u, 1e-7f);
   return -logf(-logf(u));
 }
 
+// Element (n, k, c) drawn with idx = (k*N + n)*4 + c in uint32 arithmetic, stored at [n, k, c].
+template <bool ARITH>
 __global__ void lcg_gumbel_kernel(float* __restrict__ out, uint32_t seed, int64_t N, int64_t K) {
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // element (n, k)
   if (t >= N * K) return;
   const int64_t n = t / K, k = t % K;
   const uint32_t base = ((uint32_t)k * (uint32_t)N + (uint32_t)n) * 4u;
   *reinterpret_cast<float4*>(out + 4 * t) =
-      make_float4(lcg_gumbel(seed, base), lcg_gumbel(seed, base + 1), lcg_gumbel(seed, base + 2),
-                  lcg_gumbel(seed, base + 3));
+      make_float4(lcg_gumbel<ARITH>(seed, base), lcg_gumbel<ARITH>(seed, base + 1),
+                  lcg_gumbel<ARITH>(seed, base + 2), lcg_gumbel<ARITH>(seed, base + 3));
+}
+
+// ---- reference-layout batched P / W --------------------------------------------------
+// fused_compute_P_W_batched (fused_lut_kernel.cu:2097-2158) in the reference's own layouts:
+// logits (4, K, N) fp16 planes, palette (G, 4) bf16 with row o in group o / group_size,
+// P_aos (K, N, 4) fp16 and W (K, N) bf16 = sum_c P_c pal_c (the soft weight; this build does
+// not take an argmax). Element e = j*N + o draws class c at idx e*4 + c from the CUDA hash
+// keyed by step_seed ^ (seed_offset * 0x9E3779B9) (fused_lut_kernel.cu:2129). Each thread
+// takes 4 consecutive elements of the flat (K, N) index: with vec, as one 8-byte load per
+// logit plane, two 16-byte P stores and one 8-byte W store.
+constexpr int kPwBlock = 256;
+__global__ void pw_ref_batched_kernel(const plz_pw_ref_desc* __restrict__ descs, int n_desc,
+                                      int64_t group_size, float inv_tau, uint32_t step_seed) {
+  const int64_t b = blockIdx.x;
+  int lo = 0, hi = n_desc - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (descs[mid].block_begin <= b) lo = mid; else hi = mid - 1;
+  }
+  const plz_pw_ref_desc d = descs[lo];
+  const int64_t KN = d.K * d.N;
+  const int64_t e0 = ((b - d.block_begin) * kPwBlock + threadIdx.x) * 4;
+  if (e0 >= KN) return;
+  const int cnt = KN - e0 < 4 ? (int)(KN - e0) : 4;
+  const uint32_t seed = step_seed ^ (d.seed_offset * 0x9E3779B9u);
+  float l[4][4];  // [element][class]
+  if (d.vec) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const uint2 v = *reinterpret_cast<const uint2*>(d.logits + c * KN + e0);
+      l[0][c] = h2f(v.x & 0xffffu); l[1][c] = h2f(v.x >> 16);
+      l[2][c] = h2f(v.y & 0xffffu); l[3][c] = h2f(v.y >> 16);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) l[i][c] = i < cnt ? h2f(d.logits[c * KN + e0 + i]) : 0.f;
+  }
+  int64_t o = e0 % d.N;
+  uint32_t pbits[4][2], wbits[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t idx = (uint32_t)(e0 + i) * 4u;
+    float a[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) a[c] = (l[i][c] + lcg_gumbel<false>(seed, idx + c)) * inv_tau;
+    const float m = fmaxf(fmaxf(a[0], a[1]), fmaxf(a[2], a[3]));
+    float ex[4], s = 0.f;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      ex[c] = expf(a[c] - m);
+      s += ex[c];
+    }
+    const uint2 pv = *reinterpret_cast<const uint2*>(d.palette + (o / group_size) * 4);
+    const float pal[4] = {bf2f(pv.x & 0xffffu), bf2f(pv.x >> 16), bf2f(pv.y & 0xffffu),
+                          bf2f(pv.y >> 16)};
+    float P[4], w = 0.f;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      P[c] = ex[c] / s;
+      w += P[c] * pal[c];
+    }
+    pbits[i][0] = f2h(P[0]) | (f2h(P[1]) << 16);
+    pbits[i][1] = f2h(P[2]) | (f2h(P[3]) << 16);
+    wbits[i] = f2bf(w);
+    if (++o == d.N) o = 0;
+  }
+  if (d.vec) {
+    uint4* pp = reinterpret_cast<uint4*>(d.p_aos + e0 * 4);
+    pp[0] = make_uint4(pbits[0][0], pbits[0][1], pbits[1][0], pbits[1][1]);
+    pp[1] = make_uint4(pbits[2][0], pbits[2][1], pbits[3][0], pbits[3][1]);
+    *reinterpret_cast<uint2*>(d.w + e0) =
+        make_uint2(wbits[0] | (wbits[1] << 16), wbits[2] | (wbits[3] << 16));
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (i < cnt) {
+        uint32_t* pp = reinterpret_cast<uint32_t*>(d.p_aos + (e0 + i) * 4);
+        pp[0] = pbits[i][0];
+        pp[1] = pbits[i][1];
+        d.w[e0 + i] = (uint16_t)wbits[i];
+      }
+  }
 }
 
 // ---- build W -------------------------------------------------------------------------
@@ -168,15 +261,69 @@ int plz_gumbel_philox(float* noise, int64_t n, uint64_t seed, uint64_t offset, v
   return check_launch("plz_gumbel_philox");
 }
 
-int plz_gumbel_lcg(float* noise, uint32_t seed, int64_t N, int64_t K, void* stream) {
-  PLZ_REQUIRE(N >= 0 && K >= 0, "plz_gumbel_lcg: negative shape");
+static int gumbel_lcg(float* noise, uint32_t seed, int64_t N, int64_t K, bool arith,
+                      void* stream, const char* what) {
+  PLZ_REQUIRE(N >= 0 && K >= 0, "%s: negative shape", what);
   if (N == 0 || K == 0) return PLZ_OK;
   PLZ_REQUIRE(noise && ((uintptr_t)noise & 15) == 0,
-              "plz_gumbel_lcg: noise must be non-null and 16-byte aligned");
+              "%s: noise must be non-null and 16-byte aligned", what);
   const int64_t n = N * K;
-  hipLaunchKernelGGL(lcg_gumbel_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
-                     (hipStream_t)stream, noise, seed, N, K);
-  return check_launch("plz_gumbel_lcg");
+  const dim3 grid((unsigned)((n + 255) / 256));
+  if (arith)
+    hipLaunchKernelGGL(lcg_gumbel_kernel<true>, grid, dim3(256), 0, (hipStream_t)stream, noise,
+                       seed, N, K);
+  else
+    hipLaunchKernelGGL(lcg_gumbel_kernel<false>, grid, dim3(256), 0, (hipStream_t)stream, noise,
+                       seed, N, K);
+  return check_launch(what);
+}
+
+int plz_gumbel_lcg(float* noise, uint32_t seed, int64_t N, int64_t K, void* stream) {
+  return gumbel_lcg(noise, seed, N, K, false, stream, "plz_gumbel_lcg");
+}
+
+int plz_gumbel_lcg_triton(float* noise, uint32_t seed, int64_t N, int64_t K, void* stream) {
+  return gumbel_lcg(noise, seed, N, K, true, stream, "plz_gumbel_lcg_triton");
+}
+
+int64_t plz_pw_ref_plan(plz_pw_ref_desc* descs, int n, int64_t group_size) {
+  if (n < 0 || (n > 0 && !descs) || group_size <= 0) {
+    set_error("plz_pw_ref_plan: need n >= 0, non-null descriptors and group_size > 0");
+    return -PLZ_EINVAL;
+  }
+  int64_t total = 0;
+  for (int i = 0; i < n; ++i) {
+    plz_pw_ref_desc& d = descs[i];
+    if (d.K < 0 || d.N < 0 || d.N % group_size != 0 || d.K * d.N * 4 > 0xFFFFFFFFll) {
+      set_error("plz_pw_ref_plan: descriptor %d: N (%lld) must be a multiple of group_size "
+                "(%lld) and 4*K*N must fit 32 bits", i, (long long)d.N, (long long)group_size);
+      return -PLZ_EINVAL;
+    }
+    const int64_t kn = d.K * d.N;
+    if (kn > 0 && (!d.logits || !d.palette || !d.p_aos || !d.w ||
+                   (((uintptr_t)d.logits | (uintptr_t)d.p_aos | (uintptr_t)d.w) & 1) ||
+                   ((uintptr_t)d.palette & 7))) {
+      set_error("plz_pw_ref_plan: descriptor %d: null or misaligned pointer", i);
+      return -PLZ_EINVAL;
+    }
+    d.vec = (kn % 4 == 0 && ((uintptr_t)d.logits & 7) == 0 && ((uintptr_t)d.p_aos & 15) == 0 &&
+             ((uintptr_t)d.w & 7) == 0) ? 1 : 0;
+    d.block_begin = total;
+    total += (kn + 4 * kPwBlock - 1) / (4 * kPwBlock);
+  }
+  return total;
+}
+
+int plz_soft_pw_ref_batched(const plz_pw_ref_desc* descs_device, int n, int64_t total_blocks,
+                            int64_t group_size, float tau, uint32_t step_seed, void* stream) {
+  PLZ_REQUIRE(n >= 0 && total_blocks >= 0, "plz_soft_pw_ref_batched: negative count");
+  PLZ_REQUIRE(group_size > 0, "plz_soft_pw_ref_batched: group_size must be positive");
+  PLZ_REQUIRE(tau > 0.f, "plz_soft_pw_ref_batched: tau must be positive");
+  if (n == 0 || total_blocks == 0) return PLZ_OK;
+  PLZ_REQUIRE(descs_device, "plz_soft_pw_ref_batched: null descriptor table");
+  hipLaunchKernelGGL(pw_ref_batched_kernel, dim3((unsigned)total_blocks), dim3(kPwBlock), 0,
+                     (hipStream_t)stream, descs_device, n, group_size, 1.f / tau, step_seed);
+  return check_launch("plz_soft_pw_ref_batched");
 }
 
 static int build_w(const uint16_t* logits, int logits_dtype, bool gen, const float* noise,

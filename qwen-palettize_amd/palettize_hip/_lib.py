@@ -27,6 +27,11 @@ class BuildWDesc(C.Structure):
                 ("block_begin", i64), ("noise_seed", u64)]
 
 
+class PwRefDesc(C.Structure):
+    _fields_ = [("logits", p), ("palette", p), ("p_aos", p), ("w", p), ("K", i64), ("N", i64),
+                ("block_begin", i64), ("seed_offset", u32), ("vec", i32)]
+
+
 class AdamWDesc(C.Structure):
     _fields_ = [("param", p), ("grad", p), ("master", p), ("exp_avg", p), ("exp_avg_sq", p),
                 ("n", i64), ("dtype", i32), ("clip_group", i32), ("lr", f32), ("clamp_lo", f32),
@@ -72,6 +77,9 @@ SIGNATURES: dict[str, tuple] = {
     "plz_linear_bwd_x_dense_workspace": (sz, [i64, i64, i64]),
     "plz_gumbel_philox": (i32, [p, i64, u64, u64, p]),
     "plz_gumbel_lcg": (i32, [p, u32, i64, i64, p]),
+    "plz_gumbel_lcg_triton": (i32, [p, u32, i64, i64, p]),
+    "plz_pw_ref_plan": (i64, [C.POINTER(PwRefDesc), i32, i64]),
+    "plz_soft_pw_ref_batched": (i32, [p, i32, i64, i64, f32, u32, p]),
     "plz_soft_build_w": (i32, [p, i32, p, p, f32, i32, p, p, i64, i64, p]),
     "plz_soft_build_w_philox": (i32, [p, i32, u64, u64, p, f32, i32, p, p, i64, i64, p]),
     "plz_build_w_plan": (i64, [C.POINTER(BuildWDesc), i32]),

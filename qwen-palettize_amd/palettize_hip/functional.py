@@ -27,8 +27,9 @@ def _c(t):
 
 class LUTLinearFunction(torch.autograd.Function):
     """Where the library dequantises W for the forward GEMM (from 4096 rows, see
-    ops.lut_linear_staged), the bf16 W is kept for the backward's grad_x instead of being
-    dequantised a second time (N*K*2 bytes held from forward to backward)."""
+    ops.lut_linear_staged) and x needs a gradient, the bf16 W is kept for the backward's
+    grad_x instead of being dequantised a second time (N*K*2 bytes held from forward to
+    backward); without a gradient for x nothing reads it, and it is dropped after the GEMM."""
 
     @staticmethod
     def forward(ctx, x, packed, palette, bias, lora_a, lora_b, lora_scale):
@@ -39,6 +40,8 @@ class LUTLinearFunction(torch.autograd.Function):
         if ops.lut_linear_staged(x.shape[0], packed.shape[0], x.shape[1]):
             w = ops.dequant(packed, palette)
             y = ops.linear_fwd_dense(x, w, bias, t, lora_b)
+            if not ctx.needs_input_grad[0]:
+                w = None
         else:
             y = ops.lut_linear_fwd(x, packed, palette, bias, t, lora_b)
         ctx.save_for_backward(x, packed, palette, lora_a, lora_b, t, w)

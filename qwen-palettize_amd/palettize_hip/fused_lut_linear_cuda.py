@@ -16,6 +16,10 @@ Same names, arguments, layouts and gradient tuples as the reference
       same noise integers as the reference. Forward value W_hard = palette[argmax of the
       noisy P] (straight-through); backward -> (grad_x, grad_palette, grad_logits (4, K, N)
       fp16, grad_bias, None, None) with the reference's formulas (no 1/tau factor).
+      fused_lut_linear_soft(..., semantics="triton") follows the reference's Triton path
+      instead (int32 sampler, argmax of the plain logits; triton_soft_forward.py:51-181).
+  fused_compute_P_W_batched(student, tau, step_seed, group_size=None) -> [(P_aos, W_soft)]
+      the batched soft build of every soft PalettizedLinear (fused_lut_linear_cuda.py:1016-1077).
 
 The reference layout (one palette per 256 output channels spanning all of K) is mapped onto
 the native one (palette per output row and 256-wide K chunk) by expanding the palette; its
@@ -32,7 +36,7 @@ import torch.nn.functional as F
 from torch import Tensor
 
 from . import ops
-from ._lib import PLZ_W_HARD_NOISY, PLZ_W_SOFT
+from ._lib import PLZ_W_HARD_NOISY, PLZ_W_HARD_PLAIN, PLZ_W_SOFT
 
 GROUP_SIZE = 256
 
@@ -241,15 +245,31 @@ def fused_lut_linear_pre_transposed(x: Tensor, palette: Tensor, indices: Tensor,
     return PreTransposedLUTLinear.apply(x, palette, indices, bias, group_size)
 
 
-# Global step counter for the Gumbel seed (one increment per soft forward), as in the
-# reference (fused_lut_linear_cuda.py:837-843).
+# Global step counters for the Gumbel seed (one increment per soft forward), as in the
+# reference: the CUDA-C module's (fused_lut_linear_cuda.py:837-843) and the Triton module's own
+# (triton_soft_forward.py:308-314), which advance independently.
 _SOFT_STEP_SEED = 0
+_TRITON_STEP_SEED = 0
+
+# Soft-path semantics of the reference's two implementations:
+#   "cuda"   CUDAFusedLUTLinearSoft: uint32 LCG sampler (fused_lut_kernel.cu:1245-1256),
+#            W_hard = palette[argmax of the noisy P] (fused_lut_kernel.cu:1998-2003)
+#   "triton" TritonSoftLinear, which PalettizedLinear prefers when triton imports
+#            (qwen_model.py:111-121,158-163): int32 LCG sampler (triton_soft_forward.py:51-66),
+#            W_hard = palette[argmax of the plain logits] (triton_soft_forward.py:160-176)
+SEMANTICS = ("cuda", "triton")
 
 
 def _next_soft_step_seed() -> int:
     global _SOFT_STEP_SEED
     _SOFT_STEP_SEED = (_SOFT_STEP_SEED + 1) & 0xFFFFFFFF
     return _SOFT_STEP_SEED
+
+
+def _next_triton_step_seed() -> int:
+    global _TRITON_STEP_SEED
+    _TRITON_STEP_SEED = (_TRITON_STEP_SEED + 1) & 0xFFFFFFFF
+    return _TRITON_STEP_SEED
 
 
 def logits_from_reference(logits: Tensor, K: int) -> Tensor:
@@ -275,9 +295,12 @@ def _noise_to_native(noise: Tensor, K: int, N: int, Kp: int) -> Tensor:
     return noise.contiguous()
 
 
-def _soft_forward(ctx, x, palette, logits, bias, group_size, tau, noise, ste):
-    """Forward of fused_lut_linear_soft: W from logits + noise + palette (W_hard of the noisy
-    P when ste, else W_soft), then y = x W^T + b. Saves what _soft_backward needs."""
+def _soft_forward(ctx, x, palette, logits, bias, group_size, tau, noise, ste, semantics="cuda"):
+    """Forward of fused_lut_linear_soft: W from logits + noise + palette (when ste, W_hard of
+    the noisy P for "cuda" semantics or of the plain logits for "triton"; else W_soft), then
+    y = x W^T + b. Saves what _soft_backward needs."""
+    if semantics not in SEMANTICS:
+        raise ValueError(f"semantics must be one of {SEMANTICS}, got {semantics!r}")
     if logits.dim() != 3 or logits.shape[0] != 4:
         raise ValueError("logits first dim must be 4")
     if logits.dtype not in (torch.float16, torch.bfloat16):
@@ -291,12 +314,16 @@ def _soft_forward(ctx, x, palette, logits, bias, group_size, tau, noise, ste):
     Kp = xp.shape[1]
     lg = logits_from_reference(logits, K)
     if noise is None:  # the reference's LCG draw, one seed per forward
-        noise = ops.gumbel_lcg(N, Kp, _next_soft_step_seed(), device=x.device)
+        if semantics == "triton":
+            noise = ops.gumbel_lcg(N, Kp, _next_triton_step_seed(), device=x.device,
+                                   variant="triton")
+        else:
+            noise = ops.gumbel_lcg(N, Kp, _next_soft_step_seed(), device=x.device)
     else:
         noise = _noise_to_native(noise, K, N, Kp)
     pal = palette_from_reference(palette, N, K, group_size)
-    w, _ = ops.soft_build_w(lg, noise, pal, float(tau),
-                            PLZ_W_HARD_NOISY if ste else PLZ_W_SOFT)
+    hard = PLZ_W_HARD_PLAIN if semantics == "triton" else PLZ_W_HARD_NOISY
+    w, _ = ops.soft_build_w(lg, noise, pal, float(tau), hard if ste else PLZ_W_SOFT)
     b = None if bias is None else bias.to(torch.bfloat16).contiguous()
     y = ops.linear_fwd_dense(xp, w, b)
     ctx.save_for_backward(xp, pal, lg, noise, w)
@@ -340,26 +367,84 @@ class CUDAFusedLUTLinearSoft(torch.autograd.Function):
 
 
 class _SoftLUTLinearExt(torch.autograd.Function):
-    """fused_lut_linear_soft with supplied noise and / or the pure-soft forward (ste=False);
-    the backward is the same STE backward."""
+    """fused_lut_linear_soft with supplied noise, the pure-soft forward (ste=False) and / or
+    the Triton path's semantics; the backward is the same STE backward (TritonSoftLinear's
+    backward, triton_soft_forward.py:367-411, computes the same quantities)."""
 
     @staticmethod
-    def forward(ctx, x, palette, logits, bias, group_size, tau, noise, ste):
-        return _soft_forward(ctx, x, palette, logits, bias, group_size, tau, noise, ste)
+    def forward(ctx, x, palette, logits, bias, group_size, tau, noise, ste, semantics):
+        return _soft_forward(ctx, x, palette, logits, bias, group_size, tau, noise, ste,
+                             semantics)
 
     @staticmethod
     def backward(ctx, grad_y):
-        return _soft_backward(ctx, grad_y) + (None, None, None, None)
+        return _soft_backward(ctx, grad_y) + (None, None, None, None, None)
 
 
 def fused_lut_linear_soft(x: Tensor, palette: Tensor, logits: Tensor, bias: Tensor | None = None,
                           group_size: int = GROUP_SIZE, tau: float = 1.0, *,
-                          noise: Tensor | None = None, ste: bool = True) -> Tensor:
+                          noise: Tensor | None = None, ste: bool = True,
+                          semantics: str = "cuda") -> Tensor:
     """Soft (Gumbel-Softmax) functional interface -- supports autograd.
 
     Beyond the reference's signature: ``noise`` (fp32, (4, K, N) like the logits or native
     [N, K, 4]) replaces the internal LCG draw; ``ste=False`` makes the forward use W_soft =
-    sum_c P_c pal_c instead of the straight-through W_hard (the backward is unchanged)."""
-    if noise is None and ste:
+    sum_c P_c pal_c instead of the straight-through W_hard (the backward is unchanged);
+    ``semantics="triton"`` follows the reference's Triton path (int32 sampler with its own
+    step counter, W_hard from the plain logits) instead of its CUDA-C one."""
+    if semantics not in SEMANTICS:
+        raise ValueError(f"semantics must be one of {SEMANTICS}, got {semantics!r}")
+    if noise is None and ste and semantics == "cuda":
         return CUDAFusedLUTLinearSoft.apply(x, palette, logits, bias, group_size, tau)
-    return _SoftLUTLinearExt.apply(x, palette, logits, bias, group_size, tau, noise, ste)
+    return _SoftLUTLinearExt.apply(x, palette, logits, bias, group_size, tau, noise, ste,
+                                   semantics)
+
+
+class _Extension:
+    """The raw functions of the reference's compiled module that callers reach through
+    _get_module() for the soft build (fused_lut_linear_cuda.py:388-422, :513-607; used by
+    test_batched_compute_pw.py and test_profile_kernels.py), in the reference's layouts."""
+
+    @staticmethod
+    def fused_compute_P_W_batched(logits_list, palette_list, group_size, tau, step_seed):
+        """-> [P_aos_0, W_0, P_aos_1, W_1, ...]: P_aos (K, N, 4) fp16, W (K, N) bf16 = W_soft;
+        layer i draws with seed step_seed ^ (i * 0x9E3779B9) (fused_lut_kernel.cu:2129)."""
+        return ops.soft_pw_reference_batched(list(logits_list), list(palette_list),
+                                             int(group_size), float(tau), int(step_seed))
+
+    @staticmethod
+    def fused_lut_linear_soft_fwd_aos(x, palette, logits, group_size, tau, step_seed):
+        """-> [P_aos (K, N, 4) fp16, W (K, N) bf16 = W_soft] of one layer, seed step_seed."""
+        if not x.is_cuda or x.dtype != torch.bfloat16:
+            raise TypeError("x must be bf16 cuda")
+        return ops.soft_pw_reference_batched([logits], [palette], int(group_size), float(tau),
+                                             int(step_seed))
+
+
+def _get_module():
+    return _Extension
+
+
+def fused_compute_P_W_batched(student, tau: float, step_seed: int, group_size: int | None = None):
+    """P_aos + W_soft for every PalettizedLinear of ``student`` with index_logits and
+    ``_use_cuda`` in one launch (fused_lut_linear_cuda.py:1016-1077): a list of (P_aos (K, N, 4)
+    fp16, W (K, N) bf16) in named_modules() order; [] when there is none. All layers must share
+    one group_size."""
+    from .qwen_model import PalettizedLinear
+
+    layers = [mod for _, mod in student.named_modules()
+              if isinstance(mod, PalettizedLinear) and mod.index_logits is not None
+              and getattr(mod, "_use_cuda", False)]
+    if not layers:
+        return []
+    if group_size is None:
+        group_size = layers[0].group_size
+    for i, mod in enumerate(layers):
+        if mod.group_size != group_size:
+            raise ValueError(f"All PalettizedLinears must share group_size for the batched "
+                             f"compute_P_W kernel; layer {i} has group_size={mod.group_size} "
+                             f"vs expected {group_size}")
+    flat = _get_module().fused_compute_P_W_batched(
+        [m.index_logits.detach() for m in layers], [m.palette.detach() for m in layers],
+        int(group_size), float(tau), int(step_seed))
+    return [(flat[i], flat[i + 1]) for i in range(0, len(flat), 2)]

@@ -290,6 +290,7 @@ class PalettizedDecoderLayer(nn.Module):
         self.q_norm = RMSNorm(hd, cfg.eps, device)
         self.k_norm = RMSNorm(hd, cfg.eps, device)
         self._wgroup = None
+        self._wgroup_key = None
 
     def linears(self):
         return [getattr(self, n) for n in self.NAMES]
@@ -299,10 +300,15 @@ class PalettizedDecoderLayer(nn.Module):
         each linear's own Philox key at the shared counter offset of this forward, the same
         tau. Returns {name: (w, group, noise)} for the linears' forward."""
         lins = self.linears()
-        if self._wgroup is None:
+        # the group's descriptor table holds the parameters' device addresses: rebuild it when a
+        # parameter has been replaced rather than written in place (module.to(),
+        # load_state_dict(assign=True), param.data = ...)
+        key = tuple((t.data_ptr(), t.device) for l in lins for t in (l.index_logits, l.palette))
+        if self._wgroup is None or self._wgroup_key != key:
             self._wgroup = ops.SoftBuildGroup(
                 [(l.index_logits, ops.PhiloxNoise(l.noise_seed, 0), l.palette) for l in lins],
                 PLZ_W_HARD_NOISY)
+            self._wgroup_key = key
         offset = lins[0].noise_counter
         if any(l.noise_counter != offset or l.mode != PLZ_W_HARD_NOISY or l.tau != lins[0].tau
                for l in lins):

@@ -321,10 +321,67 @@ def gumbel_philox(shape, seed: int, offset: int = 0, device="cuda"):
     return out
 
 
-def gumbel_lcg(N: int, K: int, seed: int, device="cuda"):
+def gumbel_lcg(N: int, K: int, seed: int, device="cuda", variant: str = "cuda"):
+    """The reference's LCG Gumbel noise [N, K, 4], element (n, k, c) drawn at
+    idx (k*N + n)*4 + c: the CUDA hash (variant "cuda") or the Triton one ("triton")."""
+    if variant not in ("cuda", "triton"):
+        raise ValueError(f"unknown LCG variant {variant!r}")
     out = torch.empty((N, K, 4), dtype=torch.float32, device=device)
-    call("plz_gumbel_lcg", _ptr(out), int(seed) & 0xFFFFFFFF, N, K, _stream(out))
+    call("plz_gumbel_lcg_triton" if variant == "triton" else "plz_gumbel_lcg", _ptr(out),
+         int(seed) & 0xFFFFFFFF, N, K, _stream(out))
     return out
+
+
+def soft_pw_reference_batched(logits_list, palette_list, group_size: int, tau: float,
+                              step_seed: int):
+    """[P_aos_0, W_0, P_aos_1, W_1, ...] of the reference's fused_compute_P_W_batched
+    (fused_lut_linear_cuda.py:513-607) from one launch: logits (4, K, N) fp16 and palettes
+    (G, 4) bf16 with G = N / group_size, in and out in the reference's layouts; layer i draws
+    its LCG noise with seed step_seed ^ (i * 0x9E3779B9)."""
+    n = len(logits_list)
+    if n == 0:
+        raise ValueError("logits_list must be non-empty")
+    if len(palette_list) != n:
+        raise ValueError("palette_list size must match logits_list size")
+    if n > 64:
+        raise ValueError(f"max 64 layers in batched kernel (got {n})")
+    group_size = int(group_size)
+    if group_size <= 0:
+        raise ValueError("group_size must be positive")
+    descs = (_lib.PwRefDesc * n)()
+    outs, held = [], []  # held: realigned palette copies, alive until the launch is queued
+    dev = logits_list[0].device
+    for i, (lg, pal) in enumerate(zip(logits_list, palette_list)):
+        _need(lg, f"logits[{i}]", torch.float16, 3)
+        _need(pal, f"palette[{i}]", torch.bfloat16, 2)
+        if lg.shape[0] != 4:
+            raise ValueError(f"logits[{i}] must be (4, K, N)")
+        if pal.shape[1] != 4:
+            raise ValueError(f"palette[{i}] must be (G, 4)")
+        if lg.device != dev or pal.device != dev:
+            raise ValueError("all tensors must be on one device")
+        K, N = lg.shape[1], lg.shape[2]
+        if N % group_size:
+            raise ValueError(f"layer {i}: N={N} not divisible by group_size={group_size}")
+        if N // group_size != pal.shape[0]:
+            raise ValueError(f"layer {i}: G mismatch (N/GS={N // group_size} vs "
+                             f"palette.size(0)={pal.shape[0]})")
+        if pal.data_ptr() % 8:
+            pal = pal.clone()
+            held.append(pal)
+        P = torch.empty((K, N, 4), dtype=torch.float16, device=dev)
+        w = torch.empty((K, N), dtype=torch.bfloat16, device=dev)
+        outs += [P, w]
+        descs[i] = _lib.PwRefDesc(lg.data_ptr(), pal.data_ptr(), P.data_ptr(), w.data_ptr(), K, N,
+                                  0, i, 0)
+    total = _lib.lib().plz_pw_ref_plan(descs, n, group_size)
+    if total < 0:
+        raise _lib.PalettizeError("plz_pw_ref_plan failed: " + _lib.lib().plz_last_error().decode())
+    raw = bytes(C.string_at(C.addressof(descs), C.sizeof(descs)))
+    table = torch.frombuffer(bytearray(raw), dtype=torch.uint8).to(dev)
+    call("plz_soft_pw_ref_batched", table.data_ptr(), n, int(total), group_size, float(tau),
+         int(step_seed) & 0xFFFFFFFF, torch.cuda.current_stream(dev).cuda_stream)
+    return outs
 
 
 class PhiloxNoise:

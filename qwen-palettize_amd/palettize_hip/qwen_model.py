@@ -6,8 +6,10 @@ PalettizedLinear keeps the reference's buffers and parameters -- indices (in, ou
 (4, in, out) fp16 (+-10 one-hot, only with use_soft_indices), tau, group_size, n_groups,
 palette_size, pre_transposed, in_features, out_features, bias -- and dispatches like
 qwen_model.py:147-196: soft (Gumbel-softmax, straight-through) in training mode with soft
-indices, hard otherwise. Palette groups run along the stored indices' second dimension: the
-output dimension normally, the input dimension when pre_transposed (qwen_model.py:97-102).
+indices, hard otherwise. soft_semantics picks which of the reference's soft implementations
+the soft forward follows: "cuda" (its CUDA-C kernels) or "triton" (its Triton kernels).
+Palette groups run along the stored indices' second dimension: the output dimension
+normally, the input dimension when pre_transposed (qwen_model.py:97-102).
 Both dispatch to the drop-in fused_lut_linear_cuda functions; there is no CPU fallback
 (a CPU input raises).
 """
@@ -23,8 +25,17 @@ from . import fused_lut_linear_cuda as FL
 
 class PalettizedLinear(nn.Module):
     def __init__(self, original_linear, indices, n_groups, palette_size, group_size,
-                 pre_transposed, initial_palette=None, use_soft_indices=False):
+                 pre_transposed, initial_palette=None, use_soft_indices=False,
+                 soft_semantics="cuda"):
         super().__init__()
+        if soft_semantics not in FL.SEMANTICS:
+            raise ValueError(f"soft_semantics must be one of {FL.SEMANTICS}")
+        # which of the reference's soft implementations this module follows: its CUDA-C one
+        # ("cuda") or its Triton one ("triton", which the reference prefers when triton
+        # imports, qwen_model.py:111-128); the flags mirror the reference's attributes
+        self.soft_semantics = soft_semantics
+        self._use_triton = not pre_transposed and soft_semantics == "triton"
+        self._use_cuda = not pre_transposed and soft_semantics == "cuda"
         self.register_buffer("indices", indices.long())
         self.register_buffer("indices_int8", indices.to(torch.int8).contiguous())
         self.palette = nn.Parameter(
@@ -62,7 +73,8 @@ class PalettizedLinear(nn.Module):
         x_flat = x.reshape(-1, x.shape[-1]) if x.ndim == 3 else x
         if self.training and self.use_soft_indices and self.index_logits is not None:
             y = FL.fused_lut_linear_soft(x_flat, self.palette, self.index_logits, self.bias,
-                                         self.group_size, self.tau)
+                                         self.group_size, self.tau,
+                                         semantics=self.soft_semantics)
         elif self.pre_transposed:
             # indices (out, in), palette groups along the input dimension (qwen_model.py:187-190)
             y = FL.fused_lut_linear_pre_transposed(x_flat, self.palette, self.indices_int8,

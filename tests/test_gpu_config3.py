@@ -89,3 +89,25 @@ def test_config3_grad_palette(dev, problems, name):
     gyc = f32(p["gy"][:, ns]).astype(np.float64)
     want = O.grad_palette(x64, gyc, p["idx"][ns].cpu().numpy())
     assert_close(f32(g1[ns]), want, what=f"{name} grad_palette (M={M})")
+
+
+@pytest.mark.parametrize("name", [s[0] for s in SHAPES])
+def test_config3_grad_palette_lora(dev, problems, name):
+    """The entry the benchmark times (plz_lut_linear_bwd_palette_lora): grad_palette bit-equal
+    to the plain entry's, and grad_A [r, K] / grad_B [N, r] (rank 16; 32 on o and down) from
+    the dW tiles of every split-M part, summed in fixed order, against the fp64 oracle over all
+    M = 16384 rows at the north-star bar; bit-repeatable."""
+    p = problems[name]
+    scale = 2.0
+    gp, ga, gb = ops.lut_linear_bwd_palette_lora(p["x"], p["gy"], p["packed"], p["a"], p["b"],
+                                                 scale, out_dtype=torch.bfloat16)
+    gp2, ga2, gb2 = ops.lut_linear_bwd_palette_lora(p["x"], p["gy"], p["packed"], p["a"], p["b"],
+                                                    scale, out_dtype=torch.bfloat16)
+    assert torch.equal(gp, gp2) and torch.equal(ga, ga2) and torch.equal(gb, gb2), \
+        f"{name}: LoRA grad_palette entry must be bit-repeatable"
+    assert torch.equal(gp, ops.lut_linear_bwd_palette(p["x"], p["gy"], p["packed"])), \
+        f"{name}: palette output differs from plz_lut_linear_bwd_palette"
+    want_a, want_b = O.lora_weight_grads(f32(p["x"]), f32(p["gy"]), f32(p["a"]), f32(p["b"]),
+                                         scale)
+    assert_close(f32(ga), want_a, what=f"{name} grad_A (M={M}, r={p['r']})")
+    assert_close(f32(gb), want_b, what=f"{name} grad_B (M={M}, r={p['r']})")

@@ -6,10 +6,11 @@ import torch
 
 import oracle as O
 import torch_ref as R
-from helpers import assert_close, cosine, f32
+from helpers import assert_close, cosine, f32, rel_err
 
 pytestmark = pytest.mark.gpu
 layer = pytest.importorskip("palettize_hip.layer")
+ops = pytest.importorskip("palettize_hip.ops")
 
 CFG = dict(hidden=256, heads=4, kv_heads=2, head_dim=64, intermediate=512, lora_rank=16,
            lora_alpha=16.0)
@@ -67,7 +68,7 @@ def test_layer_step_forward_backward_matches_cpu_reference(dev, cfg_kw, batch, s
     loss_ref.backward()
     lr = float(loss_ref.detach())
     rel_loss = abs(float(loss) - lr) / abs(lr)
-    cos = {}
+    cos, rel = {}, {}
     for name in tr.student.NAMES:
         lin = getattr(tr.student, name)
         for attr, key in (("palette", "palette"), ("index_logits", "logits"),
@@ -75,11 +76,20 @@ def test_layer_step_forward_backward_matches_cpu_reference(dev, cfg_kw, batch, s
             got = f32(getattr(lin, attr).grad)
             want = p[name][key].grad.numpy()
             cos[f"{name}.{attr}"] = cosine(got, want)
+            rel[f"{name}.{attr}"] = rel_err(got, want)
     worst = min(cos, key=cos.get)
-    print(f"loss rel-err {rel_loss:.3e}; worst gradient cosine {worst} {cos[worst]:.7f}",
-          flush=True)
+    worst_rel = max(rel, key=rel.get)
+    print(f"loss rel-err {rel_loss:.3e}; worst gradient cosine {worst} {cos[worst]:.7f}; "
+          f"worst gradient max-rel-err {worst_rel} {rel[worst_rel]:.3e}", flush=True)
     assert rel_loss <= 1e-3, f"loss {float(loss)} vs {lr}"
     assert cos[worst] >= 0.9999, f"{worst}: cosine {cos[worst]:.7f} (all: {cos})"
+    # Each op of the step meets max-rel-err 1e-2 against its fp64 oracle in its own test. Here
+    # two bf16 programs are compared end to end: where their accumulation orders differ, a
+    # forward activation lands one bf16 ulp apart and the flip travels through the rest of the
+    # step (measured worst 1.7e-2, on a LoRA B gradient, at cosine 0.99995); the LoRA weight
+    # gradients' two valid orderings alone, (gy^T x) A^T from the bf16 dW tile here and
+    # gy^T bf16(x A^T) in the reference, differ by 2e-3.
+    assert rel[worst_rel] <= 3e-2, f"{worst_rel}: max-rel-err {rel[worst_rel]:.3e} (all: {rel})"
 
 
 def test_layer_update_matches_adamw_clip_clamp(dev):
@@ -139,3 +149,19 @@ def test_layer_step_full_config_deterministic_and_training(dev):
         loss, _ = tr.forward_backward(hs)
         losses.append(float(loss))
     assert all(np.isfinite(losses)) and losses[-1] < losses[0], losses
+
+
+def test_build_weights_follows_replaced_parameters(dev):
+    """The layer's batched build holds device addresses of the logits and palettes: a parameter
+    replaced rather than written in place must be picked up by the next build."""
+    cfg = layer.LayerConfig(**CFG)
+    st = layer.PalettizedDecoderLayer(cfg, seed=1, device=dev)
+    st.build_weights()
+    lin = st.q_proj
+    lin.palette = torch.nn.Parameter(lin.palette.detach() * 2.0)
+    lin.index_logits = torch.nn.Parameter(lin.index_logits.detach().flip(-1).contiguous())
+    off = lin.noise_counter
+    pw = st.build_weights()
+    w, _ = ops.soft_build_w(lin.index_logits, ops.PhiloxNoise(lin.noise_seed, off), lin.palette,
+                            lin.tau, lin.mode)
+    assert torch.equal(pw["q_proj"][0], w)

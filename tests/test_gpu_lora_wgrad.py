@@ -143,3 +143,29 @@ def test_soft_autograd_lora_weight_grads_ride_on_the_dw_gemm(dev, M, N, K):
     rl, rp = ops.soft_bwd(x.detach(), gy, logits.detach(), spec, pal.detach(), tau)
     assert torch.equal(logits.grad, rl) and torch.equal(pal.grad, rp)
     assert bool(torch.isfinite(x.grad.float()).all())
+
+
+def test_lora_grads_of_an_empty_weight_are_zero(dev):
+    """N == 0: grad_A [r, K] is zero (no output row contributes); K == 0: grad_B [N, r] is zero
+    (x A^T is zero). Both entries write them although the weight itself is empty."""
+    from palettize_hip import _lib
+    lib = _lib.lib()
+    r, K, N, M = 16, 512, 256, 64
+    s = torch.cuda.current_stream().cuda_stream
+    for entry in ("plz_lut_linear_bwd_palette_lora", "plz_soft_bwd_lora"):
+        ga = torch.full((r, K), float("nan"), dtype=torch.bfloat16, device=dev)
+        gb = torch.full((N, r), float("nan"), dtype=torch.bfloat16, device=dev)
+        for n, k, out_a, out_b in ((0, K, ga, None), (N, 0, None, gb)):
+            pa = None if out_a is None else out_a.data_ptr()
+            pb = None if out_b is None else out_b.data_ptr()
+            if entry == "plz_lut_linear_bwd_palette_lora":
+                rc = lib.plz_lut_linear_bwd_palette_lora(None, None, None, None, None, r, 1.0,
+                                                         None, pa, pb, _lib.PLZ_DT_BF16, None, 0,
+                                                         M, n, k, s)
+            else:
+                rc = lib.plz_soft_bwd_lora(None, None, None, _lib.PLZ_DT_BF16, None, 0, 0, None,
+                                           0.5, 0, None, None, r, 1.0, None, None, pa, pb,
+                                           _lib.PLZ_DT_BF16, None, 0, M, n, k, s)
+            assert rc == 0, lib.plz_last_error()
+        torch.cuda.synchronize()
+        assert bool((ga == 0).all()) and bool((gb == 0).all()), entry

@@ -114,9 +114,18 @@ def test_soft_build_w_batched_philox(dev, mode):
                 got = O.bf16_to_f32(w.view(torch.int16).cpu().numpy().view(np.uint16))
                 if mode == PLZ_W_SOFT:
                     assert np.allclose(got, w_fwd, rtol=2.0 ** -7, atol=1e-6)
-                else:
+                elif mode == PLZ_W_HARD_PLAIN:
                     want = O.bf16_to_f32(O.bf16_bits(w_fwd.astype(np.float32)))
-                    assert np.mean(got == want) > 0.999
+                    assert np.array_equal(got, want)
+                else:
+                    # bit-exact except where the top two of (logit + noise) / tau are a near
+                    # tie that fp32 (GPU) and fp64 (oracle) may order differently
+                    want = O.bf16_to_f32(O.bf16_bits(w_fwd.astype(np.float32)))
+                    z = (f32(lgc).astype(np.float64) + noise) / tau
+                    top2 = np.sort(z, axis=-1)[..., -2:]
+                    tie = top2[..., 1] - top2[..., 0] <= 1e-5 * (1.0 + np.abs(top2[..., 1]))
+                    bad = got != want
+                    assert not np.any(bad & ~tie), f"{int(np.sum(bad & ~tie))} differ off a tie"
                 soft = O.bf16_to_f32(ws.view(torch.int16).cpu().numpy().view(np.uint16))
                 assert np.allclose(soft, w_soft, rtol=2.0 ** -7, atol=1e-6)
     assert grp.generation == 3

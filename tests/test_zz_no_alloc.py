@@ -3,8 +3,6 @@ workspace entry point plz_lut_linear_bwd_palette it varies, through the C ABI: t
 row, the second with a smaller input (its scratch keeps the first call's contents), bit-equal
 wherever the workspace variant's split count fits the scratch; plus the oracle and the size
 limit."""
-import ctypes as C
-
 import pytest
 import torch
 
@@ -49,7 +47,8 @@ def test_noalloc_matches_workspace_entry_point(dev, shapes):
 def test_noalloc_rejects_weights_beyond_the_scratch(dev):
     from palettize_hip import _lib
     lib = _lib.lib()
-    f = C.c_void_p(4096)  # never dereferenced: the size check comes first
+    # null pointers: the size check fires first; were it ever moved after the null-pointer
+    # check, the call would still return PLZ_EINVAL without launching anything
     N, K = 16384, 16640   # N * K / 8 bytes of partials per split > 32 MiB
-    rc = lib.plz_lut_linear_bwd_palette_noalloc(f, f, f, f, 64, N, K, None)
+    rc = lib.plz_lut_linear_bwd_palette_noalloc(None, None, None, None, 64, N, K, None)
     assert rc == 1 and b"scratch" in lib.plz_last_error()
