@@ -144,10 +144,13 @@ def kernel_rooflines(events):
 
 
 def bench_gemv(device, reps=20):
-    """Config 2: 36 layers x 7 linears per grouped launch, on the decode layouts. GB/s as the
-    metric defines it: (packed indices + fp32 palettes) / time, 1,135,411,200 B per launch;
-    stream_gbs: the bytes the decode layouts actually stream (bf16 lookup words, 8 B per row
-    and 256-k group in place of 16)."""
+    """Config 2: 36 layers x 7 linears per grouped launch. The top-level M1/M4/M16 entries are
+    the library's default (GemvGroup layout "auto": the bit-plane GEMV up to 8 tokens, its
+    x-prep kernel and the GEMV both timed; the dequantising decode-layout kernel above);
+    "planes" and "decode" hold each kernel at every M for comparison. GB/s as the metric
+    defines it: (packed indices + fp32 palettes) / time, 1,135,411,200 B per launch;
+    stream_gbs: the bytes the layouts actually stream (bf16 lookup words, 8 B per row and
+    256-k group in place of 16)."""
     import torch
     from palettize_hip import ops
     g = torch.Generator(device=device).manual_seed(1)
@@ -159,27 +162,31 @@ def bench_gemv(device, reps=20):
             weights.append((packed, pal, K))
             wbytes += packed.numel() * 4 + pal.numel() * 4
             sbytes += packed.numel() * 4 + pal.numel() * 2
-    res = {}
+    res = {"planes": {}, "decode": {}}
     for M in (1, 4, 16):
         items = [(torch.randn(M, K, generator=g, device=device).to(torch.bfloat16), p, pl)
                  for p, pl, K in weights]
-        grp = ops.GemvGroup(items)
-        for _ in range(3):
-            grp.run()
-        torch.cuda.synchronize()
-        s = torch.cuda.Event(enable_timing=True)
-        e = torch.cuda.Event(enable_timing=True)
-        s.record()
-        for _ in range(reps):
-            grp.run()
-        e.record()
-        torch.cuda.synchronize()
-        ms = s.elapsed_time(e) / reps
-        gbs = wbytes / (ms * 1e-3) / 1e9
-        res[f"M{M}"] = dict(us=round(ms * 1e3, 2), gbs=round(gbs, 1),
-                            frac=round(gbs / PEAK_HBM_GBS, 4),
-                            stream_gbs=round(sbytes / (ms * 1e-3) / 1e9, 1))
-        del grp, items
+        for layout in ("planes", "decode"):
+            grp = ops.GemvGroup(items, layout=layout)
+            for _ in range(3):
+                grp.run()
+            torch.cuda.synchronize()
+            s = torch.cuda.Event(enable_timing=True)
+            e = torch.cuda.Event(enable_timing=True)
+            s.record()
+            for _ in range(reps):
+                grp.run()
+            e.record()
+            torch.cuda.synchronize()
+            ms = s.elapsed_time(e) / reps
+            gbs = wbytes / (ms * 1e-3) / 1e9
+            r = dict(us=round(ms * 1e3, 2), gbs=round(gbs, 1), frac=round(gbs / PEAK_HBM_GBS, 4),
+                     stream_gbs=round(sbytes / (ms * 1e-3) / 1e9, 1))
+            res[layout][f"M{M}"] = r
+            if layout == ("planes" if M <= 8 else "decode"):  # what layout "auto" picks
+                res[f"M{M}"] = dict(r, layout=layout)
+            del grp
+        del items
     res["weight_bytes"] = wbytes
     res["stream_bytes"] = sbytes
     return res

@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define PLZ_ABI_VERSION 9
+#define PLZ_ABI_VERSION 10
 
 /* status codes */
 #define PLZ_OK 0
@@ -367,6 +367,35 @@ int64_t plz_gemv_plan(plz_gemv_desc* descs, int n, int M, int layout);
  * `layout` must be the layout the table was planned for. */
 int plz_lut_gemv_grouped(const plz_gemv_desc* descs_device, int n, int64_t total_blocks, int M,
                          int layout, void* stream);
+
+/* Bit-plane decode (layout PLZ_GEMV_PLANES): the GEMV of plz_lut_gemv_decode computed as
+ *   sum_k x_k w_k = p0 X + d1 S(b0) + d2 S(b1) + d3 S(b0 b1)   per row and 256-k group,
+ * with b0, b1 the bits of each 2-bit index, S(f) = sum_k x_k f_k, X = sum_k x_k, d1 = p1 - p0,
+ * d2 = p2 - p0, d3 = p3 - p2 - p1 + p0: the bit planes are FP4 operands of gfx950's scaled
+ * FP8 x FP4 MFMA, cut from the packed words by masks, and x enters as two e4m3 pieces per
+ * element with a power-of-two scale per token and group (x = 2^s (x1 + x2) exactly). Same
+ * outputs as the decode kernel up to fp32 summation order. Replaces, like plz_lut_gemv, the
+ * reference's 64-row-tile forward at M = 1 (fused_lut_kernel.cu:309-518).
+ * Indices: a one-time repack (same size as plz_gemv_packed_items_bytes) in which lane
+ * l = 16g + r of a 16-row block holds four words of its row: nibble i of word j holds the index
+ * of k = 32g + 8j + i (bits 4i, 4i+1) and that of k = 128 + 32g + 8j + i (bits 4i+2, 4i+3).
+ * Palettes: the decode lookup words (plz_gemv_pack_palettes).
+ * The workspace (plz_gemv_planes_workspace) receives the x pieces of every linear and group,
+ * written by a small kernel launched first on the same stream. */
+#define PLZ_GEMV_PLANES 2
+int plz_gemv_pack_planes(const int32_t* packed, int32_t* planes_items, int64_t N, int64_t K,
+                         void* stream);
+/* bytes of workspace for n linears whose largest K is max_K, at M tokens */
+size_t plz_gemv_planes_workspace(int n, int64_t max_K, int M);
+int plz_lut_gemv_planes(const uint16_t* x, const int32_t* planes_items,
+                        const uint32_t* palette_items, uint16_t* y, int64_t M, int64_t N, int64_t K,
+                        void* workspace, size_t workspace_bytes, void* stream);
+/* descs_device: a table planned by plz_gemv_plan(..., PLZ_GEMV_PLANES), whose packed_items
+ * hold plz_gemv_pack_planes layouts; max_K: the largest K in the table (the workspace is laid
+ * out by it). */
+int plz_lut_gemv_grouped_planes(const plz_gemv_desc* descs_device, int n, int64_t total_blocks,
+                                int M, int64_t max_K, void* workspace, size_t workspace_bytes,
+                                void* stream);
 
 /* ---- on-disk format converters ---------------------------------------------------------
  * .idx2 = the (K, N) index matrix (W^T) flattened row-major, 4 indices per byte, LSB first

@@ -168,6 +168,26 @@ def gemv_decode_layout(idx) -> np.ndarray:
     return np.ascontiguousarray(out.transpose(0, 4, 1, 2, 5, 3, 6)).reshape(-1)
 
 
+def gemv_planes_layout(idx) -> np.ndarray:
+    """idx [N, K] (0..3) -> uint32 words [ceil(N/128), K/256, 4 waves, 2 blocks, 64 lanes, 4] of
+    the bit-plane GEMV: lane l = 16g + r of block b of wave w holds item row 32w + 16b + r in
+    four words; nibble i of word j holds the index of stage k = 32g + 8j + i in bits 4i, 4i+1
+    and that of k = 128 + 32g + 8j + i in bits 4i+2, 4i+3. Rows past N are zero."""
+    idx = np.asarray(idx, np.uint32)
+    N, K = idx.shape
+    items = (N + 127) // 128
+    full = np.zeros((items * 128, K), np.uint32)
+    full[:N] = idx
+    # item, w, b, r, stage, half (k < 128 or not), g, j, i
+    v = full.reshape(items, 4, 2, 16, K // 256, 2, 4, 4, 8)
+    out = np.zeros(v.shape[:5] + (4, 4), np.uint32)  # ..., g, j
+    for i in range(8):
+        out |= (v[..., 0, :, :, i] << np.uint32(4 * i)) | (v[..., 1, :, :, i] << np.uint32(4 * i + 2))
+    # item, w, b, r, stage, g, j -> item, stage, w, b, g, r, j
+    out = out.transpose(0, 4, 1, 2, 5, 3, 6)
+    return np.ascontiguousarray(out).reshape(-1)
+
+
 def gemv_palette_luts(palette) -> np.ndarray:
     """palette fp32 [N, G, 4] -> uint32 [ceil(N/128), G, 128, 2]: per row and group the bf16
     (RNE) entries' low bytes (entry c in byte c), then their high bytes; rows past N zero."""

@@ -151,6 +151,7 @@ struct Cursor {
   int kc, nkc;
   plz_gemv_desc d;
   int64_t row0;  // first row of the item
+  int di;        // descriptor index of the item
 };
 template <bool GROUPED>
 __device__ __forceinline__ void cursor_load(Cursor& c, const Table<GROUPED>& tb) {
@@ -159,9 +160,11 @@ __device__ __forceinline__ void cursor_load(Cursor& c, const Table<GROUPED>& tb)
     c.nkc = 1;
     c.d = plz_gemv_desc{};
     c.row0 = 0;
+    c.di = 0;
     return;
   }
   const int di = tb.find_item(c.item);
+  c.di = di;
   c.d = tb.at(di);
   c.row0 = (c.item - c.d.block_begin) * ROWS;
   c.nkc = (int)((c.d.K + KC - 1) / KC);
@@ -437,10 +440,12 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_reg_kernel(const plz_gemv_des
     issue(p, lds + p * XS);
     cursor_next(pc, tb);
   }
-  while (cc.item < cc.end) {  // RD stages per pass, unrolled so that ring slots are constants
+  // RD stages per pass, unrolled so that ring slots are constants. A pass runs whole even when
+  // the range ends inside it (the stages past the end read zeros and store nothing): a break out
+  // of the unrolled body makes the compiler wait for most of the ring at the next pass.
+  while (cc.item < cc.end) {
 #pragma unroll
     for (int u = 0; u < RD; ++u) {
-      if (cc.item >= cc.end) break;
       wait_vmcnt<(RD - 2) * LOADS>();  // this lane's loads of stage s have landed
       lds_barrier();                   // everyone's x copies have; slot (s - 1) % RD is free
       stage(u, (u + RD - 1) % RD, lds + u * XS, lds + ((u + RD - 1) % RD) * XS);
@@ -574,6 +579,446 @@ __global__ void pack_indices_kernel(const uint4* __restrict__ packed, uint4* __r
   out[t] = v;
 }
 
+
+// ---- bit-plane kernel (layout PLZ_GEMV_PLANES) -------------------------------------------
+// A weight with index b = b0 + 2 b1 is w = p0 + d1 b0 + d2 b1 + d3 b0 b1 (d1 = p1 - p0,
+// d2 = p2 - p0, d3 = p3 - p2 - p1 + p0). So per row n and palette group g
+//   sum_k x_k w_k = p0 X + d1 S(b0) + d2 S(b1) + d3 S(b0 b1),   S(f) = sum_k x_k f_k,
+// and the three bit planes go into the B operand of the scaled FP8 x FP4 MFMA
+// (v_mfma_scale_f32_16x16x128_f8f6f4) straight from the packed word: a plane nibble is 0 or one
+// FP4 power of two, cut out of the word by a mask or a 3-input AND -- 7 VALU per 16 weights,
+// where dequantising to bf16 takes 23. X, the group sum of
+// x, comes with the x pieces from the prep kernel. x is the A operand, in two
+// e4m3 pieces per element, x = 2^s (x1 + x2) exactly (4 + 4 significant bits), with an E8M0
+// scale 2^s per token and stage that the MFMA applies: A row m = 2 t + piece, so one 16-row
+// operand holds 8 tokens. At the end of a stage p0 X + d1 S(b0) + d2 S(b1) + d3 S(b0 b1) is
+// folded into the row's fp32 sum (the MFMA's B scales turn every plane into 0/1); the two pieces
+// of a token are added when the item is stored.
+//
+// Operand layouts of the 16x16x128 MFMA (A fp8, B fp4), checked on the device: A lane l holds
+// row l % 16, k = 16 (l/16) + e for bytes e < 16 and k = 64 + 16 (l/16) + e - 16 above; B lane
+// l holds column l % 16, k = 32 (l/16) + e for nibble e; a lane's scale byte covers its row or
+// column over k in [32 (l/16), 32 (l/16) + 32); C lane l holds rows 4 (l/16) + i, column l % 16.
+//
+// Planes layout of the indices (plz_gemv_pack_planes): the decode layout's blocks (8 KB per
+// 128-row item and 256-k stage, 16 B per lane and 16-row block), where lane l = 16 g + nl of
+// block r of wave w holds row 16 (RB w + r) + nl in four words: nibble i of word j holds the
+// index of k = 32 g + 8 j + i in bits 4i, 4i+1 (MFMA half 0) and that of k = 128 + 32 g + 8 j + i
+// in bits 4i+2, 4i+3 (half 1). With t = q >> 1, the planes of a word are then one mask or one
+// 3-input AND each -- half 0: b0 = q & 0x11.. (0.5), b1 = q & 0x22.. (1.0), b0 b1 = q & t &
+// 0x11.. (0.5); half 1: b0 = q & 0x44.. (2.0), b1 = t & 0x44.. (2.0), b0 b1 = q & t & 0x44..
+// (2.0) -- 7 VALU per 16 weights, and the MFMA's B scale brings every plane to 0 / 1.
+__host__ __device__ inline uint32_t plane_word(uint32_t src_a, uint32_t src_b, int off) {
+  uint32_t o = 0;  // src_a / src_b: natural 16-index words holding the two halves' indices
+  for (int i = 0; i < 8; ++i)
+    o |= (((src_a >> (2 * (off + i))) & 3u) << (4 * i)) |
+         (((src_b >> (2 * (off + i))) & 3u) << (4 * i + 2));
+  return o;
+}
+
+// x prep, one chunk per (linear d, stage s) of the workspace at (d * max_stages + s) * chunk:
+// A rows m = 2 t + piece, 256 B each (the fragments of both MFMA halves: 16-byte piece
+// c = 8 h + 2 j + half, holding stage k = 128 h + 64 half + 16 j + (0..15), stored at
+// c ^ (m & 15)); then the tokens' E8M0 scale bytes (16 B), their stage sums X as fp32 (64 B)
+// and 48 B of padding.
+__host__ __device__ constexpr int pl_chunk(int M) { return 512 * M + 128; }
+__host__ __device__ constexpr int pl_nx(int M) {
+  return (pl_chunk(M) + WAVES * 1024 - 1) / (WAVES * 1024);
+}
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+
+// One wave per linear and PREP_STAGES stages: lane 16 g + c makes 16-byte piece c of work
+// item 4 i + g, the items being (token, stage) pairs of the wave's stages.
+constexpr int PREP_STAGES = 4;
+template <bool GROUPED>
+__global__ __launch_bounds__(64) void gemv_pl_prep_kernel(const plz_gemv_desc* __restrict__ descs,
+                                                          int n_desc, plz_gemv_desc single,
+                                                          int M, int max_stages,
+                                                          uint8_t* __restrict__ ws) {
+  const int blocks_per_desc = (max_stages + PREP_STAGES - 1) / PREP_STAGES;
+  const int d = blockIdx.x / blocks_per_desc;
+  const int s0 = (blockIdx.x % blocks_per_desc) * PREP_STAGES;
+  const Table<GROUPED> tb{descs, n_desc, single};
+  const plz_gemv_desc dd = tb.at(d);
+  const int stages = (int)(dd.K / KC);
+  if (s0 >= stages || dd.N == 0) return;  // uniform per block
+  const int ns = stages - s0 < PREP_STAGES ? stages - s0 : PREP_STAGES;
+  const int lane = threadIdx.x, c = lane & 15, g = lane >> 4;
+  const int k0 = 128 * (c >> 3) + 64 * (c & 1) + 16 * ((c >> 1) & 3);
+  for (int w0 = 0; w0 < M * ns; w0 += 4) {
+    const int w = w0 + g, t = w % M, s = s0 + w / M;
+    const bool live = w < M * ns;
+    uint32_t b[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (live) {
+      const uint4* src = reinterpret_cast<const uint4*>(dd.x + (int64_t)t * dd.K + (int64_t)s * KC + k0);
+      const uint4 v0 = src[0], v1 = src[1];
+      b[0] = v0.x; b[1] = v0.y; b[2] = v0.z; b[3] = v0.w;
+      b[4] = v1.x; b[5] = v1.y; b[6] = v1.z; b[7] = v1.w;
+    }
+    float v[16];
+    int emax = 0;
+    float sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const uint32_t h = (b[i / 2] >> (16 * (i & 1))) & 0xffffu;
+      v[i] = bf2f(h);
+      const int e = (int)((h >> 7) & 0xffu);
+      emax = e != 0xff && e > emax ? e : emax;  // the finite values set the scale
+      sum += v[i];
+    }
+#pragma unroll
+    for (int off = 8; off >= 1; off >>= 1) {  // over the 16 lanes of the item, fixed order
+      const int oe = __shfl_xor(emax, off);
+      emax = oe > emax ? oe : emax;
+      sum += __shfl_xor(sum, off);
+    }
+    if (!live) continue;
+    uint8_t* ch = ws + ((int64_t)d * max_stages + s) * pl_chunk(M);
+    // scale 2^s = 2^(E - 7), E the unbiased exponent of the stage's largest finite |x| plus
+    // one: |x| / 2^s < 256, well inside e4m3's 448; e8 = s + 127
+    const int e8 = emax >= 7 ? emax - 7 : 0;
+    const float inv = __builtin_bit_cast(float, (uint32_t)(254 - e8) << 23);  // 2^-s
+    uint32_t w1[4] = {0, 0, 0, 0}, w2[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const float xs = v[i] * inv;
+      uint32_t p1 = 0x7fu, p2 = 0x7fu;  // NaN and +-inf: e4m3 NaN, the token's outputs go NaN
+      if (__builtin_isfinite(xs)) {
+        const int q1 = __builtin_amdgcn_cvt_pk_fp8_f32(xs, 0.f, 0, false);
+        const float r = xs - __builtin_amdgcn_cvt_f32_fp8(q1, 0);  // exact
+        p1 = (uint32_t)q1 & 0xffu;
+        p2 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(r, 0.f, 0, false) & 0xffu;
+      }
+      w1[i / 4] |= p1 << (8 * (i & 3));
+      w2[i / 4] |= p2 << (8 * (i & 3));
+    }
+    const int m0 = 2 * t, m1 = 2 * t + 1;
+    *reinterpret_cast<uint4*>(ch + m0 * 256 + ((c ^ (m0 & 15)) << 4)) =
+        make_uint4(w1[0], w1[1], w1[2], w1[3]);
+    *reinterpret_cast<uint4*>(ch + m1 * 256 + ((c ^ (m1 & 15)) << 4)) =
+        make_uint4(w2[0], w2[1], w2[2], w2[3]);
+    if (c == 0) {
+      ch[512 * M + t] = (uint8_t)e8;
+      reinterpret_cast<float*>(ch + 512 * M + 16)[t] = sum;
+    }
+  }
+}
+
+// NX: 1 KB x-chunk copies per wave and stage (pl_nx(M)); NSET: 16-row A operands (8 tokens
+// each); NI: C rows per lane that can hold a token's piece (2 at M = 1).
+//
+// Outputs are staged in LDS (YBYTES per workgroup) and written when the staging is full or at
+// the end: a global store pending beside the register ring's loads would make the compiler
+// drain the ring (s_waitcnt vmcnt(0)) at the next wait, since it cannot order stores against
+// loads on the one counter.
+constexpr int YBYTES = 16384;
+#ifndef PLZ_GV_RDP
+#define PLZ_GV_RDP 5
+#endif
+constexpr int RDP = PLZ_GV_RDP;  // register-ring depth (stages) of the bit-plane kernel
+template <int NX, int NSET, int NI, bool GROUPED>
+__global__ __launch_bounds__(64 * WAVES) void gemv_pl_kernel(const plz_gemv_desc* __restrict__ descs,
+                                                             int n_desc, plz_gemv_desc single,
+                                                             int M, int max_stages,
+                                                             const uint8_t* __restrict__ ws,
+                                                             uint32_t ws_bytes) {
+  extern __shared__ uint4 smem[];
+  lds_u8* lds = (lds_u8*)smem;
+  constexpr int XS = NX * WAVES * 1024;
+  constexpr int LOADS = 2 * RB + NX;  // vector-memory operations per lane and stage
+  typedef __attribute__((address_space(3))) uint16_t lds_u16;
+  typedef __attribute__((address_space(3))) int64_t lds_i64;
+  lds_u16* ybuf = (lds_u16*)(lds + RDP * XS);                 // [ycap][M][ROWS] bf16
+  lds_i64* yitem = (lds_i64*)(lds + RDP * XS + YBYTES);       // [ycap] item of each slot
+  const int ycap = YBYTES / (ROWS * M * 2);
+  const Table<GROUPED> tb{descs, n_desc, single};
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+  const int nl = lane & 15, q = lane >> 4;
+  const uint32_t CH = (uint32_t)pl_chunk(M);
+
+  const int64_t T = tb.total_cost(), G = gridDim.x, wid = blockIdx.x;
+  Cursor pc, cc;
+  pc.item = cc.item = tb.item_at_cost(wid * T / G);
+  pc.end = cc.end = tb.item_at_cost((wid + 1) * T / G);
+  cursor_load(pc, tb);
+  cursor_load(cc, tb);
+
+  BufRsrc rq = make_rsrc(nullptr, 0), rp = rq;
+  const BufRsrc rx = make_rsrc(ws, ws_bytes);
+  uint32_t qbase = 0, pbase = 0, xbase = 0;
+  int64_t p_item = -1;
+  const uint32_t wlane = (uint32_t)(wave * W_WAVE + lane * 16);  // words of this lane
+  const uint32_t plane = (uint32_t)((16 * RB * wave + nl) * 8);  // lookup words of its row
+  uint4 wr[RDP][RB];  // words, [ring slot][row block]
+  uint2 lr[RDP][RB];  // lookup words {lo, hi}
+  auto issue = [&](int slot, lds_u8* __restrict__ xdst) {
+    const bool live = pc.item < pc.end;
+    const int64_t N = pc.d.N, K = pc.d.K;
+    if (pc.item != p_item) {
+      p_item = pc.item;
+      const int64_t rows = (N + ROWS - 1) / ROWS * ROWS;
+      rq = make_rsrc(pc.d.packed_items, live && pc.d.packed_items ? (uint32_t)(rows * (K / 4)) : 0u);
+      rp = make_rsrc(pc.d.palette_items,
+                     live && pc.d.palette_items ? (uint32_t)(rows * (K / kPalGroup) * 8) : 0u);
+      qbase = (uint32_t)pc.row0 * (uint32_t)(K / 4);
+      pbase = (uint32_t)pc.row0 * (uint32_t)(K / kPalGroup) * 8u;
+      xbase = live ? (uint32_t)pc.di * (uint32_t)max_stages * CH : kBufOob;
+    }
+    const uint32_t kc = (uint32_t)pc.kc;
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+      const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(
+          rq, (int)wlane, (int)(qbase + kc * (uint32_t)W_BYTES + (uint32_t)r * 1024u), 0);
+      wr[slot][r] = make_uint4(v.x, v.y, v.z, v.w);
+    }
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+      const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(
+          rp, (int)plane, (int)(pbase + kc * (uint32_t)(ROWS * 8) + (uint32_t)r * 128u), 0);
+      lr[slot][r] = make_uint2(v.x, v.y);
+    }
+#pragma unroll
+    for (int j = 0; j < NX; ++j) {
+      const uint32_t g = (uint32_t)(WAVES * j + wave);
+      dma16(rx, xbase == kBufOob ? kBufOob : xbase + kc * CH + g * 1024u + (uint32_t)lane * 16u,
+            xdst + g * 1024);
+    }
+  };
+
+  const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+  f32x4 yacc[RB][NSET];
+#pragma unroll
+  for (int r = 0; r < RB; ++r)
+#pragma unroll
+    for (int S = 0; S < NSET; ++S) yacc[r][S] = zero;
+  // E8M0 scales 1.0, 2.0 and 0.5 (every plane bit of half 1 sits at nibble bit 2, value 2.0)
+  constexpr int kScale1 = 127, kScale2 = 128, kScaleH = 126;
+  constexpr uint32_t M1 = 0x11111111u, M2 = 0x22222222u, M4 = 0x44444444u;
+
+  // One stage: the loads of stage s + RDP - 1 (registers of slot sw, x chunk into xw), then the
+  // MFMAs of stage s (registers of slot u, x chunk from xr).
+  auto stage = [&](int u, int sw, const lds_u8* __restrict__ xr, lds_u8* __restrict__ xw) {
+    issue(sw, xw);
+    cursor_next(pc, tb);
+    i32x8 a[NSET][2];
+    int sc[NSET];
+    float xsum[NSET][NI / 2];  // X of the tokens whose first piece this lane's C rows hold
+#pragma unroll
+    for (int S = 0; S < NSET; ++S) {
+      const int mr = 16 * S + nl, m = mr < 2 * M ? mr : 2 * M - 1;  // rows past 2M repeat one
+      const lds_u8* row = xr + m * 256;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int c0 = 8 * h + 2 * q;
+        const u32x4 lo = *(const lds_u32x4*)(row + ((c0 ^ (m & 15)) << 4));
+        const u32x4 hi = *(const lds_u32x4*)(row + (((c0 + 1) ^ (m & 15)) << 4));
+        a[S][h] = i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3],
+                        (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+      }
+      sc[S] = (int)xr[512 * M + (m >> 1)];
+#pragma unroll
+      for (int i = 0; i < NI; i += 2)  // token of C row 16 S + 4 q + i (a stale value past M)
+        xsum[S][i / 2] = *(const __attribute__((address_space(3))) float*)(
+            xr + 512 * M + 16 + 4 * (8 * S + 2 * q + i / 2));
+    }
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+      // the row's palette entries as fp32 (bf16 bits: high byte from hi, low byte from lo)
+      const uint32_t lo = lr[u][r].x, hi = lr[u][r].y;
+      const float p0 = __uint_as_float(perm(hi, lo, 0x04000c0cu));
+      const float p1 = __uint_as_float(perm(hi, lo, 0x05010c0cu));
+      const float p2 = __uint_as_float(perm(hi, lo, 0x06020c0cu));
+      const float p3 = __uint_as_float(perm(hi, lo, 0x07030c0cu));
+      const float c1 = p1 - p0, c2 = p2 - p0, c3 = (p3 - p2) - c1;
+      const uint4 wv = wr[u][r];
+      const uint32_t wq[4] = {wv.x, wv.y, wv.z, wv.w};
+      f32x4 cb0[NSET], cb1[NSET], cb3[NSET];
+      uint32_t t[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) t[j] = wq[j] >> 1;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const uint32_t m0 = h ? M4 : M1, m1 = h ? M4 : M2;  // b0 (and b0 b1), b1 masks
+        i32x8 B0 = {0, 0, 0, 0, 0, 0, 0, 0}, B1 = B0, B3 = B0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          B0[j] = (int)(wq[j] & m0);
+          B1[j] = (int)((h ? t[j] : wq[j]) & m1);
+          B3[j] = (int)(wq[j] & t[j] & m0);
+        }
+        // B scales that make every plane 0 / 1: half 0 planes are 0.5 / 1.0 / 0.5, half 1 2.0
+        const int s0 = h ? kScaleH : kScale2, s1 = h ? kScaleH : kScale1, s3 = h ? kScaleH : kScale2;
+#pragma unroll
+        for (int S = 0; S < NSET; ++S) {
+          cb0[S] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a[S][h], B0, h ? cb0[S] : zero,
+                                                                    0, 4, 0, sc[S], 0, s0);
+          cb1[S] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a[S][h], B1, h ? cb1[S] : zero,
+                                                                    0, 4, 0, sc[S], 0, s1);
+          cb3[S] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a[S][h], B3, h ? cb3[S] : zero,
+                                                                    0, 4, 0, sc[S], 0, s3);
+        }
+      }
+#pragma unroll
+      for (int S = 0; S < NSET; ++S)
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+          float y = __builtin_fmaf(c1, cb0[S][i], __builtin_fmaf(c2, cb1[S][i],
+                                   __builtin_fmaf(c3, cb3[S][i], yacc[r][S][i])));
+          if ((i & 1) == 0) y = __builtin_fmaf(p0, xsum[S][i / 2], y);  // first piece only
+          yacc[r][S][i] = y;
+        }
+    }
+  };
+
+  // the staged outputs of slots [0, cnt) to y (after a barrier; all waves take part)
+  auto flush = [&](int cnt) {
+    for (int it = 0; it < cnt; ++it) {
+      const int64_t iv = yitem[it];  // the same in every lane: make it scalar
+      const int64_t item = (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(iv >> 32)) << 32) |
+                                     (uint32_t)__builtin_amdgcn_readfirstlane((int)iv));
+      const plz_gemv_desc d = tb.at(tb.find_item(item));
+      const int64_t row0 = (item - d.block_begin) * ROWS;
+      for (int t = wave; t < M; t += WAVES)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int nloc = 2 * lane + h;
+          if (row0 + nloc < d.N)
+            ((__attribute__((address_space(1))) uint16_t*)d.y)[(int64_t)t * d.N + row0 + nloc] =
+                ybuf[(it * M + t) * ROWS + nloc];  // a global store (a flat one would also count
+                                                  // on lgkmcnt)
+        }
+    }
+  };
+
+#pragma unroll
+  for (int p = 0; p < RDP - 1; ++p) {
+    issue(p, lds + p * XS);
+    cursor_next(pc, tb);
+  }
+  int ycount = 0;
+  // RDP stages per pass, unrolled so that ring slots are constants. A pass runs whole even when
+  // the range ends inside it (the stages past the end read zeros and store nothing): a break out
+  // of the unrolled body makes the compiler wait for most of the ring at the next pass.
+  while (cc.item < cc.end) {
+#pragma unroll
+    for (int u = 0; u < RDP; ++u) {
+      wait_vmcnt<(RDP - 2) * LOADS>();  // this lane's loads of stage s have landed
+      lds_barrier();                   // everyone's x copies have; slot (s - 1) % RDP is free
+      stage(u, (u + RDP - 1) % RDP, lds + u * XS, lds + ((u + RDP - 1) % RDP) * XS);
+      if (++cc.kc == cc.nkc) {  // item done: C row 16 S + 4 q + i of lane l = piece i & 1 of
+                                // token 8 S + 2 q + i / 2, item row 16 (RB w + r) + nl
+        if (cc.item < cc.end) {  // a live item (the last pass may run past the range)
+#pragma unroll
+          for (int r = 0; r < RB; ++r) {
+            const int nloc = 16 * RB * wave + 16 * r + nl;
+#pragma unroll
+            for (int S = 0; S < NSET; ++S)
+#pragma unroll
+              for (int i = 0; i < NI; i += 2) {
+                const int t = 8 * S + 2 * q + i / 2;
+                if (t < M)
+                  ybuf[(ycount * M + t) * ROWS + nloc] =
+                      (uint16_t)f2bf(yacc[r][S][i] + yacc[r][S][i + 1]);
+              }
+          }
+          if (threadIdx.x == 0) yitem[ycount] = cc.item;
+          if (++ycount == ycap) {  // the same count in every wave: waves walk the same stages
+            __syncthreads();
+            flush(ycount);
+            __syncthreads();
+            ycount = 0;
+          }
+        }
+#pragma unroll
+        for (int r = 0; r < RB; ++r)
+#pragma unroll
+          for (int S = 0; S < NSET; ++S) yacc[r][S] = zero;
+        ++cc.item;
+        cursor_load(cc, tb);
+      }
+    }
+  }
+  __syncthreads();
+  flush(ycount);
+  __builtin_amdgcn_s_waitcnt(0);  // drain the trailing (empty) loads before the wave ends
+}
+
+// packed [N, K/16] -> planes layout: the decode layout's chunk order (one 16-byte chunk per
+// thread: lane l = 16 g + nl of block i of wave w, row 16 RB w + 16 i + nl), word j pairing
+// k = 32 g + 8 j + (0..7) with 128 + 32 g + 8 j + (0..7) of the stage through plane_word.
+__global__ void pack_planes_kernel(const uint32_t* __restrict__ packed, uint4* __restrict__ out,
+                                   int64_t N, int64_t K) {
+  constexpr int CHK = W_BYTES / 16;  // chunks per stage
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t stages = K / KC, items = (N + ROWS - 1) / ROWS;
+  if (t >= items * stages * CHK) return;
+  const int c = (int)(t % CHK);
+  const int64_t st = (t / CHK) % stages, item = t / (CHK * stages);
+  const int w = c / (W_WAVE / 16), i = (c / 64) % RB, l = c & 63;
+  const int64_t n = item * ROWS + 16 * RB * w + 16 * i + (l & 15);
+  uint4 v = make_uint4(0u, 0u, 0u, 0u);
+  if (n < N) {
+    const uint32_t* src = packed + n * (K / 16) + st * (KC / 16);
+    const int g = l >> 4;
+    uint32_t w[4];
+    for (int j = 0; j < 4; ++j)  // k = 32 g + 8 j lies in source word 2 g + j / 2
+      w[j] = plane_word(src[2 * g + j / 2], src[8 + 2 * g + j / 2], 8 * (j & 1));
+    v = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+  out[t] = v;
+}
+
+template <int NX, int NSET, int NI, bool GROUPED>
+static int launch_pl_nx(int64_t items, hipStream_t st, const plz_gemv_desc* descs, int n,
+                        plz_gemv_desc single, int M, int max_stages, uint8_t* ws,
+                        size_t ws_bytes, const char* what) {
+  hipLaunchKernelGGL(gemv_pl_prep_kernel<GROUPED>,
+                     dim3((unsigned)(n * ((max_stages + PREP_STAGES - 1) / PREP_STAGES))), dim3(64), 0,
+                     st, descs, n, single, M, max_stages, ws);
+  auto kern = gemv_pl_kernel<NX, NSET, NI, GROUPED>;
+  const size_t lds = (size_t)RDP * NX * WAVES * 1024 + YBYTES + (YBYTES / (ROWS * 2)) * 8;
+  static uint64_t lds_done = 0;
+  if (int rc = reserve_lds((const void*)kern, lds, lds_done, what)) return rc;
+  static int per_cu[64] = {0};  // resident workgroups per CU, per device
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  if (per_cu[dev] == 0) {
+    int v = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, (const void*)kern, 64 * WAVES, lds) !=
+            hipSuccess ||
+        v < 1)
+      v = 1;
+    per_cu[dev] = v;
+  }
+  const int64_t slots = per_cu[dev] * (int64_t)cu_count();
+  const int64_t g = items < slots ? items : slots;
+  hipLaunchKernelGGL(kern, dim3((unsigned)g), dim3(64 * WAVES), lds, st, descs, n, single, M,
+                     max_stages, (const uint8_t*)ws, (uint32_t)ws_bytes);
+  return check_launch(what);
+}
+template <bool GROUPED>
+static int launch_pl(int64_t items, hipStream_t st, const plz_gemv_desc* descs, int n,
+                     plz_gemv_desc single, int M, int max_stages, uint8_t* ws, size_t ws_bytes,
+                     const char* what) {
+  if (M == 1)
+    return launch_pl_nx<pl_nx(1), 1, 2, GROUPED>(items, st, descs, n, single, M, max_stages, ws,
+                                                 ws_bytes, what);
+  if (M <= 7)
+    return launch_pl_nx<pl_nx(7), 1, 4, GROUPED>(items, st, descs, n, single, M, max_stages, ws,
+                                                 ws_bytes, what);
+  if (M == 8)
+    return launch_pl_nx<pl_nx(8), 1, 4, GROUPED>(items, st, descs, n, single, M, max_stages, ws,
+                                                 ws_bytes, what);
+  if (M <= 15)
+    return launch_pl_nx<pl_nx(15), 2, 4, GROUPED>(items, st, descs, n, single, M, max_stages, ws,
+                                                  ws_bytes, what);
+  return launch_pl_nx<pl_nx(16), 2, 4, GROUPED>(items, st, descs, n, single, M, max_stages, ws,
+                                                ws_bytes, what);
+}
+static_assert(pl_nx(1) == 1 && pl_nx(7) == 1 && pl_nx(8) == 2 && pl_nx(15) == 2 && pl_nx(16) == 3,
+              "x chunk copies per wave");
+
 static int check_desc(const plz_gemv_desc& d, int i) {
   PLZ_REQUIRE(d.N >= 0 && d.K >= 0, "plz_gemv: descriptor %d has a negative shape", i);
   PLZ_REQUIRE(d.K % 256 == 0, "plz_gemv: descriptor %d: K (%lld) must be a multiple of 256", i,
@@ -680,7 +1125,7 @@ int64_t plz_gemv_plan(plz_gemv_desc* descs, int n, int M, int layout) {
     set_error("plz_gemv_plan: need n >= 0, non-null descriptors and M in [1, 16]");
     return -PLZ_EINVAL;
   }
-  if (layout != PLZ_GEMV_NATIVE && layout != PLZ_GEMV_DECODE) {
+  if (layout != PLZ_GEMV_NATIVE && layout != PLZ_GEMV_DECODE && layout != PLZ_GEMV_PLANES) {
     set_error("plz_gemv_plan: unknown index layout %d", layout);
     return -PLZ_EINVAL;
   }
@@ -699,10 +1144,10 @@ int64_t plz_gemv_plan(plz_gemv_desc* descs, int n, int M, int layout) {
                 "layout)", i);
       return -PLZ_EINVAL;
     }
-    if (nonempty && layout == PLZ_GEMV_DECODE &&
+    if (nonempty && layout != PLZ_GEMV_NATIVE &&
         (!descs[i].packed_items || !descs[i].palette_items)) {
       set_error("plz_gemv_plan: descriptor %d has a null packed_items or palette_items array "
-                "(decode layout)", i);
+                "(%s layout)", i, layout == PLZ_GEMV_DECODE ? "decode" : "planes");
       return -PLZ_EINVAL;
     }
     descs[i].block_begin = items;
@@ -717,6 +1162,9 @@ int64_t plz_gemv_plan(plz_gemv_desc* descs, int n, int M, int layout) {
 int plz_lut_gemv_grouped(const plz_gemv_desc* descs_device, int n, int64_t total_blocks, int M,
                          int layout, void* stream) {
   PLZ_REQUIRE(M >= 1 && M <= 16, "plz_lut_gemv_grouped: M (%d) must be in [1, 16]", M);
+  PLZ_REQUIRE(layout != PLZ_GEMV_PLANES,
+              "plz_lut_gemv_grouped: the planes layout runs through plz_lut_gemv_grouped_planes "
+              "(it needs a workspace)");
   PLZ_REQUIRE(layout == PLZ_GEMV_NATIVE || layout == PLZ_GEMV_DECODE,
               "plz_lut_gemv_grouped: unknown index layout %d", layout);
   PLZ_REQUIRE(n >= 0 && total_blocks >= 0, "plz_lut_gemv_grouped: negative count");
@@ -725,6 +1173,75 @@ int plz_lut_gemv_grouped(const plz_gemv_desc* descs_device, int n, int64_t total
   plz_gemv_desc dummy = {};
   return launch<true>(total_blocks, (hipStream_t)stream, descs_device, n, dummy, M,
                       layout == PLZ_GEMV_DECODE, "plz_lut_gemv_grouped");
+}
+
+int plz_gemv_pack_planes(const int32_t* packed, int32_t* planes_items, int64_t N, int64_t K,
+                         void* stream) {
+  PLZ_REQUIRE(N >= 0 && K >= 0 && K % KC == 0,
+              "plz_gemv_pack_planes: need N, K >= 0 and K a multiple of 256");
+  if (N == 0 || K == 0) return PLZ_OK;
+  PLZ_REQUIRE(packed && planes_items && (((uintptr_t)packed | (uintptr_t)planes_items) & 15) == 0,
+              "plz_gemv_pack_planes: packed and planes_items must be non-null, 16-byte aligned");
+  const int64_t total = (N + ROWS - 1) / ROWS * (K / KC) * (W_BYTES / 16);
+  hipLaunchKernelGGL(pack_planes_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, reinterpret_cast<const uint32_t*>(packed),
+                     reinterpret_cast<uint4*>(planes_items), N, K);
+  return check_launch("plz_gemv_pack_planes");
+}
+
+size_t plz_gemv_planes_workspace(int n, int64_t max_K, int M) {
+  if (n <= 0 || max_K <= 0 || M < 1 || M > 16) return 0;
+  return (size_t)n * (size_t)((max_K + KC - 1) / KC) * (size_t)pl_chunk(M);
+}
+
+static int planes_ws_check(int n, int64_t max_K, int M, void* workspace, size_t workspace_bytes,
+                           const char* what) {
+  const size_t need = plz_gemv_planes_workspace(n, max_K, M);
+  PLZ_REQUIRE(need < (size_t)kBufOob, "%s: workspace of %zu bytes is above 2 GiB", what, need);
+  if (!workspace || ((uintptr_t)workspace & 15) || workspace_bytes < need) {
+    set_error("%s: workspace of %zu bytes (16-byte aligned) needed, %zu given", what, need,
+              workspace_bytes);
+    return PLZ_EWORKSPACE;
+  }
+  return PLZ_OK;
+}
+
+int plz_lut_gemv_planes(const uint16_t* x, const int32_t* planes_items,
+                        const uint32_t* palette_items, uint16_t* y, int64_t M, int64_t N, int64_t K,
+                        void* workspace, size_t workspace_bytes, void* stream) {
+  const char* what = "plz_lut_gemv_planes";
+  PLZ_REQUIRE(M >= 1 && M <= 16, "%s: M (%lld) must be in [1, 16]", what, (long long)M);
+  PLZ_REQUIRE(N == 0 || K == 0 || (planes_items && palette_items), "%s: null pointer", what);
+  plz_gemv_desc d = {x, nullptr, nullptr, y, N, K, 0, 0, palette_items, planes_items};
+  int rc = check_desc(d, 0);
+  if (rc) return rc;
+  if (N == 0) return PLZ_OK;
+  if (K == 0) {
+    zero_async(y, (size_t)M * N * 2, (hipStream_t)stream);
+    return check_launch(what);
+  }
+  if ((rc = planes_ws_check(1, K, (int)M, workspace, workspace_bytes, what))) return rc;
+  const int64_t items = (N + ROWS - 1) / ROWS;
+  return launch_pl<false>(items, (hipStream_t)stream, nullptr, 1, d, (int)M, (int)(K / KC),
+                          static_cast<uint8_t*>(workspace), workspace_bytes, what);
+}
+
+int plz_lut_gemv_grouped_planes(const plz_gemv_desc* descs_device, int n, int64_t total_blocks,
+                                int M, int64_t max_K, void* workspace, size_t workspace_bytes,
+                                void* stream) {
+  const char* what = "plz_lut_gemv_grouped_planes";
+  PLZ_REQUIRE(M >= 1 && M <= 16, "%s: M (%d) must be in [1, 16]", what, M);
+  PLZ_REQUIRE(n >= 0 && total_blocks >= 0 && max_K >= 0, "%s: negative count", what);
+  PLZ_REQUIRE(max_K % KC == 0, "%s: max_K (%lld) must be a multiple of 256", what,
+              (long long)max_K);
+  if (n == 0 || total_blocks == 0) return PLZ_OK;
+  PLZ_REQUIRE(descs_device, "%s: null descriptor table", what);
+  PLZ_REQUIRE(max_K > 0, "%s: max_K must be the largest K of the table", what);
+  if (int rc = planes_ws_check(n, max_K, M, workspace, workspace_bytes, what)) return rc;
+  plz_gemv_desc dummy = {};
+  return launch_pl<true>(total_blocks, (hipStream_t)stream, descs_device, n, dummy, M,
+                         (int)(max_K / KC), static_cast<uint8_t*>(workspace), workspace_bytes,
+                         what);
 }
 
 }  // extern "C"

@@ -15,7 +15,7 @@ LIB_PATH = os.path.join(HERE, "libpalettize_hip.so")
 PLZ_OK, PLZ_EINVAL, PLZ_EHIP, PLZ_EUNSUPPORTED, PLZ_EWORKSPACE = 0, 1, 2, 3, 4
 PLZ_DT_BF16, PLZ_DT_FP16, PLZ_DT_FP32 = 0, 1, 2
 PLZ_W_SOFT, PLZ_W_HARD_NOISY, PLZ_W_HARD_PLAIN = 0, 1, 2
-PLZ_GEMV_NATIVE, PLZ_GEMV_DECODE = 0, 1
+PLZ_GEMV_NATIVE, PLZ_GEMV_DECODE, PLZ_GEMV_PLANES = 0, 1, 2
 
 p = C.c_void_p
 i32, i64, u32, u64, f32, sz = C.c_int, C.c_int64, C.c_uint32, C.c_uint64, C.c_float, C.c_size_t
@@ -103,6 +103,10 @@ SIGNATURES: dict[str, tuple] = {
     "plz_lut_gemv_decode": (i32, [p, p, p, p, i64, i64, i64, p]),
     "plz_gemv_plan": (i64, [C.POINTER(GemvDesc), i32, i32, i32]),
     "plz_lut_gemv_grouped": (i32, [p, i32, i64, i32, i32, p]),
+    "plz_gemv_pack_planes": (i32, [p, p, i64, i64, p]),
+    "plz_gemv_planes_workspace": (sz, [i32, i64, i32]),
+    "plz_lut_gemv_planes": (i32, [p, p, p, p, i64, i64, i64, p, sz, p]),
+    "plz_lut_gemv_grouped_planes": (i32, [p, i32, i64, i32, i64, p, sz, p]),
     "plz_idx2_to_packed": (i32, [p, p, i64, i64, p]),
     "plz_packed_to_idx2": (i32, [p, p, i64, i64, p]),
     "plz_logits_argmax_idx2": (i32, [p, i32, p, i64, i64, p]),

@@ -598,6 +598,34 @@ def gemv_pack_indices(packed):
     return out
 
 
+def gemv_pack_planes(packed):
+    """One-time planes layout of packed indices [N, K/16] (plz_gemv_pack_planes) for the
+    bit-plane GEMV: the decode layout's 8 KB blocks per 128-row item and 256-k stage, each
+    lane's words those of k = 128h + 32j .. +31 (h = 0, 1), a word's nibble i holding the
+    indices of k0 + i and k0 + 8 + i. Returned as a flat int32 tensor."""
+    _need(packed, "packed", torch.int32, 2)
+    N, K = packed.shape[0], packed.shape[1] * 16
+    nbytes = query("plz_gemv_packed_items_bytes", N, K)
+    out = torch.empty(max(nbytes // 4, 4), dtype=torch.int32, device=packed.device)
+    call("plz_gemv_pack_planes", _ptr(packed), _ptr(out), N, K, _stream(packed))
+    return out
+
+
+def lut_gemv_planes(x, planes_items, palette_items, N):
+    """lut_gemv on weights in the planes layout (gemv_pack_planes, gemv_pack_palettes): the
+    bit-plane FP8 x FP4 MFMA GEMV, with its x pieces in a workspace allocated here."""
+    _need(x, "x", torch.bfloat16, 2)
+    M, K = x.shape
+    if planes_items.numel() * 4 < query("plz_gemv_packed_items_bytes", N, K) or \
+            palette_items.numel() * 4 < query("plz_gemv_palette_items_bytes", N, K):
+        raise ValueError("planes-layout weights smaller than N x K needs")
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
+    ws = _opt_workspace(query("plz_gemv_planes_workspace", 1, K, M), x.device)
+    call("plz_lut_gemv_planes", _ptr(x), _ptr(planes_items), _ptr(palette_items), _ptr(y), M, N,
+         K, _ptr(ws), _numel(ws), _stream(x))
+    return y
+
+
 def lut_gemv_decode(x, packed_items, palette_items, N):
     """lut_gemv on weights in the decode layouts (gemv_pack_indices, gemv_pack_palettes)."""
     _need(x, "x", torch.bfloat16, 2)
@@ -615,15 +643,29 @@ class GemvGroup:
     """A fixed set of independent GEMVs (same M) run by one grouped launch.
 
     ``items`` is a list of (x [M,K] bf16, packed, palette); outputs are allocated once and
-    reused by every ``run()``. The descriptor table lives in device memory. With
-    ``prepack=True`` (default) the indices and palettes are repacked once into the decode
-    layouts (plz_gemv_pack_indices, plz_gemv_pack_palettes), which the kernel streams
-    contiguously.
+    reused by every ``run()``. The descriptor table lives in device memory. ``layout``:
+    "auto" (default: "planes" up to 8 tokens, where one FP8 operand holds every token's two x
+    pieces, "decode" above), "decode" (indices and palettes repacked once into the decode
+    layouts, plz_gemv_pack_indices / plz_gemv_pack_palettes, streamed contiguously and
+    dequantised to bf16), "planes" (the bit-plane MFMA GEMV on plz_gemv_pack_planes indices, with
+    a workspace for the x pieces) or "native" (the packed indices and fp32 palettes as given).
+    ``prepack=False`` is "native".
     """
 
-    def __init__(self, items, prepack=True):
+    LAYOUTS = {"native": _lib.PLZ_GEMV_NATIVE, "decode": _lib.PLZ_GEMV_DECODE,
+               "planes": _lib.PLZ_GEMV_PLANES}
+
+    def __init__(self, items, prepack=True, layout=None):
         if not items:
             raise ValueError("empty GEMV group")
+        self.M = items[0][0].shape[0]
+        if layout is None:
+            layout = "auto" if prepack else "native"
+        if layout == "auto":
+            layout = "planes" if self.M <= 8 else "decode"
+        if layout not in self.LAYOUTS:
+            raise ValueError(f"layout must be one of {sorted(self.LAYOUTS)}")
+        prepack = layout != "native"
         self.M = items[0][0].shape[0]
         self.device = items[0][0].device
         self.outputs = []
@@ -638,7 +680,8 @@ class GemvGroup:
             y = torch.empty((self.M, N), dtype=torch.bfloat16, device=self.device)
             self.outputs.append(y)
             pre = gemv_pack_palettes(palette) if prepack and N > 0 and K > 0 else None
-            pri = gemv_pack_indices(packed) if prepack and N > 0 and K > 0 else None
+            pack_i = gemv_pack_planes if layout == "planes" else gemv_pack_indices
+            pri = pack_i(packed) if prepack and N > 0 and K > 0 else None
             self._packed_palettes.append(pre)
             self._packed_indices.append(pri)
             descs[i] = _lib.GemvDesc(x.data_ptr(), packed.data_ptr(), palette.data_ptr(),
@@ -646,7 +689,12 @@ class GemvGroup:
                                      pre.data_ptr() if pre is not None else None,
                                      pri.data_ptr() if pri is not None else None)
         self._keep = items
-        self.layout = _lib.PLZ_GEMV_DECODE if prepack else _lib.PLZ_GEMV_NATIVE
+        self.layout = self.LAYOUTS[layout]
+        self.max_K = max(int(it[1].shape[1]) * 16 for it in items)
+        self.workspace = None
+        if layout == "planes":
+            self.workspace = _opt_workspace(
+                query("plz_gemv_planes_workspace", len(items), self.max_K, self.M), self.device)
         total = _lib.lib().plz_gemv_plan(descs, len(items), self.M, self.layout)
         if total < 0:
             raise _lib.PalettizeError(
@@ -658,8 +706,13 @@ class GemvGroup:
         self.n = len(items)
 
     def run(self):
-        call("plz_lut_gemv_grouped", self.table.data_ptr(), self.n, self.total_blocks, self.M,
-             self.layout, torch.cuda.current_stream(self.device).cuda_stream)
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        if self.layout == _lib.PLZ_GEMV_PLANES:
+            call("plz_lut_gemv_grouped_planes", self.table.data_ptr(), self.n, self.total_blocks,
+                 self.M, self.max_K, _ptr(self.workspace), _numel(self.workspace), stream)
+        else:
+            call("plz_lut_gemv_grouped", self.table.data_ptr(), self.n, self.total_blocks,
+                 self.M, self.layout, stream)
         return self.outputs
 
 

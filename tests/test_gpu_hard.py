@@ -190,14 +190,22 @@ def test_gemv_ragged(dev, M, N, K):
 
 
 def _single_gemv(x, p, pl, decode):
+    if decode == "planes":
+        return ops.lut_gemv_planes(x, ops.gemv_pack_planes(p), ops.gemv_pack_palettes(pl),
+                                   p.shape[0])
     if decode:
         return ops.lut_gemv_decode(x, ops.gemv_pack_indices(p), ops.gemv_pack_palettes(pl),
                                    p.shape[0])
     return ops.lut_gemv(x, p, pl)
 
 
-@pytest.mark.parametrize("decode", [False, True], ids=["native", "decode-layout"])
-@pytest.mark.parametrize("M", [1, 16])
+def _layout(decode):
+    return "planes" if decode == "planes" else ("decode" if decode else "native")
+
+
+@pytest.mark.parametrize("decode", [False, True, "planes"],
+                         ids=["native", "decode-layout", "planes-layout"])
+@pytest.mark.parametrize("M", [1, 4, 16])
 def test_gemv_grouped_many_linears(dev, M, decode):
     """A grouped launch over 3 x 7 Qwen-4B shapes plus empty linears: every output equals the
     single-linear launch on the same layout bit for bit, and sampled ones match the oracle."""
@@ -213,7 +221,7 @@ def test_gemv_grouped_many_linears(dev, M, decode):
         items.append((randn_bf16(M, 256, seed=7).to(dev), torch.zeros(0, 16, dtype=torch.int32, device=dev),
                       torch.zeros(0, 1, 4, device=dev)))
         idxs.append(None)
-    grp = ops.GemvGroup(items, prepack=decode)
+    grp = ops.GemvGroup(items, layout=_layout(decode))
     outs = grp.run()
     for j, ((x, p, pl), y) in enumerate(zip(items, outs)):
         if idxs[j] is None:
@@ -236,7 +244,8 @@ def test_gemv_pack_palettes_layout(dev):
     assert got.size >= want.size and np.array_equal(got[:want.size], want)
 
 
-@pytest.mark.parametrize("decode", [False, True], ids=["native", "decode-layout"])
+@pytest.mark.parametrize("decode", [False, True, "planes"],
+                         ids=["native", "decode-layout", "planes-layout"])
 def test_gemv_grouped_matches_single(dev, decode):
     shapes = [(4096, 2560), (1024, 2560), (2560, 4096), (264, 512), (9728, 2560)]
     M = 4
@@ -246,7 +255,7 @@ def test_gemv_grouped_matches_single(dev, decode):
         x = randn_bf16(M, K, seed=200 + i)
         items.append((x.to(dev), _packed(idx, dev), pal.to(dev)))
         wants.append(O.lut_linear_fwd(f32(x), O.dequant(idx.numpy(), pal.numpy())))
-    grp = ops.GemvGroup(items, prepack=decode)
+    grp = ops.GemvGroup(items, layout=_layout(decode))
     outs = grp.run()
     for (x, p, pl), y, want in zip(items, outs, wants):
         assert_close(f32(y), want, what="grouped gemv")
@@ -263,16 +272,49 @@ def test_gemv_pack_indices_layout(dev):
     assert got.size >= want.size and np.array_equal(got[:want.size], want)
 
 
+@pytest.mark.parametrize("layout", [True, "planes"], ids=["decode-layout", "planes-layout"])
 @pytest.mark.parametrize("M,N,K", [(1, 4096, 2560), (4, 1024, 2560), (16, 2560, 9728),
-                                   (5, 264, 256), (13, 8, 768), (1, 136, 1280)])
-def test_gemv_decode_layout(dev, M, N, K):
-    """The GEMV on the decode layouts (indices and palettes) against the oracle, including
-    token counts of every x-slice size and N not a multiple of the 128-row item."""
+                                   (5, 264, 256), (13, 8, 768), (1, 136, 1280), (2, 256, 512),
+                                   (7, 128, 256), (8, 384, 1024), (9, 256, 768), (15, 136, 512)])
+def test_gemv_decode_layout(dev, M, N, K, layout):
+    """The GEMV on the decode and planes layouts (indices and palettes) against the oracle,
+    including token counts of every x-slice and A-operand size and N not a multiple of the
+    128-row item."""
     idx, pal = make_weight(N, K, seed=M * 3 + N + K)
     x = randn_bf16(M, K, seed=M + 2)
-    y = _single_gemv(x.to(dev), _packed(idx, dev), pal.to(dev), True)
+    y = _single_gemv(x.to(dev), _packed(idx, dev), pal.to(dev), layout)
     want = O.lut_linear_fwd(f32(x), O.dequant(idx.numpy(), pal.numpy()))
-    assert_close(f32(y), want, what=f"decode gemv M={M} N={N} K={K}")
+    assert_close(f32(y), want, what=f"{_layout(layout)} gemv M={M} N={N} K={K}")
+
+
+def test_gemv_pack_planes_layout(dev):
+    """plz_gemv_pack_planes equals the oracle's planes layout word for word (ragged N: padded
+    rows are zero)."""
+    N, K = 300, 768
+    idx, _ = make_weight(N, K, seed=5)
+    got = ops.gemv_pack_planes(_packed(idx, dev)).cpu().numpy().view(np.uint32)
+    want = O.gemv_planes_layout(idx.numpy())
+    assert got.size >= want.size and np.array_equal(got[:want.size], want)
+
+
+@pytest.mark.parametrize("M", [1, 4, 16])
+def test_gemv_planes_x_dynamic_range(dev, M):
+    """x rows spanning many binades inside one 256-k group (an outlier 2^12 times the rest,
+    tiny values, exact zeros, negative zero): the two e4m3 pieces under the group's scale keep
+    the bit-plane GEMV at the parity bar against the fp64 oracle."""
+    N, K = 256, 1024
+    idx, pal = make_weight(N, K, seed=77)
+    g = gen(78)
+    x = torch.randn(M, K, generator=g)
+    x[:, 5] = 4096.0
+    x[:, 300:320] *= 1e-6
+    x[:, 600:640] = 0.0
+    x[:, 700] = -0.0
+    x[0, 900] = -3000.0
+    x = x.to(torch.bfloat16)
+    y = _single_gemv(x.to(dev), _packed(idx, dev), pal.to(dev), "planes")
+    want = O.lut_linear_fwd(f32(x), O.dequant(idx.numpy(), pal.numpy()))
+    assert_close(f32(y), want, what=f"planes gemv dynamic range M={M}")
 
 
 @pytest.mark.parametrize("M", [2048, 8192])
@@ -312,3 +354,20 @@ def test_tail_split_gemms(dev, M):
     # deterministic: the split sums its parts in a fixed order
     y2 = ops.lut_linear_fwd(x.to(dev), p, pl, bias.to(dev), lora_t=t, lora_b=b.to(dev))
     assert torch.equal(y, y2)
+
+
+@pytest.mark.parametrize("M", [1, 8, 9])
+def test_gemv_group_auto_layout(dev, M):
+    """The default grouped layout: the bit-plane kernel up to 8 tokens, the decode kernel
+    above; either way the oracle's outputs."""
+    shapes = [(1024, 2560), (264, 512)]
+    items, wants = [], []
+    for i, (N, K) in enumerate(shapes):
+        idx, pal = make_weight(N, K, seed=300 + i)
+        x = randn_bf16(M, K, seed=400 + i)
+        items.append((x.to(dev), _packed(idx, dev), pal.to(dev)))
+        wants.append(O.lut_linear_fwd(f32(x), O.dequant(idx.numpy(), pal.numpy())))
+    grp = ops.GemvGroup(items)
+    assert grp.layout == (ops._lib.PLZ_GEMV_PLANES if M <= 8 else ops._lib.PLZ_GEMV_DECODE)
+    for y, want in zip(grp.run(), wants):
+        assert_close(f32(y), want, what=f"auto-layout gemv M={M}")

@@ -46,6 +46,29 @@ def test_forward_rows_of_a_nonfinite_input_go_nonfinite(dev, M, N, K, staged):
     assert bool(torch.isnan(gv[3]).all()) and bool(torch.isfinite(gv[:3]).all())
 
 
+@pytest.mark.parametrize("M", [1, 5, 16])
+def test_planes_gemv_tokens_of_a_nonfinite_input_go_nonfinite(dev, M):
+    """The bit-plane GEMV: a NaN or +-inf in token t's x makes every output of token t
+    non-finite (its e4m3 pieces are NaN); the other tokens are bit-equal to a clean launch (the
+    scale of a group is set by its finite values only)."""
+    N, K = 264, 768
+    _, p, pl = _weight(N, K, 9, dev)
+    pi, li = ops.gemv_pack_planes(p), ops.gemv_pack_palettes(pl)
+    x = randn_bf16(M, K, seed=10).to(dev)
+    clean = ops.lut_gemv_planes(x, pi, li, N)
+    xb = x.clone()
+    xb[M - 1, 300] = NAN if M % 2 else INF
+    if M > 2:
+        xb[1, 700] = -INF
+    y = ops.lut_gemv_planes(xb, pi, li, N)
+    bad = torch.zeros(M, dtype=torch.bool, device=dev)
+    bad[M - 1] = True
+    if M > 2:
+        bad[1] = True
+    assert not bool(torch.isfinite(y[bad]).any())
+    assert torch.equal(y[~bad], clean[~bad])
+
+
 @pytest.mark.parametrize("M", [512, 4096])  # the LUT GEMM; dequantised W + dense GEMM
 def test_grad_x_rows_of_a_nonfinite_gradient_go_nonfinite(dev, M):
     N, K = 1024, 2560

@@ -419,3 +419,53 @@ def test_gemv_palette_luts_reassemble_torch_bf16():
     want = torch.from_numpy(pal).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
     assert np.array_equal(got[:130], want)
     assert not got[130:].any()
+
+
+def test_gemv_planes_layout_through_the_plane_masks():
+    """Planes-layout words read the way the bit-plane GEMV reads them give back every row's
+    indices in natural k order: with t = q >> 1, MFMA half 0 takes b0 = q & 0x11111111,
+    b1 = q & 0x22222222, b0 b1 = q & t & 0x11111111 and half 1 b0 = q & 0x44444444,
+    b1 = t & 0x44444444, b0 b1 = q & t & 0x44444444 from the lane's four words j = 0..3 as FP4
+    nibbles e = 8j + i of k = 128 h + 32 g + e (the B operand's lane layout). Padded rows are
+    zero. A wrong nibble, word, lane or row order fails here."""
+    rng = np.random.default_rng(8)
+    N, K = 200, 512
+    idx = rng.integers(0, 4, (N, K))
+    items, stages = (N + 127) // 128, K // 256
+    words = O.gemv_planes_layout(idx)
+    assert words.size == items * 128 * K // 16
+    words = words.reshape(items, stages, 4, 2, 4, 16, 4)  # item, stage, w, b, g, r, j
+    back = np.zeros((items, 4, 2, 16, stages, 256), np.int64)  # item, w, b, r, stage, k
+    for h, (m0, m1, bit0, bit1) in enumerate(((0x11111111, 0x22222222, 0, 1),
+                                               (0x44444444, 0x44444444, 2, 2))):
+        for j in range(4):
+            q = words[..., j]
+            t = q >> np.uint32(1)
+            p0 = q & np.uint32(m0)
+            p1 = (t if h else q) & np.uint32(m1)
+            p3 = q & t & np.uint32(m0)
+            for i in range(8):
+                b0 = (p0 >> np.uint32(4 * i + bit0)) & 1
+                b1 = (p1 >> np.uint32(4 * i + bit1)) & 1
+                assert np.array_equal((p3 >> np.uint32(4 * i + bit0)) & 1, b0 & b1)
+                for g in range(4):  # nibble e = 8j + i of lane group g: k = 128h + 32g + e
+                    back[:, :, :, :, :, 128 * h + 32 * g + 8 * j + i] = \
+                        (b0 + 2 * b1)[:, :, :, :, g, :].transpose(0, 2, 3, 4, 1)
+    back = back.reshape(items * 128, stages * 256)
+    assert np.array_equal(back[:N], idx)
+    assert not back[N:].any()
+
+
+def test_gemv_planes_decomposition_reproduces_the_dequantised_weight():
+    """p0 + (p1 - p0) b0 + (p2 - p0) b1 + (p3 - p2 - p1 + p0) b0 b1 is the palette entry of
+    index b0 + 2 b1 exactly, for bf16 palette entries evaluated in fp32 (the bit-plane GEMV's
+    coefficients)."""
+    rng = np.random.default_rng(9)
+    pal = O.bf16_round(rng.standard_normal((500, 4)).astype(np.float32) * 0.03)
+    idx = rng.integers(0, 4, 500)
+    b0, b1 = idx & 1, idx >> 1
+    p = pal.astype(np.float32)
+    c1, c2 = p[:, 1] - p[:, 0], p[:, 2] - p[:, 0]
+    c3 = (p[:, 3] - p[:, 2]) - c1
+    w = p[:, 0] + c1 * b0 + c2 * b1 + c3 * (b0 & b1)
+    assert np.array_equal(w.astype(np.float32), pal[np.arange(500), idx])
