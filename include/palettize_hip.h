@@ -373,8 +373,9 @@ int plz_lut_gemv_grouped(const plz_gemv_desc* descs_device, int n, int64_t total
  * with b0, b1 the bits of each 2-bit index, S(f) = sum_k x_k f_k, X = sum_k x_k, d1 = p1 - p0,
  * d2 = p2 - p0, d3 = p3 - p2 - p1 + p0: the bit planes are FP4 operands of gfx950's scaled
  * FP8 x FP4 MFMA, cut from the packed words by masks, and x enters as two e4m3 pieces per
- * element with a power-of-two scale per token and group (x = 2^s (x1 + x2) exactly). Same
- * outputs as the decode kernel up to fp32 summation order. Replaces, like plz_lut_gemv, the
+ * element with a power-of-two scale per token and group (x = 2^s (x1 + x2), exact except
+ * where x2 underflows e4m3: an error below 2^-17 of the group's largest |x|). Same outputs as
+ * the decode kernel up to that and fp32 summation order. Replaces, like plz_lut_gemv, the
  * reference's 64-row-tile forward at M = 1 (fused_lut_kernel.cu:309-518).
  * Indices: a one-time repack (same size as plz_gemv_packed_items_bytes) in which lane
  * l = 16g + r of a 16-row block holds four words of its row: nibble i of word j holds the index

@@ -6,7 +6,8 @@
 // that the stream never stops:
 //
 // * Persistent workgroups, a few per CU. The work items (128 rows of one linear, all of K) of
-//   a launch are cut into one contiguous range per workgroup, balanced by bytes (K per item).
+//   a launch are cut into one contiguous range per workgroup, balanced by bytes (K per item);
+//   each XCD runs one contiguous block of ranges (xcd_range).
 // * A workgroup walks its items as one sequence of stages (128 rows x 256 k = one palette
 //   group), with the loads of the next item in flight while this one finishes.
 // * Wave w owns rows 32w..32w+31 of the item (two MFMA row blocks of 16). Lane (row n%16,
@@ -145,6 +146,16 @@ struct Table {
   }
 };
 
+// Workgroups go to the 8 XCDs round-robin by linear id, and each XCD has its own L2. Range r
+// (the byte-balanced ranges in cost order) is given to workgroup id so that XCD x runs one
+// contiguous block of ranges: the few workgroups that share a linear then sit on one XCD, and
+// since they reach the same 256-k stage at about the same time, its x slice is read from HBM
+// once per linear instead of once per workgroup.
+__device__ __forceinline__ int64_t xcd_range(int64_t id, int64_t G) {
+  const int64_t x = id % 8, q8 = G / 8, r8 = G % 8;
+  return x * q8 + (x < r8 ? x : r8) + id / 8;
+}
+
 // Position in a workgroup's stage sequence.
 struct Cursor {
   int64_t item, end;
@@ -191,7 +202,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(const plz_gemv_desc* _
   const int nl = lane & 15, q = lane >> 4;
 
   // this workgroup's items: those whose start cost lies in [wid*T/G, (wid+1)*T/G)
-  const int64_t T = tb.total_cost(), G = gridDim.x, wid = blockIdx.x;
+  const int64_t T = tb.total_cost(), G = gridDim.x, wid = xcd_range(blockIdx.x, G);
   Cursor pc, cc;
   pc.item = cc.item = tb.item_at_cost(wid * T / G);
   pc.end = cc.end = tb.item_at_cost((wid + 1) * T / G);
@@ -347,7 +358,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_reg_kernel(const plz_gemv_des
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int nl = lane & 15, q = lane >> 4;
 
-  const int64_t T = tb.total_cost(), G = gridDim.x, wid = blockIdx.x;
+  const int64_t T = tb.total_cost(), G = gridDim.x, wid = xcd_range(blockIdx.x, G);
   Cursor pc, cc;
   pc.item = cc.item = tb.item_at_cost(wid * T / G);
   pc.end = cc.end = tb.item_at_cost((wid + 1) * T / G);
@@ -627,17 +638,23 @@ __host__ __device__ constexpr int pl_nx(int M) {
 }
 typedef int i32x8 __attribute__((ext_vector_type(8)));
 
-// One wave per linear and PREP_STAGES stages: lane 16 g + c makes 16-byte piece c of work
-// item 4 i + g, the items being (token, stage) pairs of the wave's stages.
-constexpr int PREP_STAGES = 4;
+// One wave per linear, PREP_STAGES stages and PREP_TOKENS tokens: lane 16 g + c makes 16-byte
+// piece c of work item 4 i + g, the items being the (token, stage) pairs of the wave's tokens
+// and stages (at most 4 rounds of loads in sequence per wave).
+constexpr int PREP_STAGES = 4, PREP_TOKENS = 4;
+__host__ __device__ constexpr int prep_blocks_per_desc(int M, int max_stages) {
+  return ((max_stages + PREP_STAGES - 1) / PREP_STAGES) * ((M + PREP_TOKENS - 1) / PREP_TOKENS);
+}
 template <bool GROUPED>
 __global__ __launch_bounds__(64) void gemv_pl_prep_kernel(const plz_gemv_desc* __restrict__ descs,
                                                           int n_desc, plz_gemv_desc single,
                                                           int M, int max_stages,
                                                           uint8_t* __restrict__ ws) {
-  const int blocks_per_desc = (max_stages + PREP_STAGES - 1) / PREP_STAGES;
-  const int d = blockIdx.x / blocks_per_desc;
-  const int s0 = (blockIdx.x % blocks_per_desc) * PREP_STAGES;
+  const int tgroups = (M + PREP_TOKENS - 1) / PREP_TOKENS;
+  const int blocks_per_desc = prep_blocks_per_desc(M, max_stages);
+  const int d = blockIdx.x / blocks_per_desc, r = blockIdx.x % blocks_per_desc;
+  const int s0 = (r / tgroups) * PREP_STAGES, t0 = (r % tgroups) * PREP_TOKENS;
+  const int mt = M - t0 < PREP_TOKENS ? M - t0 : PREP_TOKENS;
   const Table<GROUPED> tb{descs, n_desc, single};
   const plz_gemv_desc dd = tb.at(d);
   const int stages = (int)(dd.K / KC);
@@ -645,9 +662,9 @@ __global__ __launch_bounds__(64) void gemv_pl_prep_kernel(const plz_gemv_desc* _
   const int ns = stages - s0 < PREP_STAGES ? stages - s0 : PREP_STAGES;
   const int lane = threadIdx.x, c = lane & 15, g = lane >> 4;
   const int k0 = 128 * (c >> 3) + 64 * (c & 1) + 16 * ((c >> 1) & 3);
-  for (int w0 = 0; w0 < M * ns; w0 += 4) {
-    const int w = w0 + g, t = w % M, s = s0 + w / M;
-    const bool live = w < M * ns;
+  for (int w0 = 0; w0 < mt * ns; w0 += 4) {
+    const int w = w0 + g, t = t0 + w % mt, s = s0 + w / mt;
+    const bool live = w < mt * ns;
     uint32_t b[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     if (live) {
       const uint4* src = reinterpret_cast<const uint4*>(dd.x + (int64_t)t * dd.K + (int64_t)s * KC + k0);
@@ -737,7 +754,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_pl_kernel(const plz_gemv_desc
   const int nl = lane & 15, q = lane >> 4;
   const uint32_t CH = (uint32_t)pl_chunk(M);
 
-  const int64_t T = tb.total_cost(), G = gridDim.x, wid = blockIdx.x;
+  const int64_t T = tb.total_cost(), G = gridDim.x, wid = xcd_range(blockIdx.x, G);
   Cursor pc, cc;
   pc.item = cc.item = tb.item_at_cost(wid * T / G);
   pc.end = cc.end = tb.item_at_cost((wid + 1) * T / G);
@@ -974,7 +991,7 @@ static int launch_pl_nx(int64_t items, hipStream_t st, const plz_gemv_desc* desc
                         plz_gemv_desc single, int M, int max_stages, uint8_t* ws,
                         size_t ws_bytes, const char* what) {
   hipLaunchKernelGGL(gemv_pl_prep_kernel<GROUPED>,
-                     dim3((unsigned)(n * ((max_stages + PREP_STAGES - 1) / PREP_STAGES))), dim3(64), 0,
+                     dim3((unsigned)(n * prep_blocks_per_desc(M, max_stages))), dim3(64), 0,
                      st, descs, n, single, M, max_stages, ws);
   auto kern = gemv_pl_kernel<NX, NSET, NI, GROUPED>;
   const size_t lds = (size_t)RDP * NX * WAVES * 1024 + YBYTES + (YBYTES / (ROWS * 2)) * 8;
