@@ -305,6 +305,90 @@ __device__ __forceinline__ void mma_stage(const lds_u8* __restrict__ a_s,
   __builtin_amdgcn_sched_barrier(0);
 }
 
+// One stage of the dense kernels' two-slot ring whose last k-step overlaps the boundary with
+// the next stage. A barrier between stages stalls every SIMD: the workgroup's waves reach it
+// together, and behind it each wave must read the next stage's first fragments before its
+// next MFMA. Here the barrier runs before the last k-step instead: k-steps 0..2 issue their
+// MFMAs and the fragment reads of the following k-step; bar() waits for this wave's copies of
+// the next stage and its own fragment reads and passes the barrier, after which no wave reads
+// this stage's slot any more and the next stage's tiles are complete; dma() then copies the
+// stage after next into this stage's slot (d_a, d_b: the same LDS as a_s, b_s, written only
+// after the barrier), and the last k-step's MFMAs cover the reads of the next stage's first
+// fragments into a0/b0.
+template <bool A_COL, bool B_COL, typename Bar, typename Dma>
+__device__ __forceinline__ void mma_stage_pipe(const lds_u8* __restrict__ a_s,
+                                               const lds_u8* __restrict__ b_s,
+                                               const lds_u8* __restrict__ na_s,
+                                               const lds_u8* __restrict__ nb_s,
+                                               lds_u8* __restrict__ d_a, lds_u8* __restrict__ d_b,
+                                               f32x16 (&acc)[WT_I][WT_J], int wi, int wj,
+                                               int lane, bf16x8 (&a0)[WT_I], bf16x8 (&b0)[WT_J],
+                                               Bar&& bar, Dma&& dma) {
+  constexpr int NREAD = WT_I * (A_COL ? 2 : 1) + WT_J * (B_COL ? 2 : 1);
+  bf16x8 a1[WT_I], b1[WT_J];
+  load_frags<A_COL, B_COL>(a_s, b_s, 1, wi, wj, lane, a1, b1);
+  mma_kstep(acc, a0, b0);
+  interleave_kstep<NREAD, 0, 0, 0>();
+  __builtin_amdgcn_sched_barrier(0);
+  load_frags<A_COL, B_COL>(a_s, b_s, 2, wi, wj, lane, a0, b0);
+  mma_kstep(acc, a1, b1);
+  interleave_kstep<NREAD, 0, 0, 0>();
+  __builtin_amdgcn_sched_barrier(0);
+  load_frags<A_COL, B_COL>(a_s, b_s, 3, wi, wj, lane, a1, b1);
+  mma_kstep(acc, a0, b0);
+  interleave_kstep<NREAD, 0, 0, 0>();
+  __builtin_amdgcn_sched_barrier(0);
+  bar();
+  __builtin_amdgcn_sched_barrier(0);
+  dma(d_a, d_b);
+  load_frags<A_COL, B_COL>(na_s, nb_s, 0, wi, wj, lane, a0, b0);
+  mma_kstep(acc, a1, b1);
+  interleave_kstep<NREAD, 2 * COPY_INSTS, 0, 0>();
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// mma_stage_pipe for two Col tiles (the dW kernels' ring): fragment reads through per-stage
+// opaque addresses (ColBases, see col_bases), those of the next stage formed after the barrier
+// from its slots na_s / nb_s and carried into the next call through ca / cb.
+template <typename Bar, typename Dma>
+__device__ __forceinline__ void mma_stage_pipe_col(ColBases<WT_I>& ca, ColBases<WT_J>& cb,
+                                                   const lds_u8* __restrict__ na_s,
+                                                   const lds_u8* __restrict__ nb_s,
+                                                   lds_u8* __restrict__ d1, lds_u8* __restrict__ d2,
+                                                   f32x16 (&acc)[WT_I][WT_J], int wi, int wj,
+                                                   int lane, bf16x8 (&a0)[WT_I],
+                                                   bf16x8 (&b0)[WT_J], Bar&& bar, Dma&& dma) {
+  constexpr int NREAD = 2 * (WT_I + WT_J);
+  auto frags = [&](int ks, bf16x8 (&a)[WT_I], bf16x8 (&b)[WT_J]) {
+#pragma unroll
+    for (int i = 0; i < WT_I; ++i) a[i] = frag_col_at(ca.p1[i], ca.p2[i], ks);
+#pragma unroll
+    for (int j = 0; j < WT_J; ++j) b[j] = frag_col_at(cb.p1[j], cb.p2[j], ks);
+  };
+  bf16x8 a1[WT_I], b1[WT_J];
+  frags(1, a1, b1);
+  mma_kstep(acc, a0, b0);
+  interleave_kstep<NREAD, 0, 0, 0>();
+  __builtin_amdgcn_sched_barrier(0);
+  frags(2, a0, b0);
+  mma_kstep(acc, a1, b1);
+  interleave_kstep<NREAD, 0, 0, 0>();
+  __builtin_amdgcn_sched_barrier(0);
+  frags(3, a1, b1);
+  mma_kstep(acc, a0, b0);
+  interleave_kstep<NREAD, 0, 0, 0>();
+  __builtin_amdgcn_sched_barrier(0);
+  bar();
+  __builtin_amdgcn_sched_barrier(0);
+  dma(d1, d2);
+  col_bases(na_s, wi * (32 * WT_I), lane, ca);
+  col_bases(nb_s, wj * (32 * WT_J), lane, cb);
+  frags(0, a0, b0);
+  mma_kstep(acc, a1, b1);
+  interleave_kstep<NREAD, 2 * COPY_INSTS, 0, 0>();
+  __builtin_amdgcn_sched_barrier(0);
+}
+
 // One stage of the forward with the palettized operand dequantised in registers (B slot
 // holds the raw words and palettes, copy_lut_raw). MFMA k-slots are assigned so that no
 // dequantised weight is wasted: for the k-step pair p (32 k = two packed words per row),
@@ -685,10 +769,11 @@ __global__ __launch_bounds__(NTHR) void gemm2_kernel(const Args g) {
     // operand that changes between consecutive tiles of the walk (B when consecutive tiles
     // share their tile-row, else A) misses L2 more often and is copied two stages ahead, the
     // other one stage ahead. Copy c of the sequence lead_0, other_0, lead_1, other_1, ... goes
-    // to slot c % 5: at stage s the slots of lead_s, other_s, lead_s+1, other_s+1 and lead_s+2
-    // are distinct, and the two copies issued during stage s (other_s+1, then lead_s+2) reuse
-    // the slots of stage s-1. Past the last stage the copies repeat stage nfull-1 into those
-    // free slots, so every stage issues the same instructions.
+    // to slot c % 5. Stages run as mma_stage_pipe_col: the barrier before stage s's last k-step
+    // frees the slots of lead_s and other_s, and the two copies issued right after it,
+    // other_s+2 then lead_s+3, go to exactly those slots (c = 2s+5 and 2s+6); the slots of
+    // lead_s+1, other_s+1 and lead_s+2 stay live. Past the last stage the copies repeat stage
+    // nfull-1 into the free slots, so every stage issues the same instructions.
     auto ring = [&](auto lead_tag) {
       constexpr bool A_LEADS = decltype(lead_tag)::value;
       auto slot = [&](bool is_a, int kt) -> lds_u8* {
@@ -701,25 +786,38 @@ __global__ __launch_bounds__(NTHR) void gemm2_kernel(const Args g) {
         if (a) tile_copy(dst, dA, (uint32_t)(KA == OP_ROW ? r0 * 2 : r0 * g.lda * 2));
         else tile_copy(dst, dB, (uint32_t)(KB == OP_ROW ? r0 * 2 : r0 * g.ldb * 2));
       };
+      ColBases<WT_I> ca;
+      ColBases<WT_J> cb;
+      bf16x8 a0[WT_I], b0[WT_J];
       if (nfull > 0) {
         copy(A_LEADS, 0, slot(A_LEADS, 0));
         copy(!A_LEADS, 0, slot(!A_LEADS, 0));
         __builtin_amdgcn_sched_barrier(0);
         copy(A_LEADS, 1, slot(A_LEADS, 1));
-        wait_vmcnt<COPY_INSTS>();  // stage 0 has landed; lead_1 may be in flight
+        copy(!A_LEADS, 1, slot(!A_LEADS, 1));
+        copy(A_LEADS, 2, slot(A_LEADS, 2));
+        wait_vmcnt<3 * COPY_INSTS>();  // stage 0 has landed; lead_1, other_1, lead_2 may not
         stage_barrier();
+        col_bases(slot(true, 0), wi * (32 * WT_I), lane, ca);
+        col_bases(slot(false, 0), wj * (32 * WT_J), lane, cb);
+#pragma unroll
+        for (int i = 0; i < WT_I; ++i) a0[i] = frag_col_at(ca.p1[i], ca.p2[i], 0);
+#pragma unroll
+        for (int j = 0; j < WT_J; ++j) b0[j] = frag_col_at(cb.p1[j], cb.p2[j], 0);
       }
       for (int kt = 0; kt < nfull; ++kt) {
-        auto dma = [&](lds_u8* other_next, lds_u8* lead_next2) {
-          copy(!A_LEADS, kt + 1, other_next);
-          __builtin_amdgcn_sched_barrier(0);  // other_kt+1 is issued before lead_kt+2
-          copy(A_LEADS, kt + 2, lead_next2);
-        };
-        mma_stage<A_COL, B_COL, false>(slot(true, kt), slot(false, kt), slot(!A_LEADS, kt + 1),
-                                       slot(A_LEADS, kt + 2), acc, wi, wj, lane, dma,
-                                       [](int, lds_u8*) {});
-        wait_vmcnt<COPY_INSTS>();  // stage kt+1 has landed; lead_kt+2 may be in flight
-        stage_barrier();
+        mma_stage_pipe_col(
+            ca, cb, slot(true, kt + 1), slot(false, kt + 1), slot(A_LEADS, kt),
+            slot(!A_LEADS, kt), acc, wi, wj, lane, a0, b0,
+            [&] {
+              wait_vmcnt<COPY_INSTS>();  // stage kt+1 has landed; lead_kt+2 may not
+              stage_barrier();
+            },
+            [&](lds_u8* other_next2, lds_u8* lead_next3) {
+              copy(!A_LEADS, kt + 2, other_next2);
+              __builtin_amdgcn_sched_barrier(0);  // other_kt+2 is issued before lead_kt+3
+              copy(A_LEADS, kt + 3, lead_next3);
+            });
       }
     };
     if (g.group != 1) ring(std::true_type{});
@@ -785,6 +883,39 @@ __global__ __launch_bounds__(NTHR) void gemm2_kernel(const Args g) {
                        wi, wj, lane, [&](lds_u8* na, lds_u8* nb) { copy(kt + 2, na, nb); });
       wait_vmcnt<PER_STAGE>();  // stage kt+1 has landed; stage kt+2 may be in flight
       stage_barrier();
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // the repeated copies past the last stage
+    __syncthreads();
+  } else if constexpr (!LUT) {
+    // dense operands through two stage slots of 64 KB, the barrier between stages moved
+    // before each stage's last k-step (mma_stage_pipe): right after it the copies of stage
+    // kt+2 go into stage kt's slot, a full stage ahead of the barrier that completes them.
+    // Past the last stage the copies repeat stage nfull-1 into the idle slot, so every
+    // stage issues the same instructions.
+    auto slot = [&](int kt) { return lbase + (kt & 1) * 2 * TILE_BYTES; };
+    auto copy = [&](int kt, lds_u8* as) {
+      const int ks = kt < nfull ? kt : nfull - 1;
+      copy_stage(as, as + TILE_BYTES, rbeg + (int64_t)ks * BK);
+    };
+    bf16x8 a0[WT_I], b0[WT_J];
+    if (nfull > 0) {
+      copy(0, slot(0));
+      copy(1, slot(1));
+      wait_vmcnt<2 * COPY_INSTS>();  // stage 0 has landed; stage 1 may be in flight
+      stage_barrier();
+      load_frags<A_COL, B_COL>(slot(0), slot(0) + TILE_BYTES, 0, wi, wj, lane, a0, b0);
+    }
+    for (int kt = 0; kt < nfull; ++kt) {
+      lds_u8* const cs = slot(kt);
+      const lds_u8* const ns = slot(kt + 1);
+      mma_stage_pipe<A_COL, B_COL>(
+          cs, cs + TILE_BYTES, ns, ns + TILE_BYTES, cs, cs + TILE_BYTES, acc, wi, wj, lane, a0,
+          b0,
+          [&] {
+            wait_vmcnt<0>();  // this wave's copies of stage kt+1
+            stage_barrier();
+          },
+          [&](lds_u8* da, lds_u8*) { copy(kt + 2, da); });
     }
     __builtin_amdgcn_s_waitcnt(0);  // the repeated copies past the last stage
     __syncthreads();
