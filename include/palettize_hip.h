@@ -489,7 +489,8 @@ int plz_attn_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16
 /* Backward of plz_attn_fwd (the autograd of the same sdpa call): grad_q bf16 [batch, seq, heads,
  * 128], grad_k, grad_v bf16 [batch, seq, kv_heads, 128] (summed over the heads sharing a kv
  * head), from q, k, v, the forward's o and lse, and grad_o. Deterministic (no atomics); the
- * workspace (fp32 [batch, heads, seq]: rowsum(grad_o * o)) comes from the query. */
+ * workspace (fp32 [2][batch, heads, seq]: rowsum(grad_o * o), then -lse log2 e) comes from the
+ * query. */
 size_t plz_attn_bwd_workspace(int batch, int seq, int heads);
 int plz_attn_bwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* o,
                  const uint16_t* grad_o, const float* lse, uint16_t* grad_q, uint16_t* grad_k,

@@ -48,6 +48,13 @@ __device__ __forceinline__ int k_off(int r, int c) { return r * (KCH * 16) + ((c
 __device__ __forceinline__ int vswz(int kv) { return (kv ^ ((kv & 3) << 2)) & 15; }
 __device__ __forceinline__ int v_off(int kv, int c) { return kv * (KCH * 16) + ((c ^ vswz(kv)) << 4); }
 
+// wait until at most N vector-memory operations of this wave are outstanding
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
 __device__ __forceinline__ void dma16(BufRsrc r, lds_u8* dst, uint32_t off) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, dst, 16, off, 0, 0, 0);
 }
@@ -314,7 +321,8 @@ constexpr float kLog2e = 1.4426950408889634f;
 __global__ __launch_bounds__(NT, 2) void attn_bwd_dq_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const uint16_t* __restrict__ o, const uint16_t* __restrict__ dout,
-    const float* __restrict__ lse, uint16_t* __restrict__ dq, float* __restrict__ dsum_out, int B,
+    const float* __restrict__ lse, uint16_t* __restrict__ dq, float* __restrict__ dsum_out,
+    float* __restrict__ nl_out, int B,
     int S, int Hq, int Hkv, float scale_log2, float scale) {
   extern __shared__ uint4 smem[];
   lds_u8* lds = (lds_u8*)smem;
@@ -346,7 +354,10 @@ __global__ __launch_bounds__(NT, 2) void attn_bwd_dq_kernel(
   dsum += __shfl_xor(dsum, 32);
   const int64_t li = ((int64_t)b * Hq + h) * S + qrow;
   const float nl = -lse[li] * kLog2e;
-  if (h2 == 0) dsum_out[li] = dsum;
+  if (h2 == 0) {
+    dsum_out[li] = dsum;
+    nl_out[li] = nl;
+  }
 
   const int64_t kv_bytes = (int64_t)S * kstride * 2;
   const BufRsrc rk = make_rsrc(k + (int64_t)b * S * kstride + (int64_t)hk * D, (uint32_t)kv_bytes);
@@ -412,20 +423,158 @@ __global__ __launch_bounds__(NT, 2) void attn_bwd_dq_kernel(
                dq + ((int64_t)b * S + q0 + 32 * wave) * qstride + (int64_t)h * D, qstride, lane);
 }
 
-constexpr int BKV = 128;  // kv rows per dK/dV workgroup (32 per wave)
-constexpr int BQ = 64;    // query rows per block of the dK/dV loop
-constexpr int QSLOT = 2 * TILE + 512;  // Q tile, dO tile, lse[64], D[64]
-constexpr size_t kLdsDkv = 2 * 4 * 32 * 272 > 2 * QSLOT ? 2 * 4 * 32 * 272 : 2 * QSLOT;
+constexpr int BKV = 128;   // kv rows per dK/dV workgroup (32 per wave)
+constexpr int BQ = 64;     // query rows per block of the dK/dV loop
+constexpr int QRING = 4;   // q-block slots of the dK/dV ring: copies run two blocks ahead
+// one slot: Q tile, dO tile, then per wave 128 B: lse and D of the wave's 16 queries of the block
+constexpr int QSLOT = 2 * TILE + 512;
+constexpr int QCOPIES = 10;  // copy instructions per slot and wave: 4 Q, 4 dO, lse, D
+constexpr size_t kLdsDkv =
+    2 * 4 * 32 * 272 > QRING * QSLOT ? 2 * 4 * 32 * 272 : (size_t)QRING * QSLOT;
 
-// grid: S/128 x Hkv x B, in longest-first order (the first kv blocks see the most queries)
+// 8 MFMAs, each followed by fragment reads: two after each of the first four, one after each
+// of the others (12 reads: the next step's fragments)
+__device__ __forceinline__ void interleave12() {
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+  }
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+  }
+}
+
+// One pipelined iteration of the dK/dV loop (phases A and C; phase B follows in the kernel):
+// the copies of a later block into dst, then 8 steps of 8 MFMAs, step st = dV/dK of block i
+// (slot cs) for k-step st/2 and d blocks 2(st&1), +1, and S/dP of block i+1 (slot ns) for
+// k-step st. The fragments of step st+1 are read before the MFMAs of step st; fc holds the
+// dV/dK fragments of step 0 on entry (read before the barrier, from a slot completed by the
+// previous one) and those of the next iteration's step 0 on return, read from ns during the
+// last step together with the next softmax's -lse log2 e and D (nl, dd). The last step issues
+// its S/dP MFMAs first, so that its dV/dK MFMAs cover their latency before the softmax reads
+// them. cs, ns and dst are distinct slots, and saying so lets the compiler leave the copies in
+// flight across the reads.
+template <typename Issue>
+__device__ __forceinline__ void dkv_step(const lds_u8* __restrict__ cs,
+                                         const lds_u8* __restrict__ ns, lds_u8* __restrict__ dst,
+                                         const uint32_t (&roff)[D / 16][2],
+                                         const uint32_t (&toff)[D / 32][2], uint32_t loff,
+                                         const bf16x8 (&kf)[D / 16], const bf16x8 (&vf)[D / 16],
+                                         const bf16x8 (&pf)[4], const bf16x8 (&dsf)[4],
+                                         f32x16 (&s)[2], f32x16 (&dp)[2], f32x16 (&dvt)[D / 32],
+                                         f32x16 (&dkt)[D / 32], bf16x8 (&fc)[4],
+                                         f32x4 (&nl)[2][4], f32x4 (&dd)[2][4], Issue&& issue) {
+  auto rfrag = [&](int tile, int ks, int mb) {
+    return __builtin_bit_cast(
+        bf16x8, *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(
+                    ns + tile * TILE + roff[ks][mb]));
+  };
+  auto tfrag = [&](const lds_u8* base, int tile, int db, int ks) {
+    const v4i16 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_v4i16*)(base + tile * TILE + ks * 4096 + toff[db][0]));
+    const v4i16 y = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_v4i16*)(base + tile * TILE + ks * 4096 + toff[db][1]));
+    typedef short v8i16 __attribute__((ext_vector_type(8)));
+    return __builtin_bit_cast(bf16x8, __builtin_shufflevector(x, y, 0, 1, 2, 3, 4, 5, 6, 7));
+  };
+  // fragments of one step: [0..1] dO^T (d blocks d0, d0+1), [2..3] Q^T, [4..5] Q rows
+  // (mb 0, 1), [6..7] dO rows
+  auto load_c = [&](const lds_u8* base, int st, bf16x8 (&f)[4]) {
+    const int kc = st >> 1, d0 = 2 * (st & 1);
+    f[0] = tfrag(base, 1, d0, kc);
+    f[1] = tfrag(base, 1, d0 + 1, kc);
+    f[2] = tfrag(base, 0, d0, kc);
+    f[3] = tfrag(base, 0, d0 + 1, kc);
+  };
+  auto load_a = [&](int st, bf16x8 (&f)[4]) {
+    f[0] = rfrag(0, st, 0);
+    f[1] = rfrag(0, st, 1);
+    f[2] = rfrag(1, st, 0);
+    f[3] = rfrag(1, st, 1);
+  };
+  auto mma_c = [&](int st, const bf16x8 (&f)[4]) {
+    const int kc = st >> 1, d0 = 2 * (st & 1);
+    dvt[d0] = mfma32(f[0], pf[kc], dvt[d0]);
+    dkt[d0] = mfma32(f[2], dsf[kc], dkt[d0]);
+    dvt[d0 + 1] = mfma32(f[1], pf[kc], dvt[d0 + 1]);
+    dkt[d0 + 1] = mfma32(f[3], dsf[kc], dkt[d0 + 1]);
+  };
+  auto mma_a = [&](int st, const bf16x8 (&f)[4]) {
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb) {
+      s[mb] = mfma32(f[mb], kf[st], st == 0 ? f32x16{} : s[mb]);
+      dp[mb] = mfma32(f[2 + mb], vf[st], st == 0 ? f32x16{} : dp[mb]);
+    }
+  };
+  bf16x8 ca[4], cb[4], aa[4], ab[4];
+  issue(dst);
+  load_a(0, aa);
+  __builtin_amdgcn_sched_barrier(0);
+  // step 0 (dV/dK fragments from fc)
+  load_c(cs, 1, cb);
+  load_a(1, ab);
+  mma_c(0, fc);
+  mma_a(0, aa);
+  interleave12();
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int st = 1; st < 7; st += 2) {
+    load_c(cs, st + 1, ca);
+    load_a(st + 1, aa);
+    mma_c(st, cb);
+    mma_a(st, ab);
+    interleave12();
+    __builtin_amdgcn_sched_barrier(0);
+    load_c(cs, st + 2, cb);
+    load_a(st + 2, ab);
+    mma_c(st + 1, ca);
+    mma_a(st + 1, aa);
+    interleave12();
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  // step 7: S/dP first; reads of the next iteration's step-0 dV/dK fragments and of the next
+  // softmax's -lse log2 e and D (queries r = 32 mb + 8 j + 4 h2 + 0..3 of block i+1)
+  load_c(ns, 0, fc);
+#pragma unroll
+  for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const lds_u8* a = ns + 2 * TILE + loff + 128 * (2 * mb + (j >> 1)) + 32 * (j & 1);
+      nl[mb][j] = *reinterpret_cast<const __attribute__((address_space(3))) f32x4*>(a);
+      dd[mb][j] = *reinterpret_cast<const __attribute__((address_space(3))) f32x4*>(a + 64);
+    }
+  mma_a(7, ab);
+  mma_c(7, cb);
+#pragma unroll
+  for (int m = 0; m < 8; ++m) {  // 24 reads: three after each MFMA
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// grid: S/128 x Hkv x B, in longest-first order (the first kv blocks see the most queries).
+// The loop over the (query head, query block) pairs t is software-pipelined: iteration i issues
+// the MFMAs of S, dP for block i+1 (phase A) interleaved with those of dV, dK for block i
+// (phase C), then the softmax algebra of block i+1 (phase B: P, dS as bf16 fragments). So the
+// VALU work of a block never waits on MFMAs just issued, and the matrix core always has
+// independent MFMAs queued. The blocks go through a 4-slot LDS ring, copied two blocks ahead:
+// the barrier at the top of iteration i completes block i+1 and frees the slot of block i-1,
+// which then receives block i+3. Every wave runs every block; blocks that lie entirely before
+// a wave's kv rows are masked to P = 0 like the diagonal ones (about a tenth more MFMAs than
+// skipping them, in exchange for one instruction stream).
 __global__ __launch_bounds__(NT) void attn_bwd_dkv_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
-    const uint16_t* __restrict__ dout, const float* __restrict__ lse,
+    const uint16_t* __restrict__ dout, const float* __restrict__ nlse,
     const float* __restrict__ dsum, uint16_t* __restrict__ dk, uint16_t* __restrict__ dv, int B,
     int S, int Hq, int Hkv, float scale_log2, float scale) {
   extern __shared__ uint4 smem[];
   lds_u8* lds = (lds_u8*)smem;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h2 = lane >> 5, ql = lane & 31;
+  const int lane = threadIdx.x & 63, h2 = lane >> 5, ql = lane & 31;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   int id = blockIdx.x;
   const int kb = id / (Hkv * B);
   id %= Hkv * B;
@@ -449,9 +598,12 @@ __global__ __launch_bounds__(NT) void attn_bwd_dkv_kernel(
   const int wb = __builtin_amdgcn_readfirstlane(wave * 1024);
   const int qstart = kv0 / BQ, nq = S / BQ - qstart, T = G * nq;
   const int64_t q_bytes = (int64_t)S * qstride * 2;
-  auto issue = [&](int slot, int t) {
-    const int g = t / nq, qblk = qstart + t % nq, h = hk * G + g;
-    lds_u8* qs = lds + slot * QSLOT;
+  auto slot = [&](int t) { return lds + (t & (QRING - 1)) * QSLOT; };
+  // copies of block t into its slot (past the last block: block T-1 again, so that every
+  // iteration issues the same number of copies; its slot is free then)
+  auto issue = [&](int t, lds_u8* qs) {
+    const int tt = t < T ? t : T - 1;
+    const int g = tt / nq, qblk = qstart + tt % nq, h = hk * G + g;
     const int64_t hoff = (int64_t)b * S * qstride + (int64_t)h * D;
     const BufRsrc rq = make_rsrc(q + hoff, (uint32_t)q_bytes);
     const BufRsrc rd = make_rsrc(dout + hoff, (uint32_t)q_bytes);
@@ -460,73 +612,139 @@ __global__ __launch_bounds__(NT) void attn_bwd_dkv_kernel(
     for (int it = 0; it < 4; ++it) dma16(rq, qs + it * NT * 16 + wb, off[it] + base);
 #pragma unroll
     for (int it = 0; it < 4; ++it) dma16(rd, qs + TILE + it * NT * 16 + wb, off[it] + base);
-    if (wave < 2 && lane < 16) {  // lse (wave 0) and D (wave 1) of the 64 queries
-      const float* src = (wave == 0 ? lse : dsum) + ((int64_t)b * Hq + h) * S;
-      dma16(make_rsrc(src, (uint32_t)S * 4), qs + 2 * TILE + 256 * wave, (uint32_t)(qblk * BQ) * 4 + lane * 16);
+    // lanes 0..3: -lse log2 e of queries 16 wave .. +15 of the block; lanes 4..7: their D
+    const int64_t row = ((int64_t)b * Hq + h) * S;
+    const uint32_t loff = (uint32_t)(qblk * BQ + 16 * wave + 4 * (lane & 3)) * 4;
+    lds_u8* ldst = qs + 2 * TILE + 128 * wave;
+    if (lane < 4) dma16(make_rsrc(nlse + row, (uint32_t)S * 4), ldst, loff);
+    if (lane >= 4 && lane < 8) dma16(make_rsrc(dsum + row, (uint32_t)S * 4), ldst, loff);
+  };
+
+  // fragment addresses within a slot (lane-dependent, formed once): row fragments of the Q and
+  // dO tiles (A operands of S = Q K^T and dP = dO V^T) for k-step ks and row block mb, and the
+  // transposed fragments (A operands of dV^T += dO^T P and dK^T += Q^T dS) for d block db, whose
+  // k-step adds 16 rows = 4096 bytes (vswz sees only the low 4 bits of the row)
+  // this lane's queries' -lse log2 e and D within a slot's 512 B: 16 h2 bytes into each
+  // 32-byte half of a wave's 128 B (queries r = 32 mb + 8 j + 4 h2 + 0..3)
+  const uint32_t loff = 16 * h2;
+  uint32_t roff[D / 16][2], toff[D / 32][2];
+#pragma unroll
+  for (int ks = 0; ks < D / 16; ++ks)
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb) roff[ks][mb] = (uint32_t)v_off(32 * mb + ql, 2 * ks + h2);
+  {
+    const int j = lane >> 4, i = lane & 15, t4 = i >> 2, q4 = i & 3;
+    const int kv1 = 4 * (j >> 1) + t4, kv2 = kv1 + 8;
+#pragma unroll
+    for (int db = 0; db < D / 32; ++db) {
+      const int d = 32 * db + 16 * (j & 1) + 4 * q4;
+      const int c = d >> 3, o2 = (d & 7) * 2;
+      toff[db][0] = (uint32_t)(v_off(kv1, c) + o2);
+      toff[db][1] = (uint32_t)(v_off(kv2, c) + o2);
     }
+  }
+  auto rfrag = [&](const lds_u8* base, int tile, int ks, int mb) {
+    return __builtin_bit_cast(bf16x8, *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(
+                                          base + tile * TILE + roff[ks][mb]));
+  };
+  auto tfrag = [&](const lds_u8* base, int tile, int db, int ks) {
+    const v4i16 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_v4i16*)(base + tile * TILE + ks * 4096 + toff[db][0]));
+    const v4i16 y = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_v4i16*)(base + tile * TILE + ks * 4096 + toff[db][1]));
+    typedef short v8i16 __attribute__((ext_vector_type(8)));
+    return __builtin_bit_cast(bf16x8, __builtin_shufflevector(x, y, 0, 1, 2, 3, 4, 5, 6, 7));
   };
 
   f32x16 dvt[D / 32], dkt[D / 32];
 #pragma unroll
   for (int db = 0; db < D / 32; ++db) dvt[db] = dkt[db] = f32x16{};
-  issue(0, 0);
-  for (int t = 0; t < T; ++t) {
-    const int cur = t & 1;
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (t + 1 < T) issue(cur ^ 1, t + 1);
+  f32x16 s[2], dp[2];
+  bf16x8 pf[4], dsf[4];
+
+  // phase B: P and dS of block t (its S, dP in s, dp) as bf16 B-operand fragments
+  auto softmax = [&](int t, const f32x4 (&L)[2][4], const f32x4 (&Dv)[2][4]) {
     const int qb0 = (qstart + t % nq) * BQ;
-    if (qb0 + BQ - 1 < kvw) continue;  // every query of the block is before this wave's kv
-    const lds_u8* qs = lds + cur * QSLOT;
-    const lds_u8* dos = qs + TILE;
-    const lds_u8* lsl = qs + 2 * TILE;  // lse[64], then D[64]
-    f32x16 s[2] = {f32x16{}, f32x16{}}, dp[2] = {f32x16{}, f32x16{}};
+    const bool diag = qb0 < kvw + 31;  // some query of the block precedes a kv row of the wave
+    float p[2][16];
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        p[mb][e] = exp2_fast(fmaf(s[mb][e], scale_log2, L[mb][e >> 2][e & 3]));
+    if (diag) {  // a wave-uniform branch: the other blocks run no mask code
+      asm volatile("");  // (keeps the compiler from turning the branch into selects for all)
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+          if (qb0 + 32 * mb + 8 * (e >> 2) + 4 * h2 + (e & 3) < kvrow) p[mb][e] = 0.f;
+    }
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb) {
+      float ds[16];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) ds[e] = p[mb][e] * (dp[mb][e] - Dv[mb][e >> 2][e & 3]);
+      pack_frags(p[mb], pf[2 * mb], pf[2 * mb + 1]);
+      pack_frags(ds, dsf[2 * mb], dsf[2 * mb + 1]);
+    }
+  };
+
+  // prologue: blocks 0..2 in flight; block 0 complete; S, dP and P, dS of block 0
+  issue(0, slot(0));
+  issue(1, slot(1));
+  issue(2, slot(2));
+  wait_vmcnt<2 * QCOPIES>();
+  __syncthreads();
+  {
+    const lds_u8* qs = slot(0);
 #pragma unroll
     for (int ks = 0; ks < D / 16; ++ks)
 #pragma unroll
       for (int mb = 0; mb < 2; ++mb) {
-        s[mb] = mfma32(row_frag(qs, 32 * mb + ql, ks, h2), kf[ks], s[mb]);
-        dp[mb] = mfma32(row_frag(dos, 32 * mb + ql, ks, h2), vf[ks], dp[mb]);
+        const f32x16 zs = ks == 0 ? f32x16{} : s[mb];
+        const f32x16 zd = ks == 0 ? f32x16{} : dp[mb];
+        s[mb] = mfma32(rfrag(qs, 0, ks, mb), kf[ks], zs);
+        dp[mb] = mfma32(rfrag(qs, 1, ks, mb), vf[ks], zd);
       }
-    const bool diag = qb0 < kvw + 31;  // some query of the block precedes a kv row of the wave
-    bf16x8 pf[4], dsf[4];
+    f32x4 L[2][4], Dv[2][4];
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb) {
-      float p[16], ds[16];
+    for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int r = 32 * mb + 8 * j + 4 * h2;
-        const f32x4 L = *reinterpret_cast<const __attribute__((address_space(3))) f32x4*>(
-            lsl + r * 4);
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          p[4 * j + i] = exp2_fast(fmaf(s[mb][4 * j + i], scale_log2, -L[i] * kLog2e));
+        const lds_u8* a = qs + 2 * TILE + loff + 128 * (2 * mb + (j >> 1)) + 32 * (j & 1);
+        L[mb][j] = *reinterpret_cast<const __attribute__((address_space(3))) f32x4*>(a);
+        Dv[mb][j] = *reinterpret_cast<const __attribute__((address_space(3))) f32x4*>(a + 64);
       }
-      if (diag) {  // a wave-uniform branch: the other blocks run no mask code
+    softmax(0, L, Dv);
+  }
+
+  // dV/dK fragments of step 0 of the first iteration (block 0)
+  bf16x8 fc[4];
+  fc[0] = tfrag(slot(0), 1, 0, 0);
+  fc[1] = tfrag(slot(0), 1, 1, 0);
+  fc[2] = tfrag(slot(0), 0, 0, 0);
+  fc[3] = tfrag(slot(0), 0, 1, 0);
+  for (int i = 0; i + 1 < T; ++i) {
+    wait_vmcnt<QCOPIES>();  // block i+1 has landed (block i+2 may not)
+    __syncthreads();        // ... for every wave; no wave reads block i-1's slot any more
+    f32x4 L[2][4], Dv[2][4];
+    dkv_step(slot(i), slot(i + 1), slot(i + 3), roff, toff, loff, kf, vf, pf, dsf, s, dp, dvt,
+             dkt, fc, L, Dv, [&](lds_u8* dst) { issue(i + 3, dst); });
+    softmax(i + 1, L, Dv);
+  }
+  // phase C of the last block (its slot was completed by the last iteration's barrier)
+  {
+    const lds_u8* cs = slot(T - 1);
 #pragma unroll
-        for (int e = 0; e < 16; ++e)
-          if (qb0 + 32 * mb + 8 * (e >> 2) + 4 * h2 + (e & 3) < kvrow) p[e] = 0.f;
-      }
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int r = 32 * mb + 8 * j + 4 * h2;
-        const f32x4 Dv = *reinterpret_cast<const __attribute__((address_space(3))) f32x4*>(
-            lsl + 256 + r * 4);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) ds[4 * j + i] = p[4 * j + i] * (dp[mb][4 * j + i] - Dv[i]);
-      }
-      pack_frags(p, pf[2 * mb], pf[2 * mb + 1]);
-      pack_frags(ds, dsf[2 * mb], dsf[2 * mb + 1]);
-    }
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
+    for (int kc = 0; kc < 4; ++kc)
 #pragma unroll
       for (int db = 0; db < D / 32; ++db) {
-        dvt[db] = mfma32(vt_frag(dos, 32 * db, ks, lane), pf[ks], dvt[db]);
-        dkt[db] = mfma32(vt_frag(qs, 32 * db, ks, lane), dsf[ks], dkt[db]);
+        dvt[db] = mfma32(tfrag(cs, 1, db, kc), pf[kc], dvt[db]);
+        dkt[db] = mfma32(tfrag(cs, 0, db, kc), dsf[kc], dkt[db]);
       }
   }
-  __builtin_amdgcn_s_waitcnt(0);
+  __builtin_amdgcn_s_waitcnt(0);  // the repeated copies past the last block
   __syncthreads();
   const int64_t orow = ((int64_t)b * S + kvw) * kstride + (int64_t)hk * D;
   store_rows_t(dkt, scale, lds + wave * (32 * 272), dk + orow, kstride, lane);
@@ -587,7 +805,7 @@ int plz_attn_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16
 
 size_t plz_attn_bwd_workspace(int batch, int seq, int heads) {
   if (batch <= 0 || seq <= 0 || heads <= 0) return 0;
-  return (size_t)batch * (size_t)heads * (size_t)seq * sizeof(float);
+  return 2 * (size_t)batch * (size_t)heads * (size_t)seq * sizeof(float);
 }
 
 int plz_attn_bwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* o,
@@ -612,14 +830,15 @@ int plz_attn_bwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, const 
     lr = reserve_lds((const void*)attn_bwd_dkv_kernel, kLdsDkv, lds_dkv, "plz_attn_bwd");
   if (lr != PLZ_OK) return lr;
   const float scale_log2 = scale * kLog2e;
-  float* dsum = (float*)workspace;
+  float* dsum = (float*)workspace;  // rowsum(grad_o * o), then -lse log2 e
+  float* nlse = dsum + (size_t)batch * heads * seq;
   hipLaunchKernelGGL(attn_bwd_dq_kernel, dim3((unsigned)(seq / BM) * heads * batch), dim3(NT), kLds,
-                     (hipStream_t)stream, q, k, v, o, grad_o, lse, grad_q, dsum, batch, seq,
+                     (hipStream_t)stream, q, k, v, o, grad_o, lse, grad_q, dsum, nlse, batch, seq,
                      heads, kv_heads, scale_log2, scale);
   int r = check_launch("plz_attn_bwd (dq)");
   if (r != PLZ_OK) return r;
   hipLaunchKernelGGL(attn_bwd_dkv_kernel, dim3((unsigned)(seq / BKV) * kv_heads * batch), dim3(NT),
-                     kLdsDkv, (hipStream_t)stream, q, k, v, grad_o, lse, dsum, grad_k, grad_v,
+                     kLdsDkv, (hipStream_t)stream, q, k, v, grad_o, nlse, dsum, grad_k, grad_v,
                      batch, seq, heads, kv_heads, scale_log2, scale);
   return check_launch("plz_attn_bwd (dk, dv)");
 }

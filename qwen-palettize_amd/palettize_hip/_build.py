@@ -29,13 +29,10 @@ CFLAGS = [
 ]
 
 
-# Per-file additions. plz_attn.hip: MFMAs keep their accumulators in the VGPR form; the dK/dV
-# kernel (one wave per SIMD) otherwise moves its dK/dV accumulators between AGPRs and VGPRs
-# around the loop's skip branch (352 of 701 VALU instructions per iteration, 51 with it).
-# plz_gemv.hip: the bit-plane GEMV folds its MFMA results into VALU sums every stage; in the
-# VGPR form they need no accumulator reads first (M = 1 / 4 / 16: 4 / 6 / 4% faster).
-FILE_FLAGS = {"plz_attn.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
-              "plz_gemv.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+# Per-file additions. plz_gemv.hip: MFMAs keep their accumulators in the VGPR form; the
+# bit-plane GEMV folds its MFMA results into VALU sums every stage, and in that form they need
+# no accumulator reads first (M = 1 / 4 / 16: 4 / 6 / 4% faster).
+FILE_FLAGS = {"plz_gemv.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 
 def sources() -> list[str]:

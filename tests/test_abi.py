@@ -152,7 +152,7 @@ def test_attention_argument_errors(lib):
     rc = lib.plz_attn_fwd(f, f, f, f, f, 1, 128, 4, 2, 128, -1.0, None)
     assert rc == 1 and b"scale" in lib.plz_last_error()
     assert lib.plz_attn_fwd(None, None, None, None, None, 0, 128, 4, 2, 128, 0.1, None) == 0
-    assert lib.plz_attn_bwd_workspace(2, 256, 8) == 2 * 8 * 256 * 4
+    assert lib.plz_attn_bwd_workspace(2, 256, 8) == 2 * 2 * 8 * 256 * 4  # D and -lse log2 e
     assert lib.plz_attn_bwd_workspace(0, 256, 8) == 0
     rc = lib.plz_attn_bwd(f, f, f, f, f, f, f, f, f, None, 0, 2, 256, 8, 2, 128, 0.1, None)
     assert rc == 4 and b"workspace" in lib.plz_last_error()
