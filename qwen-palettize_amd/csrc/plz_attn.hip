@@ -90,7 +90,8 @@ __global__ __launch_bounds__(NT, 2) void attn_fwd_kernel(const uint16_t* __restr
                                                       int Hq, int Hkv, float scale_log2) {
   extern __shared__ uint4 smem[];
   lds_u8* lds = (lds_u8*)smem;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h2 = lane >> 5, ql = lane & 31;
+  const int lane = threadIdx.x & 63, h2 = lane >> 5, ql = lane & 31;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   // 1-D grid in longest-first order: the last query blocks see the most kv blocks
   int id = blockIdx.x;
   const int qb = S / BM - 1 - id / (Hq * B);
@@ -326,7 +327,8 @@ __global__ __launch_bounds__(NT, 2) void attn_bwd_dq_kernel(
     int S, int Hq, int Hkv, float scale_log2, float scale) {
   extern __shared__ uint4 smem[];
   lds_u8* lds = (lds_u8*)smem;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h2 = lane >> 5, ql = lane & 31;
+  const int lane = threadIdx.x & 63, h2 = lane >> 5, ql = lane & 31;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int nqb = S / BM;
   int id = blockIdx.x;
   const int qb = nqb - 1 - id / (Hq * B);
@@ -374,6 +376,37 @@ __global__ __launch_bounds__(NT, 2) void attn_bwd_dq_kernel(
     for (int it = 0; it < 4; ++it) dma16(rv, ks_ + TILE + it * NT * 16 + wb, off[it] + base);
   };
 
+  // fragment addresses within a K/V slot (lane-dependent, formed once): row fragments of the K
+  // and V tiles (A operands of S^T = K Q^T and dP^T = V dO^T) for k-step ks and kv block nb, and
+  // the transposed K fragments (A operands of dQ^T += K^T dS^T) for d block db, whose k-step adds
+  // 16 rows = 4096 bytes (vswz sees only the low 4 bits of the row)
+  uint32_t roff[D / 16][2], toff[D / 32][2];
+#pragma unroll
+  for (int ks = 0; ks < D / 16; ++ks)
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) roff[ks][nb] = (uint32_t)v_off(32 * nb + ql, 2 * ks + h2);
+  {
+    const int j = lane >> 4, i = lane & 15, t4 = i >> 2, q4 = i & 3;
+    const int kv1 = 4 * (j >> 1) + t4, kv2 = kv1 + 8;
+#pragma unroll
+    for (int db = 0; db < D / 32; ++db) {
+      const int d = 32 * db + 16 * (j & 1) + 4 * q4;
+      const int c = d >> 3, o2 = (d & 7) * 2;
+      toff[db][0] = (uint32_t)(v_off(kv1, c) + o2);
+      toff[db][1] = (uint32_t)(v_off(kv2, c) + o2);
+    }
+  }
+  auto rfrag = [&](const lds_u8* base, int ks, int nb) {
+    return __builtin_bit_cast(bf16x8, *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(
+                                          base + roff[ks][nb]));
+  };
+  auto tfrag = [&](const lds_u8* base, int db, int ks) {
+    const v4i16 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(base + ks * 4096 + toff[db][0]));
+    const v4i16 y = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(base + ks * 4096 + toff[db][1]));
+    typedef short v8i16 __attribute__((ext_vector_type(8)));
+    return __builtin_bit_cast(bf16x8, __builtin_shufflevector(x, y, 0, 1, 2, 3, 4, 5, 6, 7));
+  };
+
   f32x16 dqt[D / 32];
 #pragma unroll
   for (int db = 0; db < D / 32; ++db) dqt[db] = f32x16{};
@@ -388,13 +421,13 @@ __global__ __launch_bounds__(NT, 2) void attn_bwd_dq_kernel(
     const lds_u8* vs_ = ks_ + TILE;
     const int kv0 = kb * BN;
     if (kv0 > q0 + 32 * wave + 31) continue;
-    f32x16 st[2] = {f32x16{}, f32x16{}}, dpt[2] = {f32x16{}, f32x16{}};
+    f32x16 st[2], dpt[2];
 #pragma unroll
     for (int ks = 0; ks < D / 16; ++ks)
 #pragma unroll
       for (int nb = 0; nb < 2; ++nb) {
-        st[nb] = mfma32(row_frag(ks_, 32 * nb + ql, ks, h2), qf[ks], st[nb]);
-        dpt[nb] = mfma32(row_frag(vs_, 32 * nb + ql, ks, h2), df[ks], dpt[nb]);
+        st[nb] = mfma32(rfrag(ks_, ks, nb), qf[ks], ks == 0 ? f32x16{} : st[nb]);
+        dpt[nb] = mfma32(rfrag(vs_, ks, nb), df[ks], ks == 0 ? f32x16{} : dpt[nb]);
       }
     const bool diag = kv0 + BN - 1 > q0 + 32 * wave;  // the block crosses this wave's diagonal
     bf16x8 dsf[4];
@@ -415,7 +448,7 @@ __global__ __launch_bounds__(NT, 2) void attn_bwd_dq_kernel(
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
-      for (int db = 0; db < D / 32; ++db) dqt[db] = mfma32(vt_frag(ks_, 32 * db, ks, lane), dsf[ks], dqt[db]);
+      for (int db = 0; db < D / 32; ++db) dqt[db] = mfma32(tfrag(ks_, db, ks), dsf[ks], dqt[db]);
   }
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
