@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define PLZ_ABI_VERSION 10
+#define PLZ_ABI_VERSION 11
 
 /* status codes */
 #define PLZ_OK 0
@@ -463,6 +463,15 @@ int plz_swiglu_fwd(const uint16_t* gate, const uint16_t* up, uint16_t* h, int64_
                    void* stream);
 int plz_swiglu_bwd(const uint16_t* gate, const uint16_t* up, const uint16_t* grad_h,
                    uint16_t* grad_gate, uint16_t* grad_up, int64_t n, void* stream);
+/* The same on rows x F elements with row pitches in elements (multiples of 8, >= F): gate and up
+ * may sit side by side in one [rows, 2F] tensor (a fused gate/up projection: up = gate + F,
+ * ld_in = 2F), and the gradients likewise. Replaces the HF Qwen3 MLP's act_fn(gate) * up
+ * (transformers models/qwen3/modeling_qwen3.py) and its autograd, as plz_swiglu_fwd/bwd do. */
+int plz_swiglu_fwd_rows(const uint16_t* gate, const uint16_t* up, int64_t ld_in, uint16_t* h,
+                        int64_t ld_h, int64_t rows, int64_t F, void* stream);
+int plz_swiglu_bwd_rows(const uint16_t* gate, const uint16_t* up, int64_t ld_in,
+                        const uint16_t* grad_h, int64_t ld_h, uint16_t* grad_gate,
+                        uint16_t* grad_up, int64_t ld_g, int64_t rows, int64_t F, void* stream);
 
 /* ---- layer step around the linears -------------------------------------------------- */
 /* Rotary position embedding, HF Qwen3 rotate_half convention, fp32 math on bf16:

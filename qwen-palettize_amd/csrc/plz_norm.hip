@@ -212,27 +212,20 @@ __global__ __launch_bounds__(kSumWaves * 64) void sum_blocks_kernel(
 
 __device__ __forceinline__ float silu(float g) { return g / (1.f + __expf(-g)); }
 
-__global__ void swiglu_fwd_kernel(const uint16_t* __restrict__ gate, const uint16_t* __restrict__ up,
-                                  uint16_t* __restrict__ h, int64_t n8) {
-  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= n8) return;
+// 8 consecutive elements: h = bf16(silu(g)) * u, and its gradients
+__device__ __forceinline__ uint4 swiglu_fwd8(uint4 gate, uint4 up) {
   float g[8], u[8], o[8];
-  unpack8(reinterpret_cast<const uint4*>(gate)[t], g);
-  unpack8(reinterpret_cast<const uint4*>(up)[t], u);
+  unpack8(gate, g);
+  unpack8(up, u);
 #pragma unroll
   for (int j = 0; j < 8; ++j) o[j] = swiglu_elem(g[j], u[j]);
-  reinterpret_cast<uint4*>(h)[t] = pack8(o);
+  return pack8(o);
 }
-
-__global__ void swiglu_bwd_kernel(const uint16_t* __restrict__ gate, const uint16_t* __restrict__ up,
-                                  const uint16_t* __restrict__ gh, uint16_t* __restrict__ gg,
-                                  uint16_t* __restrict__ gu, int64_t n8) {
-  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= n8) return;
+__device__ __forceinline__ void swiglu_bwd8(uint4 gate, uint4 up, uint4 gh, uint4& gg, uint4& gu) {
   float g[8], u[8], d[8], og[8], ou[8];
-  unpack8(reinterpret_cast<const uint4*>(gate)[t], g);
-  unpack8(reinterpret_cast<const uint4*>(up)[t], u);
-  unpack8(reinterpret_cast<const uint4*>(gh)[t], d);
+  unpack8(gate, g);
+  unpack8(up, u);
+  unpack8(gh, d);
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const float sg = 1.f / (1.f + __expf(-g[j]));
@@ -240,8 +233,54 @@ __global__ void swiglu_bwd_kernel(const uint16_t* __restrict__ gate, const uint1
     ou[j] = d[j] * s;
     og[j] = d[j] * u[j] * sg * (1.f + g[j] * (1.f - sg));
   }
-  reinterpret_cast<uint4*>(gg)[t] = pack8(og);
-  reinterpret_cast<uint4*>(gu)[t] = pack8(ou);
+  gg = pack8(og);
+  gu = pack8(ou);
+}
+
+__global__ void swiglu_fwd_kernel(const uint16_t* __restrict__ gate, const uint16_t* __restrict__ up,
+                                  uint16_t* __restrict__ h, int64_t n8) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= n8) return;
+  reinterpret_cast<uint4*>(h)[t] =
+      swiglu_fwd8(reinterpret_cast<const uint4*>(gate)[t], reinterpret_cast<const uint4*>(up)[t]);
+}
+
+__global__ void swiglu_bwd_kernel(const uint16_t* __restrict__ gate, const uint16_t* __restrict__ up,
+                                  const uint16_t* __restrict__ gh, uint16_t* __restrict__ gg,
+                                  uint16_t* __restrict__ gu, int64_t n8) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= n8) return;
+  swiglu_bwd8(reinterpret_cast<const uint4*>(gate)[t], reinterpret_cast<const uint4*>(up)[t],
+              reinterpret_cast<const uint4*>(gh)[t], reinterpret_cast<uint4*>(gg)[t],
+              reinterpret_cast<uint4*>(gu)[t]);
+}
+
+// The same on rows x F elements whose operands have their own row pitches (elements, multiples
+// of 8): gate and up side by side in one [rows, 2F] tensor (a fused gate/up projection), h and
+// the gradients wherever the caller keeps them.
+__global__ void swiglu_fwd_rows_kernel(const uint16_t* __restrict__ gate,
+                                       const uint16_t* __restrict__ up, int64_t ld_in,
+                                       uint16_t* __restrict__ h, int64_t ld_h, int64_t rows,
+                                       int64_t f8) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= rows * f8) return;
+  const int64_t r = t / f8, c = (t % f8) * 8;
+  *reinterpret_cast<uint4*>(h + r * ld_h + c) =
+      swiglu_fwd8(*reinterpret_cast<const uint4*>(gate + r * ld_in + c),
+                  *reinterpret_cast<const uint4*>(up + r * ld_in + c));
+}
+__global__ void swiglu_bwd_rows_kernel(const uint16_t* __restrict__ gate,
+                                       const uint16_t* __restrict__ up, int64_t ld_in,
+                                       const uint16_t* __restrict__ gh, int64_t ld_h,
+                                       uint16_t* __restrict__ gg, uint16_t* __restrict__ gu,
+                                       int64_t ld_g, int64_t rows, int64_t f8) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= rows * f8) return;
+  const int64_t r = t / f8, c = (t % f8) * 8;
+  swiglu_bwd8(*reinterpret_cast<const uint4*>(gate + r * ld_in + c),
+              *reinterpret_cast<const uint4*>(up + r * ld_in + c),
+              *reinterpret_cast<const uint4*>(gh + r * ld_h + c),
+              *reinterpret_cast<uint4*>(gg + r * ld_g + c), *reinterpret_cast<uint4*>(gu + r * ld_g + c));
 }
 
 // grad_bias[n] = sum_m grad_y[m, n]: one thread per column, rows in order.
@@ -370,6 +409,37 @@ int plz_swiglu_bwd(const uint16_t* gate, const uint16_t* up, const uint16_t* gra
   hipLaunchKernelGGL(swiglu_bwd_kernel, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0,
                      (hipStream_t)stream, gate, up, grad_h, grad_gate, grad_up, n8);
   return check_launch("plz_swiglu_bwd");
+}
+
+int plz_swiglu_fwd_rows(const uint16_t* gate, const uint16_t* up, int64_t ld_in, uint16_t* h,
+                        int64_t ld_h, int64_t rows, int64_t F, void* stream) {
+  PLZ_REQUIRE(rows >= 0 && F >= 0 && F % 8 == 0 && ld_in % 8 == 0 && ld_h % 8 == 0 &&
+                  ld_in >= F && ld_h >= F,
+              "plz_swiglu_fwd_rows: F and the row pitches must be multiples of 8, pitches >= F");
+  if (rows == 0 || F == 0) return PLZ_OK;
+  PLZ_REQUIRE(gate && up && h && a16(gate) && a16(up) && a16(h),
+              "plz_swiglu_fwd_rows: operands must be non-null and 16-byte aligned");
+  const int64_t n = rows * (F / 8);
+  hipLaunchKernelGGL(swiglu_fwd_rows_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, gate, up, ld_in, h, ld_h, rows, F / 8);
+  return check_launch("plz_swiglu_fwd_rows");
+}
+
+int plz_swiglu_bwd_rows(const uint16_t* gate, const uint16_t* up, int64_t ld_in,
+                        const uint16_t* grad_h, int64_t ld_h, uint16_t* grad_gate,
+                        uint16_t* grad_up, int64_t ld_g, int64_t rows, int64_t F, void* stream) {
+  PLZ_REQUIRE(rows >= 0 && F >= 0 && F % 8 == 0 && ld_in % 8 == 0 && ld_h % 8 == 0 &&
+                  ld_g % 8 == 0 && ld_in >= F && ld_h >= F && ld_g >= F,
+              "plz_swiglu_bwd_rows: F and the row pitches must be multiples of 8, pitches >= F");
+  if (rows == 0 || F == 0) return PLZ_OK;
+  PLZ_REQUIRE(gate && up && grad_h && grad_gate && grad_up && a16(gate) && a16(up) &&
+                  a16(grad_h) && a16(grad_gate) && a16(grad_up),
+              "plz_swiglu_bwd_rows: operands must be non-null and 16-byte aligned");
+  const int64_t n = rows * (F / 8);
+  hipLaunchKernelGGL(swiglu_bwd_rows_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, gate, up, ld_in, grad_h, ld_h, grad_gate, grad_up, ld_g,
+                     rows, F / 8);
+  return check_launch("plz_swiglu_bwd_rows");
 }
 
 int plz_bias_grad(const uint16_t* grad_y, float* grad_bias, int64_t M, int64_t N, void* stream) {

@@ -120,6 +120,8 @@ SIGNATURES: dict[str, tuple] = {
     "plz_rmsnorm_bwd": (i32, [p, p, p, p, p, p, p, sz, i64, i64, p]),
     "plz_swiglu_fwd": (i32, [p, p, p, i64, p]),
     "plz_swiglu_bwd": (i32, [p, p, p, p, p, i64, p]),
+    "plz_swiglu_fwd_rows": (i32, [p, p, i64, p, i64, i64, i64, p]),
+    "plz_swiglu_bwd_rows": (i32, [p, p, i64, p, i64, p, p, i64, i64, i64, p]),
 }
 
 _lib = None

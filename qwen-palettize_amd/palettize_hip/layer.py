@@ -86,6 +86,21 @@ class RMSNorm(nn.Module):
         return RMSNormFunction.apply(x, self.weight, self.eps)
 
 
+class SwiGLUCatFunction(torch.autograd.Function):
+    """h = silu(gate) * up from a fused projection's output [..., 2F] = [gate | up]."""
+
+    @staticmethod
+    def forward(ctx, gate_up):
+        gate_up = gate_up.contiguous()
+        ctx.save_for_backward(gate_up)
+        return ops.swiglu_fwd_cat(gate_up)
+
+    @staticmethod
+    def backward(ctx, gh):
+        (gate_up,) = ctx.saved_tensors
+        return ops.swiglu_bwd_cat(gate_up, gh.contiguous())
+
+
 class SwiGLUFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx, gate, up):
@@ -193,6 +208,153 @@ class SoftPalettizedLinear(nn.Module):
         return y.reshape(*lead, self.out_features)
 
 
+class SoftLinearGroup:
+    """Sibling soft linears on the same input (the MLP's gate and up) run as one soft linear over
+    their concatenated output rows: one build-W descriptor, one dense GEMM whose LoRA stage takes
+    the parts' A stacked ([sum r, K]) and their B block-diagonal ([sum N, sum r], zeros off the
+    blocks), and one soft backward whose LoRA weight gradients come out of the same dW tiles.
+    Row n of the group is row n of its part, with that part's logits, palette and LoRA, so the
+    result is the parts' own linears; the difference is scheduling: the fused dW GEMM has
+    enough output tiles to fill the GPU without splitting its reduction (for gate and up at
+    hidden 2560: 760 tiles instead of twice 380), which saves the split's fp32 partials and
+    second pass, and the LoRA and grad_x work runs once.
+
+    The parts keep their parameters (state_dict names, optimizer groups), re-homed as row
+    slices of one storage each for the logits, the palettes and the LoRA A, so the group reads
+    them without copies; a part whose parameter was replaced rather than written in place is
+    concatenated instead. The noise is one Philox stream over the group's rows (part 0's key at
+    the shared counter offset): part p's rows continue part p-1's counters, which each part's
+    noise_seed / noise_counter report, so part p alone would draw the same values.
+    """
+
+    def __init__(self, parts):
+        if len(parts) < 2:
+            raise ValueError("a group needs at least two linears")
+        K = parts[0].in_features
+        if any(p.in_features != K for p in parts):
+            raise ValueError("grouped linears must share their input")
+        self.parts = list(parts)
+        self.rows = [p.out_features for p in parts]
+        self.ranks = [p.lora_a.shape[0] for p in parts]
+        self.N, self.K, self.R = sum(self.rows), K, sum(self.ranks)
+        if len({p.lora_scale for p in parts}) != 1:
+            raise ValueError("grouped linears must share the LoRA scale")
+        if any(n % 256 for n in self.rows[:-1]):
+            raise ValueError("every part but the last must have a multiple of 256 rows")
+        for attr in ("index_logits", "palette", "lora_a"):
+            base = torch.cat([getattr(p, attr).detach() for p in parts], 0).contiguous()
+            r = 0
+            for p in parts:
+                n = getattr(p, attr).shape[0]
+                setattr(p, attr, nn.Parameter(base[r:r + n]))
+                r += n
+        seed = parts[0].noise_seed
+        for p in parts:
+            p.noise_seed = seed
+        self._sync_counters()
+        dev = parts[0].lora_b.device
+        self._b_bd = torch.zeros(self.N, self.R, dtype=torch.bfloat16, device=dev)
+
+    def _sync_counters(self):
+        c = self.parts[0].noise_counter
+        for p, n in zip(self.parts, self.rows):
+            p.noise_counter = c
+            c += n * self.K
+
+    @property
+    def lora_scale(self):
+        return self.parts[0].lora_scale
+
+    @staticmethod
+    def _rows_of(tensors):
+        """The row-stacked tensor of `tensors`: a view when they are consecutive row slices of
+        one storage, else a copy."""
+        t0 = tensors[0]
+        es = t0.element_size()
+        ptr = t0.data_ptr()
+        for t in tensors:
+            if not t.is_contiguous() or t.data_ptr() != ptr or t.dtype != t0.dtype:
+                return torch.cat([x.detach() for x in tensors], 0)
+            ptr += t.numel() * es
+        rows = sum(t.shape[0] for t in tensors)
+        return torch.as_strided(t0.detach(), (rows,) + tuple(t0.shape[1:]), t0.stride())
+
+    def logits(self):
+        return self._rows_of([p.index_logits for p in self.parts])
+
+    def palette(self):
+        return self._rows_of([p.palette for p in self.parts])
+
+    def lora_a(self):
+        return self._rows_of([p.lora_a for p in self.parts])
+
+    def lora_b(self):
+        """The block-diagonal B [sum N, sum r] of this forward (its own buffer, off-block zeros)."""
+        r0 = c0 = 0
+        for p, n, r in zip(self.parts, self.rows, self.ranks):
+            self._b_bd[r0:r0 + n, c0:c0 + r].copy_(p.lora_b.detach())
+            r0 += n
+            c0 += r
+        return self._b_bd
+
+    def next_noise_spec(self):
+        spec = self.parts[0].next_noise_spec()
+        for p in self.parts[1:]:
+            p.next_noise_spec()
+        self._sync_counters()
+        return spec
+
+    def forward(self, x, prebuilt):
+        _gpu_bf16(x, "SoftLinearGroup input")
+        lead = x.shape[:-1]
+        params = []
+        for p in self.parts:
+            params += [p.palette, p.index_logits, p.lora_a, p.lora_b]
+        y = SoftLinearGroupFunction.apply(x.reshape(-1, x.shape[-1]), self, prebuilt, *params)
+        return y.reshape(*lead, self.N)
+
+
+class SoftLinearGroupFunction(torch.autograd.Function):
+    """Autograd of SoftLinearGroup: inputs x, the group, the prebuilt (w, build group, noise) of
+    this forward, then per part palette, logits, lora_a, lora_b; every part's gradients are row
+    slices of the fused ones (grad_B the part's diagonal block)."""
+
+    @staticmethod
+    def forward(ctx, x, grp, prebuilt, *params):
+        x = x.contiguous()
+        w, build, noise = prebuilt
+        ctx.guard = (build, build.generation)
+        a, b = grp.lora_a(), grp.lora_b()
+        t = ops.lora_project(x, a, grp.lora_scale)
+        y = ops.linear_fwd_dense(x, w, None, t, b)
+        ctx.grp, ctx.noise, ctx.tau = grp, noise, float(grp.parts[0].tau)
+        ctx.save_for_backward(x, grp.palette(), grp.logits(), w, a, b.clone())
+        return y
+
+    @staticmethod
+    def backward(ctx, gy):
+        x, pal, logits, w, a, b = ctx.saved_tensors
+        grp = ctx.grp
+        if ctx.guard[0].generation != ctx.guard[1]:
+            raise RuntimeError("the prebuilt soft weight of this forward was rebuilt by a later "
+                               "forward before this backward ran")
+        gy = gy.contiguous()
+        scale = grp.lora_scale
+        grad_x = None
+        if ctx.needs_input_grad[0]:
+            gt = ops.lora_grad_t(gy, b, scale)
+            grad_x = ops.linear_bwd_x_dense(gy, w, gt, a)
+        gl, gp, ga, gb = ops.soft_bwd_lora(x, gy, logits, ctx.noise, pal, ctx.tau, a, b, scale,
+                                           False, out_dtype=a.dtype)
+        grads = []
+        r0 = c0 = 0
+        for n, r in zip(grp.rows, grp.ranks):
+            grads += [gp[r0:r0 + n], gl[r0:r0 + n], ga[c0:c0 + r], gb[r0:r0 + n, c0:c0 + r].contiguous()]
+            r0 += n
+            c0 += r
+        return (grad_x, None, None, *grads)
+
+
 # ---- RoPE / attention -------------------------------------------------------------------------
 def rope_tables(seq, head_dim, theta, device):
     inv = 1.0 / (theta ** (torch.arange(0, head_dim, 2, device=device, dtype=torch.float32) / head_dim))
@@ -271,7 +433,7 @@ def attention(q, k, v, heads, kv_heads):
 class PalettizedDecoderLayer(nn.Module):
     NAMES = ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj")
 
-    def __init__(self, cfg: LayerConfig, seed=0, device=None, lora_b_std=0.0):
+    def __init__(self, cfg: LayerConfig, seed=0, device=None, lora_b_std=0.0, fuse_gate_up=True):
         super().__init__()
         self.cfg = cfg
         h, hd = cfg.hidden, cfg.head_dim
@@ -289,33 +451,56 @@ class PalettizedDecoderLayer(nn.Module):
         self.post_attention_layernorm = RMSNorm(h, cfg.eps, device)
         self.q_norm = RMSNorm(hd, cfg.eps, device)
         self.k_norm = RMSNorm(hd, cfg.eps, device)
+        # gate and up as one soft linear over their concatenated rows (SoftLinearGroup): its LoRA
+        # weight gradients come from the soft backward's dW tiles, which take ranks up to 32
+        self.gate_up = None
+        if fuse_gate_up and cfg.intermediate % 256 == 0 and 2 * cfg.lora_rank in (8, 16, 24, 32):
+            self.gate_up = SoftLinearGroup([self.gate_proj, self.up_proj])
         self._wgroup = None
         self._wgroup_key = None
 
     def linears(self):
         return [getattr(self, n) for n in self.NAMES]
 
+    def _units(self):
+        """(name, linear or group) in build order: the gate/up group stands for both."""
+        out = []
+        for n in self.NAMES:
+            if self.gate_up is not None and n in ("gate_proj", "up_proj"):
+                if n == "gate_proj":
+                    out.append(("gate_up", self.gate_up))
+                continue
+            out.append((n, getattr(self, n)))
+        return out
+
     def build_weights(self):
-        """The seven linears' forward weights in one launch (plz_soft_build_w_batched_philox):
-        each linear's own Philox key at the shared counter offset of this forward, the same
-        tau. Returns {name: (w, group, noise)} for the linears' forward."""
+        """The linears' forward weights in one launch (plz_soft_build_w_batched_philox): each
+        linear's (or group's) own Philox key at the shared counter offset of this forward, the
+        same tau. Returns {name: (w, group, noise)} for the forward, with "gate_up" for the
+        grouped gate and up."""
+        units = self._units()
         lins = self.linears()
+        items = []
+        for _, u in units:
+            if isinstance(u, SoftLinearGroup):
+                items.append((u.logits(), ops.PhiloxNoise(u.parts[0].noise_seed, 0), u.palette()))
+            else:
+                items.append((u.index_logits, ops.PhiloxNoise(u.noise_seed, 0), u.palette))
         # the group's descriptor table holds the parameters' device addresses: rebuild it when a
         # parameter has been replaced rather than written in place (module.to(),
         # load_state_dict(assign=True), param.data = ...)
-        key = tuple((t.data_ptr(), t.device) for l in lins for t in (l.index_logits, l.palette))
+        key = tuple((t.data_ptr(), t.device) for lg, _, pal in items for t in (lg, pal))
         if self._wgroup is None or self._wgroup_key != key:
-            self._wgroup = ops.SoftBuildGroup(
-                [(l.index_logits, ops.PhiloxNoise(l.noise_seed, 0), l.palette) for l in lins],
-                PLZ_W_HARD_NOISY)
+            self._wgroup = ops.SoftBuildGroup(items, PLZ_W_HARD_NOISY)
             self._wgroup_key = key
-        offset = lins[0].noise_counter
-        if any(l.noise_counter != offset or l.mode != PLZ_W_HARD_NOISY or l.tau != lins[0].tau
-               for l in lins):
+        first = [u.parts[0] if isinstance(u, SoftLinearGroup) else u for _, u in units]
+        offset = first[0].noise_counter
+        if any(l.noise_counter != offset for l in first) or any(
+                l.mode != PLZ_W_HARD_NOISY or l.tau != lins[0].tau for l in lins):
             raise RuntimeError("batched build: the linears must share noise offset, mode and tau")
-        specs = [l.next_noise_spec() for l in lins]
+        specs = [u.next_noise_spec() for _, u in units]
         outs = self._wgroup.run(lins[0].tau, offset)
-        return {n: (w, self._wgroup, sp) for n, (w, _), sp in zip(self.NAMES, outs, specs)}
+        return {n: (w, self._wgroup, sp) for (n, _), (w, _), sp in zip(units, outs, specs)}
 
     def forward(self, hs, cos, sin):
         cfg = self.cfg
@@ -328,9 +513,11 @@ class PalettizedDecoderLayer(nn.Module):
         q, k = apply_rope(q, cos, sin), apply_rope(k, cos, sin)
         hs = hs + self.o_proj(attention(q, k, v, cfg.heads, cfg.kv_heads), pw["o_proj"])
         x = self.post_attention_layernorm(hs)
-        mlp = self.down_proj(SwiGLUFunction.apply(self.gate_proj(x, pw["gate_proj"]),
-                                                  self.up_proj(x, pw["up_proj"])), pw["down_proj"])
-        return hs + mlp
+        if self.gate_up is not None:
+            h = SwiGLUCatFunction.apply(self.gate_up.forward(x, pw["gate_up"]))
+        else:
+            h = SwiGLUFunction.apply(self.gate_proj(x, pw["gate_proj"]), self.up_proj(x, pw["up_proj"]))
+        return hs + self.down_proj(h, pw["down_proj"])
 
 
 class DenseDecoderLayer(nn.Module):
@@ -406,10 +593,12 @@ def tau_at(step, tau_init=2.0, tau_final=0.5, warmup=500, anneal=6000):
 class LayerTrainer:
     """Owns a student/teacher pair and runs config-5 training steps."""
 
-    def __init__(self, cfg: LayerConfig, device, lrs=None, seed=0, lora_b_std=0.0):
+    def __init__(self, cfg: LayerConfig, device, lrs=None, seed=0, lora_b_std=0.0,
+                 fuse_gate_up=True):
         self.cfg = cfg
         self.device = device
-        self.student = PalettizedDecoderLayer(cfg, seed=seed, device=device, lora_b_std=lora_b_std)
+        self.student = PalettizedDecoderLayer(cfg, seed=seed, device=device, lora_b_std=lora_b_std,
+                                              fuse_gate_up=fuse_gate_up)
         self.teacher = DenseDecoderLayer(cfg, seed=seed + 1, device=device)
         lrs = lrs or {"palettes": 1e-4, "lora": 3e-4, "indices": 1e-2}
         pal, lora, logits = [], [], []

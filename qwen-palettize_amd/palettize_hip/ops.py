@@ -769,6 +769,35 @@ def swiglu_bwd(gate, up, grad_h):
     return gg, gu
 
 
+def swiglu_fwd_cat(gate_up):
+    """h [..., F] = silu(gate) * up from a fused projection's output [..., 2F] = [gate | up]."""
+    _need(gate_up, "gate_up", torch.bfloat16)
+    F2 = gate_up.shape[-1]
+    if F2 % 16:
+        raise ValueError("gate_up: the last dimension must be 2F with F a multiple of 8")
+    F = F2 // 2
+    g = gate_up.reshape(-1, F2)
+    h = torch.empty(gate_up.shape[:-1] + (F,), dtype=torch.bfloat16, device=gate_up.device)
+    call("plz_swiglu_fwd_rows", _ptr(g), _ptr(g) + 2 * F, F2, _ptr(h), F, g.shape[0], F,
+         _stream(gate_up))
+    return h
+
+
+def swiglu_bwd_cat(gate_up, grad_h):
+    """[grad_gate | grad_up] [..., 2F] of swiglu_fwd_cat for the gradient grad_h [..., F]."""
+    _need(gate_up, "gate_up", torch.bfloat16)
+    _need(grad_h, "grad_h", torch.bfloat16)
+    F2 = gate_up.shape[-1]
+    F = F2 // 2
+    if F2 % 16 or tuple(grad_h.shape) != tuple(gate_up.shape[:-1]) + (F,):
+        raise ValueError("gate_up [..., 2F] and grad_h [..., F] expected, F a multiple of 8")
+    g = gate_up.reshape(-1, F2)
+    out = torch.empty_like(g)
+    call("plz_swiglu_bwd_rows", _ptr(g), _ptr(g) + 2 * F, F2, _ptr(grad_h), F, _ptr(out),
+         _ptr(out) + 2 * F, F2, g.shape[0], F, _stream(gate_up))
+    return out.reshape(gate_up.shape)
+
+
 # ---- layer step: RoPE and the distillation loss ----------------------------------------------
 def _rope(name, x, cos, sin):
     _need(x, "x", torch.bfloat16)

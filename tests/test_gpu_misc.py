@@ -74,6 +74,25 @@ def test_swiglu(dev):
     assert_close(f32(gu), wu, what="swiglu grad_up")
 
 
+def test_swiglu_concatenated_layout(dev):
+    """The fused gate/up projection's layout [rows, 2F] = [gate | up]: swiglu_fwd_cat and
+    swiglu_bwd_cat are bit for bit the flat kernels on the separated halves, and the oracle's
+    SwiGLU holds for them as for the flat ones."""
+    rows, F = 96, 520
+    gu = torch.cat([randn_bf16(rows, F, seed=11, std=3.0), randn_bf16(rows, F, seed=12)], 1)
+    g, u = gu[:, :F].contiguous(), gu[:, F:].contiguous()
+    h = ops.swiglu_fwd_cat(gu.to(dev))
+    assert torch.equal(h, ops.swiglu_fwd(g.to(dev), u.to(dev)))
+    want = O.swiglu_fwd(f32(g), f32(u))
+    assert np.all(np.abs(f32(h) - want) <= np.abs(want) * 2.0 ** -7)
+    gh = randn_bf16(rows, F, seed=13)
+    grad = ops.swiglu_bwd_cat(gu.to(dev), gh.to(dev))
+    gg, gup = ops.swiglu_bwd(g.to(dev), u.to(dev), gh.to(dev))
+    assert torch.equal(grad[:, :F], gg) and torch.equal(grad[:, F:], gup)
+    with pytest.raises(ValueError):
+        ops.swiglu_bwd_cat(gu.to(dev), gh[:, :-8].contiguous().to(dev))
+
+
 @pytest.mark.parametrize("M,r,train_pal", [(256, 16, True), (4096, 16, True), (4096, 32, False)])
 def test_lut_linear_autograd_with_lora(dev, M, r, train_pal):
     """From 4096 rows the forward dequantises W once and grad_x reuses it; with the palette
