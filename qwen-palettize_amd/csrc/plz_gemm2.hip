@@ -516,20 +516,67 @@ __device__ __forceinline__ void mma_stage_lutreg(const lds_u8* __restrict__ a_s,
 //   grad_logits[n, k, c] = glog_scale * dW * P_c * (palette_c - W_soft)   (W_soft = sum_c P_c palette_c)
 // and the segment's P-weighted class sums of dW to partial[n][kseg/128][4] (the palette
 // gradient before the sum over the group's two segments): fused_lut_kernel.cu:1877-1924.
-__device__ __forceinline__ void soft_item(const Args& g, int64_t n, int64_t kseg, int lane,
-                                          float2 gw) {
+// The item's operands (palette row, logits, tensor noise) are loaded by soft_load, separately
+// from the math, so a loop over items can issue the next item's loads before this one's math.
+struct SoftIn {
+  float4 pal;
+  uint4 lg;
+  float4 z0, z1;  // tensor noise of the lane's two weights (unused with Philox noise)
+};
+__device__ __forceinline__ SoftIn soft_load(const Args& g, int64_t n, int64_t kseg, int lane) {
+  const int64_t k = kseg + 2 * lane, e0 = (n * g.J + k) * 4;
+  SoftIn in;
+  in.pal = *reinterpret_cast<const float4*>(g.pal + (n * (g.J / 256) + k / 256) * 4);
+  in.lg = *reinterpret_cast<const uint4*>(g.logits + e0);
+  if (g.noise) {
+    in.z0 = *reinterpret_cast<const float4*>(g.noise + e0);
+    in.z1 = *reinterpret_cast<const float4*>(g.noise + e0 + 4);
+  }
+  return in;
+}
+
+// Sum of four per-lane values over the wave, one class per 16-lane row: on return lane l holds
+// the total of class l / 16. Each step halves the values a lane carries: lanes 0-31 keep classes
+// 0, 1 and take lanes 32-63's (v_permlane32_swap: lane l <-> l + 32 in one VALU instruction),
+// then each 16-lane half keeps one class (v_permlane16_swap), then a row sums its 16 lanes by
+// DPP rotations (8, 4, 2, 1). No LDS traffic, 10 VALU instructions against 24 lane shuffles.
+__device__ __forceinline__ float swap32_sum(float lo, float hi) {
+  // lanes 0-31: lo[l] + lo[l + 32];  lanes 32-63: hi[l - 32] + hi[l]
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(lo), __float_as_uint(hi), false,
+                                                  false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float swap16_sum(float lo, float hi) {
+  // within each 32-lane half: lanes 0-15 lo[l] + lo[l + 16];  lanes 16-31 hi[l - 16] + hi[l]
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(lo), __float_as_uint(hi), false,
+                                                  false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_add(float v) {
+  return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF,
+                                                        false));
+}
+__device__ __forceinline__ float wave_sum4(const float (&sp)[4]) {
+  const float a = swap32_sum(sp[0], sp[2]);  // class 0 (lanes 0-31) / class 2 (lanes 32-63)
+  const float b = swap32_sum(sp[1], sp[3]);  // class 1 / class 3
+  float q = swap16_sum(a, b);                // class l / 16, over lanes l % 16 + 16 j
+  q = dpp_add<0x128>(q);                     // row_ror:8
+  q = dpp_add<0x124>(q);                     // row_ror:4
+  q = dpp_add<0x122>(q);                     // row_ror:2
+  return dpp_add<0x121>(q);                  // row_ror:1
+}
+
+__device__ __forceinline__ void soft_math(const Args& g, int64_t n, int64_t kseg, int lane,
+                                          float2 gw, const SoftIn& in) {
   const int64_t k = kseg + 2 * lane;
-  const float4 pal = *reinterpret_cast<const float4*>(g.pal + (n * (g.J / 256) + k / 256) * 4);
-  const float pc[4] = {pal.x, pal.y, pal.z, pal.w};
+  const float pc[4] = {in.pal.x, in.pal.y, in.pal.z, in.pal.w};
   const int64_t e0 = (n * g.J + k) * 4;
-  const uint4 lg = *reinterpret_cast<const uint4*>(g.logits + e0);
-  const uint32_t lw[4] = {lg.x, lg.y, lg.z, lg.w};
+  const uint32_t lw[4] = {in.lg.x, in.lg.y, in.lg.z, in.lg.w};
   float nz[8];
   if (g.noise) {
-    const float4 z0 = *reinterpret_cast<const float4*>(g.noise + e0);
-    const float4 z1 = *reinterpret_cast<const float4*>(g.noise + e0 + 4);
-    nz[0] = z0.x; nz[1] = z0.y; nz[2] = z0.z; nz[3] = z0.w;
-    nz[4] = z1.x; nz[5] = z1.y; nz[6] = z1.z; nz[7] = z1.w;
+    nz[0] = in.z0.x; nz[1] = in.z0.y; nz[2] = in.z0.z; nz[3] = in.z0.w;
+    nz[4] = in.z1.x; nz[5] = in.z1.y; nz[6] = in.z1.z; nz[7] = in.z1.w;
   } else {  // the noise the forward drew: Philox at noise_offset + n*K + k
     float z[4];
     philox_gumbel4(g.noise_seed, g.noise_offset + (uint64_t)(n * g.J + k), z);
@@ -574,14 +621,8 @@ __device__ __forceinline__ void soft_item(const Args& g, int64_t n, int64_t kseg
     out[2 * el + 1] = o16[2] | (o16[3] << 16);
   }
   *reinterpret_cast<uint4*>(g.grad_logits + e0) = make_uint4(out[0], out[1], out[2], out[3]);
-#pragma unroll
-  for (int c = 0; c < 4; ++c)
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) sp[c] += __shfl_xor(sp[c], off);
-  if (lane == 0) {
-    float* dst = g.partial + (n * (g.J / 128) + kseg / 128) * 4;
-    *reinterpret_cast<float4*>(dst) = make_float4(sp[0], sp[1], sp[2], sp[3]);
-  }
+  const float tot = wave_sum4(sp);
+  if ((lane & 15) == 0) g.partial[(n * (g.J / 128) + kseg / 128) * 4 + (lane >> 4)] = tot;
 }
 
 __device__ __forceinline__ void tile_of(const Args& g, int bid, int& tile_i, int& tile_j) {
@@ -1099,16 +1140,44 @@ __global__ __launch_bounds__(NTHR) void gemm2_kernel(const Args g) {
       // with the LoRA weight gradients, waves 4..7 take grad_B's share of the staged half: beside
       // the four waves that store the F32 items (cheap), after all eight walked the soft ones
       const int walkers = wgrad && EPI == EPI_F32 ? 4 : NTHR / 64;
-      for (int item = wave; wave < walkers && item < 256; item += walkers) {
-        const int row = item >> 1, h = item & 1;
-        const int64_t n = i0 + (row >> 6) * 128 + 64 * half + (row & 63);
-        const int64_t kseg = j0 + 128 * h;
-        if (n >= g.I || kseg >= g.J) continue;
-        const float2 gw = *reinterpret_cast<const float2*>(&sC[ptile(row, 128 * h + 2 * lane)]);
-        if (EPI == EPI_SOFT)
-          soft_item(g, n, kseg, lane, gw);
-        else  // this split's partial dW rows, [split][N][K] fp32
+      // item -> (row n, segment kseg); false past the tile's 256 items or the matrix edge
+      auto item_at = [&](int item, int64_t& n, int64_t& kseg) {
+        const int row = item >> 1;
+        n = i0 + (row >> 6) * 128 + 64 * half + (row & 63);
+        kseg = j0 + 128 * (item & 1);
+        return item < 256 && n < g.I && kseg < g.J;
+      };
+      if (EPI == EPI_SOFT) {
+        // each wave's items in turn, the next item's logits / palette / noise loads issued
+        // before this item's math, so their latency is covered by it
+        int64_t n, kseg;
+        bool live = item_at(wave, n, kseg);
+        SoftIn cur;
+        if (live) cur = soft_load(g, n, kseg, lane);
+        for (int item = wave; item < 256; item += walkers) {
+          int64_t n2, k2;
+          const bool live2 = item_at(item + walkers, n2, k2);
+          SoftIn nxt = cur;
+          if (live2) nxt = soft_load(g, n2, k2, lane);
+          if (live) {
+            const float2 gw =
+                *reinterpret_cast<const float2*>(&sC[ptile(item >> 1, 128 * (item & 1) + 2 * lane)]);
+            soft_math(g, n, kseg, lane, gw, cur);
+          }
+          cur = nxt;
+          live = live2;
+          n = n2;
+          kseg = k2;
+        }
+      } else {
+        for (int item = wave; wave < walkers && item < 256; item += walkers) {
+          int64_t n, kseg;
+          if (!item_at(item, n, kseg)) continue;
+          const float2 gw =
+              *reinterpret_cast<const float2*>(&sC[ptile(item >> 1, 128 * (item & 1) + 2 * lane)]);
+          // this split's partial dW rows, [split][N][K] fp32
           *reinterpret_cast<float2*>(g.acc_ws + ((int64_t)zsl * g.I + n) * g.J + kseg + 2 * lane) = gw;
+        }
       }
       if (wgrad && threadIdx.x >= 256)
         lora_grad_b(g, sC, lbase, i0, half, zsl, tile_j, wave - 4, lane);
@@ -1125,6 +1194,7 @@ __global__ __launch_bounds__(256) void soft_split_epilogue_kernel(const Args g, 
   const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);  // wave-uniform
   if (item >= g.I * segs) return;
   const int64_t n = item / segs, kseg = (item % segs) * 128;
+  const SoftIn in = soft_load(g, n, kseg, lane);  // issued beside the partial loads
   const float* p = g.acc_ws + n * g.J + kseg + 2 * lane;
   float2 gw = make_float2(0.f, 0.f);
   for (int z = 0; z < Z; ++z) {
@@ -1132,7 +1202,7 @@ __global__ __launch_bounds__(256) void soft_split_epilogue_kernel(const Args g, 
     gw.x += v.x;
     gw.y += v.y;
   }
-  soft_item(g, n, kseg, lane, gw);
+  soft_math(g, n, kseg, lane, gw, in);
 }
 
 // Tail tiles of a split launch: sum each tile's reduction parts in part order (deterministic)
