@@ -48,8 +48,16 @@ __device__ __forceinline__ void copy_col_tile_masked(uint4* lds, const uint16_t*
   }
 }
 
-__device__ __forceinline__ int ptile(int row, int col) {  // 128 x 256 fp32 staging tile
-  return row * 256 + ((((col >> 2) ^ (row & 63))) << 2) + (col & 3);
+// 128 x 256 fp32 staging tile: 16-byte group g = col / 4 of a row at g ^ key, a bijection per
+// row (key changes bits 4-5 of g only through row). The key makes each access pattern of the dW
+// epilogues conflict-free on the 64 banks:
+//   staging writes (a half-wave per row, rows r and r + 4 side by side): bit 3 follows row bit 2;
+//   class sums (16 lanes = 4 rows x 4 groups 16 apart, 16-byte reads): bits 2-3 follow g bits 4-5;
+//   soft / F32 items and the LoRA grad_B reads: one group per lane pair or per row.
+__device__ __forceinline__ int ptile(int row, int col) {
+  const int g = col >> 2;
+  const int key = (row & 63) ^ (((row >> 2) & 1) << 3) ^ (((g >> 4) & 3) << 2);
+  return row * 256 + ((g ^ key) << 2) + (col & 3);
 }
 
 // ---- LoRA weight gradients from a dW tile (EPI_PAL / EPI_SOFT / EPI_F32 with g.wg_r > 0) ---
