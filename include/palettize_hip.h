@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define PLZ_ABI_VERSION 11
+#define PLZ_ABI_VERSION 12
 
 /* status codes */
 #define PLZ_OK 0
@@ -485,6 +485,21 @@ int plz_rope_fwd(const uint16_t* x, const float* cos_table, const float* sin_tab
 int plz_rope_bwd(const uint16_t* grad_y, const float* cos_table, const float* sin_table,
                  uint16_t* grad_x, int64_t rows, int64_t seq, int heads, int head_dim,
                  void* stream);
+/* Per-head RMSNorm followed by the rotary embedding, in one pass: for each of the rows x heads
+ * vectors of 128 (x bf16 [rows, heads, 128], rows = tokens, pos = row % seq),
+ * y = rope(rmsnorm(x, weight, eps)) with the values of plz_rmsnorm_fwd then plz_rope_fwd (bit for
+ * bit), rstd fp32 [rows * heads] (optional) as plz_rmsnorm_fwd saves it. Replaces the q_norm /
+ * k_norm + apply_rotary_pos_emb pair of the HF Qwen3 attention the reference's layers run
+ * (transformers models/qwen3/modeling_qwen3.py, through qwen_model.py:590). */
+int plz_head_norm_rope_fwd(const uint16_t* x, const uint16_t* weight, const float* cos_table,
+                           const float* sin_table, uint16_t* y, float* rstd, int64_t rows,
+                           int64_t seq, int heads, int head_dim, float eps, void* stream);
+/* Its backward for grad_x (plz_rope_bwd then plz_rmsnorm_bwd, bit for bit); the norm weight's
+ * gradient is not formed, for callers whose norm weights are frozen. */
+int plz_head_norm_rope_bwd(const uint16_t* x, const uint16_t* weight, const float* rstd,
+                           const float* cos_table, const float* sin_table, const uint16_t* grad_y,
+                           uint16_t* grad_x, int64_t rows, int64_t seq, int heads, int head_dim,
+                           void* stream);
 /* Causal grouped-query attention forward (flash-style): q, o bf16 [batch, seq, heads, 128],
  * k, v bf16 [batch, seq, kv_heads, 128], heads % kv_heads == 0, seq % 128 == 0;
  * o = softmax(q k^T * scale, causal) v per head (kv head = head / (heads / kv_heads)),

@@ -83,6 +83,29 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_kernel(const uint16_t* __rest
   }
 }
 
+// Pieces of the norm backward for one 8-column chunk, each product and sum rounded on its own
+// (no contraction), so that every kernel that forms them (this one and the fused per-head norm +
+// RoPE below) produces the same bits: dot += (g w) (x r), and r ((g w) - (x r) dot).
+__device__ __forceinline__ float norm_bwd_dot(const float f[8], const float g[8], const float w[8],
+                                              float r, float dot) {
+#pragma clang fp contract(off)
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float h = f[j] * r, t = g[j] * w[j];
+    dot = dot + t * h;
+  }
+  return dot;
+}
+__device__ __forceinline__ void norm_bwd_out(const float f[8], const float g[8], const float w[8],
+                                             float r, float dot, float o[8]) {
+#pragma clang fp contract(off)
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float h = f[j] * r, t = g[j] * w[j];
+    o[j] = r * (t - h * dot);
+  }
+}
+
 // Backward. With h = x r, g = grad_y * w (fp32):
 //   grad_x = r * (g - h * mean(g * h)),  grad_w = sum_rows grad_y * bf16(h)
 // Each workgroup takes a strided set of row groups, U groups per iteration (their loads are
@@ -137,12 +160,10 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(
           unpack8(xv[u][i], f);
           unpack8(gv[u][i], g);
           unpack8(wr[c], w);
+          dot = norm_bwd_dot(f, g, w, r, dot);
 #pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            const float h = f[j] * r;
-            dot += g[j] * w[j] * h;
-            gw[i][j] += g[j] * bf2f(f2bf(h));  // zero for a missing row (g = 0)
-          }
+          for (int j = 0; j < 8; ++j)
+            gw[i][j] += g[j] * bf2f(f2bf(f[j] * r));  // zero for a missing row (g = 0)
         }
       }
       dot = row_sum<LPR>(dot) / (float)cols;
@@ -156,8 +177,7 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(
             unpack8(xv[u][i], f);
             unpack8(gv[u][i], g);
             unpack8(wr[c], w);
-#pragma unroll
-            for (int j = 0; j < 8; ++j) o[j] = r * (g[j] * w[j] - f[j] * r * dot);
+            norm_bwd_out(f, g, w, r, dot, o);
             outr[c] = pack8(o);
           }
         }
@@ -291,6 +311,125 @@ __global__ void bias_grad_kernel(const uint16_t* __restrict__ gy, float* __restr
   float s = 0.f;
   for (int64_t m = 0; m < M; ++m) s += bf2f(gy[m * N + n]);
   gb[n] = s;
+}
+
+// ---- per-head RMSNorm + RoPE (q_norm / k_norm then apply_rotary_pos_emb) ----------------
+// HF Qwen3 attention normalises each head's 128 query / key values (Qwen3RMSNorm) and then
+// rotates them (apply_rotary_pos_emb, rotate_half convention). One 16-lane DPP row per (token,
+// head): lane l holds columns 8 l .. 8 l + 7, and the rotation partner of column j < 64,
+// column j + 64, sits in lane l ^ 8 (row_ror:8). Every value is computed exactly as the
+// separate kernels compute it (rmsnorm_fwd_kernel<16, 1> then rope_kernel, and rope_kernel<true>
+// then rmsnorm_bwd_kernel<16, 1, U>), so the fused pair is bit-identical to them; the norm's own
+// weight gradient is not formed (the layer's per-head norms are frozen).
+constexpr int HNR_D = 128;
+__device__ __forceinline__ uint32_t dpp_ror8(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xF, 0xF, false);
+}
+__device__ __forceinline__ uint4 dpp_ror8(uint4 v) {
+  return make_uint4(dpp_ror8(v.x), dpp_ror8(v.y), dpp_ror8(v.z), dpp_ror8(v.w));
+}
+__device__ __forceinline__ void load8(const float* p, float f[8]) {
+  const float4 a = reinterpret_cast<const float4*>(p)[0], b = reinterpret_cast<const float4*>(p)[1];
+  f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
+  f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+}
+
+// rows = tokens x heads rows of 128; the position of row t is (t / heads) % S
+__global__ __launch_bounds__(256) void head_norm_rope_fwd_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ wt, const float* __restrict__ cosv,
+    const float* __restrict__ sinv, uint16_t* __restrict__ y, float* __restrict__ rstd,
+    int64_t rows, int64_t S, int heads, float eps) {
+  const int lane = threadIdx.x & 63, sub = lane >> 4, l = lane & 15;
+  const int64_t row = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 4 + sub;
+  const bool valid = row < rows;  // a missing row's 16 lanes compute on zeros together
+  const uint4 xv = valid ? reinterpret_cast<const uint4*>(x + row * HNR_D)[l] : make_uint4(0, 0, 0, 0);
+  float f[8];
+  unpack8(xv, f);
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) ss += f[j] * f[j];
+  ss = row_sum<16>(ss);
+  const float r = rsqrtf(ss / (float)HNR_D + eps);
+  float w[8], o[8];
+  unpack8(reinterpret_cast<const uint4*>(wt)[l], w);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) o[j] = w[j] * bf2f(f2bf(f[j] * r));
+  const uint4 nv = pack8(o);            // the norm's bf16 output
+  const uint4 pv = dpp_ror8(nv);        // the partner lane's
+  if (!valid) return;
+  if (l == 0 && rstd) rstd[row] = r;
+  const int64_t pos = (row / heads) % S;
+  float n[8], pn[8], c[8], sn[8], out[8];
+  unpack8(nv, n);
+  unpack8(pv, pn);
+  load8(cosv + pos * HNR_D + 8 * l, c);
+  load8(sinv + pos * HNR_D + 8 * l, sn);
+  {
+#pragma clang fp contract(off)  // products and sums rounded one by one, as rope_kernel does
+    if (l < 8) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float a = n[j] * c[j], b = pn[j] * sn[j];
+        out[j] = a - b;
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float a = n[j] * c[j], b = pn[j] * sn[j];
+        out[j] = a + b;
+      }
+    }
+  }
+  reinterpret_cast<uint4*>(y + row * HNR_D)[l] = pack8(out);
+}
+
+__global__ __launch_bounds__(256) void head_norm_rope_bwd_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ wt, const float* __restrict__ rstd,
+    const float* __restrict__ cosv, const float* __restrict__ sinv,
+    const uint16_t* __restrict__ gy, uint16_t* __restrict__ gx, int64_t rows, int64_t S,
+    int heads) {
+  const int lane = threadIdx.x & 63, sub = lane >> 4, l = lane & 15;
+  const int64_t row = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 4 + sub;
+  const bool valid = row < rows;
+  const uint4 zero = make_uint4(0, 0, 0, 0);
+  const uint4 gv = valid ? reinterpret_cast<const uint4*>(gy + row * HNR_D)[l] : zero;
+  const uint4 xv = valid ? reinterpret_cast<const uint4*>(x + row * HNR_D)[l] : zero;
+  const uint4 pg = dpp_ror8(gv);  // the partner lane's output gradient
+  const int64_t pos = valid ? (row / heads) % S : 0;
+  float g[8], p[8], c[8], sp[8], gn[8];
+  unpack8(gv, g);
+  unpack8(pg, p);
+  load8(cosv + pos * HNR_D + 8 * l, c);
+  load8(sinv + pos * HNR_D + 8 * (l ^ 8), sp);  // sin at the partner's columns
+  {
+#pragma clang fp contract(off)  // the transposed rotation, as rope_kernel<true>
+    if (l < 8) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float a = g[j] * c[j], b = p[j] * sp[j];
+        gn[j] = a + b;
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float a = g[j] * c[j], b = p[j] * sp[j];
+        gn[j] = a - b;
+      }
+    }
+  }
+  // the norm's backward on the rotation's bf16 gradient
+  const uint4 gnv = pack8(gn);
+  float f[8], gb[8], w[8];
+  unpack8(xv, f);
+  unpack8(gnv, gb);
+  unpack8(reinterpret_cast<const uint4*>(wt)[l], w);
+  const float r = valid ? rstd[row] : 0.f;
+  float dot = norm_bwd_dot(f, gb, w, r, 0.f);
+  dot = row_sum<16>(dot) / (float)HNR_D;
+  if (!valid) return;
+  float o[8];
+  norm_bwd_out(f, gb, w, r, dot, o);
+  reinterpret_cast<uint4*>(gx + row * HNR_D)[l] = pack8(o);
 }
 
 // Kernel shape of a row width: lanes per row, chunks per lane, row groups per iteration.
@@ -449,6 +588,42 @@ int plz_bias_grad(const uint16_t* grad_y, float* grad_bias, int64_t M, int64_t N
   hipLaunchKernelGGL(bias_grad_kernel, dim3((unsigned)((N + 255) / 256)), dim3(256), 0,
                      (hipStream_t)stream, grad_y, grad_bias, M, N);
   return check_launch("plz_bias_grad");
+}
+
+
+int plz_head_norm_rope_fwd(const uint16_t* x, const uint16_t* weight, const float* cos_table,
+                           const float* sin_table, uint16_t* y, float* rstd, int64_t rows,
+                           int64_t seq, int heads, int head_dim, float eps, void* stream) {
+  PLZ_REQUIRE(head_dim == HNR_D, "plz_head_norm_rope_fwd: head_dim %d is not supported (128 only)",
+              head_dim);
+  PLZ_REQUIRE(rows >= 0 && seq > 0 && heads > 0, "plz_head_norm_rope_fwd: need rows >= 0, seq > 0, heads > 0");
+  if (rows == 0) return PLZ_OK;
+  PLZ_REQUIRE(x && weight && cos_table && sin_table && y && a16(x) && a16(weight) &&
+                  a16(cos_table) && a16(sin_table) && a16(y),
+              "plz_head_norm_rope_fwd: operands must be non-null and 16-byte aligned");
+  const int64_t n = rows * heads;
+  hipLaunchKernelGGL(head_norm_rope_fwd_kernel, dim3((unsigned)((n + 15) / 16)), dim3(256), 0,
+                     (hipStream_t)stream, x, weight, cos_table, sin_table, y, rstd, n, seq, heads,
+                     eps);
+  return check_launch("plz_head_norm_rope_fwd");
+}
+
+int plz_head_norm_rope_bwd(const uint16_t* x, const uint16_t* weight, const float* rstd,
+                           const float* cos_table, const float* sin_table, const uint16_t* grad_y,
+                           uint16_t* grad_x, int64_t rows, int64_t seq, int heads, int head_dim,
+                           void* stream) {
+  PLZ_REQUIRE(head_dim == HNR_D, "plz_head_norm_rope_bwd: head_dim %d is not supported (128 only)",
+              head_dim);
+  PLZ_REQUIRE(rows >= 0 && seq > 0 && heads > 0, "plz_head_norm_rope_bwd: need rows >= 0, seq > 0, heads > 0");
+  if (rows == 0) return PLZ_OK;
+  PLZ_REQUIRE(x && weight && rstd && cos_table && sin_table && grad_y && grad_x && a16(x) &&
+                  a16(weight) && a16(cos_table) && a16(sin_table) && a16(grad_y) && a16(grad_x),
+              "plz_head_norm_rope_bwd: operands must be non-null and 16-byte aligned");
+  const int64_t n = rows * heads;
+  hipLaunchKernelGGL(head_norm_rope_bwd_kernel, dim3((unsigned)((n + 15) / 16)), dim3(256), 0,
+                     (hipStream_t)stream, x, weight, rstd, cos_table, sin_table, grad_y, grad_x,
+                     n, seq, heads);
+  return check_launch("plz_head_norm_rope_bwd");
 }
 
 }  // extern "C"

@@ -56,6 +56,8 @@ SIGNATURES: dict[str, tuple] = {
     "plz_attn_bwd": (i32, [p, p, p, p, p, p, p, p, p, p, sz, i32, i32, i32, i32, i32, f32, p]),
     "plz_rope_fwd": (i32, [p, p, p, p, i64, i64, i32, i32, p]),
     "plz_rope_bwd": (i32, [p, p, p, p, i64, i64, i32, i32, p]),
+    "plz_head_norm_rope_fwd": (i32, [p, p, p, p, p, p, i64, i64, i32, i32, f32, p]),
+    "plz_head_norm_rope_bwd": (i32, [p, p, p, p, p, p, p, i64, i64, i32, i32, p]),
     "plz_distill_loss_workspace": (sz, [i64]),
     "plz_distill_loss_fwd": (i32, [p, p, f32, f32, f32, p, p, sz, i64, i64, p]),
     "plz_distill_loss_bwd": (i32, [p, p, p, p, f32, f32, f32, p, p, sz, i64, i64, p]),

@@ -364,6 +364,31 @@ def rope_tables(seq, head_dim, theta, device):
     return emb.cos(), emb.sin()
 
 
+class HeadNormRopeFunction(torch.autograd.Function):
+    """apply_rope(norm(x)) for a per-head RMSNorm with a frozen weight: plz_head_norm_rope_fwd /
+    _bwd, bit-identical to RMSNormFunction followed by RopeFunction."""
+
+    @staticmethod
+    def forward(ctx, x, weight, eps, cos, sin):
+        x = x.contiguous()
+        y, rstd = ops.head_norm_rope_fwd(x, weight, cos, sin, eps)
+        ctx.save_for_backward(x, weight, rstd, cos, sin)
+        return y
+
+    @staticmethod
+    def backward(ctx, gy):
+        x, weight, rstd, cos, sin = ctx.saved_tensors
+        return ops.head_norm_rope_bwd(x, weight, rstd, cos, sin, gy.contiguous()), None, None, None, None
+
+
+def norm_rope(norm, x, cos, sin):
+    """apply_rope(norm(x)): one fused pass for a frozen 128-wide per-head norm, else the two."""
+    if (not norm.weight.requires_grad and x.shape[-1] == 128 and x.is_cuda
+            and x.dtype == torch.bfloat16):
+        return HeadNormRopeFunction.apply(x, norm.weight, norm.eps, cos, sin)
+    return apply_rope(norm(x), cos, sin)
+
+
 def apply_rope(x, cos, sin):
     """x bf16 [B, S, H, D] on the GPU: HF's rotate_half embedding (x cos + rotate_half(x) sin),
     computed in fp32 with fp32 tables, rounded once to bf16 (plz_rope_fwd / plz_rope_bwd)."""
@@ -507,10 +532,11 @@ class PalettizedDecoderLayer(nn.Module):
         B, S, _ = hs.shape
         pw = self.build_weights()
         x = self.input_layernorm(hs)
-        q = self.q_norm(self.q_proj(x, pw["q_proj"]).view(B, S, cfg.heads, cfg.head_dim))
-        k = self.k_norm(self.k_proj(x, pw["k_proj"]).view(B, S, cfg.kv_heads, cfg.head_dim))
+        q = norm_rope(self.q_norm, self.q_proj(x, pw["q_proj"]).view(B, S, cfg.heads, cfg.head_dim),
+                      cos, sin)
+        k = norm_rope(self.k_norm, self.k_proj(x, pw["k_proj"]).view(B, S, cfg.kv_heads, cfg.head_dim),
+                      cos, sin)
         v = self.v_proj(x, pw["v_proj"]).view(B, S, cfg.kv_heads, cfg.head_dim)
-        q, k = apply_rope(q, cos, sin), apply_rope(k, cos, sin)
         hs = hs + self.o_proj(attention(q, k, v, cfg.heads, cfg.kv_heads), pw["o_proj"])
         x = self.post_attention_layernorm(hs)
         if self.gate_up is not None:
@@ -553,10 +579,10 @@ class DenseDecoderLayer(nn.Module):
         B, S, _ = hs.shape
         lin = self._linear
         x = self.input_layernorm(hs)
-        q = self.q_norm(lin(x, self.q_proj).view(B, S, cfg.heads, cfg.head_dim))
-        k = self.k_norm(lin(x, self.k_proj).view(B, S, cfg.kv_heads, cfg.head_dim))
+        q = norm_rope(self.q_norm, lin(x, self.q_proj).view(B, S, cfg.heads, cfg.head_dim), cos, sin)
+        k = norm_rope(self.k_norm, lin(x, self.k_proj).view(B, S, cfg.kv_heads, cfg.head_dim),
+                      cos, sin)
         v = lin(x, self.v_proj).view(B, S, cfg.kv_heads, cfg.head_dim)
-        q, k = apply_rope(q, cos, sin), apply_rope(k, cos, sin)
         hs = hs + lin(attention(q, k, v, cfg.heads, cfg.kv_heads), self.o_proj)
         x = self.post_attention_layernorm(hs)
         if cfg.intermediate % 128 == 0:

@@ -823,6 +823,43 @@ def rope_bwd(grad_y, cos, sin):
     return _rope("plz_rope_bwd", grad_y, cos, sin)
 
 
+def _head_rows(x, cos, sin, what):
+    _need(x, what, torch.bfloat16)
+    if x.dim() < 3 or not x.is_contiguous():
+        raise ValueError(f"{what} must be contiguous [..., seq, heads, head_dim]")
+    seq, heads, hd = x.shape[-3], x.shape[-2], x.shape[-1]
+    for t, nm in ((cos, "cos"), (sin, "sin")):
+        _need(t, nm, torch.float32, 2)
+        if tuple(t.shape) != (seq, hd):
+            raise ValueError(f"{nm} must be [seq={seq}, head_dim={hd}]")
+    return x.numel() // (heads * hd), seq, heads, hd
+
+
+def head_norm_rope_fwd(x, weight, cos, sin, eps: float):
+    """rope_fwd(rmsnorm over each head's head_dim values) in one pass, bit-identical to the two:
+    x bf16 [..., seq, heads, 128] -> (y like x, rstd fp32 [x.numel() / 128])."""
+    rows, seq, heads, hd = _head_rows(x, cos, sin, "x")
+    _norm_weight(weight, hd)
+    y = torch.empty_like(x)
+    rstd = torch.empty((rows * heads,), dtype=torch.float32, device=x.device)
+    call("plz_head_norm_rope_fwd", _ptr(x), _ptr(weight), _ptr(cos), _ptr(sin), _ptr(y),
+         _ptr(rstd), rows, seq, heads, hd, float(eps), _stream(x))
+    return y, rstd
+
+
+def head_norm_rope_bwd(x, weight, rstd, cos, sin, grad_y):
+    """grad_x of head_norm_rope_fwd (rope_bwd then rmsnorm_bwd, bit for bit; no weight gradient)."""
+    rows, seq, heads, hd = _head_rows(x, cos, sin, "x")
+    _norm_weight(weight, hd)
+    _need(rstd, "rstd", torch.float32, 1)
+    if grad_y.shape != x.shape or not grad_y.is_contiguous() or rstd.numel() != rows * heads:
+        raise ValueError("grad_y / rstd do not match x")
+    gx = torch.empty_like(x)
+    call("plz_head_norm_rope_bwd", _ptr(x), _ptr(weight), _ptr(rstd), _ptr(cos), _ptr(sin),
+         _ptr(grad_y), _ptr(gx), rows, seq, heads, hd, _stream(x))
+    return gx
+
+
 def distill_loss_fwd(student, teacher, w_cos=0.5, w_mse=0.5, eps=1e-4):
     """Returns (out4 fp32 [4] = loss, l_cos, t_var, l_mse; workspace for the backward)."""
     _need(student, "student", torch.bfloat16)

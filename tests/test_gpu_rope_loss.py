@@ -1,5 +1,6 @@
 """GPU parity of the layer-step kernels around the linears: RoPE forward/backward (bit-exact
-against the torch expression of HF Qwen3's rotate_half embedding) and the distillation loss of
+against the torch expression of HF Qwen3's rotate_half embedding), the fused per-head norm +
+RoPE (bit-exact against the two kernels it replaces) and the distillation loss of
 train_qwen.py:229-249 (against torch autograd of the same expression in fp32 on the CPU)."""
 import pytest
 import torch
@@ -35,6 +36,37 @@ def test_rope_bit_exact(dev, B, S, H, D):
     xg = x.to(dev).requires_grad_(True)
     layer.apply_rope(xg, cos.to(dev), sin.to(dev)).backward(gy.to(dev))
     assert torch.equal(xg.grad.cpu().view(torch.int16), xr.grad.view(torch.int16))
+
+
+@pytest.mark.parametrize("B,S,H", [(2, 37, 3), (1, 512, 32), (3, 16, 8)])
+def test_head_norm_rope_is_norm_then_rope_bit_for_bit(dev, B, S, H):
+    """The fused per-head RMSNorm + RoPE (plz_head_norm_rope_fwd / _bwd) against the two kernels
+    it replaces (plz_rmsnorm_fwd then plz_rope_fwd; plz_rope_bwd then plz_rmsnorm_bwd), each
+    pinned above and in test_gpu_misc: every output bit, with a non-unit norm weight and a row
+    count that leaves a partial workgroup (B S H not a multiple of 16)."""
+    D = 128
+    g = torch.Generator().manual_seed(B * S * H)
+    x = (torch.randn(B, S, H, D, generator=g) * 2).to(torch.bfloat16).to(dev)
+    w = (1 + 0.3 * torch.randn(D, generator=g)).to(torch.bfloat16).to(dev)
+    gy = torch.randn(B, S, H, D, generator=g).to(torch.bfloat16).to(dev)
+    cos, sin = layer.rope_tables(S, D, 1e6, dev)
+    eps = 1e-6
+    n, rstd = ops.rmsnorm_fwd(x.view(-1, D), w, eps)
+    want = ops.rope_fwd(n.view(B, S, H, D), cos, sin)
+    y, rstd2 = ops.head_norm_rope_fwd(x, w, cos, sin, eps)
+    assert torch.equal(y.view(torch.int16), want.view(torch.int16))
+    assert torch.equal(rstd2, rstd)
+    gn = ops.rope_bwd(gy, cos, sin)
+    want_gx, _ = ops.rmsnorm_bwd(x.view(-1, D), w, rstd, gn.view(-1, D))
+    gx = ops.head_norm_rope_bwd(x, w, rstd2, cos, sin, gy)
+    assert torch.equal(gx.view(-1, D).view(torch.int16), want_gx.view(torch.int16))
+    # the layer's autograd path (frozen weight) against the unfused modules
+    norm = layer.RMSNorm(D, eps, dev)
+    norm.weight.data.copy_(w)
+    xa, xb = x.clone().requires_grad_(True), x.clone().requires_grad_(True)
+    layer.norm_rope(norm, xa, cos, sin).backward(gy)
+    layer.apply_rope(norm(xb), cos, sin).backward(gy)
+    assert torch.equal(xa.grad.view(torch.int16), xb.grad.view(torch.int16))
 
 
 def _loss_cpu(s, t, w_cos=0.5, w_mse=0.5):
