@@ -91,8 +91,9 @@ def test_distill_loss_matches_torch(dev, B, S, Dm, w):
     want.backward()
     sg = s.to(dev).requires_grad_(True)
     loss, l_cos = layer.compute_loss(sg, t.to(dev), *w)
-    assert abs(float(loss) - float(want)) <= 1e-5 * abs(float(want)) + 1e-7
-    assert abs(float(l_cos) - float(want_cos)) <= 1e-5 * abs(float(want_cos)) + 1e-7
+    lv, lc, wv, wc = (float(v.detach()) for v in (loss, l_cos, want, want_cos))
+    assert abs(lv - wv) <= 1e-5 * abs(wv) + 1e-7
+    assert abs(lc - wc) <= 1e-5 * abs(wc) + 1e-7
     (2.0 * loss).backward()
     assert_close(f32(sg.grad.cpu()), 2.0 * f32(sr.grad), what="grad_student")
 
