@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define PLZ_ABI_VERSION 12
+#define PLZ_ABI_VERSION 13
 
 /* status codes */
 #define PLZ_OK 0
@@ -458,6 +458,17 @@ int plz_rmsnorm_bwd(const uint16_t* x, const uint16_t* weight, const float* rstd
                     const uint16_t* grad_y, uint16_t* grad_x, float* grad_weight,
                     void* workspace, size_t workspace_bytes, int64_t rows, int64_t cols,
                     void* stream);
+/* A residual add followed by RMSNorm, as the HF Qwen3 decoder layer runs them
+ * (hidden = residual + attn_out; post_attention_layernorm(hidden)): sum = bf16(x + residual),
+ * written, and y, rstd of plz_rmsnorm_fwd on sum, bit for bit. */
+int plz_add_rmsnorm_fwd(const uint16_t* x, const uint16_t* residual, const uint16_t* weight,
+                        uint16_t* sum, uint16_t* y, float* rstd, int64_t rows, int64_t cols,
+                        float eps, void* stream);
+/* grad_x = bf16(plz_rmsnorm_bwd's grad_x) + grad_add (the gradient that reaches the norm's
+ * input along the residual stream), without the weight gradient (frozen norm weights). */
+int plz_rmsnorm_bwd_add(const uint16_t* x, const uint16_t* weight, const float* rstd,
+                        const uint16_t* grad_y, const uint16_t* grad_add, uint16_t* grad_x,
+                        int64_t rows, int64_t cols, void* stream);
 /* h = silu(gate) * up, elementwise over n elements (n % 8 == 0). */
 int plz_swiglu_fwd(const uint16_t* gate, const uint16_t* up, uint16_t* h, int64_t n,
                    void* stream);

@@ -37,12 +37,25 @@ __device__ __forceinline__ float row_sum(float v) {
   return v;
 }
 
-template <int LPR, int MAXC>
+// bf16 a + b as torch adds two bf16 tensors (fp32 sum, one rounding), 8 lanes at a time
+__device__ __forceinline__ uint4 add8(uint4 a, uint4 b) {
+  float fa[8], fb[8];
+  unpack8(a, fa);
+  unpack8(b, fb);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) fa[j] = fa[j] + fb[j];
+  return pack8(fa);
+}
+
+// ADD: the row is first the bf16 sum x + res (a residual add, written to sum), then normalised.
+template <int LPR, int MAXC, bool ADD = false>
 __global__ __launch_bounds__(256) void rmsnorm_fwd_kernel(const uint16_t* __restrict__ x,
                                                           const uint16_t* __restrict__ wt,
                                                           uint16_t* __restrict__ y,
                                                           float* __restrict__ rstd, int64_t rows,
-                                                          int64_t cols, float eps) {
+                                                          int64_t cols, float eps,
+                                                          const uint16_t* __restrict__ res = nullptr,
+                                                          uint16_t* __restrict__ sum = nullptr) {
   constexpr int RPW = 64 / LPR;
   const int lane = threadIdx.x & 63, sub = lane / LPR, l = lane % LPR;
   const int64_t row = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW + sub;
@@ -57,6 +70,10 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_kernel(const uint16_t* __rest
     xv[i] = make_uint4(0, 0, 0, 0);
     if (valid && c < nch) {
       xv[i] = xr[c];
+      if (ADD) {
+        xv[i] = add8(xv[i], reinterpret_cast<const uint4*>(res + row * cols)[c]);
+        reinterpret_cast<uint4*>(sum + row * cols)[c] = xv[i];
+      }
       float f[8];
       unpack8(xv[i], f);
 #pragma unroll
@@ -112,13 +129,16 @@ __device__ __forceinline__ void norm_bwd_out(const float f[8], const float g[8],
 // all issued before any is used, so short rows do not pay the memory latency per row);
 // per-lane column partials of grad_w are summed over the workgroup's rows in LDS (fixed order)
 // and written to partial[block][cols]; a second kernel adds the blocks in a fixed order.
-template <int LPR, int MAXC, int U>
+// WG = false: no weight gradient (frozen weights: no partials, no LDS, no second kernel).
+// ADD: grad_x = bf16(norm backward) + add, as autograd sums the two gradients of a residual
+// stream that also feeds this norm (bf16 + bf16, one rounding).
+template <int LPR, int MAXC, int U, bool WG = true, bool ADD = false>
 __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ wt, const float* __restrict__ rstd,
     const uint16_t* __restrict__ gy, uint16_t* __restrict__ gx, float* __restrict__ partial,
-    int64_t rows, int64_t cols) {
+    int64_t rows, int64_t cols, const uint16_t* __restrict__ add = nullptr) {
   constexpr int RPW = 64 / LPR;
-  __shared__ float red[4 * RPW][MAXC][LPR][8];
+  __shared__ float red[WG ? 4 * RPW : 1][MAXC][LPR][8];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, sub = lane / LPR, l = lane % LPR;
   const int nch = (int)(cols / 8);
   const uint4* wr = reinterpret_cast<const uint4*>(wt);
@@ -161,9 +181,10 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(
           unpack8(gv[u][i], g);
           unpack8(wr[c], w);
           dot = norm_bwd_dot(f, g, w, r, dot);
+          if (WG)
 #pragma unroll
-          for (int j = 0; j < 8; ++j)
-            gw[i][j] += g[j] * bf2f(f2bf(f[j] * r));  // zero for a missing row (g = 0)
+            for (int j = 0; j < 8; ++j)
+              gw[i][j] += g[j] * bf2f(f2bf(f[j] * r));  // zero for a missing row (g = 0)
         }
       }
       dot = row_sum<LPR>(dot) / (float)cols;
@@ -178,12 +199,14 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(
             unpack8(gv[u][i], g);
             unpack8(wr[c], w);
             norm_bwd_out(f, g, w, r, dot, o);
-            outr[c] = pack8(o);
+            outr[c] = ADD ? add8(pack8(o), reinterpret_cast<const uint4*>(add + row * cols)[c])
+                          : pack8(o);
           }
         }
       }
     }
   }
+  if (!WG) return;
 #pragma unroll
   for (int i = 0; i < MAXC; ++i)
 #pragma unroll
@@ -624,6 +647,59 @@ int plz_head_norm_rope_bwd(const uint16_t* x, const uint16_t* weight, const floa
                      (hipStream_t)stream, x, weight, rstd, cos_table, sin_table, grad_y, grad_x,
                      n, seq, heads);
   return check_launch("plz_head_norm_rope_bwd");
+}
+
+
+int plz_add_rmsnorm_fwd(const uint16_t* x, const uint16_t* residual, const uint16_t* weight,
+                        uint16_t* sum, uint16_t* y, float* rstd, int64_t rows, int64_t cols,
+                        float eps, void* stream) {
+  PLZ_REQUIRE(rows >= 0 && cols > 0 && cols % 8 == 0 && cols <= 64 * 8 * kNormMaxChunks,
+              "plz_add_rmsnorm_fwd: cols (%lld) must be a positive multiple of 8 up to 4096",
+              (long long)cols);
+  if (rows == 0) return PLZ_OK;
+  PLZ_REQUIRE(x && residual && weight && sum && y && a16(x) && a16(residual) && a16(weight) &&
+                  a16(sum) && a16(y),
+              "plz_add_rmsnorm_fwd: operands must be non-null and 16-byte aligned");
+  const NormShape sh = norm_shape(cols);
+  const int64_t per_block = 4LL * (64 / sh.lpr);
+  const dim3 grid((unsigned)((rows + per_block - 1) / per_block));
+  const hipStream_t st = (hipStream_t)stream;
+  if (sh.lpr == 16)
+    hipLaunchKernelGGL((rmsnorm_fwd_kernel<16, 1, true>), grid, dim3(256), 0, st, x, weight, y,
+                       rstd, rows, cols, eps, residual, sum);
+  else if (sh.maxc == 1)
+    hipLaunchKernelGGL((rmsnorm_fwd_kernel<64, 1, true>), grid, dim3(256), 0, st, x, weight, y,
+                       rstd, rows, cols, eps, residual, sum);
+  else
+    hipLaunchKernelGGL((rmsnorm_fwd_kernel<64, kNormMaxChunks, true>), grid, dim3(256), 0, st, x,
+                       weight, y, rstd, rows, cols, eps, residual, sum);
+  return check_launch("plz_add_rmsnorm_fwd");
+}
+
+int plz_rmsnorm_bwd_add(const uint16_t* x, const uint16_t* weight, const float* rstd,
+                        const uint16_t* grad_y, const uint16_t* grad_add, uint16_t* grad_x,
+                        int64_t rows, int64_t cols, void* stream) {
+  PLZ_REQUIRE(rows >= 0 && cols > 0 && cols % 8 == 0 && cols <= 64 * 8 * kNormMaxChunks,
+              "plz_rmsnorm_bwd_add: cols (%lld) must be a positive multiple of 8 up to 4096",
+              (long long)cols);
+  if (rows == 0) return PLZ_OK;
+  PLZ_REQUIRE(x && weight && rstd && grad_y && grad_add && grad_x && a16(x) && a16(weight) &&
+                  a16(grad_y) && a16(grad_add) && a16(grad_x),
+              "plz_rmsnorm_bwd_add: operands must be non-null and 16-byte aligned");
+  const int blocks = rmsnorm_bwd_blocks(rows, cols);
+  const NormShape sh = norm_shape(cols);
+  const hipStream_t st = (hipStream_t)stream;
+  if (sh.lpr == 16)
+    hipLaunchKernelGGL((rmsnorm_bwd_kernel<16, 1, 4, false, true>), dim3(blocks), dim3(256), 0, st,
+                       x, weight, rstd, grad_y, grad_x, nullptr, rows, cols, grad_add);
+  else if (sh.maxc == 1)
+    hipLaunchKernelGGL((rmsnorm_bwd_kernel<64, 1, 4, false, true>), dim3(blocks), dim3(256), 0, st,
+                       x, weight, rstd, grad_y, grad_x, nullptr, rows, cols, grad_add);
+  else
+    hipLaunchKernelGGL((rmsnorm_bwd_kernel<64, kNormMaxChunks, 1, false, true>), dim3(blocks),
+                       dim3(256), 0, st, x, weight, rstd, grad_y, grad_x, nullptr, rows, cols,
+                       grad_add);
+  return check_launch("plz_rmsnorm_bwd_add");
 }
 
 }  // extern "C"

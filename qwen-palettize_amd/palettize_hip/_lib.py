@@ -118,6 +118,8 @@ SIGNATURES: dict[str, tuple] = {
     "plz_adamw_step": (i32, [p, i32, i64, f32, f32, C.c_double, C.c_double, f32, f32, i64, p, p,
                              sz, p]),
     "plz_rmsnorm_fwd": (i32, [p, p, p, p, i64, i64, f32, p]),
+    "plz_add_rmsnorm_fwd": (i32, [p, p, p, p, p, p, i64, i64, f32, p]),
+    "plz_rmsnorm_bwd_add": (i32, [p, p, p, p, p, p, i64, i64, p]),
     "plz_rmsnorm_bwd_workspace": (sz, [i64, i64]),
     "plz_rmsnorm_bwd": (i32, [p, p, p, p, p, p, p, sz, i64, i64, p]),
     "plz_swiglu_fwd": (i32, [p, p, p, i64, p]),

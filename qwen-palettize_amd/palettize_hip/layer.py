@@ -75,6 +75,43 @@ class RMSNormFunction(torch.autograd.Function):
         return gx.reshape(ctx.shape), (gw.to(weight.dtype) if ctx.needs_input_grad[1] else None), None
 
 
+class AddRMSNormFunction(torch.autograd.Function):
+    """(s, norm(s)) with s = a + b (a residual add and the RMSNorm after it, frozen weight):
+    plz_add_rmsnorm_fwd, and plz_rmsnorm_bwd_add for the gradient of s along both uses."""
+
+    @staticmethod
+    def forward(ctx, a, b, weight, eps):
+        shape = a.shape
+        s, y, rstd = ops.add_rmsnorm_fwd(a.reshape(-1, shape[-1]).contiguous(),
+                                         b.reshape(-1, shape[-1]).contiguous(), weight, eps)
+        ctx.save_for_backward(s, weight, rstd)
+        ctx.shape = shape
+        return s.view(shape), y.view(shape)
+
+    @staticmethod
+    def backward(ctx, gs, gy):
+        s, weight, rstd = ctx.saved_tensors
+        if gy is None:
+            g = gs
+        else:
+            gy2 = gy.reshape(s.shape).contiguous()
+            if gs is None:
+                g, _ = ops.rmsnorm_bwd(s, weight, rstd, gy2)
+            else:
+                g = ops.rmsnorm_bwd_add(s, weight, rstd, gy2, gs.reshape(s.shape).contiguous())
+            g = g.view(ctx.shape)
+        return g, g, None, None
+
+
+def add_rmsnorm(norm, a, b):
+    """(a + b, norm(a + b)): one fused pass for a frozen norm weight on bf16 GPU tensors."""
+    if (not norm.weight.requires_grad and a.is_cuda and a.dtype == torch.bfloat16
+            and b.dtype == torch.bfloat16 and a.shape == b.shape):
+        return AddRMSNormFunction.apply(a, b, norm.weight, norm.eps)
+    s = a + b
+    return s, norm(s)
+
+
 class RMSNorm(nn.Module):
     def __init__(self, dim, eps, device=None):
         super().__init__()
@@ -537,8 +574,8 @@ class PalettizedDecoderLayer(nn.Module):
         k = norm_rope(self.k_norm, self.k_proj(x, pw["k_proj"]).view(B, S, cfg.kv_heads, cfg.head_dim),
                       cos, sin)
         v = self.v_proj(x, pw["v_proj"]).view(B, S, cfg.kv_heads, cfg.head_dim)
-        hs = hs + self.o_proj(attention(q, k, v, cfg.heads, cfg.kv_heads), pw["o_proj"])
-        x = self.post_attention_layernorm(hs)
+        hs, x = add_rmsnorm(self.post_attention_layernorm, hs,
+                            self.o_proj(attention(q, k, v, cfg.heads, cfg.kv_heads), pw["o_proj"]))
         if self.gate_up is not None:
             h = SwiGLUCatFunction.apply(self.gate_up.forward(x, pw["gate_up"]))
         else:
@@ -583,8 +620,8 @@ class DenseDecoderLayer(nn.Module):
         k = norm_rope(self.k_norm, lin(x, self.k_proj).view(B, S, cfg.kv_heads, cfg.head_dim),
                       cos, sin)
         v = lin(x, self.v_proj).view(B, S, cfg.kv_heads, cfg.head_dim)
-        hs = hs + lin(attention(q, k, v, cfg.heads, cfg.kv_heads), self.o_proj)
-        x = self.post_attention_layernorm(hs)
+        hs, x = add_rmsnorm(self.post_attention_layernorm, hs,
+                            lin(attention(q, k, v, cfg.heads, cfg.kv_heads), self.o_proj))
         if cfg.intermediate % 128 == 0:
             # gate and up in one GEMM with the SwiGLU in its epilogue (never stored)
             if getattr(self, "_gate_up", None) is None:

@@ -734,6 +734,36 @@ def rmsnorm_fwd(x, weight, eps: float):
     return y, rstd
 
 
+def add_rmsnorm_fwd(x, residual, weight, eps: float):
+    """(sum = x + residual, rmsnorm(sum), rstd) in one pass; bf16 [rows, cols] inputs."""
+    _need(x, "x", torch.bfloat16, 2)
+    _need(residual, "residual", torch.bfloat16, 2)
+    if residual.shape != x.shape:
+        raise ValueError("x / residual shape mismatch")
+    rows, cols = x.shape
+    _norm_weight(weight, cols)
+    s, y = torch.empty_like(x), torch.empty_like(x)
+    rstd = torch.empty((rows,), dtype=torch.float32, device=x.device)
+    call("plz_add_rmsnorm_fwd", _ptr(x), _ptr(residual), _ptr(weight), _ptr(s), _ptr(y),
+         _ptr(rstd), rows, cols, float(eps), _stream(x))
+    return s, y, rstd
+
+
+def rmsnorm_bwd_add(x, weight, rstd, grad_y, grad_add):
+    """rmsnorm_bwd's grad_x (bf16) + grad_add, without the weight gradient."""
+    _need(x, "x", torch.bfloat16, 2)
+    _need(grad_y, "grad_y", torch.bfloat16, 2)
+    _need(grad_add, "grad_add", torch.bfloat16, 2)
+    rows, cols = x.shape
+    _norm_weight(weight, cols)
+    if grad_y.shape != x.shape or grad_add.shape != x.shape or rstd.numel() != rows:
+        raise ValueError("grad_y / grad_add / rstd do not match x")
+    gx = torch.empty_like(x)
+    call("plz_rmsnorm_bwd_add", _ptr(x), _ptr(weight), _ptr(rstd), _ptr(grad_y), _ptr(grad_add),
+         _ptr(gx), rows, cols, _stream(x))
+    return gx
+
+
 def rmsnorm_bwd(x, weight, rstd, grad_y):
     _need(x, "x", torch.bfloat16, 2)
     _need(grad_y, "grad_y", torch.bfloat16, 2)

@@ -8,6 +8,7 @@ from helpers import assert_close, f32, gen, make_weight, randn_bf16
 
 pytestmark = pytest.mark.gpu
 ops = pytest.importorskip("palettize_hip.ops")
+layer = pytest.importorskip("palettize_hip.layer")
 import palettize_hip as P  # noqa: E402
 from palettize_hip import fused_lut_linear_cuda as FL  # noqa: E402
 
@@ -57,6 +58,38 @@ def test_rmsnorm(dev, rows, cols):
     wgx, wgw = O.rmsnorm_bwd(f32(x), f32(w), f32(gy), 1e-6)
     assert_close(f32(gx), wgx, what="rmsnorm grad_x")
     assert_close(f32(gw), wgw, max_rel=1e-4, what="rmsnorm grad_w")
+
+
+@pytest.mark.parametrize("rows,cols", [(64, 2560), (300, 128), (17, 4096), (5000, 256), (2049, 2560)])
+def test_add_rmsnorm_is_add_then_norm_bit_for_bit(dev, rows, cols):
+    """plz_add_rmsnorm_fwd / plz_rmsnorm_bwd_add against the ops they fuse (torch's bf16 add,
+    plz_rmsnorm_fwd, plz_rmsnorm_bwd's grad_x then torch's bf16 add), every bit; and the layer's
+    autograd path against the unfused modules."""
+    a = randn_bf16(rows, cols, seed=rows).to(dev)
+    b = randn_bf16(rows, cols, seed=rows + 7, std=0.5).to(dev)
+    w = (1 + 0.1 * torch.randn(cols, generator=gen(3))).to(torch.bfloat16).to(dev)
+    s, y, rstd = ops.add_rmsnorm_fwd(a, b, w, 1e-6)
+    ws = a + b
+    wy, wr = ops.rmsnorm_fwd(ws, w, 1e-6)
+    assert torch.equal(s.view(torch.int16), ws.view(torch.int16))
+    assert torch.equal(y.view(torch.int16), wy.view(torch.int16)) and torch.equal(rstd, wr)
+    gy = randn_bf16(rows, cols, seed=rows + 1).to(dev)
+    ga = randn_bf16(rows, cols, seed=rows + 2).to(dev)
+    gx = ops.rmsnorm_bwd_add(s, w, rstd, gy, ga)
+    wgx, _ = ops.rmsnorm_bwd(ws, w, wr, gy)
+    assert torch.equal(gx.view(torch.int16), (wgx + ga).view(torch.int16))
+    # the layer's fused path (frozen weight) against add + RMSNorm module, through autograd
+    norm = layer.RMSNorm(cols, 1e-6, dev)
+    norm.weight.data.copy_(w)
+    a1, b1 = a.clone().requires_grad_(True), b.clone().requires_grad_(True)
+    a2, b2 = a.clone().requires_grad_(True), b.clone().requires_grad_(True)
+    s1, y1 = layer.add_rmsnorm(norm, a1, b1)
+    s2 = a2 + b2
+    y2 = norm(s2)
+    torch.autograd.backward([s1, y1], [ga, gy])
+    torch.autograd.backward([s2, y2], [ga, gy])
+    for u, v in ((a1.grad, a2.grad), (b1.grad, b2.grad)):
+        assert torch.equal(u.view(torch.int16), v.view(torch.int16))
 
 
 def test_swiglu(dev):

@@ -103,7 +103,7 @@ def test_distill_loss_identical_inputs(dev):
     t = torch.randn(2, 8, 128).to(torch.bfloat16).to(dev)
     s = t.clone().requires_grad_(True)
     loss, l_cos = layer.compute_loss(s, t)
-    assert abs(float(loss)) < 1e-6 and abs(float(l_cos)) < 1e-6
+    assert abs(float(loss.detach())) < 1e-6 and abs(float(l_cos.detach())) < 1e-6
     loss.backward()
     assert float(s.grad.float().abs().max()) < 1e-6
 
