@@ -249,6 +249,39 @@ def test_rmsnorm_weight_and_rstd_are_checked_before_the_call(host_ops):
         ops.rmsnorm_bwd(x, torch.zeros(320, dtype=bf), torch.zeros(6, dtype=bf), x)
 
 
+def test_fused_norm_entry_points_check_arguments_before_launching(lib, host_ops):
+    """The fused per-head norm + RoPE and residual add + RMSNorm entries: bad head_dim / cols
+    and null operands are refused on the host; empty inputs return without a launch; the
+    Python wrappers check shapes before the call."""
+    rc = lib.plz_head_norm_rope_fwd(None, None, None, None, None, None, 4, 4, 2, 64, 1e-6, None)
+    assert rc == 1 and b"128" in lib.plz_last_error()
+    rc = lib.plz_head_norm_rope_bwd(None, None, None, None, None, None, None, 4, 4, 2, 128, None)
+    assert rc == 1 and b"non-null" in lib.plz_last_error()
+    assert lib.plz_head_norm_rope_fwd(None, None, None, None, None, None, 0, 4, 2, 128, 1e-6,
+                                      None) == 0
+    rc = lib.plz_add_rmsnorm_fwd(None, None, None, None, None, None, 4, 12, 1e-6, None)
+    assert rc == 1 and b"multiple of 8" in lib.plz_last_error()
+    rc = lib.plz_rmsnorm_bwd_add(None, None, None, None, None, None, 4, 256, None)
+    assert rc == 1 and b"non-null" in lib.plz_last_error()
+    assert lib.plz_add_rmsnorm_fwd(None, None, None, None, None, None, 0, 256, 1e-6, None) == 0
+    ops = host_ops
+    bf = torch.bfloat16
+    x = torch.zeros(6, 320, dtype=bf)
+    with pytest.raises(ValueError, match="shape mismatch"):
+        ops.add_rmsnorm_fwd(x, torch.zeros(6, 312, dtype=bf), torch.zeros(320, dtype=bf), 1e-6)
+    with pytest.raises(ValueError, match="weight has 300"):
+        ops.add_rmsnorm_fwd(x, x, torch.zeros(300, dtype=bf), 1e-6)
+    with pytest.raises(ValueError, match="do not match"):
+        ops.rmsnorm_bwd_add(x, torch.zeros(320, dtype=bf), torch.zeros(6), x,
+                            torch.zeros(6, 8, dtype=bf))
+    q = torch.zeros(1, 16, 2, 128, dtype=bf)
+    cos = torch.ones(16, 128)
+    with pytest.raises(ValueError, match="cos must be"):
+        ops.head_norm_rope_fwd(q, torch.zeros(128, dtype=bf), torch.ones(8, 128), cos, 1e-6)
+    with pytest.raises(ValueError, match="weight has 64"):
+        ops.head_norm_rope_fwd(q, torch.zeros(64, dtype=bf), cos, cos, 1e-6)
+
+
 def test_layer_step_has_no_cpu_path():
     """The layer-step pieces refuse CPU tensors instead of computing in torch on the CPU."""
     from palettize_hip import layer
