@@ -412,9 +412,9 @@ def main():
                          "kernel that scales rocprofv3's FETCH_SIZE / WRITE_SIZE to bytes")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py: this build measures one GPU only (the path has no multi-GPU "
-              "component; see DESIGN.md for how it would shard). Run with --gpus 1.",
-              file=sys.stderr)
+        print("bench.py: this build measures one GPU only: the LUT-linear path has no "
+              "multi-GPU component (each rank would run these kernels on its own shard of the "
+              "tokens or rows). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
     import torch
