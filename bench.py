@@ -1,9 +1,9 @@
 """Benchmark of the MI355X LUT-linear hot path (BASELINE.json metric).
 
 One step = one hard LUT-linear forward + backward (grad_x, grad_palette, LoRA grads) over
-the seven Qwen-4B linear shapes at M = 16384 tokens (batch 32 x seq 512; BASELINE config 3),
+the seven Qwen-4B linear shapes at M = 16384 tokens (batch 32 x seq 512; BASELINE.json config 3),
 straight-through through the frozen 2-bit indices, LoRA rank 16 (32 on o and down).
-`value` = sum over shapes of 6*M*K*N FLOP / step time (LoRA FLOP excluded, as in BASELINE),
+`value` = sum over shapes of 6*M*K*N FLOP / step time (LoRA FLOP excluded, as BASELINE.json counts it),
 the step's kernels issued on one stream as the library's autograd issues them: from 4096
 rows the forward dequantises W once and runs the dense GEMM, and grad_x reuses that W; the
 grad_palette GEMM also yields both LoRA weight gradients from its dW tiles; the LoRA row
@@ -29,7 +29,7 @@ import time
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "qwen-palettize_amd"))
 
-# (name, K, N, LoRA rank) of the seven Qwen-4B linears (BASELINE configs 2-3)
+# (name, K, N, LoRA rank) of the seven Qwen-4B linears (BASELINE.json configs 2-3)
 SHAPES = [("q", 2560, 4096, 16), ("k", 2560, 1024, 16), ("v", 2560, 1024, 16),
           ("o", 4096, 2560, 32), ("gate", 2560, 9728, 16), ("up", 2560, 9728, 16),
           ("down", 9728, 2560, 32)]
@@ -273,8 +273,7 @@ def bench_layer(device, steps=4, warmup=2):
 def cpu_baseline():
     """The reference's CPU PyTorch path (PalettizedLinear's fallback, qwen_model.py:183-192:
     flat palette gather with the int64 _flat_idx buffer, x @ W^T, plus QwenLoRA's
-    (x A^T) B^T, qwen_model.py:291-304; backward by torch autograd) on the host cores, as
-    BASELINE.md plans it:
+    (x A^T) B^T, qwen_model.py:291-304; backward by torch autograd) on the host cores:
       * value: the gate shape (2560 -> 9728, LoRA r16) hard fwd + bwd at M = 16384, timed
         once after a warm-up at M = 512, in TFLOP/s of 6 M K N;
       * config1: the single hard forward of config 1 (M 512, K = N = 2560, LoRA r16,

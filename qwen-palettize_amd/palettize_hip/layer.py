@@ -53,7 +53,7 @@ class LayerConfig:
     eps: float = 1e-6
     rope_theta: float = 1e6
     lora_rank: int = 16
-    lora_alpha: float = 16.0   # scaling alpha / r = 1 (BASELINE config: y += x A^T B^T)
+    lora_alpha: float = 16.0   # scaling alpha / r = 1 (y += x A^T B^T)
 
 
 # ---- fused kernels as autograd Functions ----------------------------------------------

@@ -2,7 +2,7 @@
 import numpy as np
 import torch
 
-# Parity bar for floating-point outputs (BASELINE north star): max-rel-err and cosine
+# Parity bar for floating-point outputs (BASELINE.json north_star): max-rel-err and cosine
 # against an fp32-or-better accumulated reference. The oracle computes in fp64.
 MAX_REL = 1e-2
 MIN_COS = 0.9999

@@ -1,4 +1,4 @@
-"""GPU parity at BASELINE config 3: hard forward, grad_x and grad_palette at M = 16384 on all
+"""GPU parity at BASELINE.json config 3: hard forward, grad_x and grad_palette at M = 16384 on all
 seven Qwen-4B linear shapes, LoRA rank 16 (32 on o and down), through the C ABI.
 
 These are the launch geometries the benchmark times: 640- and 2432-tile launches whose last
@@ -21,7 +21,7 @@ pytestmark = pytest.mark.gpu
 ops = pytest.importorskip("palettize_hip.ops")
 
 M = 16384
-# (name, K, N, LoRA rank) as in BASELINE config 3
+# (name, K, N, LoRA rank) as in BASELINE.json config 3
 SHAPES = [("q", 2560, 4096, 16), ("k", 2560, 1024, 16), ("v", 2560, 1024, 16),
           ("o", 4096, 2560, 32), ("gate", 2560, 9728, 16), ("up", 2560, 9728, 16),
           ("down", 9728, 2560, 32)]

@@ -1,4 +1,4 @@
-"""GPU parity at BASELINE config 4, at its size: the soft (Gumbel-softmax) forward and backward
+"""GPU parity at BASELINE.json config 4, at its size: the soft (Gumbel-softmax) forward and backward
 on the gate shape (K = 2560 -> N = 9728) at M = 16384, logits bf16 [N, K, 4] ~ N(0, 1), Gumbel
 noise fp32 from a seeded Philox stream passed in as a tensor, tau in {2.0, 0.5, 0.1} -- the
 calls the benchmark times (build-W, the dense forward and grad_x on W, the fused soft

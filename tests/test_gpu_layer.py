@@ -1,4 +1,4 @@
-"""GPU parity of the palettized decoder-layer training step (BASELINE config 5) against the
+"""GPU parity of the palettized decoder-layer training step (BASELINE.json config 5) against the
 torch CPU restatement (oracle/torch_ref.py) at a small Qwen3-shaped configuration."""
 import numpy as np
 import pytest
