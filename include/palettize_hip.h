@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define PLZ_ABI_VERSION 13
+#define PLZ_ABI_VERSION 14
 
 /* status codes */
 #define PLZ_OK 0
@@ -157,6 +157,18 @@ size_t plz_linear_fwd_dense_workspace(int64_t M, int64_t N, int64_t K);
  * counterpart in the reference, which runs the two nn.Linear and the activation apart. */
 int plz_linear_fwd_dense_swiglu(const uint16_t* x, const uint16_t* w_gate_up, uint16_t* h,
                                 int64_t M, int64_t N, int64_t K, void* stream);
+/* A trained gate/up pair (one soft linear over the concatenated rows) with the SwiGLU in the
+ * epilogue: y [M, 2F] = x w^T (+ lora_t lora_b^T), the pre-activations the SwiGLU backward
+ * needs (skipped when y is null), and h [M, F] = silu(y[:, :F]) * y[:, F:] from the bf16 y.
+ * w bf16 [2F, K] = [Wg; Wu] as stored (no interleaved copy: each output tile reads 128 gate
+ * rows and the 128 matching up rows), lora_b [2F, rank]. Bit-equal to plz_linear_fwd_dense
+ * without a workspace (no reduction split) followed by plz_swiglu_fwd_rows; this kernel never
+ * splits the reduction. F a multiple of 128, K of 8, rank of 8 up to 64. No
+ * counterpart in the reference: the HF Qwen3 MLP it trains runs gate_proj, up_proj and
+ * act_fn(gate) * up apart (transformers models/qwen3/modeling_qwen3.py). */
+int plz_linear_fwd_dense_swiglu_cat(const uint16_t* x, const uint16_t* w, const uint16_t* lora_t,
+                                    const uint16_t* lora_b, int rank, uint16_t* y, uint16_t* h,
+                                    int64_t M, int64_t F, int64_t K, void* stream);
 /* grad_x = grad_y w (+lora). Replaces torch.matmul(grad_y, W.T)
  * (fused_lut_linear_cuda.py:944). */
 int plz_linear_bwd_x_dense(const uint16_t* grad_y, const uint16_t* w, const uint16_t* lora_gt,

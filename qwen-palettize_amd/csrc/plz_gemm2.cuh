@@ -94,7 +94,18 @@ struct Args {
   int tiles_i, tiles_j;
   int group;  // tile-rows walked together (1: consecutive workgroups share the A panel);
               // < 0: column-major walk (consecutive workgroups share the B panel)
+  // EPI_SWIGLU over a [gate | up] weight: b_half = F gate rows, so that a tile's 256 columns
+  // are gate rows j0/2 .. j0/2+127 and the matching up rows F + j0/2 .. (half_row); c2, when
+  // set, receives the pre-activations [I, 2F] in that natural layout (row pitch ldc2)
+  int64_t b_half;
+  uint16_t* c2; int64_t ldc2;
 };
+
+// B row (and output column) of the tile-local logical column j when b_half > 0: the first 128
+// of every 256 columns are gate rows, the next 128 the up rows at the same offset
+__device__ __forceinline__ int64_t half_row(int64_t j, int64_t half) {
+  return half > 0 ? (j >> 8) * 128 + (j & 127) + ((j & 128) ? half : 0) : j;
+}
 
 // ---- dense operand copy, global -> LDS ---------------------------------------------------
 // Each lane's byte offsets of its COPY_INSTS 16-byte chunks are fixed for a tile; a stage adds
@@ -108,7 +119,7 @@ struct TileDma {
 // LDS bytes base + 16*l, so the swizzle is applied to the global address each lane reads.
 // Stage offset: 2*r0 bytes.
 __device__ __forceinline__ TileDma row_tile_dma(const uint16_t* p, int64_t ld, int64_t row0,
-                                                int64_t nrows) {
+                                                int64_t nrows, int64_t half = 0) {
   TileDma d;
   d.r = make_rsrc(p, (uint32_t)(nrows * ld * 2));
 #pragma unroll
@@ -117,6 +128,7 @@ __device__ __forceinline__ TileDma row_tile_dma(const uint16_t* p, int64_t ld, i
     const int row = pch >> 3, c = (pch & 7) ^ row_swz(row);
     int64_t gr = row0 + row;
     gr = gr < nrows ? gr : nrows - 1;                 // rows past the end: any valid row
+    gr = half_row(gr, half);
     d.off[it] = (uint32_t)((gr * ld + c * 8) * 2);
   }
   return d;

@@ -23,14 +23,15 @@ enum { EPI_BF16 = 0, EPI_PAL = 1, EPI_SOFT = 2, EPI_F32 = 3, EPI_SWIGLU = 4 };
 // the rank-r second segment.
 __device__ __forceinline__ void copy_row_tile_masked(uint4* lds, const uint16_t* p, int64_t ld,
                                                      int64_t row0, int64_t nrows, int64_t r0,
-                                                     int64_t rend) {
+                                                     int64_t rend, int64_t half = 0) {
 #pragma unroll
   for (int it = 0; it < COPY_INSTS; ++it) {
     const int ch = it * NTHR + threadIdx.x;
     const int row = ch >> 3, c = ch & 7;
     const int64_t gr = row0 + row, gk = r0 + 8 * c;
     uint4 v = make_uint4(0, 0, 0, 0);
-    if (gr < nrows && gk < rend) v = *reinterpret_cast<const uint4*>(p + gr * ld + gk);
+    if (gr < nrows && gk < rend)
+      v = *reinterpret_cast<const uint4*>(p + half_row(gr, half) * ld + gk);
     lds[row_chunk(row, c)] = v;
   }
 }
@@ -686,15 +687,30 @@ __device__ __forceinline__ void store_tile_bf16(const Args& g, const f32x16 (&ac
 }
 
 // EPI_SWIGLU: the tile's columns are 128 gate columns followed by the 128 matching up columns
-// (the weight's rows interleaved in 128-row blocks); writes h = swiglu(gate, up) to the 128
-// columns j0/2 .. j0/2+127 of the [I, J/2] output, from the staged bf16 values, exactly as a
-// bf16 gate/up GEMM followed by the elementwise SwiGLU.
+// (the weight's rows interleaved in 128-row blocks, or a [gate | up] weight read through
+// half_row); writes h = swiglu(gate, up) to the 128 columns j0/2 .. j0/2+127 of the [I, J/2]
+// output, from the staged bf16 values, exactly as a bf16 gate/up GEMM followed by the
+// elementwise SwiGLU, and with c2 set also the staged gate/up values themselves.
 __device__ __forceinline__ void store_tile_swiglu(const Args& g, const f32x16 (&acc)[WT_I][WT_J],
                                                   lds_u8* st, int64_t i0, int64_t j0, int wi,
                                                   int wj, int lane) {
   stage_tile_bf16(g, acc, st, j0, wi, wj, lane);
   uint16_t* C = reinterpret_cast<uint16_t*>(g.c);
   const int64_t h0 = j0 / 2;
+  if (g.c2) {
+#pragma unroll 4
+    for (int it = 0; it < TILE * TILE / 8 / NTHR; ++it) {
+      const int ch = it * NTHR + threadIdx.x;  // 32 chunks of 8 columns per row
+      const int row = ch >> 5, c8 = (ch & 31) * 8;
+      const int64_t i = i0 + row;
+      if (i < g.I) {
+        const u32x4 v = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(st + row * EPI_RS + c8 * 2);
+        // 8 consecutive columns never straddle the two halves (c8 % 8 == 0)
+        __builtin_nontemporal_store(
+            v, reinterpret_cast<u32x4*>(g.c2 + i * g.ldc2 + half_row(j0 + c8, g.b_half)));
+      }
+    }
+  }
 #pragma unroll 2
   for (int it = 0; it < TILE * (TILE / 2) / 8 / NTHR; ++it) {
     const int ch = it * NTHR + threadIdx.x;  // 16 chunks of 8 output columns per row
@@ -760,7 +776,7 @@ __global__ __launch_bounds__(NTHR) void gemm2_kernel(const Args g) {
   // have the same LDS layouts as the main ones (A row-major; B row tile in the forward,
   // col tile in grad_x), so every stage runs the same MFMA body.
   const bool tail = (rlen % BK) != 0;
-  const bool lora = EPI == EPI_BF16 && g.R2 > 0 && zsl == 0 && part == 0;
+  const bool lora = (EPI == EPI_BF16 || EPI == EPI_SWIGLU) && g.R2 > 0 && zsl == 0 && part == 0;
   const int nst = nfull + (tail ? 1 : 0) + (lora ? 1 : 0);
 
   // The palette operand's registers are loaded one stage ahead of the copies: during stage
@@ -778,7 +794,9 @@ __global__ __launch_bounds__(NTHR) void gemm2_kernel(const Args g) {
   LutDma dL;
   if (KA == OP_ROW) dA = row_tile_dma(g.a, g.lda, i0, g.I);
   else dA = col_tile_dma(g.a, g.lda, i0, g.I, g.R);
-  if (KB == OP_ROW) dB = row_tile_dma(g.b, g.ldb, j0, g.J);
+  // B rows of a [gate | up] weight (EPI_SWIGLU only: the other kernels' copies are unchanged)
+  const int64_t bhalf = EPI == EPI_SWIGLU ? g.b_half : 0;
+  if (KB == OP_ROW) dB = row_tile_dma(g.b, g.ldb, j0, g.J, bhalf);
   if (KB == OP_COL) dB = col_tile_dma(g.b, g.ldb, j0, g.J, g.R);
   if (KB == OP_LUT_REG) dL = lut_raw_dma(g, j0);
   auto copy_stage = [&](lds_u8* As, lds_u8* Bs, int64_t r0) {
@@ -796,7 +814,7 @@ __global__ __launch_bounds__(NTHR) void gemm2_kernel(const Args g) {
       const int64_t r0 = rbeg + (int64_t)nfull * BK;
       if (KA == OP_ROW) copy_row_tile_masked((uint4*)As, g.a, g.lda, i0, g.I, r0, rend);
       else copy_col_tile_masked((uint4*)As, g.a, g.lda, i0, g.I, r0, rend);
-      if (KB == OP_ROW) copy_row_tile_masked((uint4*)Bs, g.b, g.ldb, j0, g.J, r0, rend);
+      if (KB == OP_ROW) copy_row_tile_masked((uint4*)Bs, g.b, g.ldb, j0, g.J, r0, rend, bhalf);
       else if (KB == OP_COL) copy_col_tile_masked((uint4*)Bs, g.b, g.ldb, j0, g.J, r0, rend);
       else {
         LutRegs t;
@@ -807,7 +825,7 @@ __global__ __launch_bounds__(NTHR) void gemm2_kernel(const Args g) {
     } else {
       copy_row_tile_masked((uint4*)As, g.a2, g.R2, i0, g.I, 0, g.R2);
       if (B_COL) copy_col_tile_masked((uint4*)Bs, g.b2, g.J, j0, g.J, 0, g.R2);
-      else copy_row_tile_masked((uint4*)Bs, g.b2, g.R2, j0, g.J, 0, g.R2);
+      else copy_row_tile_masked((uint4*)Bs, g.b2, g.R2, j0, g.J, 0, g.R2, bhalf);
     }
   };
   constexpr bool LUT = KB == OP_LUT_ROW || KB == OP_LUT_COL;
@@ -1831,6 +1849,29 @@ int plz_linear_fwd_dense_swiglu(const uint16_t* x, const uint16_t* w_gate_up, ui
   g.group = 8;
   return launch<OP_ROW, OP_ROW, EPI_SWIGLU>(g, 1, (hipStream_t)stream,
                                             "plz_linear_fwd_dense_swiglu");
+}
+
+int plz_linear_fwd_dense_swiglu_cat(const uint16_t* x, const uint16_t* w, const uint16_t* lora_t,
+                                    const uint16_t* lora_b, int rank, uint16_t* y, uint16_t* h,
+                                    int64_t M, int64_t F, int64_t K, void* stream) {
+  const char* what = "plz_linear_fwd_dense_swiglu_cat";
+  PLZ_REQUIRE(M >= 0 && F >= 0 && K >= 0, "%s: negative shape", what);
+  PLZ_REQUIRE(K % 8 == 0 && F % 128 == 0, "%s: K must be a multiple of 8 and F of 128", what);
+  PLZ_REQUIRE(rank >= 0 && rank <= BK && rank % 8 == 0,
+              "%s: rank (%d) must be a multiple of 8 in [0, 64]", what, rank);
+  if (M == 0 || F == 0) return PLZ_OK;
+  PLZ_REQUIRE(x && w && h && a16(x) && a16(w) && a16(h) && (!y || a16(y)),
+              "%s: x, w, h must be non-null; x, w, h, y 16-byte aligned", what);
+  PLZ_REQUIRE(rank == 0 || (lora_t && lora_b && a16(lora_t) && a16(lora_b)),
+              "%s: rank > 0 needs 16-byte aligned lora_t and lora_b", what);
+  Args g = {};
+  g.a = x; g.lda = K; g.b = w; g.ldb = K;
+  g.I = M; g.J = 2 * F; g.R = K;
+  g.a2 = lora_t; g.b2 = lora_b; g.R2 = rank;
+  g.c = h; g.ldc = F; g.alpha = 1.f;
+  g.b_half = F; g.c2 = y; g.ldc2 = 2 * F;
+  g.group = kDenseGroup;
+  return launch<OP_ROW, OP_ROW, EPI_SWIGLU>(g, 1, (hipStream_t)stream, what);
 }
 
 size_t plz_linear_bwd_x_dense_workspace(int64_t M, int64_t N, int64_t K) {

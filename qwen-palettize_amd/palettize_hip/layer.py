@@ -341,14 +341,29 @@ class SoftLinearGroup:
         self._sync_counters()
         return spec
 
-    def forward(self, x, prebuilt):
-        _gpu_bf16(x, "SoftLinearGroup input")
-        lead = x.shape[:-1]
+    def _params(self):
         params = []
         for p in self.parts:
             params += [p.palette, p.index_logits, p.lora_a, p.lora_b]
-        y = SoftLinearGroupFunction.apply(x.reshape(-1, x.shape[-1]), self, prebuilt, *params)
+        return params
+
+    def forward(self, x, prebuilt):
+        _gpu_bf16(x, "SoftLinearGroup input")
+        lead = x.shape[:-1]
+        y = SoftLinearGroupFunction.apply(x.reshape(-1, x.shape[-1]), self, prebuilt,
+                                          *self._params())
         return y.reshape(*lead, self.N)
+
+    def forward_swiglu(self, x, prebuilt):
+        """silu(gate) * up of a [gate | up] group from one GEMM (the SwiGLU in its epilogue):
+        the same values as SwiGLUCatFunction over forward(x, prebuilt), bit for bit."""
+        _gpu_bf16(x, "SoftLinearGroup input")
+        if len(self.parts) != 2 or self.rows[0] != self.rows[1] or self.rows[0] % 128:
+            raise ValueError("forward_swiglu needs two parts of equal rows, a multiple of 128")
+        lead = x.shape[:-1]
+        h = SoftGateUpSwiGLUFunction.apply(x.reshape(-1, x.shape[-1]), self, prebuilt,
+                                           *self._params())
+        return h.reshape(*lead, self.N // 2)
 
 
 class SoftLinearGroupFunction(torch.autograd.Function):
@@ -357,20 +372,30 @@ class SoftLinearGroupFunction(torch.autograd.Function):
     slices of the fused ones (grad_B the part's diagonal block)."""
 
     @staticmethod
-    def forward(ctx, x, grp, prebuilt, *params):
+    def _setup(ctx, x, grp, prebuilt):
+        """(x, w, t, b) of this forward; records what the backward needs besides the saved
+        tensors."""
         x = x.contiguous()
         w, build, noise = prebuilt
         ctx.guard = (build, build.generation)
         a, b = grp.lora_a(), grp.lora_b()
         t = ops.lora_project(x, a, grp.lora_scale)
-        y = ops.linear_fwd_dense(x, w, None, t, b)
         ctx.grp, ctx.noise, ctx.tau = grp, noise, float(grp.parts[0].tau)
+        return x, w, a, b, t
+
+    @staticmethod
+    def forward(ctx, x, grp, prebuilt, *params):
+        x, w, a, b, t = SoftLinearGroupFunction._setup(ctx, x, grp, prebuilt)
+        y = ops.linear_fwd_dense(x, w, None, t, b)
         ctx.save_for_backward(x, grp.palette(), grp.logits(), w, a, b.clone())
         return y
 
     @staticmethod
     def backward(ctx, gy):
-        x, pal, logits, w, a, b = ctx.saved_tensors
+        return SoftLinearGroupFunction._backward(ctx, gy, *ctx.saved_tensors)
+
+    @staticmethod
+    def _backward(ctx, gy, x, pal, logits, w, a, b):
         grp = ctx.grp
         if ctx.guard[0].generation != ctx.guard[1]:
             raise RuntimeError("the prebuilt soft weight of this forward was rebuilt by a later "
@@ -390,6 +415,26 @@ class SoftLinearGroupFunction(torch.autograd.Function):
             r0 += n
             c0 += r
         return (grad_x, None, None, *grads)
+
+
+class SoftGateUpSwiGLUFunction(torch.autograd.Function):
+    """A [gate | up] SoftLinearGroup followed by the SwiGLU, as one GEMM whose epilogue writes
+    both the pre-activations (kept for the backward) and h (plz_linear_fwd_dense_swiglu_cat).
+    The backward is the SwiGLU's (plz_swiglu_bwd_rows) and then the group's own."""
+
+    @staticmethod
+    def forward(ctx, x, grp, prebuilt, *params):
+        x, w, a, b, t = SoftLinearGroupFunction._setup(ctx, x, grp, prebuilt)
+        y, h = ops.linear_fwd_dense_swiglu_cat(x, w, t, b)
+        ctx.save_for_backward(x, grp.palette(), grp.logits(), w, a, b.clone(), y)
+        return h
+
+    @staticmethod
+    def backward(ctx, gh):
+        x, pal, logits, w, a, b, y = ctx.saved_tensors
+        gy = ops.swiglu_bwd_cat(y, gh.contiguous())
+        del y
+        return SoftLinearGroupFunction._backward(ctx, gy, x, pal, logits, w, a, b)
 
 
 # ---- RoPE / attention -------------------------------------------------------------------------
@@ -577,7 +622,7 @@ class PalettizedDecoderLayer(nn.Module):
         hs, x = add_rmsnorm(self.post_attention_layernorm, hs,
                             self.o_proj(attention(q, k, v, cfg.heads, cfg.kv_heads), pw["o_proj"]))
         if self.gate_up is not None:
-            h = SwiGLUCatFunction.apply(self.gate_up.forward(x, pw["gate_up"]))
+            h = self.gate_up.forward_swiglu(x, pw["gate_up"])
         else:
             h = SwiGLUFunction.apply(self.gate_proj(x, pw["gate_proj"]), self.up_proj(x, pw["up_proj"]))
         return hs + self.down_proj(h, pw["down_proj"])

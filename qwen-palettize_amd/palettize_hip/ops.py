@@ -271,6 +271,24 @@ def linear_fwd_dense_swiglu(x, w_gate_up):
     return h
 
 
+def linear_fwd_dense_swiglu_cat(x, w, lora_t=None, lora_b=None, keep_pre=True):
+    """(y, h): y = x w^T (+ lora_t lora_b^T) for w = [Wg; Wu] of 2F rows, and h = silu(y[:, :F])
+    * y[:, F:] from the same GEMM (plz_linear_fwd_dense_swiglu_cat); y is None unless
+    keep_pre. Bit-equal to linear_fwd_dense followed by swiglu_fwd_cat."""
+    _need(x, "x", torch.bfloat16, 2)
+    _need(w, "w", torch.bfloat16, 2)
+    M, K = x.shape
+    F = w.shape[0] // 2
+    if w.shape[1] != K or w.shape[0] != 2 * F:
+        raise ValueError("x / w shape mismatch")
+    rank = _lora_pair(lora_t, lora_b, "lora_t", "lora_b", M, 2 * F)
+    y = torch.empty((M, 2 * F), dtype=torch.bfloat16, device=x.device) if keep_pre else None
+    h = torch.empty((M, F), dtype=torch.bfloat16, device=x.device)
+    call("plz_linear_fwd_dense_swiglu_cat", _ptr(x), _ptr(w), _ptr(lora_t), _ptr(lora_b), rank,
+         _ptr(y), _ptr(h), M, F, K, _stream(x))
+    return y, h
+
+
 def linear_fwd_dense(x, w, bias=None, lora_t=None, lora_b=None):
     _need(x, "x", torch.bfloat16, 2)
     _need(w, "w", torch.bfloat16, 2)

@@ -36,7 +36,7 @@ def test_every_declared_symbol_is_exported(lib):
         assert hasattr(lib, n), f"{n} declared in the header but not exported"
         assert n in _lib.SIGNATURES, f"{n} has no ctypes signature"
     assert set(_lib.SIGNATURES) == set(names)
-    assert lib.plz_abi_version() == 13
+    assert lib.plz_abi_version() == 14
 
 
 def test_shape_errors_are_reported_without_touching_the_gpu(lib):

@@ -126,6 +126,35 @@ def test_swiglu_concatenated_layout(dev):
         ops.swiglu_bwd_cat(gu.to(dev), gh[:, :-8].contiguous().to(dev))
 
 
+@pytest.mark.parametrize("M,F,K,r", [(300, 384, 512, 32), (64, 128, 2560, 16),
+                                     (2048, 9728, 2560, 32), (513, 640, 264, 0)])
+def test_gate_up_gemm_with_swiglu_epilogue(dev, M, F, K, r):
+    """plz_linear_fwd_dense_swiglu_cat on a [Wg; Wu] weight as stored: its pre-activations are
+    the unsplit plz_linear_fwd_dense output (no workspace, so the same reduction order) and its
+    h is swiglu_fwd_cat of them, every bit, with and without LoRA, for ragged row tiles, an odd
+    count of 128-row halves (F = 384, 640), a single tile (which the dense forward would split
+    over K when given its workspace) and the Qwen-4B gate/up shape; and the pre-activations
+    against fp64."""
+    x = randn_bf16(M, K, seed=M + F).to(dev)
+    w = randn_bf16(2 * F, K, seed=K + 1, std=0.03).to(dev)
+    t = b = None
+    if r:
+        t = randn_bf16(M, r, seed=3).to(dev)
+        b = randn_bf16(2 * F, r, seed=4, std=0.05).to(dev)
+    want_y = torch.empty((M, 2 * F), dtype=torch.bfloat16, device=dev)
+    ops.call("plz_linear_fwd_dense", x.data_ptr(), w.data_ptr(), None, ops._ptr(t), ops._ptr(b),
+             r, want_y.data_ptr(), None, 0, M, 2 * F, K, ops._stream(x))
+    want_h = ops.swiglu_fwd_cat(want_y)
+    y, h = ops.linear_fwd_dense_swiglu_cat(x, w, t, b)
+    assert torch.equal(y.view(torch.int16), want_y.view(torch.int16))
+    assert torch.equal(h.view(torch.int16), want_h.view(torch.int16))
+    none, h2 = ops.linear_fwd_dense_swiglu_cat(x, w, t, b, keep_pre=False)
+    assert none is None and torch.equal(h2.view(torch.int16), want_h.view(torch.int16))
+    xs, ws = f32(x).astype(np.float64), f32(w).astype(np.float64)
+    ref = xs @ ws.T + (f32(t).astype(np.float64) @ f32(b).T if r else 0.0)
+    assert_close(f32(y), ref, what="gate/up pre-activations")
+
+
 @pytest.mark.parametrize("M,r,train_pal", [(256, 16, True), (4096, 16, True), (4096, 32, False)])
 def test_lut_linear_autograd_with_lora(dev, M, r, train_pal):
     """From 4096 rows the forward dequantises W once and grad_x reuses it; with the palette
