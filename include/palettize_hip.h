@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define PLZ_ABI_VERSION 14
+#define PLZ_ABI_VERSION 15
 
 /* status codes */
 #define PLZ_OK 0
@@ -255,6 +255,8 @@ typedef struct plz_build_w_desc {
   int32_t reserved;
   int64_t block_begin;     /* filled by plz_build_w_plan */
   uint64_t noise_seed;     /* Philox key of a descriptor without a noise tensor */
+  uint64_t noise_counter;  /* its counter base: weight (n, k) draws at offset + noise_counter
+                              + n*K + k (0 for the layout above) */
 } plz_build_w_desc;
 /* Checks n host descriptors, fills block_begin and returns the launch's block count (or a
  * negative status). */
@@ -456,6 +458,24 @@ int plz_adamw_step(const plz_adamw_desc* descs_device, int n, int64_t total_bloc
                    float max_norm0, float max_norm1, double beta1, double beta2, float eps,
                    float weight_decay, int64_t step, float* norms_out, void* workspace,
                    size_t workspace_bytes, void* stream);
+/* The step above that also builds the next forward's soft weights from the logits it has just
+ * updated (the train loop's optimizer step followed by the next forward's
+ * fused_compute_P_W_batched, fused_lut_linear_cuda.py:1016-1075): builds[i] (n entries, w NULL
+ * for none) rebuilds descriptor i's bf16 [N, K, 4] logits (builds[i].logits == param) as
+ * plz_soft_build_w_batched_philox(noise_offset, tau, mode) would from the stored values, bit
+ * for bit. No counterpart in the reference, which runs the two passes apart; here the build's
+ * arithmetic rides on the update's memory-bound pass. The descriptors with a build come after
+ * all others; the others (the palettes the builds read) are updated by a first launch, the
+ * built ones by a second. plz_adamw_plan_build plans both tables and returns the block count,
+ * with *split_block = the first built block. */
+int64_t plz_adamw_plan_build(plz_adamw_desc* descs, const plz_build_w_desc* builds, int n,
+                             int64_t* split_block);
+int plz_adamw_step_build(const plz_adamw_desc* descs_device, const plz_build_w_desc* builds_device,
+                         int n, int64_t total_blocks, int64_t split_block, uint64_t noise_offset,
+                         float tau, int mode, float max_norm0, float max_norm1, double beta1,
+                         double beta2, float eps, float weight_decay, int64_t step,
+                         float* norms_out, void* workspace, size_t workspace_bytes,
+                         void* stream);
 
 /* ---- fused RMSNorm and SwiGLU ------------------------------------------------------------
  * The reference runs the HF Qwen3 modules unfused (Qwen3RMSNorm and Qwen3MLP, transformers

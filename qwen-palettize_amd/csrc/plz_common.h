@@ -184,6 +184,54 @@ __device__ __forceinline__ void philox_gumbel4(uint64_t seed, uint64_t ctr, floa
   z[3] = gumbel_from_bits(r.w);
 }
 
+// The soft forward weight of two consecutive weights of a row (fused_lut_kernel.cu:1974-2003;
+// triton_soft_forward.py:160-176 for PLZ_W_HARD_PLAIN) from their 8 logits (lw: bf16 or fp16
+// bits, weight-major, classes in order), their 8 noise values and the row's palette group pc:
+//   P_c = softmax_c((logit_c + noise_c) / tau)   (one reciprocal of the sum)
+//   W_soft = sum_c P_c pal_c,   W_hard = pal[argmax P] (first maximum wins), or over the plain
+//   logits with PLZ_W_HARD_PLAIN
+// wo = bf16 W of the mode, so = bf16 W_soft. The build-W kernels and the optimizer step that
+// builds the next forward's W call this one function, so their W agree bit for bit.
+__device__ __forceinline__ void build_w_two(const uint32_t (&lw)[4], int f16, const float (&nz)[8],
+                                            const float (&pc)[4], float inv_tau, int mode,
+                                            uint32_t (&wo)[2], uint32_t (&so)[2]) {
+#pragma unroll
+  for (int el = 0; el < 2; ++el) {
+    float l[4], a[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const uint32_t bits = (lw[2 * el + c / 2] >> (16 * (c & 1))) & 0xffffu;
+      l[c] = f16 ? h2f(bits) : bf2f(bits);
+      a[c] = (l[c] + nz[4 * el + c]) * inv_tau;
+    }
+    const float m = fmaxf(fmaxf(a[0], a[1]), fmaxf(a[2], a[3]));
+    float e[4], s = 0.f;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      e[c] = __expf(a[c] - m);
+      s += e[c];
+    }
+    // one reciprocal, as the soft backward's epilogue computes P: both passes see the same P
+    const float rs = 1.f / s;
+    float P[4], ws = 0.f;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      P[c] = e[c] * rs;
+      ws += P[c] * pc[c];
+    }
+    // argmax, first maximum wins (strict >), over P (noisy) or over the plain logits
+    const float* v = mode == PLZ_W_HARD_PLAIN ? l : P;
+    int am = 0;
+    float best = v[0];
+#pragma unroll
+    for (int c = 1; c < 4; ++c)
+      if (v[c] > best) { best = v[c]; am = c; }
+    const float wh = am == 0 ? pc[0] : am == 1 ? pc[1] : am == 2 ? pc[2] : pc[3];
+    wo[el] = f2bf(mode == PLZ_W_SOFT ? ws : wh);
+    so[el] = f2bf(ws);
+  }
+}
+
 // SwiGLU of one element as the HF Qwen3 MLP computes it on bf16 tensors: h = bf16(silu(g)) * u
 // for bf16 values g, u (the caller rounds h to bf16). Shared by the elementwise kernel and the
 // GEMM epilogue, so the fused and unfused paths agree bit for bit on the same g, u.

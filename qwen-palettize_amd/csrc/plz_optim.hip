@@ -166,11 +166,56 @@ __device__ __forceinline__ float adamw_one(float g, float& p, float& m, float& v
   return p;
 }
 
+// The next forward's weight of the two weights whose 8 logits (elements i0 .. i0+7 of a
+// [N, K, 4] parameter, K even) were just updated, from their new bf16 bits lw: exactly what
+// build_w_batched_kernel computes from the stored logits (same helper, same noise counters).
+__device__ __forceinline__ void build_chunk(const plz_build_w_desc& bd, int64_t i0,
+                                            const uint32_t (&lw)[4], uint64_t offset,
+                                            float inv_tau, int mode) {
+  const uint32_t w0 = (uint32_t)(i0 >> 2);  // N*K < 2^31 (checked by the plan)
+  const uint32_t K = (uint32_t)bd.K;
+  const uint32_t n = w0 / K, k = w0 - n * K;
+  const float4 p = *reinterpret_cast<const float4*>(
+      bd.palette + ((size_t)n * (K / kPalGroup) + k / kPalGroup) * 4);
+  const float pc[4] = {p.x, p.y, p.z, p.w};
+  float nz[8];
+  if (bd.noise) {
+    const float4 z0 = *reinterpret_cast<const float4*>(bd.noise + i0);
+    const float4 z1 = *reinterpret_cast<const float4*>(bd.noise + i0 + 4);
+    nz[0] = z0.x; nz[1] = z0.y; nz[2] = z0.z; nz[3] = z0.w;
+    nz[4] = z1.x; nz[5] = z1.y; nz[6] = z1.z; nz[7] = z1.w;
+  } else {
+    float z[4];
+    const uint64_t ctr = offset + bd.noise_counter + w0;
+    philox_gumbel4(bd.noise_seed, ctr, z);
+    nz[0] = z[0]; nz[1] = z[1]; nz[2] = z[2]; nz[3] = z[3];
+    philox_gumbel4(bd.noise_seed, ctr + 1, z);
+    nz[4] = z[0]; nz[5] = z[1]; nz[6] = z[2]; nz[7] = z[3];
+  }
+  uint32_t wo[2], so[2];
+  build_w_two(lw, 0, nz, pc, inv_tau, mode, wo, so);
+  *reinterpret_cast<uint32_t*>(bd.w + w0) = wo[0] | (wo[1] << 16);
+  if (bd.w_soft) *reinterpret_cast<uint32_t*>(bd.w_soft + w0) = so[0] | (so[1] << 16);
+}
+
+struct BuildArgs {
+  const plz_build_w_desc* descs;  // entry i belongs to update descriptor i
+  uint64_t offset;
+  float inv_tau;
+  int mode;
+};
+
+// The update of blocks block0 .. block0 + gridDim.x - 1. BUILD: every descriptor of these blocks
+// has a build entry (the plan puts them after all others), whose weight is rebuilt from the
+// updated logits.
+template <bool BUILD>
 __global__ __launch_bounds__(kThreads) void adamw_kernel(const plz_adamw_desc* __restrict__ descs,
                                                          int n_desc, const float* __restrict__ coef,
-                                                         const Hyper h) {
-  const int64_t b = blockIdx.x;
-  const plz_adamw_desc d = descs[find_desc(descs, n_desc, b)];
+                                                         const Hyper h, int64_t block0,
+                                                         const BuildArgs ba) {
+  const int64_t b = blockIdx.x + block0;
+  const int di = find_desc(descs, n_desc, b);
+  const plz_adamw_desc d = descs[di];
   const int64_t base = (b - d.block_begin) * kBlockElems;
   const float c = coef[d.clip_group];
   const float step_size = d.lr / h.bc1;
@@ -204,6 +249,7 @@ __global__ __launch_bounds__(kThreads) void adamw_kernel(const plz_adamw_desc* _
         for (int j = 0; j < 4; ++j) w[j] = f2bf2(p[ch][2 * j], p[ch][2 * j + 1]);
         *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(d.param) + i0) =
             make_uint4(w[0], w[1], w[2], w[3]);
+        if (BUILD) build_chunk(ba.descs[di], i0, w, ba.offset, ba.inv_tau, ba.mode);
       } else if (d.master) {
         store8(reinterpret_cast<float*>(d.param) + i0, p[ch]);
       }
@@ -231,6 +277,7 @@ __global__ __launch_bounds__(kThreads) void adamw_kernel(const plz_adamw_desc* _
         for (int j = 0; j < 4; ++j) w[j] = f2bf2(p[2 * j], p[2 * j + 1]);
         *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(d.param) + i0) =
             make_uint4(w[0], w[1], w[2], w[3]);
+        if (BUILD) build_chunk(ba.descs[di], i0, w, ba.offset, ba.inv_tau, ba.mode);
       } else if (d.master) {
         store8(reinterpret_cast<float*>(d.param) + i0, p);
       }
@@ -294,44 +341,121 @@ size_t plz_adamw_workspace(int64_t total_blocks) {
   return ((size_t)total_blocks * 8 + 63) / 64 * 64 + 64;
 }
 
-int plz_adamw_step(const plz_adamw_desc* descs_device, int n, int64_t total_blocks,
-                   float max_norm0, float max_norm1, double beta1, double beta2, float eps,
-                   float weight_decay, int64_t step, float* norms_out, void* workspace,
-                   size_t workspace_bytes, void* stream) {
-  PLZ_REQUIRE(n >= 0 && total_blocks >= 0 && step >= 1, "plz_adamw_step: bad count or step");
+// The step of plz_adamw_step / plz_adamw_step_build: norms, clip coefficients, then the update
+// of blocks [0, split) and, with builds, of blocks [split, total) with their weights rebuilt.
+static int adamw_step_impl(const plz_adamw_desc* descs_device, const BuildArgs* ba, int n,
+                           int64_t total_blocks, int64_t split, float max_norm0, float max_norm1,
+                           double beta1, double beta2, float eps, float weight_decay,
+                           int64_t step, float* norms_out, void* workspace,
+                           size_t workspace_bytes, hipStream_t s, const char* what) {
+  PLZ_REQUIRE(n >= 0 && total_blocks >= 0 && step >= 1, "%s: bad count or step", what);
   PLZ_REQUIRE(beta1 >= 0.f && beta1 < 1.f && beta2 >= 0.f && beta2 < 1.f && eps > 0.f,
-              "plz_adamw_step: need 0 <= betas < 1 and eps > 0");
+              "%s: need 0 <= betas < 1 and eps > 0", what);
   if (n == 0 || total_blocks == 0) return PLZ_OK;
-  PLZ_REQUIRE(descs_device, "plz_adamw_step: null descriptor table");
-  PLZ_REQUIRE(total_blocks < (1ll << 31), "plz_adamw_step: too many elements");
+  PLZ_REQUIRE(descs_device, "%s: null descriptor table", what);
+  PLZ_REQUIRE(total_blocks < (1ll << 31), "%s: too many elements", what);
+  PLZ_REQUIRE(split >= 0 && split <= total_blocks, "%s: split block out of range", what);
   const size_t need = plz_adamw_workspace(total_blocks);
   if (!workspace || workspace_bytes < need) {
-    set_error("plz_adamw_step: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+    set_error("%s: workspace of %zu bytes needed, %zu given", what, need, workspace_bytes);
     return PLZ_EWORKSPACE;
   }
-  hipStream_t s = (hipStream_t)stream;
   float* partial = reinterpret_cast<float*>(workspace);
   int* group = reinterpret_cast<int*>(partial + total_blocks);
   float* coef = reinterpret_cast<float*>((char*)workspace + need - 64);
   hipLaunchKernelGGL(sumsq_kernel, dim3(grid_of(total_blocks)), dim3(kThreads), 0, s, descs_device,
                      n, partial, group);
-  int rc = check_launch("plz_adamw_step/sumsq");
+  int rc = check_launch(what);
   if (rc) return rc;
   hipLaunchKernelGGL(clip_coef_kernel, dim3(2), dim3(kCoefThreads), 0, s, partial, group,
                      total_blocks, max_norm0, max_norm1, coef);
-  if ((rc = check_launch("plz_adamw_step/coef"))) return rc;
+  if ((rc = check_launch(what))) return rc;
   // bias corrections in double on the host, as torch computes its Python-float scalars
   const float bc1 = (float)(1.0 - std::pow(beta1, (double)step));
   const float bc2_sqrt = (float)std::sqrt(1.0 - std::pow(beta2, (double)step));
   const Hyper h{(float)beta1, (float)beta2, eps, weight_decay, bc1, bc2_sqrt};
-  hipLaunchKernelGGL(adamw_kernel, dim3(grid_of(total_blocks)), dim3(kThreads), 0, s, descs_device,
-                     n, coef, h);
-  if ((rc = check_launch("plz_adamw_step/update"))) return rc;
+  const BuildArgs none{nullptr, 0, 1.f, 0};
+  if (split > 0) {
+    hipLaunchKernelGGL(adamw_kernel<false>, dim3(grid_of(split)), dim3(kThreads), 0, s,
+                       descs_device, n, coef, h, (int64_t)0, none);
+    if ((rc = check_launch(what))) return rc;
+  }
+  if (split < total_blocks) {
+    // the builds read palettes that blocks [0, split) update: a second launch on the same
+    // stream starts after all of them have finished
+    if (ba)
+      hipLaunchKernelGGL(adamw_kernel<true>, dim3(grid_of(total_blocks - split)), dim3(kThreads),
+                         0, s, descs_device, n, coef, h, split, *ba);
+    else
+      hipLaunchKernelGGL(adamw_kernel<false>, dim3(grid_of(total_blocks - split)), dim3(kThreads),
+                         0, s, descs_device, n, coef, h, split, none);
+    if ((rc = check_launch(what))) return rc;
+  }
   if (norms_out) {
     hipMemcpyAsync(norms_out, coef + 2, 2 * sizeof(float), hipMemcpyDeviceToDevice, s);
-    return check_launch("plz_adamw_step/norms");
+    return check_launch(what);
   }
   return PLZ_OK;
+}
+
+int plz_adamw_step(const plz_adamw_desc* descs_device, int n, int64_t total_blocks,
+                   float max_norm0, float max_norm1, double beta1, double beta2, float eps,
+                   float weight_decay, int64_t step, float* norms_out, void* workspace,
+                   size_t workspace_bytes, void* stream) {
+  return adamw_step_impl(descs_device, nullptr, n, total_blocks, total_blocks, max_norm0,
+                         max_norm1, beta1, beta2, eps, weight_decay, step, norms_out, workspace,
+                         workspace_bytes, (hipStream_t)stream, "plz_adamw_step");
+}
+
+int64_t plz_adamw_plan_build(plz_adamw_desc* descs, const plz_build_w_desc* builds, int n,
+                             int64_t* split_block) {
+  const int64_t total = plz_adamw_plan(descs, n);
+  if (total < 0) return total;
+  if (!split_block || (n > 0 && !builds)) {
+    set_error("plz_adamw_plan_build: need the build table and split_block");
+    return -PLZ_EINVAL;
+  }
+  int first = n;
+  for (int i = 0; i < n; ++i) {
+    const plz_build_w_desc& b = builds[i];
+    if (!b.w) {
+      if (first < n) {
+        set_error("plz_adamw_plan_build: descriptor %d has no build but follows descriptor %d, "
+                  "which has one: descriptors with a build must come last", i, first);
+        return -PLZ_EINVAL;
+      }
+      continue;
+    }
+    if (first == n) first = i;
+    const plz_adamw_desc& d = descs[i];
+    plz_build_w_desc probe = b;
+    if (d.dtype != PLZ_DT_BF16 || !d.master || b.logits != d.param ||
+        b.logits_dtype != PLZ_DT_BF16 || b.N <= 0 || b.K <= 0 || b.N * b.K * 4 != d.n ||
+        b.N * b.K >= (1ll << 31) || plz_build_w_plan(&probe, 1) < 0) {
+      set_error("plz_adamw_plan_build: build %d must rebuild its own bf16 [N, K, 4] parameter "
+                "(logits == param, N*K*4 == n, N*K < 2^31, K %% 256 == 0, aligned palette and w)", i);
+      return -PLZ_EINVAL;
+    }
+  }
+  *split_block = first < n ? descs[first].block_begin : total;
+  return total;
+}
+
+int plz_adamw_step_build(const plz_adamw_desc* descs_device, const plz_build_w_desc* builds_device,
+                         int n, int64_t total_blocks, int64_t split_block, uint64_t noise_offset,
+                         float tau, int mode, float max_norm0, float max_norm1, double beta1,
+                         double beta2, float eps, float weight_decay, int64_t step,
+                         float* norms_out, void* workspace, size_t workspace_bytes,
+                         void* stream) {
+  const char* what = "plz_adamw_step_build";
+  PLZ_REQUIRE(mode == PLZ_W_SOFT || mode == PLZ_W_HARD_NOISY || mode == PLZ_W_HARD_PLAIN,
+              "%s: unknown mode %d", what, mode);
+  PLZ_REQUIRE(tau > 0.f, "%s: tau must be positive", what);
+  PLZ_REQUIRE(builds_device || split_block >= total_blocks, "%s: null build table", what);
+  const BuildArgs ba{builds_device, noise_offset, 1.f / tau, mode};
+  return adamw_step_impl(descs_device, &ba, n, total_blocks, split_block, max_norm0, max_norm1,
+                         beta1, beta2, eps, weight_decay, step, norms_out, workspace,
+                         workspace_bytes, (hipStream_t)stream, what);
 }
 
 }  // extern "C"

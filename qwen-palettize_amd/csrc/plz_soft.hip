@@ -170,41 +170,7 @@ __device__ __forceinline__ void build_w_pair(const uint16_t* __restrict__ logits
     nz[4] = z1.x; nz[5] = z1.y; nz[6] = z1.z; nz[7] = z1.w;
   }
   uint32_t wo[2], so[2];
-#pragma unroll
-  for (int el = 0; el < 2; ++el) {
-    float l[4], a[4];
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const uint32_t bits = (lw[2 * el + c / 2] >> (16 * (c & 1))) & 0xffffu;
-      l[c] = f16 ? h2f(bits) : bf2f(bits);
-      a[c] = (l[c] + nz[4 * el + c]) * inv_tau;
-    }
-    const float m = fmaxf(fmaxf(a[0], a[1]), fmaxf(a[2], a[3]));
-    float e[4], s = 0.f;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      e[c] = __expf(a[c] - m);
-      s += e[c];
-    }
-    // one reciprocal, as the soft backward's epilogue computes P: both passes see the same P
-    const float rs = 1.f / s;
-    float P[4], ws = 0.f;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      P[c] = e[c] * rs;
-      ws += P[c] * pc[c];
-    }
-    // argmax, first maximum wins (strict >), over P (noisy) or over the plain logits
-    const float* v = mode == PLZ_W_HARD_PLAIN ? l : P;
-    int am = 0;
-    float best = v[0];
-#pragma unroll
-    for (int c = 1; c < 4; ++c)
-      if (v[c] > best) { best = v[c]; am = c; }
-    const float wh = am == 0 ? pc[0] : am == 1 ? pc[1] : am == 2 ? pc[2] : pc[3];
-    wo[el] = f2bf(mode == PLZ_W_SOFT ? ws : wh);
-    so[el] = f2bf(ws);
-  }
+  build_w_two(lw, f16, nz, pc, inv_tau, mode, wo, so);
   const int64_t o = n * K + k;
   *reinterpret_cast<uint32_t*>(w + o) = wo[0] | (wo[1] << 16);
   if (w_soft) *reinterpret_cast<uint32_t*>(w_soft + o) = so[0] | (so[1] << 16);
@@ -239,8 +205,8 @@ __global__ void build_w_batched_kernel(const plz_build_w_desc* __restrict__ desc
     build_w_pair<false>(d.logits, d.logits_dtype == PLZ_DT_FP16, d.noise, 0, 0, d.palette,
                         inv_tau, mode, d.w, d.w_soft, d.K, t);
   else  // the descriptor's own Philox key (uniform per block)
-    build_w_pair<true>(d.logits, d.logits_dtype == PLZ_DT_FP16, nullptr, d.noise_seed, offset,
-                       d.palette, inv_tau, mode, d.w, d.w_soft, d.K, t);
+    build_w_pair<true>(d.logits, d.logits_dtype == PLZ_DT_FP16, nullptr, d.noise_seed,
+                       offset + d.noise_counter, d.palette, inv_tau, mode, d.w, d.w_soft, d.K, t);
 }
 
 }  // namespace plz

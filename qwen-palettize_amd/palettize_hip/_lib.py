@@ -24,7 +24,7 @@ i32, i64, u32, u64, f32, sz = C.c_int, C.c_int64, C.c_uint32, C.c_uint64, C.c_fl
 class BuildWDesc(C.Structure):
     _fields_ = [("logits", p), ("noise", p), ("palette", p), ("w", p), ("w_soft", p),
                 ("N", i64), ("K", i64), ("logits_dtype", i32), ("reserved", i32),
-                ("block_begin", i64), ("noise_seed", u64)]
+                ("block_begin", i64), ("noise_seed", u64), ("noise_counter", u64)]
 
 
 class PwRefDesc(C.Structure):
@@ -118,6 +118,10 @@ SIGNATURES: dict[str, tuple] = {
     "plz_adamw_workspace": (sz, [i64]),
     "plz_adamw_step": (i32, [p, i32, i64, f32, f32, C.c_double, C.c_double, f32, f32, i64, p, p,
                              sz, p]),
+    "plz_adamw_plan_build": (i64, [C.POINTER(AdamWDesc), C.POINTER(BuildWDesc), i32,
+                                   C.POINTER(C.c_int64)]),
+    "plz_adamw_step_build": (i32, [p, p, i32, i64, i64, u64, f32, i32, f32, f32, C.c_double,
+                                   C.c_double, f32, f32, i64, p, p, sz, p]),
     "plz_rmsnorm_fwd": (i32, [p, p, p, p, i64, i64, f32, p]),
     "plz_add_rmsnorm_fwd": (i32, [p, p, p, p, p, p, i64, i64, f32, p]),
     "plz_rmsnorm_bwd_add": (i32, [p, p, p, p, p, p, i64, i64, p]),

@@ -35,7 +35,7 @@ import torch.nn.functional as F
 from . import ops
 from ._lib import PLZ_W_HARD_NOISY
 from .functional import SoftLUTLinearFunction
-from .optim import FusedAdamW
+from .optim import FusedAdamW, NextBuild
 
 
 def _gpu_bf16(t, what):
@@ -565,6 +565,7 @@ class PalettizedDecoderLayer(nn.Module):
             self.gate_up = SoftLinearGroup([self.gate_proj, self.up_proj])
         self._wgroup = None
         self._wgroup_key = None
+        self._pending = None  # weights built by the last optimizer step (commit_next_build)
 
     def linears(self):
         return [getattr(self, n) for n in self.NAMES]
@@ -580,34 +581,89 @@ class PalettizedDecoderLayer(nn.Module):
             out.append((n, getattr(self, n)))
         return out
 
-    def build_weights(self):
-        """The linears' forward weights in one launch (plz_soft_build_w_batched_philox): each
-        linear's (or group's) own Philox key at the shared counter offset of this forward, the
-        same tau. Returns {name: (w, group, noise)} for the forward, with "gate_up" for the
-        grouped gate and up."""
+    def _build_group(self):
+        """(units, the batched build group of their weights), the group rebuilt when a
+        parameter has been replaced rather than written in place (module.to(),
+        load_state_dict(assign=True), param.data = ...): its descriptor table holds the
+        parameters' device addresses."""
         units = self._units()
-        lins = self.linears()
         items = []
         for _, u in units:
             if isinstance(u, SoftLinearGroup):
                 items.append((u.logits(), ops.PhiloxNoise(u.parts[0].noise_seed, 0), u.palette()))
             else:
                 items.append((u.index_logits, ops.PhiloxNoise(u.noise_seed, 0), u.palette))
-        # the group's descriptor table holds the parameters' device addresses: rebuild it when a
-        # parameter has been replaced rather than written in place (module.to(),
-        # load_state_dict(assign=True), param.data = ...)
         key = tuple((t.data_ptr(), t.device) for lg, _, pal in items for t in (lg, pal))
         if self._wgroup is None or self._wgroup_key != key:
             self._wgroup = ops.SoftBuildGroup(items, PLZ_W_HARD_NOISY)
             self._wgroup_key = key
+        return units, self._wgroup
+
+    def _next_offset(self, units, check_tau=True):
+        lins = self.linears()
         first = [u.parts[0] if isinstance(u, SoftLinearGroup) else u for _, u in units]
         offset = first[0].noise_counter
         if any(l.noise_counter != offset for l in first) or any(
-                l.mode != PLZ_W_HARD_NOISY or l.tau != lins[0].tau for l in lins):
+                l.mode != PLZ_W_HARD_NOISY or (check_tau and l.tau != lins[0].tau) for l in lins):
             raise RuntimeError("batched build: the linears must share noise offset, mode and tau")
+        return offset
+
+    def _weight_params(self):
+        return [t for l in self.linears() for t in (l.index_logits, l.palette)]
+
+    def build_weights(self):
+        """The linears' forward weights in one launch (plz_soft_build_w_batched_philox): each
+        linear's (or group's) own Philox key at the shared counter offset of this forward, the
+        same tau. Returns {name: (w, group, noise)} for the forward, with "gate_up" for the
+        grouped gate and up. When the last optimizer step has already built them
+        (plan_next_build / commit_next_build) and no logits, palette or tau has changed since,
+        those weights are used as they are."""
+        pend, self._pending = self._pending, None
+        units, grp = self._build_group()
+        tau = self.linears()[0].tau
+        if pend is not None:  # the noise counters have advanced already
+            self._next_offset(units)
+            if (pend["key"] == self._wgroup_key and pend["complete"] and pend["tau"] == tau and
+                    all(p._version == v for p, v in pend["versions"])):
+                outs = grp.outputs
+            else:  # built from values that have changed since: build again, same noise
+                outs = grp.run(tau, pend["offset"])
+            return {n: (w, grp, sp) for (n, _), (w, _), sp in zip(units, outs, pend["specs"])}
+        offset = self._next_offset(units)
         specs = [u.next_noise_spec() for _, u in units]
-        outs = self._wgroup.run(lins[0].tau, offset)
-        return {n: (w, self._wgroup, sp) for (n, _), (w, _), sp in zip(units, outs, specs)}
+        outs = grp.run(tau, offset)
+        return {n: (w, grp, sp) for (n, _), (w, _), sp in zip(units, outs, specs)}
+
+    def plan_next_build(self, tau):
+        """The next forward's weights as an optimizer-step build (optim.NextBuild): every
+        linear's logits, palette and output rows of the batched build group, with the noise of
+        the next forward (the counters advance now instead of in that forward). Pass it to
+        FusedAdamW.step(build=...), then to commit_next_build."""
+        units, grp = self._build_group()
+        offset = self._next_offset(units, check_tau=False)
+        specs = [u.next_noise_spec() for _, u in units]
+        items = []
+        for (_, u), (w, _) in zip(units, grp.outputs):
+            if isinstance(u, SoftLinearGroup):
+                r0 = 0
+                for p, n in zip(u.parts, u.rows):
+                    items.append((p.index_logits, p.palette, w[r0:r0 + n], u.parts[0].noise_seed,
+                                  r0 * u.K))
+                    r0 += n
+            else:
+                items.append((u.index_logits, u.palette, w, u.noise_seed, 0))
+        nb = NextBuild(items, offset, tau, PLZ_W_HARD_NOISY)
+        nb.specs = specs
+        return nb
+
+    def commit_next_build(self, nb):
+        """After the optimizer step that ran ``nb``: its weights (complete when every linear's
+        logits were updated and built) serve the next forward unless a parameter or tau
+        changes first; an incomplete build is redone there with the same noise."""
+        self._wgroup.generation += 1  # the weights were rewritten
+        self._pending = dict(key=self._wgroup_key, tau=nb.tau, offset=nb.offset, specs=nb.specs,
+                             complete=all(id(it[0]) in nb.built for it in nb.items),
+                             versions=[(p, p._version) for p in self._weight_params()])
 
     def forward(self, hs, cos, sin):
         cfg = self.cfg
@@ -702,9 +758,11 @@ class LayerTrainer:
     """Owns a student/teacher pair and runs config-5 training steps."""
 
     def __init__(self, cfg: LayerConfig, device, lrs=None, seed=0, lora_b_std=0.0,
-                 fuse_gate_up=True):
+                 fuse_gate_up=True, build_in_update=True):
         self.cfg = cfg
         self.device = device
+        # the optimizer step also builds the next forward's soft weights (plz_adamw_step_build)
+        self.build_in_update = build_in_update
         self.student = PalettizedDecoderLayer(cfg, seed=seed, device=device, lora_b_std=lora_b_std,
                                               fuse_gate_up=fuse_gate_up)
         self.teacher = DenseDecoderLayer(cfg, seed=seed + 1, device=device)
@@ -716,10 +774,13 @@ class LayerTrainer:
             logits.append(lin.index_logits)
         self.logits = logits
         self.others = pal + lora
-        # clip group 0: index logits (max norm 1.0, clamped to +-5 tau); group 1: the rest (0.3)
-        self.opt = FusedAdamW([{"params": logits, "lr": lrs["indices"], "clip_group": 0},
-                               {"params": pal, "lr": lrs["palettes"], "clip_group": 1},
-                               {"params": lora, "lr": lrs["lora"], "clip_group": 1}])
+        # clip group 0: index logits (max norm 1.0, clamped to +-5 tau); group 1: the rest (0.3).
+        # The logits come last: a step that builds the next weights updates them after the
+        # palettes those builds read.
+        self.opt = FusedAdamW([{"params": pal, "lr": lrs["palettes"], "clip_group": 1},
+                               {"params": lora, "lr": lrs["lora"], "clip_group": 1},
+                               {"params": logits, "lr": lrs["indices"], "clip_group": 0}])
+        self.logits_group = 2
         self.step_idx = 0
         self.skipped = 0
         self._rope = {}
@@ -745,10 +806,14 @@ class LayerTrainer:
 
     def update(self):
         """Two-tier clip, AdamW on fp32 masters, logits clamp +-5 tau, advance the step: one
-        fused step (plz_adamw_step)."""
+        fused step (plz_adamw_step), which with build_in_update also builds the next forward's
+        soft weights from the updated logits (plz_adamw_step_build) at the next step's tau."""
         tau = tau_at(self.step_idx)
-        self.opt.set_clamp(0, -5.0 * tau, 5.0 * tau)
-        self.opt.step(max_norms=(1.0, 0.3))
+        self.opt.set_clamp(self.logits_group, -5.0 * tau, 5.0 * tau)
+        nb = self.student.plan_next_build(tau_at(self.step_idx + 1)) if self.build_in_update else None
+        self.opt.step(max_norms=(1.0, 0.3), build=nb)
+        if nb is not None:
+            self.student.commit_next_build(nb)
         self.step_idx += 1
 
     def step(self, hs, skip_nonfinite=False):

@@ -10,7 +10,22 @@ import math
 import torch
 
 from . import _lib
-from ._lib import PLZ_DT_BF16, PLZ_DT_FP32, call, query
+from ._lib import PLZ_DT_BF16, PLZ_DT_FP32, PLZ_W_HARD_NOISY, call, query
+
+
+class NextBuild:
+    """Soft weights for the optimizer step to build from the logits it updates
+    (plz_adamw_step_build): ``items`` lists (logits parameter, palette, w, noise_seed,
+    noise_counter) -- w [N, K] bf16 receives the weight plz_soft_build_w_batched_philox would
+    build from the updated logits, drawing weight (n, k) at Philox counter offset +
+    noise_counter + n*K + k under key noise_seed -- and ``offset``, ``tau``, ``mode`` are the
+    launch's. After the step, ``built`` holds the ids of the logits whose weight was built (a
+    parameter without a gradient is not updated, so not built either)."""
+
+    def __init__(self, items, offset: int, tau: float, mode: int = PLZ_W_HARD_NOISY):
+        self.items = list(items)
+        self.offset, self.tau, self.mode = int(offset), float(tau), int(mode)
+        self.built = set()
 
 
 class FusedAdamW:
@@ -58,12 +73,20 @@ class FusedAdamW:
                 else:
                     p.clamp_(lo, hi)
 
-    def step(self, max_norms=(0.0, 0.0)):
+    def step(self, max_norms=(0.0, 0.0), build: NextBuild | None = None):
         """One step over every parameter with a gradient; max_norms[G] <= 0 disables clipping of
-        group G. Returns the two groups' unclipped gradient norms (device tensor)."""
+        group G. With ``build``, the same pass also writes the soft weights it lists from the
+        updated logits (plz_adamw_step_build); those parameters are updated after all others
+        (the palettes the builds read among them). Returns the two groups' unclipped gradient
+        norms (device tensor)."""
         live = [e for e in self.entries if e[0].grad is not None]
         if not live:
             return self.last_norms
+        bmap = {}
+        if build is not None:
+            bmap = {id(it[0]): it for it in build.items}
+            live = ([e for e in live if id(e[0]) not in bmap] +
+                    [e for e in live if id(e[0]) in bmap])
         self.step_count += 1
         descs = (_lib.AdamWDesc * len(live))()
         for i, (p, master, m, v, gi) in enumerate(live):
@@ -78,19 +101,55 @@ class FusedAdamW:
                                       PLZ_DT_BF16 if p.dtype == torch.bfloat16 else PLZ_DT_FP32,
                                       g["clip_group"], g["lr"], g["clamp"][0], g["clamp"][1],
                                       0.0, 0)
-        total = _lib.lib().plz_adamw_plan(descs, len(live))
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        if not bmap:
+            total = _lib.lib().plz_adamw_plan(descs, len(live))
+            if total < 0:
+                raise _lib.PalettizeError("plz_adamw_plan failed: " +
+                                          _lib.lib().plz_last_error().decode())
+            table = self._upload(descs)
+            ws = self._workspace(total)
+            call("plz_adamw_step", table.data_ptr(), len(live), int(total), float(max_norms[0]),
+                 float(max_norms[1]), float(self.betas[0]), float(self.betas[1]), self.eps,
+                 self.weight_decay, self.step_count, self.last_norms.data_ptr(), ws.data_ptr(),
+                 ws.numel(), stream)
+            self._table = table  # keep alive until the launch has consumed it
+            return self.last_norms
+        builds = (_lib.BuildWDesc * len(live))()
+        for i, e in enumerate(live):
+            it = bmap.get(id(e[0]))
+            if it is None:
+                continue
+            logits, palette, w, seed, counter = it
+            N, K = w.shape
+            builds[i] = _lib.BuildWDesc(logits.data_ptr(), None, palette.data_ptr(), w.data_ptr(),
+                                        None, N, K, PLZ_DT_BF16, 0, 0,
+                                        int(seed) & (2**64 - 1), int(counter) & (2**64 - 1))
+        split = C.c_int64(0)
+        total = _lib.lib().plz_adamw_plan_build(descs, builds, len(live), C.byref(split))
         if total < 0:
-            raise _lib.PalettizeError("plz_adamw_plan failed: " +
+            raise _lib.PalettizeError("plz_adamw_plan_build failed: " +
                                       _lib.lib().plz_last_error().decode())
-        raw = bytes(C.string_at(C.addressof(descs), C.sizeof(descs)))
-        table = torch.frombuffer(bytearray(raw), dtype=torch.uint8).pin_memory().to(
+        table = self._upload(descs, builds)
+        ws = self._workspace(total)
+        nd = C.sizeof(descs)
+        call("plz_adamw_step_build", table.data_ptr(), table.data_ptr() + nd, len(live),
+             int(total), int(split.value), build.offset & (2**64 - 1), build.tau, build.mode,
+             float(max_norms[0]), float(max_norms[1]), float(self.betas[0]),
+             float(self.betas[1]), self.eps, self.weight_decay, self.step_count,
+             self.last_norms.data_ptr(), ws.data_ptr(), ws.numel(), stream)
+        self._table = table
+        build.built = {id(e[0]) for e in live if id(e[0]) in bmap}
+        return self.last_norms
+
+    def _upload(self, *tables):
+        """The host tables, back to back, in one device buffer (through pinned memory)."""
+        raw = b"".join(bytes(C.string_at(C.addressof(t), C.sizeof(t))) for t in tables)
+        return torch.frombuffer(bytearray(raw), dtype=torch.uint8).pin_memory().to(
             self.device, non_blocking=True)
+
+    def _workspace(self, total):
         need = query("plz_adamw_workspace", int(total))
         if self._ws is None or self._ws.numel() < need:
             self._ws = torch.empty(need, dtype=torch.uint8, device=self.device)
-        call("plz_adamw_step", table.data_ptr(), len(live), int(total), float(max_norms[0]),
-             float(max_norms[1]), float(self.betas[0]), float(self.betas[1]), self.eps,
-             self.weight_decay, self.step_count, self.last_norms.data_ptr(), self._ws.data_ptr(),
-             self._ws.numel(), torch.cuda.current_stream(self.device).cuda_stream)
-        self._table = table  # keep alive until the launch has consumed it
-        return self.last_norms
+        return self._ws

@@ -36,7 +36,7 @@ def test_every_declared_symbol_is_exported(lib):
         assert hasattr(lib, n), f"{n} declared in the header but not exported"
         assert n in _lib.SIGNATURES, f"{n} has no ctypes signature"
     assert set(_lib.SIGNATURES) == set(names)
-    assert lib.plz_abi_version() == 14
+    assert lib.plz_abi_version() == 15
 
 
 def test_shape_errors_are_reported_without_touching_the_gpu(lib):
@@ -311,7 +311,7 @@ def test_build_w_plan_accepts_philox_descriptors(lib):
     dereferenced by the plan."""
     from palettize_hip import _lib
     f = 4096
-    assert C.sizeof(_lib.BuildWDesc) == 5 * 8 + 2 * 8 + 2 * 4 + 8 + 8
+    assert C.sizeof(_lib.BuildWDesc) == 5 * 8 + 2 * 8 + 2 * 4 + 8 + 8 + 8
     d = (_lib.BuildWDesc * 3)(
         _lib.BuildWDesc(f, f, f, f, None, 64, 512, 0, 0, 0, 0),
         _lib.BuildWDesc(f, None, f, f, None, 8, 256, 1, 0, 0, 7),

@@ -165,3 +165,56 @@ def test_build_weights_follows_replaced_parameters(dev):
     w, _ = ops.soft_build_w(lin.index_logits, ops.PhiloxNoise(lin.noise_seed, off), lin.palette,
                             lin.tau, lin.mode)
     assert torch.equal(pw["q_proj"][0], w)
+
+
+def test_update_builds_the_next_weights_bit_for_bit(dev):
+    """LayerTrainer(build_in_update=True): the optimizer step writes the next forward's soft
+    weights from the logits it has just updated (plz_adamw_step_build), in place of that
+    forward's build-W launch. Against a trainer that builds them in the forward: the same
+    losses, gradients and parameters bit for bit over three steps (the gate/up group's up rows
+    draw their noise past the gate rows through the build's counter base), the same weights;
+    and after a logits change between the step and the forward, or another tau, the forward
+    builds again, with the same noise."""
+    cfg = layer.LayerConfig(**CFG)
+    hs = torch.randn(2, 16, cfg.hidden, generator=torch.Generator().manual_seed(9))
+    hs = hs.to(torch.bfloat16).to(dev)
+    a = layer.LayerTrainer(cfg, dev, seed=9, lora_b_std=0.02, build_in_update=True)
+    b = layer.LayerTrainer(cfg, dev, seed=9, lora_b_std=0.02, build_in_update=False)
+    assert a.student.gate_up is not None
+
+    def same_state():
+        for pa, pb in zip(a.logits + a.others, b.logits + b.others):
+            assert torch.equal(pa.view(torch.int16) if pa.dtype == torch.bfloat16 else pa,
+                               pb.view(torch.int16) if pb.dtype == torch.bfloat16 else pb)
+
+    for _ in range(3):
+        la, _ = a.step(hs)
+        lb, _ = b.step(hs)
+        assert torch.equal(la, lb)
+        same_state()
+    assert a.student._pending is not None and a.student._pending["complete"]
+    wa = a.student.build_weights()  # the weights the last step built
+    wb = b.student.build_weights()  # built now, at the same noise offset
+    for name in wa:
+        assert torch.equal(wa[name][0].view(torch.int16), wb[name][0].view(torch.int16)), name
+    # rewind b's counters (it has built once more than a)
+    for la_, lb_ in zip(a.student.linears(), b.student.linears()):
+        lb_.noise_counter = la_.noise_counter
+    # a logits change after the step: the forward builds again
+    a.update()
+    b.update()
+    with torch.no_grad():
+        a.student.q_proj.index_logits.mul_(0.5)
+        b.student.q_proj.index_logits.mul_(0.5)
+    la, _ = a.forward_backward(hs)
+    lb, _ = b.forward_backward(hs)
+    assert torch.equal(la, lb)
+    # another tau than the step built with: built again
+    a.update()
+    b.update()
+    for lin in a.student.linears() + b.student.linears():
+        lin.tau = 1.25
+    wa = a.student.build_weights()
+    wb = b.student.build_weights()
+    for name in wa:
+        assert torch.equal(wa[name][0].view(torch.int16), wb[name][0].view(torch.int16)), name
