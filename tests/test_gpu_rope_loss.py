@@ -129,8 +129,9 @@ def test_distill_loss_near_zero_student_rows(dev):
     want.backward()
     sg = s.to(dev).requires_grad_(True)
     loss, l_cos = layer.compute_loss(sg, t.to(dev))
-    assert abs(float(loss) - float(want)) <= 1e-5 * abs(float(want))
-    assert abs(float(l_cos) - float(want_cos)) <= 1e-5 * abs(float(want_cos))
+    lv, lc, wv, wc = (float(v.detach()) for v in (loss, l_cos, want, want_cos))
+    assert abs(lv - wv) <= 1e-5 * abs(wv)
+    assert abs(lc - wc) <= 1e-5 * abs(wc)
     loss.backward()
     got = f32(sg.grad.cpu())
     ref = f32(sr.grad)
