@@ -320,3 +320,55 @@ def test_build_w_plan_accepts_philox_descriptors(lib):
     assert d[1].block_begin == 64 and d[2].block_begin == 68
     bad = (_lib.BuildWDesc * 1)(_lib.BuildWDesc(None, None, f, f, None, 8, 256, 0, 0, 0, 1))
     assert lib.plz_build_w_plan(bad, 1) < 0
+
+
+def test_swiglu_cat_gemm_checks_arguments_before_launching(lib):
+    """plz_linear_fwd_dense_swiglu_cat: F not a multiple of 128, a bad rank and null or
+    misaligned operands are refused on the host; an empty problem returns without a launch."""
+    f = 4096
+    rc = lib.plz_linear_fwd_dense_swiglu_cat(f, f, None, None, 0, None, f, 64, 192, 256, None)
+    assert rc == 1 and b"F of 128" in lib.plz_last_error()
+    rc = lib.plz_linear_fwd_dense_swiglu_cat(f, f, f, f, 12, None, f, 64, 128, 256, None)
+    assert rc == 1 and b"rank" in lib.plz_last_error()
+    rc = lib.plz_linear_fwd_dense_swiglu_cat(f, None, None, None, 0, None, f, 64, 128, 256, None)
+    assert rc == 1 and b"non-null" in lib.plz_last_error()
+    rc = lib.plz_linear_fwd_dense_swiglu_cat(f, f, None, None, 0, f + 2, f, 64, 128, 256, None)
+    assert rc == 1 and b"aligned" in lib.plz_last_error()
+    assert lib.plz_linear_fwd_dense_swiglu_cat(None, None, None, None, 0, None, None, 0, 128, 256,
+                                               None) == 0
+
+
+def test_adamw_build_plan_checks_the_pairs(lib):
+    """plz_adamw_plan_build: the descriptors with a build must come last, each build must
+    rebuild its own bf16 [N, K, 4] parameter; the split block is the first built block.
+    Pointers are never dereferenced by the plan."""
+    from palettize_hip import _lib
+    P, G, W = 4096, 8192, 12288
+
+    def adam(param, n):
+        return _lib.AdamWDesc(param, G, G, G, G, n, _lib.PLZ_DT_BF16, 0, 1e-3, -1.0, 1.0, 0.0, 0)
+
+    def build(param, N, K):
+        return _lib.BuildWDesc(param, None, G, W, None, N, K, _lib.PLZ_DT_BF16, 0, 0, 7, 0)
+
+    none = _lib.BuildWDesc()
+    split = C.c_int64(-1)
+    d = (_lib.AdamWDesc * 3)(adam(P, 1000), adam(P + 65536, 8 * 256 * 4), adam(P + 131072, 4 * 512 * 4))
+    b = (_lib.BuildWDesc * 3)(none, build(P + 65536, 8, 256), build(P + 131072, 4, 512))
+    total = lib.plz_adamw_plan_build(d, b, 3, C.byref(split))
+    assert total == 1 + 1 + 1 and split.value == 1
+    # a build before a descriptor without one
+    b2 = (_lib.BuildWDesc * 3)(build(P, 1, 256), none, none)
+    d2 = (_lib.AdamWDesc * 3)(adam(P, 1024), adam(P + 65536, 64), adam(P + 131072, 64))
+    assert lib.plz_adamw_plan_build(d2, b2, 3, C.byref(split)) < 0
+    assert b"must come last" in lib.plz_last_error()
+    # a build of another tensor, and a size that does not match N*K*4
+    for bad in (build(P + 4096, 8, 256), build(P + 65536, 8, 512)):
+        d3 = (_lib.AdamWDesc * 1)(adam(P + 65536, 8 * 256 * 4))
+        b3 = (_lib.BuildWDesc * 1)(bad)
+        assert lib.plz_adamw_plan_build(d3, b3, 1, C.byref(split)) < 0
+        assert b"own bf16" in lib.plz_last_error()
+    # no builds at all: the split is the end
+    d4 = (_lib.AdamWDesc * 1)(adam(P, 1000))
+    b4 = (_lib.BuildWDesc * 1)(none)
+    assert lib.plz_adamw_plan_build(d4, b4, 1, C.byref(split)) == 1 and split.value == 1
