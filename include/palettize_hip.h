@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define PLZ_ABI_VERSION 15
+#define PLZ_ABI_VERSION 16
 
 /* status codes */
 #define PLZ_OK 0
@@ -299,15 +299,19 @@ int plz_soft_bwd_philox(const uint16_t* x, const uint16_t* grad_y, const uint16_
  * under QwenLoRA, the LoRA weight gradients of QwenLoRA.forward's autograd
  * (qwen_model.py:291-304) beside the soft backward's grad_W matmul
  * (fused_lut_linear_cuda.py:952). Deterministic; the workspace (query below, 16-byte aligned)
- * holds the soft backward's and the LoRA partials. */
+ * holds the soft backward's and the LoRA partials. grad_sq (optional, fp32 [N, K/128]): the
+ * sum of squares of each run of 512 consecutive grad_logits values as stored (row n, k
+ * 128 j .. 128 j + 127), what the gradient-norm clip of the optimizer step
+ * (train_qwen.py:1303-1319) sums; plz_adamw_desc.grad_sq takes it in place of reading the
+ * gradient again. */
 size_t plz_soft_bwd_lora_workspace(int64_t M, int64_t N, int64_t K, int rank);
 int plz_soft_bwd_lora(const uint16_t* x, const uint16_t* grad_y, const uint16_t* logits,
                       int logits_dtype, const float* noise, uint64_t seed, uint64_t offset,
                       const float* palette, float tau, int scale_grad_by_inv_tau,
                       const uint16_t* lora_a, const uint16_t* lora_b, int rank, float scale,
                       uint16_t* grad_logits, float* grad_palette, void* grad_a, void* grad_b,
-                      int grads_dtype, void* workspace, size_t workspace_bytes, int64_t M,
-                      int64_t N, int64_t K, void* stream);
+                      int grads_dtype, float* grad_sq, void* workspace, size_t workspace_bytes,
+                      int64_t M, int64_t N, int64_t K, void* stream);
 
 /* ---- LoRA (QwenLoRA, qwen_model.py:213-304): y += scale * (x A^T) B^T ------------------ */
 /* t[M,rank] = scale * x[M,K] lora_a[rank,K]^T  (bf16). rank in {8,16,24,32}. */
@@ -447,6 +451,9 @@ typedef struct plz_adamw_desc {
   int32_t clip_group;    /* 0 or 1: which clip_grad_norm_ group the gradient belongs to */
   float lr, clamp_lo, clamp_hi, reserved;  /* clamp_lo/hi = -/+inf for no clamp */
   int64_t block_begin;   /* filled by plz_adamw_plan */
+  const float* grad_sq;  /* optional: the gradient's sum of squares per 512 consecutive
+                            elements (n % 512 == 0), e.g. plz_soft_bwd_lora's grad_sq; the
+                            clip norm then reads these n / 512 floats instead of the gradient */
 } plz_adamw_desc;
 /* Checks n host descriptors, fills block_begin, returns the block count (or -status). */
 int64_t plz_adamw_plan(plz_adamw_desc* descs, int n);

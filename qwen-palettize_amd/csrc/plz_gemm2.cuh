@@ -99,6 +99,9 @@ struct Args {
   // set, receives the pre-activations [I, 2F] in that natural layout (row pitch ldc2)
   int64_t b_half;
   uint16_t* c2; int64_t ldc2;
+  // soft epilogues: the sum of squares of each item's stored grad_logits (512 values: row n,
+  // 128 k), [I][J / 128] fp32, or NULL
+  float* gsq;
 };
 
 // B row (and output column) of the tile-local logical column j when b_half > 0: the first 128

@@ -566,6 +566,15 @@ __device__ __forceinline__ float dpp_add(float v) {
   return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF,
                                                         false));
 }
+// the sum of v over the 64 lanes, in every lane
+__device__ __forceinline__ float wave_sum1(float v) {
+  const float w = swap32_sum(v, v);  // lanes l, l ^ 32
+  float q = swap16_sum(w, w);          // and l ^ 16, l ^ 48
+  q = dpp_add<0x128>(q);
+  q = dpp_add<0x124>(q);
+  q = dpp_add<0x122>(q);
+  return dpp_add<0x121>(q);
+}
 __device__ __forceinline__ float wave_sum4(const float (&sp)[4]) {
   const float a = swap32_sum(sp[0], sp[2]);  // class 0 (lanes 0-31) / class 2 (lanes 32-63)
   const float b = swap32_sum(sp[1], sp[3]);  // class 1 / class 3
@@ -632,6 +641,18 @@ __device__ __forceinline__ void soft_math(const Args& g, int64_t n, int64_t kseg
   *reinterpret_cast<uint4*>(g.grad_logits + e0) = make_uint4(out[0], out[1], out[2], out[3]);
   const float tot = wave_sum4(sp);
   if ((lane & 15) == 0) g.partial[(n * (g.J / 128) + kseg / 128) * 4 + (lane >> 4)] = tot;
+  if (g.gsq) {  // the squares of the stored values, which a gradient-norm clip sums
+    float q = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float lo = g.logits_f16 ? h2f(out[i] & 0xffffu) : bf2f(out[i] & 0xffffu);
+      const float hi = g.logits_f16 ? h2f(out[i] >> 16) : bf2f(out[i] >> 16);
+      q += lo * lo;
+      q += hi * hi;
+    }
+    q = wave_sum1(q);
+    if (lane == 0) g.gsq[n * (g.J / 128) + kseg / 128] = q;
+  }
 }
 
 __device__ __forceinline__ void tile_of(const Args& g, int bid, int& tile_i, int& tile_j) {
@@ -1916,7 +1937,7 @@ static int soft_bwd(const uint16_t* x, const uint16_t* grad_y, const uint16_t* l
                     const float* palette, float tau, int scale_grad_by_inv_tau,
                     uint16_t* grad_logits, float* grad_palette, void* workspace,
                     size_t workspace_bytes, int64_t M, int64_t N, int64_t K, void* stream,
-                    const WgradArgs& wg = WgradArgs()) {
+                    const WgradArgs& wg = WgradArgs(), float* gsq = nullptr) {
   PLZ_REQUIRE(M >= 0 && N >= 0 && K >= 0, "plz_soft_bwd: negative shape");
   PLZ_REQUIRE(K % 256 == 0, "plz_soft_bwd: K (%lld) must be a multiple of 256", (long long)K);
   PLZ_REQUIRE(N % 8 == 0, "plz_soft_bwd: N (%lld) must be a multiple of 8", (long long)N);
@@ -1934,6 +1955,7 @@ static int soft_bwd(const uint16_t* x, const uint16_t* grad_y, const uint16_t* l
       zero_async(wg.grad_a, (size_t)wg.rank * K * esz, (hipStream_t)stream);
       zero_async(wg.grad_b, (size_t)N * wg.rank * esz, (hipStream_t)stream);
     }
+    if (gsq) zero_async(gsq, (size_t)N * (K / 128) * sizeof(float), (hipStream_t)stream);
     return check_launch("plz_soft_bwd");
   }
   PLZ_REQUIRE(x && grad_y, "plz_soft_bwd: null pointer");
@@ -1961,6 +1983,7 @@ static int soft_bwd(const uint16_t* x, const uint16_t* grad_y, const uint16_t* l
   g.wg_r = wg.rank;
   g.wg_a = wg.lora_a; g.wg_b = wg.lora_b;
   g.wg_part_a = wg.part_a; g.wg_part_b = wg.part_b;
+  g.gsq = gsq;
   int rc;
   if (z == 1) {
     rc = launch<OP_COL, OP_COL, EPI_SOFT>(g, 1, (hipStream_t)stream, "plz_soft_bwd");
@@ -2014,9 +2037,10 @@ int plz_soft_bwd_lora(const uint16_t* x, const uint16_t* grad_y, const uint16_t*
                       const float* palette, float tau, int scale_grad_by_inv_tau,
                       const uint16_t* lora_a, const uint16_t* lora_b, int rank, float scale,
                       uint16_t* grad_logits, float* grad_palette, void* grad_a, void* grad_b,
-                      int grads_dtype, void* workspace, size_t workspace_bytes, int64_t M,
-                      int64_t N, int64_t K, void* stream) {
+                      int grads_dtype, float* grad_sq, void* workspace, size_t workspace_bytes,
+                      int64_t M, int64_t N, int64_t K, void* stream) {
   const char* what = "plz_soft_bwd_lora";
+  PLZ_REQUIRE(((uintptr_t)grad_sq & 3) == 0, "%s: grad_sq must be 4-byte aligned", what);
   PLZ_REQUIRE(rank > 0 && rank <= 32 && rank % 8 == 0,
               "%s: rank (%d) must be a multiple of 8 in [8, 32]", what, rank);
   PLZ_REQUIRE(grads_dtype == PLZ_DT_BF16 || grads_dtype == PLZ_DT_FP32,
@@ -2044,7 +2068,7 @@ int plz_soft_bwd_lora(const uint16_t* x, const uint16_t* grad_y, const uint16_t*
       w + soft_bytes + align256(wg_part_a_floats(z, N, K, rank) * sizeof(float)));
   return soft_bwd(x, grad_y, logits, logits_dtype, noise == nullptr, noise, seed, offset, palette,
                   tau, scale_grad_by_inv_tau, grad_logits, grad_palette, workspace,
-                  soft_bytes, M, N, K, stream, wg);
+                  soft_bytes, M, N, K, stream, wg, grad_sq);
 }
 
 int plz_soft_bwd_philox(const uint16_t* x, const uint16_t* grad_y, const uint16_t* logits,

@@ -87,18 +87,23 @@ __global__ __launch_bounds__(kThreads) void sumsq_kernel(const plz_adamw_desc* _
   const plz_adamw_desc d = descs[find_desc(descs, n_desc, b)];
   const int64_t base = (b - d.block_begin) * kBlockElems;
   float s = 0.f;
+  if (d.grad_sq) {  // the producer's sums of 512 elements: 16 per full block
+    const int64_t i = base / 512 + threadIdx.x;
+    if (threadIdx.x < kBlockElems / 512 && i < d.n / 512) s = d.grad_sq[i];
+  } else {
 #pragma unroll
-  for (int c = 0; c < kChunks; ++c) {
-    const int64_t i0 = base + ((int64_t)c * kThreads + threadIdx.x) * kVec;
-    if (i0 + kVec <= d.n) {
-      float g[kVec];
-      grad8(d, i0, g);
+    for (int c = 0; c < kChunks; ++c) {
+      const int64_t i0 = base + ((int64_t)c * kThreads + threadIdx.x) * kVec;
+      if (i0 + kVec <= d.n) {
+        float g[kVec];
+        grad8(d, i0, g);
 #pragma unroll
-      for (int j = 0; j < kVec; ++j) s += g[j] * g[j];
-    } else {
-      for (int64_t i = i0; i < d.n; ++i) {
-        const float g = grad_at(d, i);
-        s += g * g;
+        for (int j = 0; j < kVec; ++j) s += g[j] * g[j];
+      } else {
+        for (int64_t i = i0; i < d.n; ++i) {
+          const float g = grad_at(d, i);
+          s += g * g;
+        }
       }
     }
   }
@@ -328,6 +333,11 @@ int64_t plz_adamw_plan(plz_adamw_desc* descs, int n) {
     if ((((uintptr_t)d.param | (uintptr_t)d.grad | (uintptr_t)d.master | (uintptr_t)d.exp_avg |
           (uintptr_t)d.exp_avg_sq) & 15) != 0) {
       set_error("plz_adamw_plan: descriptor %d: pointers must be 16-byte aligned", i);
+      return -PLZ_EINVAL;
+    }
+    if (d.grad_sq && (d.n % 512 != 0 || ((uintptr_t)d.grad_sq & 3) != 0)) {
+      set_error("plz_adamw_plan: descriptor %d: grad_sq needs n %% 512 == 0 (one sum per 512 "
+                "elements) and 4-byte alignment", i);
       return -PLZ_EINVAL;
     }
     descs[i].block_begin = total;

@@ -35,7 +35,7 @@ class PwRefDesc(C.Structure):
 class AdamWDesc(C.Structure):
     _fields_ = [("param", p), ("grad", p), ("master", p), ("exp_avg", p), ("exp_avg_sq", p),
                 ("n", i64), ("dtype", i32), ("clip_group", i32), ("lr", f32), ("clamp_lo", f32),
-                ("clamp_hi", f32), ("reserved", f32), ("block_begin", i64)]
+                ("clamp_hi", f32), ("reserved", f32), ("block_begin", i64), ("grad_sq", p)]
 
 
 class GemvDesc(C.Structure):
@@ -93,7 +93,7 @@ SIGNATURES: dict[str, tuple] = {
     "plz_soft_bwd_philox": (i32, [p, p, p, i32, u64, u64, p, f32, i32, p, p, p, sz, i64, i64, i64, p]),
     "plz_soft_bwd_lora_workspace": (sz, [i64, i64, i64, i32]),
     "plz_soft_bwd_lora": (i32, [p, p, p, i32, p, u64, u64, p, f32, i32, p, p, i32, f32, p, p, p, p,
-                                i32, p, sz, i64, i64, i64, p]),
+                                i32, p, p, sz, i64, i64, i64, p]),
     "plz_lora_project": (i32, [p, p, f32, p, i64, i64, i32, p]),
     "plz_lora_grad_t": (i32, [p, p, f32, p, i64, i64, i32, p]),
     "plz_lora_weight_grads_workspace": (sz, [i64, i64, i64, i32]),

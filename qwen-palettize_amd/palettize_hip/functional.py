@@ -91,7 +91,9 @@ def lut_linear(x, packed, palette, bias=None, lora_a=None, lora_b=None, lora_sca
 class SoftLUTLinearFunction(torch.autograd.Function):
     """``prebuilt`` (optional): (w, group) with w the forward weight already built from these
     logits, noise, palette and tau by ``group`` (an ops.SoftBuildGroup run); the backward
-    checks that no later run of the group has overwritten it."""
+    checks that no later run of the group has overwritten it. A third element, an object with
+    ``buf`` (fp32 [N * K / 128]) and ``writes``, has the backward's fused soft dW also write the
+    squared-gradient sums of the logits there (ops.soft_bwd_lora grad_sq) and count the write."""
 
     @staticmethod
     def forward(ctx, x, palette, logits, noise, tau, bias, lora_a, lora_b, lora_scale, mode,
@@ -99,11 +101,13 @@ class SoftLUTLinearFunction(torch.autograd.Function):
         x = x.contiguous()
         lora_a, lora_b = _c(lora_a), _c(lora_b)
         ctx.guard = None
+        ctx.grad_sq = None
         if prebuilt is None:
             w, _ = ops.soft_build_w(logits, noise, palette, tau, mode)
         else:
-            w, group = prebuilt
+            w, group = prebuilt[:2]
             ctx.guard = (group, group.generation)
+            ctx.grad_sq = prebuilt[2] if len(prebuilt) > 2 else None
         t = ops.lora_project(x, lora_a, lora_scale) if lora_a is not None else None
         y = ops.linear_fwd_dense(x, w, bias, t, lora_b)
         # a Philox noise descriptor is redrawn in the backward's epilogue, not stored
@@ -142,9 +146,13 @@ class SoftLUTLinearFunction(torch.autograd.Function):
         grad_x = ops.linear_bwd_x_dense(gy, w, gt, lora_a) if need_x else None
         grad_logits = grad_pal = grad_a = grad_b = None
         if fused:
+            sq = ctx.grad_sq if need_log else None
             grad_logits, grad_pal, grad_a, grad_b = ops.soft_bwd_lora(
                 x, gy, logits, noise, palette, ctx.tau, lora_a, lora_b, ctx.lora_scale,
-                ctx.scale_by_inv_tau, out_dtype=lora_a.dtype)
+                ctx.scale_by_inv_tau, out_dtype=lora_a.dtype,
+                grad_sq=sq.buf if sq is not None else None)
+            if sq is not None:
+                sq.writes += 1
         elif need_soft:
             grad_logits, grad_pal = ops.soft_bwd(x, gy, logits, noise, palette, ctx.tau,
                                                  ctx.scale_by_inv_tau)

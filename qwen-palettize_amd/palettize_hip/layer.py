@@ -188,6 +188,21 @@ class DistillLossFunction(torch.autograd.Function):
 NOISE_STRIDE = 1 << 32  # Philox counters consumed per forward of a soft linear (> N * K)
 
 
+class GradSq:
+    """The squared-gradient sums of a soft linear's (or a group's) logits, one fp32 per 512
+    consecutive gradient values (row n, 128 k), written by its backward's soft dW
+    (ops.soft_bwd_lora grad_sq) for the optimizer's clip norm; ``writes`` counts the backward
+    passes that wrote it since it was last reset, so a reader knows the sums are those of one
+    gradient."""
+
+    def __init__(self, rows, K, device):
+        self.buf = torch.empty(rows * (K // 128), dtype=torch.float32, device=device)
+        self.writes = 0
+
+    def rows(self, r0, n, K):
+        return self.buf[r0 * (K // 128):(r0 + n) * (K // 128)]
+
+
 class SoftPalettizedLinear(nn.Module):
     """y = x W_ste^T + s (x A^T) B^T with W from logits + Gumbel noise + palette.
 
@@ -219,6 +234,7 @@ class SoftPalettizedLinear(nn.Module):
         self.noise_seed = seed
         self.noise_counter = 0
         self.mode = PLZ_W_HARD_NOISY
+        self.grad_sq = None  # a GradSq: the backward writes the logits' squared-gradient sums
 
     def next_noise_spec(self):
         """The next forward's noise as a Philox descriptor (drawn inside the kernels): key
@@ -238,7 +254,7 @@ class SoftPalettizedLinear(nn.Module):
             noise = self.next_noise_spec()
         else:
             w, group, noise = prebuilt
-            prebuilt = (w, group)
+            prebuilt = (w, group) if self.grad_sq is None else (w, group, self.grad_sq)
         y = SoftLUTLinearFunction.apply(x.reshape(-1, x.shape[-1]), self.palette, self.index_logits,
                                         noise, self.tau, None, self.lora_a, self.lora_b,
                                         self.lora_scale, self.mode, False, prebuilt)
@@ -291,6 +307,7 @@ class SoftLinearGroup:
         self._sync_counters()
         dev = parts[0].lora_b.device
         self._b_bd = torch.zeros(self.N, self.R, dtype=torch.bfloat16, device=dev)
+        self.grad_sq = None  # a GradSq over the group's rows, as SoftPalettizedLinear.grad_sq
 
     def _sync_counters(self):
         c = self.parts[0].noise_counter
@@ -406,8 +423,12 @@ class SoftLinearGroupFunction(torch.autograd.Function):
         if ctx.needs_input_grad[0]:
             gt = ops.lora_grad_t(gy, b, scale)
             grad_x = ops.linear_bwd_x_dense(gy, w, gt, a)
+        sq = grp.grad_sq
         gl, gp, ga, gb = ops.soft_bwd_lora(x, gy, logits, ctx.noise, pal, ctx.tau, a, b, scale,
-                                           False, out_dtype=a.dtype)
+                                           False, out_dtype=a.dtype,
+                                           grad_sq=sq.buf if sq is not None else None)
+        if sq is not None:
+            sq.writes += 1
         grads = []
         r0 = c0 = 0
         for n, r in zip(grp.rows, grp.ranks):
@@ -758,7 +779,7 @@ class LayerTrainer:
     """Owns a student/teacher pair and runs config-5 training steps."""
 
     def __init__(self, cfg: LayerConfig, device, lrs=None, seed=0, lora_b_std=0.0,
-                 fuse_gate_up=True, build_in_update=True):
+                 fuse_gate_up=True, build_in_update=True, grad_sq_in_backward=True):
         self.cfg = cfg
         self.device = device
         # the optimizer step also builds the next forward's soft weights (plz_adamw_step_build)
@@ -781,6 +802,22 @@ class LayerTrainer:
                                {"params": lora, "lr": lrs["lora"], "clip_group": 1},
                                {"params": logits, "lr": lrs["indices"], "clip_group": 0}])
         self.logits_group = 2
+        # the soft backward also writes the logits' squared-gradient sums, which the clip norm
+        # of the update reads instead of the gradients: (logits, its GradSq, its rows there)
+        self._sq_items = []
+        if grad_sq_in_backward:
+            K_of = {id(l): l.in_features for l in self.student.linears()}
+            for _, u in self.student._units():
+                if isinstance(u, SoftLinearGroup):
+                    u.grad_sq = GradSq(u.N, u.K, device)
+                    r0 = 0
+                    for p, n in zip(u.parts, u.rows):
+                        self._sq_items.append((p, u.grad_sq, r0, n, u.K))
+                        r0 += n
+                else:
+                    u.grad_sq = GradSq(u.out_features, u.in_features, device)
+                    self._sq_items.append((u, u.grad_sq, 0, u.out_features, K_of[id(u)]))
+        self._sq_ready = []
         self.step_idx = 0
         self.skipped = 0
         self._rope = {}
@@ -801,8 +838,31 @@ class LayerTrainer:
         loss, l_cos = compute_loss(s_out, t_out)
         for p in self.logits + self.others:
             p.grad = None
-        loss.backward()
+        self._backward(loss)
         return loss.detach(), l_cos.detach()
+
+    def _backward(self, loss):
+        """loss.backward(), then note which logits gradients have their squared sums from the
+        soft backward (exactly one write since the reset) and the state of those gradients."""
+        for _, sq, _, _, _ in self._sq_items:
+            sq.writes = 0
+        loss.backward()
+        self._sq_ready = []
+        for lin, sq, r0, n, K in self._sq_items:
+            g = lin.index_logits.grad
+            if sq.writes == 1 and g is not None:
+                self._sq_ready.append((lin.index_logits, sq.rows(r0, n, K), g.data_ptr(),
+                                       g._version))
+
+    def _grad_sq(self):
+        """{id(logits): sums} for the gradients unchanged since the backward that summed them."""
+        out = {}
+        for p, sums, ptr, ver in self._sq_ready:
+            g = p.grad
+            if g is not None and g.data_ptr() == ptr and g._version == ver:
+                out[id(p)] = sums
+        self._sq_ready = []
+        return out
 
     def update(self):
         """Two-tier clip, AdamW on fp32 masters, logits clamp +-5 tau, advance the step: one
@@ -811,7 +871,7 @@ class LayerTrainer:
         tau = tau_at(self.step_idx)
         self.opt.set_clamp(self.logits_group, -5.0 * tau, 5.0 * tau)
         nb = self.student.plan_next_build(tau_at(self.step_idx + 1)) if self.build_in_update else None
-        self.opt.step(max_norms=(1.0, 0.3), build=nb)
+        self.opt.step(max_norms=(1.0, 0.3), build=nb, grad_sq=self._grad_sq())
         if nb is not None:
             self.student.commit_next_build(nb)
         self.step_idx += 1
@@ -839,6 +899,6 @@ class LayerTrainer:
             self.skipped += 1
             self.step_idx += 1
             return loss.detach(), l_cos.detach()
-        loss.backward()
+        self._backward(loss)
         self.update()
         return loss.detach(), l_cos.detach()

@@ -510,11 +510,18 @@ def soft_bwd(x, grad_y, logits, noise, palette, tau: float, scale_by_inv_tau: bo
 
 
 def soft_bwd_lora(x, grad_y, logits, noise, palette, tau: float, lora_a, lora_b,
-                  scale: float = 1.0, scale_by_inv_tau: bool = False, out_dtype=torch.bfloat16):
+                  scale: float = 1.0, scale_by_inv_tau: bool = False, out_dtype=torch.bfloat16,
+                  grad_sq=None):
     """(grad_logits, grad_palette, grad_a [r, K], grad_b [N, r]) from one dW GEMM: the soft
     backward as soft_bwd (bit for bit), and the LoRA weight gradients scale * lora_b^T dW and
-    scale * dW lora_a^T (dW = grad_y^T x), which lora_weight_grads computes from t and gt."""
+    scale * dW lora_a^T (dW = grad_y^T x), which lora_weight_grads computes from t and gt.
+    grad_sq (optional fp32 [N * K / 128]) receives the sum of squares of each 512 consecutive
+    grad_logits values, for FusedAdamW.step(grad_sq=...)."""
     N, K = _soft_shapes(logits, noise, palette)
+    if grad_sq is not None:
+        _need(grad_sq, "grad_sq", torch.float32, 1)
+        if grad_sq.numel() != N * K // 128:
+            raise ValueError(f"grad_sq must hold N*K/128 = {N * K // 128} floats")
     for name, v in (("x", x), ("grad_y", grad_y), ("lora_a", lora_a), ("lora_b", lora_b)):
         _need(v, name, torch.bfloat16, 2)
     M = x.shape[0]
@@ -533,7 +540,7 @@ def soft_bwd_lora(x, grad_y, logits, noise, palette, tau: float, lora_a, lora_b,
          None if philox else _ptr(noise), noise.seed if philox else 0,
          noise.offset if philox else 0, _ptr(palette), float(tau), int(bool(scale_by_inv_tau)),
          _ptr(lora_a), _ptr(lora_b), r, float(scale), _ptr(gl), _ptr(gp), _ptr(ga), _ptr(gb),
-         _DT[out_dtype], _ptr(ws), ws.numel(), M, N, K, _stream(x))
+         _DT[out_dtype], _ptr(grad_sq), _ptr(ws), ws.numel(), M, N, K, _stream(x))
     return gl, gp, ga, gb
 
 

@@ -73,12 +73,15 @@ class FusedAdamW:
                 else:
                     p.clamp_(lo, hi)
 
-    def step(self, max_norms=(0.0, 0.0), build: NextBuild | None = None):
+    def step(self, max_norms=(0.0, 0.0), build: NextBuild | None = None, grad_sq=None):
         """One step over every parameter with a gradient; max_norms[G] <= 0 disables clipping of
         group G. With ``build``, the same pass also writes the soft weights it lists from the
         updated logits (plz_adamw_step_build); those parameters are updated after all others
-        (the palettes the builds read among them). Returns the two groups' unclipped gradient
-        norms (device tensor)."""
+        (the palettes the builds read among them). ``grad_sq`` (optional): {id(param): fp32
+        tensor} with the sum of squares of every 512 consecutive elements of that parameter's
+        current gradient (ops.soft_bwd_lora's grad_sq), which the clip norm then reads in place
+        of the gradient. Returns the two groups' unclipped gradient norms (device tensor)."""
+        grad_sq = grad_sq or {}
         live = [e for e in self.entries if e[0].grad is not None]
         if not live:
             return self.last_norms
@@ -95,12 +98,16 @@ class FusedAdamW:
             if grad.dtype != p.dtype or not grad.is_contiguous():
                 grad = grad.to(p.dtype).contiguous()
                 p.grad = grad
+            sq = grad_sq.get(id(p))
+            if sq is not None and (sq.dtype != torch.float32 or not sq.is_contiguous() or
+                                   sq.numel() * 512 != p.numel() or sq.device != p.device):
+                raise ValueError("grad_sq: one fp32 sum per 512 elements of the parameter expected")
             descs[i] = _lib.AdamWDesc(p.data_ptr(), grad.data_ptr(),
                                       master.data_ptr() if master is not None else None,
                                       m.data_ptr(), v.data_ptr(), p.numel(),
                                       PLZ_DT_BF16 if p.dtype == torch.bfloat16 else PLZ_DT_FP32,
                                       g["clip_group"], g["lr"], g["clamp"][0], g["clamp"][1],
-                                      0.0, 0)
+                                      0.0, 0, sq.data_ptr() if sq is not None else None)
         stream = torch.cuda.current_stream(self.device).cuda_stream
         if not bmap:
             total = _lib.lib().plz_adamw_plan(descs, len(live))

@@ -36,7 +36,7 @@ def test_every_declared_symbol_is_exported(lib):
         assert hasattr(lib, n), f"{n} declared in the header but not exported"
         assert n in _lib.SIGNATURES, f"{n} has no ctypes signature"
     assert set(_lib.SIGNATURES) == set(names)
-    assert lib.plz_abi_version() == 15
+    assert lib.plz_abi_version() == 16
 
 
 def test_shape_errors_are_reported_without_touching_the_gpu(lib):
@@ -59,10 +59,10 @@ def test_shape_errors_are_reported_without_touching_the_gpu(lib):
                                              None, 0, None, 0, 64, 256, 256, None)
     assert rc == 1 and b"null" in lib.plz_last_error()
     rc = lib.plz_soft_bwd_lora(None, None, None, 0, None, 0, 0, None, 0.5, 0, None, None, 12,
-                               1.0, None, None, None, None, 0, None, 0, 64, 256, 256, None)
+                               1.0, None, None, None, None, 0, None, None, 0, 64, 256, 256, None)
     assert rc == 1 and b"rank" in lib.plz_last_error()
     rc = lib.plz_soft_bwd_lora(None, None, None, 0, None, 0, 0, None, 0.5, 0, None, None, 16,
-                               1.0, None, None, None, None, 0, None, 0, 64, 256, 256, None)
+                               1.0, None, None, None, None, 0, None, None, 0, 64, 256, 256, None)
     assert rc == 1 and b"null" in lib.plz_last_error()
 
 

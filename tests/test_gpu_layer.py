@@ -218,3 +218,29 @@ def test_update_builds_the_next_weights_bit_for_bit(dev):
     wb = b.student.build_weights()
     for name in wa:
         assert torch.equal(wa[name][0].view(torch.int16), wb[name][0].view(torch.int16)), name
+
+
+def test_clip_norm_from_the_backwards_squared_sums(dev):
+    """LayerTrainer(grad_sq_in_backward=True): the soft backward writes the logits'
+    squared-gradient sums and the update's clip norm reads them instead of the gradients.
+    Against a trainer that reads the gradients: the same norms to fp32 summation order and the
+    same losses over three steps; a gradient changed after the backward is read again."""
+    cfg = layer.LayerConfig(**CFG)
+    hs = torch.randn(2, 16, cfg.hidden, generator=torch.Generator().manual_seed(11))
+    hs = hs.to(torch.bfloat16).to(dev)
+    a = layer.LayerTrainer(cfg, dev, seed=4, lora_b_std=0.02, grad_sq_in_backward=True)
+    b = layer.LayerTrainer(cfg, dev, seed=4, lora_b_std=0.02, grad_sq_in_backward=False)
+    for step in range(3):
+        la, _ = a.forward_backward(hs)
+        lb, _ = b.forward_backward(hs)
+        # the first loss precedes any update; later ones follow updates whose clip coefficient
+        # may differ in its last bit, which can move a bf16 parameter by one ulp
+        assert abs(float(la) - float(lb)) <= (0.0 if step == 0 else 1e-3) * abs(float(lb))
+        assert len(a._sq_ready) == len(a.logits) and not b._sq_ready
+        a.update()
+        b.update()
+        assert np.allclose(f32(a.opt.last_norms), f32(b.opt.last_norms), rtol=1e-5)
+    a.forward_backward(hs)
+    with torch.no_grad():
+        a.student.q_proj.index_logits.grad.mul_(0.0)
+    assert id(a.student.q_proj.index_logits) not in a._grad_sq()

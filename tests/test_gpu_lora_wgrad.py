@@ -105,6 +105,13 @@ def test_soft_bwd_lora(dev, M, N, K, rank, scale, philox):
     _, _, fa, fb = ops.soft_bwd_lora(x, gy, logits, noise, pal, 0.5, a, b, scale,
                                      out_dtype=torch.float32)
     assert torch.equal(fa.to(torch.bfloat16), ga) and torch.equal(fb.to(torch.bfloat16), gb)
+    # the squared-gradient sums of each 512 stored values (row n, 128 k), with every other
+    # output unchanged
+    sq = torch.full((N * K // 128,), float("nan"), device=dev)
+    out3 = ops.soft_bwd_lora(x, gy, logits, noise, pal, 0.5, a, b, scale, grad_sq=sq)
+    assert all(torch.equal(u, v) for u, v in zip((gl, gp, ga, gb), out3))
+    want_sq = (f32(gl).astype(np.float64) ** 2).reshape(-1, 512).sum(1)
+    assert np.allclose(f32(sq), want_sq, rtol=1e-5, atol=0)
 
 
 def test_soft_bwd_lora_empty_reduction_gives_zeros(dev):
@@ -114,9 +121,10 @@ def test_soft_bwd_lora_empty_reduction_gives_zeros(dev):
     gy = torch.empty(0, N, dtype=torch.bfloat16, device=dev)
     a = randn_bf16(r, K, seed=14).to(dev)
     b = randn_bf16(N, r, seed=15).to(dev)
+    sq = torch.full((N * K // 128,), float("nan"), device=dev)
     gl, gp, ga, gb = ops.soft_bwd_lora(x, gy, logits.to(dev), ops.PhiloxNoise(1, 0), pal.to(dev),
-                                       0.5, a, b, 1.0)
-    assert not gl.any() and not gp.any() and not ga.any() and not gb.any()
+                                       0.5, a, b, 1.0, grad_sq=sq)
+    assert not gl.any() and not gp.any() and not ga.any() and not gb.any() and not sq.any()
     rl, rp = ops.soft_bwd(x, gy, logits.to(dev), ops.PhiloxNoise(1, 0), pal.to(dev), 0.5)
     assert not rl.any() and not rp.any()
 
@@ -165,7 +173,7 @@ def test_lora_grads_of_an_empty_weight_are_zero(dev):
             else:
                 rc = lib.plz_soft_bwd_lora(None, None, None, _lib.PLZ_DT_BF16, None, 0, 0, None,
                                            0.5, 0, None, None, r, 1.0, None, None, pa, pb,
-                                           _lib.PLZ_DT_BF16, None, 0, M, n, k, s)
+                                           _lib.PLZ_DT_BF16, None, None, 0, M, n, k, s)
             assert rc == 0, lib.plz_last_error()
         torch.cuda.synchronize()
         assert bool((ga == 0).all()) and bool((gb == 0).all()), entry

@@ -50,3 +50,36 @@ def test_fused_adamw_matches_oracle(dev):
             if specs[i][1] == torch.bfloat16:
                 m32 = next(e[1] for e in opt.entries if e[0] is params[i])
                 assert np.allclose(f32(m32), want, rtol=1e-5, atol=1e-8), (i, step)
+
+
+def test_fused_adamw_takes_the_producers_squared_sums(dev):
+    """grad_sq: the clip norm of a parameter read from one fp32 sum per 512 gradient elements
+    (what the soft backward writes) instead of from the gradient: the same norms (summation
+    order aside) and, with the clip active, the same update to fp32 rounding; sums that do not
+    cover the parameter are refused."""
+    rng = np.random.default_rng(7)
+    shape = (12, 256, 4)  # 12288 elements: one full block of 8192 and a partial one
+    base = torch.tensor(rng.standard_normal(shape) * 0.02, dtype=torch.bfloat16)
+    grad = torch.tensor(rng.standard_normal(shape) * 0.5, dtype=torch.bfloat16)
+    other = torch.tensor(rng.standard_normal((300,)) * 0.02, dtype=torch.float32)
+    results = []
+    for use_sq in (False, True):
+        p = base.clone().to(dev).requires_grad_(True)
+        q = other.clone().to(dev).requires_grad_(True)
+        opt = optim.FusedAdamW([{"params": [p], "lr": 1e-2, "clip_group": 0},
+                                {"params": [q], "lr": 1e-3, "clip_group": 1}])
+        p.grad = grad.to(dev)
+        q.grad = torch.ones(300, device=dev)
+        sq = None
+        if use_sq:
+            sq = {id(p): (p.grad.float() ** 2).reshape(-1, 512).sum(1).contiguous()}
+        norms = opt.step(max_norms=(1.0, 0.3), grad_sq=sq)
+        results.append((f32(norms), f32(p), f32(q)))
+    (n0, p0, q0), (n1, p1, q1) = results
+    assert np.allclose(n0, n1, rtol=1e-5) and n0[0] > 1.0  # the clip is active
+    assert np.allclose(p0, p1, rtol=2.0 ** -7, atol=1e-6) and np.array_equal(q0, q1)
+    p = base.clone().to(dev).requires_grad_(True)
+    opt = optim.FusedAdamW([{"params": [p], "lr": 1e-2, "clip_group": 0}])
+    p.grad = grad.to(dev)
+    with pytest.raises(ValueError, match="512"):
+        opt.step(grad_sq={id(p): torch.zeros(5, device=dev)})
