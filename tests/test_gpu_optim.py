@@ -83,3 +83,40 @@ def test_fused_adamw_takes_the_producers_squared_sums(dev):
     p.grad = grad.to(dev)
     with pytest.raises(ValueError, match="512"):
         opt.step(grad_sq={id(p): torch.zeros(5, device=dev)})
+
+
+@pytest.mark.parametrize("N,K", [(3, 256), (40, 768), (9, 2560)])
+def test_step_build_matches_a_separate_build(dev, N, K):
+    """FusedAdamW.step(build=NextBuild(...)): the soft weight written by the update pass, for
+    logits whose element count is or is not a multiple of the update's 8192-element blocks, with
+    a palette updated in the same step and a non-zero noise counter base, equals the batched
+    build of the updated logits (plz_soft_build_w_batched_philox) bit for bit; the parameters
+    equal those of the same step without the build."""
+    ops = pytest.importorskip("palettize_hip.ops")
+    from palettize_hip import _lib
+    rng = np.random.default_rng(N * K)
+    logits0 = torch.tensor(rng.standard_normal((N, K, 4)) * 2, dtype=torch.bfloat16)
+    pal0 = torch.tensor(np.sort(rng.standard_normal((N, K // 256, 4)) * 0.02, -1),
+                        dtype=torch.float32)
+    glog = torch.tensor(rng.standard_normal((N, K, 4)), dtype=torch.bfloat16)
+    gpal = torch.tensor(rng.standard_normal((N, K // 256, 4)) * 0.1, dtype=torch.float32)
+    seed, counter, offset, tau = 77, 5 * K, 123456, 0.75
+    outs = []
+    for with_build in (False, True):
+        lg = logits0.clone().to(dev).requires_grad_(True)
+        pal = pal0.clone().to(dev).requires_grad_(True)
+        opt = optim.FusedAdamW([{"params": [pal], "lr": 1e-2, "clip_group": 1},
+                                {"params": [lg], "lr": 0.5, "clip_group": 0,
+                                 "clamp": (-3.0, 3.0)}])
+        lg.grad, pal.grad = glog.to(dev), gpal.to(dev)
+        w = torch.zeros(N, K, dtype=torch.bfloat16, device=dev)
+        nb = optim.NextBuild([(lg, pal, w, seed, counter)], offset, tau) if with_build else None
+        opt.step(max_norms=(1.0, 0.3), build=nb)
+        if with_build:
+            assert nb.built == {id(lg)}
+        outs.append((lg.detach().clone(), pal.detach().clone(), w))
+    (lg_a, pal_a, _), (lg_b, pal_b, w_b) = outs
+    assert torch.equal(lg_a.view(torch.int16), lg_b.view(torch.int16)) and torch.equal(pal_a, pal_b)
+    grp = ops.SoftBuildGroup([(lg_b, ops.PhiloxNoise(seed, 0), pal_b)], _lib.PLZ_W_HARD_NOISY)
+    (w_ref, _), = grp.run(tau, offset + counter)
+    assert torch.equal(w_b.view(torch.int16), w_ref.view(torch.int16))
