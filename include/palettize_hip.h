@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define PLZ_ABI_VERSION 16
+#define PLZ_ABI_VERSION 17
 
 /* status codes */
 #define PLZ_OK 0
@@ -257,6 +257,10 @@ typedef struct plz_build_w_desc {
   uint64_t noise_seed;     /* Philox key of a descriptor without a noise tensor */
   uint64_t noise_counter;  /* its counter base: weight (n, k) draws at offset + noise_counter
                               + n*K + k (0 for the layout above) */
+  uint16_t* p_out;         /* [N, K, 4] fp16 or NULL: P = softmax((logits + noise) / tau), what
+                              the reference's forward saves as P_aos for its backward
+                              (fused_lut_linear_cuda.py:903-905, 919, 957-959);
+                              plz_soft_bwd_lora reads it */
 } plz_build_w_desc;
 /* Checks n host descriptors, fills block_begin and returns the launch's block count (or a
  * negative status). */
@@ -303,11 +307,16 @@ int plz_soft_bwd_philox(const uint16_t* x, const uint16_t* grad_y, const uint16_
  * sum of squares of each run of 512 consecutive grad_logits values as stored (row n, k
  * 128 j .. 128 j + 127), what the gradient-norm clip of the optimizer step
  * (train_qwen.py:1303-1319) sums; plz_adamw_desc.grad_sq takes it in place of reading the
- * gradient again. */
+ * gradient again. probs (optional, fp16 [N, K, 4], 16-byte aligned): the forward's P as a
+ * build with plz_build_w_desc.p_out wrote it; the epilogues then read P instead of drawing the
+ * noise again and recomputing the softmax, as the reference's backward reads its saved P_aos
+ * (fused_lut_linear_cuda.py:957-959), and noise, seed, offset and the logits' values go unused
+ * (logits_dtype still sets grad_logits' type). */
 size_t plz_soft_bwd_lora_workspace(int64_t M, int64_t N, int64_t K, int rank);
 int plz_soft_bwd_lora(const uint16_t* x, const uint16_t* grad_y, const uint16_t* logits,
                       int logits_dtype, const float* noise, uint64_t seed, uint64_t offset,
-                      const float* palette, float tau, int scale_grad_by_inv_tau,
+                      const uint16_t* probs, const float* palette, float tau,
+                      int scale_grad_by_inv_tau,
                       const uint16_t* lora_a, const uint16_t* lora_b, int rank, float scale,
                       uint16_t* grad_logits, float* grad_palette, void* grad_a, void* grad_b,
                       int grads_dtype, float* grad_sq, void* workspace, size_t workspace_bytes,

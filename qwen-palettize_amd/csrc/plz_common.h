@@ -190,11 +190,14 @@ __device__ __forceinline__ void philox_gumbel4(uint64_t seed, uint64_t ctr, floa
 //   P_c = softmax_c((logit_c + noise_c) / tau)   (one reciprocal of the sum)
 //   W_soft = sum_c P_c pal_c,   W_hard = pal[argmax P] (first maximum wins), or over the plain
 //   logits with PLZ_W_HARD_PLAIN
-// wo = bf16 W of the mode, so = bf16 W_soft. The build-W kernels and the optimizer step that
-// builds the next forward's W call this one function, so their W agree bit for bit.
+// wo = bf16 W of the mode, so = bf16 W_soft, po = P as fp16 (the reference's P_aos element
+// type; weight-major, classes in order, two per word). The build-W kernels and the optimizer
+// step that builds the next forward's W call this one function, so their outputs agree bit for
+// bit.
 __device__ __forceinline__ void build_w_two(const uint32_t (&lw)[4], int f16, const float (&nz)[8],
                                             const float (&pc)[4], float inv_tau, int mode,
-                                            uint32_t (&wo)[2], uint32_t (&so)[2]) {
+                                            uint32_t (&wo)[2], uint32_t (&so)[2],
+                                            uint32_t (&po)[4]) {
 #pragma unroll
   for (int el = 0; el < 2; ++el) {
     float l[4], a[4];
@@ -229,6 +232,8 @@ __device__ __forceinline__ void build_w_two(const uint32_t (&lw)[4], int f16, co
     const float wh = am == 0 ? pc[0] : am == 1 ? pc[1] : am == 2 ? pc[2] : pc[3];
     wo[el] = f2bf(mode == PLZ_W_SOFT ? ws : wh);
     so[el] = f2bf(ws);
+    po[2 * el] = f2h(P[0]) | (f2h(P[1]) << 16);
+    po[2 * el + 1] = f2h(P[2]) | (f2h(P[3]) << 16);
   }
 }
 

@@ -102,6 +102,8 @@ struct Args {
   // soft epilogues: the sum of squares of each item's stored grad_logits (512 values: row n,
   // 128 k), [I][J / 128] fp32, or NULL
   float* gsq;
+  // soft epilogues: the forward's P [I][J][4] fp16, read in place of logits + noise, or NULL
+  const uint16_t* pin;
 };
 
 // B row (and output column) of the tile-local logical column j when b_half > 0: the first 128

@@ -536,6 +536,10 @@ __device__ __forceinline__ SoftIn soft_load(const Args& g, int64_t n, int64_t ks
   const int64_t k = kseg + 2 * lane, e0 = (n * g.J + k) * 4;
   SoftIn in;
   in.pal = *reinterpret_cast<const float4*>(g.pal + (n * (g.J / 256) + k / 256) * 4);
+  if (g.pin) {  // the forward's P of the lane's two weights
+    in.lg = *reinterpret_cast<const uint4*>(g.pin + e0);
+    return in;
+  }
   in.lg = *reinterpret_cast<const uint4*>(g.logits + e0);
   if (g.noise) {
     in.z0 = *reinterpret_cast<const float4*>(g.noise + e0);
@@ -591,48 +595,74 @@ __device__ __forceinline__ void soft_math(const Args& g, int64_t n, int64_t kseg
   const float pc[4] = {in.pal.x, in.pal.y, in.pal.z, in.pal.w};
   const int64_t e0 = (n * g.J + k) * 4;
   const uint32_t lw[4] = {in.lg.x, in.lg.y, in.lg.z, in.lg.w};
-  float nz[8];
-  if (g.noise) {
-    nz[0] = in.z0.x; nz[1] = in.z0.y; nz[2] = in.z0.z; nz[3] = in.z0.w;
-    nz[4] = in.z1.x; nz[5] = in.z1.y; nz[6] = in.z1.z; nz[7] = in.z1.w;
-  } else {  // the noise the forward drew: Philox at noise_offset + n*K + k
-    float z[4];
-    philox_gumbel4(g.noise_seed, g.noise_offset + (uint64_t)(n * g.J + k), z);
-    nz[0] = z[0]; nz[1] = z[1]; nz[2] = z[2]; nz[3] = z[3];
-    philox_gumbel4(g.noise_seed, g.noise_offset + (uint64_t)(n * g.J + k + 1), z);
-    nz[4] = z[0]; nz[5] = z[1]; nz[6] = z[2]; nz[7] = z[3];
+  // P of the lane's two weights and dm_c = pal_c - W_soft, W_soft = sum_c P_c pal_c
+  float P[2][4], dm[2][4];
+  if (g.pin) {  // the forward's P (fp16), as the reference's backward reads its P_aos
+#pragma unroll
+    for (int el = 0; el < 2; ++el) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) P[el][c] = h2f((lw[2 * el + c / 2] >> (16 * (c & 1))) & 0xffffu);
+      // pal_c - W_soft as sum_c' P_c' (pal_c - pal_c'), which holds when sum_c P_c = 1: with
+      // P rounded to fp16 and one class near 1, pal_c - W_soft for that class would be the
+      // difference of two nearly equal numbers whose rounding errors do not cancel
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        float d = 0.f;
+#pragma unroll
+        for (int c2 = 0; c2 < 4; ++c2)
+          if (c2 != c) d += P[el][c2] * (pc[c] - pc[c2]);
+        dm[el][c] = d;
+      }
+    }
+  } else {
+    float ws[2] = {0.f, 0.f};
+    float nz[8];
+    if (g.noise) {
+      nz[0] = in.z0.x; nz[1] = in.z0.y; nz[2] = in.z0.z; nz[3] = in.z0.w;
+      nz[4] = in.z1.x; nz[5] = in.z1.y; nz[6] = in.z1.z; nz[7] = in.z1.w;
+    } else {  // the noise the forward drew: Philox at noise_offset + n*K + k
+      float z[4];
+      philox_gumbel4(g.noise_seed, g.noise_offset + (uint64_t)(n * g.J + k), z);
+      nz[0] = z[0]; nz[1] = z[1]; nz[2] = z[2]; nz[3] = z[3];
+      philox_gumbel4(g.noise_seed, g.noise_offset + (uint64_t)(n * g.J + k + 1), z);
+      nz[4] = z[0]; nz[5] = z[1]; nz[6] = z[2]; nz[7] = z[3];
+    }
+#pragma unroll
+    for (int el = 0; el < 2; ++el) {
+      float a[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const uint32_t bits = (lw[2 * el + c / 2] >> (16 * (c & 1))) & 0xffffu;
+        a[c] = ((g.logits_f16 ? h2f(bits) : bf2f(bits)) + nz[4 * el + c]) * g.inv_tau;
+      }
+      const float m = fmaxf(fmaxf(a[0], a[1]), fmaxf(a[2], a[3]));
+      float ex[4], s = 0.f;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        ex[c] = __expf(a[c] - m);
+        s += ex[c];
+      }
+      const float rs = 1.f / s;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        P[el][c] = ex[c] * rs;
+        ws[el] += P[el][c] * pc[c];
+      }
+#pragma unroll
+      for (int c = 0; c < 4; ++c) dm[el][c] = pc[c] - ws[el];
+    }
   }
   float sp[4] = {0.f, 0.f, 0.f, 0.f};
   uint32_t out[4];
 #pragma unroll
   for (int el = 0; el < 2; ++el) {
-    float a[4];
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const uint32_t bits = (lw[2 * el + c / 2] >> (16 * (c & 1))) & 0xffffu;
-      a[c] = ((g.logits_f16 ? h2f(bits) : bf2f(bits)) + nz[4 * el + c]) * g.inv_tau;
-    }
-    const float m = fmaxf(fmaxf(a[0], a[1]), fmaxf(a[2], a[3]));
-    float ex[4], s = 0.f;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      ex[c] = __expf(a[c] - m);
-      s += ex[c];
-    }
-    const float rs = 1.f / s;
-    float P[4], ws = 0.f;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      P[c] = ex[c] * rs;
-      ws += P[c] * pc[c];
-    }
     const float gv = el == 0 ? gw.x : gw.y;
     uint32_t o16[4];
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      const float gp = gv * P[c];
+      const float gp = gv * P[el][c];
       sp[c] += gp;
-      const float gl = g.glog_scale * gp * (pc[c] - ws);
+      const float gl = g.glog_scale * gp * dm[el][c];
       o16[c] = g.logits_f16 ? f2h(gl) : f2bf(gl);
     }
     out[2 * el] = o16[0] | (o16[1] << 16);
@@ -1937,7 +1967,8 @@ static int soft_bwd(const uint16_t* x, const uint16_t* grad_y, const uint16_t* l
                     const float* palette, float tau, int scale_grad_by_inv_tau,
                     uint16_t* grad_logits, float* grad_palette, void* workspace,
                     size_t workspace_bytes, int64_t M, int64_t N, int64_t K, void* stream,
-                    const WgradArgs& wg = WgradArgs(), float* gsq = nullptr) {
+                    const WgradArgs& wg = WgradArgs(), float* gsq = nullptr,
+                    const uint16_t* probs = nullptr) {
   PLZ_REQUIRE(M >= 0 && N >= 0 && K >= 0, "plz_soft_bwd: negative shape");
   PLZ_REQUIRE(K % 256 == 0, "plz_soft_bwd: K (%lld) must be a multiple of 256", (long long)K);
   PLZ_REQUIRE(N % 8 == 0, "plz_soft_bwd: N (%lld) must be a multiple of 8", (long long)N);
@@ -1945,7 +1976,7 @@ static int soft_bwd(const uint16_t* x, const uint16_t* grad_y, const uint16_t* l
               "plz_soft_bwd: logits dtype must be bf16 or fp16");
   PLZ_REQUIRE(tau > 0.f, "plz_soft_bwd: tau must be positive");
   if (N == 0 || K == 0) return PLZ_OK;
-  PLZ_REQUIRE(logits && palette && grad_logits && grad_palette && (gen || noise),
+  PLZ_REQUIRE(logits && palette && grad_logits && grad_palette && (gen || noise || probs),
               "plz_soft_bwd: null pointer");
   if (M == 0) {  // empty reduction: every gradient is zero
     zero_async(grad_logits, (size_t)N * K * 4 * 2, (hipStream_t)stream);
@@ -1960,7 +1991,7 @@ static int soft_bwd(const uint16_t* x, const uint16_t* grad_y, const uint16_t* l
   }
   PLZ_REQUIRE(x && grad_y, "plz_soft_bwd: null pointer");
   PLZ_REQUIRE(a16(x) && a16(grad_y) && a16(logits) && a16(noise) && a16(palette) &&
-                  a16(grad_logits),
+                  a16(grad_logits) && a16(probs),
               "plz_soft_bwd: operands must be 16-byte aligned");
   const size_t need = plz_soft_bwd_workspace(M, N, K);
   if (!workspace || workspace_bytes < need) {
@@ -1984,6 +2015,7 @@ static int soft_bwd(const uint16_t* x, const uint16_t* grad_y, const uint16_t* l
   g.wg_a = wg.lora_a; g.wg_b = wg.lora_b;
   g.wg_part_a = wg.part_a; g.wg_part_b = wg.part_b;
   g.gsq = gsq;
+  g.pin = probs;
   int rc;
   if (z == 1) {
     rc = launch<OP_COL, OP_COL, EPI_SOFT>(g, 1, (hipStream_t)stream, "plz_soft_bwd");
@@ -2034,7 +2066,8 @@ size_t plz_soft_bwd_lora_workspace(int64_t M, int64_t N, int64_t K, int rank) {
 
 int plz_soft_bwd_lora(const uint16_t* x, const uint16_t* grad_y, const uint16_t* logits,
                       int logits_dtype, const float* noise, uint64_t seed, uint64_t offset,
-                      const float* palette, float tau, int scale_grad_by_inv_tau,
+                      const uint16_t* probs, const float* palette, float tau,
+                      int scale_grad_by_inv_tau,
                       const uint16_t* lora_a, const uint16_t* lora_b, int rank, float scale,
                       uint16_t* grad_logits, float* grad_palette, void* grad_a, void* grad_b,
                       int grads_dtype, float* grad_sq, void* workspace, size_t workspace_bytes,
@@ -2068,7 +2101,7 @@ int plz_soft_bwd_lora(const uint16_t* x, const uint16_t* grad_y, const uint16_t*
       w + soft_bytes + align256(wg_part_a_floats(z, N, K, rank) * sizeof(float)));
   return soft_bwd(x, grad_y, logits, logits_dtype, noise == nullptr, noise, seed, offset, palette,
                   tau, scale_grad_by_inv_tau, grad_logits, grad_palette, workspace,
-                  soft_bytes, M, N, K, stream, wg, grad_sq);
+                  soft_bytes, M, N, K, stream, wg, grad_sq, probs);
 }
 
 int plz_soft_bwd_philox(const uint16_t* x, const uint16_t* grad_y, const uint16_t* logits,

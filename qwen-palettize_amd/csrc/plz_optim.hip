@@ -197,10 +197,11 @@ __device__ __forceinline__ void build_chunk(const plz_build_w_desc& bd, int64_t 
     philox_gumbel4(bd.noise_seed, ctr + 1, z);
     nz[4] = z[0]; nz[5] = z[1]; nz[6] = z[2]; nz[7] = z[3];
   }
-  uint32_t wo[2], so[2];
-  build_w_two(lw, 0, nz, pc, inv_tau, mode, wo, so);
+  uint32_t wo[2], so[2], po[4];
+  build_w_two(lw, 0, nz, pc, inv_tau, mode, wo, so, po);
   *reinterpret_cast<uint32_t*>(bd.w + w0) = wo[0] | (wo[1] << 16);
   if (bd.w_soft) *reinterpret_cast<uint32_t*>(bd.w_soft + w0) = so[0] | (so[1] << 16);
+  if (bd.p_out) *reinterpret_cast<uint4*>(bd.p_out + i0) = make_uint4(po[0], po[1], po[2], po[3]);
 }
 
 struct BuildArgs {

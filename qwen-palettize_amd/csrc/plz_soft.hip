@@ -148,7 +148,8 @@ __device__ __forceinline__ void build_w_pair(const uint16_t* __restrict__ logits
                                              const float* __restrict__ noise, uint64_t seed,
                                              uint64_t offset, const float* __restrict__ pal,
                                              float inv_tau, int mode, uint16_t* __restrict__ w,
-                                             uint16_t* __restrict__ w_soft, int64_t K, int64_t t) {
+                                             uint16_t* __restrict__ w_soft, int64_t K, int64_t t,
+                                             uint16_t* __restrict__ p_out = nullptr) {
   const int64_t half = K / 2;
   const int64_t n = t / half, k = 2 * (t % half);
   const float4 p = *reinterpret_cast<const float4*>(pal + (n * (K / kPalGroup) + k / kPalGroup) * 4);
@@ -169,8 +170,9 @@ __device__ __forceinline__ void build_w_pair(const uint16_t* __restrict__ logits
     nz[0] = z0.x; nz[1] = z0.y; nz[2] = z0.z; nz[3] = z0.w;
     nz[4] = z1.x; nz[5] = z1.y; nz[6] = z1.z; nz[7] = z1.w;
   }
-  uint32_t wo[2], so[2];
-  build_w_two(lw, f16, nz, pc, inv_tau, mode, wo, so);
+  uint32_t wo[2], so[2], po[4];
+  build_w_two(lw, f16, nz, pc, inv_tau, mode, wo, so, po);
+  if (p_out) *reinterpret_cast<uint4*>(p_out + e0) = make_uint4(po[0], po[1], po[2], po[3]);
   const int64_t o = n * K + k;
   *reinterpret_cast<uint32_t*>(w + o) = wo[0] | (wo[1] << 16);
   if (w_soft) *reinterpret_cast<uint32_t*>(w_soft + o) = so[0] | (so[1] << 16);
@@ -203,10 +205,11 @@ __global__ void build_w_batched_kernel(const plz_build_w_desc* __restrict__ desc
   if (t >= d.N * (d.K / 2)) return;
   if (d.noise)
     build_w_pair<false>(d.logits, d.logits_dtype == PLZ_DT_FP16, d.noise, 0, 0, d.palette,
-                        inv_tau, mode, d.w, d.w_soft, d.K, t);
+                        inv_tau, mode, d.w, d.w_soft, d.K, t, d.p_out);
   else  // the descriptor's own Philox key (uniform per block)
     build_w_pair<true>(d.logits, d.logits_dtype == PLZ_DT_FP16, nullptr, d.noise_seed,
-                       offset + d.noise_counter, d.palette, inv_tau, mode, d.w, d.w_soft, d.K, t);
+                       offset + d.noise_counter, d.palette, inv_tau, mode, d.w, d.w_soft, d.K, t,
+                       d.p_out);
 }
 
 }  // namespace plz
@@ -350,7 +353,8 @@ int64_t plz_build_w_plan(plz_build_w_desc* descs, int n) {
     }
     if (d.N > 0 && d.K > 0 &&
         (!d.logits || !d.palette || !d.w ||
-         (((uintptr_t)d.logits | (uintptr_t)d.noise | (uintptr_t)d.palette) & 15) ||
+         (((uintptr_t)d.logits | (uintptr_t)d.noise | (uintptr_t)d.palette |
+           (uintptr_t)d.p_out) & 15) ||
          (((uintptr_t)d.w | (uintptr_t)d.w_soft) & 3))) {
       set_error("plz_build_w_plan: descriptor %d: null or misaligned pointer", i);
       return -PLZ_EINVAL;

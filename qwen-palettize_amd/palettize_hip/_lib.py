@@ -24,7 +24,8 @@ i32, i64, u32, u64, f32, sz = C.c_int, C.c_int64, C.c_uint32, C.c_uint64, C.c_fl
 class BuildWDesc(C.Structure):
     _fields_ = [("logits", p), ("noise", p), ("palette", p), ("w", p), ("w_soft", p),
                 ("N", i64), ("K", i64), ("logits_dtype", i32), ("reserved", i32),
-                ("block_begin", i64), ("noise_seed", u64), ("noise_counter", u64)]
+                ("block_begin", i64), ("noise_seed", u64), ("noise_counter", u64),
+                ("p_out", p)]
 
 
 class PwRefDesc(C.Structure):
@@ -92,8 +93,8 @@ SIGNATURES: dict[str, tuple] = {
     "plz_soft_bwd": (i32, [p, p, p, i32, p, p, f32, i32, p, p, p, sz, i64, i64, i64, p]),
     "plz_soft_bwd_philox": (i32, [p, p, p, i32, u64, u64, p, f32, i32, p, p, p, sz, i64, i64, i64, p]),
     "plz_soft_bwd_lora_workspace": (sz, [i64, i64, i64, i32]),
-    "plz_soft_bwd_lora": (i32, [p, p, p, i32, p, u64, u64, p, f32, i32, p, p, i32, f32, p, p, p, p,
-                                i32, p, p, sz, i64, i64, i64, p]),
+    "plz_soft_bwd_lora": (i32, [p, p, p, i32, p, u64, u64, p, p, f32, i32, p, p, i32, f32, p, p, p,
+                                p, i32, p, p, sz, i64, i64, i64, p]),
     "plz_lora_project": (i32, [p, p, f32, p, i64, i64, i32, p]),
     "plz_lora_grad_t": (i32, [p, p, f32, p, i64, i64, i32, p]),
     "plz_lora_weight_grads_workspace": (sz, [i64, i64, i64, i32]),

@@ -93,7 +93,9 @@ class SoftLUTLinearFunction(torch.autograd.Function):
     logits, noise, palette and tau by ``group`` (an ops.SoftBuildGroup run); the backward
     checks that no later run of the group has overwritten it. A third element, an object with
     ``buf`` (fp32 [N * K / 128]) and ``writes``, has the backward's fused soft dW also write the
-    squared-gradient sums of the logits there (ops.soft_bwd_lora grad_sq) and count the write."""
+    squared-gradient sums of the logits there (ops.soft_bwd_lora grad_sq) and count the write
+    (None: not), and a fourth, the forward's P (fp16 [N, K, 4], the group's ``probs``), has it
+    read P instead of drawing the noise again."""
 
     @staticmethod
     def forward(ctx, x, palette, logits, noise, tau, bias, lora_a, lora_b, lora_scale, mode,
@@ -101,13 +103,14 @@ class SoftLUTLinearFunction(torch.autograd.Function):
         x = x.contiguous()
         lora_a, lora_b = _c(lora_a), _c(lora_b)
         ctx.guard = None
-        ctx.grad_sq = None
+        ctx.grad_sq = ctx.probs = None
         if prebuilt is None:
             w, _ = ops.soft_build_w(logits, noise, palette, tau, mode)
         else:
             w, group = prebuilt[:2]
             ctx.guard = (group, group.generation)
             ctx.grad_sq = prebuilt[2] if len(prebuilt) > 2 else None
+            ctx.probs = prebuilt[3] if len(prebuilt) > 3 else None
         t = ops.lora_project(x, lora_a, lora_scale) if lora_a is not None else None
         y = ops.linear_fwd_dense(x, w, bias, t, lora_b)
         # a Philox noise descriptor is redrawn in the backward's epilogue, not stored
@@ -150,7 +153,7 @@ class SoftLUTLinearFunction(torch.autograd.Function):
             grad_logits, grad_pal, grad_a, grad_b = ops.soft_bwd_lora(
                 x, gy, logits, noise, palette, ctx.tau, lora_a, lora_b, ctx.lora_scale,
                 ctx.scale_by_inv_tau, out_dtype=lora_a.dtype,
-                grad_sq=sq.buf if sq is not None else None)
+                grad_sq=sq.buf if sq is not None else None, probs=ctx.probs)
             if sq is not None:
                 sq.writes += 1
         elif need_soft:

@@ -253,8 +253,9 @@ class SoftPalettizedLinear(nn.Module):
         if prebuilt is None:
             noise = self.next_noise_spec()
         else:
-            w, group, noise = prebuilt
-            prebuilt = (w, group) if self.grad_sq is None else (w, group, self.grad_sq)
+            w, group, noise = prebuilt[:3]
+            probs = prebuilt[3] if len(prebuilt) > 3 else None
+            prebuilt = (w, group, self.grad_sq, probs)
         y = SoftLUTLinearFunction.apply(x.reshape(-1, x.shape[-1]), self.palette, self.index_logits,
                                         noise, self.tau, None, self.lora_a, self.lora_b,
                                         self.lora_scale, self.mode, False, prebuilt)
@@ -393,7 +394,8 @@ class SoftLinearGroupFunction(torch.autograd.Function):
         """(x, w, t, b) of this forward; records what the backward needs besides the saved
         tensors."""
         x = x.contiguous()
-        w, build, noise = prebuilt
+        w, build, noise = prebuilt[:3]
+        ctx.probs = prebuilt[3] if len(prebuilt) > 3 else None
         ctx.guard = (build, build.generation)
         a, b = grp.lora_a(), grp.lora_b()
         t = ops.lora_project(x, a, grp.lora_scale)
@@ -426,7 +428,8 @@ class SoftLinearGroupFunction(torch.autograd.Function):
         sq = grp.grad_sq
         gl, gp, ga, gb = ops.soft_bwd_lora(x, gy, logits, ctx.noise, pal, ctx.tau, a, b, scale,
                                            False, out_dtype=a.dtype,
-                                           grad_sq=sq.buf if sq is not None else None)
+                                           grad_sq=sq.buf if sq is not None else None,
+                                           probs=ctx.probs)
         if sq is not None:
             sq.writes += 1
         grads = []
@@ -587,6 +590,9 @@ class PalettizedDecoderLayer(nn.Module):
         self._wgroup = None
         self._wgroup_key = None
         self._pending = None  # weights built by the last optimizer step (commit_next_build)
+        # the build also keeps each weight's P (fp16), which the soft backward then reads instead
+        # of drawing the noise again, as the reference's backward reads its saved P_aos
+        self.save_probs = True
 
     def linears(self):
         return [getattr(self, n) for n in self.NAMES]
@@ -616,7 +622,8 @@ class PalettizedDecoderLayer(nn.Module):
                 items.append((u.index_logits, ops.PhiloxNoise(u.noise_seed, 0), u.palette))
         key = tuple((t.data_ptr(), t.device) for lg, _, pal in items for t in (lg, pal))
         if self._wgroup is None or self._wgroup_key != key:
-            self._wgroup = ops.SoftBuildGroup(items, PLZ_W_HARD_NOISY)
+            self._wgroup = ops.SoftBuildGroup(items, PLZ_W_HARD_NOISY,
+                                              want_probs=self.save_probs)
             self._wgroup_key = key
         return units, self._wgroup
 
@@ -649,11 +656,12 @@ class PalettizedDecoderLayer(nn.Module):
                 outs = grp.outputs
             else:  # built from values that have changed since: build again, same noise
                 outs = grp.run(tau, pend["offset"])
-            return {n: (w, grp, sp) for (n, _), (w, _), sp in zip(units, outs, pend["specs"])}
+            return {n: (w, grp, sp, pr) for (n, _), (w, _), sp, pr in
+                    zip(units, outs, pend["specs"], grp.probs)}
         offset = self._next_offset(units)
         specs = [u.next_noise_spec() for _, u in units]
         outs = grp.run(tau, offset)
-        return {n: (w, grp, sp) for (n, _), (w, _), sp in zip(units, outs, specs)}
+        return {n: (w, grp, sp, pr) for (n, _), (w, _), sp, pr in zip(units, outs, specs, grp.probs)}
 
     def plan_next_build(self, tau):
         """The next forward's weights as an optimizer-step build (optim.NextBuild): every
@@ -664,15 +672,15 @@ class PalettizedDecoderLayer(nn.Module):
         offset = self._next_offset(units, check_tau=False)
         specs = [u.next_noise_spec() for _, u in units]
         items = []
-        for (_, u), (w, _) in zip(units, grp.outputs):
+        for (_, u), (w, _), pr in zip(units, grp.outputs, grp.probs):
             if isinstance(u, SoftLinearGroup):
                 r0 = 0
                 for p, n in zip(u.parts, u.rows):
                     items.append((p.index_logits, p.palette, w[r0:r0 + n], u.parts[0].noise_seed,
-                                  r0 * u.K))
+                                  r0 * u.K, None if pr is None else pr[r0:r0 + n]))
                     r0 += n
             else:
-                items.append((u.index_logits, u.palette, w, u.noise_seed, 0))
+                items.append((u.index_logits, u.palette, w, u.noise_seed, 0, pr))
         nb = NextBuild(items, offset, tau, PLZ_W_HARD_NOISY)
         nb.specs = specs
         return nb

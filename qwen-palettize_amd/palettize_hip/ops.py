@@ -449,27 +449,35 @@ class SoftBuildGroup:
     noise is an fp32 [N, K, 4] tensor or a ``PhiloxNoise`` whose seed is that linear's Philox
     key (its noise is then drawn in the kernel at the counter offset given to ``run``). The
     outputs (w and, with want_soft, w_soft) are allocated once and rewritten by every run;
-    ``generation`` counts the runs."""
+    ``generation`` counts the runs. With want_probs, every run also writes each linear's
+    P = softmax((logits + noise) / tau) as fp16 [N, K, 4] into ``probs[i]``, which
+    soft_bwd_lora(probs=...) reads in the backward."""
 
-    def __init__(self, items, mode: int = _lib.PLZ_W_HARD_NOISY, want_soft: bool = False):
+    def __init__(self, items, mode: int = _lib.PLZ_W_HARD_NOISY, want_soft: bool = False,
+                 want_probs: bool = False):
         if not items:
             raise ValueError("empty build group")
         self.mode = int(mode)
         self.device = items[0][0].device
         self.outputs = []
+        self.probs = []
         self.generation = 0
         descs = (_lib.BuildWDesc * len(items))()
         for i, (logits, noise, palette) in enumerate(items):
             N, K = _soft_shapes(logits, noise, palette)
             w = torch.empty((N, K), dtype=torch.bfloat16, device=self.device)
             ws = torch.empty((N, K), dtype=torch.bfloat16, device=self.device) if want_soft else None
+            pr = (torch.empty((N, K, 4), dtype=torch.float16, device=self.device) if want_probs
+                  else None)
             self.outputs.append((w, ws))
+            self.probs.append(pr)
             philox = isinstance(noise, PhiloxNoise)
             descs[i] = _lib.BuildWDesc(logits.data_ptr(), None if philox else noise.data_ptr(),
                                        palette.data_ptr(), w.data_ptr(),
                                        ws.data_ptr() if ws is not None else None,
                                        N, K, _DT[logits.dtype], 0, 0,
-                                       (noise.seed & (2**64 - 1)) if philox else 0)
+                                       (noise.seed & (2**64 - 1)) if philox else 0, 0,
+                                       pr.data_ptr() if pr is not None else None)
         self._keep = items
         total = _lib.lib().plz_build_w_plan(descs, len(items))
         if total < 0:
@@ -511,13 +519,18 @@ def soft_bwd(x, grad_y, logits, noise, palette, tau: float, scale_by_inv_tau: bo
 
 def soft_bwd_lora(x, grad_y, logits, noise, palette, tau: float, lora_a, lora_b,
                   scale: float = 1.0, scale_by_inv_tau: bool = False, out_dtype=torch.bfloat16,
-                  grad_sq=None):
+                  grad_sq=None, probs=None):
     """(grad_logits, grad_palette, grad_a [r, K], grad_b [N, r]) from one dW GEMM: the soft
     backward as soft_bwd (bit for bit), and the LoRA weight gradients scale * lora_b^T dW and
     scale * dW lora_a^T (dW = grad_y^T x), which lora_weight_grads computes from t and gt.
     grad_sq (optional fp32 [N * K / 128]) receives the sum of squares of each 512 consecutive
-    grad_logits values, for FusedAdamW.step(grad_sq=...)."""
+    grad_logits values, for FusedAdamW.step(grad_sq=...). probs (optional fp16 [N, K, 4]): the
+    forward's P (SoftBuildGroup(want_probs=True)), read instead of redrawing the noise."""
     N, K = _soft_shapes(logits, noise, palette)
+    if probs is not None:
+        _need(probs, "probs", torch.float16, 3)
+        if tuple(probs.shape) != (N, K, 4):
+            raise ValueError(f"probs must be [N, K, 4] = [{N}, {K}, 4]")
     if grad_sq is not None:
         _need(grad_sq, "grad_sq", torch.float32, 1)
         if grad_sq.numel() != N * K // 128:
@@ -538,9 +551,10 @@ def soft_bwd_lora(x, grad_y, logits, noise, palette, tau: float, lora_a, lora_b,
     philox = isinstance(noise, PhiloxNoise)
     call("plz_soft_bwd_lora", _ptr(x), _ptr(grad_y), _ptr(logits), _DT[logits.dtype],
          None if philox else _ptr(noise), noise.seed if philox else 0,
-         noise.offset if philox else 0, _ptr(palette), float(tau), int(bool(scale_by_inv_tau)),
-         _ptr(lora_a), _ptr(lora_b), r, float(scale), _ptr(gl), _ptr(gp), _ptr(ga), _ptr(gb),
-         _DT[out_dtype], _ptr(grad_sq), _ptr(ws), ws.numel(), M, N, K, _stream(x))
+         noise.offset if philox else 0, _ptr(probs), _ptr(palette), float(tau),
+         int(bool(scale_by_inv_tau)), _ptr(lora_a), _ptr(lora_b), r, float(scale), _ptr(gl),
+         _ptr(gp), _ptr(ga), _ptr(gb), _DT[out_dtype], _ptr(grad_sq), _ptr(ws), ws.numel(), M, N,
+         K, _stream(x))
     return gl, gp, ga, gb
 
 

@@ -16,11 +16,12 @@ from ._lib import PLZ_DT_BF16, PLZ_DT_FP32, PLZ_W_HARD_NOISY, call, query
 class NextBuild:
     """Soft weights for the optimizer step to build from the logits it updates
     (plz_adamw_step_build): ``items`` lists (logits parameter, palette, w, noise_seed,
-    noise_counter) -- w [N, K] bf16 receives the weight plz_soft_build_w_batched_philox would
-    build from the updated logits, drawing weight (n, k) at Philox counter offset +
-    noise_counter + n*K + k under key noise_seed -- and ``offset``, ``tau``, ``mode`` are the
-    launch's. After the step, ``built`` holds the ids of the logits whose weight was built (a
-    parameter without a gradient is not updated, so not built either)."""
+    noise_counter[, probs]) -- w [N, K] bf16 receives the weight plz_soft_build_w_batched_philox
+    would build from the updated logits, drawing weight (n, k) at Philox counter offset +
+    noise_counter + n*K + k under key noise_seed, and probs (fp16 [N, K, 4], optional) its P --
+    and ``offset``, ``tau``, ``mode`` are the launch's. After the step, ``built`` holds the ids
+    of the logits whose weight was built (a parameter without a gradient is not updated, so not
+    built either)."""
 
     def __init__(self, items, offset: int, tau: float, mode: int = PLZ_W_HARD_NOISY):
         self.items = list(items)
@@ -127,11 +128,13 @@ class FusedAdamW:
             it = bmap.get(id(e[0]))
             if it is None:
                 continue
-            logits, palette, w, seed, counter = it
+            logits, palette, w, seed, counter = it[:5]
+            pr = it[5] if len(it) > 5 else None
             N, K = w.shape
             builds[i] = _lib.BuildWDesc(logits.data_ptr(), None, palette.data_ptr(), w.data_ptr(),
                                         None, N, K, PLZ_DT_BF16, 0, 0,
-                                        int(seed) & (2**64 - 1), int(counter) & (2**64 - 1))
+                                        int(seed) & (2**64 - 1), int(counter) & (2**64 - 1),
+                                        pr.data_ptr() if pr is not None else None)
         split = C.c_int64(0)
         total = _lib.lib().plz_adamw_plan_build(descs, builds, len(live), C.byref(split))
         if total < 0:

@@ -36,7 +36,7 @@ def test_every_declared_symbol_is_exported(lib):
         assert hasattr(lib, n), f"{n} declared in the header but not exported"
         assert n in _lib.SIGNATURES, f"{n} has no ctypes signature"
     assert set(_lib.SIGNATURES) == set(names)
-    assert lib.plz_abi_version() == 16
+    assert lib.plz_abi_version() == 17
 
 
 def test_shape_errors_are_reported_without_touching_the_gpu(lib):
@@ -58,11 +58,13 @@ def test_shape_errors_are_reported_without_touching_the_gpu(lib):
     rc = lib.plz_lut_linear_bwd_palette_lora(None, None, None, None, None, 16, 1.0, None, None,
                                              None, 0, None, 0, 64, 256, 256, None)
     assert rc == 1 and b"null" in lib.plz_last_error()
-    rc = lib.plz_soft_bwd_lora(None, None, None, 0, None, 0, 0, None, 0.5, 0, None, None, 12,
-                               1.0, None, None, None, None, 0, None, None, 0, 64, 256, 256, None)
+    rc = lib.plz_soft_bwd_lora(None, None, None, 0, None, 0, 0, None, None, 0.5, 0, None, None,
+                               12, 1.0, None, None, None, None, 0, None, None, 0, 64, 256, 256,
+                               None)
     assert rc == 1 and b"rank" in lib.plz_last_error()
-    rc = lib.plz_soft_bwd_lora(None, None, None, 0, None, 0, 0, None, 0.5, 0, None, None, 16,
-                               1.0, None, None, None, None, 0, None, None, 0, 64, 256, 256, None)
+    rc = lib.plz_soft_bwd_lora(None, None, None, 0, None, 0, 0, None, None, 0.5, 0, None, None,
+                               16, 1.0, None, None, None, None, 0, None, None, 0, 64, 256, 256,
+                               None)
     assert rc == 1 and b"null" in lib.plz_last_error()
 
 
@@ -311,7 +313,7 @@ def test_build_w_plan_accepts_philox_descriptors(lib):
     dereferenced by the plan."""
     from palettize_hip import _lib
     f = 4096
-    assert C.sizeof(_lib.BuildWDesc) == 5 * 8 + 2 * 8 + 2 * 4 + 8 + 8 + 8
+    assert C.sizeof(_lib.BuildWDesc) == 5 * 8 + 2 * 8 + 2 * 4 + 8 + 8 + 8 + 8
     d = (_lib.BuildWDesc * 3)(
         _lib.BuildWDesc(f, f, f, f, None, 64, 512, 0, 0, 0, 0),
         _lib.BuildWDesc(f, None, f, f, None, 8, 256, 1, 0, 0, 7),

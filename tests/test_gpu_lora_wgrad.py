@@ -172,8 +172,48 @@ def test_lora_grads_of_an_empty_weight_are_zero(dev):
                                                          M, n, k, s)
             else:
                 rc = lib.plz_soft_bwd_lora(None, None, None, _lib.PLZ_DT_BF16, None, 0, 0, None,
-                                           0.5, 0, None, None, r, 1.0, None, None, pa, pb,
+                                           None, 0.5, 0, None, None, r, 1.0, None, None, pa, pb,
                                            _lib.PLZ_DT_BF16, None, None, 0, M, n, k, s)
             assert rc == 0, lib.plz_last_error()
         torch.cuda.synchronize()
         assert bool((ga == 0).all()) and bool((gb == 0).all()), entry
+
+
+@pytest.mark.parametrize("M,N,K,philox", [(512, 2560, 2560, True), (300, 1032, 768, False),
+                                          (1024, 512, 1024, True)])
+def test_soft_bwd_lora_from_saved_probs(dev, M, N, K, philox):
+    """The forward's P saved by the build (SoftBuildGroup(want_probs=True), fp16 as the
+    reference's P_aos) and read by the backward (soft_bwd_lora(probs=...)): P against the fp64
+    softmax of logits + noise to fp16 rounding; the logits and palette gradients against those
+    recomputed from the noise to the parity bar (P rounded to fp16 is the only difference), the
+    LoRA weight gradients bit for bit; unsplit (M 512) and split (M 1024) dW."""
+    from palettize_hip import _lib
+    logits, pal = _soft_case(N, K, seed=M + 3 * N)
+    logits, pal = logits.to(dev), pal.to(dev)
+    tau = 0.5
+    if philox:
+        noise = ops.PhiloxNoise(seed=31, offset=7 * M)
+        grp = ops.SoftBuildGroup([(logits, ops.PhiloxNoise(31, 0), pal)], _lib.PLZ_W_HARD_NOISY,
+                                 want_probs=True)
+        grp.run(tau, 7 * M)
+        z = ops.gumbel_philox((N, K, 4), seed=31, offset=7 * M, device=dev)
+    else:
+        noise = ops.gumbel_philox((N, K, 4), seed=5, offset=0, device=dev)
+        grp = ops.SoftBuildGroup([(logits, noise, pal)], _lib.PLZ_W_HARD_NOISY, want_probs=True)
+        grp.run(tau)
+        z = noise
+    probs = grp.probs[0]
+    a_ = (f32(logits).astype(np.float64) + f32(z)) / tau
+    e = np.exp(a_ - a_.max(-1, keepdims=True))
+    want_p = e / e.sum(-1, keepdims=True)
+    assert np.all(np.abs(f32(probs) - want_p) <= 2.0 ** -10 * want_p + 2.0 ** -24)
+    x = randn_bf16(M, K, seed=11).to(dev)
+    gy = randn_bf16(M, N, seed=12).to(dev)
+    a = randn_bf16(16, K, seed=13, std=0.01).to(dev)
+    b = randn_bf16(N, 16, seed=14, std=0.01).to(dev)
+    gl, gp, ga, gb = ops.soft_bwd_lora(x, gy, logits, noise, pal, tau, a, b, 1.0)
+    gl2, gp2, ga2, gb2 = ops.soft_bwd_lora(x, gy, logits, noise, pal, tau, a, b, 1.0,
+                                           probs=probs)
+    assert torch.equal(ga, ga2) and torch.equal(gb, gb2)
+    assert_close(f32(gl2), f32(gl).astype(np.float64), what="grad_logits from saved P")
+    assert_close(f32(gp2), f32(gp).astype(np.float64), what="grad_palette from saved P")

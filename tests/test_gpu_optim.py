@@ -87,9 +87,9 @@ def test_fused_adamw_takes_the_producers_squared_sums(dev):
 
 @pytest.mark.parametrize("N,K", [(3, 256), (40, 768), (9, 2560)])
 def test_step_build_matches_a_separate_build(dev, N, K):
-    """FusedAdamW.step(build=NextBuild(...)): the soft weight written by the update pass, for
-    logits whose element count is or is not a multiple of the update's 8192-element blocks, with
-    a palette updated in the same step and a non-zero noise counter base, equals the batched
+    """FusedAdamW.step(build=NextBuild(...)): the soft weight and P written by the update pass,
+    for logits whose element count is or is not a multiple of the update's 8192-element blocks,
+    with a palette updated in the same step and a non-zero noise counter base, equal the batched
     build of the updated logits (plz_soft_build_w_batched_philox) bit for bit; the parameters
     equal those of the same step without the build."""
     ops = pytest.importorskip("palettize_hip.ops")
@@ -110,13 +110,17 @@ def test_step_build_matches_a_separate_build(dev, N, K):
                                  "clamp": (-3.0, 3.0)}])
         lg.grad, pal.grad = glog.to(dev), gpal.to(dev)
         w = torch.zeros(N, K, dtype=torch.bfloat16, device=dev)
-        nb = optim.NextBuild([(lg, pal, w, seed, counter)], offset, tau) if with_build else None
+        pr = torch.zeros(N, K, 4, dtype=torch.float16, device=dev)
+        nb = (optim.NextBuild([(lg, pal, w, seed, counter, pr)], offset, tau) if with_build
+              else None)
         opt.step(max_norms=(1.0, 0.3), build=nb)
         if with_build:
             assert nb.built == {id(lg)}
-        outs.append((lg.detach().clone(), pal.detach().clone(), w))
-    (lg_a, pal_a, _), (lg_b, pal_b, w_b) = outs
+        outs.append((lg.detach().clone(), pal.detach().clone(), w, pr))
+    (lg_a, pal_a, _, _), (lg_b, pal_b, w_b, pr_b) = outs
     assert torch.equal(lg_a.view(torch.int16), lg_b.view(torch.int16)) and torch.equal(pal_a, pal_b)
-    grp = ops.SoftBuildGroup([(lg_b, ops.PhiloxNoise(seed, 0), pal_b)], _lib.PLZ_W_HARD_NOISY)
+    grp = ops.SoftBuildGroup([(lg_b, ops.PhiloxNoise(seed, 0), pal_b)], _lib.PLZ_W_HARD_NOISY,
+                             want_probs=True)
     (w_ref, _), = grp.run(tau, offset + counter)
     assert torch.equal(w_b.view(torch.int16), w_ref.view(torch.int16))
+    assert torch.equal(pr_b.view(torch.int16), grp.probs[0].view(torch.int16))
