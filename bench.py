@@ -194,7 +194,9 @@ def bench_gemv(device, reps=20):
 
 def bench_soft(device, reps=5):
     """Config 4: soft (Gumbel-softmax) fwd + bwd on the gate shape 2560 -> 9728 at M=16384;
-    logits bf16 [N, K, 4] ~ N(0,1), Philox noise fp32 passed in, tau in {2.0, 0.5, 0.1}."""
+    logits bf16 [N, K, 4] ~ N(0,1), Philox noise fp32 passed in, tau in {2.0, 0.5, 0.1}. The
+    build keeps P (fp16) and the backward reads it, as the reference's forward saves P_aos
+    for its backward (fused_lut_linear_cuda.py:903-905, 919, 952-959)."""
     import torch
     from palettize_hip import ops
     K, N = 2560, 9728
@@ -204,6 +206,7 @@ def bench_soft(device, reps=5):
     pal = torch.sort(torch.randn(N, K // 256, 4, generator=g, device=device) * 0.02, -1).values.contiguous()
     x = torch.randn(M_TRAIN, K, generator=g, device=device).to(torch.bfloat16)
     gy = torch.randn(M_TRAIN, N, generator=g, device=device).to(torch.bfloat16)
+    probs = torch.empty((N, K, 4), dtype=torch.float16, device=device)
     out = {}
     ev = lambda: torch.cuda.Event(enable_timing=True)
     for tau in (2.0, 0.5, 0.1):
@@ -211,13 +214,13 @@ def bench_soft(device, reps=5):
         for rep in range(reps + 1):
             e = [ev() for _ in range(5)]
             e[0].record()
-            w, _ = ops.soft_build_w(logits, noise, pal, tau)
+            w, _ = ops.soft_build_w(logits, noise, pal, tau, probs=probs)
             e[1].record()
             ops.linear_fwd_dense(x, w)
             e[2].record()
             ops.linear_bwd_x_dense(gy, w)
             e[3].record()
-            ops.soft_bwd(x, gy, logits, noise, pal, tau)
+            ops.soft_bwd(x, gy, logits, noise, pal, tau, probs=probs)
             e[4].record()
             torch.cuda.synchronize()
             if rep:
@@ -225,7 +228,7 @@ def bench_soft(device, reps=5):
                     times[k] += e[i].elapsed_time(e[i + 1]) / reps
         tot = sum(times.values())
         flop = 6.0 * M_TRAIN * K * N
-        bw_bytes = 26.0 * N * K  # build-W: 8 B logits + 16 B noise in, 2 B W out per weight
+        bw_bytes = 34.0 * N * K  # build-W: 8 B logits + 16 B noise in, 2 B W + 8 B P out per weight
         out[f"tau{tau}"] = dict(ms=round(tot, 3), tflops=round(flop / (tot * 1e-3) / 1e12, 1),
                                 build_w_gbs=round(bw_bytes / (times["build_w"] * 1e-3) / 1e9, 1),
                                 **{f"{k}_ms": round(v, 3) for k, v in times.items()})

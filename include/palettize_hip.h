@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define PLZ_ABI_VERSION 17
+#define PLZ_ABI_VERSION 18
 
 /* status codes */
 #define PLZ_OK 0
@@ -224,18 +224,22 @@ int plz_soft_pw_ref_batched(const plz_pw_ref_desc* descs_device, int n, int64_t 
  *   P_c = softmax_c((logit_c + noise_c) / tau)
  *   w   bf16 [N, K]  per mode (PLZ_W_SOFT / PLZ_W_HARD_NOISY / PLZ_W_HARD_PLAIN)
  *   w_soft bf16 [N, K] = sum_c P_c pal_c (optional, may be null)
+ *   p_out fp16 [N, K, 4] = P (optional, may be null; 16-byte aligned): what the reference's
+ *         forward saves as P_aos for its backward (fused_lut_linear_cuda.py:903-905, 919);
+ *         plz_soft_bwd_probs reads it
  * Replaces compute_P_W_hard_aos_kernel (fused_lut_kernel.cu:1946-2004) and
  * compute_P_W_ste_kernel (triton_soft_forward.py:83-181). */
 int plz_soft_build_w(const uint16_t* logits, int logits_dtype, const float* noise,
                      const float* palette, float tau, int mode, uint16_t* w, uint16_t* w_soft,
-                     int64_t N, int64_t K, void* stream);
+                     uint16_t* p_out, int64_t N, int64_t K, void* stream);
 /* The same with the noise drawn in the kernel: element (n, k, c) = the value
  * plz_gumbel_philox(seed, offset) stores there (Philox counter offset + n*K + k), so no noise
  * tensor is written or read. Replaces the in-kernel sampling of
  * compute_P_W_hard_aos_kernel (fused_lut_kernel.cu:1946-2004) with this build's Philox. */
 int plz_soft_build_w_philox(const uint16_t* logits, int logits_dtype, uint64_t seed,
                             uint64_t offset, const float* palette, float tau, int mode,
-                            uint16_t* w, uint16_t* w_soft, int64_t N, int64_t K, void* stream);
+                            uint16_t* w, uint16_t* w_soft, uint16_t* p_out, int64_t N, int64_t K,
+                            void* stream);
 
 /* Batched build W: the linears of a layer (or of several) in one launch, each with its own
  * logits, palette and outputs and either its own noise tensor or its own Philox key; the same
@@ -294,6 +298,17 @@ int plz_soft_bwd_philox(const uint16_t* x, const uint16_t* grad_y, const uint16_
                         float tau, int scale_grad_by_inv_tau, uint16_t* grad_logits,
                         float* grad_palette, void* workspace, size_t workspace_bytes, int64_t M,
                         int64_t N, int64_t K, void* stream);
+/* The soft backward from the forward's P (p_out of a build: fp16 [N, K, 4], 16-byte aligned)
+ * instead of logits and noise, as the reference's backward reads its saved P_aos with grad_W
+ * (fused_lut_linear_cuda.py:952-959, soft_bwd_elementwise_aos_kernel fused_lut_kernel.cu:
+ * 1877-1924): grad_logits (grad_logits_dtype, PLZ_DT_BF16 or PLZ_DT_FP16) and grad_palette as
+ * plz_soft_bwd with that P, pal_c - sum_d P_d pal_d formed as sum_d P_d (pal_c - pal_d) so that
+ * the rounding of P does not cancel; same workspace as plz_soft_bwd. */
+int plz_soft_bwd_probs(const uint16_t* x, const uint16_t* grad_y, const uint16_t* probs,
+                       const float* palette, float tau, int scale_grad_by_inv_tau,
+                       uint16_t* grad_logits, int grad_logits_dtype, float* grad_palette,
+                       void* workspace, size_t workspace_bytes, int64_t M, int64_t N, int64_t K,
+                       void* stream);
 /* The soft backward (noise == NULL: the Philox noise of seed and offset, as
  * plz_soft_bwd_philox) plus both LoRA weight gradients from the same dW tiles, as
  * plz_lut_linear_bwd_palette_lora computes them for the hard path: grad_a [rank, K] =

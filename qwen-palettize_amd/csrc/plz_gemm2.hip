@@ -1976,7 +1976,8 @@ static int soft_bwd(const uint16_t* x, const uint16_t* grad_y, const uint16_t* l
               "plz_soft_bwd: logits dtype must be bf16 or fp16");
   PLZ_REQUIRE(tau > 0.f, "plz_soft_bwd: tau must be positive");
   if (N == 0 || K == 0) return PLZ_OK;
-  PLZ_REQUIRE(logits && palette && grad_logits && grad_palette && (gen || noise || probs),
+  PLZ_REQUIRE((logits || probs) && palette && grad_logits && grad_palette &&
+                  (gen || noise || probs),
               "plz_soft_bwd: null pointer");
   if (M == 0) {  // empty reduction: every gradient is zero
     zero_async(grad_logits, (size_t)N * K * 4 * 2, (hipStream_t)stream);
@@ -2054,6 +2055,17 @@ int plz_soft_bwd(const uint16_t* x, const uint16_t* grad_y, const uint16_t* logi
   return soft_bwd(x, grad_y, logits, logits_dtype, false, noise, 0, 0, palette, tau,
                   scale_grad_by_inv_tau, grad_logits, grad_palette, workspace, workspace_bytes, M,
                   N, K, stream);
+}
+
+int plz_soft_bwd_probs(const uint16_t* x, const uint16_t* grad_y, const uint16_t* probs,
+                       const float* palette, float tau, int scale_grad_by_inv_tau,
+                       uint16_t* grad_logits, int grad_logits_dtype, float* grad_palette,
+                       void* workspace, size_t workspace_bytes, int64_t M, int64_t N, int64_t K,
+                       void* stream) {
+  PLZ_REQUIRE(N == 0 || K == 0 || probs, "plz_soft_bwd_probs: null probs");
+  return soft_bwd(x, grad_y, nullptr, grad_logits_dtype, false, nullptr, 0, 0, palette, tau,
+                  scale_grad_by_inv_tau, grad_logits, grad_palette, workspace, workspace_bytes, M,
+                  N, K, stream, WgradArgs(), nullptr, probs);
 }
 
 size_t plz_soft_bwd_lora_workspace(int64_t M, int64_t N, int64_t K, int rank) {

@@ -182,11 +182,11 @@ template <bool GEN>
 __global__ void build_w_kernel(const uint16_t* __restrict__ logits, int f16,
                                const float* __restrict__ noise, uint64_t seed, uint64_t offset,
                                const float* __restrict__ pal, float inv_tau, int mode,
-                               uint16_t* __restrict__ w, uint16_t* __restrict__ w_soft, int64_t N,
-                               int64_t K) {
+                               uint16_t* __restrict__ w, uint16_t* __restrict__ w_soft,
+                               uint16_t* __restrict__ p_out, int64_t N, int64_t K) {
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= N * (K / 2)) return;
-  build_w_pair<GEN>(logits, f16, noise, seed, offset, pal, inv_tau, mode, w, w_soft, K, t);
+  build_w_pair<GEN>(logits, f16, noise, seed, offset, pal, inv_tau, mode, w, w_soft, K, t, p_out);
 }
 
 // Many linears in one launch (fused_lut_kernel.cu:2071-2211 batches the per-layer build the
@@ -297,8 +297,8 @@ int plz_soft_pw_ref_batched(const plz_pw_ref_desc* descs_device, int n, int64_t 
 
 static int build_w(const uint16_t* logits, int logits_dtype, bool gen, const float* noise,
                    uint64_t seed, uint64_t offset, const float* palette, float tau, int mode,
-                   uint16_t* w, uint16_t* w_soft, int64_t N, int64_t K, void* stream,
-                   const char* what) {
+                   uint16_t* w, uint16_t* w_soft, uint16_t* p_out, int64_t N, int64_t K,
+                   void* stream, const char* what) {
   PLZ_REQUIRE(N >= 0 && K >= 0, "%s: negative shape", what);
   PLZ_REQUIRE(K % 256 == 0, "%s: K (%lld) must be a multiple of 256", what, (long long)K);
   PLZ_REQUIRE(logits_dtype == PLZ_DT_BF16 || logits_dtype == PLZ_DT_FP16,
@@ -309,33 +309,34 @@ static int build_w(const uint16_t* logits, int logits_dtype, bool gen, const flo
   if (N == 0 || K == 0) return PLZ_OK;
   PLZ_REQUIRE(logits && palette && w && (gen || noise), "%s: null pointer", what);
   PLZ_REQUIRE((((uintptr_t)logits | (uintptr_t)noise | (uintptr_t)palette) & 15) == 0 &&
-                  (((uintptr_t)w | (uintptr_t)w_soft) & 3) == 0,
+                  (((uintptr_t)w | (uintptr_t)w_soft) & 3) == 0 && ((uintptr_t)p_out & 15) == 0,
               "%s: misaligned pointer", what);
   const int64_t n = N * K / 2;
   const dim3 grid((unsigned)((n + 255) / 256));
   const int f16 = logits_dtype == PLZ_DT_FP16 ? 1 : 0;
   if (gen)
     hipLaunchKernelGGL(build_w_kernel<true>, grid, dim3(256), 0, (hipStream_t)stream, logits, f16,
-                       nullptr, seed, offset, palette, 1.f / tau, mode, w, w_soft, N, K);
+                       nullptr, seed, offset, palette, 1.f / tau, mode, w, w_soft, p_out, N, K);
   else
     hipLaunchKernelGGL(build_w_kernel<false>, grid, dim3(256), 0, (hipStream_t)stream, logits,
                        f16, noise, (uint64_t)0, (uint64_t)0, palette, 1.f / tau, mode, w, w_soft,
-                       N, K);
+                       p_out, N, K);
   return check_launch(what);
 }
 
 int plz_soft_build_w(const uint16_t* logits, int logits_dtype, const float* noise,
                      const float* palette, float tau, int mode, uint16_t* w, uint16_t* w_soft,
-                     int64_t N, int64_t K, void* stream) {
-  return build_w(logits, logits_dtype, false, noise, 0, 0, palette, tau, mode, w, w_soft, N, K,
-                 stream, "plz_soft_build_w");
+                     uint16_t* p_out, int64_t N, int64_t K, void* stream) {
+  return build_w(logits, logits_dtype, false, noise, 0, 0, palette, tau, mode, w, w_soft, p_out,
+                 N, K, stream, "plz_soft_build_w");
 }
 
 int plz_soft_build_w_philox(const uint16_t* logits, int logits_dtype, uint64_t seed,
                             uint64_t offset, const float* palette, float tau, int mode,
-                            uint16_t* w, uint16_t* w_soft, int64_t N, int64_t K, void* stream) {
+                            uint16_t* w, uint16_t* w_soft, uint16_t* p_out, int64_t N, int64_t K,
+                            void* stream) {
   return build_w(logits, logits_dtype, true, nullptr, seed, offset, palette, tau, mode, w, w_soft,
-                 N, K, stream, "plz_soft_build_w_philox");
+                 p_out, N, K, stream, "plz_soft_build_w_philox");
 }
 
 int64_t plz_build_w_plan(plz_build_w_desc* descs, int n) {

@@ -84,14 +84,15 @@ SIGNATURES: dict[str, tuple] = {
     "plz_gumbel_lcg_triton": (i32, [p, u32, i64, i64, p]),
     "plz_pw_ref_plan": (i64, [C.POINTER(PwRefDesc), i32, i64]),
     "plz_soft_pw_ref_batched": (i32, [p, i32, i64, i64, f32, u32, p]),
-    "plz_soft_build_w": (i32, [p, i32, p, p, f32, i32, p, p, i64, i64, p]),
-    "plz_soft_build_w_philox": (i32, [p, i32, u64, u64, p, f32, i32, p, p, i64, i64, p]),
+    "plz_soft_build_w": (i32, [p, i32, p, p, f32, i32, p, p, p, i64, i64, p]),
+    "plz_soft_build_w_philox": (i32, [p, i32, u64, u64, p, f32, i32, p, p, p, i64, i64, p]),
     "plz_build_w_plan": (i64, [C.POINTER(BuildWDesc), i32]),
     "plz_soft_build_w_batched": (i32, [p, i32, i64, f32, i32, p]),
     "plz_soft_build_w_batched_philox": (i32, [p, i32, i64, u64, f32, i32, p]),
     "plz_soft_bwd_workspace": (sz, [i64, i64, i64]),
     "plz_soft_bwd": (i32, [p, p, p, i32, p, p, f32, i32, p, p, p, sz, i64, i64, i64, p]),
     "plz_soft_bwd_philox": (i32, [p, p, p, i32, u64, u64, p, f32, i32, p, p, p, sz, i64, i64, i64, p]),
+    "plz_soft_bwd_probs": (i32, [p, p, p, p, f32, i32, p, i32, p, p, sz, i64, i64, i64, p]),
     "plz_soft_bwd_lora_workspace": (sz, [i64, i64, i64, i32]),
     "plz_soft_bwd_lora": (i32, [p, p, p, i32, p, u64, u64, p, p, f32, i32, p, p, i32, f32, p, p, p,
                                 p, i32, p, p, sz, i64, i64, i64, p]),

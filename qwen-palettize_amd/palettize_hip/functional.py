@@ -95,7 +95,9 @@ class SoftLUTLinearFunction(torch.autograd.Function):
     ``buf`` (fp32 [N * K / 128]) and ``writes``, has the backward's fused soft dW also write the
     squared-gradient sums of the logits there (ops.soft_bwd_lora grad_sq) and count the write
     (None: not), and a fourth, the forward's P (fp16 [N, K, 4], the group's ``probs``), has it
-    read P instead of drawing the noise again."""
+    read P instead of drawing the noise again. Without ``prebuilt`` the forward builds w and P
+    itself and keeps P for the backward, as the reference's forward keeps its fp16 P_aos
+    (fused_lut_linear_cuda.py:903-905, 919); the noise is not kept."""
 
     @staticmethod
     def forward(ctx, x, palette, logits, noise, tau, bias, lora_a, lora_b, lora_scale, mode,
@@ -105,7 +107,9 @@ class SoftLUTLinearFunction(torch.autograd.Function):
         ctx.guard = None
         ctx.grad_sq = ctx.probs = None
         if prebuilt is None:
-            w, _ = ops.soft_build_w(logits, noise, palette, tau, mode)
+            ctx.probs = torch.empty((*logits.shape[:2], 4), dtype=torch.float16,
+                                    device=logits.device)
+            w, _ = ops.soft_build_w(logits, noise, palette, tau, mode, probs=ctx.probs)
         else:
             w, group = prebuilt[:2]
             ctx.guard = (group, group.generation)
@@ -113,9 +117,11 @@ class SoftLUTLinearFunction(torch.autograd.Function):
             ctx.probs = prebuilt[3] if len(prebuilt) > 3 else None
         t = ops.lora_project(x, lora_a, lora_scale) if lora_a is not None else None
         y = ops.linear_fwd_dense(x, w, bias, t, lora_b)
-        # a Philox noise descriptor is redrawn in the backward's epilogue, not stored
+        # a Philox noise descriptor is redrawn in the backward's epilogue, not stored; with the
+        # forward's P kept, no noise is needed at all
         ctx.philox = noise if isinstance(noise, ops.PhiloxNoise) else None
-        ctx.save_for_backward(x, palette, logits, None if ctx.philox else noise, w, lora_a, lora_b,
+        keep_noise = ctx.philox is None and ctx.probs is None
+        ctx.save_for_backward(x, palette, logits, noise if keep_noise else None, w, lora_a, lora_b,
                               t)
         ctx.tau = float(tau)
         ctx.lora_scale = float(lora_scale)
@@ -130,7 +136,7 @@ class SoftLUTLinearFunction(torch.autograd.Function):
         if ctx.guard is not None and ctx.guard[0].generation != ctx.guard[1]:
             raise RuntimeError("the prebuilt soft weight of this forward was rebuilt by a later "
                                "forward before this backward ran")
-        if ctx.philox is not None:
+        if ctx.philox is not None and ctx.probs is None:
             noise = ctx.philox
         gy = gy.contiguous()
         need = ctx.needs_input_grad
@@ -158,7 +164,7 @@ class SoftLUTLinearFunction(torch.autograd.Function):
                 sq.writes += 1
         elif need_soft:
             grad_logits, grad_pal = ops.soft_bwd(x, gy, logits, noise, palette, ctx.tau,
-                                                 ctx.scale_by_inv_tau)
+                                                 ctx.scale_by_inv_tau, probs=ctx.probs)
         grad_bias = ops.bias_grad(gy).to(ctx.bias_dtype) if (ctx.has_bias and need_b) else None
         if need_lora and not fused:
             grad_a, grad_b = ops.lora_weight_grads(x, gy, t, gt, 1.0, out_dtype=lora_a.dtype)

@@ -414,13 +414,17 @@ class PhiloxNoise:
         return gumbel_philox((N, K, 4), seed=self.seed, offset=self.offset, device=device)
 
 
-def _soft_shapes(logits, noise, palette):
+def _soft_shapes(logits, noise, palette, probs=None):
+    """noise may be None only where the forward's P (probs) replaces it."""
     if logits.dtype not in (torch.bfloat16, torch.float16):
         raise TypeError("logits must be bf16 or fp16")
     _need(logits, "logits", None, 3)
     _need(palette, "palette", torch.float32, 3)
     N, K, four = logits.shape
-    if not isinstance(noise, PhiloxNoise):
+    if noise is None:
+        if probs is None:
+            raise ValueError("noise is needed unless the forward's P (probs) is given")
+    elif not isinstance(noise, PhiloxNoise):
         _need(noise, "noise", torch.float32, 3)
         if tuple(noise.shape) != (N, K, 4):
             raise ValueError("logits [N,K,4], noise [N,K,4], palette [N,K/256,4] expected")
@@ -430,16 +434,23 @@ def _soft_shapes(logits, noise, palette):
 
 
 def soft_build_w(logits, noise, palette, tau: float, mode: int = _lib.PLZ_W_HARD_NOISY,
-                 want_soft: bool = False):
+                 want_soft: bool = False, probs=None):
+    """(w, w_soft or None). probs (optional fp16 [N, K, 4]) also receives
+    P = softmax((logits + noise) / tau), which soft_bwd(probs=...) reads in the backward."""
     N, K = _soft_shapes(logits, noise, palette)
+    if probs is not None:
+        _need(probs, "probs", torch.float16, 3)
+        if tuple(probs.shape) != (N, K, 4):
+            raise ValueError(f"probs must be [N, K, 4] = [{N}, {K}, 4]")
     w = torch.empty((N, K), dtype=torch.bfloat16, device=logits.device)
     ws = torch.empty((N, K), dtype=torch.bfloat16, device=logits.device) if want_soft else None
     if isinstance(noise, PhiloxNoise):
         call("plz_soft_build_w_philox", _ptr(logits), _DT[logits.dtype], noise.seed, noise.offset,
-             _ptr(palette), float(tau), int(mode), _ptr(w), _ptr(ws), N, K, _stream(logits))
+             _ptr(palette), float(tau), int(mode), _ptr(w), _ptr(ws), _ptr(probs), N, K,
+             _stream(logits))
     else:
         call("plz_soft_build_w", _ptr(logits), _DT[logits.dtype], _ptr(noise), _ptr(palette),
-             float(tau), int(mode), _ptr(w), _ptr(ws), N, K, _stream(logits))
+             float(tau), int(mode), _ptr(w), _ptr(ws), _ptr(probs), N, K, _stream(logits))
     return w, ws
 
 
@@ -496,8 +507,13 @@ class SoftBuildGroup:
         return self.outputs
 
 
-def soft_bwd(x, grad_y, logits, noise, palette, tau: float, scale_by_inv_tau: bool = False):
-    N, K = _soft_shapes(logits, noise, palette)
+def soft_bwd(x, grad_y, logits, noise, palette, tau: float, scale_by_inv_tau: bool = False,
+             probs=None):
+    """(grad_logits, grad_palette). probs (optional fp16 [N, K, 4], the forward's P from
+    soft_build_w(probs=...)) is read instead of logits and noise (plz_soft_bwd_probs), as the
+    reference's backward reads its saved P_aos; logits and noise then give only the shapes and
+    the gradient's dtype (noise may then be None)."""
+    N, K = _soft_shapes(logits, noise, palette, probs)
     _need(x, "x", torch.bfloat16, 2)
     _need(grad_y, "grad_y", torch.bfloat16, 2)
     M = x.shape[0]
@@ -506,7 +522,14 @@ def soft_bwd(x, grad_y, logits, noise, palette, tau: float, scale_by_inv_tau: bo
     gl = torch.empty_like(logits)
     gp = torch.empty((N, K // 256, 4), dtype=torch.float32, device=x.device)
     ws = _workspace(query("plz_soft_bwd_workspace", M, N, K), x.device)
-    if isinstance(noise, PhiloxNoise):
+    if probs is not None:
+        _need(probs, "probs", torch.float16, 3)
+        if tuple(probs.shape) != (N, K, 4):
+            raise ValueError(f"probs must be [N, K, 4] = [{N}, {K}, 4]")
+        call("plz_soft_bwd_probs", _ptr(x), _ptr(grad_y), _ptr(probs), _ptr(palette), float(tau),
+             int(bool(scale_by_inv_tau)), _ptr(gl), _DT[logits.dtype], _ptr(gp), _ptr(ws),
+             ws.numel(), M, N, K, _stream(x))
+    elif isinstance(noise, PhiloxNoise):
         call("plz_soft_bwd_philox", _ptr(x), _ptr(grad_y), _ptr(logits), _DT[logits.dtype],
              noise.seed, noise.offset, _ptr(palette), float(tau), int(bool(scale_by_inv_tau)),
              _ptr(gl), _ptr(gp), _ptr(ws), ws.numel(), M, N, K, _stream(x))
@@ -525,8 +548,9 @@ def soft_bwd_lora(x, grad_y, logits, noise, palette, tau: float, lora_a, lora_b,
     scale * dW lora_a^T (dW = grad_y^T x), which lora_weight_grads computes from t and gt.
     grad_sq (optional fp32 [N * K / 128]) receives the sum of squares of each 512 consecutive
     grad_logits values, for FusedAdamW.step(grad_sq=...). probs (optional fp16 [N, K, 4]): the
-    forward's P (SoftBuildGroup(want_probs=True)), read instead of redrawing the noise."""
-    N, K = _soft_shapes(logits, noise, palette)
+    forward's P (SoftBuildGroup(want_probs=True)), read instead of redrawing the noise (noise
+    may then be None)."""
+    N, K = _soft_shapes(logits, noise, palette, probs)
     if probs is not None:
         _need(probs, "probs", torch.float16, 3)
         if tuple(probs.shape) != (N, K, 4):

@@ -36,7 +36,7 @@ def test_every_declared_symbol_is_exported(lib):
         assert hasattr(lib, n), f"{n} declared in the header but not exported"
         assert n in _lib.SIGNATURES, f"{n} has no ctypes signature"
     assert set(_lib.SIGNATURES) == set(names)
-    assert lib.plz_abi_version() == 17
+    assert lib.plz_abi_version() == 18
 
 
 def test_shape_errors_are_reported_without_touching_the_gpu(lib):
@@ -48,7 +48,7 @@ def test_shape_errors_are_reported_without_touching_the_gpu(lib):
     assert rc == 1 and b"null" in lib.plz_last_error()
     rc = lib.plz_lut_gemv(None, None, None, None, 17, 8, 256, None)
     assert rc == 1 and b"[1, 16]" in lib.plz_last_error()
-    rc = lib.plz_soft_build_w(None, 0, None, None, 0.0, 0, None, None, 8, 256, None)
+    rc = lib.plz_soft_build_w(None, 0, None, None, 0.0, 0, None, None, None, 8, 256, None)
     assert rc == 1 and b"tau" in lib.plz_last_error()
     rc = lib.plz_rmsnorm_fwd(None, None, None, None, 4, 5000, 1e-6, None)
     assert rc == 1

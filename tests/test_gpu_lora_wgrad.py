@@ -132,7 +132,8 @@ def test_soft_bwd_lora_empty_reduction_gives_zeros(dev):
 @pytest.mark.parametrize("M,N,K", [(300, 1032, 768), (2048, 1024, 2560)])
 def test_soft_autograd_lora_weight_grads_ride_on_the_dw_gemm(dev, M, N, K):
     """soft_lut_linear with LoRA: the backward takes grad_A, grad_B from the soft dW GEMM
-    (plz_soft_bwd_lora); logits and palette gradients equal ops.soft_bwd's bit for bit."""
+    (plz_soft_bwd_lora); logits and palette gradients equal ops.soft_bwd's from the same P bit
+    for bit."""
     from palettize_hip import soft_lut_linear
     r, s, tau = 16, 2.0, 0.5
     logits, pal = _soft_case(N, K, seed=M)
@@ -148,7 +149,10 @@ def test_soft_autograd_lora_weight_grads_ride_on_the_dw_gemm(dev, M, N, K):
     wa, wb = O.lora_weight_grads(f32(x.detach()), f32(gy), f32(a.detach()), f32(b.detach()), s)
     assert_close(f32(a.grad), wa, what="grad_a")
     assert_close(f32(b.grad), wb, what="grad_b")
-    rl, rp = ops.soft_bwd(x.detach(), gy, logits.detach(), spec, pal.detach(), tau)
+    # the forward keeps its P (fp16) and the backward reads it: the same P built here
+    probs = torch.empty((N, K, 4), dtype=torch.float16, device=dev)
+    ops.soft_build_w(logits.detach(), spec, pal.detach(), tau, probs=probs)
+    rl, rp = ops.soft_bwd(x.detach(), gy, logits.detach(), None, pal.detach(), tau, probs=probs)
     assert torch.equal(logits.grad, rl) and torch.equal(pal.grad, rp)
     assert bool(torch.isfinite(x.grad.float()).all())
 
@@ -217,3 +221,41 @@ def test_soft_bwd_lora_from_saved_probs(dev, M, N, K, philox):
     assert torch.equal(ga, ga2) and torch.equal(gb, gb2)
     assert_close(f32(gl2), f32(gl).astype(np.float64), what="grad_logits from saved P")
     assert_close(f32(gp2), f32(gp).astype(np.float64), what="grad_palette from saved P")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,N,K", [(512, 256, 512), (1024, 128, 768)])
+@pytest.mark.parametrize("philox", [False, True])
+def test_soft_bwd_probs_from_the_single_build(dev, M, N, K, philox):
+    """The single-linear build's P (plz_soft_build_w(_philox) p_out) bit for bit the batched
+    build's, and plz_soft_bwd_probs (P in place of logits and noise, the reference's
+    grad_W + P_aos backward) bit for bit soft_bwd_lora(probs=...) in grad_logits and
+    grad_palette, for fp16 logits too; unsplit (M 512) and split (M 1024) dW. The batched
+    build's P and soft_bwd_lora(probs=...) are pinned against the fp64 softmax and the
+    recomputing backward in test_soft_bwd_lora_from_saved_probs."""
+    from palettize_hip import _lib
+    logits, pal = _soft_case(N, K, seed=M + 5 * N)
+    logits, pal = logits.to(dev), pal.to(dev)
+    tau = 0.5
+    for ldt in (torch.bfloat16, torch.float16):
+        lg = logits.to(ldt)
+        noise = (ops.PhiloxNoise(seed=17, offset=3 * N) if philox
+                 else ops.gumbel_philox((N, K, 4), seed=5, offset=0, device=dev))
+        p1 = torch.empty((N, K, 4), dtype=torch.float16, device=dev)
+        w1, _ = ops.soft_build_w(lg, noise, pal, tau, _lib.PLZ_W_HARD_NOISY, probs=p1)
+        if philox:
+            grp = ops.SoftBuildGroup([(lg, ops.PhiloxNoise(17, 0), pal)], _lib.PLZ_W_HARD_NOISY,
+                                     want_probs=True)
+            grp.run(tau, 3 * N)
+        else:
+            grp = ops.SoftBuildGroup([(lg, noise, pal)], _lib.PLZ_W_HARD_NOISY, want_probs=True)
+            grp.run(tau)
+        assert torch.equal(p1, grp.probs[0]) and torch.equal(w1, grp.outputs[0][0])
+        x = randn_bf16(M, K, seed=21).to(dev)
+        gy = randn_bf16(M, N, seed=22).to(dev)
+        a = randn_bf16(16, K, seed=23, std=0.01).to(dev)
+        b = randn_bf16(N, 16, seed=24, std=0.01).to(dev)
+        gl, gp, _, _ = ops.soft_bwd_lora(x, gy, lg, noise, pal, tau, a, b, 1.0, probs=p1)
+        gl2, gp2 = ops.soft_bwd(x, gy, lg, None, pal, tau, probs=p1)
+        assert gl2.dtype == ldt
+        assert torch.equal(gl, gl2) and torch.equal(gp, gp2)
