@@ -148,6 +148,17 @@ int plz_linear_fwd_dense(const uint16_t* x, const uint16_t* w, const uint16_t* b
                          const uint16_t* lora_t, const uint16_t* lora_b, int rank, uint16_t* y,
                          void* workspace, size_t workspace_bytes, int64_t M, int64_t N, int64_t K,
                          void* stream);
+/* plz_linear_fwd_dense with a residual: y = residual + (x w^T (+bias) (+lora)), the GEMM's
+ * output rounded to bf16 and the sum rounded again, as the separate bf16 add after it.
+ * residual bf16 [M, N] and y 16-byte aligned. Replaces the decoder layer's final residual add
+ * `hidden_states = residual + hidden_states` after the MLP's down projection (HF
+ * `modeling_qwen3.py` Qwen3DecoderLayer.forward, which the reference's layer runs via
+ * qwen_model.py:590) with the down GEMM's epilogue. */
+int plz_linear_fwd_dense_residual(const uint16_t* x, const uint16_t* w, const uint16_t* bias,
+                                  const uint16_t* lora_t, const uint16_t* lora_b, int rank,
+                                  const uint16_t* residual, uint16_t* y, void* workspace,
+                                  size_t workspace_bytes, int64_t M, int64_t N, int64_t K,
+                                  void* stream);
 size_t plz_linear_fwd_dense_workspace(int64_t M, int64_t N, int64_t K);
 /* Gate and up projections with the SwiGLU in the epilogue: h [M, N] = silu(x Wg^T) * (x Wu^T)
  * as the HF Qwen3 MLP computes it in bf16 (transformers modeling_qwen3.py:70-83; the gate and

@@ -77,6 +77,9 @@ struct Args {
   const uint16_t* a2; const uint16_t* b2; int R2;
   // epilogue
   void* c; int64_t ldc; const uint16_t* bias; float alpha; float* partial;
+  // EPI_BF16: bf16 [I, J] (row stride ldres) added to the stored bf16 values and rounded
+  // again, as a bf16 tensor add after the GEMM would (NULL: none)
+  const uint16_t* res; int64_t ldres;
   const uint16_t* logits; const float* noise; float inv_tau, glog_scale; uint16_t* grad_logits;
   uint64_t noise_seed, noise_offset;  // noise == nullptr: Philox at noise_offset + n*K + k
   int logits_f16;

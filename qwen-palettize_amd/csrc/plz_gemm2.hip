@@ -718,6 +718,18 @@ __device__ __forceinline__ void stage_tile_bf16(const Args& g, const f32x16 (&ac
       }
   __syncthreads();
 }
+// 8 stored bf16 values plus 8 bf16 residual values, each sum rounded to bf16: what a bf16 tensor
+// add of the residual to the GEMM's bf16 output computes
+__device__ __forceinline__ u32x4 add_residual8(u32x4 v, const uint16_t* r) {
+  const uint4 q = *reinterpret_cast<const uint4*>(r);
+  const uint32_t rs[4] = {q.x, q.y, q.z, q.w};
+  u32x4 o;
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    o[e] = f2bf2(bf2f(v[e] & 0xffffu) + bf2f(rs[e] & 0xffffu), bf2f(v[e] >> 16) + bf2f(rs[e] >> 16));
+  return o;
+}
+
 __device__ __forceinline__ void store_tile_bf16(const Args& g, const f32x16 (&acc)[WT_I][WT_J],
                                                 lds_u8* st, int64_t i0, int64_t j0, int wi,
                                                 int wj, int lane) {
@@ -729,7 +741,8 @@ __device__ __forceinline__ void store_tile_bf16(const Args& g, const f32x16 (&ac
     const int row = ch >> 5, c8 = (ch & 31) * 8;
     const int64_t i = i0 + row, j = j0 + c8;
     if (i < g.I && j < g.J) {
-      const u32x4 v = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(st + row * EPI_RS + c8 * 2);
+      u32x4 v = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(st + row * EPI_RS + c8 * 2);
+      if (g.res) v = add_residual8(v, g.res + i * g.ldres + j);
       // streaming store: the output is not read again by this launch, so it should not take
       // cache lines from the operands the other workgroups are still reading
       __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(C + i * g.ldc + j));
@@ -1345,10 +1358,11 @@ __global__ __launch_bounds__(TAIL_THREADS) void tail_reduce_kernel(const Args g)
     const int ch = it * TAIL_THREADS + threadIdx.x;  // 32 chunks of 8 columns per row
     const int row = ch >> 5, c8 = (ch & 31) * 8;
     const int64_t i = i0 + row, j = j0 + c8;
-    if (i < g.I && j < g.J)  // streaming store, as store_tile_bf16
-      __builtin_nontemporal_store(
-          *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(st + row * EPI_RS + c8 * 2),
-          reinterpret_cast<u32x4*>(C + i * g.ldc + j));
+    if (i < g.I && j < g.J) {  // streaming store, as store_tile_bf16
+      u32x4 v = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(st + row * EPI_RS + c8 * 2);
+      if (g.res) v = add_residual8(v, g.res + i * g.ldres + j);
+      __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(C + i * g.ldc + j));
+    }
   }
 }
 
@@ -1861,28 +1875,49 @@ size_t plz_linear_fwd_dense_workspace(int64_t M, int64_t N, int64_t K) {
   return M > 0 && N > 0 && K > 0 ? tail_bytes(M, N, K) : 0;
 }
 
-int plz_linear_fwd_dense(const uint16_t* x, const uint16_t* w, const uint16_t* bias,
-                         const uint16_t* lora_t, const uint16_t* lora_b, int rank, uint16_t* y,
-                         void* workspace, size_t workspace_bytes, int64_t M, int64_t N, int64_t K,
-                         void* stream) {
-  PLZ_REQUIRE(M >= 0 && N >= 0 && K >= 0, "plz_linear_fwd_dense: negative shape");
-  PLZ_REQUIRE(K % 8 == 0 && N % 8 == 0, "plz_linear_fwd_dense: K and N must be multiples of 8");
+static int linear_fwd_dense(const uint16_t* x, const uint16_t* w, const uint16_t* bias,
+                            const uint16_t* lora_t, const uint16_t* lora_b, int rank,
+                            const uint16_t* residual, uint16_t* y, void* workspace,
+                            size_t workspace_bytes, int64_t M, int64_t N, int64_t K, void* stream,
+                            const char* what) {
+  PLZ_REQUIRE(M >= 0 && N >= 0 && K >= 0, "%s: negative shape", what);
+  PLZ_REQUIRE(K % 8 == 0 && N % 8 == 0, "%s: K and N must be multiples of 8", what);
   PLZ_REQUIRE(rank >= 0 && rank <= BK && rank % 8 == 0,
-              "plz_linear_fwd_dense: rank (%d) must be a multiple of 8 in [0, 64]", rank);
+              "%s: rank (%d) must be a multiple of 8 in [0, 64]", what, rank);
   if (M == 0 || N == 0) return PLZ_OK;
   PLZ_REQUIRE(x && w && y && a16(x) && a16(w),
-              "plz_linear_fwd_dense: x, w, y must be non-null; x, w 16-byte aligned");
+              "%s: x, w, y must be non-null; x, w 16-byte aligned", what);
   PLZ_REQUIRE(rank == 0 || (lora_t && lora_b && a16(lora_t) && a16(lora_b)),
-              "plz_linear_fwd_dense: rank > 0 needs 16-byte aligned lora_t and lora_b");
+              "%s: rank > 0 needs 16-byte aligned lora_t and lora_b", what);
   Args g = {};
   g.a = x; g.lda = K; g.b = w; g.ldb = K;
   g.I = M; g.J = N; g.R = K;
   g.a2 = lora_t; g.b2 = lora_b; g.R2 = rank;
   g.c = y; g.ldc = N; g.bias = bias; g.alpha = 1.f;
+  g.res = residual; g.ldres = N;
   g.group = kDenseGroup;
-  const int rc = set_tail(g, workspace, workspace_bytes, "plz_linear_fwd_dense");
+  const int rc = set_tail(g, workspace, workspace_bytes, what);
   if (rc != PLZ_OK) return rc;
-  return launch<OP_ROW, OP_ROW, EPI_BF16>(g, 1, (hipStream_t)stream, "plz_linear_fwd_dense");
+  return launch<OP_ROW, OP_ROW, EPI_BF16>(g, 1, (hipStream_t)stream, what);
+}
+
+int plz_linear_fwd_dense(const uint16_t* x, const uint16_t* w, const uint16_t* bias,
+                         const uint16_t* lora_t, const uint16_t* lora_b, int rank, uint16_t* y,
+                         void* workspace, size_t workspace_bytes, int64_t M, int64_t N, int64_t K,
+                         void* stream) {
+  return linear_fwd_dense(x, w, bias, lora_t, lora_b, rank, nullptr, y, workspace,
+                          workspace_bytes, M, N, K, stream, "plz_linear_fwd_dense");
+}
+
+int plz_linear_fwd_dense_residual(const uint16_t* x, const uint16_t* w, const uint16_t* bias,
+                                  const uint16_t* lora_t, const uint16_t* lora_b, int rank,
+                                  const uint16_t* residual, uint16_t* y, void* workspace,
+                                  size_t workspace_bytes, int64_t M, int64_t N, int64_t K,
+                                  void* stream) {
+  PLZ_REQUIRE(M == 0 || N == 0 || (residual && a16(residual) && a16(y)),
+              "plz_linear_fwd_dense_residual: residual and y must be non-null, 16-byte aligned");
+  return linear_fwd_dense(x, w, bias, lora_t, lora_b, rank, residual, y, workspace,
+                          workspace_bytes, M, N, K, stream, "plz_linear_fwd_dense_residual");
 }
 
 int plz_linear_fwd_dense_swiglu(const uint16_t* x, const uint16_t* w_gate_up, uint16_t* h,

@@ -97,11 +97,13 @@ class SoftLUTLinearFunction(torch.autograd.Function):
     (None: not), and a fourth, the forward's P (fp16 [N, K, 4], the group's ``probs``), has it
     read P instead of drawing the noise again. Without ``prebuilt`` the forward builds w and P
     itself and keeps P for the backward, as the reference's forward keeps its fp16 P_aos
-    (fused_lut_linear_cuda.py:903-905, 919); the noise is not kept."""
+    (fused_lut_linear_cuda.py:903-905, 919); the noise is not kept. ``residual`` (optional,
+    bf16 [M, N]) is added to y in the GEMM's epilogue, as a separate bf16 add after it would
+    (its gradient is grad_y)."""
 
     @staticmethod
     def forward(ctx, x, palette, logits, noise, tau, bias, lora_a, lora_b, lora_scale, mode,
-                scale_by_inv_tau, prebuilt=None):
+                scale_by_inv_tau, prebuilt=None, residual=None):
         x = x.contiguous()
         lora_a, lora_b = _c(lora_a), _c(lora_b)
         ctx.guard = None
@@ -116,7 +118,8 @@ class SoftLUTLinearFunction(torch.autograd.Function):
             ctx.grad_sq = prebuilt[2] if len(prebuilt) > 2 else None
             ctx.probs = prebuilt[3] if len(prebuilt) > 3 else None
         t = ops.lora_project(x, lora_a, lora_scale) if lora_a is not None else None
-        y = ops.linear_fwd_dense(x, w, bias, t, lora_b)
+        y = ops.linear_fwd_dense(x, w, bias, t, lora_b,
+                                 residual=None if residual is None else residual.contiguous())
         # a Philox noise descriptor is redrawn in the backward's epilogue, not stored; with the
         # forward's P kept, no noise is needed at all
         ctx.philox = noise if isinstance(noise, ops.PhiloxNoise) else None
@@ -169,7 +172,8 @@ class SoftLUTLinearFunction(torch.autograd.Function):
         if need_lora and not fused:
             grad_a, grad_b = ops.lora_weight_grads(x, gy, t, gt, 1.0, out_dtype=lora_a.dtype)
         return (grad_x, grad_pal if need_pal else None, grad_logits if need_log else None, None,
-                None, grad_bias, grad_a, grad_b, None, None, None, None)
+                None, grad_bias, grad_a, grad_b, None, None, None, None,
+                gy if len(need) > 12 and need[12] else None)
 
 
 def soft_lut_linear(x, palette, logits, noise, tau, bias=None, lora_a=None, lora_b=None,

@@ -245,9 +245,11 @@ class SoftPalettizedLinear(nn.Module):
         self.noise_counter += NOISE_STRIDE
         return ops.PhiloxNoise(self.noise_seed, off)
 
-    def forward(self, x, prebuilt=None):
+    def forward(self, x, prebuilt=None, residual=None):
         """prebuilt: (w, group) from the layer's batched build of this forward (the noise
-        counter has then been advanced by the layer)."""
+        counter has then been advanced by the layer). residual (optional, bf16 [..., N]): added
+        to the output in the GEMM's epilogue (the layer's residual add after its down
+        projection)."""
         _gpu_bf16(x, "SoftPalettizedLinear input")
         lead = x.shape[:-1]
         if prebuilt is None:
@@ -256,9 +258,10 @@ class SoftPalettizedLinear(nn.Module):
             w, group, noise = prebuilt[:3]
             probs = prebuilt[3] if len(prebuilt) > 3 else None
             prebuilt = (w, group, self.grad_sq, probs)
+        res = None if residual is None else residual.reshape(-1, self.out_features)
         y = SoftLUTLinearFunction.apply(x.reshape(-1, x.shape[-1]), self.palette, self.index_logits,
                                         noise, self.tau, None, self.lora_a, self.lora_b,
-                                        self.lora_scale, self.mode, False, prebuilt)
+                                        self.lora_scale, self.mode, False, prebuilt, res)
         return y.reshape(*lead, self.out_features)
 
 
@@ -710,7 +713,8 @@ class PalettizedDecoderLayer(nn.Module):
             h = self.gate_up.forward_swiglu(x, pw["gate_up"])
         else:
             h = SwiGLUFunction.apply(self.gate_proj(x, pw["gate_proj"]), self.up_proj(x, pw["up_proj"]))
-        return hs + self.down_proj(h, pw["down_proj"])
+        # the residual add in the down GEMM's epilogue
+        return self.down_proj(h, pw["down_proj"], residual=hs)
 
 
 class DenseDecoderLayer(nn.Module):
@@ -760,7 +764,9 @@ class DenseDecoderLayer(nn.Module):
             h = h.view(B, S, -1)
         else:
             h = SwiGLUFunction.apply(lin(x, self.gate_proj), lin(x, self.up_proj))
-        return hs + lin(h, self.down_proj)
+        # the residual add in the down GEMM's epilogue
+        return ops.linear_fwd_dense(h.reshape(-1, h.shape[-1]).contiguous(), self.down_proj,
+                                    residual=hs.reshape(-1, cfg.hidden)).view(B, S, cfg.hidden)
 
 
 # ---- loss / schedule / optimizer ----------------------------------------------------------------

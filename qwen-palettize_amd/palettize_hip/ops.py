@@ -289,7 +289,10 @@ def linear_fwd_dense_swiglu_cat(x, w, lora_t=None, lora_b=None, keep_pre=True):
     return y, h
 
 
-def linear_fwd_dense(x, w, bias=None, lora_t=None, lora_b=None):
+def linear_fwd_dense(x, w, bias=None, lora_t=None, lora_b=None, residual=None):
+    """y = x w^T (+ bias) (+ lora_t lora_b^T); with residual (bf16 [M, N]) y = residual + that,
+    added in the GEMM's epilogue with the rounding of a separate bf16 add
+    (plz_linear_fwd_dense_residual)."""
     _need(x, "x", torch.bfloat16, 2)
     _need(w, "w", torch.bfloat16, 2)
     M, K = x.shape
@@ -300,6 +303,14 @@ def linear_fwd_dense(x, w, bias=None, lora_t=None, lora_b=None):
     rank = _lora_pair(lora_t, lora_b, "lora_t", "lora_b", M, N)
     y = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
     ws = _opt_workspace(query("plz_linear_fwd_dense_workspace", M, N, K), x.device)
+    if residual is not None:
+        _need(residual, "residual", torch.bfloat16, 2)
+        if tuple(residual.shape) != (M, N):
+            raise ValueError(f"residual must be [M, N] = [{M}, {N}]")
+        call("plz_linear_fwd_dense_residual", _ptr(x), _ptr(w), _ptr(bias), _ptr(lora_t),
+             _ptr(lora_b), rank, _ptr(residual), _ptr(y), _ptr(ws), _numel(ws), M, N, K,
+             _stream(x))
+        return y
     call("plz_linear_fwd_dense", _ptr(x), _ptr(w), _ptr(bias), _ptr(lora_t), _ptr(lora_b), rank,
          _ptr(y), _ptr(ws), _numel(ws), M, N, K, _stream(x))
     return y

@@ -48,6 +48,9 @@ def test_shape_errors_are_reported_without_touching_the_gpu(lib):
     assert rc == 1 and b"null" in lib.plz_last_error()
     rc = lib.plz_lut_gemv(None, None, None, None, 17, 8, 256, None)
     assert rc == 1 and b"[1, 16]" in lib.plz_last_error()
+    rc = lib.plz_linear_fwd_dense_residual(None, None, None, None, None, 0, None, None, None, 0,
+                                           8, 8, 8, None)
+    assert rc == 1 and b"residual" in lib.plz_last_error()
     rc = lib.plz_soft_build_w(None, 0, None, None, 0.0, 0, None, None, None, 8, 256, None)
     assert rc == 1 and b"tau" in lib.plz_last_error()
     rc = lib.plz_rmsnorm_fwd(None, None, None, None, 4, 5000, 1e-6, None)

@@ -126,6 +126,31 @@ def test_swiglu_concatenated_layout(dev):
         ops.swiglu_bwd_cat(gu.to(dev), gh[:, :-8].contiguous().to(dev))
 
 
+@pytest.mark.parametrize("M,N,K,r,bias", [(300, 1032, 768, 0, False), (2048, 1024, 512, 16, True),
+                                          (16384, 2560, 9728, 16, False), (4096, 2560, 2560, 0, True)])
+def test_dense_gemm_with_residual_epilogue(dev, M, N, K, r, bias):
+    """plz_linear_fwd_dense_residual: y = residual + x W^T (+ bias) (+ LoRA) bit for bit the
+    dense GEMM followed by a bf16 tensor add, on whole tiles, a ragged edge and the split
+    last-wave tiles (the layer's down shape); rows of y never written stay untouched."""
+    x = randn_bf16(M, K, seed=31).to(dev)
+    w = (randn_bf16(N, K, seed=32).float() * 0.02).to(torch.bfloat16).to(dev)
+    res = randn_bf16(M, N, seed=33).to(dev)
+    b = randn_bf16(N, 1, seed=34).reshape(N).to(dev) if bias else None
+    t = randn_bf16(M, r, seed=35).to(dev) if r else None
+    lb = randn_bf16(N, r, seed=36, std=0.01).to(dev) if r else None
+    y = ops.linear_fwd_dense(x, w, b, t, lb, residual=res)
+    want = ops.linear_fwd_dense(x, w, b, t, lb) + res
+    assert torch.equal(y, want)
+    # the residual may alias nothing else but may be any bf16 values, inf and nan included
+    res2 = res.clone()
+    res2[0, :8] = torch.tensor([float("inf"), float("-inf"), float("nan"), 0.0, -0.0, 1e30,
+                                -1e-30, 3.0], dtype=torch.bfloat16)
+    y2 = ops.linear_fwd_dense(x, w, b, t, lb, residual=res2)
+    want2 = ops.linear_fwd_dense(x, w, b, t, lb) + res2
+    assert torch.equal(y2.isnan(), want2.isnan())
+    assert torch.equal(torch.nan_to_num(y2), torch.nan_to_num(want2))
+
+
 @pytest.mark.parametrize("M,F,K,r", [(300, 384, 512, 32), (64, 128, 2560, 16),
                                      (2048, 9728, 2560, 32), (513, 640, 264, 0)])
 def test_gate_up_gemm_with_swiglu_epilogue(dev, M, F, K, r):
