@@ -43,7 +43,7 @@ PEAK_HBM_GBS = 8000.0
 # commands and algorithmic bytes in profiles/lut_gemm_traffic_m16384.txt).
 # fwd counts its dequant_kernel launch too (from 4096 rows it dequantises W and runs the dense
 # GEMM; grad_x runs on the same W); grad_palette includes the LoRA weight-gradient partials.
-GEMM_TRAFFIC_BYTES = {"fwd": 1005.4e6, "grad_x": 959.2e6, "grad_palette": 910.0e6}
+GEMM_TRAFFIC_BYTES = {"fwd": 1009.1e6, "grad_x": 962.8e6, "grad_palette": 905.7e6}
 KERNEL_NAMES = {"fwd": "dequant_kernel + gemm2_kernel<OP_ROW, OP_ROW, EPI_BF16> (fwd)",
                 "grad_x": "gemm2_kernel<OP_ROW, OP_COL, EPI_BF16> (grad_x on the forward's W)",
                 "grad_palette": "gemm2_kernel<OP_COL, OP_COL, EPI_PAL> (grad_palette + LoRA "
