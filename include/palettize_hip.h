@@ -186,6 +186,17 @@ int plz_linear_bwd_x_dense(const uint16_t* grad_y, const uint16_t* w, const uint
                            const uint16_t* lora_a, int rank, uint16_t* grad_x, void* workspace,
                            size_t workspace_bytes, int64_t M, int64_t N, int64_t K,
                            void* stream);
+/* plz_linear_bwd_x_dense followed by the SwiGLU backward in its epilogue: with gate_up
+ * [M, 2K] = [gate | up] the pre-activations of h = silu(gate) * up (K = the SwiGLU's width),
+ * grad_h = grad_y w (+ lora) is rounded to bf16 and grad_gate_up [M, 2K] = [grad_gate | grad_up]
+ * written from it, bit for bit plz_linear_bwd_x_dense then plz_swiglu_bwd_rows; grad_h itself
+ * is not stored. Replaces the down projection's grad_x matmul and the autograd of HF Qwen3MLP's
+ * act_fn(gate_proj(x)) * up_proj(x) (modeling_qwen3.py, via qwen_model.py:590) behind it. */
+int plz_linear_bwd_x_dense_swiglu(const uint16_t* grad_y, const uint16_t* w,
+                                  const uint16_t* lora_gt, const uint16_t* lora_a, int rank,
+                                  const uint16_t* gate_up, uint16_t* grad_gate_up, void* workspace,
+                                  size_t workspace_bytes, int64_t M, int64_t N, int64_t K,
+                                  void* stream);
 size_t plz_linear_bwd_x_dense_workspace(int64_t M, int64_t N, int64_t K);
 
 /* ---- soft (Gumbel-softmax) path --------------------------------------------------- */

@@ -80,6 +80,10 @@ struct Args {
   // EPI_BF16: bf16 [I, J] (row stride ldres) added to the stored bf16 values and rounded
   // again, as a bf16 tensor add after the GEMM would (NULL: none)
   const uint16_t* res; int64_t ldres;
+  // EPI_BF16: the [gate | up] pre-activations [I, 2J] (row stride ld_sw) of a SwiGLU whose
+  // output gradient this GEMM computes; the stored values are then the SwiGLU's gate / up
+  // gradients, into c [I, 2J] (NULL: none)
+  const uint16_t* sw_pre; int64_t ld_sw;
   const uint16_t* logits; const float* noise; float inv_tau, glog_scale; uint16_t* grad_logits;
   uint64_t noise_seed, noise_offset;  // noise == nullptr: Philox at noise_offset + n*K + k
   int logits_f16;

@@ -730,6 +730,19 @@ __device__ __forceinline__ u32x4 add_residual8(u32x4 v, const uint16_t* r) {
   return o;
 }
 
+// 8 stored bf16 values of grad_h at (i, j) through the SwiGLU backward (g.sw_pre set): its gate
+// and up gradients go to columns j and J + j of the [I, 2J] output
+__device__ __forceinline__ void store_swiglu_bwd8(const Args& g, u32x4 v, uint16_t* C, int64_t i,
+                                                  int64_t j) {
+  const uint16_t* pre = g.sw_pre + i * g.ld_sw + j;
+  uint4 gg, gu;
+  swiglu_bwd8(*reinterpret_cast<const uint4*>(pre), *reinterpret_cast<const uint4*>(pre + g.J),
+              make_uint4(v[0], v[1], v[2], v[3]), gg, gu);
+  const u32x4 a = {gg.x, gg.y, gg.z, gg.w}, b = {gu.x, gu.y, gu.z, gu.w};
+  __builtin_nontemporal_store(a, reinterpret_cast<u32x4*>(C + i * g.ldc + j));
+  __builtin_nontemporal_store(b, reinterpret_cast<u32x4*>(C + i * g.ldc + g.J + j));
+}
+
 __device__ __forceinline__ void store_tile_bf16(const Args& g, const f32x16 (&acc)[WT_I][WT_J],
                                                 lds_u8* st, int64_t i0, int64_t j0, int wi,
                                                 int wj, int lane) {
@@ -745,7 +758,10 @@ __device__ __forceinline__ void store_tile_bf16(const Args& g, const f32x16 (&ac
       if (g.res) v = add_residual8(v, g.res + i * g.ldres + j);
       // streaming store: the output is not read again by this launch, so it should not take
       // cache lines from the operands the other workgroups are still reading
-      __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(C + i * g.ldc + j));
+      if (g.sw_pre)
+        store_swiglu_bwd8(g, v, C, i, j);
+      else
+        __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(C + i * g.ldc + j));
     }
   }
 }
@@ -1361,7 +1377,10 @@ __global__ __launch_bounds__(TAIL_THREADS) void tail_reduce_kernel(const Args g)
     if (i < g.I && j < g.J) {  // streaming store, as store_tile_bf16
       u32x4 v = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(st + row * EPI_RS + c8 * 2);
       if (g.res) v = add_residual8(v, g.res + i * g.ldres + j);
-      __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(C + i * g.ldc + j));
+      if (g.sw_pre)
+        store_swiglu_bwd8(g, v, C, i, j);
+      else
+        __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(C + i * g.ldc + j));
     }
   }
 }
@@ -1964,29 +1983,50 @@ size_t plz_linear_bwd_x_dense_workspace(int64_t M, int64_t N, int64_t K) {
   return M > 0 && N > 0 && K > 0 ? tail_bytes(M, K, N) : 0;
 }
 
-int plz_linear_bwd_x_dense(const uint16_t* grad_y, const uint16_t* w, const uint16_t* lora_gt,
-                           const uint16_t* lora_a, int rank, uint16_t* grad_x, void* workspace,
-                           size_t workspace_bytes, int64_t M, int64_t N, int64_t K,
-                           void* stream) {
-  PLZ_REQUIRE(M >= 0 && N >= 0 && K >= 0, "plz_linear_bwd_x_dense: negative shape");
-  PLZ_REQUIRE(K % 8 == 0 && N % 8 == 0, "plz_linear_bwd_x_dense: K and N must be multiples of 8");
+static int linear_bwd_x_dense(const uint16_t* grad_y, const uint16_t* w, const uint16_t* lora_gt,
+                              const uint16_t* lora_a, int rank, const uint16_t* sw_pre,
+                              uint16_t* grad_x, void* workspace, size_t workspace_bytes, int64_t M,
+                              int64_t N, int64_t K, void* stream, const char* what) {
+  PLZ_REQUIRE(M >= 0 && N >= 0 && K >= 0, "%s: negative shape", what);
+  PLZ_REQUIRE(K % 8 == 0 && N % 8 == 0, "%s: K and N must be multiples of 8", what);
   PLZ_REQUIRE(rank >= 0 && rank <= BK && rank % 8 == 0,
-              "plz_linear_bwd_x_dense: rank (%d) must be a multiple of 8 in [0, 64]", rank);
+              "%s: rank (%d) must be a multiple of 8 in [0, 64]", what, rank);
   if (M == 0 || K == 0) return PLZ_OK;
   PLZ_REQUIRE(grad_y && w && grad_x && a16(grad_y) && a16(w),
-              "plz_linear_bwd_x_dense: grad_y, w, grad_x must be non-null; grad_y, w aligned");
+              "%s: grad_y, w, grad_x must be non-null; grad_y, w aligned", what);
   PLZ_REQUIRE(rank == 0 || (lora_gt && lora_a && a16(lora_gt) && a16(lora_a)),
-              "plz_linear_bwd_x_dense: rank > 0 needs 16-byte aligned lora_gt and lora_a");
+              "%s: rank > 0 needs 16-byte aligned lora_gt and lora_a", what);
   Args g = {};
   g.a = grad_y; g.lda = N;
   g.b = w; g.ldb = K;  // B(j=k, r=n) = w[n, k]   (Col tile)
   g.I = M; g.J = K; g.R = N;
   g.a2 = lora_gt; g.b2 = lora_a; g.R2 = rank;
-  g.c = grad_x; g.ldc = K; g.alpha = 1.f;
+  g.c = grad_x; g.ldc = sw_pre ? 2 * K : K; g.alpha = 1.f;
+  g.sw_pre = sw_pre; g.ld_sw = 2 * K;
   g.group = kDenseGroup;
-  const int rc = set_tail(g, workspace, workspace_bytes, "plz_linear_bwd_x_dense");
+  const int rc = set_tail(g, workspace, workspace_bytes, what);
   if (rc != PLZ_OK) return rc;
-  return launch<OP_ROW, OP_COL, EPI_BF16>(g, 1, (hipStream_t)stream, "plz_linear_bwd_x_dense");
+  return launch<OP_ROW, OP_COL, EPI_BF16>(g, 1, (hipStream_t)stream, what);
+}
+
+int plz_linear_bwd_x_dense(const uint16_t* grad_y, const uint16_t* w, const uint16_t* lora_gt,
+                           const uint16_t* lora_a, int rank, uint16_t* grad_x, void* workspace,
+                           size_t workspace_bytes, int64_t M, int64_t N, int64_t K,
+                           void* stream) {
+  return linear_bwd_x_dense(grad_y, w, lora_gt, lora_a, rank, nullptr, grad_x, workspace,
+                            workspace_bytes, M, N, K, stream, "plz_linear_bwd_x_dense");
+}
+
+int plz_linear_bwd_x_dense_swiglu(const uint16_t* grad_y, const uint16_t* w,
+                                  const uint16_t* lora_gt, const uint16_t* lora_a, int rank,
+                                  const uint16_t* gate_up, uint16_t* grad_gate_up, void* workspace,
+                                  size_t workspace_bytes, int64_t M, int64_t N, int64_t K,
+                                  void* stream) {
+  PLZ_REQUIRE(M == 0 || K == 0 || (gate_up && grad_gate_up && a16(gate_up) && a16(grad_gate_up)),
+              "plz_linear_bwd_x_dense_swiglu: gate_up and grad_gate_up must be non-null, "
+              "16-byte aligned");
+  return linear_bwd_x_dense(grad_y, w, lora_gt, lora_a, rank, gate_up, grad_gate_up, workspace,
+                            workspace_bytes, M, N, K, stream, "plz_linear_bwd_x_dense_swiglu");
 }
 
 size_t plz_soft_bwd_workspace(int64_t M, int64_t N, int64_t K) {

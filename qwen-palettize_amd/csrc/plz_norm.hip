@@ -10,21 +10,6 @@
 
 namespace plz {
 
-__device__ __forceinline__ void unpack8(uint4 v, float f[8]) {
-  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    f[2 * i] = bf2f(w[i] & 0xffffu);
-    f[2 * i + 1] = bf2f(w[i] >> 16);
-  }
-}
-__device__ __forceinline__ uint4 pack8(const float f[8]) {
-  uint32_t w[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) w[i] = f2bf(f[2 * i]) | (f2bf(f[2 * i + 1]) << 16);
-  return make_uint4(w[0], w[1], w[2], w[3]);
-}
-
 constexpr int kNormMaxChunks = 8;  // cols <= 8 * 512 = 4096
 
 // Row shapes: LPR lanes per row (RPW = 64 / LPR rows per wave) and up to MAXC 8-column chunks
@@ -263,21 +248,6 @@ __device__ __forceinline__ uint4 swiglu_fwd8(uint4 gate, uint4 up) {
 #pragma unroll
   for (int j = 0; j < 8; ++j) o[j] = swiglu_elem(g[j], u[j]);
   return pack8(o);
-}
-__device__ __forceinline__ void swiglu_bwd8(uint4 gate, uint4 up, uint4 gh, uint4& gg, uint4& gu) {
-  float g[8], u[8], d[8], og[8], ou[8];
-  unpack8(gate, g);
-  unpack8(up, u);
-  unpack8(gh, d);
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const float sg = 1.f / (1.f + __expf(-g[j]));
-    const float s = g[j] * sg;
-    ou[j] = d[j] * s;
-    og[j] = d[j] * u[j] * sg * (1.f + g[j] * (1.f - sg));
-  }
-  gg = pack8(og);
-  gu = pack8(ou);
 }
 
 __global__ void swiglu_fwd_kernel(const uint16_t* __restrict__ gate, const uint16_t* __restrict__ up,

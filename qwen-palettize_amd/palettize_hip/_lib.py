@@ -75,6 +75,7 @@ SIGNATURES: dict[str, tuple] = {
     "plz_bias_grad": (i32, [p, p, i64, i64, p]),
     "plz_linear_fwd_dense": (i32, [p, p, p, p, p, i32, p, p, sz, i64, i64, i64, p]),
     "plz_linear_fwd_dense_residual": (i32, [p, p, p, p, p, i32, p, p, p, sz, i64, i64, i64, p]),
+    "plz_linear_bwd_x_dense_swiglu": (i32, [p, p, p, p, i32, p, p, p, sz, i64, i64, i64, p]),
     "plz_linear_fwd_dense_workspace": (sz, [i64, i64, i64]),
     "plz_linear_fwd_dense_swiglu": (i32, [p, p, p, i64, i64, i64, p]),
     "plz_linear_fwd_dense_swiglu_cat": (i32, [p, p, p, p, i32, p, p, i64, i64, i64, p]),

@@ -99,11 +99,14 @@ class SoftLUTLinearFunction(torch.autograd.Function):
     itself and keeps P for the backward, as the reference's forward keeps its fp16 P_aos
     (fused_lut_linear_cuda.py:903-905, 919); the noise is not kept. ``residual`` (optional,
     bf16 [M, N]) is added to y in the GEMM's epilogue, as a separate bf16 add after it would
-    (its gradient is grad_y)."""
+    (its gradient is grad_y). ``swiglu`` (optional, a layer.SwiGLULink whose ``pre`` holds the
+    [gate | up] pre-activations of the SwiGLU that produced x) has the backward's grad_x GEMM
+    run the SwiGLU backward in its epilogue: it leaves [grad_gate | grad_up] in the link and
+    returns a placeholder for grad_x, which only that SwiGLU's backward may receive."""
 
     @staticmethod
     def forward(ctx, x, palette, logits, noise, tau, bias, lora_a, lora_b, lora_scale, mode,
-                scale_by_inv_tau, prebuilt=None, residual=None):
+                scale_by_inv_tau, prebuilt=None, residual=None, swiglu=None):
         x = x.contiguous()
         lora_a, lora_b = _c(lora_a), _c(lora_b)
         ctx.guard = None
@@ -126,6 +129,7 @@ class SoftLUTLinearFunction(torch.autograd.Function):
         keep_noise = ctx.philox is None and ctx.probs is None
         ctx.save_for_backward(x, palette, logits, noise if keep_noise else None, w, lora_a, lora_b,
                               t)
+        ctx.swiglu = swiglu
         ctx.tau = float(tau)
         ctx.lora_scale = float(lora_scale)
         ctx.scale_by_inv_tau = bool(scale_by_inv_tau)
@@ -155,7 +159,13 @@ class SoftLUTLinearFunction(torch.autograd.Function):
         gt = None
         if lora_a is not None and (need_x or (need_lora and not fused)):
             gt = ops.lora_grad_t(gy, lora_b, ctx.lora_scale)
-        grad_x = ops.linear_bwd_x_dense(gy, w, gt, lora_a) if need_x else None
+        link = ctx.swiglu
+        if need_x and link is not None and link.pre is not None:
+            link.grad = ops.linear_bwd_x_dense_swiglu(gy, w, link.pre, gt, lora_a)
+            grad_x = torch.empty(1, dtype=gy.dtype, device=gy.device).expand(x.shape)
+            link.marker = grad_x.data_ptr()
+        else:
+            grad_x = ops.linear_bwd_x_dense(gy, w, gt, lora_a) if need_x else None
         grad_logits = grad_pal = grad_a = grad_b = None
         if fused:
             sq = ctx.grad_sq if need_log else None
@@ -173,7 +183,7 @@ class SoftLUTLinearFunction(torch.autograd.Function):
             grad_a, grad_b = ops.lora_weight_grads(x, gy, t, gt, 1.0, out_dtype=lora_a.dtype)
         return (grad_x, grad_pal if need_pal else None, grad_logits if need_log else None, None,
                 None, grad_bias, grad_a, grad_b, None, None, None, None,
-                gy if len(need) > 12 and need[12] else None)
+                gy if len(need) > 12 and need[12] else None, None)
 
 
 def soft_lut_linear(x, palette, logits, noise, tau, bias=None, lora_a=None, lora_b=None,

@@ -245,11 +245,12 @@ class SoftPalettizedLinear(nn.Module):
         self.noise_counter += NOISE_STRIDE
         return ops.PhiloxNoise(self.noise_seed, off)
 
-    def forward(self, x, prebuilt=None, residual=None):
+    def forward(self, x, prebuilt=None, residual=None, swiglu=None):
         """prebuilt: (w, group) from the layer's batched build of this forward (the noise
         counter has then been advanced by the layer). residual (optional, bf16 [..., N]): added
         to the output in the GEMM's epilogue (the layer's residual add after its down
-        projection)."""
+        projection). swiglu (optional SwiGLULink): x is that SwiGLU's output, and the grad_x
+        GEMM runs its backward in the epilogue."""
         _gpu_bf16(x, "SoftPalettizedLinear input")
         lead = x.shape[:-1]
         if prebuilt is None:
@@ -261,7 +262,8 @@ class SoftPalettizedLinear(nn.Module):
         res = None if residual is None else residual.reshape(-1, self.out_features)
         y = SoftLUTLinearFunction.apply(x.reshape(-1, x.shape[-1]), self.palette, self.index_logits,
                                         noise, self.tau, None, self.lora_a, self.lora_b,
-                                        self.lora_scale, self.mode, False, prebuilt, res)
+                                        self.lora_scale, self.mode, False, prebuilt, res,
+                                        swiglu)
         return y.reshape(*lead, self.out_features)
 
 
@@ -375,14 +377,16 @@ class SoftLinearGroup:
                                           *self._params())
         return y.reshape(*lead, self.N)
 
-    def forward_swiglu(self, x, prebuilt):
+    def forward_swiglu(self, x, prebuilt, link=None):
         """silu(gate) * up of a [gate | up] group from one GEMM (the SwiGLU in its epilogue):
-        the same values as SwiGLUCatFunction over forward(x, prebuilt), bit for bit."""
+        the same values as SwiGLUCatFunction over forward(x, prebuilt), bit for bit. link
+        (optional SwiGLULink): receives the pre-activations, so that the consumer's grad_x GEMM
+        can run the SwiGLU backward."""
         _gpu_bf16(x, "SoftLinearGroup input")
         if len(self.parts) != 2 or self.rows[0] != self.rows[1] or self.rows[0] % 128:
             raise ValueError("forward_swiglu needs two parts of equal rows, a multiple of 128")
         lead = x.shape[:-1]
-        h = SoftGateUpSwiGLUFunction.apply(x.reshape(-1, x.shape[-1]), self, prebuilt,
+        h = SoftGateUpSwiGLUFunction.apply(x.reshape(-1, x.shape[-1]), self, prebuilt, link,
                                            *self._params())
         return h.reshape(*lead, self.N // 2)
 
@@ -444,24 +448,48 @@ class SoftLinearGroupFunction(torch.autograd.Function):
         return (grad_x, None, None, *grads)
 
 
+class SwiGLULink:
+    """Hands the SwiGLU's backward to the grad_x GEMM of the linear that consumes its output
+    (plz_linear_bwd_x_dense_swiglu): the SwiGLU's forward sets ``pre`` ([gate | up]
+    pre-activations), that linear's backward sets ``grad`` ([grad_gate | grad_up]) and returns a
+    placeholder grad_h whose data_ptr is ``marker``; the SwiGLU's backward takes ``grad`` when it
+    receives that placeholder and raises if it receives anything else (grad_h accumulated from
+    another consumer), since the placeholder holds no values."""
+
+    def __init__(self):
+        self.pre = self.grad = self.marker = None
+
+
 class SoftGateUpSwiGLUFunction(torch.autograd.Function):
     """A [gate | up] SoftLinearGroup followed by the SwiGLU, as one GEMM whose epilogue writes
     both the pre-activations (kept for the backward) and h (plz_linear_fwd_dense_swiglu_cat).
     The backward is the SwiGLU's (plz_swiglu_bwd_rows) and then the group's own."""
 
     @staticmethod
-    def forward(ctx, x, grp, prebuilt, *params):
+    def forward(ctx, x, grp, prebuilt, link, *params):
         x, w, a, b, t = SoftLinearGroupFunction._setup(ctx, x, grp, prebuilt)
         y, h = ops.linear_fwd_dense_swiglu_cat(x, w, t, b)
         ctx.save_for_backward(x, grp.palette(), grp.logits(), w, a, b.clone(), y)
+        ctx.link = link
+        if link is not None:
+            link.pre, link.grad, link.marker = y, None, None
         return h
 
     @staticmethod
     def backward(ctx, gh):
         x, pal, logits, w, a, b, y = ctx.saved_tensors
-        gy = ops.swiglu_bwd_cat(y, gh.contiguous())
+        link = ctx.link
+        if link is not None and link.grad is not None:
+            if gh.data_ptr() != link.marker:
+                raise RuntimeError("the SwiGLU's output gradient did not come only from the linear "
+                                   "that computed its backward (SwiGLULink)")
+            gy = link.grad
+            link.pre = link.grad = link.marker = None
+        else:
+            gy = ops.swiglu_bwd_cat(y, gh.contiguous())
         del y
-        return SoftLinearGroupFunction._backward(ctx, gy, x, pal, logits, w, a, b)
+        r = SoftLinearGroupFunction._backward(ctx, gy, x, pal, logits, w, a, b)
+        return (*r[:3], None, *r[3:])  # no gradient for the link
 
 
 # ---- RoPE / attention -------------------------------------------------------------------------
@@ -596,6 +624,8 @@ class PalettizedDecoderLayer(nn.Module):
         # the build also keeps each weight's P (fp16), which the soft backward then reads instead
         # of drawing the noise again, as the reference's backward reads its saved P_aos
         self.save_probs = True
+        # the SwiGLU backward in the epilogue of the down projection's grad_x GEMM (SwiGLULink)
+        self.swiglu_bwd_in_down = True
 
     def linears(self):
         return [getattr(self, n) for n in self.NAMES]
@@ -709,12 +739,15 @@ class PalettizedDecoderLayer(nn.Module):
         v = self.v_proj(x, pw["v_proj"]).view(B, S, cfg.kv_heads, cfg.head_dim)
         hs, x = add_rmsnorm(self.post_attention_layernorm, hs,
                             self.o_proj(attention(q, k, v, cfg.heads, cfg.kv_heads), pw["o_proj"]))
+        link = None
         if self.gate_up is not None:
-            h = self.gate_up.forward_swiglu(x, pw["gate_up"])
+            # the SwiGLU backward runs in the down projection's grad_x GEMM epilogue
+            link = SwiGLULink() if self.swiglu_bwd_in_down else None
+            h = self.gate_up.forward_swiglu(x, pw["gate_up"], link)
         else:
             h = SwiGLUFunction.apply(self.gate_proj(x, pw["gate_proj"]), self.up_proj(x, pw["up_proj"]))
         # the residual add in the down GEMM's epilogue
-        return self.down_proj(h, pw["down_proj"], residual=hs)
+        return self.down_proj(h, pw["down_proj"], residual=hs, swiglu=link)
 
 
 class DenseDecoderLayer(nn.Module):

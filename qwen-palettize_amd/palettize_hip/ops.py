@@ -339,6 +339,33 @@ def linear_bwd_x_dense(grad_y, w, lora_gt=None, lora_a=None):
     return gx
 
 
+def linear_bwd_x_dense_swiglu(grad_y, w, gate_up, lora_gt=None, lora_a=None):
+    """[grad_gate | grad_up] [M, 2K] of h = silu(gate) * up (gate_up [M, 2K] its pre-activations)
+    for grad_h = grad_y w (+ lora_gt lora_a), with the SwiGLU backward in the GEMM's epilogue:
+    bit for bit swiglu_bwd_cat(gate_up, linear_bwd_x_dense(...)), grad_h never stored."""
+    _need(grad_y, "grad_y", torch.bfloat16, 2)
+    _need(w, "w", torch.bfloat16, 2)
+    _need(gate_up, "gate_up", torch.bfloat16, 2)
+    M, N = grad_y.shape
+    K = w.shape[1]
+    if w.shape[0] != N or tuple(gate_up.shape) != (M, 2 * K):
+        raise ValueError("grad_y [M, N], w [N, K] and gate_up [M, 2K] expected")
+    rank = 0
+    if lora_gt is not None or lora_a is not None:
+        if lora_gt is None or lora_a is None:
+            raise ValueError("lora_gt and lora_a must be given together")
+        _need(lora_gt, "lora_gt", torch.bfloat16, 2)
+        _need(lora_a, "lora_a", torch.bfloat16, 2)
+        rank = lora_gt.shape[1]
+        if lora_gt.shape[0] != M or tuple(lora_a.shape) != (rank, K):
+            raise ValueError("lora_gt / lora_a shape mismatch")
+    out = torch.empty((M, 2 * K), dtype=torch.bfloat16, device=grad_y.device)
+    ws = _opt_workspace(query("plz_linear_bwd_x_dense_workspace", M, N, K), grad_y.device)
+    call("plz_linear_bwd_x_dense_swiglu", _ptr(grad_y), _ptr(w), _ptr(lora_gt), _ptr(lora_a),
+         rank, _ptr(gate_up), _ptr(out), _ptr(ws), _numel(ws), M, N, K, _stream(grad_y))
+    return out
+
+
 # ---- soft path ------------------------------------------------------------------------
 def gumbel_philox(shape, seed: int, offset: int = 0, device="cuda"):
     n = 1

@@ -51,6 +51,9 @@ def test_shape_errors_are_reported_without_touching_the_gpu(lib):
     rc = lib.plz_linear_fwd_dense_residual(None, None, None, None, None, 0, None, None, None, 0,
                                            8, 8, 8, None)
     assert rc == 1 and b"residual" in lib.plz_last_error()
+    rc = lib.plz_linear_bwd_x_dense_swiglu(None, None, None, None, 0, None, None, None, 0, 8, 8,
+                                           8, None)
+    assert rc == 1 and b"gate_up" in lib.plz_last_error()
     rc = lib.plz_soft_build_w(None, 0, None, None, 0.0, 0, None, None, None, 8, 256, None)
     assert rc == 1 and b"tau" in lib.plz_last_error()
     rc = lib.plz_rmsnorm_fwd(None, None, None, None, 4, 5000, 1e-6, None)

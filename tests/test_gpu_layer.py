@@ -244,3 +244,27 @@ def test_clip_norm_from_the_backwards_squared_sums(dev):
     with torch.no_grad():
         a.student.q_proj.index_logits.grad.mul_(0.0)
     assert id(a.student.q_proj.index_logits) not in a._grad_sq()
+
+
+def test_swiglu_backward_in_the_down_grad_x_gemm(dev):
+    """swiglu_bwd_in_down: the student's SwiGLU backward runs in the epilogue of the down
+    projection's grad_x GEMM (SwiGLULink, plz_linear_bwd_x_dense_swiglu). Against a layer that
+    runs the separate SwiGLU backward: the same loss and every gradient bit for bit over two
+    steps (the link is used afresh each step)."""
+    cfg = layer.LayerConfig(**CFG)
+    hs = torch.randn(2, 16, cfg.hidden, generator=torch.Generator().manual_seed(12))
+    hs = hs.to(torch.bfloat16).to(dev)
+    a = layer.LayerTrainer(cfg, dev, seed=6, lora_b_std=0.02)
+    b = layer.LayerTrainer(cfg, dev, seed=6, lora_b_std=0.02)
+    assert a.student.swiglu_bwd_in_down and a.student.gate_up is not None
+    b.student.swiglu_bwd_in_down = False
+    for _ in range(2):
+        la, _ = a.forward_backward(hs)
+        lb, _ = b.forward_backward(hs)
+        assert float(la) == float(lb)
+        for pa, pb in zip(a.student.parameters(), b.student.parameters()):
+            assert (pa.grad is None) == (pb.grad is None)
+            if pa.grad is not None:
+                assert torch.equal(pa.grad, pb.grad)
+        a.update()
+        b.update()

@@ -126,6 +126,22 @@ def test_swiglu_concatenated_layout(dev):
         ops.swiglu_bwd_cat(gu.to(dev), gh[:, :-8].contiguous().to(dev))
 
 
+@pytest.mark.parametrize("M,N,K,r", [(16384, 2560, 9728, 16), (300, 1032, 768, 0),
+                                     (2048, 512, 1024, 32)])
+def test_grad_x_gemm_with_swiglu_backward_epilogue(dev, M, N, K, r):
+    """plz_linear_bwd_x_dense_swiglu: [grad_gate | grad_up] bit for bit plz_linear_bwd_x_dense
+    (with LoRA) followed by the SwiGLU backward over the pre-activations, on the layer's down
+    shape (split last-wave tiles) and on a ragged edge."""
+    gy = randn_bf16(M, N, seed=41).to(dev)
+    w = (randn_bf16(N, K, seed=42).float() * 0.02).to(torch.bfloat16).to(dev)
+    pre = randn_bf16(M, 2 * K, seed=43, std=2.0).to(dev)
+    gt = randn_bf16(M, r, seed=44).to(dev) if r else None
+    la = randn_bf16(r, K, seed=45, std=0.01).to(dev) if r else None
+    got = ops.linear_bwd_x_dense_swiglu(gy, w, pre, gt, la)
+    want = ops.swiglu_bwd_cat(pre, ops.linear_bwd_x_dense(gy, w, gt, la))
+    assert torch.equal(got, want)
+
+
 @pytest.mark.parametrize("M,N,K,r,bias", [(300, 1032, 768, 0, False), (2048, 1024, 512, 16, True),
                                           (16384, 2560, 9728, 16, False), (4096, 2560, 2560, 0, True)])
 def test_dense_gemm_with_residual_epilogue(dev, M, N, K, r, bias):
